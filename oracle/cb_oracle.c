@@ -1,0 +1,645 @@
+/*
+ * cb_oracle.c -- CPU restatement of catboost_rs's oblivious-tree training path.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity checker + CPU baseline); never linked by the
+ * product library.  See cb_oracle.h for what pins each function.
+ *
+ * Arithmetic-order contract: every float sum is a sequential left-to-right f64
+ * fold in ascending object (or bin / leaf) order, exactly like the reference's
+ * cb_core::sum_f64 (crates/cb-core/src/reduction.rs:32).  Parallelism is only
+ * over independent features (crates/cb-train/src/tree.rs:1191-1252), so the
+ * result does not depend on the thread count.
+ *
+ * Build with -ffp-contract=off: the reference never fuses multiply-adds.
+ */
+#include "cb_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ======================================================================
+ * TFastRng64 (crates/cb-core/src/rng.rs:24-292)
+ * ==================================================================== */
+static const uint64_t LCG_A = 6364136223846793005ULL; /* rng.rs:26 */
+
+static inline uint32_t pcg_mix(uint64_t x) { /* rng.rs:31-38 */
+    uint32_t xs = (uint32_t)(((x >> 18) ^ x) >> 27);
+    uint32_t rot = (uint32_t)(x >> 59);
+    return (xs >> rot) | (xs << ((32 - rot) & 31));
+}
+
+/* NPrivate::LcgAdvance, closed-form jump (rng.rs:45-66). */
+static uint64_t lcg_advance(uint64_t seed, uint64_t base, uint64_t addend, uint64_t delta) {
+    uint64_t mask = 1;
+    while (mask != (1ULL << 63) && (mask << 1) <= delta) mask <<= 1;
+    uint64_t apow = 1, adiv = 0;
+    while (mask != 0) {
+        adiv = adiv * (apow + 1);
+        apow = apow * apow;
+        if (delta & mask) {
+            adiv = adiv + apow;
+            apow = apow * base;
+        }
+        mask >>= 1;
+    }
+    return seed * apow + addend * adiv;
+}
+
+static inline uint32_t lcg32_next(uint64_t* x, uint64_t c) { /* rng.rs:103-106 */
+    *x = *x * LCG_A + c;
+    return pcg_mix(*x);
+}
+
+static uint32_t fix_seq(uint32_t seq1, uint32_t seq2) { /* rng.rs:128-135 */
+    uint32_t mask = (~0u) >> 1;
+    return ((seq1 & mask) == (seq2 & mask)) ? ~seq2 : seq2;
+}
+
+void orc_rng_new(orc_rng* r, uint64_t seed1, uint32_t seq1, uint64_t seed2, uint32_t seq2) {
+    r->x1 = seed1;
+    r->c1 = ((uint64_t)seq1 << 1) | 1;
+    r->x2 = seed2;
+    r->c2 = ((uint64_t)fix_seq(seq1, seq2) << 1) | 1;
+    r->calls = 0;
+}
+
+void orc_rng_from_seed(orc_rng* r, uint64_t seed) { /* rng.rs:171-180 */
+    uint64_t x = seed;
+    uint64_t lo = lcg32_next(&x, 1), hi = lcg32_next(&x, 1);
+    uint64_t seed1 = lo | (hi << 32);
+    uint32_t seq1 = lcg32_next(&x, 1);
+    lo = lcg32_next(&x, 1);
+    hi = lcg32_next(&x, 1);
+    uint64_t seed2 = lo | (hi << 32);
+    uint32_t seq2 = lcg32_next(&x, 1);
+    orc_rng_new(r, seed1, seq1, seed2, seq2);
+}
+
+uint64_t orc_rng_gen(orc_rng* r) { /* rng.rs:183-189: stream 1 -> high half */
+    uint64_t a = lcg32_next(&r->x1, r->c1);
+    uint64_t b = lcg32_next(&r->x2, r->c2);
+    r->calls++;
+    return (a << 32) | b;
+}
+
+void orc_rng_advance(orc_rng* r, uint64_t delta) { /* rng.rs:192-197 */
+    r->x1 = lcg_advance(r->x1, LCG_A, r->c1, delta);
+    r->x2 = lcg_advance(r->x2, LCG_A, r->c2, delta);
+    r->calls += delta;
+}
+
+double orc_rng_real1(orc_rng* r) { /* rng.rs:256-259 */
+    return (double)(orc_rng_gen(r) >> 11) * (1.0 / 9007199254740991.0);
+}
+
+uint64_t orc_rng_uniform(orc_rng* r, uint64_t bound) { /* rng.rs:268-280 */
+    if (bound == 0) return 0;
+    uint64_t randmax = UINT64_MAX - (UINT64_MAX % bound);
+    for (;;) {
+        uint64_t v = orc_rng_gen(r);
+        if (v < randmax) return v % bound;
+    }
+}
+
+double orc_std_normal(orc_rng* r) { /* cb-core/src/normal.rs:50-64 (Marsaglia polar) */
+    for (;;) {
+        double x = orc_rng_real1(r) * 2.0 - 1.0;
+        double y = orc_rng_real1(r) * 2.0 - 1.0;
+        double rr = x * x + y * y;
+        if (!(rr > 1.0 || rr <= 0.0)) return x * sqrt(-2.0 * log(rr) / rr);
+    }
+}
+
+/* FastLogf (crates/cb-train/src/fast_approx.rs:154-177): all-f32 op order. */
+float orc_fast_logf(float value) {
+    uint32_t vx;
+    memcpy(&vx, &value, 4);
+    uint32_t mbits = (vx & 0x007FFFFFu) | 0x3f000000u;
+    float mx;
+    memcpy(&mx, &mbits, 4);
+    float y = (float)vx;
+    y *= 1.1920928955078125e-7f;
+    float l2 = y - 124.22551499f - 1.498030302f * mx - 1.72587999f / (0.3520887068f + mx);
+    return 0.69314718f * l2;
+}
+
+/* ======================================================================
+ * Bootstrap (crates/cb-train/src/bootstrap.rs)
+ * ==================================================================== */
+#define BAYESIAN_BLOCK 1000 /* bootstrap.rs:81 */
+
+int orc_bootstrap(int32_t type, uint64_t n, double subsample, float temperature, orc_rng* rng,
+                  double* sw, uint8_t* control) {
+    if (type == ORC_BOOT_NO) { /* BootstrapResult::identity */
+        for (uint64_t i = 0; i < n; ++i) { sw[i] = 1.0; control[i] = 1; }
+        return 0;
+    }
+    if (type == ORC_BOOT_BAYESIAN) { /* bootstrap.rs:152-169 + bayesian_weight :141-146 */
+        for (uint64_t i = 0; i < n; ++i) control[i] = 1;
+        if (temperature == 0.0f) {
+            for (uint64_t i = 0; i < n; ++i) sw[i] = 1.0;
+            return 0;
+        }
+        uint64_t seed = orc_rng_gen(rng);
+        uint64_t blocks = (n + BAYESIAN_BLOCK - 1) / BAYESIAN_BLOCK;
+        for (uint64_t b = 0; b < blocks; ++b) {
+            orc_rng br;
+            orc_rng_from_seed(&br, seed + b);
+            orc_rng_advance(&br, 10);
+            uint64_t end = (b + 1) * BAYESIAN_BLOCK;
+            if (end > n) end = n;
+            for (uint64_t i = b * BAYESIAN_BLOCK; i < end; ++i) {
+                double u = orc_rng_real1(&br);
+                float w = -orc_fast_logf((float)u + 1e-100f);
+                sw[i] = (double)powf(w, temperature);
+            }
+        }
+        return 0;
+    }
+    if (type == ORC_BOOT_BERNOULLI) { /* bootstrap.rs:178-184 set_sampled_control */
+        for (uint64_t i = 0; i < n; ++i) sw[i] = 1.0;
+        if (subsample >= 1.0) {
+            for (uint64_t i = 0; i < n; ++i) control[i] = 1;
+            return 0;
+        }
+        double rate = (double)(float)subsample;
+        for (uint64_t i = 0; i < n; ++i) control[i] = orc_rng_real1(rng) < rate;
+        return 0;
+    }
+    return -1;
+}
+
+/* ======================================================================
+ * Quantization (crates/cb-compute/src/histogram.rs:563-569 bin_of)
+ * ==================================================================== */
+void orc_quantize(const float* values, uint64_t n, const double* borders, uint32_t nb,
+                  uint8_t* out) {
+    int nan_top = nb > 0 && borders[nb - 1] == (double)3.40282346638528859812e+38F;
+    for (uint64_t i = 0; i < n; ++i) {
+        float v = values[i];
+        if (isnan(v) && nan_top) { out[i] = (uint8_t)nb; continue; }
+        double dv = (double)v;
+        uint32_t c = 0;
+        for (uint32_t k = 0; k < nb; ++k) c += borders[k] < dv;
+        out[i] = (uint8_t)c;
+    }
+}
+
+/* ======================================================================
+ * Derivatives (crates/cb-compute/src/loss.rs:35-80)
+ * ==================================================================== */
+void orc_ders(int32_t loss, const double* a, const double* t, uint64_t n, double* d1,
+              double* d2) {
+    for (uint64_t i = 0; i < n; ++i) {
+        if (loss == ORC_LOSS_RMSE) {
+            d1[i] = t[i] - a[i];
+            if (d2) d2[i] = -1.0;
+        } else {
+            double e = exp(a[i]);
+            double p = 1.0 - 1.0 / (1.0 + e);
+            d1[i] = t[i] - p;
+            if (d2) d2[i] = -p * (1.0 - p);
+        }
+    }
+}
+
+/* MultiClass softmax ders for one object (loss.rs:424-486): der1[k], packed der2[k(k+1)/2]. */
+static void softmax_ders(const double* approx, int k, int target_class, double* der1,
+                         double* der2) {
+    double mx = -INFINITY;
+    for (int d = 0; d < k; ++d)
+        if (approx[d] > mx) mx = approx[d];
+    double p[64];
+    double sum = 0.0;
+    for (int d = 0; d < k; ++d) { p[d] = exp(approx[d] - mx); }
+    for (int d = 0; d < k; ++d) sum += p[d];
+    for (int d = 0; d < k; ++d) p[d] = p[d] / sum;
+    int idx = 0;
+    for (int y = 0; y < k; ++y) {
+        der2[idx++] = p[y] * (p[y] - 1.0);
+        for (int x = y + 1; x < k; ++x) der2[idx++] = p[y] * p[x];
+    }
+    for (int d = 0; d < k; ++d) der1[d] = -p[d];
+    if (target_class >= 0 && target_class < k) der1[target_class] += 1.0;
+}
+
+/* ======================================================================
+ * Leaf estimators (crates/cb-compute/src/leaf.rs)
+ * ==================================================================== */
+static inline double calc_average(double s, double w, double l2) { /* leaf.rs:161-167 */
+    return w > 0.0 ? s / (w + l2) : 0.0;
+}
+
+static double newton_leaf_delta(double s, double d2, double l2) { /* leaf.rs:223-233 */
+    double den = -d2 + l2;
+    return den == 0.0 ? 0.0 : s / den;
+}
+
+/* leaf.rs:387-440 cholesky_solve; returns 0 on a non-positive pivot. */
+static int cholesky_solve(int k, const double* a, const double* b, double* x) {
+    double l[64 * 64];
+    double y[64];
+    memset(l, 0, sizeof(double) * (size_t)k * (size_t)k);
+    for (int i = 0; i < k; ++i) {
+        for (int j = 0; j <= i; ++j) {
+            double sum = a[i * k + j];
+            for (int p = 0; p < j; ++p) sum -= l[i * k + p] * l[j * k + p];
+            if (i == j) {
+                if (sum <= 0.0) return 0;
+                l[i * k + j] = sqrt(sum);
+            } else {
+                double ljj = l[j * k + j];
+                if (ljj == 0.0) return 0;
+                l[i * k + j] = sum / ljj;
+            }
+        }
+    }
+    for (int i = 0; i < k; ++i) {
+        double sum = b[i];
+        for (int p = 0; p < i; ++p) sum -= l[i * k + p] * y[p];
+        if (l[i * k + i] == 0.0) return 0;
+        y[i] = sum / l[i * k + i];
+    }
+    for (int i = k - 1; i >= 0; --i) {
+        double sum = y[i];
+        for (int p = i + 1; p < k; ++p) sum -= l[p * k + i] * x[p];
+        if (l[i * k + i] == 0.0) return 0;
+        x[i] = sum / l[i * k + i];
+    }
+    return 1;
+}
+
+/* solve_symmetric_newton (leaf.rs:279-335). */
+static void solve_symmetric_newton(int k, const double* sum_der, const double* packed,
+                                   double l2, double* out) {
+    double h[64 * 64];
+    int idx = 0;
+    for (int i = 0; i < k; ++i)
+        for (int j = i; j < k; ++j) {
+            h[i * k + j] = packed[idx];
+            h[j * k + i] = packed[idx];
+            idx++;
+        }
+    float max_trace = (float)l2;
+    for (int d = 0; d < k; ++d) {
+        float v = (float)(-h[d * k + d]);
+        max_trace = fmaxf(max_trace, v);
+    }
+    double adj = (double)fmaxf((float)l2, max_trace * 1.1920928955078125e-7f);
+    for (int d = 0; d < k; ++d) h[d * k + d] -= adj;
+    for (int i = 0; i < k * k; ++i) h[i] = -h[i];
+    double nd[64], x[64];
+    for (int d = 0; d < k; ++d) nd[d] = -sum_der[d];
+    if (cholesky_solve(k, h, nd, x)) {
+        for (int d = 0; d < k; ++d) out[d] = -x[d];
+    } else {
+        for (int d = 0; d < k; ++d) out[d] = 0.0;
+    }
+}
+
+void orc_leaf_sums(const uint32_t* leaf_of, uint64_t n, uint32_t n_leaves, const double* der,
+                   const double* w, double* sum_der, double* sum_w) {
+    for (uint32_t l = 0; l < n_leaves; ++l) { sum_der[l] = 0.0; if (sum_w) sum_w[l] = 0.0; }
+    for (uint64_t i = 0; i < n; ++i) {
+        uint32_t l = leaf_of[i];
+        if (l >= n_leaves) continue;
+        sum_der[l] += der[i];
+        if (sum_w) sum_w[l] += w ? w[i] : 1.0;
+    }
+}
+
+/* ======================================================================
+ * Per-feature histogram (crates/cb-compute/src/histogram.rs:188-698)
+ * layout: hist[(leaf * n_bins + bin) * C + ch], C = K + 1, ch K = weight
+ * ==================================================================== */
+
+/* build_bucket_histogram_into restricted to one feature (histogram.rs:676-697):
+ * object-outer scatter, objects with slot >= n_leaves skipped. */
+static void build_hist(double* h, uint32_t n_leaves, uint32_t n_bins, int K, const uint8_t* col,
+                       const double* der, const double* w, const uint32_t* slot, uint64_t n) {
+    const int C = K + 1;
+    memset(h, 0, sizeof(double) * (size_t)n_leaves * n_bins * C);
+    for (uint64_t o = 0; o < n; ++o) {
+        uint32_t l = slot[o];
+        if (l >= n_leaves) continue;
+        uint32_t b = col[o];
+        if (b >= n_bins) continue;
+        double* cell = h + ((size_t)l * n_bins + b) * C;
+        for (int d = 0; d < K; ++d) cell[d] += der[(size_t)d * n + o];
+        cell[K] += w[o];
+    }
+}
+
+/* derive_feature_level_hist (tree.rs:1075-1131): build the globally smaller sibling over
+ * all objects, derive the larger as parent - smaller (one f64 subtraction per cell). */
+static void derive_hist(double* out, const double* parent, uint32_t level, uint32_t n_bins,
+                        int K, const uint8_t* col, const double* der, const double* w,
+                        const uint32_t* leaf_of, uint64_t n, uint32_t* scratch_slot,
+                        uint64_t n_true) {
+    const int C = K + 1;
+    uint32_t n_parent = 1u << (level - 1);
+    uint32_t n_next = 1u << level;
+    size_t per_leaf = (size_t)n_bins * C;
+    uint64_t n_false = n - n_true;
+    int build_true = n_true <= n_false;
+    for (uint64_t o = 0; o < n; ++o) {
+        uint32_t lf = leaf_of[o];
+        int pass = (lf & n_parent) != 0;
+        scratch_slot[o] = (pass == build_true) ? (lf & (n_parent - 1)) : 0xFFFFFFFFu;
+    }
+    /* built sibling lands in the low slots of an n_next-leaf histogram */
+    double* built = (double*)malloc(sizeof(double) * per_leaf * n_next);
+    build_hist(built, n_next, n_bins, K, col, der, w, scratch_slot, n);
+    for (uint32_t p = 0; p < n_parent; ++p) {
+        const double* par = parent + p * per_leaf;
+        const double* bl = built + p * per_leaf;
+        double* fslot = out + p * per_leaf;               /* FALSE child p */
+        double* tslot = out + (p + n_parent) * per_leaf;  /* TRUE child p + n_parent */
+        for (size_t c = 0; c < per_leaf; ++c) {
+            double other = -bl[c] + par[c]; /* relocate_sub: (-minus) + parent */
+            if (build_true) { tslot[c] = bl[c]; fslot[c] = other; }
+            else { fslot[c] = bl[c]; tslot[c] = other; }
+        }
+    }
+    free(built);
+}
+
+/* scan_and_score_borders_into (histogram.rs:1007-1149) + multi_dim_split_score_into
+ * (score.rs:192-265) for one feature with n_parent = 2^level leaves. */
+static void scan_score(const double* h, uint32_t n_parent, uint32_t n_bins, int K,
+                       uint32_t n_borders, int score_fn, double l2, double* scores) {
+    const int C = K + 1;
+    double* total_w = (double*)calloc(n_parent, sizeof(double));
+    double* total_d = (double*)calloc((size_t)n_parent * K, sizeof(double));
+    double* acc_w = (double*)calloc(n_parent, sizeof(double));
+    double* acc_d = (double*)calloc((size_t)n_parent * K, sizeof(double));
+    double* sd = (double*)malloc(sizeof(double) * 2 * n_parent * K);
+    double* sw = (double*)malloc(sizeof(double) * 2 * n_parent);
+    for (uint32_t p = 0; p < n_parent; ++p) {
+        const double* blk = h + (size_t)p * n_bins * C;
+        double t = 0.0;
+        for (uint32_t b = 0; b < n_bins; ++b) t += blk[b * C + K];
+        total_w[p] = t;
+        for (int d = 0; d < K; ++d) {
+            double td = 0.0;
+            for (uint32_t b = 0; b < n_bins; ++b) td += blk[b * C + d];
+            total_d[p * K + d] = td;
+        }
+    }
+    for (uint32_t b = 0; b < n_borders; ++b) {
+        for (uint32_t p = 0; p < n_parent; ++p) {
+            const double* cell = h + ((size_t)p * n_bins + b) * C;
+            acc_w[p] += cell[K];
+            sw[p] = acc_w[p];
+            sw[p + n_parent] = total_w[p] - acc_w[p];
+            for (int d = 0; d < K; ++d) {
+                acc_d[p * K + d] += cell[d];
+                sd[(size_t)d * 2 * n_parent + p] = acc_d[p * K + d];
+                sd[(size_t)d * 2 * n_parent + p + n_parent] = total_d[p * K + d] - acc_d[p * K + d];
+            }
+        }
+        /* fold in dimension-then-leaf order; leaves 0..P-1 FALSE, P..2P-1 TRUE */
+        double num = 0.0;
+        for (int d = 0; d < K; ++d)
+            for (uint32_t l = 0; l < 2 * n_parent; ++l) {
+                double s = sd[(size_t)d * 2 * n_parent + l];
+                double avg = calc_average(s, sw[l], l2);
+                num += avg * s;
+            }
+        if (score_fn == ORC_SCORE_L2) {
+            scores[b] = num;
+        } else {
+            double den = 0.0;
+            den += 1e-100;
+            for (int d = 0; d < K; ++d)
+                for (uint32_t l = 0; l < 2 * n_parent; ++l) {
+                    double s = sd[(size_t)d * 2 * n_parent + l];
+                    double avg = calc_average(s, sw[l], l2);
+                    den += avg * avg * sw[l];
+                }
+            scores[b] = num / sqrt(den);
+        }
+    }
+    free(total_w); free(total_d); free(acc_w); free(acc_d); free(sd); free(sw);
+}
+
+int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n, uint32_t F,
+                  const double* der, const double* w, int32_t K, int32_t depth, int32_t score_fn,
+                  double l2, orc_rng* prng, int32_t n_threads, int32_t* out_splits,
+                  double* out_scores, uint32_t* out_leaf_of, double* out_hists) {
+    const int C = K + 1;
+    uint32_t n_bins = 1;
+    for (uint32_t f = 0; f < F; ++f)
+        if (n_borders[f] + 1 > n_bins) n_bins = n_borders[f] + 1;
+    uint32_t* leaf_of = out_leaf_of;
+    memset(leaf_of, 0, sizeof(uint32_t) * n);
+    double** hists = (double**)calloc(F, sizeof(double*));
+    double** scores = (double**)calloc(F, sizeof(double*));
+    size_t hist_off = 0;
+#ifdef _OPENMP
+    int nt = n_threads > 0 ? n_threads : omp_get_max_threads();
+#endif
+    int rc = 0;
+    for (int level = 0; level < depth; ++level) {
+        uint32_t n_leaves = 1u << level;
+        size_t per_f = (size_t)n_leaves * n_bins * C;
+        if (prng) /* per-level rsm reselection draws, one per listed feature (tree.rs:746-751) */
+            for (uint32_t f = 0; f < F; ++f) (void)orc_rng_real1(prng);
+        uint64_t n_true = 0;
+        if (level > 0) {
+            uint32_t bit = 1u << (level - 1);
+            for (uint64_t o = 0; o < n; ++o) n_true += (leaf_of[o] & bit) != 0;
+        }
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nt)
+#endif
+        {
+            uint32_t* slot = level > 0 ? (uint32_t*)malloc(sizeof(uint32_t) * n) : NULL;
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+            for (int64_t fi = 0; fi < (int64_t)F; ++fi) {
+                uint32_t f = (uint32_t)fi;
+                if (n_borders[f] == 0) continue; /* never scored, never built (WR-04) */
+                const uint8_t* col = bins_fm + (size_t)f * n;
+                double* h = (double*)malloc(sizeof(double) * per_f);
+                if (level == 0) {
+                    build_hist(h, 1, n_bins, K, col, der, w, leaf_of, n);
+                } else {
+                    derive_hist(h, hists[f], (uint32_t)level, n_bins, K, col, der, w, leaf_of, n,
+                                slot, n_true);
+                }
+                free(hists[f]);
+                hists[f] = h;
+                free(scores[f]);
+                scores[f] = (double*)malloc(sizeof(double) * n_borders[f]);
+                scan_score(h, n_leaves, n_bins, K, n_borders[f], score_fn, l2, scores[f]);
+            }
+            free(slot);
+        }
+        if (out_hists) {
+            for (uint32_t f = 0; f < F; ++f) {
+                double* dst = out_hists + hist_off;
+                /* dump as [leaf][f][bin][ch] */
+                for (uint32_t l = 0; l < n_leaves; ++l) {
+                    double* d = dst + ((size_t)l * F + f) * n_bins * C;
+                    if (hists[f]) memcpy(d, hists[f] + (size_t)l * n_bins * C, sizeof(double) * n_bins * C);
+                    else memset(d, 0, sizeof(double) * n_bins * C);
+                }
+            }
+            hist_off += per_f * F;
+        }
+        /* argmax, strict first-wins over (feature asc, border asc) (tree.rs:355-366).  The
+         * perturbed search at random_strength 0 picks the same candidate (instance = raw + 0)
+         * and consumes 1 gen_rand + one std_normal per listed feature on the main stream
+         * (tree.rs:1525-1611); the per-feature sub-streams never touch the main stream. */
+        int best_f = -1, best_b = -1;
+        double best = -INFINITY;
+        for (uint32_t f = 0; f < F; ++f)
+            for (uint32_t b = 0; b < n_borders[f]; ++b)
+                if (scores[f][b] > best) { best = scores[f][b]; best_f = (int)f; best_b = (int)b; }
+        if (prng) {
+            (void)orc_rng_gen(prng);
+            for (uint32_t f = 0; f < F; ++f) (void)orc_std_normal(prng);
+        }
+        if (best_f < 0) { rc = -1; break; }
+        out_splits[level * 2] = best_f;
+        out_splits[level * 2 + 1] = best_b;
+        if (out_scores) out_scores[level] = best;
+        const uint8_t* col = bins_fm + (size_t)best_f * n;
+        for (uint64_t o = 0; o < n; ++o)
+            if (col[o] > (uint32_t)best_b) leaf_of[o] += n_leaves; /* advance_leaf_only */
+    }
+    for (uint32_t f = 0; f < F; ++f) { free(hists[f]); free(scores[f]); }
+    free(hists);
+    free(scores);
+    return rc;
+}
+
+/* ======================================================================
+ * Boosting loop -- CPU branch of crates/cb-train/src/boosting.rs:7300-8900
+ * (Plain boosting, SymmetricTree, random_strength 0, pointwise losses).
+ * ==================================================================== */
+#define PRE_TREE_DRAWS 2        /* boosting.rs:59 */
+#define POST_TREE_EXTRA_DRAWS 2 /* boosting.rs:69 */
+
+int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
+              uint32_t F, const double* target, const double* weight, int32_t* out_splits,
+              double* out_leaf_values, double* out_approx, double* out_staged,
+              double* out_bias) {
+    const int K = p->loss == ORC_LOSS_MULTICLASS ? p->approx_dim : 1;
+    const int depth = p->depth;
+    const uint32_t n_leaves = 1u << depth;
+    const int pk = K * (K + 1) / 2;
+    double* w = (double*)malloc(sizeof(double) * n);
+    for (uint64_t i = 0; i < n; ++i) w[i] = weight ? weight[i] : 1.0;
+    double* approx = (double*)malloc(sizeof(double) * n * K);
+    double bias = 0.0; /* starting_approx (boosting.rs:1871-1877) */
+    if (p->boost_from_average && p->loss == ORC_LOSS_RMSE && n > 0) {
+        double s = 0.0;
+        for (uint64_t i = 0; i < n; ++i) s += target[i];
+        bias = s / (double)n;
+    }
+    for (uint64_t i = 0; i < n * K; ++i) approx[i] = bias;
+    if (out_bias) *out_bias = bias;
+
+    double sum_w = 0.0;
+    for (uint64_t i = 0; i < n; ++i) sum_w += w[i];
+    double scaled_l2 = n == 0 ? p->l2_leaf_reg : p->l2_leaf_reg * (sum_w / (double)n);
+
+    orc_rng rng;
+    orc_rng_from_seed(&rng, p->random_seed);
+    int draws_active = p->bootstrap_type != ORC_BOOT_NO;
+
+    double* d1 = (double*)malloc(sizeof(double) * n * K);
+    double* d2 = (double*)malloc(sizeof(double) * n * (p->loss == ORC_LOSS_MULTICLASS ? pk : 1));
+    double* wd = (double*)malloc(sizeof(double) * n * K);
+    double* sder = (double*)malloc(sizeof(double) * n * K);
+    double* swt = (double*)malloc(sizeof(double) * n);
+    double* samp = (double*)malloc(sizeof(double) * n);
+    uint8_t* ctrl = (uint8_t*)malloc(n);
+    uint32_t* leaf_of = (uint32_t*)malloc(sizeof(uint32_t) * n);
+    double* leaf_vals = (double*)malloc(sizeof(double) * n_leaves * K);
+    int rc = 0;
+
+    for (int it = 0; it < p->iterations; ++it) {
+        /* derivatives of the current approx */
+        if (p->loss == ORC_LOSS_MULTICLASS) {
+            double a[64], dd1[64], dd2[64 * 65 / 2];
+            for (uint64_t i = 0; i < n; ++i) {
+                for (int d = 0; d < K; ++d) a[d] = approx[(size_t)d * n + i];
+                softmax_ders(a, K, (int)target[i], dd1, dd2);
+                for (int d = 0; d < K; ++d) d1[(size_t)d * n + i] = dd1[d];
+                for (int j = 0; j < pk; ++j) d2[i * pk + j] = dd2[j];
+            }
+        } else {
+            orc_ders(p->loss, approx, target, n, d1, d2);
+        }
+        for (uint64_t x = 0; x < n * K; ++x) wd[x] = d1[x] * w[x % n];
+        if (draws_active)
+            for (int k = 0; k < PRE_TREE_DRAWS; ++k) (void)orc_rng_gen(&rng);
+        orc_bootstrap(p->bootstrap_type, n, p->subsample, p->bagging_temperature, &rng, samp, ctrl);
+        for (uint64_t x = 0; x < n * K; ++x) {
+            uint64_t i = x % n;
+            sder[x] = ctrl[i] ? wd[x] * samp[i] : 0.0;
+        }
+        for (uint64_t i = 0; i < n; ++i) swt[i] = ctrl[i] ? w[i] * samp[i] : 0.0;
+
+        int32_t* splits = out_splits + (size_t)it * depth * 2;
+        rc = orc_grow_tree(bins_fm, n_borders, n, F, sder, swt, K, depth, p->score_function,
+                           scaled_l2, draws_active ? &rng : NULL, p->n_threads, splits, NULL,
+                           leaf_of, NULL);
+        if (rc) break;
+
+        /* leaf values on the UNSAMPLED derivatives (boosting.rs:2470-2560, :2634) */
+        if (p->loss == ORC_LOSS_MULTICLASS) {
+            double* sd = (double*)calloc((size_t)n_leaves * K, sizeof(double));
+            double* s2 = (double*)calloc((size_t)n_leaves * pk, sizeof(double));
+            for (uint64_t i = 0; i < n; ++i) {
+                uint32_t l = leaf_of[i];
+                for (int d = 0; d < K; ++d) sd[(size_t)l * K + d] += wd[(size_t)d * n + i];
+                for (int j = 0; j < pk; ++j) s2[(size_t)l * pk + j] += d2[i * pk + j] * w[i];
+            }
+            for (uint32_t l = 0; l < n_leaves; ++l) {
+                double delta[64];
+                solve_symmetric_newton(K, sd + (size_t)l * K, s2 + (size_t)l * pk, scaled_l2, delta);
+                for (int d = 0; d < K; ++d) leaf_vals[(size_t)d * n_leaves + l] = delta[d];
+            }
+            free(sd);
+            free(s2);
+        } else {
+            double sd[1 << 12], s2[1 << 12];
+            for (uint32_t l = 0; l < n_leaves; ++l) { sd[l] = 0.0; s2[l] = 0.0; }
+            for (uint64_t i = 0; i < n; ++i) {
+                uint32_t l = leaf_of[i];
+                sd[l] += wd[i];
+                if (p->leaf_method == ORC_LEAF_NEWTON) s2[l] += d2[i] * w[i];
+                else s2[l] += w[i];
+            }
+            for (uint32_t l = 0; l < n_leaves; ++l)
+                leaf_vals[l] = p->leaf_method == ORC_LEAF_NEWTON
+                                   ? newton_leaf_delta(sd[l], s2[l], scaled_l2)
+                                   : calc_average(sd[l], s2[l], scaled_l2);
+        }
+        /* NormalizeLeafValues: non-pairwise losses only scale by the learning rate
+         * (boosting.rs:2844-2882); then approx += leaf value (boosting.rs:8560-8572) */
+        for (uint32_t x = 0; x < n_leaves * K; ++x) leaf_vals[x] *= p->learning_rate;
+        for (int d = 0; d < K; ++d)
+            for (uint64_t i = 0; i < n; ++i)
+                approx[(size_t)d * n + i] += leaf_vals[(size_t)d * n_leaves + leaf_of[i]];
+        if (out_leaf_values)
+            memcpy(out_leaf_values + (size_t)it * n_leaves * K, leaf_vals,
+                   sizeof(double) * n_leaves * K);
+        if (out_staged) memcpy(out_staged + (size_t)it * n * K, approx, sizeof(double) * n * K);
+        if (draws_active)
+            for (int k = 0; k < POST_TREE_EXTRA_DRAWS; ++k) (void)orc_rng_gen(&rng);
+    }
+    if (out_approx) memcpy(out_approx, approx, sizeof(double) * n * K);
+    free(w); free(approx); free(d1); free(d2); free(wd); free(sder); free(swt); free(samp);
+    free(ctrl); free(leaf_of); free(leaf_vals);
+    return rc;
+}

@@ -1,0 +1,118 @@
+/*
+ * cb_oracle.h -- CPU restatement of catboost_rs's oblivious-tree training path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * path and the CPU speed baseline in bench.py.  Only tests/, the smoke() entry
+ * of __graft_entry__.py and bench.py's cpu_baseline leg may load it; the
+ * product library (catboost_rs_amd) never links, loads or calls it.
+ *
+ * Every function restates the reference algorithm in the same arithmetic order
+ * (sequential f64 folds in object order, f32 where the reference uses f32).
+ * Citations are relative to the reference checkout (crates/...).
+ *
+ * Pinning (what proves each part, beyond retyping):
+ *   rng / std_normal      fast_ut.cpp known answers (cb-core/src/rng_test.rs)
+ *   fast_logf             1206 bit vectors in cb-train/tests/fixtures/fast_approx_ref.txt
+ *   grow_tree / leaves    bench/fixtures/expected_depth6_tree.json (numpy generator)
+ *                         + brute-force partition scoring on tiny inputs
+ *   bootstrap + boosting  upstream catboost 1.2.10 fixtures under
+ *                         crates/cb-oracle/fixtures/{bootstrap/{no,bayesian,bernoulli},regression_skeleton,
+ *                         binclf_skeleton} (splits, leaf values, staged approx)
+ *   multiclass            crates/cb-oracle/fixtures/multiclass_softmax
+ */
+#ifndef CB_ORACLE_H
+#define CB_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* TFastRng64 state: two PCG-XSH-RR streams (x = LCG state, c = odd addend). */
+typedef struct {
+    uint64_t x1, c1, x2, c2;
+    uint64_t calls;
+} orc_rng;
+
+enum { ORC_LOSS_RMSE = 0, ORC_LOSS_LOGLOSS = 1, ORC_LOSS_MULTICLASS = 2 };
+enum { ORC_SCORE_COSINE = 0, ORC_SCORE_L2 = 1 };
+enum { ORC_BOOT_NO = 0, ORC_BOOT_BAYESIAN = 1, ORC_BOOT_BERNOULLI = 2 };
+enum { ORC_LEAF_GRADIENT = 0, ORC_LEAF_NEWTON = 1 };
+
+typedef struct {
+    int32_t loss;            /* ORC_LOSS_* */
+    int32_t score_function;  /* ORC_SCORE_* */
+    int32_t bootstrap_type;  /* ORC_BOOT_* */
+    int32_t leaf_method;     /* ORC_LEAF_* */
+    int32_t depth;
+    int32_t iterations;
+    int32_t boost_from_average;
+    int32_t n_threads;       /* 0 = OpenMP default */
+    int32_t approx_dim;      /* 1 except MultiClass (class count) */
+    int32_t pad_;
+    double learning_rate;
+    double l2_leaf_reg;
+    double subsample;        /* Bernoulli rate */
+    float bagging_temperature;
+    float pad2_;
+    uint64_t random_seed;
+} orc_params;
+
+/* ---- RNG (cb-core/src/rng.rs, normal.rs) ---- */
+void orc_rng_new(orc_rng* r, uint64_t seed1, uint32_t seq1, uint64_t seed2, uint32_t seq2);
+void orc_rng_from_seed(orc_rng* r, uint64_t seed);
+uint64_t orc_rng_gen(orc_rng* r);
+void orc_rng_advance(orc_rng* r, uint64_t delta);
+double orc_rng_real1(orc_rng* r);
+uint64_t orc_rng_uniform(orc_rng* r, uint64_t bound);
+double orc_std_normal(orc_rng* r);
+float orc_fast_logf(float v);
+
+/* ---- bootstrap (cb-train/src/bootstrap.rs) ---- */
+int orc_bootstrap(int32_t type, uint64_t n, double subsample, float temperature, orc_rng* rng,
+                  double* sample_weight, uint8_t* control);
+
+/* ---- quantization (cb-compute/src/histogram.rs:563 bin_of) ---- */
+void orc_quantize(const float* values, uint64_t n, const double* borders, uint32_t n_borders,
+                  uint8_t* bins_out);
+
+/* ---- derivatives (cb-compute/src/loss.rs) ---- */
+void orc_ders(int32_t loss, const double* approx, const double* target, uint64_t n,
+              double* der1, double* der2);
+
+/* ---- one oblivious tree (cb-train/src/tree.rs:704 greedy_tensor_search_oblivious_perturbed)
+ *  bins_fm     feature-major u8 bins [F][n]
+ *  n_borders   per-feature border count (bins used: 0..n_borders[f])
+ *  score_der   dim-major score derivative channel [K][n] (already weight*sample masked)
+ *  score_w     score weight channel [n]
+ *  perturb_rng NULL -> plain search (no draws); else the draws of the perturbed search at
+ *              random_strength = 0 are consumed on it (std_dev 0 keeps scores exact)
+ *  out_splits  [depth][2] = (feature, bin_id)
+ *  out_scores  [depth] winning score per level
+ *  out_leaf_of [n]
+ *  out_hists   nullable; per level l, (2^l * F * n_bins * (K+1)) doubles, ch 0..K-1 der, K weight
+ * returns 0, or <0 on a degenerate level (no candidate). */
+int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n, uint32_t F,
+                  const double* score_der, const double* score_w, int32_t K, int32_t depth,
+                  int32_t score_function, double scaled_l2, orc_rng* perturb_rng, int32_t n_threads,
+                  int32_t* out_splits, double* out_scores, uint32_t* out_leaf_of,
+                  double* out_hists);
+
+/* Per-leaf ordered sums (cb-compute/src/histogram.rs:49 reduce_leaf_stats, :97 reduce_leaf_der2). */
+void orc_leaf_sums(const uint32_t* leaf_of, uint64_t n, uint32_t n_leaves, const double* der,
+                   const double* weight, double* sum_der, double* sum_w);
+
+/* ---- full boosting loop, CPU branch of cb-train/src/boosting.rs:7300-8900 ----
+ *  out_splits       [iterations][depth][2]
+ *  out_leaf_values  [iterations][2^depth * K]  learning-rate scaled (model leaf values)
+ *  out_approx       [K][n] final raw approx (nullable)
+ *  out_staged       [iterations][K][n] (nullable)
+ *  out_bias         starting approx (nullable) */
+int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
+              uint32_t F, const double* target, const double* weight, int32_t* out_splits,
+              double* out_leaf_values, double* out_approx, double* out_staged, double* out_bias);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

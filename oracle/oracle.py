@@ -1,0 +1,198 @@
+"""ctypes front-end of the CPU restatement in ``oracle/cb_oracle.c``.
+
+TEST INFRASTRUCTURE ONLY: the parity checker and the CPU baseline.  Only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
+import this module; the product package never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libcb_oracle.so")
+_lib = None
+
+LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2}
+SCORE = {"Cosine": 0, "L2": 1}
+BOOT = {"No": 0, "Bayesian": 1, "Bernoulli": 2}
+LEAF = {"Gradient": 0, "Newton": 1}
+
+
+class Rng(C.Structure):
+    _fields_ = [("x1", C.c_uint64), ("c1", C.c_uint64), ("x2", C.c_uint64),
+                ("c2", C.c_uint64), ("calls", C.c_uint64)]
+
+
+class Params(C.Structure):
+    _fields_ = [("loss", C.c_int32), ("score_function", C.c_int32),
+                ("bootstrap_type", C.c_int32), ("leaf_method", C.c_int32),
+                ("depth", C.c_int32), ("iterations", C.c_int32),
+                ("boost_from_average", C.c_int32), ("n_threads", C.c_int32),
+                ("approx_dim", C.c_int32), ("pad_", C.c_int32),
+                ("learning_rate", C.c_double), ("l2_leaf_reg", C.c_double),
+                ("subsample", C.c_double), ("bagging_temperature", C.c_float),
+                ("pad2_", C.c_float), ("random_seed", C.c_uint64)]
+
+
+def build(force: bool = False) -> str:
+    """Compile the restatement with its Makefile (gcc, OpenMP)."""
+    args = ["make", "-C", _HERE] + (["-B"] if force else [])
+    subprocess.run(args, check=True, stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = C.CDLL(_LIB_PATH)
+        P = C.c_void_p
+        L.orc_rng_new.argtypes = [C.POINTER(Rng), C.c_uint64, C.c_uint32, C.c_uint64, C.c_uint32]
+        L.orc_rng_from_seed.argtypes = [C.POINTER(Rng), C.c_uint64]
+        L.orc_rng_gen.argtypes = [C.POINTER(Rng)]
+        L.orc_rng_gen.restype = C.c_uint64
+        L.orc_rng_advance.argtypes = [C.POINTER(Rng), C.c_uint64]
+        L.orc_rng_real1.argtypes = [C.POINTER(Rng)]
+        L.orc_rng_real1.restype = C.c_double
+        L.orc_rng_uniform.argtypes = [C.POINTER(Rng), C.c_uint64]
+        L.orc_rng_uniform.restype = C.c_uint64
+        L.orc_std_normal.argtypes = [C.POINTER(Rng)]
+        L.orc_std_normal.restype = C.c_double
+        L.orc_fast_logf.argtypes = [C.c_float]
+        L.orc_fast_logf.restype = C.c_float
+        L.orc_bootstrap.argtypes = [C.c_int32, C.c_uint64, C.c_double, C.c_float, C.POINTER(Rng), P, P]
+        L.orc_bootstrap.restype = C.c_int
+        L.orc_quantize.argtypes = [P, C.c_uint64, P, C.c_uint32, P]
+        L.orc_ders.argtypes = [C.c_int32, P, P, C.c_uint64, P, P]
+        L.orc_grow_tree.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, C.c_int32, C.c_int32,
+                                    C.c_int32, C.c_double, C.POINTER(Rng), C.c_int32, P, P, P, P]
+        L.orc_grow_tree.restype = C.c_int
+        L.orc_leaf_sums.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P]
+        L.orc_train.argtypes = [C.POINTER(Params), P, P, C.c_uint64, C.c_uint32, P, P, P, P, P, P, P]
+        L.orc_train.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def rng_from_seed(seed: int) -> Rng:
+    r = Rng()
+    lib().orc_rng_from_seed(C.byref(r), C.c_uint64(seed & (2**64 - 1)))
+    return r
+
+
+def rng_new(seed1, seq1, seed2, seq2) -> Rng:
+    r = Rng()
+    lib().orc_rng_new(C.byref(r), seed1, seq1, seed2, seq2)
+    return r
+
+
+def fast_logf(v: float) -> float:
+    return lib().orc_fast_logf(v)
+
+
+def bootstrap(kind: str, n: int, subsample: float, temperature: float, rng: Rng):
+    sw = np.empty(n, np.float64)
+    ctrl = np.empty(n, np.uint8)
+    rc = lib().orc_bootstrap(BOOT[kind], n, subsample, temperature, C.byref(rng), _p(sw), _p(ctrl))
+    assert rc == 0
+    return sw, ctrl.astype(bool)
+
+
+def quantize(values: np.ndarray, borders: np.ndarray) -> np.ndarray:
+    v = np.ascontiguousarray(values, np.float32)
+    b = np.ascontiguousarray(borders, np.float64)
+    out = np.empty(v.shape[0], np.uint8)
+    lib().orc_quantize(_p(v), v.shape[0], _p(b), b.shape[0], _p(out))
+    return out
+
+
+def ders(loss: str, approx: np.ndarray, target: np.ndarray):
+    a = np.ascontiguousarray(approx, np.float64)
+    t = np.ascontiguousarray(target, np.float64)
+    d1 = np.empty_like(a)
+    d2 = np.empty_like(a)
+    lib().orc_ders(LOSS[loss], _p(a), _p(t), a.shape[0], _p(d1), _p(d2))
+    return d1, d2
+
+
+def grow_tree(bins_fm, n_borders, score_der, score_w, depth, score="Cosine", scaled_l2=3.0,
+              rng: Rng | None = None, want_hists=False, n_threads=0):
+    """One oblivious tree.  ``bins_fm`` is u8 [F, n]; ``score_der`` is [K, n] or [n]."""
+    bins_fm = np.ascontiguousarray(bins_fm, np.uint8)
+    F, n = bins_fm.shape
+    nb = np.ascontiguousarray(n_borders, np.uint32)
+    sd = np.ascontiguousarray(score_der, np.float64)
+    K = 1 if sd.ndim == 1 else sd.shape[0]
+    sw = np.ascontiguousarray(score_w, np.float64)
+    splits = np.zeros((depth, 2), np.int32)
+    scores = np.zeros(depth, np.float64)
+    leaf_of = np.zeros(n, np.uint32)
+    n_bins = int(nb.max()) + 1 if F else 1
+    hists = None
+    if want_hists:
+        total = sum((1 << l) * F * n_bins * (K + 1) for l in range(depth))
+        hists = np.zeros(total, np.float64)
+    rc = lib().orc_grow_tree(_p(bins_fm), _p(nb), n, F, _p(sd), _p(sw), K, depth, SCORE[score],
+                             scaled_l2, C.byref(rng) if rng is not None else None, n_threads,
+                             _p(splits), _p(scores), _p(leaf_of), _p(hists))
+    if rc != 0:
+        raise RuntimeError(f"orc_grow_tree failed rc={rc}")
+    out = {"splits": splits, "scores": scores, "leaf_of": leaf_of, "n_bins": n_bins}
+    if want_hists:
+        levels = []
+        off = 0
+        for l in range(depth):
+            sz = (1 << l) * F * n_bins * (K + 1)
+            levels.append(hists[off:off + sz].reshape(1 << l, F, n_bins, K + 1))
+            off += sz
+        out["hists"] = levels
+    return out
+
+
+def leaf_sums(leaf_of, n_leaves, der, weight=None):
+    lo = np.ascontiguousarray(leaf_of, np.uint32)
+    d = np.ascontiguousarray(der, np.float64)
+    w = None if weight is None else np.ascontiguousarray(weight, np.float64)
+    sd = np.zeros(n_leaves)
+    sw = np.zeros(n_leaves)
+    lib().orc_leaf_sums(_p(lo), lo.shape[0], n_leaves, _p(d), _p(w), _p(sd), _p(sw))
+    return sd, sw
+
+
+def train(bins_fm, n_borders, target, *, loss="RMSE", depth=6, iterations=10, learning_rate=0.1,
+          l2_leaf_reg=3.0, score="Cosine", bootstrap_type="No", subsample=0.66,
+          bagging_temperature=1.0, leaf_method="Gradient", boost_from_average=False,
+          random_seed=0, weight=None, approx_dim=1, n_threads=0, staged=False):
+    bins_fm = np.ascontiguousarray(bins_fm, np.uint8)
+    F, n = bins_fm.shape
+    nb = np.ascontiguousarray(n_borders, np.uint32)
+    t = np.ascontiguousarray(target, np.float64)
+    w = None if weight is None else np.ascontiguousarray(weight, np.float64)
+    K = approx_dim if loss == "MultiClass" else 1
+    p = Params(loss=LOSS[loss], score_function=SCORE[score], bootstrap_type=BOOT[bootstrap_type],
+               leaf_method=LEAF[leaf_method], depth=depth, iterations=iterations,
+               boost_from_average=int(boost_from_average), n_threads=n_threads, approx_dim=K,
+               learning_rate=learning_rate, l2_leaf_reg=l2_leaf_reg, subsample=subsample,
+               bagging_temperature=bagging_temperature, random_seed=random_seed)
+    splits = np.zeros((iterations, depth, 2), np.int32)
+    leaves = np.zeros((iterations, K, 1 << depth), np.float64)
+    approx = np.zeros((K, n), np.float64)
+    st = np.zeros((iterations, K, n), np.float64) if staged else None
+    bias = np.zeros(1, np.float64)
+    rc = lib().orc_train(C.byref(p), _p(bins_fm), _p(nb), n, F, _p(t), _p(w), _p(splits),
+                         _p(leaves), _p(approx), _p(st), _p(bias))
+    if rc != 0:
+        raise RuntimeError(f"orc_train failed rc={rc}")
+    out = {"splits": splits, "leaf_values": leaves, "approx": approx, "bias": float(bias[0])}
+    if staged:
+        out["staged"] = st
+    return out

@@ -1,0 +1,46 @@
+"""Loaders for the committed golden fixtures in tests/golden (data extracted from the
+reference's own test fixtures by tests/golden/make_golden.py)."""
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def upstream(name: str):
+    """One catboost 1.2.10 fit: inputs, used borders, expected trees and approximants."""
+    z = np.load(os.path.join(GOLDEN, f"upstream_{name}.npz"))
+    meta = json.load(open(os.path.join(GOLDEN, f"upstream_{name}.json")))
+    X, y = z["X"], z["y"].astype(np.float64)
+    nb = z["n_borders"]
+    offs = np.concatenate([[0], np.cumsum(nb)])
+    borders = [z["borders"][offs[i]:offs[i + 1]] for i in range(len(nb))]
+    if meta.get("label_definition"):  # "y_binary = (numeric_tiny.y > median(numeric_tiny.y))"
+        y = (y > np.median(y)).astype(np.float64)
+    if meta.get("target_rule"):  # "digitize(y, quantile(y,[1/3,2/3])) -> {0,1,2}"
+        y = np.digitize(y, np.quantile(y, [1 / 3, 2 / 3])).astype(np.float64)
+    return dict(X=X, y=y, borders=borders, n_borders=nb.astype(np.uint32),
+                split_feature=z["split_feature"], split_border=z["split_border"],
+                leaf_values=z["leaf_values"], staged=z["staged"], predictions=z["predictions"],
+                bias=z["bias"], meta=meta, params=meta["params"])
+
+
+def depth6():
+    cindex = np.load(os.path.join(GOLDEN, "depth6.npz"))["cindex"]
+    tree = json.load(open(os.path.join(GOLDEN, "depth6.json")))
+    return cindex, tree
+
+
+def rng_kat():
+    return json.load(open(os.path.join(GOLDEN, "rng_kat.json")))
+
+
+def fast_logf_rows():
+    rows = []
+    for line in open(os.path.join(GOLDEN, "fast_logf.txt")):
+        _, a, b = line.split()
+        rows.append((int(a, 16), int(b, 16)))
+    return rows
