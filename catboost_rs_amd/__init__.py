@@ -1,0 +1,327 @@
+"""MI355X (gfx950) oblivious-tree training path of catboost_rs, behind its compute seam.
+
+The product is the shared library ``libcbhip.so`` (HIP kernels + C-ABI, ``include/cbhip.h``)
+and the host mirror of cb-train's device branch (``include/cbtrain.h``).  This module is a
+thin ctypes front-end used by the tests and ``bench.py``:
+
+* :class:`HipBackend` mirrors ``trait cb_compute::Runtime``'s device-training methods
+  (crates/cb-compute/src/runtime.rs:1431-1651): ``compute_gradients``,
+  ``begin_device_training``, ``grow_tree_on_device``, ``end_device_training``.
+* :class:`Trainer` drives the boosting loop exactly like cb-train's device branch
+  (crates/cb-train/src/boosting.rs:6532-7300) through ``cbt_*``.
+
+There is no CPU fallback: if the library is missing or no GPU is present, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libcbhip.so")
+
+LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2, "CrossEntropy": 3}
+SCORE = {"Cosine": 0, "L2": 1}
+LEAF = {"Gradient": 0, "Newton": 1, "Simple": 2}
+BOOT = {"No": 0, "Bayesian": 1, "Bernoulli": 2}
+
+OK, DECLINED = 0, 1
+ERRORS = {-1: "LengthMismatch", -2: "OutOfRange", -3: "Degenerate", -4: "Unsupported",
+          -5: "InvalidArgument", -6: "Device"}
+
+
+class CbhError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{ERRORS.get(code, code)}: {msg}")
+        self.code = code
+
+
+class Config(C.Structure):
+    _fields_ = [("loss", C.c_int32), ("score_function", C.c_int32), ("leaf_method", C.c_int32),
+                ("depth", C.c_int32), ("boosting_type_is_plain", C.c_int32),
+                ("fold_count", C.c_int32), ("approx_dim", C.c_int32),
+                ("bootstrap_type", C.c_int32), ("sample_from_host", C.c_int32),
+                ("sample_rate", C.c_float), ("bagging_temperature", C.c_float),
+                ("profile", C.c_int32), ("bias", C.c_double), ("rng_seed", C.c_uint64),
+                ("one_hot_flags", C.c_void_p), ("real_folds", C.c_void_p)]
+
+
+class TreeSampling(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("bagging_temperature", C.c_float), ("subsample", C.c_double),
+                ("bayesian_seed", C.c_uint64), ("bernoulli_state", C.c_uint64 * 4)]
+
+
+class TreeOut(C.Structure):
+    _fields_ = [("split_feature", C.c_void_p), ("split_bin", C.c_void_p),
+                ("split_one_hot", C.c_void_p), ("leaf_values", C.c_void_p),
+                ("leaf_of", C.c_void_p), ("split_score", C.c_void_p)]
+
+
+class Stats(C.Structure):
+    _fields_ = [("fill_ms", C.c_double), ("derive_ms", C.c_double), ("score_ms", C.c_double),
+                ("partition_ms", C.c_double), ("leaf_ms", C.c_double), ("prepare_ms", C.c_double),
+                ("total_ms", C.c_double), ("fill_launches", C.c_uint64), ("fill_rows", C.c_uint64),
+                ("fill_row_features", C.c_uint64), ("fill_bytes", C.c_double), ("trees", C.c_uint64)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class TrainParams(C.Structure):
+    _fields_ = [("loss", C.c_int32), ("score_function", C.c_int32), ("leaf_method", C.c_int32),
+                ("depth", C.c_int32), ("bootstrap_type", C.c_int32),
+                ("boost_from_average", C.c_int32), ("approx_dim", C.c_int32), ("profile", C.c_int32),
+                ("learning_rate", C.c_double), ("l2_leaf_reg", C.c_double), ("subsample", C.c_double),
+                ("bagging_temperature", C.c_float), ("pad_", C.c_float), ("random_seed", C.c_uint64)]
+
+
+# Every symbol include/cbhip.h and include/cbtrain.h declare (the ABI test checks them).
+EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
+           "cbh_session_read_approx", "cbh_session_stats", "cbh_session_reset_stats",
+           "cbh_session_end", "cbh_compute_gradients", "cbh_hist_build", "cbh_bootstrap",
+           "cbh_version", "cbh_last_error", "cbt_open", "cbt_step", "cbt_read_approx", "cbt_stats",
+           "cbt_reset_stats", "cbt_bias", "cbt_close"]
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Load libcbhip.so; raises if it was not built (there is no fallback path)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is missing: run `python -m catboost_rs_amd.build`")
+    L = C.CDLL(path)
+    P = C.c_void_p
+    L.cbh_last_error.restype = C.c_char_p
+    L.cbh_version.restype = C.c_char_p
+    L.cbh_session_begin.argtypes = [C.POINTER(Config), P, P, C.c_uint64, C.c_uint32, C.c_uint32,
+                                    C.c_double, C.c_double, C.POINTER(P)]
+    L.cbh_session_begin_u8.argtypes = L.cbh_session_begin.argtypes
+    L.cbh_session_grow.argtypes = [P, P, P, C.c_uint64, P, C.c_uint64, C.POINTER(TreeSampling),
+                                   C.POINTER(TreeOut)]
+    L.cbh_session_read_approx.argtypes = [P, P, C.c_uint64]
+    L.cbh_session_stats.argtypes = [P, C.POINTER(Stats)]
+    L.cbh_session_reset_stats.argtypes = [P]
+    L.cbh_session_reset_stats.restype = None
+    L.cbh_session_end.argtypes = [P]
+    L.cbh_compute_gradients.argtypes = [C.c_int32, P, P, C.c_uint64, C.c_uint32, P, P]
+    L.cbh_hist_build.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, C.c_uint32, P,
+                                 C.c_uint32, P]
+    L.cbh_bootstrap.argtypes = [C.POINTER(TreeSampling), C.c_uint64, P, P]
+    L.cbt_open.argtypes = [C.POINTER(TrainParams), P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, P,
+                           P, C.POINTER(P)]
+    L.cbt_step.argtypes = [P, P, P, P, P]
+    L.cbt_read_approx.argtypes = [P, P]
+    L.cbt_stats.argtypes = [P, C.POINTER(Stats)]
+    L.cbt_reset_stats.argtypes = [P]
+    L.cbt_reset_stats.restype = None
+    L.cbt_bias.argtypes = [P]
+    L.cbt_bias.restype = C.c_double
+    L.cbt_close.argtypes = [P]
+    L.cbt_close.restype = None
+    _lib = L
+    return L
+
+
+def _check(rc: int):
+    if rc != OK:
+        raise CbhError(rc, load().cbh_last_error().decode())
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------------------------------
+# kernel-level entry points
+# ---------------------------------------------------------------------------------------
+def compute_gradients(loss: str, approx: np.ndarray, target: np.ndarray, approx_dim: int = 1):
+    """Runtime::compute_gradients (runtime.rs:1431): dim-major der1/der2 on the GPU."""
+    a = np.ascontiguousarray(approx, np.float64).reshape(-1)
+    t = np.ascontiguousarray(target, np.float64)
+    n = t.shape[0]
+    d1 = np.empty(n * approx_dim)
+    pk = approx_dim * (approx_dim + 1) // 2 if loss == "MultiClass" else 1
+    d2 = np.empty(n * pk)
+    _check(load().cbh_compute_gradients(LOSS[loss], _ptr(a), _ptr(t), n, approx_dim, _ptr(d1), _ptr(d2)))
+    return d1, d2
+
+
+def hist_build(bins_fm, n_bins, der, w, slot_of_row=None, n_slots=1):
+    """One histogram fill on the GPU; exact sums returned as f64 [slot][F][bin][K+1]."""
+    bins_fm = np.ascontiguousarray(bins_fm, np.uint8)
+    F, n = bins_fm.shape
+    der = np.ascontiguousarray(der, np.float64)
+    K = 1 if der.ndim == 1 else der.shape[0]
+    w = np.ascontiguousarray(w, np.float64)
+    slot = None if slot_of_row is None else np.ascontiguousarray(slot_of_row, np.uint32)
+    out = np.empty((n_slots, F, n_bins, K + 1), np.float64)
+    _check(load().cbh_hist_build(_ptr(bins_fm), n, F, n_bins, _ptr(der), _ptr(w), K, _ptr(slot),
+                                 n_slots, _ptr(out)))
+    return out
+
+
+def bootstrap(kind: str, n: int, *, bayesian_seed=0, bernoulli_state=(0, 1, 0, 1), subsample=1.0,
+              temperature=1.0):
+    s = TreeSampling(kind=BOOT[kind], bagging_temperature=temperature, subsample=subsample,
+                     bayesian_seed=bayesian_seed)
+    for i, v in enumerate(bernoulli_state):
+        s.bernoulli_state[i] = v
+    sw = np.empty(n)
+    ctrl = np.empty(n, np.uint8)
+    _check(load().cbh_bootstrap(C.byref(s), n, _ptr(sw), _ptr(ctrl)))
+    return sw, ctrl.astype(bool)
+
+
+# ---------------------------------------------------------------------------------------
+# The Runtime seam (begin / grow / end)
+# ---------------------------------------------------------------------------------------
+class HipBackend:
+    """Mirror of ``GpuBackend: Runtime`` (crates/cb-backend/src/gpu_backend.rs:196-425)."""
+
+    def __init__(self):
+        self._s = C.c_void_p()
+        self.n = 0
+        self.depth = 0
+        self.K = 1
+
+    def compute_gradients(self, loss, approx, target, approx_dimension=1):
+        return compute_gradients(loss, approx, target, approx_dimension)
+
+    def begin_device_training(self, loss, depth, boosting_type_is_plain, fold_count, score_function,
+                              bins_feature_major, weight, n, n_features, n_bins, learning_rate,
+                              scaled_l2, *, approx_dim=1, bias=0.0, leaf_method="Gradient",
+                              bootstrap_type="No", sample_from_host=False, profile=False,
+                              one_hot_flags=None, real_folds=None) -> bool:
+        """Returns True when the session opened, False when the config is declined."""
+        self._keep = []
+        oh = None if one_hot_flags is None else np.ascontiguousarray(one_hot_flags, np.uint8)
+        rf = None if real_folds is None else np.ascontiguousarray(real_folds, np.uint32)
+        self._keep += [oh, rf]
+        cfg = Config(loss=LOSS[loss], score_function=SCORE[score_function], leaf_method=LEAF[leaf_method],
+                     depth=depth, boosting_type_is_plain=int(boosting_type_is_plain),
+                     fold_count=fold_count, approx_dim=approx_dim, bootstrap_type=BOOT[bootstrap_type],
+                     sample_from_host=int(sample_from_host), profile=int(profile), bias=bias,
+                     one_hot_flags=_ptr(oh), real_folds=_ptr(rf))
+        bins = np.ascontiguousarray(bins_feature_major)
+        w = None if weight is None else np.ascontiguousarray(weight, np.float64)
+        fn = load().cbh_session_begin_u8 if bins.dtype == np.uint8 else load().cbh_session_begin
+        if bins.dtype not in (np.uint8, np.uint32):
+            bins = bins.astype(np.uint32)
+        rc = fn(C.byref(cfg), _ptr(bins), _ptr(w), n, n_features, n_bins, learning_rate, scaled_l2,
+                C.byref(self._s))
+        if rc == DECLINED:
+            return False
+        _check(rc)
+        self.n, self.depth, self.K = n, depth, approx_dim
+        return True
+
+    def grow_tree_on_device(self, approx=None, target=None, sample=None, sampling=None,
+                            want_leaf_of=False):
+        d = self.depth
+        sf = np.zeros(d, np.uint32)
+        sb = np.zeros(d, np.uint32)
+        so = np.zeros(d, np.uint8)
+        sc = np.zeros(d, np.float64)
+        lv = np.zeros((1 << d) * self.K, np.float64)
+        lo = np.zeros(self.n, np.uint32) if want_leaf_of else None
+        out = TreeOut(_ptr(sf), _ptr(sb), _ptr(so), _ptr(lv), _ptr(lo), _ptr(sc))
+        a = None if approx is None else np.ascontiguousarray(approx, np.float64)
+        t = None if target is None else np.ascontiguousarray(target, np.float64)
+        s = None if sample is None else np.ascontiguousarray(sample, np.float64)
+        _check(load().cbh_session_grow(self._s, _ptr(a), _ptr(t), self.n, _ptr(s),
+                                       0 if s is None else s.shape[0],
+                                       None if sampling is None else C.byref(sampling), C.byref(out)))
+        return {"splits": [(int(f), int(b), bool(o)) for f, b, o in zip(sf, sb, so)],
+                "leaf_values": lv.reshape(1 << d, self.K), "leaf_of": lo, "scores": sc}
+
+    def read_approx(self):
+        a = np.zeros(self.n * self.K)
+        _check(load().cbh_session_read_approx(self._s, _ptr(a), a.shape[0]))
+        return a.reshape(self.K, self.n)
+
+    def stats(self):
+        st = Stats()
+        _check(load().cbh_session_stats(self._s, C.byref(st)))
+        return st.as_dict()
+
+    def end_device_training(self):
+        if self._s:
+            _check(load().cbh_session_end(self._s))
+        self._s = C.c_void_p()
+
+
+class Trainer:
+    """cb-train's device branch over the C-ABI (host RNG phase, draw replay)."""
+
+    def __init__(self, bins_fm, n_bins, target, *, loss="RMSE", depth=6, learning_rate=0.1,
+                 l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient", bootstrap_type="No",
+                 subsample=0.66, bagging_temperature=1.0, boost_from_average=False, random_seed=0,
+                 weight=None, approx_dim=1, profile=False, real_folds=None, one_hot_flags=None):
+        self.bins = np.ascontiguousarray(bins_fm, np.uint8)
+        F, n = self.bins.shape
+        self.n, self.F, self.depth = n, F, depth
+        self.K = approx_dim if loss == "MultiClass" else 1
+        p = TrainParams(loss=LOSS[loss], score_function=SCORE[score], leaf_method=LEAF[leaf_method],
+                        depth=depth, bootstrap_type=BOOT[bootstrap_type],
+                        boost_from_average=int(boost_from_average), approx_dim=self.K,
+                        profile=int(profile), learning_rate=learning_rate, l2_leaf_reg=l2_leaf_reg,
+                        subsample=subsample, bagging_temperature=bagging_temperature,
+                        random_seed=random_seed)
+        t = np.ascontiguousarray(target, np.float64)
+        w = None if weight is None else np.ascontiguousarray(weight, np.float64)
+        rf = None if real_folds is None else np.ascontiguousarray(real_folds, np.uint32)
+        oh = None if one_hot_flags is None else np.ascontiguousarray(one_hot_flags, np.uint8)
+        self._keep = (t, w, rf, oh)
+        self._h = C.c_void_p()
+        _check(load().cbt_open(C.byref(p), _ptr(self.bins), n, F, n_bins, _ptr(rf), _ptr(oh), _ptr(t),
+                               _ptr(w), C.byref(self._h)))
+
+    def step(self):
+        d = self.depth
+        sf = np.zeros(d, np.uint32)
+        sb = np.zeros(d, np.uint32)
+        so = np.zeros(d, np.uint8)
+        lv = np.zeros((self.K, 1 << d), np.float64)
+        _check(load().cbt_step(self._h, _ptr(sf), _ptr(sb), _ptr(so), _ptr(lv)))
+        return np.stack([sf, sb], 1).astype(np.int32), lv, so
+
+    def fit(self, iterations):
+        splits, leaves = [], []
+        for _ in range(iterations):
+            s, lv, _ = self.step()
+            splits.append(s)
+            leaves.append(lv)
+        return np.array(splits), np.array(leaves)
+
+    def approx(self):
+        a = np.zeros(self.n * self.K)
+        _check(load().cbt_read_approx(self._h, _ptr(a)))
+        return a.reshape(self.K, self.n)
+
+    @property
+    def bias(self):
+        return load().cbt_bias(self._h)
+
+    def stats(self):
+        st = Stats()
+        _check(load().cbt_stats(self._h, C.byref(st)))
+        return st.as_dict()
+
+    def reset_stats(self):
+        load().cbt_reset_stats(self._h)
+
+    def close(self):
+        if self._h:
+            load().cbt_close(self._h)
+        self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,176 @@
+// Host mirror of cb-train's device branch (crates/cb-train/src/boosting.rs:6532-7300),
+// written against the public C-ABI only.  It owns the persistent training RNG: the
+// device never draws on the main stream, it receives the per-tree sampling phase
+// (Bayesian seed / Bernoulli raw state) and the host advances its stream exactly as the
+// CPU branch would, including the per-level draws of the perturbed level search that the
+// device path does not run (crates/cb-train/src/device_draw_replay.rs).
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/cbhip.h"
+#include "../../include/cbtrain.h"
+#include "common.hpp"
+
+namespace {
+
+constexpr int kPreTreeDraws = 2;        // boosting.rs:59
+constexpr int kPostTreeExtraDraws = 2;  // boosting.rs:69
+
+// StdNormalDistribution, Marsaglia polar (crates/cb-core/src/normal.rs:50-64).
+double std_normal(cbh::Rng& r) {
+    for (;;) {
+        const double x = cbh::rng_real1(r) * 2.0 - 1.0;
+        const double y = cbh::rng_real1(r) * 2.0 - 1.0;
+        const double rr = x * x + y * y;
+        if (!(rr > 1.0 || rr <= 0.0)) return x * std::sqrt(-2.0 * std::log(rr) / rr);
+    }
+}
+
+}  // namespace
+
+struct cbt_trainer {
+    cbt_params p{};
+    cbh_session* s = nullptr;
+    uint64_t n = 0;
+    uint32_t F = 0, K = 1;
+    cbh::Rng rng{};
+    bool draws_active = false;
+    bool first = true;
+    std::vector<double> target;
+    double bias = 0.0;
+    std::vector<uint32_t> sf, sb;
+    std::vector<uint8_t> so;
+    std::vector<double> leaves;
+    ~cbt_trainer() {
+        if (s) cbh_session_end(s);
+    }
+};
+
+extern "C" {
+
+int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t n_bins,
+             const uint32_t* real_folds, const uint8_t* one_hot_flags, const double* target,
+             const double* weight, cbt_trainer** out) {
+    if (!p || !bins_fm || !target || !out) return CBH_ERR_INVALID_ARG;
+    *out = nullptr;
+    std::unique_ptr<cbt_trainer> t(new cbt_trainer());
+    t->p = *p;
+    t->n = n;
+    t->F = F;
+    t->K = p->loss == CBH_LOSS_MULTICLASS ? (uint32_t)p->approx_dim : 1u;
+    t->target.assign(target, target + n);
+    // starting approx: RMSE + boost_from_average -> mean target (boosting.rs:1871-1877)
+    if (p->boost_from_average && p->loss == CBH_LOSS_RMSE && n > 0) {
+        double s = 0.0;
+        for (uint64_t i = 0; i < n; ++i) s += target[i];
+        t->bias = s / (double)n;
+    }
+    double sum_w = 0.0;
+    for (uint64_t i = 0; i < n; ++i) sum_w += weight ? weight[i] : 1.0;
+    const double scaled_l2 = p->l2_leaf_reg * (sum_w / (double)n);  // scale_l2_reg
+    cbh_config cfg{};
+    cfg.loss = p->loss;
+    cfg.score_function = p->score_function;
+    cfg.leaf_method = p->leaf_method;
+    cfg.depth = p->depth;
+    cfg.boosting_type_is_plain = 1;
+    cfg.fold_count = 1;
+    cfg.approx_dim = (int32_t)t->K;
+    cfg.bootstrap_type = p->bootstrap_type;
+    cfg.sample_from_host = 0;
+    cfg.sample_rate = (float)p->subsample;
+    cfg.bagging_temperature = p->bagging_temperature;
+    cfg.profile = p->profile;
+    cfg.bias = t->bias;
+    cfg.rng_seed = p->random_seed;
+    cfg.one_hot_flags = one_hot_flags;
+    cfg.real_folds = real_folds;
+    int rc = cbh_session_begin_u8(&cfg, bins_fm, weight, n, F, n_bins, p->learning_rate, scaled_l2, &t->s);
+    if (rc != CBH_OK) return rc;
+    t->rng = cbh::rng_from_seed(p->random_seed);
+    t->draws_active = p->bootstrap_type != CBH_BOOT_NO;
+    t->sf.resize(p->depth);
+    t->sb.resize(p->depth);
+    t->so.resize(p->depth);
+    t->leaves.resize(((size_t)1 << p->depth) * t->K);
+    *out = t.release();
+    return CBH_OK;
+}
+
+int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8_t* split_one_hot,
+             double* leaf_values) {
+    if (!t) return CBH_ERR_INVALID_ARG;
+    const cbt_params& p = t->p;
+    // 1a. pre-bootstrap draws (train.cpp:208,211)
+    if (t->draws_active)
+        for (int k = 0; k < kPreTreeDraws; ++k) (void)cbh::rng_gen(t->rng);
+    // 1b. bootstrap phase on the main stream (bootstrap.rs:402-466)
+    cbh_tree_sampling smp{};
+    smp.kind = CBH_BOOT_NO;
+    if (p.bootstrap_type == CBH_BOOT_BAYESIAN && p.bagging_temperature != 0.0f) {
+        smp.kind = CBH_BOOT_BAYESIAN;
+        smp.bagging_temperature = p.bagging_temperature;
+        smp.bayesian_seed = cbh::rng_gen(t->rng);
+    } else if (p.bootstrap_type == CBH_BOOT_BERNOULLI && p.subsample < 1.0) {
+        smp.kind = CBH_BOOT_BERNOULLI;
+        smp.subsample = p.subsample;
+        smp.bernoulli_state[0] = t->rng.x1;
+        smp.bernoulli_state[1] = t->rng.c1;
+        smp.bernoulli_state[2] = t->rng.x2;
+        smp.bernoulli_state[3] = t->rng.c2;
+        cbh::rng_advance(t->rng, t->n);  // the n sequential real1 draws
+    }
+    // 2. grow on the device
+    cbh_tree_out out{};
+    out.split_feature = t->sf.data();
+    out.split_bin = t->sb.data();
+    out.split_one_hot = t->so.data();
+    out.leaf_values = t->leaves.data();
+    int rc = cbh_session_grow(t->s, nullptr, t->first ? t->target.data() : nullptr, t->n, nullptr, 0,
+                              &smp, &out);
+    if (rc != CBH_OK) return rc;
+    t->first = false;
+    // 3. replay the CPU grower's per-level draws, then the post-tree draws
+    if (t->draws_active) {
+        for (int level = 0; level < p.depth; ++level) {
+            for (uint32_t f = 0; f < t->F; ++f) (void)cbh::rng_real1(t->rng);
+            (void)cbh::rng_gen(t->rng);
+            for (uint32_t f = 0; f < t->F; ++f) (void)std_normal(t->rng);
+        }
+        for (int k = 0; k < kPostTreeExtraDraws; ++k) (void)cbh::rng_gen(t->rng);
+    }
+    if (split_feature) std::memcpy(split_feature, t->sf.data(), sizeof(uint32_t) * p.depth);
+    if (split_bin) std::memcpy(split_bin, t->sb.data(), sizeof(uint32_t) * p.depth);
+    if (split_one_hot) std::memcpy(split_one_hot, t->so.data(), p.depth);
+    if (leaf_values) {
+        // model leaves: dim-major [K][leaves], scaled by the learning rate
+        const size_t L = (size_t)1 << p.depth;
+        for (size_t l = 0; l < L; ++l)
+            for (uint32_t d = 0; d < t->K; ++d)
+                leaf_values[(size_t)d * L + l] = t->leaves[l * t->K + d] * p.learning_rate;
+    }
+    return CBH_OK;
+}
+
+int cbt_read_approx(cbt_trainer* t, double* approx_out) {
+    if (!t || !approx_out) return CBH_ERR_INVALID_ARG;
+    return cbh_session_read_approx(t->s, approx_out, t->n * t->K);
+}
+
+int cbt_stats(const cbt_trainer* t, cbh_stats* out) {
+    if (!t) return CBH_ERR_INVALID_ARG;
+    return cbh_session_stats(t->s, out);
+}
+
+void cbt_reset_stats(cbt_trainer* t) {
+    if (t) cbh_session_reset_stats(t->s);
+}
+
+double cbt_bias(const cbt_trainer* t) { return t ? t->bias : 0.0; }
+
+void cbt_close(cbt_trainer* t) { delete t; }
+
+}  // extern "C"

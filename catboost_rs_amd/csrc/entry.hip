@@ -1,0 +1,292 @@
+// Stand-alone C-ABI entry points: compute_gradients and the kernel-level entry points
+// that run one kernel of the training path on host buffers (used to check each kernel
+// alone against the CPU restatement).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/cbhip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+using namespace cbh;
+
+int cbh_internal_fail(int code, const std::string& msg);  // session.hip
+
+namespace {
+
+int fail2(int code, const std::string& msg);
+
+#define HIP_OK(expr)                                                                        \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) return fail2(CBH_ERR_DEVICE, std::string(#expr ": ") + hipGetErrorString(e_)); \
+    } while (0)
+
+// RAII device buffer
+template <typename T>
+struct DBuf {
+    T* p = nullptr;
+    size_t n = 0;
+    ~DBuf() {
+        if (p) (void)hipFree(p);
+    }
+    hipError_t alloc(size_t count) {
+        n = count;
+        return hipMalloc((void**)&p, std::max<size_t>(count, 1) * sizeof(T));
+    }
+};
+
+__global__ void ders_kernel(int loss, const double* __restrict__ a, const double* __restrict__ t,
+                            uint64_t n, double* __restrict__ d1, double* __restrict__ d2) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        double g, h;
+        scalar_ders(loss, a[i], t[i], g, h);
+        d1[i] = g;
+        d2[i] = h;
+    }
+}
+
+template <int K>
+__global__ void softmax_ders_kernel(const double* __restrict__ a, const double* __restrict__ t,
+                                    uint64_t n, double* __restrict__ d1, double* __restrict__ d2) {
+    constexpr int PK = K * (K + 1) / 2;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        double x[K], p[K];
+        for (int d = 0; d < K; ++d) x[d] = a[(size_t)d * n + i];
+        softmax_probs<K>(x, p);
+        int j = 0;
+        for (int y = 0; y < K; ++y) {
+            d2[i * PK + j++] = p[y] * (p[y] - 1.0);
+            for (int z = y + 1; z < K; ++z) d2[i * PK + j++] = p[y] * p[z];
+        }
+        const int tc = (int)t[i];
+        for (int d = 0; d < K; ++d) d1[(size_t)d * n + i] = (d == tc ? 1.0 : 0.0) - p[d];
+    }
+}
+
+__global__ void bootstrap_kernel(SampleParams smp, uint64_t n, double* __restrict__ sw,
+                                 uint8_t* __restrict__ ctrl) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        double s = 1.0;
+        bool c = true;
+        if (smp.kind == 1) {
+            Rng r = rng_from_seed(smp.bayes_seed + i / 1000);
+            rng_advance(r, 10 + i % 1000);
+            const double u = rng_real1(r);
+            const float bw = -fast_logf((float)u + 0.0f);
+            s = smp.temperature == 1.0f ? (double)bw : (double)powf(bw, smp.temperature);
+        } else if (smp.kind == 2) {
+            Rng r = smp.bern;
+            rng_advance(r, i);
+            c = rng_real1(r) < smp.rate;
+        }
+        sw[i] = s;
+        ctrl[i] = c ? 1 : 0;
+    }
+}
+
+__global__ void pack_stats_kernel(const double* __restrict__ der, const double* __restrict__ w,
+                                  uint64_t n, uint32_t K, double* __restrict__ sstat) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        for (uint32_t d = 0; d < K; ++d) sstat[i * (K + 1) + d] = der[(size_t)d * n + i];
+        sstat[i * (K + 1) + K] = w[i];
+    }
+}
+
+unsigned grid_of(uint64_t work, unsigned block) {
+    uint64_t g = (work + block - 1) / block;
+    return (unsigned)std::max<uint64_t>(1, std::min<uint64_t>(g, 65535u * 4));
+}
+
+int fail2(int code, const std::string& msg) { return cbh_internal_fail(code, msg); }
+
+template <int C>
+int run_fill(const uint32_t* rows, uint32_t W, uint64_t n, const uint32_t* idx, const Chunk* chunks,
+             const LevelPlan* plan, uint32_t dense_chunks, const double* sstat, const Scales* sc,
+             const uint32_t* tile_w0, uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t slots,
+             size_t lds, long long* hist) {
+    HIP_OK(hipFuncSetAttribute((const void*)fill_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    fill_kernel<C><<<slots * n_tiles, 1024, lds, 0>>>(rows, W, n, idx, chunks, plan, 8192, dense_chunks,
+                                                      sstat, sc, tile_w0, n_tiles, F, B, slots, hist);
+    HIP_OK(hipGetLastError());
+    return CBH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cbh_compute_gradients(int32_t loss, const double* approx, const double* target, uint64_t n,
+                          uint32_t approx_dim, double* der1, double* der2) {
+    if (!approx || !target || !der1 || !der2) return fail2(CBH_ERR_INVALID_ARG, "null argument");
+    const uint32_t K = approx_dim;
+    if (loss == CBH_LOSS_MULTICLASS ? (K < 2 || K > 16) : K != 1)
+        return fail2(CBH_ERR_UNSUPPORTED, "approx_dim not covered");
+    const size_t pk = loss == CBH_LOSS_MULTICLASS ? (size_t)K * (K + 1) / 2 : 1;
+    DBuf<double> a, t, d1, d2;
+    HIP_OK(a.alloc(n * K));
+    HIP_OK(t.alloc(n));
+    HIP_OK(d1.alloc(n * K));
+    HIP_OK(d2.alloc(n * (loss == CBH_LOSS_MULTICLASS ? pk : 1)));
+    HIP_OK(hipMemcpy(a.p, approx, sizeof(double) * n * K, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(t.p, target, sizeof(double) * n, hipMemcpyHostToDevice));
+    if (loss == CBH_LOSS_MULTICLASS) {
+        switch (K) {
+#define CASE(k) case k: softmax_ders_kernel<k><<<grid_of(n, 256), 256>>>(a.p, t.p, n, d1.p, d2.p); break;
+            CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(10) CASE(12) CASE(16)
+#undef CASE
+            default: return fail2(CBH_ERR_UNSUPPORTED, "approx_dim has no compiled variant");
+        }
+    } else {
+        ders_kernel<<<grid_of(n, 256), 256>>>(loss == CBH_LOSS_RMSE ? 0 : 1, a.p, t.p, n, d1.p, d2.p);
+    }
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipMemcpy(der1, d1.p, sizeof(double) * n * K, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(der2, d2.p, sizeof(double) * n * (loss == CBH_LOSS_MULTICLASS ? pk : 1),
+                     hipMemcpyDeviceToHost));
+    return CBH_OK;
+}
+
+int cbh_bootstrap(const cbh_tree_sampling* sampling, uint64_t n, double* sample_weight, uint8_t* control) {
+    if (!sampling || !sample_weight || !control) return fail2(CBH_ERR_INVALID_ARG, "null argument");
+    SampleParams smp{};
+    smp.kind = sampling->kind;
+    smp.temperature = sampling->bagging_temperature;
+    smp.rate = (double)(float)sampling->subsample;
+    smp.bayes_seed = sampling->bayesian_seed;
+    smp.bern = Rng{sampling->bernoulli_state[0], sampling->bernoulli_state[1],
+                   sampling->bernoulli_state[2], sampling->bernoulli_state[3]};
+    if (smp.kind == CBH_BOOT_BERNOULLI && sampling->subsample >= 1.0) smp.kind = 0;
+    if (smp.kind == CBH_BOOT_BAYESIAN && sampling->bagging_temperature == 0.0f) smp.kind = 0;
+    DBuf<double> sw;
+    DBuf<uint8_t> c;
+    HIP_OK(sw.alloc(n));
+    HIP_OK(c.alloc(n));
+    bootstrap_kernel<<<grid_of(n, 256), 256>>>(smp, n, sw.p, c.p);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipMemcpy(sample_weight, sw.p, sizeof(double) * n, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(control, c.p, n, hipMemcpyDeviceToHost));
+    return CBH_OK;
+}
+
+int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t B, const double* der,
+                   const double* w, uint32_t K, const uint32_t* slot_of_row, uint32_t n_slots,
+                   double* hist_out) {
+    if (!bins_fm || !der || !w || !hist_out) return fail2(CBH_ERR_INVALID_ARG, "null argument");
+    if (K < 1 || K > 16 || B < 1 || B > 256 || n == 0 || F == 0 || n_slots == 0)
+        return fail2(CBH_ERR_INVALID_ARG, "bad shape");
+    for (uint64_t i = 0; i < n * F; ++i)
+        if (bins_fm[i] >= B) return fail2(CBH_ERR_OUT_OF_RANGE, "bin >= n_bins");
+    const uint32_t C = K + 1, W = (F + 3) / 4;
+    // scales from sum |v| bounds (same rule as the session)
+    double bd = 0.0, bw = 0.0;
+    for (uint64_t i = 0; i < n; ++i) {
+        double m = 0.0;
+        for (uint32_t d = 0; d < K; ++d) m = std::max(m, std::fabs(der[(size_t)d * n + i]));
+        bd += m;
+        bw += std::fabs(w[i]);
+    }
+    Scales sc{};
+    const double bounds[2] = {bd, bw};
+    for (int k = 0; k < kNumScales; ++k) {
+        int e = -20;
+        if (k < 2 && bounds[k] > 0.0) std::frexp(bounds[k] * 1.0000001 + 1e-300, &e);
+        const int s = std::min(61 - e, 100);
+        sc.shift[k] = s;
+        sc.mul[k] = std::ldexp(1.0, s);
+        sc.inv[k] = std::ldexp(1.0, -s);
+    }
+    // rows grouped by slot, ascending row order; chunks of 8192 rows
+    std::vector<uint32_t> idx;
+    std::vector<Chunk> chunks;
+    if (slot_of_row) {
+        std::vector<std::vector<uint32_t>> per(n_slots);
+        for (uint64_t i = 0; i < n; ++i)
+            if (slot_of_row[i] < n_slots) per[slot_of_row[i]].push_back((uint32_t)i);
+        for (uint32_t s = 0; s < n_slots; ++s) {
+            const uint32_t b0 = (uint32_t)idx.size();
+            idx.insert(idx.end(), per[s].begin(), per[s].end());
+            for (uint32_t o = 0; o < per[s].size(); o += 8192)
+                chunks.push_back(Chunk{b0 + o, b0 + std::min<uint32_t>((uint32_t)per[s].size(), o + 8192), s, 0});
+        }
+    }
+    int lds_max = 0, dev = 0;
+    HIP_OK(hipGetDevice(&dev));
+    HIP_OK(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+    const size_t budget = std::min<size_t>((size_t)lds_max, 160 * 1024);
+    const size_t per_feature = (size_t)B * C * 8;
+    const size_t max_words = budget / (per_feature * 4);
+    if (max_words == 0) return fail2(CBH_ERR_UNSUPPORTED, "histogram line too wide for LDS");
+    const uint32_t n_tiles = (uint32_t)((W + max_words - 1) / max_words);
+    const uint32_t tw = (W + n_tiles - 1) / n_tiles;
+    std::vector<uint32_t> w0(n_tiles + 1);
+    for (uint32_t t = 0; t <= n_tiles; ++t) w0[t] = std::min(W, t * tw);
+    const size_t lds = (size_t)std::min<uint32_t>(tw * 4, F) * per_feature;
+
+    DBuf<uint8_t> cols;
+    DBuf<uint32_t> rows, didx, dw0;
+    DBuf<double> dder, dw, sstat, dout;
+    DBuf<Chunk> dch;
+    DBuf<LevelPlan> dplan;
+    DBuf<Scales> dsc;
+    DBuf<long long> hist;
+    const size_t cells = (size_t)n_slots * F * B * C;
+    HIP_OK(cols.alloc(n * F));
+    HIP_OK(rows.alloc(n * W));
+    HIP_OK(dder.alloc(n * K));
+    HIP_OK(dw.alloc(n));
+    HIP_OK(sstat.alloc(n * C));
+    HIP_OK(dw0.alloc(n_tiles + 1));
+    HIP_OK(dsc.alloc(1));
+    HIP_OK(hist.alloc(cells));
+    HIP_OK(dout.alloc(cells));
+    HIP_OK(hipMemcpy(cols.p, bins_fm, n * F, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dder.p, der, sizeof(double) * n * K, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dw.p, w, sizeof(double) * n, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dw0.p, w0.data(), sizeof(uint32_t) * (n_tiles + 1), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dsc.p, &sc, sizeof(Scales), hipMemcpyHostToDevice));
+    HIP_OK(hipMemset(hist.p, 0, cells * sizeof(long long)));
+    pack_rows_kernel<<<grid_of(n * W, 256), 256>>>(cols.p, n, F, W, rows.p);
+    pack_stats_kernel<<<grid_of(n, 256), 256>>>(dder.p, dw.p, n, K, sstat.p);
+    HIP_OK(hipGetLastError());
+    uint32_t dense_chunks = 0, slots;
+    if (slot_of_row) {
+        LevelPlan plan{};
+        plan.n_chunks = (uint32_t)chunks.size();
+        HIP_OK(didx.alloc(std::max<size_t>(idx.size(), 1)));
+        HIP_OK(dch.alloc(std::max<size_t>(chunks.size(), 1)));
+        HIP_OK(dplan.alloc(1));
+        if (!idx.empty()) HIP_OK(hipMemcpy(didx.p, idx.data(), sizeof(uint32_t) * idx.size(), hipMemcpyHostToDevice));
+        if (!chunks.empty()) HIP_OK(hipMemcpy(dch.p, chunks.data(), sizeof(Chunk) * chunks.size(), hipMemcpyHostToDevice));
+        HIP_OK(hipMemcpy(dplan.p, &plan, sizeof(LevelPlan), hipMemcpyHostToDevice));
+        slots = std::max<uint32_t>(1, (uint32_t)chunks.size());
+    } else {
+        dense_chunks = (uint32_t)((n + 8191) / 8192);
+        slots = dense_chunks;
+    }
+    slots = std::min<uint32_t>(slots, std::max<uint32_t>(8, 1024 / n_tiles));
+    slots = (slots + 7) / 8 * 8;
+    int rc;
+    switch (C) {
+#define CASE(c) case c: rc = run_fill<c>(rows.p, W, n, slot_of_row ? didx.p : nullptr, dch.p, dplan.p, dense_chunks, sstat.p, dsc.p, dw0.p, n_tiles, F, B, slots, lds, hist.p); break;
+        CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(9) CASE(11) CASE(13) CASE(17)
+#undef CASE
+        default: return fail2(CBH_ERR_UNSUPPORTED, "K has no compiled fill variant");
+    }
+    if (rc != CBH_OK) return rc;
+    hist_to_f64_kernel<<<grid_of(cells, 256), 256>>>(hist.p, cells, C, dsc.p, dout.p);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipMemcpy(hist_out, dout.p, sizeof(double) * cells, hipMemcpyDeviceToHost));
+    return CBH_OK;
+}
+
+}  // extern "C"

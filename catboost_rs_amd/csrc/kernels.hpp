@@ -1,0 +1,805 @@
+// HIP kernels of the gfx950 oblivious-tree training path.
+//
+// Data layout in HBM (per session):
+//   rows   u32 [n][W]      row-major packed bins, 4 features per word (byte k of word w is
+//                          feature 4w+k); a fill reads only the words of its feature tile
+//   cols   u8  [F][n]      feature-major bins, read once per level by the split kernel
+//   sstat  f64 [n][K+1]    score channels per row: K weighted, sampled derivatives, then the
+//                          sampled weight (zero for rows outside the bootstrap sample)
+//   leaf   u16 [n]         leaf index, bit 15 set for rows outside the score sample
+//   idx    u32 [<= n]      row ids of the directly built children, grouped by parent leaf,
+//                          ascending row order inside each group (stable partition)
+//   hist   i64 [2^l][F][B][K+1]  exact fixed-point histograms of level l
+#pragma once
+#include "common.hpp"
+
+namespace cbh {
+
+struct Chunk {
+    uint32_t begin, end, slot, pad;
+};
+
+struct SplitRec {
+    uint32_t feature;
+    uint32_t bin;
+    uint32_t one_hot;
+    uint32_t valid;
+    double score;
+};
+
+struct LevelPlan {            // written by plan_finalize, read by fill/derive/compact
+    uint32_t n_chunks;
+    uint32_t n_parent;
+    uint32_t rows;            // rows visited by the next fill (sum of built segments)
+    uint32_t pad;
+    uint32_t built[kMaxLeaves / 2];
+    uint32_t seg_begin[kMaxLeaves / 2];
+};
+
+struct SampleParams {
+    int32_t kind;             // 0 none, 1 Bayesian, 2 Bernoulli
+    float temperature;
+    double rate;              // (double)(float)subsample
+    uint64_t bayes_seed;
+    Rng bern;                 // main-stream state before the n Bernoulli draws
+};
+
+// ---------------------------------------------------------------------------------
+// wave64 helpers
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint32_t mbcnt64(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ---------------------------------------------------------------------------------
+// zero fill (graph-safe replacement for memset)
+// ---------------------------------------------------------------------------------
+static __global__ void zero_i64_kernel(long long* __restrict__ p, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) p[i] = 0;
+}
+
+// ---------------------------------------------------------------------------------
+// Bin packing: feature-major u8 [F][n] -> row-major words [n][W].
+// ---------------------------------------------------------------------------------
+static __global__ void pack_rows_kernel(const uint8_t* __restrict__ cols, uint64_t n, uint32_t F,
+                                 uint32_t W, uint32_t* __restrict__ rows) {
+    uint64_t total = n * W;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (uint64_t)gridDim.x * blockDim.x) {
+        uint64_t i = t / W;
+        uint32_t w = (uint32_t)(t % W);
+        uint32_t word = 0;
+        for (uint32_t k = 0; k < 4; ++k) {
+            uint32_t f = 4 * w + k;
+            if (f < F) word |= (uint32_t)cols[(size_t)f * n + i] << (8 * k);
+        }
+        rows[t] = word;
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Derivatives (crates/cb-compute/src/loss.rs:35-80, 424-486).
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ void scalar_ders(int loss, double a, double t, double& d1, double& d2) {
+    if (loss == 0) {          // RMSE
+        d1 = t - a;
+        d2 = -1.0;
+    } else {                  // Logloss / CrossEntropy: p = 1 - 1/(1+e^a)
+        double e = exp(a);
+        double p = 1.0 - 1.0 / (1.0 + e);
+        d1 = t - p;
+        d2 = -p * (1.0 - p);
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void softmax_probs(const double* a, double* p) {
+    double mx = -INFINITY;
+#pragma unroll
+    for (int d = 0; d < K; ++d) mx = a[d] > mx ? a[d] : mx;
+    double sum = 0.0;
+#pragma unroll
+    for (int d = 0; d < K; ++d) p[d] = exp(a[d] - mx);
+#pragma unroll
+    for (int d = 0; d < K; ++d) sum += p[d];
+#pragma unroll
+    for (int d = 0; d < K; ++d) p[d] = p[d] / sum;
+}
+
+// ---------------------------------------------------------------------------------
+// Per-tree preparation: apply the previous tree (approx += lr * leaf), derivatives,
+// bootstrap sample (bootstrap.rs:141-184), score channels, leaf flags, scale bounds.
+// One thread per row; the Bayesian stream of row i is block (i / 1000) of the per-tree
+// seed advanced by 10 + (i % 1000) draws, the Bernoulli draw of row i is the main stream
+// advanced by i draws -- both by the LCG closed-form jump, so rows are independent.
+// ---------------------------------------------------------------------------------
+template <int K>
+static __global__ __launch_bounds__(256) void prepare_kernel(
+    uint64_t n, int loss, double* __restrict__ approx, const double* __restrict__ target,
+    const double* __restrict__ weight, uint16_t* __restrict__ leaf,
+    const double* __restrict__ pending /* [leaves][K] lr-scaled, nullable */,
+    SampleParams smp, const double* __restrict__ host_sample,
+    double* __restrict__ sstat /* [n][K+1] */, int newton, Bounds* __restrict__ bounds) {
+    constexpr int C = K + 1;
+    unsigned long long acc[kNumScales] = {0, 0, 0, 0};
+    unsigned long long sampled = 0;
+    const double bscale = (double)(1 << kBoundShift);
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        double a[K];
+#pragma unroll
+        for (int d = 0; d < K; ++d) a[d] = approx[(size_t)d * n + i];
+        if (pending) {
+            uint32_t l = leaf[i] & 0x7FFFu;
+#pragma unroll
+            for (int d = 0; d < K; ++d) {
+                a[d] += pending[(size_t)l * K + d];
+                approx[(size_t)d * n + i] = a[d];
+            }
+        }
+        const double t = target[i];
+        const double w = weight ? weight[i] : 1.0;
+        double d1[K];
+        double h_leaf;  // leaf weight channel bound: w (Gradient) or |der2 * w| (Newton)
+        if (K == 1) {
+            double g, h;
+            scalar_ders(loss, a[0], t, g, h);
+            d1[0] = g;
+            h_leaf = newton ? fabs(h * w) : fabs(w);
+        } else {
+            double p[K];
+            softmax_probs<K>(a, p);
+#pragma unroll
+            for (int d = 0; d < K; ++d) d1[d] = -p[d];
+            int tc = (int)t;
+            if (tc >= 0 && tc < K) d1[tc] += 1.0;
+            h_leaf = fabs(w);
+        }
+        // bootstrap sample
+        double s = 1.0;
+        bool ctrl = true;
+        if (host_sample) {
+            s = host_sample[i];
+        } else if (smp.kind == 1) {
+            Rng r = rng_from_seed(smp.bayes_seed + i / 1000);
+            rng_advance(r, 10 + i % 1000);
+            double u = rng_real1(r);
+            float bw = -fast_logf((float)u + 0.0f);  // 1e-100f rounds to 0 in f32
+            s = smp.temperature == 1.0f ? (double)bw : (double)powf(bw, smp.temperature);
+        } else if (smp.kind == 2) {
+            Rng r = smp.bern;
+            rng_advance(r, i);
+            ctrl = rng_real1(r) < smp.rate;
+        }
+        double mx_sd = 0.0, mx_ld = 0.0;
+#pragma unroll
+        for (int d = 0; d < K; ++d) {
+            double wd = d1[d] * w;                   // weighted_der1 (boosting.rs:7479)
+            double sd = ctrl ? wd * s : 0.0;         // score_weighted_der1 (:7709)
+            sstat[i * C + d] = sd;
+            mx_sd = fmax(mx_sd, fabs(sd));
+            mx_ld = fmax(mx_ld, fabs(wd));
+        }
+        double sw = ctrl ? w * s : 0.0;              // score_weights (:7728)
+        sstat[i * C + K] = sw;
+        leaf[i] = sw == 0.0 ? (uint16_t)0x8000u : (uint16_t)0;
+        sampled += sw != 0.0;
+        acc[kScoreDer] += (unsigned long long)ceil(mx_sd * bscale);
+        acc[kScoreW] += (unsigned long long)ceil(fabs(sw) * bscale);
+        acc[kLeafDer] += (unsigned long long)ceil(mx_ld * bscale);
+        acc[kLeafW] += (unsigned long long)ceil(h_leaf * bscale);
+    }
+#pragma unroll
+    for (int k = 0; k < kNumScales; ++k) acc[k] = wave_sum_u64(acc[k]);
+    sampled = wave_sum_u64(sampled);
+    if (lane_id() == 0) {
+#pragma unroll
+        for (int k = 0; k < kNumScales; ++k) atomicAdd(&bounds->sum_abs[k], acc[k]);
+        atomicAdd(&bounds->sampled_rows, sampled);
+    }
+}
+
+// Pick S per slot so that 2^S * sum|v| <= 2^61 (no partial sum of rounded values can
+// overflow int64) -- a single thread.
+static __global__ void scales_kernel(const Bounds* __restrict__ b, Scales* __restrict__ sc) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    for (int k = 0; k < kNumScales; ++k) {
+        double bound = (double)b->sum_abs[k] / (double)(1 << kBoundShift);
+        int e = 0;
+        if (bound > 0.0) {
+            frexp(bound, &e);             // bound < 2^e
+        } else {
+            e = -20;
+        }
+        int s = 61 - e;
+        if (s > 100) s = 100;
+        sc->shift[k] = s;
+        sc->mul[k] = ldexp(1.0, s);
+        sc->inv[k] = ldexp(1.0, -s);
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Histogram fill.  One workgroup = (feature tile, chunk slot); it loops over chunks
+// (row ranges of one leaf), accumulating round(v * 2^S) into an LDS histogram of its
+// feature tile with 64-bit integer LDS atomics, then flushes non-zero cells into the
+// level histogram with 64-bit global atomics (integer adds: any order gives the same
+// bits).  The blockIdx -> (tile, chunk slot) map keeps all tiles of a chunk slot on one
+// XCD (blocks are dealt to the 8 XCDs round-robin), so the rows a chunk reads are fetched
+// into that XCD's L2 once and shared by its tiles.
+// ---------------------------------------------------------------------------------
+template <int C>
+static __global__ __launch_bounds__(1024) void fill_kernel(
+    const uint32_t* __restrict__ rows, uint32_t W, uint64_t n,
+    const uint32_t* __restrict__ idx,                  // null: dense rows [0, n)
+    const Chunk* __restrict__ chunks, const LevelPlan* __restrict__ plan,
+    uint32_t dense_chunk_rows, uint32_t dense_n_chunks,
+    const double* __restrict__ sstat, const Scales* __restrict__ sc,
+    const uint32_t* __restrict__ tile_w0, uint32_t n_tiles, uint32_t F, uint32_t B,
+    uint32_t n_slots, long long* __restrict__ hist) {
+    extern __shared__ long long lds[];
+    constexpr int K = C - 1;
+    const uint32_t b = blockIdx.x;
+    const uint32_t xcd = b & 7u, q = b >> 3;
+    const uint32_t t = q % n_tiles;
+    const uint32_t g = (q / n_tiles) * 8u + xcd;
+    const uint32_t w0 = tile_w0[t], w1 = tile_w0[t + 1];
+    const uint32_t TW = w1 - w0;
+    const uint32_t f0 = 4u * w0;
+    const uint32_t f1 = min(4u * w1, F);
+    const uint32_t TF = f1 - f0;
+    const uint32_t cells = TF * B * C;
+    for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) lds[i] = 0;
+    __syncthreads();
+    const uint32_t rows_per_pass = blockDim.x / TW;
+    const uint32_t r0 = threadIdx.x / TW;
+    const uint32_t wl = threadIdx.x - r0 * TW;
+    const bool active = r0 < rows_per_pass;
+    const uint32_t nch = idx ? plan->n_chunks : dense_n_chunks;
+    const double md = sc->mul[kScoreDer], mw = sc->mul[kScoreW];
+    for (uint32_t c = g; c < nch; c += n_slots) {
+        uint32_t beg, end, slot;
+        if (idx) {
+            const Chunk ch = chunks[c];
+            beg = ch.begin;
+            end = ch.end;
+            slot = ch.slot;
+        } else {
+            beg = c * dense_chunk_rows;
+            end = (uint32_t)min((uint64_t)beg + dense_chunk_rows, n);
+            slot = 0;
+        }
+        if (active) {
+            for (uint32_t p = beg + r0; p < end; p += rows_per_pass) {
+                const uint32_t doc = idx ? idx[p] : p;
+                const double* st = sstat + (size_t)doc * C;
+                const double wv = st[K];
+                if (wv == 0.0) continue;  // outside the sample: contributes exactly zero
+                long long fx[C];
+#pragma unroll
+                for (int d = 0; d < K; ++d) fx[d] = to_fixed(st[d], md);
+                fx[K] = to_fixed(wv, mw);
+                const uint32_t word = rows[(size_t)doc * W + w0 + wl];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t fl = 4u * wl + (uint32_t)k;
+                    if (fl < TF) {
+                        const uint32_t bin = (word >> (8 * k)) & 0xFFu;
+                        unsigned long long* cell =
+                            (unsigned long long*)(lds + ((size_t)fl * B + bin) * C);
+#pragma unroll
+                        for (int ch = 0; ch < C; ++ch) atomicAdd(cell + ch, (unsigned long long)fx[ch]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        unsigned long long* dst = (unsigned long long*)(hist + ((size_t)slot * F + f0) * B * C);
+        for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) {
+            const long long v = lds[i];
+            if (v != 0) {
+                atomicAdd(dst + i, (unsigned long long)v);
+                lds[i] = 0;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Sibling by subtraction: for each parent p, the child not built directly is
+// parent - built (exact in integers).  hist_cur has 2 * n_parent leaves.
+static __global__ void derive_kernel(const long long* __restrict__ parent, long long* __restrict__ cur,
+                              const LevelPlan* __restrict__ plan, uint32_t n_parent,
+                              size_t per_leaf) {
+    const size_t total = (size_t)n_parent * per_leaf;
+    for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (size_t)gridDim.x * blockDim.x) {
+        const uint32_t p = (uint32_t)(t / per_leaf);
+        const size_t j = t - (size_t)p * per_leaf;
+        const uint32_t built = plan->built[p];
+        const uint32_t other = built == p ? p + n_parent : p;
+        cur[(size_t)other * per_leaf + j] = parent[t] - cur[(size_t)built * per_leaf + j];
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Split scoring.  One workgroup per feature, one thread per border; for every leaf the
+// exact integer prefix over bins gives FALSE = prefix, TRUE = total - prefix (one-hot:
+// TRUE = the bin, FALSE = total - bin).  Scores fold in the reference order
+// (crates/cb-compute/src/score.rs:192-265): dimension-major, FALSE children 0..P-1 then
+// TRUE children 0..P-1; Cosine = num / sqrt(1e-100 + sum avg^2 w).  The block argmax keeps
+// the highest score, ties to the lowest border (strict first-wins, tree.rs:355-366).
+// ---------------------------------------------------------------------------------
+template <int NW>
+__device__ __forceinline__ void block_scan2(long long vd, long long vw, long long& pd, long long& pw,
+                                            long long& td, long long& tw, long long* sh /*[2*NW+2]*/) {
+    const uint32_t lane = lane_id();
+    const uint32_t wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        long long ud = __shfl_up(vd, o, 64);
+        long long uw = __shfl_up(vw, o, 64);
+        if (lane >= (uint32_t)o) {
+            vd += ud;
+            vw += uw;
+        }
+    }
+    if (lane == 63) {
+        sh[wave] = vd;
+        sh[NW + wave] = vw;
+    }
+    __syncthreads();
+    long long od = 0, ow = 0, sd = 0, sw = 0;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+        if ((uint32_t)k < wave) {
+            od += sh[k];
+            ow += sh[NW + k];
+        }
+        sd += sh[k];
+        sw += sh[NW + k];
+    }
+    __syncthreads();
+    pd = vd + od;
+    pw = vw + ow;
+    td = sd;
+    tw = sw;
+}
+
+template <int K, int NW>
+__global__ __launch_bounds__(64 * NW) void score_kernel(
+    const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
+    const uint32_t* __restrict__ n_cand, const uint8_t* __restrict__ one_hot,
+    const Scales* __restrict__ sc, double l2, int cosine, double* __restrict__ best_score,
+    uint32_t* __restrict__ best_bin) {
+    constexpr int C = K + 1;
+    __shared__ long long sh[2 * NW + 2];
+    __shared__ double red_s[NW];
+    __shared__ uint32_t red_b[NW];
+    const uint32_t f = blockIdx.x;
+    const uint32_t b = threadIdx.x;
+    const uint32_t nc = n_cand[f];
+    if (nc == 0) {
+        if (b == 0) {
+            best_score[f] = -INFINITY;
+            best_bin[f] = 0;
+        }
+        return;
+    }
+    const bool oh = one_hot != nullptr && one_hot[f] != 0;
+    const double inv_d = sc->inv[kScoreDer], inv_w = sc->inv[kScoreW];
+    double num = 0.0;
+    double den = 0.0;
+    den += 1e-100;
+    for (int d = 0; d < K; ++d) {
+        for (int side = 0; side < 2; ++side) {
+            for (uint32_t p = 0; p < P; ++p) {
+                const long long* row = hist + ((size_t)p * F + f) * B * C;
+                const long long vd = b < B ? row[(size_t)b * C + d] : 0;
+                const long long vw = b < B ? row[(size_t)b * C + K] : 0;
+                long long pd, pw, td, tw;
+                block_scan2<NW>(vd, vw, pd, pw, td, tw, sh);
+                long long xd, xw;
+                if (!oh) {
+                    xd = side == 0 ? pd : td - pd;
+                    xw = side == 0 ? pw : tw - pw;
+                } else {
+                    xd = side == 0 ? td - vd : vd;
+                    xw = side == 0 ? tw - vw : vw;
+                }
+                const double s = (double)xd * inv_d;
+                const double w = (double)xw * inv_w;
+                const double avg = w > 0.0 ? s / (w + l2) : 0.0;
+                num += avg * s;
+                den += avg * avg * w;
+            }
+        }
+    }
+    double score = cosine ? num / sqrt(den) : num;
+    if (b >= nc || score != score) score = -INFINITY;
+    // block argmax: max score, ties -> lowest border
+    uint32_t bb = b;
+    for (int o = 32; o > 0; o >>= 1) {
+        double os = __shfl_xor(score, o, 64);
+        uint32_t ob = __shfl_xor(bb, o, 64);
+        if (os > score || (os == score && ob < bb)) {
+            score = os;
+            bb = ob;
+        }
+    }
+    const uint32_t wave = threadIdx.x >> 6;
+    if (lane_id() == 0) {
+        red_s[wave] = score;
+        red_b[wave] = bb;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double s0 = red_s[0];
+        uint32_t b0 = red_b[0];
+        for (int k = 1; k < NW; ++k)
+            if (red_s[k] > s0 || (red_s[k] == s0 && red_b[k] < b0)) {
+                s0 = red_s[k];
+                b0 = red_b[k];
+            }
+        best_score[f] = s0;
+        best_bin[f] = b0;
+    }
+}
+
+// Level argmax over features in enumeration order (floats ascending, then one-hot
+// columns ascending); strict first-wins.  One workgroup of 1024 threads.
+static __global__ __launch_bounds__(1024) void argmax_kernel(const double* __restrict__ best_score,
+                                                      const uint32_t* __restrict__ best_bin,
+                                                      const uint8_t* __restrict__ one_hot,
+                                                      uint32_t F, SplitRec* __restrict__ out) {
+    __shared__ double rs[16];
+    __shared__ uint32_t rk[16];
+    double s = -INFINITY;
+    uint32_t key = 0xFFFFFFFFu;
+    for (uint32_t f = threadIdx.x; f < F; f += blockDim.x) {
+        const double v = best_score[f];
+        const uint32_t k = f + ((one_hot && one_hot[f]) ? F : 0u);
+        if (v > s || (v == s && k < key)) {
+            s = v;
+            key = k;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        double os = __shfl_xor(s, o, 64);
+        uint32_t ok = __shfl_xor(key, o, 64);
+        if (os > s || (os == s && ok < key)) {
+            s = os;
+            key = ok;
+        }
+    }
+    const uint32_t wave = threadIdx.x >> 6;
+    if (lane_id() == 0) {
+        rs[wave] = s;
+        rk[wave] = key;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t nw = (blockDim.x + 63) / 64;
+        for (uint32_t k = 1; k < nw; ++k)
+            if (rs[k] > s || (rs[k] == s && rk[k] < key)) {
+                s = rs[k];
+                key = rk[k];
+            }
+        SplitRec r;
+        r.valid = (s > -INFINITY) ? 1u : 0u;
+        r.feature = key == 0xFFFFFFFFu ? 0u : (key >= F ? key - F : key);
+        r.one_hot = (key != 0xFFFFFFFFu && key >= F) ? 1u : 0u;
+        r.bin = r.valid ? best_bin[r.feature] : 0u;
+        r.score = s;
+        *out = r;
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Stable partition by leaf.
+//   split_count: leaf |= pass << level for every row; per-block counts of sampled rows
+//                per new leaf -> cnt[leaf][block]
+//   plan_scan:   per leaf, exclusive scan over blocks (in place) + total
+//   plan_finalize: smaller child per parent (ties -> the TRUE child, tree.rs:1109), segment
+//                offsets, chunk list of the next fill
+//   compact:     rows of the built children written in ascending row order per segment;
+//                inside a block, ranks come from wave ballots (match on the key bits) and
+//                mbcnt, across waves from per-wave counts in LDS.
+// ---------------------------------------------------------------------------------
+constexpr uint32_t kPartRows = 4096;   // rows per partition block
+
+static __global__ __launch_bounds__(256) void split_count_kernel(
+    const uint8_t* __restrict__ cols, uint64_t n, const SplitRec* __restrict__ split,
+    uint32_t level, uint16_t* __restrict__ leaf, uint32_t* __restrict__ cnt, uint32_t n_blocks,
+    int write_counts) {
+    __shared__ uint32_t c[kMaxLeaves];
+    const uint32_t n_new = 2u << level;
+    for (uint32_t i = threadIdx.x; i < n_new; i += blockDim.x) c[i] = 0;
+    __syncthreads();
+    const SplitRec s = *split;
+    const uint8_t* col = cols + (size_t)s.feature * n;
+    const uint64_t beg = (uint64_t)blockIdx.x * kPartRows;
+    const uint64_t end = min(beg + kPartRows, n);
+    for (uint64_t i = beg + threadIdx.x; i < end; i += blockDim.x) {
+        const uint32_t bin = col[i];
+        const bool pass = s.one_hot ? bin == s.bin : bin > s.bin;
+        uint32_t lf = leaf[i];
+        lf |= (uint32_t)pass << level;
+        leaf[i] = (uint16_t)lf;
+        if (write_counts && !(lf & 0x8000u)) atomicAdd(&c[lf], 1u);
+    }
+    if (!write_counts) return;
+    __syncthreads();
+    for (uint32_t l = threadIdx.x; l < n_new; l += blockDim.x) cnt[(size_t)l * n_blocks + blockIdx.x] = c[l];
+}
+
+static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __restrict__ cnt,
+                                                         uint32_t n_blocks,
+                                                         uint32_t* __restrict__ totals) {
+    __shared__ uint32_t sh[1024];
+    uint32_t* row = cnt + (size_t)blockIdx.x * n_blocks;
+    const uint32_t per = (n_blocks + blockDim.x - 1) / blockDim.x;
+    const uint32_t b0 = threadIdx.x * per;
+    uint32_t local = 0;
+    for (uint32_t k = 0; k < per; ++k)
+        if (b0 + k < n_blocks) local += row[b0 + k];
+    sh[threadIdx.x] = local;
+    __syncthreads();
+    for (uint32_t o = 1; o < blockDim.x; o <<= 1) {
+        uint32_t v = threadIdx.x >= o ? sh[threadIdx.x - o] : 0;
+        __syncthreads();
+        sh[threadIdx.x] += v;
+        __syncthreads();
+    }
+    uint32_t run = sh[threadIdx.x] - local;  // exclusive prefix of this thread's range
+    for (uint32_t k = 0; k < per; ++k)
+        if (b0 + k < n_blocks) {
+            uint32_t v = row[b0 + k];
+            row[b0 + k] = run;
+            run += v;
+        }
+    if (threadIdx.x == blockDim.x - 1) totals[blockIdx.x] = sh[threadIdx.x];
+}
+
+static __global__ void plan_finalize_kernel(const uint32_t* __restrict__ totals, uint32_t level,
+                                     uint32_t chunk_rows, LevelPlan* __restrict__ plan,
+                                     Chunk* __restrict__ chunks, uint32_t max_chunks) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const uint32_t n_parent = 1u << level;  // parents of the next level = current leaves
+    uint32_t off = 0, nch = 0;
+    for (uint32_t p = 0; p < n_parent; ++p) {
+        const uint32_t nf = totals[p], nt = totals[p + n_parent];
+        const uint32_t built = nt <= nf ? p + n_parent : p;
+        const uint32_t cntb = nt <= nf ? nt : nf;
+        plan->built[p] = built;
+        plan->seg_begin[p] = off;
+        for (uint32_t b = 0; b < cntb && nch < max_chunks; b += chunk_rows) {
+            Chunk ch;
+            ch.begin = off + b;
+            ch.end = off + min(cntb, b + chunk_rows);
+            ch.slot = built;
+            ch.pad = 0;
+            chunks[nch++] = ch;
+        }
+        off += cntb;
+    }
+    plan->n_chunks = nch;
+    plan->n_parent = n_parent;
+    plan->rows = off;
+}
+
+static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __restrict__ leaf, uint64_t n,
+                                                      uint32_t level, const uint32_t* __restrict__ cnt,
+                                                      uint32_t n_blocks, const LevelPlan* __restrict__ plan,
+                                                      uint32_t* __restrict__ idx) {
+    constexpr uint32_t NW = 4;
+    __shared__ uint32_t base[kMaxLeaves / 2];
+    __shared__ uint32_t wcnt[NW][kMaxLeaves / 2];
+    const uint32_t n_parent = 1u << level;
+    for (uint32_t p = threadIdx.x; p < n_parent; p += blockDim.x) {
+        const uint32_t built = plan->built[p];
+        base[p] = plan->seg_begin[p] + cnt[(size_t)built * n_blocks + blockIdx.x];
+        for (uint32_t w = 0; w < NW; ++w) wcnt[w][p] = 0;
+    }
+    __syncthreads();
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint64_t beg = (uint64_t)blockIdx.x * kPartRows;
+    const uint64_t end = min(beg + kPartRows, n);
+    for (uint64_t t0 = beg; t0 < end; t0 += blockDim.x) {
+        const uint64_t i = t0 + threadIdx.x;
+        uint32_t key = 0;
+        bool valid = false;
+        if (i < end) {
+            const uint32_t lf = leaf[i];
+            if (!(lf & 0x8000u)) {
+                const uint32_t p = lf & (n_parent - 1u);
+                if (plan->built[p] == lf) {
+                    key = p;
+                    valid = true;
+                }
+            }
+        }
+        uint64_t mask = __ballot(valid);
+        for (uint32_t bit = 0; bit < level; ++bit) {
+            const uint64_t m = __ballot((key >> bit) & 1u);
+            mask &= ((key >> bit) & 1u) ? m : ~m;
+        }
+        const uint32_t rank = mbcnt64(mask);
+        if (valid && rank == 0) wcnt[wave][key] = (uint32_t)__popcll(mask);
+        __syncthreads();
+        if (valid) {
+            uint32_t off = 0;
+            for (uint32_t w = 0; w < wave; ++w) off += wcnt[w][key];
+            idx[base[key] + off + rank] = (uint32_t)i;
+        }
+        __syncthreads();
+        for (uint32_t p = threadIdx.x; p < n_parent; p += blockDim.x) {
+            uint32_t s = 0;
+            for (uint32_t w = 0; w < NW; ++w) {
+                s += wcnt[w][p];
+                wcnt[w][p] = 0;
+            }
+            base[p] += s;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Leaf statistics on the UNSAMPLED derivatives (boosting.rs:2470-2560, :2634): per leaf
+// sum(w * der1[d]) and sum(w) (Gradient) / sum(w * der2) (Newton) / packed sum(w * H)
+// (MultiClass), exact in fixed point.  LDS accumulators per block, global atomics.
+// ---------------------------------------------------------------------------------
+template <int K>
+static __global__ __launch_bounds__(256) void leaf_reduce_kernel(
+    uint64_t n, int loss, int newton, const double* __restrict__ approx,
+    const double* __restrict__ target, const double* __restrict__ weight,
+    const uint16_t* __restrict__ leaf, const Scales* __restrict__ sc, uint32_t n_leaves,
+    long long* __restrict__ out) {
+    constexpr int PK = K * (K + 1) / 2;
+    constexpr int CL = K == 1 ? 2 : K + PK;
+    extern __shared__ long long acc[];
+    const uint32_t cells = n_leaves * CL;
+    for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) acc[i] = 0;
+    __syncthreads();
+    const double md = sc->mul[kLeafDer], mw = sc->mul[kLeafW];
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t l = leaf[i] & 0x7FFFu;
+        const double w = weight ? weight[i] : 1.0;
+        unsigned long long* cell = (unsigned long long*)(acc + (size_t)l * CL);
+        if (K == 1) {
+            double g, h;
+            scalar_ders(loss, approx[i], target[i], g, h);
+            atomicAdd(cell, (unsigned long long)to_fixed(g * w, md));
+            atomicAdd(cell + 1, (unsigned long long)to_fixed(newton ? h * w : w, mw));
+        } else {
+            double a[K], p[K];
+#pragma unroll
+            for (int d = 0; d < K; ++d) a[d] = approx[(size_t)d * n + i];
+            softmax_probs<K>(a, p);
+            const int tc = (int)target[i];
+#pragma unroll
+            for (int d = 0; d < K; ++d) {
+                double g = -p[d];
+                if (d == tc) g += 1.0;
+                atomicAdd(cell + d, (unsigned long long)to_fixed(g * w, md));
+            }
+            int j = 0;
+#pragma unroll
+            for (int y = 0; y < K; ++y) {
+                atomicAdd(cell + K + j, (unsigned long long)to_fixed((p[y] * (p[y] - 1.0)) * w, mw));
+                ++j;
+                for (int x = y + 1; x < K; ++x) {
+                    atomicAdd(cell + K + j, (unsigned long long)to_fixed((p[y] * p[x]) * w, mw));
+                    ++j;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x)
+        if (acc[i] != 0) atomicAdd((unsigned long long*)(out + i), (unsigned long long)acc[i]);
+}
+
+__device__ inline int cholesky_solve_dev(int k, double* a, const double* b, double* x) {
+    double l[kMaxK * kMaxK];
+    double y[kMaxK];
+    for (int i = 0; i < k * k; ++i) l[i] = 0.0;
+    for (int i = 0; i < k; ++i) {
+        for (int j = 0; j <= i; ++j) {
+            double sum = a[i * k + j];
+            for (int p = 0; p < j; ++p) sum -= l[i * k + p] * l[j * k + p];
+            if (i == j) {
+                if (sum <= 0.0) return 0;
+                l[i * k + j] = sqrt(sum);
+            } else {
+                double ljj = l[j * k + j];
+                if (ljj == 0.0) return 0;
+                l[i * k + j] = sum / ljj;
+            }
+        }
+    }
+    for (int i = 0; i < k; ++i) {
+        double sum = b[i];
+        for (int p = 0; p < i; ++p) sum -= l[i * k + p] * y[p];
+        y[i] = sum / l[i * k + i];
+    }
+    for (int i = k - 1; i >= 0; --i) {
+        double sum = y[i];
+        for (int p = i + 1; p < k; ++p) sum -= l[p * k + i] * x[p];
+        x[i] = sum / l[i * k + i];
+    }
+    return 1;
+}
+
+// Leaf values (leaf.rs:161-335): one thread per leaf.  raw[leaf][d] unscaled, scaled =
+// raw * learning_rate (NormalizeLeafValues, boosting.rs:2879-2881).
+template <int K>
+static __global__ void leaf_values_kernel(const long long* __restrict__ sums, const Scales* __restrict__ sc,
+                                   uint32_t n_leaves, int newton, double l2, double lr,
+                                   double* __restrict__ raw, double* __restrict__ scaled) {
+    constexpr int PK = K * (K + 1) / 2;
+    constexpr int CL = K == 1 ? 2 : K + PK;
+    const uint32_t l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= n_leaves) return;
+    const long long* s = sums + (size_t)l * CL;
+    const double id = sc->inv[kLeafDer], iw = sc->inv[kLeafW];
+    if (K == 1) {
+        const double sd = (double)s[0] * id;
+        const double sw = (double)s[1] * iw;
+        double v;
+        if (newton) {
+            const double den = -sw + l2;
+            v = den == 0.0 ? 0.0 : sd / den;
+        } else {
+            v = sw > 0.0 ? sd / (sw + l2) : 0.0;
+        }
+        raw[l] = v;
+        scaled[l] = v * lr;
+        return;
+    }
+    double h[kMaxK * kMaxK], nd[kMaxK], x[kMaxK];
+    int idx = 0;
+    for (int i = 0; i < K; ++i)
+        for (int j = i; j < K; ++j) {
+            const double v = (double)s[K + idx] * iw;
+            h[i * K + j] = v;
+            h[j * K + i] = v;
+            ++idx;
+        }
+    float max_trace = (float)l2;
+    for (int d = 0; d < K; ++d) max_trace = fmaxf(max_trace, (float)(-h[d * K + d]));
+    const double adj = (double)fmaxf((float)l2, max_trace * 1.1920928955078125e-7f);
+    for (int d = 0; d < K; ++d) h[d * K + d] -= adj;
+    for (int i = 0; i < K * K; ++i) h[i] = -h[i];
+    for (int d = 0; d < K; ++d) nd[d] = -((double)s[d] * id);
+    const int ok = cholesky_solve_dev(K, h, nd, x);
+    for (int d = 0; d < K; ++d) {
+        const double v = ok ? -x[d] : 0.0;
+        raw[(size_t)l * K + d] = v;
+        scaled[(size_t)l * K + d] = v * lr;
+    }
+}
+
+// Exact fixed-point histogram -> f64 (kernel-level entry point and tests).
+static __global__ void hist_to_f64_kernel(const long long* __restrict__ h, size_t n_cells, uint32_t C,
+                                   const Scales* __restrict__ sc, double* __restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_cells;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const uint32_t ch = (uint32_t)(i % C);
+        out[i] = (double)h[i] * (ch == C - 1 ? sc->inv[kScoreW] : sc->inv[kScoreDer]);
+    }
+}
+
+}  // namespace cbh

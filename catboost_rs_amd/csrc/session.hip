@@ -1,0 +1,641 @@
+// Host side of the gfx950 training path: the C-ABI declared in include/cbhip.h.
+//
+// A session keeps every per-fit buffer resident in HBM (bins in two layouts, target,
+// weights, approximant, score channels, leaf ids, level histograms) and grows each tree
+// with a fixed sequence of kernel launches on one stream, with no host synchronisation
+// between levels: the split of every level is chosen, applied and planned on the device.
+// The only per-tree transfer is the tree itself (depth splits + 2^depth leaf values).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/cbhip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+using namespace cbh;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                     \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return fail(CBH_ERR_DEVICE, std::string(#expr " failed: ") + hipGetErrorString(e_)); \
+    } while (0)
+
+template <typename T>
+int dalloc(T** p, size_t count) {
+    *p = nullptr;
+    if (count == 0) return CBH_OK;
+    hipError_t e = hipMalloc((void**)p, count * sizeof(T));
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return fail(CBH_ERR_DEVICE, std::string("hipMalloc failed: ") + hipGetErrorString(e));
+    }
+    return CBH_OK;
+}
+
+template <typename T>
+void dfree(T*& p) {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+}
+
+#define CHECK(expr)              \
+    do {                         \
+        int rc_ = (expr);        \
+        if (rc_ != CBH_OK) return rc_; \
+    } while (0)
+
+unsigned grid_for(uint64_t work, unsigned block, unsigned cap = 65535u * 4) {
+    uint64_t g = (work + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (unsigned)g;
+}
+
+// Dispatch a runtime approx dimension to a compile-time K.
+template <typename F>
+int with_k(int k, F&& f) {
+    switch (k) {
+        case 1: return f(std::integral_constant<int, 1>{});
+        case 2: return f(std::integral_constant<int, 2>{});
+        case 3: return f(std::integral_constant<int, 3>{});
+        case 4: return f(std::integral_constant<int, 4>{});
+        case 5: return f(std::integral_constant<int, 5>{});
+        case 6: return f(std::integral_constant<int, 6>{});
+        case 7: return f(std::integral_constant<int, 7>{});
+        case 8: return f(std::integral_constant<int, 8>{});
+        case 10: return f(std::integral_constant<int, 10>{});
+        case 12: return f(std::integral_constant<int, 12>{});
+        case 16: return f(std::integral_constant<int, 16>{});
+        default: return fail(CBH_ERR_UNSUPPORTED, "approx_dim " + std::to_string(k) +
+                                                      " has no compiled kernel variant");
+    }
+}
+
+constexpr uint32_t kChunkRows = 8192;  // rows per fill chunk
+
+struct StageTimer {
+    hipEvent_t a = nullptr, b = nullptr;
+};
+
+}  // namespace
+
+int cbh_internal_fail(int code, const std::string& msg) { return fail(code, msg); }
+
+struct cbh_session {
+    cbh_config cfg{};
+    std::vector<uint8_t> one_hot_host;
+    uint64_t n = 0;
+    uint32_t F = 0, B = 0, W = 0, K = 1, C = 2, depth = 0;
+    double lr = 0.0, l2 = 0.0;
+    bool has_weight = false, target_set = false, pending = false;
+    hipStream_t stream = nullptr;
+    int device = 0;
+
+    // resident buffers
+    uint32_t* rows = nullptr;
+    uint8_t* cols = nullptr;
+    double* weight = nullptr;
+    double* target = nullptr;
+    double* approx = nullptr;
+    double* sstat = nullptr;
+    double* host_sample = nullptr;
+    uint16_t* leaf = nullptr;
+    uint32_t* idx = nullptr;
+    long long* hist[2] = {nullptr, nullptr};
+    size_t hist_cells_max = 0;
+    uint32_t* cnt = nullptr;
+    uint32_t* totals = nullptr;
+    uint32_t n_part_blocks = 0;
+    Chunk* chunks = nullptr;
+    uint32_t max_chunks = 0;
+    LevelPlan* plans = nullptr;   // [depth]
+    SplitRec* splits = nullptr;   // [depth]
+    double* best_score = nullptr;
+    uint32_t* best_bin = nullptr;
+    uint32_t* n_cand = nullptr;
+    uint8_t* one_hot = nullptr;
+    Scales* scales = nullptr;
+    Bounds* bounds = nullptr;
+    long long* leaf_sums = nullptr;
+    double* leaf_raw = nullptr;
+    double* leaf_scaled = nullptr;
+    uint32_t* tile_w0 = nullptr;
+    uint32_t n_tiles = 0;
+    size_t fill_lds = 0;
+
+    // profiling
+    cbh_stats stats{};
+    std::vector<std::pair<int, StageTimer>> timers;
+    size_t timer_used = 0;
+
+    ~cbh_session() { release(); }
+
+    void release() {
+        dfree(rows); dfree(cols); dfree(weight); dfree(target); dfree(approx); dfree(sstat);
+        dfree(host_sample); dfree(leaf); dfree(idx); dfree(hist[0]); dfree(hist[1]); dfree(cnt);
+        dfree(totals); dfree(chunks); dfree(plans); dfree(splits); dfree(best_score);
+        dfree(best_bin); dfree(n_cand); dfree(one_hot); dfree(scales); dfree(bounds);
+        dfree(leaf_sums); dfree(leaf_raw); dfree(leaf_scaled); dfree(tile_w0);
+        for (auto& t : timers) {
+            if (t.second.a) (void)hipEventDestroy(t.second.a);
+            if (t.second.b) (void)hipEventDestroy(t.second.b);
+        }
+        timers.clear();
+        if (stream) (void)hipStreamDestroy(stream);
+        stream = nullptr;
+    }
+
+    // Stage timing: begin() records the start event of a stage, end() the stop event.
+    int stage_begin(int stage) {
+        if (!cfg.profile) return CBH_OK;
+        if (timer_used == timers.size()) {
+            StageTimer t;
+            HIP_TRY(hipEventCreate(&t.a));
+            HIP_TRY(hipEventCreate(&t.b));
+            timers.push_back({stage, t});
+        }
+        timers[timer_used].first = stage;
+        HIP_TRY(hipEventRecord(timers[timer_used].second.a, stream));
+        return CBH_OK;
+    }
+    int stage_end() {
+        if (!cfg.profile) return CBH_OK;
+        HIP_TRY(hipEventRecord(timers[timer_used].second.b, stream));
+        ++timer_used;
+        return CBH_OK;
+    }
+    int collect_timers() {
+        for (size_t i = 0; i < timer_used; ++i) {
+            float ms = 0.f;
+            HIP_TRY(hipEventElapsedTime(&ms, timers[i].second.a, timers[i].second.b));
+            double* dst = nullptr;
+            switch (timers[i].first) {
+                case 0: dst = &stats.fill_ms; break;
+                case 1: dst = &stats.derive_ms; break;
+                case 2: dst = &stats.score_ms; break;
+                case 3: dst = &stats.partition_ms; break;
+                case 4: dst = &stats.leaf_ms; break;
+                default: dst = &stats.prepare_ms; break;
+            }
+            *dst += ms;
+            stats.total_ms += ms;
+        }
+        timer_used = 0;
+        return CBH_OK;
+    }
+};
+
+namespace {
+
+enum { kStFill = 0, kStDerive = 1, kStScore = 2, kStPartition = 3, kStLeaf = 4, kStPrepare = 5 };
+
+int validate_config(const cbh_config* cfg, uint32_t n_bins, uint64_t n, uint32_t F) {
+    if (!cfg) return fail(CBH_ERR_INVALID_ARG, "config is null");
+    if (cfg->boosting_type_is_plain != 1 || cfg->fold_count != 1)
+        return fail(CBH_DECLINED, "ordered boosting / several folds are not covered on device");
+    if (cfg->depth < 1 || cfg->depth > kMaxDepth)
+        return fail(CBH_DECLINED, "depth outside 1..8 is not covered on device");
+    if (cfg->loss < CBH_LOSS_RMSE || cfg->loss > CBH_LOSS_CROSSENTROPY)
+        return fail(CBH_DECLINED, "loss not covered on device");
+    if (cfg->loss == CBH_LOSS_MULTICLASS) {
+        if (cfg->approx_dim < 2 || cfg->approx_dim > kMaxK)
+            return fail(CBH_DECLINED, "MultiClass approx_dim must be 2..16");
+        if (cfg->leaf_method != CBH_LEAF_NEWTON)
+            return fail(CBH_DECLINED, "MultiClass needs Newton leaves (boosting.rs:2169-2186)");
+    } else if (cfg->approx_dim != 1) {
+        return fail(CBH_ERR_INVALID_ARG, "approx_dim must be 1 for scalar losses");
+    }
+    if (cfg->score_function != CBH_SCORE_COSINE && cfg->score_function != CBH_SCORE_L2)
+        return fail(CBH_DECLINED, "score function not covered on device");
+    if (n_bins < 2 || n_bins > 256)
+        return fail(CBH_DECLINED, "n_bins must be in 2..256 (u8 bins)");
+    if (n == 0 || F == 0) return fail(CBH_ERR_DEGENERATE, "empty dataset");
+    if (n >= (1ull << 32)) return fail(CBH_DECLINED, "more than 2^32-1 rows");
+    return CBH_OK;
+}
+
+int session_alloc(cbh_session* s) {
+    const uint64_t n = s->n;
+    CHECK(dalloc(&s->rows, (size_t)n * s->W));
+    CHECK(dalloc(&s->cols, (size_t)n * s->F));
+    if (s->has_weight) CHECK(dalloc(&s->weight, n));
+    CHECK(dalloc(&s->target, n));
+    CHECK(dalloc(&s->approx, (size_t)n * s->K));
+    CHECK(dalloc(&s->sstat, (size_t)n * s->C));
+    CHECK(dalloc(&s->leaf, n));
+    CHECK(dalloc(&s->idx, n));
+    const size_t per_leaf = (size_t)s->F * s->B * s->C;
+    s->hist_cells_max = per_leaf << (s->depth - 1);
+    CHECK(dalloc(&s->hist[0], s->hist_cells_max));
+    CHECK(dalloc(&s->hist[1], s->hist_cells_max));
+    s->n_part_blocks = (uint32_t)((n + kPartRows - 1) / kPartRows);
+    CHECK(dalloc(&s->cnt, (size_t)s->n_part_blocks << s->depth));
+    CHECK(dalloc(&s->totals, (size_t)1 << s->depth));
+    s->max_chunks = (uint32_t)((n + kChunkRows - 1) / kChunkRows) + (1u << s->depth) + 1;
+    CHECK(dalloc(&s->chunks, s->max_chunks));
+    CHECK(dalloc(&s->plans, s->depth));
+    CHECK(dalloc(&s->splits, s->depth));
+    CHECK(dalloc(&s->best_score, s->F));
+    CHECK(dalloc(&s->best_bin, s->F));
+    CHECK(dalloc(&s->n_cand, s->F));
+    CHECK(dalloc(&s->scales, 1));
+    CHECK(dalloc(&s->bounds, 1));
+    const uint32_t CL = s->K == 1 ? 2 : s->K + s->K * (s->K + 1) / 2;
+    CHECK(dalloc(&s->leaf_sums, ((size_t)1 << s->depth) * CL));
+    CHECK(dalloc(&s->leaf_raw, ((size_t)1 << s->depth) * s->K));
+    CHECK(dalloc(&s->leaf_scaled, ((size_t)1 << s->depth) * s->K));
+    return CBH_OK;
+}
+
+// Feature tiles of the fill: as many whole words per tile as the LDS budget allows,
+// balanced across tiles.
+int plan_tiles(cbh_session* s) {
+    int lds_max = 0;
+    HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device));
+    size_t budget = std::min<size_t>((size_t)lds_max, 160 * 1024);
+    const size_t per_feature = (size_t)s->B * s->C * sizeof(long long);
+    const size_t max_words = budget / (per_feature * 4);
+    if (max_words == 0)
+        return fail(CBH_DECLINED, "histogram line of 4 features does not fit in LDS");
+    const uint32_t n_tiles = (uint32_t)((s->W + max_words - 1) / max_words);
+    const uint32_t tw = (s->W + n_tiles - 1) / n_tiles;
+    std::vector<uint32_t> w0(n_tiles + 1);
+    for (uint32_t t = 0; t <= n_tiles; ++t) w0[t] = std::min(s->W, t * tw);
+    s->n_tiles = n_tiles;
+    s->fill_lds = (size_t)std::min<uint32_t>(tw * 4, s->F) * per_feature;
+    CHECK(dalloc(&s->tile_w0, n_tiles + 1));
+    HIP_TRY(hipMemcpy(s->tile_w0, w0.data(), sizeof(uint32_t) * (n_tiles + 1), hipMemcpyHostToDevice));
+    return CBH_OK;
+}
+
+template <int C>
+int set_fill_attr(size_t lds) {
+    HIP_TRY(hipFuncSetAttribute((const void*)fill_kernel<C>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    return CBH_OK;
+}
+
+template <typename BinT>
+int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double* weight,
+                       uint64_t n, uint32_t F, uint32_t n_bins, double lr, double l2,
+                       cbh_session** out) {
+    if (!out) return fail(CBH_ERR_INVALID_ARG, "out is null");
+    *out = nullptr;
+    CHECK(validate_config(cfg, n_bins, n, F));
+    if (!bins_fm) return fail(CBH_ERR_INVALID_ARG, "bins_fm is null");
+    // validate bins (the reference surfaces an out-of-range bin as a typed error)
+    for (uint64_t i = 0, total = n * F; i < total; ++i)
+        if ((uint32_t)bins_fm[i] >= n_bins)
+            return fail(CBH_ERR_OUT_OF_RANGE, "bin value >= n_bins at flat index " + std::to_string(i));
+    std::unique_ptr<cbh_session> s(new cbh_session());
+    s->cfg = *cfg;
+    if (cfg->one_hot_flags) s->one_hot_host.assign(cfg->one_hot_flags, cfg->one_hot_flags + F);
+    s->cfg.one_hot_flags = nullptr;
+    s->cfg.real_folds = nullptr;
+    s->n = n;
+    s->F = F;
+    s->B = n_bins;
+    s->W = (F + 3) / 4;
+    s->K = (uint32_t)cfg->approx_dim;
+    s->C = s->K + 1;
+    s->depth = (uint32_t)cfg->depth;
+    s->lr = lr;
+    s->l2 = l2;
+    s->has_weight = weight != nullptr;
+    HIP_TRY(hipGetDevice(&s->device));
+    HIP_TRY(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+    CHECK(session_alloc(s.get()));
+    CHECK(plan_tiles(s.get()));
+    CHECK(with_k((int)s->K, [&](auto kc) {
+        constexpr int K = decltype(kc)::value;
+        return set_fill_attr<K + 1>(s->fill_lds);
+    }));
+    // candidates per feature: float -> real_folds-1 borders; one-hot -> real_folds values
+    std::vector<uint32_t> nc(F);
+    for (uint32_t f = 0; f < F; ++f) {
+        const uint32_t folds = cfg->real_folds ? cfg->real_folds[f] : n_bins;
+        if (folds > n_bins) return fail(CBH_ERR_OUT_OF_RANGE, "real_folds[f] > n_bins");
+        const bool oh = !s->one_hot_host.empty() && s->one_hot_host[f];
+        nc[f] = oh ? folds : (folds > 0 ? folds - 1 : 0);
+    }
+    HIP_TRY(hipMemcpy(s->n_cand, nc.data(), sizeof(uint32_t) * F, hipMemcpyHostToDevice));
+    bool any_oh = false;
+    for (uint8_t v : s->one_hot_host) any_oh |= v != 0;
+    if (any_oh) {
+        CHECK(dalloc(&s->one_hot, F));
+        HIP_TRY(hipMemcpy(s->one_hot, s->one_hot_host.data(), F, hipMemcpyHostToDevice));
+    }
+    // upload bins feature-major as u8, then pack the row-major words on the device
+    if (sizeof(BinT) == 1) {
+        HIP_TRY(hipMemcpy(s->cols, bins_fm, (size_t)n * F, hipMemcpyHostToDevice));
+    } else {
+        std::vector<uint8_t> tmp;
+        const uint64_t step = 1ull << 26;
+        for (uint64_t off = 0, total = n * F; off < total; off += step) {
+            const uint64_t m = std::min(step, total - off);
+            tmp.resize(m);
+            for (uint64_t i = 0; i < m; ++i) tmp[i] = (uint8_t)bins_fm[off + i];
+            HIP_TRY(hipMemcpy(s->cols + off, tmp.data(), m, hipMemcpyHostToDevice));
+        }
+    }
+    pack_rows_kernel<<<grid_for((uint64_t)n * s->W, 256), 256, 0, s->stream>>>(s->cols, n, F, s->W, s->rows);
+    HIP_TRY(hipGetLastError());
+    if (weight) HIP_TRY(hipMemcpy(s->weight, weight, sizeof(double) * n, hipMemcpyHostToDevice));
+    // resident approximant seeded with the bias (DeviceTrainConfig::bias, runtime.rs:1276)
+    std::vector<double> a0(std::min<uint64_t>(n * s->K, 1ull << 22), cfg->bias);
+    for (uint64_t off = 0, total = n * s->K; off < total; off += a0.size()) {
+        const uint64_t m = std::min<uint64_t>(a0.size(), total - off);
+        HIP_TRY(hipMemcpyAsync(s->approx + off, a0.data(), sizeof(double) * m, hipMemcpyHostToDevice, s->stream));
+        HIP_TRY(hipStreamSynchronize(s->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    *out = s.release();
+    return CBH_OK;
+}
+
+int launch_zero(long long* p, size_t n, hipStream_t st) {
+    zero_i64_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(p, n);
+    HIP_TRY(hipGetLastError());
+    return CBH_OK;
+}
+
+template <int K>
+int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
+              std::vector<SplitRec>& splits_out, std::vector<LevelPlan>& plans_out,
+              Bounds& bounds_out, std::vector<double>& leaf_out) {
+    constexpr int C = K + 1;
+    const uint64_t n = s->n;
+    hipStream_t st = s->stream;
+    const int newton = s->cfg.leaf_method == CBH_LEAF_NEWTON ? 1 : 0;
+    const int cosine = s->cfg.score_function == CBH_SCORE_COSINE ? 1 : 0;
+    const int loss = s->cfg.loss == CBH_LOSS_RMSE ? 0 : 1;
+
+    // ---- prepare: apply previous tree, ders, sample, score channels, bounds ----
+    CHECK(s->stage_begin(kStPrepare));
+    HIP_TRY(hipMemsetAsync(s->bounds, 0, sizeof(Bounds), st));
+    prepare_kernel<K><<<grid_for(n, 256, 16384), 256, 0, st>>>(
+        n, loss, s->approx, s->target, s->weight, s->leaf, s->pending ? s->leaf_scaled : nullptr,
+        smp, use_host_sample ? s->host_sample : nullptr, s->sstat, newton, s->bounds);
+    HIP_TRY(hipGetLastError());
+    s->pending = false;
+    scales_kernel<<<1, 64, 0, st>>>(s->bounds, s->scales);
+    HIP_TRY(hipGetLastError());
+    CHECK(s->stage_end());
+
+    const size_t per_leaf = (size_t)s->F * s->B * C;
+    const uint32_t NB = s->n_part_blocks;
+    for (uint32_t level = 0; level < s->depth; ++level) {
+        long long* cur = s->hist[level & 1];
+        long long* par = s->hist[(level + 1) & 1];
+        const uint32_t n_leaves = 1u << level;
+        // ---- fill ----
+        CHECK(s->stage_begin(kStFill));
+        CHECK(launch_zero(cur, per_leaf * n_leaves, st));
+        uint32_t dense_chunks = 0, slots;
+        if (level == 0) {
+            dense_chunks = (uint32_t)((n + kChunkRows - 1) / kChunkRows);
+            slots = dense_chunks;
+        } else {
+            slots = (uint32_t)((n / 2 + kChunkRows - 1) / kChunkRows) + (n_leaves / 2);
+        }
+        uint32_t target_slots = std::max<uint32_t>(8, (1024 + s->n_tiles - 1) / s->n_tiles);
+        slots = std::min(slots, target_slots);
+        slots = (slots + 7) / 8 * 8;
+        const unsigned grid = slots * s->n_tiles;
+        fill_kernel<C><<<grid, 1024, s->fill_lds, st>>>(
+            s->rows, s->W, n, level == 0 ? nullptr : s->idx, s->chunks,
+            level == 0 ? nullptr : s->plans + (level - 1), kChunkRows, dense_chunks, s->sstat,
+            s->scales, s->tile_w0, s->n_tiles, s->F, s->B, slots, cur);
+        HIP_TRY(hipGetLastError());
+        CHECK(s->stage_end());
+        // ---- derive the sibling of every directly built child ----
+        if (level > 0) {
+            CHECK(s->stage_begin(kStDerive));
+            const uint32_t n_parent = n_leaves / 2;
+            derive_kernel<<<grid_for(per_leaf * n_parent, 256, 16384), 256, 0, st>>>(
+                par, cur, s->plans + (level - 1), n_parent, per_leaf);
+            HIP_TRY(hipGetLastError());
+            CHECK(s->stage_end());
+        }
+        // ---- score + argmax ----
+        CHECK(s->stage_begin(kStScore));
+        if (s->B <= 64)
+            score_kernel<K, 1><<<s->F, 64, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
+                                                   s->scales, s->l2, cosine, s->best_score, s->best_bin);
+        else if (s->B <= 128)
+            score_kernel<K, 2><<<s->F, 128, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
+                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin);
+        else
+            score_kernel<K, 4><<<s->F, 256, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
+                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin);
+        HIP_TRY(hipGetLastError());
+        argmax_kernel<<<1, 1024, 0, st>>>(s->best_score, s->best_bin, s->one_hot, s->F, s->splits + level);
+        HIP_TRY(hipGetLastError());
+        CHECK(s->stage_end());
+        // ---- partition ----
+        CHECK(s->stage_begin(kStPartition));
+        const bool last = level + 1 == s->depth;
+        split_count_kernel<<<NB, 256, 0, st>>>(s->cols, n, s->splits + level, level, s->leaf, s->cnt,
+                                               NB, last ? 0 : 1);
+        HIP_TRY(hipGetLastError());
+        if (!last) {
+            plan_scan_kernel<<<2u << level, 1024, 0, st>>>(s->cnt, NB, s->totals);
+            HIP_TRY(hipGetLastError());
+            plan_finalize_kernel<<<1, 64, 0, st>>>(s->totals, level, kChunkRows, s->plans + level,
+                                                   s->chunks, s->max_chunks);
+            HIP_TRY(hipGetLastError());
+            compact_kernel<<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, NB, s->plans + level, s->idx);
+            HIP_TRY(hipGetLastError());
+        }
+        CHECK(s->stage_end());
+    }
+
+    // ---- leaf statistics + values ----
+    CHECK(s->stage_begin(kStLeaf));
+    const uint32_t n_leaves = 1u << s->depth;
+    const uint32_t CL = K == 1 ? 2 : K + K * (K + 1) / 2;
+    CHECK(launch_zero(s->leaf_sums, (size_t)n_leaves * CL, st));
+    const size_t lds = (size_t)n_leaves * CL * sizeof(long long);
+    HIP_TRY(hipFuncSetAttribute((const void*)leaf_reduce_kernel<K>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    leaf_reduce_kernel<K><<<grid_for(n, 256, 1024), 256, lds, st>>>(
+        n, loss, newton, s->approx, s->target, s->weight, s->leaf, s->scales, n_leaves, s->leaf_sums);
+    HIP_TRY(hipGetLastError());
+    leaf_values_kernel<K><<<(n_leaves + 63) / 64, 64, 0, st>>>(s->leaf_sums, s->scales, n_leaves, newton,
+                                                              s->l2, s->lr, s->leaf_raw, s->leaf_scaled);
+    HIP_TRY(hipGetLastError());
+    CHECK(s->stage_end());
+    s->pending = true;
+
+    splits_out.resize(s->depth);
+    plans_out.resize(s->depth);
+    leaf_out.resize((size_t)n_leaves * K);
+    HIP_TRY(hipMemcpyAsync(splits_out.data(), s->splits, sizeof(SplitRec) * s->depth, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(plans_out.data(), s->plans, sizeof(LevelPlan) * s->depth, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(&bounds_out, s->bounds, sizeof(Bounds), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(leaf_out.data(), s->leaf_raw, sizeof(double) * leaf_out.size(), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    return CBH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cbh_last_error(void) { return g_last_error.c_str(); }
+
+const char* cbh_version(void) { return "cbhip 0.1 gfx950"; }
+
+int cbh_session_begin(const cbh_config* cfg, const uint32_t* bins_fm, const double* weight,
+                      uint64_t n, uint32_t n_features, uint32_t n_bins, double learning_rate,
+                      double scaled_l2, cbh_session** out) {
+    return session_begin_impl<uint32_t>(cfg, bins_fm, weight, n, n_features, n_bins, learning_rate,
+                                        scaled_l2, out);
+}
+
+int cbh_session_begin_u8(const cbh_config* cfg, const uint8_t* bins_fm, const double* weight,
+                         uint64_t n, uint32_t n_features, uint32_t n_bins, double learning_rate,
+                         double scaled_l2, cbh_session** out) {
+    return session_begin_impl<uint8_t>(cfg, bins_fm, weight, n, n_features, n_bins, learning_rate,
+                                       scaled_l2, out);
+}
+
+int cbh_session_grow(cbh_session* s, const double* approx, const double* target, uint64_t n,
+                     const double* sample, uint64_t n_sample, const cbh_tree_sampling* sampling,
+                     cbh_tree_out* out) {
+    if (!s) return fail(CBH_ERR_INVALID_ARG, "session is null");
+    if (!out || !out->split_feature || !out->split_bin || !out->leaf_values)
+        return fail(CBH_ERR_INVALID_ARG, "tree output buffers are null");
+    if (n != s->n) return fail(CBH_ERR_LENGTH_MISMATCH, "n differs from the session's row count");
+    if (n_sample != 0 && n_sample != n)
+        return fail(CBH_ERR_LENGTH_MISMATCH, "sample must be empty or of length n (runtime.rs:1605)");
+    if (n_sample != 0 && !sample) return fail(CBH_ERR_INVALID_ARG, "sample is null");
+    if (n_sample != 0 && !s->cfg.sample_from_host)
+        return fail(CBH_ERR_INVALID_ARG, "host sample given to a session without sample_from_host");
+    if (n_sample != 0 && sampling && sampling->kind != CBH_BOOT_NO)
+        return fail(CBH_ERR_INVALID_ARG, "host sample and device sampling are mutually exclusive");
+    hipStream_t st = s->stream;
+    if (target) {
+        HIP_TRY(hipMemcpyAsync(s->target, target, sizeof(double) * n, hipMemcpyHostToDevice, st));
+        s->target_set = true;
+    }
+    if (!s->target_set) return fail(CBH_ERR_INVALID_ARG, "target was never provided");
+    if (approx) {
+        HIP_TRY(hipMemcpyAsync(s->approx, approx, sizeof(double) * n * s->K, hipMemcpyHostToDevice, st));
+        s->pending = false;
+    }
+    if (n_sample) {
+        if (!s->host_sample) CHECK(dalloc(&s->host_sample, n));
+        HIP_TRY(hipMemcpyAsync(s->host_sample, sample, sizeof(double) * n, hipMemcpyHostToDevice, st));
+    }
+    SampleParams smp{};
+    if (sampling && sampling->kind != CBH_BOOT_NO) {
+        smp.kind = sampling->kind;
+        smp.temperature = sampling->bagging_temperature;
+        smp.rate = (double)(float)sampling->subsample;
+        smp.bayes_seed = sampling->bayesian_seed;
+        smp.bern.x1 = sampling->bernoulli_state[0];
+        smp.bern.c1 = sampling->bernoulli_state[1];
+        smp.bern.x2 = sampling->bernoulli_state[2];
+        smp.bern.c2 = sampling->bernoulli_state[3];
+        if (smp.kind == CBH_BOOT_BERNOULLI && sampling->subsample >= 1.0) smp.kind = 0;
+        if (smp.kind == CBH_BOOT_BAYESIAN && sampling->bagging_temperature == 0.0f) smp.kind = 0;
+    }
+    std::vector<SplitRec> splits;
+    std::vector<LevelPlan> plans;
+    Bounds bounds{};
+    std::vector<double> leaves;
+    int rc = with_k((int)s->K, [&](auto kc) {
+        constexpr int K = decltype(kc)::value;
+        return grow_impl<K>(s, smp, n_sample != 0, splits, plans, bounds, leaves);
+    });
+    if (rc != CBH_OK) return rc;
+    for (uint32_t l = 0; l < s->depth; ++l) {
+        if (!splits[l].valid) return fail(CBH_ERR_DEGENERATE, "no candidate split at level " + std::to_string(l));
+        out->split_feature[l] = splits[l].feature;
+        out->split_bin[l] = splits[l].bin;
+        if (out->split_one_hot) out->split_one_hot[l] = (uint8_t)splits[l].one_hot;
+        if (out->split_score) out->split_score[l] = splits[l].score;
+    }
+    std::memcpy(out->leaf_values, leaves.data(), sizeof(double) * leaves.size());
+    if (out->leaf_of) {
+        std::vector<uint16_t> lf(n);
+        HIP_TRY(hipMemcpy(lf.data(), s->leaf, sizeof(uint16_t) * n, hipMemcpyDeviceToHost));
+        for (uint64_t i = 0; i < n; ++i) out->leaf_of[i] = lf[i] & 0x7FFFu;
+    }
+    // traffic accounting of the fill launches (algorithmic bytes per launch)
+    const double wbytes = 4.0 * s->W, sbytes = 8.0 * s->C;
+    const double per_leaf_bytes = (double)s->F * s->B * s->C * 8.0;
+    for (uint32_t l = 0; l < s->depth; ++l) {
+        const uint64_t V = l == 0 ? bounds.sampled_rows : plans[l - 1].rows;
+        const uint32_t built = l == 0 ? 1u : (1u << (l - 1));
+        s->stats.fill_launches += 1;
+        s->stats.fill_rows += V;
+        s->stats.fill_row_features += V * s->F;
+        s->stats.fill_bytes += (double)V * (wbytes + sbytes + (l == 0 ? 0.0 : 4.0)) + built * per_leaf_bytes;
+    }
+    s->stats.trees += 1;
+    return s->collect_timers();
+}
+
+int cbh_session_read_approx(cbh_session* s, double* approx_out, uint64_t n_times_k) {
+    if (!s || !approx_out) return fail(CBH_ERR_INVALID_ARG, "null argument");
+    if (n_times_k != s->n * s->K) return fail(CBH_ERR_LENGTH_MISMATCH, "approx buffer size != n*K");
+    if (s->pending) {
+        // apply the last tree: the prepare kernel does it as part of the next tree, so run
+        // just its update arm here with an inert sample
+        int rc = with_k((int)s->K, [&](auto kc) {
+            constexpr int K = decltype(kc)::value;
+            HIP_TRY(hipMemsetAsync(s->bounds, 0, sizeof(Bounds), s->stream));
+            prepare_kernel<K><<<grid_for(s->n, 256, 16384), 256, 0, s->stream>>>(
+                s->n, s->cfg.loss == CBH_LOSS_RMSE ? 0 : 1, s->approx, s->target, s->weight, s->leaf,
+                s->leaf_scaled, SampleParams{}, nullptr, s->sstat, 0, s->bounds);
+            HIP_TRY(hipGetLastError());
+            return CBH_OK;
+        });
+        if (rc != CBH_OK) return rc;
+        s->pending = false;
+    }
+    HIP_TRY(hipMemcpyAsync(approx_out, s->approx, sizeof(double) * n_times_k, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return CBH_OK;
+}
+
+int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
+    if (!s || !out) return fail(CBH_ERR_INVALID_ARG, "null argument");
+    *out = s->stats;
+    return CBH_OK;
+}
+
+void cbh_session_reset_stats(cbh_session* s) {
+    if (s) s->stats = cbh_stats{};
+}
+
+int cbh_session_end(cbh_session* s) {
+    if (!s) return CBH_OK;
+    if (s->stream) (void)hipStreamSynchronize(s->stream);
+    delete s;
+    return CBH_OK;
+}
+
+int cbh_compute_gradients(int32_t loss, const double* approx, const double* target, uint64_t n,
+                          uint32_t approx_dim, double* der1, double* der2);
+
+}  // extern "C"

@@ -1,0 +1,147 @@
+"""Seeded synthetic workloads of the BASELINE.json configs (no dataset downloads).
+
+Each generator returns feature-major u8 bins ``bins_fm[F][n]``, the border count per
+feature, the target and the training parameters of the config.  Borders are per-feature
+quantiles of a fixed-seed 200k-row sample (the reference subsamples 200k rows for border
+selection too, crates/cb-data/src/borders.rs:504); duplicate quantiles are dropped, so a
+feature with heavy ties gets fewer borders.  A value's bin is the number of borders
+strictly below it (crates/cb-compute/src/histogram.rs:563 ``bin_of``).  Columns are
+generated from independent per-column streams, so the result does not depend on the
+thread count.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+
+import numpy as np
+
+SAMPLE_ROWS = 200_000
+
+
+def _borders(col: np.ndarray, n_borders: int, seed: int) -> np.ndarray:
+    n = col.shape[0]
+    if n > SAMPLE_ROWS:
+        sel = np.random.default_rng(seed).choice(n, SAMPLE_ROWS, replace=False)
+        sample = col[sel]
+    else:
+        sample = col
+    qs = np.linspace(0.0, 1.0, n_borders + 2)[1:-1]
+    b = np.quantile(sample.astype(np.float64), qs).astype(np.float32)
+    b = np.unique(b)
+    # a border at or above the column maximum separates nothing
+    b = b[b < sample.max()] if b.size else b
+    return b.astype(np.float64)
+
+
+def _quantize(col: np.ndarray, borders: np.ndarray) -> np.ndarray:
+    # count of borders strictly below the value == searchsorted(..., side="left")
+    return np.searchsorted(borders, col.astype(np.float64), side="left").astype(np.uint8)
+
+
+def _columns(n, F, make_col, n_borders, seed, threads=None):
+    bins = np.empty((F, n), np.uint8)
+    nb = np.empty(F, np.uint32)
+    keep = {}
+
+    def work(f):
+        col = make_col(f)
+        b = _borders(col, n_borders, seed * 7919 + f)
+        bins[f] = _quantize(col, b)
+        nb[f] = b.size
+        return f, col
+
+    threads = threads or min(16, os.cpu_count() or 4)
+    with cf.ThreadPoolExecutor(threads) as ex:
+        for f, col in ex.map(work, range(F)):
+            keep[f] = col
+    return bins, nb, keep
+
+
+def config1(scale=1.0, seed=0):
+    """RMSE regression: n x 50 N(0,1), y = X.w + 0.1 N(0,1), w ~ U(-1,1); 128 borders;
+    depth 6, 100 iterations, lr 0.1, no bootstrap."""
+    n, F = int(100_000 * scale), 50
+    g = np.random.default_rng(seed)
+    X = g.standard_normal((n, F)).astype(np.float32)
+    w = g.uniform(-1, 1, F)
+    y = X.astype(np.float64) @ w + 0.1 * g.standard_normal(n)
+    bins, nb, _ = _columns(n, F, lambda f: X[:, f], 128, seed)
+    return dict(name="config1", bins=bins, n_borders=nb, target=y,
+                params=dict(loss="RMSE", depth=6, iterations=100, learning_rate=0.1,
+                            l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient",
+                            bootstrap_type="No", boost_from_average=True))
+
+
+def config2(scale=1.0, seed=1, n_rows=None, n_features=200):
+    """Logloss: n x 200 (half N(0,1), half lognormal(0,1)); 254 borders; labels
+    Bernoulli(sigmoid(X[:, :20].w)); depth 6, 200 iterations, Bayesian bootstrap T=1."""
+    n = int(n_rows if n_rows is not None else 10_000_000 * scale)
+    F = n_features
+    half = F // 2
+
+    def make_col(f):
+        g = np.random.default_rng([seed, f])
+        c = g.standard_normal(n, dtype=np.float32)
+        if f >= half:
+            c = np.exp(c)
+        return c
+
+    bins, nb, cols = _columns(n, F, make_col, 254, seed)
+    g = np.random.default_rng([seed, 10_000])
+    w = g.uniform(-1, 1, 20)
+    logit = np.zeros(n)
+    for f in range(min(20, F)):
+        logit += cols[f].astype(np.float64) * w[f]
+    p = 1.0 / (1.0 + np.exp(-logit))
+    y = (g.random(n) < p).astype(np.float64)
+    del cols
+    return dict(name="config2", bins=bins, n_borders=nb, target=y,
+                params=dict(loss="Logloss", depth=6, iterations=200, learning_rate=0.03,
+                            l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient",
+                            bootstrap_type="Bayesian", bagging_temperature=1.0,
+                            boost_from_average=False, random_seed=0))
+
+
+def config5(scale=1.0, seed=5, n_rows=None, n_features=4096, n_classes=10):
+    """MultiClass K=10: n x 4096 sparse-ish (70% exact zeros, else N(0,1)); 64 borders;
+    depth 8, 50 iterations, Newton leaves, no bootstrap.  Labels: argmax of 10 noisy
+    linear scores of the first 32 features."""
+    n = int(n_rows if n_rows is not None else 1_000_000 * scale)
+    F = n_features
+
+    def make_col(f):
+        g = np.random.default_rng([seed, f])
+        c = g.standard_normal(n, dtype=np.float32)
+        c[g.random(n) < 0.7] = 0.0
+        return c
+
+    bins, nb, cols = _columns(n, F, make_col, 64, seed)
+    g = np.random.default_rng([seed, 99_999])
+    Wc = g.standard_normal((min(32, F), n_classes))
+    s = np.zeros((n, n_classes))
+    for f in range(min(32, F)):
+        s += np.outer(cols[f].astype(np.float64), Wc[f])
+    s += g.standard_normal((n, n_classes))
+    y = np.argmax(s, axis=1).astype(np.float64)
+    del cols
+    return dict(name="config5", bins=bins, n_borders=nb, target=y,
+                params=dict(loss="MultiClass", depth=8, iterations=50, learning_rate=0.1,
+                            l2_leaf_reg=3.0, score="Cosine", leaf_method="Newton",
+                            bootstrap_type="No", approx_dim=n_classes, boost_from_average=False))
+
+
+def random_case(seed, n, F, max_borders=16, K=1, zero_weight_frac=0.0):
+    """Small randomized case for parity tests: varying border counts per feature."""
+    g = np.random.default_rng(seed)
+    nb = g.integers(1, max_borders + 1, size=F).astype(np.uint32)
+    nb[g.random(F) < 0.1] = 0  # border-less features are listed but never scored
+    bins = np.stack([g.integers(0, int(nb[f]) + 1, size=n) for f in range(F)]).astype(np.uint8)
+    if K == 1:
+        y = g.standard_normal(n)
+    else:
+        y = g.integers(0, K, size=n).astype(np.float64)
+    w = g.uniform(0.5, 2.0, size=n)
+    if zero_weight_frac:
+        w[g.random(n) < zero_weight_frac] = 0.0
+    return bins, nb, y, w

@@ -1,0 +1,175 @@
+/*
+ * cbhip.h -- C-ABI of the MI355X (gfx950) oblivious-tree training path.
+ *
+ * This library is a drop-in device backend behind catboost_rs's compute seam
+ * `trait cb_compute::Runtime` (crates/cb-compute/src/runtime.rs:1410-1651).  A thin
+ * Rust crate (`HipBackend: Runtime`) binds these symbols one to
+ * one.  Plain pointers and sizes only; no HIP or torch types cross the boundary.
+ *
+ * Status codes: 0 = OK, 1 = DECLINED (the caller falls back to its CPU grower, as a
+ * trait default returning Ok(false)/Ok(None) does), negative = error mirroring the
+ * CbError variants (crates/cb-core/src/error.rs:17-117).  A thread-local message for
+ * the last error is available from cbh_last_error().
+ *
+ * Threading: a session is driven from one thread at a time (the reference guards its
+ * session with a Mutex, crates/cb-backend/src/gpu_backend.rs:53-84).  Different
+ * sessions may run concurrently on different streams.
+ */
+#ifndef CBHIP_H
+#define CBHIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (CbError mirror) ---- */
+#define CBH_OK 0
+#define CBH_DECLINED 1
+#define CBH_ERR_LENGTH_MISMATCH (-1) /* CbError::LengthMismatch */
+#define CBH_ERR_OUT_OF_RANGE (-2)    /* CbError::OutOfRange */
+#define CBH_ERR_DEGENERATE (-3)      /* CbError::Degenerate (e.g. no candidate split) */
+#define CBH_ERR_UNSUPPORTED (-4)     /* CbError::Unsupported */
+#define CBH_ERR_INVALID_ARG (-5)     /* CbError::InvalidArgument-style caller bug */
+#define CBH_ERR_DEVICE (-6)          /* HIP runtime / allocation failure */
+
+/* ---- enums (cb-compute Loss / EScoreFunction / ELeavesEstimation / bootstrap) ---- */
+enum { CBH_LOSS_RMSE = 0, CBH_LOSS_LOGLOSS = 1, CBH_LOSS_MULTICLASS = 2, CBH_LOSS_CROSSENTROPY = 3 };
+enum { CBH_SCORE_COSINE = 0, CBH_SCORE_L2 = 1 };
+enum { CBH_LEAF_GRADIENT = 0, CBH_LEAF_NEWTON = 1, CBH_LEAF_SIMPLE = 2 };
+enum { CBH_BOOT_NO = 0, CBH_BOOT_BAYESIAN = 1, CBH_BOOT_BERNOULLI = 2 };
+
+/* Mirrors DeviceTrainConfig (runtime.rs:1260-1341) plus the scalar arguments of
+ * begin_device_training (runtime.rs:1497-1529).  Fields the device path does not cover
+ * (non-symmetric policies, ordered boosting, CTR computation, exact leaves) are absent:
+ * a caller that needs them must not open a session (the reference declines the same). */
+typedef struct {
+    int32_t loss;                 /* CBH_LOSS_* */
+    int32_t score_function;       /* CBH_SCORE_* */
+    int32_t leaf_method;          /* CBH_LEAF_* (Simple == Gradient, leaf.rs:242) */
+    int32_t depth;                /* 1..8 */
+    int32_t boosting_type_is_plain; /* must be 1 (ordered boosting declines) */
+    int32_t fold_count;           /* must be 1 */
+    int32_t approx_dim;           /* 1, or the class count for MultiClass */
+    int32_t bootstrap_type;       /* CBH_BOOT_* (describes the sampler; see grow) */
+    int32_t sample_from_host;     /* 1: grow receives a host multiplier (len n) */
+    float sample_rate;            /* Bernoulli subsample */
+    float bagging_temperature;    /* Bayesian temperature */
+    int32_t profile;              /* 1: time every kernel with HIP events */
+    double bias;                  /* starting approximant (boost_from_average) */
+    uint64_t rng_seed;            /* informational; draws come from the host RNG phase */
+    /* one-hot columns (SPEC-OH-21/24): nullable, length n_features.  A one-hot feature's
+     * candidates are the equality splits bin == v for v < real_folds[f]; float features
+     * use bin > b for b < real_folds[f]-1.  NULL real_folds: every feature has n_bins. */
+    const uint8_t* one_hot_flags;
+    const uint32_t* real_folds;
+} cbh_config;
+
+typedef struct cbh_session cbh_session;
+
+/* Open a device-resident session.  Mirrors begin_device_training (runtime.rs:1497-1529):
+ *   bins_fm    feature-major quantized matrix, bins_fm[f * n + i] < n_bins (u32 like the
+ *              reference; values must fit a byte: n_bins <= 256)
+ *   weight     per-object weight (NULL = unit weights)
+ *   scaled_l2  l2_leaf_reg * sum(weight) / n  (scale_l2_reg, leaf.rs:177)
+ * Returns CBH_OK and *out, CBH_DECLINED for an uncovered config, or an error. */
+int cbh_session_begin(const cbh_config* cfg, const uint32_t* bins_fm, const double* weight,
+                      uint64_t n, uint32_t n_features, uint32_t n_bins, double learning_rate,
+                      double scaled_l2, cbh_session** out);
+
+/* Same, with a byte-per-bin feature-major matrix (4x less host memory). */
+int cbh_session_begin_u8(const cbh_config* cfg, const uint8_t* bins_fm, const double* weight,
+                         uint64_t n, uint32_t n_features, uint32_t n_bins, double learning_rate,
+                         double scaled_l2, cbh_session** out);
+
+/* Per-tree device-resident sampling: the device regenerates exactly the sample the host
+ * bootstrap() would draw at the current host RNG phase (bootstrap.rs:402-466), so no
+ * n-length multiplier crosses PCIe.  bayesian_seed = the main-stream GenRand() the
+ * Bayesian sampler consumes; bernoulli_state = TFastRng64 raw state [x1, c1, x2, c2]
+ * before the n Bernoulli draws (rng.rs:221 raw_state). */
+typedef struct {
+    int32_t kind;                 /* CBH_BOOT_* */
+    float bagging_temperature;
+    double subsample;
+    uint64_t bayesian_seed;
+    uint64_t bernoulli_state[4];
+} cbh_tree_sampling;
+
+/* Output of one grown tree; mirrors DeviceGrownTree (runtime.rs:990-1059).  Buffers are
+ * caller-owned and sized by the caller: split_* [depth], leaf_values [2^depth * K]
+ * (row-major leaf x dim, UNscaled by the learning rate), leaf_of [n] or NULL. */
+typedef struct {
+    uint32_t* split_feature;
+    uint32_t* split_bin;
+    uint8_t* split_one_hot;
+    double* leaf_values;
+    uint32_t* leaf_of;
+    double* split_score;          /* nullable [depth]: winning score per level */
+} cbh_tree_out;
+
+/* Grow one oblivious tree.  Mirrors grow_tree_on_device (runtime.rs:1629-1638):
+ *   approx   NULL: use the session's resident approximant (the hot path); else [K][n]
+ *            host approximant uploaded for this tree
+ *   target   NULL after the first call (resident); [n] (class index for MultiClass)
+ *   sample   NULL/0, or the host multiplier control ? weight : 0 of length n (session
+ *            opened with sample_from_host)
+ *   sampling NULL, or device-resident sampling parameters for this tree
+ * The session applies approx += learning_rate * leaf_value[leaf_of] itself before the
+ * next tree (the resident update of the reference's device branch). */
+int cbh_session_grow(cbh_session* s, const double* approx, const double* target, uint64_t n,
+                     const double* sample, uint64_t n_sample, const cbh_tree_sampling* sampling,
+                     cbh_tree_out* out);
+
+/* Copy the resident approximant ([K][n]) to the host (applies any pending tree). */
+int cbh_session_read_approx(cbh_session* s, double* approx_out, uint64_t n_times_k);
+
+/* Per-session kernel timing (profile = 1) and fill traffic accounting.  Times are the
+ * sums of HIP-event durations measured on the session stream. */
+typedef struct {
+    double fill_ms;               /* histogram fill kernels */
+    double derive_ms;             /* sibling subtraction */
+    double score_ms;              /* split scoring + argmax */
+    double partition_ms;          /* leaf update + stable compaction */
+    double leaf_ms;               /* leaf reduction + values */
+    double prepare_ms;            /* ders, bootstrap, approx update */
+    double total_ms;              /* all of the above */
+    uint64_t fill_launches;
+    uint64_t fill_rows;           /* rows visited by fill launches (sum of V) */
+    uint64_t fill_row_features;   /* sum of V * n_features */
+    double fill_bytes;            /* algorithmic bytes V*(W*4 + 8*(K+1) + 4) + H */
+    uint64_t trees;
+} cbh_stats;
+
+int cbh_session_stats(const cbh_session* s, cbh_stats* out);
+void cbh_session_reset_stats(cbh_session* s);
+
+/* Release the session.  Mirrors end_device_training (runtime.rs:1648). */
+int cbh_session_end(cbh_session* s);
+
+/* Mirrors compute_gradients (runtime.rs:1431-1437): dim-major der1/der2 on the device.
+ * For MultiClass der2 is the packed per-object Hessian [n][K(K+1)/2]. */
+int cbh_compute_gradients(int32_t loss, const double* approx, const double* target, uint64_t n,
+                          uint32_t approx_dim, double* der1, double* der2);
+
+/* ---- kernel-level entry points (host buffers in/out), each kernel checked alone ---- */
+
+/* Histogram of one leaf set: rows listed in idx (NULL = all n in order) with leaf slot
+ * slot_of_row[i] (NULL = 0), score channels der [K][n], w [n].  Output exact sums as f64
+ * in [n_slots][F][n_bins][K+1] (channel K = weight). */
+int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t n_features, uint32_t n_bins,
+                   const double* der, const double* w, uint32_t K, const uint32_t* slot_of_row,
+                   uint32_t n_slots, double* hist_out);
+
+/* Device bootstrap (bootstrap.rs:141-184): sample weights and control mask for n rows. */
+int cbh_bootstrap(const cbh_tree_sampling* sampling, uint64_t n, double* sample_weight,
+                  uint8_t* control);
+
+/* Version / build information. */
+const char* cbh_version(void);
+const char* cbh_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

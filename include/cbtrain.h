@@ -1,0 +1,61 @@
+/*
+ * cbtrain.h -- host mirror of the caller side of the seam: the device branch of
+ * cb-train's boosting loop (crates/cb-train/src/boosting.rs:6532-7300) driving the
+ * cbhip.h session exactly as cb_train::train does:
+ *   starting approx (boosting.rs:1871), scale_l2_reg (leaf.rs:177),
+ *   per tree: PRE_TREE_DRAWS, bootstrap phase on the host RNG (bootstrap.rs:402),
+ *   grow_tree_on_device, replay of the CPU grower's per-level draws
+ *   (crates/cb-train/src/device_draw_replay.rs), POST_TREE_EXTRA_DRAWS, model leaf
+ *   values scaled by the learning rate (boosting.rs:2879-2881).
+ * The reference's caller is Rust; Rust is not available in this build, so the caller is
+ * restated in C++ above the C-ABI.  It only calls functions declared in cbhip.h.
+ */
+#ifndef CBTRAIN_H
+#define CBTRAIN_H
+#include <stdint.h>
+
+#include "cbhip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    int32_t loss;                 /* CBH_LOSS_* */
+    int32_t score_function;       /* CBH_SCORE_* */
+    int32_t leaf_method;          /* CBH_LEAF_* */
+    int32_t depth;
+    int32_t bootstrap_type;       /* CBH_BOOT_* */
+    int32_t boost_from_average;
+    int32_t approx_dim;           /* class count for MultiClass, else 1 */
+    int32_t profile;
+    double learning_rate;
+    double l2_leaf_reg;
+    double subsample;
+    float bagging_temperature;
+    float pad_;
+    uint64_t random_seed;
+} cbt_params;
+
+typedef struct cbt_trainer cbt_trainer;
+
+/* Open: upload the u8 feature-major bins once (begin_device_training). */
+int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t n_features,
+             uint32_t n_bins, const uint32_t* real_folds, const uint8_t* one_hot_flags,
+             const double* target, const double* weight, cbt_trainer** out);
+
+/* One boosting iteration.  Outputs (nullable): split_feature/split_bin/split_one_hot
+ * [depth]; leaf_values [K][2^depth] as stored in the model (learning-rate scaled). */
+int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8_t* split_one_hot,
+             double* leaf_values);
+
+int cbt_read_approx(cbt_trainer* t, double* approx_out);     /* [K][n] */
+int cbt_stats(const cbt_trainer* t, cbh_stats* out);
+void cbt_reset_stats(cbt_trainer* t);
+double cbt_bias(const cbt_trainer* t);
+void cbt_close(cbt_trainer* t);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

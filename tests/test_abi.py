@@ -1,0 +1,93 @@
+"""CPU-side checks of the C-ABI library: it loads, and it exports every function the
+public headers declare (no compute call is made -- there is no GPU here)."""
+import os
+import re
+import subprocess
+
+import pytest
+
+import catboost_rs_amd as cb
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    names = set()
+    for h in ("cbhip.h", "cbtrain.h"):
+        src = open(os.path.join(ROOT, "include", h)).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(cb[ht]_\w+)\s*\(", src, re.M):
+            names.add(m.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(cb.LIB_PATH):
+        pytest.fail("libcbhip.so is not built (run __graft_entry__.build())")
+    return cb.load()
+
+
+def test_library_loads(lib):
+    assert lib.cbh_version().decode().startswith("cbhip")
+
+
+def test_every_declared_symbol_is_exported(lib):
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    assert declared == set(cb.EXPORTS), (declared ^ set(cb.EXPORTS))
+    out = subprocess.run(["nm", "-D", "--defined-only", cb.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if l.strip()}
+    missing = declared - exported
+    assert not missing, f"declared but not exported: {sorted(missing)}"
+
+
+def test_library_is_gfx950_only():
+    out = subprocess.run(["strings", "-n", "8", cb.LIB_PATH], capture_output=True, text=True).stdout
+    assert "gfx950" in out
+    assert "gfx942" not in out and "gfx90a" not in out
+
+
+def test_errors_without_device_are_reported_not_faulting(lib):
+    """With no GPU, opening a session must fail with a status code, never crash."""
+    import ctypes as C
+    import numpy as np
+    if os.environ.get("HIP_VISIBLE_DEVICES") is None and os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU may be present; this check is for GPU-less hosts")
+    bins = np.zeros((2, 8), np.uint8)
+    cfg = cb.Config(loss=0, score_function=0, leaf_method=0, depth=2, boosting_type_is_plain=1,
+                    fold_count=1, approx_dim=1)
+    s = C.c_void_p()
+    rc = lib.cbh_session_begin_u8(C.byref(cfg), bins.ctypes.data_as(C.c_void_p), None, 8, 2, 4,
+                                  0.1, 3.0, C.byref(s))
+    assert rc != 0
+
+
+def test_config_decline_paths(lib):
+    """Uncovered configs decline (status 1) before touching the device, like the reference's
+    trait defaults (runtime.rs:1497-1529); invalid shapes are typed errors."""
+    import ctypes as C
+    import numpy as np
+    bins = np.zeros((2, 8), np.uint8)
+    s = C.c_void_p()
+
+    def begin(**kw):
+        base = dict(loss=0, score_function=0, leaf_method=0, depth=2, boosting_type_is_plain=1,
+                    fold_count=1, approx_dim=1)
+        base.update(kw)
+        cfg = cb.Config(**base)
+        return lib.cbh_session_begin_u8(C.byref(cfg), bins.ctypes.data_as(C.c_void_p), None, 8, 2, 4,
+                                        0.1, 3.0, C.byref(s))
+
+    assert begin(boosting_type_is_plain=0) == cb.DECLINED
+    assert begin(fold_count=2) == cb.DECLINED
+    assert begin(depth=9) == cb.DECLINED
+    assert begin(loss=2, approx_dim=3, leaf_method=0) == cb.DECLINED  # MultiClass needs Newton
+    assert begin(approx_dim=2) == -5
+    bad = np.full((2, 8), 7, np.uint8)
+    cfg = cb.Config(loss=0, score_function=0, leaf_method=0, depth=2, boosting_type_is_plain=1,
+                    fold_count=1, approx_dim=1)
+    rc = lib.cbh_session_begin_u8(C.byref(cfg), bad.ctypes.data_as(C.c_void_p), None, 8, 2, 4, 0.1,
+                                  3.0, C.byref(s))
+    assert rc == -2  # bin >= n_bins -> OutOfRange
