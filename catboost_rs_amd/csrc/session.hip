@@ -405,9 +405,11 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         long long* cur = s->hist[level & 1];
         long long* par = s->hist[(level + 1) & 1];
         const uint32_t n_leaves = 1u << level;
-        // ---- fill ----
-        CHECK(s->stage_begin(kStFill));
+        // ---- fill (the histogram it accumulates into is zeroed first, timed apart) ----
+        CHECK(s->stage_begin(kStPrepare));
         CHECK(launch_zero(cur, per_leaf * n_leaves, st));
+        CHECK(s->stage_end());
+        CHECK(s->stage_begin(kStFill));
         uint32_t dense_chunks = 0, slots;
         if (level == 0) {
             dense_chunks = (uint32_t)((n + kChunkRows - 1) / kChunkRows);

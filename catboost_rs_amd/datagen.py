@@ -35,11 +35,16 @@ def _borders(col: np.ndarray, n_borders: int, seed: int) -> np.ndarray:
 
 
 def _quantize(col: np.ndarray, borders: np.ndarray) -> np.ndarray:
-    # count of borders strictly below the value == searchsorted(..., side="left")
+    # count of borders strictly below the value == searchsorted(..., side="left"); borders
+    # are f32 values, so comparing f32 columns against f32 borders is exact
+    if col.dtype == np.float32:
+        return np.searchsorted(borders.astype(np.float32), col, side="left").astype(np.uint8)
     return np.searchsorted(borders, col.astype(np.float64), side="left").astype(np.uint8)
 
 
-def _columns(n, F, make_col, n_borders, seed, threads=None):
+def _columns(n, F, make_col, n_borders, seed, threads=None, keep_cols=None):
+    """Quantize F generated columns; only the columns listed in keep_cols stay in memory."""
+    keep_cols = set(range(F)) if keep_cols is None else set(keep_cols)
     bins = np.empty((F, n), np.uint8)
     nb = np.empty(F, np.uint32)
     keep = {}
@@ -49,12 +54,13 @@ def _columns(n, F, make_col, n_borders, seed, threads=None):
         b = _borders(col, n_borders, seed * 7919 + f)
         bins[f] = _quantize(col, b)
         nb[f] = b.size
-        return f, col
+        return f, (col if f in keep_cols else None)
 
     threads = threads or min(16, os.cpu_count() or 4)
     with cf.ThreadPoolExecutor(threads) as ex:
         for f, col in ex.map(work, range(F)):
-            keep[f] = col
+            if col is not None:
+                keep[f] = col
     return bins, nb, keep
 
 
@@ -66,7 +72,7 @@ def config1(scale=1.0, seed=0):
     X = g.standard_normal((n, F)).astype(np.float32)
     w = g.uniform(-1, 1, F)
     y = X.astype(np.float64) @ w + 0.1 * g.standard_normal(n)
-    bins, nb, _ = _columns(n, F, lambda f: X[:, f], 128, seed)
+    bins, nb, _ = _columns(n, F, lambda f: np.ascontiguousarray(X[:, f]), 128, seed, keep_cols=())
     return dict(name="config1", bins=bins, n_borders=nb, target=y,
                 params=dict(loss="RMSE", depth=6, iterations=100, learning_rate=0.1,
                             l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient",
@@ -84,10 +90,10 @@ def config2(scale=1.0, seed=1, n_rows=None, n_features=200):
         g = np.random.default_rng([seed, f])
         c = g.standard_normal(n, dtype=np.float32)
         if f >= half:
-            c = np.exp(c)
+            np.exp(c, out=c)
         return c
 
-    bins, nb, cols = _columns(n, F, make_col, 254, seed)
+    bins, nb, cols = _columns(n, F, make_col, 254, seed, keep_cols=range(20))
     g = np.random.default_rng([seed, 10_000])
     w = g.uniform(-1, 1, 20)
     logit = np.zeros(n)
@@ -116,7 +122,7 @@ def config5(scale=1.0, seed=5, n_rows=None, n_features=4096, n_classes=10):
         c[g.random(n) < 0.7] = 0.0
         return c
 
-    bins, nb, cols = _columns(n, F, make_col, 64, seed)
+    bins, nb, cols = _columns(n, F, make_col, 64, seed, keep_cols=range(32))
     g = np.random.default_rng([seed, 99_999])
     Wc = g.standard_normal((min(32, F), n_classes))
     s = np.zeros((n, n_classes))

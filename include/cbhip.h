@@ -132,7 +132,7 @@ typedef struct {
     double score_ms;              /* split scoring + argmax */
     double partition_ms;          /* leaf update + stable compaction */
     double leaf_ms;               /* leaf reduction + values */
-    double prepare_ms;            /* ders, bootstrap, approx update */
+    double prepare_ms;            /* ders, bootstrap, approx update, histogram zeroing */
     double total_ms;              /* all of the above */
     uint64_t fill_launches;
     uint64_t fill_rows;           /* rows visited by fill launches (sum of V) */
