@@ -87,6 +87,27 @@ __host__ __device__ inline double rng_real1(Rng& r) {
     return (double)(rng_gen(r) >> 11) * (1.0 / 9007199254740991.0);
 }
 
+// Affine jump tables of the LCG: fine[j] = (A^j, (A^j-1)/(A-1)) for j < 1024 and
+// coarse[q] = the same for j = 1024 q, q < n_coarse.
+inline void make_jump_tables(uint64_t n_coarse, uint64_t* fine_a, uint64_t* fine_d,
+                             uint64_t* coarse_a, uint64_t* coarse_d) {
+    uint64_t a = 1, d = 0;
+    for (int j = 0; j < 1024; ++j) {
+        fine_a[j] = a;
+        fine_d[j] = d;
+        d = d + a;
+        a = a * kLcgA;
+    }
+    const uint64_t a1024 = a, d1024 = d;
+    uint64_t ca = 1, cd = 0;
+    for (uint64_t q = 0; q < n_coarse; ++q) {
+        coarse_a[q] = ca;
+        coarse_d[q] = cd;
+        cd = cd * a1024 + d1024;
+        ca = ca * a1024;
+    }
+}
+
 // FastLogf (crates/cb-train/src/fast_approx.rs:154-177).  Every operation is a single
 // IEEE f32 op in the reference order; the library is compiled with -ffp-contract=off so
 // no multiply-add is fused.

@@ -71,23 +71,13 @@ __global__ void softmax_ders_kernel(const double* __restrict__ a, const double* 
     }
 }
 
-__global__ void bootstrap_kernel(SampleParams smp, uint64_t n, double* __restrict__ sw,
+__global__ void bootstrap_kernel(SampleParams smp, JumpTabs jt, uint64_t n, double* __restrict__ sw,
                                  uint8_t* __restrict__ ctrl) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
-        double s = 1.0;
-        bool c = true;
-        if (smp.kind == 1) {
-            Rng r = rng_from_seed(smp.bayes_seed + i / 1000);
-            rng_advance(r, 10 + i % 1000);
-            const double u = rng_real1(r);
-            const float bw = -fast_logf((float)u + 0.0f);
-            s = smp.temperature == 1.0f ? (double)bw : (double)powf(bw, smp.temperature);
-        } else if (smp.kind == 2) {
-            Rng r = smp.bern;
-            rng_advance(r, i);
-            c = rng_real1(r) < smp.rate;
-        }
+        double s;
+        bool c;
+        sample_row(smp, jt, i, s, c);
         sw[i] = s;
         ctrl[i] = c ? 1 : 0;
     }
@@ -110,13 +100,16 @@ unsigned grid_of(uint64_t work, unsigned block) {
 int fail2(int code, const std::string& msg) { return cbh_internal_fail(code, msg); }
 
 template <int C>
-int run_fill(const uint32_t* rows, uint32_t W, uint64_t n, const uint32_t* idx, const Chunk* chunks,
-             const LevelPlan* plan, uint32_t dense_chunks, const double* sstat, const Scales* sc,
-             const uint32_t* tile_w0, uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t slots,
-             size_t lds, long long* hist) {
-    HIP_OK(hipFuncSetAttribute((const void*)fill_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    fill_kernel<C><<<slots * n_tiles, 1024, lds, 0>>>(rows, W, n, idx, chunks, plan, 8192, dense_chunks,
-                                                      sstat, sc, tile_w0, n_tiles, F, B, slots, hist);
+int run_fill(const uint32_t* rows, uint32_t W, uint64_t n, const uint32_t* idx,
+             const Chunk* chunks, const LevelPlan* plan, uint32_t dense_chunks, double* sstat,
+             const Scales* sc, const FillTiles& ft, uint32_t F, uint32_t B, uint32_t slots,
+             long long* hist) {
+    quantize_stats_kernel<C><<<grid_of(n * C, 256), 256>>>(sstat, n, sc);
+    HIP_OK(hipFuncSetAttribute((const void*)fill_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)ft.lds_bytes));
+    fill_kernel<C><<<slots * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, n, idx, chunks, plan, 8192,
+                                                                 dense_chunks, (const long long*)sstat,
+                                                                 ft.n_tiles, ft.tw, F, B, slots, hist);
     HIP_OK(hipGetLastError());
     return CBH_OK;
 }
@@ -169,9 +162,16 @@ int cbh_bootstrap(const cbh_tree_sampling* sampling, uint64_t n, double* sample_
     if (smp.kind == CBH_BOOT_BAYESIAN && sampling->bagging_temperature == 0.0f) smp.kind = 0;
     DBuf<double> sw;
     DBuf<uint8_t> c;
+    DBuf<uint64_t> jump;
+    const uint64_t n_coarse = (n >> 10) + 2;
+    std::vector<uint64_t> h(2048 + 2 * n_coarse);
+    make_jump_tables(n_coarse, h.data(), h.data() + 1024, h.data() + 2048, h.data() + 2048 + n_coarse);
+    HIP_OK(jump.alloc(h.size()));
+    HIP_OK(hipMemcpy(jump.p, h.data(), sizeof(uint64_t) * h.size(), hipMemcpyHostToDevice));
+    const JumpTabs jt{jump.p, jump.p + 1024, jump.p + 2048, jump.p + 2048 + n_coarse};
     HIP_OK(sw.alloc(n));
     HIP_OK(c.alloc(n));
-    bootstrap_kernel<<<grid_of(n, 256), 256>>>(smp, n, sw.p, c.p);
+    bootstrap_kernel<<<grid_of(n, 256), 256>>>(smp, jt, n, sw.p, c.p);
     HIP_OK(hipGetLastError());
     HIP_OK(hipMemcpy(sample_weight, sw.p, sizeof(double) * n, hipMemcpyDeviceToHost));
     HIP_OK(hipMemcpy(control, c.p, n, hipMemcpyDeviceToHost));
@@ -222,18 +222,11 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t B, c
     int lds_max = 0, dev = 0;
     HIP_OK(hipGetDevice(&dev));
     HIP_OK(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
-    const size_t budget = std::min<size_t>((size_t)lds_max, 160 * 1024);
-    const size_t per_feature = (size_t)B * C * 8;
-    const size_t max_words = budget / (per_feature * 4);
-    if (max_words == 0) return fail2(CBH_ERR_UNSUPPORTED, "histogram line too wide for LDS");
-    const uint32_t n_tiles = (uint32_t)((W + max_words - 1) / max_words);
-    const uint32_t tw = (W + n_tiles - 1) / n_tiles;
-    std::vector<uint32_t> w0(n_tiles + 1);
-    for (uint32_t t = 0; t <= n_tiles; ++t) w0[t] = std::min(W, t * tw);
-    const size_t lds = (size_t)std::min<uint32_t>(tw * 4, F) * per_feature;
+    const FillTiles ft = plan_fill_tiles(F, B, C, std::min<size_t>((size_t)lds_max, 160 * 1024));
+    if (ft.n_tiles == 0) return fail2(CBH_ERR_UNSUPPORTED, "histogram line too wide for LDS");
 
     DBuf<uint8_t> cols;
-    DBuf<uint32_t> rows, didx, dw0;
+    DBuf<uint32_t> rows, didx;
     DBuf<double> dder, dw, sstat, dout;
     DBuf<Chunk> dch;
     DBuf<LevelPlan> dplan;
@@ -245,14 +238,12 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t B, c
     HIP_OK(dder.alloc(n * K));
     HIP_OK(dw.alloc(n));
     HIP_OK(sstat.alloc(n * C));
-    HIP_OK(dw0.alloc(n_tiles + 1));
     HIP_OK(dsc.alloc(1));
     HIP_OK(hist.alloc(cells));
     HIP_OK(dout.alloc(cells));
     HIP_OK(hipMemcpy(cols.p, bins_fm, n * F, hipMemcpyHostToDevice));
     HIP_OK(hipMemcpy(dder.p, der, sizeof(double) * n * K, hipMemcpyHostToDevice));
     HIP_OK(hipMemcpy(dw.p, w, sizeof(double) * n, hipMemcpyHostToDevice));
-    HIP_OK(hipMemcpy(dw0.p, w0.data(), sizeof(uint32_t) * (n_tiles + 1), hipMemcpyHostToDevice));
     HIP_OK(hipMemcpy(dsc.p, &sc, sizeof(Scales), hipMemcpyHostToDevice));
     HIP_OK(hipMemset(hist.p, 0, cells * sizeof(long long)));
     pack_rows_kernel<<<grid_of(n * W, 256), 256>>>(cols.p, n, F, W, rows.p);
@@ -273,17 +264,17 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t B, c
         dense_chunks = (uint32_t)((n + 8191) / 8192);
         slots = dense_chunks;
     }
-    slots = std::min<uint32_t>(slots, std::max<uint32_t>(8, 1024 / n_tiles));
+    slots = std::min<uint32_t>(slots, std::max<uint32_t>(8, 2048 / ft.n_tiles));
     slots = (slots + 7) / 8 * 8;
     int rc;
     switch (C) {
-#define CASE(c) case c: rc = run_fill<c>(rows.p, W, n, slot_of_row ? didx.p : nullptr, dch.p, dplan.p, dense_chunks, sstat.p, dsc.p, dw0.p, n_tiles, F, B, slots, lds, hist.p); break;
+#define CASE(c) case c: rc = run_fill<c>(rows.p, W, n, slot_of_row ? didx.p : nullptr, dch.p, dplan.p, dense_chunks, sstat.p, dsc.p, ft, F, B, slots, hist.p); break;
         CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(9) CASE(11) CASE(13) CASE(17)
 #undef CASE
         default: return fail2(CBH_ERR_UNSUPPORTED, "K has no compiled fill variant");
     }
     if (rc != CBH_OK) return rc;
-    hist_to_f64_kernel<<<grid_of(cells, 256), 256>>>(hist.p, cells, C, dsc.p, dout.p);
+    hist_to_f64_kernel<<<grid_of(cells, 256), 256>>>(hist.p, cells, C, F, B, dsc.p, dout.p);
     HIP_OK(hipGetLastError());
     HIP_OK(hipMemcpy(hist_out, dout.p, sizeof(double) * cells, hipMemcpyDeviceToHost));
     return CBH_OK;

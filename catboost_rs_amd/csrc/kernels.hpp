@@ -5,12 +5,16 @@
 //                          feature 4w+k); a fill reads only the words of its feature tile
 //   cols   u8  [F][n]      feature-major bins, read once per level by the split kernel
 //   sstat  f64 [n][K+1]    score channels per row: K weighted, sampled derivatives, then the
-//                          sampled weight (zero for rows outside the bootstrap sample)
+//                          sampled weight (zero for rows outside the bootstrap sample);
+//                          quantized in place to int64 fixed point once the tree's scales
+//                          are known
 //   leaf   u16 [n]         leaf index, bit 15 set for rows outside the score sample
 //   idx    u32 [<= n]      row ids of the directly built children, grouped by parent leaf,
 //                          ascending row order inside each group (stable partition)
-//   hist   i64 [2^l][F][B][K+1]  exact fixed-point histograms of level l
+//   hist   i64 [2^l][K+1][F][B]  exact fixed-point histograms of level l (channel planes)
 #pragma once
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace cbh {
@@ -117,22 +121,64 @@ __device__ __forceinline__ void softmax_probs(const double* a, double* p) {
 }
 
 // ---------------------------------------------------------------------------------
-// Per-tree preparation: apply the previous tree (approx += lr * leaf), derivatives,
-// bootstrap sample (bootstrap.rs:141-184), score channels, leaf flags, scale bounds.
-// One thread per row; the Bayesian stream of row i is block (i / 1000) of the per-tree
-// seed advanced by 10 + (i % 1000) draws, the Bernoulli draw of row i is the main stream
-// advanced by i draws -- both by the LCG closed-form jump, so rows are independent.
+// RNG stream positions.  Advancing a PCG/LCG stream by j draws is the affine map
+// x -> A^j x + c (A^j - 1)/(A - 1); the session precomputes (A^j, (A^j-1)/(A-1)) for
+// j < 1024 (fine) and for j = 1024 q (coarse), so a row's stream position costs two
+// table lookups and four 64-bit multiplies instead of a log-time jump.
 // ---------------------------------------------------------------------------------
+struct JumpTabs {
+    const uint64_t* fine_a;
+    const uint64_t* fine_d;
+    const uint64_t* coarse_a;
+    const uint64_t* coarse_d;
+};
+
+__device__ __forceinline__ void rng_jump(Rng& r, uint64_t a, uint64_t d) {
+    r.x1 = a * r.x1 + r.c1 * d;
+    r.x2 = a * r.x2 + r.c2 * d;
+}
+
+// Bootstrap sample of row i (bootstrap.rs:141-184): Bayesian rows of block b = i / 1000
+// draw from TFastRng64(seed + b) advanced by 10 + (i % 1000); Bernoulli row i is draw i of
+// the main stream.
+__device__ __forceinline__ void sample_row(const SampleParams& smp, const JumpTabs& jt, uint64_t i,
+                                           double& s, bool& ctrl) {
+    s = 1.0;
+    ctrl = true;
+    if (smp.kind == 1) {
+        Rng r = rng_from_seed(smp.bayes_seed + i / 1000);
+        const uint32_t j = 10u + (uint32_t)(i % 1000);
+        rng_jump(r, jt.fine_a[j], jt.fine_d[j]);
+        const double u = rng_real1(r);
+        const float bw = -fast_logf((float)u + 0.0f);  // 1e-100f rounds to 0 in f32
+        s = smp.temperature == 1.0f ? (double)bw : (double)powf(bw, smp.temperature);
+    } else if (smp.kind == 2) {
+        Rng r = smp.bern;
+        rng_jump(r, jt.fine_a[i & 1023u], jt.fine_d[i & 1023u]);
+        rng_jump(r, jt.coarse_a[i >> 10], jt.coarse_d[i >> 10]);
+        ctrl = rng_real1(r) < smp.rate;
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Per-tree preparation: apply the previous tree (approx += lr * leaf), derivatives,
+// bootstrap sample, score channels, leaf flags, and per-block partial bounds for the
+// fixed-point scales (summed deterministically by scales_kernel).
+// ---------------------------------------------------------------------------------
+constexpr int kPrepBlocks = 2048;
+constexpr int kPartials = 8;   // per block: 4 bounds, sampled rows, 3 spare
+
 template <int K>
 static __global__ __launch_bounds__(256) void prepare_kernel(
     uint64_t n, int loss, double* __restrict__ approx, const double* __restrict__ target,
     const double* __restrict__ weight, uint16_t* __restrict__ leaf,
     const double* __restrict__ pending /* [leaves][K] lr-scaled, nullable */,
-    SampleParams smp, const double* __restrict__ host_sample,
-    double* __restrict__ sstat /* [n][K+1] */, int newton, Bounds* __restrict__ bounds) {
+    SampleParams smp, JumpTabs jt, const double* __restrict__ host_sample,
+    double* __restrict__ sstat /* [n][K+1] */, int newton,
+    unsigned long long* __restrict__ partials /* [gridDim.x][kPartials] */) {
     constexpr int C = K + 1;
-    unsigned long long acc[kNumScales] = {0, 0, 0, 0};
-    unsigned long long sampled = 0;
+    __shared__ unsigned long long red[4][kPartials];
+    unsigned long long acc[kPartials] = {0, 0, 0, 0, 0, 0, 0, 0};
     const double bscale = (double)(1 << kBoundShift);
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
@@ -140,7 +186,7 @@ static __global__ __launch_bounds__(256) void prepare_kernel(
 #pragma unroll
         for (int d = 0; d < K; ++d) a[d] = approx[(size_t)d * n + i];
         if (pending) {
-            uint32_t l = leaf[i] & 0x7FFFu;
+            const uint32_t l = leaf[i] & 0x7FFFu;
 #pragma unroll
             for (int d = 0; d < K; ++d) {
                 a[d] += pending[(size_t)l * K + d];
@@ -161,71 +207,93 @@ static __global__ __launch_bounds__(256) void prepare_kernel(
             softmax_probs<K>(a, p);
 #pragma unroll
             for (int d = 0; d < K; ++d) d1[d] = -p[d];
-            int tc = (int)t;
+            const int tc = (int)t;
             if (tc >= 0 && tc < K) d1[tc] += 1.0;
             h_leaf = fabs(w);
         }
-        // bootstrap sample
-        double s = 1.0;
-        bool ctrl = true;
+        double s;
+        bool ctrl;
         if (host_sample) {
             s = host_sample[i];
-        } else if (smp.kind == 1) {
-            Rng r = rng_from_seed(smp.bayes_seed + i / 1000);
-            rng_advance(r, 10 + i % 1000);
-            double u = rng_real1(r);
-            float bw = -fast_logf((float)u + 0.0f);  // 1e-100f rounds to 0 in f32
-            s = smp.temperature == 1.0f ? (double)bw : (double)powf(bw, smp.temperature);
-        } else if (smp.kind == 2) {
-            Rng r = smp.bern;
-            rng_advance(r, i);
-            ctrl = rng_real1(r) < smp.rate;
+            ctrl = true;
+        } else {
+            sample_row(smp, jt, i, s, ctrl);
         }
         double mx_sd = 0.0, mx_ld = 0.0;
 #pragma unroll
         for (int d = 0; d < K; ++d) {
-            double wd = d1[d] * w;                   // weighted_der1 (boosting.rs:7479)
-            double sd = ctrl ? wd * s : 0.0;         // score_weighted_der1 (:7709)
+            const double wd = d1[d] * w;             // weighted_der1 (boosting.rs:7479)
+            const double sd = ctrl ? wd * s : 0.0;   // score_weighted_der1 (:7709)
             sstat[i * C + d] = sd;
             mx_sd = fmax(mx_sd, fabs(sd));
             mx_ld = fmax(mx_ld, fabs(wd));
         }
-        double sw = ctrl ? w * s : 0.0;              // score_weights (:7728)
+        const double sw = ctrl ? w * s : 0.0;        // score_weights (:7728)
         sstat[i * C + K] = sw;
         leaf[i] = sw == 0.0 ? (uint16_t)0x8000u : (uint16_t)0;
-        sampled += sw != 0.0;
         acc[kScoreDer] += (unsigned long long)ceil(mx_sd * bscale);
         acc[kScoreW] += (unsigned long long)ceil(fabs(sw) * bscale);
         acc[kLeafDer] += (unsigned long long)ceil(mx_ld * bscale);
         acc[kLeafW] += (unsigned long long)ceil(h_leaf * bscale);
+        acc[4] += sw != 0.0;
     }
+    const uint32_t wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int k = 0; k < kNumScales; ++k) acc[k] = wave_sum_u64(acc[k]);
-    sampled = wave_sum_u64(sampled);
-    if (lane_id() == 0) {
-#pragma unroll
-        for (int k = 0; k < kNumScales; ++k) atomicAdd(&bounds->sum_abs[k], acc[k]);
-        atomicAdd(&bounds->sampled_rows, sampled);
+    for (int k = 0; k < kPartials; ++k) {
+        const unsigned long long v = wave_sum_u64(acc[k]);
+        if (lane_id() == 0) red[wave][k] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < kPartials) {
+        unsigned long long v = 0;
+        for (int w = 0; w < 4; ++w) v += red[w][threadIdx.x];
+        partials[(size_t)blockIdx.x * kPartials + threadIdx.x] = v;
     }
 }
 
-// Pick S per slot so that 2^S * sum|v| <= 2^61 (no partial sum of rounded values can
-// overflow int64) -- a single thread.
-static __global__ void scales_kernel(const Bounds* __restrict__ b, Scales* __restrict__ sc) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// Sum the per-block partials (integers: exact in any order) and pick S per slot so that
+// 2^S * sum|v| <= 2^61: no partial sum of rounded values can overflow int64.
+static __global__ __launch_bounds__(256) void scales_kernel(const unsigned long long* __restrict__ partials,
+                                                           uint32_t n_blocks, Bounds* __restrict__ b,
+                                                           Scales* __restrict__ sc) {
+    __shared__ unsigned long long red[256][5];
+    unsigned long long acc[5] = {0, 0, 0, 0, 0};
+    for (uint32_t i = threadIdx.x; i < n_blocks; i += blockDim.x)
+        for (int k = 0; k < 5; ++k) acc[k] += partials[(size_t)i * kPartials + k];
+    for (int k = 0; k < 5; ++k) red[threadIdx.x][k] = acc[k];
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int k = 0; k < 5; ++k) {
+        unsigned long long v = 0;
+        for (uint32_t tI = 0; tI < blockDim.x; ++tI) v += red[tI][k];
+        acc[k] = v;
+    }
+    for (int k = 0; k < kNumScales; ++k) b->sum_abs[k] = acc[k];
+    b->sampled_rows = acc[4];
     for (int k = 0; k < kNumScales; ++k) {
-        double bound = (double)b->sum_abs[k] / (double)(1 << kBoundShift);
-        int e = 0;
-        if (bound > 0.0) {
-            frexp(bound, &e);             // bound < 2^e
-        } else {
-            e = -20;
-        }
+        const double bound = (double)acc[k] / (double)(1 << kBoundShift);
+        int e = -20;
+        if (bound > 0.0) frexp(bound, &e);   // bound < 2^e
         int s = 61 - e;
         if (s > 100) s = 100;
         sc->shift[k] = s;
         sc->mul[k] = ldexp(1.0, s);
         sc->inv[k] = ldexp(1.0, -s);
+    }
+}
+
+// Score channels f64 -> fixed point, in place ([n][C] doubles become [n][C] int64), once
+// per tree, so the fill's inner loop only moves integers.
+template <int C>
+static __global__ void quantize_stats_kernel(double* __restrict__ sstat, uint64_t n,
+                                             const Scales* __restrict__ sc) {
+    const double md = sc->mul[kScoreDer], mw = sc->mul[kScoreW];
+    long long* out = (long long*)sstat;
+    const uint64_t total = n * C;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t ch = (uint32_t)(i % C);
+        out[i] = to_fixed(sstat[i], ch == C - 1 ? mw : md);
     }
 }
 
@@ -237,28 +305,58 @@ static __global__ void scales_kernel(const Bounds* __restrict__ b, Scales* __res
 // bits).  The blockIdx -> (tile, chunk slot) map keeps all tiles of a chunk slot on one
 // XCD (blocks are dealt to the 8 XCDs round-robin), so the rows a chunk reads are fetched
 // into that XCD's L2 once and shared by its tiles.
+//
+// Lane layout (word per lane): a lane takes one 4-byte word (4 features) of a row; the
+// TW lanes of a row cover the tile's words and a 1024-thread workgroup covers
+// 1024 / TW rows per pass.  The VALU work per LDS atomic is a byte extract and an address
+// add, so the loop runs at the LDS atomic rate: 64-bit LDS atomics with scattered
+// addresses are the bound of this kernel on gfx950 (the stats are pre-quantized int64
+// per row, so nothing is converted in the loop).  LDS histogram layout is [ch][f][bin].
+// Every lane keeps kFillRows rows in flight.
 // ---------------------------------------------------------------------------------
+constexpr int kFillRows = 4;
+
+struct FillTiles {       // host-side plan of the feature tiles
+    uint32_t n_tiles;
+    uint32_t tw;         // words (4 features) per tile
+    uint32_t pad;
+    uint32_t pad2;
+    size_t lds_bytes;
+};
+
+inline FillTiles plan_fill_tiles(uint32_t F, uint32_t B, uint32_t C, size_t budget) {
+    FillTiles t{0, 0, 0, 0, 0};
+    const uint32_t W = (F + 3) / 4;
+    const size_t per_word = (size_t)4 * B * C * sizeof(long long);
+    const size_t max_words = budget / per_word;
+    if (max_words == 0) return t;
+    t.n_tiles = (uint32_t)((W + max_words - 1) / max_words);
+    t.tw = (W + t.n_tiles - 1) / t.n_tiles;       // balanced tiles
+    t.n_tiles = (W + t.tw - 1) / t.tw;
+    t.lds_bytes = (size_t)std::min<uint32_t>(4 * t.tw, F) * B * C * sizeof(long long);
+    return t;
+}
+
 template <int C>
 static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t* __restrict__ rows, uint32_t W, uint64_t n,
     const uint32_t* __restrict__ idx,                  // null: dense rows [0, n)
     const Chunk* __restrict__ chunks, const LevelPlan* __restrict__ plan,
     uint32_t dense_chunk_rows, uint32_t dense_n_chunks,
-    const double* __restrict__ sstat, const Scales* __restrict__ sc,
-    const uint32_t* __restrict__ tile_w0, uint32_t n_tiles, uint32_t F, uint32_t B,
+    const long long* __restrict__ sfix, uint32_t n_tiles, uint32_t tw, uint32_t F, uint32_t B,
     uint32_t n_slots, long long* __restrict__ hist) {
     extern __shared__ long long lds[];
-    constexpr int K = C - 1;
+    constexpr int U = kFillRows;
     const uint32_t b = blockIdx.x;
     const uint32_t xcd = b & 7u, q = b >> 3;
     const uint32_t t = q % n_tiles;
     const uint32_t g = (q / n_tiles) * 8u + xcd;
-    const uint32_t w0 = tile_w0[t], w1 = tile_w0[t + 1];
-    const uint32_t TW = w1 - w0;
+    const uint32_t w0 = t * tw;
+    const uint32_t TW = min(tw, W - w0);
     const uint32_t f0 = 4u * w0;
-    const uint32_t f1 = min(4u * w1, F);
-    const uint32_t TF = f1 - f0;
-    const uint32_t cells = TF * B * C;
+    const uint32_t TF = min(4u * TW, F - f0);
+    const uint32_t plane = TF * B;                      // cells of one channel plane
+    const uint32_t cells = plane * C;
     for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) lds[i] = 0;
     __syncthreads();
     const uint32_t rows_per_pass = blockDim.x / TW;
@@ -266,7 +364,8 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t wl = threadIdx.x - r0 * TW;
     const bool active = r0 < rows_per_pass;
     const uint32_t nch = idx ? plan->n_chunks : dense_n_chunks;
-    const double md = sc->mul[kScoreDer], mw = sc->mul[kScoreW];
+    unsigned long long* lbase = (unsigned long long*)lds + 4u * wl * B;
+    const uint32_t nf = min(4u, TF - min(TF, 4u * wl));   // valid features of this lane's word
     for (uint32_t c = g; c < nch; c += n_slots) {
         uint32_t beg, end, slot;
         if (idx) {
@@ -280,35 +379,57 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
             slot = 0;
         }
         if (active) {
-            for (uint32_t p = beg + r0; p < end; p += rows_per_pass) {
-                const uint32_t doc = idx ? idx[p] : p;
-                const double* st = sstat + (size_t)doc * C;
-                const double wv = st[K];
-                if (wv == 0.0) continue;  // outside the sample: contributes exactly zero
-                long long fx[C];
+            for (uint32_t p0 = beg + r0; p0 < end; p0 += U * rows_per_pass) {
+                uint32_t doc[U];
 #pragma unroll
-                for (int d = 0; d < K; ++d) fx[d] = to_fixed(st[d], md);
-                fx[K] = to_fixed(wv, mw);
-                const uint32_t word = rows[(size_t)doc * W + w0 + wl];
+                for (int u = 0; u < U; ++u) {
+                    const uint32_t p = p0 + (uint32_t)u * rows_per_pass;
+                    doc[u] = p < end ? (idx ? idx[p] : p) : 0xFFFFFFFFu;
+                }
+                long long st[U][C];
+                uint32_t word[U];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint32_t fl = 4u * wl + (uint32_t)k;
-                    if (fl < TF) {
-                        const uint32_t bin = (word >> (8 * k)) & 0xFFu;
-                        unsigned long long* cell =
-                            (unsigned long long*)(lds + ((size_t)fl * B + bin) * C);
+                for (int u = 0; u < U; ++u) {
+                    if (doc[u] != 0xFFFFFFFFu) {
+                        const long long* sp_ = sfix + (size_t)doc[u] * C;
 #pragma unroll
-                        for (int ch = 0; ch < C; ++ch) atomicAdd(cell + ch, (unsigned long long)fx[ch]);
+                        for (int ch = 0; ch < C; ++ch) st[u][ch] = sp_[ch];
+                        word[u] = rows[(size_t)doc[u] * W + w0 + wl];
+                    } else {
+#pragma unroll
+                        for (int ch = 0; ch < C; ++ch) st[u][ch] = 0;
+                        word[u] = 0;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    bool zero = true;  // a row of zeros (outside the sample, padding) adds nothing
+#pragma unroll
+                    for (int ch = 0; ch < C; ++ch) zero &= st[u][ch] == 0;
+                    if (zero) continue;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        if ((uint32_t)k < nf) {
+                            const uint32_t bin = (word[u] >> (8 * k)) & 0xFFu;
+                            unsigned long long* cell = lbase + (uint32_t)k * B + bin;
+#pragma unroll
+                            for (int ch = 0; ch < C; ++ch)
+                                atomicAdd(cell + (size_t)ch * plane, (unsigned long long)st[u][ch]);
+                        }
                     }
                 }
             }
         }
         __syncthreads();
-        unsigned long long* dst = (unsigned long long*)(hist + ((size_t)slot * F + f0) * B * C);
+        // flush LDS [ch][f][bin] -> hist[leaf][ch][f0 + f][bin]: contiguous per channel plane
         for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) {
             const long long v = lds[i];
             if (v != 0) {
-                atomicAdd(dst + i, (unsigned long long)v);
+                const uint32_t ch = i / plane;
+                const uint32_t r = i - ch * plane;
+                unsigned long long* dst = (unsigned long long*)hist +
+                    (((size_t)slot * C + ch) * F + f0) * B + r;
+                atomicAdd(dst, (unsigned long long)v);
                 lds[i] = 0;
             }
         }
@@ -404,9 +525,9 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     for (int d = 0; d < K; ++d) {
         for (int side = 0; side < 2; ++side) {
             for (uint32_t p = 0; p < P; ++p) {
-                const long long* row = hist + ((size_t)p * F + f) * B * C;
-                const long long vd = b < B ? row[(size_t)b * C + d] : 0;
-                const long long vw = b < B ? row[(size_t)b * C + K] : 0;
+                const long long* leafh = hist + (size_t)p * C * F * B;
+                const long long vd = b < B ? leafh[((size_t)d * F + f) * B + b] : 0;
+                const long long vw = b < B ? leafh[((size_t)K * F + f) * B + b] : 0;
                 long long pd, pw, td, tw;
                 block_scan2<NW>(vd, vw, pd, pw, td, tw, sh);
                 long long xd, xw;
@@ -793,12 +914,20 @@ static __global__ void leaf_values_kernel(const long long* __restrict__ sums, co
 }
 
 // Exact fixed-point histogram -> f64 (kernel-level entry point and tests).
+// h is [slot][ch][f][bin]; out is [slot][f][bin][ch].
 static __global__ void hist_to_f64_kernel(const long long* __restrict__ h, size_t n_cells, uint32_t C,
-                                   const Scales* __restrict__ sc, double* __restrict__ out) {
+                                          uint32_t F, uint32_t B, const Scales* __restrict__ sc,
+                                          double* __restrict__ out) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_cells;
          i += (size_t)gridDim.x * blockDim.x) {
         const uint32_t ch = (uint32_t)(i % C);
-        out[i] = (double)h[i] * (ch == C - 1 ? sc->inv[kScoreW] : sc->inv[kScoreDer]);
+        size_t r = i / C;
+        const uint32_t bin = (uint32_t)(r % B);
+        r /= B;
+        const uint32_t f = (uint32_t)(r % F);
+        const size_t slot = r / F;
+        const long long v = h[((slot * C + ch) * F + f) * B + bin];
+        out[i] = (double)v * (ch == C - 1 ? sc->inv[kScoreW] : sc->inv[kScoreDer]);
     }
 }
 

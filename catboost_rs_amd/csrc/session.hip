@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -136,9 +137,13 @@ struct cbh_session {
     long long* leaf_sums = nullptr;
     double* leaf_raw = nullptr;
     double* leaf_scaled = nullptr;
-    uint32_t* tile_w0 = nullptr;
-    uint32_t n_tiles = 0;
-    size_t fill_lds = 0;
+    FillTiles tiles{};
+    uint64_t* jump = nullptr;               // [2048 + 2 * n_coarse]: fine a, fine d, coarse a, coarse d
+    uint64_t n_coarse = 0;
+    unsigned long long* partials = nullptr; // [kPrepBlocks][kPartials]
+    JumpTabs jt() const {
+        return JumpTabs{jump, jump + 1024, jump + 2048, jump + 2048 + n_coarse};
+    }
 
     // profiling
     cbh_stats stats{};
@@ -152,7 +157,8 @@ struct cbh_session {
         dfree(host_sample); dfree(leaf); dfree(idx); dfree(hist[0]); dfree(hist[1]); dfree(cnt);
         dfree(totals); dfree(chunks); dfree(plans); dfree(splits); dfree(best_score);
         dfree(best_bin); dfree(n_cand); dfree(one_hot); dfree(scales); dfree(bounds);
-        dfree(leaf_sums); dfree(leaf_raw); dfree(leaf_scaled); dfree(tile_w0);
+        dfree(leaf_sums); dfree(leaf_raw); dfree(leaf_scaled); dfree(jump);
+        dfree(partials);
         for (auto& t : timers) {
             if (t.second.a) (void)hipEventDestroy(t.second.a);
             if (t.second.b) (void)hipEventDestroy(t.second.b);
@@ -261,27 +267,31 @@ int session_alloc(cbh_session* s) {
     CHECK(dalloc(&s->leaf_sums, ((size_t)1 << s->depth) * CL));
     CHECK(dalloc(&s->leaf_raw, ((size_t)1 << s->depth) * s->K));
     CHECK(dalloc(&s->leaf_scaled, ((size_t)1 << s->depth) * s->K));
+    CHECK(dalloc(&s->partials, (size_t)kPrepBlocks * kPartials));
+    s->n_coarse = (n >> 10) + 2;
+    CHECK(dalloc(&s->jump, 2048 + 2 * s->n_coarse));
+    {
+        std::vector<uint64_t> h(2048 + 2 * s->n_coarse);
+        make_jump_tables(s->n_coarse, h.data(), h.data() + 1024, h.data() + 2048,
+                         h.data() + 2048 + s->n_coarse);
+        HIP_TRY(hipMemcpy(s->jump, h.data(), sizeof(uint64_t) * h.size(), hipMemcpyHostToDevice));
+    }
     return CBH_OK;
 }
 
-// Feature tiles of the fill: as many whole words per tile as the LDS budget allows,
-// balanced across tiles.
+// Feature tiles of the fill: the widest LDS slot stride whose histogram fits the budget.
 int plan_tiles(cbh_session* s) {
     int lds_max = 0;
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device));
     size_t budget = std::min<size_t>((size_t)lds_max, 160 * 1024);
-    const size_t per_feature = (size_t)s->B * s->C * sizeof(long long);
-    const size_t max_words = budget / (per_feature * 4);
-    if (max_words == 0)
-        return fail(CBH_DECLINED, "histogram line of 4 features does not fit in LDS");
-    const uint32_t n_tiles = (uint32_t)((s->W + max_words - 1) / max_words);
-    const uint32_t tw = (s->W + n_tiles - 1) / n_tiles;
-    std::vector<uint32_t> w0(n_tiles + 1);
-    for (uint32_t t = 0; t <= n_tiles; ++t) w0[t] = std::min(s->W, t * tw);
-    s->n_tiles = n_tiles;
-    s->fill_lds = (size_t)std::min<uint32_t>(tw * 4, s->F) * per_feature;
-    CHECK(dalloc(&s->tile_w0, n_tiles + 1));
-    HIP_TRY(hipMemcpy(s->tile_w0, w0.data(), sizeof(uint32_t) * (n_tiles + 1), hipMemcpyHostToDevice));
+    // CBH_FILL_LDS_KB lowers the per-workgroup LDS budget (a tuning knob; the default uses
+    // the whole LDS of a CU)
+    if (const char* e = std::getenv("CBH_FILL_LDS_KB")) {
+        const long kb = std::strtol(e, nullptr, 10);
+        if (kb >= 8) budget = std::min<size_t>(budget, (size_t)kb * 1024);
+    }
+    s->tiles = plan_fill_tiles(s->F, s->B, s->C, budget);
+    if (s->tiles.n_tiles == 0) return fail(CBH_DECLINED, "histogram of 4 features does not fit in LDS");
     return CBH_OK;
 }
 
@@ -325,7 +335,7 @@ int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double*
     CHECK(plan_tiles(s.get()));
     CHECK(with_k((int)s->K, [&](auto kc) {
         constexpr int K = decltype(kc)::value;
-        return set_fill_attr<K + 1>(s->fill_lds);
+        return set_fill_attr<K + 1>(s->tiles.lds_bytes);
     }));
     // candidates per feature: float -> real_folds-1 borders; one-hot -> real_folds values
     std::vector<uint32_t> nc(F);
@@ -389,13 +399,15 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
 
     // ---- prepare: apply previous tree, ders, sample, score channels, bounds ----
     CHECK(s->stage_begin(kStPrepare));
-    HIP_TRY(hipMemsetAsync(s->bounds, 0, sizeof(Bounds), st));
-    prepare_kernel<K><<<grid_for(n, 256, 16384), 256, 0, st>>>(
+    const unsigned pgrid = grid_for(n, 256, kPrepBlocks);
+    prepare_kernel<K><<<pgrid, 256, 0, st>>>(
         n, loss, s->approx, s->target, s->weight, s->leaf, s->pending ? s->leaf_scaled : nullptr,
-        smp, use_host_sample ? s->host_sample : nullptr, s->sstat, newton, s->bounds);
+        smp, s->jt(), use_host_sample ? s->host_sample : nullptr, s->sstat, newton, s->partials);
     HIP_TRY(hipGetLastError());
     s->pending = false;
-    scales_kernel<<<1, 64, 0, st>>>(s->bounds, s->scales);
+    scales_kernel<<<1, 256, 0, st>>>(s->partials, pgrid, s->bounds, s->scales);
+    HIP_TRY(hipGetLastError());
+    quantize_stats_kernel<C><<<grid_for(n * C, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales);
     HIP_TRY(hipGetLastError());
     CHECK(s->stage_end());
 
@@ -417,14 +429,15 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         } else {
             slots = (uint32_t)((n / 2 + kChunkRows - 1) / kChunkRows) + (n_leaves / 2);
         }
-        uint32_t target_slots = std::max<uint32_t>(8, (1024 + s->n_tiles - 1) / s->n_tiles);
+        const uint32_t nt = s->tiles.n_tiles;
+        uint32_t target_slots = std::max<uint32_t>(8, (2048 + nt - 1) / nt);
         slots = std::min(slots, target_slots);
         slots = (slots + 7) / 8 * 8;
-        const unsigned grid = slots * s->n_tiles;
-        fill_kernel<C><<<grid, 1024, s->fill_lds, st>>>(
+        const unsigned grid = slots * nt;
+        fill_kernel<C><<<grid, 1024, s->tiles.lds_bytes, st>>>(
             s->rows, s->W, n, level == 0 ? nullptr : s->idx, s->chunks,
-            level == 0 ? nullptr : s->plans + (level - 1), kChunkRows, dense_chunks, s->sstat,
-            s->scales, s->tile_w0, s->n_tiles, s->F, s->B, slots, cur);
+            level == 0 ? nullptr : s->plans + (level - 1), kChunkRows, dense_chunks,
+            (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, slots, cur);
         HIP_TRY(hipGetLastError());
         CHECK(s->stage_end());
         // ---- derive the sibling of every directly built child ----
@@ -605,10 +618,9 @@ int cbh_session_read_approx(cbh_session* s, double* approx_out, uint64_t n_times
         // just its update arm here with an inert sample
         int rc = with_k((int)s->K, [&](auto kc) {
             constexpr int K = decltype(kc)::value;
-            HIP_TRY(hipMemsetAsync(s->bounds, 0, sizeof(Bounds), s->stream));
-            prepare_kernel<K><<<grid_for(s->n, 256, 16384), 256, 0, s->stream>>>(
+            prepare_kernel<K><<<grid_for(s->n, 256, kPrepBlocks), 256, 0, s->stream>>>(
                 s->n, s->cfg.loss == CBH_LOSS_RMSE ? 0 : 1, s->approx, s->target, s->weight, s->leaf,
-                s->leaf_scaled, SampleParams{}, nullptr, s->sstat, 0, s->bounds);
+                s->leaf_scaled, SampleParams{}, s->jt(), nullptr, s->sstat, 0, s->partials);
             HIP_TRY(hipGetLastError());
             return CBH_OK;
         });
