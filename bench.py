@@ -45,7 +45,19 @@ def main():
     ap.add_argument("--cpu-trees", type=int, default=2)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib", type=int, default=0,
+                    help="only copy this many bytes device-to-device (counter calibration)")
     args = ap.parse_args()
+    if args.copy_calib:
+        import torch
+
+        a = torch.empty(args.copy_calib, dtype=torch.uint8, device="cuda:0")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copied {args.copy_calib} bytes x3")
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               "row-parallel design is described in DESIGN.md and is not built.", file=sys.stderr)

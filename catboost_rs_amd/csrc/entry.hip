@@ -101,15 +101,15 @@ int fail2(int code, const std::string& msg) { return cbh_internal_fail(code, msg
 
 template <int C>
 int run_fill(const uint32_t* rows, uint32_t W, uint64_t n, const uint32_t* idx,
-             const Chunk* chunks, const LevelPlan* plan, uint32_t dense_chunks, double* sstat,
-             const Scales* sc, const FillTiles& ft, uint32_t F, uint32_t B, uint32_t slots,
-             long long* hist) {
+             const LevelPlan* plan, double* sstat, const Scales* sc, const FillTiles& ft, uint32_t F,
+             uint32_t B, long long* hist) {
     quantize_stats_kernel<C><<<grid_of(n * C, 256), 256>>>(sstat, n, sc);
     HIP_OK(hipFuncSetAttribute((const void*)fill_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)ft.lds_bytes));
-    fill_kernel<C><<<slots * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, n, idx, chunks, plan, 8192,
-                                                                 dense_chunks, (const long long*)sstat,
-                                                                 ft.n_tiles, ft.tw, F, B, slots, hist);
+    const uint32_t G = 64;
+    fill_kernel<C><<<G * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, n, idx, plan,
+                                                             (const long long*)sstat, ft.n_tiles, ft.tw,
+                                                             F, B, G, hist);
     HIP_OK(hipGetLastError());
     return CBH_OK;
 }
@@ -205,19 +205,21 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t B, c
         sc.mul[k] = std::ldexp(1.0, s);
         sc.inv[k] = std::ldexp(1.0, -s);
     }
-    // rows grouped by slot, ascending row order; chunks of 8192 rows
+    // rows grouped by slot, ascending row order (the layout the partition kernels produce)
     std::vector<uint32_t> idx;
-    std::vector<Chunk> chunks;
+    LevelPlan plan{};
     if (slot_of_row) {
+        if (n_slots > kMaxLeaves / 2) return fail2(CBH_ERR_INVALID_ARG, "at most 128 slots");
         std::vector<std::vector<uint32_t>> per(n_slots);
         for (uint64_t i = 0; i < n; ++i)
             if (slot_of_row[i] < n_slots) per[slot_of_row[i]].push_back((uint32_t)i);
         for (uint32_t s = 0; s < n_slots; ++s) {
-            const uint32_t b0 = (uint32_t)idx.size();
+            plan.seg_begin[s] = (uint32_t)idx.size();
+            plan.built[s] = s;
             idx.insert(idx.end(), per[s].begin(), per[s].end());
-            for (uint32_t o = 0; o < per[s].size(); o += 8192)
-                chunks.push_back(Chunk{b0 + o, b0 + std::min<uint32_t>((uint32_t)per[s].size(), o + 8192), s, 0});
         }
+        plan.n_parent = n_slots;
+        plan.rows = (uint32_t)idx.size();
     }
     int lds_max = 0, dev = 0;
     HIP_OK(hipGetDevice(&dev));
@@ -228,7 +230,6 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t B, c
     DBuf<uint8_t> cols;
     DBuf<uint32_t> rows, didx;
     DBuf<double> dder, dw, sstat, dout;
-    DBuf<Chunk> dch;
     DBuf<LevelPlan> dplan;
     DBuf<Scales> dsc;
     DBuf<long long> hist;
@@ -249,26 +250,15 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t B, c
     pack_rows_kernel<<<grid_of(n * W, 256), 256>>>(cols.p, n, F, W, rows.p);
     pack_stats_kernel<<<grid_of(n, 256), 256>>>(dder.p, dw.p, n, K, sstat.p);
     HIP_OK(hipGetLastError());
-    uint32_t dense_chunks = 0, slots;
     if (slot_of_row) {
-        LevelPlan plan{};
-        plan.n_chunks = (uint32_t)chunks.size();
         HIP_OK(didx.alloc(std::max<size_t>(idx.size(), 1)));
-        HIP_OK(dch.alloc(std::max<size_t>(chunks.size(), 1)));
         HIP_OK(dplan.alloc(1));
         if (!idx.empty()) HIP_OK(hipMemcpy(didx.p, idx.data(), sizeof(uint32_t) * idx.size(), hipMemcpyHostToDevice));
-        if (!chunks.empty()) HIP_OK(hipMemcpy(dch.p, chunks.data(), sizeof(Chunk) * chunks.size(), hipMemcpyHostToDevice));
         HIP_OK(hipMemcpy(dplan.p, &plan, sizeof(LevelPlan), hipMemcpyHostToDevice));
-        slots = std::max<uint32_t>(1, (uint32_t)chunks.size());
-    } else {
-        dense_chunks = (uint32_t)((n + 8191) / 8192);
-        slots = dense_chunks;
     }
-    slots = std::min<uint32_t>(slots, std::max<uint32_t>(8, 2048 / ft.n_tiles));
-    slots = (slots + 7) / 8 * 8;
     int rc;
     switch (C) {
-#define CASE(c) case c: rc = run_fill<c>(rows.p, W, n, slot_of_row ? didx.p : nullptr, dch.p, dplan.p, dense_chunks, sstat.p, dsc.p, ft, F, B, slots, hist.p); break;
+#define CASE(c) case c: rc = run_fill<c>(rows.p, W, n, slot_of_row ? didx.p : nullptr, dplan.p, sstat.p, dsc.p, ft, F, B, hist.p); break;
         CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(9) CASE(11) CASE(13) CASE(17)
 #undef CASE
         default: return fail2(CBH_ERR_UNSUPPORTED, "K has no compiled fill variant");

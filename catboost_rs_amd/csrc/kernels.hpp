@@ -19,10 +19,6 @@
 
 namespace cbh {
 
-struct Chunk {
-    uint32_t begin, end, slot, pad;
-};
-
 struct SplitRec {
     uint32_t feature;
     uint32_t bin;
@@ -32,7 +28,7 @@ struct SplitRec {
 };
 
 struct LevelPlan {            // written by plan_finalize, read by fill/derive/compact
-    uint32_t n_chunks;
+    uint32_t pad0;
     uint32_t n_parent;
     uint32_t rows;            // rows visited by the next fill (sum of built segments)
     uint32_t pad;
@@ -298,13 +294,12 @@ static __global__ void quantize_stats_kernel(double* __restrict__ sstat, uint64_
 }
 
 // ---------------------------------------------------------------------------------
-// Histogram fill.  One workgroup = (feature tile, chunk slot); it loops over chunks
-// (row ranges of one leaf), accumulating round(v * 2^S) into an LDS histogram of its
-// feature tile with 64-bit integer LDS atomics, then flushes non-zero cells into the
-// level histogram with 64-bit global atomics (integer adds: any order gives the same
-// bits).  The blockIdx -> (tile, chunk slot) map keeps all tiles of a chunk slot on one
-// XCD (blocks are dealt to the 8 XCDs round-robin), so the rows a chunk reads are fetched
-// into that XCD's L2 once and shared by its tiles.
+// Histogram fill.  One workgroup = (feature tile, row range); it accumulates
+// round(v * 2^S) of its rows into an LDS histogram of its feature tile with 64-bit integer
+// LDS atomics, then flushes non-zero cells into the level histogram with 64-bit global
+// atomics (integer adds: any order gives the same bits).  The blockIdx -> (tile, range)
+// map keeps all tiles of a range on one XCD (blocks are dealt to the 8 XCDs round-robin),
+// so the rows a range reads are fetched into that XCD's L2 once and shared by its tiles.
 //
 // Lane layout (word per lane): a lane takes one 4-byte word (4 features) of a row; the
 // TW lanes of a row cover the tile's words and a 1024-thread workgroup covers
@@ -337,20 +332,77 @@ inline FillTiles plan_fill_tiles(uint32_t F, uint32_t B, uint32_t C, size_t budg
     return t;
 }
 
+// One workgroup per (feature tile, row range): the rows to histogram (all n rows at level
+// 0, else the concatenated segments of the directly built children listed in idx) are
+// split into G equal contiguous ranges; a workgroup walks its range and flushes its LDS
+// histogram only when it crosses into the next segment (leaf) and at the end, so the
+// global-atomic flush traffic is about G * tiles * cells per launch instead of one flush
+// per small chunk.  G * tiles is sized to the number of workgroups the CUs hold at once.
+template <int C>
+__device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, uint32_t W,
+                                           const uint32_t* __restrict__ idx,
+                                           const long long* __restrict__ sfix, uint32_t beg,
+                                           uint32_t end, uint32_t w0, uint32_t TW, uint32_t nf,
+                                           uint32_t B, uint32_t plane,
+                                           unsigned long long* __restrict__ lbase) {
+    constexpr int U = kFillRows;
+    const uint32_t rows_per_pass = blockDim.x / TW;
+    const uint32_t r0 = threadIdx.x / TW;
+    const uint32_t wl = threadIdx.x - r0 * TW;
+    if (r0 >= rows_per_pass) return;
+    for (uint32_t p0 = beg + r0; p0 < end; p0 += U * rows_per_pass) {
+        uint32_t doc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t p = p0 + (uint32_t)u * rows_per_pass;
+            doc[u] = p < end ? (idx ? idx[p] : p) : 0xFFFFFFFFu;
+        }
+        long long st[U][C];
+        uint32_t word[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (doc[u] != 0xFFFFFFFFu) {
+                const long long* sp_ = sfix + (size_t)doc[u] * C;
+#pragma unroll
+                for (int ch = 0; ch < C; ++ch) st[u][ch] = sp_[ch];
+                word[u] = rows[(size_t)doc[u] * W + w0 + wl];
+            } else {
+#pragma unroll
+                for (int ch = 0; ch < C; ++ch) st[u][ch] = 0;
+                word[u] = 0;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            bool zero = true;  // a row of zeros (outside the sample, padding) adds nothing
+#pragma unroll
+            for (int ch = 0; ch < C; ++ch) zero &= st[u][ch] == 0;
+            if (zero) continue;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if ((uint32_t)k < nf) {
+                    const uint32_t bin = (word[u] >> (8 * k)) & 0xFFu;
+                    unsigned long long* cell = lbase + (uint32_t)k * B + bin;
+#pragma unroll
+                    for (int ch = 0; ch < C; ++ch)
+                        atomicAdd(cell + (size_t)ch * plane, (unsigned long long)st[u][ch]);
+                }
+            }
+        }
+    }
+}
+
 template <int C>
 static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t* __restrict__ rows, uint32_t W, uint64_t n,
-    const uint32_t* __restrict__ idx,                  // null: dense rows [0, n)
-    const Chunk* __restrict__ chunks, const LevelPlan* __restrict__ plan,
-    uint32_t dense_chunk_rows, uint32_t dense_n_chunks,
-    const long long* __restrict__ sfix, uint32_t n_tiles, uint32_t tw, uint32_t F, uint32_t B,
-    uint32_t n_slots, long long* __restrict__ hist) {
+    const uint32_t* __restrict__ idx,                  // null: dense rows [0, n), leaf 0
+    const LevelPlan* __restrict__ plan, const long long* __restrict__ sfix, uint32_t n_tiles,
+    uint32_t tw, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist) {
     extern __shared__ long long lds[];
-    constexpr int U = kFillRows;
     const uint32_t b = blockIdx.x;
     const uint32_t xcd = b & 7u, q = b >> 3;
     const uint32_t t = q % n_tiles;
-    const uint32_t g = (q / n_tiles) * 8u + xcd;
+    const uint32_t g = (q / n_tiles) * 8u + xcd;       // row range
     const uint32_t w0 = t * tw;
     const uint32_t TW = min(tw, W - w0);
     const uint32_t f0 = 4u * w0;
@@ -359,81 +411,41 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t cells = plane * C;
     for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) lds[i] = 0;
     __syncthreads();
-    const uint32_t rows_per_pass = blockDim.x / TW;
     const uint32_t r0 = threadIdx.x / TW;
     const uint32_t wl = threadIdx.x - r0 * TW;
-    const bool active = r0 < rows_per_pass;
-    const uint32_t nch = idx ? plan->n_chunks : dense_n_chunks;
     unsigned long long* lbase = (unsigned long long*)lds + 4u * wl * B;
     const uint32_t nf = min(4u, TF - min(TF, 4u * wl));   // valid features of this lane's word
-    for (uint32_t c = g; c < nch; c += n_slots) {
-        uint32_t beg, end, slot;
-        if (idx) {
-            const Chunk ch = chunks[c];
-            beg = ch.begin;
-            end = ch.end;
-            slot = ch.slot;
-        } else {
-            beg = c * dense_chunk_rows;
-            end = (uint32_t)min((uint64_t)beg + dense_chunk_rows, n);
-            slot = 0;
-        }
-        if (active) {
-            for (uint32_t p0 = beg + r0; p0 < end; p0 += U * rows_per_pass) {
-                uint32_t doc[U];
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const uint32_t p = p0 + (uint32_t)u * rows_per_pass;
-                    doc[u] = p < end ? (idx ? idx[p] : p) : 0xFFFFFFFFu;
-                }
-                long long st[U][C];
-                uint32_t word[U];
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    if (doc[u] != 0xFFFFFFFFu) {
-                        const long long* sp_ = sfix + (size_t)doc[u] * C;
-#pragma unroll
-                        for (int ch = 0; ch < C; ++ch) st[u][ch] = sp_[ch];
-                        word[u] = rows[(size_t)doc[u] * W + w0 + wl];
-                    } else {
-#pragma unroll
-                        for (int ch = 0; ch < C; ++ch) st[u][ch] = 0;
-                        word[u] = 0;
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    bool zero = true;  // a row of zeros (outside the sample, padding) adds nothing
-#pragma unroll
-                    for (int ch = 0; ch < C; ++ch) zero &= st[u][ch] == 0;
-                    if (zero) continue;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        if ((uint32_t)k < nf) {
-                            const uint32_t bin = (word[u] >> (8 * k)) & 0xFFu;
-                            unsigned long long* cell = lbase + (uint32_t)k * B + bin;
-#pragma unroll
-                            for (int ch = 0; ch < C; ++ch)
-                                atomicAdd(cell + (size_t)ch * plane, (unsigned long long)st[u][ch]);
-                        }
-                    }
+    const uint32_t V = idx ? plan->rows : (uint32_t)n;
+    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
+    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
+    const uint32_t n_seg = idx ? plan->n_parent : 1u;
+    uint32_t seg = 0;
+    if (idx)
+        while (seg + 1 < n_seg && plan->seg_begin[seg + 1] <= rb) ++seg;
+    uint32_t pos = rb;
+    while (pos < re) {
+        const uint32_t seg_end = (idx && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
+        const uint32_t end = min(re, seg_end);
+        const uint32_t slot = idx ? plan->built[seg] : 0u;
+        if (end > pos) {
+            fill_range<C>(rows, W, idx, sfix, pos, end, w0, TW, nf, B, plane, lbase);
+            __syncthreads();
+            // flush LDS [ch][f][bin] -> hist[leaf][ch][f0 + f][bin]: contiguous per plane
+            for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) {
+                const long long v = lds[i];
+                if (v != 0) {
+                    const uint32_t ch = i / plane;
+                    const uint32_t r = i - ch * plane;
+                    unsigned long long* dst = (unsigned long long*)hist +
+                        (((size_t)slot * C + ch) * F + f0) * B + r;
+                    atomicAdd(dst, (unsigned long long)v);
+                    lds[i] = 0;
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
-        // flush LDS [ch][f][bin] -> hist[leaf][ch][f0 + f][bin]: contiguous per channel plane
-        for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) {
-            const long long v = lds[i];
-            if (v != 0) {
-                const uint32_t ch = i / plane;
-                const uint32_t r = i - ch * plane;
-                unsigned long long* dst = (unsigned long long*)hist +
-                    (((size_t)slot * C + ch) * F + f0) * B + r;
-                atomicAdd(dst, (unsigned long long)v);
-                lds[i] = 0;
-            }
-        }
-        __syncthreads();
+        pos = end;
+        ++seg;
     }
 }
 
@@ -631,8 +643,8 @@ static __global__ __launch_bounds__(1024) void argmax_kernel(const double* __res
 //   split_count: leaf |= pass << level for every row; per-block counts of sampled rows
 //                per new leaf -> cnt[leaf][block]
 //   plan_scan:   per leaf, exclusive scan over blocks (in place) + total
-//   plan_finalize: smaller child per parent (ties -> the TRUE child, tree.rs:1109), segment
-//                offsets, chunk list of the next fill
+//   plan_finalize: smaller child per parent (ties -> the TRUE child, tree.rs:1109) and the
+//                segment offsets of the next fill
 //   compact:     rows of the built children written in ascending row order per segment;
 //                inside a block, ranks come from wave ballots (match on the key bits) and
 //                mbcnt, across waves from per-wave counts in LDS.
@@ -693,28 +705,17 @@ static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __rest
 }
 
 static __global__ void plan_finalize_kernel(const uint32_t* __restrict__ totals, uint32_t level,
-                                     uint32_t chunk_rows, LevelPlan* __restrict__ plan,
-                                     Chunk* __restrict__ chunks, uint32_t max_chunks) {
+                                            LevelPlan* __restrict__ plan) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     const uint32_t n_parent = 1u << level;  // parents of the next level = current leaves
-    uint32_t off = 0, nch = 0;
+    uint32_t off = 0;
     for (uint32_t p = 0; p < n_parent; ++p) {
         const uint32_t nf = totals[p], nt = totals[p + n_parent];
-        const uint32_t built = nt <= nf ? p + n_parent : p;
-        const uint32_t cntb = nt <= nf ? nt : nf;
-        plan->built[p] = built;
+        const bool true_smaller = nt <= nf;
+        plan->built[p] = true_smaller ? p + n_parent : p;
         plan->seg_begin[p] = off;
-        for (uint32_t b = 0; b < cntb && nch < max_chunks; b += chunk_rows) {
-            Chunk ch;
-            ch.begin = off + b;
-            ch.end = off + min(cntb, b + chunk_rows);
-            ch.slot = built;
-            ch.pad = 0;
-            chunks[nch++] = ch;
-        }
-        off += cntb;
+        off += true_smaller ? nt : nf;
     }
-    plan->n_chunks = nch;
     plan->n_parent = n_parent;
     plan->rows = off;
 }

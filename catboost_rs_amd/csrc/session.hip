@@ -89,7 +89,6 @@ int with_k(int k, F&& f) {
     }
 }
 
-constexpr uint32_t kChunkRows = 8192;  // rows per fill chunk
 
 struct StageTimer {
     hipEvent_t a = nullptr, b = nullptr;
@@ -124,8 +123,6 @@ struct cbh_session {
     uint32_t* cnt = nullptr;
     uint32_t* totals = nullptr;
     uint32_t n_part_blocks = 0;
-    Chunk* chunks = nullptr;
-    uint32_t max_chunks = 0;
     LevelPlan* plans = nullptr;   // [depth]
     SplitRec* splits = nullptr;   // [depth]
     double* best_score = nullptr;
@@ -138,6 +135,7 @@ struct cbh_session {
     double* leaf_raw = nullptr;
     double* leaf_scaled = nullptr;
     FillTiles tiles{};
+    uint32_t fill_ranges = 8;   // row ranges per tile (multiple of 8)
     uint64_t* jump = nullptr;               // [2048 + 2 * n_coarse]: fine a, fine d, coarse a, coarse d
     uint64_t n_coarse = 0;
     unsigned long long* partials = nullptr; // [kPrepBlocks][kPartials]
@@ -155,7 +153,7 @@ struct cbh_session {
     void release() {
         dfree(rows); dfree(cols); dfree(weight); dfree(target); dfree(approx); dfree(sstat);
         dfree(host_sample); dfree(leaf); dfree(idx); dfree(hist[0]); dfree(hist[1]); dfree(cnt);
-        dfree(totals); dfree(chunks); dfree(plans); dfree(splits); dfree(best_score);
+        dfree(totals); dfree(plans); dfree(splits); dfree(best_score);
         dfree(best_bin); dfree(n_cand); dfree(one_hot); dfree(scales); dfree(bounds);
         dfree(leaf_sums); dfree(leaf_raw); dfree(leaf_scaled); dfree(jump);
         dfree(partials);
@@ -254,8 +252,6 @@ int session_alloc(cbh_session* s) {
     s->n_part_blocks = (uint32_t)((n + kPartRows - 1) / kPartRows);
     CHECK(dalloc(&s->cnt, (size_t)s->n_part_blocks << s->depth));
     CHECK(dalloc(&s->totals, (size_t)1 << s->depth));
-    s->max_chunks = (uint32_t)((n + kChunkRows - 1) / kChunkRows) + (1u << s->depth) + 1;
-    CHECK(dalloc(&s->chunks, s->max_chunks));
     CHECK(dalloc(&s->plans, s->depth));
     CHECK(dalloc(&s->splits, s->depth));
     CHECK(dalloc(&s->best_score, s->F));
@@ -292,6 +288,17 @@ int plan_tiles(cbh_session* s) {
     }
     s->tiles = plan_fill_tiles(s->F, s->B, s->C, budget);
     if (s->tiles.n_tiles == 0) return fail(CBH_DECLINED, "histogram of 4 features does not fit in LDS");
+    // as many (tile, range) workgroups as the CUs hold at once, ranges a multiple of 8
+    int cus = 0;
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
+    const uint32_t per_cu = std::max<uint32_t>(1, (uint32_t)((size_t)lds_max / s->tiles.lds_bytes));
+    uint32_t resident = (uint32_t)cus * std::min<uint32_t>(per_cu, 2);
+    if (const char* e = std::getenv("CBH_FILL_WAVES")) {   // tuning knob: workgroups per CU
+        const long m = std::strtol(e, nullptr, 10);
+        if (m >= 1 && m <= 16) resident = (uint32_t)cus * (uint32_t)m;
+    }
+    uint32_t G = resident / s->tiles.n_tiles / 8 * 8;
+    s->fill_ranges = std::max<uint32_t>(8, G);
     return CBH_OK;
 }
 
@@ -422,22 +429,12 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         CHECK(launch_zero(cur, per_leaf * n_leaves, st));
         CHECK(s->stage_end());
         CHECK(s->stage_begin(kStFill));
-        uint32_t dense_chunks = 0, slots;
-        if (level == 0) {
-            dense_chunks = (uint32_t)((n + kChunkRows - 1) / kChunkRows);
-            slots = dense_chunks;
-        } else {
-            slots = (uint32_t)((n / 2 + kChunkRows - 1) / kChunkRows) + (n_leaves / 2);
-        }
         const uint32_t nt = s->tiles.n_tiles;
-        uint32_t target_slots = std::max<uint32_t>(8, (2048 + nt - 1) / nt);
-        slots = std::min(slots, target_slots);
-        slots = (slots + 7) / 8 * 8;
-        const unsigned grid = slots * nt;
-        fill_kernel<C><<<grid, 1024, s->tiles.lds_bytes, st>>>(
-            s->rows, s->W, n, level == 0 ? nullptr : s->idx, s->chunks,
-            level == 0 ? nullptr : s->plans + (level - 1), kChunkRows, dense_chunks,
-            (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, slots, cur);
+        const uint32_t G = s->fill_ranges;
+        fill_kernel<C><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
+            s->rows, s->W, n, level == 0 ? nullptr : s->idx,
+            level == 0 ? nullptr : s->plans + (level - 1), (const long long*)s->sstat, nt,
+            s->tiles.tw, s->F, s->B, G, cur);
         HIP_TRY(hipGetLastError());
         CHECK(s->stage_end());
         // ---- derive the sibling of every directly built child ----
@@ -473,8 +470,7 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         if (!last) {
             plan_scan_kernel<<<2u << level, 1024, 0, st>>>(s->cnt, NB, s->totals);
             HIP_TRY(hipGetLastError());
-            plan_finalize_kernel<<<1, 64, 0, st>>>(s->totals, level, kChunkRows, s->plans + level,
-                                                   s->chunks, s->max_chunks);
+            plan_finalize_kernel<<<1, 64, 0, st>>>(s->totals, level, s->plans + level);
             HIP_TRY(hipGetLastError());
             compact_kernel<<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, NB, s->plans + level, s->idx);
             HIP_TRY(hipGetLastError());
