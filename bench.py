@@ -35,6 +35,18 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def _profiled_traffic(n, F):
+    """HBM bytes per fill launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, copy-calibrated)
+    for this workload shape, read from the committed profile summary; None if absent."""
+    path = os.path.join(ROOT, "profiles", "fill_kernel_config2.md")
+    if n != 10_000_000 or F != 200 or not os.path.exists(path):
+        return None
+    import re
+
+    m = re.search(r"mean per dispatch: fetch ([0-9.]+) GB write ([0-9.]+) GB", open(path).read())
+    return round((float(m.group(1)) + float(m.group(2))) * 1e9) if m else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -105,6 +117,26 @@ def main():
     log(f"fill: {st['fill_launches']} launches, avg {st['fill_ms'] / max(1, st['fill_launches']):.4f} ms, "
         f"{achieved:.1f} GB/s algorithmic")
 
+    # LDS-atomic roofline of the fill: every visited (row, feature) adds K+1 64-bit integer
+    # cells; the cap is the scattered 64-bit LDS atomic rate measured on this GPU
+    lds = None
+    lane_atomics = st["fill_row_features"] * 2
+    probe = os.path.join(ROOT, "catboost_rs_amd", "lds_atomic_rate")
+    if os.path.exists(probe):
+        import subprocess
+
+        r = subprocess.run([probe], capture_output=True, text=True, timeout=120)
+        rates = dict((l.split()[0], float(l.split()[1])) for l in r.stdout.splitlines() if len(l.split()) == 2)
+        if "scattered_u64" in rates and fill_s > 0:
+            ach = lane_atomics / fill_s
+            lds = {"achieved_lane_atomics_per_s": round(ach, 1),
+                   "cap_scattered_u64_per_s": rates["scattered_u64"],
+                   "cap_contiguous_u64_per_s": rates.get("contiguous_u64"),
+                   "frac_of_scattered_cap": round(ach / rates["scattered_u64"], 4)}
+            log(f"fill LDS atomics: {ach:.3e}/s = {100 * ach / rates['scattered_u64']:.1f}% of the "
+                f"measured scattered-u64 cap {rates['scattered_u64']:.3e}/s")
+    traffic = _profiled_traffic(n, F)
+
     cpu = None
     if not args.no_cpu and args.cpu_trees > 0:
         from oracle import oracle as O
@@ -154,10 +186,11 @@ def main():
                               ("fill_ms", "derive_ms", "score_ms", "partition_ms", "leaf_ms", "prepare_ms")},
         "roofline": {"bound": "hbm", "kernel": "fill_kernel", "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": traffic,
                      "launches": st["fill_launches"],
                      "avg_launch_ms": round(st["fill_ms"] / max(1, st["fill_launches"]), 5),
                      "algorithmic_bytes_per_launch": round(st["fill_bytes"] / max(1, st["fill_launches"]))},
+        "lds_atomic_roofline": lds,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -44,6 +44,20 @@ def _compile(src: str) -> str:
     return obj
 
 
+RATE_SRC = os.path.join(CSRC, "lds_atomic_rate.hip")
+RATE_BIN = os.path.join(HERE, "lds_atomic_rate")
+
+
+def build_rate_probe() -> str:
+    """The LDS atomic-rate probe bench.py runs to report the fill's LDS-atomic roofline."""
+    cmd = [HIPCC, "-x", "hip"] + DEVICE + ["-O3", "-std=c++17", RATE_SRC, "-o", RATE_BIN + ".tmp"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for lds_atomic_rate.hip:\n{r.stdout}\n{r.stderr}")
+    os.replace(RATE_BIN + ".tmp", RATE_BIN)
+    return RATE_BIN
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(OBJ_DIR, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as ex:
@@ -54,6 +68,7 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, OUT)
+    build_rate_probe()
     if verbose:
         print(f"built {OUT}")
     return OUT
