@@ -1,4 +1,4 @@
-"""Benchmark of the MI355X oblivious-tree training path.
+"""Benchmark of the MI355X oblivious-tree training path (headline config 2).
 
 Workload: Logloss, 10M rows x 200 features (100 N(0,1) + 100 lognormal(0,1)), 254
 borders (u8 bins, 4 per u32 word), depth 6, Bayesian bootstrap T=1, synthetic seeded
@@ -72,7 +72,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
-              "row-parallel design is described in DESIGN.md and is not built.", file=sys.stderr)
+              "row-parallel (integer histogram all-reduce) design is not built in this library.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -1,4 +1,4 @@
-"""Seeded synthetic workloads of the BASELINE.json configs (no dataset downloads).
+"""Seeded synthetic workloads of the benchmark configs 1-5 (no dataset downloads).
 
 Each generator returns feature-major u8 bins ``bins_fm[F][n]``, the border count per
 feature, the target and the training parameters of the config.  Borders are per-feature

@@ -3,8 +3,7 @@
  *
  * This library is a drop-in device backend behind catboost_rs's compute seam
  * `trait cb_compute::Runtime` (crates/cb-compute/src/runtime.rs:1410-1651).  A thin
- * Rust crate (`HipBackend: Runtime`) binds these symbols one to
- * one.  Plain pointers and sizes only; no HIP or torch types cross the boundary.
+ * Rust crate (`HipBackend: Runtime`) binds these symbols one to one.  Plain pointers and sizes only; no HIP or torch types cross the boundary.
  *
  * Status codes: 0 = OK, 1 = DECLINED (the caller falls back to its CPU grower, as a
  * trait default returning Ok(false)/Ok(None) does), negative = error mirroring the
@@ -59,7 +58,8 @@ typedef struct {
     int32_t profile;              /* 1: time every kernel with HIP events */
     double bias;                  /* starting approximant (boost_from_average) */
     uint64_t rng_seed;            /* informational; draws come from the host RNG phase */
-    /* one-hot columns (SPEC-OH-21/24): nullable, length n_features.  A one-hot feature's
+    /* one-hot columns (DeviceTrainConfig.one_hot_flags / real_folds, runtime.rs:1315-1332;
+     * real_folds built as in boosting.rs:4334-4372): nullable, length n_features.  A one-hot feature's
      * candidates are the equality splits bin == v for v < real_folds[f]; float features
      * use bin > b for b < real_folds[f]-1.  NULL real_folds: every feature has n_bins. */
     const uint8_t* one_hot_flags;
