@@ -290,12 +290,17 @@ class Trainer:
         _check(load().cbt_step(self._h, _ptr(sf), _ptr(sb), _ptr(so), _ptr(lv)))
         return np.stack([sf, sb], 1).astype(np.int32), lv, so
 
-    def fit(self, iterations):
-        splits, leaves = [], []
+    def fit(self, iterations, with_one_hot=False):
+        """Grow ``iterations`` trees; returns (splits [it][depth][2], leaves [it][K][2^d]) and,
+        with ``with_one_hot``, the per-level one-hot flags [it][depth]."""
+        splits, leaves, kinds = [], [], []
         for _ in range(iterations):
-            s, lv, _ = self.step()
+            s, lv, so = self.step()
             splits.append(s)
             leaves.append(lv)
+            kinds.append(so.astype(bool))
+        if with_one_hot:
+            return np.array(splits), np.array(leaves), np.array(kinds)
         return np.array(splits), np.array(leaves)
 
     def approx(self):

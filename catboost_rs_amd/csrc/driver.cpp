@@ -1,5 +1,5 @@
 // Host mirror of cb-train's device branch (crates/cb-train/src/boosting.rs:6532-7300),
-// written against the public C-ABI only.  It owns the persistent training RNG: the
+// driving the session through the public C-ABI only.  It owns the persistent training RNG: the
 // device never draws on the main stream, it receives the per-tree sampling phase
 // (Bayesian seed / Bernoulli raw state) and the host advances its stream exactly as the
 // CPU branch would, including the per-level draws of the perturbed level search that the
@@ -13,6 +13,8 @@
 #include "../../include/cbhip.h"
 #include "../../include/cbtrain.h"
 #include "common.hpp"
+
+int cbh_internal_fail(int code, const std::string& msg);  // session.hip: sets cbh_last_error()
 
 namespace {
 
@@ -56,8 +58,18 @@ int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F
              const double* weight, cbt_trainer** out) {
     if (!p || !bins_fm || !target || !out) return CBH_ERR_INVALID_ARG;
     *out = nullptr;
+    bool any_one_hot = false;
+    for (uint32_t f = 0; one_hot_flags && f < F; ++f) any_one_hot |= one_hot_flags[f] != 0;
+    // one-hot columns with active RNG draws are refused (boosting.rs:5744-5756)
+    if (any_one_hot && p->bootstrap_type != CBH_BOOT_NO)
+        return cbh_internal_fail(CBH_ERR_UNSUPPORTED,
+                                 "one-hot columns are not supported with bootstrap_type != No "
+                                 "(the per-level RNG draw accounting of one-hot candidates is unset)");
     std::unique_ptr<cbt_trainer> t(new cbt_trainer());
     t->p = *p;
+    // the learning rate that multiplies every leaf is the f32-representable one
+    // (boosting.rs:4958); the session applies the same value to the resident approx
+    t->p.learning_rate = (double)(float)p->learning_rate;
     t->n = n;
     t->F = F;
     t->K = p->loss == CBH_LOSS_MULTICLASS ? (uint32_t)p->approx_dim : 1u;
@@ -88,7 +100,7 @@ int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F
     cfg.rng_seed = p->random_seed;
     cfg.one_hot_flags = one_hot_flags;
     cfg.real_folds = real_folds;
-    int rc = cbh_session_begin_u8(&cfg, bins_fm, weight, n, F, n_bins, p->learning_rate, scaled_l2, &t->s);
+    int rc = cbh_session_begin_u8(&cfg, bins_fm, weight, n, F, n_bins, t->p.learning_rate, scaled_l2, &t->s);
     if (rc != CBH_OK) return rc;
     t->rng = cbh::rng_from_seed(p->random_seed);
     t->draws_active = p->bootstrap_type != CBH_BOOT_NO;

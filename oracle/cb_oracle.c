@@ -368,17 +368,11 @@ static void derive_hist(double* out, const double* parent, uint32_t level, uint3
     free(built);
 }
 
-/* scan_and_score_borders_into (histogram.rs:1007-1149) + multi_dim_split_score_into
- * (score.rs:192-265) for one feature with n_parent = 2^level leaves. */
-static void scan_score(const double* h, uint32_t n_parent, uint32_t n_bins, int K,
-                       uint32_t n_borders, int score_fn, double l2, double* scores) {
+/* Per-parent totals of one feature: ordered f64 sums over the bins (histogram.rs:1040-1075
+ * and :1207-1235 compute them the same way for the border and the one-hot scans). */
+static void parent_totals(const double* h, uint32_t n_parent, uint32_t n_bins, int K,
+                          double* total_w, double* total_d) {
     const int C = K + 1;
-    double* total_w = (double*)calloc(n_parent, sizeof(double));
-    double* total_d = (double*)calloc((size_t)n_parent * K, sizeof(double));
-    double* acc_w = (double*)calloc(n_parent, sizeof(double));
-    double* acc_d = (double*)calloc((size_t)n_parent * K, sizeof(double));
-    double* sd = (double*)malloc(sizeof(double) * 2 * n_parent * K);
-    double* sw = (double*)malloc(sizeof(double) * 2 * n_parent);
     for (uint32_t p = 0; p < n_parent; ++p) {
         const double* blk = h + (size_t)p * n_bins * C;
         double t = 0.0;
@@ -390,6 +384,43 @@ static void scan_score(const double* h, uint32_t n_parent, uint32_t n_bins, int 
             total_d[p * K + d] = td;
         }
     }
+}
+
+/* multi_dim_split_score_into (score.rs:192-265): fold in dimension-then-leaf order over the
+ * 2P children (leaves 0..P-1 FALSE, P..2P-1 TRUE); sd is [K][2P], sw is [2P]. */
+static double fold_score(const double* sd, const double* sw, uint32_t n_parent, int K,
+                         int score_fn, double l2) {
+    double num = 0.0;
+    for (int d = 0; d < K; ++d)
+        for (uint32_t l = 0; l < 2 * n_parent; ++l) {
+            double s = sd[(size_t)d * 2 * n_parent + l];
+            double avg = calc_average(s, sw[l], l2);
+            num += avg * s;
+        }
+    if (score_fn == ORC_SCORE_L2) return num;
+    double den = 0.0;
+    den += 1e-100;
+    for (int d = 0; d < K; ++d)
+        for (uint32_t l = 0; l < 2 * n_parent; ++l) {
+            double s = sd[(size_t)d * 2 * n_parent + l];
+            double avg = calc_average(s, sw[l], l2);
+            den += avg * avg * sw[l];
+        }
+    return num / sqrt(den);
+}
+
+/* scan_and_score_borders_into (histogram.rs:1007-1149) + multi_dim_split_score_into
+ * (score.rs:192-265) for one feature with n_parent = 2^level leaves. */
+static void scan_score(const double* h, uint32_t n_parent, uint32_t n_bins, int K,
+                       uint32_t n_borders, int score_fn, double l2, double* scores) {
+    const int C = K + 1;
+    double* total_w = (double*)calloc(n_parent, sizeof(double));
+    double* total_d = (double*)calloc((size_t)n_parent * K, sizeof(double));
+    double* acc_w = (double*)calloc(n_parent, sizeof(double));
+    double* acc_d = (double*)calloc((size_t)n_parent * K, sizeof(double));
+    double* sd = (double*)malloc(sizeof(double) * 2 * n_parent * K);
+    double* sw = (double*)malloc(sizeof(double) * 2 * n_parent);
+    parent_totals(h, n_parent, n_bins, K, total_w, total_d);
     for (uint32_t b = 0; b < n_borders; ++b) {
         for (uint32_t p = 0; p < n_parent; ++p) {
             const double* cell = h + ((size_t)p * n_bins + b) * C;
@@ -402,35 +433,44 @@ static void scan_score(const double* h, uint32_t n_parent, uint32_t n_bins, int 
                 sd[(size_t)d * 2 * n_parent + p + n_parent] = total_d[p * K + d] - acc_d[p * K + d];
             }
         }
-        /* fold in dimension-then-leaf order; leaves 0..P-1 FALSE, P..2P-1 TRUE */
-        double num = 0.0;
-        for (int d = 0; d < K; ++d)
-            for (uint32_t l = 0; l < 2 * n_parent; ++l) {
-                double s = sd[(size_t)d * 2 * n_parent + l];
-                double avg = calc_average(s, sw[l], l2);
-                num += avg * s;
-            }
-        if (score_fn == ORC_SCORE_L2) {
-            scores[b] = num;
-        } else {
-            double den = 0.0;
-            den += 1e-100;
-            for (int d = 0; d < K; ++d)
-                for (uint32_t l = 0; l < 2 * n_parent; ++l) {
-                    double s = sd[(size_t)d * 2 * n_parent + l];
-                    double avg = calc_average(s, sw[l], l2);
-                    den += avg * avg * sw[l];
-                }
-            scores[b] = num / sqrt(den);
-        }
+        scores[b] = fold_score(sd, sw, n_parent, K, score_fn, l2);
     }
     free(total_w); free(total_d); free(acc_w); free(acc_d); free(sd); free(sw);
+}
+
+/* scan_and_score_one_hot_bins_into (histogram.rs:1175-1287): per candidate value the TRUE
+ * child is that one bin's cell, the FALSE child the per-parent total minus it (totals are
+ * the same ordered bin sums as the border path); no prefix across candidates. */
+static void scan_score_one_hot(const double* h, uint32_t n_parent, uint32_t n_bins, int K,
+                               const uint32_t* values, uint32_t n_values, int score_fn,
+                               double l2, double* scores) {
+    const int C = K + 1;
+    double* total_w = (double*)calloc(n_parent, sizeof(double));
+    double* total_d = (double*)calloc((size_t)n_parent * K, sizeof(double));
+    double* sd = (double*)malloc(sizeof(double) * 2 * n_parent * K);
+    double* sw = (double*)malloc(sizeof(double) * 2 * n_parent);
+    parent_totals(h, n_parent, n_bins, K, total_w, total_d);
+    for (uint32_t v = 0; v < n_values; ++v) {
+        const uint32_t b = values[v];
+        for (uint32_t p = 0; p < n_parent; ++p) {
+            const double* cell = h + ((size_t)p * n_bins + b) * C;
+            sw[p] = total_w[p] - cell[K];
+            sw[p + n_parent] = cell[K];
+            for (int d = 0; d < K; ++d) {
+                sd[(size_t)d * 2 * n_parent + p] = total_d[p * K + d] - cell[d];
+                sd[(size_t)d * 2 * n_parent + p + n_parent] = cell[d];
+            }
+        }
+        scores[v] = fold_score(sd, sw, n_parent, K, score_fn, l2);
+    }
+    free(total_w); free(total_d); free(sd); free(sw);
 }
 
 int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n, uint32_t F,
                   const double* der, const double* w, int32_t K, int32_t depth, int32_t score_fn,
                   double l2, orc_rng* prng, int32_t n_threads, int32_t* out_splits,
-                  double* out_scores, uint32_t* out_leaf_of, double* out_hists) {
+                  double* out_scores, uint32_t* out_leaf_of, double* out_hists,
+                  const uint8_t* one_hot) {
     const int C = K + 1;
     uint32_t n_bins = 1;
     for (uint32_t f = 0; f < F; ++f)
@@ -439,6 +479,19 @@ int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
     memset(leaf_of, 0, sizeof(uint32_t) * n);
     double** hists = (double**)calloc(F, sizeof(double*));
     double** scores = (double**)calloc(F, sizeof(double*));
+    /* one-hot candidates: one per DISTINCT bin of the whole column, ascending
+     * (tree.rs:1305-1380 distinct_bins_ascending) */
+    uint32_t** oh_values = (uint32_t**)calloc(F, sizeof(uint32_t*));
+    uint32_t* n_cand = (uint32_t*)calloc(F, sizeof(uint32_t));
+    for (uint32_t f = 0; f < F; ++f) {
+        if (!(one_hot && one_hot[f])) { n_cand[f] = n_borders[f]; continue; }
+        uint8_t seen[256] = {0};
+        const uint8_t* col = bins_fm + (size_t)f * n;
+        for (uint64_t o = 0; o < n; ++o) seen[col[o]] = 1;
+        oh_values[f] = (uint32_t*)malloc(sizeof(uint32_t) * 256);
+        for (uint32_t v = 0; v < 256; ++v)
+            if (seen[v]) oh_values[f][n_cand[f]++] = v;
+    }
     size_t hist_off = 0;
 #ifdef _OPENMP
     int nt = n_threads > 0 ? n_threads : omp_get_max_threads();
@@ -447,8 +500,9 @@ int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
     for (int level = 0; level < depth; ++level) {
         uint32_t n_leaves = 1u << level;
         size_t per_f = (size_t)n_leaves * n_bins * C;
-        if (prng) /* per-level rsm reselection draws, one per listed feature (tree.rs:746-751) */
-            for (uint32_t f = 0; f < F; ++f) (void)orc_rng_real1(prng);
+        if (prng) /* per-level rsm reselection draws, one per listed float feature (tree.rs:746-751) */
+            for (uint32_t f = 0; f < F; ++f)
+                if (!(one_hot && one_hot[f])) (void)orc_rng_real1(prng);
         uint64_t n_true = 0;
         if (level > 0) {
             uint32_t bit = 1u << (level - 1);
@@ -464,7 +518,7 @@ int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
 #endif
             for (int64_t fi = 0; fi < (int64_t)F; ++fi) {
                 uint32_t f = (uint32_t)fi;
-                if (n_borders[f] == 0) continue; /* never scored, never built (WR-04) */
+                if (n_cand[f] == 0) continue; /* never scored, never built (WR-04) */
                 const uint8_t* col = bins_fm + (size_t)f * n;
                 double* h = (double*)malloc(sizeof(double) * per_f);
                 if (level == 0) {
@@ -476,8 +530,12 @@ int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
                 free(hists[f]);
                 hists[f] = h;
                 free(scores[f]);
-                scores[f] = (double*)malloc(sizeof(double) * n_borders[f]);
-                scan_score(h, n_leaves, n_bins, K, n_borders[f], score_fn, l2, scores[f]);
+                scores[f] = (double*)malloc(sizeof(double) * n_cand[f]);
+                if (oh_values[f])
+                    scan_score_one_hot(h, n_leaves, n_bins, K, oh_values[f], n_cand[f], score_fn, l2,
+                                       scores[f]);
+                else
+                    scan_score(h, n_leaves, n_bins, K, n_borders[f], score_fn, l2, scores[f]);
             }
             free(slot);
         }
@@ -497,26 +555,41 @@ int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
          * perturbed search at random_strength 0 picks the same candidate (instance = raw + 0)
          * and consumes 1 gen_rand + one std_normal per listed feature on the main stream
          * (tree.rs:1525-1611); the per-feature sub-streams never touch the main stream. */
-        int best_f = -1, best_b = -1;
+        /* one flat candidate list: every float (feature asc, border asc), then every one-hot
+         * column (feature asc, value asc) (tree.rs:1261-1290, select_best :355-366) */
+        int best_f = -1, best_b = -1, best_oh = 0;
         double best = -INFINITY;
-        for (uint32_t f = 0; f < F; ++f)
-            for (uint32_t b = 0; b < n_borders[f]; ++b)
-                if (scores[f][b] > best) { best = scores[f][b]; best_f = (int)f; best_b = (int)b; }
+        for (int pass = 0; pass < 2; ++pass)
+            for (uint32_t f = 0; f < F; ++f) {
+                if ((oh_values[f] != NULL) != (pass == 1)) continue;
+                for (uint32_t c = 0; c < n_cand[f]; ++c)
+                    if (scores[f][c] > best) {
+                        best = scores[f][c];
+                        best_f = (int)f;
+                        best_b = pass ? (int)oh_values[f][c] : (int)c;
+                        best_oh = pass;
+                    }
+            }
         if (prng) {
             (void)orc_rng_gen(prng);
-            for (uint32_t f = 0; f < F; ++f) (void)orc_std_normal(prng);
+            for (uint32_t f = 0; f < F; ++f)
+                if (!(one_hot && one_hot[f])) (void)orc_std_normal(prng);
         }
         if (best_f < 0) { rc = -1; break; }
-        out_splits[level * 2] = best_f;
+        out_splits[level * 2] = best_oh ? best_f | ORC_ONE_HOT_SPLIT : best_f;
         out_splits[level * 2 + 1] = best_b;
         if (out_scores) out_scores[level] = best;
         const uint8_t* col = bins_fm + (size_t)best_f * n;
-        for (uint64_t o = 0; o < n; ++o)
-            if (col[o] > (uint32_t)best_b) leaf_of[o] += n_leaves; /* advance_leaf_only */
+        for (uint64_t o = 0; o < n; ++o) { /* advance_leaf_only; one-hot passes on equality */
+            const int pass_bit = best_oh ? col[o] == (uint32_t)best_b : col[o] > (uint32_t)best_b;
+            if (pass_bit) leaf_of[o] += n_leaves;
+        }
     }
-    for (uint32_t f = 0; f < F; ++f) { free(hists[f]); free(scores[f]); }
+    for (uint32_t f = 0; f < F; ++f) { free(hists[f]); free(scores[f]); free(oh_values[f]); }
     free(hists);
     free(scores);
+    free(oh_values);
+    free(n_cand);
     return rc;
 }
 
@@ -532,6 +605,13 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
               double* out_leaf_values, double* out_approx, double* out_staged,
               double* out_bias) {
     const int K = p->loss == ORC_LOSS_MULTICLASS ? p->approx_dim : 1;
+    /* the learning rate that multiplies every leaf is the f32-representable one
+     * (boosting.rs:4958) */
+    const double lr = (double)(float)p->learning_rate;
+    int any_one_hot = 0;
+    for (uint32_t f = 0; p->one_hot_flags && f < F; ++f) any_one_hot |= p->one_hot_flags[f] != 0;
+    /* one-hot columns with active RNG draws are refused (boosting.rs:5744-5756) */
+    if (any_one_hot && p->bootstrap_type != ORC_BOOT_NO) return -4;
     const int depth = p->depth;
     const uint32_t n_leaves = 1u << depth;
     const int pk = K * (K + 1) / 2;
@@ -592,7 +672,7 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
         int32_t* splits = out_splits + (size_t)it * depth * 2;
         rc = orc_grow_tree(bins_fm, n_borders, n, F, sder, swt, K, depth, p->score_function,
                            scaled_l2, draws_active ? &rng : NULL, p->n_threads, splits, NULL,
-                           leaf_of, NULL);
+                           leaf_of, NULL, p->one_hot_flags);
         if (rc) break;
 
         /* leaf values on the UNSAMPLED derivatives (boosting.rs:2470-2560, :2634) */
@@ -627,7 +707,7 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
         }
         /* NormalizeLeafValues: non-pairwise losses only scale by the learning rate
          * (boosting.rs:2844-2882); then approx += leaf value (boosting.rs:8560-8572) */
-        for (uint32_t x = 0; x < n_leaves * K; ++x) leaf_vals[x] *= p->learning_rate;
+        for (uint32_t x = 0; x < n_leaves * K; ++x) leaf_vals[x] *= lr;
         for (int d = 0; d < K; ++d)
             for (uint64_t i = 0; i < n; ++i)
                 approx[(size_t)d * n + i] += leaf_vals[(size_t)d * n_leaves + leaf_of[i]];

@@ -56,7 +56,11 @@ typedef struct {
     float bagging_temperature;
     float pad2_;
     uint64_t random_seed;
+    const uint8_t* one_hot_flags; /* nullable [F]: one-hot categorical columns */
 } orc_params;
+
+/* out_splits feature entries of one-hot (equality) splits carry this flag bit */
+#define ORC_ONE_HOT_SPLIT 0x40000000
 
 /* ---- RNG (cb-core/src/rng.rs, normal.rs) ---- */
 void orc_rng_new(orc_rng* r, uint64_t seed1, uint32_t seq1, uint64_t seed2, uint32_t seq2);
@@ -91,12 +95,15 @@ void orc_ders(int32_t loss, const double* approx, const double* target, uint64_t
  *  out_scores  [depth] winning score per level
  *  out_leaf_of [n]
  *  out_hists   nullable; per level l, (2^l * F * n_bins * (K+1)) doubles, ch 0..K-1 der, K weight
+ *  one_hot     nullable [F]: one-hot columns; their candidates are the distinct bins of the
+ *              column (equality splits, scored after every float candidate), reported as
+ *              (feature | ORC_ONE_HOT_SPLIT, value); n_borders[f] + 1 bounds their bins
  * returns 0, or <0 on a degenerate level (no candidate). */
 int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n, uint32_t F,
                   const double* score_der, const double* score_w, int32_t K, int32_t depth,
                   int32_t score_function, double scaled_l2, orc_rng* perturb_rng, int32_t n_threads,
                   int32_t* out_splits, double* out_scores, uint32_t* out_leaf_of,
-                  double* out_hists);
+                  double* out_hists, const uint8_t* one_hot);
 
 /* Per-leaf ordered sums (cb-compute/src/histogram.rs:49 reduce_leaf_stats, :97 reduce_leaf_der2). */
 void orc_leaf_sums(const uint32_t* leaf_of, uint64_t n, uint32_t n_leaves, const double* der,
@@ -107,7 +114,8 @@ void orc_leaf_sums(const uint32_t* leaf_of, uint64_t n, uint32_t n_leaves, const
  *  out_leaf_values  [iterations][2^depth * K]  learning-rate scaled (model leaf values)
  *  out_approx       [K][n] final raw approx (nullable)
  *  out_staged       [iterations][K][n] (nullable)
- *  out_bias         starting approx (nullable) */
+ *  out_bias         starting approx (nullable)
+ * returns 0, -1 on a degenerate level, -4 for one-hot columns with active RNG draws. */
 int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
               uint32_t F, const double* target, const double* weight, int32_t* out_splits,
               double* out_leaf_values, double* out_approx, double* out_staged, double* out_bias);

@@ -35,7 +35,11 @@ class Params(C.Structure):
                 ("approx_dim", C.c_int32), ("pad_", C.c_int32),
                 ("learning_rate", C.c_double), ("l2_leaf_reg", C.c_double),
                 ("subsample", C.c_double), ("bagging_temperature", C.c_float),
-                ("pad2_", C.c_float), ("random_seed", C.c_uint64)]
+                ("pad2_", C.c_float), ("random_seed", C.c_uint64),
+                ("one_hot_flags", C.c_void_p)]
+
+
+ONE_HOT_SPLIT = 0x40000000  # flag bit on the feature entry of an equality split
 
 
 def build(force: bool = False) -> str:
@@ -70,7 +74,7 @@ def lib():
         L.orc_quantize.argtypes = [P, C.c_uint64, P, C.c_uint32, P]
         L.orc_ders.argtypes = [C.c_int32, P, P, C.c_uint64, P, P]
         L.orc_grow_tree.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, C.c_int32, C.c_int32,
-                                    C.c_int32, C.c_double, C.POINTER(Rng), C.c_int32, P, P, P, P]
+                                    C.c_int32, C.c_double, C.POINTER(Rng), C.c_int32, P, P, P, P, P]
         L.orc_grow_tree.restype = C.c_int
         L.orc_leaf_sums.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P]
         L.orc_train.argtypes = [C.POINTER(Params), P, P, C.c_uint64, C.c_uint32, P, P, P, P, P, P, P]
@@ -124,9 +128,19 @@ def ders(loss: str, approx: np.ndarray, target: np.ndarray):
     return d1, d2
 
 
+def _split_flags(splits):
+    """Strip the one-hot flag bit from the feature entries; return (splits, one_hot)."""
+    one_hot = (splits[..., 0] & ONE_HOT_SPLIT) != 0
+    splits = splits.copy()
+    splits[..., 0] &= ~ONE_HOT_SPLIT
+    return splits, one_hot
+
+
 def grow_tree(bins_fm, n_borders, score_der, score_w, depth, score="Cosine", scaled_l2=3.0,
-              rng: Rng | None = None, want_hists=False, n_threads=0):
-    """One oblivious tree.  ``bins_fm`` is u8 [F, n]; ``score_der`` is [K, n] or [n]."""
+              rng: Rng | None = None, want_hists=False, n_threads=0, one_hot=None):
+    """One oblivious tree.  ``bins_fm`` is u8 [F, n]; ``score_der`` is [K, n] or [n].
+    ``one_hot`` (optional, [F]) flags one-hot columns; for them ``n_borders[f] + 1`` is the
+    column's cardinality."""
     bins_fm = np.ascontiguousarray(bins_fm, np.uint8)
     F, n = bins_fm.shape
     nb = np.ascontiguousarray(n_borders, np.uint32)
@@ -141,12 +155,14 @@ def grow_tree(bins_fm, n_borders, score_der, score_w, depth, score="Cosine", sca
     if want_hists:
         total = sum((1 << l) * F * n_bins * (K + 1) for l in range(depth))
         hists = np.zeros(total, np.float64)
+    oh = None if one_hot is None else np.ascontiguousarray(one_hot, np.uint8)
     rc = lib().orc_grow_tree(_p(bins_fm), _p(nb), n, F, _p(sd), _p(sw), K, depth, SCORE[score],
                              scaled_l2, C.byref(rng) if rng is not None else None, n_threads,
-                             _p(splits), _p(scores), _p(leaf_of), _p(hists))
+                             _p(splits), _p(scores), _p(leaf_of), _p(hists), _p(oh))
     if rc != 0:
         raise RuntimeError(f"orc_grow_tree failed rc={rc}")
-    out = {"splits": splits, "scores": scores, "leaf_of": leaf_of, "n_bins": n_bins}
+    splits, is_oh = _split_flags(splits)
+    out = {"splits": splits, "one_hot": is_oh, "scores": scores, "leaf_of": leaf_of, "n_bins": n_bins}
     if want_hists:
         levels = []
         off = 0
@@ -171,7 +187,10 @@ def leaf_sums(leaf_of, n_leaves, der, weight=None):
 def train(bins_fm, n_borders, target, *, loss="RMSE", depth=6, iterations=10, learning_rate=0.1,
           l2_leaf_reg=3.0, score="Cosine", bootstrap_type="No", subsample=0.66,
           bagging_temperature=1.0, leaf_method="Gradient", boost_from_average=False,
-          random_seed=0, weight=None, approx_dim=1, n_threads=0, staged=False):
+          random_seed=0, weight=None, approx_dim=1, n_threads=0, staged=False, one_hot=None):
+    """CPU boosting loop.  ``one_hot`` (optional, [F]) flags one-hot columns (for them
+    ``n_borders[f] + 1`` is the cardinality); one-hot with bootstrap raises (-4), as the
+    reference refuses it."""
     bins_fm = np.ascontiguousarray(bins_fm, np.uint8)
     F, n = bins_fm.shape
     nb = np.ascontiguousarray(n_borders, np.uint32)
@@ -183,6 +202,8 @@ def train(bins_fm, n_borders, target, *, loss="RMSE", depth=6, iterations=10, le
                boost_from_average=int(boost_from_average), n_threads=n_threads, approx_dim=K,
                learning_rate=learning_rate, l2_leaf_reg=l2_leaf_reg, subsample=subsample,
                bagging_temperature=bagging_temperature, random_seed=random_seed)
+    oh = None if one_hot is None else np.ascontiguousarray(one_hot, np.uint8)
+    p.one_hot_flags = None if oh is None else oh.ctypes.data
     splits = np.zeros((iterations, depth, 2), np.int32)
     leaves = np.zeros((iterations, K, 1 << depth), np.float64)
     approx = np.zeros((K, n), np.float64)
@@ -192,7 +213,9 @@ def train(bins_fm, n_borders, target, *, loss="RMSE", depth=6, iterations=10, le
                          _p(leaves), _p(approx), _p(st), _p(bias))
     if rc != 0:
         raise RuntimeError(f"orc_train failed rc={rc}")
-    out = {"splits": splits, "leaf_values": leaves, "approx": approx, "bias": float(bias[0])}
+    splits, is_oh = _split_flags(splits)
+    out = {"splits": splits, "one_hot": is_oh, "leaf_values": leaves, "approx": approx,
+           "bias": float(bias[0])}
     if staged:
         out["staged"] = st
     return out

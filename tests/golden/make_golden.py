@@ -16,6 +16,9 @@ expected outputs); no reference source is copied.  Sources:
 * ``upstream_*.npz``      -- catboost 1.2.10 fits under crates/cb-oracle/fixtures/
                              (inputs, used borders, per-tree splits and leaf values, staged
                              approx, predictions).
+* ``upstream_one_hot_*``  -- catboost 1.2.10 one-hot fits (one_hot_train/*): float inputs,
+                             categorical columns as first-seen bins, used borders, splits
+                             (one-hot values as bins), leaf values, predictions.
 """
 from __future__ import annotations
 
@@ -87,6 +90,82 @@ def upstream(ref, scen):
     json.dump(meta, open(os.path.join(HERE, name + ".json"), "w"), indent=1)
 
 
+def _first_seen_bins(col):
+    """Dense bins in first-seen order (the PerfectHash remap, cb-data/src/cat_hash.rs:380-471)."""
+    index, bins = {}, np.empty(len(col), np.uint8)
+    for i, v in enumerate(col):
+        bins[i] = index.setdefault(v, len(index))
+    return bins, list(index)
+
+
+def one_hot_train(ref, scen):
+    """catboost 1.2.10 one-hot fits (one_hot_train/{default_binary,multi}).  The model stores a
+    one-hot split as the CityHash of the category label; which label that is follows from the
+    model itself: the label assignment under which applying the model reproduces the
+    fixture's predictions.  Splits are written as first-seen bins of that label."""
+    import itertools
+
+    fx = os.path.join(ref, "crates/cb-oracle/fixtures/one_hot_train", scen)
+    cfg = json.load(open(os.path.join(fx, "config.json")))
+    model = json.load(open(os.path.join(fx, "model.json")))
+    X = np.load(os.path.join(fx, "X_float.npy"))
+    y = np.load(os.path.join(fx, "y.npy"))
+    preds = np.load(os.path.join(fx, "predictions.npy"))
+    cols = json.load(open(os.path.join(fx, "cat_cols.json")))["columns"]
+    cat = [_first_seen_bins(c) for c in cols]
+    cat_bins = np.stack([b for b, _ in cat])
+    labels = [l for _, l in cat]
+    borders = [np.asarray(f["borders"], np.float64) for f in model["features_info"]["float_features"]]
+    trees = model["oblivious_trees"]
+    hashes = {}  # cat feature -> sorted used hash values
+    for t in trees:
+        for sp in t["splits"]:
+            if sp["split_type"] == "OneHotFeature":
+                hashes.setdefault(sp["cat_feature_index"], set()).add(sp["value"])
+    feats = sorted(hashes)
+    choices = [list(itertools.permutations(range(len(labels[c])), len(hashes[c]))) for c in feats]
+
+    def apply(assign):
+        out = np.zeros(X.shape[0])
+        for t in trees:
+            idx = np.zeros(X.shape[0], np.int64)
+            for lvl, sp in enumerate(t["splits"]):
+                if sp["split_type"] == "FloatFeature":
+                    bit = X[:, sp["float_feature_index"]].astype(np.float32) > sp["border"]
+                else:
+                    c = sp["cat_feature_index"]
+                    bit = cat_bins[c] == assign[c][sp["value"]]
+                idx |= bit.astype(np.int64) << lvl
+            out += np.asarray(t["leaf_values"])[idx]
+        return out
+
+    found = None
+    for combo in itertools.product(*choices):
+        assign = {c: dict(zip(sorted(hashes[c]), perm)) for c, perm in zip(feats, combo)}
+        if np.max(np.abs(apply(assign) - preds)) < 1e-9:
+            assert found is None, "label assignment is ambiguous"
+            found = assign
+    assert found is not None, "no label assignment reproduces the predictions"
+    depth = len(trees[0]["splits"])
+    kind = np.array([[sp["split_type"] == "OneHotFeature" for sp in t["splits"]] for t in trees])
+    feat = np.array([[sp.get("float_feature_index", sp.get("cat_feature_index")) for sp in t["splits"]]
+                     for t in trees], np.int64)
+    border = np.array([[sp.get("border", np.nan) for sp in t["splits"]] for t in trees], np.float64)
+    value_bin = np.array([[found[sp["cat_feature_index"]][sp["value"]] if sp["split_type"] == "OneHotFeature"
+                           else -1 for sp in t["splits"]] for t in trees], np.int64)
+    name = "upstream_one_hot_" + scen
+    np.savez_compressed(os.path.join(HERE, name + ".npz"), X=X, y=y, cat_bins=cat_bins,
+                        borders=np.concatenate(borders) if borders else np.zeros(0),
+                        n_borders=np.array([len(b) for b in borders], np.int64),
+                        split_one_hot=kind, split_feature=feat, split_border=border,
+                        split_value_bin=value_bin,
+                        leaf_values=np.array([t["leaf_values"] for t in trees], np.float64),
+                        predictions=preds)
+    meta = {"scenario": "one_hot_train/" + scen, "params": cfg["params"], "depth": depth,
+            "cat_labels_first_seen": labels, "catboost_version": cfg.get("catboost_version")}
+    json.dump(meta, open(os.path.join(HERE, name + ".json"), "w"), indent=1)
+
+
 def main():
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     rng_kat(ref)
@@ -94,6 +173,8 @@ def main():
     depth6(ref)
     for s in UPSTREAM:
         upstream(ref, s)
+    for s in ("default_binary", "multi"):
+        one_hot_train(ref, s)
 
 
 if __name__ == "__main__":

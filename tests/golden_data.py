@@ -44,3 +44,28 @@ def fast_logf_rows():
         _, a, b = line.split()
         rows.append((int(a, 16), int(b, 16)))
     return rows
+
+
+def upstream_one_hot(name: str):
+    """One catboost 1.2.10 one-hot fit: float columns (to be quantized with the model's used
+    borders) and categorical first-seen bins, laid out float | one-hot as on the reference's
+    device feature axis."""
+    z = np.load(os.path.join(GOLDEN, f"upstream_one_hot_{name}.npz"))
+    meta = json.load(open(os.path.join(GOLDEN, f"upstream_one_hot_{name}.json")))
+    nb = z["n_borders"]
+    offs = np.concatenate([[0], np.cumsum(nb)])
+    borders = [z["borders"][offs[i]:offs[i + 1]] for i in range(len(nb))]
+    cat = z["cat_bins"]
+    card = [int(c.max()) + 1 for c in cat]
+    n_float = z["X"].shape[1]
+    return dict(X=z["X"], y=z["y"].astype(np.float64), borders=borders, cat_bins=cat,
+                n_float=n_float,
+                # oracle convention: n_borders[f] + 1 = bins of f (cardinality for one-hot)
+                n_borders=np.array(list(nb) + [c - 1 for c in card], np.uint32),
+                one_hot=np.array([0] * n_float + [1] * len(card), np.uint8),
+                # device convention (real_folds, boosting.rs:4334-4372)
+                real_folds=np.array([len(b) + 1 for b in borders] + card, np.uint32),
+                split_one_hot=z["split_one_hot"], split_feature=z["split_feature"],
+                split_border=z["split_border"], split_value_bin=z["split_value_bin"],
+                leaf_values=z["leaf_values"], predictions=z["predictions"], meta=meta,
+                params=meta["params"])

@@ -91,3 +91,15 @@ def test_config_decline_paths(lib):
     rc = lib.cbh_session_begin_u8(C.byref(cfg), bad.ctypes.data_as(C.c_void_p), None, 8, 2, 4, 0.1,
                                   3.0, C.byref(s))
     assert rc == -2  # bin >= n_bins -> OutOfRange
+
+
+def test_one_hot_with_bootstrap_is_refused(lib):
+    """The caller side refuses one-hot columns with active RNG draws (boosting.rs:5744-5756)
+    before any device call."""
+    import numpy as np
+    bins = np.zeros((2, 8), np.uint8)
+    bins[1, ::2] = 1
+    with pytest.raises(cb.CbhError) as e:
+        cb.Trainer(bins, 2, np.zeros(8), loss="RMSE", depth=2, bootstrap_type="Bernoulli",
+                   one_hot_flags=np.array([0, 1], np.uint8), real_folds=np.array([2, 2], np.uint32))
+    assert e.value.code == -4

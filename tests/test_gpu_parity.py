@@ -16,6 +16,7 @@ import catboost_rs_amd as cb
 from catboost_rs_amd import datagen
 from oracle import oracle as O
 from tests import golden_data as G
+from tests.trees import one_hot_bins, same_partition, upstream_one_hot_splits
 
 pytestmark = pytest.mark.gpu
 
@@ -199,3 +200,79 @@ def test_upstream_catboost_fits_on_gpu(name):
     n = u["X"].shape[0]
     final = u["staged"].reshape(P["iterations"], n, K)[-1]
     np.testing.assert_allclose(approx.T, final, rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------------------- one-hot columns
+@pytest.mark.parametrize("name", ["default_binary", "multi"])
+def test_one_hot_upstream_fits_on_gpu(name):
+    """catboost 1.2.10 one-hot fits on the device: equality candidates bounded by real_folds
+    (runtime.rs:1315-1332), scored after every float candidate.  Same partitions as
+    upstream every tree (a tied binary column may be tested on its other value), leaf values
+    after that bit flip, predictions to 1e-5."""
+    u = G.upstream_one_hot(name)
+    p = u["params"]
+    bins = one_hot_bins(u, O.quantize)
+    tr = cb.Trainer(bins, int(u["real_folds"].max()), u["y"], loss="Logloss", depth=p["depth"],
+                    learning_rate=p["learning_rate"], l2_leaf_reg=p["l2_leaf_reg"],
+                    score=p["score_function"], leaf_method="Gradient", bootstrap_type="No",
+                    boost_from_average=p["boost_from_average"], real_folds=u["real_folds"],
+                    one_hot_flags=u["one_hot"])
+    try:
+        splits, leaves, kinds = tr.fit(p["iterations"], with_one_hot=True)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    assert kinds.any()
+    for t in range(p["iterations"]):
+        sp, oh = upstream_one_hot_splits(u, t)
+        ok, flip = same_partition(bins, splits[t], kinds[t], sp, oh)
+        assert ok, f"tree {t}: {splits[t].tolist()} vs {sp}"
+        perm = np.arange(leaves.shape[2]) ^ flip
+        _close(leaves[t, 0][perm], u["leaf_values"][t])
+    _close(approx[0], u["predictions"])
+
+
+def _mixed_case(seed, n, n_float, cards):
+    g = np.random.default_rng(seed)
+    nb = g.integers(1, 48, size=n_float)
+    fb = [g.integers(0, b + 1, size=n) for b in nb]
+    cb_ = []
+    for c in cards:  # skewed category frequencies, every value present
+        p = 1.0 / np.arange(1, c + 1) ** 1.1
+        col = g.choice(c, size=n, p=p / p.sum())
+        col[:c] = np.arange(c)
+        cb_.append(col)
+    bins = np.stack(fb + cb_).astype(np.uint8)
+    one_hot = np.array([0] * n_float + [1] * len(cards), np.uint8)
+    n_borders = np.array(list(nb) + [c - 1 for c in cards], np.uint32)      # oracle convention
+    real_folds = np.array([b + 1 for b in nb] + list(cards), np.uint32)     # device convention
+    return bins, one_hot, n_borders, real_folds, g
+
+
+@pytest.mark.parametrize("loss,score", [("RMSE", "Cosine"), ("Logloss", "L2"), ("RMSE", "L2")])
+def test_one_hot_boosting_matches_oracle(loss, score):
+    bins, one_hot, nb, rf, g = _mixed_case(7 if loss == "RMSE" else 8, 20_000, 9, [2, 3, 5, 9, 16])
+    # a target driven by the categorical columns so that equality splits win often
+    y = g.normal(size=bins.shape[1]) + 0.8 * (bins[11] == 2) - 0.6 * (bins[13] == 7) + 0.3 * bins[0] / 40
+    if loss == "Logloss":
+        y = (y > 0.4).astype(np.float64)
+    depth, iters = 5, 10
+    exp = O.train(bins, nb, y, loss=loss, depth=depth, iterations=iters, learning_rate=0.3,
+                  l2_leaf_reg=2.0, score=score, leaf_method="Gradient", bootstrap_type="No",
+                  one_hot=one_hot)
+    tr = cb.Trainer(bins, int(rf.max()), y, loss=loss, depth=depth, learning_rate=0.3, l2_leaf_reg=2.0,
+                    score=score, leaf_method="Gradient", bootstrap_type="No", real_folds=rf,
+                    one_hot_flags=one_hot)
+    try:
+        splits, leaves, kinds = tr.fit(iters, with_one_hot=True)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    assert exp["one_hot"].any() and kinds.any()
+    for t in range(iters):
+        ok, flip = same_partition(bins, splits[t], kinds[t], exp["splits"][t], exp["one_hot"][t])
+        assert ok, f"tree {t}: {splits[t].tolist()} {kinds[t].tolist()} vs " \
+                   f"{exp['splits'][t].tolist()} {exp['one_hot'][t].tolist()}"
+        perm = np.arange(leaves.shape[2]) ^ flip
+        _close(leaves[t, 0][perm], exp["leaf_values"][t, 0])
+    _close(approx, exp["approx"])

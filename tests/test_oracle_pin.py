@@ -12,6 +12,7 @@ import pytest
 
 from oracle import oracle as O
 from tests import golden_data as G
+from tests.trees import one_hot_bins, same_partition, upstream_one_hot_splits
 
 
 def test_rng_known_answers():
@@ -166,4 +167,88 @@ def test_tree_matches_bruteforce_partition_scoring(seed):
         np.testing.assert_allclose(h[:, :, :, 1].sum(axis=2), np.repeat(tot_w[:, None], F, 1)
                                    * (nb[None, :] > 0), rtol=1e-12, atol=1e-12)
         leaf_of = leaf_of + (bins[f] > b) * (1 << level)
+    assert np.array_equal(out["leaf_of"], leaf_of)
+
+
+# ------------------------------------------------------------------------------ one-hot
+def _upstream_one_hot_fit(name):
+    u = G.upstream_one_hot(name)
+    p = u["params"]
+    bins = one_hot_bins(u, O.quantize)
+    out = O.train(bins, u["n_borders"], u["y"], loss="Logloss", depth=p["depth"],
+                  iterations=p["iterations"], learning_rate=p["learning_rate"],
+                  l2_leaf_reg=p["l2_leaf_reg"], score=p["score_function"], leaf_method="Gradient",
+                  bootstrap_type="No", boost_from_average=p["boost_from_average"],
+                  one_hot=u["one_hot"], staged=True)
+    return u, bins, out
+
+
+@pytest.mark.parametrize("name", ["default_binary", "multi"])
+def test_one_hot_upstream_fit(name):
+    """One-hot equality candidates (scan_and_score_one_hot_bins_into, histogram.rs:1175-1287;
+    append_one_hot_candidates, tree.rs:1305) and the f32 learning rate (boosting.rs:4958)
+    against catboost 1.2.10: same partitions every tree, leaf values (after the bit flip of a
+    tied binary column) and predictions to 1e-12."""
+    u, bins, out = _upstream_one_hot_fit(name)
+    T = u["split_feature"].shape[0]
+    for t in range(T):
+        sp, oh = upstream_one_hot_splits(u, t)
+        ok, flip = same_partition(bins, out["splits"][t], out["one_hot"][t], sp, oh)
+        assert ok, f"tree {t}: {out['splits'][t].tolist()} vs {sp}"
+        mine = out["leaf_values"][t, 0]
+        perm = np.arange(mine.shape[0]) ^ flip
+        np.testing.assert_allclose(mine[perm], u["leaf_values"][t], rtol=0, atol=1e-12)
+    assert np.abs(out["approx"][0] - u["predictions"]).max() <= 1e-12
+    assert out["one_hot"].any()
+
+
+def test_one_hot_with_bootstrap_is_refused():
+    """boosting.rs:5744-5756: one-hot columns with active RNG draws -> Unsupported."""
+    u = G.upstream_one_hot("default_binary")
+    bins = one_hot_bins(u, O.quantize)
+    with pytest.raises(RuntimeError, match="rc=-4"):
+        O.train(bins, u["n_borders"], u["y"], loss="Logloss", depth=2, iterations=1,
+                bootstrap_type="Bernoulli", one_hot=u["one_hot"])
+
+
+def _brute_scores_one_hot(bins_fm, n_borders, one_hot, der, w, leaf_of, n_leaves, l2):
+    """Every float and one-hot candidate scored from scratch (bincount partitions), keyed in
+    enumeration order: (0, f, b) floats first, then (1, f, v) one-hot values present."""
+    res = {}
+    for f in range(bins_fm.shape[0]):
+        cands = np.unique(bins_fm[f]) if one_hot[f] else range(int(n_borders[f]))
+        for b in cands:
+            passed = (bins_fm[f] == b) if one_hot[f] else (bins_fm[f] > b)
+            new_leaf = leaf_of + passed * n_leaves
+            s = np.bincount(new_leaf, weights=der, minlength=2 * n_leaves)
+            ww = np.bincount(new_leaf, weights=w, minlength=2 * n_leaves)
+            avg = np.where(ww > 0, s / (ww + l2), 0.0)
+            res[(int(one_hot[f]), f, int(b))] = float(np.sum(avg * s)) / np.sqrt(
+                1e-100 + float(np.sum(avg * avg * ww)))
+    return res
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_one_hot_tree_matches_bruteforce(seed):
+    rng = np.random.default_rng(100 + seed)
+    n, depth = 400, 4
+    nb = np.array([7, 5, 0, 9, 4, 2, 6], np.uint32)      # floats: borders; one-hot: card - 1
+    one_hot = np.array([0, 0, 0, 1, 1, 1, 0], np.uint8)
+    bins = np.stack([rng.integers(0, nb[f] + 1, size=n) for f in range(nb.shape[0])]).astype(np.uint8)
+    der = rng.normal(size=n)
+    w = rng.uniform(0.2, 2.0, size=n)
+    out = O.grow_tree(bins, nb, der, w, depth, "Cosine", 1.5, one_hot=one_hot)
+    leaf_of = np.zeros(n, np.int64)
+    for level in range(depth):
+        sc = _brute_scores_one_hot(bins, nb, one_hot, der, w, leaf_of, 1 << level, 1.5)
+        best = max(sc.values())
+        f, b = (int(x) for x in out["splits"][level])
+        key = (int(out["one_hot"][level]), f, b)
+        assert key[0] == one_hot[f]
+        assert abs(sc[key] - best) <= 1e-12 * abs(best)
+        tied = [k for k, v in sc.items() if v >= best * (1 - 1e-12)]
+        # first in enumeration order, or the complementary value of a binary one-hot column
+        assert key == min(tied) or (key[0] == 1 and nb[f] == 1 and min(tied)[:2] == key[:2])
+        passed = (bins[f] == b) if key[0] else (bins[f] > b)
+        leaf_of = leaf_of + passed * (1 << level)
     assert np.array_equal(out["leaf_of"], leaf_of)
