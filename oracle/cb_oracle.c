@@ -241,19 +241,19 @@ static double newton_leaf_delta(double s, double d2, double l2) { /* leaf.rs:223
 
 /* leaf.rs:387-440 cholesky_solve; returns 0 on a non-positive pivot. */
 static int cholesky_solve(int k, const double* a, const double* b, double* x) {
-    double l[64 * 64];
-    double y[64];
-    memset(l, 0, sizeof(double) * (size_t)k * (size_t)k);
+    double* l = (double*)calloc((size_t)k * (size_t)k + (size_t)k, sizeof(double));
+    double* y = l + (size_t)k * k;
+    int ok = 1;
     for (int i = 0; i < k; ++i) {
         for (int j = 0; j <= i; ++j) {
             double sum = a[i * k + j];
             for (int p = 0; p < j; ++p) sum -= l[i * k + p] * l[j * k + p];
             if (i == j) {
-                if (sum <= 0.0) return 0;
+                if (sum <= 0.0) { ok = 0; goto done; }
                 l[i * k + j] = sqrt(sum);
             } else {
                 double ljj = l[j * k + j];
-                if (ljj == 0.0) return 0;
+                if (ljj == 0.0) { ok = 0; goto done; }
                 l[i * k + j] = sum / ljj;
             }
         }
@@ -261,16 +261,18 @@ static int cholesky_solve(int k, const double* a, const double* b, double* x) {
     for (int i = 0; i < k; ++i) {
         double sum = b[i];
         for (int p = 0; p < i; ++p) sum -= l[i * k + p] * y[p];
-        if (l[i * k + i] == 0.0) return 0;
+        if (l[i * k + i] == 0.0) { ok = 0; goto done; }
         y[i] = sum / l[i * k + i];
     }
     for (int i = k - 1; i >= 0; --i) {
         double sum = y[i];
         for (int p = i + 1; p < k; ++p) sum -= l[p * k + i] * x[p];
-        if (l[i * k + i] == 0.0) return 0;
+        if (l[i * k + i] == 0.0) { ok = 0; goto done; }
         x[i] = sum / l[i * k + i];
     }
-    return 1;
+done:
+    free(l);
+    return ok;
 }
 
 /* solve_symmetric_newton (leaf.rs:279-335). */
@@ -593,6 +595,310 @@ int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
     return rc;
 }
 
+
+/* ======================================================================
+ * Pairwise ranking: PairLogit / PairLogitPairwise
+ *   pairs are given in the reference's competitor order: group ascending, winner
+ *   ascending, insertion order within a winner (query_info.rs:205-250 builds
+ *   competitors[winner] in input order; tree.rs:3790-3800 flattens them group by group).
+ *   orc_pairs_order() produces that order from an arbitrary input order.
+ * ==================================================================== */
+
+/* Stable order of the pairs by winner (counting sort): out_perm[k] = input index. */
+void orc_pairs_order(const uint32_t* winner, uint64_t m, uint64_t n, uint64_t* out_perm) {
+    uint64_t* cnt = (uint64_t*)calloc(n + 1, sizeof(uint64_t));
+    for (uint64_t k = 0; k < m; ++k) cnt[winner[k] + 1]++;
+    for (uint64_t i = 0; i < n; ++i) cnt[i + 1] += cnt[i];
+    for (uint64_t k = 0; k < m; ++k) out_perm[cnt[winner[k]]++] = k;
+    free(cnt);
+}
+
+/* pairlogit_pair_prob (loss.rs:640-651). */
+static double pairlogit_p(double winner_approx, double loser_approx) {
+    double el = exp(loser_approx), ew = exp(winner_approx);
+    double den = el + ew;
+    return den > 0.0 ? el / den : 0.5;
+}
+
+/* pairlogit_group_der (ranking_der.rs:408-445): docs ascending, each winner's competitors
+ * in order; a loser's der is decremented as each winner is visited, a winner's own der is
+ * added after its competitor loop.  Groups are contiguous and pairs never cross groups,
+ * so visiting all docs in global order is the per-group visit order. */
+void orc_pairlogit_ders(const double* approx, uint64_t n, const uint32_t* winner,
+                        const uint32_t* loser, const double* weight, uint64_t m, double* der1,
+                        double* der2) {
+    for (uint64_t i = 0; i < n; ++i) { der1[i] = 0.0; der2[i] = 0.0; }
+    uint64_t k = 0;
+    for (uint64_t doc = 0; doc < n; ++doc) {
+        double wd = 0.0, wd2 = 0.0;
+        for (; k < m && winner[k] == doc; ++k) {
+            double p = pairlogit_p(approx[doc], approx[loser[k]]);
+            double w = weight ? weight[k] : 1.0;
+            wd += w * p;
+            wd2 += w * p * (p - 1.0);
+            der1[loser[k]] -= w * p;
+            der2[loser[k]] += w * p * (p - 1.0);
+        }
+        der1[doc] += wd;
+        der2[doc] += wd2;
+    }
+}
+
+/* calc_pairwise_weights (boosting.rs:1760-1783): pw[obj] = sum of the weights of the pairs
+ * incident on obj, in pair order. */
+void orc_pairwise_weights(uint64_t n, const uint32_t* winner, const uint32_t* loser,
+                          const double* weight, uint64_t m, double* pw) {
+    for (uint64_t i = 0; i < n; ++i) pw[i] = 0.0;
+    for (uint64_t k = 0; k < m; ++k) {
+        double w = weight ? weight[k] : 1.0;
+        pw[winner[k]] += w;
+        pw[loser[k]] += w;
+    }
+}
+
+/* MakeZeroAverage (pairwise_scoring.rs:255-265). */
+static void make_zero_average(double* r, int n) {
+    if (n == 0) return;
+    double avg = 0.0;
+    for (int i = 0; i < n; ++i) avg += r[i];
+    avg /= (double)n;
+    for (int i = 0; i < n; ++i) r[i] -= avg;
+}
+
+/* calculate_pairwise_leaf_values (pairwise_leaves.rs:120-200, pairwise_scoring.rs:283-345):
+ * (n-1)x(n-1) SPD system with the bucket-weight prior, last value pinned to 0, then
+ * zero-averaged.  w is n x n row-major. */
+static void pairwise_leaf_values(const double* w, const double* der, int n, double l2,
+                                 double prior, double* res) {
+    if (n == 0) return;
+    double cell_prior = 1.0 / (double)n;
+    double non_diag = -prior * cell_prior;
+    double diag = prior * (1.0 - cell_prior) + l2;
+    if (n == 1) { res[0] = 0.0; return; }
+    if (n == 2) {
+        double den = w[0] + diag;
+        res[0] = den != 0.0 ? der[0] / den : 0.0;
+        res[1] = 0.0;
+        make_zero_average(res, 2);
+        return;
+    }
+    int m = n - 1;
+    double* a = (double*)calloc((size_t)m * m, sizeof(double));
+    for (int y = 0; y < m; ++y) {
+        for (int x = 0; x < y; ++x) {
+            double v = w[y * n + x] + non_diag;
+            a[y * m + x] = v;
+            a[x * m + y] = v;
+        }
+        a[y * m + y] = w[y * n + y] + diag;
+    }
+    if (!cholesky_solve(m, a, der, res))
+        for (int i = 0; i < m; ++i) res[i] = 0.0;
+    res[m] = 0.0;
+    make_zero_average(res, n);
+    free(a);
+}
+
+/* CalculateScore (pairwise_scoring.rs:352-375): sum_x a[x] (der[x] - 0.5 sum_y a[y] w[x][y]). */
+static double pairwise_score_value(const double* a, const double* der, const double* w, int n) {
+    double outer = 0.0;
+    for (int x = 0; x < n; ++x) {
+        double inner = 0.0;
+        for (int y = 0; y < n; ++y) inner += a[y] * w[x * n + y];
+        outer += a[x] * (der[x] - 0.5 * inner);
+    }
+    return outer;
+}
+
+static inline void wadd(double* w, int n, int r, int c, double d) { w[r * n + c] += d; }
+
+/* calculate_pairwise_score (pairwise_scoring.rs:450-560) for one feature.
+ *  ds     [P][B] der sums (doc-ascending scatter, compute_der_sums :101-135)
+ *  st     [P][P][B][2] pair-weight statistics (smaller, greater_right; :163-196)
+ *  scores [B-1] */
+static void pairwise_scores(const double* ds, const double* st, int P, int B, double l2,
+                            double prior, double* scores) {
+    const int n = 2 * P;
+    double* w = (double*)calloc((size_t)n * n, sizeof(double));
+    double* der = (double*)calloc((size_t)n, sizeof(double));
+    double* a = (double*)malloc(sizeof(double) * (size_t)n);
+#define ST(x, y, b, c) st[((((size_t)(x) * P + (y)) * B + (b)) << 1) + (c)]
+    for (int leaf = 0; leaf < P; ++leaf) {
+        double t = 0.0;
+        for (int b = 0; b < B; ++b) t += ds[(size_t)leaf * B + b];
+        der[2 * leaf + 1] += t;
+    }
+    for (int y = 0; y < P; ++y)
+        for (int x = y + 1; x < P; ++x) {
+            double total = 0.0; /* buckets interleaved xy, yx (:480-490) */
+            for (int b = 0; b < B; ++b) { total += ST(x, y, b, 0); total += ST(y, x, b, 0); }
+            wadd(w, n, 2 * y + 1, 2 * x + 1, total);
+            wadd(w, n, 2 * x + 1, 2 * y + 1, total);
+            wadd(w, n, 2 * x + 1, 2 * x + 1, -total);
+            wadd(w, n, 2 * y + 1, 2 * y + 1, -total);
+        }
+    for (int s = 0; s + 1 < B; ++s) {
+        for (int y = 0; y < P; ++y) {
+            double dd = ds[(size_t)y * B + s];
+            der[2 * y] += dd;
+            der[2 * y + 1] += -dd;
+            double wd = ST(y, y, s, 0) - ST(y, y, s, 1);
+            wadd(w, n, 2 * y, 2 * y + 1, wd);
+            wadd(w, n, 2 * y + 1, 2 * y, wd);
+            wadd(w, n, 2 * y, 2 * y, -wd);
+            wadd(w, n, 2 * y + 1, 2 * y + 1, -wd);
+            for (int x = y + 1; x < P; ++x) {
+                double xs = ST(x, y, s, 0), xg = ST(x, y, s, 1);
+                double ys = ST(y, x, s, 0), yg = ST(y, x, s, 1);
+                double w00 = xg + yg, w01 = xs - xg, w10 = ys - yg, w11 = -(xs + ys);
+                wadd(w, n, 2 * x, 2 * y, w00);
+                wadd(w, n, 2 * y, 2 * x, w00);
+                wadd(w, n, 2 * x, 2 * y + 1, w01);
+                wadd(w, n, 2 * y + 1, 2 * x, w01);
+                wadd(w, n, 2 * x + 1, 2 * y, w10);
+                wadd(w, n, 2 * y, 2 * x + 1, w10);
+                wadd(w, n, 2 * x + 1, 2 * y + 1, w11);
+                wadd(w, n, 2 * y + 1, 2 * x + 1, w11);
+                wadd(w, n, 2 * y, 2 * y, -(w00 + w10));
+                wadd(w, n, 2 * x, 2 * x, -(w00 + w01));
+                wadd(w, n, 2 * x + 1, 2 * x + 1, -(w10 + w11));
+                wadd(w, n, 2 * y + 1, 2 * y + 1, -(w01 + w11));
+            }
+        }
+        pairwise_leaf_values(w, der, n, l2, prior, a);
+        scores[s] = pairwise_score_value(a, der, w, n);
+    }
+#undef ST
+    free(w); free(der); free(a);
+}
+
+/* Pairwise statistics of one feature at one level (compute_der_sums :101-135 and
+ * compute_pair_weight_statistics :163-196).  ds [P][B], st [P][P][B][2]. */
+static void pairwise_stats(const uint8_t* col, const uint32_t* leaf_of, const double* der,
+                           uint64_t n, const uint32_t* winner, const uint32_t* loser,
+                           const double* weight, uint64_t m, int P, int B, double* ds,
+                           double* st) {
+    memset(ds, 0, sizeof(double) * (size_t)P * B);
+    memset(st, 0, sizeof(double) * (size_t)P * P * B * 2);
+    for (uint64_t i = 0; i < n; ++i) ds[(size_t)leaf_of[i] * B + col[i]] += der[i];
+    for (uint64_t k = 0; k < m; ++k) {
+        uint32_t wi = winner[k], lo = loser[k];
+        if (wi == lo) continue;
+        double w = weight ? weight[k] : 1.0;
+        int wb = col[wi], lb = col[lo];
+        int wl = (int)leaf_of[wi], ll = (int)leaf_of[lo];
+        if (wb > lb) {
+            st[((((size_t)ll * P + wl) * B + lb) << 1) + 0] -= w;
+            st[((((size_t)ll * P + wl) * B + wb) << 1) + 1] -= w;
+        } else {
+            st[((((size_t)wl * P + ll) * B + wb) << 1) + 0] -= w;
+            st[((((size_t)wl * P + ll) * B + lb) << 1) + 1] -= w;
+        }
+    }
+}
+
+/* Pairwise scores of every border of one feature at one level (test entry). */
+void orc_pairwise_feature_scores(const uint8_t* col, const uint32_t* leaf_of, const double* der,
+                                 uint64_t n, const uint32_t* winner, const uint32_t* loser,
+                                 const double* weight, uint64_t m, int32_t P, int32_t B, double l2,
+                                 double prior, double* scores) {
+    double* ds = (double*)malloc(sizeof(double) * (size_t)P * B);
+    double* st = (double*)malloc(sizeof(double) * (size_t)P * P * B * 2);
+    pairwise_stats(col, leaf_of, der, n, winner, loser, weight, m, P, B, ds, st);
+    pairwise_scores(ds, st, P, B, l2, prior, scores);
+    free(ds);
+    free(st);
+}
+
+int orc_grow_tree_pairwise(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
+                           uint32_t F, const double* der, const uint32_t* winner,
+                           const uint32_t* loser, const double* weight, uint64_t m,
+                           int32_t depth, double l2, double prior, int32_t n_threads,
+                           int32_t* out_splits, double* out_scores, uint32_t* out_leaf_of) {
+    uint32_t* leaf_of = out_leaf_of;
+    memset(leaf_of, 0, sizeof(uint32_t) * n);
+    double** scores = (double**)calloc(F, sizeof(double*));
+#ifdef _OPENMP
+    int nt = n_threads > 0 ? n_threads : omp_get_max_threads();
+#endif
+    int rc = 0;
+    for (int level = 0; level < depth; ++level) {
+        const int P = 1 << level;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+#endif
+        for (int64_t fi = 0; fi < (int64_t)F; ++fi) {
+            uint32_t f = (uint32_t)fi;
+            free(scores[f]);
+            scores[f] = NULL;
+            if (n_borders[f] == 0) continue;
+            const int B = (int)n_borders[f] + 1;
+            double* ds = (double*)malloc(sizeof(double) * (size_t)P * B);
+            double* st = (double*)malloc(sizeof(double) * (size_t)P * P * B * 2);
+            pairwise_stats(bins_fm + (size_t)f * n, leaf_of, der, n, winner, loser, weight, m, P, B,
+                           ds, st);
+            scores[f] = (double*)malloc(sizeof(double) * (size_t)(B - 1));
+            pairwise_scores(ds, st, P, B, l2, prior, scores[f]);
+            free(ds);
+            free(st);
+        }
+        /* select_level_pairwise (tree.rs:3852-3900): feature asc, border asc, strict > */
+        int best_f = -1, best_b = -1;
+        double best = -INFINITY;
+        for (uint32_t f = 0; f < F; ++f)
+            for (uint32_t b = 0; b < n_borders[f]; ++b)
+                if (scores[f][b] > best) { best = scores[f][b]; best_f = (int)f; best_b = (int)b; }
+        if (best_f < 0) { rc = -1; break; }
+        out_splits[level * 2] = best_f;
+        out_splits[level * 2 + 1] = best_b;
+        if (out_scores) out_scores[level] = best;
+        const uint8_t* col = bins_fm + (size_t)best_f * n;
+        for (uint64_t o = 0; o < n; ++o)
+            if (col[o] > (uint32_t)best_b) leaf_of[o] += (uint32_t)P;
+    }
+    for (uint32_t f = 0; f < F; ++f) free(scores[f]);
+    free(scores);
+    return rc;
+}
+
+/* compute_pairwise_leaf_deltas (pairwise_leaves.rs:219-238): per-leaf weight sums from the
+ * pairs (compute_pairwise_weight_sums :47-88, same-leaf pairs skipped), per-leaf der sums
+ * (docs ascending), then the pairwise leaf solve. */
+void orc_pairwise_leaf_deltas(const uint32_t* leaf_of, uint64_t n, const double* der,
+                              const uint32_t* winner, const uint32_t* loser, const double* weight,
+                              uint64_t m, uint32_t n_leaves, double l2, double prior, double* out) {
+    double* w = (double*)calloc((size_t)n_leaves * n_leaves, sizeof(double));
+    double* ds = (double*)calloc(n_leaves, sizeof(double));
+    for (uint64_t k = 0; k < m; ++k) {
+        uint32_t wl = leaf_of[winner[k]], ll = leaf_of[loser[k]];
+        if (wl == ll) continue;
+        double x = weight ? weight[k] : 1.0;
+        w[(size_t)wl * n_leaves + ll] -= x;
+        w[(size_t)ll * n_leaves + wl] -= x;
+        w[(size_t)wl * n_leaves + wl] += x;
+        w[(size_t)ll * n_leaves + ll] += x;
+    }
+    for (uint64_t i = 0; i < n; ++i) ds[leaf_of[i]] += der[i];
+    pairwise_leaf_values(w, ds, (int)n_leaves, l2, prior, out);
+    free(w);
+    free(ds);
+}
+
+/* normalize_leaf_values for pairwise losses (boosting.rs:2844-2875): subtract the
+ * document-weighted mean leaf value; leaves with |weight| <= 1e-9 become 0. */
+static void pairwise_center(double* v, const double* leaf_w, uint32_t n_leaves) {
+    double total = 0.0;
+    for (uint32_t l = 0; l < n_leaves; ++l) total += leaf_w[l];
+    if (!(fabs(total) > 1e-9)) return;
+    double weighted = 0.0;
+    for (uint32_t l = 0; l < n_leaves; ++l) weighted += v[l] * leaf_w[l];
+    double avg = weighted / total;
+    for (uint32_t l = 0; l < n_leaves; ++l) {
+        if (fabs(leaf_w[l]) > 1e-9) v[l] -= avg;
+        else v[l] = 0.0;
+    }
+}
+
 /* ======================================================================
  * Boosting loop -- CPU branch of crates/cb-train/src/boosting.rs:7300-8900
  * (Plain boosting, SymmetricTree, random_strength 0, pointwise losses).
@@ -612,6 +918,32 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
     for (uint32_t f = 0; p->one_hot_flags && f < F; ++f) any_one_hot |= p->one_hot_flags[f] != 0;
     /* one-hot columns with active RNG draws are refused (boosting.rs:5744-5756) */
     if (any_one_hot && p->bootstrap_type != ORC_BOOT_NO) return -4;
+    /* ranking losses over explicit pairs (boosting.rs:1716-1783): PairLogit scores with the
+     * pointwise histogram over pairwise weights; PairLogitPairwise with the pairwise
+     * statistics (tree.rs:3930-3974) and solves its leaves by Cholesky (pairwise_leaves.rs) */
+    const int ranking = p->loss == ORC_LOSS_PAIRLOGIT || p->loss == ORC_LOSS_PAIRLOGIT_PAIRWISE;
+    const int pairwise_scoring = p->loss == ORC_LOSS_PAIRLOGIT_PAIRWISE;
+    if (ranking && (weight || any_one_hot)) return -4;
+    if (pairwise_scoring && p->bootstrap_type != ORC_BOOT_NO) return -4;
+    const double prior = p->pairwise_non_diag_reg;
+    uint32_t *pw_win = NULL, *pw_los = NULL;
+    double *pw_wt = NULL, *pw = NULL;
+    const uint64_t m = ranking ? p->n_pairs : 0;
+    if (ranking) {
+        uint64_t* perm = (uint64_t*)malloc(sizeof(uint64_t) * (m + 1));
+        orc_pairs_order(p->pair_winner, m, n, perm);
+        pw_win = (uint32_t*)malloc(sizeof(uint32_t) * (m + 1));
+        pw_los = (uint32_t*)malloc(sizeof(uint32_t) * (m + 1));
+        pw_wt = (double*)malloc(sizeof(double) * (m + 1));
+        for (uint64_t k = 0; k < m; ++k) {
+            pw_win[k] = p->pair_winner[perm[k]];
+            pw_los[k] = p->pair_loser[perm[k]];
+            pw_wt[k] = p->pair_weight ? p->pair_weight[perm[k]] : 1.0;
+        }
+        free(perm);
+        pw = (double*)malloc(sizeof(double) * n);
+        orc_pairwise_weights(n, pw_win, pw_los, pw_wt, m, pw);
+    }
     const int depth = p->depth;
     const uint32_t n_leaves = 1u << depth;
     const int pk = K * (K + 1) / 2;
@@ -656,6 +988,8 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
                 for (int d = 0; d < K; ++d) d1[(size_t)d * n + i] = dd1[d];
                 for (int j = 0; j < pk; ++j) d2[i * pk + j] = dd2[j];
             }
+        } else if (ranking) {
+            orc_pairlogit_ders(approx, n, pw_win, pw_los, pw_wt, m, d1, d2);
         } else {
             orc_ders(p->loss, approx, target, n, d1, d2);
         }
@@ -667,12 +1001,18 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
             uint64_t i = x % n;
             sder[x] = ctrl[i] ? wd[x] * samp[i] : 0.0;
         }
-        for (uint64_t i = 0; i < n; ++i) swt[i] = ctrl[i] ? w[i] * samp[i] : 0.0;
+        /* the histogram weight of a pairwise-weight loss is the pairwise weight
+         * (eff_weights, boosting.rs:7575-7579) */
+        for (uint64_t i = 0; i < n; ++i) swt[i] = ctrl[i] ? (ranking ? pw[i] : w[i]) * samp[i] : 0.0;
 
         int32_t* splits = out_splits + (size_t)it * depth * 2;
-        rc = orc_grow_tree(bins_fm, n_borders, n, F, sder, swt, K, depth, p->score_function,
-                           scaled_l2, draws_active ? &rng : NULL, p->n_threads, splits, NULL,
-                           leaf_of, NULL, p->one_hot_flags);
+        if (pairwise_scoring)
+            rc = orc_grow_tree_pairwise(bins_fm, n_borders, n, F, d1, pw_win, pw_los, pw_wt, m, depth,
+                                        p->l2_leaf_reg, prior, p->n_threads, splits, NULL, leaf_of);
+        else
+            rc = orc_grow_tree(bins_fm, n_borders, n, F, sder, swt, K, depth, p->score_function,
+                               scaled_l2, draws_active ? &rng : NULL, p->n_threads, splits, NULL,
+                               leaf_of, NULL, p->one_hot_flags);
         if (rc) break;
 
         /* leaf values on the UNSAMPLED derivatives (boosting.rs:2470-2560, :2634) */
@@ -691,6 +1031,9 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
             }
             free(sd);
             free(s2);
+        } else if (pairwise_scoring) {
+            orc_pairwise_leaf_deltas(leaf_of, n, d1, pw_win, pw_los, pw_wt, m, n_leaves,
+                                     p->l2_leaf_reg, prior, leaf_vals);
         } else {
             double sd[1 << 12], s2[1 << 12];
             for (uint32_t l = 0; l < n_leaves; ++l) { sd[l] = 0.0; s2[l] = 0.0; }
@@ -698,15 +1041,22 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
                 uint32_t l = leaf_of[i];
                 sd[l] += wd[i];
                 if (p->leaf_method == ORC_LEAF_NEWTON) s2[l] += d2[i] * w[i];
-                else s2[l] += w[i];
+                else s2[l] += ranking ? pw[i] : w[i]; /* Gradient sumWeight (boosting.rs:8352-8380) */
             }
             for (uint32_t l = 0; l < n_leaves; ++l)
                 leaf_vals[l] = p->leaf_method == ORC_LEAF_NEWTON
                                    ? newton_leaf_delta(sd[l], s2[l], scaled_l2)
                                    : calc_average(sd[l], s2[l], scaled_l2);
         }
-        /* NormalizeLeafValues: non-pairwise losses only scale by the learning rate
-         * (boosting.rs:2844-2882); then approx += leaf value (boosting.rs:8560-8572) */
+        /* NormalizeLeafValues (boosting.rs:2844-2882): pairwise-weight losses first subtract
+         * the document-weighted mean leaf value; every loss is then scaled by the learning
+         * rate; then approx += leaf value (boosting.rs:8560-8572) */
+        if (ranking) {
+            double lw[1 << 12];
+            for (uint32_t l = 0; l < n_leaves; ++l) lw[l] = 0.0;
+            for (uint64_t i = 0; i < n; ++i) lw[leaf_of[i]] += w[i];
+            pairwise_center(leaf_vals, lw, n_leaves);
+        }
         for (uint32_t x = 0; x < n_leaves * K; ++x) leaf_vals[x] *= lr;
         for (int d = 0; d < K; ++d)
             for (uint64_t i = 0; i < n; ++i)
@@ -721,5 +1071,6 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
     if (out_approx) memcpy(out_approx, approx, sizeof(double) * n * K);
     free(w); free(approx); free(d1); free(d2); free(wd); free(sder); free(swt); free(samp);
     free(ctrl); free(leaf_of); free(leaf_vals);
+    free(pw_win); free(pw_los); free(pw_wt); free(pw);
     return rc;
 }

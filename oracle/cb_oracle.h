@@ -34,7 +34,8 @@ typedef struct {
     uint64_t calls;
 } orc_rng;
 
-enum { ORC_LOSS_RMSE = 0, ORC_LOSS_LOGLOSS = 1, ORC_LOSS_MULTICLASS = 2 };
+enum { ORC_LOSS_RMSE = 0, ORC_LOSS_LOGLOSS = 1, ORC_LOSS_MULTICLASS = 2, ORC_LOSS_PAIRLOGIT = 3,
+       ORC_LOSS_PAIRLOGIT_PAIRWISE = 4 };
 enum { ORC_SCORE_COSINE = 0, ORC_SCORE_L2 = 1 };
 enum { ORC_BOOT_NO = 0, ORC_BOOT_BAYESIAN = 1, ORC_BOOT_BERNOULLI = 2 };
 enum { ORC_LEAF_GRADIENT = 0, ORC_LEAF_NEWTON = 1 };
@@ -57,6 +58,12 @@ typedef struct {
     float pad2_;
     uint64_t random_seed;
     const uint8_t* one_hot_flags; /* nullable [F]: one-hot categorical columns */
+    /* PairLogit / PairLogitPairwise: explicit pairs (any order; pairs never cross groups) */
+    const uint32_t* pair_winner;
+    const uint32_t* pair_loser;
+    const double* pair_weight;    /* nullable: weight 1 (query_info.rs:236-239) */
+    uint64_t n_pairs;
+    double pairwise_non_diag_reg; /* bayesian_matrix_reg, 0.1 by default (boosting.rs:1790) */
 } orc_params;
 
 /* out_splits feature entries of one-hot (equality) splits carry this flag bit */
@@ -104,6 +111,28 @@ int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
                   int32_t score_function, double scaled_l2, orc_rng* perturb_rng, int32_t n_threads,
                   int32_t* out_splits, double* out_scores, uint32_t* out_leaf_of,
                   double* out_hists, const uint8_t* one_hot);
+
+/* ---- pairwise ranking (cb-compute/src/ranking_der.rs, pairwise_scoring.rs;
+ *      cb-train/src/pairwise_leaves.rs, tree.rs:3790-3974) ----
+ * Pair arrays are in the reference's competitor order (stable by winner). */
+void orc_pairs_order(const uint32_t* winner, uint64_t m, uint64_t n, uint64_t* out_perm);
+void orc_pairlogit_ders(const double* approx, uint64_t n, const uint32_t* winner,
+                        const uint32_t* loser, const double* weight, uint64_t m, double* der1,
+                        double* der2);
+void orc_pairwise_weights(uint64_t n, const uint32_t* winner, const uint32_t* loser,
+                          const double* weight, uint64_t m, double* pw);
+int orc_grow_tree_pairwise(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
+                           uint32_t F, const double* der, const uint32_t* winner,
+                           const uint32_t* loser, const double* weight, uint64_t m,
+                           int32_t depth, double l2, double prior, int32_t n_threads,
+                           int32_t* out_splits, double* out_scores, uint32_t* out_leaf_of);
+void orc_pairwise_feature_scores(const uint8_t* col, const uint32_t* leaf_of, const double* der,
+                                 uint64_t n, const uint32_t* winner, const uint32_t* loser,
+                                 const double* weight, uint64_t m, int32_t P, int32_t B, double l2,
+                                 double prior, double* scores);
+void orc_pairwise_leaf_deltas(const uint32_t* leaf_of, uint64_t n, const double* der,
+                              const uint32_t* winner, const uint32_t* loser, const double* weight,
+                              uint64_t m, uint32_t n_leaves, double l2, double prior, double* out);
 
 /* Per-leaf ordered sums (cb-compute/src/histogram.rs:49 reduce_leaf_stats, :97 reduce_leaf_der2). */
 void orc_leaf_sums(const uint32_t* leaf_of, uint64_t n, uint32_t n_leaves, const double* der,

@@ -16,7 +16,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libcb_oracle.so")
 _lib = None
 
-LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2}
+LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2, "PairLogit": 3, "PairLogitPairwise": 4}
 SCORE = {"Cosine": 0, "L2": 1}
 BOOT = {"No": 0, "Bayesian": 1, "Bernoulli": 2}
 LEAF = {"Gradient": 0, "Newton": 1}
@@ -36,7 +36,9 @@ class Params(C.Structure):
                 ("learning_rate", C.c_double), ("l2_leaf_reg", C.c_double),
                 ("subsample", C.c_double), ("bagging_temperature", C.c_float),
                 ("pad2_", C.c_float), ("random_seed", C.c_uint64),
-                ("one_hot_flags", C.c_void_p)]
+                ("one_hot_flags", C.c_void_p),
+                ("pair_winner", C.c_void_p), ("pair_loser", C.c_void_p), ("pair_weight", C.c_void_p),
+                ("n_pairs", C.c_uint64), ("pairwise_non_diag_reg", C.c_double)]
 
 
 ONE_HOT_SPLIT = 0x40000000  # flag bit on the feature entry of an equality split
@@ -79,6 +81,16 @@ def lib():
         L.orc_leaf_sums.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P]
         L.orc_train.argtypes = [C.POINTER(Params), P, P, C.c_uint64, C.c_uint32, P, P, P, P, P, P, P]
         L.orc_train.restype = C.c_int
+        L.orc_pairs_order.argtypes = [P, C.c_uint64, C.c_uint64, P]
+        L.orc_pairlogit_ders.argtypes = [P, C.c_uint64, P, P, P, C.c_uint64, P, P]
+        L.orc_pairwise_weights.argtypes = [C.c_uint64, P, P, P, C.c_uint64, P]
+        L.orc_grow_tree_pairwise.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, P, P, C.c_uint64,
+                                             C.c_int32, C.c_double, C.c_double, C.c_int32, P, P, P]
+        L.orc_grow_tree_pairwise.restype = C.c_int
+        L.orc_pairwise_feature_scores.argtypes = [P, P, P, C.c_uint64, P, P, P, C.c_uint64, C.c_int32,
+                                                  C.c_int32, C.c_double, C.c_double, P]
+        L.orc_pairwise_leaf_deltas.argtypes = [P, C.c_uint64, P, P, P, P, C.c_uint64, C.c_uint32,
+                                               C.c_double, C.c_double, P]
         _lib = L
     return _lib
 
@@ -174,6 +186,77 @@ def grow_tree(bins_fm, n_borders, score_der, score_w, depth, score="Cosine", sca
     return out
 
 
+def pairs_in_competitor_order(winner, loser, weight=None, n=None):
+    """Pairs stably ordered by winner: the reference's competitor order (group ascending,
+    winner ascending, input order per winner)."""
+    w = np.ascontiguousarray(winner, np.uint32)
+    l = np.ascontiguousarray(loser, np.uint32)
+    n = int(max(w.max(), l.max()) + 1) if n is None else n
+    perm = np.empty(w.shape[0], np.uint64)
+    lib().orc_pairs_order(_p(w), w.shape[0], n, _p(perm))
+    perm = perm.astype(np.int64)
+    wt = np.ones(w.shape[0]) if weight is None else np.asarray(weight, np.float64)
+    return w[perm].copy(), l[perm].copy(), np.ascontiguousarray(wt[perm])
+
+
+def pairlogit_ders(approx, winner, loser, weight):
+    """PairLogit der1/der2 (pairs in competitor order)."""
+    a = np.ascontiguousarray(approx, np.float64)
+    w, l, wt = (np.ascontiguousarray(x) for x in (winner, loser, weight))
+    d1 = np.empty_like(a)
+    d2 = np.empty_like(a)
+    lib().orc_pairlogit_ders(_p(a), a.shape[0], _p(w), _p(l), _p(wt), w.shape[0], _p(d1), _p(d2))
+    return d1, d2
+
+
+def pairwise_weights(n, winner, loser, weight):
+    w, l, wt = (np.ascontiguousarray(x) for x in (winner, loser, weight))
+    pw = np.empty(n)
+    lib().orc_pairwise_weights(n, _p(w), _p(l), _p(wt), w.shape[0], _p(pw))
+    return pw
+
+
+def grow_tree_pairwise(bins_fm, n_borders, der, winner, loser, weight, depth, l2, prior=0.1,
+                       n_threads=0):
+    """One PairLogitPairwise tree (pairs in competitor order)."""
+    bins_fm = np.ascontiguousarray(bins_fm, np.uint8)
+    F, n = bins_fm.shape
+    nb = np.ascontiguousarray(n_borders, np.uint32)
+    d = np.ascontiguousarray(der, np.float64)
+    w, l, wt = (np.ascontiguousarray(x) for x in (winner, loser, weight))
+    splits = np.zeros((depth, 2), np.int32)
+    scores = np.zeros(depth)
+    leaf_of = np.zeros(n, np.uint32)
+    rc = lib().orc_grow_tree_pairwise(_p(bins_fm), _p(nb), n, F, _p(d), _p(w), _p(l), _p(wt),
+                                      w.shape[0], depth, l2, prior, n_threads, _p(splits),
+                                      _p(scores), _p(leaf_of))
+    if rc != 0:
+        raise RuntimeError(f"orc_grow_tree_pairwise failed rc={rc}")
+    return {"splits": splits, "scores": scores, "leaf_of": leaf_of}
+
+
+def pairwise_feature_scores(col, leaf_of, der, winner, loser, weight, P, B, l2, prior=0.1):
+    """Pairwise score of every border (B-1 values) of one feature with P parent leaves."""
+    c = np.ascontiguousarray(col, np.uint8)
+    lo = np.ascontiguousarray(leaf_of, np.uint32)
+    d = np.ascontiguousarray(der, np.float64)
+    w, l, wt = (np.ascontiguousarray(x) for x in (winner, loser, weight))
+    out = np.zeros(B - 1)
+    lib().orc_pairwise_feature_scores(_p(c), _p(lo), _p(d), c.shape[0], _p(w), _p(l), _p(wt),
+                                      w.shape[0], P, B, l2, prior, _p(out))
+    return out
+
+
+def pairwise_leaf_deltas(leaf_of, der, winner, loser, weight, n_leaves, l2, prior=0.1):
+    lo = np.ascontiguousarray(leaf_of, np.uint32)
+    d = np.ascontiguousarray(der, np.float64)
+    w, l, wt = (np.ascontiguousarray(x) for x in (winner, loser, weight))
+    out = np.zeros(n_leaves)
+    lib().orc_pairwise_leaf_deltas(_p(lo), lo.shape[0], _p(d), _p(w), _p(l), _p(wt), w.shape[0],
+                                   n_leaves, l2, prior, _p(out))
+    return out
+
+
 def leaf_sums(leaf_of, n_leaves, der, weight=None):
     lo = np.ascontiguousarray(leaf_of, np.uint32)
     d = np.ascontiguousarray(der, np.float64)
@@ -187,10 +270,12 @@ def leaf_sums(leaf_of, n_leaves, der, weight=None):
 def train(bins_fm, n_borders, target, *, loss="RMSE", depth=6, iterations=10, learning_rate=0.1,
           l2_leaf_reg=3.0, score="Cosine", bootstrap_type="No", subsample=0.66,
           bagging_temperature=1.0, leaf_method="Gradient", boost_from_average=False,
-          random_seed=0, weight=None, approx_dim=1, n_threads=0, staged=False, one_hot=None):
+          random_seed=0, weight=None, approx_dim=1, n_threads=0, staged=False, one_hot=None,
+          pairs=None, pairwise_non_diag_reg=0.1):
     """CPU boosting loop.  ``one_hot`` (optional, [F]) flags one-hot columns (for them
     ``n_borders[f] + 1`` is the cardinality); one-hot with bootstrap raises (-4), as the
-    reference refuses it."""
+    reference refuses it.  ``pairs`` = (winner, loser[, weight]) for PairLogit /
+    PairLogitPairwise, in any order."""
     bins_fm = np.ascontiguousarray(bins_fm, np.uint8)
     F, n = bins_fm.shape
     nb = np.ascontiguousarray(n_borders, np.uint32)
@@ -204,6 +289,16 @@ def train(bins_fm, n_borders, target, *, loss="RMSE", depth=6, iterations=10, le
                bagging_temperature=bagging_temperature, random_seed=random_seed)
     oh = None if one_hot is None else np.ascontiguousarray(one_hot, np.uint8)
     p.one_hot_flags = None if oh is None else oh.ctypes.data
+    keep = []
+    if pairs is not None:
+        pw_ = np.ascontiguousarray(pairs[0], np.uint32)
+        pl_ = np.ascontiguousarray(pairs[1], np.uint32)
+        pwt = None if len(pairs) < 3 or pairs[2] is None else np.ascontiguousarray(pairs[2], np.float64)
+        keep += [pw_, pl_, pwt]
+        p.pair_winner, p.pair_loser = pw_.ctypes.data, pl_.ctypes.data
+        p.pair_weight = None if pwt is None else pwt.ctypes.data
+        p.n_pairs = pw_.shape[0]
+    p.pairwise_non_diag_reg = pairwise_non_diag_reg
     splits = np.zeros((iterations, depth, 2), np.int32)
     leaves = np.zeros((iterations, K, 1 << depth), np.float64)
     approx = np.zeros((K, n), np.float64)

@@ -16,6 +16,9 @@ expected outputs); no reference source is copied.  Sources:
 * ``upstream_*.npz``      -- catboost 1.2.10 fits under crates/cb-oracle/fixtures/
                              (inputs, used borders, per-tree splits and leaf values, staged
                              approx, predictions).
+* ``upstream_ranking.npz`` -- catboost 1.2.10 PairLogit / PairLogitPairwise fits over the
+                             12-document ranking corpus (inputs, pairs, used borders, splits,
+                             leaf values, staged approx, predictions).
 * ``upstream_one_hot_*``  -- catboost 1.2.10 one-hot fits (one_hot_train/*): float inputs,
                              categorical columns as first-seen bins, used borders, splits
                              (one-hot values as bins), leaf values, predictions.
@@ -166,6 +169,30 @@ def one_hot_train(ref, scen):
     json.dump(meta, open(os.path.join(HERE, name + ".json"), "w"), indent=1)
 
 
+def ranking(ref):
+    """catboost 1.2.10 PairLogit / PairLogitPairwise fits over the 12-document ranking
+    corpus (ranking_corpus/inputs + per-loss model.json, staged.npy, predictions.npy)."""
+    fx = os.path.join(ref, "crates/cb-oracle/fixtures/ranking_corpus")
+    arrays = {k: np.load(os.path.join(fx, "inputs", k + ".npy"))
+              for k in ("X", "y", "group_id", "pairs")}
+    for loss in ("PairLogit", "PairLogitPairwise"):
+        model = json.load(open(os.path.join(fx, loss, "model.json")))
+        cfg = json.load(open(os.path.join(fx, loss, "config.json")))
+        feats = model["features_info"]["float_features"]
+        borders = [np.asarray(f["borders"], np.float64) for f in feats]
+        trees = model["oblivious_trees"]
+        arrays[loss + "_borders"] = np.concatenate(borders)
+        arrays[loss + "_n_borders"] = np.array([len(b) for b in borders], np.int64)
+        arrays[loss + "_split_feature"] = np.array(
+            [[sp["float_feature_index"] for sp in t["splits"]] for t in trees], np.int64)
+        arrays[loss + "_split_border"] = np.array([[sp["border"] for sp in t["splits"]] for t in trees])
+        arrays[loss + "_leaf_values"] = np.array([t["leaf_values"] for t in trees])
+        arrays[loss + "_staged"] = np.load(os.path.join(fx, loss, "staged.npy"))
+        arrays[loss + "_predictions"] = np.load(os.path.join(fx, loss, "predictions.npy"))
+        arrays[loss + "_config"] = np.frombuffer(json.dumps(cfg).encode(), np.uint8)
+    np.savez_compressed(os.path.join(HERE, "upstream_ranking.npz"), **arrays)
+
+
 def main():
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     rng_kat(ref)
@@ -175,6 +202,7 @@ def main():
         upstream(ref, s)
     for s in ("default_binary", "multi"):
         one_hot_train(ref, s)
+    ranking(ref)
 
 
 if __name__ == "__main__":

@@ -69,3 +69,17 @@ def upstream_one_hot(name: str):
                 split_border=z["split_border"], split_value_bin=z["split_value_bin"],
                 leaf_values=z["leaf_values"], predictions=z["predictions"], meta=meta,
                 params=meta["params"])
+
+
+def ranking(loss: str):
+    """catboost 1.2.10 fit of ``loss`` (PairLogit / PairLogitPairwise) over the ranking corpus."""
+    z = np.load(os.path.join(GOLDEN, "upstream_ranking.npz"))
+    nb = z[loss + "_n_borders"]
+    offs = np.concatenate([[0], np.cumsum(nb)])
+    borders = [z[loss + "_borders"][offs[i]:offs[i + 1]] for i in range(len(nb))]
+    cfg = json.loads(bytes(z[loss + "_config"]).decode())
+    return dict(X=z["X"], y=z["y"].astype(np.float64), pairs=z["pairs"].astype(np.uint32),
+                group_id=z["group_id"], borders=borders, n_borders=nb.astype(np.uint32),
+                split_feature=z[loss + "_split_feature"], split_border=z[loss + "_split_border"],
+                leaf_values=z[loss + "_leaf_values"], staged=z[loss + "_staged"],
+                predictions=z[loss + "_predictions"], config=cfg)

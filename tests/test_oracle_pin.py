@@ -252,3 +252,119 @@ def test_one_hot_tree_matches_bruteforce(seed):
         passed = (bins[f] == b) if key[0] else (bins[f] > b)
         leaf_of = leaf_of + passed * (1 << level)
     assert np.array_equal(out["leaf_of"], leaf_of)
+
+
+# ------------------------------------------------------------------------------ pairwise ranking
+# l2 of the reference's own oracle tests for these fixtures: PairLogit 3 (Newton leaves,
+# crates/cb-train/tests/pairlogit_oracle_test.rs:84-89), PairLogitPairwise 5
+# (pairlogit_pairwise_oracle_test.rs base_params).
+RANKING = {"PairLogit": (3.0, "Newton"), "PairLogitPairwise": (5.0, "Gradient")}
+
+
+def ranking_bins(u):
+    return np.stack([O.quantize(u["X"][:, j].astype(np.float32), u["borders"][j])
+                     for j in range(u["X"].shape[1])])
+
+
+@pytest.mark.parametrize("loss", sorted(RANKING))
+def test_ranking_upstream_fit(loss):
+    """PairLogit ders (ranking_der.rs:408-445), pairwise histogram weights, doc-weighted leaf
+    centering (boosting.rs:2844-2882), and for PairLogitPairwise the pairwise split scoring
+    (pairwise_scoring.rs) + Cholesky leaves (pairwise_leaves.rs), against catboost 1.2.10."""
+    u = G.ranking(loss)
+    l2, leaf = RANKING[loss]
+    cfg = u["config"]
+    bins = ranking_bins(u)
+    out = O.train(bins, u["n_borders"], u["y"], loss=loss, depth=cfg["depth"],
+                  iterations=cfg["iterations"], learning_rate=cfg["learning_rate"], l2_leaf_reg=l2,
+                  score="Cosine", leaf_method=leaf, bootstrap_type="No",
+                  pairs=(u["pairs"][:, 0], u["pairs"][:, 1]), staged=True)
+    T, n = cfg["iterations"], u["X"].shape[0]
+    for t in range(T):
+        got = [(int(f), u["borders"][f][b]) for f, b in out["splits"][t]]
+        exp = list(zip(u["split_feature"][t].tolist(), u["split_border"][t].tolist()))
+        assert got == exp, f"tree {t}"
+        np.testing.assert_allclose(out["leaf_values"][t, 0], u["leaf_values"][t], rtol=0, atol=1e-10)
+    np.testing.assert_allclose(out["staged"][:, 0, :], u["staged"].reshape(T, n), rtol=0, atol=1e-10)
+    np.testing.assert_allclose(out["approx"][0], u["predictions"], rtol=0, atol=1e-10)
+
+
+def _ranking_case(seed, n_groups=12, gsize=6, pairs_per_group=5, F=3, max_b=6):
+    g = np.random.default_rng(seed)
+    n = n_groups * gsize
+    win, los = [], []
+    for q in range(n_groups):
+        for _ in range(pairs_per_group):
+            a, b = g.choice(gsize, 2, replace=False)
+            win.append(q * gsize + a)
+            los.append(q * gsize + b)
+    win, los = np.array(win, np.uint32), np.array(los, np.uint32)
+    wt = g.uniform(0.5, 2.0, size=win.shape[0])
+    nb = g.integers(1, max_b, size=F).astype(np.uint32)
+    bins = np.stack([g.integers(0, nb[f] + 1, size=n) for f in range(F)]).astype(np.uint8)
+    return g, n, bins, nb, win, los, wt
+
+
+def test_pairlogit_ders_closed_form():
+    """der1[i] = sum_{i wins} w p - sum_{i loses} w p, p = e^{a_l} / (e^{a_l} + e^{a_w});
+    der2 likewise with w p (p - 1), vectorized (no scatter order)."""
+    g, n, _, _, win, los, wt = _ranking_case(3)
+    a = g.normal(size=n)
+    w, l, x = O.pairs_in_competitor_order(win, los, wt, n)
+    d1, d2 = O.pairlogit_ders(a, w, l, x)
+    p = np.exp(a[l]) / (np.exp(a[l]) + np.exp(a[w]))
+    e1 = np.bincount(w, x * p, n) - np.bincount(l, x * p, n)
+    e2 = np.bincount(w, x * p * (p - 1), n) + np.bincount(l, x * p * (p - 1), n)
+    np.testing.assert_allclose(d1, e1, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(d2, e2, rtol=1e-12, atol=1e-14)
+    pw = O.pairwise_weights(n, w, l, x)
+    np.testing.assert_allclose(pw, np.bincount(w, x, n) + np.bincount(l, x, n), rtol=1e-14)
+
+
+def _direct_pairwise(child, der, win, los, wt, n_children, l2, prior):
+    """The leaf system of a partition built from scratch: W from the pairs incident on two
+    different children, der per child, (n-1)x(n-1) solve with the priors, zero-averaged;
+    score = a.der - 0.5 a.W.a."""
+    W = np.zeros((n_children, n_children))
+    for a_, b_, x in zip(child[win], child[los], wt):
+        if a_ == b_:
+            continue
+        W[a_, b_] -= x
+        W[b_, a_] -= x
+        W[a_, a_] += x
+        W[b_, b_] += x
+    d = np.bincount(child, der, n_children)
+    m = n_children - 1
+    reg = (np.full((m, m), -prior / n_children) + np.eye(m) * (prior + l2))
+    res = np.append(np.linalg.solve(W[:m, :m] + reg, d[:m]), 0.0)
+    res -= res.mean()
+    return res, float(res @ d - 0.5 * res @ W @ res)
+
+
+@pytest.mark.parametrize("seed,level", [(0, 0), (1, 1), (2, 2), (3, 3)])
+def test_pairwise_scores_match_direct_partition(seed, level):
+    """The incremental per-border weight matrix of calculate_pairwise_score
+    (UpdateWeightSumFromTotal / FromNonDiagStats) equals the pairwise weight matrix of the
+    2P-child partition built directly (child 2y = bucket <= s, 2y+1 = bucket > s)."""
+    g, n, bins, nb, win, los, wt = _ranking_case(10 + seed, n_groups=20)
+    P = 1 << level
+    leaf_of = g.integers(0, P, size=n).astype(np.uint32)
+    der = g.normal(size=n)
+    w, l, x = O.pairs_in_competitor_order(win, los, wt, n)
+    for f in range(bins.shape[0]):
+        B = int(nb[f]) + 1
+        got = O.pairwise_feature_scores(bins[f], leaf_of, der, w, l, x, P, B, 5.0, 0.1)
+        for s in range(B - 1):
+            child = (2 * leaf_of + (bins[f] > s)).astype(np.int64)
+            _, exp = _direct_pairwise(child, der, w.astype(np.int64), l.astype(np.int64), x, 2 * P, 5.0, 0.1)
+            assert abs(got[s] - exp) <= 1e-9 * max(1.0, abs(exp)), (f, s, got[s], exp)
+
+
+def test_pairwise_leaf_deltas_match_direct_solve():
+    g, n, _, _, win, los, wt = _ranking_case(21, n_groups=30)
+    leaf_of = g.integers(0, 8, size=n).astype(np.uint32)
+    der = g.normal(size=n)
+    w, l, x = O.pairs_in_competitor_order(win, los, wt, n)
+    got = O.pairwise_leaf_deltas(leaf_of, der, w, l, x, 8, 3.0, 0.1)
+    exp, _ = _direct_pairwise(leaf_of.astype(np.int64), der, w.astype(np.int64), l.astype(np.int64), x, 8, 3.0, 0.1)
+    np.testing.assert_allclose(got, exp, rtol=1e-9, atol=1e-12)
