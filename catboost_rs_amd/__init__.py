@@ -22,7 +22,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcbhip.so")
 
-LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2, "CrossEntropy": 3}
+LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2, "CrossEntropy": 3, "PairLogit": 4,
+        "PairLogitPairwise": 5}
 SCORE = {"Cosine": 0, "L2": 1}
 LEAF = {"Gradient": 0, "Newton": 1, "Simple": 2}
 BOOT = {"No": 0, "Bayesian": 1, "Bernoulli": 2}
@@ -45,7 +46,15 @@ class Config(C.Structure):
                 ("bootstrap_type", C.c_int32), ("sample_from_host", C.c_int32),
                 ("sample_rate", C.c_float), ("bagging_temperature", C.c_float),
                 ("profile", C.c_int32), ("bias", C.c_double), ("rng_seed", C.c_uint64),
-                ("one_hot_flags", C.c_void_p), ("real_folds", C.c_void_p)]
+                ("one_hot_flags", C.c_void_p), ("real_folds", C.c_void_p),
+                ("pairwise_non_diag_reg", C.c_double)]
+
+
+class Family(C.Structure):
+    """FamilyTreeArgs::Pairwise (runtime.rs:925-934)."""
+    _fields_ = [("kind", C.c_int32), ("n_groups", C.c_uint32), ("group_offsets", C.c_void_p),
+                ("pair_winner", C.c_void_p), ("pair_loser", C.c_void_p), ("pair_weight", C.c_void_p),
+                ("n_pairs", C.c_uint64)]
 
 
 class TreeSampling(C.Structure):
@@ -74,15 +83,16 @@ class TrainParams(C.Structure):
                 ("depth", C.c_int32), ("bootstrap_type", C.c_int32),
                 ("boost_from_average", C.c_int32), ("approx_dim", C.c_int32), ("profile", C.c_int32),
                 ("learning_rate", C.c_double), ("l2_leaf_reg", C.c_double), ("subsample", C.c_double),
-                ("bagging_temperature", C.c_float), ("pad_", C.c_float), ("random_seed", C.c_uint64)]
+                ("bagging_temperature", C.c_float), ("pad_", C.c_float), ("random_seed", C.c_uint64),
+                ("pairwise_non_diag_reg", C.c_double)]
 
 
 # Every symbol include/cbhip.h and include/cbtrain.h declare (the ABI test checks them).
 EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_session_read_approx", "cbh_session_stats", "cbh_session_reset_stats",
            "cbh_session_end", "cbh_compute_gradients", "cbh_hist_build", "cbh_bootstrap",
-           "cbh_version", "cbh_last_error", "cbt_open", "cbt_step", "cbt_read_approx", "cbt_stats",
-           "cbt_reset_stats", "cbt_bias", "cbt_close"]
+           "cbh_version", "cbh_last_error", "cbt_open", "cbt_set_pairs", "cbt_step", "cbt_read_approx",
+           "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close"]
 
 _lib = None
 
@@ -102,7 +112,7 @@ def load(path: str = LIB_PATH):
                                     C.c_double, C.c_double, C.POINTER(P)]
     L.cbh_session_begin_u8.argtypes = L.cbh_session_begin.argtypes
     L.cbh_session_grow.argtypes = [P, P, P, C.c_uint64, P, C.c_uint64, C.POINTER(TreeSampling),
-                                   C.POINTER(TreeOut)]
+                                   C.POINTER(Family), C.POINTER(TreeOut)]
     L.cbh_session_read_approx.argtypes = [P, P, C.c_uint64]
     L.cbh_session_stats.argtypes = [P, C.POINTER(Stats)]
     L.cbh_session_reset_stats.argtypes = [P]
@@ -114,6 +124,7 @@ def load(path: str = LIB_PATH):
     L.cbh_bootstrap.argtypes = [C.POINTER(TreeSampling), C.c_uint64, P, P]
     L.cbt_open.argtypes = [C.POINTER(TrainParams), P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, P,
                            P, C.POINTER(P)]
+    L.cbt_set_pairs.argtypes = [P, P, C.c_uint32, P, P, P, C.c_uint64]
     L.cbt_step.argtypes = [P, P, P, P, P]
     L.cbt_read_approx.argtypes = [P, P]
     L.cbt_stats.argtypes = [P, C.POINTER(Stats)]
@@ -180,6 +191,19 @@ def bootstrap(kind: str, n: int, *, bayesian_seed=0, bernoulli_state=(0, 1, 0, 1
 # ---------------------------------------------------------------------------------------
 # The Runtime seam (begin / grow / end)
 # ---------------------------------------------------------------------------------------
+def _family_arrays(group_offsets, winner, loser, weight=None):
+    go = np.ascontiguousarray(group_offsets, np.uint32)
+    w = np.ascontiguousarray(winner, np.uint32)
+    l = np.ascontiguousarray(loser, np.uint32)
+    wt = None if weight is None else np.ascontiguousarray(weight, np.float64)
+    return go, w, l, wt
+
+
+def _family(go, w, l, wt):
+    return Family(kind=1, n_groups=go.shape[0] - 1, group_offsets=_ptr(go), pair_winner=_ptr(w),
+                  pair_loser=_ptr(l), pair_weight=_ptr(wt), n_pairs=w.shape[0])
+
+
 class HipBackend:
     """Mirror of ``GpuBackend: Runtime`` (crates/cb-backend/src/gpu_backend.rs:196-425)."""
 
@@ -196,7 +220,7 @@ class HipBackend:
                               bins_feature_major, weight, n, n_features, n_bins, learning_rate,
                               scaled_l2, *, approx_dim=1, bias=0.0, leaf_method="Gradient",
                               bootstrap_type="No", sample_from_host=False, profile=False,
-                              one_hot_flags=None, real_folds=None) -> bool:
+                              one_hot_flags=None, real_folds=None, pairwise_non_diag_reg=0.1) -> bool:
         """Returns True when the session opened, False when the config is declined."""
         self._keep = []
         oh = None if one_hot_flags is None else np.ascontiguousarray(one_hot_flags, np.uint8)
@@ -206,7 +230,8 @@ class HipBackend:
                      depth=depth, boosting_type_is_plain=int(boosting_type_is_plain),
                      fold_count=fold_count, approx_dim=approx_dim, bootstrap_type=BOOT[bootstrap_type],
                      sample_from_host=int(sample_from_host), profile=int(profile), bias=bias,
-                     one_hot_flags=_ptr(oh), real_folds=_ptr(rf))
+                     one_hot_flags=_ptr(oh), real_folds=_ptr(rf),
+                     pairwise_non_diag_reg=pairwise_non_diag_reg)
         bins = np.ascontiguousarray(bins_feature_major)
         w = None if weight is None else np.ascontiguousarray(weight, np.float64)
         fn = load().cbh_session_begin_u8 if bins.dtype == np.uint8 else load().cbh_session_begin
@@ -221,7 +246,8 @@ class HipBackend:
         return True
 
     def grow_tree_on_device(self, approx=None, target=None, sample=None, sampling=None,
-                            want_leaf_of=False):
+                            want_leaf_of=False, family=None):
+        """``family`` = (group_offsets, winner, loser[, weight]) for a pair loss (first tree)."""
         d = self.depth
         sf = np.zeros(d, np.uint32)
         sb = np.zeros(d, np.uint32)
@@ -233,9 +259,15 @@ class HipBackend:
         a = None if approx is None else np.ascontiguousarray(approx, np.float64)
         t = None if target is None else np.ascontiguousarray(target, np.float64)
         s = None if sample is None else np.ascontiguousarray(sample, np.float64)
+        fam = None
+        if family is not None:
+            arrs = _family_arrays(*family)
+            self._fam_keep = arrs
+            fam = _family(*arrs)
         _check(load().cbh_session_grow(self._s, _ptr(a), _ptr(t), self.n, _ptr(s),
                                        0 if s is None else s.shape[0],
-                                       None if sampling is None else C.byref(sampling), C.byref(out)))
+                                       None if sampling is None else C.byref(sampling),
+                                       None if fam is None else C.byref(fam), C.byref(out)))
         return {"splits": [(int(f), int(b), bool(o)) for f, b, o in zip(sf, sb, so)],
                 "leaf_values": lv.reshape(1 << d, self.K), "leaf_of": lo, "scores": sc}
 
@@ -261,7 +293,10 @@ class Trainer:
     def __init__(self, bins_fm, n_bins, target, *, loss="RMSE", depth=6, learning_rate=0.1,
                  l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient", bootstrap_type="No",
                  subsample=0.66, bagging_temperature=1.0, boost_from_average=False, random_seed=0,
-                 weight=None, approx_dim=1, profile=False, real_folds=None, one_hot_flags=None):
+                 weight=None, approx_dim=1, profile=False, real_folds=None, one_hot_flags=None,
+                 pairs=None, group_offsets=None, pairwise_non_diag_reg=0.1):
+        """``pairs`` = (winner, loser[, weight]) and ``group_offsets`` (CSR over row order) for
+        PairLogit / PairLogitPairwise."""
         self.bins = np.ascontiguousarray(bins_fm, np.uint8)
         F, n = self.bins.shape
         self.n, self.F, self.depth = n, F, depth
@@ -271,7 +306,7 @@ class Trainer:
                         boost_from_average=int(boost_from_average), approx_dim=self.K,
                         profile=int(profile), learning_rate=learning_rate, l2_leaf_reg=l2_leaf_reg,
                         subsample=subsample, bagging_temperature=bagging_temperature,
-                        random_seed=random_seed)
+                        random_seed=random_seed, pairwise_non_diag_reg=pairwise_non_diag_reg)
         t = np.ascontiguousarray(target, np.float64)
         w = None if weight is None else np.ascontiguousarray(weight, np.float64)
         rf = None if real_folds is None else np.ascontiguousarray(real_folds, np.uint32)
@@ -280,6 +315,10 @@ class Trainer:
         self._h = C.c_void_p()
         _check(load().cbt_open(C.byref(p), _ptr(self.bins), n, F, n_bins, _ptr(rf), _ptr(oh), _ptr(t),
                                _ptr(w), C.byref(self._h)))
+        if pairs is not None:
+            go, pw_, pl_, pwt = _family_arrays(group_offsets, *pairs)
+            _check(load().cbt_set_pairs(self._h, _ptr(go), go.shape[0] - 1, _ptr(pw_), _ptr(pl_),
+                                        _ptr(pwt), pw_.shape[0]))
 
     def step(self):
         d = self.depth

@@ -46,6 +46,10 @@ struct cbt_trainer {
     std::vector<uint32_t> sf, sb;
     std::vector<uint8_t> so;
     std::vector<double> leaves;
+    // pairs of a pair loss, handed to the session with the first tree
+    bool ranking = false, pairs_pending = false;
+    std::vector<uint32_t> group_off, pair_win, pair_los;
+    std::vector<double> pair_w;
     ~cbt_trainer() {
         if (s) cbh_session_end(s);
     }
@@ -65,6 +69,9 @@ int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F
         return cbh_internal_fail(CBH_ERR_UNSUPPORTED,
                                  "one-hot columns are not supported with bootstrap_type != No "
                                  "(the per-level RNG draw accounting of one-hot candidates is unset)");
+    // PairLogitPairwise scores the unsampled derivatives (boosting.rs:7877-7905)
+    if (p->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE && p->bootstrap_type != CBH_BOOT_NO)
+        return cbh_internal_fail(CBH_ERR_UNSUPPORTED, "PairLogitPairwise is covered without bootstrap");
     std::unique_ptr<cbt_trainer> t(new cbt_trainer());
     t->p = *p;
     // the learning rate that multiplies every leaf is the f32-representable one
@@ -100,6 +107,8 @@ int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F
     cfg.rng_seed = p->random_seed;
     cfg.one_hot_flags = one_hot_flags;
     cfg.real_folds = real_folds;
+    cfg.pairwise_non_diag_reg = p->pairwise_non_diag_reg;
+    t->ranking = p->loss == CBH_LOSS_PAIRLOGIT || p->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE;
     int rc = cbh_session_begin_u8(&cfg, bins_fm, weight, n, F, n_bins, t->p.learning_rate, scaled_l2, &t->s);
     if (rc != CBH_OK) return rc;
     t->rng = cbh::rng_from_seed(p->random_seed);
@@ -112,9 +121,25 @@ int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F
     return CBH_OK;
 }
 
+int cbt_set_pairs(cbt_trainer* t, const uint32_t* group_offsets, uint32_t n_groups,
+                  const uint32_t* pair_winner, const uint32_t* pair_loser, const double* pair_weight,
+                  uint64_t n_pairs) {
+    if (!t || !group_offsets || (n_pairs && (!pair_winner || !pair_loser))) return CBH_ERR_INVALID_ARG;
+    if (!t->ranking) return cbh_internal_fail(CBH_ERR_INVALID_ARG, "pairs given to a pointwise loss");
+    t->group_off.assign(group_offsets, group_offsets + (size_t)n_groups + 1);
+    t->pair_win.assign(pair_winner, pair_winner + n_pairs);
+    t->pair_los.assign(pair_loser, pair_loser + n_pairs);
+    if (pair_weight) t->pair_w.assign(pair_weight, pair_weight + n_pairs);
+    else t->pair_w.clear();
+    t->pairs_pending = true;
+    return CBH_OK;
+}
+
 int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8_t* split_one_hot,
              double* leaf_values) {
     if (!t) return CBH_ERR_INVALID_ARG;
+    if (t->ranking && t->first && !t->pairs_pending)
+        return cbh_internal_fail(CBH_ERR_INVALID_ARG, "a pair loss needs cbt_set_pairs before the first step");
     const cbt_params& p = t->p;
     // 1a. pre-bootstrap draws (train.cpp:208,211)
     if (t->draws_active)
@@ -141,10 +166,21 @@ int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8
     out.split_bin = t->sb.data();
     out.split_one_hot = t->so.data();
     out.leaf_values = t->leaves.data();
+    cbh_family fam{};
+    if (t->pairs_pending) {
+        fam.kind = CBH_FAMILY_PAIRWISE;
+        fam.n_groups = (uint32_t)(t->group_off.size() - 1);
+        fam.group_offsets = t->group_off.data();
+        fam.pair_winner = t->pair_win.data();
+        fam.pair_loser = t->pair_los.data();
+        fam.pair_weight = t->pair_w.empty() ? nullptr : t->pair_w.data();
+        fam.n_pairs = t->pair_win.size();
+    }
     int rc = cbh_session_grow(t->s, nullptr, t->first ? t->target.data() : nullptr, t->n, nullptr, 0,
-                              &smp, &out);
+                              &smp, t->pairs_pending ? &fam : nullptr, &out);
     if (rc != CBH_OK) return rc;
     t->first = false;
+    t->pairs_pending = false;
     // 3. replay the CPU grower's per-level draws, then the post-tree draws
     if (t->draws_active) {
         for (int level = 0; level < p.depth; ++level) {

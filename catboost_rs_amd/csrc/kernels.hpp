@@ -171,7 +171,9 @@ static __global__ __launch_bounds__(256) void prepare_kernel(
     const double* __restrict__ pending /* [leaves][K] lr-scaled, nullable */,
     SampleParams smp, JumpTabs jt, const double* __restrict__ host_sample,
     double* __restrict__ sstat /* [n][K+1] */, int newton,
-    unsigned long long* __restrict__ partials /* [gridDim.x][kPartials] */) {
+    unsigned long long* __restrict__ partials /* [gridDim.x][kPartials] */,
+    const double* __restrict__ ext_der /* nullable [2][n]: der1, der2 of a pair loss */,
+    const double* __restrict__ score_w /* nullable [n]: histogram weight (pairwise weights) */) {
     constexpr int C = K + 1;
     __shared__ unsigned long long red[4][kPartials];
     unsigned long long acc[kPartials] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -193,11 +195,19 @@ static __global__ __launch_bounds__(256) void prepare_kernel(
         const double w = weight ? weight[i] : 1.0;
         double d1[K];
         double h_leaf;  // leaf weight channel bound: w (Gradient) or |der2 * w| (Newton)
+        // histogram / Gradient-leaf weight: the pairwise weight for a pair loss
+        // (eff_weights, boosting.rs:7575-7579), else the object weight
+        const double hw = score_w ? score_w[i] : w;
         if (K == 1) {
             double g, h;
-            scalar_ders(loss, a[0], t, g, h);
+            if (ext_der) {
+                g = ext_der[i];
+                h = ext_der[n + i];
+            } else {
+                scalar_ders(loss, a[0], t, g, h);
+            }
             d1[0] = g;
-            h_leaf = newton ? fabs(h * w) : fabs(w);
+            h_leaf = newton ? fabs(h * w) : fabs(hw);
         } else {
             double p[K];
             softmax_probs<K>(a, p);
@@ -224,7 +234,7 @@ static __global__ __launch_bounds__(256) void prepare_kernel(
             mx_sd = fmax(mx_sd, fabs(sd));
             mx_ld = fmax(mx_ld, fabs(wd));
         }
-        const double sw = ctrl ? w * s : 0.0;        // score_weights (:7728)
+        const double sw = ctrl ? hw * s : 0.0;       // score_weights (:7728)
         sstat[i * C + K] = sw;
         leaf[i] = sw == 0.0 ? (uint16_t)0x8000u : (uint16_t)0;
         acc[kScoreDer] += (unsigned long long)ceil(mx_sd * bscale);
@@ -782,14 +792,20 @@ static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __r
 // sum(w * der1[d]) and sum(w) (Gradient) / sum(w * der2) (Newton) / packed sum(w * H)
 // (MultiClass), exact in fixed point.  LDS accumulators per block, global atomics.
 // ---------------------------------------------------------------------------------
+// Per-leaf sums over ALL rows (unsampled, boosting.rs:2470-2560), int64 fixed point.
+// K == 1 cells: [sum w der1, sum (Newton: w der2 | Gradient: weight), document count];
+// the count is filled for pair losses (centring of the leaf values), else left 0.
+template <int K>
+constexpr int leaf_cells() { return K == 1 ? 3 : K + K * (K + 1) / 2; }
+
 template <int K>
 static __global__ __launch_bounds__(256) void leaf_reduce_kernel(
     uint64_t n, int loss, int newton, const double* __restrict__ approx,
     const double* __restrict__ target, const double* __restrict__ weight,
     const uint16_t* __restrict__ leaf, const Scales* __restrict__ sc, uint32_t n_leaves,
-    long long* __restrict__ out) {
-    constexpr int PK = K * (K + 1) / 2;
-    constexpr int CL = K == 1 ? 2 : K + PK;
+    long long* __restrict__ out, const double* __restrict__ ext_der,
+    const double* __restrict__ score_w) {
+    constexpr int CL = leaf_cells<K>();
     extern __shared__ long long acc[];
     const uint32_t cells = n_leaves * CL;
     for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) acc[i] = 0;
@@ -802,9 +818,16 @@ static __global__ __launch_bounds__(256) void leaf_reduce_kernel(
         unsigned long long* cell = (unsigned long long*)(acc + (size_t)l * CL);
         if (K == 1) {
             double g, h;
-            scalar_ders(loss, approx[i], target[i], g, h);
+            if (ext_der) {
+                g = ext_der[i];
+                h = ext_der[n + i];
+            } else {
+                scalar_ders(loss, approx[i], target[i], g, h);
+            }
+            const double hw = score_w ? score_w[i] : w;
             atomicAdd(cell, (unsigned long long)to_fixed(g * w, md));
-            atomicAdd(cell + 1, (unsigned long long)to_fixed(newton ? h * w : w, mw));
+            atomicAdd(cell + 1, (unsigned long long)to_fixed(newton ? h * w : hw, mw));
+            if (ext_der) atomicAdd(cell + 2, 1ull);
         } else {
             double a[K], p[K];
 #pragma unroll
@@ -871,8 +894,7 @@ template <int K>
 static __global__ void leaf_values_kernel(const long long* __restrict__ sums, const Scales* __restrict__ sc,
                                    uint32_t n_leaves, int newton, double l2, double lr,
                                    double* __restrict__ raw, double* __restrict__ scaled) {
-    constexpr int PK = K * (K + 1) / 2;
-    constexpr int CL = K == 1 ? 2 : K + PK;
+    constexpr int CL = leaf_cells<K>();
     const uint32_t l = blockIdx.x * blockDim.x + threadIdx.x;
     if (l >= n_leaves) return;
     const long long* s = sums + (size_t)l * CL;

@@ -1,0 +1,442 @@
+// Ranking kernels of the gfx950 path: PairLogit derivatives over explicit pairs, and the
+// pairwise split scoring and leaf solve of PairLogitPairwise.
+//
+// Pairs are resident in the reference's competitor order (query group ascending, winner
+// ascending, input order per winner; crates/cb-train/src/query_info.rs:205-250):
+//   comp_win, comp_los  u32 [m]   winner / loser row of pair k
+//   comp_w              f64 [m]   pair weight
+//   comp_wq             i64 [m]   pair weight in fixed point (x 2^pair_shift, exact sums)
+//   comp_off            u32 [n+1] pairs of winner row i are comp_off[i] .. comp_off[i+1]
+//   group_off           u32 [G+1] query groups (contiguous rows)
+//
+// Pairwise statistics of a level (compute_pair_weight_statistics,
+// crates/cb-compute/src/pairwise_scoring.rs:163-196) are int64 fixed point, laid out
+//   st  i64 [F][B][P][P][2]   (bucket, first leaf, second leaf, {smaller, greater_right})
+// and turned into inclusive prefix sums over the bucket axis, so the running per-border
+// state of calculate_pairwise_score (:450-560) is read directly at border s.
+#pragma once
+#include "kernels.hpp"
+
+namespace cbh {
+
+constexpr uint32_t kPairMaxParents = 32;   // pairwise scoring: 2P <= 64 unknowns (depth <= 6)
+constexpr uint32_t kPairChunk = 8192;      // pairs per workgroup of the statistics kernel
+
+__device__ __forceinline__ uint32_t tri(uint32_t r, uint32_t c) {   // packed lower triangle
+    return r >= c ? r * (r + 1) / 2 + c : c * (c + 1) / 2 + r;
+}
+
+// pairlogit_pair_prob (crates/cb-compute/src/loss.rs:640-651).
+__device__ __forceinline__ double pairlogit_p(double winner_approx, double loser_approx) {
+    const double el = exp(loser_approx), ew = exp(winner_approx);
+    const double den = el + ew;
+    return den > 0.0 ? el / den : 0.5;
+}
+
+// PairLogit derivatives, one thread per query group (pairlogit_group_der,
+// crates/cb-compute/src/ranking_der.rs:408-445): rows of the group ascending, each winner's
+// pairs in order, a loser's derivatives decremented as its winners are visited and a
+// winner's own sums added after its pair loop -- the reference's accumulation order.  The
+// thread first applies the previous tree's leaf values to its rows (the rows of a group
+// belong to it alone).
+static __global__ __launch_bounds__(256) void pairlogit_ders_kernel(
+    const uint32_t* __restrict__ group_off, uint32_t n_groups, const uint32_t* __restrict__ comp_off,
+    const uint32_t* __restrict__ comp_los, const double* __restrict__ comp_w,
+    double* __restrict__ approx, const uint16_t* __restrict__ leaf,
+    const double* __restrict__ pending /* [leaves] lr-scaled, nullable */,
+    double* __restrict__ der1, double* __restrict__ der2) {
+    const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_groups) return;
+    const uint32_t b = group_off[g], e = group_off[g + 1];
+    if (pending)
+        for (uint32_t i = b; i < e; ++i) approx[i] += pending[leaf[i] & 0x7FFFu];
+    for (uint32_t i = b; i < e; ++i) {
+        der1[i] = 0.0;
+        der2[i] = 0.0;
+    }
+    for (uint32_t doc = b; doc < e; ++doc) {
+        const double wa = approx[doc];
+        double wd = 0.0, wd2 = 0.0;
+        for (uint32_t k = comp_off[doc]; k < comp_off[doc + 1]; ++k) {
+            const uint32_t l = comp_los[k];
+            const double p = pairlogit_p(wa, approx[l]);
+            const double w = comp_w[k];
+            wd += w * p;
+            wd2 += w * p * (p - 1.0);
+            der1[l] -= w * p;
+            der2[l] += w * p * (p - 1.0);
+        }
+        der1[doc] += wd;
+        der2[doc] += wd2;
+    }
+}
+
+// Pair-weight statistics of one level for every feature.  Grid (pair chunks, F).  For a
+// pair with winner bucket > loser bucket the cells [loserLeaf][winnerLeaf] are decremented at
+// (loser bucket, smaller) and (winner bucket, greater); otherwise [winnerLeaf][loserLeaf] at
+// (winner bucket, smaller) and (loser bucket, greater).  kLds: the P*P*B*2 cells of the
+// feature fit in LDS (P <= 4) and a workgroup accumulates its chunk there first.
+template <bool kLds>
+static __global__ __launch_bounds__(256) void pair_stats_kernel(
+    const uint8_t* __restrict__ cols, uint64_t n, const uint16_t* __restrict__ leaf,
+    const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los,
+    const long long* __restrict__ comp_wq, uint64_t m, uint32_t P, uint32_t B,
+    long long* __restrict__ st) {
+    extern __shared__ long long sh_st[];
+    const uint32_t f = blockIdx.y;
+    const size_t cells = (size_t)B * P * P * 2;
+    unsigned long long* out = (unsigned long long*)(st + (size_t)f * cells);
+    unsigned long long* acc = kLds ? (unsigned long long*)sh_st : out;
+    if (kLds) {
+        for (size_t i = threadIdx.x; i < cells; i += blockDim.x) sh_st[i] = 0;
+        __syncthreads();
+    }
+    const uint8_t* col = cols + (size_t)f * n;
+    const uint64_t k0 = (uint64_t)blockIdx.x * kPairChunk;
+    const uint64_t k1 = min(k0 + kPairChunk, m);
+    for (uint64_t k = k0 + threadIdx.x; k < k1; k += blockDim.x) {
+        const uint32_t wi = comp_win[k], lo = comp_los[k];
+        if (wi == lo) continue;
+        const unsigned long long neg = (unsigned long long)(-comp_wq[k]);
+        const uint32_t wb = col[wi], lb = col[lo];
+        const uint32_t wl = leaf[wi] & 0x7FFFu, ll = leaf[lo] & 0x7FFFu;
+        size_t c_small, c_great;
+        if (wb > lb) {
+            c_small = ((size_t)lb * P + ll) * P + wl;
+            c_great = ((size_t)wb * P + ll) * P + wl;
+        } else {
+            c_small = ((size_t)wb * P + wl) * P + ll;
+            c_great = ((size_t)lb * P + wl) * P + ll;
+        }
+        atomicAdd(acc + 2 * c_small, neg);
+        atomicAdd(acc + 2 * c_great + 1, neg);
+    }
+    if (kLds) {
+        __syncthreads();
+        for (size_t i = threadIdx.x; i < cells; i += blockDim.x)
+            if (sh_st[i] != 0) atomicAdd(out + i, (unsigned long long)sh_st[i]);
+    }
+}
+
+// Inclusive prefix over the bucket axis, in place; one thread per (f, x, y, c).
+static __global__ __launch_bounds__(256) void pair_scan_kernel(long long* __restrict__ st, uint32_t F,
+                                                               uint32_t P, uint32_t B) {
+    const size_t row = (size_t)P * P * 2;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (size_t)F * row) return;
+    long long* p = st + (t / row) * B * row + (t % row);
+    long long run = 0;
+    for (uint32_t b = 0; b < B; ++b) {
+        run += p[(size_t)b * row];
+        p[(size_t)b * row] = run;
+    }
+}
+
+// Inclusive prefix over buckets of the der channel of the level histogram
+// (hist [P][C][F][B], channel 0): dcum [F][B][P].  One thread per (f, leaf).
+static __global__ __launch_bounds__(256) void der_scan_kernel(const long long* __restrict__ hist, uint32_t P,
+                                                              uint32_t C, uint32_t F, uint32_t B,
+                                                              long long* __restrict__ dcum) {
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= F * P) return;
+    const uint32_t f = t / P, y = t % P;
+    const long long* h = hist + ((size_t)y * C * F + f) * B;
+    long long run = 0;
+    for (uint32_t b = 0; b < B; ++b) {
+        run += h[b];
+        dcum[((size_t)f * B + b) * P + y] = run;
+    }
+}
+
+// MakeZeroAverage (pairwise_scoring.rs:255-265), sequential sum as the reference.
+__device__ inline void zero_average_wave(double* r, int n) {
+    __shared__ double avg_s;
+    if ((threadIdx.x & 63) == 0) {
+        double avg = 0.0;
+        for (int i = 0; i < n; ++i) avg += r[i];
+        avg_s = avg / (double)n;
+    }
+    __syncthreads();
+    const double avg = avg_s;
+    for (int i = threadIdx.x & 63; i < n; i += 64) r[i] -= avg;
+    __syncthreads();
+}
+
+// One wavefront (the whole workgroup) solves the pairwise leaf system of n <= 64 unknowns
+// (calculate_pairwise_leaf_values, pairwise_scoring.rs:283-345, pairwise_leaves.rs:120-200):
+// W (packed lower triangle, n x n) plus the bucket-weight prior gives the (n-1)x(n-1) SPD
+// matrix M; right-looking Cholesky in LDS (every element receives its pivot subtractions in
+// ascending order, as the reference's left-looking loop applies them), forward and back
+// substitution, res[n-1] = 0, zero average.  A non-positive pivot yields zeros.
+__device__ inline void pairwise_solve_wave(const double* W, const double* der, int n, double l2,
+                                           double prior, double* M, double* y, double* res) {
+    const int lane = threadIdx.x & 63;
+    const double cell_prior = 1.0 / (double)n;
+    const double non_diag = -prior * cell_prior;
+    const double diag = prior * (1.0 - cell_prior) + l2;
+    if (n <= 2) {
+        if (lane == 0) {
+            if (n == 1) {
+                res[0] = 0.0;
+            } else {
+                const double den = W[0] + diag;
+                res[0] = den != 0.0 ? der[0] / den : 0.0;
+                res[1] = 0.0;
+            }
+        }
+        __syncthreads();
+        if (n == 2) zero_average_wave(res, 2);
+        return;
+    }
+    const int m = n - 1;
+    for (int r = lane; r < m; r += 64) {
+        for (int c = 0; c < r; ++c) M[tri(r, c)] = W[tri(r, c)] + non_diag;
+        M[tri(r, r)] = W[tri(r, r)] + diag;
+        y[r] = der[r];
+    }
+    __syncthreads();
+    bool good = true;
+    for (int j = 0; j < m; ++j) {
+        const double d = M[tri(j, j)];
+        if (d <= 0.0) {
+            good = false;
+            break;
+        }
+        const double ljj = sqrt(d);
+        __syncthreads();
+        for (int i = j + 1 + lane; i < m; i += 64) M[tri(i, j)] = M[tri(i, j)] / ljj;
+        if (lane == 0) M[tri(j, j)] = ljj;
+        __syncthreads();
+        for (int i = j + 1 + lane; i < m; i += 64) {
+            const double lij = M[tri(i, j)];
+            for (int k = j + 1; k <= i; ++k) M[tri(i, k)] -= lij * M[tri(k, j)];
+        }
+        __syncthreads();
+    }
+    if (good) {
+        for (int p = 0; p < m; ++p) {   // forward: y[i] -= L[i][p] y[p], p ascending
+            if (lane == 0) y[p] = y[p] / M[tri(p, p)];
+            __syncthreads();
+            const double yp = y[p];
+            for (int i = p + 1 + lane; i < m; i += 64) y[i] -= M[tri(i, p)] * yp;
+            __syncthreads();
+        }
+        for (int p = m - 1; p >= 0; --p) {   // back: L^T x = y
+            if (lane == 0) res[p] = y[p] / M[tri(p, p)];
+            __syncthreads();
+            const double xp = res[p];
+            for (int i = lane; i < p; i += 64) y[i] -= M[tri(p, i)] * xp;
+            __syncthreads();
+        }
+    } else {
+        for (int i = lane; i < m; i += 64) res[i] = 0.0;
+    }
+    if (lane == 0) res[m] = 0.0;
+    __syncthreads();
+    zero_average_wave(res, n);
+}
+
+// calculate_score (pairwise_scoring.rs:352-375): sum_x a[x] (der[x] - 0.5 sum_y a[y] W[x][y]),
+// inner and outer sums sequential.  Returns the value on lane 0.
+__device__ inline double pairwise_score_wave(const double* a, const double* der, const double* W, int n,
+                                             double* part) {
+    const int lane = threadIdx.x & 63;
+    for (int x = lane; x < n; x += 64) {
+        double inner = 0.0;
+        for (int yy = 0; yy < n; ++yy) inner += a[yy] * W[tri(x, yy)];
+        part[x] = a[x] * (der[x] - 0.5 * inner);
+    }
+    __syncthreads();
+    double outer = 0.0;
+    if (lane == 0)
+        for (int x = 0; x < n; ++x) outer += part[x];
+    return outer;
+}
+
+// LDS of the candidate and leaf solves: W and M packed (2 x 2080 doubles) + 4 vectors of 64.
+constexpr size_t kPairSolveLds = (2 * 2080 + 4 * 64) * sizeof(double);
+
+// One wavefront per (border s, feature f): the weight matrix of border s from the cumulative
+// statistics (all terms exact in int64 -- UpdateWeightSumFromTotal plus the accumulated
+// UpdateWeightSumFromNonDiagStats / diagonal deltas, pairwise_scoring.rs:377-430 -- converted
+// once), the der vector from the cumulative der histogram, the leaf solve and the score.
+static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
+    const long long* __restrict__ st, const long long* __restrict__ dcum,
+    const uint32_t* __restrict__ n_cand, uint32_t P, uint32_t B, const Scales* __restrict__ sc,
+    double pair_inv, double l2, double prior, double* __restrict__ scores /* [F][B] */) {
+    extern __shared__ double sh_pw[];
+    const uint32_t s = blockIdx.x, f = blockIdx.y;
+    const int lane = threadIdx.x;
+    if (s >= n_cand[f]) {
+        if (lane == 0) scores[(size_t)f * B + s] = -INFINITY;
+        return;
+    }
+    double* W = sh_pw;
+    double* M = W + 2080;
+    double* der = M + 2080;
+    double* yv = der + 64;
+    double* res = yv + 64;
+    double* part = res + 64;
+    const int n = 2 * (int)P;
+    const size_t row = (size_t)P * P * 2;
+    const long long* R = st + ((size_t)f * B + s) * row;
+    const long long* T = st + ((size_t)f * B + (B - 1)) * row;
+    const double inv_d = sc->inv[kScoreDer];
+    for (uint32_t yl = lane; yl < P; yl += 64) {
+        const long long dp = dcum[((size_t)f * B + s) * P + yl];
+        const long long dt = dcum[((size_t)f * B + (B - 1)) * P + yl];
+        der[2 * yl] = (double)dp * inv_d;
+        der[2 * yl + 1] = (double)(dt - dp) * inv_d;
+    }
+    for (int r = lane; r < n; r += 64) {
+        const uint32_t a = (uint32_t)r >> 1, u = (uint32_t)r & 1u;
+        const long long da = R[((size_t)a * P + a) * 2] - R[((size_t)a * P + a) * 2 + 1];
+        long long dg = -da;   // W[r][r]
+        for (uint32_t b = 0; b < P; ++b) {
+            if (b == a) continue;
+            const uint32_t yv_ = a < b ? a : b, xv = a < b ? b : a;
+            const long long xs = R[((size_t)xv * P + yv_) * 2], xg = R[((size_t)xv * P + yv_) * 2 + 1];
+            const long long ys = R[((size_t)yv_ * P + xv) * 2], yg = R[((size_t)yv_ * P + xv) * 2 + 1];
+            const long long total = T[((size_t)xv * P + yv_) * 2] + T[((size_t)yv_ * P + xv) * 2];
+            const long long w00 = xg + yg, w01 = xs - xg, w10 = ys - yg, w11 = -(xs + ys);
+            long long e0, e1;   // W[r][2b], W[r][2b+1]
+            if (u == 0) {
+                e0 = w00;
+                e1 = a > b ? w01 : w10;
+                dg -= a < b ? (w00 + w10) : (w00 + w01);
+            } else {
+                e0 = a > b ? w10 : w01;
+                e1 = w11 + total;
+                dg -= (a < b ? (w01 + w11) : (w10 + w11)) + total;
+            }
+            if (2 * b <= (uint32_t)r) W[tri(r, 2 * b)] = (double)e0 * pair_inv;
+            if (2 * b + 1 <= (uint32_t)r) W[tri(r, 2 * b + 1)] = (double)e1 * pair_inv;
+        }
+        W[tri(r, r)] = (double)dg * pair_inv;
+        if (u == 1) W[tri(r, r - 1)] = (double)da * pair_inv;
+    }
+    __syncthreads();
+    pairwise_solve_wave(W, der, n, l2, prior, M, yv, res);
+    const double score = pairwise_score_wave(res, der, W, n, part);
+    if (lane == 0) scores[(size_t)f * B + s] = score;
+}
+
+// Best border of each feature: maximum score, lowest border on ties (strict first-wins over
+// border ascending, select_level_pairwise tree.rs:3852-3900).
+static __global__ __launch_bounds__(256) void pairwise_best_kernel(const double* __restrict__ scores,
+                                                                   const uint32_t* __restrict__ n_cand,
+                                                                   uint32_t B, double* __restrict__ best_score,
+                                                                   uint32_t* __restrict__ best_bin) {
+    __shared__ double rs[4];
+    __shared__ uint32_t rb[4];
+    const uint32_t f = blockIdx.x;
+    double s = -INFINITY;
+    uint32_t bb = 0xFFFFFFFFu;
+    for (uint32_t b = threadIdx.x; b < n_cand[f]; b += blockDim.x) {
+        const double v = scores[(size_t)f * B + b];
+        if (v > s || (v == s && b < bb)) {
+            s = v;
+            bb = b;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const double os = __shfl_xor(s, o, 64);
+        const uint32_t ob = __shfl_xor(bb, o, 64);
+        if (os > s || (os == s && ob < bb)) {
+            s = os;
+            bb = ob;
+        }
+    }
+    if (lane_id() == 0) {
+        rs[threadIdx.x >> 6] = s;
+        rb[threadIdx.x >> 6] = bb;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; ++k)
+            if (rs[k] > s || (rs[k] == s && rb[k] < bb)) {
+                s = rs[k];
+                bb = rb[k];
+            }
+        best_score[f] = s;
+        best_bin[f] = bb == 0xFFFFFFFFu ? 0u : bb;
+    }
+}
+
+// Pairwise weight sums of the final leaves (compute_pairwise_weight_sums,
+// pairwise_leaves.rs:47-88): out [L][L] int64, same-leaf pairs skipped.
+static __global__ __launch_bounds__(256) void pair_leaf_weights_kernel(
+    const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los,
+    const long long* __restrict__ comp_wq, uint64_t m, const uint16_t* __restrict__ leaf, uint32_t L,
+    long long* __restrict__ out) {
+    extern __shared__ long long sh_lw[];
+    for (uint32_t i = threadIdx.x; i < L * L; i += blockDim.x) sh_lw[i] = 0;
+    __syncthreads();
+    unsigned long long* acc = (unsigned long long*)sh_lw;
+    for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < m;
+         k += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t wl = leaf[comp_win[k]] & 0x7FFFu, ll = leaf[comp_los[k]] & 0x7FFFu;
+        if (wl == ll) continue;
+        const long long q = comp_wq[k];
+        atomicAdd(acc + (size_t)wl * L + ll, (unsigned long long)(-q));
+        atomicAdd(acc + (size_t)ll * L + wl, (unsigned long long)(-q));
+        atomicAdd(acc + (size_t)wl * L + wl, (unsigned long long)q);
+        atomicAdd(acc + (size_t)ll * L + ll, (unsigned long long)q);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < L * L; i += blockDim.x)
+        if (sh_lw[i] != 0) atomicAdd((unsigned long long*)out + i, (unsigned long long)sh_lw[i]);
+}
+
+// normalize_leaf_values for pairwise-weight losses (boosting.rs:2844-2882): subtract the
+// document-weighted mean leaf value (leaves with |weight| <= 1e-9 become 0), then scale by
+// the learning rate.  counts are the per-leaf document weights (integers).  Lane 0 only.
+__device__ inline void pairwise_center_lane0(double* raw, const long long* sums, uint32_t CL, uint32_t L,
+                                             double lr, double* scaled) {
+    double total = 0.0;
+    for (uint32_t l = 0; l < L; ++l) total += (double)sums[(size_t)l * CL + 2];
+    if (fabs(total) > 1e-9) {
+        double weighted = 0.0;
+        for (uint32_t l = 0; l < L; ++l) weighted += raw[l] * (double)sums[(size_t)l * CL + 2];
+        const double avg = weighted / total;
+        for (uint32_t l = 0; l < L; ++l) {
+            if (fabs((double)sums[(size_t)l * CL + 2]) > 1e-9) raw[l] -= avg;
+            else raw[l] = 0.0;
+        }
+    }
+    for (uint32_t l = 0; l < L; ++l) scaled[l] = raw[l] * lr;
+}
+
+// PairLogit leaves: centring of the Newton / Gradient values of leaf_values_kernel.
+static __global__ void pairwise_center_kernel(double* __restrict__ raw, const long long* __restrict__ sums,
+                                              uint32_t CL, uint32_t L, double lr, double* __restrict__ scaled) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) pairwise_center_lane0(raw, sums, CL, L, lr, scaled);
+}
+
+// PairLogitPairwise leaves (compute_pairwise_leaf_deltas, pairwise_leaves.rs:219-238): one
+// wavefront solves the L-leaf system from the pair weight sums and the per-leaf der sums,
+// then the centring.
+static __global__ __launch_bounds__(64) void pairwise_leaf_kernel(
+    const long long* __restrict__ lw, uint32_t L, const long long* __restrict__ sums, uint32_t CL,
+    const Scales* __restrict__ sc, double pair_inv, double l2, double prior, double lr,
+    double* __restrict__ raw, double* __restrict__ scaled) {
+    extern __shared__ double sh_pl[];
+    double* W = sh_pl;
+    double* M = W + 2080;
+    double* der = M + 2080;
+    double* yv = der + 64;
+    double* res = yv + 64;
+    const int lane = threadIdx.x;
+    const double inv_d = sc->inv[kLeafDer];
+    for (uint32_t r = lane; r < L; r += 64) {
+        for (uint32_t c = 0; c <= r; ++c) W[tri(r, c)] = (double)lw[(size_t)r * L + c] * pair_inv;
+        der[r] = (double)sums[(size_t)r * CL] * inv_d;
+    }
+    __syncthreads();
+    pairwise_solve_wave(W, der, (int)L, l2, prior, M, yv, res);
+    for (uint32_t l = lane; l < L; l += 64) raw[l] = res[l];
+    __syncthreads();
+    if (lane == 0) pairwise_center_lane0(raw, sums, CL, L, lr, scaled);
+}
+
+}  // namespace cbh

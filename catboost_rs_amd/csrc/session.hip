@@ -19,6 +19,7 @@
 #include "../../include/cbhip.h"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "ranking.hpp"
 
 using namespace cbh;
 
@@ -139,6 +140,26 @@ struct cbh_session {
     uint64_t* jump = nullptr;               // [2048 + 2 * n_coarse]: fine a, fine d, coarse a, coarse d
     uint64_t n_coarse = 0;
     unsigned long long* partials = nullptr; // [kPrepBlocks][kPartials]
+
+    // pair losses (PairLogit: pointwise scoring over pairwise weights; PairLogitPairwise:
+    // pairwise statistics scoring and Cholesky leaves)
+    bool ranking = false, pairwise = false, pairs_set = false;
+    double prior = 0.1;
+    uint32_t n_groups = 0;
+    uint64_t n_pairs = 0;
+    double pair_inv = 1.0;
+    uint32_t* group_off = nullptr;   // [n_groups + 1]
+    uint32_t* comp_off = nullptr;    // [n + 1]
+    uint32_t* comp_win = nullptr;    // [m]
+    uint32_t* comp_los = nullptr;    // [m]
+    double* comp_w = nullptr;        // [m]
+    long long* comp_wq = nullptr;    // [m]
+    double* ext_der = nullptr;       // [2][n] der1, der2
+    double* score_w = nullptr;       // [n] pairwise weights
+    long long* pair_st = nullptr;    // [F][B][Pmax][Pmax][2]
+    long long* dcum = nullptr;       // [F][B][Pmax]
+    double* cand_scores = nullptr;   // [F][B]
+    long long* leaf_w = nullptr;     // [L][L]
     JumpTabs jt() const {
         return JumpTabs{jump, jump + 1024, jump + 2048, jump + 2048 + n_coarse};
     }
@@ -157,6 +178,9 @@ struct cbh_session {
         dfree(best_bin); dfree(n_cand); dfree(one_hot); dfree(scales); dfree(bounds);
         dfree(leaf_sums); dfree(leaf_raw); dfree(leaf_scaled); dfree(jump);
         dfree(partials);
+        dfree(group_off); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
+        dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st); dfree(dcum);
+        dfree(cand_scores); dfree(leaf_w);
         for (auto& t : timers) {
             if (t.second.a) (void)hipEventDestroy(t.second.a);
             if (t.second.b) (void)hipEventDestroy(t.second.b);
@@ -216,8 +240,10 @@ int validate_config(const cbh_config* cfg, uint32_t n_bins, uint64_t n, uint32_t
         return fail(CBH_DECLINED, "ordered boosting / several folds are not covered on device");
     if (cfg->depth < 1 || cfg->depth > kMaxDepth)
         return fail(CBH_DECLINED, "depth outside 1..8 is not covered on device");
-    if (cfg->loss < CBH_LOSS_RMSE || cfg->loss > CBH_LOSS_CROSSENTROPY)
+    if (cfg->loss < CBH_LOSS_RMSE || cfg->loss > CBH_LOSS_PAIRLOGIT_PAIRWISE)
         return fail(CBH_DECLINED, "loss not covered on device");
+    if (cfg->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE && cfg->depth > 6)
+        return fail(CBH_DECLINED, "PairLogitPairwise is covered up to depth 6 (64-leaf systems)");
     if (cfg->loss == CBH_LOSS_MULTICLASS) {
         if (cfg->approx_dim < 2 || cfg->approx_dim > kMaxK)
             return fail(CBH_DECLINED, "MultiClass approx_dim must be 2..16");
@@ -259,8 +285,20 @@ int session_alloc(cbh_session* s) {
     CHECK(dalloc(&s->n_cand, s->F));
     CHECK(dalloc(&s->scales, 1));
     CHECK(dalloc(&s->bounds, 1));
-    const uint32_t CL = s->K == 1 ? 2 : s->K + s->K * (s->K + 1) / 2;
+    const uint32_t CL = s->K == 1 ? 3 : s->K + s->K * (s->K + 1) / 2;
     CHECK(dalloc(&s->leaf_sums, ((size_t)1 << s->depth) * CL));
+    if (s->ranking) {
+        CHECK(dalloc(&s->ext_der, 2 * n));
+        CHECK(dalloc(&s->score_w, n));
+        CHECK(dalloc(&s->comp_off, n + 1));
+    }
+    if (s->pairwise) {
+        const size_t pmax = (size_t)1 << (s->depth - 1);
+        CHECK(dalloc(&s->pair_st, (size_t)s->F * s->B * pmax * pmax * 2));
+        CHECK(dalloc(&s->dcum, (size_t)s->F * s->B * pmax));
+        CHECK(dalloc(&s->cand_scores, (size_t)s->F * s->B));
+        CHECK(dalloc(&s->leaf_w, ((size_t)1 << s->depth) << s->depth));
+    }
     CHECK(dalloc(&s->leaf_raw, ((size_t)1 << s->depth) * s->K));
     CHECK(dalloc(&s->leaf_scaled, ((size_t)1 << s->depth) * s->K));
     CHECK(dalloc(&s->partials, (size_t)kPrepBlocks * kPartials));
@@ -336,6 +374,15 @@ int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double*
     s->lr = lr;
     s->l2 = l2;
     s->has_weight = weight != nullptr;
+    s->ranking = cfg->loss == CBH_LOSS_PAIRLOGIT || cfg->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE;
+    s->pairwise = cfg->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE;
+    s->prior = cfg->pairwise_non_diag_reg;
+    if (s->ranking && weight)
+        return fail(CBH_ERR_UNSUPPORTED, "pair losses take their weights from the pairs, not per object");
+    if (s->ranking && cfg->one_hot_flags)
+        for (uint32_t f = 0; f < F; ++f)
+            if (cfg->one_hot_flags[f])
+                return fail(CBH_ERR_UNSUPPORTED, "one-hot columns are not covered with pair losses");
     HIP_TRY(hipGetDevice(&s->device));
     HIP_TRY(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
     CHECK(session_alloc(s.get()));
@@ -393,6 +440,120 @@ int launch_zero(long long* p, size_t n, hipStream_t st) {
     return CBH_OK;
 }
 
+// Pairs of a pair loss (FamilyTreeArgs::Pairwise, runtime.rs:925-934): validated, put in the
+// reference's competitor order (stable by winner, query_info.rs:205-250), pairwise weights per
+// row in pair order (calc_pairwise_weights, boosting.rs:1760-1783), pair weights in fixed
+// point 2^shift with 2^shift * sum|w| <= 2^60 (every statistic and weight-matrix entry is a
+// sum of at most 4 sum|w|), uploaded once.
+int upload_pairs(cbh_session* s, const cbh_family* fam) {
+    const uint64_t n = s->n;
+    if (fam->kind != CBH_FAMILY_PAIRWISE) return fail(CBH_ERR_INVALID_ARG, "family kind is not CBH_FAMILY_PAIRWISE");
+    if (!fam->group_offsets || fam->n_groups == 0) return fail(CBH_ERR_INVALID_ARG, "group_offsets are missing");
+    const uint32_t G = fam->n_groups;
+    const uint32_t* go = fam->group_offsets;
+    if (go[0] != 0 || go[G] != n) return fail(CBH_ERR_LENGTH_MISMATCH, "group_offsets must run from 0 to n");
+    for (uint32_t g = 0; g < G; ++g)
+        if (go[g + 1] < go[g]) return fail(CBH_ERR_OUT_OF_RANGE, "group_offsets decrease at group " + std::to_string(g));
+    const uint64_t m = fam->n_pairs;
+    if (m >= (1ull << 32)) return fail(CBH_ERR_UNSUPPORTED, "more than 2^32-1 pairs");
+    if (m && (!fam->pair_winner || !fam->pair_loser)) return fail(CBH_ERR_INVALID_ARG, "pair arrays are null");
+    std::vector<uint32_t> grp(n);
+    for (uint32_t g = 0; g < G; ++g)
+        for (uint32_t i = go[g]; i < go[g + 1]; ++i) grp[i] = g;
+    for (uint64_t k = 0; k < m; ++k) {
+        const uint32_t w = fam->pair_winner[k], l = fam->pair_loser[k];
+        if (w >= n || l >= n || grp[w] != grp[l])
+            return fail(CBH_ERR_OUT_OF_RANGE, "pair " + std::to_string(k) + " is out of range or crosses query groups");
+        if (fam->pair_weight && !std::isfinite(fam->pair_weight[k]))
+            return fail(CBH_ERR_OUT_OF_RANGE, "pair weight " + std::to_string(k) + " is not finite");
+    }
+    std::vector<uint32_t> off(n + 1, 0);
+    for (uint64_t k = 0; k < m; ++k) off[fam->pair_winner[k] + 1]++;
+    for (uint64_t i = 0; i < n; ++i) off[i + 1] += off[i];
+    std::vector<uint32_t> pos(off.begin(), off.end() - 1), win(m), los(m);
+    std::vector<double> w(m);
+    for (uint64_t k = 0; k < m; ++k) {
+        const uint32_t j = pos[fam->pair_winner[k]]++;
+        win[j] = fam->pair_winner[k];
+        los[j] = fam->pair_loser[k];
+        w[j] = fam->pair_weight ? fam->pair_weight[k] : 1.0;
+    }
+    std::vector<double> pw(n, 0.0);
+    double sum_abs = 0.0;
+    for (uint64_t j = 0; j < m; ++j) {
+        pw[win[j]] += w[j];
+        pw[los[j]] += w[j];
+        sum_abs += std::fabs(w[j]);
+    }
+    int e = 0;
+    if (sum_abs > 0.0) std::frexp(sum_abs, &e);
+    const int shift = std::min(60 - e, 100);
+    std::vector<long long> wq(m);
+    for (uint64_t j = 0; j < m; ++j) wq[j] = std::llrint(std::ldexp(w[j], shift));
+    s->pair_inv = std::ldexp(1.0, -shift);
+    if (m != s->n_pairs || !s->comp_win) {
+        dfree(s->comp_win); dfree(s->comp_los); dfree(s->comp_w); dfree(s->comp_wq);
+        CHECK(dalloc(&s->comp_win, m));
+        CHECK(dalloc(&s->comp_los, m));
+        CHECK(dalloc(&s->comp_w, m));
+        CHECK(dalloc(&s->comp_wq, m));
+    }
+    if (G != s->n_groups || !s->group_off) {
+        dfree(s->group_off);
+        CHECK(dalloc(&s->group_off, (size_t)G + 1));
+    }
+    s->n_pairs = m;
+    s->n_groups = G;
+    hipStream_t st = s->stream;
+    if (m) {
+        HIP_TRY(hipMemcpyAsync(s->comp_win, win.data(), sizeof(uint32_t) * m, hipMemcpyHostToDevice, st));
+        HIP_TRY(hipMemcpyAsync(s->comp_los, los.data(), sizeof(uint32_t) * m, hipMemcpyHostToDevice, st));
+        HIP_TRY(hipMemcpyAsync(s->comp_w, w.data(), sizeof(double) * m, hipMemcpyHostToDevice, st));
+        HIP_TRY(hipMemcpyAsync(s->comp_wq, wq.data(), sizeof(long long) * m, hipMemcpyHostToDevice, st));
+    }
+    HIP_TRY(hipMemcpyAsync(s->comp_off, off.data(), sizeof(uint32_t) * (n + 1), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(s->group_off, go, sizeof(uint32_t) * ((size_t)G + 1), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(s->score_w, pw.data(), sizeof(double) * n, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    s->pairs_set = true;
+    return CBH_OK;
+}
+
+// Pairwise scoring of one level (PairLogitPairwise, tree.rs:3810-3900): statistics, prefix
+// sums over buckets, one wavefront per (border, feature), per-feature best, level argmax.
+int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
+    hipStream_t st = s->stream;
+    const uint32_t P = 1u << level, B = s->B, F = s->F;
+    const size_t cells = (size_t)F * B * P * P * 2;
+    CHECK(launch_zero(s->pair_st, cells, st));
+    if (s->n_pairs) {
+        const dim3 grid((unsigned)((s->n_pairs + kPairChunk - 1) / kPairChunk), F);
+        if (P <= 4) {
+            const size_t lds = (size_t)B * P * P * 2 * sizeof(long long);
+            HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_kernel<true>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            pair_stats_kernel<true><<<grid, 256, lds, st>>>(s->cols, s->n, s->leaf, s->comp_win, s->comp_los,
+                                                           s->comp_wq, s->n_pairs, P, B, s->pair_st);
+        } else {
+            pair_stats_kernel<false><<<grid, 256, 0, st>>>(s->cols, s->n, s->leaf, s->comp_win, s->comp_los,
+                                                           s->comp_wq, s->n_pairs, P, B, s->pair_st);
+        }
+        HIP_TRY(hipGetLastError());
+    }
+    pair_scan_kernel<<<grid_for((uint64_t)F * P * P * 2, 256), 256, 0, st>>>(s->pair_st, F, P, B);
+    HIP_TRY(hipGetLastError());
+    der_scan_kernel<<<grid_for((uint64_t)F * P, 256), 256, 0, st>>>(cur, P, s->C, F, B, s->dcum);
+    HIP_TRY(hipGetLastError());
+    pairwise_candidate_kernel<<<dim3(B - 1, F), 64, kPairSolveLds, st>>>(
+        s->pair_st, s->dcum, s->n_cand, P, B, s->scales, s->pair_inv, s->l2, s->prior, s->cand_scores);
+    HIP_TRY(hipGetLastError());
+    pairwise_best_kernel<<<F, 256, 0, st>>>(s->cand_scores, s->n_cand, B, s->best_score, s->best_bin);
+    HIP_TRY(hipGetLastError());
+    argmax_kernel<<<1, 1024, 0, st>>>(s->best_score, s->best_bin, nullptr, F, s->splits + level);
+    HIP_TRY(hipGetLastError());
+    return CBH_OK;
+}
+
 template <int K>
 int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
               std::vector<SplitRec>& splits_out, std::vector<LevelPlan>& plans_out,
@@ -406,10 +567,18 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
 
     // ---- prepare: apply previous tree, ders, sample, score channels, bounds ----
     CHECK(s->stage_begin(kStPrepare));
+    if (s->ranking) {   // pair ders need every row's updated approximant: apply, then ders
+        pairlogit_ders_kernel<<<grid_for(s->n_groups, 256), 256, 0, st>>>(
+            s->group_off, s->n_groups, s->comp_off, s->comp_los, s->comp_w, s->approx, s->leaf,
+            s->pending ? s->leaf_scaled : nullptr, s->ext_der, s->ext_der + n);
+        HIP_TRY(hipGetLastError());
+        s->pending = false;
+    }
     const unsigned pgrid = grid_for(n, 256, kPrepBlocks);
     prepare_kernel<K><<<pgrid, 256, 0, st>>>(
         n, loss, s->approx, s->target, s->weight, s->leaf, s->pending ? s->leaf_scaled : nullptr,
-        smp, s->jt(), use_host_sample ? s->host_sample : nullptr, s->sstat, newton, s->partials);
+        smp, s->jt(), use_host_sample ? s->host_sample : nullptr, s->sstat, newton, s->partials,
+        s->ranking ? s->ext_der : nullptr, s->ranking ? s->score_w : nullptr);
     HIP_TRY(hipGetLastError());
     s->pending = false;
     scales_kernel<<<1, 256, 0, st>>>(s->partials, pgrid, s->bounds, s->scales);
@@ -448,7 +617,9 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         }
         // ---- score + argmax ----
         CHECK(s->stage_begin(kStScore));
-        if (s->B <= 64)
+        if (s->pairwise) {
+            CHECK(pairwise_level(s, cur, level));
+        } else if (s->B <= 64)
             score_kernel<K, 1><<<s->F, 64, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin);
         else if (s->B <= 128)
@@ -458,8 +629,10 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
             score_kernel<K, 4><<<s->F, 256, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
                                                     s->scales, s->l2, cosine, s->best_score, s->best_bin);
         HIP_TRY(hipGetLastError());
-        argmax_kernel<<<1, 1024, 0, st>>>(s->best_score, s->best_bin, s->one_hot, s->F, s->splits + level);
-        HIP_TRY(hipGetLastError());
+        if (!s->pairwise) {
+            argmax_kernel<<<1, 1024, 0, st>>>(s->best_score, s->best_bin, s->one_hot, s->F, s->splits + level);
+            HIP_TRY(hipGetLastError());
+        }
         CHECK(s->stage_end());
         // ---- partition ----
         CHECK(s->stage_begin(kStPartition));
@@ -481,17 +654,37 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     // ---- leaf statistics + values ----
     CHECK(s->stage_begin(kStLeaf));
     const uint32_t n_leaves = 1u << s->depth;
-    const uint32_t CL = K == 1 ? 2 : K + K * (K + 1) / 2;
+    const uint32_t CL = (uint32_t)leaf_cells<K>();
     CHECK(launch_zero(s->leaf_sums, (size_t)n_leaves * CL, st));
     const size_t lds = (size_t)n_leaves * CL * sizeof(long long);
     HIP_TRY(hipFuncSetAttribute((const void*)leaf_reduce_kernel<K>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     leaf_reduce_kernel<K><<<grid_for(n, 256, 1024), 256, lds, st>>>(
-        n, loss, newton, s->approx, s->target, s->weight, s->leaf, s->scales, n_leaves, s->leaf_sums);
+        n, loss, newton, s->approx, s->target, s->weight, s->leaf, s->scales, n_leaves, s->leaf_sums,
+        s->ranking ? s->ext_der : nullptr, s->ranking ? s->score_w : nullptr);
     HIP_TRY(hipGetLastError());
-    leaf_values_kernel<K><<<(n_leaves + 63) / 64, 64, 0, st>>>(s->leaf_sums, s->scales, n_leaves, newton,
-                                                              s->l2, s->lr, s->leaf_raw, s->leaf_scaled);
-    HIP_TRY(hipGetLastError());
+    if (s->pairwise) {
+        CHECK(launch_zero(s->leaf_w, (size_t)n_leaves * n_leaves, st));
+        if (s->n_pairs) {
+            pair_leaf_weights_kernel<<<grid_for(s->n_pairs, 256, 1024), 256,
+                                       (size_t)n_leaves * n_leaves * sizeof(long long), st>>>(
+                s->comp_win, s->comp_los, s->comp_wq, s->n_pairs, s->leaf, n_leaves, s->leaf_w);
+            HIP_TRY(hipGetLastError());
+        }
+        pairwise_leaf_kernel<<<1, 64, kPairSolveLds, st>>>(s->leaf_w, n_leaves, s->leaf_sums, CL, s->scales,
+                                                          s->pair_inv, s->l2, s->prior, s->lr,
+                                                          s->leaf_raw, s->leaf_scaled);
+        HIP_TRY(hipGetLastError());
+    } else {
+        leaf_values_kernel<K><<<(n_leaves + 63) / 64, 64, 0, st>>>(s->leaf_sums, s->scales, n_leaves, newton,
+                                                                  s->l2, s->lr, s->leaf_raw, s->leaf_scaled);
+        HIP_TRY(hipGetLastError());
+        if (s->ranking) {
+            pairwise_center_kernel<<<1, 64, 0, st>>>(s->leaf_raw, s->leaf_sums, CL, n_leaves, s->lr,
+                                                     s->leaf_scaled);
+            HIP_TRY(hipGetLastError());
+        }
+    }
     CHECK(s->stage_end());
     s->pending = true;
 
@@ -530,8 +723,16 @@ int cbh_session_begin_u8(const cbh_config* cfg, const uint8_t* bins_fm, const do
 
 int cbh_session_grow(cbh_session* s, const double* approx, const double* target, uint64_t n,
                      const double* sample, uint64_t n_sample, const cbh_tree_sampling* sampling,
-                     cbh_tree_out* out) {
+                     const cbh_family* family, cbh_tree_out* out) {
     if (!s) return fail(CBH_ERR_INVALID_ARG, "session is null");
+    if (family && !s->ranking) return fail(CBH_ERR_INVALID_ARG, "a family descriptor is given to a pointwise session");
+    if (s->pairwise && (n_sample != 0 || (sampling && sampling->kind != CBH_BOOT_NO)))
+        return fail(CBH_ERR_UNSUPPORTED, "PairLogitPairwise scores unsampled derivatives (no bootstrap)");
+    if (s->ranking) {
+        if (n != s->n) return fail(CBH_ERR_LENGTH_MISMATCH, "n differs from the session's row count");
+        if (family) CHECK(upload_pairs(s, family));
+        if (!s->pairs_set) return fail(CBH_ERR_INVALID_ARG, "a pair loss needs the pairs (family) on its first grow");
+    }
     if (!out || !out->split_feature || !out->split_bin || !out->leaf_values)
         return fail(CBH_ERR_INVALID_ARG, "tree output buffers are null");
     if (n != s->n) return fail(CBH_ERR_LENGTH_MISMATCH, "n differs from the session's row count");
@@ -616,7 +817,8 @@ int cbh_session_read_approx(cbh_session* s, double* approx_out, uint64_t n_times
             constexpr int K = decltype(kc)::value;
             prepare_kernel<K><<<grid_for(s->n, 256, kPrepBlocks), 256, 0, s->stream>>>(
                 s->n, s->cfg.loss == CBH_LOSS_RMSE ? 0 : 1, s->approx, s->target, s->weight, s->leaf,
-                s->leaf_scaled, SampleParams{}, s->jt(), nullptr, s->sstat, 0, s->partials);
+                s->leaf_scaled, SampleParams{}, s->jt(), nullptr, s->sstat, 0, s->partials, nullptr,
+                nullptr);
             HIP_TRY(hipGetLastError());
             return CBH_OK;
         });

@@ -34,7 +34,14 @@ extern "C" {
 #define CBH_ERR_DEVICE (-6)          /* HIP runtime / allocation failure */
 
 /* ---- enums (cb-compute Loss / EScoreFunction / ELeavesEstimation / bootstrap) ---- */
-enum { CBH_LOSS_RMSE = 0, CBH_LOSS_LOGLOSS = 1, CBH_LOSS_MULTICLASS = 2, CBH_LOSS_CROSSENTROPY = 3 };
+enum {
+    CBH_LOSS_RMSE = 0,
+    CBH_LOSS_LOGLOSS = 1,
+    CBH_LOSS_MULTICLASS = 2,
+    CBH_LOSS_CROSSENTROPY = 3,
+    CBH_LOSS_PAIRLOGIT = 4,          /* pointwise scoring over pairwise weights */
+    CBH_LOSS_PAIRLOGIT_PAIRWISE = 5  /* pairwise split scoring + Cholesky leaves */
+};
 enum { CBH_SCORE_COSINE = 0, CBH_SCORE_L2 = 1 };
 enum { CBH_LEAF_GRADIENT = 0, CBH_LEAF_NEWTON = 1, CBH_LEAF_SIMPLE = 2 };
 enum { CBH_BOOT_NO = 0, CBH_BOOT_BAYESIAN = 1, CBH_BOOT_BERNOULLI = 2 };
@@ -64,6 +71,9 @@ typedef struct {
      * use bin > b for b < real_folds[f]-1.  NULL real_folds: every feature has n_bins. */
     const uint8_t* one_hot_flags;
     const uint32_t* real_folds;
+    /* PairLogitPairwise: the bucket-weight prior of the pairwise leaf system
+     * (bayesian_matrix_reg, 0.1 by default; boosting.rs:1785-1790) */
+    double pairwise_non_diag_reg;
 } cbh_config;
 
 typedef struct cbh_session cbh_session;
@@ -96,6 +106,23 @@ typedef struct {
     uint64_t bernoulli_state[4];
 } cbh_tree_sampling;
 
+/* Per-tree family descriptor; mirrors FamilyTreeArgs::Pairwise (runtime.rs:913-934).
+ * Required on the first grow of a PairLogit / PairLogitPairwise session; NULL later keeps
+ * the resident pairs.  Rows of a query group are contiguous (group_offsets, CSR over row
+ * order, n_groups + 1 entries, [0] = 0, [n_groups] = n); pairs are (winner, loser, weight)
+ * inside one group, in any order (the session orders them as the reference's competitor
+ * lists: stable by winner).  pair_weight NULL = weight 1 (query_info.rs:236-239). */
+enum { CBH_FAMILY_PAIRWISE = 1 };
+typedef struct {
+    int32_t kind;                 /* CBH_FAMILY_PAIRWISE */
+    uint32_t n_groups;
+    const uint32_t* group_offsets;
+    const uint32_t* pair_winner;
+    const uint32_t* pair_loser;
+    const double* pair_weight;
+    uint64_t n_pairs;
+} cbh_family;
+
 /* Output of one grown tree; mirrors DeviceGrownTree (runtime.rs:990-1059).  Buffers are
  * caller-owned and sized by the caller: split_* [depth], leaf_values [2^depth * K]
  * (row-major leaf x dim, UNscaled by the learning rate), leaf_of [n] or NULL. */
@@ -115,11 +142,12 @@ typedef struct {
  *   sample   NULL/0, or the host multiplier control ? weight : 0 of length n (session
  *            opened with sample_from_host)
  *   sampling NULL, or device-resident sampling parameters for this tree
+ *   family   NULL, or the pairs of a pair loss (see cbh_family)
  * The session applies approx += learning_rate * leaf_value[leaf_of] itself before the
  * next tree (the resident update of the reference's device branch). */
 int cbh_session_grow(cbh_session* s, const double* approx, const double* target, uint64_t n,
                      const double* sample, uint64_t n_sample, const cbh_tree_sampling* sampling,
-                     cbh_tree_out* out);
+                     const cbh_family* family, cbh_tree_out* out);
 
 /* Copy the resident approximant ([K][n]) to the host (applies any pending tree). */
 int cbh_session_read_approx(cbh_session* s, double* approx_out, uint64_t n_times_k);

@@ -35,6 +35,7 @@ typedef struct {
     float bagging_temperature;
     float pad_;
     uint64_t random_seed;
+    double pairwise_non_diag_reg; /* PairLogitPairwise leaf prior (0.1 by default) */
 } cbt_params;
 
 typedef struct cbt_trainer cbt_trainer;
@@ -43,6 +44,12 @@ typedef struct cbt_trainer cbt_trainer;
 int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t n_features,
              uint32_t n_bins, const uint32_t* real_folds, const uint8_t* one_hot_flags,
              const double* target, const double* weight, cbt_trainer** out);
+
+/* PairLogit / PairLogitPairwise: the query groups and explicit pairs of the pool (copied;
+ * call once after cbt_open, before the first cbt_step).  See cbh_family. */
+int cbt_set_pairs(cbt_trainer* t, const uint32_t* group_offsets, uint32_t n_groups,
+                  const uint32_t* pair_winner, const uint32_t* pair_loser, const double* pair_weight,
+                  uint64_t n_pairs);
 
 /* One boosting iteration.  Outputs (nullable): split_feature/split_bin/split_one_hot
  * [depth]; leaf_values [K][2^depth] as stored in the model (learning-rate scaled). */

@@ -276,3 +276,96 @@ def test_one_hot_boosting_matches_oracle(loss, score):
         perm = np.arange(leaves.shape[2]) ^ flip
         _close(leaves[t, 0][perm], exp["leaf_values"][t, 0])
     _close(approx, exp["approx"])
+
+
+# ----------------------------------------------------------------------------- pair losses
+RANKING = {"PairLogit": (3.0, "Newton"), "PairLogitPairwise": (5.0, "Gradient")}
+
+
+def _group_offsets(group_id):
+    _, counts = np.unique(group_id, return_counts=True)
+    return np.concatenate([[0], np.cumsum(counts)]).astype(np.uint32)
+
+
+@pytest.mark.parametrize("loss", sorted(RANKING))
+def test_ranking_upstream_fits_on_gpu(loss):
+    """catboost 1.2.10 PairLogit / PairLogitPairwise fits (12-document ranking corpus) on the
+    device: same splits every tree, leaf values and staged approximants to 1e-5."""
+    u = G.ranking(loss)
+    l2, leaf = RANKING[loss]
+    cfg = u["config"]
+    bins = np.stack([O.quantize(u["X"][:, j].astype(np.float32), u["borders"][j])
+                     for j in range(u["X"].shape[1])])
+    nb = u["n_borders"]
+    T, n = cfg["iterations"], u["X"].shape[0]
+    tr = cb.Trainer(bins, max(2, int(nb.max()) + 1), u["y"], loss=loss, depth=cfg["depth"],
+                    learning_rate=cfg["learning_rate"], l2_leaf_reg=l2, score="Cosine",
+                    leaf_method=leaf, bootstrap_type="No", real_folds=nb + 1,
+                    pairs=(u["pairs"][:, 0], u["pairs"][:, 1]),
+                    group_offsets=_group_offsets(u["group_id"]))
+    try:
+        approx = []
+        for t in range(T):
+            s, lv, _ = tr.step()
+            got = [(int(f), u["borders"][f][b]) for f, b in s]
+            exp = list(zip(u["split_feature"][t].tolist(), u["split_border"][t].tolist()))
+            assert got == exp, f"tree {t}"
+            _close(lv[0], u["leaf_values"][t])
+            approx.append(tr.approx()[0])
+    finally:
+        tr.close()
+    _close(np.array(approx), u["staged"].reshape(T, n))
+
+
+def _ranking_pool(seed, n_groups, gsize, pairs_per_group, F, max_borders):
+    g = np.random.default_rng(seed)
+    n = n_groups * gsize
+    nb = g.integers(2, max_borders + 1, size=F).astype(np.uint32)
+    bins = np.stack([g.integers(0, b + 1, size=n) for b in nb]).astype(np.uint8)
+    rel = np.clip((bins[0].astype(float) / nb[0] * 3 + bins[1].astype(float) / nb[1] * 2
+                   + g.normal(size=n)).round(), 0, 4)
+    win, los = [], []
+    for q in range(n_groups):
+        base = q * gsize
+        r = rel[base:base + gsize]
+        cand = [(i, j) for i in range(gsize) for j in range(gsize) if r[i] > r[j]]
+        if not cand:
+            continue
+        pick = g.choice(len(cand), size=min(pairs_per_group, len(cand)), replace=False)
+        for k in pick:
+            win.append(base + cand[k][0])
+            los.append(base + cand[k][1])
+    go = np.arange(0, n + 1, gsize, dtype=np.uint32)
+    return bins, nb, rel, np.array(win, np.uint32), np.array(los, np.uint32), go
+
+
+RANK_CASES = [
+    dict(loss="PairLogit", leaf_method="Newton", score="Cosine", bootstrap_type="No", depth=6),
+    dict(loss="PairLogit", leaf_method="Gradient", score="L2", bootstrap_type="Bernoulli", depth=5),
+    dict(loss="PairLogitPairwise", leaf_method="Gradient", score="Cosine", bootstrap_type="No", depth=4),
+    dict(loss="PairLogitPairwise", leaf_method="Gradient", score="Cosine", bootstrap_type="No", depth=6),
+]
+
+
+@pytest.mark.parametrize("case", range(len(RANK_CASES)))
+def test_ranking_boosting_matches_oracle(case):
+    p = dict(RANK_CASES[case])
+    depth = p.pop("depth")
+    pairwise = p["loss"] == "PairLogitPairwise"
+    bins, nb, rel, win, los, go = _ranking_pool(40 + case, 150 if pairwise else 600, 20, 10, 9, 40)
+    wt = np.random.default_rng(case).uniform(0.5, 2.0, size=win.shape[0]) if case == 1 else None
+    iters, l2 = 6, 3.0
+    exp = O.train(bins, nb, rel, depth=depth, iterations=iters, learning_rate=0.3, l2_leaf_reg=l2,
+                  random_seed=7, subsample=0.7, pairs=(win, los, wt), **p)
+    tr = cb.Trainer(bins, int(nb.max()) + 1, rel, depth=depth, learning_rate=0.3, l2_leaf_reg=l2,
+                    random_seed=7, subsample=0.7, real_folds=nb + 1, pairs=(win, los, wt),
+                    group_offsets=go, **p)
+    try:
+        splits, leaves = tr.fit(iters)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    for it in range(iters):
+        assert np.array_equal(splits[it], exp["splits"][it]), f"tree {it} splits differ"
+        _close(leaves[it], exp["leaf_values"][it])
+    _close(approx, exp["approx"])
