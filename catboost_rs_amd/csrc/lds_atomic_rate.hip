@@ -1,7 +1,8 @@
-// Measures the 64-bit LDS atomic-add rate of the GPU for the address patterns that bound
-// the histogram fill: scattered cells (the fill's pattern: every lane a random bin) and
-// contiguous cells (64 lanes on 64 neighbouring cells, the best case).  One 1024-thread
-// workgroup per CU-slot, 128 KB of LDS, every address masked into the array.
+// Measures the LDS atomic-add rate of the GPU for the address patterns that bound the
+// histogram fill: scattered cells (the fill's pattern: every lane a random bin) and
+// contiguous cells (64 lanes on 64 neighbouring cells, the best case), for 64-bit cells
+// (the fill's) and 32-bit cells with and without a returned value.  Two 1024-thread
+// workgroups per CU, 128 KB of LDS each, every address reduced into the array.
 // Prints one line per pattern: "<pattern> <lane-atomics per second>".
 #include <hip/hip_runtime.h>
 
@@ -29,39 +30,44 @@ __device__ __forceinline__ uint32_t mix32(uint32_t x) {
     return x;
 }
 
-template <int kScattered>
+// T: cell type (u64 or u32); kRtn: use the returned old value (an atomic with return).
+template <int kScattered, typename T, int kRtn>
 __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uint32_t seed) {
-    extern __shared__ unsigned long long cells[];
-    for (int i = threadIdx.x; i < kCells; i += blockDim.x) cells[i] = 0;
+    extern __shared__ unsigned long long cells_raw[];
+    T* cells = (T*)cells_raw;
+    constexpr uint32_t n_cells = kCells * 8 / sizeof(T);
+    for (uint32_t i = threadIdx.x; i < n_cells; i += blockDim.x) cells[i] = 0;
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t h = mix32(threadIdx.x * 7919u + blockIdx.x * 104729u + seed);
+    T carry = 0;
     for (int it = 0; it < kIters; ++it) {
         uint32_t idx;
         if (kScattered) {
             h = mix32(h + (uint32_t)it);
-            idx = h % kCells;
+            idx = h % n_cells;
         } else {
-            idx = ((uint32_t)it * 64u + lane) % kCells;
+            idx = ((uint32_t)it * 64u + lane) % n_cells;
         }
-        atomicAdd(&cells[idx], 1ull);
+        if (kRtn) carry += atomicAdd(&cells[idx], (T)1) >> 31;
+        else atomicAdd(&cells[idx], (T)1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) out[blockIdx.x] = cells[0];
+    if (threadIdx.x == 0) out[blockIdx.x] = (unsigned long long)cells[0] + (unsigned long long)carry;
 }
 
-template <int kScattered>
+template <int kScattered, typename T, int kRtn>
 int measure(const char* name, int blocks, unsigned long long* d) {
-    CK(hipFuncSetAttribute((const void*)rate_kernel<kScattered>,
+    CK(hipFuncSetAttribute((const void*)rate_kernel<kScattered, T, kRtn>,
                            hipFuncAttributeMaxDynamicSharedMemorySize, kCells * 8));
-    rate_kernel<kScattered><<<blocks, 1024, kCells * 8>>>(d, 1u);
+    rate_kernel<kScattered, T, kRtn><<<blocks, 1024, kCells * 8>>>(d, 1u);
     CK(hipGetLastError());
     CK(hipDeviceSynchronize());
     hipEvent_t a, b;
     CK(hipEventCreate(&a));
     CK(hipEventCreate(&b));
     CK(hipEventRecord(a));
-    rate_kernel<kScattered><<<blocks, 1024, kCells * 8>>>(d, 2u);
+    rate_kernel<kScattered, T, kRtn><<<blocks, 1024, kCells * 8>>>(d, 2u);
     CK(hipEventRecord(b));
     CK(hipEventSynchronize(b));
     float ms = 0.f;
@@ -78,8 +84,11 @@ int main() {
     unsigned long long* d = nullptr;
     const int blocks = 2 * cus;
     CK(hipMalloc(&d, sizeof(unsigned long long) * blocks));
-    if (measure<1>("scattered_u64", blocks, d)) return 1;
-    if (measure<0>("contiguous_u64", blocks, d)) return 1;
+    if (measure<1, unsigned long long, 0>("scattered_u64", blocks, d)) return 1;
+    if (measure<0, unsigned long long, 0>("contiguous_u64", blocks, d)) return 1;
+    if (measure<1, unsigned int, 0>("scattered_u32", blocks, d)) return 1;
+    if (measure<1, unsigned int, 1>("scattered_u32_rtn", blocks, d)) return 1;
+    if (measure<0, unsigned int, 0>("contiguous_u32", blocks, d)) return 1;
     CK(hipFree(d));
     return 0;
 }

@@ -109,6 +109,50 @@ def config2(scale=1.0, seed=1, n_rows=None, n_features=200):
                             boost_from_average=False, random_seed=0))
 
 
+def config3(scale=1.0, seed=3, n_rows=None, n_features=100, group_size=20, pairs_per_group=10,
+            loss="PairLogit"):
+    """Pairwise ranking: n docs in query groups of 20, n x 100 N(0,1); 254 borders; relevance
+    0..4 from a quantized noisy linear score of the first 10 features; about 10 random
+    winner > loser pairs per group (pairs whose relevance differs); depth 6, 100 iterations."""
+    n = int(n_rows if n_rows is not None else 1_000_000 * scale) // group_size * group_size
+    F = n_features
+
+    def make_col(f):
+        return np.random.default_rng([seed, f]).standard_normal(n, dtype=np.float32)
+
+    bins, nb, cols = _columns(n, F, make_col, 254, seed, keep_cols=range(min(10, F)))
+    g = np.random.default_rng([seed, 77_777])
+    w = g.uniform(-1, 1, min(10, F))
+    score = np.zeros(n)
+    for f in range(min(10, F)):
+        score += cols[f].astype(np.float64) * w[f]
+    score += 0.5 * g.standard_normal(n)
+    rel = np.digitize(score, np.quantile(score, [0.2, 0.4, 0.6, 0.8])).astype(np.float64)
+    del cols
+    G = n // group_size
+    # candidate pairs: 4x the target count per group, keep those with rel_i > rel_j (or the
+    # swapped pair when rel_j > rel_i), first pairs_per_group of them
+    c = 4 * pairs_per_group
+    i = g.integers(0, group_size, size=(G, c))
+    j = g.integers(0, group_size, size=(G, c))
+    base = (np.arange(G) * group_size)[:, None]
+    ri, rj = rel[base + i], rel[base + j]
+    win = np.where(ri > rj, i, j)
+    los = np.where(ri > rj, j, i)
+    ok = ri != rj
+    rank = np.cumsum(ok, axis=1)
+    keep = ok & (rank <= pairs_per_group)
+    winner = (base + win)[keep].astype(np.uint32)
+    loser = (base + los)[keep].astype(np.uint32)
+    group_offsets = np.arange(0, n + 1, group_size, dtype=np.uint32)
+    return dict(name="config3", bins=bins, n_borders=nb, target=rel, pairs=(winner, loser),
+                group_offsets=group_offsets,
+                params=dict(loss=loss, depth=6, iterations=100, learning_rate=0.03,
+                            l2_leaf_reg=3.0, score="Cosine",
+                            leaf_method="Newton" if loss == "PairLogit" else "Gradient",
+                            bootstrap_type="No", boost_from_average=False))
+
+
 def config5(scale=1.0, seed=5, n_rows=None, n_features=4096, n_classes=10):
     """MultiClass K=10: n x 4096 sparse-ish (70% exact zeros, else N(0,1)); 64 borders;
     depth 8, 50 iterations, Newton leaves, no bootstrap.  Labels: argmax of 10 noisy

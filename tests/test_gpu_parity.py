@@ -369,3 +369,62 @@ def test_ranking_boosting_matches_oracle(case):
         assert np.array_equal(splits[it], exp["splits"][it]), f"tree {it} splits differ"
         _close(leaves[it], exp["leaf_values"][it])
     _close(approx, exp["approx"])
+
+
+# --------------------------------------------------------------- benchmark configs vs oracle
+def _fit_both(d, iters, n_threads=0, **over):
+    """The config's boosting on the device (C-ABI driver) and in the oracle."""
+    P = dict(d["params"])
+    P.update(over)
+    P.pop("iterations", None)
+    nb = d["n_borders"]
+    K = P.pop("approx_dim", 1)
+    common = dict(loss=P["loss"], depth=P["depth"], learning_rate=P["learning_rate"],
+                  l2_leaf_reg=P["l2_leaf_reg"], score=P["score"], leaf_method=P["leaf_method"],
+                  bootstrap_type=P["bootstrap_type"], boost_from_average=P["boost_from_average"],
+                  bagging_temperature=P.get("bagging_temperature", 1.0),
+                  subsample=P.get("subsample", 0.66), random_seed=P.get("random_seed", 0),
+                  approx_dim=K)
+    pairs = d.get("pairs")
+    exp = O.train(d["bins"], nb, d["target"], iterations=iters, n_threads=n_threads, pairs=pairs,
+                  **common)
+    tr = cb.Trainer(d["bins"], int(nb.max()) + 1, d["target"], real_folds=nb + 1, pairs=pairs,
+                    group_offsets=d.get("group_offsets"), **common)
+    try:
+        splits, leaves = tr.fit(iters)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    return exp, splits, leaves, approx
+
+
+def _assert_same_fit(exp, splits, leaves, approx):
+    for it in range(splits.shape[0]):
+        assert np.array_equal(splits[it], exp["splits"][it]), f"tree {it} splits differ"
+        _close(leaves[it], exp["leaf_values"][it])
+    _close(approx, exp["approx"])
+
+
+def test_config1_full_size_matches_oracle():
+    """Config 1 at its full size: RMSE, 100k x 50, 128 borders, depth 6, 100 trees."""
+    d = datagen.config1()
+    _assert_same_fit(*_fit_both(d, d["params"]["iterations"]))
+
+
+def test_config2_reduced_matches_oracle():
+    """Config 2 shape (Logloss, 200 features, 254 borders, depth 6, Bayesian T=1) at 200k rows."""
+    d = datagen.config2(n_rows=200_000)
+    _assert_same_fit(*_fit_both(d, 8))
+
+
+@pytest.mark.parametrize("loss", ["PairLogit", "PairLogitPairwise"])
+def test_config3_reduced_matches_oracle(loss):
+    """Config 3 shape (groups of 20, ~10 pairs per group, 100 features, 254 borders, depth 6)."""
+    d = datagen.config3(n_rows=20_000 if loss == "PairLogit" else 4_000, loss=loss)
+    _assert_same_fit(*_fit_both(d, 5))
+
+
+def test_config5_shape_matches_oracle():
+    """Config 5 shape (MultiClass K=10, depth 8, 70%-zero columns, 64 borders) at 20k x 256."""
+    d = datagen.config5(n_rows=20_000, n_features=256)
+    _assert_same_fit(*_fit_both(d, 4))
