@@ -1,60 +1,103 @@
-"""Benchmark of the MI355X oblivious-tree training path (headline config 2).
+"""Benchmark of the MI355X oblivious-tree training path.
 
-Workload: Logloss, 10M rows x 200 features (100 N(0,1) + 100 lognormal(0,1)), 254
-borders (u8 bins, 4 per u32 word), depth 6, Bayesian bootstrap T=1, synthetic seeded
-data.  A step is one boosting iteration (one tree) through the C-ABI
-(``cbt_step`` -> ``cbh_session_grow``); the bins, target and approximant are resident in
-HBM before the timed region starts.  Each step ends with a stream synchronisation (the
-tree is copied back), so wall time around the steps is the device time of the steps.
+Default workload (the headline metric): config 2 -- Logloss, 10M rows x 200 features
+(100 N(0,1) + 100 lognormal(0,1)), 254 borders (u8 bins, 4 per u32 word), depth 6,
+Bayesian bootstrap T=1, synthetic seeded data.  ``--config 1|3|5`` measures the other
+configs of the scope the same way (config 3 = PairLogit over query groups with pairs,
+``--pairwise`` for PairLogitPairwise; config 5 = MultiClass K=10, depth 8, 4096 features).
+
+A step is one boosting iteration (one tree) through the C-ABI (``cbt_step`` ->
+``cbh_session_grow``); the bins, target and approximant are resident in HBM before the
+timed region starts.  Each step ends with a stream synchronisation (the tree is copied
+back), so wall time around the steps is the device time of the steps.
 
 Reported next to the GPU figure:
   * roofline of the dominant kernel (histogram fill): algorithmic bytes per launch
     (V rows x (W*4 + 8*(K+1) + 4) + histogram bytes) / average launch time from HIP events
-    recorded on the session stream, against MI355X's 8 TB/s;
+    recorded on the session stream, against MI355X's 8 TB/s; HBM traffic per launch from
+    the copy-calibrated rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/;
+  * the fill's LDS-atomic rate against the measured scattered 64-bit LDS atomic cap;
   * cpu_baseline: the CPU restatement of the reference algorithm (oracle/) timed on the
-    host cores for a few trees of the same data.
+    host cores for the first trees of the same data, with a check that its splits equal
+    the GPU's.
 
-Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 3] [--rows N] [--cpu-trees 2]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--rows N]
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
+import subprocess
 import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-METRIC = ("histogram rows·features/s + HBM GB/s; boosting iters/s at 10M×200, depth 6")
+METRIC = "histogram rows·features/s + HBM GB/s; boosting iters/s at 10M×200, depth 6"
 HBM_PEAK_GBS = 8000.0
+DEFAULT_STEPS = {1: 100, 2: 200, 3: 100, 5: 20}
+DEFAULT_CPU_TREES = {1: 5, 2: 2, 3: 3, 5: 1}
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def _profiled_traffic(n, F):
+def _profiled_traffic(config, n, F):
     """HBM bytes per fill launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, copy-calibrated)
-    for this workload shape, read from the committed profile summary; None if absent."""
+    for the default workload shape, read from the committed profile summary; None if absent."""
     path = os.path.join(ROOT, "profiles", "fill_kernel_config2.md")
-    if n != 10_000_000 or F != 200 or not os.path.exists(path):
+    if config != 2 or n != 10_000_000 or F != 200 or not os.path.exists(path):
         return None
-    import re
-
     m = re.search(r"mean per dispatch: fetch ([0-9.]+) GB write ([0-9.]+) GB", open(path).read())
     return round((float(m.group(1)) + float(m.group(2))) * 1e9) if m else None
+
+
+def _lds_rates():
+    probe = os.path.join(ROOT, "catboost_rs_amd", "lds_atomic_rate")
+    if not os.path.exists(probe):
+        return {}
+    r = subprocess.run([probe], capture_output=True, text=True, timeout=120)
+    return dict((l.split()[0], float(l.split()[1])) for l in r.stdout.splitlines() if len(l.split()) == 2)
+
+
+def _workload(args):
+    from catboost_rs_amd import datagen
+
+    if args.config == 1:
+        return datagen.config1(scale=args.rows / 100_000 if args.rows else 1.0)
+    if args.config == 2:
+        return datagen.config2(n_rows=args.rows or 10_000_000, n_features=args.features or 200)
+    if args.config == 3:
+        return datagen.config3(n_rows=args.rows or 1_000_000, n_features=args.features or 100,
+                               loss="PairLogitPairwise" if args.pairwise else "PairLogit")
+    if args.config == 5:
+        return datagen.config5(n_rows=args.rows or 1_000_000, n_features=args.features or 4096)
+    raise SystemExit(f"--config {args.config}: configs 1, 2, 3 and 5 are measured (config 4 needs "
+                     "categorical CTR inputs, not built)")
+
+
+def _train_kwargs(P):
+    return dict(loss=P["loss"], depth=P["depth"], learning_rate=P["learning_rate"],
+                l2_leaf_reg=P["l2_leaf_reg"], score=P["score"], leaf_method=P["leaf_method"],
+                bootstrap_type=P["bootstrap_type"], bagging_temperature=P.get("bagging_temperature", 1.0),
+                subsample=P.get("subsample", 0.66), boost_from_average=P["boost_from_average"],
+                random_seed=P.get("random_seed", 0), approx_dim=P.get("approx_dim", 1))
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--pairwise", action="store_true", help="config 3 with PairLogitPairwise")
+    ap.add_argument("--steps", type=int, default=0)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--rows", type=int, default=10_000_000)
-    ap.add_argument("--features", type=int, default=200)
-    ap.add_argument("--cpu-trees", type=int, default=2)
+    ap.add_argument("--rows", type=int, default=0)
+    ap.add_argument("--features", type=int, default=0)
+    ap.add_argument("--cpu-trees", type=int, default=-1)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib", type=int, default=0,
@@ -72,121 +115,112 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
-              "row-parallel (integer histogram all-reduce) design is not built in this library.", file=sys.stderr)
+              "row-parallel (integer histogram all-reduce) design is not built in this library.",
+              file=sys.stderr)
         sys.exit(2)
+    steps = args.steps or DEFAULT_STEPS.get(args.config, 50)
+    cpu_trees = args.cpu_trees if args.cpu_trees >= 0 else DEFAULT_CPU_TREES.get(args.config, 1)
 
     import numpy as np
 
     import catboost_rs_amd as cb
-    from catboost_rs_amd import datagen
 
     cb.load()
     t0 = time.perf_counter()
-    data = datagen.config2(n_rows=args.rows, n_features=args.features)
+    data = _workload(args)
     bins, nb, y = data["bins"], data["n_borders"], data["target"]
     P = data["params"]
     F, n = bins.shape
     n_bins = int(nb.max()) + 1
-    log(f"data: {n} x {F}, max borders {int(nb.max())}, generated in {time.perf_counter() - t0:.1f}s")
+    kw = _train_kwargs(P)
+    pairs, go = data.get("pairs"), data.get("group_offsets")
+    log(f"data: config {args.config} {P['loss']}: {n} x {F}, max borders {int(nb.max())}"
+        + (f", {len(pairs[0])} pairs" if pairs is not None else "")
+        + f", generated in {time.perf_counter() - t0:.1f}s")
 
     t0 = time.perf_counter()
-    tr = cb.Trainer(bins, n_bins, y, loss=P["loss"], depth=P["depth"], learning_rate=P["learning_rate"],
-                    l2_leaf_reg=P["l2_leaf_reg"], score=P["score"], leaf_method=P["leaf_method"],
-                    bootstrap_type=P["bootstrap_type"], bagging_temperature=P["bagging_temperature"],
-                    boost_from_average=P["boost_from_average"], random_seed=P["random_seed"],
-                    real_folds=nb + 1, profile=True)
+    tr = cb.Trainer(bins, n_bins, y, real_folds=nb + 1, profile=True, pairs=pairs, group_offsets=go, **kw)
     log(f"session open (upload + pack) {time.perf_counter() - t0:.2f}s")
     for _ in range(args.warmup):
         tr.step()
     tr.reset_stats()
     t0 = time.perf_counter()
-    gpu_splits = []
-    for _ in range(args.steps):
-        s, _, _ = tr.step()
-        gpu_splits.append(s)
+    for _ in range(steps):
+        tr.step()
     wall = time.perf_counter() - t0
     st = tr.stats()
     tr.close()
-    iters_per_s = args.steps / wall
-    ms_per_step = 1000.0 * wall / args.steps
+    iters_per_s = steps / wall
+    ms_per_step = 1000.0 * wall / steps
     fill_s = st["fill_ms"] / 1000.0
     achieved = st["fill_bytes"] / 1e9 / fill_s if fill_s > 0 else 0.0
+    stages = ("fill_ms", "derive_ms", "score_ms", "partition_ms", "leaf_ms", "prepare_ms")
     log(f"gpu: {iters_per_s:.2f} iters/s, {ms_per_step:.3f} ms/tree; stage ms/tree: " +
-        ", ".join(f"{k[:-3]} {st[k] / args.steps:.3f}" for k in
-                  ("fill_ms", "derive_ms", "score_ms", "partition_ms", "leaf_ms", "prepare_ms")))
+        ", ".join(f"{k[:-3]} {st[k] / steps:.3f}" for k in stages))
     log(f"fill: {st['fill_launches']} launches, avg {st['fill_ms'] / max(1, st['fill_launches']):.4f} ms, "
         f"{achieved:.1f} GB/s algorithmic")
 
     # LDS-atomic roofline of the fill: every visited (row, feature) adds K+1 64-bit integer
     # cells; the cap is the scattered 64-bit LDS atomic rate measured on this GPU
+    K = kw["approx_dim"] if P["loss"] == "MultiClass" else 1
     lds = None
-    lane_atomics = st["fill_row_features"] * 2
-    probe = os.path.join(ROOT, "catboost_rs_amd", "lds_atomic_rate")
-    if os.path.exists(probe):
-        import subprocess
-
-        r = subprocess.run([probe], capture_output=True, text=True, timeout=120)
-        rates = dict((l.split()[0], float(l.split()[1])) for l in r.stdout.splitlines() if len(l.split()) == 2)
-        if "scattered_u64" in rates and fill_s > 0:
-            ach = lane_atomics / fill_s
-            lds = {"achieved_lane_atomics_per_s": round(ach, 1),
-                   "cap_scattered_u64_per_s": rates["scattered_u64"],
-                   "cap_contiguous_u64_per_s": rates.get("contiguous_u64"),
-                   "frac_of_scattered_cap": round(ach / rates["scattered_u64"], 4)}
-            log(f"fill LDS atomics: {ach:.3e}/s = {100 * ach / rates['scattered_u64']:.1f}% of the "
-                f"measured scattered-u64 cap {rates['scattered_u64']:.3e}/s")
-    traffic = _profiled_traffic(n, F)
+    rates = _lds_rates()
+    if "scattered_u64" in rates and fill_s > 0:
+        ach = st["fill_row_features"] * (K + 1) / fill_s
+        # with a dominant-bin skip (sparse columns) fewer atomics are issued than counted
+        lds = {"achieved_lane_atomics_per_s": round(ach, 1),
+               "counted_as": "all (row, feature) pairs" if not st["skip_features"] else
+               f"all (row, feature) pairs; {st['skip_features']} of {F} features skip their dominant bin",
+               "cap_scattered_u64_per_s": rates["scattered_u64"],
+               "cap_contiguous_u64_per_s": rates.get("contiguous_u64"),
+               "frac_of_scattered_cap": round(ach / rates["scattered_u64"], 4)}
+        log(f"fill LDS atomics: {ach:.3e}/s = {100 * ach / rates['scattered_u64']:.1f}% of the "
+            f"measured scattered-u64 cap {rates['scattered_u64']:.3e}/s")
 
     cpu = None
-    if not args.no_cpu and args.cpu_trees > 0:
+    if not args.no_cpu and cpu_trees > 0:
         from oracle import oracle as O
 
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         t0 = time.perf_counter()
-        exp = O.train(bins, nb, y, loss=P["loss"], depth=P["depth"], iterations=args.cpu_trees,
-                      learning_rate=P["learning_rate"], l2_leaf_reg=P["l2_leaf_reg"], score=P["score"],
-                      leaf_method=P["leaf_method"], bootstrap_type=P["bootstrap_type"],
-                      bagging_temperature=P["bagging_temperature"],
-                      boost_from_average=P["boost_from_average"], random_seed=P["random_seed"],
-                      n_threads=threads)
+        exp = O.train(bins, nb, y, iterations=cpu_trees, n_threads=threads, pairs=pairs, **kw)
         cpu_wall = time.perf_counter() - t0
-        cpu = {"value": round(args.cpu_trees / cpu_wall, 6), "unit": "iters/s", "cores": threads,
+        cpu = {"value": round(cpu_trees / cpu_wall, 6), "unit": "iters/s", "cores": threads,
                "kind": "port",
-               "sample": f"first {args.cpu_trees} trees of the same {n}x{F} workload "
+               "sample": f"first {cpu_trees} trees of the same {n}x{F} workload "
                          f"(CPU restatement of the reference algorithm, OpenMP over features)"}
-        log(f"cpu: {args.cpu_trees} trees in {cpu_wall:.1f}s on {threads} threads")
+        log(f"cpu: {cpu_trees} trees in {cpu_wall:.1f}s on {threads} threads")
         # the CPU trees must be the GPU run's first trees (parity on the full-size workload)
-        tr2 = cb.Trainer(bins, n_bins, y, loss=P["loss"], depth=P["depth"], learning_rate=P["learning_rate"],
-                         l2_leaf_reg=P["l2_leaf_reg"], score=P["score"], leaf_method=P["leaf_method"],
-                         bootstrap_type=P["bootstrap_type"], bagging_temperature=P["bagging_temperature"],
-                         boost_from_average=P["boost_from_average"], random_seed=P["random_seed"],
-                         real_folds=nb + 1)
-        first, _ = tr2.fit(args.cpu_trees)
+        tr2 = cb.Trainer(bins, n_bins, y, real_folds=nb + 1, pairs=pairs, group_offsets=go, **kw)
+        first, _ = tr2.fit(cpu_trees)
         tr2.close()
         cpu["splits_match_gpu"] = bool(np.array_equal(first, exp["splits"]))
 
+    names = {1: "config1: RMSE, no bootstrap, depth 6, 128 borders",
+             2: "config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 borders",
+             3: f"config3: {P['loss']}, groups of 20, ~10 pairs per group, depth 6, 254 borders",
+             5: "config5: MultiClass K=10, depth 8, 64 borders, 70% zeros"}
     out = {
         "metric": METRIC,
         "value": round(iters_per_s, 4),
         "unit": "iters/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u8 bins, int64 fixed-point sums, f64 scores",
-        "data": "synthetic (seeded; datagen.config2)",
-        "config": {"workload": "config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 borders",
-                   "rows": n, "features": F, "depth": P["depth"], "parallelism": "single GPU"},
+        "data": f"synthetic (seeded; datagen.config{args.config})",
+        "config": {"workload": names[args.config], "rows": n, "features": F, "depth": P["depth"],
+                   "parallelism": "single GPU"},
         "hist_rows_features_per_s": round(st["fill_row_features"] / fill_s, 1) if fill_s else None,
-        "hist_rows_features_per_s_logical": round(n * F * P["depth"] * args.steps / fill_s, 1) if fill_s else None,
-        "stage_ms_per_tree": {k[:-3]: round(st[k] / args.steps, 4) for k in
-                              ("fill_ms", "derive_ms", "score_ms", "partition_ms", "leaf_ms", "prepare_ms")},
+        "hist_rows_features_per_s_logical": round(n * F * P["depth"] * steps / fill_s, 1) if fill_s else None,
+        "stage_ms_per_tree": {k[:-3]: round(st[k] / steps, 4) for k in stages},
         "roofline": {"bound": "hbm", "kernel": "fill_kernel", "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic,
+                     "traffic": _profiled_traffic(args.config, n, F),
                      "launches": st["fill_launches"],
                      "avg_launch_ms": round(st["fill_ms"] / max(1, st["fill_launches"]), 5),
                      "algorithmic_bytes_per_launch": round(st["fill_bytes"] / max(1, st["fill_launches"]))},

@@ -109,7 +109,7 @@ int run_fill(const uint32_t* rows, uint32_t W, uint64_t n, const uint32_t* idx,
     const uint32_t G = 64;
     fill_kernel<C><<<G * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, n, idx, plan,
                                                              (const long long*)sstat, ft.n_tiles, ft.tw,
-                                                             F, B, G, hist);
+                                                             F, B, G, hist, nullptr);
     HIP_OK(hipGetLastError());
     return CBH_OK;
 }

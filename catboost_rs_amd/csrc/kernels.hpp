@@ -354,7 +354,8 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
                                            const long long* __restrict__ sfix, uint32_t beg,
                                            uint32_t end, uint32_t w0, uint32_t TW, uint32_t nf,
                                            uint32_t B, uint32_t plane,
-                                           unsigned long long* __restrict__ lbase) {
+                                           unsigned long long* __restrict__ lbase,
+                                           const uint32_t (&skip)[4]) {
     constexpr int U = kFillRows;
     const uint32_t rows_per_pass = blockDim.x / TW;
     const uint32_t r0 = threadIdx.x / TW;
@@ -392,6 +393,7 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
             for (int k = 0; k < 4; ++k) {
                 if ((uint32_t)k < nf) {
                     const uint32_t bin = (word[u] >> (8 * k)) & 0xFFu;
+                    if (bin == skip[k]) continue;   // dominant bin: rebuilt from the totals
                     unsigned long long* cell = lbase + (uint32_t)k * B + bin;
 #pragma unroll
                     for (int ch = 0; ch < C; ++ch)
@@ -407,7 +409,8 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t* __restrict__ rows, uint32_t W, uint64_t n,
     const uint32_t* __restrict__ idx,                  // null: dense rows [0, n), leaf 0
     const LevelPlan* __restrict__ plan, const long long* __restrict__ sfix, uint32_t n_tiles,
-    uint32_t tw, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist) {
+    uint32_t tw, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
+    const uint32_t* __restrict__ skip_bin /* nullable [F]: dominant bin left out, or >= B */) {
     extern __shared__ long long lds[];
     const uint32_t b = blockIdx.x;
     const uint32_t xcd = b & 7u, q = b >> 3;
@@ -425,6 +428,9 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t wl = threadIdx.x - r0 * TW;
     unsigned long long* lbase = (unsigned long long*)lds + 4u * wl * B;
     const uint32_t nf = min(4u, TF - min(TF, 4u * wl));   // valid features of this lane's word
+    uint32_t skip[4] = {256u, 256u, 256u, 256u};
+    if (skip_bin)
+        for (uint32_t k = 0; k < nf; ++k) skip[k] = skip_bin[f0 + 4u * wl + k];
     const uint32_t V = idx ? plan->rows : (uint32_t)n;
     const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
     const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
@@ -438,7 +444,7 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = idx ? plan->built[seg] : 0u;
         if (end > pos) {
-            fill_range<C>(rows, W, idx, sfix, pos, end, w0, TW, nf, B, plane, lbase);
+            fill_range<C>(rows, W, idx, sfix, pos, end, w0, TW, nf, B, plane, lbase, skip);
             __syncthreads();
             // flush LDS [ch][f][bin] -> hist[leaf][ch][f0 + f][bin]: contiguous per plane
             for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) {
@@ -472,6 +478,90 @@ static __global__ void derive_kernel(const long long* __restrict__ parent, long 
         const uint32_t built = plan->built[p];
         const uint32_t other = built == p ? p + n_parent : p;
         cur[(size_t)other * per_leaf + j] = parent[t] - cur[(size_t)built * per_leaf + j];
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Dominant-bin skip.  A feature whose most frequent bin holds a large share of the rows
+// (sparse columns: 70% exact zeros put 70% of the rows in one bin) makes the fill's LDS
+// atomics collide on one cell.  The fill leaves that bin out; the per-segment channel totals
+// are summed apart (seg_totals_kernel) and the bin is rebuilt as total - sum(other bins),
+// exact in int64 (default_bin_fixup_kernel).
+// ---------------------------------------------------------------------------------
+constexpr int kMaxC = kMaxK + 1;
+
+// Per-feature bin counts over the feature-major columns (one workgroup per feature).
+static __global__ __launch_bounds__(256) void bin_census_kernel(const uint8_t* __restrict__ cols, uint64_t n,
+                                                                unsigned long long* __restrict__ counts) {
+    __shared__ unsigned int c[256];
+    c[threadIdx.x] = 0;
+    __syncthreads();
+    const uint8_t* col = cols + (size_t)blockIdx.x * n;
+    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&c[col[i]], 1u);
+    __syncthreads();
+    atomicAdd(counts + (size_t)blockIdx.x * 256 + threadIdx.x, (unsigned long long)c[threadIdx.x]);
+}
+
+// Channel totals of the rows of every directly built segment: tot [segment][C].
+static __global__ __launch_bounds__(256) void seg_totals_kernel(const uint32_t* __restrict__ idx,
+                                                                const LevelPlan* __restrict__ plan, uint64_t n,
+                                                                const long long* __restrict__ sfix, uint32_t C,
+                                                                long long* __restrict__ tot) {
+    __shared__ unsigned long long acc[(kMaxLeaves / 2) * kMaxC];
+    const uint32_t V = idx ? plan->rows : (uint32_t)n;
+    const uint32_t n_seg = idx ? plan->n_parent : 1u;
+    for (uint32_t i = threadIdx.x; i < n_seg * C; i += blockDim.x) acc[i] = 0;
+    __syncthreads();
+    // block-uniform loop; a wave whose rows all lie in one segment reduces in registers
+    for (uint32_t base = blockIdx.x * blockDim.x; base < V; base += gridDim.x * blockDim.x) {
+        const uint32_t p = base + threadIdx.x;
+        const bool act = p < V;
+        uint32_t seg = 0;
+        if (act && idx) {   // last segment whose begin <= p
+            uint32_t lo = 0, hi = n_seg - 1;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi + 1) >> 1;
+                if (plan->seg_begin[mid] <= p) lo = mid;
+                else hi = mid - 1;
+            }
+            seg = lo;
+        }
+        const long long* st = act ? sfix + (size_t)(idx ? idx[p] : p) * C : nullptr;
+        const uint32_t seg0 = __shfl(seg, 0, 64);
+        const bool uniform = __all(!act || seg == seg0);
+        for (uint32_t ch = 0; ch < C; ++ch) {
+            const long long v = act ? st[ch] : 0;
+            if (uniform) {
+                const unsigned long long u = wave_sum_u64((unsigned long long)v);
+                if (lane_id() == 0 && u != 0) atomicAdd(acc + seg0 * C + ch, u);
+            } else if (v != 0) {
+                atomicAdd(acc + seg * C + ch, (unsigned long long)v);
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n_seg * C; i += blockDim.x)
+        if (acc[i] != 0) atomicAdd((unsigned long long*)tot + i, acc[i]);
+}
+
+// hist[slot][ch][f][skip] = tot[segment][ch] - sum of the other bins.  Grid (F, segments).
+static __global__ __launch_bounds__(64) void default_bin_fixup_kernel(long long* __restrict__ hist,
+                                                                      const LevelPlan* __restrict__ plan,
+                                                                      const uint32_t* __restrict__ skip_bin,
+                                                                      const long long* __restrict__ tot,
+                                                                      uint32_t C, uint32_t F, uint32_t B) {
+    const uint32_t f = blockIdx.x, seg = blockIdx.y;
+    const uint32_t d = skip_bin[f];
+    if (d >= B) return;
+    if (plan && seg >= plan->n_parent) return;
+    const uint32_t slot = plan ? plan->built[seg] : 0u;
+    for (uint32_t ch = 0; ch < C; ++ch) {
+        long long* h = hist + (((size_t)slot * C + ch) * F + f) * B;
+        unsigned long long part = 0;
+        for (uint32_t b = threadIdx.x; b < B; b += 64)
+            if (b != d) part += (unsigned long long)h[b];
+        part = wave_sum_u64(part);
+        if (threadIdx.x == 0) h[d] = tot[(size_t)seg * C + ch] - (long long)part;
     }
 }
 

@@ -160,6 +160,12 @@ struct cbh_session {
     long long* dcum = nullptr;       // [F][B][Pmax]
     double* cand_scores = nullptr;   // [F][B]
     long long* leaf_w = nullptr;     // [L][L]
+
+    // dominant-bin skip of the fill (features whose most frequent bin holds >= 1/8 of rows)
+    uint32_t* skip_bin = nullptr;    // [F] dominant bin, or 256 (no skip)
+    long long* seg_tot = nullptr;    // [kMaxLeaves / 2][C] channel totals per built segment
+    bool use_skip = false;
+    uint64_t n_skip = 0;
     JumpTabs jt() const {
         return JumpTabs{jump, jump + 1024, jump + 2048, jump + 2048 + n_coarse};
     }
@@ -180,7 +186,7 @@ struct cbh_session {
         dfree(partials);
         dfree(group_off); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st); dfree(dcum);
-        dfree(cand_scores); dfree(leaf_w);
+        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot);
         for (auto& t : timers) {
             if (t.second.a) (void)hipEventDestroy(t.second.a);
             if (t.second.b) (void)hipEventDestroy(t.second.b);
@@ -347,6 +353,50 @@ int set_fill_attr(size_t lds) {
     return CBH_OK;
 }
 
+// Dominant bins: a device census of every column, then per feature the most frequent bin
+// if it holds at least 1/8 of the rows (the fill leaves it out and rebuilds it exactly).
+int plan_skip_bins(cbh_session* s) {
+    unsigned long long* cnt = nullptr;
+    CHECK(dalloc(&cnt, (size_t)s->F * 256));
+    std::vector<unsigned long long> h((size_t)s->F * 256);
+    int rc = CBH_OK;
+    do {
+        zero_i64_kernel<<<grid_for((size_t)s->F * 256, 256, 8192), 256, 0, s->stream>>>((long long*)cnt,
+                                                                                       (size_t)s->F * 256);
+        if (hipGetLastError() != hipSuccess) { rc = fail(CBH_ERR_DEVICE, "census zero launch failed"); break; }
+        bin_census_kernel<<<s->F, 256, 0, s->stream>>>(s->cols, s->n, cnt);
+        if (hipGetLastError() != hipSuccess) { rc = fail(CBH_ERR_DEVICE, "census launch failed"); break; }
+        if (hipMemcpyAsync(h.data(), cnt, sizeof(unsigned long long) * h.size(), hipMemcpyDeviceToHost,
+                           s->stream) != hipSuccess ||
+            hipStreamSynchronize(s->stream) != hipSuccess) {
+            rc = fail(CBH_ERR_DEVICE, "census copy failed");
+            break;
+        }
+    } while (false);
+    dfree(cnt);
+    if (rc != CBH_OK) return rc;
+    std::vector<uint32_t> skip(s->F, 256u);
+    bool any = false;
+    for (uint32_t f = 0; f < s->F; ++f) {
+        const unsigned long long* c = h.data() + (size_t)f * 256;
+        uint32_t best = 0;
+        for (uint32_t b = 1; b < s->B; ++b)
+            if (c[b] > c[best]) best = b;
+        if (c[best] * 8 >= s->n) {
+            skip[f] = best;
+            any = true;
+        }
+    }
+    s->use_skip = any;
+    s->n_skip = 0;
+    for (uint32_t v : skip) s->n_skip += v < 256u;
+    if (!any) return CBH_OK;
+    CHECK(dalloc(&s->skip_bin, s->F));
+    CHECK(dalloc(&s->seg_tot, (size_t)(kMaxLeaves / 2) * s->C));
+    HIP_TRY(hipMemcpy(s->skip_bin, skip.data(), sizeof(uint32_t) * s->F, hipMemcpyHostToDevice));
+    return CBH_OK;
+}
+
 template <typename BinT>
 int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double* weight,
                        uint64_t n, uint32_t F, uint32_t n_bins, double lr, double l2,
@@ -421,6 +471,7 @@ int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double*
     }
     pack_rows_kernel<<<grid_for((uint64_t)n * s->W, 256), 256, 0, s->stream>>>(s->cols, n, F, s->W, s->rows);
     HIP_TRY(hipGetLastError());
+    CHECK(plan_skip_bins(s.get()));
     if (weight) HIP_TRY(hipMemcpy(s->weight, weight, sizeof(double) * n, hipMemcpyHostToDevice));
     // resident approximant seeded with the bias (DeviceTrainConfig::bias, runtime.rs:1276)
     std::vector<double> a0(std::min<uint64_t>(n * s->K, 1ull << 22), cfg->bias);
@@ -600,11 +651,24 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         CHECK(s->stage_begin(kStFill));
         const uint32_t nt = s->tiles.n_tiles;
         const uint32_t G = s->fill_ranges;
+        const uint32_t* lidx = level == 0 ? nullptr : s->idx;
+        const LevelPlan* lplan = level == 0 ? nullptr : s->plans + (level - 1);
+        const uint32_t n_seg = level == 0 ? 1u : (1u << (level - 1));
+        if (s->use_skip) {
+            CHECK(launch_zero(s->seg_tot, (size_t)n_seg * C, st));
+            seg_totals_kernel<<<grid_for(n, 256, 1024), 256, 0, st>>>(lidx, lplan, n,
+                                                                     (const long long*)s->sstat, C, s->seg_tot);
+            HIP_TRY(hipGetLastError());
+        }
         fill_kernel<C><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
-            s->rows, s->W, n, level == 0 ? nullptr : s->idx,
-            level == 0 ? nullptr : s->plans + (level - 1), (const long long*)s->sstat, nt,
-            s->tiles.tw, s->F, s->B, G, cur);
+            s->rows, s->W, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
+            s->use_skip ? s->skip_bin : nullptr);
         HIP_TRY(hipGetLastError());
+        if (s->use_skip) {
+            default_bin_fixup_kernel<<<dim3(s->F, n_seg), 64, 0, st>>>(cur, lplan, s->skip_bin, s->seg_tot, C,
+                                                                      s->F, s->B);
+            HIP_TRY(hipGetLastError());
+        }
         CHECK(s->stage_end());
         // ---- derive the sibling of every directly built child ----
         if (level > 0) {
@@ -833,6 +897,7 @@ int cbh_session_read_approx(cbh_session* s, double* approx_out, uint64_t n_times
 int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
     if (!s || !out) return fail(CBH_ERR_INVALID_ARG, "null argument");
     *out = s->stats;
+    out->skip_features = s->n_skip;
     return CBH_OK;
 }
 

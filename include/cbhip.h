@@ -167,6 +167,7 @@ typedef struct {
     uint64_t fill_row_features;   /* sum of V * n_features */
     double fill_bytes;            /* algorithmic bytes V*(W*4 + 8*(K+1) + 4) + H */
     uint64_t trees;
+    uint64_t skip_features;       /* features whose dominant bin the fill leaves out */
 } cbh_stats;
 
 int cbh_session_stats(const cbh_session* s, cbh_stats* out);
