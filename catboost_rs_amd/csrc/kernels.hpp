@@ -62,6 +62,11 @@ __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v)
 // ---------------------------------------------------------------------------------
 // zero fill (graph-safe replacement for memset)
 // ---------------------------------------------------------------------------------
+static __global__ void zero_u32_kernel(uint32_t* __restrict__ p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
 static __global__ void zero_i64_kernel(long long* __restrict__ p, size_t n) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;

@@ -20,7 +20,7 @@
 namespace cbh {
 
 constexpr uint32_t kPairMaxParents = 32;   // pairwise scoring: 2P <= 64 unknowns (depth <= 6)
-constexpr uint32_t kPairChunk = 8192;      // pairs per workgroup of the statistics kernel
+constexpr uint32_t kPairChunk = 65536;     // pairs per workgroup of the LDS statistics kernel
 
 __device__ __forceinline__ uint32_t tri(uint32_t r, uint32_t c) {   // packed lower triangle
     return r >= c ? r * (r + 1) / 2 + c : c * (c + 1) / 2 + r;
@@ -118,6 +118,171 @@ static __global__ __launch_bounds__(256) void pair_stats_kernel(
     }
 }
 
+// ---- statistics with many parents (P >= 8): pairs grouped by their unordered leaf pair
+// {a, b}; one workgroup per (feature, leaf pair) owns the cells [a][b][*][*] and [b][a][*][*]
+// of that feature, accumulates them in LDS, takes the prefix over buckets and writes the
+// cumulative values (no zeroing, no global atomics, no separate scan).
+
+__device__ __forceinline__ uint32_t pair_key(uint32_t wl, uint32_t ll, uint32_t P) {
+    return wl < ll ? wl * P + ll : ll * P + wl;
+}
+
+// Count the pairs of every key (P*P keys, those with a > b stay 0).
+static __global__ __launch_bounds__(256) void pair_key_count_kernel(
+    const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los, uint64_t m,
+    const uint16_t* __restrict__ leaf, uint32_t P, uint32_t* __restrict__ cnt) {
+    __shared__ uint32_t c[kPairMaxParents * kPairMaxParents];
+    for (uint32_t i = threadIdx.x; i < P * P; i += blockDim.x) c[i] = 0;
+    __syncthreads();
+    for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < m;
+         k += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t wi = comp_win[k], lo = comp_los[k];
+        if (wi == lo) continue;
+        atomicAdd(&c[pair_key(leaf[wi] & 0x7FFFu, leaf[lo] & 0x7FFFu, P)], 1u);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < P * P; i += blockDim.x)
+        if (c[i]) atomicAdd(cnt + i, c[i]);
+}
+
+// Exclusive scan of the P*P key counts (one workgroup of 1024 threads): key_off[P*P + 1],
+// cursor = key_off[0 .. P*P).
+static __global__ __launch_bounds__(1024) void pair_key_scan_kernel(const uint32_t* __restrict__ cnt, uint32_t nk,
+                                                                    uint32_t* __restrict__ key_off,
+                                                                    uint32_t* __restrict__ cursor) {
+    __shared__ uint32_t sh[1024];
+    const uint32_t t = threadIdx.x;
+    const uint32_t v = t < nk ? cnt[t] : 0u;
+    sh[t] = v;
+    __syncthreads();
+    for (uint32_t o = 1; o < 1024; o <<= 1) {
+        const uint32_t a = t >= o ? sh[t - o] : 0u;
+        __syncthreads();
+        sh[t] += a;
+        __syncthreads();
+    }
+    if (t < nk) {
+        key_off[t] = sh[t] - v;
+        cursor[t] = sh[t] - v;
+    }
+    if (t == nk - 1) key_off[nk] = sh[t];
+}
+
+// Scatter the pairs by key as compact records (order inside a key is free: the sums are
+// exact integers): rec = (winner, loser | winner-in-leaf-a << 31), weight in fixed point.
+// Each workgroup takes kScatterItems pairs per thread, ranks them per key in LDS, reserves one
+// range per key with a single global atomic, then writes.
+constexpr uint32_t kScatterItems = 8;
+static __global__ __launch_bounds__(256) void pair_key_scatter_kernel(
+    const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los,
+    const long long* __restrict__ comp_wq, uint64_t m, const uint16_t* __restrict__ leaf, uint32_t P,
+    uint32_t* __restrict__ cursor, uint2* __restrict__ rec, long long* __restrict__ rec_wq) {
+    __shared__ uint32_t lcnt[kPairMaxParents * kPairMaxParents];
+    const uint32_t nk = P * P;
+    for (uint32_t i = threadIdx.x; i < nk; i += blockDim.x) lcnt[i] = 0;
+    __syncthreads();
+    const uint64_t base = (uint64_t)blockIdx.x * blockDim.x * kScatterItems;
+    uint32_t key[kScatterItems], slot[kScatterItems];
+    for (uint32_t r = 0; r < kScatterItems; ++r) {
+        const uint64_t k = base + (uint64_t)r * blockDim.x + threadIdx.x;
+        key[r] = 0xFFFFFFFFu;
+        if (k < m) {
+            const uint32_t wi = comp_win[k], lo = comp_los[k];
+            if (wi != lo) {
+                key[r] = pair_key(leaf[wi] & 0x7FFFu, leaf[lo] & 0x7FFFu, P);
+                slot[r] = atomicAdd(&lcnt[key[r]], 1u);
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < nk; i += blockDim.x)
+        if (lcnt[i]) lcnt[i] = atomicAdd(cursor + i, lcnt[i]);   // count -> reserved base
+    __syncthreads();
+    for (uint32_t r = 0; r < kScatterItems; ++r) {
+        if (key[r] == 0xFFFFFFFFu) continue;
+        const uint64_t k = base + (uint64_t)r * blockDim.x + threadIdx.x;
+        const uint32_t wi = comp_win[k], lo = comp_los[k];
+        const uint32_t pos = lcnt[key[r]] + slot[r];
+        const uint32_t wl = leaf[wi] & 0x7FFFu, ll = leaf[lo] & 0x7FFFu;
+        rec[pos] = make_uint2(wi, lo | ((wl <= ll ? 1u : 0u) << 31));
+        rec_wq[pos] = comp_wq[k];
+    }
+}
+
+// Feature tiles of the keyed statistics: tf features (a multiple of 4, whole row words) whose
+// cells [tf][2][B][2] fit the LDS budget.
+inline uint32_t pair_tile_features(uint32_t F, uint32_t B, size_t budget) {
+    const size_t per_f = (size_t)2 * B * 2 * sizeof(long long);
+    uint32_t tf = (uint32_t)(budget / per_f) & ~3u;
+    if (tf < 4) tf = 4;
+    return std::min<uint32_t>(tf, (F + 3) / 4 * 4);
+}
+
+// One workgroup per (leaf pair {a <= b}, feature tile); linear block ids are mapped so that
+// the workgroups of one tile run on one XCD.  Each pair reads the row words of its winner and
+// loser once for the whole tile.  Writes the cumulative statistics st [F][B][P][P][2] of the
+// cells [a][b] and [b][a] of the tile's features (every cell of st is written once per level:
+// no zeroing, no global atomics, no separate scan).
+static __global__ __launch_bounds__(256) void pair_stats_key_kernel(
+    const uint32_t* __restrict__ rows, uint32_t W, const uint2* __restrict__ rec,
+    const long long* __restrict__ rec_wq, const uint32_t* __restrict__ key_off, uint32_t F,
+    uint32_t P, uint32_t B, uint32_t tf, uint32_t n_tiles, long long* __restrict__ st) {
+    extern __shared__ unsigned long long cell_k[];   // [tf][blk][bucket][c]
+    const uint32_t bid = blockIdx.x;
+    const uint32_t xcd = bid & 7u, q = bid >> 3;
+    const uint32_t key = q % (P * P);
+    const uint32_t tile = (q / (P * P)) * 8u + xcd;
+    const uint32_t a = key / P, b = key % P;
+    if (tile >= n_tiles || a > b) return;
+    const uint32_t f0 = tile * tf;
+    const uint32_t nf = min(tf, F - f0);
+    const uint32_t w0 = f0 / 4, nw = (nf + 3) / 4;
+    const size_t per_f = (size_t)2 * B * 2;
+    for (size_t i = threadIdx.x; i < (size_t)nf * per_f; i += blockDim.x) cell_k[i] = 0;
+    __syncthreads();
+    for (uint32_t j = key_off[key] + threadIdx.x; j < key_off[key + 1]; j += blockDim.x) {
+        const uint2 r = rec[j];
+        const uint32_t wi = r.x, lo = r.y & 0x7FFFFFFFu;
+        const bool win_in_a = (r.y >> 31) != 0;
+        const unsigned long long neg = (unsigned long long)(-rec_wq[j]);
+        const uint32_t* rw = rows + (size_t)wi * W + w0;
+        const uint32_t* rl = rows + (size_t)lo * W + w0;
+        for (uint32_t w = 0; w < nw; ++w) {
+            const uint32_t ww = rw[w], wlw = rl[w];
+            for (uint32_t k = 0; k < 4; ++k) {
+                const uint32_t f = 4 * w + k;
+                if (f >= nf) break;
+                const uint32_t wb = (ww >> (8 * k)) & 0xFFu, lb = (wlw >> (8 * k)) & 0xFFu;
+                // first index x = loser leaf when wb > lb, else winner leaf; block 0 = [a][b]
+                const uint32_t blk = a == b ? 0u : ((wb > lb) == win_in_a ? 1u : 0u);
+                const uint32_t bs = wb > lb ? lb : wb, bg = wb > lb ? wb : lb;
+                unsigned long long* c = cell_k + (size_t)f * per_f + (size_t)blk * B * 2;
+                atomicAdd(c + bs * 2, neg);
+                atomicAdd(c + bg * 2 + 1, neg);
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t sq = threadIdx.x; sq < nf * 4; sq += blockDim.x) {   // prefix of (f, blk, c)
+        const uint32_t f = sq >> 2, blk = (sq >> 1) & 1u, c = sq & 1u;
+        unsigned long long* p = cell_k + (size_t)f * per_f + (size_t)blk * B * 2 + c;
+        unsigned long long run = 0;
+        for (uint32_t bb = 0; bb < B; ++bb) {
+            run += p[bb * 2];
+            p[bb * 2] = run;
+        }
+    }
+    __syncthreads();
+    const uint32_t nblk = a == b ? 1u : 2u;
+    for (size_t i = threadIdx.x; i < (size_t)nf * per_f; i += blockDim.x) {
+        const uint32_t f = (uint32_t)(i / per_f), r = (uint32_t)(i % per_f);
+        const uint32_t blk = r / (B * 2), bb = (r / 2) % B, c = r & 1u;
+        if (blk >= nblk) continue;
+        const uint32_t x = blk == 0 ? a : b, y = blk == 0 ? b : a;
+        st[((((size_t)(f0 + f) * B + bb) * P + x) * P + y) * 2 + c] = (long long)cell_k[i];
+    }
+}
+
 // Inclusive prefix over the bucket axis, in place; one thread per (f, x, y, c).
 static __global__ __launch_bounds__(256) void pair_scan_kernel(long long* __restrict__ st, uint32_t F,
                                                                uint32_t P, uint32_t B) {
@@ -168,8 +333,11 @@ __device__ inline void zero_average_wave(double* r, int n) {
 // matrix M; right-looking Cholesky in LDS (every element receives its pivot subtractions in
 // ascending order, as the reference's left-looking loop applies them), forward and back
 // substitution, res[n-1] = 0, zero average.  A non-positive pivot yields zeros.
-__device__ inline void pairwise_solve_wave(const double* W, const double* der, int n, double l2,
-                                           double prior, double* M, double* y, double* res) {
+// M holds (n-1) n / 2 doubles (packed), cj / y / res n doubles each.
+__device__ inline void pairwise_solve_wave(const double* __restrict__ W, const double* __restrict__ der, int n,
+                                           double l2, double prior, double* __restrict__ M,
+                                           double* __restrict__ cj, double* __restrict__ y,
+                                           double* __restrict__ res) {
     const int lane = threadIdx.x & 63;
     const double cell_prior = 1.0 / (double)n;
     const double non_diag = -prior * cell_prior;
@@ -190,8 +358,10 @@ __device__ inline void pairwise_solve_wave(const double* W, const double* der, i
     }
     const int m = n - 1;
     for (int r = lane; r < m; r += 64) {
-        for (int c = 0; c < r; ++c) M[tri(r, c)] = W[tri(r, c)] + non_diag;
-        M[tri(r, r)] = W[tri(r, r)] + diag;
+        const double* wr = W + r * (r + 1) / 2;
+        double* mr = M + r * (r + 1) / 2;
+        for (int c = 0; c < r; ++c) mr[c] = wr[c] + non_diag;
+        mr[r] = wr[r] + diag;
         y[r] = der[r];
     }
     __syncthreads();
@@ -203,13 +373,28 @@ __device__ inline void pairwise_solve_wave(const double* W, const double* der, i
             break;
         }
         const double ljj = sqrt(d);
-        __syncthreads();
-        for (int i = j + 1 + lane; i < m; i += 64) M[tri(i, j)] = M[tri(i, j)] / ljj;
-        if (lane == 0) M[tri(j, j)] = ljj;
-        __syncthreads();
         for (int i = j + 1 + lane; i < m; i += 64) {
-            const double lij = M[tri(i, j)];
-            for (int k = j + 1; k <= i; ++k) M[tri(i, k)] -= lij * M[tri(k, j)];
+            const double v = M[tri(i, j)] / ljj;
+            M[tri(i, j)] = v;
+            cj[i] = v;
+        }
+        __syncthreads();
+        if (lane == 0) M[tri(j, j)] = ljj;
+        // trailing update of row i: M[i][k] -= L[i][j] L[k][j], k in (j, i]; the row is
+        // contiguous in the packed layout and the pivot column is a separate array
+        for (int i = j + 1 + lane; i < m; i += 64) {
+            const double lij = cj[i];
+            double* __restrict__ row = M + i * (i + 1) / 2;
+            int k = j + 1;
+            for (; k + 3 <= i; k += 4) {
+                const double r0 = row[k], r1 = row[k + 1], r2 = row[k + 2], r3 = row[k + 3];
+                const double c0 = cj[k], c1 = cj[k + 1], c2 = cj[k + 2], c3 = cj[k + 3];
+                row[k] = r0 - lij * c0;
+                row[k + 1] = r1 - lij * c1;
+                row[k + 2] = r2 - lij * c2;
+                row[k + 3] = r3 - lij * c3;
+            }
+            for (; k <= i; ++k) row[k] = row[k] - lij * cj[k];
         }
         __syncthreads();
     }
@@ -253,8 +438,10 @@ __device__ inline double pairwise_score_wave(const double* a, const double* der,
     return outer;
 }
 
-// LDS of the candidate and leaf solves: W and M packed (2 x 2080 doubles) + 4 vectors of 64.
-constexpr size_t kPairSolveLds = (2 * 2080 + 4 * 64) * sizeof(double);
+// LDS of the candidate and leaf solves (doubles): W 2080 | M 2080 (the candidate kernel stages
+// the statistics of its border there first: 2048 cumulative cells + 1024 totals, which is
+// why the region is 3072 long) | der, cj, y, res, part 64 each.
+constexpr size_t kPairSolveLds = (2080 + 3072 + 5 * 64) * sizeof(double);
 
 // One wavefront per (border s, feature f): the weight matrix of border s from the cumulative
 // statistics (all terms exact in int64 -- UpdateWeightSumFromTotal plus the accumulated
@@ -273,14 +460,19 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
     }
     double* W = sh_pw;
     double* M = W + 2080;
-    double* der = M + 2080;
-    double* yv = der + 64;
+    long long* Rs = (long long*)M;           // staged [P][P][2] cumulative at s
+    long long* Ts = Rs + 2048;               // staged [P][P] smaller-border totals
+    double* der = M + 3072;
+    double* cj = der + 64;
+    double* yv = cj + 64;
     double* res = yv + 64;
     double* part = res + 64;
     const int n = 2 * (int)P;
-    const size_t row = (size_t)P * P * 2;
-    const long long* R = st + ((size_t)f * B + s) * row;
-    const long long* T = st + ((size_t)f * B + (B - 1)) * row;
+    const uint32_t PP = P * P;
+    const long long* R = st + ((size_t)f * B + s) * PP * 2;
+    const long long* T = st + ((size_t)f * B + (B - 1)) * PP * 2;
+    for (uint32_t i = lane; i < 2 * PP; i += 64) Rs[i] = R[i];
+    for (uint32_t i = lane; i < PP; i += 64) Ts[i] = T[2 * i];
     const double inv_d = sc->inv[kScoreDer];
     for (uint32_t yl = lane; yl < P; yl += 64) {
         const long long dp = dcum[((size_t)f * B + s) * P + yl];
@@ -288,16 +480,17 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
         der[2 * yl] = (double)dp * inv_d;
         der[2 * yl + 1] = (double)(dt - dp) * inv_d;
     }
+    __syncthreads();
     for (int r = lane; r < n; r += 64) {
         const uint32_t a = (uint32_t)r >> 1, u = (uint32_t)r & 1u;
-        const long long da = R[((size_t)a * P + a) * 2] - R[((size_t)a * P + a) * 2 + 1];
+        const long long da = Rs[(a * P + a) * 2] - Rs[(a * P + a) * 2 + 1];
         long long dg = -da;   // W[r][r]
         for (uint32_t b = 0; b < P; ++b) {
             if (b == a) continue;
             const uint32_t yv_ = a < b ? a : b, xv = a < b ? b : a;
-            const long long xs = R[((size_t)xv * P + yv_) * 2], xg = R[((size_t)xv * P + yv_) * 2 + 1];
-            const long long ys = R[((size_t)yv_ * P + xv) * 2], yg = R[((size_t)yv_ * P + xv) * 2 + 1];
-            const long long total = T[((size_t)xv * P + yv_) * 2] + T[((size_t)yv_ * P + xv) * 2];
+            const long long xs = Rs[(xv * P + yv_) * 2], xg = Rs[(xv * P + yv_) * 2 + 1];
+            const long long ys = Rs[(yv_ * P + xv) * 2], yg = Rs[(yv_ * P + xv) * 2 + 1];
+            const long long total = Ts[xv * P + yv_] + Ts[yv_ * P + xv];
             const long long w00 = xg + yg, w01 = xs - xg, w10 = ys - yg, w11 = -(xs + ys);
             long long e0, e1;   // W[r][2b], W[r][2b+1]
             if (u == 0) {
@@ -316,7 +509,7 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
         if (u == 1) W[tri(r, r - 1)] = (double)da * pair_inv;
     }
     __syncthreads();
-    pairwise_solve_wave(W, der, n, l2, prior, M, yv, res);
+    pairwise_solve_wave(W, der, n, l2, prior, M, cj, yv, res);
     const double score = pairwise_score_wave(res, der, W, n, part);
     if (lane == 0) scores[(size_t)f * B + s] = score;
 }
@@ -423,8 +616,9 @@ static __global__ __launch_bounds__(64) void pairwise_leaf_kernel(
     extern __shared__ double sh_pl[];
     double* W = sh_pl;
     double* M = W + 2080;
-    double* der = M + 2080;
-    double* yv = der + 64;
+    double* der = M + 3072;
+    double* cj = der + 64;
+    double* yv = cj + 64;
     double* res = yv + 64;
     const int lane = threadIdx.x;
     const double inv_d = sc->inv[kLeafDer];
@@ -433,7 +627,7 @@ static __global__ __launch_bounds__(64) void pairwise_leaf_kernel(
         der[r] = (double)sums[(size_t)r * CL] * inv_d;
     }
     __syncthreads();
-    pairwise_solve_wave(W, der, (int)L, l2, prior, M, yv, res);
+    pairwise_solve_wave(W, der, (int)L, l2, prior, M, cj, yv, res);
     for (uint32_t l = lane; l < L; l += 64) raw[l] = res[l];
     __syncthreads();
     if (lane == 0) pairwise_center_lane0(raw, sums, CL, L, lr, scaled);

@@ -160,6 +160,12 @@ struct cbh_session {
     long long* dcum = nullptr;       // [F][B][Pmax]
     double* cand_scores = nullptr;   // [F][B]
     long long* leaf_w = nullptr;     // [L][L]
+    uint32_t* key_cnt = nullptr;     // [Pmax^2] pairs per unordered leaf pair
+    uint32_t* key_off = nullptr;     // [Pmax^2 + 1]
+    uint32_t* key_cur = nullptr;     // [Pmax^2]
+    uint2* key_rec = nullptr;        // [m] pair records grouped by leaf pair
+    long long* key_wq = nullptr;     // [m]
+    uint32_t pair_tf = 4, pair_tiles = 1;
 
     // dominant-bin skip of the fill (features whose most frequent bin holds >= 1/8 of rows)
     uint32_t* skip_bin = nullptr;    // [F] dominant bin, or 256 (no skip)
@@ -187,6 +193,7 @@ struct cbh_session {
         dfree(group_off); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st); dfree(dcum);
         dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot);
+        dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq);
         for (auto& t : timers) {
             if (t.second.a) (void)hipEventDestroy(t.second.a);
             if (t.second.b) (void)hipEventDestroy(t.second.b);
@@ -304,6 +311,14 @@ int session_alloc(cbh_session* s) {
         CHECK(dalloc(&s->dcum, (size_t)s->F * s->B * pmax));
         CHECK(dalloc(&s->cand_scores, (size_t)s->F * s->B));
         CHECK(dalloc(&s->leaf_w, ((size_t)1 << s->depth) << s->depth));
+        CHECK(dalloc(&s->key_cnt, pmax * pmax));
+        CHECK(dalloc(&s->key_off, pmax * pmax + 1));
+        CHECK(dalloc(&s->key_cur, pmax * pmax));
+        s->pair_tf = pair_tile_features(s->F, s->B, 128 * 1024);
+        s->pair_tiles = (s->F + s->pair_tf - 1) / s->pair_tf;
+        HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_key_kernel,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)((size_t)s->pair_tf * 2 * s->B * 2 * sizeof(long long))));
     }
     CHECK(dalloc(&s->leaf_raw, ((size_t)1 << s->depth) * s->K));
     CHECK(dalloc(&s->leaf_scaled, ((size_t)1 << s->depth) * s->K));
@@ -544,10 +559,15 @@ int upload_pairs(cbh_session* s, const cbh_family* fam) {
     s->pair_inv = std::ldexp(1.0, -shift);
     if (m != s->n_pairs || !s->comp_win) {
         dfree(s->comp_win); dfree(s->comp_los); dfree(s->comp_w); dfree(s->comp_wq);
+        dfree(s->key_rec); dfree(s->key_wq);
         CHECK(dalloc(&s->comp_win, m));
         CHECK(dalloc(&s->comp_los, m));
         CHECK(dalloc(&s->comp_w, m));
         CHECK(dalloc(&s->comp_wq, m));
+        if (s->pairwise) {
+            CHECK(dalloc(&s->key_rec, m));
+            CHECK(dalloc(&s->key_wq, m));
+        }
     }
     if (G != s->n_groups || !s->group_off) {
         dfree(s->group_off);
@@ -576,23 +596,43 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     hipStream_t st = s->stream;
     const uint32_t P = 1u << level, B = s->B, F = s->F;
     const size_t cells = (size_t)F * B * P * P * 2;
-    CHECK(launch_zero(s->pair_st, cells, st));
-    if (s->n_pairs) {
-        const dim3 grid((unsigned)((s->n_pairs + kPairChunk - 1) / kPairChunk), F);
-        if (P <= 4) {
+    if (P <= 4) {   // few cells per feature: LDS-privatized chunks, global flush, bucket scan
+        CHECK(launch_zero(s->pair_st, cells, st));
+        if (s->n_pairs) {
+            const dim3 grid((unsigned)((s->n_pairs + kPairChunk - 1) / kPairChunk), F);
             const size_t lds = (size_t)B * P * P * 2 * sizeof(long long);
             HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_kernel<true>,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
             pair_stats_kernel<true><<<grid, 256, lds, st>>>(s->cols, s->n, s->leaf, s->comp_win, s->comp_los,
                                                            s->comp_wq, s->n_pairs, P, B, s->pair_st);
-        } else {
-            pair_stats_kernel<false><<<grid, 256, 0, st>>>(s->cols, s->n, s->leaf, s->comp_win, s->comp_los,
-                                                           s->comp_wq, s->n_pairs, P, B, s->pair_st);
+            HIP_TRY(hipGetLastError());
         }
+        pair_scan_kernel<<<grid_for((uint64_t)F * P * P * 2, 256), 256, 0, st>>>(s->pair_st, F, P, B);
+        HIP_TRY(hipGetLastError());
+    } else {        // pairs grouped by leaf pair; one workgroup per (feature, leaf pair)
+        const uint32_t nk = P * P;
+        zero_u32_kernel<<<grid_for(nk, 256), 256, 0, st>>>(s->key_cnt, nk);
+        HIP_TRY(hipGetLastError());
+        if (s->n_pairs) {
+            pair_key_count_kernel<<<grid_for(s->n_pairs, 256, 1024), 256, 0, st>>>(
+                s->comp_win, s->comp_los, s->n_pairs, s->leaf, P, s->key_cnt);
+            HIP_TRY(hipGetLastError());
+        }
+        pair_key_scan_kernel<<<1, 1024, 0, st>>>(s->key_cnt, nk, s->key_off, s->key_cur);
+        HIP_TRY(hipGetLastError());
+        if (s->n_pairs) {
+            pair_key_scatter_kernel<<<(unsigned)((s->n_pairs + 256 * kScatterItems - 1) / (256 * kScatterItems)),
+                                      256, 0, st>>>(
+                s->comp_win, s->comp_los, s->comp_wq, s->n_pairs, s->leaf, P, s->key_cur, s->key_rec,
+                s->key_wq);
+            HIP_TRY(hipGetLastError());
+        }
+        const uint32_t tpad = (s->pair_tiles + 7) / 8 * 8;
+        const size_t lds = (size_t)s->pair_tf * 2 * B * 2 * sizeof(long long);
+        pair_stats_key_kernel<<<tpad * nk, 256, lds, st>>>(s->rows, s->W, s->key_rec, s->key_wq, s->key_off, F,
+                                                          P, B, s->pair_tf, s->pair_tiles, s->pair_st);
         HIP_TRY(hipGetLastError());
     }
-    pair_scan_kernel<<<grid_for((uint64_t)F * P * P * 2, 256), 256, 0, st>>>(s->pair_st, F, P, B);
-    HIP_TRY(hipGetLastError());
     der_scan_kernel<<<grid_for((uint64_t)F * P, 256), 256, 0, st>>>(cur, P, s->C, F, B, s->dcum);
     HIP_TRY(hipGetLastError());
     pairwise_candidate_kernel<<<dim3(B - 1, F), 64, kPairSolveLds, st>>>(
