@@ -104,10 +104,10 @@ int run_fill(const uint32_t* rows, uint32_t W, uint64_t n, const uint32_t* idx,
              const LevelPlan* plan, double* sstat, const Scales* sc, const FillTiles& ft, uint32_t F,
              uint32_t B, long long* hist) {
     quantize_stats_kernel<C><<<grid_of(n * C, 256), 256>>>(sstat, n, sc);
-    HIP_OK(hipFuncSetAttribute((const void*)fill_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    HIP_OK(hipFuncSetAttribute((const void*)fill_kernel<C, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)ft.lds_bytes));
     const uint32_t G = 64;
-    fill_kernel<C><<<G * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, n, idx, plan,
+    fill_kernel<C, false><<<G * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, n, idx, plan,
                                                              (const long long*)sstat, ft.n_tiles, ft.tw,
                                                              F, B, G, hist, nullptr);
     HIP_OK(hipGetLastError());

@@ -353,7 +353,7 @@ inline FillTiles plan_fill_tiles(uint32_t F, uint32_t B, uint32_t C, size_t budg
 // histogram only when it crosses into the next segment (leaf) and at the end, so the
 // global-atomic flush traffic is about G * tiles * cells per launch instead of one flush
 // per small chunk.  G * tiles is sized to the number of workgroups the CUs hold at once.
-template <int C>
+template <int C, bool kSkip>
 __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, uint32_t W,
                                            const uint32_t* __restrict__ idx,
                                            const long long* __restrict__ sfix, uint32_t beg,
@@ -398,7 +398,7 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
             for (int k = 0; k < 4; ++k) {
                 if ((uint32_t)k < nf) {
                     const uint32_t bin = (word[u] >> (8 * k)) & 0xFFu;
-                    if (bin == skip[k]) continue;   // dominant bin: rebuilt from the totals
+                    if (kSkip && bin == skip[k]) continue;   // dominant bin: rebuilt from the totals
                     unsigned long long* cell = lbase + (uint32_t)k * B + bin;
 #pragma unroll
                     for (int ch = 0; ch < C; ++ch)
@@ -409,7 +409,7 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
     }
 }
 
-template <int C>
+template <int C, bool kSkip>
 static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t* __restrict__ rows, uint32_t W, uint64_t n,
     const uint32_t* __restrict__ idx,                  // null: dense rows [0, n), leaf 0
@@ -434,7 +434,7 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     unsigned long long* lbase = (unsigned long long*)lds + 4u * wl * B;
     const uint32_t nf = min(4u, TF - min(TF, 4u * wl));   // valid features of this lane's word
     uint32_t skip[4] = {256u, 256u, 256u, 256u};
-    if (skip_bin)
+    if (kSkip)
         for (uint32_t k = 0; k < nf; ++k) skip[k] = skip_bin[f0 + 4u * wl + k];
     const uint32_t V = idx ? plan->rows : (uint32_t)n;
     const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
@@ -449,7 +449,7 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = idx ? plan->built[seg] : 0u;
         if (end > pos) {
-            fill_range<C>(rows, W, idx, sfix, pos, end, w0, TW, nf, B, plane, lbase, skip);
+            fill_range<C, kSkip>(rows, W, idx, sfix, pos, end, w0, TW, nf, B, plane, lbase, skip);
             __syncthreads();
             // flush LDS [ch][f][bin] -> hist[leaf][ch][f0 + f][bin]: contiguous per plane
             for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) {
@@ -639,27 +639,41 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     double num = 0.0;
     double den = 0.0;
     den += 1e-100;
+    // the histogram cells of kPre parents are loaded ahead of their scans (the loop is
+    // otherwise bound by one dependent global load per iteration); the fold order over
+    // (d, side, p) is unchanged
+    constexpr uint32_t kPre = 8;
     for (int d = 0; d < K; ++d) {
         for (int side = 0; side < 2; ++side) {
-            for (uint32_t p = 0; p < P; ++p) {
-                const long long* leafh = hist + (size_t)p * C * F * B;
-                const long long vd = b < B ? leafh[((size_t)d * F + f) * B + b] : 0;
-                const long long vw = b < B ? leafh[((size_t)K * F + f) * B + b] : 0;
-                long long pd, pw, td, tw;
-                block_scan2<NW>(vd, vw, pd, pw, td, tw, sh);
-                long long xd, xw;
-                if (!oh) {
-                    xd = side == 0 ? pd : td - pd;
-                    xw = side == 0 ? pw : tw - pw;
-                } else {
-                    xd = side == 0 ? td - vd : vd;
-                    xw = side == 0 ? tw - vw : vw;
+            for (uint32_t p0 = 0; p0 < P; p0 += kPre) {
+                long long vdv[kPre], vwv[kPre];
+#pragma unroll
+                for (uint32_t u = 0; u < kPre; ++u) {
+                    const uint32_t p = p0 + u;
+                    const long long* leafh = hist + (size_t)p * C * F * B;
+                    vdv[u] = (b < B && p < P) ? leafh[((size_t)d * F + f) * B + b] : 0;
+                    vwv[u] = (b < B && p < P) ? leafh[((size_t)K * F + f) * B + b] : 0;
                 }
-                const double s = (double)xd * inv_d;
-                const double w = (double)xw * inv_w;
-                const double avg = w > 0.0 ? s / (w + l2) : 0.0;
-                num += avg * s;
-                den += avg * avg * w;
+#pragma unroll
+                for (uint32_t u = 0; u < kPre; ++u) {
+                    if (p0 + u >= P) break;
+                    const long long vd = vdv[u], vw = vwv[u];
+                    long long pd, pw, td, tw;
+                    block_scan2<NW>(vd, vw, pd, pw, td, tw, sh);
+                    long long xd, xw;
+                    if (!oh) {
+                        xd = side == 0 ? pd : td - pd;
+                        xw = side == 0 ? pw : tw - pw;
+                    } else {
+                        xd = side == 0 ? td - vd : vd;
+                        xw = side == 0 ? tw - vw : vw;
+                    }
+                    const double s = (double)xd * inv_d;
+                    const double w = (double)xw * inv_w;
+                    const double avg = w > 0.0 ? s / (w + l2) : 0.0;
+                    num += avg * s;
+                    den += avg * avg * w;
+                }
             }
         }
     }

@@ -363,7 +363,9 @@ int plan_tiles(cbh_session* s) {
 
 template <int C>
 int set_fill_attr(size_t lds) {
-    HIP_TRY(hipFuncSetAttribute((const void*)fill_kernel<C>,
+    HIP_TRY(hipFuncSetAttribute((const void*)fill_kernel<C, false>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    HIP_TRY(hipFuncSetAttribute((const void*)fill_kernel<C, true>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     return CBH_OK;
 }
@@ -700,9 +702,14 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
                                                                      (const long long*)s->sstat, C, s->seg_tot);
             HIP_TRY(hipGetLastError());
         }
-        fill_kernel<C><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
-            s->rows, s->W, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
-            s->use_skip ? s->skip_bin : nullptr);
+        if (s->use_skip)
+            fill_kernel<C, true><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
+                s->rows, s->W, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
+                s->skip_bin);
+        else
+            fill_kernel<C, false><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
+                s->rows, s->W, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
+                nullptr);
         HIP_TRY(hipGetLastError());
         if (s->use_skip) {
             default_bin_fixup_kernel<<<dim3(s->F, n_seg), 64, 0, st>>>(cur, lplan, s->skip_bin, s->seg_tot, C,
