@@ -92,7 +92,7 @@ class TrainParams(C.Structure):
 EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_session_read_approx", "cbh_session_stats", "cbh_session_reset_stats",
            "cbh_session_end", "cbh_compute_gradients", "cbh_hist_build", "cbh_bootstrap",
-           "cbh_version", "cbh_last_error", "cbt_open", "cbt_set_pairs", "cbt_step", "cbt_read_approx",
+           "cbh_apply_oblivious", "cbh_version", "cbh_last_error", "cbt_open", "cbt_set_pairs", "cbt_step", "cbt_read_approx",
            "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close"]
 
 _lib = None
@@ -125,6 +125,8 @@ def load(path: str = LIB_PATH):
     L.cbh_bootstrap.argtypes = [C.POINTER(TreeSampling), C.c_uint64, P, P]
     L.cbt_open.argtypes = [C.POINTER(TrainParams), P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, P,
                            P, C.POINTER(P)]
+    L.cbh_apply_oblivious.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, P, C.c_uint32, C.c_uint32,
+                                      P, P, P]
     L.cbt_set_pairs.argtypes = [P, P, C.c_uint32, P, P, P, C.c_uint64]
     L.cbt_step.argtypes = [P, P, P, P, P]
     L.cbt_read_approx.argtypes = [P, P]
@@ -192,6 +194,25 @@ def bootstrap(kind: str, n: int, *, bayesian_seed=0, bernoulli_state=(0, 1, 0, 1
 # ---------------------------------------------------------------------------------------
 # The Runtime seam (begin / grow / end)
 # ---------------------------------------------------------------------------------------
+def apply_oblivious(features_fm, split_features, split_borders, tree_split_offsets, leaf_values,
+                    tree_leaf_offsets, approx_dim=1, bias=None, nan_as_true=None):
+    """Raw predictions [approx_dim][n] of an oblivious float ensemble on the device
+    (``cbh_apply_oblivious``); features_fm is f32 [F][n], model arrays are flat CSR."""
+    x = np.ascontiguousarray(features_fm, np.float32)
+    F, n = x.shape
+    sf = np.ascontiguousarray(split_features, np.uint32)
+    sb = np.ascontiguousarray(split_borders, np.float64)
+    so = np.ascontiguousarray(tree_split_offsets, np.uint32)
+    lv = np.ascontiguousarray(leaf_values, np.float64)
+    lo = np.ascontiguousarray(tree_leaf_offsets, np.uint32)
+    b = None if bias is None else np.ascontiguousarray(np.broadcast_to(bias, (approx_dim,)), np.float64)
+    na = None if nan_as_true is None else np.ascontiguousarray(nan_as_true, np.uint8)
+    out = np.zeros((approx_dim, n))
+    _check(load().cbh_apply_oblivious(_ptr(x), n, F, _ptr(sf), _ptr(sb), _ptr(so), _ptr(lv), _ptr(lo),
+                                      so.shape[0] - 1, approx_dim, _ptr(b), _ptr(na), _ptr(out)))
+    return out
+
+
 def _family_arrays(group_offsets, winner, loser, weight=None):
     go = np.ascontiguousarray(group_offsets, np.uint32)
     w = np.ascontiguousarray(winner, np.uint32)

@@ -48,12 +48,14 @@ def _columns(n, F, make_col, n_borders, seed, threads=None, keep_cols=None):
     bins = np.empty((F, n), np.uint8)
     nb = np.empty(F, np.uint32)
     keep = {}
+    borders = [None] * F
 
     def work(f):
         col = make_col(f)
         b = _borders(col, n_borders, seed * 7919 + f)
         bins[f] = _quantize(col, b)
         nb[f] = b.size
+        borders[f] = b
         return f, (col if f in keep_cols else None)
 
     threads = threads or min(16, os.cpu_count() or 4)
@@ -61,6 +63,7 @@ def _columns(n, F, make_col, n_borders, seed, threads=None, keep_cols=None):
         for f, col in ex.map(work, range(F)):
             if col is not None:
                 keep[f] = col
+    keep["borders"] = borders
     return bins, nb, keep
 
 
@@ -72,8 +75,8 @@ def config1(scale=1.0, seed=0):
     X = g.standard_normal((n, F)).astype(np.float32)
     w = g.uniform(-1, 1, F)
     y = X.astype(np.float64) @ w + 0.1 * g.standard_normal(n)
-    bins, nb, _ = _columns(n, F, lambda f: np.ascontiguousarray(X[:, f]), 128, seed, keep_cols=())
-    return dict(name="config1", bins=bins, n_borders=nb, target=y,
+    bins, nb, kept = _columns(n, F, lambda f: np.ascontiguousarray(X[:, f]), 128, seed, keep_cols=())
+    return dict(name="config1", bins=bins, n_borders=nb, target=y, features=X, borders=kept["borders"],
                 params=dict(loss="RMSE", depth=6, iterations=100, learning_rate=0.1,
                             l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient",
                             bootstrap_type="No", boost_from_average=True))

@@ -194,6 +194,26 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t n_features, uint
 int cbh_bootstrap(const cbh_tree_sampling* sampling, uint64_t n, double* sample_weight,
                   uint8_t* control);
 
+/* Raw predictions of an oblivious float ensemble (final prediction / model apply).
+ * Mirrors launch_apply_oblivious_f64 (crates/cb-backend/src/gpu_runtime/mod.rs:337, kernel
+ * crates/cb-backend/src/kernels.rs:629) and predict_raw (crates/cb-model/src/apply.rs):
+ *   features_fm        f32 [n_features][n_objects] (the reference widens f32 values to f64,
+ *                      as this comparison does)
+ *   split_features, split_borders   [tree_split_offsets[n_trees]], pass test value > border
+ *   tree_split_offsets [n_trees + 1] CSR, starting at 0; split i of a tree is leaf bit i
+ *   leaf_values        [tree_leaf_offsets[n_trees] * approx_dim], the approx_dim values of a
+ *                      leaf contiguous (DeviceGrownTree layout); tree_leaf_offsets CSR in leaves
+ *   bias               nullable [approx_dim], added once after the trees
+ *   nan_as_true        nullable [n_features]: NaN passes every split of the feature (borders
+ *                      of nan_mode=Max); otherwise NaN fails
+ *   out                [approx_dim][n_objects]
+ * A split feature >= n_features is absent (bit 0); a leaf index past the tree adds 0. */
+int cbh_apply_oblivious(const float* features_fm, uint64_t n_objects, uint32_t n_features,
+                        const uint32_t* split_features, const double* split_borders,
+                        const uint32_t* tree_split_offsets, const double* leaf_values,
+                        const uint32_t* tree_leaf_offsets, uint32_t n_trees, uint32_t approx_dim,
+                        const double* bias, const uint8_t* nan_as_true, double* out);
+
 /* Version / build information. */
 const char* cbh_version(void);
 const char* cbh_last_error(void);

@@ -900,6 +900,42 @@ static void pairwise_center(double* v, const double* leaf_w, uint32_t n_leaves) 
 }
 
 /* ======================================================================
+ * Model apply (crates/cb-model/src/apply.rs predict_raw_one; device twin
+ * crates/cb-backend/src/kernels.rs:629 apply_oblivious_float_kernel): per object, each
+ * tree's leaf from its float splits (value > border, forward bit order; NaN passes only
+ * for a feature flagged nan_as_true, apply.rs:160-166), contributions summed in tree order
+ * from 0, bias added once after the trees.  Leaf values of tree t are
+ * leaf_values[(tree_leaf_offsets[t] + leaf) * K + d]; out is dim-major [K][n].
+ * ==================================================================== */
+int orc_apply_oblivious(const float* x_fm, uint64_t n, uint32_t F, const uint32_t* split_features,
+                        const double* split_borders, const uint32_t* tree_split_offsets,
+                        const double* leaf_values, const uint32_t* tree_leaf_offsets,
+                        uint32_t n_trees, uint32_t K, const double* bias,
+                        const uint8_t* nan_as_true, double* out) {
+    for (uint64_t i = 0; i < n; ++i) {
+        for (uint32_t d = 0; d < K; ++d) {
+            double acc = 0.0;
+            for (uint32_t t = 0; t < n_trees; ++t) {
+                uint32_t leaf = 0, bit = 0;
+                for (uint32_t s = tree_split_offsets[t]; s < tree_split_offsets[t + 1]; ++s, ++bit) {
+                    uint32_t f = split_features[s];
+                    int pass = 0;
+                    if (f < F) {
+                        float v = x_fm[(size_t)f * n + i];
+                        pass = isnan(v) ? (nan_as_true && nan_as_true[f]) : ((double)v > split_borders[s]);
+                    }
+                    leaf |= (uint32_t)pass << bit;
+                }
+                uint32_t li = tree_leaf_offsets[t] + leaf;
+                acc += li < tree_leaf_offsets[t + 1] ? leaf_values[(size_t)li * K + d] : 0.0;
+            }
+            out[(size_t)d * n + i] = acc + (bias ? bias[d] : 0.0);
+        }
+    }
+    return 0;
+}
+
+/* ======================================================================
  * Boosting loop -- CPU branch of crates/cb-train/src/boosting.rs:7300-8900
  * (Plain boosting, SymmetricTree, random_strength 0, pointwise losses).
  * ==================================================================== */

@@ -134,6 +134,14 @@ void orc_pairwise_leaf_deltas(const uint32_t* leaf_of, uint64_t n, const double*
                               const uint32_t* winner, const uint32_t* loser, const double* weight,
                               uint64_t m, uint32_t n_leaves, double l2, double prior, double* out);
 
+/* ---- model apply (cb-model/src/apply.rs; device kernels.rs:629) ----
+ * Float splits, CSR per tree; leaf values [(tree_leaf_offsets[t] + leaf) * K + d]; out [K][n]. */
+int orc_apply_oblivious(const float* x_fm, uint64_t n, uint32_t F, const uint32_t* split_features,
+                        const double* split_borders, const uint32_t* tree_split_offsets,
+                        const double* leaf_values, const uint32_t* tree_leaf_offsets,
+                        uint32_t n_trees, uint32_t K, const double* bias,
+                        const uint8_t* nan_as_true, double* out);
+
 /* Per-leaf ordered sums (cb-compute/src/histogram.rs:49 reduce_leaf_stats, :97 reduce_leaf_der2). */
 void orc_leaf_sums(const uint32_t* leaf_of, uint64_t n, uint32_t n_leaves, const double* der,
                    const double* weight, double* sum_der, double* sum_w);

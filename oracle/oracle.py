@@ -87,6 +87,9 @@ def lib():
         L.orc_grow_tree_pairwise.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, P, P, C.c_uint64,
                                              C.c_int32, C.c_double, C.c_double, C.c_int32, P, P, P]
         L.orc_grow_tree_pairwise.restype = C.c_int
+        L.orc_apply_oblivious.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, P, C.c_uint32,
+                                          C.c_uint32, P, P, P]
+        L.orc_apply_oblivious.restype = C.c_int
         L.orc_pairwise_feature_scores.argtypes = [P, P, P, C.c_uint64, P, P, P, C.c_uint64, C.c_int32,
                                                   C.c_int32, C.c_double, C.c_double, P]
         L.orc_pairwise_leaf_deltas.argtypes = [P, C.c_uint64, P, P, P, P, C.c_uint64, C.c_uint32,
@@ -254,6 +257,32 @@ def pairwise_leaf_deltas(leaf_of, der, winner, loser, weight, n_leaves, l2, prio
     out = np.zeros(n_leaves)
     lib().orc_pairwise_leaf_deltas(_p(lo), lo.shape[0], _p(d), _p(w), _p(l), _p(wt), w.shape[0],
                                    n_leaves, l2, prior, _p(out))
+    return out
+
+
+def model_arrays(split_features, split_borders, leaf_values, K=1):
+    """Flat CSR model arrays of an oblivious ensemble: split_features / split_borders are
+    per-tree lists, leaf_values per-tree arrays of 2^depth * K (leaf-major)."""
+    sf = np.ascontiguousarray(np.concatenate([np.asarray(t, np.uint32) for t in split_features]), np.uint32)
+    sb = np.ascontiguousarray(np.concatenate([np.asarray(t, np.float64) for t in split_borders]), np.float64)
+    so = np.concatenate([[0], np.cumsum([len(t) for t in split_features])]).astype(np.uint32)
+    lv = np.ascontiguousarray(np.concatenate([np.asarray(t, np.float64).ravel() for t in leaf_values]))
+    lo = np.concatenate([[0], np.cumsum([np.asarray(t).size // K for t in leaf_values])]).astype(np.uint32)
+    return sf, sb, so, lv, lo
+
+
+def apply_oblivious(x_fm, split_features, split_borders, tree_split_offsets, leaf_values,
+                    tree_leaf_offsets, K=1, bias=None, nan_as_true=None):
+    """Raw predictions [K][n] of float features x_fm [F][n] (f32)."""
+    x = np.ascontiguousarray(x_fm, np.float32)
+    F, n = x.shape
+    b = None if bias is None else np.ascontiguousarray(np.broadcast_to(bias, (K,)), np.float64)
+    na = None if nan_as_true is None else np.ascontiguousarray(nan_as_true, np.uint8)
+    out = np.zeros((K, n))
+    arrs = [np.ascontiguousarray(a) for a in (split_features, split_borders, tree_split_offsets,
+                                               leaf_values, tree_leaf_offsets)]
+    lib().orc_apply_oblivious(_p(x), n, F, _p(arrs[0]), _p(arrs[1]), _p(arrs[2]), _p(arrs[3]),
+                              _p(arrs[4]), arrs[2].shape[0] - 1, K, _p(b), _p(na), _p(out))
     return out
 
 

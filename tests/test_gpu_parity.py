@@ -428,3 +428,59 @@ def test_config5_shape_matches_oracle():
     """Config 5 shape (MultiClass K=10, depth 8, 70%-zero columns, 64 borders) at 20k x 256."""
     d = datagen.config5(n_rows=20_000, n_features=256)
     _assert_same_fit(*_fit_both(d, 4))
+
+
+# ------------------------------------------------------------------------------ model apply
+def test_apply_on_gpu_matches_oracle_and_upstream():
+    """cbh_apply_oblivious: bit-equal to the oracle's predict_raw restatement on every
+    upstream fixture (and so to catboost 1.2.10's predictions)."""
+    from tests.test_oracle_pin import APPLY_FIXTURES, upstream_model
+    for name in APPLY_FIXTURES:
+        u = G.upstream(name)
+        arrs, K = upstream_model(u)
+        x = u["X"].T.astype(np.float32)
+        got = cb.apply_oblivious(x, *arrs, approx_dim=K, bias=u["bias"])
+        exp = O.apply_oblivious(x, *arrs, K=K, bias=u["bias"])
+        assert np.array_equal(got, exp), name
+
+
+@pytest.mark.parametrize("K", [1, 3])
+def test_apply_on_gpu_random_models(K):
+    g = np.random.default_rng(10 + K)
+    n, F, T, d = 200_003, 24, 60, 6
+    x = g.normal(size=(F, n)).astype(np.float32)
+    x[g.random((F, n)) < 0.02] = np.nan
+    sf = [g.integers(0, F + 1, size=d) for _ in range(T)]
+    sb = [g.normal(size=d) for _ in range(T)]
+    lv = [g.normal(size=(1 << d) * K) for _ in range(T)]
+    arrs = O.model_arrays(sf, sb, lv, K)
+    nan_true = (g.random(F) < 0.5).astype(np.uint8)
+    bias = g.normal(size=K)
+    got = cb.apply_oblivious(x, *arrs, approx_dim=K, bias=bias, nan_as_true=nan_true)
+    exp = O.apply_oblivious(x, *arrs, K=K, bias=bias, nan_as_true=nan_true)
+    assert np.array_equal(got, exp)
+
+
+def test_trained_model_applied_to_floats_reproduces_training_approx():
+    """End to end: grow 20 config-1 trees on the device, turn (feature, bin) splits into
+    float borders, apply the model to the float columns: the predictions equal the resident
+    training approximant (bin > b  <=>  value > border[b])."""
+    d = datagen.config1()
+    P = d["params"]
+    nb = d["n_borders"]
+    tr = cb.Trainer(d["bins"], int(nb.max()) + 1, d["target"], loss=P["loss"], depth=P["depth"],
+                    learning_rate=P["learning_rate"], l2_leaf_reg=P["l2_leaf_reg"], score=P["score"],
+                    leaf_method=P["leaf_method"], bootstrap_type="No", boost_from_average=True,
+                    real_folds=nb + 1)
+    try:
+        splits, leaves = tr.fit(20)
+        approx = tr.approx()
+        bias = tr.bias
+    finally:
+        tr.close()
+    borders = d["borders"]
+    sf = [s[:, 0] for s in splits]
+    sb = [[borders[f][b] for f, b in s] for s in splits]
+    arrs = O.model_arrays(sf, sb, [lv[0] for lv in leaves], 1)
+    got = cb.apply_oblivious(d["features"].T, *arrs, bias=[bias])
+    _close(got, approx)

@@ -368,3 +368,60 @@ def test_pairwise_leaf_deltas_match_direct_solve():
     got = O.pairwise_leaf_deltas(leaf_of, der, w, l, x, 8, 3.0, 0.1)
     exp, _ = _direct_pairwise(leaf_of.astype(np.int64), der, w.astype(np.int64), l.astype(np.int64), x, 8, 3.0, 0.1)
     np.testing.assert_allclose(got, exp, rtol=1e-9, atol=1e-12)
+
+
+# ------------------------------------------------------------------------------ model apply
+APPLY_FIXTURES = ["regression_skeleton", "binclf_skeleton", "bootstrap_no", "bootstrap_bayesian",
+                  "bootstrap_bernoulli", "multiclass_softmax"]
+
+
+def upstream_model(u):
+    """Flat CSR model arrays of an upstream fixture (float splits, leaf-major leaf values)."""
+    T, d = u["split_feature"].shape
+    K = u["leaf_values"].shape[1] >> d
+    arrs = O.model_arrays(list(u["split_feature"]), list(u["split_border"]), list(u["leaf_values"]), K)
+    return arrs, K
+
+
+@pytest.mark.parametrize("name", APPLY_FIXTURES)
+def test_apply_matches_upstream_predictions(name):
+    """predict_raw (cb-model/src/apply.rs) against catboost 1.2.10 RawFormulaVal predictions
+    (the last staged approximant for the multiclass fixture, whose predictions are
+    probabilities)."""
+    u = G.upstream(name)
+    arrs, K = upstream_model(u)
+    out = O.apply_oblivious(u["X"].T.astype(np.float32), *arrs, K=K, bias=u["bias"])
+    n = u["X"].shape[0]
+    exp = u["staged"].reshape(-1, n, K)[-1].T if K > 1 else u["predictions"][None]
+    np.testing.assert_allclose(out, exp, rtol=0, atol=1e-12)
+
+
+def test_apply_nan_and_absent_features():
+    """NaN fails every split unless its feature is flagged (nan_mode=Max), a split on a
+    feature the matrix lacks is absent, a leaf index past the tree contributes 0 -- against
+    a direct per-object evaluation."""
+    g = np.random.default_rng(5)
+    n, F, T, d, K = 300, 6, 7, 3, 2
+    x = g.normal(size=(F, n)).astype(np.float32)
+    x[g.random((F, n)) < 0.1] = np.nan
+    sf = [g.integers(0, F + 2, size=d) for _ in range(T)]          # F, F+1 are absent
+    sb = [g.normal(size=d) for _ in range(T)]
+    lv = [g.normal(size=(1 << d) * K) for _ in range(T)]
+    lv[3] = lv[3][: 4 * K]                                             # a short tree: leaves 4..7 add 0
+    arrs = O.model_arrays(sf, sb, lv, K)
+    nan_true = (np.arange(F) % 2).astype(np.uint8)
+    out = O.apply_oblivious(x, *arrs, K=K, bias=[0.5, -0.25], nan_as_true=nan_true)
+    exp = np.zeros((K, n))
+    for i in range(n):
+        for t in range(T):
+            leaf = 0
+            for lvl in range(d):
+                f = int(sf[t][lvl])
+                if f < F:
+                    v = x[f, i]
+                    p = bool(nan_true[f]) if np.isnan(v) else float(v) > sb[t][lvl]
+                    leaf |= int(p) << lvl
+            if leaf < lv[t].size // K:
+                exp[:, i] += lv[t][leaf * K:(leaf + 1) * K]
+    exp += np.array([0.5, -0.25])[:, None]
+    np.testing.assert_allclose(out, exp, rtol=1e-14, atol=1e-14)
