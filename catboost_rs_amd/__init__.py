@@ -92,8 +92,9 @@ class TrainParams(C.Structure):
 EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_session_read_approx", "cbh_session_stats", "cbh_session_reset_stats",
            "cbh_session_end", "cbh_compute_gradients", "cbh_hist_build", "cbh_bootstrap",
-           "cbh_apply_oblivious", "cbh_version", "cbh_last_error", "cbt_open", "cbt_set_pairs", "cbt_step", "cbt_read_approx",
-           "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close"]
+           "cbh_apply_oblivious", "cbh_session_begin_raw", "cbh_select_borders", "cbh_quantize",
+           "cbh_version", "cbh_last_error", "cbt_open", "cbt_open_raw", "cbt_set_pairs", "cbt_step",
+           "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close"]
 
 _lib = None
 
@@ -127,6 +128,11 @@ def load(path: str = LIB_PATH):
                            P, C.POINTER(P)]
     L.cbh_apply_oblivious.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, P, C.c_uint32, C.c_uint32,
                                       P, P, P]
+    L.cbh_session_begin_raw.argtypes = [C.POINTER(Config), P, P, P, P, C.c_uint64, C.c_uint32, C.c_uint32,
+                                        C.c_double, C.c_double, C.POINTER(P)]
+    L.cbh_select_borders.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_int32, C.c_int32, P, P]
+    L.cbh_quantize.argtypes = [P, C.c_uint64, P, C.c_uint32, P]
+    L.cbt_open_raw.argtypes = [C.POINTER(TrainParams), P, P, P, C.c_uint64, C.c_uint32, P, P, C.POINTER(P)]
     L.cbt_set_pairs.argtypes = [P, P, C.c_uint32, P, P, P, C.c_uint64]
     L.cbt_step.argtypes = [P, P, P, P, P]
     L.cbt_read_approx.argtypes = [P, P]
@@ -213,6 +219,51 @@ def apply_oblivious(features_fm, split_features, split_borders, tree_split_offse
     return out
 
 
+BORDER_TYPE = {"GreedyLogSum": 0, "GreedyMinEntropy": 1}
+NAN_MODE = {"Min": 0, "Max": 1, "Forbidden": 2}
+
+
+def _column_ptrs(columns):
+    """f32 feature-major matrix [F][n] -> (kept array, C array of F column pointers)."""
+    x = np.ascontiguousarray(columns, np.float32)
+    if x.ndim != 2:
+        raise ValueError("columns must be a [n_features][n] matrix")
+    ptrs = (C.c_void_p * max(x.shape[0], 1))()
+    for f in range(x.shape[0]):
+        ptrs[f] = x.ctypes.data + f * x.strides[0]
+    return x, ptrs
+
+
+def _border_ptrs(borders):
+    bs = [np.ascontiguousarray(b, np.float64) for b in borders]
+    ptrs = (C.c_void_p * max(len(bs), 1))()
+    for f, b in enumerate(bs):
+        ptrs[f] = b.ctypes.data if b.size else None
+    nb = np.array([b.size for b in bs], np.uint32)
+    return bs, ptrs, nb
+
+
+def select_borders(columns, border_count=254, nan_mode="Min", border_type="GreedyLogSum"):
+    """Greedy border sets of f32 columns [F][n] (``cbh_select_borders``): a list of F
+    ascending f64 arrays, sentinels of ``nan_mode`` included for NaN-bearing columns."""
+    x, ptrs = _column_ptrs(columns)
+    F, n = x.shape
+    out = np.zeros((F, border_count + 1))
+    cnt = np.zeros(F, np.uint32)
+    _check(load().cbh_select_borders(ptrs, n, F, border_count, NAN_MODE[nan_mode],
+                                     BORDER_TYPE[border_type], _ptr(out), _ptr(cnt)))
+    return [out[f, :cnt[f]].copy() for f in range(F)]
+
+
+def quantize(column, borders):
+    """u8 bins of one f32 column over ascending borders (``cbh_quantize``)."""
+    c = np.ascontiguousarray(column, np.float32)
+    b = np.ascontiguousarray(borders, np.float64)
+    out = np.zeros(c.shape[0], np.uint8)
+    _check(load().cbh_quantize(_ptr(c), c.shape[0], _ptr(b) if b.size else None, b.size, _ptr(out)))
+    return out
+
+
 def _family_arrays(group_offsets, winner, loser, weight=None):
     go = np.ascontiguousarray(group_offsets, np.uint32)
     w = np.ascontiguousarray(winner, np.uint32)
@@ -261,6 +312,32 @@ class HipBackend:
             bins = bins.astype(np.uint32)
         rc = fn(C.byref(cfg), _ptr(bins), _ptr(w), n, n_features, n_bins, learning_rate, scaled_l2,
                 C.byref(self._s))
+        if rc == DECLINED:
+            return False
+        _check(rc)
+        self.n, self.depth, self.K = n, depth, approx_dim
+        return True
+
+    def begin_device_training_raw(self, loss, depth, boosting_type_is_plain, fold_count, score_function,
+                                  float_columns, feature_borders, weight, n, n_features, n_bins,
+                                  learning_rate, scaled_l2, *, approx_dim=1, bias=0.0,
+                                  leaf_method="Gradient", bootstrap_type="No", sample_from_host=False,
+                                  profile=False, real_folds=None, pairwise_non_diag_reg=0.1) -> bool:
+        """Raw float channel (runtime.rs:1546): f32 columns [F][n] + per-feature borders; the
+        device quantizes.  Returns True when the session opened, False when declined."""
+        rf = None if real_folds is None else np.ascontiguousarray(real_folds, np.uint32)
+        x, cp = _column_ptrs(float_columns)
+        bs, bp, nb = _border_ptrs(feature_borders)
+        w = None if weight is None else np.ascontiguousarray(weight, np.float64)
+        self._keep = [rf, x, cp, bs, bp, nb, w]
+        cfg = Config(loss=LOSS[loss], score_function=SCORE[score_function], leaf_method=LEAF[leaf_method],
+                     depth=depth, boosting_type_is_plain=int(boosting_type_is_plain),
+                     fold_count=fold_count, approx_dim=approx_dim, bootstrap_type=BOOT[bootstrap_type],
+                     sample_from_host=int(sample_from_host), profile=int(profile), bias=bias,
+                     one_hot_flags=None, real_folds=_ptr(rf),
+                     pairwise_non_diag_reg=pairwise_non_diag_reg)
+        rc = load().cbh_session_begin_raw(C.byref(cfg), cp, bp, _ptr(nb), _ptr(w), n, n_features, n_bins,
+                                          learning_rate, scaled_l2, C.byref(self._s))
         if rc == DECLINED:
             return False
         _check(rc)
@@ -316,11 +393,20 @@ class Trainer:
                  l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient", bootstrap_type="No",
                  subsample=0.66, bagging_temperature=1.0, boost_from_average=False, random_seed=0,
                  weight=None, approx_dim=1, profile=False, real_folds=None, one_hot_flags=None,
-                 pairs=None, group_offsets=None, pairwise_non_diag_reg=0.1):
+                 pairs=None, group_offsets=None, pairwise_non_diag_reg=0.1, float_columns=None,
+                 float_borders=None):
         """``pairs`` = (winner, loser[, weight]) and ``group_offsets`` (CSR over row order) for
-        PairLogit / PairLogitPairwise."""
-        self.bins = np.ascontiguousarray(bins_fm, np.uint8)
-        F, n = self.bins.shape
+        PairLogit / PairLogitPairwise.  With ``bins_fm`` None the trainer opens over the raw
+        float channel: ``float_columns`` f32 [F][n] and ``float_borders`` (F arrays)."""
+        raw = bins_fm is None
+        if raw:
+            x, cp = _column_ptrs(float_columns)
+            bs, bp, nb = _border_ptrs(float_borders)
+            self.bins = None
+            F, n = x.shape
+        else:
+            self.bins = np.ascontiguousarray(bins_fm, np.uint8)
+            F, n = self.bins.shape
         self.n, self.F, self.depth = n, F, depth
         self.K = approx_dim if loss == "MultiClass" else 1
         p = TrainParams(loss=LOSS[loss], score_function=SCORE[score], leaf_method=LEAF[leaf_method],
@@ -335,12 +421,23 @@ class Trainer:
         oh = None if one_hot_flags is None else np.ascontiguousarray(one_hot_flags, np.uint8)
         self._keep = (t, w, rf, oh)
         self._h = C.c_void_p()
-        _check(load().cbt_open(C.byref(p), _ptr(self.bins), n, F, n_bins, _ptr(rf), _ptr(oh), _ptr(t),
-                               _ptr(w), C.byref(self._h)))
+        if raw:
+            if real_folds is not None or one_hot_flags is not None:
+                raise ValueError("the raw float channel takes its folds from the borders and has no one-hot columns")
+            self._keep += (x, cp, bs, bp, nb)
+            _check(load().cbt_open_raw(C.byref(p), cp, bp, _ptr(nb), n, F, _ptr(t), _ptr(w), C.byref(self._h)))
+        else:
+            _check(load().cbt_open(C.byref(p), _ptr(self.bins), n, F, n_bins, _ptr(rf), _ptr(oh), _ptr(t),
+                                   _ptr(w), C.byref(self._h)))
         if pairs is not None:
             go, pw_, pl_, pwt = _family_arrays(group_offsets, *pairs)
             _check(load().cbt_set_pairs(self._h, _ptr(go), go.shape[0] - 1, _ptr(pw_), _ptr(pl_),
                                         _ptr(pwt), pw_.shape[0]))
+
+    @classmethod
+    def from_floats(cls, float_columns, float_borders, target, **kw):
+        """Trainer over the raw float channel (the device quantizes the columns)."""
+        return cls(None, None, target, float_columns=float_columns, float_borders=float_borders, **kw)
 
     def step(self):
         d = self.depth

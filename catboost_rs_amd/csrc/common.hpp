@@ -87,6 +87,16 @@ __host__ __device__ inline double rng_real1(Rng& r) {
     return (double)(rng_gen(r) >> 11) * (1.0 / 9007199254740991.0);
 }
 
+// Uniform draw in [0, bound) by rejection (rng.rs:268-280).
+__host__ __device__ inline uint64_t rng_uniform(Rng& r, uint64_t bound) {
+    if (bound == 0) return 0;
+    const uint64_t randmax = ~0ull - (~0ull % bound);
+    for (;;) {
+        const uint64_t v = rng_gen(r);
+        if (v < randmax) return v % bound;
+    }
+}
+
 // Affine jump tables of the LCG: fine[j] = (A^j, (A^j-1)/(A-1)) for j < 1024 and
 // coarse[q] = the same for j = 1024 q, q < n_coarse.
 inline void make_jump_tables(uint64_t n_coarse, uint64_t* fine_a, uint64_t* fine_d,

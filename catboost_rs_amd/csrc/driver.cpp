@@ -4,6 +4,7 @@
 // (Bayesian seed / Bernoulli raw state) and the host advances its stream exactly as the
 // CPU branch would, including the per-level draws of the perturbed level search that the
 // device path does not run (crates/cb-train/src/device_draw_replay.rs).
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -55,12 +56,15 @@ struct cbt_trainer {
     }
 };
 
-extern "C" {
+namespace {
 
-int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t n_bins,
-             const uint32_t* real_folds, const uint8_t* one_hot_flags, const double* target,
-             const double* weight, cbt_trainer** out) {
-    if (!p || !bins_fm || !target || !out) return CBH_ERR_INVALID_ARG;
+// Shared open: validation, starting approx, scaled l2, the session config; `begin` opens
+// the device session over whichever input channel the caller has.
+template <typename Begin>
+int trainer_open(const cbt_params* p, uint64_t n, uint32_t F, const uint32_t* real_folds,
+                 const uint8_t* one_hot_flags, const double* target, const double* weight,
+                 cbt_trainer** out, Begin&& begin) {
+    if (!p || !target || !out) return CBH_ERR_INVALID_ARG;
     *out = nullptr;
     bool any_one_hot = false;
     for (uint32_t f = 0; one_hot_flags && f < F; ++f) any_one_hot |= one_hot_flags[f] != 0;
@@ -109,7 +113,7 @@ int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F
     cfg.real_folds = real_folds;
     cfg.pairwise_non_diag_reg = p->pairwise_non_diag_reg;
     t->ranking = p->loss == CBH_LOSS_PAIRLOGIT || p->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE;
-    int rc = cbh_session_begin_u8(&cfg, bins_fm, weight, n, F, n_bins, t->p.learning_rate, scaled_l2, &t->s);
+    int rc = begin(&cfg, t->p.learning_rate, scaled_l2, &t->s);
     if (rc != CBH_OK) return rc;
     t->rng = cbh::rng_from_seed(p->random_seed);
     t->draws_active = p->bootstrap_type != CBH_BOOT_NO;
@@ -119,6 +123,33 @@ int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F
     t->leaves.resize(((size_t)1 << p->depth) * t->K);
     *out = t.release();
     return CBH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t n_bins,
+             const uint32_t* real_folds, const uint8_t* one_hot_flags, const double* target,
+             const double* weight, cbt_trainer** out) {
+    if (!bins_fm) return CBH_ERR_INVALID_ARG;
+    return trainer_open(p, n, F, real_folds, one_hot_flags, target, weight, out,
+                        [&](const cbh_config* cfg, double lr, double l2, cbh_session** s) {
+                            return cbh_session_begin_u8(cfg, bins_fm, weight, n, F, n_bins, lr, l2, s);
+                        });
+}
+
+int cbt_open_raw(const cbt_params* p, const float* const* columns, const double* const* borders,
+                 const uint32_t* n_borders, uint64_t n, uint32_t F, const double* target,
+                 const double* weight, cbt_trainer** out) {
+    if (!columns || !borders || !n_borders) return CBH_ERR_INVALID_ARG;
+    uint32_t n_bins = 1;
+    for (uint32_t f = 0; f < F; ++f) n_bins = std::max(n_bins, n_borders[f] + 1);
+    return trainer_open(p, n, F, nullptr, nullptr, target, weight, out,
+                        [&](const cbh_config* cfg, double lr, double l2, cbh_session** s) {
+                            return cbh_session_begin_raw(cfg, columns, borders, n_borders, weight, n, F,
+                                                         n_bins, lr, l2, s);
+                        });
 }
 
 int cbt_set_pairs(cbt_trainer* t, const uint32_t* group_offsets, uint32_t n_groups,

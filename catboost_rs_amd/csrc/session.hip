@@ -98,6 +98,8 @@ struct StageTimer {
 }  // namespace
 
 int cbh_internal_fail(int code, const std::string& msg) { return fail(code, msg); }
+int cbh_internal_quantize(const float* d_col, uint64_t n, const double* d_borders, uint32_t nb, uint8_t* d_out,
+                          hipStream_t st);  // borders.hip
 
 struct cbh_session {
     cbh_config cfg{};
@@ -414,6 +416,10 @@ int plan_skip_bins(cbh_session* s) {
     return CBH_OK;
 }
 
+template <typename Load>
+int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32_t F, uint32_t n_bins,
+                 double lr, double l2, cbh_session** out, Load&& load_cols);
+
 template <typename BinT>
 int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double* weight,
                        uint64_t n, uint32_t F, uint32_t n_bins, double lr, double l2,
@@ -426,6 +432,84 @@ int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double*
     for (uint64_t i = 0, total = n * F; i < total; ++i)
         if ((uint32_t)bins_fm[i] >= n_bins)
             return fail(CBH_ERR_OUT_OF_RANGE, "bin value >= n_bins at flat index " + std::to_string(i));
+    // upload bins feature-major as u8 (the rows are packed from them on the device)
+    return session_open(cfg, weight, n, F, n_bins, lr, l2, out, [&](cbh_session* s) -> int {
+        if (sizeof(BinT) == 1) {
+            HIP_TRY(hipMemcpy(s->cols, bins_fm, (size_t)n * F, hipMemcpyHostToDevice));
+        } else {
+            std::vector<uint8_t> tmp;
+            const uint64_t step = 1ull << 26;
+            for (uint64_t off = 0, total = n * F; off < total; off += step) {
+                const uint64_t m = std::min(step, total - off);
+                tmp.resize(m);
+                for (uint64_t i = 0; i < m; ++i) tmp[i] = (uint8_t)bins_fm[off + i];
+                HIP_TRY(hipMemcpy(s->cols + off, tmp.data(), m, hipMemcpyHostToDevice));
+            }
+        }
+        return CBH_OK;
+    });
+}
+
+// Raw float channel: every column is staged on the device and quantized there into the
+// session's feature-major bins (one quantize launch per column on the session stream).
+int session_begin_raw_impl(const cbh_config* cfg, const float* const* columns, const double* const* borders,
+                           const uint32_t* n_borders, const double* weight, uint64_t n, uint32_t F,
+                           uint32_t n_bins, double lr, double l2, cbh_session** out) {
+    if (!out) return fail(CBH_ERR_INVALID_ARG, "out is null");
+    *out = nullptr;
+    CHECK(validate_config(cfg, n_bins, n, F));
+    if (!columns || !borders || !n_borders) return fail(CBH_ERR_INVALID_ARG, "columns / borders / n_borders is null");
+    if (cfg->one_hot_flags)
+        for (uint32_t f = 0; f < F; ++f)
+            if (cfg->one_hot_flags[f]) return fail(CBH_ERR_UNSUPPORTED, "the raw float channel carries no one-hot columns");
+    std::vector<uint64_t> off(F + 1, 0);
+    for (uint32_t f = 0; f < F; ++f) {
+        if (n && !columns[f]) return fail(CBH_ERR_INVALID_ARG, "column " + std::to_string(f) + " is null");
+        if (n_borders[f] && !borders[f]) return fail(CBH_ERR_INVALID_ARG, "borders of feature " + std::to_string(f) + " are null");
+        if (n_borders[f] + 1 > n_bins)
+            return fail(CBH_ERR_OUT_OF_RANGE, "feature " + std::to_string(f) + " has more borders than n_bins - 1");
+        for (uint32_t k = 1; k < n_borders[f]; ++k)
+            if (!(borders[f][k - 1] < borders[f][k]))
+                return fail(CBH_ERR_OUT_OF_RANGE, "borders of feature " + std::to_string(f) + " do not ascend");
+        off[f + 1] = off[f] + n_borders[f];
+    }
+    // candidate folds follow the borders (real_folds = borders + 1, boosting.rs:4334-4372)
+    // unless the caller gives them
+    std::vector<uint32_t> folds(F);
+    for (uint32_t f = 0; f < F; ++f) folds[f] = n_borders[f] + 1;
+    cbh_config c = *cfg;
+    if (!c.real_folds) c.real_folds = folds.data();
+    return session_open(&c, weight, n, F, n_bins, lr, l2, out, [&](cbh_session* s) -> int {
+        if (n == 0 || F == 0) return CBH_OK;
+        std::vector<double> flat(std::max<uint64_t>(off[F], 1));
+        for (uint32_t f = 0; f < F; ++f)
+            if (n_borders[f]) std::memcpy(flat.data() + off[f], borders[f], sizeof(double) * n_borders[f]);
+        double* db = nullptr;
+        float* stage = nullptr;
+        int rc = CBH_OK;
+        if (hipMalloc((void**)&db, sizeof(double) * flat.size()) != hipSuccess ||
+            hipMalloc((void**)&stage, sizeof(float) * n) != hipSuccess) {
+            rc = fail(CBH_ERR_DEVICE, "staging allocation failed");
+        }
+        if (rc == CBH_OK && hipMemcpy(db, flat.data(), sizeof(double) * flat.size(), hipMemcpyHostToDevice) != hipSuccess)
+            rc = fail(CBH_ERR_DEVICE, "border upload failed");
+        for (uint32_t f = 0; rc == CBH_OK && f < F; ++f) {
+            if (hipMemcpyAsync(stage, columns[f], sizeof(float) * n, hipMemcpyHostToDevice, s->stream) != hipSuccess) {
+                rc = fail(CBH_ERR_DEVICE, "column upload failed");
+                break;
+            }
+            rc = cbh_internal_quantize(stage, n, db + off[f], n_borders[f], s->cols + (size_t)f * n, s->stream);
+        }
+        if (hipStreamSynchronize(s->stream) != hipSuccess && rc == CBH_OK) rc = fail(CBH_ERR_DEVICE, "quantize failed");
+        if (db) (void)hipFree(db);
+        if (stage) (void)hipFree(stage);
+        return rc;
+    });
+}
+
+template <typename Load>
+int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32_t F, uint32_t n_bins,
+                 double lr, double l2, cbh_session** out, Load&& load_cols) {
     std::unique_ptr<cbh_session> s(new cbh_session());
     s->cfg = *cfg;
     if (cfg->one_hot_flags) s->one_hot_host.assign(cfg->one_hot_flags, cfg->one_hot_flags + F);
@@ -473,19 +557,8 @@ int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double*
         CHECK(dalloc(&s->one_hot, F));
         HIP_TRY(hipMemcpy(s->one_hot, s->one_hot_host.data(), F, hipMemcpyHostToDevice));
     }
-    // upload bins feature-major as u8, then pack the row-major words on the device
-    if (sizeof(BinT) == 1) {
-        HIP_TRY(hipMemcpy(s->cols, bins_fm, (size_t)n * F, hipMemcpyHostToDevice));
-    } else {
-        std::vector<uint8_t> tmp;
-        const uint64_t step = 1ull << 26;
-        for (uint64_t off = 0, total = n * F; off < total; off += step) {
-            const uint64_t m = std::min(step, total - off);
-            tmp.resize(m);
-            for (uint64_t i = 0; i < m; ++i) tmp[i] = (uint8_t)bins_fm[off + i];
-            HIP_TRY(hipMemcpy(s->cols + off, tmp.data(), m, hipMemcpyHostToDevice));
-        }
-    }
+    // feature-major u8 bins in place, then pack the row-major words on the device
+    CHECK(load_cols(s.get()));
     pack_rows_kernel<<<grid_for((uint64_t)n * s->W, 256), 256, 0, s->stream>>>(s->cols, n, F, s->W, s->rows);
     HIP_TRY(hipGetLastError());
     CHECK(plan_skip_bins(s.get()));
@@ -830,6 +903,13 @@ int cbh_session_begin_u8(const cbh_config* cfg, const uint8_t* bins_fm, const do
                          double scaled_l2, cbh_session** out) {
     return session_begin_impl<uint8_t>(cfg, bins_fm, weight, n, n_features, n_bins, learning_rate,
                                        scaled_l2, out);
+}
+
+int cbh_session_begin_raw(const cbh_config* cfg, const float* const* columns, const double* const* borders,
+                          const uint32_t* n_borders, const double* weight, uint64_t n, uint32_t n_features,
+                          uint32_t n_bins, double learning_rate, double scaled_l2, cbh_session** out) {
+    return session_begin_raw_impl(cfg, columns, borders, n_borders, weight, n, n_features, n_bins,
+                                  learning_rate, scaled_l2, out);
 }
 
 int cbh_session_grow(cbh_session* s, const double* approx, const double* target, uint64_t n,

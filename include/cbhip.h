@@ -45,6 +45,9 @@ enum {
 enum { CBH_SCORE_COSINE = 0, CBH_SCORE_L2 = 1 };
 enum { CBH_LEAF_GRADIENT = 0, CBH_LEAF_NEWTON = 1, CBH_LEAF_SIMPLE = 2 };
 enum { CBH_BOOT_NO = 0, CBH_BOOT_BAYESIAN = 1, CBH_BOOT_BERNOULLI = 2 };
+/* float-feature preparation (crates/cb-data/src/borders.rs, nan_mode.rs) */
+enum { CBH_BORDERS_GREEDY_LOGSUM = 0, CBH_BORDERS_GREEDY_MIN_ENTROPY = 1 };
+enum { CBH_NAN_MIN = 0, CBH_NAN_MAX = 1, CBH_NAN_FORBIDDEN = 2 };
 
 /* Mirrors DeviceTrainConfig (runtime.rs:1260-1341) plus the scalar arguments of
  * begin_device_training (runtime.rs:1497-1529).  Fields the device path does not cover
@@ -92,6 +95,21 @@ int cbh_session_begin(const cbh_config* cfg, const uint32_t* bins_fm, const doub
 int cbh_session_begin_u8(const cbh_config* cfg, const uint8_t* bins_fm, const double* weight,
                          uint64_t n, uint32_t n_features, uint32_t n_bins, double learning_rate,
                          double scaled_l2, cbh_session** out);
+
+/* Same, over the RAW float channel: the device quantizes the f32 columns with the
+ * per-feature borders and packs the resident rows itself, so no host bin matrix exists.
+ * Mirrors begin_device_training_raw (runtime.rs:1546-1580; device quantize twin
+ * quantize_pack_feature_kernel, crates/cb-backend/src/kernels.rs:2852):
+ *   columns   [n_features] pointers to n f32 values
+ *   borders   [n_features] pointers to n_borders[f] ascending f64 borders (a border set
+ *             ending with f32::MAX sends NaN to the top bin, else NaN goes to bin 0)
+ *   n_bins    >= n_borders[f] + 1 for every f, <= 256
+ * The resident bins equal bin_of (crates/cb-compute/src/histogram.rs:563-569) of every
+ * value.  One-hot columns are not part of this channel (cfg->one_hot_flags must be NULL). */
+int cbh_session_begin_raw(const cbh_config* cfg, const float* const* columns,
+                          const double* const* borders, const uint32_t* n_borders,
+                          const double* weight, uint64_t n, uint32_t n_features, uint32_t n_bins,
+                          double learning_rate, double scaled_l2, cbh_session** out);
 
 /* Per-tree device-resident sampling: the device regenerates exactly the sample the host
  * bootstrap() would draw at the current host RNG phase (bootstrap.rs:402-466), so no
@@ -213,6 +231,30 @@ int cbh_apply_oblivious(const float* features_fm, uint64_t n_objects, uint32_t n
                         const uint32_t* tree_split_offsets, const double* leaf_values,
                         const uint32_t* tree_leaf_offsets, uint32_t n_trees, uint32_t approx_dim,
                         const double* bias, const uint8_t* nan_as_true, double* out);
+
+/* Greedy border selection of float columns; mirrors Pool::quantize's border step
+ * (crates/cb-data/src/quantize.rs:74-110) over select_borders_greedy_logsum_f32 and its
+ * GreedyMinEntropy twin (crates/cb-data/src/borders.rs:298-420):
+ *   columns         [n_features] pointers to n f32 values (NaN allowed)
+ *   border_count    budget per feature (the Min sentinel takes one slot); at most 255, 254
+ *                   under CBH_NAN_MAX (its f32::MAX sentinel is appended on top)
+ *   nan_mode        CBH_NAN_*: applied to a column holding at least one NaN; a NaN-free
+ *                   column has no sentinel
+ *   border_type     CBH_BORDERS_*
+ *   borders_out     [n_features][border_count + 1] f64; feature f's n_borders_out[f]
+ *                   ascending borders (f32-exact values) lead its row
+ * Columns over 200000 rows use the fixed-seed 200000-row subset of the reference
+ * (sample_indices_for_build_borders, borders.rs:504-516).  The subset's values are sorted
+ * on the device; the greedy split runs on the host. */
+int cbh_select_borders(const float* const* columns, uint64_t n, uint32_t n_features,
+                       uint32_t border_count, int32_t nan_mode, int32_t border_type,
+                       double* borders_out, uint32_t* n_borders_out);
+
+/* Quantize one f32 column into u8 bins on the device: bin_of (histogram.rs:563-569) --
+ * the count of borders strictly below the value; NaN to the top bin when the borders end
+ * with f32::MAX, else to bin 0.  At most 255 ascending borders. */
+int cbh_quantize(const float* column, uint64_t n, const double* borders, uint32_t n_borders,
+                 uint8_t* bins_out);
 
 /* Version / build information. */
 const char* cbh_version(void);

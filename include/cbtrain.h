@@ -45,6 +45,13 @@ int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t n
              uint32_t n_bins, const uint32_t* real_folds, const uint8_t* one_hot_flags,
              const double* target, const double* weight, cbt_trainer** out);
 
+/* Open over the raw float channel (the trainer's float-only first choice,
+ * runtime.rs:1530-1545): f32 columns + per-feature borders; the device quantizes.
+ * n_bins = max(n_borders) + 1; candidate folds per feature = n_borders[f] + 1. */
+int cbt_open_raw(const cbt_params* p, const float* const* columns, const double* const* borders,
+                 const uint32_t* n_borders, uint64_t n, uint32_t n_features, const double* target,
+                 const double* weight, cbt_trainer** out);
+
 /* PairLogit / PairLogitPairwise: the query groups and explicit pairs of the pool (copied;
  * call once after cbt_open, before the first cbt_step).  See cbh_family. */
 int cbt_set_pairs(cbt_trainer* t, const uint32_t* group_offsets, uint32_t n_groups,

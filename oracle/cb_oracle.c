@@ -900,6 +900,131 @@ static void pairwise_center(double* v, const double* leaf_w, uint32_t n_leaves) 
 }
 
 /* ======================================================================
+ * Border selection: GreedyLogSum / GreedyMinEntropy (crates/cb-data/src/borders.rs,
+ * restating catboost's library/cpp/grid_creator/binarization.cpp).
+ * ==================================================================== */
+#define ORC_MAX_SUBSET_FOR_BORDERS 200000 /* borders.rs:48 */
+
+/* sample_indices_for_build_borders (borders.rs:504-516): partial Fisher-Yates with
+ * TFastRng64::from_seed(0), ascending index set. */
+void orc_sample_indices_for_borders(uint64_t n, uint64_t sample_size, uint32_t* out) {
+    uint32_t* idx = (uint32_t*)malloc(sizeof(uint32_t) * (n ? n : 1));
+    for (uint64_t i = 0; i < n; ++i) idx[i] = (uint32_t)i;
+    orc_rng r;
+    orc_rng_from_seed(&r, 0);
+    uint64_t take = sample_size < n ? sample_size : n;
+    for (uint64_t i = 0; i < take; ++i) {
+        uint64_t off = orc_rng_uniform(&r, n - i);
+        uint32_t t = idx[i]; idx[i] = idx[i + off]; idx[i + off] = t;
+    }
+    /* ascending */
+    uint8_t* mark = (uint8_t*)calloc(n ? n : 1, 1);
+    for (uint64_t i = 0; i < take; ++i) mark[idx[i]] = 1;
+    uint64_t k = 0;
+    for (uint64_t i = 0; i < n; ++i) if (mark[i]) out[k++] = (uint32_t)i;
+    free(mark);
+    free(idx);
+}
+
+static double border_penalty(int kind, double w) { /* borders.rs:51-62 */
+    return kind == 0 ? -log(w + 1e-8) : w * log(w + 1e-8);
+}
+
+typedef struct { uint64_t start, end, best; double score; uint64_t seq; } orc_gbin;
+
+static uint64_t lb_f32(const float* v, uint64_t lo, uint64_t hi, float t) { /* borders.rs:228 */
+    while (lo < hi) { uint64_t mid = lo + (hi - lo) / 2; if (v[mid] < t) lo = mid + 1; else hi = mid; }
+    return lo;
+}
+static uint64_t ub_f32(const float* v, uint64_t lo, uint64_t hi, float t) { /* borders.rs:244 */
+    while (lo < hi) { uint64_t mid = lo + (hi - lo) / 2; if (v[mid] <= t) lo = mid + 1; else hi = mid; }
+    return lo;
+}
+static double gbin_score(const orc_gbin* b, uint64_t pos, int kind) { /* CalcSplitScore */
+    if (pos == b->start || pos == b->end) return -INFINITY;
+    double left = -border_penalty(kind, (double)(pos - b->start));
+    double right = -border_penalty(kind, (double)(b->end - pos));
+    double curr = -border_penalty(kind, (double)(b->end - b->start));
+    return left + right - curr;
+}
+static void gbin_update(orc_gbin* b, const float* v, int kind) { /* UpdateBestSplitProperties */
+    uint64_t mid = b->start + (b->end - b->start) / 2;
+    float mv = v[mid];
+    uint64_t lb = lb_f32(v, b->start, mid, mv);
+    uint64_t ub = ub_f32(v, mid, b->end, mv);
+    double sl = gbin_score(b, lb, kind), sr = gbin_score(b, ub, kind);
+    if (sl >= sr) { b->best = lb; b->score = sl; } else { b->best = ub; b->score = sr; }
+}
+
+static int cmp_f32(const void* a, const void* b) {
+    float x = *(const float*)a, y = *(const float*)b;
+    return x < y ? -1 : (x > y ? 1 : 0);
+}
+
+/* Greedy border selection of one column (borders.rs:298-345 + 400-470 + 572-640):
+ * values with NaNs, sampled when n > 200000; returns the count written to out
+ * (<= border_count, sentinel f32::MIN first when nan_sentinel). kind 0 = MaxSumLog
+ * (GreedyLogSum), 1 = MinEntropy (GreedyMinEntropy). */
+uint32_t orc_select_borders_greedy(const float* column, uint64_t n, uint32_t border_count,
+                                   int32_t nan_sentinel, int32_t kind, double* out) {
+    float* v = (float*)malloc(sizeof(float) * (n ? n : 1));
+    uint64_t m = 0;
+    if (n > ORC_MAX_SUBSET_FOR_BORDERS) {
+        uint32_t* s = (uint32_t*)malloc(sizeof(uint32_t) * ORC_MAX_SUBSET_FOR_BORDERS);
+        orc_sample_indices_for_borders(n, ORC_MAX_SUBSET_FOR_BORDERS, s);
+        for (uint64_t i = 0; i < ORC_MAX_SUBSET_FOR_BORDERS; ++i)
+            if (!isnan(column[s[i]])) v[m++] = column[s[i]];
+        free(s);
+    } else {
+        for (uint64_t i = 0; i < n; ++i) if (!isnan(column[i])) v[m++] = column[i];
+    }
+    qsort(v, m, sizeof(float), cmp_f32);
+    uint32_t budget = nan_sentinel ? (border_count > 0 ? border_count - 1 : 0) : border_count;
+    float* b32 = (float*)malloc(sizeof(float) * (budget + 2));
+    uint32_t nb = 0;
+    if (m >= 2) {
+        orc_gbin* q = (orc_gbin*)malloc(sizeof(orc_gbin) * (budget + 3));
+        uint64_t nq = 0, seq = 0;
+        q[0].start = 0; q[0].end = m; q[0].seq = seq++;
+        gbin_update(&q[0], v, kind);
+        nq = 1;
+        while (nq <= budget) {
+            /* top: highest score, earliest insertion on ties (borders.rs:600-640) */
+            uint64_t top = 0;
+            for (uint64_t i = 1; i < nq; ++i)
+                if (q[i].score > q[top].score || (q[i].score == q[top].score && q[i].seq < q[top].seq)) top = i;
+            if (!(q[top].start != q[top].best && q[top].end != q[top].best)) break;
+            orc_gbin t = q[top];
+            q[top] = q[nq - 1];
+            --nq;
+            orc_gbin left;
+            left.start = t.start; left.end = t.best; left.seq = seq++;
+            gbin_update(&left, v, kind);
+            t.start = t.best; t.seq = seq++;
+            gbin_update(&t, v, kind);
+            q[nq++] = left;
+            q[nq++] = t;
+        }
+        for (uint64_t i = 0; i < nq; ++i) {
+            if (q[i].start == 0) continue;
+            float border = 0.5f * v[q[i].start - 1];
+            border += 0.5f * v[q[i].start];
+            if (border == 0.0f) border = 0.0f;  /* -0 -> +0 */
+            b32[nb++] = border;
+        }
+        free(q);
+    }
+    qsort(b32, nb, sizeof(float), cmp_f32);
+    uint32_t k = 0;
+    if (nan_sentinel) out[k++] = (double)(-3.40282346638528859812e+38F);
+    for (uint32_t i = 0; i < nb; ++i)
+        if (i == 0 || b32[i] != b32[i - 1]) out[k++] = (double)b32[i];
+    free(b32);
+    free(v);
+    return k;
+}
+
+/* ======================================================================
  * Model apply (crates/cb-model/src/apply.rs predict_raw_one; device twin
  * crates/cb-backend/src/kernels.rs:629 apply_oblivious_float_kernel): per object, each
  * tree's leaf from its float splits (value > border, forward bit order; NaN passes only

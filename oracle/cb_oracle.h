@@ -134,6 +134,12 @@ void orc_pairwise_leaf_deltas(const uint32_t* leaf_of, uint64_t n, const double*
                               const uint32_t* winner, const uint32_t* loser, const double* weight,
                               uint64_t m, uint32_t n_leaves, double l2, double prior, double* out);
 
+/* ---- border selection (cb-data/src/borders.rs) ----
+ * out has room for border_count + 1 values; returns the count written. */
+void orc_sample_indices_for_borders(uint64_t n, uint64_t sample_size, uint32_t* out);
+uint32_t orc_select_borders_greedy(const float* column, uint64_t n, uint32_t border_count,
+                                   int32_t nan_sentinel, int32_t kind, double* out);
+
 /* ---- model apply (cb-model/src/apply.rs; device kernels.rs:629) ----
  * Float splits, CSR per tree; leaf values [(tree_leaf_offsets[t] + leaf) * K + d]; out [K][n]. */
 int orc_apply_oblivious(const float* x_fm, uint64_t n, uint32_t F, const uint32_t* split_features,

@@ -87,6 +87,9 @@ def lib():
         L.orc_grow_tree_pairwise.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, P, P, C.c_uint64,
                                              C.c_int32, C.c_double, C.c_double, C.c_int32, P, P, P]
         L.orc_grow_tree_pairwise.restype = C.c_int
+        L.orc_sample_indices_for_borders.argtypes = [C.c_uint64, C.c_uint64, P]
+        L.orc_select_borders_greedy.argtypes = [P, C.c_uint64, C.c_uint32, C.c_int32, C.c_int32, P]
+        L.orc_select_borders_greedy.restype = C.c_uint32
         L.orc_apply_oblivious.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, P, C.c_uint32,
                                           C.c_uint32, P, P, P]
         L.orc_apply_oblivious.restype = C.c_int
@@ -257,6 +260,24 @@ def pairwise_leaf_deltas(leaf_of, der, winner, loser, weight, n_leaves, l2, prio
     out = np.zeros(n_leaves)
     lib().orc_pairwise_leaf_deltas(_p(lo), lo.shape[0], _p(d), _p(w), _p(l), _p(wt), w.shape[0],
                                    n_leaves, l2, prior, _p(out))
+    return out
+
+
+PENALTY = {"GreedyLogSum": 0, "GreedyMinEntropy": 1}
+
+
+def select_borders(column, border_count, nan_sentinel=False, kind="GreedyLogSum"):
+    """Greedy border set of one f32 column (NaNs allowed; sampled above 200000 rows)."""
+    c = np.ascontiguousarray(column, np.float32)
+    out = np.zeros(border_count + 1)
+    k = lib().orc_select_borders_greedy(_p(c), c.shape[0], border_count, int(nan_sentinel),
+                                        PENALTY[kind], _p(out))
+    return out[:k].copy()
+
+
+def sample_indices_for_borders(n, sample_size=200_000):
+    out = np.zeros(min(n, sample_size), np.uint32)
+    lib().orc_sample_indices_for_borders(n, sample_size, _p(out))
     return out
 
 

@@ -22,6 +22,11 @@ expected outputs); no reference source is copied.  Sources:
 * ``upstream_one_hot_*``  -- catboost 1.2.10 one-hot fits (one_hot_train/*): float inputs,
                              categorical columns as first-seen bins, used borders, splits
                              (one-hot values as bins), leaf values, predictions.
+* ``borders.npz/.json``   -- catboost 1.2.10 standalone quantization borders
+                             (Pool.quantize().save_quantization_borders()) of the greedy
+                             border types: border_types/<dataset>.bc<k>.Greedy* and
+                             borders_quant/numeric_{tiny,nan} (border_count 254), with the
+                             input matrices they were computed from.
 """
 from __future__ import annotations
 
@@ -193,6 +198,37 @@ def ranking(ref):
     np.savez_compressed(os.path.join(HERE, "upstream_ranking.npz"), **arrays)
 
 
+def borders(ref):
+    """Greedy border cells of border_types/ and borders_quant/ plus their input matrices."""
+    fx = os.path.join(ref, "crates/cb-oracle/fixtures")
+    inputs = {"borders_dense": "inputs/borders_dense", "borders_runs": "inputs/borders_runs",
+              "numeric_nan": "inputs/numeric_nan", "numeric_tiny": "inputs/numeric_tiny",
+              "float_only_byte_identity": "float_only_byte_identity/inputs"}
+    arrays = {"X_" + d: np.load(os.path.join(fx, rel, "X.npy")) for d, rel in inputs.items()}
+    cells = []
+    cfg = json.load(open(os.path.join(fx, "border_types", "config.json")))
+    for stem, sc in sorted(cfg["scenarios"].items()):
+        if sc["feature_border_type"] not in ("GreedyLogSum", "GreedyMinEntropy"):
+            continue
+        b = np.load(os.path.join(fx, "border_types", stem + ".borders.npy"))
+        per = np.load(os.path.join(fx, "border_types", stem + ".borders_per_feature.npy"))
+        arrays[stem + ".borders"] = b
+        arrays[stem + ".per_feature"] = per.astype(np.int64)
+        cells.append({"stem": stem, "dataset": sc["dataset"], "border_count": sc["border_count"],
+                      "border_type": sc["feature_border_type"], "nan_mode": sc["nan_mode"]})
+    qcfg = json.load(open(os.path.join(fx, "borders_quant", "config.json")))
+    for d, sc in sorted(qcfg["scenarios"].items()):
+        stem = "borders_quant." + d
+        arrays[stem + ".borders"] = np.load(os.path.join(fx, "borders_quant", d + ".borders.npy"))
+        arrays[stem + ".per_feature"] = np.load(
+            os.path.join(fx, "borders_quant", d + ".borders_per_feature.npy")).astype(np.int64)
+        cells.append({"stem": stem, "dataset": sc["input_dataset"], "border_count": sc["border_count"],
+                      "border_type": sc["border_selection_type"], "nan_mode": sc["nan_mode"]})
+    np.savez_compressed(os.path.join(HERE, "borders.npz"), **arrays)
+    json.dump({"catboost_version": cfg.get("catboost_version"), "cells": cells},
+              open(os.path.join(HERE, "borders.json"), "w"), indent=1)
+
+
 def main():
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     rng_kat(ref)
@@ -203,6 +239,7 @@ def main():
     for s in ("default_binary", "multi"):
         one_hot_train(ref, s)
     ranking(ref)
+    borders(ref)
 
 
 if __name__ == "__main__":

@@ -83,3 +83,19 @@ def ranking(loss: str):
                 split_feature=z[loss + "_split_feature"], split_border=z[loss + "_split_border"],
                 leaf_values=z[loss + "_leaf_values"], staged=z[loss + "_staged"],
                 predictions=z[loss + "_predictions"], config=cfg)
+
+
+def borders():
+    """catboost 1.2.10 standalone greedy border sets: (cells, matrices) where each cell is a
+    dict(stem, dataset, border_count, border_type, nan_mode, borders=[per-feature arrays])
+    and matrices maps a dataset name to its f64 input matrix [n][F]."""
+    z = np.load(os.path.join(GOLDEN, "borders.npz"))
+    meta = json.load(open(os.path.join(GOLDEN, "borders.json")))
+    mats = {k[2:]: z[k] for k in z.files if k.startswith("X_")}
+    cells = []
+    for c in meta["cells"]:
+        per = z[c["stem"] + ".per_feature"]
+        offs = np.concatenate([[0], np.cumsum(per)])
+        flat = z[c["stem"] + ".borders"]
+        cells.append(dict(c, borders=[flat[offs[i]:offs[i + 1]] for i in range(len(per))]))
+    return cells, mats

@@ -103,3 +103,35 @@ def test_one_hot_with_bootstrap_is_refused(lib):
         cb.Trainer(bins, 2, np.zeros(8), loss="RMSE", depth=2, bootstrap_type="Bernoulli",
                    one_hot_flags=np.array([0, 1], np.uint8), real_folds=np.array([2, 2], np.uint32))
     assert e.value.code == -4
+
+
+def test_float_preparation_argument_checks(lib):
+    """Border selection, quantization and the raw float channel validate their arguments
+    before any device call (typed errors, no fault)."""
+    import numpy as np
+    col = np.array([[0.0, 1.0, 2.0, 3.0]], np.float32)
+    for kw, code in ((dict(border_count=0), -2), (dict(border_count=255, nan_mode="Max"), -2),
+                     (dict(border_count=256), -2)):
+        with pytest.raises(cb.CbhError) as e:
+            cb.select_borders(col, **kw)
+        assert e.value.code == code
+    with pytest.raises(KeyError):
+        cb.select_borders(col, border_type="Median")
+    with pytest.raises(cb.CbhError) as e:
+        cb.quantize(col[0], np.array([2.0, 1.0]))
+    assert e.value.code == -2
+    with pytest.raises(cb.CbhError) as e:
+        cb.quantize(col[0], np.arange(256.0))
+    assert e.value.code == -2
+
+    def raw(borders, n_bins=4, **cfg_kw):
+        be = cb.HipBackend()
+        return be.begin_device_training_raw("RMSE", 2, True, 1, "Cosine", col, borders, None, 4, 1,
+                                            n_bins, 0.1, 3.0, **cfg_kw)
+
+    with pytest.raises(cb.CbhError) as e:
+        raw([np.array([1.0, 0.5])])
+    assert e.value.code == -2  # borders must ascend
+    with pytest.raises(cb.CbhError) as e:
+        raw([np.array([0.5, 1.5, 2.5, 3.5])])
+    assert e.value.code == -2  # n_borders + 1 > n_bins

@@ -425,3 +425,114 @@ def test_apply_nan_and_absent_features():
                 exp[:, i] += lv[t][leaf * K:(leaf + 1) * K]
     exp += np.array([0.5, -0.25])[:, None]
     np.testing.assert_allclose(out, exp, rtol=1e-14, atol=1e-14)
+
+
+# --------------------------------------------------------------------------------------
+# float-feature preparation: greedy borders and bin_of
+# --------------------------------------------------------------------------------------
+F32_MAX = float(np.finfo(np.float32).max)
+
+
+def oracle_borders_of(col, border_count, nan_mode, kind):
+    """Pool::quantize's per-feature border step (quantize.rs:74-110) over the oracle."""
+    has_nan = bool(np.isnan(col).any())
+    b = O.select_borders(col, border_count, has_nan and nan_mode == "Min", kind)
+    if has_nan and nan_mode == "Max":
+        b = np.append(b, F32_MAX)
+    return b
+
+
+def test_borders_match_upstream_fixtures():
+    """Every greedy cell of border_types/ and borders_quant/ (catboost 1.2.10 standalone
+    quantization) reproduced exactly, per feature."""
+    cells, mats = G.borders()
+    assert len(cells) == 20
+    for c in cells:
+        X = mats[c["dataset"]].astype(np.float32)
+        for f, want in enumerate(c["borders"]):
+            got = oracle_borders_of(X[:, f], c["border_count"], c["nan_mode"], c["border_type"])
+            assert np.array_equal(got.astype(np.float32), want.astype(np.float32)), (c["stem"], f)
+
+
+def test_borders_tiny_known_answers():
+    # two distinct values -> one border, the f32 midpoint (borders_test.rs two-value case)
+    assert O.select_borders(np.array([-1.0, 1.0], np.float32), 8).tolist() == [0.0]
+    b = O.select_borders(np.array([1.0, 2.0], np.float32), 8)
+    assert b.tolist() == [float(np.float32(0.5) * np.float32(1) + np.float32(0.5) * np.float32(2))]
+    # constant, empty and all-NaN columns have no border; the Min sentinel still leads
+    assert O.select_borders(np.full(10, 3.0, np.float32), 8).size == 0
+    assert O.select_borders(np.zeros(0, np.float32), 8).size == 0
+    assert O.select_borders(np.full(4, np.nan, np.float32), 8, True).tolist() == [
+        float(np.finfo(np.float32).min)]
+    # -0/+0 midpoint normalizes to +0
+    z = O.select_borders(np.array([-0.0, -0.0, 0.0, 1.0], np.float32), 8)
+    assert all(np.copysign(1.0, v) > 0 for v in z if v == 0.0)
+
+
+def test_borders_are_order_free_and_budgeted():
+    """A pure function of the value multiset; never over budget; ascending; inside range."""
+    rng = np.random.default_rng(3)
+    col = np.round(rng.normal(size=3000) * 4).astype(np.float32) / 4
+    for k in (1, 2, 7, 31, 128, 254):
+        a = O.select_borders(col, k)
+        assert a.size <= k and np.all(np.diff(a) > 0)
+        assert a[0] > col.min() and a[-1] < col.max()
+        assert np.array_equal(a, O.select_borders(col[::-1].copy(), k))
+        assert np.array_equal(a, O.select_borders(rng.permutation(col), k))
+    # budget reached on a column with enough distinct values; one slot goes to the sentinel
+    u = np.arange(1000, dtype=np.float32)
+    assert O.select_borders(u, 31).size == 31
+    assert O.select_borders(np.append(u, np.nan).astype(np.float32), 31, True).size == 31
+
+
+def test_border_sample_is_a_fixed_seed_fisher_yates():
+    """sample_indices_for_build_borders (borders.rs:504-516): partial Fisher-Yates over
+    TFastRng64.from_seed(0) (uniform() pinned by the rng known answers), sorted."""
+    n, k = 200_000 + 7_345, 200_000
+    idx = np.arange(n, dtype=np.int64)
+    r = O.rng_from_seed(0)
+    for i in range(k):
+        off = O.lib().orc_rng_uniform(C.byref(r), n - i)
+        idx[i], idx[i + off] = idx[i + off], idx[i]
+    want = np.sort(idx[:k])
+    got = O.sample_indices_for_borders(n)
+    assert np.array_equal(got.astype(np.int64), want)
+    assert np.array_equal(O.sample_indices_for_borders(1000), np.arange(1000))
+
+
+def test_oversized_column_is_subsampled_before_nan_drop():
+    """Above 200000 rows the borders come from the sampled objects, NaN dropped after the
+    draw (borders_test.rs presampled case) -- and the smooth-column quality bound of
+    borders_test.rs (g): 31 borders, each within 0.01 of the uniform quantile."""
+    n = 200_000 * 2 + 12_345
+    i = np.arange(n, dtype=np.uint64)
+    h = i * np.uint64(0x9E3779B97F4A7C15)
+    h = (h << np.uint64(31)) | (h >> np.uint64(33))
+    col = ((h >> np.uint64(40)).astype(np.float32) / np.float32(1 << 24)) * np.float32(2e3) - np.float32(1e3)
+    col[(h % np.uint64(7)) == 0] = 42.5
+    col[(h % np.uint64(100)) == 0] = np.nan
+    s = O.sample_indices_for_borders(n)
+    assert np.array_equal(O.select_borders(col, 31), O.select_borders(col[s], 31))
+    n3 = 600_000
+    j = np.arange(n3, dtype=np.uint64)
+    g = j * np.uint64(0x9E3779B97F4A7C15)
+    g = (g << np.uint64(31)) | (g >> np.uint64(33))
+    smooth = (g >> np.uint64(40)).astype(np.float32) / np.float32(1 << 24)
+    a = O.select_borders(smooth, 31)
+    assert a.size == 31
+    assert np.all(np.abs(a - (np.arange(31) + 1) / 32.0) < 0.01)
+
+
+def test_quantize_is_bin_of():
+    """bin_of (histogram.rs:563-569) by brute force: count of borders strictly below the
+    value; NaN to the top bin behind an f32::MAX last border, else bin 0."""
+    rng = np.random.default_rng(5)
+    b = np.unique(rng.normal(size=40).astype(np.float32)).astype(np.float64)
+    v = np.concatenate([rng.normal(size=500).astype(np.float32), b.astype(np.float32),
+                        np.array([np.nan, np.inf, -np.inf, 0.0, -0.0], np.float32)])
+    brute = np.array([0 if np.isnan(x) else int(np.sum(b < float(x))) for x in v])
+    assert np.array_equal(O.quantize(v, b), brute)
+    bm = np.append(b, F32_MAX)
+    brute_m = np.array([len(bm) if np.isnan(x) else int(np.sum(bm < float(x))) for x in v])
+    assert np.array_equal(O.quantize(v, bm), brute_m)
+    assert O.quantize(v, np.zeros(0)).max() == 0
