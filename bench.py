@@ -88,6 +88,74 @@ def _train_kwargs(P):
                 random_seed=P.get("random_seed", 0), approx_dim=P.get("approx_dim", 1))
 
 
+def prep_bench(args):
+    """Float-feature preparation at config 2's size (10M x 200 f32 columns, 254 GreedyLogSum
+    borders): device border selection (host subset gather, device NaN drop + segmented
+    radix sort, host greedy heap) and the raw-channel session open (PCIe upload + device
+    quantize + row packing).  The quantize kernel's roofline comes from HIP events around
+    its launches (algorithmic bytes: 4 read + 1 written per value)."""
+    import numpy as np
+
+    import catboost_rs_amd as cb
+    from catboost_rs_amd import datagen
+
+    n, F = args.rows or 10_000_000, args.features or 200
+    t0 = time.perf_counter()
+    X = datagen.config2_floats(n, F)
+    y = np.zeros(n)
+    log(f"prep data: {n} x {F} f32 generated in {time.perf_counter() - t0:.1f}s")
+    cb.select_borders(X[:2, :1000], 254)  # load the library / first-use costs
+    sel = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        borders = cb.select_borders(X, 254, "Min")
+        sel.append(time.perf_counter() - t0)
+    sel_s = min(sel)
+    log(f"select_borders: {', '.join(f'{v:.3f}' for v in sel)} s")
+    opens, st = [], None
+    for _ in range(2):
+        t0 = time.perf_counter()
+        tr = cb.Trainer.from_floats(X, borders, y, loss="Logloss", depth=6, profile=True)
+        opens.append(time.perf_counter() - t0)
+        st = tr.stats()
+        tr.close()
+    open_s = min(opens)
+    q_s = st["quantize_ms"] / 1000.0
+    q_gbs = st["quantize_bytes"] / 1e9 / q_s if q_s > 0 else 0.0
+    log(f"raw open: {', '.join(f'{v:.3f}' for v in opens)} s; quantize {st['quantize_launches']} launches, "
+        f"{st['quantize_ms']:.3f} ms, {q_gbs:.1f} GB/s algorithmic")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+
+        k = 4
+        t0 = time.perf_counter()
+        cpu_b = [O.select_borders(X[f], 254, bool(np.isnan(X[f]).any())) for f in range(k)]
+        for f in range(k):
+            O.quantize(X[f], cpu_b[f])
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(k / cpu_s, 4), "unit": "columns/s", "cores": 1, "kind": "port",
+               "sample": f"borders + quantize of the first {k} of the same {n}-row columns "
+                         "(CPU restatement: greedy borders over the 200000-row subset, bin_of)",
+               "borders_match_gpu": all(np.array_equal(a, b) for a, b in zip(cpu_b, borders[:k]))}
+        log(f"cpu: {k} columns in {cpu_s:.1f}s")
+    out = {
+        "metric": "float feature preparation (greedy borders + quantize + pack), columns/s",
+        "value": round(F / (sel_s + open_s), 3), "unit": "columns/s", "n_gpus": 1,
+        "higher_is_better": True, "dtype": "f32 values, f64 borders, u8 bins",
+        "data": "synthetic (seeded; datagen.config2_floats)",
+        "config": {"workload": "config2 float columns", "rows": n, "features": F, "border_count": 254},
+        "select_borders_s": round(sel_s, 4), "raw_open_s_pcie_inclusive": round(open_s, 4),
+        "roofline": {"bound": "hbm", "kernel": "quantize_kernel", "achieved": round(q_gbs, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(q_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "launches": st["quantize_launches"],
+                     "avg_launch_ms": round(st["quantize_ms"] / max(1, st["quantize_launches"]), 5),
+                     "algorithmic_bytes_per_launch": round(st["quantize_bytes"] / max(1, st["quantize_launches"]))},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -100,6 +168,8 @@ def main():
     ap.add_argument("--cpu-trees", type=int, default=-1)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prep", action="store_true",
+                    help="measure float-feature preparation (borders, quantize) instead of boosting")
     ap.add_argument("--copy-calib", type=int, default=0,
                     help="only copy this many bytes device-to-device (counter calibration)")
     args = ap.parse_args()
@@ -118,6 +188,9 @@ def main():
               "row-parallel (integer histogram all-reduce) design is not built in this library.",
               file=sys.stderr)
         sys.exit(2)
+    if args.prep:
+        prep_bench(args)
+        return
     steps = args.steps or DEFAULT_STEPS.get(args.config, 50)
     cpu_trees = args.cpu_trees if args.cpu_trees >= 0 else DEFAULT_CPU_TREES.get(args.config, 1)
 

@@ -4,16 +4,19 @@
 // crates/cb-backend/src/kernels.rs:2852).
 //
 // Border selection keeps the reference's split of work: the object subset (200000 rows
-// drawn by a fixed-seed partial Fisher-Yates, borders.rs:504-516) is gathered on the host,
-// NaNs are dropped and the values of every column sorted on the GPU in one segmented radix
-// sort (the sort dominates border selection at scale), and the greedy bin heap -- at most
-// border_count pops per column -- runs on the host, one worker per column.
+// drawn by a fixed-seed partial Fisher-Yates, borders.rs:504-516) is gathered on the host
+// with its NaNs made the positive quiet NaN, the values of every column are sorted on the
+// GPU in one segmented radix sort (NaNs land after +inf and are cut off; the sort dominates
+// border selection at scale), and the greedy bin heap -- at most border_count pops per
+// column -- runs on the host, one worker per column.  Device atomics on one address cost
+// about a microsecond each in series here, so no step counts through a shared counter.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <limits>
 #include <queue>
 #include <string>
 #include <thread>
@@ -43,17 +46,6 @@ struct Buf {
     }
     hipError_t alloc(size_t count) { return hipMalloc((void**)&p, (count ? count : 1) * sizeof(T)); }
 };
-
-// Drop the NaNs of every column segment: vals [F][S] -> packed [F][S] (count[f] leading
-// values; their order is free, they are sorted next).
-__global__ void drop_nan_kernel(const float* __restrict__ vals, uint32_t S, float* __restrict__ packed,
-                                unsigned int* __restrict__ count) {
-    const uint32_t f = blockIdx.y;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < S; i += gridDim.x * blockDim.x) {
-        const float v = vals[(size_t)f * S + i];
-        if (!isnan(v)) packed[(size_t)f * S + atomicAdd(count + f, 1u)] = v;
-    }
-}
 
 // ---- greedy split over sorted values (borders.rs:120-270, 572-640) ----
 struct GBin {
@@ -249,50 +241,55 @@ int cbh_select_borders(const float* const* columns, uint64_t n, uint32_t n_featu
             pool.emplace_back([&, w]() {
                 for (uint32_t f = w; f < F; f += nt) {
                     const float* c = columns[f];
+                    // every NaN becomes the positive quiet NaN, which the radix sort puts
+                    // after +inf: each sorted segment is its non-NaN values, then the NaNs
                     float* dst = vals.data() + (size_t)f * S;
-                    if (sampled)
-                        for (uint64_t i = 0; i < S; ++i) dst[i] = c[sample[i]];
-                    else
-                        std::memcpy(dst, c, sizeof(float) * S);
+                    const float qnan = std::numeric_limits<float>::quiet_NaN();
+                    for (uint64_t i = 0; i < S; ++i) {
+                        const float x = c[sampled ? sample[i] : i];
+                        dst[i] = x != x ? qnan : x;
+                    }
+                    // NaN scan over the whole column, in blocks the compiler vectorizes
                     bool any = false;
-                    for (uint64_t i = 0; i < n && !any; ++i) any = std::isnan(c[i]);
+                    for (uint64_t b0 = 0; b0 < n && !any; b0 += 4096) {
+                        const uint64_t b1 = std::min<uint64_t>(n, b0 + 4096);
+                        int acc = 0;
+                        for (uint64_t i = b0; i < b1; ++i) acc |= (c[i] != c[i]);
+                        any = acc != 0;
+                    }
                     has_nan[f] = any;
                 }
             });
         for (auto& t : pool) t.join();
     }
-    // device: drop NaNs, sort every column's values
-    Buf<float> dv, dp, ds;
-    Buf<unsigned int> dcnt;
+    // device: sort the values of every column (one segmented radix sort)
+    Buf<float> dv, ds;
     Buf<int> dbeg, dend;
     BRD_TRY(dv.alloc(vals.size()));
-    BRD_TRY(dp.alloc(vals.size()));
     BRD_TRY(ds.alloc(vals.size()));
-    BRD_TRY(dcnt.alloc(F));
     BRD_TRY(dbeg.alloc(F));
     BRD_TRY(dend.alloc(F));
     BRD_TRY(hipMemcpy(dv.p, vals.data(), sizeof(float) * vals.size(), hipMemcpyHostToDevice));
-    BRD_TRY(hipMemset(dcnt.p, 0, sizeof(unsigned int) * F));
-    const unsigned gx = (unsigned)std::min<uint64_t>((S + 255) / 256, 1024);
-    drop_nan_kernel<<<dim3(std::max(gx, 1u), F), 256>>>(dv.p, (uint32_t)S, dp.p, dcnt.p);
-    BRD_TRY(hipGetLastError());
-    std::vector<unsigned int> cnt(F);
-    BRD_TRY(hipMemcpy(cnt.data(), dcnt.p, sizeof(unsigned int) * F, hipMemcpyDeviceToHost));
     std::vector<int> beg(F), end(F);
     for (uint32_t f = 0; f < F; ++f) {
         beg[f] = (int)((uint64_t)f * S);
-        end[f] = beg[f] + (int)cnt[f];
+        end[f] = beg[f] + (int)S;
     }
     BRD_TRY(hipMemcpy(dbeg.p, beg.data(), sizeof(int) * F, hipMemcpyHostToDevice));
     BRD_TRY(hipMemcpy(dend.p, end.data(), sizeof(int) * F, hipMemcpyHostToDevice));
     size_t tmp_bytes = 0;
-    BRD_TRY(hipcub::DeviceSegmentedRadixSort::SortKeys(nullptr, tmp_bytes, dp.p, ds.p, (int)vals.size(), (int)F,
+    BRD_TRY(hipcub::DeviceSegmentedRadixSort::SortKeys(nullptr, tmp_bytes, dv.p, ds.p, (int)vals.size(), (int)F,
                                                        dbeg.p, dend.p, 0, 32));
     Buf<uint8_t> tmp;
     BRD_TRY(tmp.alloc(tmp_bytes));
-    BRD_TRY(hipcub::DeviceSegmentedRadixSort::SortKeys(tmp.p, tmp_bytes, dp.p, ds.p, (int)vals.size(), (int)F,
+    BRD_TRY(hipcub::DeviceSegmentedRadixSort::SortKeys(tmp.p, tmp_bytes, dv.p, ds.p, (int)vals.size(), (int)F,
                                                        dbeg.p, dend.p, 0, 32));
     BRD_TRY(hipMemcpy(vals.data(), ds.p, sizeof(float) * vals.size(), hipMemcpyDeviceToHost));
+    std::vector<uint64_t> cnt(F);
+    for (uint32_t f = 0; f < F; ++f) {
+        const float* seg = vals.data() + (size_t)f * S;
+        cnt[f] = (uint64_t)(std::partition_point(seg, seg + S, [](float x) { return x == x; }) - seg);
+    }
     // host: the greedy heap of every column, then the NaN sentinel of its mode
     const int kind = border_type == CBH_BORDERS_GREEDY_LOGSUM ? 0 : 1;
     const uint32_t stride = border_count + 1;

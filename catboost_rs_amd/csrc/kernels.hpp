@@ -495,16 +495,38 @@ static __global__ void derive_kernel(const long long* __restrict__ parent, long 
 // ---------------------------------------------------------------------------------
 constexpr int kMaxC = kMaxK + 1;
 
-// Per-feature bin counts over the feature-major columns (one workgroup per feature).
+// Per-feature bin counts over the feature-major columns: grid (row chunks, features); a
+// block counts its chunk in LDS with 16-byte loads over the aligned body of the chunk.
 static __global__ __launch_bounds__(256) void bin_census_kernel(const uint8_t* __restrict__ cols, uint64_t n,
+                                                                uint64_t chunk,
                                                                 unsigned long long* __restrict__ counts) {
     __shared__ unsigned int c[256];
     c[threadIdx.x] = 0;
     __syncthreads();
-    const uint8_t* col = cols + (size_t)blockIdx.x * n;
-    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&c[col[i]], 1u);
+    const uint8_t* col = cols + (size_t)blockIdx.y * n;
+    const uint64_t lo = (uint64_t)blockIdx.x * chunk;
+    const uint64_t hi = lo + chunk < n ? lo + chunk : n;
+    if (lo < hi) {
+        const uint64_t mis = (uint64_t)(uintptr_t)(col + lo) & 15u;
+        uint64_t head = mis ? 16u - mis : 0u;
+        if (head > hi - lo) head = hi - lo;
+        const uint64_t nvec = (hi - lo - head) / 16;
+        const uint64_t body = lo + head, tail = body + nvec * 16;
+        for (uint64_t i = lo + threadIdx.x; i < body; i += blockDim.x) atomicAdd(&c[col[i]], 1u);
+        const uint4* v = reinterpret_cast<const uint4*>(col + body);
+        for (uint64_t j = threadIdx.x; j < nvec; j += blockDim.x) {
+            const uint4 w = v[j];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) atomicAdd(&c[(ws[q] >> (8 * b)) & 0xffu], 1u);
+        }
+        for (uint64_t i = tail + threadIdx.x; i < hi; i += blockDim.x) atomicAdd(&c[col[i]], 1u);
+    }
     __syncthreads();
-    atomicAdd(counts + (size_t)blockIdx.x * 256 + threadIdx.x, (unsigned long long)c[threadIdx.x]);
+    if (c[threadIdx.x])
+        atomicAdd(counts + (size_t)blockIdx.y * 256 + threadIdx.x, (unsigned long long)c[threadIdx.x]);
 }
 
 // Channel totals of the rows of every directly built segment: tot [segment][C].

@@ -383,7 +383,12 @@ int plan_skip_bins(cbh_session* s) {
         zero_i64_kernel<<<grid_for((size_t)s->F * 256, 256, 8192), 256, 0, s->stream>>>((long long*)cnt,
                                                                                        (size_t)s->F * 256);
         if (hipGetLastError() != hipSuccess) { rc = fail(CBH_ERR_DEVICE, "census zero launch failed"); break; }
-        bin_census_kernel<<<s->F, 256, 0, s->stream>>>(s->cols, s->n, cnt);
+        // about 4 blocks per CU over all features, chunks of at least 64 KiB
+        const uint64_t want = std::max<uint64_t>(1, 1024 / std::max<uint32_t>(s->F, 1));
+        const uint64_t chunk = std::max<uint64_t>(65536, ((s->n + want - 1) / want + 15) & ~15ull);
+        const uint64_t gx = (s->n + chunk - 1) / chunk;
+        bin_census_kernel<<<dim3((unsigned)std::max<uint64_t>(gx, 1), s->F), 256, 0, s->stream>>>(s->cols, s->n,
+                                                                                              chunk, cnt);
         if (hipGetLastError() != hipSuccess) { rc = fail(CBH_ERR_DEVICE, "census launch failed"); break; }
         if (hipMemcpyAsync(h.data(), cnt, sizeof(unsigned long long) * h.size(), hipMemcpyDeviceToHost,
                            s->stream) != hipSuccess ||
@@ -493,14 +498,30 @@ int session_begin_raw_impl(const cbh_config* cfg, const float* const* columns, c
         }
         if (rc == CBH_OK && hipMemcpy(db, flat.data(), sizeof(double) * flat.size(), hipMemcpyHostToDevice) != hipSuccess)
             rc = fail(CBH_ERR_DEVICE, "border upload failed");
+        // with profiling, every quantize launch is bracketed by its own event pair
+        std::vector<hipEvent_t> ev(s->cfg.profile ? 2 * (size_t)F : 0, nullptr);
+        for (auto& e : ev)
+            if (rc == CBH_OK && hipEventCreate(&e) != hipSuccess) rc = fail(CBH_ERR_DEVICE, "event creation failed");
         for (uint32_t f = 0; rc == CBH_OK && f < F; ++f) {
             if (hipMemcpyAsync(stage, columns[f], sizeof(float) * n, hipMemcpyHostToDevice, s->stream) != hipSuccess) {
                 rc = fail(CBH_ERR_DEVICE, "column upload failed");
                 break;
             }
+            if (!ev.empty()) (void)hipEventRecord(ev[2 * f], s->stream);
             rc = cbh_internal_quantize(stage, n, db + off[f], n_borders[f], s->cols + (size_t)f * n, s->stream);
+            if (!ev.empty()) (void)hipEventRecord(ev[2 * f + 1], s->stream);
         }
         if (hipStreamSynchronize(s->stream) != hipSuccess && rc == CBH_OK) rc = fail(CBH_ERR_DEVICE, "quantize failed");
+        for (uint32_t f = 0; rc == CBH_OK && !ev.empty() && f < F; ++f) {
+            float ms = 0.f;
+            if (hipEventElapsedTime(&ms, ev[2 * f], ev[2 * f + 1]) == hipSuccess) {
+                s->stats.quantize_ms += ms;
+                s->stats.quantize_launches += 1;
+                s->stats.quantize_bytes += 5.0 * (double)n + 8.0 * n_borders[f];
+            }
+        }
+        for (auto& e : ev)
+            if (e) (void)hipEventDestroy(e);
         if (db) (void)hipFree(db);
         if (stage) (void)hipFree(stage);
         return rc;

@@ -82,6 +82,23 @@ def config1(scale=1.0, seed=0):
                             bootstrap_type="No", boost_from_average=True))
 
 
+def config2_floats(n_rows=10_000_000, n_features=200, seed=1, threads=None):
+    """The float columns of config 2 before quantization, feature-major f32 [F][n]: half
+    N(0,1), half lognormal(0,1) (the same generator streams as config2)."""
+    n, F, half = int(n_rows), n_features, n_features // 2
+    X = np.empty((F, n), np.float32)
+
+    def work(f):
+        g = np.random.default_rng([seed, f])
+        X[f] = g.standard_normal(n, dtype=np.float32)
+        if f >= half:
+            np.exp(X[f], out=X[f])
+
+    with cf.ThreadPoolExecutor(threads or min(16, os.cpu_count() or 4)) as ex:
+        list(ex.map(work, range(F)))
+    return X
+
+
 def config2(scale=1.0, seed=1, n_rows=None, n_features=200):
     """Logloss: n x 200 (half N(0,1), half lognormal(0,1)); 254 borders; labels
     Bernoulli(sigmoid(X[:, :20].w)); depth 6, 200 iterations, Bayesian bootstrap T=1."""

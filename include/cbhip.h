@@ -186,6 +186,9 @@ typedef struct {
     double fill_bytes;            /* algorithmic bytes V*(W*4 + 8*(K+1) + 4) + H */
     uint64_t trees;
     uint64_t skip_features;       /* features whose dominant bin the fill leaves out */
+    double quantize_ms;           /* raw float channel: device quantize launches at open */
+    uint64_t quantize_launches;
+    double quantize_bytes;        /* algorithmic bytes: 4 read + 1 written per value + borders */
 } cbh_stats;
 
 int cbh_session_stats(const cbh_session* s, cbh_stats* out);
