@@ -93,7 +93,7 @@ class TrainParams(C.Structure):
 EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_session_read_approx", "cbh_session_stats", "cbh_session_reset_stats",
            "cbh_session_end", "cbh_compute_gradients", "cbh_hist_build", "cbh_bootstrap",
-           "cbh_apply_oblivious", "cbh_session_begin_raw", "cbh_select_borders", "cbh_quantize",
+           "cbh_apply_oblivious", "cbh_session_begin_raw", "cbh_select_borders", "cbh_quantize", "cbh_perfect_hash", "cbh_ctr_columns",
            "cbh_version", "cbh_last_error", "cbt_open", "cbt_open_raw", "cbt_set_pairs", "cbt_step",
            "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close"]
 
@@ -133,6 +133,8 @@ def load(path: str = LIB_PATH):
                                         C.c_double, C.c_double, C.POINTER(P)]
     L.cbh_select_borders.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_int32, C.c_int32, P, P]
     L.cbh_quantize.argtypes = [P, C.c_uint64, P, C.c_uint32, P]
+    L.cbh_perfect_hash.argtypes = [P, C.c_uint64, P, P]
+    L.cbh_ctr_columns.argtypes = [P, C.c_uint32, C.c_uint64, P, P, P, C.c_uint32, C.c_uint32, P, P, P]
     L.cbt_open_raw.argtypes = [C.POINTER(TrainParams), P, P, P, C.c_uint64, C.c_uint32, P, P, C.POINTER(P)]
     L.cbt_set_pairs.argtypes = [P, P, C.c_uint32, P, P, P, C.c_uint64]
     L.cbt_step.argtypes = [P, P, P, P, P]
@@ -263,6 +265,49 @@ def quantize(column, borders):
     out = np.zeros(c.shape[0], np.uint8)
     _check(load().cbh_quantize(_ptr(c), c.shape[0], _ptr(b) if b.size else None, b.size, _ptr(out)))
     return out
+
+
+CTR_TYPE = {"Borders": 0, "Buckets": 1, "BinarizedTargetMeanValue": 2, "Counter": 4}
+
+
+class CtrSpec(C.Structure):
+    _fields_ = [("ctr_type", C.c_int32), ("target_border_idx", C.c_uint32), ("prior_num", C.c_double),
+                ("prior_denom", C.c_double)]
+
+
+def perfect_hash(keys):
+    """First-seen dense bins of u32 keys on the device (``cbh_perfect_hash``)."""
+    k = np.ascontiguousarray(keys, np.uint32)
+    out = np.zeros(k.shape[0], np.uint32)
+    d = C.c_uint32()
+    _check(load().cbh_perfect_hash(_ptr(k), k.shape[0], _ptr(out), C.byref(d)))
+    return out, int(d.value)
+
+
+def ctr_columns(buckets, permutation, target_class, specs, border_count=15, n_buckets=None,
+                want_values=False, want_counts=False):
+    """Online CTR columns of one categorical feature on the device (``cbh_ctr_columns``).
+    ``specs``: list of (ctr_type, prior) or (ctr_type, prior, target_border_idx).  Returns
+    bins [n_specs][n] u8 (and values [n_specs][n], counts [2][n] when asked)."""
+    b = np.ascontiguousarray(buckets, np.uint32)
+    pm = np.ascontiguousarray(permutation, np.uint32)
+    tc = np.ascontiguousarray(target_class, np.uint8)
+    n = b.shape[0]
+    nb = (int(b.max()) + 1 if n else 1) if n_buckets is None else int(n_buckets)
+    arr = (CtrSpec * len(specs))()
+    for k, sp in enumerate(specs):
+        arr[k] = CtrSpec(CTR_TYPE[sp[0]], sp[2] if len(sp) > 2 else 0, float(sp[1]), 1.0)
+    bins = np.zeros((len(specs), n), np.uint8)
+    vals = np.zeros((len(specs), n)) if want_values else None
+    cnt = np.zeros((2, n), np.uint32) if want_counts else None
+    _check(load().cbh_ctr_columns(_ptr(b), nb, n, _ptr(pm), _ptr(tc), arr, len(specs), border_count,
+                                  _ptr(bins), _ptr(vals), _ptr(cnt)))
+    out = [bins]
+    if want_values:
+        out.append(vals)
+    if want_counts:
+        out.append(cnt)
+    return out[0] if len(out) == 1 else tuple(out)
 
 
 def _family_arrays(group_offsets, winner, loser, weight=None):

@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libcbhip.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["session.hip", "entry.hip", "apply.hip", "borders.hip", "driver.cpp"]
+SOURCES = ["session.hip", "entry.hip", "apply.hip", "borders.hip", "categorical.hip", "driver.cpp"]
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 

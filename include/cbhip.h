@@ -48,6 +48,8 @@ enum { CBH_BOOT_NO = 0, CBH_BOOT_BAYESIAN = 1, CBH_BOOT_BERNOULLI = 2 };
 /* float-feature preparation (crates/cb-data/src/borders.rs, nan_mode.rs) */
 enum { CBH_BORDERS_GREEDY_LOGSUM = 0, CBH_BORDERS_GREEDY_MIN_ENTROPY = 1 };
 enum { CBH_NAN_MIN = 0, CBH_NAN_MAX = 1, CBH_NAN_FORBIDDEN = 2 };
+/* CTR types (ECtrType, crates/cb-train/src/ctr/mod.rs; the CPU-task subset) */
+enum { CBH_CTR_BORDERS = 0, CBH_CTR_BUCKETS = 1, CBH_CTR_BTMV = 2, CBH_CTR_COUNTER = 4 };
 
 /* Mirrors DeviceTrainConfig (runtime.rs:1260-1341) plus the scalar arguments of
  * begin_device_training (runtime.rs:1497-1529).  Fields the device path does not cover
@@ -258,6 +260,42 @@ int cbh_select_borders(const float* const* columns, uint64_t n, uint32_t n_featu
  * with f32::MAX, else to bin 0.  At most 255 ascending borders. */
 int cbh_quantize(const float* column, uint64_t n, const double* borders, uint32_t n_borders,
                  uint8_t* bins_out);
+
+/* ---- categorical inputs ---- */
+
+/* First-seen dense bins of u32 category keys (the reference hashes a category to a u32 with
+ * calc_cat_feature_hash and remaps with PerfectHash, crates/cb-data/src/cat_hash.rs:389-479):
+ * bins_out[i] = the rank of keys[i] among the distinct keys ordered by first occurrence. */
+int cbh_perfect_hash(const uint32_t* keys, uint64_t n, uint32_t* bins_out, uint32_t* n_distinct_out);
+
+/* One CTR column spec (DeviceCtrColumn's ctr_type / target_border_idx / prior,
+ * runtime.rs:1104-1160; prior_denom must be non-zero, the CPU path uses 1). */
+typedef struct {
+    int32_t ctr_type;             /* CBH_CTR_* */
+    uint32_t target_border_idx;   /* Buckets: the class counted; Borders: classes <= it excluded */
+    double prior_num;
+    double prior_denom;
+} cbh_ctr_spec;
+
+/* Online CTR columns of one categorical feature (or one projection, given its combined
+ * bucket per object), all specs at once.  Mirrors materialize_ctr_feature
+ * (crates/cb-train/src/ctr/ctr_feature.rs) over online_class_prefix_column /
+ * online_mean_prefix / online_counter_column (crates/cb-train/src/ctr/online.rs) and the
+ * device twin ordered_ctr_prefix_kernel (crates/cb-backend/src/kernels/ctr_device.rs:164):
+ *   buckets        [n], each < n_buckets (first-seen bins of the category or projection)
+ *   permutation    [n], the learn order: object permutation[p] sits at position p
+ *   target_class   [n], 0 or 1 (binclf class; the reference binarizes t > 0.5)
+ *   bins_out       [n_specs][n] u8: trunc((value + shift) / norm * border_count) clamped to
+ *                  [0, border_count], shift/norm = calc_normalization(prior), in f32 for BTMV
+ *   values_out     nullable [n_specs][n] f64: (num + prior) / (total + 1)
+ *   class_counts_out nullable [2][n]: the per-object predecessor counts N0, N1
+ * Borders / Buckets / BinarizedTargetMeanValue read the counts of the object's bucket over
+ * its PREDECESSORS in the permutation (read before increment); Counter uses whole-set bucket
+ * sizes over the largest bucket size (counter_calc_method SkipTest). */
+int cbh_ctr_columns(const uint32_t* buckets, uint32_t n_buckets, uint64_t n, const uint32_t* permutation,
+                    const uint8_t* target_class, const cbh_ctr_spec* specs, uint32_t n_specs,
+                    uint32_t border_count, uint8_t* bins_out, double* values_out,
+                    uint32_t* class_counts_out);
 
 /* Version / build information. */
 const char* cbh_version(void);

@@ -1235,3 +1235,138 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
     free(pw_win); free(pw_los); free(pw_wt); free(pw);
     return rc;
 }
+
+
+/* ======================================================================
+ * Categorical inputs: permutations, first-seen bins, online CTR columns
+ * ==================================================================== */
+static void shuffle_from(uint64_t n, orc_rng* r, uint32_t* v) { /* permutation.rs shuffle_in_place */
+    for (uint64_t i = 0; i < n; ++i) v[i] = (uint32_t)i;
+    for (uint64_t i = 1; i < n; ++i) {
+        uint64_t j = orc_rng_uniform(r, i + 1);
+        uint32_t t = v[i]; v[i] = v[j]; v[j] = t;
+    }
+}
+
+void orc_shuffled_indices(uint64_t n, uint64_t seed, uint32_t* out) {
+    orc_rng r;
+    orc_rng_from_seed(&r, seed);
+    shuffle_from(n, &r, out);
+}
+
+void orc_permutations(uint64_t n, uint32_t count, uint64_t seed, uint32_t* out) {
+    orc_rng r;
+    orc_rng_from_seed(&r, seed);
+    for (uint32_t k = 0; k < count; ++k) shuffle_from(n, &r, out + (size_t)k * n);
+}
+
+typedef struct { uint32_t key; uint32_t idx; } orc_key_idx;
+static int cmp_key_idx(const void* a, const void* b) {
+    const orc_key_idx* x = (const orc_key_idx*)a;
+    const orc_key_idx* y = (const orc_key_idx*)b;
+    if (x->key != y->key) return x->key < y->key ? -1 : 1;
+    return x->idx < y->idx ? -1 : (x->idx > y->idx);
+}
+
+uint32_t orc_perfect_hash(const uint32_t* keys, uint64_t n, uint32_t* bins) {
+    /* first occurrence of every key, then keys ranked by their first occurrence */
+    orc_key_idx* a = (orc_key_idx*)malloc(sizeof(orc_key_idx) * (n ? n : 1));
+    for (uint64_t i = 0; i < n; ++i) { a[i].key = keys[i]; a[i].idx = (uint32_t)i; }
+    qsort(a, n, sizeof(orc_key_idx), cmp_key_idx);
+    uint32_t* first = (uint32_t*)malloc(sizeof(uint32_t) * (n ? n : 1));  /* first idx per object */
+    uint64_t d = 0;
+    orc_key_idx* heads = (orc_key_idx*)malloc(sizeof(orc_key_idx) * (n ? n : 1));
+    for (uint64_t i = 0; i < n; ++i) {
+        if (i == 0 || a[i].key != a[i - 1].key) { heads[d].key = a[i].idx; heads[d].idx = (uint32_t)d; ++d; }
+        first[a[i].idx] = (uint32_t)(d - 1);  /* segment id of the object */
+    }
+    qsort(heads, d, sizeof(orc_key_idx), cmp_key_idx);  /* by first index */
+    uint32_t* rank = (uint32_t*)malloc(sizeof(uint32_t) * (d ? d : 1));
+    for (uint64_t r = 0; r < d; ++r) rank[heads[r].idx] = (uint32_t)r;
+    for (uint64_t i = 0; i < n; ++i) bins[i] = rank[first[i]];
+    free(a); free(first); free(heads); free(rank);
+    return (uint32_t)d;
+}
+
+/* calc_normalization (calc_ctr.rs): shift = -min(0, prior), norm = max(1, prior) - min(0, prior) */
+static void ctr_norm(double prior, double* shift, double* norm) {
+    double left = prior < 0.0 ? prior : 0.0;
+    double right = prior > 1.0 ? prior : 1.0;
+    *shift = -left;
+    *norm = right - left;
+}
+
+static uint8_t ctr_clamp_bin(double bin_f, uint32_t border_count) {
+    double t = trunc(bin_f);
+    if (t < 0.0) return 0;
+    if (t > (double)border_count) return (uint8_t)border_count;
+    return (uint8_t)t;
+}
+
+int orc_ctr_column(int32_t ctr_type, uint32_t target_border_idx, double prior_num, double prior_denom,
+                   uint32_t border_count, const uint32_t* bucket, uint32_t n_buckets, uint64_t n,
+                   const uint32_t* permutation, const uint8_t* target_class, double* good,
+                   int64_t* total, double* value, uint8_t* bin) {
+    if (prior_denom == 0.0) return -3;
+    if (border_count > 255) return -2;
+    const double prior = prior_num / prior_denom;
+    double shift, norm;
+    ctr_norm(prior, &shift, &norm);
+    double* g = (double*)malloc(sizeof(double) * (n ? n : 1));
+    int64_t* t = (int64_t*)malloc(sizeof(int64_t) * (n ? n : 1));
+    int f32_bins = 0;
+    if (ctr_type == ORC_CTR_COUNTER) {  /* whole-set bucket counts, max count denominator */
+        int64_t* cnt = (int64_t*)calloc(n_buckets ? n_buckets : 1, sizeof(int64_t));
+        for (uint64_t i = 0; i < n; ++i) cnt[bucket[i]] += 1;
+        int64_t den = 0;
+        for (uint32_t b = 0; b < n_buckets; ++b) if (cnt[b] > den) den = cnt[b];
+        for (uint64_t i = 0; i < n; ++i) { g[i] = (double)cnt[bucket[i]]; t[i] = den; }
+        free(cnt);
+    } else if (ctr_type == ORC_CTR_BTMV) {  /* online_mean_prefix: f32 running sum of class/1 */
+        float* sum = (float*)calloc(n_buckets ? n_buckets : 1, sizeof(float));
+        int64_t* cnt = (int64_t*)calloc(n_buckets ? n_buckets : 1, sizeof(int64_t));
+        for (uint64_t p = 0; p < n; ++p) {
+            uint32_t doc = permutation[p], b = bucket[doc];
+            g[doc] = (double)sum[b];
+            t[doc] = cnt[b];
+            sum[b] += (float)target_class[doc] / 1.0f;
+            cnt[b] += 1;
+        }
+        free(sum); free(cnt);
+        f32_bins = 1;
+    } else if (ctr_type == ORC_CTR_BORDERS || ctr_type == ORC_CTR_BUCKETS) {
+        /* online_class_prefix_column: read the bucket's class counts, then increment */
+        int64_t* cnt = (int64_t*)calloc((size_t)(n_buckets ? n_buckets : 1) * 2, sizeof(int64_t));
+        for (uint64_t p = 0; p < n; ++p) {
+            uint32_t doc = permutation[p], b = bucket[doc];
+            int64_t n0 = cnt[2 * (size_t)b], n1 = cnt[2 * (size_t)b + 1];
+            int64_t tot = n0 + n1, num;
+            if (ctr_type == ORC_CTR_BUCKETS) num = target_border_idx == 0 ? n0 : (target_border_idx == 1 ? n1 : 0);
+            else num = tot - (target_border_idx == 0 ? n0 : n0 + n1);
+            g[doc] = (double)num;
+            t[doc] = tot;
+            if (target_class[doc] < 2) cnt[2 * (size_t)b + target_class[doc]] += 1;
+        }
+        free(cnt);
+    } else {
+        free(g); free(t);
+        return -4;
+    }
+    for (uint64_t i = 0; i < n; ++i) {
+        double v = (g[i] + prior) / ((double)t[i] + 1.0);  /* calc_ctr_online */
+        if (value) value[i] = v;
+        if (good) good[i] = g[i];
+        if (total) total[i] = t[i];
+        double bf;
+        if (f32_bins) {   /* ctr_feature.rs quantize_in_f32 branch */
+            float den = (float)t[i] + 1.0f;
+            float c = ((float)g[i] + (float)prior) / den;
+            bf = (double)(((c + (float)shift) / (float)norm) * (float)border_count);
+        } else {          /* calc_ctr_online_bin */
+            bf = norm == 0.0 ? 0.0 : (v + shift) / norm * (double)border_count;
+        }
+        bin[i] = ctr_clamp_bin(bf, border_count);
+    }
+    free(g); free(t);
+    return 0;
+}

@@ -19,6 +19,9 @@
  *                         crates/cb-oracle/fixtures/{bootstrap/{no,bayesian,bernoulli},regression_skeleton,
  *                         binclf_skeleton} (splits, leaf values, staged approx)
  *   multiclass            crates/cb-oracle/fixtures/multiclass_softmax
+ *   permutations / CTR    cb-oracle/fixtures/{plain_ctr,ordered_ctr,tensor_ctr,one_hot_cat}
+ *                         permutations, cat_hash first-seen bins, the hand scenarios of
+ *                         cb-train/tests/{plain,tensor}_ctr_oracle_test.rs, brute-force recounts
  */
 #ifndef CB_ORACLE_H
 #define CB_ORACLE_H
@@ -147,6 +150,30 @@ int orc_apply_oblivious(const float* x_fm, uint64_t n, uint32_t F, const uint32_
                         const double* leaf_values, const uint32_t* tree_leaf_offsets,
                         uint32_t n_trees, uint32_t K, const double* bias,
                         const uint8_t* nan_as_true, double* out);
+
+/* ---- categorical inputs (cb-train/src/permutation.rs, cb-data/src/cat_hash.rs,
+ *      cb-train/src/ctr/{online,calc_ctr,ctr_feature}.rs) ---- */
+enum { ORC_CTR_BORDERS = 0, ORC_CTR_BUCKETS = 1, ORC_CTR_BTMV = 2, ORC_CTR_COUNTER = 4 };
+
+/* Fisher-Yates over TFastRng64::from_seed(seed): for i in 1..n swap(i, uniform(i + 1))
+ * (permutation.rs:131 create_shuffled_indices / shuffle_in_place). */
+void orc_shuffled_indices(uint64_t n, uint64_t seed, uint32_t* out);
+/* count permutations drawn one after another off one from_seed(seed) stream
+ * (permutation.rs:236 permutations); out [count][n]. */
+void orc_permutations(uint64_t n, uint32_t count, uint64_t seed, uint32_t* out);
+/* First-seen dense remap of u32 keys (PerfectHash::remap, cat_hash.rs:389-479); returns the
+ * number of distinct keys. */
+uint32_t orc_perfect_hash(const uint32_t* keys, uint64_t n, uint32_t* bins);
+/* One online CTR column (materialize_ctr_feature, ctr_feature.rs, over
+ * online_class_prefix_column / online_mean_prefix / online_counter_column, online.rs;
+ * value calc_ctr_online, bin calc_ctr_online_bin or its f32 twin for BTMV):
+ *   bucket [n] (< n_buckets), permutation [n], target_class [n] in {0,1}
+ *   out: good / total [n] (the numerator as f64 -- the f32 sum for BTMV -- and the
+ *   denominator), value [n], bin [n] in [0, border_count].  All nullable except bin. */
+int orc_ctr_column(int32_t ctr_type, uint32_t target_border_idx, double prior_num, double prior_denom,
+                   uint32_t border_count, const uint32_t* bucket, uint32_t n_buckets, uint64_t n,
+                   const uint32_t* permutation, const uint8_t* target_class, double* good,
+                   int64_t* total, double* value, uint8_t* bin);
 
 /* Per-leaf ordered sums (cb-compute/src/histogram.rs:49 reduce_leaf_stats, :97 reduce_leaf_der2). */
 void orc_leaf_sums(const uint32_t* leaf_of, uint64_t n, uint32_t n_leaves, const double* der,

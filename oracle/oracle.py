@@ -90,6 +90,13 @@ def lib():
         L.orc_sample_indices_for_borders.argtypes = [C.c_uint64, C.c_uint64, P]
         L.orc_select_borders_greedy.argtypes = [P, C.c_uint64, C.c_uint32, C.c_int32, C.c_int32, P]
         L.orc_select_borders_greedy.restype = C.c_uint32
+        L.orc_shuffled_indices.argtypes = [C.c_uint64, C.c_uint64, P]
+        L.orc_permutations.argtypes = [C.c_uint64, C.c_uint32, C.c_uint64, P]
+        L.orc_perfect_hash.argtypes = [P, C.c_uint64, P]
+        L.orc_perfect_hash.restype = C.c_uint32
+        L.orc_ctr_column.argtypes = [C.c_int32, C.c_uint32, C.c_double, C.c_double, C.c_uint32, P,
+                                     C.c_uint32, C.c_uint64, P, P, P, P, P, P]
+        L.orc_ctr_column.restype = C.c_int
         L.orc_apply_oblivious.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, P, C.c_uint32,
                                           C.c_uint32, P, P, P]
         L.orc_apply_oblivious.restype = C.c_int
@@ -279,6 +286,46 @@ def sample_indices_for_borders(n, sample_size=200_000):
     out = np.zeros(min(n, sample_size), np.uint32)
     lib().orc_sample_indices_for_borders(n, sample_size, _p(out))
     return out
+
+
+CTR = {"Borders": 0, "Buckets": 1, "BinarizedTargetMeanValue": 2, "Counter": 4}
+
+
+def shuffled_indices(n, seed):
+    out = np.zeros(n, np.uint32)
+    lib().orc_shuffled_indices(n, seed, _p(out))
+    return out
+
+
+def permutations(n, count, seed):
+    out = np.zeros((count, n), np.uint32)
+    lib().orc_permutations(n, count, seed, _p(out))
+    return out
+
+
+def perfect_hash(keys):
+    """First-seen dense bins of u32 keys and the number of distinct keys."""
+    k = np.ascontiguousarray(keys, np.uint32)
+    out = np.zeros(k.shape[0], np.uint32)
+    d = lib().orc_perfect_hash(_p(k), k.shape[0], _p(out))
+    return out, int(d)
+
+
+def ctr_column(ctr_type, bucket, permutation, target_class, prior=0.5, target_border_idx=0,
+               border_count=15, n_buckets=None, prior_denom=1.0):
+    """One online CTR column: dict(good, total, value, bin) in object order."""
+    b = np.ascontiguousarray(bucket, np.uint32)
+    pm = np.ascontiguousarray(permutation, np.uint32)
+    tc = np.ascontiguousarray(target_class, np.uint8)
+    n = b.shape[0]
+    nb = int(b.max()) + 1 if n_buckets is None and n else (n_buckets or 0)
+    good, total = np.zeros(n), np.zeros(n, np.int64)
+    value, bins = np.zeros(n), np.zeros(n, np.uint8)
+    rc = lib().orc_ctr_column(CTR[ctr_type], target_border_idx, prior, prior_denom, border_count,
+                              _p(b), nb, n, _p(pm), _p(tc), _p(good), _p(total), _p(value), _p(bins))
+    if rc != 0:
+        raise ValueError(f"orc_ctr_column rc={rc}")
+    return dict(good=good, total=total, value=value, bin=bins)
 
 
 def model_arrays(split_features, split_borders, leaf_values, K=1):

@@ -27,6 +27,10 @@ expected outputs); no reference source is copied.  Sources:
                              border types: border_types/<dataset>.bc<k>.Greedy* and
                              borders_quant/numeric_{tiny,nan} (border_count 254), with the
                              input matrices they were computed from.
+* ``categorical.npz``     -- catboost 1.2.10 learn permutations and per-object online CTR
+                             anchors (good / total counts, values) of plain_ctr,
+                             ordered_ctr, tensor_ctr and one_hot_cat, and the cat_hash
+                             category hashes with their first-seen bins.
 """
 from __future__ import annotations
 
@@ -229,6 +233,22 @@ def borders(ref):
               open(os.path.join(HERE, "borders.json"), "w"), indent=1)
 
 
+def categorical(ref):
+    """Permutations, online CTR anchors and first-seen bins (data only)."""
+    fx = os.path.join(ref, "crates/cb-oracle/fixtures")
+    arrays = {}
+    for scen in ("plain_ctr", "ordered_ctr", "tensor_ctr", "one_hot_cat"):
+        for f in sorted(os.listdir(os.path.join(fx, scen))):
+            if f.startswith(("permutation_fold", "ctr_good_count", "ctr_total_count", "ctr_value")):
+                arrays[scen + "." + f[:-4]] = np.load(os.path.join(fx, scen, f))
+        cfg = json.load(open(os.path.join(fx, scen, "config.json")))
+        arrays[scen + ".seed"] = np.array(cfg["seed"], np.int64)
+        arrays[scen + ".prior"] = np.array(float(cfg["params"]["simple_ctr"][0].split("=")[1]))
+    arrays["cat_hash.hashes"] = np.load(os.path.join(fx, "cat_hash", "cat_hashes.npy")).astype(np.uint32)
+    arrays["cat_hash.bins"] = np.load(os.path.join(fx, "cat_hash", "perfect_hash_bins.npy")).astype(np.uint32)
+    np.savez_compressed(os.path.join(HERE, "categorical.npz"), **arrays)
+
+
 def main():
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     rng_kat(ref)
@@ -240,6 +260,7 @@ def main():
         one_hot_train(ref, s)
     ranking(ref)
     borders(ref)
+    categorical(ref)
 
 
 if __name__ == "__main__":

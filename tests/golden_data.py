@@ -99,3 +99,10 @@ def borders():
         flat = z[c["stem"] + ".borders"]
         cells.append(dict(c, borders=[flat[offs[i]:offs[i + 1]] for i in range(len(per))]))
     return cells, mats
+
+
+def categorical():
+    """catboost 1.2.10 learn permutations, online CTR anchors and first-seen bins (a dict of
+    arrays keyed '<scenario>.<name>')."""
+    z = np.load(os.path.join(GOLDEN, "categorical.npz"))
+    return {k: z[k] for k in z.files}

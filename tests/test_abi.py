@@ -135,3 +135,17 @@ def test_float_preparation_argument_checks(lib):
     with pytest.raises(cb.CbhError) as e:
         raw([np.array([0.5, 1.5, 2.5, 3.5])])
     assert e.value.code == -2  # n_borders + 1 > n_bins
+
+
+def test_categorical_argument_checks(lib):
+    """CTR columns validate the permutation, bucket range and classes before any device call."""
+    import numpy as np
+    for args, kw in (((np.zeros(3, np.uint32), np.array([0, 0, 1]), np.zeros(3)), {}),
+                     ((np.array([0, 5, 1], np.uint32), np.arange(3), np.zeros(3)), dict(n_buckets=2)),
+                     ((np.zeros(3, np.uint32), np.arange(3), np.array([0, 2, 1])), {})):
+        with pytest.raises(cb.CbhError) as e:
+            cb.ctr_columns(*args, [("Borders", 0.5)], **kw)
+        assert e.value.code == -2
+    with pytest.raises(cb.CbhError) as e:
+        cb.ctr_columns(np.zeros(3, np.uint32), np.arange(3), np.zeros(3), [("Borders", 0.5)] * 17)
+    assert e.value.code == -2

@@ -536,3 +536,112 @@ def test_quantize_is_bin_of():
     brute_m = np.array([len(bm) if np.isnan(x) else int(np.sum(bm < float(x))) for x in v])
     assert np.array_equal(O.quantize(v, bm), brute_m)
     assert O.quantize(v, np.zeros(0)).max() == 0
+
+
+# --------------------------------------------------------------------------------------
+# categorical inputs: learn permutations, first-seen bins, online CTR columns
+# --------------------------------------------------------------------------------------
+CTR_SCENARIOS = ("plain_ctr", "ordered_ctr", "tensor_ctr", "one_hot_cat")
+
+
+def test_permutations_match_upstream():
+    """create_shuffled_indices / permutations (permutation.rs) against catboost 1.2.10's fold
+    permutations; fold 1 continues the same stream."""
+    g = G.categorical()
+    for scen in CTR_SCENARIOS:
+        want = g[scen + ".permutation_fold0"]
+        assert np.array_equal(O.shuffled_indices(want.size, int(g[scen + ".seed"])), want), scen
+    two = O.permutations(30, 2, 0)
+    assert np.array_equal(two[0], g["ordered_ctr.permutation_fold0"])
+    assert np.array_equal(two[1], g["ordered_ctr.permutation_fold1"])
+
+
+def test_ctr_value_formula_matches_upstream_anchors():
+    """calc_ctr_online (num + prior) / (total + 1) reproduces catboost's per-object CTR values
+    from its own integer anchors, in all four scenarios (catboost keeps them in f32: equal
+    after rounding to f32)."""
+    g = G.categorical()
+    for scen in CTR_SCENARIOS:
+        good, total = g[scen + ".ctr_good_count"].astype(float), g[scen + ".ctr_total_count"]
+        calc = (good + float(g[scen + ".prior"])) / (total + 1.0)
+        assert np.array_equal(calc.astype(np.float32), g[scen + ".ctr_value"].astype(np.float32)), scen
+        assert np.all((good >= 0) & (good <= total))
+
+
+def test_perfect_hash_matches_upstream_bins():
+    g = G.categorical()
+    h, b = g["cat_hash.hashes"], g["cat_hash.bins"]
+    n = h.size // 2
+    for c in range(2):
+        bins, d = O.perfect_hash(h[c * n:(c + 1) * n])
+        assert np.array_equal(bins, b[c * n:(c + 1) * n]) and d == int(b[c * n:(c + 1) * n].max()) + 1
+
+
+def test_perfect_hash_is_first_seen_order():
+    rng = np.random.default_rng(1)
+    keys = rng.integers(0, 2**32, 50, dtype=np.uint64).astype(np.uint32)[rng.integers(0, 50, 3000)]
+    bins, d = O.perfect_hash(keys)
+    seen = {}
+    want = np.array([seen.setdefault(int(k), len(seen)) for k in keys], np.uint32)
+    assert np.array_equal(bins, want) and d == len(seen)
+
+
+def _bruteforce_ctr(kind, bucket, perm, cls, prior, tbi, bc):
+    """Independent recount: per bucket, the classes of its objects in permutation order."""
+    n = bucket.size
+    pos = np.empty(n, np.int64)
+    pos[perm] = np.arange(n)
+    n0 = np.zeros(n, np.int64)
+    n1 = np.zeros(n, np.int64)
+    size = np.bincount(bucket, minlength=int(bucket.max()) + 1)
+    for b in np.unique(bucket):
+        objs = np.nonzero(bucket == b)[0]
+        objs = objs[np.argsort(pos[objs])]
+        c = cls[objs].astype(np.int64)
+        n1[objs] = np.cumsum(c) - c
+        n0[objs] = np.arange(objs.size) - n1[objs]
+    total = n0 + n1
+    if kind == "Counter":
+        num, total = size[bucket].astype(float), np.full(n, size.max())
+    elif kind == "Buckets":
+        num = (n0 if tbi == 0 else n1 if tbi == 1 else 0 * n0).astype(float)
+    elif kind == "Borders":
+        num = (n1 if tbi == 0 else 0 * n1).astype(float)
+    else:  # BinarizedTargetMeanValue: f32 running sum of ones
+        num = np.minimum(n1, 2**24).astype(np.float32).astype(float)
+    value = (num + prior) / (total + 1.0)
+    shift, norm = -min(0.0, prior), max(1.0, prior) - min(0.0, prior)
+    if kind == "BinarizedTargetMeanValue":
+        c32 = (num.astype(np.float32) + np.float32(prior)) / (total.astype(np.float32) + np.float32(1))
+        bf = (((c32 + np.float32(shift)) / np.float32(norm)) * np.float32(bc)).astype(float)
+    else:
+        bf = (value + shift) / norm * bc
+    return dict(good=num, total=total, value=value, bin=np.clip(np.trunc(bf), 0, bc).astype(np.uint8))
+
+
+@pytest.mark.parametrize("kind,tbi", [("Borders", 0), ("Borders", 1), ("Buckets", 0), ("Buckets", 1),
+                                      ("BinarizedTargetMeanValue", 0), ("Counter", 0)])
+@pytest.mark.parametrize("prior", [0.0, 0.5, 1.0, 2.0, -0.5])
+def test_ctr_column_matches_bruteforce(kind, tbi, prior):
+    rng = np.random.default_rng(7)
+    n = 4000
+    bucket = np.minimum(rng.zipf(1.3, n) - 1, 300).astype(np.uint32)
+    bucket = O.perfect_hash(bucket)[0]
+    perm = O.shuffled_indices(n, 3)
+    cls = (rng.random(n) < 0.4).astype(np.uint8)
+    got = O.ctr_column(kind, bucket, perm, cls, prior=prior, target_border_idx=tbi)
+    exp = _bruteforce_ctr(kind, bucket, perm, cls, prior, tbi, 15)
+    for k in ("good", "total", "value", "bin"):
+        assert np.array_equal(got[k], exp[k]), k
+
+
+def test_ctr_hand_scenarios():
+    """The read-before-increment scenarios of plain_ctr_oracle_test.rs / tensor_ctr_oracle_test.rs."""
+    r = O.ctr_column("Borders", [0, 0, 0, 0], [0, 1, 2, 3], [1, 0, 1, 1], prior=0.5)
+    assert r["value"].tolist() == [0.5, 0.75, 0.5, 0.625]
+    assert r["bin"].tolist() == [7, 11, 7, 9]
+    # (p,x) (p,y) (q,x) (p,x) (q,y) (q,x) as first-seen buckets, identity order
+    combo = O.perfect_hash(np.array([0, 1, 2, 0, 3, 2], np.uint32))[0]
+    r = O.ctr_column("Borders", combo, np.arange(6), [1, 0, 1, 0, 1, 1], prior=0.5)
+    assert r["good"].tolist() == [0, 0, 0, 1, 0, 1] and r["total"].tolist() == [0, 0, 0, 1, 0, 1]
+    assert r["value"][3] == 0.75
