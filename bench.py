@@ -2,9 +2,11 @@
 
 Default workload (the headline metric): config 2 -- Logloss, 10M rows x 200 features
 (100 N(0,1) + 100 lognormal(0,1)), 254 borders (u8 bins, 4 per u32 word), depth 6,
-Bayesian bootstrap T=1, synthetic seeded data.  ``--config 1|3|5`` measures the other
+Bayesian bootstrap T=1, synthetic seeded data.  ``--config 1|3|4|5`` measures the other
 configs of the scope the same way (config 3 = PairLogit over query groups with pairs,
-``--pairwise`` for PairLogitPairwise; config 5 = MultiClass K=10, depth 8, 4096 features).
+``--pairwise`` for PairLogitPairwise; config 4 = RMSE over 30 floats + 20 categorical
+columns as online CTR columns built on the device; config 5 = MultiClass K=10, depth 8,
+4096 features).
 
 A step is one boosting iteration (one tree) through the C-ABI (``cbt_step`` ->
 ``cbh_session_grow``); the bins, target and approximant are resident in HBM before the
@@ -38,8 +40,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "histogram rows·features/s + HBM GB/s; boosting iters/s at 10M×200, depth 6"
 HBM_PEAK_GBS = 8000.0
-DEFAULT_STEPS = {1: 100, 2: 200, 3: 100, 5: 20}
-DEFAULT_CPU_TREES = {1: 5, 2: 2, 3: 3, 5: 1}
+DEFAULT_STEPS = {1: 100, 2: 200, 3: 100, 4: 200, 5: 20}
+DEFAULT_CPU_TREES = {1: 5, 2: 2, 3: 3, 4: 3, 5: 1}
 
 
 def log(*a):
@@ -74,10 +76,34 @@ def _workload(args):
     if args.config == 3:
         return datagen.config3(n_rows=args.rows or 1_000_000, n_features=args.features or 100,
                                loss="PairLogitPairwise" if args.pairwise else "PairLogit")
+    if args.config == 4:
+        return _config4(args.rows or 2_000_000)
     if args.config == 5:
         return datagen.config5(n_rows=args.rows or 1_000_000, n_features=args.features or 4096)
-    raise SystemExit(f"--config {args.config}: configs 1, 2, 3 and 5 are measured (config 4 needs "
-                     "categorical CTR inputs, not built)")
+    raise SystemExit(f"--config {args.config}: configs 1 to 5 are measured")
+
+
+def _config4(n):
+    """Config 4 with its categorical columns as Borders CTR columns (prior 0.5, 16 bins) built
+    on the device over the learn permutation: the reference-legal all-CTR variant."""
+    import numpy as np
+
+    import catboost_rs_amd as cb
+    from catboost_rs_amd import datagen
+
+    d = datagen.config4(n_rows=n)
+    P = d["params"]
+    perm = cb.shuffled_indices(n, P["random_seed"])
+    t0 = time.perf_counter()
+    ctr, counts = cb.ctr_bin_columns(d["cat_keys"], perm, d["target_class"], [P["ctr"]], P["ctr_border_count"])
+    ctr_s = time.perf_counter() - t0
+    bc = P["ctr_border_count"]
+    d["bins"] = np.concatenate([d["bins"], ctr], 0)
+    d["n_borders"] = np.concatenate([d["n_borders"], np.full(ctr.shape[0], bc, np.uint32)])
+    d["ctr_s"], d["ctr_perm"], d["ctr_bucket_counts"] = ctr_s, perm, counts
+    log(f"config 4 CTR columns: {ctr.shape[0]} built on the device in {ctr_s:.3f}s "
+        f"(bucket counts {counts.min()}..{counts.max()})")
+    return d
 
 
 def _train_kwargs(P):
@@ -272,6 +298,8 @@ def main():
     names = {1: "config1: RMSE, no bootstrap, depth 6, 128 borders",
              2: "config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 borders",
              3: f"config3: {P['loss']}, groups of 20, ~10 pairs per group, depth 6, 254 borders",
+             4: "config4: RMSE, Bernoulli 0.66, depth 6, 30 float (254 borders) + 20 categorical as "
+                "Borders CTR columns (prior 0.5, 16 bins)",
              5: "config5: MultiClass K=10, depth 8, 64 borders, 70% zeros"}
     out = {
         "metric": METRIC,
@@ -300,6 +328,8 @@ def main():
         "lds_atomic_roofline": lds,
         "cpu_baseline": cpu,
     }
+    if "ctr_s" in data:
+        out["ctr_columns_s"] = round(data["ctr_s"], 4)
     print(json.dumps(out), flush=True)
 
 

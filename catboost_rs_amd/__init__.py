@@ -93,7 +93,7 @@ class TrainParams(C.Structure):
 EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_session_read_approx", "cbh_session_stats", "cbh_session_reset_stats",
            "cbh_session_end", "cbh_compute_gradients", "cbh_hist_build", "cbh_bootstrap",
-           "cbh_apply_oblivious", "cbh_session_begin_raw", "cbh_select_borders", "cbh_quantize", "cbh_perfect_hash", "cbh_ctr_columns",
+           "cbh_apply_oblivious", "cbh_session_begin_raw", "cbh_select_borders", "cbh_quantize", "cbh_perfect_hash", "cbh_ctr_columns", "cbh_shuffled_indices",
            "cbh_version", "cbh_last_error", "cbt_open", "cbt_open_raw", "cbt_set_pairs", "cbt_step",
            "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close"]
 
@@ -134,6 +134,7 @@ def load(path: str = LIB_PATH):
     L.cbh_select_borders.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_int32, C.c_int32, P, P]
     L.cbh_quantize.argtypes = [P, C.c_uint64, P, C.c_uint32, P]
     L.cbh_perfect_hash.argtypes = [P, C.c_uint64, P, P]
+    L.cbh_shuffled_indices.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32, P]
     L.cbh_ctr_columns.argtypes = [P, C.c_uint32, C.c_uint64, P, P, P, C.c_uint32, C.c_uint32, P, P, P]
     L.cbt_open_raw.argtypes = [C.POINTER(TrainParams), P, P, P, C.c_uint64, C.c_uint32, P, P, C.POINTER(P)]
     L.cbt_set_pairs.argtypes = [P, P, C.c_uint32, P, P, P, C.c_uint64]
@@ -275,6 +276,13 @@ class CtrSpec(C.Structure):
                 ("prior_denom", C.c_double)]
 
 
+def shuffled_indices(n, seed, count=1):
+    """Learn permutations [count][n] (``cbh_shuffled_indices``, host)."""
+    out = np.zeros((count, n), np.uint32)
+    _check(load().cbh_shuffled_indices(n, seed, count, _ptr(out)))
+    return out[0] if count == 1 else out
+
+
 def perfect_hash(keys):
     """First-seen dense bins of u32 keys on the device (``cbh_perfect_hash``)."""
     k = np.ascontiguousarray(keys, np.uint32)
@@ -308,6 +316,21 @@ def ctr_columns(buckets, permutation, target_class, specs, border_count=15, n_bu
     if want_counts:
         out.append(cnt)
     return out[0] if len(out) == 1 else tuple(out)
+
+
+def ctr_bin_columns(cat_keys, permutation, target_class, specs=(("Borders", 0.5),), border_count=15):
+    """CTR bin columns of every categorical column [n_cat][n] (category keys) on the device:
+    first-seen buckets, then the online CTR of each spec over the learn permutation.
+    Returns (bins [n_cat * n_specs][n] u8, feature-major in (column, spec) order, and the
+    bucket count of each column)."""
+    keys = np.ascontiguousarray(cat_keys, np.uint32)
+    out, counts = [], []
+    for j in range(keys.shape[0]):
+        bucket, d = perfect_hash(keys[j])
+        out.append(ctr_columns(bucket, permutation, target_class, list(specs), border_count=border_count,
+                               n_buckets=d))
+        counts.append(d)
+    return np.concatenate(out, 0), np.array(counts, np.int64)
 
 
 def _family_arrays(group_offsets, winner, loser, weight=None):

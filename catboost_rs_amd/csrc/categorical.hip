@@ -193,6 +193,24 @@ __global__ void assign_bins_kernel(const uint32_t* __restrict__ sidx, const uint
 
 extern "C" {
 
+int cbh_shuffled_indices(uint64_t n, uint64_t seed, uint32_t count, uint32_t* out) {
+    if (n && !out) return cbh_internal_fail(CBH_ERR_INVALID_ARG, "out is null");
+    if (n >= (1ull << 32)) return cbh_internal_fail(CBH_ERR_UNSUPPORTED, "more than 2^32 objects");
+    // count Fisher-Yates shuffles drawn one after another off one TFastRng64 stream: for i in
+    // 1..n swap(i, uniform(i + 1)) (permutation.rs:131-160, :236); a sequential host loop, every
+    // swap depends on the previous ones
+    cbh::Rng r = cbh::rng_from_seed(seed);
+    for (uint32_t k = 0; k < count; ++k) {
+        uint32_t* v = out + (size_t)k * n;
+        for (uint64_t i = 0; i < n; ++i) v[i] = (uint32_t)i;
+        for (uint64_t i = 1; i < n; ++i) {
+            const uint64_t j = cbh::rng_uniform(r, i + 1);
+            std::swap(v[i], v[j]);
+        }
+    }
+    return CBH_OK;
+}
+
 int cbh_perfect_hash(const uint32_t* keys, uint64_t n, uint32_t* bins_out, uint32_t* n_distinct_out) {
     if ((n && (!keys || !bins_out)) || !n_distinct_out) return cbh_internal_fail(CBH_ERR_INVALID_ARG, "null argument");
     if (n >= (1ull << 31)) return cbh_internal_fail(CBH_ERR_UNSUPPORTED, "more than 2^31 objects");

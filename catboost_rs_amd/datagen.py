@@ -173,6 +173,37 @@ def config3(scale=1.0, seed=3, n_rows=None, n_features=100, group_size=20, pairs
                             bootstrap_type="No", boost_from_average=False))
 
 
+def config4(n_rows=2_000_000, n_float=30, n_cat=20, seed=4):
+    """RMSE with categorical columns: n x 30 N(0,1) floats (254 borders) and 20 categorical
+    columns, cardinality log-uniform in [2, 10000], values Zipf(1.1)-distributed over the
+    categories; y = X.w + per-category effects + 0.1 N(0,1); depth 6, 200 iterations,
+    Bernoulli 0.66.  Returns the float bins, every categorical column as first-seen keys
+    (category codes; the caller turns them into bins on the device), the CTR target class
+    (y > 0.5, the reference's binclf binarization) and the parameters.  The CTR columns
+    themselves depend on the learn permutation and are built by the caller."""
+    n = int(n_rows)
+    g = np.random.default_rng(seed)
+    X = g.standard_normal((n, n_float)).astype(np.float32)
+    w = g.uniform(-1, 1, n_float)
+    y = X.astype(np.float64) @ w
+    bins, nb, _ = _columns(n, n_float, lambda f: np.ascontiguousarray(X[:, f]), 254, seed, keep_cols=())
+    del X
+    card = np.round(np.exp(g.uniform(np.log(2), np.log(10_000), n_cat))).astype(np.int64)
+    cats = np.empty((n_cat, n), np.uint32)
+    for j in range(n_cat):
+        p = 1.0 / np.arange(1, card[j] + 1) ** 1.1
+        cdf = np.cumsum(p / p.sum())
+        cats[j] = np.minimum(np.searchsorted(cdf, g.random(n)), card[j] - 1)
+        y += g.normal(0, 0.5, card[j])[cats[j]]
+    y += 0.1 * g.standard_normal(n)
+    return dict(name="config4", bins=bins, n_borders=nb, target=y, cat_keys=cats, cardinality=card,
+                target_class=(y > 0.5).astype(np.uint8),
+                params=dict(loss="RMSE", depth=6, iterations=200, learning_rate=0.1, l2_leaf_reg=3.0,
+                            score="Cosine", leaf_method="Gradient", bootstrap_type="Bernoulli",
+                            subsample=0.66, boost_from_average=True, random_seed=0,
+                            ctr=("Borders", 0.5), ctr_border_count=15))
+
+
 def config5(scale=1.0, seed=5, n_rows=None, n_features=4096, n_classes=10):
     """MultiClass K=10: n x 4096 sparse-ish (70% exact zeros, else N(0,1)); 64 borders;
     depth 8, 50 iterations, Newton leaves, no bootstrap.  Labels: argmax of 10 noisy

@@ -263,6 +263,11 @@ int cbh_quantize(const float* column, uint64_t n, const double* borders, uint32_
 
 /* ---- categorical inputs ---- */
 
+/* count learn permutations drawn one after another off TFastRng64::from_seed(seed)
+ * (create_shuffled_indices / permutations, crates/cb-train/src/permutation.rs:131, :236):
+ * out [count][n].  Host code (each Fisher-Yates swap depends on the previous draws). */
+int cbh_shuffled_indices(uint64_t n, uint64_t seed, uint32_t count, uint32_t* out);
+
 /* First-seen dense bins of u32 category keys (the reference hashes a category to a u32 with
  * calc_cat_feature_hash and remaps with PerfectHash, crates/cb-data/src/cat_hash.rs:389-479):
  * bins_out[i] = the rank of keys[i] among the distinct keys ordered by first occurrence. */

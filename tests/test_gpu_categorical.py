@@ -68,3 +68,75 @@ def test_ctr_columns_hand_scenario_and_bins_at_31_borders():
     got = cb.ctr_columns(bucket, perm, cls, SPECS, border_count=31)
     eb, _ = _oracle_cols(bucket, perm, cls, SPECS, bc=31)
     assert np.array_equal(got, eb)
+
+
+def _config4_columns(d, perm):
+    """Device CTR columns of every categorical column, checked against the oracle's."""
+    P = d["params"]
+    dev, counts = cb.ctr_bin_columns(d["cat_keys"], perm, d["target_class"], [P["ctr"]], P["ctr_border_count"])
+    for j, keys in enumerate(d["cat_keys"]):
+        bucket, nb = O.perfect_hash(keys)
+        assert nb == counts[j]
+        exp = O.ctr_column(P["ctr"][0], bucket, perm, d["target_class"], prior=P["ctr"][1],
+                           border_count=P["ctr_border_count"])["bin"]
+        assert np.array_equal(dev[j], exp), f"CTR column {j}"
+    return dev
+
+
+def test_config4_all_ctr_reduced_matches_oracle():
+    """Config 4's reference-legal all-CTR variant at 200k rows (RMSE, Bernoulli 0.66, depth 6):
+    device CTR columns equal the oracle's, then 6 trees equal the oracle's."""
+    from catboost_rs_amd import datagen
+    from tests.test_gpu_parity import _close
+    d = datagen.config4(n_rows=200_000)
+    P = d["params"]
+    n = d["target"].size
+    perm = cb.shuffled_indices(n, P["random_seed"])
+    assert np.array_equal(perm, O.shuffled_indices(n, P["random_seed"]))
+    ctr = _config4_columns(d, perm)
+    bins = np.concatenate([d["bins"], ctr], 0)
+    nb = np.concatenate([d["n_borders"], np.full(ctr.shape[0], P["ctr_border_count"], np.uint32)])
+    kw = dict(loss="RMSE", depth=6, learning_rate=0.1, l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient",
+              bootstrap_type="Bernoulli", subsample=0.66, boost_from_average=True, random_seed=0)
+    exp = O.train(bins, nb, d["target"], iterations=6, **kw)
+    tr = cb.Trainer(bins, int(nb.max()) + 1, d["target"], real_folds=nb + 1, **kw)
+    try:
+        splits, leaves = tr.fit(6)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    assert np.array_equal(splits, exp["splits"])
+    _close(leaves, exp["leaf_values"])
+    _close(approx, exp["approx"])
+
+
+def test_config4_one_hot_and_ctr_extension_matches_oracle():
+    """The stated config 4 mix (categorical columns of cardinality <= 16 one-hot, the rest
+    CTR) -- a combination the reference refuses -- against the oracle's extension, without
+    bootstrap (one-hot columns with RNG draws are refused as in the reference)."""
+    from catboost_rs_amd import datagen
+    from tests.test_gpu_parity import _close
+    d = datagen.config4(n_rows=100_000)
+    P = d["params"]
+    n = d["target"].size
+    perm = cb.shuffled_indices(n, P["random_seed"])
+    small = d["cardinality"] <= 16
+    assert small.any() and (~small).any()
+    ctr = _config4_columns(dict(d, cat_keys=d["cat_keys"][~small]), perm)
+    oh = np.stack([cb.perfect_hash(k)[0] for k in d["cat_keys"][small]]).astype(np.uint8)
+    card = np.array([int(c.max()) + 1 for c in oh], np.uint32)
+    bins = np.concatenate([d["bins"], ctr, oh], 0)
+    nb = np.concatenate([d["n_borders"], np.full(ctr.shape[0], P["ctr_border_count"], np.uint32), card - 1])
+    flags = np.concatenate([np.zeros(bins.shape[0] - oh.shape[0], np.uint8), np.ones(oh.shape[0], np.uint8)])
+    kw = dict(loss="RMSE", depth=6, learning_rate=0.1, l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient",
+              bootstrap_type="No", boost_from_average=True, random_seed=0)
+    exp = O.train(bins, nb, d["target"], iterations=6, one_hot=flags, **kw)
+    tr = cb.Trainer(bins, int(nb.max()) + 1, d["target"], real_folds=nb + 1, one_hot_flags=flags, **kw)
+    try:
+        splits, leaves = tr.fit(6)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    assert np.array_equal(splits, exp["splits"])
+    _close(leaves, exp["leaf_values"])
+    _close(approx, exp["approx"])
