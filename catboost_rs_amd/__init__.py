@@ -95,7 +95,8 @@ EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_session_end", "cbh_compute_gradients", "cbh_hist_build", "cbh_bootstrap",
            "cbh_apply_oblivious", "cbh_session_begin_raw", "cbh_select_borders", "cbh_quantize", "cbh_perfect_hash", "cbh_ctr_columns", "cbh_shuffled_indices",
            "cbh_version", "cbh_last_error", "cbt_open", "cbt_open_raw", "cbt_set_pairs", "cbt_step",
-           "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close"]
+           "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close", "cbh_session_set_profile",
+           "cbt_set_profile"]
 
 _lib = None
 
@@ -145,6 +146,8 @@ def load(path: str = LIB_PATH):
     L.cbt_reset_stats.restype = None
     L.cbt_bias.argtypes = [P]
     L.cbt_bias.restype = C.c_double
+    L.cbh_session_set_profile.argtypes = [P, C.c_int32]
+    L.cbt_set_profile.argtypes = [P, C.c_int32]
     L.cbt_close.argtypes = [P]
     L.cbt_close.restype = None
     _lib = L
@@ -546,6 +549,10 @@ class Trainer:
 
     def reset_stats(self):
         load().cbt_reset_stats(self._h)
+
+    def set_profile(self, on):
+        """Per-stage HIP-event timing on (eager trees) or off (recorded trees replayed)."""
+        _check(load().cbt_set_profile(self._h, int(bool(on))))
 
     def close(self):
         if self._h:

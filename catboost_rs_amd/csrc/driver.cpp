@@ -248,6 +248,12 @@ void cbt_reset_stats(cbt_trainer* t) {
     if (t) cbh_session_reset_stats(t->s);
 }
 
+int cbt_set_profile(cbt_trainer* t, int32_t on) {
+    if (!t) return CBH_ERR_INVALID_ARG;
+    t->p.profile = on;
+    return cbh_session_set_profile(t->s, on);
+}
+
 double cbt_bias(const cbt_trainer* t) { return t ? t->bias : 0.0; }
 
 void cbt_close(cbt_trainer* t) { delete t; }

@@ -174,7 +174,7 @@ static __global__ __launch_bounds__(256) void prepare_kernel(
     uint64_t n, int loss, double* __restrict__ approx, const double* __restrict__ target,
     const double* __restrict__ weight, uint16_t* __restrict__ leaf,
     const double* __restrict__ pending /* [leaves][K] lr-scaled, nullable */,
-    SampleParams smp, JumpTabs jt, const double* __restrict__ host_sample,
+    const SampleParams* __restrict__ smpp, JumpTabs jt, const double* __restrict__ host_sample,
     double* __restrict__ sstat /* [n][K+1] */, int newton,
     unsigned long long* __restrict__ partials /* [gridDim.x][kPartials] */,
     const double* __restrict__ ext_der /* nullable [2][n]: der1, der2 of a pair loss */,
@@ -183,6 +183,9 @@ static __global__ __launch_bounds__(256) void prepare_kernel(
     __shared__ unsigned long long red[4][kPartials];
     unsigned long long acc[kPartials] = {0, 0, 0, 0, 0, 0, 0, 0};
     const double bscale = (double)(1 << kBoundShift);
+    // the tree's sampling parameters live in device memory, so a recorded launch sequence
+    // replays unchanged from tree to tree
+    const SampleParams smp = *smpp;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
         double a[K];

@@ -178,6 +178,17 @@ struct cbh_session {
         return JumpTabs{jump, jump + 1024, jump + 2048, jump + 2048 + n_coarse};
     }
 
+    // per-tree launch sequence recorded once and replayed (index: host sample given or not)
+    hipGraphExec_t tree_graph[2] = {nullptr, nullptr};
+    bool graph_off = false;          // recording failed once: stay eager
+    SampleParams* smp_dev = nullptr; // [2]: the tree's sampling parameters, an inert set
+    // pinned staging of the per-tree results (the recorded copies land here)
+    SampleParams* pin_smp = nullptr;
+    SplitRec* pin_splits = nullptr;
+    LevelPlan* pin_plans = nullptr;
+    Bounds* pin_bounds = nullptr;
+    double* pin_leaves = nullptr;
+
     // profiling
     cbh_stats stats{};
     std::vector<std::pair<int, StageTimer>> timers;
@@ -196,6 +207,13 @@ struct cbh_session {
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st); dfree(dcum);
         dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot);
         dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq);
+        for (auto& g : tree_graph)
+            if (g) (void)hipGraphExecDestroy(g);
+        tree_graph[0] = tree_graph[1] = nullptr;
+        dfree(smp_dev);
+        for (void* p : {(void*)pin_smp, (void*)pin_splits, (void*)pin_plans, (void*)pin_bounds, (void*)pin_leaves})
+            if (p) (void)hipHostFree(p);
+        pin_smp = nullptr; pin_splits = nullptr; pin_plans = nullptr; pin_bounds = nullptr; pin_leaves = nullptr;
         for (auto& t : timers) {
             if (t.second.a) (void)hipEventDestroy(t.second.a);
             if (t.second.b) (void)hipEventDestroy(t.second.b);
@@ -322,6 +340,14 @@ int session_alloc(cbh_session* s) {
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)((size_t)s->pair_tf * 2 * s->B * 2 * sizeof(long long))));
     }
+    CHECK(dalloc(&s->smp_dev, 2));
+    HIP_TRY(hipMemset(s->smp_dev, 0, 2 * sizeof(SampleParams)));
+    HIP_TRY(hipHostMalloc((void**)&s->pin_smp, sizeof(SampleParams), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void**)&s->pin_splits, sizeof(SplitRec) * s->depth, hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void**)&s->pin_plans, sizeof(LevelPlan) * s->depth, hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void**)&s->pin_bounds, sizeof(Bounds), hipHostMallocDefault));
+    HIP_TRY(hipHostMalloc((void**)&s->pin_leaves, sizeof(double) * ((size_t)1 << s->depth) * s->K,
+                          hipHostMallocDefault));
     CHECK(dalloc(&s->leaf_raw, ((size_t)1 << s->depth) * s->K));
     CHECK(dalloc(&s->leaf_scaled, ((size_t)1 << s->depth) * s->K));
     CHECK(dalloc(&s->partials, (size_t)kPrepBlocks * kPartials));
@@ -561,7 +587,11 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     CHECK(plan_tiles(s.get()));
     CHECK(with_k((int)s->K, [&](auto kc) {
         constexpr int K = decltype(kc)::value;
-        return set_fill_attr<K + 1>(s->tiles.lds_bytes);
+        CHECK(set_fill_attr<K + 1>(s->tiles.lds_bytes));
+        const size_t lds = ((size_t)1 << s->depth) * (size_t)leaf_cells<K>() * sizeof(long long);
+        HIP_TRY(hipFuncSetAttribute((const void*)leaf_reduce_kernel<K>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        return CBH_OK;
     }));
     // candidates per feature: float -> real_folds-1 borders; one-hot -> real_folds values
     std::vector<uint32_t> nc(F);
@@ -741,11 +771,14 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     return CBH_OK;
 }
 
+// Every launch of one tree on the session stream, ending with the copies of its results
+// into pinned staging.  No host decision happens between launches (the split, partition
+// plan and leaf values stay on the device), so the sequence can be recorded once as a graph
+// and replayed for every later tree.
 template <int K>
-int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
-              std::vector<SplitRec>& splits_out, std::vector<LevelPlan>& plans_out,
-              Bounds& bounds_out, std::vector<double>& leaf_out) {
+int enqueue_tree(cbh_session* s, bool use_host_sample) {
     constexpr int C = K + 1;
+    const bool apply_prev = s->pending;   // the previous tree's leaves are applied by prepare
     const uint64_t n = s->n;
     hipStream_t st = s->stream;
     const int newton = s->cfg.leaf_method == CBH_LEAF_NEWTON ? 1 : 0;
@@ -757,17 +790,16 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     if (s->ranking) {   // pair ders need every row's updated approximant: apply, then ders
         pairlogit_ders_kernel<<<grid_for(s->n_groups, 256), 256, 0, st>>>(
             s->group_off, s->n_groups, s->comp_off, s->comp_los, s->comp_w, s->approx, s->leaf,
-            s->pending ? s->leaf_scaled : nullptr, s->ext_der, s->ext_der + n);
+            apply_prev ? s->leaf_scaled : nullptr, s->ext_der, s->ext_der + n);
         HIP_TRY(hipGetLastError());
-        s->pending = false;
     }
     const unsigned pgrid = grid_for(n, 256, kPrepBlocks);
     prepare_kernel<K><<<pgrid, 256, 0, st>>>(
-        n, loss, s->approx, s->target, s->weight, s->leaf, s->pending ? s->leaf_scaled : nullptr,
-        smp, s->jt(), use_host_sample ? s->host_sample : nullptr, s->sstat, newton, s->partials,
+        n, loss, s->approx, s->target, s->weight, s->leaf,
+        apply_prev && !s->ranking ? s->leaf_scaled : nullptr,   // a pair loss applied them above
+        s->smp_dev, s->jt(), use_host_sample ? s->host_sample : nullptr, s->sstat, newton, s->partials,
         s->ranking ? s->ext_der : nullptr, s->ranking ? s->score_w : nullptr);
     HIP_TRY(hipGetLastError());
-    s->pending = false;
     scales_kernel<<<1, 256, 0, st>>>(s->partials, pgrid, s->bounds, s->scales);
     HIP_TRY(hipGetLastError());
     quantize_stats_kernel<C><<<grid_for(n * C, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales);
@@ -861,9 +893,7 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     const uint32_t n_leaves = 1u << s->depth;
     const uint32_t CL = (uint32_t)leaf_cells<K>();
     CHECK(launch_zero(s->leaf_sums, (size_t)n_leaves * CL, st));
-    const size_t lds = (size_t)n_leaves * CL * sizeof(long long);
-    HIP_TRY(hipFuncSetAttribute((const void*)leaf_reduce_kernel<K>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    const size_t lds = (size_t)n_leaves * CL * sizeof(long long);   // attribute set at open
     leaf_reduce_kernel<K><<<grid_for(n, 256, 1024), 256, lds, st>>>(
         n, loss, newton, s->approx, s->target, s->weight, s->leaf, s->scales, n_leaves, s->leaf_sums,
         s->ranking ? s->ext_der : nullptr, s->ranking ? s->score_w : nullptr);
@@ -891,16 +921,59 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         }
     }
     CHECK(s->stage_end());
-    s->pending = true;
 
-    splits_out.resize(s->depth);
-    plans_out.resize(s->depth);
-    leaf_out.resize((size_t)n_leaves * K);
-    HIP_TRY(hipMemcpyAsync(splits_out.data(), s->splits, sizeof(SplitRec) * s->depth, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(plans_out.data(), s->plans, sizeof(LevelPlan) * s->depth, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(&bounds_out, s->bounds, sizeof(Bounds), hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(leaf_out.data(), s->leaf_raw, sizeof(double) * leaf_out.size(), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(s->pin_splits, s->splits, sizeof(SplitRec) * s->depth, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(s->pin_plans, s->plans, sizeof(LevelPlan) * s->depth, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(s->pin_bounds, s->bounds, sizeof(Bounds), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(s->pin_leaves, s->leaf_raw, sizeof(double) * n_leaves * K, hipMemcpyDeviceToHost, st));
+    return CBH_OK;
+}
+
+// Record the steady-state tree (previous leaves pending) once per host-sample mode.  A
+// recording failure leaves the session eager for good; it never fails the tree.
+template <int K>
+void record_tree(cbh_session* s, bool use_host_sample) {
+    hipGraphExec_t& ge = s->tree_graph[use_host_sample ? 1 : 0];
+    hipGraph_t g = nullptr;
+    if (hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        (void)hipGetLastError();
+        s->graph_off = true;
+        return;
+    }
+    const int rc = enqueue_tree<K>(s, use_host_sample);
+    const hipError_t e = hipStreamEndCapture(s->stream, &g);
+    if (rc != CBH_OK || e != hipSuccess || !g || hipGraphInstantiateWithFlags(&ge, g, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        ge = nullptr;
+        s->graph_off = true;
+    }
+    if (g) (void)hipGraphDestroy(g);
+}
+
+template <int K>
+int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
+              std::vector<SplitRec>& splits_out, std::vector<LevelPlan>& plans_out,
+              Bounds& bounds_out, std::vector<double>& leaf_out) {
+    hipStream_t st = s->stream;
+    *s->pin_smp = smp;
+    HIP_TRY(hipMemcpyAsync(s->smp_dev, s->pin_smp, sizeof(SampleParams), hipMemcpyHostToDevice, st));
+    // replay the recorded tree when nothing differs from it: previous leaves pending, no
+    // per-stage events, no pairwise stage (its level solves are not recorded)
+    const bool replay = s->pending && !s->cfg.profile && !s->pairwise && !s->graph_off;
+    hipGraphExec_t& ge = s->tree_graph[use_host_sample ? 1 : 0];
+    if (replay && !ge) record_tree<K>(s, use_host_sample);
+    if (replay && ge) {
+        HIP_TRY(hipGraphLaunch(ge, st));
+    } else {
+        CHECK(enqueue_tree<K>(s, use_host_sample));
+    }
+    s->pending = true;
     HIP_TRY(hipStreamSynchronize(st));
+    const size_t n_leaves = (size_t)1 << s->depth;
+    splits_out.assign(s->pin_splits, s->pin_splits + s->depth);
+    plans_out.assign(s->pin_plans, s->pin_plans + s->depth);
+    bounds_out = *s->pin_bounds;
+    leaf_out.assign(s->pin_leaves, s->pin_leaves + n_leaves * K);
     return CBH_OK;
 }
 
@@ -1029,7 +1102,7 @@ int cbh_session_read_approx(cbh_session* s, double* approx_out, uint64_t n_times
             constexpr int K = decltype(kc)::value;
             prepare_kernel<K><<<grid_for(s->n, 256, kPrepBlocks), 256, 0, s->stream>>>(
                 s->n, s->cfg.loss == CBH_LOSS_RMSE ? 0 : 1, s->approx, s->target, s->weight, s->leaf,
-                s->leaf_scaled, SampleParams{}, s->jt(), nullptr, s->sstat, 0, s->partials, nullptr,
+                s->leaf_scaled, s->smp_dev + 1, s->jt(), nullptr, s->sstat, 0, s->partials, nullptr,
                 nullptr);
             HIP_TRY(hipGetLastError());
             return CBH_OK;
@@ -1051,6 +1124,12 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
 
 void cbh_session_reset_stats(cbh_session* s) {
     if (s) s->stats = cbh_stats{};
+}
+
+int cbh_session_set_profile(cbh_session* s, int32_t on) {
+    if (!s) return fail(CBH_ERR_INVALID_ARG, "session is null");
+    s->cfg.profile = on ? 1 : 0;
+    return CBH_OK;
 }
 
 int cbh_session_end(cbh_session* s) {

@@ -194,6 +194,13 @@ typedef struct {
 } cbh_stats;
 
 int cbh_session_stats(const cbh_session* s, cbh_stats* out);
+
+/* Per-stage timing switch (cbh_config.profile).  While it is off, every tree after the
+ * first whose previous leaves are still pending replays one recorded launch sequence (a
+ * HIP graph) instead of launching its ~60 kernels one by one; while it is on, trees run
+ * eagerly with HIP events around every stage.  No counterpart in the reference (its
+ * per-kernel timing is a build-time diagnostic). */
+int cbh_session_set_profile(cbh_session* s, int32_t on);
 void cbh_session_reset_stats(cbh_session* s);
 
 /* Release the session.  Mirrors end_device_training (runtime.rs:1648). */

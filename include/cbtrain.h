@@ -66,6 +66,7 @@ int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8
 int cbt_read_approx(cbt_trainer* t, double* approx_out);     /* [K][n] */
 int cbt_stats(const cbt_trainer* t, cbh_stats* out);
 void cbt_reset_stats(cbt_trainer* t);
+int cbt_set_profile(cbt_trainer* t, int32_t on);   /* cbh_session_set_profile */
 double cbt_bias(const cbt_trainer* t);
 void cbt_close(cbt_trainer* t);
 

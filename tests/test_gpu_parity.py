@@ -484,3 +484,49 @@ def test_trained_model_applied_to_floats_reproduces_training_approx():
     arrs = O.model_arrays(sf, sb, [lv[0] for lv in leaves], 1)
     got = cb.apply_oblivious(d["features"].T, *arrs, bias=[bias])
     _close(got, approx)
+
+
+# ------------------------------------------------------------------ recorded tree replays
+@pytest.mark.parametrize("loss,boot,K", [("RMSE", "No", 1), ("Logloss", "Bayesian", 1), ("RMSE", "Bernoulli", 1),
+                                         ("MultiClass", "Bayesian", 3)])
+def test_recorded_tree_replays_equal_eager_trees(loss, boot, K):
+    """Trees replayed from the recorded launch sequence (profile off) are bit-identical to
+    eagerly launched trees (profile on), every tree, with the per-tree sampling parameters
+    changing between replays, a mid-fit approximant read (which applies the pending leaves
+    eagerly) and a profile switch in the middle of the fit."""
+    g = np.random.default_rng(5)
+    n, F = 30_000, 12
+    bins = g.integers(0, 32, (F, n)).astype(np.uint8)
+    if loss == "MultiClass":
+        y = g.integers(0, K, n).astype(np.float64)
+    elif loss == "Logloss":
+        y = (g.random(n) < 0.4).astype(np.float64)
+    else:
+        y = g.normal(size=n)
+    kw = dict(loss=loss, depth=5, learning_rate=0.2, bootstrap_type=boot, subsample=0.7,
+              leaf_method="Newton" if loss == "MultiClass" else "Gradient", approx_dim=K, random_seed=3)
+
+    def run(profile_schedule):
+        tr = cb.Trainer(bins, 32, y, profile=profile_schedule(0), **kw)
+        out = []
+        try:
+            for it in range(10):
+                tr.set_profile(profile_schedule(it))
+                s, lv, _ = tr.step()
+                out.append((s.copy(), lv.copy()))
+                if it == 4:
+                    out.append((tr.approx().copy(), None))
+            out.append((tr.approx().copy(), None))
+        finally:
+            tr.close()
+        return out
+
+    eager = run(lambda it: True)
+    replay = run(lambda it: False)
+    mixed = run(lambda it: it in (6, 7))
+    for a, b, c in zip(eager, replay, mixed):
+        for x, y_, z in ((a[0], b[0], c[0]), (a[1], b[1], c[1])):
+            if x is None:
+                continue
+            assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(y_).view(np.uint8))
+            assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(z).view(np.uint8))
