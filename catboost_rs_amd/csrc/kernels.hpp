@@ -793,31 +793,61 @@ static __global__ __launch_bounds__(1024) void argmax_kernel(const double* __res
 //                inside a block, ranks come from wave ballots (match on the key bits) and
 //                mbcnt, across waves from per-wave counts in LDS.
 // ---------------------------------------------------------------------------------
-constexpr uint32_t kPartRows = 4096;   // rows per partition block
+constexpr uint32_t kPartRows = 4096;   // rows per partition block (4 waves)
+constexpr uint32_t kPartWaveRows = kPartRows / 4;
 
+// Lanes of this wave whose key equals mine (valid lanes only): one ballot per key bit.
+__device__ __forceinline__ uint64_t wave_peers(uint32_t key, bool valid, uint32_t nbits) {
+    uint64_t mask = __ballot(valid);
+    for (uint32_t bit = 0; bit < nbits; ++bit) {
+        const uint64_t m = __ballot((key >> bit) & 1u);
+        mask &= ((key >> bit) & 1u) ? m : ~m;
+    }
+    return mask;
+}
+
+// Leaf update of one level and the per-wave row counts of every new leaf.  Each wave owns
+// kPartWaveRows consecutive rows; its counts go to cnt[leaf][wave] (one leader per distinct
+// leaf adds the popcount of its peers, so no LDS cell takes more than one add per 64 rows).
 static __global__ __launch_bounds__(256) void split_count_kernel(
     const uint8_t* __restrict__ cols, uint64_t n, const SplitRec* __restrict__ split,
-    uint32_t level, uint16_t* __restrict__ leaf, uint32_t* __restrict__ cnt, uint32_t n_blocks,
+    uint32_t level, uint16_t* __restrict__ leaf, uint32_t* __restrict__ cnt, uint32_t n_waves,
     int write_counts) {
-    __shared__ uint32_t c[kMaxLeaves];
+    __shared__ uint32_t c[4][kMaxLeaves];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t n_new = 2u << level;
-    for (uint32_t i = threadIdx.x; i < n_new; i += blockDim.x) c[i] = 0;
+    for (uint32_t k = lane; k < n_new; k += 64) c[wave][k] = 0;
     __syncthreads();
     const SplitRec s = *split;
     const uint8_t* col = cols + (size_t)s.feature * n;
-    const uint64_t beg = (uint64_t)blockIdx.x * kPartRows;
-    const uint64_t end = min(beg + kPartRows, n);
-    for (uint64_t i = beg + threadIdx.x; i < end; i += blockDim.x) {
-        const uint32_t bin = col[i];
-        const bool pass = s.one_hot ? bin == s.bin : bin > s.bin;
-        uint32_t lf = leaf[i];
-        lf |= (uint32_t)pass << level;
-        leaf[i] = (uint16_t)lf;
-        if (write_counts && !(lf & 0x8000u)) atomicAdd(&c[lf], 1u);
+    const uint64_t wid = (uint64_t)blockIdx.x * 4 + wave;
+    const uint64_t beg = wid * kPartWaveRows;
+    const uint64_t end = min(beg + kPartWaveRows, n);
+    // every load of the wave's rows is issued before any is used (one memory round trip
+    // per wave instead of one per 64 rows)
+    constexpr int U = kPartWaveRows / 64;
+    uint32_t bin[U], lf[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint64_t i = beg + (uint64_t)u * 64 + lane;
+        bin[u] = i < end ? col[i] : 0u;
+        lf[u] = i < end ? leaf[i] : 0x8000u;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint64_t i = beg + (uint64_t)u * 64 + lane;
+        const bool in = i < end;
+        const bool pass = s.one_hot ? bin[u] == s.bin : bin[u] > s.bin;
+        lf[u] |= (uint32_t)pass << level;
+        if (in) leaf[i] = (uint16_t)lf[u];
+        if (write_counts) {
+            const bool valid = in && !(lf[u] & 0x8000u);
+            const uint64_t mask = wave_peers(lf[u], valid, level + 1);
+            if (valid && mbcnt64(mask) == 0) c[wave][lf[u]] += (uint32_t)__popcll(mask);
+        }
     }
     if (!write_counts) return;
-    __syncthreads();
-    for (uint32_t l = threadIdx.x; l < n_new; l += blockDim.x) cnt[(size_t)l * n_blocks + blockIdx.x] = c[l];
+    for (uint32_t k = lane; k < n_new; k += 64) cnt[(size_t)k * n_waves + wid] = c[wave][k];
 }
 
 static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __restrict__ cnt,
@@ -864,60 +894,51 @@ static __global__ void plan_finalize_kernel(const uint32_t* __restrict__ totals,
     plan->rows = off;
 }
 
+// Stable compaction of the rows of every directly built child into idx (grouped by parent in
+// plan order, object order inside each group).  Each wave walks its own rows with per-leaf
+// running offsets in its LDS slice (seeded from the scanned per-wave counts), so the loop
+// needs no block barrier: lanes read their group's offset, then one leader per group
+// advances it.
 static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __restrict__ leaf, uint64_t n,
                                                       uint32_t level, const uint32_t* __restrict__ cnt,
-                                                      uint32_t n_blocks, const LevelPlan* __restrict__ plan,
+                                                      uint32_t n_waves, const LevelPlan* __restrict__ plan,
                                                       uint32_t* __restrict__ idx) {
-    constexpr uint32_t NW = 4;
-    __shared__ uint32_t base[kMaxLeaves / 2];
-    __shared__ uint32_t wcnt[NW][kMaxLeaves / 2];
+    __shared__ uint32_t run[4][kMaxLeaves / 2];
+    __shared__ uint32_t built[kMaxLeaves / 2];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t n_parent = 1u << level;
-    for (uint32_t p = threadIdx.x; p < n_parent; p += blockDim.x) {
-        const uint32_t built = plan->built[p];
-        base[p] = plan->seg_begin[p] + cnt[(size_t)built * n_blocks + blockIdx.x];
-        for (uint32_t w = 0; w < NW; ++w) wcnt[w][p] = 0;
-    }
+    const uint64_t wid = (uint64_t)blockIdx.x * 4 + wave;
+    for (uint32_t p = threadIdx.x; p < n_parent; p += blockDim.x) built[p] = plan->built[p];
+    for (uint32_t p = lane; p < n_parent; p += 64)
+        run[wave][p] = plan->seg_begin[p] + cnt[(size_t)plan->built[p] * n_waves + wid];
     __syncthreads();
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint64_t beg = (uint64_t)blockIdx.x * kPartRows;
-    const uint64_t end = min(beg + kPartRows, n);
-    for (uint64_t t0 = beg; t0 < end; t0 += blockDim.x) {
-        const uint64_t i = t0 + threadIdx.x;
+    const uint64_t beg = wid * kPartWaveRows;
+    const uint64_t end = min(beg + kPartWaveRows, n);
+    constexpr int U = kPartWaveRows / 64;
+    uint32_t lfs[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {   // all loads in flight before the first use
+        const uint64_t i = beg + (uint64_t)u * 64 + lane;
+        lfs[u] = i < end ? leaf[i] : 0x8000u;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint64_t i = beg + (uint64_t)u * 64 + lane;
         uint32_t key = 0;
         bool valid = false;
-        if (i < end) {
-            const uint32_t lf = leaf[i];
-            if (!(lf & 0x8000u)) {
-                const uint32_t p = lf & (n_parent - 1u);
-                if (plan->built[p] == lf) {
-                    key = p;
-                    valid = true;
-                }
+        const uint32_t lf = lfs[u];
+        if (!(lf & 0x8000u)) {
+            const uint32_t p = lf & (n_parent - 1u);
+            if (built[p] == lf) {
+                key = p;
+                valid = true;
             }
         }
-        uint64_t mask = __ballot(valid);
-        for (uint32_t bit = 0; bit < level; ++bit) {
-            const uint64_t m = __ballot((key >> bit) & 1u);
-            mask &= ((key >> bit) & 1u) ? m : ~m;
-        }
+        const uint64_t mask = wave_peers(key, valid, level);
         const uint32_t rank = mbcnt64(mask);
-        if (valid && rank == 0) wcnt[wave][key] = (uint32_t)__popcll(mask);
-        __syncthreads();
-        if (valid) {
-            uint32_t off = 0;
-            for (uint32_t w = 0; w < wave; ++w) off += wcnt[w][key];
-            idx[base[key] + off + rank] = (uint32_t)i;
-        }
-        __syncthreads();
-        for (uint32_t p = threadIdx.x; p < n_parent; p += blockDim.x) {
-            uint32_t s = 0;
-            for (uint32_t w = 0; w < NW; ++w) {
-                s += wcnt[w][p];
-                wcnt[w][p] = 0;
-            }
-            base[p] += s;
-        }
-        __syncthreads();
+        const uint32_t base = valid ? run[wave][key] : 0u;
+        if (valid) idx[base + rank] = (uint32_t)i;
+        if (valid && rank == 0) run[wave][key] = base + (uint32_t)__popcll(mask);
     }
 }
 

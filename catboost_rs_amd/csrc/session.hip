@@ -309,7 +309,7 @@ int session_alloc(cbh_session* s) {
     CHECK(dalloc(&s->hist[0], s->hist_cells_max));
     CHECK(dalloc(&s->hist[1], s->hist_cells_max));
     s->n_part_blocks = (uint32_t)((n + kPartRows - 1) / kPartRows);
-    CHECK(dalloc(&s->cnt, (size_t)s->n_part_blocks << s->depth));
+    CHECK(dalloc(&s->cnt, ((size_t)s->n_part_blocks * 4) << s->depth));   // [leaf][wave]
     CHECK(dalloc(&s->totals, (size_t)1 << s->depth));
     CHECK(dalloc(&s->plans, s->depth));
     CHECK(dalloc(&s->splits, s->depth));
@@ -875,14 +875,14 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         CHECK(s->stage_begin(kStPartition));
         const bool last = level + 1 == s->depth;
         split_count_kernel<<<NB, 256, 0, st>>>(s->cols, n, s->splits + level, level, s->leaf, s->cnt,
-                                               NB, last ? 0 : 1);
+                                               4 * NB, last ? 0 : 1);
         HIP_TRY(hipGetLastError());
         if (!last) {
-            plan_scan_kernel<<<2u << level, 1024, 0, st>>>(s->cnt, NB, s->totals);
+            plan_scan_kernel<<<2u << level, 1024, 0, st>>>(s->cnt, 4 * NB, s->totals);
             HIP_TRY(hipGetLastError());
             plan_finalize_kernel<<<1, 64, 0, st>>>(s->totals, level, s->plans + level);
             HIP_TRY(hipGetLastError());
-            compact_kernel<<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, NB, s->plans + level, s->idx);
+            compact_kernel<<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->plans + level, s->idx);
             HIP_TRY(hipGetLastError());
         }
         CHECK(s->stage_end());
