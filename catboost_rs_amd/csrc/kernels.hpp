@@ -489,6 +489,48 @@ static __global__ void derive_kernel(const long long* __restrict__ parent, long 
     }
 }
 
+// Histograms are kept in PREFIX form over bins (cell b holds the sum of bins 0..b): the
+// split scorer then reads FALSE = prefix[b], TRUE = prefix[B-1] - prefix[b] directly, and
+// the sibling subtraction stays valid because the prefix is linear.  This pass turns the
+// directly built children of a level (raw sums from the fill) into prefix form: one wave per
+// (child, channel, feature) row, each lane scanning up to 4 consecutive bins.
+static __global__ __launch_bounds__(256) void hist_prefix_kernel(long long* __restrict__ hist,
+                                                                 const LevelPlan* __restrict__ plan,
+                                                                 uint32_t n_built, uint32_t C, uint32_t F,
+                                                                 uint32_t B) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint64_t row = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint64_t rows = (uint64_t)n_built * C * F;
+    if (row >= rows) return;   // wave-uniform
+    const uint32_t seg = (uint32_t)(row / ((uint64_t)C * F));
+    const uint32_t rem = (uint32_t)(row - (uint64_t)seg * C * F);
+    const uint32_t slot = plan ? plan->built[seg] : 0u;
+    long long* h = hist + ((size_t)slot * C * F + rem) * B;
+    const uint32_t E = (B + 63) / 64;   // bins per lane, <= 4
+    const uint32_t b0 = lane * E;
+    long long v[4];
+    long long run = 0;
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e) {
+        const uint32_t b = b0 + e;
+        v[e] = (e < E && b < B) ? h[b] : 0;
+        run += v[e];
+        v[e] = run;
+    }
+    long long incl = run;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const long long u = __shfl_up(incl, o, 64);
+        if (lane >= (uint32_t)o) incl += u;
+    }
+    const long long off = incl - run;
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e) {
+        const uint32_t b = b0 + e;
+        if (e < E && b < B) h[b] = v[e] + off;
+    }
+}
+
 // ---------------------------------------------------------------------------------
 // Dominant-bin skip.  A feature whose most frequent bin holds a large share of the rows
 // (sparse columns: 70% exact zeros put 70% of the rows in one bin) makes the fill's LDS
@@ -603,42 +645,6 @@ static __global__ __launch_bounds__(64) void default_bin_fixup_kernel(long long*
 // TRUE children 0..P-1; Cosine = num / sqrt(1e-100 + sum avg^2 w).  The block argmax keeps
 // the highest score, ties to the lowest border (strict first-wins, tree.rs:355-366).
 // ---------------------------------------------------------------------------------
-template <int NW>
-__device__ __forceinline__ void block_scan2(long long vd, long long vw, long long& pd, long long& pw,
-                                            long long& td, long long& tw, long long* sh /*[2*NW+2]*/) {
-    const uint32_t lane = lane_id();
-    const uint32_t wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        long long ud = __shfl_up(vd, o, 64);
-        long long uw = __shfl_up(vw, o, 64);
-        if (lane >= (uint32_t)o) {
-            vd += ud;
-            vw += uw;
-        }
-    }
-    if (lane == 63) {
-        sh[wave] = vd;
-        sh[NW + wave] = vw;
-    }
-    __syncthreads();
-    long long od = 0, ow = 0, sd = 0, sw = 0;
-#pragma unroll
-    for (int k = 0; k < NW; ++k) {
-        if ((uint32_t)k < wave) {
-            od += sh[k];
-            ow += sh[NW + k];
-        }
-        sd += sh[k];
-        sw += sh[NW + k];
-    }
-    __syncthreads();
-    pd = vd + od;
-    pw = vw + ow;
-    td = sd;
-    tw = sw;
-}
-
 template <int K, int NW>
 __global__ __launch_bounds__(64 * NW) void score_kernel(
     const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
@@ -646,7 +652,7 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     const Scales* __restrict__ sc, double l2, int cosine, double* __restrict__ best_score,
     uint32_t* __restrict__ best_bin) {
     constexpr int C = K + 1;
-    __shared__ long long sh[2 * NW + 2];
+    constexpr uint32_t kPre = 8;   // parents whose cells are loaded ahead of their terms
     __shared__ double red_s[NW];
     __shared__ uint32_t red_b[NW];
     const uint32_t f = blockIdx.x;
@@ -664,27 +670,32 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     double num = 0.0;
     double den = 0.0;
     den += 1e-100;
-    // the histogram cells of kPre parents are loaded ahead of their scans (the loop is
-    // otherwise bound by one dependent global load per iteration); the fold order over
-    // (d, side, p) is unchanged
-    constexpr uint32_t kPre = 8;
+    // the histograms are in prefix form over bins: prefix = cell b, total = cell B-1, the
+    // bin itself (one-hot) = cell b - cell b-1.  The cells of kPre parents are loaded ahead
+    // of their terms; the fold order over (d, side, p) is the reference's
+    const bool in = b < B;
     for (int d = 0; d < K; ++d) {
         for (int side = 0; side < 2; ++side) {
             for (uint32_t p0 = 0; p0 < P; p0 += kPre) {
-                long long vdv[kPre], vwv[kPre];
+                long long pdv[kPre], pwv[kPre], tdv[kPre], twv[kPre], qdv[kPre], qwv[kPre];
 #pragma unroll
                 for (uint32_t u = 0; u < kPre; ++u) {
                     const uint32_t p = p0 + u;
-                    const long long* leafh = hist + (size_t)p * C * F * B;
-                    vdv[u] = (b < B && p < P) ? leafh[((size_t)d * F + f) * B + b] : 0;
-                    vwv[u] = (b < B && p < P) ? leafh[((size_t)K * F + f) * B + b] : 0;
+                    const bool ok = in && p < P;
+                    const long long* hd = hist + (((size_t)p * C + d) * F + f) * B;
+                    const long long* hw = hist + (((size_t)p * C + K) * F + f) * B;
+                    pdv[u] = ok ? hd[b] : 0;
+                    pwv[u] = ok ? hw[b] : 0;
+                    tdv[u] = ok ? hd[B - 1] : 0;
+                    twv[u] = ok ? hw[B - 1] : 0;
+                    qdv[u] = (ok && oh && b > 0) ? hd[b - 1] : 0;
+                    qwv[u] = (ok && oh && b > 0) ? hw[b - 1] : 0;
                 }
 #pragma unroll
                 for (uint32_t u = 0; u < kPre; ++u) {
                     if (p0 + u >= P) break;
-                    const long long vd = vdv[u], vw = vwv[u];
-                    long long pd, pw, td, tw;
-                    block_scan2<NW>(vd, vw, pd, pw, td, tw, sh);
+                    const long long pd = pdv[u], pw = pwv[u], td = tdv[u], tw = twv[u];
+                    const long long vd = pd - qdv[u], vw = pw - qwv[u];
                     long long xd, xw;
                     if (!oh) {
                         xd = side == 0 ? pd : td - pd;

@@ -297,20 +297,16 @@ static __global__ __launch_bounds__(256) void pair_scan_kernel(long long* __rest
     }
 }
 
-// Inclusive prefix over buckets of the der channel of the level histogram
-// (hist [P][C][F][B], channel 0): dcum [F][B][P].  One thread per (f, leaf).
+// Inclusive prefix over buckets of the der channel of the level histogram (hist [P][C][F][B]
+// is kept in prefix form, channel 0) regrouped as dcum [F][B][P].  One thread per (f, leaf).
 static __global__ __launch_bounds__(256) void der_scan_kernel(const long long* __restrict__ hist, uint32_t P,
                                                               uint32_t C, uint32_t F, uint32_t B,
                                                               long long* __restrict__ dcum) {
     const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= F * P) return;
     const uint32_t f = t / P, y = t % P;
-    const long long* h = hist + ((size_t)y * C * F + f) * B;
-    long long run = 0;
-    for (uint32_t b = 0; b < B; ++b) {
-        run += h[b];
-        dcum[((size_t)f * B + b) * P + y] = run;
-    }
+    const long long* h = hist + ((size_t)y * C * F + f) * B;   // already a prefix over bins
+    for (uint32_t b = 0; b < B; ++b) dcum[((size_t)f * B + b) * P + y] = h[b];
 }
 
 // MakeZeroAverage (pairwise_scoring.rs:255-265), sequential sum as the reference.

@@ -842,6 +842,11 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
                                                                       s->F, s->B);
             HIP_TRY(hipGetLastError());
         }
+        {   // built children to prefix form over bins (the level's histograms stay in it)
+            const uint64_t rows = (uint64_t)n_seg * C * s->F;
+            hist_prefix_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(cur, lplan, n_seg, C, s->F, s->B);
+            HIP_TRY(hipGetLastError());
+        }
         CHECK(s->stage_end());
         // ---- derive the sibling of every directly built child ----
         if (level > 0) {
