@@ -80,6 +80,12 @@ class Stats(C.Structure):
         return {k: getattr(self, k) for k, _ in self._fields_}
 
 
+class CtrInfo(C.Structure):
+    _fields_ = [("n_ctr", C.c_uint32), ("averaging_bins", C.c_void_p), ("bucket_count", C.c_void_p),
+                ("weight_group", C.c_void_p), ("n_cat", C.c_uint32), ("cat_buckets", C.c_void_p),
+                ("cat_bucket_count", C.c_void_p), ("model_size_reg", C.c_double)]
+
+
 class TrainParams(C.Structure):
     _fields_ = [("loss", C.c_int32), ("score_function", C.c_int32), ("leaf_method", C.c_int32),
                 ("depth", C.c_int32), ("bootstrap_type", C.c_int32),
@@ -96,7 +102,7 @@ EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_apply_oblivious", "cbh_session_begin_raw", "cbh_select_borders", "cbh_quantize", "cbh_perfect_hash", "cbh_ctr_columns", "cbh_shuffled_indices",
            "cbh_version", "cbh_last_error", "cbt_open", "cbt_open_raw", "cbt_set_pairs", "cbt_step",
            "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close", "cbh_session_set_profile",
-           "cbt_set_profile"]
+           "cbt_set_profile", "cbh_session_set_ctr", "cbt_set_ctr"]
 
 _lib = None
 
@@ -147,6 +153,8 @@ def load(path: str = LIB_PATH):
     L.cbt_bias.argtypes = [P]
     L.cbt_bias.restype = C.c_double
     L.cbh_session_set_profile.argtypes = [P, C.c_int32]
+    L.cbh_session_set_ctr.argtypes = [P, C.POINTER(CtrInfo)]
+    L.cbt_set_ctr.argtypes = [P, C.POINTER(CtrInfo)]
     L.cbt_set_profile.argtypes = [P, C.c_int32]
     L.cbt_close.argtypes = [P]
     L.cbt_close.restype = None
@@ -466,10 +474,12 @@ class Trainer:
                  subsample=0.66, bagging_temperature=1.0, boost_from_average=False, random_seed=0,
                  weight=None, approx_dim=1, profile=False, real_folds=None, one_hot_flags=None,
                  pairs=None, group_offsets=None, pairwise_non_diag_reg=0.1, float_columns=None,
-                 float_borders=None):
+                 float_borders=None, ctr=None):
         """``pairs`` = (winner, loser[, weight]) and ``group_offsets`` (CSR over row order) for
         PairLogit / PairLogitPairwise.  With ``bins_fm`` None the trainer opens over the raw
-        float channel: ``float_columns`` f32 [F][n] and ``float_borders`` (F arrays)."""
+        float channel: ``float_columns`` f32 [F][n] and ``float_borders`` (F arrays).  ``ctr`` =
+        dict(avg_bins [n_ctr][n], bucket_count, group, cat_buckets [n_cat][n], cat_bucket_count,
+        model_size_reg) when the last n_ctr columns are CTR columns (``cbt_set_ctr``)."""
         raw = bins_fm is None
         if raw:
             x, cp = _column_ptrs(float_columns)
@@ -501,10 +511,25 @@ class Trainer:
         else:
             _check(load().cbt_open(C.byref(p), _ptr(self.bins), n, F, n_bins, _ptr(rf), _ptr(oh), _ptr(t),
                                    _ptr(w), C.byref(self._h)))
+        if ctr is not None:
+            self._set_ctr(ctr, n)
         if pairs is not None:
             go, pw_, pl_, pwt = _family_arrays(group_offsets, *pairs)
             _check(load().cbt_set_pairs(self._h, _ptr(go), go.shape[0] - 1, _ptr(pw_), _ptr(pl_),
                                         _ptr(pwt), pw_.shape[0]))
+
+    def _set_ctr(self, ctr, n):
+        avg = np.ascontiguousarray(ctr["avg_bins"], np.uint8)
+        m = avg.shape[0]
+        bc = np.ascontiguousarray(ctr["bucket_count"], np.uint32)
+        grp = np.ascontiguousarray(ctr.get("group", np.arange(m)), np.uint32)
+        cat = np.ascontiguousarray(ctr.get("cat_buckets", np.zeros((0, n))), np.uint32)
+        cnb = np.ascontiguousarray(ctr.get("cat_bucket_count",
+                                           [int(c.max()) + 1 if c.size else 0 for c in cat]), np.uint32)
+        self._ctr_keep = (avg, bc, grp, cat, cnb)
+        info = CtrInfo(m, _ptr(avg), _ptr(bc), _ptr(grp), cat.shape[0], _ptr(cat) if cat.shape[0] else None,
+                       _ptr(cnb) if cat.shape[0] else None, float(ctr.get("model_size_reg", 0.5)))
+        _check(load().cbt_set_ctr(self._h, C.byref(info)))
 
     @classmethod
     def from_floats(cls, float_columns, float_borders, target, **kw):

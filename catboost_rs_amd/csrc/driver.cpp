@@ -48,7 +48,7 @@ struct cbt_trainer {
     std::vector<uint8_t> so;
     std::vector<double> leaves;
     // pairs of a pair loss, handed to the session with the first tree
-    bool ranking = false, pairs_pending = false;
+    bool ranking = false, pairs_pending = false, ctr = false;
     std::vector<uint32_t> group_off, pair_win, pair_los;
     std::vector<double> pair_w;
     ~cbt_trainer() {
@@ -166,6 +166,14 @@ int cbt_set_pairs(cbt_trainer* t, const uint32_t* group_offsets, uint32_t n_grou
     return CBH_OK;
 }
 
+int cbt_set_ctr(cbt_trainer* t, const cbh_ctr_info* info) {
+    if (!t) return CBH_ERR_INVALID_ARG;
+    if (!t->first) return cbh_internal_fail(CBH_ERR_INVALID_ARG, "CTR columns are set before the first step");
+    const int rc = cbh_session_set_ctr(t->s, info);
+    if (rc == CBH_OK) t->ctr = true;
+    return rc;
+}
+
 int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8_t* split_one_hot,
              double* leaf_values) {
     if (!t) return CBH_ERR_INVALID_ARG;
@@ -214,7 +222,7 @@ int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8
     t->pairs_pending = false;
     // 3. replay the CPU grower's per-level draws, then the post-tree draws
     if (t->draws_active) {
-        for (int level = 0; level < p.depth; ++level) {
+        for (int level = 0; level < p.depth && !t->ctr; ++level) {
             for (uint32_t f = 0; f < t->F; ++f) (void)cbh::rng_real1(t->rng);
             (void)cbh::rng_gen(t->rng);
             for (uint32_t f = 0; f < t->F; ++f) (void)std_normal(t->rng);

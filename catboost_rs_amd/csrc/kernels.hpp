@@ -650,7 +650,7 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
     const uint32_t* __restrict__ n_cand, const uint8_t* __restrict__ one_hot,
     const Scales* __restrict__ sc, double l2, int cosine, double* __restrict__ best_score,
-    uint32_t* __restrict__ best_bin) {
+    uint32_t* __restrict__ best_bin, const double* __restrict__ fweight /* nullable [F] */) {
     constexpr int C = K + 1;
     constexpr uint32_t kPre = 8;   // parents whose cells are loaded ahead of their terms
     __shared__ double red_s[NW];
@@ -714,6 +714,9 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
         }
     }
     double score = cosine ? num / sqrt(den) : num;
+    // the model_size_reg weight of a CTR column multiplies every candidate's score
+    // (weight * score, tree.rs:3340-3346)
+    if (fweight) score = fweight[f] * score;
     if (b >= nc || score != score) score = -INFINITY;
     // block argmax: max score, ties -> lowest border
     uint32_t bb = b;
@@ -950,6 +953,80 @@ static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __r
         const uint32_t base = valid ? run[wave][key] : 0u;
         if (valid) idx[base + rank] = (uint32_t)i;
         if (valid && rank == 0) run[wave][key] = base + (uint32_t)__popcll(mask);
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// CTR columns.  (1) The model_size_reg weight needs, once the tree holds a float split, the
+// number of distinct (float-partition leaf, bucket) pairs of every CTR-eligible categorical
+// column (phantom_mixed_bucket_count, tree.rs:3093-3178): a bitmap [bucket][leaf] per column,
+// set per block in LDS and OR-ed into the global bitmap once per block (a hot category would
+// otherwise put every one of its rows on one global word), then popcounted.  (2) Leaf values
+// and the approximant use the partition in which each CTR level re-tests the column built
+// under the averaging permutation (assign_leaf_over_ctr_columns, boosting.rs:2905).
+// ---------------------------------------------------------------------------------
+constexpr uint32_t kPhantomLdsWords = 16384;   // 64 KiB of bitmap per block
+
+static __global__ __launch_bounds__(256) void phantom_bits_kernel(
+    const uint16_t* __restrict__ leaf, uint64_t n, uint32_t float_mask, uint32_t L,
+    const uint32_t* __restrict__ cat_bk, const uint32_t* __restrict__ cat_nb,
+    const uint64_t* __restrict__ word_off, uint32_t* __restrict__ bits) {
+    extern __shared__ uint32_t lbits[];
+    const uint32_t c = blockIdx.y;
+    const uint64_t words = ((uint64_t)cat_nb[c] * L + 31) / 32;
+    const bool lds = words <= kPhantomLdsWords;
+    uint32_t* gbits = bits + word_off[c];
+    if (lds) {
+        for (uint32_t w = threadIdx.x; w < words; w += blockDim.x) lbits[w] = 0;
+        __syncthreads();
+    }
+    const uint32_t* bk = cat_bk + (size_t)c * n;
+    const uint64_t per = (n + gridDim.x - 1) / gridDim.x;
+    const uint64_t beg = (uint64_t)blockIdx.x * per;
+    const uint64_t end = min(beg + per, n);
+    for (uint64_t i = beg + threadIdx.x; i < end; i += blockDim.x) {
+        const uint64_t bit = (uint64_t)bk[i] * L + ((uint32_t)leaf[i] & float_mask);
+        if (lds) atomicOr(&lbits[bit >> 5], 1u << (bit & 31u));
+        else atomicOr(&gbits[bit >> 5], 1u << (bit & 31u));
+    }
+    if (!lds) return;
+    __syncthreads();
+    for (uint32_t w = threadIdx.x; w < words; w += blockDim.x)
+        if (lbits[w]) atomicOr(&gbits[w], lbits[w]);
+}
+
+// distinct pairs of every column: one block per column
+static __global__ __launch_bounds__(256) void phantom_count_kernel(const uint32_t* __restrict__ bits,
+                                                                   const uint64_t* __restrict__ word_off,
+                                                                   const uint32_t* __restrict__ cat_nb, uint32_t L,
+                                                                   unsigned long long* __restrict__ cnt) {
+    __shared__ unsigned long long red[256];
+    const uint32_t c = blockIdx.x;
+    const uint64_t words = ((uint64_t)cat_nb[c] * L + 31) / 32;
+    unsigned long long acc = 0;
+    for (uint64_t w = threadIdx.x; w < words; w += blockDim.x) acc += (unsigned long long)__popc(bits[word_off[c] + w]);
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (uint32_t o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) cnt[c] = red[0];
+}
+
+static __global__ __launch_bounds__(256) void averaging_leaf_kernel(uint16_t* __restrict__ leaf, uint64_t n,
+                                                                    const SplitRec* __restrict__ splits,
+                                                                    uint32_t depth, uint32_t fc0,
+                                                                    const uint8_t* __restrict__ avg) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+        uint32_t lf = leaf[i];
+        for (uint32_t l = 0; l < depth; ++l) {
+            const SplitRec sp = splits[l];
+            if (sp.feature < fc0) continue;
+            const uint32_t bit = avg[(size_t)(sp.feature - fc0) * n + i] > sp.bin ? 1u : 0u;
+            lf = (lf & ~(1u << l)) | (bit << l);
+        }
+        leaf[i] = (uint16_t)lf;
     }
 }
 

@@ -178,6 +178,24 @@ struct cbh_session {
         return JumpTabs{jump, jump + 1024, jump + 2048, jump + 2048 + n_coarse};
     }
 
+    // CTR columns: the last ctr_n features, scored with the model_size_reg weight of a
+    // (ctr type, projection) group not used yet; leaves over the averaging-permutation bins
+    uint32_t ctr_n = 0;
+    uint8_t* ctr_avg = nullptr;                 // [ctr_n][n]
+    std::vector<uint32_t> ctr_bc, ctr_group;    // bucket count, group of every CTR column
+    std::vector<uint8_t> ctr_used;              // [ctr_n] groups chosen by an earlier tree
+    uint64_t ctr_eligible_max = 1;
+    uint32_t cat_n = 0;
+    uint32_t* cat_bk = nullptr;                 // [cat_n][n] first-seen buckets
+    uint32_t* cat_nb_dev = nullptr;             // [cat_n]
+    std::vector<uint32_t> cat_nb;
+    uint64_t* phantom_off = nullptr;            // [cat_n] word offsets of the bitmaps
+    uint32_t* phantom_bits = nullptr;
+    unsigned long long* phantom_cnt = nullptr;  // [cat_n]
+    double msr = 0.5;
+    double* fweight = nullptr;                  // [F] score multiplier (1 except CTR columns)
+    std::vector<double> fweight_host;
+
     // per-tree launch sequence recorded once and replayed (index: host sample given or not)
     hipGraphExec_t tree_graph[2] = {nullptr, nullptr};
     bool graph_off = false;          // recording failed once: stay eager
@@ -207,6 +225,8 @@ struct cbh_session {
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st); dfree(dcum);
         dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot);
         dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq);
+        dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
+        dfree(phantom_cnt); dfree(fweight);
         for (auto& g : tree_graph)
             if (g) (void)hipGraphExecDestroy(g);
         tree_graph[0] = tree_graph[1] = nullptr;
@@ -771,6 +791,60 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     return CBH_OK;
 }
 
+// model_size_reg weights of the CTR columns for one level (tree.rs:3245-3346): a column whose
+// (ctr type, projection) group an earlier tree or an earlier level of this tree used scores at
+// weight 1, any other at (1 + buckets / max_count)^(-model_size_reg), max_count the largest
+// bucket count of the CTR columns and, once the tree holds a float split, of the distinct
+// (float-partition leaf, bucket) pairs of the categorical columns.  The weight is computed on
+// the host with the C library's pow, the function the reference calls.
+int ctr_level_weights(cbh_session* s, uint32_t level) {
+    hipStream_t st = s->stream;
+    std::vector<SplitRec> prev(level);
+    if (level) {
+        HIP_TRY(hipMemcpyAsync(prev.data(), s->splits, sizeof(SplitRec) * level, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipStreamSynchronize(st));
+    }
+    const uint32_t fc0 = s->F - s->ctr_n;
+    uint64_t max_count = s->ctr_eligible_max;
+    uint32_t float_mask = 0;
+    for (uint32_t l = 0; l < level; ++l)
+        if (prev[l].feature < fc0) float_mask |= 1u << l;
+    if (float_mask && s->cat_n) {
+        const uint32_t L = 1u << level;
+        std::vector<uint64_t> off(s->cat_n);
+        uint64_t words = 0;
+        for (uint32_t c = 0; c < s->cat_n; ++c) {
+            off[c] = words;
+            words += ((uint64_t)s->cat_nb[c] * L + 31) / 32;
+        }
+        HIP_TRY(hipMemcpyAsync(s->phantom_off, off.data(), sizeof(uint64_t) * s->cat_n, hipMemcpyHostToDevice, st));
+        zero_u32_kernel<<<grid_for(words, 256, 4096), 256, 0, st>>>(s->phantom_bits, words);
+        HIP_TRY(hipGetLastError());
+        phantom_bits_kernel<<<dim3(64, s->cat_n), 256, kPhantomLdsWords * sizeof(uint32_t), st>>>(
+            s->leaf, s->n, float_mask, L, s->cat_bk, s->cat_nb_dev, s->phantom_off, s->phantom_bits);
+        HIP_TRY(hipGetLastError());
+        phantom_count_kernel<<<s->cat_n, 256, 0, st>>>(s->phantom_bits, s->phantom_off, s->cat_nb_dev, L,
+                                                       s->phantom_cnt);
+        HIP_TRY(hipGetLastError());
+        std::vector<unsigned long long> cnt(s->cat_n);
+        HIP_TRY(hipMemcpyAsync(cnt.data(), s->phantom_cnt, sizeof(unsigned long long) * s->cat_n,
+                               hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipStreamSynchronize(st));
+        for (unsigned long long v : cnt) max_count = std::max<uint64_t>(max_count, v);
+    }
+    for (uint32_t c = 0; c < s->ctr_n; ++c) {
+        bool used = s->ctr_used[s->ctr_group[c]] != 0;
+        for (uint32_t l = 0; l < level; ++l)
+            if (prev[l].feature >= fc0 && s->ctr_group[prev[l].feature - fc0] == s->ctr_group[c]) used = true;
+        double w = 1.0;
+        if (!used && s->msr != 0.0 && max_count != 0)
+            w = std::pow(1.0 + (double)s->ctr_bc[c] / (double)max_count, -s->msr);
+        s->fweight_host[fc0 + c] = w;
+    }
+    HIP_TRY(hipMemcpyAsync(s->fweight, s->fweight_host.data(), sizeof(double) * s->F, hipMemcpyHostToDevice, st));
+    return CBH_OK;
+}
+
 // Every launch of one tree on the session stream, ending with the copies of its results
 // into pinned staging.  No host decision happens between launches (the split, partition
 // plan and leaf values stay on the device), so the sequence can be recorded once as a graph
@@ -858,18 +932,22 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             CHECK(s->stage_end());
         }
         // ---- score + argmax ----
+        if (s->ctr_n) CHECK(ctr_level_weights(s, level));
         CHECK(s->stage_begin(kStScore));
         if (s->pairwise) {
             CHECK(pairwise_level(s, cur, level));
         } else if (s->B <= 64)
             score_kernel<K, 1><<<s->F, 64, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
-                                                   s->scales, s->l2, cosine, s->best_score, s->best_bin);
+                                                   s->scales, s->l2, cosine, s->best_score, s->best_bin,
+                                                   s->ctr_n ? s->fweight : nullptr);
         else if (s->B <= 128)
             score_kernel<K, 2><<<s->F, 128, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
-                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin);
+                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin,
+                                                   s->ctr_n ? s->fweight : nullptr);
         else
             score_kernel<K, 4><<<s->F, 256, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
-                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin);
+                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin,
+                                                   s->ctr_n ? s->fweight : nullptr);
         HIP_TRY(hipGetLastError());
         if (!s->pairwise) {
             argmax_kernel<<<1, 1024, 0, st>>>(s->best_score, s->best_bin, s->one_hot, s->F, s->splits + level);
@@ -894,6 +972,11 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
     }
 
     // ---- leaf statistics + values ----
+    if (s->ctr_n) {   // leaves over the averaging-permutation CTR bins
+        averaging_leaf_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->leaf, n, s->splits, s->depth,
+                                                                      s->F - s->ctr_n, s->ctr_avg);
+        HIP_TRY(hipGetLastError());
+    }
     CHECK(s->stage_begin(kStLeaf));
     const uint32_t n_leaves = 1u << s->depth;
     const uint32_t CL = (uint32_t)leaf_cells<K>();
@@ -964,7 +1047,7 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     HIP_TRY(hipMemcpyAsync(s->smp_dev, s->pin_smp, sizeof(SampleParams), hipMemcpyHostToDevice, st));
     // replay the recorded tree when nothing differs from it: previous leaves pending, no
     // per-stage events, no pairwise stage (its level solves are not recorded)
-    const bool replay = s->pending && !s->cfg.profile && !s->pairwise && !s->graph_off;
+    const bool replay = s->pending && !s->cfg.profile && !s->pairwise && !s->graph_off && !s->ctr_n;
     hipGraphExec_t& ge = s->tree_graph[use_host_sample ? 1 : 0];
     if (replay && !ge) record_tree<K>(s, use_host_sample);
     if (replay && ge) {
@@ -979,6 +1062,8 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     plans_out.assign(s->pin_plans, s->pin_plans + s->depth);
     bounds_out = *s->pin_bounds;
     leaf_out.assign(s->pin_leaves, s->pin_leaves + n_leaves * K);
+    for (const SplitRec& sp : splits_out)   // groups used by this tree (ProcessCtrSplit)
+        if (s->ctr_n && sp.feature >= s->F - s->ctr_n) s->ctr_used[s->ctr_group[sp.feature - (s->F - s->ctr_n)]] = 1;
     return CBH_OK;
 }
 
@@ -1129,6 +1214,59 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
 
 void cbh_session_reset_stats(cbh_session* s) {
     if (s) s->stats = cbh_stats{};
+}
+
+int cbh_session_set_ctr(cbh_session* s, const cbh_ctr_info* info) {
+    if (!s || !info) return fail(CBH_ERR_INVALID_ARG, "null argument");
+    const uint64_t n = s->n;
+    const uint32_t m = info->n_ctr;
+    if (m == 0 || m > s->F) return fail(CBH_ERR_OUT_OF_RANGE, "n_ctr must be 1..n_features");
+    if (s->ranking) return fail(CBH_ERR_UNSUPPORTED, "CTR columns are not covered with pair losses");
+    if (s->ctr_n) return fail(CBH_ERR_INVALID_ARG, "the CTR columns are already set");
+    if (!info->averaging_bins || !info->bucket_count || !info->weight_group || (info->n_cat && !info->cat_buckets) ||
+        (info->n_cat && !info->cat_bucket_count))
+        return fail(CBH_ERR_INVALID_ARG, "null CTR array");
+    const uint32_t fc0 = s->F - m;
+    for (uint32_t f = fc0; f < s->F; ++f)
+        if (!s->one_hot_host.empty() && s->one_hot_host[f])
+            return fail(CBH_ERR_UNSUPPORTED, "a CTR column cannot be one-hot");
+    for (uint32_t c = 0; c < m; ++c)
+        if (info->weight_group[c] >= m) return fail(CBH_ERR_OUT_OF_RANGE, "weight_group >= n_ctr");
+    for (uint32_t c = 0; c < info->n_cat; ++c)
+        for (uint64_t i = 0; i < n; ++i)
+            if (info->cat_buckets[(size_t)c * n + i] >= info->cat_bucket_count[c])
+                return fail(CBH_ERR_OUT_OF_RANGE, "categorical bucket >= its bucket count");
+    for (uint64_t i = 0, total = (uint64_t)m * n; i < total; ++i)
+        if (info->averaging_bins[i] >= s->B) return fail(CBH_ERR_OUT_OF_RANGE, "averaging bin >= n_bins");
+    const uint32_t lmax = 1u << (s->depth - 1);
+    uint64_t words = 0;
+    for (uint32_t c = 0; c < info->n_cat; ++c) words += ((uint64_t)info->cat_bucket_count[c] * lmax + 31) / 32;
+    CHECK(dalloc(&s->ctr_avg, (size_t)m * n));
+    HIP_TRY(hipMemcpy(s->ctr_avg, info->averaging_bins, (size_t)m * n, hipMemcpyHostToDevice));
+    CHECK(dalloc(&s->fweight, s->F));
+    s->fweight_host.assign(s->F, 1.0);
+    HIP_TRY(hipMemcpy(s->fweight, s->fweight_host.data(), sizeof(double) * s->F, hipMemcpyHostToDevice));
+    if (info->n_cat) {
+        CHECK(dalloc(&s->cat_bk, (size_t)info->n_cat * n));
+        HIP_TRY(hipMemcpy(s->cat_bk, info->cat_buckets, sizeof(uint32_t) * info->n_cat * n, hipMemcpyHostToDevice));
+        CHECK(dalloc(&s->cat_nb_dev, info->n_cat));
+        HIP_TRY(hipMemcpy(s->cat_nb_dev, info->cat_bucket_count, sizeof(uint32_t) * info->n_cat, hipMemcpyHostToDevice));
+        CHECK(dalloc(&s->phantom_off, info->n_cat));
+        CHECK(dalloc(&s->phantom_bits, std::max<uint64_t>(words, 1)));
+        CHECK(dalloc(&s->phantom_cnt, info->n_cat));
+    }
+    s->ctr_bc.assign(info->bucket_count, info->bucket_count + m);
+    s->ctr_group.assign(info->weight_group, info->weight_group + m);
+    s->ctr_used.assign(m, 0);
+    s->ctr_eligible_max = 1;
+    for (uint32_t v : s->ctr_bc) s->ctr_eligible_max = std::max<uint64_t>(s->ctr_eligible_max, v);
+    HIP_TRY(hipFuncSetAttribute((const void*)phantom_bits_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(kPhantomLdsWords * sizeof(uint32_t))));
+    s->cat_n = info->n_cat;
+    s->cat_nb.assign(info->cat_bucket_count, info->cat_bucket_count + info->n_cat);
+    s->msr = info->model_size_reg;
+    s->ctr_n = m;
+    return CBH_OK;
 }
 
 int cbh_session_set_profile(cbh_session* s, int32_t on) {

@@ -195,6 +195,29 @@ typedef struct {
 
 int cbh_session_stats(const cbh_session* s, cbh_stats* out);
 
+/* CTR columns of a session (DeviceCtrConfig, runtime.rs:1160-1230, for simple projections and
+ * one learning permutation).  The LAST n_ctr features of the session are CTR columns built
+ * under the structure (learning) permutation (cbh_ctr_columns).  They are scored after the
+ * float columns, each candidate's score multiplied by the model_size_reg weight of its
+ * (ctr type, projection) group while no earlier tree and no earlier level of the tree used
+ * the group: (1 + bucket_count / max_count)^(-model_size_reg), max_count the largest bucket
+ * count of the CTR columns and, once the tree holds a float split, of the distinct
+ * (float-partition leaf, bucket) pairs of the categorical columns (tree.rs:2907, :3146-3346).
+ * Leaf values and the resident approximant use the partition in which every CTR level
+ * re-tests the column built under the averaging permutation (assign_leaf_over_ctr_columns,
+ * boosting.rs:2905, :8206).  Trees of such a session run eagerly (per-level host step). */
+typedef struct {
+    uint32_t n_ctr;
+    const uint8_t* averaging_bins;    /* [n_ctr][n] */
+    const uint32_t* bucket_count;     /* [n_ctr] distinct buckets of each column's projection */
+    const uint32_t* weight_group;     /* [n_ctr] group id (< n_ctr) per (ctr type, projection) */
+    uint32_t n_cat;                   /* CTR-eligible categorical columns */
+    const uint32_t* cat_buckets;      /* [n_cat][n] first-seen buckets */
+    const uint32_t* cat_bucket_count; /* [n_cat] */
+    double model_size_reg;            /* 0.5 by default; 0 disables the weight */
+} cbh_ctr_info;
+int cbh_session_set_ctr(cbh_session* s, const cbh_ctr_info* info);
+
 /* Per-stage timing switch (cbh_config.profile).  While it is off, every tree after the
  * first whose previous leaves are still pending replays one recorded launch sequence (a
  * HIP graph) instead of launching its ~60 kernels one by one; while it is on, trees run

@@ -60,6 +60,11 @@ int cbt_set_pairs(cbt_trainer* t, const uint32_t* group_offsets, uint32_t n_grou
 
 /* One boosting iteration.  Outputs (nullable): split_feature/split_bin/split_one_hot
  * [depth]; leaf_values [K][2^depth] as stored in the model (learning-rate scaled). */
+/* CTR columns of the fit (cbh_session_set_ctr; call once after cbt_open, before the first
+ * cbt_step).  A CTR fit consumes no per-level RNG draws (the reference's CTR-aware search,
+ * tree.rs:3445-3470, draws nothing). */
+int cbt_set_ctr(cbt_trainer* t, const cbh_ctr_info* info);
+
 int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8_t* split_one_hot,
              double* leaf_values);
 

@@ -468,11 +468,60 @@ static void scan_score_one_hot(const double* h, uint32_t n_parent, uint32_t n_bi
     free(total_w); free(total_d); free(sd); free(sw);
 }
 
+/* CTR context of one tree (see orc_params) */
+typedef struct {
+    uint32_t n_ctr;
+    const uint32_t* bucket_count;
+    const uint32_t* group;
+    const uint8_t* used_model;   /* [n_ctr] groups chosen by an earlier tree */
+    uint32_t n_cat;
+    const uint32_t* cat_buckets;
+    double model_size_reg;
+} orc_ctr_ctx;
+
+/* number of distinct (float-partition leaf, bucket) pairs (phantom_mixed_bucket_count,
+ * tree.rs:3093-3100) */
+static uint64_t distinct_pairs(const uint32_t* leaf_of, uint32_t leaf_mask, const uint32_t* bucket,
+                               uint64_t n, uint32_t n_leaves) {
+    uint32_t nb = 0;
+    for (uint64_t i = 0; i < n; ++i) if (bucket[i] + 1 > nb) nb = bucket[i] + 1;
+    uint8_t* seen = (uint8_t*)calloc((size_t)n_leaves * nb + 1, 1);
+    uint64_t d = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        size_t k = (size_t)(leaf_of[i] & leaf_mask) * nb + bucket[i];
+        if (!seen[k]) { seen[k] = 1; ++d; }
+    }
+    free(seen);
+    return d;
+}
+
+/* (1 + count / max_count)^(-model_size_reg) (cat_feature_weight, tree.rs:2907-2913) */
+static double cat_feature_weight(uint64_t count, uint64_t max_count, double msr) {
+    if (msr == 0.0 || max_count == 0) return 1.0;
+    double ratio = (double)count / (double)max_count;
+    return pow(1.0 + ratio, -msr);
+}
+
+static int grow_tree_impl(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n, uint32_t F,
+                          const double* der, const double* w, int32_t K, int32_t depth, int32_t score_fn,
+                          double l2, orc_rng* prng, int32_t n_threads, int32_t* out_splits,
+                          double* out_scores, uint32_t* out_leaf_of, double* out_hists,
+                          const uint8_t* one_hot, const orc_ctr_ctx* ctr);
+
 int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n, uint32_t F,
                   const double* der, const double* w, int32_t K, int32_t depth, int32_t score_fn,
                   double l2, orc_rng* prng, int32_t n_threads, int32_t* out_splits,
                   double* out_scores, uint32_t* out_leaf_of, double* out_hists,
                   const uint8_t* one_hot) {
+    return grow_tree_impl(bins_fm, n_borders, n, F, der, w, K, depth, score_fn, l2, prng, n_threads,
+                          out_splits, out_scores, out_leaf_of, out_hists, one_hot, NULL);
+}
+
+static int grow_tree_impl(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n, uint32_t F,
+                          const double* der, const double* w, int32_t K, int32_t depth, int32_t score_fn,
+                          double l2, orc_rng* prng, int32_t n_threads, int32_t* out_splits,
+                          double* out_scores, uint32_t* out_leaf_of, double* out_hists,
+                          const uint8_t* one_hot, const orc_ctr_ctx* ctr) {
     const int C = K + 1;
     uint32_t n_bins = 1;
     for (uint32_t f = 0; f < F; ++f)
@@ -525,6 +574,10 @@ int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
                 double* h = (double*)malloc(sizeof(double) * per_f);
                 if (level == 0) {
                     build_hist(h, 1, n_bins, K, col, der, w, leaf_of, n);
+                } else if (ctr) {
+                    /* the CTR-aware search builds every leaf of the level directly, in object
+                     * order (build_ctr_aware_histogram, tree.rs:3214-3225) */
+                    build_hist(h, n_leaves, n_bins, K, col, der, w, leaf_of, n);
                 } else {
                     derive_hist(h, hists[f], (uint32_t)level, n_bins, K, col, der, w, leaf_of, n,
                                 slot, n_true);
@@ -559,6 +612,36 @@ int orc_grow_tree(const uint8_t* bins_fm, const uint32_t* n_borders, uint64_t n,
          * (tree.rs:1525-1611); the per-feature sub-streams never touch the main stream. */
         /* one flat candidate list: every float (feature asc, border asc), then every one-hot
          * column (feature asc, value asc) (tree.rs:1261-1290, select_best :355-366) */
+        /* CTR columns: score x the model_size_reg weight of a projection no earlier tree
+         * and no earlier level of this tree used (tree.rs:3290-3340); max_count over the CTR
+         * columns and, once a float split is chosen, over the distinct (float-partition leaf,
+         * bucket) pairs of every CTR-eligible categorical column (tree.rs:3146-3178) */
+        if (ctr && ctr->n_ctr) {
+            uint64_t max_count = 0;
+            for (uint32_t c = 0; c < ctr->n_ctr; ++c)
+                if (ctr->bucket_count[c] > max_count) max_count = ctr->bucket_count[c];
+            if (max_count == 0) max_count = 1;
+            uint32_t float_mask = 0;
+            for (int l = 0; l < level; ++l)
+                if ((uint32_t)out_splits[l * 2] < F - ctr->n_ctr) float_mask |= 1u << l;
+            if (float_mask)
+                for (uint32_t c = 0; c < ctr->n_cat; ++c) {
+                    uint64_t d = distinct_pairs(leaf_of, float_mask, ctr->cat_buckets + (size_t)c * n, n,
+                                                1u << level);
+                    if (d > max_count) max_count = d;
+                }
+            for (uint32_t c = 0; c < ctr->n_ctr; ++c) {
+                const uint32_t f = F - ctr->n_ctr + c;
+                int used = ctr->used_model[ctr->group[c]];
+                for (int l = 0; l < level; ++l) {
+                    uint32_t lf = (uint32_t)out_splits[l * 2];
+                    if (lf >= F - ctr->n_ctr && ctr->group[lf - (F - ctr->n_ctr)] == ctr->group[c]) used = 1;
+                }
+                if (used || !scores[f]) continue;
+                const double wgt = cat_feature_weight(ctr->bucket_count[c], max_count, ctr->model_size_reg);
+                for (uint32_t k = 0; k < n_cand[f]; ++k) scores[f][k] = wgt * scores[f][k];
+            }
+        }
         int best_f = -1, best_b = -1, best_oh = 0;
         double best = -INFINITY;
         for (int pass = 0; pass < 2; ++pass)
@@ -1137,7 +1220,9 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
     uint8_t* ctrl = (uint8_t*)malloc(n);
     uint32_t* leaf_of = (uint32_t*)malloc(sizeof(uint32_t) * n);
     double* leaf_vals = (double*)malloc(sizeof(double) * n_leaves * K);
+    uint8_t* used_groups = (uint8_t*)calloc(p->n_ctr + 1, 1);
     int rc = 0;
+    if (p->n_ctr && (any_one_hot || ranking || p->n_ctr > F)) rc = -4;
 
     for (int it = 0; it < p->iterations; ++it) {
         /* derivatives of the current approx */
@@ -1167,7 +1252,20 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
         for (uint64_t i = 0; i < n; ++i) swt[i] = ctrl[i] ? (ranking ? pw[i] : w[i]) * samp[i] : 0.0;
 
         int32_t* splits = out_splits + (size_t)it * depth * 2;
-        if (pairwise_scoring)
+        orc_ctr_ctx cctx;
+        if (p->n_ctr) {
+            cctx.n_ctr = p->n_ctr;
+            cctx.bucket_count = p->ctr_bucket_count;
+            cctx.group = p->ctr_group;
+            cctx.used_model = used_groups;
+            cctx.n_cat = p->n_cat;
+            cctx.cat_buckets = p->cat_buckets;
+            cctx.model_size_reg = p->model_size_reg;
+        }
+        if (p->n_ctr)   /* the CTR search draws nothing per level */
+            rc = grow_tree_impl(bins_fm, n_borders, n, F, sder, swt, K, depth, p->score_function, scaled_l2,
+                                NULL, p->n_threads, splits, NULL, leaf_of, NULL, p->one_hot_flags, &cctx);
+        else if (pairwise_scoring)
             rc = orc_grow_tree_pairwise(bins_fm, n_borders, n, F, d1, pw_win, pw_los, pw_wt, m, depth,
                                         p->l2_leaf_reg, prior, p->n_threads, splits, NULL, leaf_of);
         else
@@ -1175,6 +1273,20 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
                                scaled_l2, draws_active ? &rng : NULL, p->n_threads, splits, NULL,
                                leaf_of, NULL, p->one_hot_flags);
         if (rc) break;
+        if (p->n_ctr) {
+            /* leaf values and approx over the averaging-permutation columns: every CTR level
+             * re-tests its column's averaging bins, float levels keep their bit */
+            const uint32_t fc0 = F - p->n_ctr;
+            for (int l = 0; l < depth; ++l) {
+                uint32_t f = (uint32_t)splits[l * 2];
+                if (f < fc0) continue;
+                used_groups[p->ctr_group[f - fc0]] = 1;
+                const uint8_t* avg = p->ctr_avg_bins + (size_t)(f - fc0) * n;
+                const uint32_t b = (uint32_t)splits[l * 2 + 1];
+                for (uint64_t i = 0; i < n; ++i)
+                    leaf_of[i] = (leaf_of[i] & ~(1u << l)) | ((uint32_t)(avg[i] > b) << l);
+            }
+        }
 
         /* leaf values on the UNSAMPLED derivatives (boosting.rs:2470-2560, :2634) */
         if (p->loss == ORC_LOSS_MULTICLASS) {
@@ -1231,7 +1343,7 @@ int orc_train(const orc_params* p, const uint8_t* bins_fm, const uint32_t* n_bor
     }
     if (out_approx) memcpy(out_approx, approx, sizeof(double) * n * K);
     free(w); free(approx); free(d1); free(d2); free(wd); free(sder); free(swt); free(samp);
-    free(ctrl); free(leaf_of); free(leaf_vals);
+    free(ctrl); free(leaf_of); free(leaf_vals); free(used_groups);
     free(pw_win); free(pw_los); free(pw_wt); free(pw);
     return rc;
 }

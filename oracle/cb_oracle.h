@@ -67,6 +67,20 @@ typedef struct {
     const double* pair_weight;    /* nullable: weight 1 (query_info.rs:236-239) */
     uint64_t n_pairs;
     double pairwise_non_diag_reg; /* bayesian_matrix_reg, 0.1 by default (boosting.rs:1790) */
+    /* CTR columns (greedy_tensor_search_oblivious_with_ctr, tree.rs:3445-3520; simple
+     * projections, one learning permutation): the LAST n_ctr features of bins_fm are the CTR
+     * columns materialized under the structure permutation, scored after the floats with the
+     * model_size_reg weight of a projection not yet used (tree.rs:2907, :3290-3340);
+     * leaf values and the approximant use the partition in which every CTR level re-tests
+     * the column materialized under the averaging permutation (assign_leaf_over_ctr_columns,
+     * boosting.rs:2905, :8206).  The CTR search consumes no per-level RNG draws. */
+    uint32_t n_ctr;
+    const uint8_t* ctr_avg_bins;      /* [n_ctr][n] */
+    const uint32_t* ctr_bucket_count; /* [n_ctr] distinct buckets of each column's projection */
+    const uint32_t* ctr_group;        /* [n_ctr] (ctr_type, projection) identity, < n_ctr */
+    uint32_t n_cat;                   /* CTR-eligible categorical columns (phantom count) */
+    const uint32_t* cat_buckets;      /* [n_cat][n] first-seen buckets */
+    double model_size_reg;            /* 0.5 by default */
 } orc_params;
 
 /* out_splits feature entries of one-hot (equality) splits carry this flag bit */

@@ -38,7 +38,10 @@ class Params(C.Structure):
                 ("pad2_", C.c_float), ("random_seed", C.c_uint64),
                 ("one_hot_flags", C.c_void_p),
                 ("pair_winner", C.c_void_p), ("pair_loser", C.c_void_p), ("pair_weight", C.c_void_p),
-                ("n_pairs", C.c_uint64), ("pairwise_non_diag_reg", C.c_double)]
+                ("n_pairs", C.c_uint64), ("pairwise_non_diag_reg", C.c_double),
+                ("n_ctr", C.c_uint32), ("ctr_avg_bins", C.c_void_p), ("ctr_bucket_count", C.c_void_p),
+                ("ctr_group", C.c_void_p), ("n_cat", C.c_uint32), ("cat_buckets", C.c_void_p),
+                ("model_size_reg", C.c_double)]
 
 
 ONE_HOT_SPLIT = 0x40000000  # flag bit on the feature entry of an equality split
@@ -368,11 +371,13 @@ def train(bins_fm, n_borders, target, *, loss="RMSE", depth=6, iterations=10, le
           l2_leaf_reg=3.0, score="Cosine", bootstrap_type="No", subsample=0.66,
           bagging_temperature=1.0, leaf_method="Gradient", boost_from_average=False,
           random_seed=0, weight=None, approx_dim=1, n_threads=0, staged=False, one_hot=None,
-          pairs=None, pairwise_non_diag_reg=0.1):
+          pairs=None, pairwise_non_diag_reg=0.1, ctr=None):
     """CPU boosting loop.  ``one_hot`` (optional, [F]) flags one-hot columns (for them
     ``n_borders[f] + 1`` is the cardinality); one-hot with bootstrap raises (-4), as the
     reference refuses it.  ``pairs`` = (winner, loser[, weight]) for PairLogit /
-    PairLogitPairwise, in any order."""
+    PairLogitPairwise, in any order.  ``ctr`` = dict(avg_bins [n_ctr][n], bucket_count,
+    group, cat_buckets [n_cat][n], model_size_reg) for fits whose last n_ctr columns are CTR
+    columns under the structure permutation."""
     bins_fm = np.ascontiguousarray(bins_fm, np.uint8)
     F, n = bins_fm.shape
     nb = np.ascontiguousarray(n_borders, np.uint32)
@@ -396,6 +401,16 @@ def train(bins_fm, n_borders, target, *, loss="RMSE", depth=6, iterations=10, le
         p.pair_weight = None if pwt is None else pwt.ctypes.data
         p.n_pairs = pw_.shape[0]
     p.pairwise_non_diag_reg = pairwise_non_diag_reg
+    if ctr is not None:
+        # the last ctr["avg_bins"].shape[0] features are CTR columns (structure permutation)
+        avg = np.ascontiguousarray(ctr["avg_bins"], np.uint8)
+        bc = np.ascontiguousarray(ctr["bucket_count"], np.uint32)
+        grp = np.ascontiguousarray(ctr.get("group", np.arange(avg.shape[0])), np.uint32)
+        cat = np.ascontiguousarray(ctr.get("cat_buckets", np.zeros((0, n))), np.uint32)
+        keep += [avg, bc, grp, cat]
+        p.n_ctr, p.ctr_avg_bins, p.ctr_bucket_count = avg.shape[0], avg.ctypes.data, bc.ctypes.data
+        p.ctr_group, p.n_cat, p.cat_buckets = grp.ctypes.data, cat.shape[0], cat.ctypes.data
+        p.model_size_reg = ctr.get("model_size_reg", 0.5)
     splits = np.zeros((iterations, depth, 2), np.int32)
     leaves = np.zeros((iterations, K, 1 << depth), np.float64)
     approx = np.zeros((K, n), np.float64)

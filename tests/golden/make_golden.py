@@ -31,6 +31,10 @@ expected outputs); no reference source is copied.  Sources:
                              anchors (good / total counts, values) of plain_ctr,
                              ordered_ctr, tensor_ctr and one_hot_cat, and the cat_hash
                              category hashes with their first-seen bins.
+* ``upstream_ctr_fits.npz`` -- catboost 1.2.10 CTR fits ctr_device_{counter,btmv,mixed,buckets}:
+                             float inputs, categorical codes, labels, the full float border
+                             set, per-tree splits (float feature / CTR target border index,
+                             value-space border) and leaf values.
 """
 from __future__ import annotations
 
@@ -249,6 +253,31 @@ def categorical(ref):
     np.savez_compressed(os.path.join(HERE, "categorical.npz"), **arrays)
 
 
+def ctr_fits(ref):
+    """Small CTR fits of catboost 1.2.10 (data only)."""
+    fx = os.path.join(ref, "crates/cb-oracle/fixtures")
+    arrays = {}
+    for name in ("counter", "btmv", "mixed", "buckets"):
+        d = os.path.join(fx, "ctr_device_" + name)
+        m = json.load(open(os.path.join(d, "model.json")))
+        cfg = json.load(open(os.path.join(d, "config.json")))
+        for k in ("X", "X_cat", "y", "borders"):
+            arrays[name + "." + k] = np.load(os.path.join(d, k + ".npy"))
+        kind, idx, border = [], [], []
+        for t in m["oblivious_trees"]:
+            for sp in t["splits"]:
+                ctr = sp["split_type"] != "FloatFeature"
+                kind.append(int(ctr))
+                idx.append(sp.get("ctr_target_border_idx", 0) if ctr else sp["float_feature_index"])
+                border.append(sp["border"])
+        arrays[name + ".split_is_ctr"] = np.array(kind, np.int64)
+        arrays[name + ".split_index"] = np.array(idx, np.int64)
+        arrays[name + ".split_border"] = np.array(border)
+        arrays[name + ".leaf_values"] = np.array([t["leaf_values"] for t in m["oblivious_trees"]])
+        arrays[name + ".params"] = np.frombuffer(json.dumps(cfg["params"]).encode(), np.uint8)
+    np.savez_compressed(os.path.join(HERE, "upstream_ctr_fits.npz"), **arrays)
+
+
 def main():
     ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     rng_kat(ref)
@@ -261,6 +290,7 @@ def main():
     ranking(ref)
     borders(ref)
     categorical(ref)
+    ctr_fits(ref)
 
 
 if __name__ == "__main__":

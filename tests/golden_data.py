@@ -106,3 +106,22 @@ def categorical():
     arrays keyed '<scenario>.<name>')."""
     z = np.load(os.path.join(GOLDEN, "categorical.npz"))
     return {k: z[k] for k in z.files}
+
+
+CTR_SPECS = {"counter": [("Counter", 0.5, 0)], "btmv": [("BinarizedTargetMeanValue", 0.5, 0)],
+             "mixed": [("Borders", 0.5, 0)], "buckets": [("Buckets", 0.5, 0), ("Buckets", 0.5, 1)]}
+
+
+def ctr_fit(name: str):
+    """catboost 1.2.10 CTR fit ``name`` (counter / btmv / mixed / buckets): inputs, params, and
+    per-tree expected splits [(is_ctr, float feature or CTR target border index, border)] and
+    leaf values."""
+    z = np.load(os.path.join(GOLDEN, "upstream_ctr_fits.npz"))
+    g = {k.split(".", 1)[1]: z[k] for k in z.files if k.startswith(name + ".")}
+    params = json.loads(bytes(g.pop("params")).decode())
+    depth = params["depth"]
+    splits = list(zip(g["split_is_ctr"].tolist(), g["split_index"].tolist(), g["split_border"].tolist()))
+    trees = [splits[i:i + depth] for i in range(0, len(splits), depth)]
+    return dict(X=g["X"].astype(np.float32), X_cat=g["X_cat"], y=g["y"].astype(np.float64),
+                borders=g["borders"], trees=trees, leaf_values=g["leaf_values"], params=params,
+                specs=CTR_SPECS[name])

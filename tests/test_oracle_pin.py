@@ -645,3 +645,47 @@ def test_ctr_hand_scenarios():
     r = O.ctr_column("Borders", combo, np.arange(6), [1, 0, 1, 0, 1, 1], prior=0.5)
     assert r["good"].tolist() == [0, 0, 0, 1, 0, 1] and r["total"].tolist() == [0, 0, 0, 1, 0, 1]
     assert r["value"][3] == 0.75
+
+
+@pytest.mark.parametrize("name", ["counter", "btmv", "mixed"])
+def test_ctr_fit_matches_upstream(name):
+    """catboost 1.2.10 CTR fits (Counter / BinarizedTargetMeanValue / Borders, prior 0.5,
+    model_size_reg 0.5, Logloss depth 2 x 5, L2): every split (CTR borders in value space) and
+    every leaf value reproduced -- online CTR columns under the learn permutation, the
+    model_size_reg weights, leaves over the averaging-permutation columns."""
+    from tests.trees import ctr_fit_inputs, ctr_tree_matches
+    u = G.ctr_fit(name)
+    fit = ctr_fit_inputs(u, O)
+    P = u["params"]
+    r = O.train(fit["bins"], fit["n_borders"], u["y"], loss=P["loss_function"], depth=P["depth"],
+                iterations=P["iterations"], learning_rate=P["learning_rate"], l2_leaf_reg=P["l2_leaf_reg"],
+                score=P["score_function"], bootstrap_type="No", boost_from_average=P["boost_from_average"],
+                random_seed=0, ctr=fit["ctr"])
+    for t in range(P["iterations"]):
+        assert ctr_tree_matches(u, fit, r["splits"][t], r["leaf_values"][t][0], t, None), f"tree {t}"
+
+
+def test_ctr_fit_buckets_first_tree_up_to_mirror_tie():
+    """The Buckets fit has two complementary columns (class 0 and class 1 counts of one
+    projection), whose mirrored splits tie exactly in real arithmetic; the first tree's
+    partition and leaf values are reproduced (catboost takes the other side of the tie), later
+    trees are not pinned."""
+    from tests.trees import ctr_fit_inputs
+    u = G.ctr_fit("buckets")
+    fit = ctr_fit_inputs(u, O)
+    P = u["params"]
+    r = O.train(fit["bins"], fit["n_borders"], u["y"], loss=P["loss_function"], depth=P["depth"], iterations=1,
+                learning_rate=P["learning_rate"], l2_leaf_reg=P["l2_leaf_reg"], score=P["score_function"],
+                bootstrap_type="No", boost_from_average=P["boost_from_average"], random_seed=0, ctr=fit["ctr"])
+    F0, av = fit["n_float"], fit["ctr"]["avg_bins"]
+    n = u["y"].size
+    el, gl = np.zeros(n, int), np.zeros(n, int)
+    for l, (is_ctr, idx, border) in enumerate(u["trees"][0]):
+        assert is_ctr
+        el |= (av[idx] > int(round(border - 1))).astype(int) << l
+    for l, (f, b) in enumerate(r["splits"][0]):
+        gl |= ((av[f - F0] if f >= F0 else fit["bins"][f]) > b).astype(int) << l
+    relabel = {}
+    assert all(relabel.setdefault(int(a), int(b)) == int(b) for a, b in zip(el, gl))   # same grouping
+    assert len(set(relabel.values())) == len(relabel)
+    np.testing.assert_allclose(r["leaf_values"][0][0][gl], u["leaf_values"][0][el], rtol=1e-9, atol=1e-15)

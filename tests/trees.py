@@ -53,3 +53,43 @@ def upstream_one_hot_splits(u, t):
             sp.append((f, b))
             oh.append(False)
     return sp, oh
+
+
+def ctr_fit_inputs(u, O, seed=0):
+    """Inputs of a CTR fit from a ``golden_data.ctr_fit`` record, built with the oracle ``O``:
+    float bins over the full border set, first-seen buckets of the categorical codes, the
+    learn permutation S and the averaging permutation Q = S[P_avg] (permutations(n, 2, seed):
+    one learning fold, boosting.rs:5470-5520), the CTR columns of every spec under both."""
+    import numpy as np
+    X, y, B = u["X"], u["y"], u["borders"]
+    n, F0 = X.shape
+    fb = np.stack([O.quantize(X[:, j], B[j]) for j in range(F0)])
+    bucket, nb = O.perfect_hash(np.asarray(u["X_cat"]).reshape(n, -1)[:, 0].astype(np.uint32))
+    st = O.permutations(n, 2, seed)
+    S, Q = st[0], st[0][st[1]]
+    cls = (y > 0.5).astype(np.uint8)
+    col = lambda perm: np.stack([O.ctr_column(t, bucket, perm, cls, prior=pr, target_border_idx=tb)["bin"]
+                                 for t, pr, tb in u["specs"]])
+    sc, av = col(S), col(Q)
+    groups = {}
+    group = np.array([groups.setdefault(t, len(groups)) for t, _, _ in u["specs"]], np.uint32)
+    return dict(bins=np.concatenate([fb, sc]), n_borders=np.full(F0 + sc.shape[0], 15, np.uint32),
+                n_float=F0, ctr=dict(avg_bins=av, bucket_count=np.full(sc.shape[0], nb, np.uint32), group=group,
+                                     cat_buckets=bucket[None, :], cat_bucket_count=np.array([nb], np.uint32),
+                                     model_size_reg=0.5))
+
+
+def ctr_tree_matches(u, fit, splits, leaves, t, bins_avg_float):
+    """Tree t of a CTR fit against catboost's: the same splits (CTR borders in catboost's value
+    space (b + 1) - 2^-20, computed in f32) and leaf values to 1e-9 relative."""
+    import numpy as np
+    F0 = fit["n_float"]
+    got = []
+    for f, b in splits:
+        if f < F0:
+            got.append((0, int(f), float(np.float32(u["borders"][f][b]))))
+        else:
+            tb = u["specs"][f - F0][2]
+            got.append((1, tb, float(np.float32(np.float32(b) + np.float32(1)) - np.float32(2.0 ** -20))))
+    exp = [(k, i, float(np.float32(b))) for k, i, b in u["trees"][t]]
+    return got == exp and np.allclose(leaves, u["leaf_values"][t], rtol=1e-9, atol=1e-15)
