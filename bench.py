@@ -96,15 +96,22 @@ def _config4(n):
 
     d = datagen.config4(n_rows=n)
     P = d["params"]
-    perm = cb.shuffled_indices(n, P["random_seed"])
+    # learn permutation S and averaging permutation Q = S[P_avg] off one seeded stream
+    two = cb.shuffled_indices(n, P["random_seed"], count=2)
+    perm, avg_perm = two[0], two[0][two[1]]
     t0 = time.perf_counter()
     ctr, counts = cb.ctr_bin_columns(d["cat_keys"], perm, d["target_class"], [P["ctr"]], P["ctr_border_count"])
+    avg, _ = cb.ctr_bin_columns(d["cat_keys"], avg_perm, d["target_class"], [P["ctr"]], P["ctr_border_count"])
+    buckets = np.stack([cb.perfect_hash(k)[0] for k in d["cat_keys"]])
     ctr_s = time.perf_counter() - t0
     bc = P["ctr_border_count"]
     d["bins"] = np.concatenate([d["bins"], ctr], 0)
     d["n_borders"] = np.concatenate([d["n_borders"], np.full(ctr.shape[0], bc, np.uint32)])
-    d["ctr_s"], d["ctr_perm"], d["ctr_bucket_counts"] = ctr_s, perm, counts
-    log(f"config 4 CTR columns: {ctr.shape[0]} built on the device in {ctr_s:.3f}s "
+    d["ctr"] = dict(avg_bins=avg, bucket_count=counts.astype(np.uint32),
+                    group=np.arange(len(counts), dtype=np.uint32), cat_buckets=buckets,
+                    cat_bucket_count=counts.astype(np.uint32), model_size_reg=0.5)
+    d["ctr_s"] = ctr_s
+    log(f"config 4 CTR columns: {ctr.shape[0]} x 2 permutations built on the device in {ctr_s:.3f}s "
         f"(bucket counts {counts.min()}..{counts.max()})")
     return d
 
@@ -241,7 +248,9 @@ def main():
         + f", generated in {time.perf_counter() - t0:.1f}s")
 
     t0 = time.perf_counter()
-    tr = cb.Trainer(bins, n_bins, y, real_folds=nb + 1, profile=False, pairs=pairs, group_offsets=go, **kw)
+    ctr = data.get("ctr")
+    tr = cb.Trainer(bins, n_bins, y, real_folds=nb + 1, profile=False, pairs=pairs, group_offsets=go, ctr=ctr,
+                    **kw)
     log(f"session open (upload + pack) {time.perf_counter() - t0:.2f}s")
     for _ in range(args.warmup):
         tr.step()
@@ -297,7 +306,7 @@ def main():
 
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         t0 = time.perf_counter()
-        exp = O.train(bins, nb, y, iterations=cpu_trees, n_threads=threads, pairs=pairs, **kw)
+        exp = O.train(bins, nb, y, iterations=cpu_trees, n_threads=threads, pairs=pairs, ctr=ctr, **kw)
         cpu_wall = time.perf_counter() - t0
         cpu = {"value": round(cpu_trees / cpu_wall, 6), "unit": "iters/s", "cores": threads,
                "kind": "port",
@@ -305,7 +314,7 @@ def main():
                          f"(CPU restatement of the reference algorithm, OpenMP over features)"}
         log(f"cpu: {cpu_trees} trees in {cpu_wall:.1f}s on {threads} threads")
         # the CPU trees must be the GPU run's first trees (parity on the full-size workload)
-        tr2 = cb.Trainer(bins, n_bins, y, real_folds=nb + 1, pairs=pairs, group_offsets=go, **kw)
+        tr2 = cb.Trainer(bins, n_bins, y, real_folds=nb + 1, pairs=pairs, group_offsets=go, ctr=ctr, **kw)
         first, _ = tr2.fit(cpu_trees)
         tr2.close()
         cpu["splits_match_gpu"] = bool(np.array_equal(first, exp["splits"]))
@@ -314,7 +323,7 @@ def main():
              2: "config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 borders",
              3: f"config3: {P['loss']}, groups of 20, ~10 pairs per group, depth 6, 254 borders",
              4: "config4: RMSE, Bernoulli 0.66, depth 6, 30 float (254 borders) + 20 categorical as "
-                "Borders CTR columns (prior 0.5, 16 bins)",
+                "Borders CTR columns (prior 0.5, 16 bins; model_size_reg 0.5, averaging-permutation leaves)",
              5: "config5: MultiClass K=10, depth 8, 64 borders, 70% zeros"}
     out = {
         "metric": METRIC,

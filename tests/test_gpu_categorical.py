@@ -84,22 +84,31 @@ def _config4_columns(d, perm):
 
 
 def test_config4_all_ctr_reduced_matches_oracle():
-    """Config 4's reference-legal all-CTR variant at 200k rows (RMSE, Bernoulli 0.66, depth 6):
-    device CTR columns equal the oracle's, then 6 trees equal the oracle's."""
+    """Config 4's reference-legal all-CTR variant at 200k rows (RMSE, Bernoulli 0.66, depth 6)
+    with the reference's CTR training semantics (model_size_reg weights with the phantom
+    count, leaves over the averaging-permutation columns): device CTR columns equal the
+    oracle's, then 6 trees equal the oracle's."""
     from catboost_rs_amd import datagen
     from tests.test_gpu_parity import _close
     d = datagen.config4(n_rows=200_000)
     P = d["params"]
     n = d["target"].size
-    perm = cb.shuffled_indices(n, P["random_seed"])
+    two = cb.shuffled_indices(n, P["random_seed"], count=2)
+    perm, avg_perm = two[0], two[0][two[1]]
     assert np.array_equal(perm, O.shuffled_indices(n, P["random_seed"]))
     ctr = _config4_columns(d, perm)
+    avg = _config4_columns(d, avg_perm)
+    buckets = np.stack([O.perfect_hash(k)[0] for k in d["cat_keys"]])
+    counts = np.array([int(b.max()) + 1 for b in buckets], np.uint32)
+    info = dict(avg_bins=avg, bucket_count=counts, group=np.arange(len(counts), dtype=np.uint32),
+                cat_buckets=buckets, cat_bucket_count=counts, model_size_reg=0.5)
     bins = np.concatenate([d["bins"], ctr], 0)
     nb = np.concatenate([d["n_borders"], np.full(ctr.shape[0], P["ctr_border_count"], np.uint32)])
     kw = dict(loss="RMSE", depth=6, learning_rate=0.1, l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient",
               bootstrap_type="Bernoulli", subsample=0.66, boost_from_average=True, random_seed=0)
-    exp = O.train(bins, nb, d["target"], iterations=6, **kw)
-    tr = cb.Trainer(bins, int(nb.max()) + 1, d["target"], real_folds=nb + 1, **kw)
+    exp = O.train(bins, nb, d["target"], iterations=6, ctr=info, **kw)
+    assert any(f >= d["bins"].shape[0] for t in exp["splits"] for f, _ in t), "no CTR split chosen"
+    tr = cb.Trainer(bins, int(nb.max()) + 1, d["target"], real_folds=nb + 1, ctr=info, **kw)
     try:
         splits, leaves = tr.fit(6)
         approx = tr.approx()
@@ -140,3 +149,24 @@ def test_config4_one_hot_and_ctr_extension_matches_oracle():
     assert np.array_equal(splits, exp["splits"])
     _close(leaves, exp["leaf_values"])
     _close(approx, exp["approx"])
+
+
+@pytest.mark.parametrize("name", ["counter", "btmv", "mixed"])
+def test_ctr_fit_upstream_on_gpu(name):
+    """catboost 1.2.10's CTR fits reproduced by a device session with CTR columns: every split
+    (CTR borders in catboost's value space) and every leaf value."""
+    from tests.trees import ctr_fit_inputs, ctr_tree_matches
+    u = G.ctr_fit(name)
+    fit = ctr_fit_inputs(u, O)
+    P = u["params"]
+    nb = fit["n_borders"]
+    tr = cb.Trainer(fit["bins"], int(nb.max()) + 1, u["y"], loss=P["loss_function"], depth=P["depth"],
+                    learning_rate=P["learning_rate"], l2_leaf_reg=P["l2_leaf_reg"], score=P["score_function"],
+                    bootstrap_type="No", boost_from_average=P["boost_from_average"], random_seed=0,
+                    real_folds=nb + 1, ctr=fit["ctr"])
+    try:
+        splits, leaves = tr.fit(P["iterations"])
+    finally:
+        tr.close()
+    for t in range(P["iterations"]):
+        assert ctr_tree_matches(u, fit, splits[t], leaves[t][0], t, None), f"tree {t}"
