@@ -966,45 +966,71 @@ static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __r
 // under the averaging permutation (assign_leaf_over_ctr_columns, boosting.rs:2905).
 // ---------------------------------------------------------------------------------
 constexpr uint32_t kPhantomLdsWords = 16384;   // 64 KiB of bitmap per block
+constexpr uint32_t kPhantomBlocks = 32;        // row chunks per column
 
+// Block g of column c sets its rows' (bucket, float leaf) bits in an LDS bitmap and stores
+// it whole into its own slice of part (no global atomics: a hot category would otherwise
+// put thousands of atomics on one word); a column too large for LDS sets its slice directly.
 static __global__ __launch_bounds__(256) void phantom_bits_kernel(
     const uint16_t* __restrict__ leaf, uint64_t n, uint32_t float_mask, uint32_t L,
     const uint32_t* __restrict__ cat_bk, const uint32_t* __restrict__ cat_nb,
-    const uint64_t* __restrict__ word_off, uint32_t* __restrict__ bits) {
+    const uint64_t* __restrict__ word_off, uint32_t* __restrict__ part) {
     extern __shared__ uint32_t lbits[];
-    const uint32_t c = blockIdx.y;
+    const uint32_t c = blockIdx.y, g = blockIdx.x;
     const uint64_t words = ((uint64_t)cat_nb[c] * L + 31) / 32;
     const bool lds = words <= kPhantomLdsWords;
-    uint32_t* gbits = bits + word_off[c];
+    uint32_t* slice = part + word_off[c] + (uint64_t)g * words;
     if (lds) {
         for (uint32_t w = threadIdx.x; w < words; w += blockDim.x) lbits[w] = 0;
         __syncthreads();
     }
     const uint32_t* bk = cat_bk + (size_t)c * n;
     const uint64_t per = (n + gridDim.x - 1) / gridDim.x;
-    const uint64_t beg = (uint64_t)blockIdx.x * per;
+    const uint64_t beg = (uint64_t)g * per;
     const uint64_t end = min(beg + per, n);
-    for (uint64_t i = beg + threadIdx.x; i < end; i += blockDim.x) {
-        const uint64_t bit = (uint64_t)bk[i] * L + ((uint32_t)leaf[i] & float_mask);
-        if (lds) atomicOr(&lbits[bit >> 5], 1u << (bit & 31u));
-        else atomicOr(&gbits[bit >> 5], 1u << (bit & 31u));
+    // a bit already set is only read (reads of one word broadcast; the atomic, which a hot
+    // category would serialize across the lanes of a wave, runs only for a first occurrence)
+    // rows are loaded kU at a time before any is used (the loop is otherwise one memory
+    // round trip per row)
+    constexpr int kU = 16;
+    for (uint64_t i0 = beg + threadIdx.x; i0 < end; i0 += (uint64_t)kU * blockDim.x) {
+        uint32_t b[kU], lf[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const uint64_t i = i0 + (uint64_t)u * blockDim.x;
+            b[u] = i < end ? bk[i] : 0xFFFFFFFFu;
+            lf[u] = i < end ? (uint32_t)leaf[i] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            if (b[u] == 0xFFFFFFFFu) continue;
+            const uint64_t bit = (uint64_t)b[u] * L + (lf[u] & float_mask);
+            const uint32_t m = 1u << (bit & 31u);
+            uint32_t* wp = lds ? &lbits[bit >> 5] : &slice[bit >> 5];
+            if (!(*wp & m)) atomicOr(wp, m);
+        }
     }
     if (!lds) return;
     __syncthreads();
-    for (uint32_t w = threadIdx.x; w < words; w += blockDim.x)
-        if (lbits[w]) atomicOr(&gbits[w], lbits[w]);
+    for (uint32_t w = threadIdx.x; w < words; w += blockDim.x) slice[w] = lbits[w];
 }
 
-// distinct pairs of every column: one block per column
-static __global__ __launch_bounds__(256) void phantom_count_kernel(const uint32_t* __restrict__ bits,
+// distinct pairs of every column: OR of its kPhantomBlocks slices, popcounted (one block per
+// column)
+static __global__ __launch_bounds__(256) void phantom_count_kernel(const uint32_t* __restrict__ part,
                                                                    const uint64_t* __restrict__ word_off,
                                                                    const uint32_t* __restrict__ cat_nb, uint32_t L,
                                                                    unsigned long long* __restrict__ cnt) {
     __shared__ unsigned long long red[256];
     const uint32_t c = blockIdx.x;
     const uint64_t words = ((uint64_t)cat_nb[c] * L + 31) / 32;
+    const uint32_t* base = part + word_off[c];
     unsigned long long acc = 0;
-    for (uint64_t w = threadIdx.x; w < words; w += blockDim.x) acc += (unsigned long long)__popc(bits[word_off[c] + w]);
+    for (uint64_t w = threadIdx.x; w < words; w += blockDim.x) {
+        uint32_t v = 0;
+        for (uint32_t g = 0; g < kPhantomBlocks; ++g) v |= base[(uint64_t)g * words + w];
+        acc += (unsigned long long)__popc(v);
+    }
     red[threadIdx.x] = acc;
     __syncthreads();
     for (uint32_t o = 128; o > 0; o >>= 1) {

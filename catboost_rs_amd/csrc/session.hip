@@ -195,6 +195,7 @@ struct cbh_session {
     double msr = 0.5;
     double* fweight = nullptr;                  // [F] score multiplier (1 except CTR columns)
     std::vector<double> fweight_host;
+    bool fweight_one = false;                   // the device weights are all 1
 
     // per-tree launch sequence recorded once and replayed (index: host sample given or not)
     hipGraphExec_t tree_graph[2] = {nullptr, nullptr};
@@ -797,8 +798,24 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
 // bucket count of the CTR columns and, once the tree holds a float split, of the distinct
 // (float-partition leaf, bucket) pairs of the categorical columns.  The weight is computed on
 // the host with the C library's pow, the function the reference calls.
+bool ctr_all_used(const cbh_session* s) {
+    for (uint32_t c = 0; c < s->ctr_n; ++c)
+        if (!s->ctr_used[s->ctr_group[c]]) return false;
+    return true;
+}
+
 int ctr_level_weights(cbh_session* s, uint32_t level) {
     hipStream_t st = s->stream;
+    if (ctr_all_used(s)) {   // every group is in the model already: every weight is 1
+        if (!s->fweight_one) {
+            std::fill(s->fweight_host.begin(), s->fweight_host.end(), 1.0);
+            HIP_TRY(hipMemcpyAsync(s->fweight, s->fweight_host.data(), sizeof(double) * s->F,
+                                   hipMemcpyHostToDevice, st));
+            s->fweight_one = true;
+        }
+        return CBH_OK;
+    }
+    s->fweight_one = false;
     std::vector<SplitRec> prev(level);
     if (level) {
         HIP_TRY(hipMemcpyAsync(prev.data(), s->splits, sizeof(SplitRec) * level, hipMemcpyDeviceToHost, st));
@@ -813,14 +830,14 @@ int ctr_level_weights(cbh_session* s, uint32_t level) {
         const uint32_t L = 1u << level;
         std::vector<uint64_t> off(s->cat_n);
         uint64_t words = 0;
-        for (uint32_t c = 0; c < s->cat_n; ++c) {
+        for (uint32_t c = 0; c < s->cat_n; ++c) {   // kPhantomBlocks slices per column
             off[c] = words;
-            words += ((uint64_t)s->cat_nb[c] * L + 31) / 32;
+            words += kPhantomBlocks * (((uint64_t)s->cat_nb[c] * L + 31) / 32);
         }
         HIP_TRY(hipMemcpyAsync(s->phantom_off, off.data(), sizeof(uint64_t) * s->cat_n, hipMemcpyHostToDevice, st));
         zero_u32_kernel<<<grid_for(words, 256, 4096), 256, 0, st>>>(s->phantom_bits, words);
         HIP_TRY(hipGetLastError());
-        phantom_bits_kernel<<<dim3(64, s->cat_n), 256, kPhantomLdsWords * sizeof(uint32_t), st>>>(
+        phantom_bits_kernel<<<dim3(kPhantomBlocks, s->cat_n), 256, kPhantomLdsWords * sizeof(uint32_t), st>>>(
             s->leaf, s->n, float_mask, L, s->cat_bk, s->cat_nb_dev, s->phantom_off, s->phantom_bits);
         HIP_TRY(hipGetLastError());
         phantom_count_kernel<<<s->cat_n, 256, 0, st>>>(s->phantom_bits, s->phantom_off, s->cat_nb_dev, L,
@@ -1047,7 +1064,9 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     HIP_TRY(hipMemcpyAsync(s->smp_dev, s->pin_smp, sizeof(SampleParams), hipMemcpyHostToDevice, st));
     // replay the recorded tree when nothing differs from it: previous leaves pending, no
     // per-stage events, no pairwise stage (its level solves are not recorded)
-    const bool replay = s->pending && !s->cfg.profile && !s->pairwise && !s->graph_off && !s->ctr_n;
+    // a CTR session replays once every CTR group is in the model (no per-level host step left)
+    const bool ctr_static = !s->ctr_n || (ctr_all_used(s) && s->fweight_one);
+    const bool replay = s->pending && !s->cfg.profile && !s->pairwise && !s->graph_off && ctr_static;
     hipGraphExec_t& ge = s->tree_graph[use_host_sample ? 1 : 0];
     if (replay && !ge) record_tree<K>(s, use_host_sample);
     if (replay && ge) {
@@ -1240,7 +1259,8 @@ int cbh_session_set_ctr(cbh_session* s, const cbh_ctr_info* info) {
         if (info->averaging_bins[i] >= s->B) return fail(CBH_ERR_OUT_OF_RANGE, "averaging bin >= n_bins");
     const uint32_t lmax = 1u << (s->depth - 1);
     uint64_t words = 0;
-    for (uint32_t c = 0; c < info->n_cat; ++c) words += ((uint64_t)info->cat_bucket_count[c] * lmax + 31) / 32;
+    for (uint32_t c = 0; c < info->n_cat; ++c)
+        words += kPhantomBlocks * (((uint64_t)info->cat_bucket_count[c] * lmax + 31) / 32);
     CHECK(dalloc(&s->ctr_avg, (size_t)m * n));
     HIP_TRY(hipMemcpy(s->ctr_avg, info->averaging_bins, (size_t)m * n, hipMemcpyHostToDevice));
     CHECK(dalloc(&s->fweight, s->F));
