@@ -323,44 +323,12 @@ __device__ inline void zero_average_wave(double* r, int n) {
     __syncthreads();
 }
 
-// One wavefront (the whole workgroup) solves the pairwise leaf system of n <= 64 unknowns
-// (calculate_pairwise_leaf_values, pairwise_scoring.rs:283-345, pairwise_leaves.rs:120-200):
-// W (packed lower triangle, n x n) plus the bucket-weight prior gives the (n-1)x(n-1) SPD
-// matrix M; right-looking Cholesky in LDS (every element receives its pivot subtractions in
-// ascending order, as the reference's left-looking loop applies them), forward and back
-// substitution, res[n-1] = 0, zero average.  A non-positive pivot yields zeros.
-// M holds (n-1) n / 2 doubles (packed), cj / y / res n doubles each.
-__device__ inline void pairwise_solve_wave(const double* __restrict__ W, const double* __restrict__ der, int n,
-                                           double l2, double prior, double* __restrict__ M,
-                                           double* __restrict__ cj, double* __restrict__ y,
-                                           double* __restrict__ res) {
+// In-place Cholesky of the m x m packed system M (right-looking, the reference's row order)
+// and the forward / back substitutions of y; the solution lands in res[0..m), res[m] = 0.  A
+// non-positive pivot gives the zero solution (cholesky_solve's failure arm).
+__device__ inline void pairwise_factor_solve_wave(double* __restrict__ M, int m, double* __restrict__ cj,
+                                                  double* __restrict__ y, double* __restrict__ res) {
     const int lane = threadIdx.x & 63;
-    const double cell_prior = 1.0 / (double)n;
-    const double non_diag = -prior * cell_prior;
-    const double diag = prior * (1.0 - cell_prior) + l2;
-    if (n <= 2) {
-        if (lane == 0) {
-            if (n == 1) {
-                res[0] = 0.0;
-            } else {
-                const double den = W[0] + diag;
-                res[0] = den != 0.0 ? der[0] / den : 0.0;
-                res[1] = 0.0;
-            }
-        }
-        __syncthreads();
-        if (n == 2) zero_average_wave(res, 2);
-        return;
-    }
-    const int m = n - 1;
-    for (int r = lane; r < m; r += 64) {
-        const double* wr = W + r * (r + 1) / 2;
-        double* mr = M + r * (r + 1) / 2;
-        for (int c = 0; c < r; ++c) mr[c] = wr[c] + non_diag;
-        mr[r] = wr[r] + diag;
-        y[r] = der[r];
-    }
-    __syncthreads();
     bool good = true;
     for (int j = 0; j < m; ++j) {
         const double d = M[tri(j, j)];
@@ -414,35 +382,100 @@ __device__ inline void pairwise_solve_wave(const double* __restrict__ W, const d
     }
     if (lane == 0) res[m] = 0.0;
     __syncthreads();
+}
+
+// One wavefront (the whole workgroup) solves the pairwise leaf system of n <= 64 unknowns
+// (calculate_pairwise_leaf_values, pairwise_scoring.rs:283-345, pairwise_leaves.rs:120-200):
+// W (packed lower triangle, n x n) plus the bucket-weight prior gives the (n-1)x(n-1) SPD
+// matrix M; right-looking Cholesky in LDS (every element receives its pivot subtractions in
+// ascending order, as the reference's left-looking loop applies them), forward and back
+// substitution, res[n-1] = 0, zero average.  A non-positive pivot yields zeros.
+// M holds (n-1) n / 2 doubles (packed), cj / y / res n doubles each.
+__device__ inline void pairwise_solve_wave(const double* __restrict__ W, const double* __restrict__ der, int n,
+                                           double l2, double prior, double* __restrict__ M,
+                                           double* __restrict__ cj, double* __restrict__ y,
+                                           double* __restrict__ res) {
+    const int lane = threadIdx.x & 63;
+    const double cell_prior = 1.0 / (double)n;
+    const double non_diag = -prior * cell_prior;
+    const double diag = prior * (1.0 - cell_prior) + l2;
+    if (n <= 2) {
+        if (lane == 0) {
+            if (n == 1) {
+                res[0] = 0.0;
+            } else {
+                const double den = W[0] + diag;
+                res[0] = den != 0.0 ? der[0] / den : 0.0;
+                res[1] = 0.0;
+            }
+        }
+        __syncthreads();
+        if (n == 2) zero_average_wave(res, 2);
+        return;
+    }
+    const int m = n - 1;
+    for (int r = lane; r < m; r += 64) {
+        const double* wr = W + r * (r + 1) / 2;
+        double* mr = M + r * (r + 1) / 2;
+        for (int c = 0; c < r; ++c) mr[c] = wr[c] + non_diag;
+        mr[r] = wr[r] + diag;
+        y[r] = der[r];
+    }
+    __syncthreads();
+    pairwise_factor_solve_wave(M, m, cj, y, res);
     zero_average_wave(res, n);
 }
 
-// calculate_score (pairwise_scoring.rs:352-375): sum_x a[x] (der[x] - 0.5 sum_y a[y] W[x][y]),
-// inner and outer sums sequential.  Returns the value on lane 0.
-__device__ inline double pairwise_score_wave(const double* a, const double* der, const double* W, int n,
-                                             double* part) {
-    const int lane = threadIdx.x & 63;
-    for (int x = lane; x < n; x += 64) {
-        double inner = 0.0;
-        for (int yy = 0; yy < n; ++yy) inner += a[yy] * W[tri(x, yy)];
-        part[x] = a[x] * (der[x] - 0.5 * inner);
-    }
-    __syncthreads();
-    double outer = 0.0;
-    if (lane == 0)
-        for (int x = 0; x < n; ++x) outer += part[x];
-    return outer;
-}
+// LDS of the leaf solve (doubles): W 2080 | M 2080 | der, cj, y, res, part 64 each.
+constexpr size_t kPairSolveLds = (2080 + 2080 + 5 * 64) * sizeof(double);
 
-// LDS of the candidate and leaf solves (doubles): W 2080 | M 2080 (the candidate kernel stages
-// the statistics of its border there first: 2048 cumulative cells + 1024 totals, which is
-// why the region is 3072 long) | der, cj, y, res, part 64 each.
-constexpr size_t kPairSolveLds = (2080 + 3072 + 5 * 64) * sizeof(double);
+// LDS of the candidate solve (doubles): the factorized system M (packed lower triangle, up
+// to 63 rows) | der, cj, y, res, part 64 each.  ~19 KB, so eight waves share a CU.
+constexpr size_t kPairCandLds = (2080 + 5 * 64) * sizeof(double);
+
+// Entries of row r = 2a + u of the 2P x 2P pairwise weight matrix of one border, read from the
+// cumulative statistics R = [P][P][2] at the border and T (the last border's, i.e. totals):
+// wp(b) gives (W[r][2b], W[r][2b+1]) for b != a in fixed point; the diagonal block of row r is
+// (dg, da) (u == 0) or (da, dg) (u == 1).  Integer sums are exact, so every entry equals the
+// staged assembly's bit for bit whatever the order.
+struct PairRow {
+    const long long* R;
+    const long long* T;
+    uint32_t P, a, u;
+    __device__ inline long long da() const { return R[(a * P + a) * 2] - R[(a * P + a) * 2 + 1]; }
+    __device__ inline void wp(uint32_t b, long long& e0, long long& e1, long long& dg_part) const {
+        const uint32_t yv_ = a < b ? a : b, xv = a < b ? b : a;
+        const long long xs = R[(xv * P + yv_) * 2], xg = R[(xv * P + yv_) * 2 + 1];
+        const long long ys = R[(yv_ * P + xv) * 2], yg = R[(yv_ * P + xv) * 2 + 1];
+        const long long total = T[2 * (xv * P + yv_)] + T[2 * (yv_ * P + xv)];
+        const long long w00 = xg + yg, w01 = xs - xg, w10 = ys - yg, w11 = -(xs + ys);
+        if (u == 0) {
+            e0 = w00;
+            e1 = a > b ? w01 : w10;
+            dg_part = a < b ? (w00 + w10) : (w00 + w01);
+        } else {
+            e0 = a > b ? w10 : w01;
+            e1 = w11 + total;
+            dg_part = (a < b ? (w01 + w11) : (w10 + w11)) + total;
+        }
+    }
+    __device__ inline long long dg() const {
+        long long d = -da();
+        for (uint32_t b = 0; b < P; ++b) {
+            if (b == a) continue;
+            long long e0, e1, part;
+            wp(b, e0, e1, part);
+            d -= part;
+        }
+        return d;
+    }
+};
 
 // One wavefront per (border s, feature f): the weight matrix of border s from the cumulative
-// statistics (all terms exact in int64 -- UpdateWeightSumFromTotal plus the accumulated
-// UpdateWeightSumFromNonDiagStats / diagonal deltas, pairwise_scoring.rs:377-430 -- converted
-// once), the der vector from the cumulative der histogram, the leaf solve and the score.
+// pair statistics (calculate_pairwise_score's leaf system, pairwise_scoring.rs:471-581), the
+// prior terms, the 2P-1 Cholesky solve, MakeZeroAverage and the score.  The matrix is built
+// straight into the factorization buffer from the statistics (L2-resident), and the score
+// rebuilds each row from them again instead of keeping a second copy in LDS.
 static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
     const long long* __restrict__ st, const long long* __restrict__ dcum,
     const uint32_t* __restrict__ n_cand, uint32_t P, uint32_t B, const Scales* __restrict__ sc,
@@ -454,11 +487,8 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
         if (lane == 0) scores[(size_t)f * B + s] = -INFINITY;
         return;
     }
-    double* W = sh_pw;
-    double* M = W + 2080;
-    long long* Rs = (long long*)M;           // staged [P][P][2] cumulative at s
-    long long* Ts = Rs + 2048;               // staged [P][P] smaller-border totals
-    double* der = M + 3072;
+    double* M = sh_pw;
+    double* der = M + 2080;
     double* cj = der + 64;
     double* yv = cj + 64;
     double* res = yv + 64;
@@ -467,8 +497,6 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
     const uint32_t PP = P * P;
     const long long* R = st + ((size_t)f * B + s) * PP * 2;
     const long long* T = st + ((size_t)f * B + (B - 1)) * PP * 2;
-    for (uint32_t i = lane; i < 2 * PP; i += 64) Rs[i] = R[i];
-    for (uint32_t i = lane; i < PP; i += 64) Ts[i] = T[2 * i];
     const double inv_d = sc->inv[kScoreDer];
     for (uint32_t yl = lane; yl < P; yl += 64) {
         const long long dp = dcum[((size_t)f * B + s) * P + yl];
@@ -477,37 +505,66 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
         der[2 * yl + 1] = (double)(dt - dp) * inv_d;
     }
     __syncthreads();
-    for (int r = lane; r < n; r += 64) {
-        const uint32_t a = (uint32_t)r >> 1, u = (uint32_t)r & 1u;
-        const long long da = Rs[(a * P + a) * 2] - Rs[(a * P + a) * 2 + 1];
-        long long dg = -da;   // W[r][r]
-        for (uint32_t b = 0; b < P; ++b) {
-            if (b == a) continue;
-            const uint32_t yv_ = a < b ? a : b, xv = a < b ? b : a;
-            const long long xs = Rs[(xv * P + yv_) * 2], xg = Rs[(xv * P + yv_) * 2 + 1];
-            const long long ys = Rs[(yv_ * P + xv) * 2], yg = Rs[(yv_ * P + xv) * 2 + 1];
-            const long long total = Ts[xv * P + yv_] + Ts[yv_ * P + xv];
-            const long long w00 = xg + yg, w01 = xs - xg, w10 = ys - yg, w11 = -(xs + ys);
-            long long e0, e1;   // W[r][2b], W[r][2b+1]
-            if (u == 0) {
-                e0 = w00;
-                e1 = a > b ? w01 : w10;
-                dg -= a < b ? (w00 + w10) : (w00 + w01);
-            } else {
-                e0 = a > b ? w10 : w01;
-                e1 = w11 + total;
-                dg -= (a < b ? (w01 + w11) : (w10 + w11)) + total;
-            }
-            if (2 * b <= (uint32_t)r) W[tri(r, 2 * b)] = (double)e0 * pair_inv;
-            if (2 * b + 1 <= (uint32_t)r) W[tri(r, 2 * b + 1)] = (double)e1 * pair_inv;
+    const double cell_prior = 1.0 / (double)n;
+    const double non_diag = -prior * cell_prior;
+    const double diag = prior * (1.0 - cell_prior) + l2;
+    const int m = n - 1;
+    if (n == 2) {   // one leaf pair: a 1 x 1 system
+        if (lane == 0) {
+            const PairRow pr{R, T, P, 0, 0};
+            const double w00 = (double)pr.dg() * pair_inv;
+            const double den = w00 + diag;
+            res[0] = den != 0.0 ? der[0] / den : 0.0;
+            res[1] = 0.0;
         }
-        W[tri(r, r)] = (double)dg * pair_inv;
-        if (u == 1) W[tri(r, r - 1)] = (double)da * pair_inv;
+        __syncthreads();
+        zero_average_wave(res, 2);
+    } else {
+        // M = W + prior terms on the first m rows (lower triangle)
+        for (int r = lane; r < m; r += 64) {
+            const PairRow pr{R, T, P, (uint32_t)r >> 1, (uint32_t)r & 1u};
+            double* mr = M + r * (r + 1) / 2;
+            long long dg = -pr.da();
+            for (uint32_t b = 0; b < P; ++b) {
+                if (b == pr.a) continue;
+                long long e0, e1, dpart;
+                pr.wp(b, e0, e1, dpart);
+                dg -= dpart;
+                if ((int)(2 * b) < r) mr[2 * b] = (double)e0 * pair_inv + non_diag;
+                if ((int)(2 * b + 1) < r) mr[2 * b + 1] = (double)e1 * pair_inv + non_diag;
+            }
+            mr[r] = (double)dg * pair_inv + diag;
+            if (pr.u == 1) mr[r - 1] = (double)pr.da() * pair_inv + non_diag;
+            yv[r] = der[r];
+        }
+        __syncthreads();
+        pairwise_factor_solve_wave(M, m, cj, yv, res);
+        zero_average_wave(res, n);
+    }
+    // score (calculate_score, pairwise_scoring.rs:352-375): inner and outer sums sequential
+    for (int x = lane; x < n; x += 64) {
+        const PairRow pr{R, T, P, (uint32_t)x >> 1, (uint32_t)x & 1u};
+        const long long dg = pr.dg(), da = pr.da();
+        double inner = 0.0;
+        for (uint32_t b = 0; b < P; ++b) {
+            long long e0, e1, dpart;
+            if (b == pr.a) {
+                e0 = pr.u == 0 ? dg : da;
+                e1 = pr.u == 0 ? da : dg;
+            } else {
+                pr.wp(b, e0, e1, dpart);
+            }
+            inner += res[2 * b] * ((double)e0 * pair_inv);
+            inner += res[2 * b + 1] * ((double)e1 * pair_inv);
+        }
+        part[x] = res[x] * (der[x] - 0.5 * inner);
     }
     __syncthreads();
-    pairwise_solve_wave(W, der, n, l2, prior, M, cj, yv, res);
-    const double score = pairwise_score_wave(res, der, W, n, part);
-    if (lane == 0) scores[(size_t)f * B + s] = score;
+    if (lane == 0) {
+        double outer = 0.0;
+        for (int x = 0; x < n; ++x) outer += part[x];
+        scores[(size_t)f * B + s] = outer;
+    }
 }
 
 // Best border of each feature: maximum score, lowest border on ties (strict first-wins over
@@ -612,7 +669,7 @@ static __global__ __launch_bounds__(64) void pairwise_leaf_kernel(
     extern __shared__ double sh_pl[];
     double* W = sh_pl;
     double* M = W + 2080;
-    double* der = M + 3072;
+    double* der = M + 2080;
     double* cj = der + 64;
     double* yv = cj + 64;
     double* res = yv + 64;

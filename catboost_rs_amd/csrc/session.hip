@@ -782,7 +782,7 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     }
     der_scan_kernel<<<grid_for((uint64_t)F * P, 256), 256, 0, st>>>(cur, P, s->C, F, B, s->dcum);
     HIP_TRY(hipGetLastError());
-    pairwise_candidate_kernel<<<dim3(B - 1, F), 64, kPairSolveLds, st>>>(
+    pairwise_candidate_kernel<<<dim3(B - 1, F), 64, kPairCandLds, st>>>(
         s->pair_st, s->dcum, s->n_cand, P, B, s->scales, s->pair_inv, s->l2, s->prior, s->cand_scores);
     HIP_TRY(hipGetLastError());
     pairwise_best_kernel<<<F, 256, 0, st>>>(s->cand_scores, s->n_cand, B, s->best_score, s->best_bin);
