@@ -363,17 +363,17 @@ __device__ inline void pairwise_factor_solve_wave(double* __restrict__ M, int m,
         __syncthreads();
     }
     if (good) {
+        // every lane divides (the same IEEE quotient) instead of lane 0 publishing it, so a
+        // step needs one barrier; y[p] is read by all lanes before lane 0 overwrites it
         for (int p = 0; p < m; ++p) {   // forward: y[i] -= L[i][p] y[p], p ascending
-            if (lane == 0) y[p] = y[p] / M[tri(p, p)];
-            __syncthreads();
-            const double yp = y[p];
+            const double yp = y[p] / M[tri(p, p)];
+            if (lane == 0) y[p] = yp;
             for (int i = p + 1 + lane; i < m; i += 64) y[i] -= M[tri(i, p)] * yp;
             __syncthreads();
         }
         for (int p = m - 1; p >= 0; --p) {   // back: L^T x = y
-            if (lane == 0) res[p] = y[p] / M[tri(p, p)];
-            __syncthreads();
-            const double xp = res[p];
+            const double xp = y[p] / M[tri(p, p)];
+            if (lane == 0) res[p] = xp;
             for (int i = lane; i < p; i += 64) y[i] -= M[tri(p, i)] * xp;
             __syncthreads();
         }
@@ -429,9 +429,12 @@ __device__ inline void pairwise_solve_wave(const double* __restrict__ W, const d
 // LDS of the leaf solve (doubles): W 2080 | M 2080 | der, cj, y, res, part 64 each.
 constexpr size_t kPairSolveLds = (2080 + 2080 + 5 * 64) * sizeof(double);
 
-// LDS of the candidate solve (doubles): the factorized system M (packed lower triangle, up
-// to 63 rows) | der, cj, y, res, part 64 each.  ~19 KB, so eight waves share a CU.
-constexpr size_t kPairCandLds = (2080 + 5 * 64) * sizeof(double);
+// LDS of the candidate solve (8-byte words): L (packed lower triangle, up to 63 rows; the
+// border's statistics once the solve is done) | der, res, part, dgs 64 each.  ~18 KB, so eight
+// waves share a CU.
+constexpr size_t kPairCandLds = (2080 + 4 * 64) * sizeof(double);
+// Leaf pairs whose statistics one lane loads before using any of them.
+constexpr uint32_t kPairBatch = 8;
 
 // Entries of row r = 2a + u of the 2P x 2P pairwise weight matrix of one border, read from the
 // cumulative statistics R = [P][P][2] at the border and T (the last border's, i.e. totals):
@@ -471,15 +474,31 @@ struct PairRow {
     }
 };
 
-// One wavefront per (border s, feature f): the weight matrix of border s from the cumulative
-// pair statistics (calculate_pairwise_score's leaf system, pairwise_scoring.rs:471-581), the
-// prior terms, the 2P-1 Cholesky solve, MakeZeroAverage and the score.  The matrix is built
-// straight into the factorization buffer from the statistics (L2-resident), and the score
-// rebuilds each row from them again instead of keeping a second copy in LDS.
+// The double of lane l (uniform l) on every lane.
+__device__ inline double readlane_f64(double v, int l) {
+    const long long bits = __double_as_longlong(v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)bits, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(bits >> 32), l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// One wavefront per (border s, feature f) at a level of P_ leaves: the weight matrix of border
+// s from the cumulative pair statistics (calculate_pairwise_score's leaf system,
+// pairwise_scoring.rs:471-581), the prior terms, the 2P-1 Cholesky solve, MakeZeroAverage and
+// the score.  Lane r holds row r of the system in registers (entries above the diagonal are
+// don't-care), so the factorization runs without LDS traffic: the pivot and the pivot column
+// come from the owning lanes by readlane, and every element still receives its pivot
+// subtractions in ascending order with the reference's roundings (pairwise_factor_solve_wave
+// is the same arithmetic over LDS).  The back substitution reads L^T from LDS; the score
+// rebuilds each row of W from the statistics staged over that buffer afterwards.
+template <uint32_t P_>
 static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
     const long long* __restrict__ st, const long long* __restrict__ dcum,
-    const uint32_t* __restrict__ n_cand, uint32_t P, uint32_t B, const Scales* __restrict__ sc,
-    double pair_inv, double l2, double prior, double* __restrict__ scores /* [F][B] */) {
+    const uint32_t* __restrict__ n_cand, uint32_t B, const Scales* __restrict__ sc, double pair_inv,
+    double l2, double prior, double* __restrict__ scores /* [F][B] */) {
+    constexpr uint32_t P = P_;
+    constexpr int n = 2 * (int)P_, m = n - 1;
+    static_assert(n <= 64, "one row per lane");
     extern __shared__ double sh_pw[];
     const uint32_t s = blockIdx.x, f = blockIdx.y;
     const int lane = threadIdx.x;
@@ -487,14 +506,12 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
         if (lane == 0) scores[(size_t)f * B + s] = -INFINITY;
         return;
     }
-    double* M = sh_pw;
+    double* M = sh_pw;   // L for the back substitution, then the staged statistics
     double* der = M + 2080;
-    double* cj = der + 64;
-    double* yv = cj + 64;
-    double* res = yv + 64;
+    double* res = der + 64;
     double* part = res + 64;
-    const int n = 2 * (int)P;
-    const uint32_t PP = P * P;
+    long long* dgs = (long long*)(part + 64);   // W[r][r] per row, kept for the score
+    constexpr uint32_t PP = P * P;
     const long long* R = st + ((size_t)f * B + s) * PP * 2;
     const long long* T = st + ((size_t)f * B + (B - 1)) * PP * 2;
     const double inv_d = sc->inv[kScoreDer];
@@ -504,65 +521,114 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
         der[2 * yl] = (double)dp * inv_d;
         der[2 * yl + 1] = (double)(dt - dp) * inv_d;
     }
-    __syncthreads();
     const double cell_prior = 1.0 / (double)n;
     const double non_diag = -prior * cell_prior;
     const double diag = prior * (1.0 - cell_prior) + l2;
-    const int m = n - 1;
-    if (n == 2) {   // one leaf pair: a 1 x 1 system
-        if (lane == 0) {
-            const PairRow pr{R, T, P, 0, 0};
-            const double w00 = (double)pr.dg() * pair_inv;
-            const double den = w00 + diag;
-            res[0] = den != 0.0 ? der[0] / den : 0.0;
-            res[1] = 0.0;
-        }
-        __syncthreads();
-        zero_average_wave(res, 2);
-    } else {
-        // M = W + prior terms on the first m rows (lower triangle)
-        for (int r = lane; r < m; r += 64) {
-            const PairRow pr{R, T, P, (uint32_t)r >> 1, (uint32_t)r & 1u};
-            double* mr = M + r * (r + 1) / 2;
-            long long dg = -pr.da();
-            for (uint32_t b = 0; b < P; ++b) {
-                if (b == pr.a) continue;
-                long long e0, e1, dpart;
-                pr.wp(b, e0, e1, dpart);
-                dg -= dpart;
-                if ((int)(2 * b) < r) mr[2 * b] = (double)e0 * pair_inv + non_diag;
-                if ((int)(2 * b + 1) < r) mr[2 * b + 1] = (double)e1 * pair_inv + non_diag;
-            }
-            mr[r] = (double)dg * pair_inv + diag;
-            if (pr.u == 1) mr[r - 1] = (double)pr.da() * pair_inv + non_diag;
-            yv[r] = der[r];
-        }
-        __syncthreads();
-        pairwise_factor_solve_wave(M, m, cj, yv, res);
-        zero_average_wave(res, n);
+    // row r of M = W + prior terms (lanes past the system repeat row 0 and write nothing)
+    const int r = lane < n ? lane : 0;
+    const PairRow pr{R, T, P, (uint32_t)r >> 1, (uint32_t)r & 1u};
+    const long long da = pr.da();
+    long long dg = -da;
+    double row[m];
+#pragma unroll
+    for (uint32_t b = 0; b < P; ++b) {
+        long long e0, e1, dpart;
+        pr.wp(b, e0, e1, dpart);   // b == a reads in-bounds cells; its values are replaced below
+        if (b != pr.a) dg -= dpart;
+        if ((int)(2 * b) < m) row[2 * b] = (double)e0 * pair_inv + non_diag;
+        if ((int)(2 * b + 1) < m) row[2 * b + 1] = (double)e1 * pair_inv + non_diag;
     }
-    // score (calculate_score, pairwise_scoring.rs:352-375): inner and outer sums sequential
-    for (int x = lane; x < n; x += 64) {
-        const PairRow pr{R, T, P, (uint32_t)x >> 1, (uint32_t)x & 1u};
-        const long long dg = pr.dg(), da = pr.da();
-        double inner = 0.0;
-        for (uint32_t b = 0; b < P; ++b) {
-            long long e0, e1, dpart;
-            if (b == pr.a) {
-                e0 = pr.u == 0 ? dg : da;
-                e1 = pr.u == 0 ? da : dg;
-            } else {
-                pr.wp(b, e0, e1, dpart);
-            }
-            inner += res[2 * b] * ((double)e0 * pair_inv);
-            inner += res[2 * b + 1] * ((double)e1 * pair_inv);
+    {
+        const double diag_v = (double)dg * pair_inv + diag;
+        const double da_v = (double)da * pair_inv + non_diag;
+#pragma unroll
+        for (int c = 0; c < m; ++c) {
+            if (c == r) row[c] = diag_v;
+            else if (c == r - 1 && (r & 1)) row[c] = da_v;
         }
-        part[x] = res[x] * (der[x] - 0.5 * inner);
+    }
+    if (lane < n) dgs[lane] = dg;
+    __syncthreads();
+    double x;   // this lane's component of the solution
+    if constexpr (m == 1) {   // one leaf pair: a 1 x 1 system
+        const double den = readlane_f64(row[0], 0);
+        x = lane == 0 && den != 0.0 ? der[0] / den : 0.0;
+    } else {
+        bool good = true;
+#pragma unroll
+        for (int j = 0; j < m; ++j) {
+            const double d = readlane_f64(row[j], j);
+            if (d <= 0.0) {
+                good = false;
+                break;
+            }
+            const double ljj = sqrt(d);
+            row[j] = lane == j ? ljj : row[j] / ljj;
+#pragma unroll
+            for (int k = j + 1; k < m; ++k) row[k] = row[k] - row[j] * readlane_f64(row[j], k);
+        }
+        double y = lane < m ? der[lane] : 0.0;
+        if (good) {
+#pragma unroll
+            for (int p = 0; p < m; ++p) {   // forward: y[i] -= L[i][p] y[p], p ascending
+                const double yp = readlane_f64(y, p) / readlane_f64(row[p], p);
+                y = lane == p ? yp : (lane > p ? y - row[p] * yp : y);
+            }
+            if (lane < m) {
+#pragma unroll
+                for (int c = 0; c < m; ++c)
+                    if (c <= lane) M[tri(lane, c)] = row[c];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int p = m - 1; p >= 0; --p) {   // back: L^T x = y
+                const double xp = readlane_f64(y, p) / readlane_f64(row[p], p);
+                const double lpi = lane < p ? M[tri(p, lane)] : 0.0;
+                y = lane == p ? xp : (lane < p ? y - lpi * xp : y);
+            }
+        }
+        x = good && lane < m ? y : 0.0;
+    }
+    if (lane < n) res[lane] = x;
+    __syncthreads();
+    zero_average_wave(res, n);
+    // the staged statistics replace L for the score's pass over the rows of W
+    long long* Rs = (long long*)M;
+    for (uint32_t i = lane; i < 2 * PP; i += 64) Rs[i] = R[i];
+    __syncthreads();
+    // score (calculate_score, pairwise_scoring.rs:352-375): inner and outer sums sequential
+    if (lane < n) {
+        const PairRow ps{Rs, T, P, (uint32_t)lane >> 1, (uint32_t)lane & 1u};
+        const long long dgx = dgs[lane], dax = ps.da();
+        double inner = 0.0;
+        for (uint32_t b0 = 0; b0 < P; b0 += kPairBatch) {
+            long long e0[kPairBatch], e1[kPairBatch];
+#pragma unroll
+            for (uint32_t q = 0; q < kPairBatch; ++q) {
+                const uint32_t b = b0 + q;
+                if (b >= P) continue;
+                if (b == ps.a) {
+                    e0[q] = ps.u == 0 ? dgx : dax;
+                    e1[q] = ps.u == 0 ? dax : dgx;
+                } else {
+                    long long dpart;
+                    ps.wp(b, e0[q], e1[q], dpart);
+                }
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < kPairBatch; ++q) {
+                const uint32_t b = b0 + q;
+                if (b >= P) continue;
+                inner += res[2 * b] * ((double)e0[q] * pair_inv);
+                inner += res[2 * b + 1] * ((double)e1[q] * pair_inv);
+            }
+        }
+        part[lane] = res[lane] * (der[lane] - 0.5 * inner);
     }
     __syncthreads();
     if (lane == 0) {
         double outer = 0.0;
-        for (int x = 0; x < n; ++x) outer += part[x];
+        for (int i = 0; i < n; ++i) outer += part[i];
         scores[(size_t)f * B + s] = outer;
     }
 }

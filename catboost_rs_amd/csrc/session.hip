@@ -782,9 +782,23 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     }
     der_scan_kernel<<<grid_for((uint64_t)F * P, 256), 256, 0, st>>>(cur, P, s->C, F, B, s->dcum);
     HIP_TRY(hipGetLastError());
-    pairwise_candidate_kernel<<<dim3(B - 1, F), 64, kPairCandLds, st>>>(
-        s->pair_st, s->dcum, s->n_cand, P, B, s->scales, s->pair_inv, s->l2, s->prior, s->cand_scores);
-    HIP_TRY(hipGetLastError());
+    {
+        const dim3 grid(B - 1, F);
+#define CBH_PAIR_CAND(PV)                                                                                \
+    pairwise_candidate_kernel<PV><<<grid, 64, kPairCandLds, st>>>(s->pair_st, s->dcum, s->n_cand, B, s->scales, \
+                                                                  s->pair_inv, s->l2, s->prior, s->cand_scores)
+        switch (P) {
+            case 1: CBH_PAIR_CAND(1); break;
+            case 2: CBH_PAIR_CAND(2); break;
+            case 4: CBH_PAIR_CAND(4); break;
+            case 8: CBH_PAIR_CAND(8); break;
+            case 16: CBH_PAIR_CAND(16); break;
+            case 32: CBH_PAIR_CAND(32); break;
+            default: return fail(CBH_ERR_UNSUPPORTED, "pairwise scoring: level of " + std::to_string(P) + " leaves");
+        }
+#undef CBH_PAIR_CAND
+        HIP_TRY(hipGetLastError());
+    }
     pairwise_best_kernel<<<F, 256, 0, st>>>(s->cand_scores, s->n_cand, B, s->best_score, s->best_bin);
     HIP_TRY(hipGetLastError());
     argmax_kernel<<<1, 1024, 0, st>>>(s->best_score, s->best_bin, nullptr, F, s->splits + level);
