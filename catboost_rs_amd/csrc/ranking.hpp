@@ -11,9 +11,10 @@
 //
 // Pairwise statistics of a level (compute_pair_weight_statistics,
 // crates/cb-compute/src/pairwise_scoring.rs:163-196) are int64 fixed point, laid out
-//   st  i64 [F][B][P][P][2]   (bucket, first leaf, second leaf, {smaller, greater_right})
+//   st  i64 [F][P][P][B][2]   (first leaf, second leaf, bucket, {smaller, greater_right})
 // and turned into inclusive prefix sums over the bucket axis, so the running per-border
-// state of calculate_pairwise_score (:450-560) is read directly at border s.
+// state of calculate_pairwise_score (:450-560) is read directly at border s.  The bucket runs
+// of one (feature, leaf pair) are contiguous: the producers write whole runs.
 #pragma once
 #include "kernels.hpp"
 
@@ -21,6 +22,9 @@ namespace cbh {
 
 constexpr uint32_t kPairMaxParents = 32;   // pairwise scoring: 2P <= 64 unknowns (depth <= 6)
 constexpr uint32_t kPairChunk = 65536;     // pairs per workgroup of the LDS statistics kernel
+constexpr uint32_t kPairLoadAhead = 8;      // pairs whose gathers one thread issues together
+constexpr uint32_t kKeyLoadAhead = 8;       // the same for the keyed statistics
+constexpr uint32_t kKeyWords = 4;           // row words of one pair loaded together
 
 __device__ __forceinline__ uint32_t tri(uint32_t r, uint32_t c) {   // packed lower triangle
     return r >= c ? r * (r + 1) / 2 + c : c * (c + 1) / 2 + r;
@@ -71,50 +75,78 @@ static __global__ __launch_bounds__(256) void pairlogit_ders_kernel(
     }
 }
 
-// Pair-weight statistics of one level for every feature.  Grid (pair chunks, F).  For a
+// Leaves of both rows of every pair for one level: pair_lv[k] = winner leaf | loser leaf << 16.
+static __global__ __launch_bounds__(256) void pair_leaves_kernel(const uint32_t* __restrict__ comp_win,
+                                                                 const uint32_t* __restrict__ comp_los, uint64_t m,
+                                                                 const uint16_t* __restrict__ leaf,
+                                                                 uint32_t* __restrict__ pair_lv) {
+    for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < m; k += (uint64_t)gridDim.x * blockDim.x)
+        pair_lv[k] = (leaf[comp_win[k]] & 0x7FFFu) | ((uint32_t)(leaf[comp_los[k]] & 0x7FFFu) << 16);
+}
+
+// Pair-weight statistics of one level for every feature.  For a
 // pair with winner bucket > loser bucket the cells [loserLeaf][winnerLeaf] are decremented at
 // (loser bucket, smaller) and (winner bucket, greater); otherwise [winnerLeaf][loserLeaf] at
-// (winner bucket, smaller) and (loser bucket, greater).  kLds: the P*P*B*2 cells of the
-// feature fit in LDS (P <= 4) and a workgroup accumulates its chunk there first.
-template <bool kLds>
+// (winner bucket, smaller) and (loser bucket, greater).  The P*P*B*2 cells of the feature fit
+// in LDS (P <= 4): a workgroup accumulates its chunk there, then adds it to st.  In LDS the
+// two channels of a leaf pair are separate runs of B ([P][P][2][B]), so a wave's atomics on
+// random buckets spread over every bank.
 static __global__ __launch_bounds__(256) void pair_stats_kernel(
-    const uint8_t* __restrict__ cols, uint64_t n, const uint16_t* __restrict__ leaf,
+    const uint8_t* __restrict__ cols, uint64_t n, const uint32_t* __restrict__ pair_lv,
     const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los,
-    const long long* __restrict__ comp_wq, uint64_t m, uint32_t P, uint32_t B,
+    const long long* __restrict__ comp_wq, uint64_t m, uint32_t n_chunks, uint32_t F, uint32_t P, uint32_t B,
     long long* __restrict__ st) {
     extern __shared__ long long sh_st[];
-    const uint32_t f = blockIdx.y;
+    // 1-D grid of 8 * n_chunks * ceil(F / 8) blocks, round-robin over the 8 XCDs: all chunks of
+    // a feature run on one XCD, which keeps its bucket column in that XCD's L2
+    const uint32_t xcd = blockIdx.x & 7u, q = blockIdx.x >> 3;
+    const uint32_t f = xcd + 8u * (q / n_chunks), chunk = q % n_chunks;
+    if (f >= F) return;
     const size_t cells = (size_t)B * P * P * 2;
     unsigned long long* out = (unsigned long long*)(st + (size_t)f * cells);
-    unsigned long long* acc = kLds ? (unsigned long long*)sh_st : out;
-    if (kLds) {
-        for (size_t i = threadIdx.x; i < cells; i += blockDim.x) sh_st[i] = 0;
-        __syncthreads();
-    }
+    unsigned long long* acc = (unsigned long long*)sh_st;
+    for (size_t i = threadIdx.x; i < cells; i += blockDim.x) sh_st[i] = 0;
+    __syncthreads();
     const uint8_t* col = cols + (size_t)f * n;
-    const uint64_t k0 = (uint64_t)blockIdx.x * kPairChunk;
+    const uint64_t k0 = (uint64_t)chunk * kPairChunk;
     const uint64_t k1 = min(k0 + kPairChunk, m);
-    for (uint64_t k = k0 + threadIdx.x; k < k1; k += blockDim.x) {
-        const uint32_t wi = comp_win[k], lo = comp_los[k];
-        if (wi == lo) continue;
-        const unsigned long long neg = (unsigned long long)(-comp_wq[k]);
-        const uint32_t wb = col[wi], lb = col[lo];
-        const uint32_t wl = leaf[wi] & 0x7FFFu, ll = leaf[lo] & 0x7FFFu;
-        size_t c_small, c_great;
-        if (wb > lb) {
-            c_small = ((size_t)lb * P + ll) * P + wl;
-            c_great = ((size_t)wb * P + ll) * P + wl;
-        } else {
-            c_small = ((size_t)wb * P + wl) * P + ll;
-            c_great = ((size_t)lb * P + wl) * P + ll;
+    // kPairLoadAhead pairs per thread at a time: their indices, then all their bucket and leaf
+    // gathers, are in flight together (the loop is latency-bound otherwise)
+    for (uint64_t kb = k0 + threadIdx.x; kb < k1; kb += (uint64_t)blockDim.x * kPairLoadAhead) {
+        uint32_t wi[kPairLoadAhead], lo[kPairLoadAhead], lv[kPairLoadAhead];
+        long long wq[kPairLoadAhead];
+#pragma unroll
+        for (uint32_t u = 0; u < kPairLoadAhead; ++u) {
+            const uint64_t k = kb + (uint64_t)u * blockDim.x;
+            const bool ok = k < k1;
+            wi[u] = ok ? comp_win[k] : 0u;
+            lo[u] = ok ? comp_los[k] : 0u;
+            lv[u] = ok ? pair_lv[k] : 0u;
+            wq[u] = ok ? comp_wq[k] : 0;
         }
-        atomicAdd(acc + 2 * c_small, neg);
-        atomicAdd(acc + 2 * c_great + 1, neg);
+        uint32_t wb[kPairLoadAhead], lb[kPairLoadAhead], wl[kPairLoadAhead], ll[kPairLoadAhead];
+#pragma unroll
+        for (uint32_t u = 0; u < kPairLoadAhead; ++u) {
+            wb[u] = col[wi[u]];
+            lb[u] = col[lo[u]];
+            wl[u] = lv[u] & 0x7FFFu;
+            ll[u] = (lv[u] >> 16) & 0x7FFFu;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kPairLoadAhead; ++u) {
+            if (kb + (uint64_t)u * blockDim.x >= k1 || wi[u] == lo[u]) continue;
+            const unsigned long long neg = (unsigned long long)(-wq[u]);
+            const bool wg = wb[u] > lb[u];
+            const size_t run = ((size_t)(wg ? ll[u] : wl[u]) * P + (wg ? wl[u] : ll[u])) * 2 * B;
+            atomicAdd(acc + run + (wg ? lb[u] : wb[u]), neg);
+            atomicAdd(acc + run + B + (wg ? wb[u] : lb[u]), neg);
+        }
     }
-    if (kLds) {
-        __syncthreads();
-        for (size_t i = threadIdx.x; i < cells; i += blockDim.x)
-            if (sh_st[i] != 0) atomicAdd(out + i, (unsigned long long)sh_st[i]);
+    __syncthreads();
+    for (size_t i = threadIdx.x; i < cells; i += blockDim.x) {   // st index i = (pair, bucket, c)
+        const size_t pr = i / (2 * B), rem = i % (2 * B);
+        const long long v = sh_st[(pr * 2 + (rem & 1)) * B + (rem >> 1)];
+        if (v != 0) atomicAdd(out + i, (unsigned long long)v);
     }
 }
 
@@ -218,95 +250,147 @@ inline uint32_t pair_tile_features(uint32_t F, uint32_t B, size_t budget) {
     return std::min<uint32_t>(tf, (F + 3) / 4 * 4);
 }
 
-// One workgroup per (leaf pair {a <= b}, feature tile); linear block ids are mapped so that
-// the workgroups of one tile run on one XCD.  Each pair reads the row words of its winner and
-// loser once for the whole tile.  Writes the cumulative statistics st [F][B][P][P][2] of the
-// cells [a][b] and [b][a] of the tile's features (every cell of st is written once per level:
-// no zeroing, no global atomics, no separate scan).
+// Inclusive prefix, in place, of nseq contiguous runs of B values in LDS (run q starts at
+// base + q B): a workgroup-wide two-level scan, tps threads per run.
+__device__ inline void lds_runs_prefix(unsigned long long* base, uint32_t nseq, uint32_t B,
+                                       unsigned long long* part /* [blockDim.x] */) {
+    uint32_t tps = 1;
+    while (tps * 2 * nseq <= blockDim.x && tps * 2 <= 64) tps *= 2;
+    const uint32_t t = threadIdx.x, q = t / tps, j = t % tps;
+    const uint32_t chunk = (B + tps - 1) / tps;
+    const uint32_t b0 = min(j * chunk, B), b1 = min(b0 + chunk, B);
+    unsigned long long* p = q < nseq ? base + (size_t)q * B : nullptr;
+    unsigned long long run = 0;
+    if (p)
+        for (uint32_t bb = b0; bb < b1; ++bb) {
+            run += p[bb];
+            p[bb] = run;
+        }
+    part[t] = run;
+    __syncthreads();
+    if (p && j > 0) {
+        unsigned long long off = 0;
+        for (uint32_t i = 0; i < j; ++i) off += part[q * tps + i];
+        for (uint32_t bb = b0; bb < b1; ++bb) p[bb] += off;
+    }
+    __syncthreads();
+}
+
+// One workgroup per (leaf pair {a <= b}, feature tile).  Each pair reads the row words of its
+// winner and loser once for the whole tile.  Writes the cumulative statistics of the cells [a][b] and
+// [b][a] of the tile's features, whole bucket runs (every cell of st is written once per
+// level: no zeroing, no global atomics, no separate scan).
 static __global__ __launch_bounds__(256) void pair_stats_key_kernel(
     const uint32_t* __restrict__ rows, uint32_t W, const uint2* __restrict__ rec,
     const long long* __restrict__ rec_wq, const uint32_t* __restrict__ key_off, uint32_t F,
     uint32_t P, uint32_t B, uint32_t tf, uint32_t n_tiles, long long* __restrict__ st) {
-    extern __shared__ unsigned long long cell_k[];   // [tf][blk][bucket][c]
+    extern __shared__ unsigned long long cell_k[];   // [tf][blk][c][bucket]
+    // block ids go round-robin over the 8 XCDs: the tiles of one leaf pair run on one XCD,
+    // consecutively, so the rows its pairs gather come from that XCD's L2 after the first tile
     const uint32_t bid = blockIdx.x;
     const uint32_t xcd = bid & 7u, q = bid >> 3;
-    const uint32_t key = q % (P * P);
-    const uint32_t tile = (q / (P * P)) * 8u + xcd;
-    const uint32_t a = key / P, b = key % P;
-    if (tile >= n_tiles || a > b) return;
+    const uint32_t tile = q % n_tiles;
+    const uint32_t idx = (q / n_tiles) * 8u + xcd;   // leaf pair {a <= b}: idx = b (b + 1) / 2 + a
+    if (idx >= P * (P + 1) / 2) return;
+    uint32_t b = (uint32_t)((sqrtf(8.0f * (float)idx + 1.0f) - 1.0f) * 0.5f);
+    while (b * (b + 1) / 2 > idx) --b;
+    while ((b + 1) * (b + 2) / 2 <= idx) ++b;
+    const uint32_t a = idx - b * (b + 1) / 2;
+    const uint32_t key = a * P + b;
     const uint32_t f0 = tile * tf;
     const uint32_t nf = min(tf, F - f0);
     const uint32_t w0 = f0 / 4, nw = (nf + 3) / 4;
     const size_t per_f = (size_t)2 * B * 2;
     for (size_t i = threadIdx.x; i < (size_t)nf * per_f; i += blockDim.x) cell_k[i] = 0;
     __syncthreads();
-    for (uint32_t j = key_off[key] + threadIdx.x; j < key_off[key + 1]; j += blockDim.x) {
-        const uint2 r = rec[j];
-        const uint32_t wi = r.x, lo = r.y & 0x7FFFFFFFu;
-        const bool win_in_a = (r.y >> 31) != 0;
-        const unsigned long long neg = (unsigned long long)(-rec_wq[j]);
-        const uint32_t* rw = rows + (size_t)wi * W + w0;
-        const uint32_t* rl = rows + (size_t)lo * W + w0;
-        for (uint32_t w = 0; w < nw; ++w) {
-            const uint32_t ww = rw[w], wlw = rl[w];
-            for (uint32_t k = 0; k < 4; ++k) {
-                const uint32_t f = 4 * w + k;
-                if (f >= nf) break;
-                const uint32_t wb = (ww >> (8 * k)) & 0xFFu, lb = (wlw >> (8 * k)) & 0xFFu;
-                // first index x = loser leaf when wb > lb, else winner leaf; block 0 = [a][b]
-                const uint32_t blk = a == b ? 0u : ((wb > lb) == win_in_a ? 1u : 0u);
-                const uint32_t bs = wb > lb ? lb : wb, bg = wb > lb ? wb : lb;
-                unsigned long long* c = cell_k + (size_t)f * per_f + (size_t)blk * B * 2;
-                atomicAdd(c + bs * 2, neg);
-                atomicAdd(c + bg * 2 + 1, neg);
+    const uint32_t j0 = key_off[key], j1 = key_off[key + 1];
+    for (uint32_t jb = j0 + threadIdx.x; jb < j1; jb += blockDim.x * kKeyLoadAhead) {
+        // kKeyLoadAhead pairs per thread at a time: records first, then kKeyWords row words
+        // of each winner and loser, all in flight together
+        uint2 r[kKeyLoadAhead];
+        long long wq[kKeyLoadAhead];
+#pragma unroll
+        for (uint32_t u = 0; u < kKeyLoadAhead; ++u) {
+            const uint32_t j = jb + u * blockDim.x;
+            const bool ok = j < j1;
+            r[u] = ok ? rec[j] : make_uint2(0u, 0u);
+            wq[u] = ok ? rec_wq[j] : 0;
+        }
+        for (uint32_t wc = 0; wc < nw; wc += kKeyWords) {
+            uint32_t ww[kKeyLoadAhead][kKeyWords], wlw[kKeyLoadAhead][kKeyWords];
+#pragma unroll
+            for (uint32_t u = 0; u < kKeyLoadAhead; ++u)
+#pragma unroll
+                for (uint32_t w = 0; w < kKeyWords; ++w) {
+                    const uint32_t wa = wc + w < nw ? w0 + wc + w : w0;   // in-row, in-bounds
+                    ww[u][w] = rows[(size_t)r[u].x * W + wa];
+                    wlw[u][w] = rows[(size_t)(r[u].y & 0x7FFFFFFFu) * W + wa];
+                }
+#pragma unroll
+            for (uint32_t u = 0; u < kKeyLoadAhead; ++u) {
+                if (jb + u * blockDim.x >= j1) continue;
+                const bool win_in_a = (r[u].y >> 31) != 0;
+                const unsigned long long neg = (unsigned long long)(-wq[u]);
+#pragma unroll
+                for (uint32_t w = 0; w < kKeyWords; ++w) {
+                    if (wc + w >= nw) break;
+                    for (uint32_t k = 0; k < 4; ++k) {
+                        const uint32_t f = 4 * (wc + w) + k;
+                        if (f >= nf) break;
+                        const uint32_t wb = (ww[u][w] >> (8 * k)) & 0xFFu, lb = (wlw[u][w] >> (8 * k)) & 0xFFu;
+                        // first index x = loser leaf when wb > lb, else winner leaf; block 0 = [a][b]
+                        const uint32_t blk = a == b ? 0u : ((wb > lb) == win_in_a ? 1u : 0u);
+                        const uint32_t bs = wb > lb ? lb : wb, bg = wb > lb ? wb : lb;
+                        unsigned long long* c = cell_k + (size_t)f * per_f + (size_t)blk * B * 2;
+                        atomicAdd(c + bs, neg);
+                        atomicAdd(c + B + bg, neg);
+                    }
+                }
             }
         }
     }
     __syncthreads();
-    for (uint32_t sq = threadIdx.x; sq < nf * 4; sq += blockDim.x) {   // prefix of (f, blk, c)
-        const uint32_t f = sq >> 2, blk = (sq >> 1) & 1u, c = sq & 1u;
-        unsigned long long* p = cell_k + (size_t)f * per_f + (size_t)blk * B * 2 + c;
-        unsigned long long run = 0;
-        for (uint32_t bb = 0; bb < B; ++bb) {
-            run += p[bb * 2];
-            p[bb * 2] = run;
-        }
-    }
-    __syncthreads();
+    // prefix over buckets of every (f, blk, c) run
+    __shared__ unsigned long long part[256];
+    lds_runs_prefix(cell_k, nf * 4, B, part);
     const uint32_t nblk = a == b ? 1u : 2u;
-    for (size_t i = threadIdx.x; i < (size_t)nf * per_f; i += blockDim.x) {
-        const uint32_t f = (uint32_t)(i / per_f), r = (uint32_t)(i % per_f);
-        const uint32_t blk = r / (B * 2), bb = (r / 2) % B, c = r & 1u;
-        if (blk >= nblk) continue;
+    for (uint32_t fb = 0; fb < nf * nblk; ++fb) {   // whole contiguous runs of 2B values
+        const uint32_t f = fb / nblk, blk = fb % nblk;
         const uint32_t x = blk == 0 ? a : b, y = blk == 0 ? b : a;
-        st[((((size_t)(f0 + f) * B + bb) * P + x) * P + y) * 2 + c] = (long long)cell_k[i];
+        const unsigned long long* src = cell_k + (size_t)f * per_f + (size_t)blk * B * 2;
+        long long* dst = st + (((size_t)(f0 + f) * P + x) * P + y) * B * 2;
+        for (uint32_t i = threadIdx.x; i < 2 * B; i += blockDim.x) dst[i] = (long long)src[(i & 1u) * B + (i >> 1)];
     }
 }
 
-// Inclusive prefix over the bucket axis, in place; one thread per (f, x, y, c).
-static __global__ __launch_bounds__(256) void pair_scan_kernel(long long* __restrict__ st, uint32_t F,
-                                                               uint32_t P, uint32_t B) {
-    const size_t row = (size_t)P * P * 2;
-    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (size_t)F * row) return;
-    long long* p = st + (t / row) * B * row + (t % row);
-    long long run = 0;
-    for (uint32_t b = 0; b < B; ++b) {
-        run += p[(size_t)b * row];
-        p[(size_t)b * row] = run;
+// Inclusive prefix over the bucket axis, in place: one wavefront per (f, x, y, c) run of B
+// values at stride 2; lane l takes buckets [l k, l k + k), k = ceil(B / 64), and the lane
+// totals are scanned across the wave.
+static __global__ __launch_bounds__(256) void pair_scan_kernel(long long* __restrict__ st, uint32_t n_runs,
+                                                               uint32_t B) {
+    const uint32_t run = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (run >= n_runs) return;
+    long long* p = st + (size_t)(run >> 1) * B * 2 + (run & 1u);
+    const uint32_t k = (B + 63) / 64;
+    const uint32_t b0 = min(lane * k, B), b1 = min(b0 + k, B);
+    long long v[4];   // B <= 256
+    long long tot = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        v[i] = b0 + i < b1 ? p[(size_t)(b0 + i) * 2] : 0;
+        tot += v[i];
+        v[i] = tot;
     }
-}
-
-// Inclusive prefix over buckets of the der channel of the level histogram (hist [P][C][F][B]
-// is kept in prefix form, channel 0) regrouped as dcum [F][B][P].  One thread per (f, leaf).
-static __global__ __launch_bounds__(256) void der_scan_kernel(const long long* __restrict__ hist, uint32_t P,
-                                                              uint32_t C, uint32_t F, uint32_t B,
-                                                              long long* __restrict__ dcum) {
-    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= F * P) return;
-    const uint32_t f = t / P, y = t % P;
-    const long long* h = hist + ((size_t)y * C * F + f) * B;   // already a prefix over bins
-    for (uint32_t b = 0; b < B; ++b) dcum[((size_t)f * B + b) * P + y] = h[b];
+    long long incl = tot;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const long long t = __shfl_up(incl, o, 64);
+        if ((int)lane >= o) incl += t;
+    }
+    const long long off = incl - tot;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i)
+        if (b0 + i < b1) p[(size_t)(b0 + i) * 2] = v[i] + off;
 }
 
 // MakeZeroAverage (pairwise_scoring.rs:255-265), sequential sum as the reference.
@@ -442,15 +526,15 @@ constexpr uint32_t kPairBatch = 8;
 // (dg, da) (u == 0) or (da, dg) (u == 1).  Integer sums are exact, so every entry equals the
 // staged assembly's bit for bit whatever the order.
 struct PairRow {
-    const long long* R;
-    const long long* T;
-    uint32_t P, a, u;
-    __device__ inline long long da() const { return R[(a * P + a) * 2] - R[(a * P + a) * 2 + 1]; }
+    const long long* R;   // cell (x, y) at R + (x P + y) rs: {smaller, greater}
+    const long long* T;   // cell (x, y) at T + (x P + y) ts: smaller at the last border
+    uint32_t rs, ts, P, a, u;
+    __device__ inline long long da() const { return R[(a * P + a) * rs] - R[(a * P + a) * rs + 1]; }
     __device__ inline void wp(uint32_t b, long long& e0, long long& e1, long long& dg_part) const {
         const uint32_t yv_ = a < b ? a : b, xv = a < b ? b : a;
-        const long long xs = R[(xv * P + yv_) * 2], xg = R[(xv * P + yv_) * 2 + 1];
-        const long long ys = R[(yv_ * P + xv) * 2], yg = R[(yv_ * P + xv) * 2 + 1];
-        const long long total = T[2 * (xv * P + yv_)] + T[2 * (yv_ * P + xv)];
+        const long long xs = R[(xv * P + yv_) * rs], xg = R[(xv * P + yv_) * rs + 1];
+        const long long ys = R[(yv_ * P + xv) * rs], yg = R[(yv_ * P + xv) * rs + 1];
+        const long long total = T[(xv * P + yv_) * ts] + T[(yv_ * P + xv) * ts];
         const long long w00 = xg + yg, w01 = xs - xg, w10 = ys - yg, w11 = -(xs + ys);
         if (u == 0) {
             e0 = w00;
@@ -474,6 +558,15 @@ struct PairRow {
     }
 };
 
+// Cells (x, y) of one border, {smaller, greater} 16 bytes at stride 2B in st, into Rs[2 PP].
+__device__ inline void stage_pair_cells(long long* Rs, const long long* R, uint32_t PP, uint32_t B) {
+    for (uint32_t i = threadIdx.x; i < PP; i += blockDim.x) {
+        const longlong2 v = *reinterpret_cast<const longlong2*>(R + (size_t)i * 2 * B);
+        Rs[2 * i] = v.x;
+        Rs[2 * i + 1] = v.y;
+    }
+}
+
 // The double of lane l (uniform l) on every lane.
 __device__ inline double readlane_f64(double v, int l) {
     const long long bits = __double_as_longlong(v);
@@ -493,15 +586,18 @@ __device__ inline double readlane_f64(double v, int l) {
 // rebuilds each row of W from the statistics staged over that buffer afterwards.
 template <uint32_t P_>
 static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
-    const long long* __restrict__ st, const long long* __restrict__ dcum,
+    const long long* __restrict__ st, const long long* __restrict__ hist, uint32_t C, uint32_t F,
     const uint32_t* __restrict__ n_cand, uint32_t B, const Scales* __restrict__ sc, double pair_inv,
     double l2, double prior, double* __restrict__ scores /* [F][B] */) {
     constexpr uint32_t P = P_;
     constexpr int n = 2 * (int)P_, m = n - 1;
     static_assert(n <= 64, "one row per lane");
     extern __shared__ double sh_pw[];
-    const uint32_t s = blockIdx.x, f = blockIdx.y;
+    // gridDim.x = 8 * ceil((B - 1) / 8): consecutive borders of a feature run on one XCD (block
+    // ids go round-robin over the 8 XCDs), where their statistics share L2 lines
+    const uint32_t s = (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3), f = blockIdx.y;
     const int lane = threadIdx.x;
+    if (s >= B - 1) return;
     if (s >= n_cand[f]) {
         if (lane == 0) scores[(size_t)f * B + s] = -INFINITY;
         return;
@@ -512,21 +608,27 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
     double* part = res + 64;
     long long* dgs = (long long*)(part + 64);   // W[r][r] per row, kept for the score
     constexpr uint32_t PP = P * P;
-    const long long* R = st + ((size_t)f * B + s) * PP * 2;
-    const long long* T = st + ((size_t)f * B + (B - 1)) * PP * 2;
+    const long long* R = st + (size_t)f * PP * B * 2 + (size_t)s * 2;          // cell stride 2B
+    const long long* T = st + (size_t)f * PP * B * 2 + (size_t)(B - 1) * 2;
     const double inv_d = sc->inv[kScoreDer];
     for (uint32_t yl = lane; yl < P; yl += 64) {
-        const long long dp = dcum[((size_t)f * B + s) * P + yl];
-        const long long dt = dcum[((size_t)f * B + (B - 1)) * P + yl];
+        // der channel of the level histogram hist [P][C][F][B], kept as a prefix over bins
+        const long long* h = hist + ((size_t)yl * C * F + f) * B;
+        const long long dp = h[s], dt = h[B - 1];
         der[2 * yl] = (double)dp * inv_d;
         der[2 * yl + 1] = (double)(dt - dp) * inv_d;
     }
     const double cell_prior = 1.0 / (double)n;
     const double non_diag = -prior * cell_prior;
     const double diag = prior * (1.0 - cell_prior) + l2;
+    // this border's cells, one 16-byte load each, staged in LDS (the L buffer is free until
+    // the back substitution)
+    long long* Rs = (long long*)M;
+    stage_pair_cells(Rs, R, PP, B);
+    __syncthreads();
     // row r of M = W + prior terms (lanes past the system repeat row 0 and write nothing)
     const int r = lane < n ? lane : 0;
-    const PairRow pr{R, T, P, (uint32_t)r >> 1, (uint32_t)r & 1u};
+    const PairRow pr{Rs, T, 2, 2 * B, P, (uint32_t)r >> 1, (uint32_t)r & 1u};
     const long long da = pr.da();
     long long dg = -da;
     double row[m];
@@ -592,13 +694,12 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
     if (lane < n) res[lane] = x;
     __syncthreads();
     zero_average_wave(res, n);
-    // the staged statistics replace L for the score's pass over the rows of W
-    long long* Rs = (long long*)M;
-    for (uint32_t i = lane; i < 2 * PP; i += 64) Rs[i] = R[i];
+    // the statistics replace L again for the score's pass over the rows of W
+    stage_pair_cells(Rs, R, PP, B);
     __syncthreads();
     // score (calculate_score, pairwise_scoring.rs:352-375): inner and outer sums sequential
     if (lane < n) {
-        const PairRow ps{Rs, T, P, (uint32_t)lane >> 1, (uint32_t)lane & 1u};
+        const PairRow ps{Rs, T, 2, 2 * B, P, (uint32_t)lane >> 1, (uint32_t)lane & 1u};
         const long long dgx = dgs[lane], dax = ps.da();
         double inner = 0.0;
         for (uint32_t b0 = 0; b0 < P; b0 += kPairBatch) {

@@ -158,14 +158,14 @@ struct cbh_session {
     long long* comp_wq = nullptr;    // [m]
     double* ext_der = nullptr;       // [2][n] der1, der2
     double* score_w = nullptr;       // [n] pairwise weights
-    long long* pair_st = nullptr;    // [F][B][Pmax][Pmax][2]
-    long long* dcum = nullptr;       // [F][B][Pmax]
+    long long* pair_st = nullptr;    // [F][Pmax][Pmax][B][2]
     double* cand_scores = nullptr;   // [F][B]
     long long* leaf_w = nullptr;     // [L][L]
     uint32_t* key_cnt = nullptr;     // [Pmax^2] pairs per unordered leaf pair
     uint32_t* key_off = nullptr;     // [Pmax^2 + 1]
     uint32_t* key_cur = nullptr;     // [Pmax^2]
     uint2* key_rec = nullptr;        // [m] pair records grouped by leaf pair
+    uint32_t* pair_lv = nullptr;     // [m] leaves of winner and loser of every pair, this level
     long long* key_wq = nullptr;     // [m]
     uint32_t pair_tf = 4, pair_tiles = 1;
 
@@ -223,9 +223,9 @@ struct cbh_session {
         dfree(leaf_sums); dfree(leaf_raw); dfree(leaf_scaled); dfree(jump);
         dfree(partials);
         dfree(group_off); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
-        dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st); dfree(dcum);
+        dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st);
         dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot);
-        dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq);
+        dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_lv);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
         dfree(phantom_cnt); dfree(fweight);
         for (auto& g : tree_graph)
@@ -349,13 +349,12 @@ int session_alloc(cbh_session* s) {
     if (s->pairwise) {
         const size_t pmax = (size_t)1 << (s->depth - 1);
         CHECK(dalloc(&s->pair_st, (size_t)s->F * s->B * pmax * pmax * 2));
-        CHECK(dalloc(&s->dcum, (size_t)s->F * s->B * pmax));
         CHECK(dalloc(&s->cand_scores, (size_t)s->F * s->B));
         CHECK(dalloc(&s->leaf_w, ((size_t)1 << s->depth) << s->depth));
         CHECK(dalloc(&s->key_cnt, pmax * pmax));
         CHECK(dalloc(&s->key_off, pmax * pmax + 1));
         CHECK(dalloc(&s->key_cur, pmax * pmax));
-        s->pair_tf = pair_tile_features(s->F, s->B, 128 * 1024);
+        s->pair_tf = pair_tile_features(s->F, s->B, 64 * 1024);
         s->pair_tiles = (s->F + s->pair_tf - 1) / s->pair_tf;
         HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_key_kernel,
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -706,7 +705,7 @@ int upload_pairs(cbh_session* s, const cbh_family* fam) {
     s->pair_inv = std::ldexp(1.0, -shift);
     if (m != s->n_pairs || !s->comp_win) {
         dfree(s->comp_win); dfree(s->comp_los); dfree(s->comp_w); dfree(s->comp_wq);
-        dfree(s->key_rec); dfree(s->key_wq);
+        dfree(s->key_rec); dfree(s->key_wq); dfree(s->pair_lv);
         CHECK(dalloc(&s->comp_win, m));
         CHECK(dalloc(&s->comp_los, m));
         CHECK(dalloc(&s->comp_w, m));
@@ -714,6 +713,7 @@ int upload_pairs(cbh_session* s, const cbh_family* fam) {
         if (s->pairwise) {
             CHECK(dalloc(&s->key_rec, m));
             CHECK(dalloc(&s->key_wq, m));
+            CHECK(dalloc(&s->pair_lv, m));
         }
     }
     if (G != s->n_groups || !s->group_off) {
@@ -746,15 +746,20 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     if (P <= 4) {   // few cells per feature: LDS-privatized chunks, global flush, bucket scan
         CHECK(launch_zero(s->pair_st, cells, st));
         if (s->n_pairs) {
-            const dim3 grid((unsigned)((s->n_pairs + kPairChunk - 1) / kPairChunk), F);
+            pair_leaves_kernel<<<grid_for(s->n_pairs, 256, 2048), 256, 0, st>>>(s->comp_win, s->comp_los,
+                                                                               s->n_pairs, s->leaf, s->pair_lv);
+            HIP_TRY(hipGetLastError());
+            const uint32_t n_chunks = (uint32_t)((s->n_pairs + kPairChunk - 1) / kPairChunk);
+            const uint32_t grid = 8u * n_chunks * ((F + 7) / 8);
             const size_t lds = (size_t)B * P * P * 2 * sizeof(long long);
-            HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_kernel<true>,
+            HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_kernel,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-            pair_stats_kernel<true><<<grid, 256, lds, st>>>(s->cols, s->n, s->leaf, s->comp_win, s->comp_los,
-                                                           s->comp_wq, s->n_pairs, P, B, s->pair_st);
+            pair_stats_kernel<<<grid, 256, lds, st>>>(s->cols, s->n, s->pair_lv, s->comp_win, s->comp_los,
+                                                     s->comp_wq, s->n_pairs, n_chunks, F, P, B, s->pair_st);
             HIP_TRY(hipGetLastError());
         }
-        pair_scan_kernel<<<grid_for((uint64_t)F * P * P * 2, 256), 256, 0, st>>>(s->pair_st, F, P, B);
+        const uint32_t runs = F * P * P * 2;
+        pair_scan_kernel<<<(runs + 3) / 4, 256, 0, st>>>(s->pair_st, runs, B);
         HIP_TRY(hipGetLastError());
     } else {        // pairs grouped by leaf pair; one workgroup per (feature, leaf pair)
         const uint32_t nk = P * P;
@@ -774,18 +779,17 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
                 s->key_wq);
             HIP_TRY(hipGetLastError());
         }
-        const uint32_t tpad = (s->pair_tiles + 7) / 8 * 8;
+        const uint32_t n_tri = P * (P + 1) / 2;   // leaf pairs {a <= b}
+        const uint32_t grid = 8u * s->pair_tiles * ((n_tri + 7) / 8);
         const size_t lds = (size_t)s->pair_tf * 2 * B * 2 * sizeof(long long);
-        pair_stats_key_kernel<<<tpad * nk, 256, lds, st>>>(s->rows, s->W, s->key_rec, s->key_wq, s->key_off, F,
+        pair_stats_key_kernel<<<grid, 256, lds, st>>>(s->rows, s->W, s->key_rec, s->key_wq, s->key_off, F,
                                                           P, B, s->pair_tf, s->pair_tiles, s->pair_st);
         HIP_TRY(hipGetLastError());
     }
-    der_scan_kernel<<<grid_for((uint64_t)F * P, 256), 256, 0, st>>>(cur, P, s->C, F, B, s->dcum);
-    HIP_TRY(hipGetLastError());
     {
-        const dim3 grid(B - 1, F);
+        const dim3 grid((B - 1 + 7) / 8 * 8, F);
 #define CBH_PAIR_CAND(PV)                                                                                \
-    pairwise_candidate_kernel<PV><<<grid, 64, kPairCandLds, st>>>(s->pair_st, s->dcum, s->n_cand, B, s->scales, \
+    pairwise_candidate_kernel<PV><<<grid, 64, kPairCandLds, st>>>(s->pair_st, cur, s->C, F, s->n_cand, B, s->scales, \
                                                                   s->pair_inv, s->l2, s->prior, s->cand_scores)
         switch (P) {
             case 1: CBH_PAIR_CAND(1); break;
