@@ -131,6 +131,7 @@ struct cbh_session {
     double* best_score = nullptr;
     uint32_t* best_bin = nullptr;
     uint32_t* n_cand = nullptr;
+    uint32_t max_cand = 0;           // most candidates of any feature (threads of the scorer)
     uint8_t* one_hot = nullptr;
     Scales* scales = nullptr;
     Bounds* bounds = nullptr;
@@ -620,6 +621,7 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
         if (folds > n_bins) return fail(CBH_ERR_OUT_OF_RANGE, "real_folds[f] > n_bins");
         const bool oh = !s->one_hot_host.empty() && s->one_hot_host[f];
         nc[f] = oh ? folds : (folds > 0 ? folds - 1 : 0);
+        s->max_cand = std::max(s->max_cand, nc[f]);
     }
     HIP_TRY(hipMemcpy(s->n_cand, nc.data(), sizeof(uint32_t) * F, hipMemcpyHostToDevice));
     bool any_oh = false;
@@ -971,11 +973,11 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         CHECK(s->stage_begin(kStScore));
         if (s->pairwise) {
             CHECK(pairwise_level(s, cur, level));
-        } else if (s->B <= 64)
+        } else if (s->max_cand <= 64)
             score_kernel<K, 1><<<s->F, 64, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin,
                                                    s->ctr_n ? s->fweight : nullptr);
-        else if (s->B <= 128)
+        else if (s->max_cand <= 128)
             score_kernel<K, 2><<<s->F, 128, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
                                                     s->scales, s->l2, cosine, s->best_score, s->best_bin,
                                                    s->ctr_n ? s->fweight : nullptr);
