@@ -364,7 +364,7 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
                                            uint32_t B, uint32_t plane,
                                            unsigned long long* __restrict__ lbase,
                                            const uint32_t (&skip)[4]) {
-    constexpr int U = kFillRows;
+    constexpr int U = C > 12 ? 2 : kFillRows;   // rows in flight per lane (registers bound it)
     const uint32_t rows_per_pass = blockDim.x / TW;
     const uint32_t r0 = threadIdx.x / TW;
     const uint32_t wl = threadIdx.x - r0 * TW;
@@ -438,7 +438,9 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t nf = min(4u, TF - min(TF, 4u * wl));   // valid features of this lane's word
     uint32_t skip[4] = {256u, 256u, 256u, 256u};
     if (kSkip)
-        for (uint32_t k = 0; k < nf; ++k) skip[k] = skip_bin[f0 + 4u * wl + k];
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k)   // constant indices: the array stays in registers
+            if (k < nf) skip[k] = skip_bin[f0 + 4u * wl + k];
     const uint32_t V = idx ? plan->rows : (uint32_t)n;
     const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
     const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
