@@ -109,7 +109,7 @@ int run_fill(const uint32_t* rows, uint32_t W, uint64_t n, const uint32_t* idx,
     const uint32_t G = 64;
     fill_kernel<C, false><<<G * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, n, idx, plan,
                                                              (const long long*)sstat, ft.n_tiles, ft.tw,
-                                                             F, B, G, hist, nullptr);
+                                                             F, B, G, hist, nullptr, (int)ft.bin_major);
     HIP_OK(hipGetLastError());
     return CBH_OK;
 }
@@ -224,7 +224,7 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t B, c
     int lds_max = 0, dev = 0;
     HIP_OK(hipGetDevice(&dev));
     HIP_OK(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
-    const FillTiles ft = plan_fill_tiles(F, B, C, std::min<size_t>((size_t)lds_max, 160 * 1024));
+    const FillTiles ft = plan_fill_tiles(F, B, C, std::min<size_t>((size_t)lds_max, 160 * 1024), 1, n);
     if (ft.n_tiles == 0) return fail2(CBH_ERR_UNSUPPORTED, "histogram line too wide for LDS");
 
     DBuf<uint8_t> cols;

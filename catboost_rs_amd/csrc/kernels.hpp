@@ -332,17 +332,28 @@ constexpr int kFillRows = 4;
 struct FillTiles {       // host-side plan of the feature tiles
     uint32_t n_tiles;
     uint32_t tw;         // words (4 features) per tile
-    uint32_t pad;
+    uint32_t bin_major;  // LDS [ch][bin][f] with rotated visits (tw == 8)
     uint32_t pad2;
     size_t lds_bytes;
 };
 
-inline FillTiles plan_fill_tiles(uint32_t F, uint32_t B, uint32_t C, size_t budget) {
+// layout: 0 feature-major, 1 bin-major where it pays (>= 4 channels, or many rows), 2 bin-major
+// whenever it fits
+inline FillTiles plan_fill_tiles(uint32_t F, uint32_t B, uint32_t C, size_t budget, int layout,
+                                 uint64_t n_rows) {
     FillTiles t{0, 0, 0, 0, 0};
     const uint32_t W = (F + 3) / 4;
     const size_t per_word = (size_t)4 * B * C * sizeof(long long);
     const size_t max_words = budget / per_word;
     if (max_words == 0) return t;
+    const bool pays = C >= 4 || n_rows >= (4u << 20);
+    if ((layout == 2 || (layout == 1 && pays)) && max_words >= 8) {   // 32-feature tiles, bin-major
+        t.tw = std::min<uint32_t>(8, W);
+        t.n_tiles = (W + t.tw - 1) / t.tw;
+        t.bin_major = 1;
+        t.lds_bytes = (size_t)std::min<uint32_t>(4 * t.tw, F) * B * C * sizeof(long long);
+        return t;
+    }
     t.n_tiles = (uint32_t)((W + max_words - 1) / max_words);
     t.tw = (W + t.n_tiles - 1) / t.n_tiles;       // balanced tiles
     t.n_tiles = (W + t.tw - 1) / t.tw;
@@ -356,15 +367,28 @@ inline FillTiles plan_fill_tiles(uint32_t F, uint32_t B, uint32_t C, size_t budg
 // histogram only when it crosses into the next segment (leaf) and at the end, so the
 // global-atomic flush traffic is about G * tiles * cells per launch instead of one flush
 // per small chunk.  G * tiles is sized to the number of workgroups the CUs hold at once.
+// What a lane does with the 4 bytes of its word, fixed for the whole launch: visit order,
+// byte shift, LDS cell offset, validity and dominant bin per visit.  Feature-major layout
+// [ch][f][bin]: cell = f * B + bin, visits in byte order.  Bin-major layout [ch][bin][f]
+// (tiles of 32 features, 8 lanes per row, 8 rows per wave): cell = bin * 32 + f, and the row
+// of a lane rotates its visit order by (row & 3), so one atomic instruction of a wave covers
+// the 32 features of the tile twice -- every bank pair takes two lanes whatever the bins
+// (the conflict-free rate of 64-bit LDS atomics, against scattered bins over [f][bin]).
+struct FillLane {
+    uint32_t sh[4], off[4], skip[4];
+    bool ok[4];
+    uint32_t bin_stride;
+};
+
 template <int C, bool kSkip>
 __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, uint32_t W,
                                            const uint32_t* __restrict__ idx,
                                            const long long* __restrict__ sfix, uint32_t beg,
-                                           uint32_t end, uint32_t w0, uint32_t TW, uint32_t nf,
-                                           uint32_t B, uint32_t plane,
-                                           unsigned long long* __restrict__ lbase,
-                                           const uint32_t (&skip)[4]) {
-    constexpr int U = C > 12 ? 2 : kFillRows;   // rows in flight per lane (registers bound it)
+                                           uint32_t end, uint32_t w0, uint32_t TW, uint32_t plane,
+                                           unsigned long long* __restrict__ lds64,
+                                           const FillLane& fl) {
+    // rows in flight per lane: more for few channels (latency), fewer for many (registers)
+    constexpr int U = C <= 3 ? 2 * kFillRows : (C > 12 ? 2 : kFillRows);
     const uint32_t rows_per_pass = blockDim.x / TW;
     const uint32_t r0 = threadIdx.x / TW;
     const uint32_t wl = threadIdx.x - r0 * TW;
@@ -399,10 +423,10 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
             if (zero) continue;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                if ((uint32_t)k < nf) {
-                    const uint32_t bin = (word[u] >> (8 * k)) & 0xFFu;
-                    if (kSkip && bin == skip[k]) continue;   // dominant bin: rebuilt from the totals
-                    unsigned long long* cell = lbase + (uint32_t)k * B + bin;
+                if (fl.ok[k]) {
+                    const uint32_t bin = (word[u] >> fl.sh[k]) & 0xFFu;
+                    if (kSkip && bin == fl.skip[k]) continue;   // dominant bin: rebuilt from the totals
+                    unsigned long long* cell = lds64 + bin * fl.bin_stride + fl.off[k];
 #pragma unroll
                     for (int ch = 0; ch < C; ++ch)
                         atomicAdd(cell + (size_t)ch * plane, (unsigned long long)st[u][ch]);
@@ -418,7 +442,8 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t* __restrict__ idx,                  // null: dense rows [0, n), leaf 0
     const LevelPlan* __restrict__ plan, const long long* __restrict__ sfix, uint32_t n_tiles,
     uint32_t tw, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
-    const uint32_t* __restrict__ skip_bin /* nullable [F]: dominant bin left out, or >= B */) {
+    const uint32_t* __restrict__ skip_bin /* nullable [F]: dominant bin left out, or >= B */,
+    int bin_major /* LDS [ch][bin][f] with rotated visits (tw == 8), else [ch][f][bin] */) {
     extern __shared__ long long lds[];
     const uint32_t b = blockIdx.x;
     const uint32_t xcd = b & 7u, q = b >> 3;
@@ -434,13 +459,19 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     __syncthreads();
     const uint32_t r0 = threadIdx.x / TW;
     const uint32_t wl = threadIdx.x - r0 * TW;
-    unsigned long long* lbase = (unsigned long long*)lds + 4u * wl * B;
     const uint32_t nf = min(4u, TF - min(TF, 4u * wl));   // valid features of this lane's word
-    uint32_t skip[4] = {256u, 256u, 256u, 256u};
-    if (kSkip)
+    FillLane fl;
+    fl.bin_stride = bin_major ? TF : 1u;
+    const uint32_t rot = bin_major ? (r0 & 3u) : 0u;
 #pragma unroll
-        for (uint32_t k = 0; k < 4; ++k)   // constant indices: the array stays in registers
-            if (k < nf) skip[k] = skip_bin[f0 + 4u * wl + k];
+    for (uint32_t k = 0; k < 4; ++k) {   // constant indices: the tables stay in registers
+        const uint32_t kb = (k + rot) & 3u;   // byte visited at step k
+        const uint32_t f = 4u * wl + kb;
+        fl.sh[k] = 8u * kb;
+        fl.off[k] = bin_major ? f : f * B;
+        fl.ok[k] = kb < nf;
+        fl.skip[k] = (kSkip && kb < nf) ? skip_bin[f0 + f] : 256u;
+    }
     const uint32_t V = idx ? plan->rows : (uint32_t)n;
     const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
     const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
@@ -454,18 +485,38 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = idx ? plan->built[seg] : 0u;
         if (end > pos) {
-            fill_range<C, kSkip>(rows, W, idx, sfix, pos, end, w0, TW, nf, B, plane, lbase, skip);
+            fill_range<C, kSkip>(rows, W, idx, sfix, pos, end, w0, TW, plane, (unsigned long long*)lds, fl);
             __syncthreads();
-            // flush LDS [ch][f][bin] -> hist[leaf][ch][f0 + f][bin]: contiguous per plane
-            for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) {
-                const long long v = lds[i];
-                if (v != 0) {
-                    const uint32_t ch = i / plane;
-                    const uint32_t r = i - ch * plane;
-                    unsigned long long* dst = (unsigned long long*)hist +
-                        (((size_t)slot * C + ch) * F + f0) * B + r;
-                    atomicAdd(dst, (unsigned long long)v);
-                    lds[i] = 0;
+            // flush LDS -> hist[leaf][ch][f0 + f][bin]
+            if (!bin_major) {   // [ch][f][bin]: i is the global order (coalesced atomics)
+                for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) {
+                    const long long v = lds[i];
+                    if (v != 0) {
+                        const uint32_t ch = i / plane;
+                        const uint32_t r = i - ch * plane;
+                        unsigned long long* dst = (unsigned long long*)hist +
+                            (((size_t)slot * C + ch) * F + f0) * B + r;
+                        atomicAdd(dst, (unsigned long long)v);
+                        lds[i] = 0;
+                    }
+                }
+            } else {   // [ch][bin][f]: a wave takes 8 features x 8 bins (8-way LDS conflicts,
+                       // 64-byte runs of bins in the global histogram)
+                const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
+                const uint32_t vcells = C * nfb * nbb * 64;
+                for (uint32_t i = threadIdx.x; i < vcells; i += blockDim.x) {
+                    const uint32_t l = i & 63u, j = i >> 6;
+                    const uint32_t ch = j / (nfb * nbb), jb = j - ch * (nfb * nbb);
+                    const uint32_t f = (jb / nbb) * 8 + (l >> 3), bin = (jb % nbb) * 8 + (l & 7u);
+                    if (f >= TF || bin >= B) continue;
+                    const uint32_t li = ch * plane + bin * TF + f;
+                    const long long v = lds[li];
+                    if (v != 0) {
+                        unsigned long long* dst = (unsigned long long*)hist +
+                            (((size_t)slot * C + ch) * F + f0 + f) * B + bin;
+                        atomicAdd(dst, (unsigned long long)v);
+                        lds[li] = 0;
+                    }
                 }
             }
             __syncthreads();

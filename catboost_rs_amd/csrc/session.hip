@@ -394,7 +394,16 @@ int plan_tiles(cbh_session* s) {
         const long kb = std::strtol(e, nullptr, 10);
         if (kb >= 8) budget = std::min<size_t>(budget, (size_t)kb * 1024);
     }
-    s->tiles = plan_fill_tiles(s->F, s->B, s->C, budget);
+    // bin-major LDS with rotated visits (conflict-free atomics) for >= 4 channels, where the
+    // atomics per loaded word dominate (config 5: 31 -> 38 iters/s), and for >= 4M rows
+    // (config 2: fill 0.654 -> 0.621 ms per launch); at 1M rows and 2 channels its extra
+    // 32-feature tiles cost more than the bank conflicts they remove (config 3: 0.060 ->
+    // 0.073 ms).
+    // CBH_FILL_LAYOUT=feature|bin forces one layout (a measurement knob)
+    const char* lv = std::getenv("CBH_FILL_LAYOUT");
+    const std::string lay = lv ? lv : "";
+    const int layout = lay == "feature" ? 0 : lay == "bin" ? 2 : 1;
+    s->tiles = plan_fill_tiles(s->F, s->B, s->C, budget, layout, s->n);
     if (s->tiles.n_tiles == 0) return fail(CBH_DECLINED, "histogram of 4 features does not fit in LDS");
     // as many (tile, range) workgroups as the CUs hold at once, ranges a multiple of 8
     int cus = 0;
@@ -942,11 +951,11 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         if (s->use_skip)
             fill_kernel<C, true><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
                 s->rows, s->W, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
-                s->skip_bin);
+                s->skip_bin, (int)s->tiles.bin_major);
         else
             fill_kernel<C, false><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
                 s->rows, s->W, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
-                nullptr);
+                nullptr, (int)s->tiles.bin_major);
         HIP_TRY(hipGetLastError());
         if (s->use_skip) {
             default_bin_fixup_kernel<<<dim3(s->F, n_seg), 64, 0, st>>>(cur, lplan, s->skip_bin, s->seg_tot, C,

@@ -411,8 +411,12 @@ def test_config1_full_size_matches_oracle():
     _assert_same_fit(*_fit_both(d, d["params"]["iterations"]))
 
 
-def test_config2_reduced_matches_oracle():
-    """Config 2 shape (Logloss, 200 features, 254 borders, depth 6, Bayesian T=1) at 200k rows."""
+@pytest.mark.parametrize("layout", ["auto", "bin", "feature"])
+def test_config2_reduced_matches_oracle(layout, monkeypatch):
+    """Config 2 shape (Logloss, 200 features, 254 borders, depth 6, Bayesian T=1) at 200k rows,
+    with each LDS histogram layout of the fill (bin-major is what 10M rows use)."""
+    if layout != "auto":
+        monkeypatch.setenv("CBH_FILL_LAYOUT", layout)
     d = datagen.config2(n_rows=200_000)
     _assert_same_fit(*_fit_both(d, 8))
 
