@@ -370,10 +370,11 @@ inline FillTiles plan_fill_tiles(uint32_t F, uint32_t B, uint32_t C, size_t budg
 // What a lane does with the 4 bytes of its word, fixed for the whole launch: visit order,
 // byte shift, LDS cell offset, validity and dominant bin per visit.  Feature-major layout
 // [ch][f][bin]: cell = f * B + bin, visits in byte order.  Bin-major layout [ch][bin][f]
-// (tiles of 32 features, 8 lanes per row, 8 rows per wave): cell = bin * 32 + f, and the row
-// of a lane rotates its visit order by (row & 3), so one atomic instruction of a wave covers
-// the 32 features of the tile twice -- every bank pair takes two lanes whatever the bins
-// (the conflict-free rate of 64-bit LDS atomics, against scattered bins over [f][bin]).
+// (tiles of 32 features, 8 lanes per row, 8 rows per wave): cell = bin * 32 + f, and each lane
+// rotates its visit order by a function of (row, word), so one atomic instruction of a wave
+// covers the 32 features of the tile twice and any 16 consecutive lanes hit 16 distinct
+// features modulo 16 -- every bank pair takes the fewest lanes whatever the bins (the
+// conflict-free rate of 64-bit LDS atomics, against scattered bins over [f][bin]).
 struct FillLane {
     uint32_t sh[4], off[4], skip[4];
     bool ok[4];
@@ -462,7 +463,9 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t nf = min(4u, TF - min(TF, 4u * wl));   // valid features of this lane's word
     FillLane fl;
     fl.bin_stride = bin_major ? TF : 1u;
-    const uint32_t rot = bin_major ? (r0 & 3u) : 0u;
+    // visit rotation: within every 16 lanes (2 rows x 8 words) and every 32 lanes (4 rows)
+    // the features of one step are distinct modulo 16 and 32 (bank pairs at 32 and 64 banks)
+    const uint32_t rot = bin_major ? ((2u * (r0 & 1u) + ((wl >> 2) ^ ((r0 >> 1) & 1u))) & 3u) : 0u;
 #pragma unroll
     for (uint32_t k = 0; k < 4; ++k) {   // constant indices: the tables stay in registers
         const uint32_t kb = (k + rot) & 3u;   // byte visited at step k
