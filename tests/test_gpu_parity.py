@@ -421,6 +421,30 @@ def test_config2_reduced_matches_oracle(layout, monkeypatch):
     _assert_same_fit(*_fit_both(d, 8))
 
 
+@pytest.mark.parametrize("layout", ["bin", "feature"])
+@pytest.mark.parametrize("F,B,K", [(37, 17, 1), (5, 256, 1), (65, 33, 3), (33, 2, 1), (100, 255, 1)])
+def test_fill_layouts_ragged_shapes_match_oracle(layout, F, B, K, monkeypatch):
+    """Both LDS layouts of the fill on ragged tiles: feature counts that leave a short last
+    tile or a partial word, 2 to 256 bins, K = 1 and a 3-class MultiClass (4 channels)."""
+    monkeypatch.setenv("CBH_FILL_LAYOUT", layout)
+    g = np.random.default_rng(F * 1000 + B)
+    n = 30_000
+    nb = g.integers(1, B, F).astype(np.uint32)
+    nb[0] = B - 1
+    bins = np.minimum((g.random((F, n)) * (nb[:, None] + 1)).astype(np.int64), nb[:, None]).astype(np.uint8)
+    score = bins[: min(F, 4)].astype(np.float64).sum(0) / (4.0 * B) + 0.3 * g.standard_normal(n)
+    if K == 1:
+        y = (score > np.median(score)).astype(np.float64)
+        params = dict(loss="Logloss", leaf_method="Gradient", approx_dim=1)
+    else:
+        y = np.digitize(score, np.quantile(score, [1 / 3, 2 / 3])).astype(np.float64)
+        params = dict(loss="MultiClass", leaf_method="Newton", approx_dim=K)
+    d = dict(bins=bins, n_borders=nb, target=y,
+             params=dict(params, depth=5, learning_rate=0.1, l2_leaf_reg=3.0, score="Cosine",
+                         bootstrap_type="Bernoulli", subsample=0.7, boost_from_average=False))
+    _assert_same_fit(*_fit_both(d, 3))
+
+
 @pytest.mark.parametrize("loss", ["PairLogit", "PairLogitPairwise"])
 def test_config3_reduced_matches_oracle(loss):
     """Config 3 shape (groups of 20, ~10 pairs per group, 100 features, 254 borders, depth 6)."""
