@@ -405,17 +405,27 @@ int plan_tiles(cbh_session* s) {
     const int layout = lay == "feature" ? 0 : lay == "bin" ? 2 : 1;
     s->tiles = plan_fill_tiles(s->F, s->B, s->C, budget, layout, s->n);
     if (s->tiles.n_tiles == 0) return fail(CBH_DECLINED, "histogram of 4 features does not fit in LDS");
-    // as many (tile, range) workgroups as the CUs hold at once, ranges a multiple of 8
+    // (tile, range) workgroups for one or two rounds of the CUs' resident slots, ranges a
+    // multiple of 8: one round when it fills >= 97% of the slots, else the better of the two
+    // (config 2: 7 tiles on 256 one-workgroup CUs -> 1 round uses 224 slots, 2 rounds 504 of
+    // 512: fill 0.594 -> 0.563 ms per launch; more rounds add flushes and lose)
     int cus = 0;
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
     const uint32_t per_cu = std::max<uint32_t>(1, (uint32_t)((size_t)lds_max / s->tiles.lds_bytes));
-    uint32_t resident = (uint32_t)cus * std::min<uint32_t>(per_cu, 2);
+    const uint32_t cap = (uint32_t)cus * std::min<uint32_t>(per_cu, 2);
+    const uint32_t nt = s->tiles.n_tiles;
+    auto ranges_for = [&](uint32_t slots) { return std::max<uint32_t>(8, slots / nt / 8 * 8); };
+    auto fill_frac = [&](uint32_t G, uint32_t rounds) { return (double)G * nt / ((double)rounds * cap); };
+    uint32_t G = ranges_for(cap);
+    const uint32_t G2 = ranges_for(2 * cap);
+    // (two rounds only with long ranges: each workgroup's flush is a fixed cost, and at 1M rows
+    // the second round's extra flushes lose: config 3 fill 0.060 -> 0.083 ms)
+    if (fill_frac(G, 1) < 0.97 && fill_frac(G2, 2) > fill_frac(G, 1) && s->n / G2 >= 65536) G = G2;
     if (const char* e = std::getenv("CBH_FILL_WAVES")) {   // tuning knob: workgroups per CU
         const long m = std::strtol(e, nullptr, 10);
-        if (m >= 1 && m <= 16) resident = (uint32_t)cus * (uint32_t)m;
+        if (m >= 1 && m <= 16) G = ranges_for((uint32_t)cus * (uint32_t)m);
     }
-    uint32_t G = resident / s->tiles.n_tiles / 8 * 8;
-    s->fill_ranges = std::max<uint32_t>(8, G);
+    s->fill_ranges = G;
     return CBH_OK;
 }
 
