@@ -928,8 +928,17 @@ static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __rest
     const uint32_t per = (n_blocks + blockDim.x - 1) / blockDim.x;
     const uint32_t b0 = threadIdx.x * per;
     uint32_t local = 0;
-    for (uint32_t k = 0; k < per; ++k)
-        if (b0 + k < n_blocks) local += row[b0 + k];
+    constexpr uint32_t kBatch = 8;   // loads in flight per thread
+    for (uint32_t k0 = 0; k0 < per; k0 += kBatch) {
+        uint32_t v[kBatch];
+#pragma unroll
+        for (uint32_t q = 0; q < kBatch; ++q) {
+            const uint32_t k = k0 + q;
+            v[q] = (k < per && b0 + k < n_blocks) ? row[b0 + k] : 0u;
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < kBatch; ++q) local += v[q];
+    }
     sh[threadIdx.x] = local;
     __syncthreads();
     for (uint32_t o = 1; o < blockDim.x; o <<= 1) {
@@ -939,12 +948,22 @@ static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __rest
         __syncthreads();
     }
     uint32_t run = sh[threadIdx.x] - local;  // exclusive prefix of this thread's range
-    for (uint32_t k = 0; k < per; ++k)
-        if (b0 + k < n_blocks) {
-            uint32_t v = row[b0 + k];
-            row[b0 + k] = run;
-            run += v;
+    for (uint32_t k0 = 0; k0 < per; k0 += kBatch) {
+        uint32_t v[kBatch];
+#pragma unroll
+        for (uint32_t q = 0; q < kBatch; ++q) {
+            const uint32_t k = k0 + q;
+            v[q] = (k < per && b0 + k < n_blocks) ? row[b0 + k] : 0u;
         }
+#pragma unroll
+        for (uint32_t q = 0; q < kBatch; ++q) {
+            const uint32_t k = k0 + q;
+            if (k < per && b0 + k < n_blocks) {
+                row[b0 + k] = run;
+                run += v[q];
+            }
+        }
+    }
     if (threadIdx.x == blockDim.x - 1) totals[blockIdx.x] = sh[threadIdx.x];
 }
 

@@ -204,6 +204,11 @@ struct cbh_session {
     SampleParams* smp_dev = nullptr; // [2]: the tree's sampling parameters, an inert set
     // pinned staging of the per-tree results (the recorded copies land here)
     SampleParams* pin_smp = nullptr;
+    // the per-tree results (splits, plans, bounds, raw leaves) live in one device block and come
+    // back in one copy into its pinned mirror; the pointers below are views into the blocks
+    unsigned char* out_dev = nullptr;
+    unsigned char* pin_out = nullptr;
+    size_t out_bytes = 0;
     SplitRec* pin_splits = nullptr;
     LevelPlan* pin_plans = nullptr;
     Bounds* pin_bounds = nullptr;
@@ -219,9 +224,11 @@ struct cbh_session {
     void release() {
         dfree(rows); dfree(cols); dfree(weight); dfree(target); dfree(approx); dfree(sstat);
         dfree(host_sample); dfree(leaf); dfree(idx); dfree(hist[0]); dfree(hist[1]); dfree(cnt);
-        dfree(totals); dfree(plans); dfree(splits); dfree(best_score);
-        dfree(best_bin); dfree(n_cand); dfree(one_hot); dfree(scales); dfree(bounds);
-        dfree(leaf_sums); dfree(leaf_raw); dfree(leaf_scaled); dfree(jump);
+        dfree(totals); dfree(best_score);
+        dfree(best_bin); dfree(n_cand); dfree(one_hot); dfree(scales);
+        dfree(leaf_sums); dfree(leaf_scaled); dfree(jump);
+        dfree(out_dev);
+        plans = nullptr; splits = nullptr; bounds = nullptr; leaf_raw = nullptr;
         dfree(partials);
         dfree(group_off); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st);
@@ -233,9 +240,10 @@ struct cbh_session {
             if (g) (void)hipGraphExecDestroy(g);
         tree_graph[0] = tree_graph[1] = nullptr;
         dfree(smp_dev);
-        for (void* p : {(void*)pin_smp, (void*)pin_splits, (void*)pin_plans, (void*)pin_bounds, (void*)pin_leaves})
+        for (void* p : {(void*)pin_smp, (void*)pin_out})
             if (p) (void)hipHostFree(p);
-        pin_smp = nullptr; pin_splits = nullptr; pin_plans = nullptr; pin_bounds = nullptr; pin_leaves = nullptr;
+        pin_smp = nullptr; pin_out = nullptr;
+        pin_splits = nullptr; pin_plans = nullptr; pin_bounds = nullptr; pin_leaves = nullptr;
         for (auto& t : timers) {
             if (t.second.a) (void)hipEventDestroy(t.second.a);
             if (t.second.b) (void)hipEventDestroy(t.second.b);
@@ -333,13 +341,27 @@ int session_alloc(cbh_session* s) {
     s->n_part_blocks = (uint32_t)((n + kPartRows - 1) / kPartRows);
     CHECK(dalloc(&s->cnt, ((size_t)s->n_part_blocks * 4) << s->depth));   // [leaf][wave]
     CHECK(dalloc(&s->totals, (size_t)1 << s->depth));
-    CHECK(dalloc(&s->plans, s->depth));
-    CHECK(dalloc(&s->splits, s->depth));
+    {   // one block for the per-tree results, sections 256-byte aligned
+        auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+        const size_t o_plans = up(sizeof(SplitRec) * s->depth);
+        const size_t o_bounds = o_plans + up(sizeof(LevelPlan) * s->depth);
+        const size_t o_leaves = o_bounds + up(sizeof(Bounds));
+        s->out_bytes = o_leaves + sizeof(double) * ((size_t)1 << s->depth) * s->K;
+        CHECK(dalloc(&s->out_dev, s->out_bytes));
+        HIP_TRY(hipHostMalloc((void**)&s->pin_out, s->out_bytes, hipHostMallocDefault));
+        s->splits = (SplitRec*)s->out_dev;
+        s->plans = (LevelPlan*)(s->out_dev + o_plans);
+        s->bounds = (Bounds*)(s->out_dev + o_bounds);
+        s->leaf_raw = (double*)(s->out_dev + o_leaves);
+        s->pin_splits = (SplitRec*)s->pin_out;
+        s->pin_plans = (LevelPlan*)(s->pin_out + o_plans);
+        s->pin_bounds = (Bounds*)(s->pin_out + o_bounds);
+        s->pin_leaves = (double*)(s->pin_out + o_leaves);
+    }
     CHECK(dalloc(&s->best_score, s->F));
     CHECK(dalloc(&s->best_bin, s->F));
     CHECK(dalloc(&s->n_cand, s->F));
     CHECK(dalloc(&s->scales, 1));
-    CHECK(dalloc(&s->bounds, 1));
     const uint32_t CL = s->K == 1 ? 3 : s->K + s->K * (s->K + 1) / 2;
     CHECK(dalloc(&s->leaf_sums, ((size_t)1 << s->depth) * CL));
     if (s->ranking) {
@@ -364,12 +386,6 @@ int session_alloc(cbh_session* s) {
     CHECK(dalloc(&s->smp_dev, 2));
     HIP_TRY(hipMemset(s->smp_dev, 0, 2 * sizeof(SampleParams)));
     HIP_TRY(hipHostMalloc((void**)&s->pin_smp, sizeof(SampleParams), hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc((void**)&s->pin_splits, sizeof(SplitRec) * s->depth, hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc((void**)&s->pin_plans, sizeof(LevelPlan) * s->depth, hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc((void**)&s->pin_bounds, sizeof(Bounds), hipHostMallocDefault));
-    HIP_TRY(hipHostMalloc((void**)&s->pin_leaves, sizeof(double) * ((size_t)1 << s->depth) * s->K,
-                          hipHostMallocDefault));
-    CHECK(dalloc(&s->leaf_raw, ((size_t)1 << s->depth) * s->K));
     CHECK(dalloc(&s->leaf_scaled, ((size_t)1 << s->depth) * s->K));
     CHECK(dalloc(&s->partials, (size_t)kPrepBlocks * kPartials));
     s->n_coarse = (n >> 10) + 2;
@@ -1066,10 +1082,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
     }
     CHECK(s->stage_end());
 
-    HIP_TRY(hipMemcpyAsync(s->pin_splits, s->splits, sizeof(SplitRec) * s->depth, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(s->pin_plans, s->plans, sizeof(LevelPlan) * s->depth, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(s->pin_bounds, s->bounds, sizeof(Bounds), hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(s->pin_leaves, s->leaf_raw, sizeof(double) * n_leaves * K, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(s->pin_out, s->out_dev, s->out_bytes, hipMemcpyDeviceToHost, st));
     return CBH_OK;
 }
 
