@@ -1046,19 +1046,37 @@ constexpr uint32_t kPhantomBlocks = 32;        // row chunks per column
 // Block g of column c sets its rows' (bucket, float leaf) bits in an LDS bitmap and stores
 // it whole into its own slice of part (no global atomics: a hot category would otherwise
 // put thousands of atomics on one word); a column too large for LDS sets its slice directly.
+// Leaf bits of the splits before `level` on float columns (features below fc0).
+__device__ __forceinline__ uint32_t float_split_mask(const SplitRec* __restrict__ splits, uint32_t level,
+                                                     uint32_t fc0) {
+    uint32_t m = 0;
+    for (uint32_t l = 0; l < level; ++l)
+        if (splits[l].feature < fc0) m |= 1u << l;
+    return m;
+}
+
+// float_mask < 0: taken from the device splits (float_split_mask); a level with no float split
+// yet sets nothing (its phantom count is not used).
 static __global__ __launch_bounds__(256) void phantom_bits_kernel(
-    const uint16_t* __restrict__ leaf, uint64_t n, uint32_t float_mask, uint32_t L,
+    const uint16_t* __restrict__ leaf, uint64_t n, int64_t float_mask_arg, uint32_t L,
     const uint32_t* __restrict__ cat_bk, const uint32_t* __restrict__ cat_nb,
-    const uint64_t* __restrict__ word_off, uint32_t* __restrict__ part) {
+    const uint64_t* __restrict__ word_off, uint32_t* __restrict__ part, const SplitRec* __restrict__ splits,
+    uint32_t level, uint32_t fc0, const uint8_t* __restrict__ skip /* nullable: set = no count needed */,
+    uint64_t m_lo) {
     extern __shared__ uint32_t lbits[];
+    if (skip && *skip) return;
+    const uint32_t float_mask =
+        float_mask_arg >= 0 ? (uint32_t)float_mask_arg : float_split_mask(splits, level, fc0);
+    if (float_mask == 0) return;
     const uint32_t c = blockIdx.y, g = blockIdx.x;
+    // a column with at most m_lo possible pairs cannot raise the max count above m_lo
+    if ((uint64_t)cat_nb[c] << __popc(float_mask) <= m_lo) return;
     const uint64_t words = ((uint64_t)cat_nb[c] * L + 31) / 32;
     const bool lds = words <= kPhantomLdsWords;
     uint32_t* slice = part + word_off[c] + (uint64_t)g * words;
-    if (lds) {
-        for (uint32_t w = threadIdx.x; w < words; w += blockDim.x) lbits[w] = 0;
-        __syncthreads();
-    }
+    uint32_t* bits = lds ? lbits : slice;   // a block owns its slice: it clears it itself
+    for (uint64_t w = threadIdx.x; w < words; w += blockDim.x) bits[w] = 0;
+    __syncthreads();
     const uint32_t* bk = cat_bk + (size_t)c * n;
     const uint64_t per = (n + gridDim.x - 1) / gridDim.x;
     const uint64_t beg = (uint64_t)g * per;
@@ -1095,9 +1113,18 @@ static __global__ __launch_bounds__(256) void phantom_bits_kernel(
 static __global__ __launch_bounds__(256) void phantom_count_kernel(const uint32_t* __restrict__ part,
                                                                    const uint64_t* __restrict__ word_off,
                                                                    const uint32_t* __restrict__ cat_nb, uint32_t L,
-                                                                   unsigned long long* __restrict__ cnt) {
+                                                                   unsigned long long* __restrict__ cnt,
+                                                                   const SplitRec* __restrict__ splits,
+                                                                   uint32_t level, uint32_t fc0,
+                                                                   const uint8_t* __restrict__ skip,
+                                                                   int64_t float_mask_arg, uint64_t m_lo) {
     __shared__ unsigned long long red[256];
     const uint32_t c = blockIdx.x;
+    const uint32_t fm = float_mask_arg >= 0 ? (uint32_t)float_mask_arg : float_split_mask(splits, level, fc0);
+    if ((skip && *skip) || fm == 0 || ((uint64_t)cat_nb[c] << __popc(fm)) <= m_lo) {   // no count
+        if (threadIdx.x == 0) cnt[c] = 0;
+        return;
+    }
     const uint64_t words = ((uint64_t)cat_nb[c] * L + 31) / 32;
     const uint32_t* base = part + word_off[c];
     unsigned long long acc = 0;
@@ -1113,6 +1140,30 @@ static __global__ __launch_bounds__(256) void phantom_count_kernel(const uint32_
         __syncthreads();
     }
     if (threadIdx.x == 0) cnt[c] = red[0];
+}
+
+// model_size_reg weights of the CTR columns for one level, on the device: a column whose
+// (type, projection) group is in the model (group_used, from earlier trees) or in this tree's
+// earlier levels scores with weight 1; any other with pow_table[c][max_count - m_lo], the
+// host's pow(1 + bc_c / m, -model_size_reg) for every m in [m_lo, m_hi], where max_count is
+// the larger of the eligible maximum m_lo and the phantom counts once a float split is in the
+// tree (tree.rs:3093-3178, 3340-3346).
+static __global__ __launch_bounds__(64) void ctr_weights_kernel(
+    const SplitRec* __restrict__ splits, uint32_t level, uint32_t fc0, uint32_t ctr_n,
+    const uint32_t* __restrict__ group, const uint8_t* __restrict__ group_used,
+    const unsigned long long* __restrict__ phantom_cnt, uint32_t cat_n, const double* __restrict__ pow_table,
+    uint64_t m_lo, uint64_t m_hi, int msr_zero, double* __restrict__ fweight) {
+    uint64_t max_count = m_lo;
+    if (cat_n && float_split_mask(splits, level, fc0) != 0)
+        for (uint32_t c = 0; c < cat_n; ++c) max_count = max(max_count, (uint64_t)phantom_cnt[c]);
+    max_count = min(max_count, m_hi);   // the table covers every reachable count
+    const uint64_t span = m_hi - m_lo + 1;
+    for (uint32_t c = threadIdx.x; c < ctr_n; c += blockDim.x) {
+        bool used = group_used[group[c]] != 0;
+        for (uint32_t l = 0; l < level; ++l)
+            if (splits[l].feature >= fc0 && group[splits[l].feature - fc0] == group[c]) used = true;
+        fweight[fc0 + c] = (used || msr_zero) ? 1.0 : pow_table[(size_t)c * span + (max_count - m_lo)];
+    }
 }
 
 static __global__ __launch_bounds__(256) void averaging_leaf_kernel(uint16_t* __restrict__ leaf, uint64_t n,

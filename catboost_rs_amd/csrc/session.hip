@@ -197,6 +197,16 @@ struct cbh_session {
     double* fweight = nullptr;                  // [F] score multiplier (1 except CTR columns)
     std::vector<double> fweight_host;
     bool fweight_one = false;                   // the device weights are all 1
+    // device-side weights (ctr_dev): pow(1 + bc_c / m, -model_size_reg) tabulated on the host
+    // for every reachable max count m in [ctr_m_lo, ctr_m_hi], per-level bitmap offsets, and
+    // the model's used groups mirrored before every tree
+    bool ctr_dev = false;
+    double* ctr_pow = nullptr;                  // [ctr_n][m_hi - m_lo + 1]
+    uint64_t ctr_m_lo = 0, ctr_m_hi = 0;
+    uint32_t* ctr_group_dev = nullptr;          // [ctr_n]
+    uint8_t* ctr_used_dev = nullptr;            // [ctr_n] by group
+    uint8_t* pin_ctr_used = nullptr;
+    uint64_t* phantom_off_lv = nullptr;         // [depth][cat_n] word offsets at each level
 
     // per-tree launch sequence recorded once and replayed (index: host sample given or not)
     hipGraphExec_t tree_graph[2] = {nullptr, nullptr};
@@ -235,7 +245,10 @@ struct cbh_session {
         dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot);
         dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_lv);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
-        dfree(phantom_cnt); dfree(fweight);
+        dfree(phantom_cnt); dfree(fweight); dfree(ctr_pow); dfree(ctr_group_dev); dfree(ctr_used_dev);
+        dfree(phantom_off_lv);
+        if (pin_ctr_used) (void)hipHostFree(pin_ctr_used);
+        pin_ctr_used = nullptr;
         for (auto& g : tree_graph)
             if (g) (void)hipGraphExecDestroy(g);
         tree_graph[0] = tree_graph[1] = nullptr;
@@ -890,13 +903,14 @@ int ctr_level_weights(cbh_session* s, uint32_t level) {
             words += kPhantomBlocks * (((uint64_t)s->cat_nb[c] * L + 31) / 32);
         }
         HIP_TRY(hipMemcpyAsync(s->phantom_off, off.data(), sizeof(uint64_t) * s->cat_n, hipMemcpyHostToDevice, st));
-        zero_u32_kernel<<<grid_for(words, 256, 4096), 256, 0, st>>>(s->phantom_bits, words);
-        HIP_TRY(hipGetLastError());
+        (void)words;
         phantom_bits_kernel<<<dim3(kPhantomBlocks, s->cat_n), 256, kPhantomLdsWords * sizeof(uint32_t), st>>>(
-            s->leaf, s->n, float_mask, L, s->cat_bk, s->cat_nb_dev, s->phantom_off, s->phantom_bits);
+            s->leaf, s->n, (int64_t)float_mask, L, s->cat_bk, s->cat_nb_dev, s->phantom_off, s->phantom_bits,
+            nullptr, 0u, 0u, nullptr, s->ctr_eligible_max);
         HIP_TRY(hipGetLastError());
         phantom_count_kernel<<<s->cat_n, 256, 0, st>>>(s->phantom_bits, s->phantom_off, s->cat_nb_dev, L,
-                                                       s->phantom_cnt);
+                                                       s->phantom_cnt, nullptr, 0u, 0u, nullptr, (int64_t)float_mask,
+                                                       s->ctr_eligible_max);
         HIP_TRY(hipGetLastError());
         std::vector<unsigned long long> cnt(s->cat_n);
         HIP_TRY(hipMemcpyAsync(cnt.data(), s->phantom_cnt, sizeof(unsigned long long) * s->cat_n,
@@ -914,6 +928,31 @@ int ctr_level_weights(cbh_session* s, uint32_t level) {
         s->fweight_host[fc0 + c] = w;
     }
     HIP_TRY(hipMemcpyAsync(s->fweight, s->fweight_host.data(), sizeof(double) * s->F, hipMemcpyHostToDevice, st));
+    return CBH_OK;
+}
+
+// The same weights without the host: phantom bitmaps and counts read the float splits from the
+// device (nothing is set before the first float split), and ctr_weights_kernel picks each
+// column's weight from the host-built pow table.  Recordable into the tree graph.
+int ctr_level_weights_dev(cbh_session* s, uint32_t level) {
+    hipStream_t st = s->stream;
+    const uint32_t fc0 = s->F - s->ctr_n;
+    if (level >= 1 && s->cat_n) {
+        const uint32_t L = 1u << level;
+        const uint64_t* off = s->phantom_off_lv + (size_t)level * s->cat_n;
+        phantom_bits_kernel<<<dim3(kPhantomBlocks, s->cat_n), 256, kPhantomLdsWords * sizeof(uint32_t), st>>>(
+            s->leaf, s->n, -1, L, s->cat_bk, s->cat_nb_dev, off, s->phantom_bits, s->splits, level, fc0,
+            s->ctr_used_dev + s->ctr_n, s->ctr_m_lo);
+        HIP_TRY(hipGetLastError());
+        phantom_count_kernel<<<s->cat_n, 256, 0, st>>>(s->phantom_bits, off, s->cat_nb_dev, L, s->phantom_cnt,
+                                                       s->splits, level, fc0, s->ctr_used_dev + s->ctr_n, -1,
+                                                       s->ctr_m_lo);
+        HIP_TRY(hipGetLastError());
+    }
+    ctr_weights_kernel<<<1, 64, 0, st>>>(s->splits, level, fc0, s->ctr_n, s->ctr_group_dev, s->ctr_used_dev,
+                                         s->phantom_cnt, level >= 1 ? s->cat_n : 0u, s->ctr_pow, s->ctr_m_lo,
+                                         s->ctr_m_hi, s->msr == 0.0 ? 1 : 0, s->fweight);
+    HIP_TRY(hipGetLastError());
     return CBH_OK;
 }
 
@@ -1004,7 +1043,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             CHECK(s->stage_end());
         }
         // ---- score + argmax ----
-        if (s->ctr_n) CHECK(ctr_level_weights(s, level));
+        if (s->ctr_n) CHECK(s->ctr_dev ? ctr_level_weights_dev(s, level) : ctr_level_weights(s, level));
         CHECK(s->stage_begin(kStScore));
         if (s->pairwise) {
             CHECK(pairwise_level(s, cur, level));
@@ -1117,7 +1156,12 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     // replay the recorded tree when nothing differs from it: previous leaves pending, no
     // per-stage events, no pairwise stage (its level solves are not recorded)
     // a CTR session replays once every CTR group is in the model (no per-level host step left)
-    const bool ctr_static = !s->ctr_n || (ctr_all_used(s) && s->fweight_one);
+    const bool ctr_static = !s->ctr_n || s->ctr_dev || (ctr_all_used(s) && s->fweight_one);
+    if (s->ctr_dev) {   // the groups earlier trees used (and whether all are), for this tree
+        std::copy(s->ctr_used.begin(), s->ctr_used.end(), s->pin_ctr_used);
+        s->pin_ctr_used[s->ctr_n] = ctr_all_used(s) ? 1 : 0;   // then no phantom count is needed
+        HIP_TRY(hipMemcpyAsync(s->ctr_used_dev, s->pin_ctr_used, s->ctr_n + 1, hipMemcpyHostToDevice, st));
+    }
     const bool replay = s->pending && !s->cfg.profile && !s->pairwise && !s->graph_off && ctr_static;
     hipGraphExec_t& ge = s->tree_graph[use_host_sample ? 1 : 0];
     if (replay && !ge) record_tree<K>(s, use_host_sample);
@@ -1338,6 +1382,46 @@ int cbh_session_set_ctr(cbh_session* s, const cbh_ctr_info* info) {
     s->cat_nb.assign(info->cat_bucket_count, info->cat_bucket_count + info->n_cat);
     s->msr = info->model_size_reg;
     s->ctr_n = m;
+    // device weights when the pow table stays modest: counts reachable at any level are the
+    // eligible maximum and the phantom counts, at most (float leaves) x (buckets)
+    {
+        uint64_t nb_max = 0;
+        for (uint32_t v : s->cat_nb) nb_max = std::max<uint64_t>(nb_max, v);
+        const uint64_t m_lo = s->ctr_eligible_max;
+        const uint64_t m_hi = std::max<uint64_t>(m_lo, (uint64_t)lmax * nb_max);
+        const uint64_t span = m_hi - m_lo + 1;
+        // CBH_CTR_WEIGHTS=host keeps the per-level host step (a test knob for that path)
+        const char* cw = std::getenv("CBH_CTR_WEIGHTS");
+        const bool host_only = cw && std::string(cw) == "host";
+        if (!host_only && (uint64_t)m * span <= (32ull << 20)) {
+            std::vector<double> table((size_t)m * span);
+            for (uint32_t c = 0; c < m; ++c)
+                for (uint64_t k = 0; k < span; ++k)
+                    table[(size_t)c * span + k] =
+                        std::pow(1.0 + (double)s->ctr_bc[c] / (double)(m_lo + k), -s->msr);
+            CHECK(dalloc(&s->ctr_pow, table.size()));
+            HIP_TRY(hipMemcpy(s->ctr_pow, table.data(), sizeof(double) * table.size(), hipMemcpyHostToDevice));
+            CHECK(dalloc(&s->ctr_group_dev, m));
+            HIP_TRY(hipMemcpy(s->ctr_group_dev, s->ctr_group.data(), sizeof(uint32_t) * m, hipMemcpyHostToDevice));
+            CHECK(dalloc(&s->ctr_used_dev, m + 1));   // [m] by group, then the all-used flag
+            HIP_TRY(hipHostMalloc((void**)&s->pin_ctr_used, m + 1, hipHostMallocDefault));
+            if (s->cat_n) {
+                std::vector<uint64_t> offs((size_t)s->depth * s->cat_n, 0);
+                for (uint32_t lv = 1; lv < s->depth; ++lv) {
+                    uint64_t w = 0;
+                    for (uint32_t c = 0; c < s->cat_n; ++c) {
+                        offs[(size_t)lv * s->cat_n + c] = w;
+                        w += kPhantomBlocks * (((uint64_t)s->cat_nb[c] * (1u << lv) + 31) / 32);
+                    }
+                }
+                CHECK(dalloc(&s->phantom_off_lv, offs.size()));
+                HIP_TRY(hipMemcpy(s->phantom_off_lv, offs.data(), sizeof(uint64_t) * offs.size(), hipMemcpyHostToDevice));
+            }
+            s->ctr_m_lo = m_lo;
+            s->ctr_m_hi = m_hi;
+            s->ctr_dev = true;
+        }
+    }
     return CBH_OK;
 }
 

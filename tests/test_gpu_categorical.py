@@ -83,11 +83,15 @@ def _config4_columns(d, perm):
     return dev
 
 
-def test_config4_all_ctr_reduced_matches_oracle():
+@pytest.mark.parametrize("weights", ["device", "host"])
+def test_config4_all_ctr_reduced_matches_oracle(weights, monkeypatch):
     """Config 4's reference-legal all-CTR variant at 200k rows (RMSE, Bernoulli 0.66, depth 6)
     with the reference's CTR training semantics (model_size_reg weights with the phantom
     count, leaves over the averaging-permutation columns): device CTR columns equal the
-    oracle's, then 6 trees equal the oracle's."""
+    oracle's, then 6 trees equal the oracle's -- with the weights picked on the device from
+    the tabulated pow values, and with the per-level host step."""
+    if weights == "host":
+        monkeypatch.setenv("CBH_CTR_WEIGHTS", "host")
     from catboost_rs_amd import datagen
     from tests.test_gpu_parity import _close
     d = datagen.config4(n_rows=200_000)
