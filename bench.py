@@ -284,7 +284,8 @@ def main():
         f"{achieved:.1f} GB/s algorithmic")
 
     # LDS-atomic roofline of the fill: every visited (row, feature) adds K+1 64-bit integer
-    # cells; the cap is the scattered 64-bit LDS atomic rate measured on this GPU
+    # cells; the caps are the 64-bit LDS atomic rates measured on this GPU, scattered (random
+    # bins: the feature-major layout) and contiguous (the bin-major layout's pattern)
     K = kw["approx_dim"] if P["loss"] == "MultiClass" else 1
     lds = None
     rates = _lds_rates()
@@ -297,8 +298,11 @@ def main():
                "cap_scattered_u64_per_s": rates["scattered_u64"],
                "cap_contiguous_u64_per_s": rates.get("contiguous_u64"),
                "frac_of_scattered_cap": round(ach / rates["scattered_u64"], 4)}
+        if rates.get("contiguous_u64"):
+            lds["frac_of_contiguous_cap"] = round(ach / rates["contiguous_u64"], 4)
         log(f"fill LDS atomics: {ach:.3e}/s = {100 * ach / rates['scattered_u64']:.1f}% of the "
-            f"measured scattered-u64 cap {rates['scattered_u64']:.3e}/s")
+            f"measured scattered-u64 cap {rates['scattered_u64']:.3e}/s, "
+            f"{100 * ach / rates.get('contiguous_u64', float('inf')):.1f}% of the contiguous-u64 cap")
 
     cpu = None
     if not args.no_cpu and cpu_trees > 0:
