@@ -703,6 +703,7 @@ static __global__ __launch_bounds__(64) void default_bin_fixup_kernel(long long*
 // ---------------------------------------------------------------------------------
 template <int K, int NW>
 __global__ __launch_bounds__(64 * NW) void score_kernel(
+    long long* __restrict__ zero_buf, uint32_t zero_leaves, uint32_t HC,   // next level's histogram
     const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
     const uint32_t* __restrict__ n_cand, const uint8_t* __restrict__ one_hot,
     const Scales* __restrict__ sc, double l2, int cosine, double* __restrict__ best_score,
@@ -713,6 +714,11 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     __shared__ uint32_t red_b[NW];
     const uint32_t f = blockIdx.x;
     const uint32_t b = threadIdx.x;
+    // clear feature f's cells of the next level's histogram [leaf][HC][F][B] (its fill adds)
+    for (uint32_t i = threadIdx.x; i < zero_leaves * HC * B; i += blockDim.x) {
+        const uint32_t lc = i / B, bb = i - lc * B;
+        zero_buf[((size_t)lc * F + f) * B + bb] = 0;
+    }
     const uint32_t nc = n_cand[f];
     if (nc == 0) {
         if (b == 0) {

@@ -997,10 +997,13 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         long long* cur = s->hist[level & 1];
         long long* par = s->hist[(level + 1) & 1];
         const uint32_t n_leaves = 1u << level;
-        // ---- fill (the histogram it accumulates into is zeroed first, timed apart) ----
-        CHECK(s->stage_begin(kStPrepare));
-        CHECK(launch_zero(cur, per_leaf * n_leaves, st));
-        CHECK(s->stage_end());
+        // ---- fill (the histogram it accumulates into is zeroed first: here at level 0 and with
+        // pairwise scoring, else by the previous level's score kernel) ----
+        if (level == 0 || s->pairwise) {
+            CHECK(s->stage_begin(kStPrepare));
+            CHECK(launch_zero(cur, per_leaf * n_leaves, st));
+            CHECK(s->stage_end());
+        }
         CHECK(s->stage_begin(kStFill));
         const uint32_t nt = s->tiles.n_tiles;
         const uint32_t G = s->fill_ranges;
@@ -1045,18 +1048,22 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         // ---- score + argmax ----
         if (s->ctr_n) CHECK(s->ctr_dev ? ctr_level_weights_dev(s, level) : ctr_level_weights(s, level));
         CHECK(s->stage_begin(kStScore));
+        // the score also clears the next level's histogram (the parent buffer, dead once the
+        // derive above has run)
+        long long* zbuf = level + 1 < s->depth ? par : nullptr;
+        const uint32_t zleaves = level + 1 < s->depth ? 2u * n_leaves : 0u;
         if (s->pairwise) {
             CHECK(pairwise_level(s, cur, level));
         } else if (s->max_cand <= 64)
-            score_kernel<K, 1><<<s->F, 64, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
+            score_kernel<K, 1><<<s->F, 64, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin,
                                                    s->ctr_n ? s->fweight : nullptr);
         else if (s->max_cand <= 128)
-            score_kernel<K, 2><<<s->F, 128, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
+            score_kernel<K, 2><<<s->F, 128, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
                                                     s->scales, s->l2, cosine, s->best_score, s->best_bin,
                                                    s->ctr_n ? s->fweight : nullptr);
         else
-            score_kernel<K, 4><<<s->F, 256, 0, st>>>(cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
+            score_kernel<K, 4><<<s->F, 256, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
                                                     s->scales, s->l2, cosine, s->best_score, s->best_bin,
                                                    s->ctr_n ? s->fweight : nullptr);
         HIP_TRY(hipGetLastError());
