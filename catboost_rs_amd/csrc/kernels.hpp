@@ -529,31 +529,18 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     }
 }
 
-// Sibling by subtraction: for each parent p, the child not built directly is
-// parent - built (exact in integers).  hist_cur has 2 * n_parent leaves.
-static __global__ void derive_kernel(const long long* __restrict__ parent, long long* __restrict__ cur,
-                              const LevelPlan* __restrict__ plan, uint32_t n_parent,
-                              size_t per_leaf) {
-    const size_t total = (size_t)n_parent * per_leaf;
-    for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
-         t += (size_t)gridDim.x * blockDim.x) {
-        const uint32_t p = (uint32_t)(t / per_leaf);
-        const size_t j = t - (size_t)p * per_leaf;
-        const uint32_t built = plan->built[p];
-        const uint32_t other = built == p ? p + n_parent : p;
-        cur[(size_t)other * per_leaf + j] = parent[t] - cur[(size_t)built * per_leaf + j];
-    }
-}
-
 // Histograms are kept in PREFIX form over bins (cell b holds the sum of bins 0..b): the
 // split scorer then reads FALSE = prefix[b], TRUE = prefix[B-1] - prefix[b] directly, and
 // the sibling subtraction stays valid because the prefix is linear.  This pass turns the
 // directly built children of a level (raw sums from the fill) into prefix form: one wave per
 // (child, channel, feature) row, each lane scanning up to 4 consecutive bins.
+// With `parent` given (levels >= 1) the same wave then writes the sibling row, parent - built,
+// both in prefix form (the subtraction is linear), so no separate derive pass is needed.
 static __global__ __launch_bounds__(256) void hist_prefix_kernel(long long* __restrict__ hist,
                                                                  const LevelPlan* __restrict__ plan,
                                                                  uint32_t n_built, uint32_t C, uint32_t F,
-                                                                 uint32_t B) {
+                                                                 uint32_t B,
+                                                                 const long long* __restrict__ parent) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint64_t row = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint64_t rows = (uint64_t)n_built * C * F;
@@ -584,6 +571,16 @@ static __global__ __launch_bounds__(256) void hist_prefix_kernel(long long* __re
     for (uint32_t e = 0; e < 4; ++e) {
         const uint32_t b = b0 + e;
         if (e < E && b < B) h[b] = v[e] + off;
+    }
+    if (!parent) return;
+    // sibling of the built child: parent segment seg has children seg and seg + n_built
+    const uint32_t other = slot == seg ? seg + n_built : seg;
+    const long long* pr = parent + ((size_t)seg * C * F + rem) * B;
+    long long* sib = hist + ((size_t)other * C * F + rem) * B;
+#pragma unroll
+    for (uint32_t e = 0; e < 4; ++e) {
+        const uint32_t b = b0 + e;
+        if (e < E && b < B) sib[b] = pr[b] - (v[e] + off);
     }
 }
 

@@ -1030,21 +1030,14 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
                                                                       s->F, s->B);
             HIP_TRY(hipGetLastError());
         }
-        {   // built children to prefix form over bins (the level's histograms stay in it)
+        {   // built children to prefix form over bins (the level's histograms stay in it), and
+            // their siblings = parent - built (levels >= 1)
             const uint64_t rows = (uint64_t)n_seg * C * s->F;
-            hist_prefix_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(cur, lplan, n_seg, C, s->F, s->B);
+            hist_prefix_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(cur, lplan, n_seg, C, s->F, s->B,
+                                                                           level > 0 ? par : nullptr);
             HIP_TRY(hipGetLastError());
         }
         CHECK(s->stage_end());
-        // ---- derive the sibling of every directly built child ----
-        if (level > 0) {
-            CHECK(s->stage_begin(kStDerive));
-            const uint32_t n_parent = n_leaves / 2;
-            derive_kernel<<<grid_for(per_leaf * n_parent, 256, 16384), 256, 0, st>>>(
-                par, cur, s->plans + (level - 1), n_parent, per_leaf);
-            HIP_TRY(hipGetLastError());
-            CHECK(s->stage_end());
-        }
         // ---- score + argmax ----
         if (s->ctr_n) CHECK(s->ctr_dev ? ctr_level_weights_dev(s, level) : ctr_level_weights(s, level));
         CHECK(s->stage_begin(kStScore));
