@@ -16,7 +16,7 @@ import catboost_rs_amd as cb
 from catboost_rs_amd import datagen
 from oracle import oracle as O
 from tests import golden_data as G
-from tests.trees import one_hot_bins, same_partition, upstream_one_hot_splits
+from tests.trees import one_hot_bins, same_partition, tree_rows, upstream_one_hot_splits
 
 pytestmark = pytest.mark.gpu
 
@@ -168,6 +168,72 @@ def test_boosting_matches_oracle(case):
         assert np.array_equal(splits[it], exp["splits"][it]), f"tree {it} splits differ"
         _close(leaves[it], exp["leaf_values"][it])
     _close(approx, exp["approx"])
+
+
+@pytest.mark.parametrize("n", [1, 2, 5, 63, 65, 257])
+@pytest.mark.parametrize("F", [1, 3])
+@pytest.mark.parametrize("case", [0, 1, 2, 4])
+def test_tiny_inputs_match_oracle(case, F, n):
+    """Fewer rows than leaves at depth 6: empty children, leaves of one row, borders with no
+    row between them (identical scores: the first wins), bootstrap samples of a handful of
+    rows, and row counts either side of a wave.
+
+    With one feature every tie is between candidates whose sums are identical, so the splits
+    must be equal.  With several features, tiny leaves also produce candidates that are tied
+    only in exact arithmetic: two features that cut every leaf's rows into the same two
+    groups, with TRUE and FALSE swapped in some leaves, fold the same terms in another order.
+    The reference breaks such a tie by the rounding of its sequential f64 sums and the device
+    by its exact sums, so there the test asks for the same row groups and the same value for
+    every row instead of the same (feature, border)."""
+    p = dict(CASES[case])
+    K = p.get("approx_dim", 1)
+    bins, nb, y, w = datagen.random_case(7 * n + F, n, F, max_borders=9, K=K,
+                                         zero_weight_frac=0.2 if n > 5 else 0.0)
+    if p["loss"] == "Logloss":
+        y = (y > 0.3).astype(np.float64)
+    depth, iters = 6, 3
+    exp = O.train(bins, nb, y, depth=depth, iterations=iters, learning_rate=0.2, l2_leaf_reg=3.0,
+                  weight=w, random_seed=42, **p)
+    tr = cb.Trainer(bins, max(2, int(nb.max()) + 1), y, depth=depth, learning_rate=0.2,
+                    l2_leaf_reg=3.0, weight=w, random_seed=42, real_folds=nb + 1, **p)
+    try:
+        splits, leaves = tr.fit(iters)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    flat = [False] * depth
+    for it in range(iters):
+        if F == 1:
+            assert np.array_equal(splits[it], exp["splits"][it]), f"n={n}: tree {it} splits differ"
+        ga = tree_rows(bins, splits[it], flat)
+        ea = tree_rows(bins, exp["splits"][it], flat)
+        pairs = np.unique(np.stack([ga, ea]), axis=1)
+        assert pairs.shape[1] == np.unique(ga).size == np.unique(ea).size, \
+            f"n={n} F={F}: tree {it} groups the rows differently"
+        _close(np.asarray(leaves[it])[:, ga], np.asarray(exp["leaf_values"][it])[:, ea])  # [K][row]
+    _close(approx, exp["approx"])
+
+
+def test_no_candidate_split_is_degenerate():
+    """No feature has a border: the first level has no candidate split, which the reference
+    reports as CbError::Degenerate (crates/cb-train/src/tree.rs:2604-2606); the oracle
+    refuses the same input."""
+    g = np.random.default_rng(3)
+    n, F = 1000, 4
+    bins = np.zeros((F, n), np.uint8)
+    nb = np.zeros(F, np.uint32)
+    y = g.standard_normal(n)
+    with pytest.raises(RuntimeError):
+        O.train(bins, nb, y, depth=4, iterations=2, learning_rate=0.2, l2_leaf_reg=3.0,
+                random_seed=42, **CASES[0])
+    tr = cb.Trainer(bins, 2, y, depth=4, learning_rate=0.2, l2_leaf_reg=3.0, random_seed=42,
+                    real_folds=nb + 1, **CASES[0])
+    try:
+        with pytest.raises(cb.CbhError) as e:
+            tr.fit(2)
+        assert e.value.code == -3
+    finally:
+        tr.close()
 
 
 @pytest.mark.parametrize("name", ["bootstrap_no", "bootstrap_bayesian", "bootstrap_bernoulli",
