@@ -107,7 +107,7 @@ int run_fill(const uint32_t* rows, uint32_t W, uint64_t n, const uint32_t* idx,
     HIP_OK(hipFuncSetAttribute((const void*)fill_kernel<C, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)ft.lds_bytes));
     const uint32_t G = 64;
-    fill_kernel<C, false><<<G * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, n, idx, plan,
+    fill_kernel<C, false><<<G * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, W, n, idx, plan,
                                                              (const long long*)sstat, ft.n_tiles, ft.tw,
                                                              F, B, G, hist, nullptr, (int)ft.bin_major);
     HIP_OK(hipGetLastError());

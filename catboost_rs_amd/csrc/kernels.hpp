@@ -439,7 +439,8 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
 
 template <int C, bool kSkip>
 static __global__ __launch_bounds__(1024) void fill_kernel(
-    const uint32_t* __restrict__ rows, uint32_t W, uint64_t n,
+    const uint32_t* __restrict__ rows, uint32_t W, uint32_t stride /* words per row in memory, >= W */,
+    uint64_t n,
     const uint32_t* __restrict__ idx,                  // null: dense rows [0, n), leaf 0
     const LevelPlan* __restrict__ plan, const long long* __restrict__ sfix, uint32_t n_tiles,
     uint32_t tw, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
@@ -488,7 +489,7 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = idx ? plan->built[seg] : 0u;
         if (end > pos) {
-            fill_range<C, kSkip>(rows, W, idx, sfix, pos, end, w0, TW, plane, (unsigned long long*)lds, fl);
+            fill_range<C, kSkip>(rows, stride, idx, sfix, pos, end, w0, TW, plane, (unsigned long long*)lds, fl);
             __syncthreads();
             // flush LDS -> hist[leaf][ch][f0 + f][bin]
             if (!bin_major) {   // [ch][f][bin]: i is the global order (coalesced atomics)

@@ -105,7 +105,7 @@ struct cbh_session {
     cbh_config cfg{};
     std::vector<uint8_t> one_hot_host;
     uint64_t n = 0;
-    uint32_t F = 0, B = 0, W = 0, K = 1, C = 2, depth = 0;
+    uint32_t F = 0, B = 0, W = 0, Ws = 0, K = 1, C = 2, depth = 0;   // Ws: words per packed row in memory
     double lr = 0.0, l2 = 0.0;
     bool has_weight = false, target_set = false, pending = false;
     hipStream_t stream = nullptr;
@@ -339,7 +339,7 @@ int validate_config(const cbh_config* cfg, uint32_t n_bins, uint64_t n, uint32_t
 
 int session_alloc(cbh_session* s) {
     const uint64_t n = s->n;
-    CHECK(dalloc(&s->rows, (size_t)n * s->W));
+    CHECK(dalloc(&s->rows, (size_t)n * s->Ws));
     CHECK(dalloc(&s->cols, (size_t)n * s->F));
     if (s->has_weight) CHECK(dalloc(&s->weight, n));
     CHECK(dalloc(&s->target, n));
@@ -635,6 +635,17 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     s->F = F;
     s->B = n_bins;
     s->W = (F + 3) / 4;
+    // packed rows padded to a multiple of 16 words (64 bytes): a feature tile's 32-byte run
+    // of a row never straddles a 64-byte sector and a row spans whole 128-byte lines, which
+    // the fill's gathers through the partitioned index list fetch (config 2: fill 0.559 ->
+    // 0.531 ms per launch; configs 1, 3, 4 unchanged).  CBH_ROW_ALIGN_WORDS sets another
+    // multiple (1: unpadded), a measurement knob
+    uint32_t align = 16;
+    if (const char* e = std::getenv("CBH_ROW_ALIGN_WORDS")) {
+        const long a = std::strtol(e, nullptr, 10);
+        if (a >= 1 && a <= 64) align = (uint32_t)a;
+    }
+    s->Ws = (s->W + align - 1) / align * align;
     s->K = (uint32_t)cfg->approx_dim;
     s->C = s->K + 1;
     s->depth = (uint32_t)cfg->depth;
@@ -680,7 +691,7 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     }
     // feature-major u8 bins in place, then pack the row-major words on the device
     CHECK(load_cols(s.get()));
-    pack_rows_kernel<<<grid_for((uint64_t)n * s->W, 256), 256, 0, s->stream>>>(s->cols, n, F, s->W, s->rows);
+    pack_rows_kernel<<<grid_for((uint64_t)n * s->Ws, 256), 256, 0, s->stream>>>(s->cols, n, F, s->Ws, s->rows);
     HIP_TRY(hipGetLastError());
     CHECK(plan_skip_bins(s.get()));
     if (weight) HIP_TRY(hipMemcpy(s->weight, weight, sizeof(double) * n, hipMemcpyHostToDevice));
@@ -832,7 +843,7 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
         const uint32_t n_tri = P * (P + 1) / 2;   // leaf pairs {a <= b}
         const uint32_t grid = 8u * s->pair_tiles * ((n_tri + 7) / 8);
         const size_t lds = (size_t)s->pair_tf * 2 * B * 2 * sizeof(long long);
-        pair_stats_key_kernel<<<grid, 256, lds, st>>>(s->rows, s->W, s->key_rec, s->key_wq, s->key_off, F,
+        pair_stats_key_kernel<<<grid, 256, lds, st>>>(s->rows, s->Ws, s->key_rec, s->key_wq, s->key_off, F,
                                                           P, B, s->pair_tf, s->pair_tiles, s->pair_st);
         HIP_TRY(hipGetLastError());
     }
@@ -1004,27 +1015,32 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             CHECK(launch_zero(cur, per_leaf * n_leaves, st));
             CHECK(s->stage_end());
         }
-        CHECK(s->stage_begin(kStFill));
         const uint32_t nt = s->tiles.n_tiles;
         const uint32_t G = s->fill_ranges;
         const uint32_t* lidx = level == 0 ? nullptr : s->idx;
         const LevelPlan* lplan = level == 0 ? nullptr : s->plans + (level - 1);
         const uint32_t n_seg = level == 0 ? 1u : (1u << (level - 1));
-        if (s->use_skip) {
+        if (s->use_skip) {   // segment totals for the dominant-bin rebuild (timed with the finishing)
+            CHECK(s->stage_begin(kStDerive));
             CHECK(launch_zero(s->seg_tot, (size_t)n_seg * C, st));
             seg_totals_kernel<<<grid_for(n, 256, 1024), 256, 0, st>>>(lidx, lplan, n,
                                                                      (const long long*)s->sstat, C, s->seg_tot);
             HIP_TRY(hipGetLastError());
+            CHECK(s->stage_end());
         }
+        CHECK(s->stage_begin(kStFill));   // the fill kernel alone
         if (s->use_skip)
             fill_kernel<C, true><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
-                s->rows, s->W, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
+                s->rows, s->W, s->Ws, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
                 s->skip_bin, (int)s->tiles.bin_major);
         else
             fill_kernel<C, false><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
-                s->rows, s->W, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
+                s->rows, s->W, s->Ws, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
                 nullptr, (int)s->tiles.bin_major);
         HIP_TRY(hipGetLastError());
+        CHECK(s->stage_end());
+        // ---- histogram finishing: dominant bins, prefix form, siblings ----
+        CHECK(s->stage_begin(kStDerive));
         if (s->use_skip) {
             default_bin_fixup_kernel<<<dim3(s->F, n_seg), 64, 0, st>>>(cur, lplan, s->skip_bin, s->seg_tot, C,
                                                                       s->F, s->B);

@@ -176,7 +176,7 @@ int cbh_session_read_approx(cbh_session* s, double* approx_out, uint64_t n_times
  * sums of HIP-event durations measured on the session stream. */
 typedef struct {
     double fill_ms;               /* histogram fill kernels */
-    double derive_ms;             /* sibling subtraction */
+    double derive_ms;             /* histogram finishing: dominant-bin rebuild, prefix form, siblings */
     double score_ms;              /* split scoring + argmax */
     double partition_ms;          /* leaf update + stable compaction */
     double leaf_ms;               /* leaf reduction + values */
