@@ -487,6 +487,14 @@ def test_config2_reduced_matches_oracle(layout, monkeypatch):
     _assert_same_fit(*_fit_both(d, 8))
 
 
+def test_config2_full_size_first_trees_match_oracle():
+    """Config 2 at its full 10M x 200 size: the first two trees (splits, leaf values,
+    approximant) against the oracle on 16 host threads; about a minute, most of it data
+    generation."""
+    d = datagen.config2()
+    _assert_same_fit(*_fit_both(d, 2, n_threads=16))
+
+
 @pytest.mark.parametrize("layout", ["bin", "feature"])
 @pytest.mark.parametrize("F,B,K", [(37, 17, 1), (5, 256, 1), (65, 33, 3), (33, 2, 1), (100, 255, 1)])
 def test_fill_layouts_ragged_shapes_match_oracle(layout, F, B, K, monkeypatch):
