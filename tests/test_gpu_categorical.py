@@ -83,18 +83,19 @@ def _config4_columns(d, perm):
     return dev
 
 
-@pytest.mark.parametrize("weights", ["device", "host"])
-def test_config4_all_ctr_reduced_matches_oracle(weights, monkeypatch):
-    """Config 4's reference-legal all-CTR variant at 200k rows (RMSE, Bernoulli 0.66, depth 6)
-    with the reference's CTR training semantics (model_size_reg weights with the phantom
-    count, leaves over the averaging-permutation columns): device CTR columns equal the
-    oracle's, then 6 trees equal the oracle's -- with the weights picked on the device from
-    the tabulated pow values, and with the per-level host step."""
+@pytest.mark.parametrize("weights,n_rows,iters", [("device", 200_000, 6), ("host", 200_000, 6),
+                                                  ("device", 2_000_000, 10)])
+def test_config4_all_ctr_matches_oracle(weights, n_rows, iters, monkeypatch):
+    """Config 4's reference-legal all-CTR variant (RMSE, Bernoulli 0.66, depth 6) with the
+    reference's CTR training semantics (model_size_reg weights with the phantom count, leaves
+    over the averaging-permutation columns): device CTR columns equal the oracle's, then the
+    trees equal the oracle's -- at 200k rows with the weights picked on the device from the
+    tabulated pow values and with the per-level host step, and at the full 2M rows."""
     if weights == "host":
         monkeypatch.setenv("CBH_CTR_WEIGHTS", "host")
     from catboost_rs_amd import datagen
     from tests.test_gpu_parity import _close
-    d = datagen.config4(n_rows=200_000)
+    d = datagen.config4(n_rows=n_rows)
     P = d["params"]
     n = d["target"].size
     two = cb.shuffled_indices(n, P["random_seed"], count=2)
@@ -110,11 +111,11 @@ def test_config4_all_ctr_reduced_matches_oracle(weights, monkeypatch):
     nb = np.concatenate([d["n_borders"], np.full(ctr.shape[0], P["ctr_border_count"], np.uint32)])
     kw = dict(loss="RMSE", depth=6, learning_rate=0.1, l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient",
               bootstrap_type="Bernoulli", subsample=0.66, boost_from_average=True, random_seed=0)
-    exp = O.train(bins, nb, d["target"], iterations=6, ctr=info, **kw)
+    exp = O.train(bins, nb, d["target"], iterations=iters, ctr=info, **kw)
     assert any(f >= d["bins"].shape[0] for t in exp["splits"] for f, _ in t), "no CTR split chosen"
     tr = cb.Trainer(bins, int(nb.max()) + 1, d["target"], real_folds=nb + 1, ctr=info, **kw)
     try:
-        splits, leaves = tr.fit(6)
+        splits, leaves = tr.fit(iters)
         approx = tr.approx()
     finally:
         tr.close()
@@ -146,7 +147,7 @@ def test_config4_one_hot_and_ctr_extension_matches_oracle():
     exp = O.train(bins, nb, d["target"], iterations=6, one_hot=flags, **kw)
     tr = cb.Trainer(bins, int(nb.max()) + 1, d["target"], real_folds=nb + 1, one_hot_flags=flags, **kw)
     try:
-        splits, leaves = tr.fit(6)
+        splits, leaves = tr.fit(iters)
         approx = tr.approx()
     finally:
         tr.close()

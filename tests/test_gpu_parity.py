@@ -532,6 +532,21 @@ def test_config5_shape_matches_oracle():
     _assert_same_fit(*_fit_both(d, 4))
 
 
+@pytest.mark.parametrize("loss", ["PairLogit", "PairLogitPairwise"])
+def test_config3_full_size_first_trees_match_oracle(loss):
+    """Config 3 at its full size (1M docs in 50k groups, ~500k pairs, 100 features): the
+    first two trees against the oracle."""
+    d = datagen.config3(loss=loss)
+    _assert_same_fit(*_fit_both(d, 2, n_threads=16))
+
+
+def test_config5_full_size_first_tree_matches_oracle():
+    """Config 5 at its full size (1M x 4096, 70% zeros, MultiClass K=10, depth 8): the first
+    tree against the oracle; about a minute, most of it data generation."""
+    d = datagen.config5()
+    _assert_same_fit(*_fit_both(d, 1, n_threads=16))
+
+
 # ------------------------------------------------------------------------------ model apply
 def test_apply_on_gpu_matches_oracle_and_upstream():
     """cbh_apply_oblivious: bit-equal to the oracle's predict_raw restatement on every
