@@ -147,7 +147,7 @@ def test_config4_one_hot_and_ctr_extension_matches_oracle():
     exp = O.train(bins, nb, d["target"], iterations=6, one_hot=flags, **kw)
     tr = cb.Trainer(bins, int(nb.max()) + 1, d["target"], real_folds=nb + 1, one_hot_flags=flags, **kw)
     try:
-        splits, leaves = tr.fit(iters)
+        splits, leaves = tr.fit(6)
         approx = tr.approx()
     finally:
         tr.close()
