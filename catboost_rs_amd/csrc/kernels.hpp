@@ -541,7 +541,9 @@ static __global__ __launch_bounds__(256) void hist_prefix_kernel(long long* __re
                                                                  const LevelPlan* __restrict__ plan,
                                                                  uint32_t n_built, uint32_t C, uint32_t F,
                                                                  uint32_t B,
-                                                                 const long long* __restrict__ parent) {
+                                                                 const long long* __restrict__ parent,
+                                                                 const uint32_t* __restrict__ skip_bin,
+                                                                 const long long* __restrict__ seg_tot) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint64_t row = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint64_t rows = (uint64_t)n_built * C * F;
@@ -568,10 +570,20 @@ static __global__ __launch_bounds__(256) void hist_prefix_kernel(long long* __re
         if (lane >= (uint32_t)o) incl += u;
     }
     const long long off = incl - run;
+    // a dominant bin the fill left out (its cell still 0) is rebuilt as the segment's channel
+    // total minus the other bins, i.e. every prefix from that bin on grows by it
+    long long dv = 0;
+    uint32_t d = B;
+    if (skip_bin) {
+        const uint32_t ch = rem / F, f = rem - ch * F;
+        d = skip_bin[f];
+        if (d < B) dv = seg_tot[(size_t)seg * C + ch] - __shfl(incl, 63, 64);
+    }
 #pragma unroll
     for (uint32_t e = 0; e < 4; ++e) {
         const uint32_t b = b0 + e;
-        if (e < E && b < B) h[b] = v[e] + off;
+        v[e] += off + (b >= d ? dv : 0);
+        if (e < E && b < B) h[b] = v[e];
     }
     if (!parent) return;
     // sibling of the built child: parent segment seg has children seg and seg + n_built
@@ -581,7 +593,7 @@ static __global__ __launch_bounds__(256) void hist_prefix_kernel(long long* __re
 #pragma unroll
     for (uint32_t e = 0; e < 4; ++e) {
         const uint32_t b = b0 + e;
-        if (e < E && b < B) sib[b] = pr[b] - (v[e] + off);
+        if (e < E && b < B) sib[b] = pr[b] - v[e];
     }
 }
 
@@ -590,7 +602,7 @@ static __global__ __launch_bounds__(256) void hist_prefix_kernel(long long* __re
 // (sparse columns: 70% exact zeros put 70% of the rows in one bin) makes the fill's LDS
 // atomics collide on one cell.  The fill leaves that bin out; the per-segment channel totals
 // are summed apart (seg_totals_kernel) and the bin is rebuilt as total - sum(other bins),
-// exact in int64 (default_bin_fixup_kernel).
+// exact in int64 (hist_prefix_kernel).
 // ---------------------------------------------------------------------------------
 constexpr int kMaxC = kMaxK + 1;
 
@@ -670,26 +682,6 @@ static __global__ __launch_bounds__(256) void seg_totals_kernel(const uint32_t* 
         if (acc[i] != 0) atomicAdd((unsigned long long*)tot + i, acc[i]);
 }
 
-// hist[slot][ch][f][skip] = tot[segment][ch] - sum of the other bins.  Grid (F, segments).
-static __global__ __launch_bounds__(64) void default_bin_fixup_kernel(long long* __restrict__ hist,
-                                                                      const LevelPlan* __restrict__ plan,
-                                                                      const uint32_t* __restrict__ skip_bin,
-                                                                      const long long* __restrict__ tot,
-                                                                      uint32_t C, uint32_t F, uint32_t B) {
-    const uint32_t f = blockIdx.x, seg = blockIdx.y;
-    const uint32_t d = skip_bin[f];
-    if (d >= B) return;
-    if (plan && seg >= plan->n_parent) return;
-    const uint32_t slot = plan ? plan->built[seg] : 0u;
-    for (uint32_t ch = 0; ch < C; ++ch) {
-        long long* h = hist + (((size_t)slot * C + ch) * F + f) * B;
-        unsigned long long part = 0;
-        for (uint32_t b = threadIdx.x; b < B; b += 64)
-            if (b != d) part += (unsigned long long)h[b];
-        part = wave_sum_u64(part);
-        if (threadIdx.x == 0) h[d] = tot[(size_t)seg * C + ch] - (long long)part;
-    }
-}
 
 // ---------------------------------------------------------------------------------
 // Split scoring.  One workgroup per feature, one thread per border; for every leaf the

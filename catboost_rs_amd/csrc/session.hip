@@ -1041,16 +1041,13 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         CHECK(s->stage_end());
         // ---- histogram finishing: dominant bins, prefix form, siblings ----
         CHECK(s->stage_begin(kStDerive));
-        if (s->use_skip) {
-            default_bin_fixup_kernel<<<dim3(s->F, n_seg), 64, 0, st>>>(cur, lplan, s->skip_bin, s->seg_tot, C,
-                                                                      s->F, s->B);
-            HIP_TRY(hipGetLastError());
-        }
-        {   // built children to prefix form over bins (the level's histograms stay in it), and
-            // their siblings = parent - built (levels >= 1)
+        {   // built children to prefix form over bins (the level's histograms stay in it), with
+            // their dominant bins rebuilt from the segment totals, and their siblings = parent -
+            // built (levels >= 1)
             const uint64_t rows = (uint64_t)n_seg * C * s->F;
-            hist_prefix_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(cur, lplan, n_seg, C, s->F, s->B,
-                                                                           level > 0 ? par : nullptr);
+            hist_prefix_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(
+                cur, lplan, n_seg, C, s->F, s->B, level > 0 ? par : nullptr, s->use_skip ? s->skip_bin : nullptr,
+                s->seg_tot);
             HIP_TRY(hipGetLastError());
         }
         CHECK(s->stage_end());
