@@ -18,10 +18,11 @@ for the stage breakdown and the fill roofline.
 
 Reported next to the GPU figure:
   * roofline of the dominant kernel (histogram fill): algorithmic bytes per launch
-    (V rows x (W*4 + 8*(K+1) + 4) + histogram bytes) / average launch time from HIP events
+    (V rows x (W*4 + S + 4) + histogram bytes, S = 8 bytes of packed statistics per row for the
+    packed fill, 8*(K+1) otherwise) / average launch time from HIP events
     recorded on the session stream, against MI355X's 8 TB/s; HBM traffic per launch from
     the copy-calibrated rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/;
-  * the fill's LDS-atomic rate against the measured scattered 64-bit LDS atomic cap;
+  * the fill's LDS-atomic rate against the measured conflict-free 64-bit LDS atomic cap;
   * cpu_baseline: the CPU restatement of the reference algorithm (oracle/) timed on the
     host cores for the first trees of the same data, with a check that its splits equal
     the GPU's.
@@ -51,14 +52,20 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def _profiled_traffic(config, n, F):
+def _profiled_traffic(config, n, F, kernel):
     """HBM bytes per fill launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, copy-calibrated)
-    for the default workload shape, read from the committed profile summary; None if absent."""
+    for the default workload shape, read from the committed profile summary of the same fill
+    kernel on the same bench command (its last 120 fill dispatches are the 20 profiled trees this
+    line's avg_launch_ms and algorithmic bytes come from); None if absent or of another kernel."""
     path = os.path.join(ROOT, "profiles", "fill_kernel_config2.md")
     if config != 2 or n != 10_000_000 or F != 200 or not os.path.exists(path):
         return None
-    m = re.search(r"mean per dispatch: fetch ([0-9.]+) GB write ([0-9.]+) GB", open(path).read())
-    return round((float(m.group(1)) + float(m.group(2))) * 1e9) if m else None
+    text = open(path).read()
+    k = re.search(r"^kernel: (\S+)", text, re.M)
+    m = re.search(r"mean per dispatch: fetch ([0-9.]+) GB write ([0-9.]+) GB", text)
+    if not k or k.group(1) != kernel or not m:
+        return None
+    return round((float(m.group(1)) + float(m.group(2))) * 1e9)
 
 
 def _lds_rates():
@@ -283,26 +290,26 @@ def main():
     log(f"fill: {st['fill_launches']} launches, avg {st['fill_ms'] / max(1, st['fill_launches']):.4f} ms, "
         f"{achieved:.1f} GB/s algorithmic")
 
-    # LDS-atomic roofline of the fill: every visited (row, feature) adds K+1 64-bit integer
-    # cells; the caps are the 64-bit LDS atomic rates measured on this GPU, scattered (random
-    # bins: the feature-major layout) and contiguous (the bin-major layout's pattern)
+    # LDS-atomic roofline of the fill: every visited (row, feature) adds one 64-bit LDS atomic
+    # (packed fill: both channels in one word) or K+1 (two-channel / channel-split fills); the
+    # cap is the contiguous (conflict-free) 64-bit LDS atomic rate measured on this GPU, the
+    # pattern the fills' rotated lane layouts reach
     K = kw["approx_dim"] if P["loss"] == "MultiClass" else 1
+    per_pair = 1 if st["fill_mode"] == 1 else K + 1
     lds = None
     rates = _lds_rates()
-    if "scattered_u64" in rates and fill_s > 0:
-        ach = st["fill_row_features"] * (K + 1) / fill_s
+    if "contiguous_u64" in rates and fill_s > 0:
+        ach = st["fill_row_features"] * per_pair / fill_s
         # with a dominant-bin skip (sparse columns) fewer atomics are issued than counted
         lds = {"achieved_lane_atomics_per_s": round(ach, 1),
+               "atomics_per_row_feature": per_pair,
                "counted_as": "all (row, feature) pairs" if not st["skip_features"] else
                f"all (row, feature) pairs; {st['skip_features']} of {F} features skip their dominant bin",
-               "cap_scattered_u64_per_s": rates["scattered_u64"],
-               "cap_contiguous_u64_per_s": rates.get("contiguous_u64"),
-               "frac_of_scattered_cap": round(ach / rates["scattered_u64"], 4)}
-        if rates.get("contiguous_u64"):
-            lds["frac_of_contiguous_cap"] = round(ach / rates["contiguous_u64"], 4)
-        log(f"fill LDS atomics: {ach:.3e}/s = {100 * ach / rates['scattered_u64']:.1f}% of the "
-            f"measured scattered-u64 cap {rates['scattered_u64']:.3e}/s, "
-            f"{100 * ach / rates.get('contiguous_u64', float('inf')):.1f}% of the contiguous-u64 cap")
+               "cap_contiguous_u64_per_s": rates["contiguous_u64"],
+               "frac_of_contiguous_cap": round(ach / rates["contiguous_u64"], 4)}
+        log(f"fill LDS atomics: {ach:.3e}/s ({per_pair} per row-feature) = "
+            f"{100 * ach / rates['contiguous_u64']:.1f}% of the measured conflict-free 64-bit cap "
+            f"{rates['contiguous_u64']:.3e}/s")
 
     cpu = None
     if not args.no_cpu and cpu_trees > 0:
@@ -323,6 +330,7 @@ def main():
         tr2.close()
         cpu["splits_match_gpu"] = bool(np.array_equal(first, exp["splits"]))
 
+    fill_kernel = {0: "fill_kernel", 1: "fill_packed_kernel", 2: "fill_split_kernel"}[st["fill_mode"]]
     names = {1: "config1: RMSE, no bootstrap, depth 6, 128 borders",
              2: "config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 borders",
              3: f"config3: {P['loss']}, groups of 20, ~10 pairs per group, depth 6, 254 borders",
@@ -341,6 +349,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u8 bins, int64 fixed-point sums, f64 scores",
+        "fill": {0: "two-channel 32-feature tiles", 1: f"packed 64-feature tiles ({st['fill_pack_bits']}-bit rows)",
+                 2: "channel-split 64-feature tiles"}[st["fill_mode"]],
         "data": f"synthetic (seeded; datagen.config{args.config})",
         "config": {"workload": names[args.config], "rows": n, "features": F, "depth": P["depth"],
                    "parallelism": "single GPU"},
@@ -349,9 +359,9 @@ def main():
         "stage_ms_per_tree": {k[:-3]: round(st[k] / prof_steps, 4) for k in stages},
         "profiled_trees": prof_steps,
         "ms_per_step_profiled_eager": round(1000.0 * prof_wall / prof_steps, 4),
-        "roofline": {"bound": "hbm", "kernel": "fill_kernel", "achieved": round(achieved, 2),
+        "roofline": {"bound": "hbm", "kernel": fill_kernel, "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": _profiled_traffic(args.config, n, F),
+                     "traffic": _profiled_traffic(args.config, n, F, fill_kernel),
                      "launches": st["fill_launches"],
                      "avg_launch_ms": round(st["fill_ms"] / max(1, st["fill_launches"]), 5),
                      "algorithmic_bytes_per_launch": round(st["fill_bytes"] / max(1, st["fill_launches"]))},

@@ -92,6 +92,29 @@ static __global__ void pack_rows_kernel(const uint8_t* __restrict__ cols, uint64
     }
 }
 
+// Tile-major packing for the 64-feature fills: tile t (words [16t, 16t + TW_t), TW_t = min(16,
+// W - 16t)) of row r at trows[n * 16t + r * TW_t + w], so a workgroup of a tile streams its rows
+// contiguously (64 bytes per row of a full tile).
+static __global__ void pack_tiles_kernel(const uint8_t* __restrict__ cols, uint64_t n, uint32_t F, uint32_t W,
+                                         uint32_t* __restrict__ trows) {
+    const uint64_t total = n * W;
+    for (uint64_t o = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
+         o += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t t = (uint32_t)(o / (n * 16u));
+        const uint32_t w0 = 16u * t;
+        const uint32_t TW = min(16u, W - w0);
+        const uint64_t rem = o - (uint64_t)n * w0;
+        const uint64_t r = rem / TW;
+        const uint32_t w = (uint32_t)(rem - r * TW) + w0;
+        uint32_t word = 0;
+        for (uint32_t k = 0; k < 4; ++k) {
+            const uint32_t f = 4 * w + k;
+            if (f < F) word |= (uint32_t)cols[(size_t)f * n + r] << (8 * k);
+        }
+        trows[o] = word;
+    }
+}
+
 // ---------------------------------------------------------------------------------
 // Derivatives (crates/cb-compute/src/loss.rs:35-80, 424-486).
 // ---------------------------------------------------------------------------------
@@ -245,50 +268,78 @@ static __global__ __launch_bounds__(256) void prepare_kernel(
         const double sw = ctrl ? hw * s : 0.0;       // score_weights (:7728)
         sstat[i * C + K] = sw;
         leaf[i] = sw == 0.0 ? (uint16_t)0x8000u : (uint16_t)0;
-        acc[kScoreDer] += (unsigned long long)ceil(mx_sd * bscale);
-        acc[kScoreW] += (unsigned long long)ceil(fabs(sw) * bscale);
+        const unsigned long long qsd = (unsigned long long)ceil(mx_sd * bscale);
+        const unsigned long long qsw = (unsigned long long)ceil(fabs(sw) * bscale);
+        acc[kScoreDer] += qsd;
+        acc[kScoreW] += qsw;
         acc[kLeafDer] += (unsigned long long)ceil(mx_ld * bscale);
         acc[kLeafW] += (unsigned long long)ceil(h_leaf * bscale);
         acc[4] += sw != 0.0;
+        acc[5] = qsd > acc[5] ? qsd : acc[5];   // per-row maxima (the packed fill's scales)
+        acc[6] = qsw > acc[6] ? qsw : acc[6];
     }
     const uint32_t wave = threadIdx.x >> 6;
 #pragma unroll
     for (int k = 0; k < kPartials; ++k) {
-        const unsigned long long v = wave_sum_u64(acc[k]);
+        unsigned long long v = acc[k];
+        if (k == 5 || k == 6) {
+            for (int o = 32; o > 0; o >>= 1) {
+                const unsigned long long u = __shfl_xor(v, o, 64);
+                v = u > v ? u : v;
+            }
+        } else {
+            v = wave_sum_u64(v);
+        }
         if (lane_id() == 0) red[wave][k] = v;
     }
     __syncthreads();
     if (threadIdx.x < kPartials) {
         unsigned long long v = 0;
-        for (int w = 0; w < 4; ++w) v += red[w][threadIdx.x];
+        const bool mx = threadIdx.x == 5 || threadIdx.x == 6;
+        for (int w = 0; w < 4; ++w) {
+            const unsigned long long u = red[w][threadIdx.x];
+            v = mx ? (u > v ? u : v) : v + u;
+        }
         partials[(size_t)blockIdx.x * kPartials + threadIdx.x] = v;
     }
 }
 
 // Sum the per-block partials (integers: exact in any order) and pick S per slot so that
-// 2^S * sum|v| <= 2^61: no partial sum of rounded values can overflow int64.
+// 2^S * sum|v| <= 2^61: no partial sum of rounded values can overflow int64.  With
+// pack_bits > 0 the two score slots instead take S = pack_bits - e for the largest row
+// bound M < 2^e, so every rounded row value fits pack_bits bits (|q| <= 2^pack_bits): the
+// packed fill's 32-bit fields.
 static __global__ __launch_bounds__(256) void scales_kernel(const unsigned long long* __restrict__ partials,
                                                            uint32_t n_blocks, Bounds* __restrict__ b,
-                                                           Scales* __restrict__ sc) {
-    __shared__ unsigned long long red[256][5];
-    unsigned long long acc[5] = {0, 0, 0, 0, 0};
-    for (uint32_t i = threadIdx.x; i < n_blocks; i += blockDim.x)
+                                                           Scales* __restrict__ sc, int pack_bits) {
+    __shared__ unsigned long long red[256][7];
+    unsigned long long acc[7] = {0, 0, 0, 0, 0, 0, 0};
+    for (uint32_t i = threadIdx.x; i < n_blocks; i += blockDim.x) {
         for (int k = 0; k < 5; ++k) acc[k] += partials[(size_t)i * kPartials + k];
-    for (int k = 0; k < 5; ++k) red[threadIdx.x][k] = acc[k];
+        for (int k = 5; k < 7; ++k) {
+            const unsigned long long u = partials[(size_t)i * kPartials + k];
+            acc[k] = u > acc[k] ? u : acc[k];
+        }
+    }
+    for (int k = 0; k < 7; ++k) red[threadIdx.x][k] = acc[k];
     __syncthreads();
     if (threadIdx.x != 0) return;
-    for (int k = 0; k < 5; ++k) {
+    for (int k = 0; k < 7; ++k) {
         unsigned long long v = 0;
-        for (uint32_t tI = 0; tI < blockDim.x; ++tI) v += red[tI][k];
+        for (uint32_t tI = 0; tI < blockDim.x; ++tI) {
+            const unsigned long long u = red[tI][k];
+            v = k < 5 ? v + u : (u > v ? u : v);
+        }
         acc[k] = v;
     }
     for (int k = 0; k < kNumScales; ++k) b->sum_abs[k] = acc[k];
     b->sampled_rows = acc[4];
     for (int k = 0; k < kNumScales; ++k) {
-        const double bound = (double)acc[k] / (double)(1 << kBoundShift);
+        const bool packed = pack_bits > 0 && (k == kScoreDer || k == kScoreW);
+        const double bound = (double)acc[packed ? 5 + k : k] / (double)(1 << kBoundShift);
         int e = -20;
         if (bound > 0.0) frexp(bound, &e);   // bound < 2^e
-        int s = 61 - e;
+        int s = (packed ? pack_bits : 61) - e;
         if (s > 100) s = 100;
         sc->shift[k] = s;
         sc->mul[k] = ldexp(1.0, s);
@@ -527,6 +578,461 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
         }
         pos = end;
         ++seg;
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Packed fill (two score channels, K == 1).  A row's two fixed-point channels travel in one
+// 64-bit word, p = q_der * 2^32 + q_w (mod 2^64) with |q| <= 2^pack_bits, so ONE 64-bit LDS
+// atomic per (row, feature) adds both channels.  The 32-bit fields of an LDS cell stay
+// exactly decodable while the contributions that landed since the cell was last emptied sum
+// to less than 2^31 in magnitude.  Every thread owns kPackOwn cells of the tile and swaps
+// them with zero (ds_wrxchg) after the barrier that ends every block of at most
+// kPackIterRows rows; atomics of threads already in the next block may land before the swap,
+// so at most 2 * kPackIterRows rows fall between two swaps of a cell, and pack_bits =
+// 30 - log2(2 * kPackIterRows) keeps every field below 2^30.  The swapped words are decoded
+// into int64 registers, which flush to the level histogram at segment ends.  Every sum stays
+// an exact integer (order-free, reproducible); only the per-row quantization step is coarser
+// than the two-atomic fill's (2^-pack_bits of the largest row instead of 2^-61 of the sum).
+//
+// Tiles are 64 features (16 words): a workgroup reads one aligned 64-byte sector of every
+// 256-byte padded row it visits, so no two tiles share a sector and the gathers of the deeper
+// levels fetch no bytes they do not use.  LDS layout [bin][64] (stride 64 whatever the tile
+// width): a wave covers 4 rows x 16 words; the lane of word w of row r visits the bytes of its
+// word starting at byte (w / 4 + r) mod 4, so every 16 consecutive lanes of an atomic
+// instruction touch 16 distinct features mod 16 (32 lanes: 32 distinct mod 32), i.e. distinct
+// bank pairs -- the conflict-free rate whatever the bins.
+// ---------------------------------------------------------------------------------
+constexpr uint32_t kPackTileWords = 16;
+constexpr uint32_t kPackStride = 64;        // LDS cells per bin row
+constexpr uint32_t kPackThreads = 1024;     // 16 waves, one workgroup per CU
+constexpr uint32_t kPackIterRows = 1024;    // rows of the workgroup per block (between two swaps)
+constexpr int kPackOwn = 16;                // cells per thread: 64 x 256 / 1024
+constexpr int kPackBitsDefault = 19;        // 2 * 1024 * 2^19 = 2^30 < 2^31
+constexpr int kPackHalf = 8;                // passes per half block of a full tile (64 rows each)
+constexpr int kPackRowsPart = 8;            // rows in flight per lane, a partial last tile
+constexpr size_t kPackStageBytes = (kPackThreads / 64) * 128 * (sizeof(unsigned long long) + sizeof(uint32_t));
+
+__device__ __forceinline__ void unpack_add(unsigned long long v, long long& acc_d, long long& acc_w) {
+    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    acc_w += (long long)(int32_t)lo;                 // weight field, sign-extended
+    acc_d += (long long)(int32_t)(hi + (lo >> 31));  // der field: undo the borrow of a negative weight
+}
+
+// Level histogram flush of one channel: every thread stages its registers into the cells it
+// owns, then the workgroup walks the tile 8 features x 8 bins per wave (64-byte runs of bins in
+// the global histogram) with integer global atomics.
+__device__ __forceinline__ void packed_flush_channel(unsigned long long* __restrict__ pk, const long long* acc,
+                                                    uint32_t TF, uint32_t B, uint32_t F, uint32_t f0,
+                                                    long long* __restrict__ dst_plane /* hist + ((slot*C+ch)*F)*B */) {
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kPackOwn; ++k) {
+        const uint32_t i = threadIdx.x + (uint32_t)k * kPackThreads;
+        if (i < kPackStride * B) pk[i] = (unsigned long long)acc[k];
+    }
+    __syncthreads();
+    const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
+    const uint32_t vcells = nfb * nbb * 64;
+    for (uint32_t i = threadIdx.x; i < vcells; i += kPackThreads) {
+        const uint32_t l = i & 63u, j = i >> 6;
+        const uint32_t f = (j / nbb) * 8 + (l >> 3), bin = (j % nbb) * 8 + (l & 7u);
+        if (f >= TF || bin >= B) continue;
+        const unsigned long long v = pk[bin * kPackStride + f];
+        if (v != 0) atomicAdd((unsigned long long*)dst_plane + ((size_t)(f0 + f) * B + bin), v);
+    }
+}
+
+// The four byte visits of one row's word: rotated once so step k reads byte k, cell column
+// byte k of offs (the rotation spreads the lanes of an instruction over distinct bank pairs).
+__device__ __forceinline__ void packed_row_atomics(unsigned long long* __restrict__ pk, uint32_t word, uint32_t rot,
+                                                   uint32_t offs, unsigned long long st) {
+    const uint32_t wr = __builtin_amdgcn_alignbyte(word, word, rot);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        atomicAdd(pk + ((wr >> (8 * k)) & 0xFFu) * kPackStride + ((offs >> (8 * k)) & 0xFFu), st);
+}
+
+// A row word at a 32-bit byte offset from a workgroup-uniform base (one address register per
+// load: the SGPR-base form of global loads).  The session keeps the packed rows under 4 GiB for
+// the 64-feature fills.
+__device__ __forceinline__ uint32_t ldw(const char* __restrict__ base, uint32_t off) {
+    return *(const uint32_t*)(base + off);
+}
+
+// Swap the cells a thread owns with zero and add their decoded fields to its registers.
+// The cells of thread t are t + k * kPackThreads for k < own_n (a thread's column t % 64 is the
+// same for all k; a column >= TF is never touched and not swapped).
+__device__ __forceinline__ void packed_swap(unsigned long long* __restrict__ pk, uint32_t own_n,
+                                            long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
+    unsigned long long* c = pk + threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < kPackOwn; ++k)
+        if ((uint32_t)k < own_n) unpack_add(atomicExch(c + (uint32_t)k * kPackThreads, 0ull), acc_d[k], acc_w[k]);
+}
+
+// The rows [pos, end) of a FULL tile (16 words: 16 lanes per row, 4 rows per wave, passes of 64
+// rows), in blocks of kPackIterRows rows, each block in two halves of kPackHalf passes.  Each
+// row's packed statistic (and, gathered, its row index) is loaded once per wave -- lane j of
+// wave w stages row 4w + (j & 3) of pass (j & 31) / 4 of half j / 32 into the wave's LDS slots --
+// and read back by the row's 16 lanes, so a lane holds only the words of its rows in registers.
+// Software pipeline: the staging loads of block j+1 are issued when block j starts, and the words
+// of a half of block j+1 right after that half of block j is consumed, so they are in flight
+// across the other half, the barrier and the swap.
+template <bool kGather>
+__device__ __forceinline__ void packed_range_full(unsigned long long* __restrict__ pk,
+                                                  unsigned long long* __restrict__ wst /* wave's 128 slots */,
+                                                  uint32_t* __restrict__ wix /* wave's 128 slots */,
+                                                  const char* __restrict__ rbase, uint32_t stride4, uint32_t wl4,
+                                                  const uint32_t* __restrict__ idx,
+                                                  const unsigned long long* __restrict__ sbase, uint32_t pos,
+                                                  uint32_t end, uint32_t r0, uint32_t rot, uint32_t offs,
+                                                  uint32_t swap_every, uint32_t own_n,
+                                                  long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
+    constexpr uint32_t rpp = kPackThreads / kPackTileWords;   // rows per pass
+    constexpr uint32_t half_rows = kPackHalf * rpp;           // rows per half block
+    constexpr uint32_t hs = 4u * kPackHalf;                   // a wave's rows (slots) per half
+    static_assert(hs == 32 && 2 * half_rows == kPackIterRows, "staging layout: one row per lane per block");
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    // lane j stages slot j & 31 of half j / 32 (slots 64.. hold half B)
+    const uint32_t h = lane >> 5, sl = lane & 31u;
+    const uint32_t srow = wave * 4u + (sl & 3u) + (sl >> 2) * rpp + h * half_rows;   // row in the block
+    const uint32_t slot = sl + 64u * h;
+    const uint32_t rr = r0 & 3u;                                                    // row of this lane in its wave
+    uint32_t base = pos;
+    uint32_t six;
+    unsigned long long ssv;
+    auto stage_load = [&](uint32_t bb) {
+        const uint32_t p = bb + srow;
+        const uint32_t pc = p < end ? p : bb;
+        six = kGather ? idx[pc] : pc;
+        ssv = sbase[pc];
+        if (p >= end) ssv = 0ull;   // rows past the range add nothing
+    };
+    auto row_of = [&](uint32_t bb, uint32_t u) {   // row of this lane's pass u (level 0)
+        const uint32_t p = bb + r0 + u * rpp;
+        return p < end ? p : bb;
+    };
+    uint32_t wA[kPackHalf], wB[kPackHalf];
+    stage_load(base);
+    wix[slot] = six;
+    wst[slot] = ssv;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < kPackHalf; ++u) {
+        wA[u] = ldw(rbase, (kGather ? wix[rr + 4u * u] : row_of(base, u)) * stride4 + wl4);
+        wB[u] = ldw(rbase, (kGather ? wix[64u + rr + 4u * u] : row_of(base, kPackHalf + u)) * stride4 + wl4);
+    }
+    uint32_t blk = 0;
+    for (;;) {   // workgroup-uniform
+        const uint32_t nb = base + kPackIterRows;
+        const bool more = nb < end;
+        if (more) stage_load(nb);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int u = 0; u < kPackHalf; ++u) {
+            const unsigned long long st = wst[rr + 4u * u];
+            if (st != 0ull) packed_row_atomics(pk, wA[u], rot, offs, st);   // zero: outside the sample or range
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (more) {
+            if (h == 0) {
+                wix[slot] = six;
+                wst[slot] = ssv;
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int u = 0; u < kPackHalf; ++u)
+                wA[u] = ldw(rbase, (kGather ? wix[rr + 4u * u] : row_of(nb, u)) * stride4 + wl4);
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int u = 0; u < kPackHalf; ++u) {
+            const unsigned long long st = wst[64u + rr + 4u * u];
+            if (st != 0ull) packed_row_atomics(pk, wB[u], rot, offs, st);
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (more) {
+            if (h == 1) {
+                wix[slot] = six;
+                wst[slot] = ssv;
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int u = 0; u < kPackHalf; ++u)
+                wB[u] = ldw(rbase, (kGather ? wix[64u + rr + 4u * u] : row_of(nb, kPackHalf + u)) * stride4 + wl4);
+        }
+        if (++blk >= swap_every || !more) {
+            blk = 0;
+            __syncthreads();
+            packed_swap(pk, own_n, acc_d, acc_w);
+        }
+        if (!more) break;
+        base = nb;
+    }
+}
+
+// One block of at most kPackIterRows rows of a partial tile (TW < 16 words): per-lane loads.
+template <bool kGather>
+__device__ __forceinline__ void packed_block_part(unsigned long long* __restrict__ pk,
+                                                  const char* __restrict__ rbase, uint32_t stride4, uint32_t wl4,
+                                                  const uint32_t* __restrict__ idx,
+                                                  const unsigned long long* __restrict__ sbase, bool seq,
+                                                  uint32_t base, uint32_t end, uint32_t r0, uint32_t rpp,
+                                                  uint32_t un, bool lane_on, uint32_t rot, uint32_t offs) {
+    uint32_t pu[kPackRowsPart], vmask = 0;
+#pragma unroll
+    for (int u = 0; u < kPackRowsPart; ++u) {
+        const uint32_t p = base + r0 + (uint32_t)u * rpp;
+        const bool v = lane_on && (uint32_t)u < un && p < end;
+        vmask |= (v ? 1u : 0u) << u;
+        pu[u] = v ? p : base;
+    }
+    uint32_t doc[kPackRowsPart];
+#pragma unroll
+    for (int u = 0; u < kPackRowsPart; ++u) doc[u] = kGather ? idx[pu[u]] : pu[u];
+    unsigned long long st[kPackRowsPart];
+    uint32_t word[kPackRowsPart];
+#pragma unroll
+    for (int u = 0; u < kPackRowsPart; ++u) {
+        st[u] = sbase[(kGather && seq) ? pu[u] : doc[u]];
+        word[u] = ldw(rbase, doc[u] * stride4 + wl4);
+    }
+#pragma unroll
+    for (int u = 0; u < kPackRowsPart; ++u)
+        if (((vmask >> u) & 1u) && st[u] != 0ull) packed_row_atomics(pk, word[u], rot, offs, st[u]);
+}
+
+template <bool kGather>
+static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
+    const uint32_t* __restrict__ rows /* tile-major (pack_tiles_kernel) */, uint32_t W,
+    uint64_t n, const uint32_t* __restrict__ idx /* kGather: rows listed by the partition */,
+    const LevelPlan* __restrict__ plan, const unsigned long long* __restrict__ spack /* [n] */,
+    const unsigned long long* __restrict__ sseq /* nullable [V]: packed stats in idx order */,
+    uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
+    uint32_t swap_every /* blocks of rows between two swaps: 2 * swap_every * kPackIterRows * 2^pack_bits <= 2^30 */) {
+    constexpr uint32_t C = 2;
+    extern __shared__ unsigned long long pk[];   // [B][64] packed cells, then the waves' stat and index slots
+    const uint32_t b = blockIdx.x;
+    const uint32_t xcd = b & 7u, q = b >> 3;
+    const uint32_t t = q % n_tiles;
+    const uint32_t g = (q / n_tiles) * 8u + xcd;
+    const uint32_t w0 = t * kPackTileWords;
+    const uint32_t TW = min(kPackTileWords, W - w0);
+    const uint32_t f0 = 4u * w0;
+    const uint32_t TF = min(4u * TW, F - f0);
+    const bool full = TW == kPackTileWords && (!kGather || sseq != nullptr);   // workgroup-uniform
+    constexpr uint32_t kWaves = kPackThreads / 64;
+    unsigned long long* wst = pk + (size_t)kPackStride * B + (threadIdx.x >> 6) * 128u;
+    uint32_t* wix = (uint32_t*)(pk + (size_t)kPackStride * B + kWaves * 128u) + (threadIdx.x >> 6) * 128u;
+    for (uint32_t i = threadIdx.x; i < kPackStride * B; i += kPackThreads) pk[i] = 0ull;
+    // lanes: TW per row; partial tiles make un passes of rpp rows, at most kPackIterRows rows
+    const uint32_t rpp = min(kPackThreads / TW, kPackIterRows);
+    const uint32_t un = min((uint32_t)kPackRowsPart, kPackIterRows / rpp);
+    const uint32_t iter_rows = un * rpp;
+    const uint32_t r0 = threadIdx.x / TW;
+    const uint32_t wl = threadIdx.x - r0 * TW;
+    const bool lane_on = r0 < rpp;
+    // the word is rotated right by rot bytes once per row, so step k reads byte k of the rotated
+    // word: feature 4 * wl + ((k + rot) & 3).  rot = (wl / 4 + r) mod 4 makes the 16 lanes of a
+    // row hit 16 distinct features mod 16 and any two rows 32 distinct features mod 32, i.e.
+    // distinct bank pairs of the [bin][64] cells whatever the bins.  Bytes past the tile's last
+    // feature (a partial last word: zero padding) land in LDS columns >= TF, never read.
+    const uint32_t rot = ((wl >> 2) + (r0 & 1u)) & 3u;
+    uint32_t offs = 0;   // column of step k in byte k
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) offs |= (4u * wl + ((k + rot) & 3u)) << (8 * k);
+    long long acc_d[kPackOwn], acc_w[kPackOwn];
+#pragma unroll
+    for (int k = 0; k < kPackOwn; ++k) acc_d[k] = acc_w[k] = 0;
+    __syncthreads();
+    const uint32_t V = kGather ? plan->rows : (uint32_t)n;
+    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
+    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
+    const uint32_t n_seg = kGather ? plan->n_parent : 1u;
+    uint32_t seg = 0;
+    if (kGather)
+        while (seg + 1 < n_seg && plan->seg_begin[seg + 1] <= rb) ++seg;
+    // tile-major rows: this tile's slice starts at word n * w0, TW words per row
+    const char* rbase = (const char*)(rows + n * w0);
+    const uint32_t stride4 = 4u * TW, wl4 = 4u * wl;
+    const uint32_t own_n = ((threadIdx.x & (kPackStride - 1u)) < TF && threadIdx.x < kPackStride * B)
+                               ? (kPackStride * B - threadIdx.x + kPackThreads - 1) / kPackThreads
+                               : 0u;
+    const bool seq = kGather && sseq != nullptr;
+    const unsigned long long* sbase = seq ? sseq : spack;
+    uint32_t pos = rb;
+    while (pos < re) {
+        const uint32_t seg_end = (kGather && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
+        const uint32_t end = min(re, seg_end);
+        const uint32_t slot = kGather ? plan->built[seg] : 0u;
+        if (end > pos && full) {
+            packed_range_full<kGather>(pk, wst, wix, rbase, stride4, wl4, idx, sbase, pos, end, r0, rot, offs,
+                                       swap_every, own_n, acc_d, acc_w);
+        } else if (end > pos) {
+            uint32_t blk = 0;
+            for (uint32_t base = pos; base < end; base += iter_rows) {   // workgroup-uniform
+                packed_block_part<kGather>(pk, rbase, stride4, wl4, idx, sbase, seq, base, end, r0, rpp, un, lane_on,
+                                           rot, offs);
+                if (++blk < swap_every && base + iter_rows < end) continue;
+                blk = 0;
+                __syncthreads();
+                packed_swap(pk, own_n, acc_d, acc_w);
+            }
+        }
+        if (end > pos) {
+            // every contribution of the segment is in the registers now (the last swap follows
+            // the last barrier); flush both channels, then clear the cells and registers
+            long long* hd = hist + (size_t)slot * C * F * B;
+            packed_flush_channel(pk, acc_d, TF, B, F, f0, hd);
+            packed_flush_channel(pk, acc_w, TF, B, F, f0, hd + (size_t)F * B);
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kPackOwn; ++k) {
+                const uint32_t i = threadIdx.x + (uint32_t)k * kPackThreads;
+                if (i < kPackStride * B) pk[i] = 0ull;
+                acc_d[k] = acc_w[k] = 0;
+            }
+            __syncthreads();
+        }
+        pos = end;
+        ++seg;
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Channel-split fill (exact int64, any K).  One workgroup = (64-feature tile, channel, row
+// range): its LDS holds one channel of the tile, [bin][64] int64 (130 KB at 255 bins), and it
+// adds one 64-bit atomic per (row, feature) -- no packing, no periodic drains, no barrier
+// inside the row loop, so every lane keeps kSplitRows rows in flight.  The C channel
+// workgroups of a (tile, range) are adjacent blocks on one XCD and walk the same rows in the
+// same order at the same speed, so a row's 64-byte sector comes from HBM once and from L2 for
+// the other channels.  Statistics are channel-planar int64 ([C][n], and [C][V] in idx order
+// for the gathered levels): every workgroup reads 8 contiguous bytes per row.  Lane layout and
+// visit rotation as in the packed fill (conflict-free bank pairs).
+// ---------------------------------------------------------------------------------
+constexpr int kSplitRows = 16;
+
+template <bool kGather>
+static __global__ __launch_bounds__(1024) void fill_split_kernel(
+    const uint32_t* __restrict__ rows, uint32_t stride, uint32_t W, uint64_t n,
+    const uint32_t* __restrict__ idx, const LevelPlan* __restrict__ plan,
+    const long long* __restrict__ splanar /* [C][n] fixed point */,
+    const long long* __restrict__ sseqp /* nullable [C][n]: the idx rows' values in idx order */,
+    uint32_t C, uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist) {
+    extern __shared__ unsigned long long pk[];
+    const uint32_t b = blockIdx.x;
+    const uint32_t xcd = b & 7u, q = b >> 3;
+    const uint32_t c = q % C;
+    const uint32_t t = (q / C) % n_tiles;
+    const uint32_t g = (q / (C * n_tiles)) * 8u + xcd;
+    const uint32_t w0 = t * kPackTileWords;
+    const uint32_t TW = min(kPackTileWords, W - w0);
+    const uint32_t f0 = 4u * w0;
+    const uint32_t TF = min(4u * TW, F - f0);
+    for (uint32_t i = threadIdx.x; i < kPackStride * B; i += blockDim.x) pk[i] = 0ull;
+    __syncthreads();
+    const uint32_t rpp = blockDim.x / TW;
+    const uint32_t r0 = threadIdx.x / TW;
+    const uint32_t wl = threadIdx.x - r0 * TW;
+    const bool lane_on = r0 < rpp;
+    const uint32_t rot = ((wl >> 2) + (r0 & 1u)) & 3u;
+    uint32_t off[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) off[k] = 4u * wl + ((k + rot) & 3u);
+    const uint32_t V = kGather ? plan->rows : (uint32_t)n;
+    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
+    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
+    const uint32_t n_seg = kGather ? plan->n_parent : 1u;
+    uint32_t seg = 0;
+    if (kGather)
+        while (seg + 1 < n_seg && plan->seg_begin[seg + 1] <= rb) ++seg;
+    const uint32_t* rsrc = rows + w0 + wl;
+    const bool seq = kGather && sseqp != nullptr;
+    const long long* sbase = (seq ? sseqp : splanar) + (size_t)c * n;
+    uint32_t pos = rb;
+    while (pos < re) {
+        const uint32_t seg_end = (kGather && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
+        const uint32_t end = min(re, seg_end);
+        const uint32_t slot = kGather ? plan->built[seg] : 0u;
+        if (end > pos) {
+            if (lane_on) {
+                for (uint32_t p0 = pos + r0; p0 < end; p0 += kSplitRows * rpp) {
+                    uint32_t pu[kSplitRows], vmask = 0;
+#pragma unroll
+                    for (int u = 0; u < kSplitRows; ++u) {
+                        const uint32_t p = p0 + (uint32_t)u * rpp;
+                        const bool v = p < end;
+                        vmask |= (v ? 1u : 0u) << u;
+                        pu[u] = v ? p : p0;
+                    }
+                    uint32_t doc[kSplitRows];
+#pragma unroll
+                    for (int u = 0; u < kSplitRows; ++u) doc[u] = kGather ? idx[pu[u]] : pu[u];
+                    long long st[kSplitRows];
+                    uint32_t word[kSplitRows];
+#pragma unroll
+                    for (int u = 0; u < kSplitRows; ++u) {
+                        st[u] = sbase[seq ? pu[u] : doc[u]];
+                        word[u] = rsrc[(size_t)doc[u] * stride];
+                    }
+#pragma unroll
+                    for (int u = 0; u < kSplitRows; ++u) {
+                        if (!((vmask >> u) & 1u) || st[u] == 0) continue;
+                        const uint32_t wr = __builtin_amdgcn_alignbyte(word[u], word[u], rot);
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            atomicAdd(pk + ((wr >> (8 * k)) & 0xFFu) * kPackStride + off[k],
+                                      (unsigned long long)st[u]);
+                    }
+                }
+            }
+            __syncthreads();
+            // flush: a wave takes 8 features x 8 bins (64-byte runs of bins in the histogram);
+            // each cell is read and cleared by one thread
+            long long* dst = hist + ((size_t)slot * C + c) * F * B;
+            const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
+            for (uint32_t i = threadIdx.x; i < nfb * nbb * 64; i += blockDim.x) {
+                const uint32_t l = i & 63u, j = i >> 6;
+                const uint32_t f = (j / nbb) * 8 + (l >> 3), bin = (j % nbb) * 8 + (l & 7u);
+                if (f >= TF || bin >= B) continue;
+                const uint32_t li = bin * kPackStride + f;
+                const unsigned long long v = pk[li];
+                if (v != 0) {
+                    atomicAdd((unsigned long long*)dst + ((size_t)(f0 + f) * B + bin), v);
+                    pk[li] = 0ull;
+                }
+            }
+            __syncthreads();
+        }
+        pos = end;
+        ++seg;
+    }
+}
+
+// Fixed-point score channels, channel-planar: sstat f64 [n][C] -> out int64 [C][n].
+template <int C>
+static __global__ void planar_stats_fixed_kernel(const double* __restrict__ sstat, uint64_t n,
+                                                 const Scales* __restrict__ sc, long long* __restrict__ out) {
+    const double md = sc->mul[kScoreDer], mw = sc->mul[kScoreW];
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch) out[(size_t)ch * n + i] = to_fixed(sstat[i * C + ch], ch == C - 1 ? mw : md);
+    }
+}
+
+// Score channels f64 [n][2] -> one packed word per row (der in the high field, weight in the
+// low field), each channel rounded with its own scale.
+static __global__ void pack_stats_fixed_kernel(const double* __restrict__ sstat, uint64_t n,
+                                               const Scales* __restrict__ sc,
+                                               unsigned long long* __restrict__ spack) {
+    const double md = sc->mul[kScoreDer], mw = sc->mul[kScoreW];
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const long long qd = to_fixed(sstat[2 * i], md);
+        const long long qw = to_fixed(sstat[2 * i + 1], mw);
+        spack[i] = ((unsigned long long)qd << 32) + (unsigned long long)qw;
     }
 }
 
@@ -984,10 +1490,15 @@ static __global__ void plan_finalize_kernel(const uint32_t* __restrict__ totals,
 // running offsets in its LDS slice (seeded from the scanned per-wave counts), so the loop
 // needs no block barrier: lanes read their group's offset, then one leader per group
 // advances it.
+// With sp_out given, the score words of every listed row are written beside its index
+// (sp_out[c][k] = sp_in[c][idx[k]] for the sp_ch planes of n words), so the next fill reads the
+// statistics of its rows in order instead of gathering them.
 static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __restrict__ leaf, uint64_t n,
                                                       uint32_t level, const uint32_t* __restrict__ cnt,
                                                       uint32_t n_waves, const LevelPlan* __restrict__ plan,
-                                                      uint32_t* __restrict__ idx) {
+                                                      uint32_t* __restrict__ idx,
+                                                      const unsigned long long* __restrict__ sp_in,
+                                                      unsigned long long* __restrict__ sp_out, uint32_t sp_ch) {
     __shared__ uint32_t run[4][kMaxLeaves / 2];
     __shared__ uint32_t built[kMaxLeaves / 2];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
@@ -1023,6 +1534,8 @@ static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __r
         const uint32_t rank = mbcnt64(mask);
         const uint32_t base = valid ? run[wave][key] : 0u;
         if (valid) idx[base + rank] = (uint32_t)i;
+        if (valid && sp_out)
+            for (uint32_t c = 0; c < sp_ch; ++c) sp_out[(size_t)c * n + base + rank] = sp_in[(size_t)c * n + i];
         if (valid && rank == 0) run[wave][key] = base + (uint32_t)__popcll(mask);
     }
 }

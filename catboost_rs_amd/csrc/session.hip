@@ -175,6 +175,16 @@ struct cbh_session {
     long long* seg_tot = nullptr;    // [kMaxLeaves / 2][C] channel totals per built segment
     bool use_skip = false;
     uint64_t n_skip = 0;
+
+    // 64-feature-tile fills: packed (K == 1: both score channels in one 64-bit word per row,
+    // one LDS atomic per (row, feature)) or channel-split (exact int64, one workgroup per
+    // channel of a tile)
+    bool packed = false, split = false;
+    int pack_bits = 0;
+    unsigned long long* spack = nullptr;   // packed: [n] words; split: [C][n] fixed-point planes
+    unsigned long long* sseq = nullptr;    // the same for the idx rows, in idx order
+    uint32_t pk_tiles = 0, pk_ranges = 8, pk_swap = 1;
+    size_t pk_lds = 0;
     JumpTabs jt() const {
         return JumpTabs{jump, jump + 1024, jump + 2048, jump + 2048 + n_coarse};
     }
@@ -242,7 +252,7 @@ struct cbh_session {
         dfree(partials);
         dfree(group_off); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st);
-        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot);
+        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq);
         dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_lv);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
         dfree(phantom_cnt); dfree(fweight); dfree(ctr_pow); dfree(ctr_group_dev); dfree(ctr_used_dev);
@@ -412,6 +422,27 @@ int session_alloc(cbh_session* s) {
     return CBH_OK;
 }
 
+// Row ranges per feature tile: (tile, range) workgroups for one or two rounds of the CUs'
+// resident slots, ranges a multiple of 8: one round when it fills >= 97% of the slots, else
+// the better of the two (config 2: 7 tiles on 256 one-workgroup CUs -> 1 round uses 224
+// slots, 2 rounds 504 of 512: fill 0.594 -> 0.563 ms per launch; more rounds add flushes and
+// lose).  CBH_FILL_WAVES overrides the workgroups per CU (a tuning knob).
+uint32_t pick_ranges(uint32_t cus, uint32_t per_cu, uint32_t nt, uint64_t n) {
+    const uint32_t cap = cus * std::max<uint32_t>(per_cu, 1);
+    auto ranges_for = [&](uint32_t slots) { return std::max<uint32_t>(8, slots / nt / 8 * 8); };
+    auto fill_frac = [&](uint32_t G, uint32_t rounds) { return (double)G * nt / ((double)rounds * cap); };
+    uint32_t G = ranges_for(cap);
+    const uint32_t G2 = ranges_for(2 * cap);
+    // (two rounds only with long ranges: each workgroup's flush is a fixed cost, and at 1M rows
+    // the second round's extra flushes lose: config 3 fill 0.060 -> 0.083 ms)
+    if (fill_frac(G, 1) < 0.97 && fill_frac(G2, 2) > fill_frac(G, 1) && n / G2 >= 65536) G = G2;
+    if (const char* e = std::getenv("CBH_FILL_WAVES")) {
+        const long m = std::strtol(e, nullptr, 10);
+        if (m >= 1 && m <= 16) G = ranges_for(cus * (uint32_t)m);
+    }
+    return G;
+}
+
 // Feature tiles of the fill: the widest LDS slot stride whose histogram fits the budget.
 int plan_tiles(cbh_session* s) {
     int lds_max = 0;
@@ -441,20 +472,66 @@ int plan_tiles(cbh_session* s) {
     int cus = 0;
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
     const uint32_t per_cu = std::max<uint32_t>(1, (uint32_t)((size_t)lds_max / s->tiles.lds_bytes));
-    const uint32_t cap = (uint32_t)cus * std::min<uint32_t>(per_cu, 2);
-    const uint32_t nt = s->tiles.n_tiles;
-    auto ranges_for = [&](uint32_t slots) { return std::max<uint32_t>(8, slots / nt / 8 * 8); };
-    auto fill_frac = [&](uint32_t G, uint32_t rounds) { return (double)G * nt / ((double)rounds * cap); };
-    uint32_t G = ranges_for(cap);
-    const uint32_t G2 = ranges_for(2 * cap);
-    // (two rounds only with long ranges: each workgroup's flush is a fixed cost, and at 1M rows
-    // the second round's extra flushes lose: config 3 fill 0.060 -> 0.083 ms)
-    if (fill_frac(G, 1) < 0.97 && fill_frac(G2, 2) > fill_frac(G, 1) && s->n / G2 >= 65536) G = G2;
-    if (const char* e = std::getenv("CBH_FILL_WAVES")) {   // tuning knob: workgroups per CU
-        const long m = std::strtol(e, nullptr, 10);
-        if (m >= 1 && m <= 16) G = ranges_for((uint32_t)cus * (uint32_t)m);
+    s->fill_ranges = pick_ranges((uint32_t)cus, std::min<uint32_t>(per_cu, 2), s->tiles.n_tiles, s->n);
+    return CBH_OK;
+}
+
+// Fill plan.  CBH_FILL=exact keeps the 32-feature two-channel fill, =packed the packed
+// 64-feature fill (K == 1), =split the channel-split 64-feature fill; the default picks the
+// channel-split fill from 2^20 rows on (where the fill's memory traffic dominates the tree).
+// None of the 64-feature fills handles the dominant-bin skip.
+int plan_fill_mode(cbh_session* s) {
+    s->packed = s->split = false;
+    const char* e = std::getenv("CBH_FILL");
+    const std::string v = e ? e : "";
+    if (v == "exact" || s->use_skip) return CBH_OK;
+    const bool want_packed = (v == "packed" || (v.empty() && s->n >= (1ull << 20))) && s->K == 1;
+    const bool want_split = v == "split";
+    if (!want_packed && !want_split) return CBH_OK;
+    // the packed fill addresses the row words of a tile by 32-bit byte offsets
+    if (want_packed && (uint64_t)s->n * kPackTileWords * 4u >= (1ull << 32)) return CBH_OK;
+    int lds_max = 0, cus = 0, per_cu = 0;
+    HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device));
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
+    const size_t lds = (size_t)kPackStride * s->B * sizeof(unsigned long long) + (want_packed ? kPackStageBytes : 0);
+    if (lds > (size_t)lds_max) return CBH_OK;
+    const void* kg = want_packed ? (const void*)fill_packed_kernel<true> : (const void*)fill_split_kernel<true>;
+    const void* kd = want_packed ? (const void*)fill_packed_kernel<false> : (const void*)fill_split_kernel<false>;
+    for (const void* k : {kg, kd})
+        HIP_TRY(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    const int threads = want_packed ? (int)kPackThreads : 1024;
+    HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kg, threads, lds));
+    if (per_cu < 1) return CBH_OK;
+    s->pk_lds = lds;
+    s->pk_tiles = (s->W + kPackTileWords - 1) / kPackTileWords;
+    const uint32_t planes = want_packed ? 1u : s->C;
+    s->pk_ranges = pick_ranges((uint32_t)cus, (uint32_t)per_cu, s->pk_tiles * planes, s->n);
+    if (want_packed) {
+        // CBH_PACK_SWAP (1, 2, 4, 8): blocks of rows between two swaps; each doubling costs
+        // one bit of a row's rounded value (a measurement knob).  Default 2: 18-bit rows, and
+        // half the swap work of 1 (config 2: fill 3.59 -> 3.40 ms per tree)
+        s->pk_swap = 2;
+        if (const char* sw = std::getenv("CBH_PACK_SWAP")) {
+            const long v2 = std::strtol(sw, nullptr, 10);
+            if (v2 == 1 || v2 == 2 || v2 == 4 || v2 == 8) s->pk_swap = (uint32_t)v2;
+        }
+        s->pack_bits = kPackBitsDefault - (s->pk_swap >= 2) - (s->pk_swap >= 4) - (s->pk_swap >= 8);
     }
-    s->fill_ranges = G;
+    CHECK(dalloc(&s->spack, (size_t)s->n * planes));
+    CHECK(dalloc(&s->sseq, (size_t)s->n * planes));
+    if (want_packed) {   // the packed fill reads tile-major rows: repack, free the row-major words
+        uint32_t* trows = nullptr;
+        CHECK(dalloc(&trows, (size_t)s->n * s->W));
+        pack_tiles_kernel<<<grid_for((uint64_t)s->n * s->W, 256), 256, 0, s->stream>>>(s->cols, s->n, s->F, s->W, trows);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess) {
+            dfree(trows);
+            return fail(CBH_ERR_DEVICE, "tile-major packing failed");
+        }
+        dfree(s->rows);
+        s->rows = trows;
+    }
+    s->packed = want_packed;
+    s->split = !want_packed;
     return CBH_OK;
 }
 
@@ -694,6 +771,7 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     pack_rows_kernel<<<grid_for((uint64_t)n * s->Ws, 256), 256, 0, s->stream>>>(s->cols, n, F, s->Ws, s->rows);
     HIP_TRY(hipGetLastError());
     CHECK(plan_skip_bins(s.get()));
+    CHECK(plan_fill_mode(s.get()));
     if (weight) HIP_TRY(hipMemcpy(s->weight, weight, sizeof(double) * n, hipMemcpyHostToDevice));
     // resident approximant seeded with the bias (DeviceTrainConfig::bias, runtime.rs:1276)
     std::vector<double> a0(std::min<uint64_t>(n * s->K, 1ull << 22), cfg->bias);
@@ -996,9 +1074,15 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         s->smp_dev, s->jt(), use_host_sample ? s->host_sample : nullptr, s->sstat, newton, s->partials,
         s->ranking ? s->ext_der : nullptr, s->ranking ? s->score_w : nullptr);
     HIP_TRY(hipGetLastError());
-    scales_kernel<<<1, 256, 0, st>>>(s->partials, pgrid, s->bounds, s->scales);
+    scales_kernel<<<1, 256, 0, st>>>(s->partials, pgrid, s->bounds, s->scales, s->packed ? s->pack_bits : 0);
     HIP_TRY(hipGetLastError());
-    quantize_stats_kernel<C><<<grid_for(n * C, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales);
+    if (s->packed)
+        pack_stats_fixed_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack);
+    else if (s->split)
+        planar_stats_fixed_kernel<C><<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales,
+                                                                           (long long*)s->spack);
+    else
+        quantize_stats_kernel<C><<<grid_for(n * C, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales);
     HIP_TRY(hipGetLastError());
     CHECK(s->stage_end());
 
@@ -1029,7 +1113,23 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             CHECK(s->stage_end());
         }
         CHECK(s->stage_begin(kStFill));   // the fill kernel alone
-        if (s->use_skip)
+        if (s->packed && level == 0)
+            fill_packed_kernel<false><<<s->pk_ranges * s->pk_tiles, kPackThreads, s->pk_lds, st>>>(
+                s->rows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_tiles, s->F, s->B,
+                s->pk_ranges, cur, s->pk_swap);
+        else if (s->packed)
+            fill_packed_kernel<true><<<s->pk_ranges * s->pk_tiles, kPackThreads, s->pk_lds, st>>>(
+                s->rows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_tiles, s->F, s->B,
+                s->pk_ranges, cur, s->pk_swap);
+        else if (s->split && level == 0)
+            fill_split_kernel<false><<<s->pk_ranges * s->pk_tiles * C, 1024, s->pk_lds, st>>>(
+                s->rows, s->Ws, s->W, n, nullptr, nullptr, (const long long*)s->spack, nullptr, C, s->pk_tiles,
+                s->F, s->B, s->pk_ranges, cur);
+        else if (s->split)
+            fill_split_kernel<true><<<s->pk_ranges * s->pk_tiles * C, 1024, s->pk_lds, st>>>(
+                s->rows, s->Ws, s->W, n, lidx, lplan, (const long long*)s->spack, (const long long*)s->sseq, C,
+                s->pk_tiles, s->F, s->B, s->pk_ranges, cur);
+        else if (s->use_skip)
             fill_kernel<C, true><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
                 s->rows, s->W, s->Ws, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
                 s->skip_bin, (int)s->tiles.bin_major);
@@ -1089,7 +1189,9 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             HIP_TRY(hipGetLastError());
             plan_finalize_kernel<<<1, 64, 0, st>>>(s->totals, level, s->plans + level);
             HIP_TRY(hipGetLastError());
-            compact_kernel<<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->plans + level, s->idx);
+            compact_kernel<<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->plans + level, s->idx,
+                                               (s->packed || s->split) ? s->spack : nullptr,
+                                               (s->packed || s->split) ? s->sseq : nullptr, s->split ? C : 1u);
             HIP_TRY(hipGetLastError());
         }
         CHECK(s->stage_end());
@@ -1296,7 +1398,7 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
         for (uint64_t i = 0; i < n; ++i) out->leaf_of[i] = lf[i] & 0x7FFFu;
     }
     // traffic accounting of the fill launches (algorithmic bytes per launch)
-    const double wbytes = 4.0 * s->W, sbytes = 8.0 * s->C;
+    const double wbytes = 4.0 * s->W, sbytes = s->packed ? 8.0 : 8.0 * s->C;   // split: 8 per channel
     const double per_leaf_bytes = (double)s->F * s->B * s->C * 8.0;
     for (uint32_t l = 0; l < s->depth; ++l) {
         const uint64_t V = l == 0 ? bounds.sampled_rows : plans[l - 1].rows;
@@ -1337,6 +1439,8 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
     if (!s || !out) return fail(CBH_ERR_INVALID_ARG, "null argument");
     *out = s->stats;
     out->skip_features = s->n_skip;
+    out->fill_mode = s->packed ? 1u : s->split ? 2u : 0u;
+    out->fill_pack_bits = s->packed ? s->pack_bits : 0;
     return CBH_OK;
 }
 

@@ -471,36 +471,79 @@ def _assert_same_fit(exp, splits, leaves, approx):
     _close(approx, exp["approx"])
 
 
-def test_config1_full_size_matches_oracle():
-    """Config 1 at its full size: RMSE, 100k x 50, 128 borders, depth 6, 100 trees."""
+@pytest.mark.parametrize("fill", ["auto", "packed"])
+def test_config1_full_size_matches_oracle(fill, monkeypatch):
+    """Config 1 at its full size: RMSE, 100k x 50, 128 borders, depth 6, 100 trees (the
+    default two-channel fill below 2^20 rows, and the packed fill forced)."""
+    if fill != "auto":
+        monkeypatch.setenv("CBH_FILL", fill)
     d = datagen.config1()
     _assert_same_fit(*_fit_both(d, d["params"]["iterations"]))
 
 
-@pytest.mark.parametrize("layout", ["auto", "bin", "feature"])
+@pytest.mark.parametrize("layout", ["auto", "bin", "feature", "packed", "split"])
 def test_config2_reduced_matches_oracle(layout, monkeypatch):
     """Config 2 shape (Logloss, 200 features, 254 borders, depth 6, Bayesian T=1) at 200k rows,
-    with each LDS histogram layout of the fill (bin-major is what 10M rows use)."""
-    if layout != "auto":
+    with each fill: the 32-feature two-channel fill in both LDS layouts (bin-major is what it
+    uses at 10M rows), the packed 64-feature fill (the default from 2^20 rows: one 64-bit atomic
+    carries both channels, 18-bit rounded rows) and the channel-split 64-feature fill."""
+    if layout in ("bin", "feature"):
+        monkeypatch.setenv("CBH_FILL", "exact")
         monkeypatch.setenv("CBH_FILL_LAYOUT", layout)
+    elif layout != "auto":
+        monkeypatch.setenv("CBH_FILL", layout)
     d = datagen.config2(n_rows=200_000)
     _assert_same_fit(*_fit_both(d, 8))
 
 
 def test_config2_full_size_first_trees_match_oracle():
-    """Config 2 at its full 10M x 200 size: the first two trees (splits, leaf values,
-    approximant) against the oracle on 16 host threads; about a minute, most of it data
-    generation."""
+    """Config 2 at its full 10M x 200 size (the packed fill): the first ten trees (splits, leaf
+    values, approximant) against the oracle on 16 host threads; about a minute, most of it data
+    generation and the oracle."""
     d = datagen.config2()
-    _assert_same_fit(*_fit_both(d, 2, n_threads=16))
+    _assert_same_fit(*_fit_both(d, 10, n_threads=16))
 
 
-@pytest.mark.parametrize("layout", ["bin", "feature"])
-@pytest.mark.parametrize("F,B,K", [(37, 17, 1), (5, 256, 1), (65, 33, 3), (33, 2, 1), (100, 255, 1)])
+def test_config2_full_size_packed_equals_two_channel_fill(monkeypatch):
+    """Config 2 at 10M x 200 over 40 trees: the packed fill (18-bit rounded rows in 32-bit
+    fields) chooses the same split at every level as the two-channel fill (61-bit exact sums),
+    so the trees, leaves and approximant are identical."""
+    d = datagen.config2()
+    P = dict(d["params"])
+    nb = d["n_borders"]
+    kw = dict(loss=P["loss"], depth=P["depth"], learning_rate=P["learning_rate"],
+              l2_leaf_reg=P["l2_leaf_reg"], score=P["score"], leaf_method=P["leaf_method"],
+              bootstrap_type=P["bootstrap_type"], boost_from_average=P["boost_from_average"],
+              bagging_temperature=P.get("bagging_temperature", 1.0), random_seed=P.get("random_seed", 0))
+    out = {}
+    for mode in ("exact", "packed"):
+        monkeypatch.setenv("CBH_FILL", mode)
+        tr = cb.Trainer(d["bins"], int(nb.max()) + 1, d["target"], real_folds=nb + 1, **kw)
+        try:
+            assert tr.stats()["fill_mode"] == (0 if mode == "exact" else 1)
+            sp, lv = tr.fit(40)
+            out[mode] = (sp, lv, tr.approx())
+        finally:
+            tr.close()
+    (s0, l0, a0), (s1, l1, a1) = out["exact"], out["packed"]
+    for it in range(40):
+        assert np.array_equal(s0[it], s1[it]), f"tree {it} splits differ"
+    assert np.array_equal(l0, l1)
+    assert np.array_equal(a0, a1)
+
+
+@pytest.mark.parametrize("layout", ["bin", "feature", "packed", "split"])
+@pytest.mark.parametrize("F,B,K", [(37, 17, 1), (5, 256, 1), (65, 33, 3), (33, 2, 1), (100, 255, 1),
+                                   (129, 256, 1), (64, 255, 1)])
 def test_fill_layouts_ragged_shapes_match_oracle(layout, F, B, K, monkeypatch):
-    """Both LDS layouts of the fill on ragged tiles: feature counts that leave a short last
-    tile or a partial word, 2 to 256 bins, K = 1 and a 3-class MultiClass (4 channels)."""
-    monkeypatch.setenv("CBH_FILL_LAYOUT", layout)
+    """Every fill on ragged tiles: feature counts that leave a short last tile or a partial
+    word, 2 to 256 bins, K = 1 and a 3-class MultiClass (4 channels; the packed fill is K = 1
+    only, so that case runs the two-channel fill)."""
+    if layout in ("bin", "feature"):
+        monkeypatch.setenv("CBH_FILL", "exact")
+        monkeypatch.setenv("CBH_FILL_LAYOUT", layout)
+    else:
+        monkeypatch.setenv("CBH_FILL", layout)
     g = np.random.default_rng(F * 1000 + B)
     n = 30_000
     nb = g.integers(1, B, F).astype(np.uint32)
@@ -519,9 +562,13 @@ def test_fill_layouts_ragged_shapes_match_oracle(layout, F, B, K, monkeypatch):
     _assert_same_fit(*_fit_both(d, 3))
 
 
-@pytest.mark.parametrize("loss", ["PairLogit", "PairLogitPairwise"])
-def test_config3_reduced_matches_oracle(loss):
-    """Config 3 shape (groups of 20, ~10 pairs per group, 100 features, 254 borders, depth 6)."""
+@pytest.mark.parametrize("loss,fill", [("PairLogit", "auto"), ("PairLogit", "packed"),
+                                       ("PairLogitPairwise", "auto")])
+def test_config3_reduced_matches_oracle(loss, fill, monkeypatch):
+    """Config 3 shape (groups of 20, ~10 pairs per group, 100 features, 254 borders, depth 6);
+    PairLogit also through the packed fill (its weight channel holds the pairwise weights)."""
+    if fill != "auto":
+        monkeypatch.setenv("CBH_FILL", fill)
     d = datagen.config3(n_rows=20_000 if loss == "PairLogit" else 4_000, loss=loss)
     _assert_same_fit(*_fit_both(d, 5))
 
