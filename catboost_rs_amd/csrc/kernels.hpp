@@ -610,13 +610,13 @@ constexpr uint32_t kPackIterRows = 1024;    // rows of the workgroup per block (
 constexpr int kPackOwn = 16;                // cells per thread: 64 x 256 / 1024
 constexpr int kPackBitsDefault = 19;        // 2 * 1024 * 2^19 = 2^30 < 2^31
 constexpr int kPackHalf = 8;                // passes per half block of a full tile (64 rows each)
-constexpr int kPackRowsPart = 8;            // rows in flight per lane, a partial last tile
-constexpr size_t kPackStageBytes = (kPackThreads / 64) * 128 * (sizeof(unsigned long long) + sizeof(uint32_t));
+constexpr int kPackRowsPart = 4;            // rows in flight per lane, a partial last tile
 
-__device__ __forceinline__ void unpack_add(unsigned long long v, long long& acc_d, long long& acc_w) {
-    const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-    acc_w += (long long)(int32_t)lo;                 // weight field, sign-extended
-    acc_d += (long long)(int32_t)(hi + (lo >> 31));  // der field: undo the borrow of a negative weight
+// Decode a swapped cell: no weight is negative (the session checks), so the weight field is a
+// sum of non-negative values below 2^31 that never borrows from the der field.
+__device__ __forceinline__ void unpack_add_nonneg(unsigned long long v, long long& acc_d, long long& acc_w) {
+    acc_w += (long long)(uint32_t)v;
+    acc_d += (long long)(int32_t)(uint32_t)(v >> 32);
 }
 
 // Level histogram flush of one channel: every thread stages its registers into the cells it
@@ -646,18 +646,31 @@ __device__ __forceinline__ void packed_flush_channel(unsigned long long* __restr
 // The four byte visits of one row's word: rotated once so step k reads byte k, cell column
 // byte k of offs (the rotation spreads the lanes of an instruction over distinct bank pairs).
 __device__ __forceinline__ void packed_row_atomics(unsigned long long* __restrict__ pk, uint32_t word, uint32_t rot,
-                                                   uint32_t offs, unsigned long long st) {
+                                                   const uint32_t* off8 /* byte offsets of the 4 columns */,
+                                                   unsigned long long st) {
     const uint32_t wr = __builtin_amdgcn_alignbyte(word, word, rot);
+    char* base = (char*)pk;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-        atomicAdd(pk + ((wr >> (8 * k)) & 0xFFu) * kPackStride + ((offs >> (8 * k)) & 0xFFu), st);
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t bin = __builtin_amdgcn_ubfe(wr, 8 * k, 8);
+        atomicAdd((unsigned long long*)(base + ((bin << 9) + off8[k])), st);   // [bin][64] x 8 bytes
+    }
 }
 
-// A row word at a 32-bit byte offset from a workgroup-uniform base (one address register per
-// load: the SGPR-base form of global loads).  The session keeps the packed rows under 4 GiB for
-// the 64-feature fills.
-__device__ __forceinline__ uint32_t ldw(const char* __restrict__ base, uint32_t off) {
-    return *(const uint32_t*)(base + off);
+// Buffer loads at 32-bit byte offsets from a workgroup-uniform resource (one address register
+// per load, no 64-bit address arithmetic; an offset past the resource's size reads 0).  The
+// session keeps each buffer of the packed fill under 4 GiB.
+constexpr int kBufWord3 = 0x00020000;   // gfx9 raw-buffer resource word 3
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                             (int)(uint32_t)(bytes < 0xFFFFFFFFull ? bytes : 0xFFFFFFFFull), kBufWord3);
+}
+__device__ __forceinline__ uint32_t ldw(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ unsigned long long ldq(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    return (unsigned long long)v[0] | ((unsigned long long)v[1] << 32);
 }
 
 // Swap the cells a thread owns with zero and add their decoded fields to its registers.
@@ -668,100 +681,84 @@ __device__ __forceinline__ void packed_swap(unsigned long long* __restrict__ pk,
     unsigned long long* c = pk + threadIdx.x;
 #pragma unroll
     for (int k = 0; k < kPackOwn; ++k)
-        if ((uint32_t)k < own_n) unpack_add(atomicExch(c + (uint32_t)k * kPackThreads, 0ull), acc_d[k], acc_w[k]);
+        if ((uint32_t)k < own_n) unpack_add_nonneg(atomicExch(c + (uint32_t)k * kPackThreads, 0ull), acc_d[k], acc_w[k]);
 }
 
-// The rows [pos, end) of a FULL tile (16 words: 16 lanes per row, 4 rows per wave, passes of 64
-// rows), in blocks of kPackIterRows rows, each block in two halves of kPackHalf passes.  Each
-// row's packed statistic (and, gathered, its row index) is loaded once per wave -- lane j of
-// wave w stages row 4w + (j & 3) of pass (j & 31) / 4 of half j / 32 into the wave's LDS slots --
-// and read back by the row's 16 lanes, so a lane holds only the words of its rows in registers.
-// Software pipeline: the staging loads of block j+1 are issued when block j starts, and the words
-// of a half of block j+1 right after that half of block j is consumed, so they are in flight
-// across the other half, the barrier and the swap.
+// Broadcast lane U of each 16-lane DPP row to the row (row_newbcast).
+template <int U>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + U, 0xF, 0xF, true);
+}
+template <int U>
+__device__ __forceinline__ unsigned long long row_bcast64(unsigned long long v) {
+    return (unsigned long long)row_bcast<U>((uint32_t)v) | ((unsigned long long)row_bcast<U>((uint32_t)(v >> 32)) << 32);
+}
+
+// The rows [pos, end) of a FULL tile (16 words: the 16 lanes of a row are one 16-lane DPP row of
+// the wave, 4 rows per wave, passes of 64 rows), in blocks of kPackIterRows = 16 passes, each
+// block in two halves of 8 passes.  Lane w of a DPP row loads the packed statistic (and,
+// gathered, the row index) of that row's pass w; pass u broadcasts lane u to the row's 16 lanes
+// (row_newbcast), so statistics and indices cost one load per row and no LDS round trip -- the
+// atomics of consecutive rows issue back to back.  Software pipeline: block j+1's statistics and
+// indices are loaded when block j starts, and the words of a half of block j+1 right after that
+// half of block j is consumed, so they are in flight across the other half, the barrier and the
+// swap.  Rows past the range carry a zero statistic (their atomics add nothing).
 template <bool kGather>
 __device__ __forceinline__ void packed_range_full(unsigned long long* __restrict__ pk,
-                                                  unsigned long long* __restrict__ wst /* wave's 128 slots */,
-                                                  uint32_t* __restrict__ wix /* wave's 128 slots */,
-                                                  const char* __restrict__ rbase, uint32_t stride4, uint32_t wl4,
-                                                  const uint32_t* __restrict__ idx,
-                                                  const unsigned long long* __restrict__ sbase, uint32_t pos,
-                                                  uint32_t end, uint32_t r0, uint32_t rot, uint32_t offs,
+                                                  __amdgpu_buffer_rsrc_t rbase, uint32_t stride4, uint32_t wl4,
+                                                  uint32_t wl, __amdgpu_buffer_rsrc_t idx,
+                                                  __amdgpu_buffer_rsrc_t sbase, uint32_t pos,
+                                                  uint32_t end, uint32_t r0, uint32_t rot, const uint32_t* off8,
                                                   uint32_t swap_every, uint32_t own_n,
                                                   long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
-    constexpr uint32_t rpp = kPackThreads / kPackTileWords;   // rows per pass
-    constexpr uint32_t half_rows = kPackHalf * rpp;           // rows per half block
-    constexpr uint32_t hs = 4u * kPackHalf;                   // a wave's rows (slots) per half
-    static_assert(hs == 32 && 2 * half_rows == kPackIterRows, "staging layout: one row per lane per block");
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    // lane j stages slot j & 31 of half j / 32 (slots 64.. hold half B)
-    const uint32_t h = lane >> 5, sl = lane & 31u;
-    const uint32_t srow = wave * 4u + (sl & 3u) + (sl >> 2) * rpp + h * half_rows;   // row in the block
-    const uint32_t slot = sl + 64u * h;
-    const uint32_t rr = r0 & 3u;                                                    // row of this lane in its wave
-    uint32_t base = pos;
-    uint32_t six;
-    unsigned long long ssv;
-    auto stage_load = [&](uint32_t bb) {
-        const uint32_t p = bb + srow;
+    constexpr uint32_t rpp = kPackThreads / kPackTileWords;   // 64 rows per pass
+    static_assert(2 * kPackHalf * rpp == kPackIterRows && kPackHalf == 8, "block layout");
+    uint32_t six, six_n = 0;
+    unsigned long long ssv, ssv_n = 0;
+    auto stage = [&](uint32_t bb, uint32_t& ix, unsigned long long& sv) {   // this lane: pass wl of block bb
+        const uint32_t p = bb + r0 + wl * rpp;
         const uint32_t pc = p < end ? p : bb;
-        six = kGather ? idx[pc] : pc;
-        ssv = sbase[pc];
-        if (p >= end) ssv = 0ull;   // rows past the range add nothing
+        ix = kGather ? ldw(idx, 4u * pc) : pc;
+        sv = ldq(sbase, 8u * pc);
+        if (p >= end) sv = 0ull;
     };
-    auto row_of = [&](uint32_t bb, uint32_t u) {   // row of this lane's pass u (level 0)
-        const uint32_t p = bb + r0 + u * rpp;
-        return p < end ? p : bb;
-    };
+    // row index of pass U (this lane's DPP row) from the staged indices of a block
+#define CBH_DOC(U, SIX) (kGather ? row_bcast<U>(SIX) : row_bcast<U>(SIX))
     uint32_t wA[kPackHalf], wB[kPackHalf];
-    stage_load(base);
-    wix[slot] = six;
-    wst[slot] = ssv;
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int u = 0; u < kPackHalf; ++u) {
-        wA[u] = ldw(rbase, (kGather ? wix[rr + 4u * u] : row_of(base, u)) * stride4 + wl4);
-        wB[u] = ldw(rbase, (kGather ? wix[64u + rr + 4u * u] : row_of(base, kPackHalf + u)) * stride4 + wl4);
-    }
+    uint32_t base = pos;
+    stage(base, six, ssv);
+#define CBH_LOADA(SIX)                                                                       \
+    wA[0] = ldw(rbase, (CBH_DOC(0, SIX) << 6) + wl4); wA[1] = ldw(rbase, (CBH_DOC(1, SIX) << 6) + wl4); \
+    wA[2] = ldw(rbase, (CBH_DOC(2, SIX) << 6) + wl4); wA[3] = ldw(rbase, (CBH_DOC(3, SIX) << 6) + wl4); \
+    wA[4] = ldw(rbase, (CBH_DOC(4, SIX) << 6) + wl4); wA[5] = ldw(rbase, (CBH_DOC(5, SIX) << 6) + wl4); \
+    wA[6] = ldw(rbase, (CBH_DOC(6, SIX) << 6) + wl4); wA[7] = ldw(rbase, (CBH_DOC(7, SIX) << 6) + wl4);
+#define CBH_LOADB(SIX)                                                                       \
+    wB[0] = ldw(rbase, (CBH_DOC(8, SIX) << 6) + wl4); wB[1] = ldw(rbase, (CBH_DOC(9, SIX) << 6) + wl4); \
+    wB[2] = ldw(rbase, (CBH_DOC(10, SIX) << 6) + wl4); wB[3] = ldw(rbase, (CBH_DOC(11, SIX) << 6) + wl4); \
+    wB[4] = ldw(rbase, (CBH_DOC(12, SIX) << 6) + wl4); wB[5] = ldw(rbase, (CBH_DOC(13, SIX) << 6) + wl4); \
+    wB[6] = ldw(rbase, (CBH_DOC(14, SIX) << 6) + wl4); wB[7] = ldw(rbase, (CBH_DOC(15, SIX) << 6) + wl4);
+#define CBH_ATOMS(W, U0, SSV)                                                                \
+    packed_row_atomics(pk, W[0], rot, off8, row_bcast64<U0 + 0>(SSV));                       \
+    packed_row_atomics(pk, W[1], rot, off8, row_bcast64<U0 + 1>(SSV));                       \
+    packed_row_atomics(pk, W[2], rot, off8, row_bcast64<U0 + 2>(SSV));                       \
+    packed_row_atomics(pk, W[3], rot, off8, row_bcast64<U0 + 3>(SSV));                       \
+    packed_row_atomics(pk, W[4], rot, off8, row_bcast64<U0 + 4>(SSV));                       \
+    packed_row_atomics(pk, W[5], rot, off8, row_bcast64<U0 + 5>(SSV));                       \
+    packed_row_atomics(pk, W[6], rot, off8, row_bcast64<U0 + 6>(SSV));                       \
+    packed_row_atomics(pk, W[7], rot, off8, row_bcast64<U0 + 7>(SSV));
+    CBH_LOADA(six)
+    CBH_LOADB(six)
     uint32_t blk = 0;
     for (;;) {   // workgroup-uniform
         const uint32_t nb = base + kPackIterRows;
         const bool more = nb < end;
-        if (more) stage_load(nb);
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int u = 0; u < kPackHalf; ++u) {
-            const unsigned long long st = wst[rr + 4u * u];
-            if (st != 0ull) packed_row_atomics(pk, wA[u], rot, offs, st);   // zero: outside the sample or range
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (more) {
-            if (h == 0) {
-                wix[slot] = six;
-                wst[slot] = ssv;
-            }
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int u = 0; u < kPackHalf; ++u)
-                wA[u] = ldw(rbase, (kGather ? wix[rr + 4u * u] : row_of(nb, u)) * stride4 + wl4);
-        }
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int u = 0; u < kPackHalf; ++u) {
-            const unsigned long long st = wst[64u + rr + 4u * u];
-            if (st != 0ull) packed_row_atomics(pk, wB[u], rot, offs, st);
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (more) {
-            if (h == 1) {
-                wix[slot] = six;
-                wst[slot] = ssv;
-            }
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int u = 0; u < kPackHalf; ++u)
-                wB[u] = ldw(rbase, (kGather ? wix[64u + rr + 4u * u] : row_of(nb, kPackHalf + u)) * stride4 + wl4);
-        }
+        if (more) stage(nb, six_n, ssv_n);
+        CBH_ATOMS(wA, 0, ssv)
+        if (more) { CBH_LOADA(six_n) }
+        CBH_ATOMS(wB, 8, ssv)
+        if (more) { CBH_LOADB(six_n) }
+        six = six_n;
+        ssv = ssv_n;
         if (++blk >= swap_every || !more) {
             blk = 0;
             __syncthreads();
@@ -770,16 +767,20 @@ __device__ __forceinline__ void packed_range_full(unsigned long long* __restrict
         if (!more) break;
         base = nb;
     }
+#undef CBH_ATOMS
+#undef CBH_LOADB
+#undef CBH_LOADA
+#undef CBH_DOC
 }
 
 // One block of at most kPackIterRows rows of a partial tile (TW < 16 words): per-lane loads.
 template <bool kGather>
 __device__ __forceinline__ void packed_block_part(unsigned long long* __restrict__ pk,
-                                                  const char* __restrict__ rbase, uint32_t stride4, uint32_t wl4,
-                                                  const uint32_t* __restrict__ idx,
-                                                  const unsigned long long* __restrict__ sbase, bool seq,
+                                                  __amdgpu_buffer_rsrc_t rbase, uint32_t stride4, uint32_t wl4,
+                                                  __amdgpu_buffer_rsrc_t idx,
+                                                  __amdgpu_buffer_rsrc_t sbase, bool seq,
                                                   uint32_t base, uint32_t end, uint32_t r0, uint32_t rpp,
-                                                  uint32_t un, bool lane_on, uint32_t rot, uint32_t offs) {
+                                                  uint32_t un, bool lane_on, uint32_t rot, const uint32_t* off8) {
     uint32_t pu[kPackRowsPart], vmask = 0;
 #pragma unroll
     for (int u = 0; u < kPackRowsPart; ++u) {
@@ -790,17 +791,17 @@ __device__ __forceinline__ void packed_block_part(unsigned long long* __restrict
     }
     uint32_t doc[kPackRowsPart];
 #pragma unroll
-    for (int u = 0; u < kPackRowsPart; ++u) doc[u] = kGather ? idx[pu[u]] : pu[u];
+    for (int u = 0; u < kPackRowsPart; ++u) doc[u] = kGather ? ldw(idx, 4u * pu[u]) : pu[u];
     unsigned long long st[kPackRowsPart];
     uint32_t word[kPackRowsPart];
 #pragma unroll
     for (int u = 0; u < kPackRowsPart; ++u) {
-        st[u] = sbase[(kGather && seq) ? pu[u] : doc[u]];
+        st[u] = ldq(sbase, 8u * ((kGather && seq) ? pu[u] : doc[u]));
         word[u] = ldw(rbase, doc[u] * stride4 + wl4);
     }
 #pragma unroll
     for (int u = 0; u < kPackRowsPart; ++u)
-        if (((vmask >> u) & 1u) && st[u] != 0ull) packed_row_atomics(pk, word[u], rot, offs, st[u]);
+        if (((vmask >> u) & 1u) && st[u] != 0ull) packed_row_atomics(pk, word[u], rot, off8, st[u]);
 }
 
 template <bool kGather>
@@ -812,7 +813,7 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
     uint32_t swap_every /* blocks of rows between two swaps: 2 * swap_every * kPackIterRows * 2^pack_bits <= 2^30 */) {
     constexpr uint32_t C = 2;
-    extern __shared__ unsigned long long pk[];   // [B][64] packed cells, then the waves' stat and index slots
+    extern __shared__ unsigned long long pk[];   // [B][64] packed cells
     const uint32_t b = blockIdx.x;
     const uint32_t xcd = b & 7u, q = b >> 3;
     const uint32_t t = q % n_tiles;
@@ -822,9 +823,6 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     const uint32_t f0 = 4u * w0;
     const uint32_t TF = min(4u * TW, F - f0);
     const bool full = TW == kPackTileWords && (!kGather || sseq != nullptr);   // workgroup-uniform
-    constexpr uint32_t kWaves = kPackThreads / 64;
-    unsigned long long* wst = pk + (size_t)kPackStride * B + (threadIdx.x >> 6) * 128u;
-    uint32_t* wix = (uint32_t*)(pk + (size_t)kPackStride * B + kWaves * 128u) + (threadIdx.x >> 6) * 128u;
     for (uint32_t i = threadIdx.x; i < kPackStride * B; i += kPackThreads) pk[i] = 0ull;
     // lanes: TW per row; partial tiles make un passes of rpp rows, at most kPackIterRows rows
     const uint32_t rpp = min(kPackThreads / TW, kPackIterRows);
@@ -839,9 +837,9 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     // distinct bank pairs of the [bin][64] cells whatever the bins.  Bytes past the tile's last
     // feature (a partial last word: zero padding) land in LDS columns >= TF, never read.
     const uint32_t rot = ((wl >> 2) + (r0 & 1u)) & 3u;
-    uint32_t offs = 0;   // column of step k in byte k
+    uint32_t off8[4];   // byte offset of the column of step k
 #pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) offs |= (4u * wl + ((k + rot) & 3u)) << (8 * k);
+    for (uint32_t k = 0; k < 4; ++k) off8[k] = 8u * (4u * wl + ((k + rot) & 3u));
     long long acc_d[kPackOwn], acc_w[kPackOwn];
 #pragma unroll
     for (int k = 0; k < kPackOwn; ++k) acc_d[k] = acc_w[k] = 0;
@@ -854,26 +852,27 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     if (kGather)
         while (seg + 1 < n_seg && plan->seg_begin[seg + 1] <= rb) ++seg;
     // tile-major rows: this tile's slice starts at word n * w0, TW words per row
-    const char* rbase = (const char*)(rows + n * w0);
+    const __amdgpu_buffer_rsrc_t rbase = make_rsrc(rows + n * w0, n * TW * 4u);
     const uint32_t stride4 = 4u * TW, wl4 = 4u * wl;
     const uint32_t own_n = ((threadIdx.x & (kPackStride - 1u)) < TF && threadIdx.x < kPackStride * B)
                                ? (kPackStride * B - threadIdx.x + kPackThreads - 1) / kPackThreads
                                : 0u;
     const bool seq = kGather && sseq != nullptr;
-    const unsigned long long* sbase = seq ? sseq : spack;
+    const __amdgpu_buffer_rsrc_t sbase = make_rsrc(seq ? sseq : spack, n * 8u);
+    const __amdgpu_buffer_rsrc_t ibase = make_rsrc(kGather ? (const void*)idx : (const void*)spack, kGather ? n * 4u : 0u);
     uint32_t pos = rb;
     while (pos < re) {
         const uint32_t seg_end = (kGather && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = kGather ? plan->built[seg] : 0u;
         if (end > pos && full) {
-            packed_range_full<kGather>(pk, wst, wix, rbase, stride4, wl4, idx, sbase, pos, end, r0, rot, offs,
+            packed_range_full<kGather>(pk, rbase, stride4, wl4, wl, ibase, sbase, pos, end, r0, rot, off8,
                                        swap_every, own_n, acc_d, acc_w);
         } else if (end > pos) {
             uint32_t blk = 0;
             for (uint32_t base = pos; base < end; base += iter_rows) {   // workgroup-uniform
-                packed_block_part<kGather>(pk, rbase, stride4, wl4, idx, sbase, seq, base, end, r0, rpp, un, lane_on,
-                                           rot, offs);
+                packed_block_part<kGather>(pk, rbase, stride4, wl4, ibase, sbase, seq, base, end, r0, rpp, un, lane_on,
+                                           rot, off8);
                 if (++blk < swap_every && base + iter_rows < end) continue;
                 blk = 0;
                 __syncthreads();

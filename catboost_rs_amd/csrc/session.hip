@@ -183,7 +183,9 @@ struct cbh_session {
     int pack_bits = 0;
     unsigned long long* spack = nullptr;   // packed: [n] words; split: [C][n] fixed-point planes
     unsigned long long* sseq = nullptr;    // the same for the idx rows, in idx order
+    uint32_t* trows = nullptr;             // packed fill: tile-major row words (pack_tiles_kernel)
     uint32_t pk_tiles = 0, pk_ranges = 8, pk_swap = 1;
+    bool pk_signed_w = false;              // some object or pair weight is negative
     size_t pk_lds = 0;
     JumpTabs jt() const {
         return JumpTabs{jump, jump + 1024, jump + 2048, jump + 2048 + n_coarse};
@@ -252,7 +254,7 @@ struct cbh_session {
         dfree(partials);
         dfree(group_off); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st);
-        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq);
+        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows);
         dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_lv);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
         dfree(phantom_cnt); dfree(fweight); dfree(ctr_pow); dfree(ctr_group_dev); dfree(ctr_used_dev);
@@ -485,15 +487,16 @@ int plan_fill_mode(cbh_session* s) {
     const char* e = std::getenv("CBH_FILL");
     const std::string v = e ? e : "";
     if (v == "exact" || s->use_skip) return CBH_OK;
-    const bool want_packed = (v == "packed" || (v.empty() && s->n >= (1ull << 20))) && s->K == 1;
+    // (the packed decode takes non-negative weights: a negative object weight keeps the other fills)
+    const bool want_packed = (v == "packed" || (v.empty() && s->n >= (1ull << 20))) && s->K == 1 && !s->pk_signed_w;
     const bool want_split = v == "split";
     if (!want_packed && !want_split) return CBH_OK;
-    // the packed fill addresses the row words of a tile by 32-bit byte offsets
+    // the packed fill addresses its buffers (a tile's row words, statistics) by 32-bit byte offsets
     if (want_packed && (uint64_t)s->n * kPackTileWords * 4u >= (1ull << 32)) return CBH_OK;
     int lds_max = 0, cus = 0, per_cu = 0;
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device));
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
-    const size_t lds = (size_t)kPackStride * s->B * sizeof(unsigned long long) + (want_packed ? kPackStageBytes : 0);
+    const size_t lds = (size_t)kPackStride * s->B * sizeof(unsigned long long);
     if (lds > (size_t)lds_max) return CBH_OK;
     const void* kg = want_packed ? (const void*)fill_packed_kernel<true> : (const void*)fill_split_kernel<true>;
     const void* kd = want_packed ? (const void*)fill_packed_kernel<false> : (const void*)fill_split_kernel<false>;
@@ -519,16 +522,12 @@ int plan_fill_mode(cbh_session* s) {
     }
     CHECK(dalloc(&s->spack, (size_t)s->n * planes));
     CHECK(dalloc(&s->sseq, (size_t)s->n * planes));
-    if (want_packed) {   // the packed fill reads tile-major rows: repack, free the row-major words
-        uint32_t* trows = nullptr;
-        CHECK(dalloc(&trows, (size_t)s->n * s->W));
-        pack_tiles_kernel<<<grid_for((uint64_t)s->n * s->W, 256), 256, 0, s->stream>>>(s->cols, s->n, s->F, s->W, trows);
-        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess) {
-            dfree(trows);
+    if (want_packed) {   // the packed fill reads tile-major rows (the row-major words stay for a fallback)
+        CHECK(dalloc(&s->trows, (size_t)s->n * s->W));
+        pack_tiles_kernel<<<grid_for((uint64_t)s->n * s->W, 256), 256, 0, s->stream>>>(s->cols, s->n, s->F, s->W,
+                                                                                     s->trows);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess)
             return fail(CBH_ERR_DEVICE, "tile-major packing failed");
-        }
-        dfree(s->rows);
-        s->rows = trows;
     }
     s->packed = want_packed;
     s->split = !want_packed;
@@ -771,8 +770,11 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     pack_rows_kernel<<<grid_for((uint64_t)n * s->Ws, 256), 256, 0, s->stream>>>(s->cols, n, F, s->Ws, s->rows);
     HIP_TRY(hipGetLastError());
     CHECK(plan_skip_bins(s.get()));
+    if (weight) {
+        HIP_TRY(hipMemcpy(s->weight, weight, sizeof(double) * n, hipMemcpyHostToDevice));
+        for (uint64_t i = 0; i < n && !s->pk_signed_w; ++i) s->pk_signed_w = weight[i] < 0.0;
+    }
     CHECK(plan_fill_mode(s.get()));
-    if (weight) HIP_TRY(hipMemcpy(s->weight, weight, sizeof(double) * n, hipMemcpyHostToDevice));
     // resident approximant seeded with the bias (DeviceTrainConfig::bias, runtime.rs:1276)
     std::vector<double> a0(std::min<uint64_t>(n * s->K, 1ull << 22), cfg->bias);
     for (uint64_t off = 0, total = n * s->K; off < total; off += a0.size()) {
@@ -831,10 +833,19 @@ int upload_pairs(cbh_session* s, const cbh_family* fam) {
     }
     std::vector<double> pw(n, 0.0);
     double sum_abs = 0.0;
+    bool neg = false;
     for (uint64_t j = 0; j < m; ++j) {
         pw[win[j]] += w[j];
         pw[los[j]] += w[j];
         sum_abs += std::fabs(w[j]);
+        neg |= w[j] < 0.0;
+    }
+    if (neg && s->packed) {   // the packed fill takes non-negative weights only: back to the two-channel fill
+        s->packed = false;
+        s->pk_signed_w = true;
+        for (auto& g : s->tree_graph)
+            if (g) (void)hipGraphExecDestroy(g);
+        s->tree_graph[0] = s->tree_graph[1] = nullptr;
     }
     int e = 0;
     if (sum_abs > 0.0) std::frexp(sum_abs, &e);
@@ -1115,11 +1126,11 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         CHECK(s->stage_begin(kStFill));   // the fill kernel alone
         if (s->packed && level == 0)
             fill_packed_kernel<false><<<s->pk_ranges * s->pk_tiles, kPackThreads, s->pk_lds, st>>>(
-                s->rows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_tiles, s->F, s->B,
+                s->trows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_tiles, s->F, s->B,
                 s->pk_ranges, cur, s->pk_swap);
         else if (s->packed)
             fill_packed_kernel<true><<<s->pk_ranges * s->pk_tiles, kPackThreads, s->pk_lds, st>>>(
-                s->rows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_tiles, s->F, s->B,
+                s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_tiles, s->F, s->B,
                 s->pk_ranges, cur, s->pk_swap);
         else if (s->split && level == 0)
             fill_split_kernel<false><<<s->pk_ranges * s->pk_tiles * C, 1024, s->pk_lds, st>>>(
