@@ -47,14 +47,14 @@ class Config(C.Structure):
                 ("sample_rate", C.c_float), ("bagging_temperature", C.c_float),
                 ("profile", C.c_int32), ("bias", C.c_double), ("rng_seed", C.c_uint64),
                 ("one_hot_flags", C.c_void_p), ("real_folds", C.c_void_p),
-                ("pairwise_non_diag_reg", C.c_double)]
+                ("pairwise_non_diag_reg", C.c_double), ("ctr", C.c_void_p)]
 
 
 class Family(C.Structure):
-    """FamilyTreeArgs::Pairwise (runtime.rs:925-934)."""
+    """FamilyTreeArgs::Pairwise / ::MultiOutput (runtime.rs:925-950)."""
     _fields_ = [("kind", C.c_int32), ("n_groups", C.c_uint32), ("group_offsets", C.c_void_p),
                 ("pair_winner", C.c_void_p), ("pair_loser", C.c_void_p), ("pair_weight", C.c_void_p),
-                ("n_pairs", C.c_uint64)]
+                ("n_pairs", C.c_uint64), ("approx_k", C.c_void_p), ("approx_dim", C.c_uint32)]
 
 
 class TreeSampling(C.Structure):
@@ -87,6 +87,27 @@ class CtrInfo(C.Structure):
                 ("cat_bucket_count", C.c_void_p), ("model_size_reg", C.c_double)]
 
 
+class DeviceCtrColumn(C.Structure):
+    """DeviceCtrColumn (runtime.rs:1104-1160)."""
+    _fields_ = [("n_members", C.c_uint32), ("member_bins", C.c_void_p), ("prior", C.c_double),
+                ("borders", C.c_void_p), ("n_borders", C.c_uint32), ("bucket_count", C.c_uint64),
+                ("weight_group", C.c_uint32), ("ctr_type", C.c_int32), ("target_border_idx", C.c_uint32),
+                ("projection_members", C.c_void_p), ("n_projection_members", C.c_uint32)]
+
+
+class DeviceCtrAveraging(C.Structure):
+    """DeviceCtrAveraging (runtime.rs:1212-1224)."""
+    _fields_ = [("permutation", C.c_void_p), ("target_class", C.c_void_p), ("columns", C.c_void_p),
+                ("n_columns", C.c_uint32)]
+
+
+class DeviceCtrConfig(C.Structure):
+    """DeviceCtrConfig (runtime.rs:1174-1200)."""
+    _fields_ = [("permutation", C.c_void_p), ("target_class", C.c_void_p), ("columns", C.c_void_p),
+                ("n_columns", C.c_uint32), ("averaging", C.c_void_p), ("n_cat", C.c_uint32),
+                ("cat_eligible_buckets", C.c_void_p), ("model_size_reg", C.c_double)]
+
+
 class TrainParams(C.Structure):
     _fields_ = [("loss", C.c_int32), ("score_function", C.c_int32), ("leaf_method", C.c_int32),
                 ("depth", C.c_int32), ("bootstrap_type", C.c_int32),
@@ -103,7 +124,8 @@ EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_apply_oblivious", "cbh_session_begin_raw", "cbh_select_borders", "cbh_quantize", "cbh_perfect_hash", "cbh_ctr_columns", "cbh_shuffled_indices",
            "cbh_version", "cbh_last_error", "cbt_open", "cbt_open_raw", "cbt_set_pairs", "cbt_step",
            "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close", "cbh_session_set_profile",
-           "cbt_set_profile", "cbh_session_set_ctr", "cbt_set_ctr"]
+           "cbt_set_profile", "cbh_session_set_ctr", "cbt_set_ctr", "cbh_session_read_ctr_bins",
+           "cbt_open_ctr"]
 
 _lib = None
 
@@ -157,6 +179,9 @@ def load(path: str = LIB_PATH):
     L.cbh_session_set_ctr.argtypes = [P, C.POINTER(CtrInfo)]
     L.cbt_set_ctr.argtypes = [P, C.POINTER(CtrInfo)]
     L.cbt_set_profile.argtypes = [P, C.c_int32]
+    L.cbh_session_read_ctr_bins.argtypes = [P, C.c_int32, P, C.c_uint64]
+    L.cbt_open_ctr.argtypes = [C.POINTER(TrainParams), P, C.c_uint64, C.c_uint32, C.c_uint32, P, P,
+                               C.POINTER(DeviceCtrConfig), P, P, C.POINTER(P)]
     L.cbt_close.argtypes = [P]
     L.cbt_close.restype = None
     _lib = L
@@ -345,6 +370,71 @@ def ctr_bin_columns(cat_keys, permutation, target_class, specs=(("Borders", 0.5)
     return np.concatenate(out, 0), np.array(counts, np.int64)
 
 
+def ctr_borders(prior, border_count=15):
+    """Border table of a CTR column as build_device_ctr_config makes it (boosting.rs:3620-3627):
+    next_down((k + 1) * norm / border_count - shift), shift/norm = calc_normalization(prior)."""
+    left, right = min(0.0, float(prior)), max(1.0, float(prior))
+    shift, norm = -left, right - left
+    k = np.arange(border_count, dtype=np.float64)
+    return np.nextafter((k + 1.0) * norm / border_count - shift, -np.inf)
+
+
+class DeviceCtr:
+    """A DeviceCtrConfig (``cbh_device_ctr_config``) and the host arrays it points into.
+
+    Built as cb-train's build_device_ctr_config does (boosting.rs:3590-3707) for simple
+    projections: one column per (categorical column, spec) in that order, each spec
+    (ctr_type, prior[, target_border_idx]); the border table of ``ctr_borders``; one weight
+    group per (ctr type, categorical column); the averaging half the same specs under the
+    averaging permutation.  ``cat_buckets`` [n_cat][n] are the first-seen buckets of the
+    CTR-eligible columns, which are also their member bins."""
+
+    def __init__(self, cat_buckets, permutation, averaging_permutation, target_class, specs,
+                 border_count=15, bucket_counts=None, model_size_reg=0.5):
+        cat = np.ascontiguousarray(cat_buckets, np.uint32)
+        n_cat, n = cat.shape
+        if bucket_counts is None:
+            bucket_counts = [int(c.max()) + 1 if n else 0 for c in cat]
+        keep = [cat]
+        self.perm = np.ascontiguousarray(permutation, np.uint32)
+        self.avg_perm = np.ascontiguousarray(averaging_permutation, np.uint32)
+        self.cls = np.ascontiguousarray(target_class, np.uint32)
+        keep += [self.perm, self.avg_perm, self.cls]
+        member_ptrs = [(C.c_void_p * 1)(cat[j].ctypes.data) for j in range(n_cat)]
+        proj = [np.array([j], np.uint32) for j in range(n_cat)]
+        keep += [member_ptrs, proj]
+        groups = {}
+        specs = [tuple(sp) for sp in specs]
+        m = n_cat * len(specs)
+        cols = (DeviceCtrColumn * m)()
+        k = 0
+        for j in range(n_cat):
+            for sp in specs:
+                ctype = CTR_TYPE[sp[0]]
+                b = ctr_borders(sp[1], border_count)
+                keep.append(b)
+                g = groups.setdefault((ctype, j), len(groups))
+                cols[k] = DeviceCtrColumn(1, C.cast(member_ptrs[j], C.c_void_p), float(sp[1]), _ptr(b),
+                                          b.shape[0], int(bucket_counts[j]), g, ctype,
+                                          sp[2] if len(sp) > 2 else 0, _ptr(proj[j]), 1)
+                k += 1
+        self.n_columns = m
+        self.columns = cols
+        self.averaging = DeviceCtrAveraging(_ptr(self.avg_perm), _ptr(self.cls), C.cast(cols, C.c_void_p), m)
+        cat_ptrs = (C.c_void_p * max(n_cat, 1))(*[cat[j].ctypes.data for j in range(n_cat)])
+        keep.append(cat_ptrs)
+        self.config = DeviceCtrConfig(_ptr(self.perm), _ptr(self.cls), C.cast(cols, C.c_void_p), m,
+                                      C.cast(C.pointer(self.averaging), C.c_void_p), n_cat,
+                                      C.cast(cat_ptrs, C.c_void_p), float(model_size_reg))
+        self._keep = keep
+
+    def ref(self):
+        return C.byref(self.config)
+
+    def as_pointer(self):
+        return C.cast(C.pointer(self.config), C.c_void_p)
+
+
 def _family_arrays(group_offsets, winner, loser, weight=None):
     go = np.ascontiguousarray(group_offsets, np.uint32)
     w = np.ascontiguousarray(winner, np.uint32)
@@ -374,9 +464,11 @@ class HipBackend:
                               bins_feature_major, weight, n, n_features, n_bins, learning_rate,
                               scaled_l2, *, approx_dim=1, bias=0.0, leaf_method="Gradient",
                               bootstrap_type="No", sample_from_host=False, profile=False,
-                              one_hot_flags=None, real_folds=None, pairwise_non_diag_reg=0.1) -> bool:
-        """Returns True when the session opened, False when the config is declined."""
-        self._keep = []
+                              one_hot_flags=None, real_folds=None, pairwise_non_diag_reg=0.1,
+                              ctr=None) -> bool:
+        """Returns True when the session opened, False when the config is declined.  ``ctr``: a
+        ``DeviceCtr`` (DeviceTrainConfig.ctr); its columns follow the n_features base features."""
+        self._keep = [ctr]
         oh = None if one_hot_flags is None else np.ascontiguousarray(one_hot_flags, np.uint8)
         rf = None if real_folds is None else np.ascontiguousarray(real_folds, np.uint32)
         self._keep += [oh, rf]
@@ -385,7 +477,8 @@ class HipBackend:
                      fold_count=fold_count, approx_dim=approx_dim, bootstrap_type=BOOT[bootstrap_type],
                      sample_from_host=int(sample_from_host), profile=int(profile), bias=bias,
                      one_hot_flags=_ptr(oh), real_folds=_ptr(rf),
-                     pairwise_non_diag_reg=pairwise_non_diag_reg)
+                     pairwise_non_diag_reg=pairwise_non_diag_reg,
+                     ctr=None if ctr is None else ctr.as_pointer())
         bins = np.ascontiguousarray(bins_feature_major)
         w = None if weight is None else np.ascontiguousarray(weight, np.float64)
         fn = load().cbh_session_begin_u8 if bins.dtype == np.uint8 else load().cbh_session_begin
@@ -397,7 +490,14 @@ class HipBackend:
             return False
         _check(rc)
         self.n, self.depth, self.K = n, depth, approx_dim
+        self.n_ctr = 0 if ctr is None else ctr.n_columns
         return True
+
+    def read_ctr_bins(self, averaging=False):
+        """The session's CTR bins [n_ctr][n] of the structure (or averaging) materialization."""
+        out = np.zeros((self.n_ctr, self.n), np.uint8)
+        _check(load().cbh_session_read_ctr_bins(self._s, int(bool(averaging)), _ptr(out), out.size))
+        return out
 
     def begin_device_training_raw(self, loss, depth, boosting_type_is_plain, fold_count, score_function,
                                   float_columns, feature_borders, weight, n, n_features, n_bins,
@@ -427,7 +527,8 @@ class HipBackend:
 
     def grow_tree_on_device(self, approx=None, target=None, sample=None, sampling=None,
                             want_leaf_of=False, family=None):
-        """``family`` = (group_offsets, winner, loser[, weight]) for a pair loss (first tree)."""
+        """``family`` = (group_offsets, winner, loser[, weight]) for a pair loss (first tree), or
+        dict(approx_k=[K][n], approx_dim=K) for FamilyTreeArgs::MultiOutput."""
         d = self.depth
         sf = np.zeros(d, np.uint32)
         sb = np.zeros(d, np.uint32)
@@ -440,7 +541,11 @@ class HipBackend:
         t = None if target is None else np.ascontiguousarray(target, np.float64)
         s = None if sample is None else np.ascontiguousarray(sample, np.float64)
         fam = None
-        if family is not None:
+        if isinstance(family, dict):
+            ak = np.ascontiguousarray(family["approx_k"], np.float64)
+            self._fam_keep = ak
+            fam = Family(kind=2, approx_k=_ptr(ak), approx_dim=int(family["approx_dim"]))
+        elif family is not None:
             arrs = _family_arrays(*family)
             self._fam_keep = arrs
             fam = _family(*arrs)
@@ -475,12 +580,14 @@ class Trainer:
                  subsample=0.66, bagging_temperature=1.0, boost_from_average=False, random_seed=0,
                  weight=None, approx_dim=1, profile=False, real_folds=None, one_hot_flags=None,
                  pairs=None, group_offsets=None, pairwise_non_diag_reg=0.1, float_columns=None,
-                 float_borders=None, ctr=None):
+                 float_borders=None, ctr=None, device_ctr=None):
         """``pairs`` = (winner, loser[, weight]) and ``group_offsets`` (CSR over row order) for
         PairLogit / PairLogitPairwise.  With ``bins_fm`` None the trainer opens over the raw
         float channel: ``float_columns`` f32 [F][n] and ``float_borders`` (F arrays).  ``ctr`` =
         dict(avg_bins [n_ctr][n], bucket_count, group, cat_buckets [n_cat][n], cat_bucket_count,
-        model_size_reg) when the last n_ctr columns are CTR columns (``cbt_set_ctr``)."""
+        model_size_reg) when the last n_ctr columns are CTR columns (``cbt_set_ctr``);
+        ``device_ctr`` = a ``DeviceCtr`` whose columns the session builds on the device and
+        appends after the base features (``cbt_open_ctr``)."""
         raw = bins_fm is None
         if raw:
             x, cp = _column_ptrs(float_columns)
@@ -509,6 +616,11 @@ class Trainer:
                 raise ValueError("the raw float channel takes its folds from the borders and has no one-hot columns")
             self._keep += (x, cp, bs, bp, nb)
             _check(load().cbt_open_raw(C.byref(p), cp, bp, _ptr(nb), n, F, _ptr(t), _ptr(w), C.byref(self._h)))
+        elif device_ctr is not None:
+            self._keep += (device_ctr,)
+            _check(load().cbt_open_ctr(C.byref(p), _ptr(self.bins), n, F, n_bins, _ptr(rf), _ptr(oh),
+                                       device_ctr.ref(), _ptr(t), _ptr(w), C.byref(self._h)))
+            self.F = F + device_ctr.n_columns
         else:
             _check(load().cbt_open(C.byref(p), _ptr(self.bins), n, F, n_bins, _ptr(rf), _ptr(oh), _ptr(t),
                                    _ptr(w), C.byref(self._h)))

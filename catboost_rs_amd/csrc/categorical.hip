@@ -161,6 +161,50 @@ __global__ void ctr_finalize_kernel(const uint32_t* __restrict__ skey, const uin
     }
 }
 
+// One CTR column of a session (build_ctr_cindex_columns, gpu_runtime/session.rs:262-360):
+// the spec's value of every object (as ctr_finalize_kernel) binarized by the column's own
+// border table, bin = the number of borders strictly below the value (binarize_ctr_kernel,
+// kernels/ctr_device.rs:399-413; a NaN border never counts).  The table sits in LDS.
+__global__ __launch_bounds__(256) void ctr_table_kernel(
+    const uint32_t* __restrict__ skey, const uint32_t* __restrict__ spos, const uint32_t* __restrict__ perm,
+    const uint32_t* __restrict__ excl, const uint32_t* __restrict__ start, const uint32_t* __restrict__ bsize,
+    const uint32_t* __restrict__ max_size, uint64_t n, int32_t type, uint32_t tbi, double prior,
+    const double* __restrict__ borders, uint32_t n_borders, uint8_t* __restrict__ bins) {
+    __shared__ double bd[256];
+    for (uint32_t j = threadIdx.x; j < n_borders; j += blockDim.x) bd[j] = borders[j];
+    __syncthreads();
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t obj = perm[spos[i]];
+        const uint32_t s = start[i];
+        const uint32_t total = (uint32_t)(i - s);
+        const uint32_t n1 = excl[i] - excl[s];
+        const uint32_t n0 = total - n1;
+        double num, den;
+        switch (type) {
+            case CBH_CTR_BUCKETS:
+                num = tbi == 0 ? (double)n0 : (tbi == 1 ? (double)n1 : 0.0);
+                den = (double)total;
+                break;
+            case CBH_CTR_BTMV:   // the f32 running sum of the classes
+                num = (double)(n1 < 16777216u ? (float)n1 : 16777216.0f);
+                den = (double)total;
+                break;
+            case CBH_CTR_COUNTER:
+                num = (double)bsize[skey[i]];
+                den = (double)*max_size;
+                break;
+            default:   // Borders
+                num = tbi == 0 ? (double)n1 : 0.0;
+                den = (double)total;
+                break;
+        }
+        const double v = (num + prior) / (den + 1.0);
+        uint32_t b = 0;
+        for (uint32_t j = 0; j < n_borders; ++j) b += v > bd[j] ? 1u : 0u;
+        bins[obj] = (uint8_t)b;
+    }
+}
+
 // ---- first-seen bins ----
 __global__ void head_flag_kernel(const uint32_t* __restrict__ skey, uint64_t n, uint32_t* __restrict__ flag) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
@@ -190,6 +234,89 @@ __global__ void assign_bins_kernel(const uint32_t* __restrict__ sidx, const uint
 }
 
 }  // namespace
+
+// The CTR bins of m session columns under one permutation, written to the device array
+// dst [m][n] on stream st (the caller has validated every input: a permutation of 0..n-1,
+// classes 0/1, member codes below n_buckets[c], at most 255 borders per column).  Columns
+// that share a member column share its sort: the sorted bucket segments do not depend on
+// the spec.
+int cbh_internal_ctr_bins(const cbh_device_ctr_column* cols, uint32_t m, const uint64_t* n_buckets,
+                          const uint32_t* permutation, const uint32_t* target_class, uint64_t n,
+                          uint8_t* dst, hipStream_t st) {
+    if (m == 0 || n == 0) return CBH_OK;
+    Buf<uint32_t> db, dperm, key, pos, skey, spos, c, head, excl, start, bsize, maxsz;
+    Buf<uint8_t> dcls;
+    Buf<double> dbord;
+    for (Buf<uint32_t>* b : {&db, &dperm, &key, &pos, &skey, &spos, &c, &head, &excl, &start})
+        CAT_TRY(b->alloc(n));
+    uint64_t nb_max = 1;
+    for (uint32_t k = 0; k < m; ++k) nb_max = std::max<uint64_t>(nb_max, n_buckets[k]);
+    CAT_TRY(bsize.alloc(nb_max));
+    CAT_TRY(maxsz.alloc(1));
+    CAT_TRY(dcls.alloc(n));
+    CAT_TRY(dbord.alloc(256));
+    {
+        std::vector<uint8_t> cls(n);
+        for (uint64_t i = 0; i < n; ++i) cls[i] = (uint8_t)target_class[i];
+        CAT_TRY(hipMemcpyAsync(dcls.p, cls.data(), n, hipMemcpyHostToDevice, st));
+        CAT_TRY(hipMemcpyAsync(dperm.p, permutation, sizeof(uint32_t) * n, hipMemcpyHostToDevice, st));
+        CAT_TRY(hipStreamSynchronize(st));
+    }
+    const int N = (int)n;
+    Buf<uint8_t> tmp;
+    size_t tb = 0;
+    std::vector<bool> done(m, false);
+    for (uint32_t c0 = 0; c0 < m; ++c0) {
+        if (done[c0]) continue;
+        const uint32_t* member = cols[c0].member_bins[0];
+        const uint64_t nb = n_buckets[c0];
+        const int kbits = (int)bits_for(nb ? nb - 1 : 0);
+        size_t t1 = 0, t2 = 0, t3 = 0, t4 = 0;
+        CAT_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, t1, key.p, skey.p, pos.p, spos.p, N, 0, kbits, st));
+        CAT_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, t2, c.p, excl.p, N, st));
+        CAT_TRY(hipcub::DeviceScan::InclusiveScan(nullptr, t3, head.p, start.p, hipcub::Max(), N, st));
+        CAT_TRY(hipcub::DeviceReduce::Max(nullptr, t4, bsize.p, maxsz.p, (int)nb, st));
+        const size_t need = std::max(std::max(t1, t2), std::max(t3, t4));
+        if (need > tb) {
+            CAT_TRY(hipStreamSynchronize(st));
+            if (tmp.p) (void)hipFree(tmp.p);
+            tmp.p = nullptr;
+            CAT_TRY(tmp.alloc(need));
+            tb = need;
+        }
+        CAT_TRY(hipMemcpyAsync(db.p, member, sizeof(uint32_t) * n, hipMemcpyHostToDevice, st));
+        gather_keys_kernel<<<grid_for(n), 256, 0, st>>>(db.p, dperm.p, n, key.p, pos.p);
+        CAT_TRY(hipGetLastError());
+        size_t tbx = tb;
+        CAT_TRY(hipcub::DeviceRadixSort::SortPairs(tmp.p, tbx, key.p, skey.p, pos.p, spos.p, N, 0, kbits, st));
+        segment_prep_kernel<<<grid_for(n), 256, 0, st>>>(skey.p, spos.p, dperm.p, dcls.p, n, c.p, head.p);
+        CAT_TRY(hipGetLastError());
+        tbx = tb;
+        CAT_TRY(hipcub::DeviceScan::ExclusiveSum(tmp.p, tbx, c.p, excl.p, N, st));
+        tbx = tb;
+        CAT_TRY(hipcub::DeviceScan::InclusiveScan(tmp.p, tbx, head.p, start.p, hipcub::Max(), N, st));
+        CAT_TRY(hipMemsetAsync(bsize.p, 0, sizeof(uint32_t) * nb, st));
+        segment_size_kernel<<<grid_for(n), 256, 0, st>>>(skey.p, start.p, n, bsize.p);
+        CAT_TRY(hipGetLastError());
+        tbx = tb;
+        CAT_TRY(hipcub::DeviceReduce::Max(tmp.p, tbx, bsize.p, maxsz.p, (int)nb, st));
+        for (uint32_t k = c0; k < m; ++k) {
+            if (done[k] || cols[k].member_bins[0] != member) continue;
+            done[k] = true;
+            const cbh_device_ctr_column& col = cols[k];
+            if (col.n_borders)
+                CAT_TRY(hipMemcpyAsync(dbord.p, col.borders, sizeof(double) * col.n_borders,
+                                       hipMemcpyHostToDevice, st));
+            ctr_table_kernel<<<grid_for(n), 256, 0, st>>>(skey.p, spos.p, dperm.p, excl.p, start.p, bsize.p,
+                                                          maxsz.p, n, col.ctr_type, col.target_border_idx,
+                                                          col.prior, dbord.p, col.n_borders, dst + (size_t)k * n);
+            CAT_TRY(hipGetLastError());
+            // the border table is reused by the next column: wait for this launch
+            CAT_TRY(hipStreamSynchronize(st));
+        }
+    }
+    return CBH_OK;
+}
 
 extern "C" {
 

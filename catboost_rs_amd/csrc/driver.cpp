@@ -62,8 +62,8 @@ namespace {
 // the device session over whichever input channel the caller has.
 template <typename Begin>
 int trainer_open(const cbt_params* p, uint64_t n, uint32_t F, const uint32_t* real_folds,
-                 const uint8_t* one_hot_flags, const double* target, const double* weight,
-                 cbt_trainer** out, Begin&& begin) {
+                 const uint8_t* one_hot_flags, const cbh_device_ctr_config* ctr, const double* target,
+                 const double* weight, cbt_trainer** out, Begin&& begin) {
     if (!p || !target || !out) return CBH_ERR_INVALID_ARG;
     *out = nullptr;
     bool any_one_hot = false;
@@ -112,9 +112,14 @@ int trainer_open(const cbt_params* p, uint64_t n, uint32_t F, const uint32_t* re
     cfg.one_hot_flags = one_hot_flags;
     cfg.real_folds = real_folds;
     cfg.pairwise_non_diag_reg = p->pairwise_non_diag_reg;
+    cfg.ctr = ctr;
     t->ranking = p->loss == CBH_LOSS_PAIRLOGIT || p->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE;
     int rc = begin(&cfg, t->p.learning_rate, scaled_l2, &t->s);
     if (rc != CBH_OK) return rc;
+    if (ctr) {   // the session appended the CTR columns after the F base features
+        t->F = F + ctr->n_columns;
+        t->ctr = true;
+    }
     t->rng = cbh::rng_from_seed(p->random_seed);
     t->draws_active = p->bootstrap_type != CBH_BOOT_NO;
     t->sf.resize(p->depth);
@@ -133,7 +138,7 @@ int cbt_open(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F
              const uint32_t* real_folds, const uint8_t* one_hot_flags, const double* target,
              const double* weight, cbt_trainer** out) {
     if (!bins_fm) return CBH_ERR_INVALID_ARG;
-    return trainer_open(p, n, F, real_folds, one_hot_flags, target, weight, out,
+    return trainer_open(p, n, F, real_folds, one_hot_flags, nullptr, target, weight, out,
                         [&](const cbh_config* cfg, double lr, double l2, cbh_session** s) {
                             return cbh_session_begin_u8(cfg, bins_fm, weight, n, F, n_bins, lr, l2, s);
                         });
@@ -145,10 +150,20 @@ int cbt_open_raw(const cbt_params* p, const float* const* columns, const double*
     if (!columns || !borders || !n_borders) return CBH_ERR_INVALID_ARG;
     uint32_t n_bins = 1;
     for (uint32_t f = 0; f < F; ++f) n_bins = std::max(n_bins, n_borders[f] + 1);
-    return trainer_open(p, n, F, nullptr, nullptr, target, weight, out,
+    return trainer_open(p, n, F, nullptr, nullptr, nullptr, target, weight, out,
                         [&](const cbh_config* cfg, double lr, double l2, cbh_session** s) {
                             return cbh_session_begin_raw(cfg, columns, borders, n_borders, weight, n, F,
                                                          n_bins, lr, l2, s);
+                        });
+}
+
+int cbt_open_ctr(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t n_bins,
+                 const uint32_t* real_folds, const uint8_t* one_hot_flags, const cbh_device_ctr_config* ctr,
+                 const double* target, const double* weight, cbt_trainer** out) {
+    if (!bins_fm || !ctr) return CBH_ERR_INVALID_ARG;
+    return trainer_open(p, n, F, real_folds, one_hot_flags, ctr, target, weight, out,
+                        [&](const cbh_config* cfg, double lr, double l2, cbh_session** s) {
+                            return cbh_session_begin_u8(cfg, bins_fm, weight, n, F, n_bins, lr, l2, s);
                         });
 }
 

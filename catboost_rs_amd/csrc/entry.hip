@@ -135,7 +135,8 @@ int cbh_compute_gradients(int32_t loss, const double* approx, const double* targ
     if (loss == CBH_LOSS_MULTICLASS) {
         switch (K) {
 #define CASE(k) case k: softmax_ders_kernel<k><<<grid_of(n, 256), 256>>>(a.p, t.p, n, d1.p, d2.p); break;
-            CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(10) CASE(12) CASE(16)
+            CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(9) CASE(10) CASE(11) CASE(12)
+            CASE(13) CASE(14) CASE(15) CASE(16)
 #undef CASE
             default: return fail2(CBH_ERR_UNSUPPORTED, "approx_dim has no compiled variant");
         }

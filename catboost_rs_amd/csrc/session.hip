@@ -98,6 +98,9 @@ struct StageTimer {
 }  // namespace
 
 int cbh_internal_fail(int code, const std::string& msg) { return fail(code, msg); }
+int cbh_internal_ctr_bins(const cbh_device_ctr_column* cols, uint32_t m, const uint64_t* n_buckets,
+                          const uint32_t* permutation, const uint32_t* target_class, uint64_t n,
+                          uint8_t* dst, hipStream_t st);   // categorical.hip
 int cbh_internal_quantize(const float* d_col, uint64_t n, const double* d_borders, uint32_t nb, uint8_t* d_out,
                           hipStream_t st);  // borders.hip
 
@@ -333,8 +336,16 @@ int validate_config(const cbh_config* cfg, uint32_t n_bins, uint64_t n, uint32_t
     if (cfg->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE && cfg->depth > 6)
         return fail(CBH_DECLINED, "PairLogitPairwise is covered up to depth 6 (64-leaf systems)");
     if (cfg->loss == CBH_LOSS_MULTICLASS) {
-        if (cfg->approx_dim < 2 || cfg->approx_dim > kMaxK)
-            return fail(CBH_DECLINED, "MultiClass approx_dim must be 2..16");
+        const int k = cfg->approx_dim;
+        if (k < 2 || k > kMaxK) return fail(CBH_DECLINED, "MultiClass approx_dim must be 2..16");
+        if (!(k <= 8 || k == 10 || k == 12 || k == 16))   // the compiled variants (with_k)
+            return fail(CBH_DECLINED, "MultiClass approx_dim " + std::to_string(k) + " has no compiled kernel variant");
+        // the leaf reduction keeps 2^depth leaves x (K + K(K+1)/2) int64 cells in one
+        // workgroup's LDS (160 KiB on gfx950)
+        const uint64_t lds = ((uint64_t)1 << cfg->depth) * (uint64_t)(k + k * (k + 1) / 2) * 8u;
+        if (lds > 160u * 1024u)
+            return fail(CBH_DECLINED, "MultiClass leaf statistics of approx_dim " + std::to_string(k) + " at depth " +
+                                          std::to_string(cfg->depth) + " exceed the LDS of one workgroup");
         if (cfg->leaf_method != CBH_LEAF_NEWTON)
             return fail(CBH_DECLINED, "MultiClass needs Newton leaves (boosting.rs:2169-2186)");
     } else if (cfg->approx_dim != 1) {
@@ -596,6 +607,149 @@ template <typename Load>
 int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32_t F, uint32_t n_bins,
                  double lr, double l2, cbh_session** out, Load&& load_cols);
 
+// ---- device CTR config at open (DeviceTrainConfig.ctr) ----
+struct CtrOpen {
+    uint32_t m = 0;                      // CTR columns appended after the base features
+    std::vector<uint8_t> one_hot;        // base flags extended with zeros
+    std::vector<uint32_t> folds;         // base folds extended with n_borders + 1
+    std::vector<uint64_t> nb_struct, nb_avg;   // bucket scratch sizes (largest code + 1)
+    std::vector<uint32_t> bucket_count, group;
+    std::vector<uint32_t> cat_nb;
+};
+
+bool ctr_type_covered(int32_t t) {
+    return t == CBH_CTR_BORDERS || t == CBH_CTR_BUCKETS || t == CBH_CTR_BTMV || t == CBH_CTR_COUNTER;
+}
+
+// Admission (ctr_covered, gpu_runtime/session.rs:177-215) and host validation of the
+// inputs the device build reads.  Fills the extended one-hot flags / folds of the session.
+int admit_device_ctr(const cbh_config* cfg, uint64_t n, uint32_t F, uint32_t n_bins, CtrOpen& co) {
+    const cbh_device_ctr_config* c = cfg->ctr;
+    if (cfg->loss == CBH_LOSS_PAIRLOGIT || cfg->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE)
+        return fail(CBH_DECLINED, "CTR columns are not covered with pair losses");
+    const cbh_device_ctr_averaging* a = c->averaging;
+    if (!a) return fail(CBH_DECLINED, "a CTR config without its averaging half is not covered");
+    if (c->n_columns == 0) return fail(CBH_DECLINED, "a CTR config without columns is not covered");
+    if (a->n_columns != c->n_columns)
+        return fail(CBH_DECLINED, "the averaging half has another column count than the structure half");
+    if (!c->permutation || !c->target_class || !c->columns || !a->permutation || !a->target_class || !a->columns)
+        return fail(CBH_ERR_INVALID_ARG, "null CTR array");
+    if (n >= (1ull << 31)) return fail(CBH_DECLINED, "device CTR columns cover fewer than 2^31 objects");
+    if ((uint64_t)F + c->n_columns > (1u << 20)) return fail(CBH_ERR_OUT_OF_RANGE, "too many CTR columns");
+    const uint32_t m = c->n_columns;
+    // largest code and distinct count of every member column, once per column pointer
+    std::vector<std::pair<const uint32_t*, std::pair<uint64_t, uint64_t>>> seen;
+    auto census = [&](const uint32_t* col) -> std::pair<uint64_t, uint64_t> {
+        for (auto& e : seen)
+            if (e.first == col) return e.second;
+        uint32_t mx = 0;
+        for (uint64_t i = 0; i < n; ++i) mx = std::max(mx, col[i]);
+        std::vector<uint8_t> hit((size_t)mx + 1, 0);
+        uint64_t d = 0;
+        for (uint64_t i = 0; i < n; ++i) {
+            d += hit[col[i]] ? 0 : 1;
+            hit[col[i]] = 1;
+        }
+        seen.push_back({col, {(uint64_t)mx + 1, d}});
+        return seen.back().second;
+    };
+    auto check_half = [&](const cbh_device_ctr_column* cols, std::vector<uint64_t>& nb) -> int {
+        nb.assign(m, 1);
+        for (uint32_t k = 0; k < m; ++k) {
+            const cbh_device_ctr_column& col = cols[k];
+            if (!ctr_type_covered(col.ctr_type))
+                return fail(CBH_DECLINED, "CTR type " + std::to_string(col.ctr_type) + " is not covered on device");
+            if (col.n_members == 0) return fail(CBH_DECLINED, "a CTR column without members is not covered");
+            if (col.n_members >= 2)
+                return fail(CBH_DECLINED, "combination (multi-member) CTR projections are not covered on device");
+            if (col.n_borders == 0 || col.n_borders + 1 > n_bins)
+                return fail(CBH_DECLINED, "a CTR border table needs 1 .. n_bins - 1 borders");
+            if (!col.member_bins || !col.member_bins[0] || !col.borders)
+                return fail(CBH_ERR_INVALID_ARG, "null CTR column array");
+            if ((col.ctr_type == CBH_CTR_BORDERS || col.ctr_type == CBH_CTR_BUCKETS) && col.target_border_idx > 1)
+                return fail(CBH_ERR_OUT_OF_RANGE, "CTR target_border_idx > 1 (binary classes)");
+            if (col.weight_group >= m) return fail(CBH_ERR_OUT_OF_RANGE, "CTR weight_group >= n_columns");
+            nb[k] = census(col.member_bins[0]).first;
+        }
+        return CBH_OK;
+    };
+    CHECK(check_half(c->columns, co.nb_struct));
+    CHECK(check_half(a->columns, co.nb_avg));
+    for (const uint32_t* perm : {c->permutation, a->permutation}) {
+        std::vector<uint8_t> hit(n, 0);
+        for (uint64_t p = 0; p < n; ++p) {
+            if (perm[p] >= n || hit[perm[p]])
+                return fail(CBH_ERR_OUT_OF_RANGE, "a CTR permutation is not a permutation of 0..n-1");
+            hit[perm[p]] = 1;
+        }
+    }
+    for (const uint32_t* cls : {c->target_class, a->target_class})
+        for (uint64_t i = 0; i < n; ++i)
+            if (cls[i] > 1) return fail(CBH_ERR_OUT_OF_RANGE, "CTR target_class must be 0 or 1");
+    co.m = m;
+    co.bucket_count.resize(m);
+    co.group.resize(m);
+    for (uint32_t k = 0; k < m; ++k) {
+        const cbh_device_ctr_column& col = c->columns[k];
+        // 0 = unknown: the column's own observed distinct-bucket count (runtime.rs:1116-1122)
+        const uint64_t bc = col.bucket_count ? col.bucket_count : census(col.member_bins[0]).second;
+        if (bc > 0xFFFFFFFFull) return fail(CBH_ERR_OUT_OF_RANGE, "CTR bucket_count does not fit u32");
+        co.bucket_count[k] = (uint32_t)bc;
+        co.group[k] = col.weight_group;
+    }
+    if (c->n_cat && !c->cat_eligible_buckets) return fail(CBH_ERR_INVALID_ARG, "null cat_eligible_buckets");
+    co.cat_nb.resize(c->n_cat);
+    for (uint32_t j = 0; j < c->n_cat; ++j) {
+        if (!c->cat_eligible_buckets[j]) return fail(CBH_ERR_INVALID_ARG, "null categorical bucket column");
+        co.cat_nb[j] = (uint32_t)std::min<uint64_t>(census(c->cat_eligible_buckets[j]).first, 0xFFFFFFFFull);
+    }
+    if (cfg->one_hot_flags) {
+        co.one_hot.assign(cfg->one_hot_flags, cfg->one_hot_flags + F);
+        co.one_hot.resize((size_t)F + m, 0);
+    }
+    co.folds.resize((size_t)F + m);
+    for (uint32_t f = 0; f < F; ++f) co.folds[f] = cfg->real_folds ? cfg->real_folds[f] : n_bins;
+    for (uint32_t k = 0; k < m; ++k) co.folds[F + k] = c->columns[k].n_borders + 1;
+    return CBH_OK;
+}
+
+// Both materializations on the device: the structure columns into the session's
+// feature-major bins after the F base features, the averaging columns into ctr_avg.
+int build_device_ctr(cbh_session* s, uint32_t F, const cbh_device_ctr_config* c, const CtrOpen& co) {
+    CHECK(cbh_internal_ctr_bins(c->columns, co.m, co.nb_struct.data(), c->permutation, c->target_class, s->n,
+                                s->cols + (size_t)F * s->n, s->stream));
+    CHECK(dalloc(&s->ctr_avg, (size_t)co.m * s->n));
+    const cbh_device_ctr_averaging* a = c->averaging;
+    CHECK(cbh_internal_ctr_bins(a->columns, co.m, co.nb_avg.data(), a->permutation, a->target_class, s->n,
+                                s->ctr_avg, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return CBH_OK;
+}
+
+int install_ctr(cbh_session* s, uint32_t m, const uint32_t* bucket_count, const uint32_t* weight_group,
+                uint32_t n_cat, const uint32_t* const* cat_cols, const uint32_t* cat_bucket_count, double msr);
+
+// Open with the device CTR config, if any: admission, the extended session shape, the
+// device build inside the load step and the scoring state once the session exists.
+template <typename Open>
+int open_with_ctr(const cbh_config* cfg, uint64_t n, uint32_t F, uint32_t n_bins, cbh_session** out, Open&& open) {
+    if (!cfg->ctr) return open(cfg, F, [](cbh_session*) { return CBH_OK; });
+    CtrOpen co;
+    CHECK(admit_device_ctr(cfg, n, F, n_bins, co));
+    cbh_config c2 = *cfg;
+    c2.one_hot_flags = co.one_hot.empty() ? nullptr : co.one_hot.data();
+    c2.real_folds = co.folds.data();
+    const cbh_device_ctr_config* c = cfg->ctr;
+    CHECK(open(&c2, F + co.m, [&](cbh_session* s) { return build_device_ctr(s, F, c, co); }));
+    const int rc = install_ctr(*out, co.m, co.bucket_count.data(), co.group.data(), c->n_cat,
+                               c->cat_eligible_buckets, co.cat_nb.data(), c->model_size_reg);
+    if (rc != CBH_OK) {
+        (void)cbh_session_end(*out);
+        *out = nullptr;
+    }
+    return rc;
+}
+
 template <typename BinT>
 int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double* weight,
                        uint64_t n, uint32_t F, uint32_t n_bins, double lr, double l2,
@@ -609,20 +763,22 @@ int session_begin_impl(const cbh_config* cfg, const BinT* bins_fm, const double*
         if ((uint32_t)bins_fm[i] >= n_bins)
             return fail(CBH_ERR_OUT_OF_RANGE, "bin value >= n_bins at flat index " + std::to_string(i));
     // upload bins feature-major as u8 (the rows are packed from them on the device)
-    return session_open(cfg, weight, n, F, n_bins, lr, l2, out, [&](cbh_session* s) -> int {
-        if (sizeof(BinT) == 1) {
-            HIP_TRY(hipMemcpy(s->cols, bins_fm, (size_t)n * F, hipMemcpyHostToDevice));
-        } else {
-            std::vector<uint8_t> tmp;
-            const uint64_t step = 1ull << 26;
-            for (uint64_t off = 0, total = n * F; off < total; off += step) {
-                const uint64_t m = std::min(step, total - off);
-                tmp.resize(m);
-                for (uint64_t i = 0; i < m; ++i) tmp[i] = (uint8_t)bins_fm[off + i];
-                HIP_TRY(hipMemcpy(s->cols + off, tmp.data(), m, hipMemcpyHostToDevice));
+    return open_with_ctr(cfg, n, F, n_bins, out, [&](const cbh_config* c, uint32_t F_all, auto&& ctr_build) {
+        return session_open(c, weight, n, F_all, n_bins, lr, l2, out, [&](cbh_session* s) -> int {
+            if (sizeof(BinT) == 1) {
+                HIP_TRY(hipMemcpy(s->cols, bins_fm, (size_t)n * F, hipMemcpyHostToDevice));
+            } else {
+                std::vector<uint8_t> tmp;
+                const uint64_t step = 1ull << 26;
+                for (uint64_t off = 0, total = n * F; off < total; off += step) {
+                    const uint64_t m = std::min(step, total - off);
+                    tmp.resize(m);
+                    for (uint64_t i = 0; i < m; ++i) tmp[i] = (uint8_t)bins_fm[off + i];
+                    HIP_TRY(hipMemcpy(s->cols + off, tmp.data(), m, hipMemcpyHostToDevice));
+                }
             }
-        }
-        return CBH_OK;
+            return ctr_build(s);
+        });
     });
 }
 
@@ -655,7 +811,8 @@ int session_begin_raw_impl(const cbh_config* cfg, const float* const* columns, c
     for (uint32_t f = 0; f < F; ++f) folds[f] = n_borders[f] + 1;
     cbh_config c = *cfg;
     if (!c.real_folds) c.real_folds = folds.data();
-    return session_open(&c, weight, n, F, n_bins, lr, l2, out, [&](cbh_session* s) -> int {
+    return open_with_ctr(&c, n, F, n_bins, out, [&](const cbh_config* c2, uint32_t F_all, auto&& ctr_build) {
+      return session_open(c2, weight, n, F_all, n_bins, lr, l2, out, [&](cbh_session* s) -> int {
         if (n == 0 || F == 0) return CBH_OK;
         std::vector<double> flat(std::max<uint64_t>(off[F], 1));
         for (uint32_t f = 0; f < F; ++f)
@@ -695,7 +852,9 @@ int session_begin_raw_impl(const cbh_config* cfg, const float* const* columns, c
             if (e) (void)hipEventDestroy(e);
         if (db) (void)hipFree(db);
         if (stage) (void)hipFree(stage);
-        return rc;
+        if (rc != CBH_OK) return rc;
+        return ctr_build(s);
+      });
     });
 }
 
@@ -707,6 +866,7 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     if (cfg->one_hot_flags) s->one_hot_host.assign(cfg->one_hot_flags, cfg->one_hot_flags + F);
     s->cfg.one_hot_flags = nullptr;
     s->cfg.real_folds = nullptr;
+    s->cfg.ctr = nullptr;
     s->n = n;
     s->F = F;
     s->B = n_bins;
@@ -1303,10 +1463,100 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     plans_out.assign(s->pin_plans, s->pin_plans + s->depth);
     bounds_out = *s->pin_bounds;
     leaf_out.assign(s->pin_leaves, s->pin_leaves + n_leaves * K);
+    // a level without a candidate split: the tree is not part of the model (CbError::Degenerate
+    // leaves it untouched), so its leaves are never applied and its CTR groups stay unused
+    for (uint32_t l = 0; l < s->depth; ++l)
+        if (!splits_out[l].valid) {
+            s->pending = false;
+            return fail(CBH_ERR_DEGENERATE, "no candidate split at level " + std::to_string(l));
+        }
     for (const SplitRec& sp : splits_out)   // groups used by this tree (ProcessCtrSplit)
         if (s->ctr_n && sp.feature >= s->F - s->ctr_n) s->ctr_used[s->ctr_group[sp.feature - (s->F - s->ctr_n)]] = 1;
     return CBH_OK;
 }
+
+// The CTR scoring state of a session whose last m features are CTR columns and whose
+// ctr_avg holds the averaging bins (cbh_session_set_ctr and the device CTR config at open).
+int install_ctr(cbh_session* s, uint32_t m, const uint32_t* bucket_count, const uint32_t* weight_group,
+                uint32_t n_cat, const uint32_t* const* cat_cols, const uint32_t* cat_bucket_count, double msr) {
+    const uint64_t n = s->n;
+    const uint32_t fc0 = s->F - m;
+    for (uint32_t f = fc0; f < s->F; ++f)
+        if (!s->one_hot_host.empty() && s->one_hot_host[f])
+            return fail(CBH_ERR_UNSUPPORTED, "a CTR column cannot be one-hot");
+    for (uint32_t c = 0; c < m; ++c)
+        if (weight_group[c] >= m) return fail(CBH_ERR_OUT_OF_RANGE, "weight_group >= n_ctr");
+    const uint32_t lmax = 1u << (s->depth - 1);
+    uint64_t words = 0;
+    for (uint32_t c = 0; c < n_cat; ++c)
+        words += kPhantomBlocks * (((uint64_t)cat_bucket_count[c] * lmax + 31) / 32);
+    CHECK(dalloc(&s->fweight, s->F));
+    s->fweight_host.assign(s->F, 1.0);
+    HIP_TRY(hipMemcpy(s->fweight, s->fweight_host.data(), sizeof(double) * s->F, hipMemcpyHostToDevice));
+    if (n_cat) {
+        CHECK(dalloc(&s->cat_bk, (size_t)n_cat * n));
+        for (uint32_t c = 0; c < n_cat; ++c)
+            HIP_TRY(hipMemcpy(s->cat_bk + (size_t)c * n, cat_cols[c], sizeof(uint32_t) * n, hipMemcpyHostToDevice));
+        CHECK(dalloc(&s->cat_nb_dev, n_cat));
+        HIP_TRY(hipMemcpy(s->cat_nb_dev, cat_bucket_count, sizeof(uint32_t) * n_cat, hipMemcpyHostToDevice));
+        CHECK(dalloc(&s->phantom_off, n_cat));
+        CHECK(dalloc(&s->phantom_bits, std::max<uint64_t>(words, 1)));
+        CHECK(dalloc(&s->phantom_cnt, n_cat));
+    }
+    s->ctr_bc.assign(bucket_count, bucket_count + m);
+    s->ctr_group.assign(weight_group, weight_group + m);
+    s->ctr_used.assign(m, 0);
+    s->ctr_eligible_max = 1;
+    for (uint32_t v : s->ctr_bc) s->ctr_eligible_max = std::max<uint64_t>(s->ctr_eligible_max, v);
+    HIP_TRY(hipFuncSetAttribute((const void*)phantom_bits_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(kPhantomLdsWords * sizeof(uint32_t))));
+    s->cat_n = n_cat;
+    s->cat_nb.assign(cat_bucket_count, cat_bucket_count + n_cat);
+    s->msr = msr;
+    s->ctr_n = m;
+    // device weights when the pow table stays modest: counts reachable at any level are the
+    // eligible maximum and the phantom counts, at most (float leaves) x (buckets)
+    {
+        uint64_t nb_max = 0;
+        for (uint32_t v : s->cat_nb) nb_max = std::max<uint64_t>(nb_max, v);
+        const uint64_t m_lo = s->ctr_eligible_max;
+        const uint64_t m_hi = std::max<uint64_t>(m_lo, (uint64_t)lmax * nb_max);
+        const uint64_t span = m_hi - m_lo + 1;
+        // CBH_CTR_WEIGHTS=host keeps the per-level host step (a test knob for that path)
+        const char* cw = std::getenv("CBH_CTR_WEIGHTS");
+        const bool host_only = cw && std::string(cw) == "host";
+        if (!host_only && (uint64_t)m * span <= (32ull << 20)) {
+            std::vector<double> table((size_t)m * span);
+            for (uint32_t c = 0; c < m; ++c)
+                for (uint64_t k = 0; k < span; ++k)
+                    table[(size_t)c * span + k] =
+                        std::pow(1.0 + (double)s->ctr_bc[c] / (double)(m_lo + k), -s->msr);
+            CHECK(dalloc(&s->ctr_pow, table.size()));
+            HIP_TRY(hipMemcpy(s->ctr_pow, table.data(), sizeof(double) * table.size(), hipMemcpyHostToDevice));
+            CHECK(dalloc(&s->ctr_group_dev, m));
+            HIP_TRY(hipMemcpy(s->ctr_group_dev, s->ctr_group.data(), sizeof(uint32_t) * m, hipMemcpyHostToDevice));
+            CHECK(dalloc(&s->ctr_used_dev, m + 1));   // [m] by group, then the all-used flag
+            HIP_TRY(hipHostMalloc((void**)&s->pin_ctr_used, m + 1, hipHostMallocDefault));
+            if (s->cat_n) {
+                std::vector<uint64_t> offs((size_t)s->depth * s->cat_n, 0);
+                for (uint32_t lv = 1; lv < s->depth; ++lv) {
+                    uint64_t w = 0;
+                    for (uint32_t c = 0; c < s->cat_n; ++c) {
+                        offs[(size_t)lv * s->cat_n + c] = w;
+                        w += kPhantomBlocks * (((uint64_t)s->cat_nb[c] * (1u << lv) + 31) / 32);
+                    }
+                }
+                CHECK(dalloc(&s->phantom_off_lv, offs.size()));
+                HIP_TRY(hipMemcpy(s->phantom_off_lv, offs.data(), sizeof(uint64_t) * offs.size(), hipMemcpyHostToDevice));
+            }
+            s->ctr_m_lo = m_lo;
+            s->ctr_m_hi = m_hi;
+            s->ctr_dev = true;
+        }
+    }
+    return CBH_OK;
+}
+
 
 }  // namespace
 
@@ -1341,6 +1591,18 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
                      const double* sample, uint64_t n_sample, const cbh_tree_sampling* sampling,
                      const cbh_family* family, cbh_tree_out* out) {
     if (!s) return fail(CBH_ERR_INVALID_ARG, "session is null");
+    if (family && family->kind == CBH_FAMILY_MULTI_OUTPUT) {
+        // FamilyTreeArgs::MultiOutput (runtime.rs:935-950): the dim-major K x n approximant of
+        // this tree, the same upload as the approx argument
+        if (!family->approx_k) return fail(CBH_ERR_INVALID_ARG, "MultiOutput approx_k is null");
+        if (family->approx_dim != s->K)
+            return fail(CBH_ERR_LENGTH_MISMATCH, "MultiOutput approx_dim differs from the session's approx_dim");
+        if (approx && approx != family->approx_k)
+            return fail(CBH_ERR_INVALID_ARG, "the approximant is given both as approx and as MultiOutput approx_k");
+        approx = family->approx_k;
+        family = nullptr;
+    }
+    if (family && family->kind != CBH_FAMILY_PAIRWISE) return fail(CBH_ERR_INVALID_ARG, "unknown family kind");
     if (family && !s->ranking) return fail(CBH_ERR_INVALID_ARG, "a family descriptor is given to a pointwise session");
     if (s->pairwise && (n_sample != 0 || (sampling && sampling->kind != CBH_BOOT_NO)))
         return fail(CBH_ERR_UNSUPPORTED, "PairLogitPairwise scores unsampled derivatives (no bootstrap)");
@@ -1396,7 +1658,6 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
     });
     if (rc != CBH_OK) return rc;
     for (uint32_t l = 0; l < s->depth; ++l) {
-        if (!splits[l].valid) return fail(CBH_ERR_DEGENERATE, "no candidate split at level " + std::to_string(l));
         out->split_feature[l] = splits[l].feature;
         out->split_bin[l] = splits[l].bin;
         if (out->split_one_hot) out->split_one_hot[l] = (uint8_t)splits[l].one_hot;
@@ -1469,87 +1730,30 @@ int cbh_session_set_ctr(cbh_session* s, const cbh_ctr_info* info) {
     if (!info->averaging_bins || !info->bucket_count || !info->weight_group || (info->n_cat && !info->cat_buckets) ||
         (info->n_cat && !info->cat_bucket_count))
         return fail(CBH_ERR_INVALID_ARG, "null CTR array");
-    const uint32_t fc0 = s->F - m;
-    for (uint32_t f = fc0; f < s->F; ++f)
-        if (!s->one_hot_host.empty() && s->one_hot_host[f])
-            return fail(CBH_ERR_UNSUPPORTED, "a CTR column cannot be one-hot");
-    for (uint32_t c = 0; c < m; ++c)
-        if (info->weight_group[c] >= m) return fail(CBH_ERR_OUT_OF_RANGE, "weight_group >= n_ctr");
-    for (uint32_t c = 0; c < info->n_cat; ++c)
-        for (uint64_t i = 0; i < n; ++i)
-            if (info->cat_buckets[(size_t)c * n + i] >= info->cat_bucket_count[c])
-                return fail(CBH_ERR_OUT_OF_RANGE, "categorical bucket >= its bucket count");
     for (uint64_t i = 0, total = (uint64_t)m * n; i < total; ++i)
         if (info->averaging_bins[i] >= s->B) return fail(CBH_ERR_OUT_OF_RANGE, "averaging bin >= n_bins");
-    const uint32_t lmax = 1u << (s->depth - 1);
-    uint64_t words = 0;
+    std::vector<const uint32_t*> cat_cols(info->n_cat);
+    for (uint32_t c = 0; c < info->n_cat; ++c) cat_cols[c] = info->cat_buckets + (size_t)c * n;
     for (uint32_t c = 0; c < info->n_cat; ++c)
-        words += kPhantomBlocks * (((uint64_t)info->cat_bucket_count[c] * lmax + 31) / 32);
+        for (uint64_t i = 0; i < n; ++i)
+            if (cat_cols[c][i] >= info->cat_bucket_count[c])
+                return fail(CBH_ERR_OUT_OF_RANGE, "categorical bucket >= its bucket count");
     CHECK(dalloc(&s->ctr_avg, (size_t)m * n));
     HIP_TRY(hipMemcpy(s->ctr_avg, info->averaging_bins, (size_t)m * n, hipMemcpyHostToDevice));
-    CHECK(dalloc(&s->fweight, s->F));
-    s->fweight_host.assign(s->F, 1.0);
-    HIP_TRY(hipMemcpy(s->fweight, s->fweight_host.data(), sizeof(double) * s->F, hipMemcpyHostToDevice));
-    if (info->n_cat) {
-        CHECK(dalloc(&s->cat_bk, (size_t)info->n_cat * n));
-        HIP_TRY(hipMemcpy(s->cat_bk, info->cat_buckets, sizeof(uint32_t) * info->n_cat * n, hipMemcpyHostToDevice));
-        CHECK(dalloc(&s->cat_nb_dev, info->n_cat));
-        HIP_TRY(hipMemcpy(s->cat_nb_dev, info->cat_bucket_count, sizeof(uint32_t) * info->n_cat, hipMemcpyHostToDevice));
-        CHECK(dalloc(&s->phantom_off, info->n_cat));
-        CHECK(dalloc(&s->phantom_bits, std::max<uint64_t>(words, 1)));
-        CHECK(dalloc(&s->phantom_cnt, info->n_cat));
-    }
-    s->ctr_bc.assign(info->bucket_count, info->bucket_count + m);
-    s->ctr_group.assign(info->weight_group, info->weight_group + m);
-    s->ctr_used.assign(m, 0);
-    s->ctr_eligible_max = 1;
-    for (uint32_t v : s->ctr_bc) s->ctr_eligible_max = std::max<uint64_t>(s->ctr_eligible_max, v);
-    HIP_TRY(hipFuncSetAttribute((const void*)phantom_bits_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)(kPhantomLdsWords * sizeof(uint32_t))));
-    s->cat_n = info->n_cat;
-    s->cat_nb.assign(info->cat_bucket_count, info->cat_bucket_count + info->n_cat);
-    s->msr = info->model_size_reg;
-    s->ctr_n = m;
-    // device weights when the pow table stays modest: counts reachable at any level are the
-    // eligible maximum and the phantom counts, at most (float leaves) x (buckets)
-    {
-        uint64_t nb_max = 0;
-        for (uint32_t v : s->cat_nb) nb_max = std::max<uint64_t>(nb_max, v);
-        const uint64_t m_lo = s->ctr_eligible_max;
-        const uint64_t m_hi = std::max<uint64_t>(m_lo, (uint64_t)lmax * nb_max);
-        const uint64_t span = m_hi - m_lo + 1;
-        // CBH_CTR_WEIGHTS=host keeps the per-level host step (a test knob for that path)
-        const char* cw = std::getenv("CBH_CTR_WEIGHTS");
-        const bool host_only = cw && std::string(cw) == "host";
-        if (!host_only && (uint64_t)m * span <= (32ull << 20)) {
-            std::vector<double> table((size_t)m * span);
-            for (uint32_t c = 0; c < m; ++c)
-                for (uint64_t k = 0; k < span; ++k)
-                    table[(size_t)c * span + k] =
-                        std::pow(1.0 + (double)s->ctr_bc[c] / (double)(m_lo + k), -s->msr);
-            CHECK(dalloc(&s->ctr_pow, table.size()));
-            HIP_TRY(hipMemcpy(s->ctr_pow, table.data(), sizeof(double) * table.size(), hipMemcpyHostToDevice));
-            CHECK(dalloc(&s->ctr_group_dev, m));
-            HIP_TRY(hipMemcpy(s->ctr_group_dev, s->ctr_group.data(), sizeof(uint32_t) * m, hipMemcpyHostToDevice));
-            CHECK(dalloc(&s->ctr_used_dev, m + 1));   // [m] by group, then the all-used flag
-            HIP_TRY(hipHostMalloc((void**)&s->pin_ctr_used, m + 1, hipHostMallocDefault));
-            if (s->cat_n) {
-                std::vector<uint64_t> offs((size_t)s->depth * s->cat_n, 0);
-                for (uint32_t lv = 1; lv < s->depth; ++lv) {
-                    uint64_t w = 0;
-                    for (uint32_t c = 0; c < s->cat_n; ++c) {
-                        offs[(size_t)lv * s->cat_n + c] = w;
-                        w += kPhantomBlocks * (((uint64_t)s->cat_nb[c] * (1u << lv) + 31) / 32);
-                    }
-                }
-                CHECK(dalloc(&s->phantom_off_lv, offs.size()));
-                HIP_TRY(hipMemcpy(s->phantom_off_lv, offs.data(), sizeof(uint64_t) * offs.size(), hipMemcpyHostToDevice));
-            }
-            s->ctr_m_lo = m_lo;
-            s->ctr_m_hi = m_hi;
-            s->ctr_dev = true;
-        }
-    }
+    const int rc = install_ctr(s, m, info->bucket_count, info->weight_group, info->n_cat, cat_cols.data(),
+                               info->cat_bucket_count, info->model_size_reg);
+    if (rc != CBH_OK) dfree(s->ctr_avg);
+    return rc;
+}
+
+int cbh_session_read_ctr_bins(const cbh_session* s, int32_t averaging, uint8_t* out, uint64_t n_times_ctr) {
+    if (!s || !out) return fail(CBH_ERR_INVALID_ARG, "null argument");
+    if (s->ctr_n == 0) return fail(CBH_ERR_INVALID_ARG, "the session has no CTR columns");
+    const size_t total = (size_t)s->ctr_n * s->n;
+    if (n_times_ctr != total) return fail(CBH_ERR_LENGTH_MISMATCH, "out must hold n_ctr * n bins");
+    const uint8_t* src = averaging ? s->ctr_avg : s->cols + (size_t)(s->F - s->ctr_n) * s->n;
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    HIP_TRY(hipMemcpy(out, src, total, hipMemcpyDeviceToHost));
     return CBH_OK;
 }
 

@@ -51,10 +51,13 @@ enum { CBH_NAN_MIN = 0, CBH_NAN_MAX = 1, CBH_NAN_FORBIDDEN = 2 };
 /* CTR types (ECtrType, crates/cb-train/src/ctr/mod.rs; the CPU-task subset) */
 enum { CBH_CTR_BORDERS = 0, CBH_CTR_BUCKETS = 1, CBH_CTR_BTMV = 2, CBH_CTR_COUNTER = 4 };
 
+/* The device CTR config (DeviceCtrConfig, runtime.rs:1174-1200); defined below. */
+typedef struct cbh_device_ctr_config cbh_device_ctr_config;
+
 /* Mirrors DeviceTrainConfig (runtime.rs:1260-1341) plus the scalar arguments of
  * begin_device_training (runtime.rs:1497-1529).  Fields the device path does not cover
- * (non-symmetric policies, ordered boosting, CTR computation, exact leaves) are absent:
- * a caller that needs them must not open a session (the reference declines the same). */
+ * (non-symmetric policies, ordered boosting, exact leaves) are absent: a caller that needs
+ * them must not open a session (the reference declines the same). */
 typedef struct {
     int32_t loss;                 /* CBH_LOSS_* */
     int32_t score_function;       /* CBH_SCORE_* */
@@ -79,6 +82,10 @@ typedef struct {
     /* PairLogitPairwise: the bucket-weight prior of the pairwise leaf system
      * (bayesian_matrix_reg, 0.1 by default; boosting.rs:1785-1790) */
     double pairwise_non_diag_reg;
+    /* DeviceTrainConfig.ctr (runtime.rs:1174-1230): NULL, or the CTR columns the session
+     * builds on the device at open and appends after the n_features given (see
+     * cbh_device_ctr_config) */
+    const cbh_device_ctr_config* ctr;
 } cbh_config;
 
 typedef struct cbh_session cbh_session;
@@ -126,21 +133,28 @@ typedef struct {
     uint64_t bernoulli_state[4];
 } cbh_tree_sampling;
 
-/* Per-tree family descriptor; mirrors FamilyTreeArgs::Pairwise (runtime.rs:913-934).
- * Required on the first grow of a PairLogit / PairLogitPairwise session; NULL later keeps
- * the resident pairs.  Rows of a query group are contiguous (group_offsets, CSR over row
- * order, n_groups + 1 entries, [0] = 0, [n_groups] = n); pairs are (winner, loser, weight)
- * inside one group, in any order (the session orders them as the reference's competitor
- * lists: stable by winner).  pair_weight NULL = weight 1 (query_info.rs:236-239). */
-enum { CBH_FAMILY_PAIRWISE = 1 };
+/* Per-tree family descriptor; mirrors FamilyTreeArgs (runtime.rs:913-950).
+ * CBH_FAMILY_PAIRWISE (FamilyTreeArgs::Pairwise): required on the first grow of a PairLogit /
+ * PairLogitPairwise session; NULL later keeps the resident pairs.  Rows of a query group are
+ * contiguous (group_offsets, CSR over row order, n_groups + 1 entries, [0] = 0,
+ * [n_groups] = n); pairs are (winner, loser, weight) inside one group, in any order (the
+ * session orders them as the reference's competitor lists: stable by winner).
+ * pair_weight NULL = weight 1 (query_info.rs:236-239).
+ * CBH_FAMILY_MULTI_OUTPUT (FamilyTreeArgs::MultiOutput): approx_k is the dim-major
+ * [approx_dim][n] approximant of this tree, approx_dim the session's; it is uploaded as the
+ * approx argument of cbh_session_grow would be (which must then be NULL or the same
+ * pointer).  The pair fields are unused. */
+enum { CBH_FAMILY_PAIRWISE = 1, CBH_FAMILY_MULTI_OUTPUT = 2 };
 typedef struct {
-    int32_t kind;                 /* CBH_FAMILY_PAIRWISE */
+    int32_t kind;                 /* CBH_FAMILY_* */
     uint32_t n_groups;
     const uint32_t* group_offsets;
     const uint32_t* pair_winner;
     const uint32_t* pair_loser;
     const double* pair_weight;
     uint64_t n_pairs;
+    const double* approx_k;       /* MultiOutput: [approx_dim][n] */
+    uint32_t approx_dim;          /* MultiOutput: K */
 } cbh_family;
 
 /* Output of one grown tree; mirrors DeviceGrownTree (runtime.rs:990-1059).  Buffers are
@@ -209,7 +223,10 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out);
  * (float-partition leaf, bucket) pairs of the categorical columns (tree.rs:2907, :3146-3346).
  * Leaf values and the resident approximant use the partition in which every CTR level
  * re-tests the column built under the averaging permutation (assign_leaf_over_ctr_columns,
- * boosting.rs:2905, :8206).  Trees of such a session run eagerly (per-level host step). */
+ * boosting.rs:2905, :8206).  The weights come from a table of pow values over every
+ * reachable max_count (tabulated here at set-up, picked per level on the device), so such
+ * trees replay their recorded launch sequence like any other; when the table would pass
+ * 32 Mi entries each level takes a host step instead and the trees run eagerly. */
 typedef struct {
     uint32_t n_ctr;
     const uint8_t* averaging_bins;    /* [n_ctr][n] */
@@ -221,6 +238,59 @@ typedef struct {
     double model_size_reg;            /* 0.5 by default; 0 disables the weight */
 } cbh_ctr_info;
 int cbh_session_set_ctr(cbh_session* s, const cbh_ctr_info* info);
+
+/* The device CTR config given at open (cbh_config.ctr): DeviceCtrColumn,
+ * DeviceCtrAveraging and DeviceCtrConfig (runtime.rs:1104-1230).  The session builds both
+ * CTR materializations on the device, as build_ctr_cindex_columns does
+ * (crates/cb-backend/src/gpu_runtime/session.rs:262-360): for every column, the ordered
+ * statistic of its bucket column under the permutation (Borders / Buckets / BTMV read the
+ * object's predecessors in its bucket, Counter whole-set bucket sizes), value
+ * (num + prior) / (total + 1), binarized by the column's border table: bin = the number of
+ * borders strictly below the value (binarize_ctr_kernel, kernels/ctr_device.rs:399-413).
+ * The structure columns become features n_features .. n_features + n_columns - 1 of the
+ * session (candidate folds n_borders + 1) and are scored as cbh_session_set_ctr describes;
+ * the averaging columns re-test the CTR levels for leaf values and the resident
+ * approximant.  Admission follows ctr_covered (session.rs:177-215): a NULL averaging half,
+ * a column count that differs between the halves, a type outside CBH_CTR_*, a column with
+ * no member, or a pair loss DECLINES; so does a projection of two or more members (the
+ * combination gate is not built).  A border table may be shorter than n_bins - 1 (the
+ * reference asks for equality and declines otherwise). */
+typedef struct {
+    uint32_t n_members;                  /* 1: a simple projection */
+    const uint32_t* const* member_bins;  /* [n_members] pointers to n category codes */
+    double prior;                        /* prior numerator (prior_num / prior_denom) */
+    const double* borders;               /* [n_borders] */
+    uint32_t n_borders;                  /* 1 .. n_bins - 1 */
+    uint64_t bucket_count;               /* the projection's distinct buckets; 0 = observed */
+    uint32_t weight_group;               /* (ctr type, projection) group id, < n_columns */
+    int32_t ctr_type;                    /* CBH_CTR_* */
+    uint32_t target_border_idx;          /* Borders / Buckets numerator selector, <= 1 */
+    const uint32_t* projection_members;  /* [n_projection_members] sorted absolute cat ids */
+    uint32_t n_projection_members;
+} cbh_device_ctr_column;
+
+typedef struct {
+    const uint32_t* permutation;             /* [n] averaging-fold order */
+    const uint32_t* target_class;            /* [n] 0 or 1 */
+    const cbh_device_ctr_column* columns;    /* [n_columns], aligned with the structure set */
+    uint32_t n_columns;
+} cbh_device_ctr_averaging;
+
+struct cbh_device_ctr_config {
+    const uint32_t* permutation;             /* [n] learn order: object permutation[p] at position p */
+    const uint32_t* target_class;            /* [n] 0 or 1 */
+    const cbh_device_ctr_column* columns;    /* [n_columns] */
+    uint32_t n_columns;
+    const cbh_device_ctr_averaging* averaging;    /* NULL declines */
+    uint32_t n_cat;                               /* CTR-eligible categorical columns */
+    const uint32_t* const* cat_eligible_buckets;  /* [n_cat] pointers to n first-seen buckets */
+    double model_size_reg;                        /* 0.5 by default; 0 disables the weight */
+};
+
+/* Test entry: the session's CTR bins, [n_ctr][n] u8, of the structure (averaging = 0) or
+ * the averaging (averaging = 1) materialization.  No counterpart in the reference, whose
+ * builder returns the bin columns to its caller. */
+int cbh_session_read_ctr_bins(const cbh_session* s, int32_t averaging, uint8_t* out, uint64_t n_times_ctr);
 
 /* Per-stage timing switch (cbh_config.profile).  While it is off, every tree after the
  * first whose previous leaves are still pending replays one recorded launch sequence (a

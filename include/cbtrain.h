@@ -52,6 +52,15 @@ int cbt_open_raw(const cbt_params* p, const float* const* columns, const double*
                  const uint32_t* n_borders, uint64_t n, uint32_t n_features, const double* target,
                  const double* weight, cbt_trainer** out);
 
+/* Open with the device CTR config (DeviceTrainConfig.ctr, see cbh_device_ctr_config): the
+ * session builds both CTR materializations on the device and appends the structure columns
+ * after the n_features base features, so split features >= n_features name CTR columns
+ * (in config order).  real_folds / one_hot_flags cover the base features only. */
+int cbt_open_ctr(const cbt_params* p, const uint8_t* bins_fm, uint64_t n, uint32_t n_features,
+                 uint32_t n_bins, const uint32_t* real_folds, const uint8_t* one_hot_flags,
+                 const cbh_device_ctr_config* ctr, const double* target, const double* weight,
+                 cbt_trainer** out);
+
 /* PairLogit / PairLogitPairwise: the query groups and explicit pairs of the pool (copied;
  * call once after cbt_open, before the first cbt_step).  See cbh_family. */
 int cbt_set_pairs(cbt_trainer* t, const uint32_t* group_offsets, uint32_t n_groups,

@@ -149,3 +149,106 @@ def test_categorical_argument_checks(lib):
     with pytest.raises(cb.CbhError) as e:
         cb.ctr_columns(np.zeros(3, np.uint32), np.arange(3), np.zeros(3), [("Borders", 0.5)] * 17)
     assert e.value.code == -2
+
+
+def test_multiclass_dimensions_without_a_variant_decline(lib):
+    """MultiClass dimensions with no compiled kernel variant, and leaf systems larger than one
+    workgroup's LDS, decline to the CPU grower (status 1) instead of failing on the device."""
+    import ctypes as C
+    import numpy as np
+    bins = np.zeros((2, 8), np.uint8)
+    s = C.c_void_p()
+    for k, depth in ((9, 6), (11, 6), (13, 4), (15, 2), (12, 8), (16, 8)):
+        cfg = cb.Config(loss=2, score_function=0, leaf_method=1, depth=depth, boosting_type_is_plain=1,
+                        fold_count=1, approx_dim=k)
+        rc = lib.cbh_session_begin_u8(C.byref(cfg), bins.ctypes.data_as(C.c_void_p), None, 8, 2, 4,
+                                      0.1, 3.0, C.byref(s))
+        assert rc == cb.DECLINED, (k, depth, rc)
+
+
+def test_device_ctr_config_admission(lib):
+    """The device CTR config declines what ctr_covered declines (gpu_runtime/session.rs:177-215)
+    and rejects malformed inputs with typed errors, all before any device call."""
+    import ctypes as C
+    import numpy as np
+    n = 8
+    bins = np.zeros((2, n), np.uint8)
+    cat = np.array([[0, 1, 0, 2, 1, 0, 2, 2]], np.uint32)
+    perm = np.arange(n)[::-1]
+    cls = np.array([0, 1, 1, 0, 1, 0, 0, 1])
+
+    def begin(dc, loss="RMSE", n_bins=16):
+        be = cb.HipBackend()
+        try:
+            return be.begin_device_training(loss, 2, True, 1, "Cosine", bins, None, n, 2, n_bins, 0.1, 3.0,
+                                            ctr=dc)
+        finally:
+            be.end_device_training()
+
+    def make(**kw):
+        return cb.DeviceCtr(cat, kw.pop("perm", perm), kw.pop("avg", perm), kw.pop("cls", cls),
+                            kw.pop("specs", [("Borders", 0.5)]), **kw)
+
+    dc = make()
+    dc.config.averaging = None
+    assert begin(dc) is False                                   # no averaging half
+    assert begin(make(), loss="PairLogit") is False             # pair loss
+    assert begin(make(border_count=15), n_bins=8) is False      # border table longer than n_bins - 1
+    dc = make()
+    dc.columns[0].ctr_type = 3                                  # FloatTargetMeanValue
+    assert begin(dc) is False
+    dc = make()
+    dc.columns[0].n_members = 2                                 # a combination projection
+    assert begin(dc) is False
+    for mutate, code in ((lambda d: setattr(d.columns[0], "target_border_idx", 2), -2),
+                         (lambda d: setattr(d.columns[0], "weight_group", 1), -2),
+                         (lambda d: setattr(d.columns[0], "borders", None), -5)):
+        dc = make()
+        mutate(dc)
+        with pytest.raises(cb.CbhError) as e:
+            begin(dc)
+        assert e.value.code == code
+    for kw in (dict(perm=np.zeros(n, np.uint32)), dict(avg=np.array([0] * n)), dict(cls=np.full(n, 2))):
+        with pytest.raises(cb.CbhError) as e:
+            begin(make(**kw))
+        assert e.value.code == -2
+
+
+def test_ctr_border_table_reproduces_the_oracle_binarization():
+    """The border table the caller builds (next_down of the bin edges, boosting.rs:3620-3627)
+    binarizes every CTR value the oracle produces to the oracle's own bin for the default
+    priors 0, 0.5 and 1: values from skewed buckets and random classes cover tens of thousands
+    of (count, total) pairs.  With other priors the table (the reference's device
+    binarization, binarize_ctr_kernel) and the oracle's truncation formula (its CPU path) can
+    round apart, by one bin, and only for a value that sits exactly on a bin edge -- checked
+    in exact rational arithmetic."""
+    from fractions import Fraction as Fr
+
+    import numpy as np
+    from oracle import oracle as O
+    rng = np.random.default_rng(11)
+    n = 60_000
+    bucket = np.minimum(rng.zipf(1.3, n) - 1, 400).astype(np.uint32)
+    bucket, _ = O.perfect_hash(bucket)
+    perm = O.shuffled_indices(n, 3)
+    cls = (rng.random(n) < 0.4).astype(np.uint8)
+    edges_seen = 0
+    for kind, tbi in (("Borders", 0), ("Buckets", 0), ("Buckets", 1), ("BinarizedTargetMeanValue", 0),
+                      ("Counter", 0)):
+        for prior in (0.0, 0.5, 1.0, 2.5, -0.75):
+            for bc in (1, 15, 31, 255):
+                col = O.ctr_column(kind, bucket, perm, cls, prior=prior, target_border_idx=tbi, border_count=bc)
+                table = cb.ctr_borders(prior, bc)
+                got = (col["value"][:, None] > table[None, :]).sum(1)
+                bad = np.nonzero(got != col["bin"])[0]
+                if prior in (0.0, 0.5, 1.0):
+                    assert bad.size == 0, (kind, tbi, prior, bc)
+                    continue
+                pr = Fr(prior)
+                shift, norm = -min(Fr(0), pr), max(Fr(1), pr) - min(Fr(0), pr)
+                for i in bad:
+                    x = (Fr(int(col["good"][i])) + pr) / (Fr(int(col["total"][i])) + 1)
+                    assert ((x + shift) / norm * bc).denominator == 1, (kind, prior, bc, i)
+                    assert abs(int(got[i]) - int(col["bin"][i])) == 1
+                edges_seen += bad.size
+    assert edges_seen > 0   # the exact-edge case occurs in this sample

@@ -124,6 +124,69 @@ def test_config4_all_ctr_matches_oracle(weights, n_rows, iters, monkeypatch):
     _close(approx, exp["approx"])
 
 
+CONFIG4_MIX = [("Borders", 0.5), ("Buckets", 0.0, 1), ("BinarizedTargetMeanValue", 0.0), ("Counter", 0.0)]
+
+
+@pytest.mark.parametrize("specs,n_rows,iters", [("config", 200_000, 6), ("mix", 200_000, 4),
+                                                ("config", 2_000_000, 10)])
+def test_config4_device_ctr_config_matches_oracle(specs, n_rows, iters):
+    """Config 4 opened through the device CTR config (DeviceTrainConfig.ctr, runtime.rs:1174-1230):
+    the session builds both CTR materializations on the device from the bucket columns, the
+    two permutations and the border tables (build_ctr_cindex_columns, gpu_runtime/session.rs:
+    262-360).  The structure and averaging bins it holds equal the oracle's columns, and the
+    trees, leaves and approximant equal the oracle's fit over those columns -- with config 4's
+    Borders prior 0.5 spec at 200k and the full 2M rows, and with one spec of every covered
+    type (shared sorts, one weight group per (type, column)) at 200k."""
+    from catboost_rs_amd import datagen
+    from tests.test_gpu_parity import _close
+    d = datagen.config4(n_rows=n_rows)
+    P = d["params"]
+    sp = [P["ctr"]] if specs == "config" else CONFIG4_MIX
+    bc = P["ctr_border_count"]
+    n = d["target"].size
+    two = cb.shuffled_indices(n, P["random_seed"], count=2)
+    perm, avg_perm = two[0], two[0][two[1]]
+    buckets = np.stack([O.perfect_hash(k)[0] for k in d["cat_keys"]])
+    assert np.array_equal(buckets, np.stack([cb.perfect_hash(k)[0] for k in d["cat_keys"]]))
+    counts = np.array([int(b.max()) + 1 for b in buckets], np.uint32)
+    dc = cb.DeviceCtr(buckets, perm, avg_perm, d["target_class"], sp, border_count=bc, bucket_counts=counts,
+                      model_size_reg=0.5)
+
+    def oracle_cols(pm):
+        return np.stack([O.ctr_column(s[0], b, pm, d["target_class"], prior=s[1],
+                                      target_border_idx=s[2] if len(s) > 2 else 0, border_count=bc)["bin"]
+                         for b in buckets for s in sp])
+    ctr, avg = oracle_cols(perm), oracle_cols(avg_perm)
+    nb_base = d["n_borders"]
+    n_bins = int(max(nb_base.max(), bc)) + 1
+    be = cb.HipBackend()
+    assert be.begin_device_training("RMSE", 6, True, 1, "Cosine", d["bins"], None, n, nb_base.size, n_bins, 0.1,
+                                    3.0, real_folds=nb_base + 1, ctr=dc)
+    try:
+        assert np.array_equal(be.read_ctr_bins(), ctr)
+        assert np.array_equal(be.read_ctr_bins(averaging=True), avg)
+    finally:
+        be.end_device_training()
+    groups = np.array([dc.columns[k].weight_group for k in range(dc.n_columns)], np.uint32)
+    info = dict(avg_bins=avg, bucket_count=np.repeat(counts, len(sp)), group=groups, cat_buckets=buckets,
+                cat_bucket_count=counts, model_size_reg=0.5)
+    bins = np.concatenate([d["bins"], ctr], 0)
+    nb = np.concatenate([nb_base, np.full(ctr.shape[0], bc, np.uint32)])
+    kw = dict(loss="RMSE", depth=6, learning_rate=0.1, l2_leaf_reg=3.0, score="Cosine", leaf_method="Gradient",
+              bootstrap_type="Bernoulli", subsample=0.66, boost_from_average=True, random_seed=0)
+    exp = O.train(bins, nb, d["target"], iterations=iters, ctr=info, **kw)
+    assert any(f >= nb_base.size for t in exp["splits"] for f, _ in t), "no CTR split chosen"
+    tr = cb.Trainer(d["bins"], n_bins, d["target"], real_folds=nb_base + 1, device_ctr=dc, **kw)
+    try:
+        splits, leaves = tr.fit(iters)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    assert np.array_equal(splits, exp["splits"])
+    _close(leaves, exp["leaf_values"])
+    _close(approx, exp["approx"])
+
+
 def test_config4_one_hot_and_ctr_extension_matches_oracle():
     """The stated config 4 mix (categorical columns of cardinality <= 16 one-hot, the rest
     CTR) -- a combination the reference refuses -- against the oracle's extension, without

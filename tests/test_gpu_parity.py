@@ -135,6 +135,37 @@ def test_weighted_tree_matches_oracle():
     assert np.array_equal(t["leaf_of"], o["leaf_of"])
 
 
+def test_multi_output_family_is_the_approx_upload():
+    """FamilyTreeArgs::MultiOutput (runtime.rs:935-950) carries a tree's dim-major K x n
+    approximant: growing with it gives the same tree as growing with that approximant as the
+    approx argument, and a K that differs from the session's is a length mismatch."""
+    bins, nb, y, _ = datagen.random_case(5, 6_000, 9, max_borders=30)
+    n, K = y.shape[0], 3
+    cls = (np.abs(y * 7).astype(np.int64) % K).astype(np.float64)
+    approx_k = np.random.default_rng(2).standard_normal((K, n))
+    out = []
+    for mode in ("approx", "family"):
+        be = cb.HipBackend()
+        be.begin_device_training("MultiClass", 4, True, 1, "Cosine", bins, None, n, bins.shape[0],
+                                 int(nb.max()) + 1, 0.1, 3.0, approx_dim=K, leaf_method="Newton",
+                                 real_folds=nb + 1)
+        try:
+            if mode == "approx":
+                t = be.grow_tree_on_device(approx=approx_k, target=cls, want_leaf_of=True)
+            else:
+                t = be.grow_tree_on_device(target=cls, want_leaf_of=True,
+                                           family=dict(approx_k=approx_k, approx_dim=K))
+                with pytest.raises(cb.CbhError) as e:
+                    be.grow_tree_on_device(family=dict(approx_k=approx_k[:2], approx_dim=2))
+                assert e.value.code == -1
+        finally:
+            be.end_device_training()
+        out.append(t)
+    assert out[0]["splits"] == out[1]["splits"]
+    assert np.array_equal(out[0]["leaf_of"], out[1]["leaf_of"])
+    assert np.array_equal(out[0]["leaf_values"], out[1]["leaf_values"])
+
+
 # ------------------------------------------------------------------ boosting vs oracle
 CASES = [
     dict(loss="RMSE", score="Cosine", leaf_method="Gradient", bootstrap_type="No", boost_from_average=True),
@@ -217,7 +248,8 @@ def test_tiny_inputs_match_oracle(case, F, n):
 def test_no_candidate_split_is_degenerate():
     """No feature has a border: the first level has no candidate split, which the reference
     reports as CbError::Degenerate (crates/cb-train/src/tree.rs:2604-2606); the oracle
-    refuses the same input."""
+    refuses the same input.  The failed tree leaves the model as it was: the resident
+    approximant still holds the starting values afterwards."""
     g = np.random.default_rng(3)
     n, F = 1000, 4
     bins = np.zeros((F, n), np.uint8)
@@ -229,9 +261,11 @@ def test_no_candidate_split_is_degenerate():
     tr = cb.Trainer(bins, 2, y, depth=4, learning_rate=0.2, l2_leaf_reg=3.0, random_seed=42,
                     real_folds=nb + 1, **CASES[0])
     try:
+        a0 = tr.approx()
         with pytest.raises(cb.CbhError) as e:
             tr.fit(2)
         assert e.value.code == -3
+        assert np.array_equal(tr.approx(), a0)
     finally:
         tr.close()
 
