@@ -125,7 +125,7 @@ EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_version", "cbh_last_error", "cbt_open", "cbt_open_raw", "cbt_set_pairs", "cbt_step",
            "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close", "cbh_session_set_profile",
            "cbt_set_profile", "cbh_session_set_ctr", "cbt_set_ctr", "cbh_session_read_ctr_bins",
-           "cbt_open_ctr"]
+           "cbt_open_ctr", "cbh_hist_build_noalloc"]
 
 _lib = None
 
@@ -155,6 +155,7 @@ def load(path: str = LIB_PATH):
     L.cbh_hist_build.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, C.c_uint32, P,
                                  C.c_uint32, P]
     L.cbh_bootstrap.argtypes = [C.POINTER(TreeSampling), C.c_uint64, P, P]
+    L.cbh_hist_build_noalloc.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, C.c_uint32, P, P]
     L.cbt_open.argtypes = [C.POINTER(TrainParams), P, C.c_uint64, C.c_uint32, C.c_uint32, P, P, P,
                            P, C.POINTER(P)]
     L.cbh_apply_oblivious.argtypes = [P, C.c_uint64, C.c_uint32, P, P, P, P, P, C.c_uint32, C.c_uint32,

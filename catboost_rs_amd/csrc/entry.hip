@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -92,6 +93,84 @@ __global__ void pack_stats_kernel(const double* __restrict__ der, const double* 
     }
 }
 
+// ---- histogram build without allocation (cbh_hist_build_noalloc) ----
+// Device scratch of the no-allocation entry: one copy per GPU, alive until the process
+// ends.  Host code never passes `scratch` itself (its host-side name is no device address):
+// it uses the per-device address hipGetSymbolAddress returns.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr unsigned kBoundBlocks = 256;
+
+// Per-block sums of max_d |der[d][i]| and |w[i]| (the bounds cbh_hist_build takes on the
+// host), in a fixed order so the result does not depend on scheduling.
+__global__ __launch_bounds__(256) void bound_partials_kernel(const double* __restrict__ der,
+                                                             const double* __restrict__ w, uint64_t n,
+                                                             uint32_t K, double* __restrict__ part) {
+    __shared__ double sd[256], sw[256];
+    double ad = 0.0, aw = 0.0;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        double m = 0.0;
+        for (uint32_t d = 0; d < K; ++d) m = fmax(m, fabs(der[(size_t)d * n + i]));
+        ad += m;
+        aw += fabs(w[i]);
+    }
+    sd[threadIdx.x] = ad;
+    sw[threadIdx.x] = aw;
+    __syncthreads();
+    for (unsigned o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            sd[threadIdx.x] += sd[threadIdx.x + o];
+            sw[threadIdx.x] += sw[threadIdx.x + o];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        part[2 * blockIdx.x] = sd[0];
+        part[2 * blockIdx.x + 1] = sw[0];
+    }
+}
+
+// The scales of cbh_hist_build from the partial bounds (one thread, blocks in order).
+__global__ void bound_scales_kernel(const double* __restrict__ part, unsigned n_part, Scales* __restrict__ sc) {
+    if (blockIdx.x != 0 || threadIdx.x != 0) return;
+    double b[2] = {0.0, 0.0};
+    for (unsigned k = 0; k < n_part; ++k) {
+        b[0] += part[2 * k];
+        b[1] += part[2 * k + 1];
+    }
+    for (int k = 0; k < kNumScales; ++k) {
+        int e = -20;
+        if (k < 2 && b[k] > 0.0) frexp(b[k] * 1.0000001 + 1e-300, &e);
+        const int s = min(61 - e, 100);
+        sc->shift[k] = s;
+        sc->mul[k] = ldexp(1.0, s);
+        sc->inv[k] = ldexp(1.0, -s);
+    }
+}
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};   // per device: the address of that GPU's `scratch`
+
+// The calling device's scratch address, looked up once per device.
+int scratch_address(void** out) {
+    int dev = 0;
+    HIP_OK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail2(CBH_ERR_UNSUPPORTED, "device index beyond 63");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail2(CBH_ERR_DEVICE, "no device address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return CBH_OK;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
 unsigned grid_of(uint64_t work, unsigned block) {
     uint64_t g = (work + block - 1) / block;
     return (unsigned)std::max<uint64_t>(1, std::min<uint64_t>(g, 65535u * 4));
@@ -110,6 +189,20 @@ int run_fill(const uint32_t* rows, uint32_t W, uint64_t n, const uint32_t* idx,
     fill_kernel<C, false><<<G * ft.n_tiles, 1024, ft.lds_bytes, 0>>>(rows, W, W, n, idx, plan,
                                                              (const long long*)sstat, ft.n_tiles, ft.tw,
                                                              F, B, G, hist, nullptr, (int)ft.bin_major);
+    HIP_OK(hipGetLastError());
+    return CBH_OK;
+}
+
+template <int C>
+int run_fill_on(const uint32_t* rows, uint32_t W, uint64_t n, double* sstat, const Scales* sc, const FillTiles& ft,
+                uint32_t F, uint32_t B, long long* hist, hipStream_t st) {
+    quantize_stats_kernel<C><<<grid_of(n * C, 256), 256, 0, st>>>(sstat, n, sc);
+    HIP_OK(hipFuncSetAttribute((const void*)fill_kernel<C, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)ft.lds_bytes));
+    const uint32_t G = 64;
+    fill_kernel<C, false><<<G * ft.n_tiles, 1024, ft.lds_bytes, st>>>(rows, W, W, n, nullptr, nullptr,
+                                                                     (const long long*)sstat, ft.n_tiles, ft.tw,
+                                                                     F, B, G, hist, nullptr, (int)ft.bin_major);
     HIP_OK(hipGetLastError());
     return CBH_OK;
 }
@@ -268,6 +361,57 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t F, uint32_t B, c
     hist_to_f64_kernel<<<grid_of(cells, 256), 256>>>(hist.p, cells, C, F, B, dsc.p, dout.p);
     HIP_OK(hipGetLastError());
     HIP_OK(hipMemcpy(hist_out, dout.p, sizeof(double) * cells, hipMemcpyDeviceToHost));
+    return CBH_OK;
+}
+
+int cbh_hist_build_noalloc(const uint8_t* bins_fm, uint64_t n, uint32_t n_features, uint32_t n_bins,
+                           const double* der, const double* w, uint32_t K, double* hist_out, void* stream) {
+    if (!bins_fm || !der || !w || !hist_out) return fail2(CBH_ERR_INVALID_ARG, "null argument");
+    const uint32_t F = n_features, B = n_bins;
+    if (K < 1 || K > 16 || B < 1 || B > 256 || n == 0 || F == 0) return fail2(CBH_ERR_INVALID_ARG, "bad shape");
+    const uint32_t C = K + 1, W = (F + 3) / 4;
+    // scratch layout: bound partials | scales | packed rows | row statistics | int64 histogram
+    const size_t off_sc = align256(sizeof(double) * 2 * kBoundBlocks);
+    const size_t off_rows = off_sc + align256(sizeof(Scales));
+    const size_t off_sstat = off_rows + align256(sizeof(uint32_t) * (size_t)n * W);
+    const size_t off_hist = off_sstat + align256(sizeof(double) * (size_t)n * C);
+    const size_t cells = (size_t)F * B * C;
+    const size_t need = off_hist + sizeof(long long) * cells;
+    if (n >= ((size_t)1 << 32) || need > kNoAllocScratchBytes)
+        return fail2(CBH_ERR_OUT_OF_RANGE, "n x (4 ceil(F/4) + 8 (K+1)) + 8 F n_bins (K+1) bytes exceed the " +
+                                               std::to_string(kNoAllocScratchBytes >> 20) + " MiB scratch (" +
+                                               std::to_string(need) + " bytes asked)");
+    int lds_max = 0, dev = 0;
+    HIP_OK(hipGetDevice(&dev));
+    HIP_OK(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+    const FillTiles ft = plan_fill_tiles(F, B, C, std::min<size_t>((size_t)lds_max, 160 * 1024), 1, n);
+    if (ft.n_tiles == 0) return fail2(CBH_ERR_UNSUPPORTED, "histogram line too wide for LDS");
+    if (!(C <= 9 || C == 11 || C == 13 || C == 17)) return fail2(CBH_ERR_UNSUPPORTED, "K has no compiled fill variant");
+    void* base = nullptr;
+    int rc = scratch_address(&base);
+    if (rc != CBH_OK) return rc;
+    unsigned char* sp = (unsigned char*)base;
+    double* part = (double*)sp;
+    Scales* sc = (Scales*)(sp + off_sc);
+    uint32_t* rows = (uint32_t*)(sp + off_rows);
+    double* sstat = (double*)(sp + off_sstat);
+    long long* hist = (long long*)(sp + off_hist);
+    hipStream_t st = (hipStream_t)stream;
+    bound_partials_kernel<<<kBoundBlocks, 256, 0, st>>>(der, w, n, K, part);
+    bound_scales_kernel<<<1, 64, 0, st>>>(part, kBoundBlocks, sc);
+    zero_i64_kernel<<<grid_of(cells, 256), 256, 0, st>>>(hist, cells);
+    pack_rows_kernel<<<grid_of((uint64_t)n * W, 256), 256, 0, st>>>(bins_fm, n, F, W, rows);
+    pack_stats_kernel<<<grid_of(n, 256), 256, 0, st>>>(der, w, n, K, sstat);
+    HIP_OK(hipGetLastError());
+    switch (C) {
+#define CASE(c) case c: rc = run_fill_on<c>(rows, W, n, sstat, sc, ft, F, B, hist, st); break;
+        CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8) CASE(9) CASE(11) CASE(13) CASE(17)
+#undef CASE
+        default: return fail2(CBH_ERR_UNSUPPORTED, "K has no compiled fill variant");
+    }
+    if (rc != CBH_OK) return rc;
+    hist_to_f64_kernel<<<grid_of(cells, 256), 256, 0, st>>>(hist, cells, C, F, B, sc, hist_out);
+    HIP_OK(hipGetLastError());
     return CBH_OK;
 }
 

@@ -317,6 +317,21 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t n_features, uint
                    const double* der, const double* w, uint32_t K, const uint32_t* slot_of_row,
                    uint32_t n_slots, double* hist_out);
 
+/* cbh_hist_build of the whole row set (one slot) over DEVICE buffers, allocating nothing.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ *   bins_fm [n_features][n] u8, der [K][n], w [n], hist_out [n_features][n_bins][K+1] f64:
+ *   device pointers; stream: a hipStream_t (NULL = the default stream).
+ * The work is enqueued on stream and not waited for.  Packed rows, quantized statistics,
+ * the integer histogram and the scales live in a 32 MiB static device array per GPU, held
+ * until the process ends: n * (4 ceil(n_features / 4) + 8 (K + 1)) + 8 n_features n_bins
+ * (K + 1) bytes plus 5 KiB must fit, else CBH_ERR_OUT_OF_RANGE.  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (other streams, other host threads)
+ * race.  The result equals cbh_hist_build's with slot_of_row NULL (the same scale rule
+ * from the sums of max_d |der| and |w|, summed on the device). */
+int cbh_hist_build_noalloc(const uint8_t* bins_fm, uint64_t n, uint32_t n_features, uint32_t n_bins,
+                           const double* der, const double* w, uint32_t K, double* hist_out, void* stream);
+
 /* Device bootstrap (bootstrap.rs:141-184): sample weights and control mask for n rows. */
 int cbh_bootstrap(const cbh_tree_sampling* sampling, uint64_t n, double* sample_weight,
                   uint8_t* control);
