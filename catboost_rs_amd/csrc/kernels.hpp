@@ -810,14 +810,30 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     uint64_t n, const uint32_t* __restrict__ idx /* kGather: rows listed by the partition */,
     const LevelPlan* __restrict__ plan, const unsigned long long* __restrict__ spack /* [n] */,
     const unsigned long long* __restrict__ sseq /* nullable [V]: packed stats in idx order */,
-    uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
+    uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, uint32_t Gn, long long* __restrict__ hist,
     uint32_t swap_every /* blocks of rows between two swaps: 2 * swap_every * kPackIterRows * 2^pack_bits <= 2^30 */) {
     constexpr uint32_t C = 2;
     extern __shared__ unsigned long long pk[];   // [B][64] packed cells
+    // blocks: the full 64-feature tiles first, G row ranges each, (tile, range) on XCD
+    // range % 8 so the tiles of one range share its rows' lines in that XCD's L2 (blocks
+    // whose range is >= G exit); then the narrow last tile (W not a multiple of 16 words)
+    // in Gn ranges, sized by the host from the relative cost of its rows so the workgroups
+    // carry about equal work
+    const uint32_t n_full = (W % kPackTileWords) ? n_tiles - 1u : n_tiles;
+    const uint32_t full_blocks = n_full * ((G + 7u) / 8u) * 8u;
     const uint32_t b = blockIdx.x;
-    const uint32_t xcd = b & 7u, q = b >> 3;
-    const uint32_t t = q % n_tiles;
-    const uint32_t g = (q / n_tiles) * 8u + xcd;
+    uint32_t t, g, GR;
+    if (b < full_blocks) {
+        const uint32_t xcd = b & 7u, q = b >> 3;
+        t = q % n_full;
+        g = (q / n_full) * 8u + xcd;
+        GR = G;
+        if (g >= G) return;   // workgroup-uniform, before any barrier
+    } else {
+        t = n_tiles - 1u;
+        g = b - full_blocks;
+        GR = Gn;
+    }
     const uint32_t w0 = t * kPackTileWords;
     const uint32_t TW = min(kPackTileWords, W - w0);
     const uint32_t f0 = 4u * w0;
@@ -845,8 +861,8 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     for (int k = 0; k < kPackOwn; ++k) acc_d[k] = acc_w[k] = 0;
     __syncthreads();
     const uint32_t V = kGather ? plan->rows : (uint32_t)n;
-    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
-    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
+    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / GR);
+    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / GR);
     const uint32_t n_seg = kGather ? plan->n_parent : 1u;
     uint32_t seg = 0;
     if (kGather)

@@ -37,6 +37,32 @@ def test_rng_advance_matches_stepping():
     assert O.lib().orc_rng_gen(C.byref(c)) == O.lib().orc_rng_gen(C.byref(d))
 
 
+def test_std_normal_known_answers():
+    """orc_std_normal against the reference's known answers (cb-core/src/normal_test.rs:35-99):
+    seed 17's first normal rejects one uniform pair (4 draws) and its second takes 2; seeds 0
+    and 42 accept their first pair.  The draw counts are read off the generator state: after
+    the normals it equals a fresh generator advanced by that many draws."""
+    def state(r):
+        return (r.x1, r.c1, r.x2, r.c2)
+
+    r = O.rng_from_seed(17)
+    n1 = O.lib().orc_std_normal(C.byref(r))
+    a = O.rng_from_seed(17)
+    O.lib().orc_rng_advance(C.byref(a), 4)
+    assert state(r) == state(a)
+    n2 = O.lib().orc_std_normal(C.byref(r))
+    O.lib().orc_rng_advance(C.byref(a), 2)
+    assert state(r) == state(a)
+    assert abs(n1 - (-1.812286613368193e-1)) < 1e-15
+    assert abs(n2 - 2.8332477304781295e-1) < 1e-15
+    for seed, want in ((0, 6.337067335392765e-1), (42, 1.9692715540692288e-1)):
+        r = O.rng_from_seed(seed)
+        v = O.lib().orc_std_normal(C.byref(r))
+        a = O.rng_from_seed(seed)
+        O.lib().orc_rng_advance(C.byref(a), 2)
+        assert state(r) == state(a) and abs(v - want) < 1e-15, seed
+
+
 def test_real1_is_53bit_closed_interval():
     r = O.rng_from_seed(17)
     v = O.lib().orc_rng_real1(C.byref(r))

@@ -93,3 +93,56 @@ def ctr_tree_matches(u, fit, splits, leaves, t, bins_avg_float):
             got.append((1, tb, float(np.float32(np.float32(b) + np.float32(1)) - np.float32(2.0 ** -20))))
     exp = [(k, i, float(np.float32(b))) for k, i, b in u["trees"][t]]
     return got == exp and np.allclose(leaves, u["leaf_values"][t], rtol=1e-9, atol=1e-15)
+
+
+def level_tie_levels(bins, splits_a, splits_b):
+    """Levels where two oblivious trees choose different float splits that are tied in exact
+    arithmetic whatever the row statistics: before the level both trees hold the same leaf
+    partition (as sets of rows), and in every leaf the two candidates send the same rows to
+    one side -- TRUE of one is TRUE or FALSE of the other.  The score (Cosine or L2) is a sum
+    over (leaf, side) of terms that depend on that side's rows only, so such candidates fold
+    the same terms in another order and their exact scores are equal.  Returns the tied
+    levels; raises AssertionError when a differing level is not such a tie."""
+    n = bins.shape[1]
+    ia = np.zeros(n, np.int64)
+    ib = np.zeros(n, np.int64)
+    tied = []
+    for lvl, ((fa, ba), (fb, bb)) in enumerate(zip(splits_a, splits_b)):
+        pa = bins[int(fa)] > ba
+        pb = bins[int(fb)] > bb
+        pairs = np.unique(np.stack([ia, ib]), axis=1)
+        assert pairs.shape[1] == np.unique(ia).size == np.unique(ib).size, \
+            f"level {lvl}: the leaf partitions before the level differ"
+        if (int(fa), int(ba)) != (int(fb), int(bb)):
+            for leaf in np.unique(ia):
+                rows = ia == leaf
+                same = np.array_equal(pa[rows], pb[rows])
+                swapped = np.array_equal(pa[rows], ~pb[rows])
+                assert same or swapped, f"level {lvl}: candidates ({fa},{ba}) and ({fb},{bb}) split a leaf differently"
+            tied.append(lvl)
+        ia |= pa.astype(np.int64) << lvl
+        ib |= pb.astype(np.int64) << lvl
+    return tied
+
+
+def exact_cosine_terms(bins, prior_splits, cand, der, w, lam):
+    """Numerator and denominator of the Cosine score of candidate ``cand`` = (feature, bin)
+    after the levels ``prior_splits``, in exact rational arithmetic over the f64 inputs:
+    sum over (leaf, side) of avg * s and avg^2 * W, s = sum w der, W = sum w,
+    avg = s / (W + lam) when W > 0 (score.rs:93-147, leaf.rs:161)."""
+    from fractions import Fraction as Fr
+    leaf = np.zeros(bins.shape[1], np.int64)
+    for lvl, (f, b) in enumerate(prior_splits):
+        leaf |= (bins[int(f)] > b).astype(np.int64) << lvl
+    side = bins[int(cand[0])] > cand[1]
+    lam = Fr(float(lam))
+    num, den = Fr(0), Fr(0)
+    for key in np.unique(leaf * 2 + side):
+        rows = np.nonzero(leaf * 2 + side == key)[0]
+        s = sum((Fr(float(w[i])) * Fr(float(der[i])) for i in rows), Fr(0))
+        W = sum((Fr(float(w[i])) for i in rows), Fr(0))
+        if W > 0:
+            avg = s / (W + lam)
+            num += avg * s
+            den += avg * avg * W
+    return num, den
