@@ -81,8 +81,10 @@ def _workload(args):
 
     if args.config == 1:
         return datagen.config1(scale=args.rows / 100_000 if args.rows else 1.0)
-    if args.config == 2:
+    if args.config == 2 and args.quantile_borders:
         return datagen.config2(n_rows=args.rows or 10_000_000, n_features=args.features or 200)
+    if args.config == 2:
+        return _config2_raw(args.rows or 10_000_000, args.features or 200)
     if args.config == 3:
         return datagen.config3(n_rows=args.rows or 1_000_000, n_features=args.features or 100,
                                loss="PairLogitPairwise" if args.pairwise else "PairLogit")
@@ -91,6 +93,25 @@ def _workload(args):
     if args.config == 5:
         return datagen.config5(n_rows=args.rows or 1_000_000, n_features=args.features or 4096)
     raise SystemExit(f"--config {args.config}: configs 1 to 5 are measured")
+
+
+def _config2_raw(n, F):
+    """Config 2 as a user feeds it: raw f32 columns, 254 GreedyLogSum borders selected on the
+    device (cbh_select_borders), the session opened over the raw float channel (the device
+    quantizes the columns).  Border selection is timed here, outside the boosting steps."""
+    import numpy as np
+
+    import catboost_rs_amd as cb
+    from catboost_rs_amd import datagen
+
+    d = datagen.config2_raw(n_rows=n, n_features=F)
+    P = d["params"]
+    t0 = time.perf_counter()
+    borders = cb.select_borders(d["floats"], P["border_count"], "Min", P["border_type"])
+    d["borders_s"] = time.perf_counter() - t0
+    d["borders"] = borders
+    d["n_borders"] = np.array([b.size for b in borders], np.uint32)
+    return d
 
 
 def _config4(n):
@@ -204,6 +225,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--pairwise", action="store_true", help="config 3 with PairLogitPairwise")
+    ap.add_argument("--quantile-borders", action="store_true",
+                    help="config 2 from host bins over quantile borders instead of raw floats")
     ap.add_argument("--steps", type=int, default=0)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--rows", type=int, default=0)
@@ -244,21 +267,29 @@ def main():
     cb.load()
     t0 = time.perf_counter()
     data = _workload(args)
-    bins, nb, y = data["bins"], data["n_borders"], data["target"]
+    raw = "floats" in data
+    bins, nb, y = data.get("bins"), data["n_borders"], data["target"]
     P = data["params"]
-    F, n = bins.shape
+    F, n = (data["floats"] if raw else bins).shape
     n_bins = int(nb.max()) + 1
     kw = _train_kwargs(P)
     pairs, go = data.get("pairs"), data.get("group_offsets")
     log(f"data: config {args.config} {P['loss']}: {n} x {F}, max borders {int(nb.max())}"
         + (f", {len(pairs[0])} pairs" if pairs is not None else "")
+        + (f", {P['border_type']} borders selected on the device in {data['borders_s']:.3f}s" if raw else "")
         + f", generated in {time.perf_counter() - t0:.1f}s")
 
     t0 = time.perf_counter()
     ctr = data.get("ctr")
-    tr = cb.Trainer(bins, n_bins, y, real_folds=nb + 1, profile=False, pairs=pairs, group_offsets=go, ctr=ctr,
-                    **kw)
-    log(f"session open (upload + pack) {time.perf_counter() - t0:.2f}s")
+
+    def open_trainer(profile):
+        if raw:   # raw f32 columns: the device quantizes them
+            return cb.Trainer.from_floats(data["floats"], data["borders"], y, profile=profile, **kw)
+        return cb.Trainer(bins, n_bins, y, real_folds=nb + 1, profile=profile, pairs=pairs, group_offsets=go,
+                          ctr=ctr, **kw)
+
+    tr = open_trainer(False)
+    log(f"session open (upload{' + device quantize' if raw else ''} + pack) {time.perf_counter() - t0:.2f}s")
     for _ in range(args.warmup):
         tr.step()
     # timed region: trees as a caller runs them (after the first, each tree replays one
@@ -316,6 +347,10 @@ def main():
         from oracle import oracle as O
 
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        if raw:   # the oracle's bins: the same borders, quantized on the host (bin_of)
+            from catboost_rs_amd import datagen
+
+            bins = datagen.quantize_columns(data["floats"], data["borders"])
         t0 = time.perf_counter()
         exp = O.train(bins, nb, y, iterations=cpu_trees, n_threads=threads, pairs=pairs, ctr=ctr, **kw)
         cpu_wall = time.perf_counter() - t0
@@ -325,14 +360,16 @@ def main():
                          f"(CPU restatement of the reference algorithm, OpenMP over features)"}
         log(f"cpu: {cpu_trees} trees in {cpu_wall:.1f}s on {threads} threads")
         # the CPU trees must be the GPU run's first trees (parity on the full-size workload)
-        tr2 = cb.Trainer(bins, n_bins, y, real_folds=nb + 1, pairs=pairs, group_offsets=go, ctr=ctr, **kw)
+        tr2 = open_trainer(False)
         first, _ = tr2.fit(cpu_trees)
         tr2.close()
         cpu["splits_match_gpu"] = bool(np.array_equal(first, exp["splits"]))
 
     fill_kernel = {0: "fill_kernel", 1: "fill_packed_kernel", 2: "fill_split_kernel"}[st["fill_mode"]]
     names = {1: "config1: RMSE, no bootstrap, depth 6, 128 borders",
-             2: "config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 borders",
+             2: ("config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 GreedyLogSum borders selected on the "
+                 "device from the raw f32 columns, quantized on the device" if raw else
+                 "config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 quantile borders (host bins)"),
              3: f"config3: {P['loss']}, groups of 20, ~10 pairs per group, depth 6, 254 borders",
              4: "config4: RMSE, Bernoulli 0.66, depth 6, 30 float (254 borders) + 20 categorical as "
                 "Borders CTR columns (prior 0.5, 16 bins; model_size_reg 0.5, averaging-permutation leaves)",
@@ -351,7 +388,7 @@ def main():
         "dtype": "u8 bins, int64 fixed-point sums, f64 scores",
         "fill": {0: "two-channel 32-feature tiles", 1: f"packed 64-feature tiles ({st['fill_pack_bits']}-bit rows)",
                  2: "channel-split 64-feature tiles"}[st["fill_mode"]],
-        "data": f"synthetic (seeded; datagen.config{args.config})",
+        "data": f"synthetic (seeded; datagen.config{args.config}{'_raw' if raw else ''})",
         "config": {"workload": names[args.config], "rows": n, "features": F, "depth": P["depth"],
                    "parallelism": "single GPU"},
         "hist_rows_features_per_s": round(st["fill_row_features"] / fill_s, 1) if fill_s else None,
@@ -370,6 +407,8 @@ def main():
     }
     if "ctr_s" in data:
         out["ctr_columns_s"] = round(data["ctr_s"], 4)
+    if raw:
+        out["select_borders_s"] = round(data["borders_s"], 4)
     print(json.dumps(out), flush=True)
 
 

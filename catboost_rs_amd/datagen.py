@@ -99,6 +99,40 @@ def config2_floats(n_rows=10_000_000, n_features=200, seed=1, threads=None):
     return X
 
 
+def config2_raw(n_rows=10_000_000, n_features=200, seed=1, threads=None):
+    """Config 2 before quantization: the f32 columns of ``config2_floats`` and config 2's
+    labels (the same streams: Bernoulli(sigmoid(X[:, :20].w))), for a caller that selects
+    the borders itself (GreedyLogSum, 254) and quantizes on the device."""
+    X = config2_floats(n_rows, n_features, seed, threads)
+    n = X.shape[1]
+    g = np.random.default_rng([seed, 10_000])
+    w = g.uniform(-1, 1, 20)
+    logit = np.zeros(n)
+    for f in range(min(20, n_features)):
+        logit += X[f].astype(np.float64) * w[f]
+    p = 1.0 / (1.0 + np.exp(-logit))
+    y = (g.random(n) < p).astype(np.float64)
+    return dict(name="config2", floats=X, target=y,
+                params=dict(loss="Logloss", depth=6, iterations=200, learning_rate=0.03, l2_leaf_reg=3.0,
+                            score="Cosine", leaf_method="Gradient", bootstrap_type="Bayesian",
+                            bagging_temperature=1.0, boost_from_average=False, random_seed=0,
+                            border_count=254, border_type="GreedyLogSum"))
+
+
+def quantize_columns(X, borders, threads=None):
+    """Host bins [F][n] u8 of f32 columns: bin_of, the count of borders strictly below each
+    value (NaN-free columns)."""
+    F, n = X.shape
+    bins = np.empty((F, n), np.uint8)
+
+    def work(f):
+        bins[f] = _quantize(X[f], np.asarray(borders[f], np.float64))
+
+    with cf.ThreadPoolExecutor(threads or min(16, os.cpu_count() or 4)) as ex:
+        list(ex.map(work, range(F)))
+    return bins
+
+
 def config2(scale=1.0, seed=1, n_rows=None, n_features=200):
     """Logloss: n x 200 (half N(0,1), half lognormal(0,1)); 254 borders; labels
     Bernoulli(sigmoid(X[:, :20].w)); depth 6, 200 iterations, Bayesian bootstrap T=1."""

@@ -175,3 +175,26 @@ def test_config1_from_floats_end_to_end():
                   l2_leaf_reg=3.0, score="Cosine", boost_from_average=True)
     assert np.array_equal(splits, exp["splits"])
     np.testing.assert_allclose(approx, exp["approx"], rtol=1e-5, atol=1e-9)
+
+
+def test_config2_from_raw_floats_matches_oracle():
+    """Config 2 at 200k rows from its raw f32 columns, as the benchmark feeds it: the 254
+    GreedyLogSum borders selected on the device equal the oracle's for all 200 columns, and
+    the session over the raw float channel (device quantization) grows the oracle's trees."""
+    from tests.test_gpu_parity import _close
+    d = datagen.config2_raw(n_rows=200_000)
+    X, P = d["floats"], d["params"]
+    borders = cb.select_borders(X, P["border_count"], "Min", P["border_type"])
+    exp_b = [oracle_borders_of(X[f], P["border_count"], "Min", P["border_type"]) for f in range(X.shape[0])]
+    _same_sets(borders, exp_b, "config2")
+    nb = np.array([b.size for b in exp_b], np.uint32)
+    bins = np.stack([O.quantize(X[f], exp_b[f]) for f in range(X.shape[0])])
+    kw = dict(loss=P["loss"], depth=P["depth"], learning_rate=P["learning_rate"], l2_leaf_reg=P["l2_leaf_reg"],
+              score=P["score"], leaf_method=P["leaf_method"], bootstrap_type=P["bootstrap_type"],
+              bagging_temperature=P["bagging_temperature"], boost_from_average=P["boost_from_average"],
+              random_seed=P["random_seed"])
+    splits, leaves, approx = _fit(cb.Trainer.from_floats(X, borders, d["target"], **kw), 8)
+    exp = O.train(bins, nb, d["target"], iterations=8, n_threads=16, **kw)
+    assert np.array_equal(splits, exp["splits"])
+    _close(leaves, exp["leaf_values"])
+    _close(approx, exp["approx"])
