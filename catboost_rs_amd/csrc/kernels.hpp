@@ -92,24 +92,32 @@ static __global__ void pack_rows_kernel(const uint8_t* __restrict__ cols, uint64
     }
 }
 
-// Tile-major packing for the 64-feature fills: tile t (words [16t, 16t + TW_t), TW_t = min(16,
-// W - 16t)) of row r at trows[n * 16t + r * TW_t + w], so a workgroup of a tile streams its rows
-// contiguously (64 bytes per row of a full tile).
+// Tile-major packing for the packed fill: tile t (words [16t, 16t + TW_t), TW_t = min(16,
+// W - 16t)) of row r at trows[n * 16t + r * TS_t + w], so a workgroup of a tile streams its rows
+// contiguously.  TS_t = 2^(shift - 2) words: 16 (64 bytes) for a full tile, the next power of
+// two of TW for a narrow last tile (its padding words are zero), so a row's offset is one
+// shift whatever the tile.
+__host__ __device__ inline uint32_t packed_slice_shift(uint32_t TW) {
+    uint32_t sh = 2;
+    while ((1u << sh) < 4u * TW) ++sh;
+    return sh;
+}
+__host__ __device__ inline uint32_t packed_slice_words(uint32_t TW) { return 1u << (packed_slice_shift(TW) - 2); }
+
 static __global__ void pack_tiles_kernel(const uint8_t* __restrict__ cols, uint64_t n, uint32_t F, uint32_t W,
-                                         uint32_t* __restrict__ trows) {
-    const uint64_t total = n * W;
+                                         uint32_t* __restrict__ trows, uint64_t total /* words of trows */) {
     for (uint64_t o = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
          o += (uint64_t)gridDim.x * blockDim.x) {
         const uint32_t t = (uint32_t)(o / (n * 16u));
         const uint32_t w0 = 16u * t;
-        const uint32_t TW = min(16u, W - w0);
+        const uint32_t TS = packed_slice_words(min(16u, W - w0));   // words per row in the slice
         const uint64_t rem = o - (uint64_t)n * w0;
-        const uint64_t r = rem / TW;
-        const uint32_t w = (uint32_t)(rem - r * TW) + w0;
+        const uint64_t r = rem / TS;
+        const uint32_t w = (uint32_t)(rem - r * TS) + w0;
         uint32_t word = 0;
         for (uint32_t k = 0; k < 4; ++k) {
             const uint32_t f = 4 * w + k;
-            if (f < F) word |= (uint32_t)cols[(size_t)f * n + r] << (8 * k);
+            if (w < W && f < F) word |= (uint32_t)cols[(size_t)f * n + r] << (8 * k);
         }
         trows[o] = word;
     }
@@ -608,9 +616,10 @@ constexpr uint32_t kPackStride = 64;        // LDS cells per bin row
 constexpr uint32_t kPackThreads = 1024;     // 16 waves, one workgroup per CU
 constexpr uint32_t kPackIterRows = 1024;    // rows of the workgroup per block (between two swaps)
 constexpr int kPackOwn = 16;                // cells per thread: 64 x 256 / 1024
+constexpr uint32_t kPackCells = kPackStride * 256;   // LDS cells of a packed tile (any B <= 256)
+static_assert(kPackOwn * kPackThreads == kPackCells, "every thread owns kPackOwn cells");
 constexpr int kPackBitsDefault = 19;        // 2 * 1024 * 2^19 = 2^30 < 2^31
 constexpr int kPackHalf = 8;                // passes per half block of a full tile (64 rows each)
-constexpr int kPackRowsPart = 4;            // rows in flight per lane, a partial last tile
 
 // Decode a swapped cell: no weight is negative (the session checks), so the weight field is a
 // sum of non-negative values below 2^31 that never borrows from the der field.
@@ -627,10 +636,7 @@ __device__ __forceinline__ void packed_flush_channel(unsigned long long* __restr
                                                     long long* __restrict__ dst_plane /* hist + ((slot*C+ch)*F)*B */) {
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kPackOwn; ++k) {
-        const uint32_t i = threadIdx.x + (uint32_t)k * kPackThreads;
-        if (i < kPackStride * B) pk[i] = (unsigned long long)acc[k];
-    }
+    for (int k = 0; k < kPackOwn; ++k) pk[threadIdx.x + (uint32_t)k * kPackThreads] = (unsigned long long)acc[k];
     __syncthreads();
     const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
     const uint32_t vcells = nfb * nbb * 64;
@@ -668,20 +674,30 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 __device__ __forceinline__ uint32_t ldw(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
+constexpr uint32_t kPastEnd = 0xFFFFFFF0u;   // a byte offset past every packed-fill buffer
+
 __device__ __forceinline__ unsigned long long ldq(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
     return (unsigned long long)v[0] | ((unsigned long long)v[1] << 32);
 }
 
 // Swap the cells a thread owns with zero and add their decoded fields to its registers.
-// The cells of thread t are t + k * kPackThreads for k < own_n (a thread's column t % 64 is the
-// same for all k; a column >= TF is never touched and not swapped).
-__device__ __forceinline__ void packed_swap(unsigned long long* __restrict__ pk, uint32_t own_n,
+// The cells of thread t are t + k * kPackThreads, k < kPackOwn: the LDS always holds 256 bin
+// rows, so every thread owns kPackOwn cells and the swaps carry no per-cell branch (the LDS
+// exchanges issue back to back and return together).  Cells of bins >= B, or of columns
+// >= TF (the zero padding of a partial last word), are swapped too and never flushed.
+__device__ __forceinline__ void packed_swap(unsigned long long* __restrict__ pk,
                                             long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
     unsigned long long* c = pk + threadIdx.x;
+    constexpr int kBatch = 4;   // exchanges in flight: few registers beyond the accumulators
 #pragma unroll
-    for (int k = 0; k < kPackOwn; ++k)
-        if ((uint32_t)k < own_n) unpack_add_nonneg(atomicExch(c + (uint32_t)k * kPackThreads, 0ull), acc_d[k], acc_w[k]);
+    for (int k0 = 0; k0 < kPackOwn; k0 += kBatch) {
+        unsigned long long v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) v[j] = atomicExch(c + (uint32_t)(k0 + j) * kPackThreads, 0ull);
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) unpack_add_nonneg(v[j], acc_d[k0 + j], acc_w[k0 + j]);
+    }
 }
 
 // Broadcast lane U of each 16-lane DPP row to the row (row_newbcast).
@@ -694,8 +710,8 @@ __device__ __forceinline__ unsigned long long row_bcast64(unsigned long long v) 
     return (unsigned long long)row_bcast<U>((uint32_t)v) | ((unsigned long long)row_bcast<U>((uint32_t)(v >> 32)) << 32);
 }
 
-// The rows [pos, end) of a FULL tile (16 words: the 16 lanes of a row are one 16-lane DPP row of
-// the wave, 4 rows per wave, passes of 64 rows), in blocks of kPackIterRows = 16 passes, each
+// The rows [pos, end) of a tile (up to 16 words: the 16 lanes of a row are one 16-lane DPP row
+// of the wave, 4 rows per wave, passes of 64 rows), in blocks of kPackIterRows = 16 passes, each
 // block in two halves of 8 passes.  Lane w of a DPP row loads the packed statistic (and,
 // gathered, the row index) of that row's pass w; pass u broadcasts lane u to the row's 16 lanes
 // (row_newbcast), so statistics and indices cost one load per row and no LDS round trip -- the
@@ -704,23 +720,24 @@ __device__ __forceinline__ unsigned long long row_bcast64(unsigned long long v) 
 // half of block j is consumed, so they are in flight across the other half, the barrier and the
 // swap.  Rows past the range carry a zero statistic (their atomics add nothing).
 template <bool kGather>
-__device__ __forceinline__ void packed_range_full(unsigned long long* __restrict__ pk,
-                                                  __amdgpu_buffer_rsrc_t rbase, uint32_t stride4, uint32_t wl4,
+__device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk,
+                                             __amdgpu_buffer_rsrc_t rbase, uint32_t sh, uint32_t wl4,
                                                   uint32_t wl, __amdgpu_buffer_rsrc_t idx,
                                                   __amdgpu_buffer_rsrc_t sbase, uint32_t pos,
                                                   uint32_t end, uint32_t r0, uint32_t rot, const uint32_t* off8,
-                                                  uint32_t swap_every, uint32_t own_n,
+                                                  uint32_t swap_every,
                                                   long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
     constexpr uint32_t rpp = kPackThreads / kPackTileWords;   // 64 rows per pass
     static_assert(2 * kPackHalf * rpp == kPackIterRows && kPackHalf == 8, "block layout");
     uint32_t six, six_n = 0;
     unsigned long long ssv, ssv_n = 0;
-    auto stage = [&](uint32_t bb, uint32_t& ix, unsigned long long& sv) {   // this lane: pass wl of block bb
+    // this lane: pass wl of block bb.  A row past the range reads its statistic from past the
+    // end of the buffer, which returns 0 (buffer range checking), so no select waits on the load
+    auto stage = [&](uint32_t bb, uint32_t& ix, unsigned long long& sv) {
         const uint32_t p = bb + r0 + wl * rpp;
-        const uint32_t pc = p < end ? p : bb;
-        ix = kGather ? ldw(idx, 4u * pc) : pc;
-        sv = ldq(sbase, 8u * pc);
-        if (p >= end) sv = 0ull;
+        const bool ok = p < end;
+        ix = kGather ? ldw(idx, 4u * (ok ? p : bb)) : (ok ? p : bb);
+        sv = ldq(sbase, ok ? 8u * p : kPastEnd);
     };
     // row index of pass U (this lane's DPP row) from the staged indices of a block
 #define CBH_DOC(U, SIX) (kGather ? row_bcast<U>(SIX) : row_bcast<U>(SIX))
@@ -728,15 +745,15 @@ __device__ __forceinline__ void packed_range_full(unsigned long long* __restrict
     uint32_t base = pos;
     stage(base, six, ssv);
 #define CBH_LOADA(SIX)                                                                       \
-    wA[0] = ldw(rbase, (CBH_DOC(0, SIX) << 6) + wl4); wA[1] = ldw(rbase, (CBH_DOC(1, SIX) << 6) + wl4); \
-    wA[2] = ldw(rbase, (CBH_DOC(2, SIX) << 6) + wl4); wA[3] = ldw(rbase, (CBH_DOC(3, SIX) << 6) + wl4); \
-    wA[4] = ldw(rbase, (CBH_DOC(4, SIX) << 6) + wl4); wA[5] = ldw(rbase, (CBH_DOC(5, SIX) << 6) + wl4); \
-    wA[6] = ldw(rbase, (CBH_DOC(6, SIX) << 6) + wl4); wA[7] = ldw(rbase, (CBH_DOC(7, SIX) << 6) + wl4);
+    wA[0] = ldw(rbase, (CBH_DOC(0, SIX) << sh) + wl4); wA[1] = ldw(rbase, (CBH_DOC(1, SIX) << sh) + wl4); \
+    wA[2] = ldw(rbase, (CBH_DOC(2, SIX) << sh) + wl4); wA[3] = ldw(rbase, (CBH_DOC(3, SIX) << sh) + wl4); \
+    wA[4] = ldw(rbase, (CBH_DOC(4, SIX) << sh) + wl4); wA[5] = ldw(rbase, (CBH_DOC(5, SIX) << sh) + wl4); \
+    wA[6] = ldw(rbase, (CBH_DOC(6, SIX) << sh) + wl4); wA[7] = ldw(rbase, (CBH_DOC(7, SIX) << sh) + wl4);
 #define CBH_LOADB(SIX)                                                                       \
-    wB[0] = ldw(rbase, (CBH_DOC(8, SIX) << 6) + wl4); wB[1] = ldw(rbase, (CBH_DOC(9, SIX) << 6) + wl4); \
-    wB[2] = ldw(rbase, (CBH_DOC(10, SIX) << 6) + wl4); wB[3] = ldw(rbase, (CBH_DOC(11, SIX) << 6) + wl4); \
-    wB[4] = ldw(rbase, (CBH_DOC(12, SIX) << 6) + wl4); wB[5] = ldw(rbase, (CBH_DOC(13, SIX) << 6) + wl4); \
-    wB[6] = ldw(rbase, (CBH_DOC(14, SIX) << 6) + wl4); wB[7] = ldw(rbase, (CBH_DOC(15, SIX) << 6) + wl4);
+    wB[0] = ldw(rbase, (CBH_DOC(8, SIX) << sh) + wl4); wB[1] = ldw(rbase, (CBH_DOC(9, SIX) << sh) + wl4); \
+    wB[2] = ldw(rbase, (CBH_DOC(10, SIX) << sh) + wl4); wB[3] = ldw(rbase, (CBH_DOC(11, SIX) << sh) + wl4); \
+    wB[4] = ldw(rbase, (CBH_DOC(12, SIX) << sh) + wl4); wB[5] = ldw(rbase, (CBH_DOC(13, SIX) << sh) + wl4); \
+    wB[6] = ldw(rbase, (CBH_DOC(14, SIX) << sh) + wl4); wB[7] = ldw(rbase, (CBH_DOC(15, SIX) << sh) + wl4);
 #define CBH_ATOMS(W, U0, SSV)                                                                \
     packed_row_atomics(pk, W[0], rot, off8, row_bcast64<U0 + 0>(SSV));                       \
     packed_row_atomics(pk, W[1], rot, off8, row_bcast64<U0 + 1>(SSV));                       \
@@ -762,7 +779,7 @@ __device__ __forceinline__ void packed_range_full(unsigned long long* __restrict
         if (++blk >= swap_every || !more) {
             blk = 0;
             __syncthreads();
-            packed_swap(pk, own_n, acc_d, acc_w);
+            packed_swap(pk, acc_d, acc_w);
         }
         if (!more) break;
         base = nb;
@@ -771,37 +788,6 @@ __device__ __forceinline__ void packed_range_full(unsigned long long* __restrict
 #undef CBH_LOADB
 #undef CBH_LOADA
 #undef CBH_DOC
-}
-
-// One block of at most kPackIterRows rows of a partial tile (TW < 16 words): per-lane loads.
-template <bool kGather>
-__device__ __forceinline__ void packed_block_part(unsigned long long* __restrict__ pk,
-                                                  __amdgpu_buffer_rsrc_t rbase, uint32_t stride4, uint32_t wl4,
-                                                  __amdgpu_buffer_rsrc_t idx,
-                                                  __amdgpu_buffer_rsrc_t sbase, bool seq,
-                                                  uint32_t base, uint32_t end, uint32_t r0, uint32_t rpp,
-                                                  uint32_t un, bool lane_on, uint32_t rot, const uint32_t* off8) {
-    uint32_t pu[kPackRowsPart], vmask = 0;
-#pragma unroll
-    for (int u = 0; u < kPackRowsPart; ++u) {
-        const uint32_t p = base + r0 + (uint32_t)u * rpp;
-        const bool v = lane_on && (uint32_t)u < un && p < end;
-        vmask |= (v ? 1u : 0u) << u;
-        pu[u] = v ? p : base;
-    }
-    uint32_t doc[kPackRowsPart];
-#pragma unroll
-    for (int u = 0; u < kPackRowsPart; ++u) doc[u] = kGather ? ldw(idx, 4u * pu[u]) : pu[u];
-    unsigned long long st[kPackRowsPart];
-    uint32_t word[kPackRowsPart];
-#pragma unroll
-    for (int u = 0; u < kPackRowsPart; ++u) {
-        st[u] = ldq(sbase, 8u * ((kGather && seq) ? pu[u] : doc[u]));
-        word[u] = ldw(rbase, doc[u] * stride4 + wl4);
-    }
-#pragma unroll
-    for (int u = 0; u < kPackRowsPart; ++u)
-        if (((vmask >> u) & 1u) && st[u] != 0ull) packed_row_atomics(pk, word[u], rot, off8, st[u]);
 }
 
 template <bool kGather>
@@ -838,20 +824,17 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     const uint32_t TW = min(kPackTileWords, W - w0);
     const uint32_t f0 = 4u * w0;
     const uint32_t TF = min(4u * TW, F - f0);
-    const bool full = TW == kPackTileWords && (!kGather || sseq != nullptr);   // workgroup-uniform
-    for (uint32_t i = threadIdx.x; i < kPackStride * B; i += kPackThreads) pk[i] = 0ull;
-    // lanes: TW per row; partial tiles make un passes of rpp rows, at most kPackIterRows rows
-    const uint32_t rpp = min(kPackThreads / TW, kPackIterRows);
-    const uint32_t un = min((uint32_t)kPackRowsPart, kPackIterRows / rpp);
-    const uint32_t iter_rows = un * rpp;
-    const uint32_t r0 = threadIdx.x / TW;
-    const uint32_t wl = threadIdx.x - r0 * TW;
-    const bool lane_on = r0 < rpp;
+    const uint32_t sh = packed_slice_shift(TW);   // a row of this tile's slice: 2^sh bytes
+    for (uint32_t i = threadIdx.x; i < kPackCells; i += kPackThreads) pk[i] = 0ull;
+    // lanes: a 16-lane DPP row per row; a narrow tile's lanes past its words read the zero
+    // padding of the slice (or the next row's words) and add to LDS columns >= TF, never read
+    constexpr uint32_t rpp = kPackThreads / kPackTileWords;
+    const uint32_t r0 = threadIdx.x / kPackTileWords;
+    const uint32_t wl = threadIdx.x % kPackTileWords;
     // the word is rotated right by rot bytes once per row, so step k reads byte k of the rotated
     // word: feature 4 * wl + ((k + rot) & 3).  rot = (wl / 4 + r) mod 4 makes the 16 lanes of a
     // row hit 16 distinct features mod 16 and any two rows 32 distinct features mod 32, i.e.
-    // distinct bank pairs of the [bin][64] cells whatever the bins.  Bytes past the tile's last
-    // feature (a partial last word: zero padding) land in LDS columns >= TF, never read.
+    // distinct bank pairs of the [bin][64] cells whatever the bins.
     const uint32_t rot = ((wl >> 2) + (r0 & 1u)) & 3u;
     uint32_t off8[4];   // byte offset of the column of step k
 #pragma unroll
@@ -867,35 +850,19 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     uint32_t seg = 0;
     if (kGather)
         while (seg + 1 < n_seg && plan->seg_begin[seg + 1] <= rb) ++seg;
-    // tile-major rows: this tile's slice starts at word n * w0, TW words per row
-    const __amdgpu_buffer_rsrc_t rbase = make_rsrc(rows + n * w0, n * TW * 4u);
-    const uint32_t stride4 = 4u * TW, wl4 = 4u * wl;
-    const uint32_t own_n = ((threadIdx.x & (kPackStride - 1u)) < TF && threadIdx.x < kPackStride * B)
-                               ? (kPackStride * B - threadIdx.x + kPackThreads - 1) / kPackThreads
-                               : 0u;
-    const bool seq = kGather && sseq != nullptr;
-    const __amdgpu_buffer_rsrc_t sbase = make_rsrc(seq ? sseq : spack, n * 8u);
+    // tile-major rows: this tile's slice starts at word n * w0, 2^sh bytes per row
+    const __amdgpu_buffer_rsrc_t rbase = make_rsrc(rows + n * w0, (uint64_t)n << sh);
+    const uint32_t wl4 = 4u * wl;
+    const __amdgpu_buffer_rsrc_t sbase = make_rsrc(kGather ? sseq : spack, n * 8u);
     const __amdgpu_buffer_rsrc_t ibase = make_rsrc(kGather ? (const void*)idx : (const void*)spack, kGather ? n * 4u : 0u);
     uint32_t pos = rb;
     while (pos < re) {
         const uint32_t seg_end = (kGather && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = kGather ? plan->built[seg] : 0u;
-        if (end > pos && full) {
-            packed_range_full<kGather>(pk, rbase, stride4, wl4, wl, ibase, sbase, pos, end, r0, rot, off8,
-                                       swap_every, own_n, acc_d, acc_w);
-        } else if (end > pos) {
-            uint32_t blk = 0;
-            for (uint32_t base = pos; base < end; base += iter_rows) {   // workgroup-uniform
-                packed_block_part<kGather>(pk, rbase, stride4, wl4, ibase, sbase, seq, base, end, r0, rpp, un, lane_on,
-                                           rot, off8);
-                if (++blk < swap_every && base + iter_rows < end) continue;
-                blk = 0;
-                __syncthreads();
-                packed_swap(pk, own_n, acc_d, acc_w);
-            }
-        }
         if (end > pos) {
+            packed_range<kGather>(pk, rbase, sh, wl4, wl, ibase, sbase, pos, end, r0, rot, off8, swap_every,
+                                  acc_d, acc_w);
             // every contribution of the segment is in the registers now (the last swap follows
             // the last barrier); flush both channels, then clear the cells and registers
             long long* hd = hist + (size_t)slot * C * F * B;
@@ -904,8 +871,7 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
             __syncthreads();
 #pragma unroll
             for (int k = 0; k < kPackOwn; ++k) {
-                const uint32_t i = threadIdx.x + (uint32_t)k * kPackThreads;
-                if (i < kPackStride * B) pk[i] = 0ull;
+                pk[threadIdx.x + (uint32_t)k * kPackThreads] = 0ull;
                 acc_d[k] = acc_w[k] = 0;
             }
             __syncthreads();
@@ -913,6 +879,7 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
         pos = end;
         ++seg;
     }
+    (void)rpp;
 }
 
 // ---------------------------------------------------------------------------------

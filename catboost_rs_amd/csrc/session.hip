@@ -545,7 +545,8 @@ int plan_fill_mode(cbh_session* s) {
     int lds_max = 0, cus = 0, per_cu = 0;
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device));
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
-    const size_t lds = (size_t)kPackStride * s->B * sizeof(unsigned long long);
+    // packed: every thread owns kPackOwn cells of a 256-bin tile whatever B (branch-free swaps)
+    const size_t lds = (want_packed ? (size_t)kPackCells : (size_t)kPackStride * s->B) * sizeof(unsigned long long);
     if (lds > (size_t)lds_max) return CBH_OK;
     const void* kg = want_packed ? (const void*)fill_packed_kernel<true> : (const void*)fill_split_kernel<true>;
     const void* kd = want_packed ? (const void*)fill_packed_kernel<false> : (const void*)fill_split_kernel<false>;
@@ -573,9 +574,10 @@ int plan_fill_mode(cbh_session* s) {
     CHECK(dalloc(&s->spack, (size_t)s->n * planes));
     CHECK(dalloc(&s->sseq, (size_t)s->n * planes));
     if (want_packed) {   // the packed fill reads tile-major rows (the row-major words stay for a fallback)
-        CHECK(dalloc(&s->trows, (size_t)s->n * s->W));
-        pack_tiles_kernel<<<grid_for((uint64_t)s->n * s->W, 256), 256, 0, s->stream>>>(s->cols, s->n, s->F, s->W,
-                                                                                     s->trows);
+        const uint32_t tw_last = s->W - kPackTileWords * (s->pk_tiles - 1);
+        const uint64_t words = (uint64_t)s->n * (kPackTileWords * (s->pk_tiles - 1) + packed_slice_words(tw_last));
+        CHECK(dalloc(&s->trows, words));
+        pack_tiles_kernel<<<grid_for(words, 256), 256, 0, s->stream>>>(s->cols, s->n, s->F, s->W, s->trows, words);
         if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess)
             return fail(CBH_ERR_DEVICE, "tile-major packing failed");
     }
