@@ -729,21 +729,28 @@ __device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk
                                                   long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
     constexpr uint32_t rpp = kPackThreads / kPackTileWords;   // 64 rows per pass
     static_assert(2 * kPackHalf * rpp == kPackIterRows && kPackHalf == 8, "block layout");
-    uint32_t six, six_n = 0;
+    uint32_t six, six_n = 0, six_nn = 0;
     unsigned long long ssv, ssv_n = 0;
-    // this lane: pass wl of block bb.  A row past the range reads its statistic from past the
+    // this lane: pass wl of block bb.  The row index (a load when gathered) is staged two blocks
+    // ahead, so the word loads that depend on it never wait for it; the statistic (stored in
+    // position order) one block ahead.  A row past the range reads its statistic from past the
     // end of the buffer, which returns 0 (buffer range checking), so no select waits on the load
-    auto stage = [&](uint32_t bb, uint32_t& ix, unsigned long long& sv) {
+    auto stage_ix = [&](uint32_t bb) -> uint32_t {
         const uint32_t p = bb + r0 + wl * rpp;
-        const bool ok = p < end;
-        ix = kGather ? ldw(idx, 4u * (ok ? p : bb)) : (ok ? p : bb);
-        sv = ldq(sbase, ok ? 8u * p : kPastEnd);
+        const uint32_t pc = p < end ? p : bb;
+        return kGather ? ldw(idx, 4u * pc) : pc;
+    };
+    auto stage_sv = [&](uint32_t bb) -> unsigned long long {
+        const uint32_t p = bb + r0 + wl * rpp;
+        return ldq(sbase, p < end ? 8u * p : kPastEnd);
     };
     // row index of pass U (this lane's DPP row) from the staged indices of a block
 #define CBH_DOC(U, SIX) (kGather ? row_bcast<U>(SIX) : row_bcast<U>(SIX))
     uint32_t wA[kPackHalf], wB[kPackHalf];
     uint32_t base = pos;
-    stage(base, six, ssv);
+    six = stage_ix(base);
+    ssv = stage_sv(base);
+    if (base + kPackIterRows < end) six_n = stage_ix(base + kPackIterRows);
 #define CBH_LOADA(SIX)                                                                       \
     wA[0] = ldw(rbase, (CBH_DOC(0, SIX) << sh) + wl4); wA[1] = ldw(rbase, (CBH_DOC(1, SIX) << sh) + wl4); \
     wA[2] = ldw(rbase, (CBH_DOC(2, SIX) << sh) + wl4); wA[3] = ldw(rbase, (CBH_DOC(3, SIX) << sh) + wl4); \
@@ -769,12 +776,13 @@ __device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk
     for (;;) {   // workgroup-uniform
         const uint32_t nb = base + kPackIterRows;
         const bool more = nb < end;
-        if (more) stage(nb, six_n, ssv_n);
+        if (nb + kPackIterRows < end) six_nn = stage_ix(nb + kPackIterRows);
+        if (more) ssv_n = stage_sv(nb);
         CBH_ATOMS(wA, 0, ssv)
         if (more) { CBH_LOADA(six_n) }
         CBH_ATOMS(wB, 8, ssv)
         if (more) { CBH_LOADB(six_n) }
-        six = six_n;
+        six_n = six_nn;
         ssv = ssv_n;
         if (++blk >= swap_every || !more) {
             blk = 0;
@@ -796,27 +804,30 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     uint64_t n, const uint32_t* __restrict__ idx /* kGather: rows listed by the partition */,
     const LevelPlan* __restrict__ plan, const unsigned long long* __restrict__ spack /* [n] */,
     const unsigned long long* __restrict__ sseq /* nullable [V]: packed stats in idx order */,
-    uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, uint32_t Gn, long long* __restrict__ hist,
+    uint32_t n_full, uint32_t F, uint32_t B, uint32_t G, uint32_t Gn, long long* __restrict__ hist,
     uint32_t swap_every /* blocks of rows between two swaps: 2 * swap_every * kPackIterRows * 2^pack_bits <= 2^30 */) {
     constexpr uint32_t C = 2;
     extern __shared__ unsigned long long pk[];   // [B][64] packed cells
-    // blocks: the full 64-feature tiles first, G row ranges each, (tile, range) on XCD
-    // range % 8 so the tiles of one range share its rows' lines in that XCD's L2 (blocks
-    // whose range is >= G exit); then the narrow last tile (W not a multiple of 16 words)
-    // in Gn ranges, sized by the host from the relative cost of its rows so the workgroups
-    // carry about equal work
-    const uint32_t n_full = (W % kPackTileWords) ? n_tiles - 1u : n_tiles;
-    const uint32_t full_blocks = n_full * ((G + 7u) / 8u) * 8u;
+    // blocks: the n_full full 64-feature tiles first, G row ranges each.  Workgroups go to the
+    // 8 XCDs round robin (block b to XCD b % 8), so the (range, tile) pairs are numbered
+    // range-major and XCD x takes the x-th run of per = ceil(n_full G / 8) of them: the tiles
+    // of one range sit on one XCD and share its rows' lines in that L2, and no XCD holds more
+    // pairs than its CUs when n_full G fits the resident slots (pairs past the last exit).
+    // Then, when Gn > 0, the narrow last tile (tile n_full, W not a multiple of 16 words) in
+    // Gn ranges, sized by the host from the relative cost of its rows.
+    const uint32_t pairs = n_full * G;
+    const uint32_t per = (pairs + 7u) / 8u;
+    const uint32_t full_blocks = 8u * per;
     const uint32_t b = blockIdx.x;
     uint32_t t, g, GR;
     if (b < full_blocks) {
-        const uint32_t xcd = b & 7u, q = b >> 3;
-        t = q % n_full;
-        g = (q / n_full) * 8u + xcd;
+        const uint32_t i = (b & 7u) * per + (b >> 3);
+        if (i >= pairs) return;   // workgroup-uniform, before any barrier
+        t = i % n_full;
+        g = i / n_full;
         GR = G;
-        if (g >= G) return;   // workgroup-uniform, before any barrier
     } else {
-        t = n_tiles - 1u;
+        t = n_full;
         g = b - full_blocks;
         GR = Gn;
     }

@@ -188,7 +188,8 @@ struct cbh_session {
     unsigned long long* sseq = nullptr;    // the same for the idx rows, in idx order
     uint32_t* trows = nullptr;             // packed fill: tile-major row words (pack_tiles_kernel)
     uint32_t pk_tiles = 0, pk_ranges = 8, pk_swap = 1;
-    uint32_t pk_ranges_n = 0, pk_blocks = 0;   // packed fill: ranges of the narrow last tile, blocks
+    uint32_t pk_ranges_n = 0, pk_blocks = 0;   // packed fill: ranges of a narrow last tile, blocks
+    uint32_t pk_full = 0;                      // full 64-feature tiles
     bool pk_signed_w = false;              // some object or pair weight is negative
     size_t pk_lds = 0;
     JumpTabs jt() const {
@@ -459,23 +460,23 @@ uint32_t pick_ranges(uint32_t cus, uint32_t per_cu, uint32_t nt, uint64_t n) {
 
 // Row ranges of the packed fill: G per full 64-feature tile and Gn for a narrow last tile
 // (TW < 16 words), in the ratio of their cost per row, so one round of workgroups fills the
-// resident slots with about equal work each.  A row of a narrow tile costs about as much as a
-// full one: its partial-tile loop keeps only two rows per lane in flight and waits on every
-// block's loads (config 2, 2-word last tile, fill per tree: 3.08 ms with equal ranges, 5.84
-// with the narrow tile in 0.4 x as many, 7.62 at 0.23 x).  CBH_PACK_NARROW_COST sets the
-// ratio (a measurement knob).
+// resident slots with about equal work each.  A narrow tile runs the full tiles' loop (its
+// lanes past TW add to columns that are never read), so a row costs as much as a full one:
+// Gn = G.  (Measured alternatives, config 2's 2-word last tile: 0.4 x as many ranges, 2.1x
+// slower fill; a launch of its own with 8 rows per DPP row and per-copy LDS columns, 5%
+// slower -- its loop stays latency-bound.)  CBH_PACK_NARROW_COST sets the ratio (a
+// measurement knob).
 void pick_packed_ranges(cbh_session* s, uint32_t cus, uint32_t per_cu) {
     const uint32_t cap = cus * std::max<uint32_t>(per_cu, 1);
     const uint32_t tw_last = s->W % kPackTileWords;
-    const uint32_t n_full = tw_last ? s->pk_tiles - 1 : s->pk_tiles;
+    const uint32_t n_full = s->W / kPackTileWords;
     double r = tw_last ? 1.0 : 0.0;
     if (const char* e = std::getenv("CBH_PACK_NARROW_COST")) {
         const double v = std::strtod(e, nullptr);
         if (v > 0.0 && v <= 1.0 && tw_last) r = v;
     }
-    uint32_t G, Gn;
+    uint32_t G = 0, Gn = 0;
     if (n_full == 0) {   // one narrow tile: every slot
-        G = 0;
         Gn = cap;
     } else {
         G = std::max<uint32_t>(1, (uint32_t)std::floor((double)cap / ((double)n_full + r)));
@@ -487,11 +488,12 @@ void pick_packed_ranges(cbh_session* s, uint32_t cus, uint32_t per_cu) {
     }
     // short inputs: at least 4096 rows per range, so the per-workgroup flush stays small
     const uint64_t min_rows = 4096;
-    while (G > 8 && s->n / G < min_rows) G -= 8;
+    while (G > 1 && s->n / G < min_rows) G = G / 2;
     while (Gn > 1 && s->n / Gn < min_rows) Gn = Gn / 2;
+    s->pk_full = n_full;
     s->pk_ranges = G;
     s->pk_ranges_n = Gn;
-    s->pk_blocks = n_full * ((G + 7) / 8) * 8 + Gn;
+    s->pk_blocks = 8 * ((n_full * G + 7) / 8) + Gn;
 }
 
 // Feature tiles of the fill: the widest LDS slot stride whose histogram fits the budget.
@@ -1327,11 +1329,11 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         CHECK(s->stage_begin(kStFill));   // the fill kernel alone
         if (s->packed && level == 0)
             fill_packed_kernel<false><<<s->pk_blocks, kPackThreads, s->pk_lds, st>>>(
-                s->trows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_tiles, s->F, s->B,
+                s->trows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_full, s->F, s->B,
                 s->pk_ranges, s->pk_ranges_n, cur, s->pk_swap);
         else if (s->packed)
             fill_packed_kernel<true><<<s->pk_blocks, kPackThreads, s->pk_lds, st>>>(
-                s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_tiles, s->F, s->B,
+                s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_full, s->F, s->B,
                 s->pk_ranges, s->pk_ranges_n, cur, s->pk_swap);
         else if (s->split && level == 0)
             fill_split_kernel<false><<<s->pk_ranges * s->pk_tiles * C, 1024, s->pk_lds, st>>>(
