@@ -399,6 +399,12 @@ def main():
         "roofline": {"bound": "hbm", "kernel": fill_kernel, "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": _profiled_traffic(args.config, n, F, fill_kernel),
+                     "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE (copy-calibrated) of the last 120 fill "
+                                       "dispatches of this command, profiles/fill_kernel_config2.md"
+                                       if _profiled_traffic(args.config, n, F, fill_kernel) else None,
+                     "limiter": "issue of dependent VALU-address / LDS-atomic pairs (LDS pipe and VALU each "
+                                "busy <= 50% of CU cycles, HBM 56% of peak; counters in profiles/)"
+                                if fill_kernel == "fill_packed_kernel" else None,
                      "launches": st["fill_launches"],
                      "avg_launch_ms": round(st["fill_ms"] / max(1, st["fill_launches"]), 5),
                      "algorithmic_bytes_per_launch": round(st["fill_bytes"] / max(1, st["fill_launches"]))},
