@@ -20,7 +20,10 @@
 
 namespace cbh {
 
-constexpr uint32_t kPairMaxParents = 32;   // pairwise scoring: 2P <= 64 unknowns (depth <= 6)
+constexpr uint32_t kPairMaxParents = 128;  // pairwise scoring: 2P <= 256 unknowns (depth <= 8)
+constexpr uint32_t kPairWaveParents = 32;  // levels of up to 32 leaves: one system per wavefront
+constexpr size_t kPairLdsMax = 160 * 1024;   // LDS of one workgroup (gfx950)
+constexpr uint32_t kPairCandGlobalWgs = 1024; // persistent workgroups of the 128-leaf candidate solves
 constexpr uint32_t kPairChunk = 65536;     // pairs per workgroup of the LDS statistics kernel
 constexpr uint32_t kPairLoadAhead = 8;      // pairs whose gathers one thread issues together
 constexpr uint32_t kKeyLoadAhead = 8;       // the same for the keyed statistics
@@ -163,7 +166,7 @@ __device__ __forceinline__ uint32_t pair_key(uint32_t wl, uint32_t ll, uint32_t 
 static __global__ __launch_bounds__(256) void pair_key_count_kernel(
     const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los, uint64_t m,
     const uint16_t* __restrict__ leaf, uint32_t P, uint32_t* __restrict__ cnt) {
-    __shared__ uint32_t c[kPairMaxParents * kPairMaxParents];
+    extern __shared__ uint32_t c[];   // [P * P]
     for (uint32_t i = threadIdx.x; i < P * P; i += blockDim.x) c[i] = 0;
     __syncthreads();
     for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < m;
@@ -177,14 +180,17 @@ static __global__ __launch_bounds__(256) void pair_key_count_kernel(
         if (c[i]) atomicAdd(cnt + i, c[i]);
 }
 
-// Exclusive scan of the P*P key counts (one workgroup of 1024 threads): key_off[P*P + 1],
-// cursor = key_off[0 .. P*P).
+// Exclusive scan of the P*P key counts (one workgroup of 1024 threads, each over a run of
+// ceil(nk / 1024) consecutive keys): key_off[P*P + 1], cursor = key_off[0 .. P*P).
 static __global__ __launch_bounds__(1024) void pair_key_scan_kernel(const uint32_t* __restrict__ cnt, uint32_t nk,
                                                                     uint32_t* __restrict__ key_off,
                                                                     uint32_t* __restrict__ cursor) {
     __shared__ uint32_t sh[1024];
     const uint32_t t = threadIdx.x;
-    const uint32_t v = t < nk ? cnt[t] : 0u;
+    const uint32_t per = (nk + 1023) / 1024;
+    const uint32_t k0 = min(t * per, nk), k1 = min(k0 + per, nk);
+    uint32_t v = 0;
+    for (uint32_t k = k0; k < k1; ++k) v += cnt[k];
     sh[t] = v;
     __syncthreads();
     for (uint32_t o = 1; o < 1024; o <<= 1) {
@@ -193,11 +199,13 @@ static __global__ __launch_bounds__(1024) void pair_key_scan_kernel(const uint32
         sh[t] += a;
         __syncthreads();
     }
-    if (t < nk) {
-        key_off[t] = sh[t] - v;
-        cursor[t] = sh[t] - v;
+    uint32_t run = sh[t] - v;
+    for (uint32_t k = k0; k < k1; ++k) {
+        key_off[k] = run;
+        cursor[k] = run;
+        run += cnt[k];
     }
-    if (t == nk - 1) key_off[nk] = sh[t];
+    if (t == 1023) key_off[nk] = sh[t];
 }
 
 // Scatter the pairs by key as compact records (order inside a key is free: the sums are
@@ -209,7 +217,7 @@ static __global__ __launch_bounds__(256) void pair_key_scatter_kernel(
     const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los,
     const long long* __restrict__ comp_wq, uint64_t m, const uint16_t* __restrict__ leaf, uint32_t P,
     uint32_t* __restrict__ cursor, uint2* __restrict__ rec, long long* __restrict__ rec_wq) {
-    __shared__ uint32_t lcnt[kPairMaxParents * kPairMaxParents];
+    extern __shared__ uint32_t lcnt[];   // [P * P]
     const uint32_t nk = P * P;
     for (uint32_t i = threadIdx.x; i < nk; i += blockDim.x) lcnt[i] = 0;
     __syncthreads();
@@ -393,44 +401,49 @@ static __global__ __launch_bounds__(256) void pair_scan_kernel(long long* __rest
         if (b0 + i < b1) p[(size_t)(b0 + i) * 2] = v[i] + off;
 }
 
-// MakeZeroAverage (pairwise_scoring.rs:255-265), sequential sum as the reference.
-__device__ inline void zero_average_wave(double* r, int n) {
+// MakeZeroAverage (pairwise_scoring.rs:255-265), sequential sum as the reference; every
+// thread of the workgroup takes part.
+__device__ inline void zero_average_block(double* r, int n) {
     __shared__ double avg_s;
-    if ((threadIdx.x & 63) == 0) {
+    if (threadIdx.x == 0) {
         double avg = 0.0;
         for (int i = 0; i < n; ++i) avg += r[i];
         avg_s = avg / (double)n;
     }
     __syncthreads();
     const double avg = avg_s;
-    for (int i = threadIdx.x & 63; i < n; i += 64) r[i] -= avg;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) r[i] -= avg;
     __syncthreads();
 }
 
 // In-place Cholesky of the m x m packed system M (right-looking, the reference's row order)
-// and the forward / back substitutions of y; the solution lands in res[0..m), res[m] = 0.  A
-// non-positive pivot gives the zero solution (cholesky_solve's failure arm).
-__device__ inline void pairwise_factor_solve_wave(double* __restrict__ M, int m, double* __restrict__ cj,
-                                                  double* __restrict__ y, double* __restrict__ res) {
-    const int lane = threadIdx.x & 63;
+// and the forward / back substitutions of y, by every thread of the workgroup (rows strided
+// over the threads); M may be in LDS or global memory.  The forward pass writes its result
+// to fwd (y[p] is read by every thread of step p while other rows of y change), the back
+// pass to res[0..m); res[m] = 0.  A non-positive pivot gives the zero solution
+// (cholesky_solve's failure arm).
+__device__ inline void pairwise_factor_solve_block(double* __restrict__ M, int m, double* __restrict__ cj,
+                                                   double* __restrict__ y, double* __restrict__ fwd,
+                                                   double* __restrict__ res) {
+    const int t = threadIdx.x, nt = blockDim.x;
     bool good = true;
     for (int j = 0; j < m; ++j) {
-        const double d = M[tri(j, j)];
+        const double d = M[tri(j, j)];   // the same value in every thread: a uniform exit
         if (d <= 0.0) {
             good = false;
             break;
         }
         const double ljj = sqrt(d);
-        for (int i = j + 1 + lane; i < m; i += 64) {
+        for (int i = j + 1 + t; i < m; i += nt) {
             const double v = M[tri(i, j)] / ljj;
             M[tri(i, j)] = v;
             cj[i] = v;
         }
         __syncthreads();
-        if (lane == 0) M[tri(j, j)] = ljj;
+        if (t == 0) M[tri(j, j)] = ljj;
         // trailing update of row i: M[i][k] -= L[i][j] L[k][j], k in (j, i]; the row is
         // contiguous in the packed layout and the pivot column is a separate array
-        for (int i = j + 1 + lane; i < m; i += 64) {
+        for (int i = j + 1 + t; i < m; i += nt) {
             const double lij = cj[i];
             double* __restrict__ row = M + i * (i + 1) / 2;
             int k = j + 1;
@@ -447,44 +460,42 @@ __device__ inline void pairwise_factor_solve_wave(double* __restrict__ M, int m,
         __syncthreads();
     }
     if (good) {
-        // every lane divides (the same IEEE quotient) instead of lane 0 publishing it, so a
-        // step needs one barrier; y[p] is read by all lanes before lane 0 overwrites it
         for (int p = 0; p < m; ++p) {   // forward: y[i] -= L[i][p] y[p], p ascending
             const double yp = y[p] / M[tri(p, p)];
-            if (lane == 0) y[p] = yp;
-            for (int i = p + 1 + lane; i < m; i += 64) y[i] -= M[tri(i, p)] * yp;
+            if (t == 0) fwd[p] = yp;
+            for (int i = p + 1 + t; i < m; i += nt) y[i] -= M[tri(i, p)] * yp;
             __syncthreads();
         }
         for (int p = m - 1; p >= 0; --p) {   // back: L^T x = y
-            const double xp = y[p] / M[tri(p, p)];
-            if (lane == 0) res[p] = xp;
-            for (int i = lane; i < p; i += 64) y[i] -= M[tri(p, i)] * xp;
+            const double xp = fwd[p] / M[tri(p, p)];
+            if (t == 0) res[p] = xp;
+            for (int i = t; i < p; i += nt) fwd[i] -= M[tri(p, i)] * xp;
             __syncthreads();
         }
     } else {
-        for (int i = lane; i < m; i += 64) res[i] = 0.0;
+        for (int i = t; i < m; i += nt) res[i] = 0.0;
     }
-    if (lane == 0) res[m] = 0.0;
+    if (t == 0) res[m] = 0.0;
     __syncthreads();
 }
 
-// One wavefront (the whole workgroup) solves the pairwise leaf system of n <= 64 unknowns
-// (calculate_pairwise_leaf_values, pairwise_scoring.rs:283-345, pairwise_leaves.rs:120-200):
-// W (packed lower triangle, n x n) plus the bucket-weight prior gives the (n-1)x(n-1) SPD
-// matrix M; right-looking Cholesky in LDS (every element receives its pivot subtractions in
-// ascending order, as the reference's left-looking loop applies them), forward and back
-// substitution, res[n-1] = 0, zero average.  A non-positive pivot yields zeros.
-// M holds (n-1) n / 2 doubles (packed), cj / y / res n doubles each.
-__device__ inline void pairwise_solve_wave(const double* __restrict__ W, const double* __restrict__ der, int n,
-                                           double l2, double prior, double* __restrict__ M,
-                                           double* __restrict__ cj, double* __restrict__ y,
-                                           double* __restrict__ res) {
-    const int lane = threadIdx.x & 63;
+// The workgroup solves the pairwise leaf system of n unknowns (calculate_pairwise_leaf_values,
+// pairwise_scoring.rs:283-345, pairwise_leaves.rs:120-200): W (packed lower triangle, n x n)
+// plus the bucket-weight prior gives the (n-1)x(n-1) SPD matrix M; right-looking Cholesky
+// (every element receives its pivot subtractions in ascending order, as the reference's
+// left-looking loop applies them), forward and back substitution, res[n-1] = 0, zero
+// average.  A non-positive pivot yields zeros.  M holds (n-1) n / 2 doubles (packed);
+// cj / y / fwd / res n doubles each.
+__device__ inline void pairwise_solve_block(const double* __restrict__ W, const double* __restrict__ der, int n,
+                                            double l2, double prior, double* __restrict__ M,
+                                            double* __restrict__ cj, double* __restrict__ y,
+                                            double* __restrict__ fwd, double* __restrict__ res) {
+    const int t = threadIdx.x, nt = blockDim.x;
     const double cell_prior = 1.0 / (double)n;
     const double non_diag = -prior * cell_prior;
     const double diag = prior * (1.0 - cell_prior) + l2;
     if (n <= 2) {
-        if (lane == 0) {
+        if (t == 0) {
             if (n == 1) {
                 res[0] = 0.0;
             } else {
@@ -494,11 +505,11 @@ __device__ inline void pairwise_solve_wave(const double* __restrict__ W, const d
             }
         }
         __syncthreads();
-        if (n == 2) zero_average_wave(res, 2);
+        if (n == 2) zero_average_block(res, 2);
         return;
     }
     const int m = n - 1;
-    for (int r = lane; r < m; r += 64) {
+    for (int r = t; r < m; r += nt) {
         const double* wr = W + r * (r + 1) / 2;
         double* mr = M + r * (r + 1) / 2;
         for (int c = 0; c < r; ++c) mr[c] = wr[c] + non_diag;
@@ -506,12 +517,13 @@ __device__ inline void pairwise_solve_wave(const double* __restrict__ W, const d
         y[r] = der[r];
     }
     __syncthreads();
-    pairwise_factor_solve_wave(M, m, cj, y, res);
-    zero_average_wave(res, n);
+    pairwise_factor_solve_block(M, m, cj, y, fwd, res);
+    zero_average_block(res, n);
 }
 
-// LDS of the leaf solve (doubles): W 2080 | M 2080 | der, cj, y, res, part 64 each.
-constexpr size_t kPairSolveLds = (2080 + 2080 + 5 * 64) * sizeof(double);
+// Doubles of the leaf solve of L leaves: W L (L+1) / 2 | M (L-1) L / 2 | der, cj, y, fwd, res L
+// each.  In LDS up to 128 leaves (136 KB), else in a global workspace.
+__host__ __device__ constexpr size_t pair_leaf_solve_doubles(uint32_t L) { return (size_t)L * L + 5 * (size_t)L; }
 
 // LDS of the candidate solve (8-byte words): L (packed lower triangle, up to 63 rows; the
 // border's statistics once the solve is done) | der, res, part, dgs 64 each.  ~18 KB, so eight
@@ -581,8 +593,8 @@ __device__ inline double readlane_f64(double v, int l) {
 // the score.  Lane r holds row r of the system in registers (entries above the diagonal are
 // don't-care), so the factorization runs without LDS traffic: the pivot and the pivot column
 // come from the owning lanes by readlane, and every element still receives its pivot
-// subtractions in ascending order with the reference's roundings (pairwise_factor_solve_wave
-// is the same arithmetic over LDS).  The back substitution reads L^T from LDS; the score
+// subtractions in ascending order with the reference's roundings (pairwise_factor_solve_block
+// is the same arithmetic over memory).  The back substitution reads L^T from LDS; the score
 // rebuilds each row of W from the statistics staged over that buffer afterwards.
 template <uint32_t P_>
 static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
@@ -693,7 +705,7 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
     }
     if (lane < n) res[lane] = x;
     __syncthreads();
-    zero_average_wave(res, n);
+    zero_average_block(res, n);
     // the statistics replace L again for the score's pass over the rows of W
     stage_pair_cells(Rs, R, PP, B);
     __syncthreads();
@@ -777,15 +789,17 @@ static __global__ __launch_bounds__(256) void pairwise_best_kernel(const double*
 }
 
 // Pairwise weight sums of the final leaves (compute_pairwise_weight_sums,
-// pairwise_leaves.rs:47-88): out [L][L] int64, same-leaf pairs skipped.
+// pairwise_leaves.rs:47-88): out [L][L] int64, same-leaf pairs skipped.  The L x L sums are
+// privatized in LDS up to 128 leaves (in_lds), else added to out directly.
 static __global__ __launch_bounds__(256) void pair_leaf_weights_kernel(
     const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los,
     const long long* __restrict__ comp_wq, uint64_t m, const uint16_t* __restrict__ leaf, uint32_t L,
-    long long* __restrict__ out) {
+    long long* __restrict__ out, int in_lds) {
     extern __shared__ long long sh_lw[];
-    for (uint32_t i = threadIdx.x; i < L * L; i += blockDim.x) sh_lw[i] = 0;
+    if (in_lds)
+        for (uint32_t i = threadIdx.x; i < L * L; i += blockDim.x) sh_lw[i] = 0;
     __syncthreads();
-    unsigned long long* acc = (unsigned long long*)sh_lw;
+    unsigned long long* acc = in_lds ? (unsigned long long*)sh_lw : (unsigned long long*)out;
     for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < m;
          k += (uint64_t)gridDim.x * blockDim.x) {
         const uint32_t wl = leaf[comp_win[k]] & 0x7FFFu, ll = leaf[comp_los[k]] & 0x7FFFu;
@@ -797,8 +811,9 @@ static __global__ __launch_bounds__(256) void pair_leaf_weights_kernel(
         atomicAdd(acc + (size_t)ll * L + ll, (unsigned long long)q);
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < L * L; i += blockDim.x)
-        if (sh_lw[i] != 0) atomicAdd((unsigned long long*)out + i, (unsigned long long)sh_lw[i]);
+    if (in_lds)
+        for (uint32_t i = threadIdx.x; i < L * L; i += blockDim.x)
+            if (sh_lw[i] != 0) atomicAdd((unsigned long long*)out + i, (unsigned long long)sh_lw[i]);
 }
 
 // normalize_leaf_values for pairwise-weight losses (boosting.rs:2844-2882): subtract the
@@ -827,30 +842,134 @@ static __global__ void pairwise_center_kernel(double* __restrict__ raw, const lo
 }
 
 // PairLogitPairwise leaves (compute_pairwise_leaf_deltas, pairwise_leaves.rs:219-238): one
-// wavefront solves the L-leaf system from the pair weight sums and the per-leaf der sums,
-// then the centring.
-static __global__ __launch_bounds__(64) void pairwise_leaf_kernel(
+// workgroup solves the L-leaf system from the pair weight sums and the per-leaf der sums,
+// then the centring.  Its pair_leaf_solve_doubles(L) doubles are in LDS (ws null) or at ws.
+static __global__ __launch_bounds__(256) void pairwise_leaf_kernel(
     const long long* __restrict__ lw, uint32_t L, const long long* __restrict__ sums, uint32_t CL,
     const Scales* __restrict__ sc, double pair_inv, double l2, double prior, double lr,
-    double* __restrict__ raw, double* __restrict__ scaled) {
+    double* __restrict__ raw, double* __restrict__ scaled, double* __restrict__ ws) {
     extern __shared__ double sh_pl[];
-    double* W = sh_pl;
-    double* M = W + 2080;
-    double* der = M + 2080;
-    double* cj = der + 64;
-    double* yv = cj + 64;
-    double* res = yv + 64;
-    const int lane = threadIdx.x;
+    double* W = ws ? ws : sh_pl;
+    double* M = W + (size_t)L * (L + 1) / 2;
+    double* der = M + (size_t)(L - 1) * L / 2;
+    double* cj = der + L;
+    double* yv = cj + L;
+    double* fwd = yv + L;
+    double* res = fwd + L;
     const double inv_d = sc->inv[kLeafDer];
-    for (uint32_t r = lane; r < L; r += 64) {
+    for (uint32_t r = threadIdx.x; r < L; r += blockDim.x) {
         for (uint32_t c = 0; c <= r; ++c) W[tri(r, c)] = (double)lw[(size_t)r * L + c] * pair_inv;
         der[r] = (double)sums[(size_t)r * CL] * inv_d;
     }
     __syncthreads();
-    pairwise_solve_wave(W, der, (int)L, l2, prior, M, cj, yv, res);
-    for (uint32_t l = lane; l < L; l += 64) raw[l] = res[l];
+    pairwise_solve_block(W, der, (int)L, l2, prior, M, cj, yv, fwd, res);
+    for (uint32_t l = threadIdx.x; l < L; l += blockDim.x) raw[l] = res[l];
     __syncthreads();
-    if (lane == 0) pairwise_center_lane0(raw, sums, CL, L, lr, scaled);
+    if (threadIdx.x == 0) pairwise_center_lane0(raw, sums, CL, L, lr, scaled);
+}
+
+// Doubles of one candidate solve of the workgroup kernel at a level of P leaves (n = 2P
+// unknowns, m = n - 1): M m (m + 1) / 2 | der, y, fwd, res, cj, part n each | dgs n (int64).
+__host__ __device__ constexpr size_t pair_cand_block_doubles(uint32_t P) {
+    return (size_t)(2 * P - 1) * (2 * P) / 2 + 7 * (size_t)(2 * P);
+}
+
+static_assert(pair_cand_block_doubles(64) * sizeof(double) <= kPairLdsMax, "64-leaf candidates solve in LDS");
+static_assert(pair_cand_block_doubles(128) * sizeof(double) > kPairLdsMax, "128-leaf candidates solve in memory");
+
+// Candidate solves of levels with more than 32 leaves (2P = 128 or 256 unknowns): one
+// workgroup per (border s, feature f) at a time, looping over the F (B - 1) candidates with
+// a stride of the grid.  The same arithmetic as pairwise_candidate_kernel (calculate_pairwise_score,
+// pairwise_scoring.rs:471-581): rows of M = W + prior terms assembled from the cumulative
+// statistics (threads over rows), the right-looking Cholesky and substitutions of
+// pairwise_factor_solve_block, MakeZeroAverage, then the score with sequential inner and outer
+// sums.  The workspace of a candidate is in LDS (ws null) or at ws + blockIdx.x * doubles.
+static __global__ __launch_bounds__(256) void pairwise_candidate_block_kernel(
+    const long long* __restrict__ st, const long long* __restrict__ hist, uint32_t C, uint32_t F,
+    const uint32_t* __restrict__ n_cand, uint32_t B, uint32_t P, const Scales* __restrict__ sc, double pair_inv,
+    double l2, double prior, double* __restrict__ scores /* [F][B] */, double* __restrict__ ws) {
+    extern __shared__ double sh_pb[];
+    const int n = 2 * (int)P, m = n - 1;
+    double* M = ws ? ws + (size_t)blockIdx.x * pair_cand_block_doubles(P) : sh_pb;
+    double* der = M + (size_t)m * (m + 1) / 2;
+    double* y = der + n;
+    double* fwd = y + n;
+    double* res = fwd + n;
+    double* cj = res + n;
+    double* part = cj + n;
+    long long* dgs = (long long*)(part + n);
+    const int t = threadIdx.x, nt = blockDim.x;
+    const double inv_d = sc->inv[kScoreDer];
+    const double cell_prior = 1.0 / (double)n;
+    const double non_diag = -prior * cell_prior;
+    const double diag = prior * (1.0 - cell_prior) + l2;
+    const uint64_t per_f = B - 1, total = (uint64_t)F * per_f;
+    for (uint64_t cand = blockIdx.x; cand < total; cand += gridDim.x) {
+        const uint32_t f = (uint32_t)(cand / per_f), s = (uint32_t)(cand % per_f);
+        if (s >= n_cand[f]) {   // uniform over the workgroup
+            if (t == 0) scores[(size_t)f * B + s] = -INFINITY;
+            continue;
+        }
+        const long long* R = st + (size_t)f * P * P * B * 2 + (size_t)s * 2;   // cell stride 2B
+        const long long* T = st + (size_t)f * P * P * B * 2 + (size_t)(B - 1) * 2;
+        for (uint32_t yl = t; yl < P; yl += nt) {
+            const long long* h = hist + ((size_t)yl * C * F + f) * B;
+            const long long dp = h[s], dt = h[B - 1];
+            der[2 * yl] = (double)dp * inv_d;
+            der[2 * yl + 1] = (double)(dt - dp) * inv_d;
+        }
+        // rows of M (r < m) and the diagonal entries of W (every row, kept for the score)
+        for (int r = t; r < n; r += nt) {
+            const PairRow pr{R, T, 2 * B, 2 * B, P, (uint32_t)r >> 1, (uint32_t)r & 1u};
+            const long long da = pr.da();
+            long long dg = -da;
+            double* mr = M + (size_t)r * (r + 1) / 2;
+            for (uint32_t b = 0; b < P; ++b) {
+                if (b == pr.a) continue;
+                long long e0, e1, dpart;
+                pr.wp(b, e0, e1, dpart);
+                dg -= dpart;
+                if (r < m && (int)(2 * b) <= r) mr[2 * b] = (double)e0 * pair_inv + non_diag;
+                if (r < m && (int)(2 * b + 1) <= r) mr[2 * b + 1] = (double)e1 * pair_inv + non_diag;
+            }
+            dgs[r] = dg;
+            if (r < m) {
+                mr[r] = (double)dg * pair_inv + diag;
+                if (r & 1) mr[r - 1] = (double)da * pair_inv + non_diag;
+            }
+        }
+        __syncthreads();
+        for (int r = t; r < m; r += nt) y[r] = der[r];   // der is complete after the barrier
+        __syncthreads();
+        pairwise_factor_solve_block(M, m, cj, y, fwd, res);
+        zero_average_block(res, n);
+        // score (calculate_score, pairwise_scoring.rs:352-375): inner and outer sums sequential
+        for (int r = t; r < n; r += nt) {
+            const PairRow ps{R, T, 2 * B, 2 * B, P, (uint32_t)r >> 1, (uint32_t)r & 1u};
+            const long long dgx = dgs[r], dax = ps.da();
+            double inner = 0.0;
+            for (uint32_t b = 0; b < P; ++b) {
+                long long e0, e1;
+                if (b == ps.a) {
+                    e0 = ps.u == 0 ? dgx : dax;
+                    e1 = ps.u == 0 ? dax : dgx;
+                } else {
+                    long long dpart;
+                    ps.wp(b, e0, e1, dpart);
+                }
+                inner += res[2 * b] * ((double)e0 * pair_inv);
+                inner += res[2 * b + 1] * ((double)e1 * pair_inv);
+            }
+            part[r] = res[r] * (der[r] - 0.5 * inner);
+        }
+        __syncthreads();
+        if (t == 0) {
+            double outer = 0.0;
+            for (int i = 0; i < n; ++i) outer += part[i];
+            scores[(size_t)f * B + s] = outer;
+        }
+        __syncthreads();   // the workspace is rewritten by the next candidate
+    }
 }
 
 }  // namespace cbh

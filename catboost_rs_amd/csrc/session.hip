@@ -172,6 +172,9 @@ struct cbh_session {
     uint32_t* pair_lv = nullptr;     // [m] leaves of winner and loser of every pair, this level
     long long* key_wq = nullptr;     // [m]
     uint32_t pair_tf = 4, pair_tiles = 1;
+    double* pair_ws = nullptr;       // global workspace of the 256-leaf solves (depth 8)
+    uint32_t pair_cand_wgs = 0;      // workgroups of the 128-leaf-level candidate solves (global workspace)
+    size_t pair_leaf_lds = 0;        // LDS of the leaf solve (0: global workspace)
 
     // dominant-bin skip of the fill (features whose most frequent bin holds >= 1/8 of rows)
     uint32_t* skip_bin = nullptr;    // [F] dominant bin, or 256 (no skip)
@@ -260,7 +263,7 @@ struct cbh_session {
         dfree(group_off); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st);
         dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows);
-        dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_lv);
+        dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_lv); dfree(pair_ws);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
         dfree(phantom_cnt); dfree(fweight); dfree(ctr_pow); dfree(ctr_group_dev); dfree(ctr_used_dev);
         dfree(phantom_off_lv);
@@ -335,8 +338,6 @@ int validate_config(const cbh_config* cfg, uint32_t n_bins, uint64_t n, uint32_t
         return fail(CBH_DECLINED, "depth outside 1..8 is not covered on device");
     if (cfg->loss < CBH_LOSS_RMSE || cfg->loss > CBH_LOSS_PAIRLOGIT_PAIRWISE)
         return fail(CBH_DECLINED, "loss not covered on device");
-    if (cfg->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE && cfg->depth > 6)
-        return fail(CBH_DECLINED, "PairLogitPairwise is covered up to depth 6 (64-leaf systems)");
     if (cfg->loss == CBH_LOSS_MULTICLASS) {
         const int k = cfg->approx_dim;
         if (k < 2 || k > kMaxK) return fail(CBH_DECLINED, "MultiClass approx_dim must be 2..16");
@@ -420,6 +421,40 @@ int session_alloc(cbh_session* s) {
         HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_key_kernel,
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)((size_t)s->pair_tf * 2 * s->B * 2 * sizeof(long long))));
+        // every LDS size a level can ask for is set here, before any tree is recorded as a graph
+        const size_t p4 = std::min<size_t>(pmax, 4);
+        HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)((size_t)s->B * p4 * p4 * 2 * sizeof(long long))));
+        HIP_TRY(hipFuncSetAttribute((const void*)pair_key_count_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)(pmax * pmax * sizeof(uint32_t))));
+        HIP_TRY(hipFuncSetAttribute((const void*)pair_key_scatter_kernel,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)(pmax * pmax * sizeof(uint32_t))));
+        const uint32_t L = 1u << s->depth;
+        const size_t leaf_bytes = pair_leaf_solve_doubles(L) * sizeof(double);
+        size_t ws_doubles = 0;
+        if (leaf_bytes <= kPairLdsMax) {
+            s->pair_leaf_lds = leaf_bytes;
+            HIP_TRY(hipFuncSetAttribute((const void*)pairwise_leaf_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)leaf_bytes));
+        } else {
+            ws_doubles = pair_leaf_solve_doubles(L);
+        }
+        if ((size_t)L * L * sizeof(long long) <= kPairLdsMax)
+            HIP_TRY(hipFuncSetAttribute((const void*)pair_leaf_weights_kernel,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)((size_t)L * L * sizeof(long long))));
+        // levels of 64 leaves solve their candidates in LDS, the level of 128 in a global
+        // workspace, one slot per workgroup of a persistent grid
+        if (pmax >= 64)
+            HIP_TRY(hipFuncSetAttribute((const void*)pairwise_candidate_block_kernel,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)(pair_cand_block_doubles(64) * sizeof(double))));
+        if (pmax >= 128) {
+            const uint64_t total = (uint64_t)s->F * (s->B - 1);
+            s->pair_cand_wgs = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(total, 1), kPairCandGlobalWgs);
+            ws_doubles = std::max(ws_doubles, (size_t)s->pair_cand_wgs * pair_cand_block_doubles(128));
+        }
+        if (ws_doubles) CHECK(dalloc(&s->pair_ws, ws_doubles));
     }
     CHECK(dalloc(&s->smp_dev, 2));
     HIP_TRY(hipMemset(s->smp_dev, 0, 2 * sizeof(SampleParams)));
@@ -1001,6 +1036,12 @@ int launch_zero(long long* p, size_t n, hipStream_t st) {
 // row in pair order (calc_pairwise_weights, boosting.rs:1760-1783), pair weights in fixed
 // point 2^shift with 2^shift * sum|w| <= 2^60 (every statistic and weight-matrix entry is a
 // sum of at most 4 sum|w|), uploaded once.
+void drop_tree_graphs(cbh_session* s) {
+    for (auto& g : s->tree_graph)
+        if (g) (void)hipGraphExecDestroy(g);
+    s->tree_graph[0] = s->tree_graph[1] = nullptr;
+}
+
 int upload_pairs(cbh_session* s, const cbh_family* fam) {
     const uint64_t n = s->n;
     if (fam->kind != CBH_FAMILY_PAIRWISE) return fail(CBH_ERR_INVALID_ARG, "family kind is not CBH_FAMILY_PAIRWISE");
@@ -1046,15 +1087,16 @@ int upload_pairs(cbh_session* s, const cbh_family* fam) {
     if (neg && s->packed) {   // the packed fill takes non-negative weights only: back to the two-channel fill
         s->packed = false;
         s->pk_signed_w = true;
-        for (auto& g : s->tree_graph)
-            if (g) (void)hipGraphExecDestroy(g);
-        s->tree_graph[0] = s->tree_graph[1] = nullptr;
+        drop_tree_graphs(s);
     }
     int e = 0;
     if (sum_abs > 0.0) std::frexp(sum_abs, &e);
     const int shift = std::min(60 - e, 100);
     std::vector<long long> wq(m);
     for (uint64_t j = 0; j < m; ++j) wq[j] = std::llrint(std::ldexp(w[j], shift));
+    // a recorded tree holds the pair count, the group count, the weight scale and the pair
+    // buffers: a change of any of them records it again
+    if (m != s->n_pairs || G != s->n_groups || std::ldexp(1.0, -shift) != s->pair_inv) drop_tree_graphs(s);
     s->pair_inv = std::ldexp(1.0, -shift);
     if (m != s->n_pairs || !s->comp_win) {
         dfree(s->comp_win); dfree(s->comp_los); dfree(s->comp_w); dfree(s->comp_wq);
@@ -1104,9 +1146,7 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
             HIP_TRY(hipGetLastError());
             const uint32_t n_chunks = (uint32_t)((s->n_pairs + kPairChunk - 1) / kPairChunk);
             const uint32_t grid = 8u * n_chunks * ((F + 7) / 8);
-            const size_t lds = (size_t)B * P * P * 2 * sizeof(long long);
-            HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_kernel,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            const size_t lds = (size_t)B * P * P * 2 * sizeof(long long);   // attribute set at open
             pair_stats_kernel<<<grid, 256, lds, st>>>(s->cols, s->n, s->pair_lv, s->comp_win, s->comp_los,
                                                      s->comp_wq, s->n_pairs, n_chunks, F, P, B, s->pair_st);
             HIP_TRY(hipGetLastError());
@@ -1119,7 +1159,7 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
         zero_u32_kernel<<<grid_for(nk, 256), 256, 0, st>>>(s->key_cnt, nk);
         HIP_TRY(hipGetLastError());
         if (s->n_pairs) {
-            pair_key_count_kernel<<<grid_for(s->n_pairs, 256, 1024), 256, 0, st>>>(
+            pair_key_count_kernel<<<grid_for(s->n_pairs, 256, 1024), 256, nk * sizeof(uint32_t), st>>>(
                 s->comp_win, s->comp_los, s->n_pairs, s->leaf, P, s->key_cnt);
             HIP_TRY(hipGetLastError());
         }
@@ -1127,7 +1167,7 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
         HIP_TRY(hipGetLastError());
         if (s->n_pairs) {
             pair_key_scatter_kernel<<<(unsigned)((s->n_pairs + 256 * kScatterItems - 1) / (256 * kScatterItems)),
-                                      256, 0, st>>>(
+                                      256, nk * sizeof(uint32_t), st>>>(
                 s->comp_win, s->comp_los, s->comp_wq, s->n_pairs, s->leaf, P, s->key_cur, s->key_rec,
                 s->key_wq);
             HIP_TRY(hipGetLastError());
@@ -1151,6 +1191,16 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
             case 8: CBH_PAIR_CAND(8); break;
             case 16: CBH_PAIR_CAND(16); break;
             case 32: CBH_PAIR_CAND(32); break;
+            case 64:   // one workgroup per candidate, its system in LDS
+                pairwise_candidate_block_kernel<<<F * (B - 1), 256, pair_cand_block_doubles(64) * sizeof(double), st>>>(
+                    s->pair_st, cur, s->C, F, s->n_cand, B, P, s->scales, s->pair_inv, s->l2, s->prior,
+                    s->cand_scores, nullptr);
+                break;
+            case 128:  // a persistent grid, one global workspace slot per workgroup
+                pairwise_candidate_block_kernel<<<s->pair_cand_wgs, 256, 0, st>>>(
+                    s->pair_st, cur, s->C, F, s->n_cand, B, P, s->scales, s->pair_inv, s->l2, s->prior,
+                    s->cand_scores, s->pair_ws);
+                break;
             default: return fail(CBH_ERR_UNSUPPORTED, "pairwise scoring: level of " + std::to_string(P) + " leaves");
         }
 #undef CBH_PAIR_CAND
@@ -1429,14 +1479,16 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
     if (s->pairwise) {
         CHECK(launch_zero(s->leaf_w, (size_t)n_leaves * n_leaves, st));
         if (s->n_pairs) {
-            pair_leaf_weights_kernel<<<grid_for(s->n_pairs, 256, 1024), 256,
-                                       (size_t)n_leaves * n_leaves * sizeof(long long), st>>>(
-                s->comp_win, s->comp_los, s->comp_wq, s->n_pairs, s->leaf, n_leaves, s->leaf_w);
+            const size_t lw_bytes = (size_t)n_leaves * n_leaves * sizeof(long long);
+            const bool lw_lds = lw_bytes <= kPairLdsMax;
+            pair_leaf_weights_kernel<<<grid_for(s->n_pairs, 256, 1024), 256, lw_lds ? lw_bytes : 0, st>>>(
+                s->comp_win, s->comp_los, s->comp_wq, s->n_pairs, s->leaf, n_leaves, s->leaf_w, lw_lds ? 1 : 0);
             HIP_TRY(hipGetLastError());
         }
-        pairwise_leaf_kernel<<<1, 64, kPairSolveLds, st>>>(s->leaf_w, n_leaves, s->leaf_sums, CL, s->scales,
-                                                          s->pair_inv, s->l2, s->prior, s->lr,
-                                                          s->leaf_raw, s->leaf_scaled);
+        // one wavefront up to 64 leaves (the solve is a chain of short steps), else 256 threads
+        pairwise_leaf_kernel<<<1, n_leaves <= 64 ? 64 : 256, s->pair_leaf_lds, st>>>(
+            s->leaf_w, n_leaves, s->leaf_sums, CL, s->scales, s->pair_inv, s->l2, s->prior, s->lr, s->leaf_raw,
+            s->leaf_scaled, s->pair_leaf_lds ? nullptr : s->pair_ws);
         HIP_TRY(hipGetLastError());
     } else {
         leaf_values_kernel<K><<<(n_leaves + 63) / 64, 64, 0, st>>>(s->leaf_sums, s->scales, n_leaves, newton,
@@ -1483,7 +1535,7 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     *s->pin_smp = smp;
     HIP_TRY(hipMemcpyAsync(s->smp_dev, s->pin_smp, sizeof(SampleParams), hipMemcpyHostToDevice, st));
     // replay the recorded tree when nothing differs from it: previous leaves pending, no
-    // per-stage events, no pairwise stage (its level solves are not recorded)
+    // per-stage events
     // a CTR session replays once every CTR group is in the model (no per-level host step left)
     const bool ctr_static = !s->ctr_n || s->ctr_dev || (ctr_all_used(s) && s->fweight_one);
     if (s->ctr_dev) {   // the groups earlier trees used (and whether all are), for this tree
@@ -1491,7 +1543,7 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         s->pin_ctr_used[s->ctr_n] = ctr_all_used(s) ? 1 : 0;   // then no phantom count is needed
         HIP_TRY(hipMemcpyAsync(s->ctr_used_dev, s->pin_ctr_used, s->ctr_n + 1, hipMemcpyHostToDevice, st));
     }
-    const bool replay = s->pending && !s->cfg.profile && !s->pairwise && !s->graph_off && ctr_static;
+    const bool replay = s->pending && !s->cfg.profile && !s->graph_off && ctr_static;
     hipGraphExec_t& ge = s->tree_graph[use_host_sample ? 1 : 0];
     if (replay && !ge) record_tree<K>(s, use_host_sample);
     if (replay && ge) {

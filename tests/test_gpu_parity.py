@@ -460,6 +460,11 @@ RANK_CASES = [
     dict(loss="PairLogit", leaf_method="Gradient", score="L2", bootstrap_type="Bernoulli", depth=5),
     dict(loss="PairLogitPairwise", leaf_method="Gradient", score="Cosine", bootstrap_type="No", depth=4),
     dict(loss="PairLogitPairwise", leaf_method="Gradient", score="Cosine", bootstrap_type="No", depth=6),
+    # deeper than 32-leaf levels: the workgroup candidate solve (64 leaves in LDS; 128 leaves in
+    # a global workspace over a persistent grid, here with more candidates than workgroups) and
+    # the 128 / 256-leaf leaf solves
+    dict(loss="PairLogitPairwise", leaf_method="Gradient", score="Cosine", bootstrap_type="No", depth=7),
+    dict(loss="PairLogitPairwise", leaf_method="Gradient", score="Cosine", bootstrap_type="No", depth=8),
 ]
 
 
@@ -468,9 +473,12 @@ def test_ranking_boosting_matches_oracle(case):
     p = dict(RANK_CASES[case])
     depth = p.pop("depth")
     pairwise = p["loss"] == "PairLogitPairwise"
-    bins, nb, rel, win, los, go = _ranking_pool(40 + case, 150 if pairwise else 600, 20, 10, 9, 40)
+    F = 60 if depth == 8 else 9   # depth 8: > 1024 candidates at the 128-leaf level
+    bins, nb, rel, win, los, go = _ranking_pool(40 + case, 150 if pairwise else 600, 20, 10, F, 40)
     wt = np.random.default_rng(case).uniform(0.5, 2.0, size=win.shape[0]) if case == 1 else None
-    iters, l2 = 6, 3.0
+    if depth == 8:
+        assert int(nb.sum()) > 1024
+    iters, l2 = (3 if depth == 8 else 6), 3.0
     exp = O.train(bins, nb, rel, depth=depth, iterations=iters, learning_rate=0.3, l2_leaf_reg=l2,
                   random_seed=7, subsample=0.7, pairs=(win, los, wt), **p)
     tr = cb.Trainer(bins, int(nb.max()) + 1, rel, depth=depth, learning_rate=0.3, l2_leaf_reg=l2,
