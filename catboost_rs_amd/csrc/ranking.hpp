@@ -24,10 +24,6 @@ constexpr uint32_t kPairMaxParents = 128;  // pairwise scoring: 2P <= 256 unknow
 constexpr uint32_t kPairWaveParents = 32;  // levels of up to 32 leaves: one system per wavefront
 constexpr size_t kPairLdsMax = 160 * 1024;   // LDS of one workgroup (gfx950)
 constexpr uint32_t kPairCandGlobalWgs = 1024; // persistent workgroups of the 128-leaf candidate solves
-constexpr uint32_t kPairChunk = 65536;     // pairs per workgroup of the LDS statistics kernel
-constexpr uint32_t kPairLoadAhead = 8;      // pairs whose gathers one thread issues together
-constexpr uint32_t kKeyLoadAhead = 8;       // the same for the keyed statistics
-constexpr uint32_t kKeyWords = 4;           // row words of one pair loaded together
 
 __device__ __forceinline__ uint32_t tri(uint32_t r, uint32_t c) {   // packed lower triangle
     return r >= c ? r * (r + 1) / 2 + c : c * (c + 1) / 2 + r;
@@ -40,123 +36,66 @@ __device__ __forceinline__ double pairlogit_p(double winner_approx, double loser
     return den > 0.0 ? el / den : 0.5;
 }
 
-// PairLogit derivatives, one thread per query group (pairlogit_group_der,
-// crates/cb-compute/src/ranking_der.rs:408-445): rows of the group ascending, each winner's
-// pairs in order, a loser's derivatives decremented as its winners are visited and a
-// winner's own sums added after its pair loop -- the reference's accumulation order.  The
-// thread first applies the previous tree's leaf values to its rows (the rows of a group
-// belong to it alone).
-static __global__ __launch_bounds__(256) void pairlogit_ders_kernel(
-    const uint32_t* __restrict__ group_off, uint32_t n_groups, const uint32_t* __restrict__ comp_off,
-    const uint32_t* __restrict__ comp_los, const double* __restrict__ comp_w,
-    double* __restrict__ approx, const uint16_t* __restrict__ leaf,
-    const double* __restrict__ pending /* [leaves] lr-scaled, nullable */,
-    double* __restrict__ der1, double* __restrict__ der2) {
-    const uint32_t g = blockIdx.x * blockDim.x + threadIdx.x;
-    if (g >= n_groups) return;
-    const uint32_t b = group_off[g], e = group_off[g + 1];
-    if (pending)
-        for (uint32_t i = b; i < e; ++i) approx[i] += pending[leaf[i] & 0x7FFFu];
-    for (uint32_t i = b; i < e; ++i) {
-        der1[i] = 0.0;
-        der2[i] = 0.0;
-    }
-    for (uint32_t doc = b; doc < e; ++doc) {
-        const double wa = approx[doc];
-        double wd = 0.0, wd2 = 0.0;
-        for (uint32_t k = comp_off[doc]; k < comp_off[doc + 1]; ++k) {
-            const uint32_t l = comp_los[k];
-            const double p = pairlogit_p(wa, approx[l]);
-            const double w = comp_w[k];
-            wd += w * p;
-            wd2 += w * p * (p - 1.0);
-            der1[l] -= w * p;
-            der2[l] += w * p * (p - 1.0);
-        }
-        der1[doc] += wd;
-        der2[doc] += wd2;
-    }
+// The previous tree's leaf values (lr-scaled) applied to every row (pair losses: their
+// derivatives need every row's updated approximant, so this runs before them).
+static __global__ __launch_bounds__(256) void apply_leaves_kernel(double* __restrict__ approx,
+                                                                  const uint16_t* __restrict__ leaf,
+                                                                  const double* __restrict__ pending, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        approx[i] += pending[leaf[i] & 0x7FFFu];
 }
 
-// Leaves of both rows of every pair for one level: pair_lv[k] = winner leaf | loser leaf << 16.
-static __global__ __launch_bounds__(256) void pair_leaves_kernel(const uint32_t* __restrict__ comp_win,
-                                                                 const uint32_t* __restrict__ comp_los, uint64_t m,
-                                                                 const uint16_t* __restrict__ leaf,
-                                                                 uint32_t* __restrict__ pair_lv) {
-    for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < m; k += (uint64_t)gridDim.x * blockDim.x)
-        pair_lv[k] = (leaf[comp_win[k]] & 0x7FFFu) | ((uint32_t)(leaf[comp_los[k]] & 0x7FFFu) << 16);
-}
-
-// Pair-weight statistics of one level for every feature.  For a
-// pair with winner bucket > loser bucket the cells [loserLeaf][winnerLeaf] are decremented at
-// (loser bucket, smaller) and (winner bucket, greater); otherwise [winnerLeaf][loserLeaf] at
-// (winner bucket, smaller) and (loser bucket, greater).  The P*P*B*2 cells of the feature fit
-// in LDS (P <= 4): a workgroup accumulates its chunk there, then adds it to st.  In LDS the
-// two channels of a leaf pair are separate runs of B ([P][P][2][B]), so a wave's atomics on
-// random buckets spread over every bank.
-static __global__ __launch_bounds__(256) void pair_stats_kernel(
-    const uint8_t* __restrict__ cols, uint64_t n, const uint32_t* __restrict__ pair_lv,
-    const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los,
-    const long long* __restrict__ comp_wq, uint64_t m, uint32_t n_chunks, uint32_t F, uint32_t P, uint32_t B,
-    long long* __restrict__ st) {
-    extern __shared__ long long sh_st[];
-    // 1-D grid of 8 * n_chunks * ceil(F / 8) blocks, round-robin over the 8 XCDs: all chunks of
-    // a feature run on one XCD, which keeps its bucket column in that XCD's L2
-    const uint32_t xcd = blockIdx.x & 7u, q = blockIdx.x >> 3;
-    const uint32_t f = xcd + 8u * (q / n_chunks), chunk = q % n_chunks;
-    if (f >= F) return;
-    const size_t cells = (size_t)B * P * P * 2;
-    unsigned long long* out = (unsigned long long*)(st + (size_t)f * cells);
-    unsigned long long* acc = (unsigned long long*)sh_st;
-    for (size_t i = threadIdx.x; i < cells; i += blockDim.x) sh_st[i] = 0;
-    __syncthreads();
-    const uint8_t* col = cols + (size_t)f * n;
-    const uint64_t k0 = (uint64_t)chunk * kPairChunk;
-    const uint64_t k1 = min(k0 + kPairChunk, m);
-    // kPairLoadAhead pairs per thread at a time: their indices, then all their bucket and leaf
-    // gathers, are in flight together (the loop is latency-bound otherwise)
-    for (uint64_t kb = k0 + threadIdx.x; kb < k1; kb += (uint64_t)blockDim.x * kPairLoadAhead) {
-        uint32_t wi[kPairLoadAhead], lo[kPairLoadAhead], lv[kPairLoadAhead];
-        long long wq[kPairLoadAhead];
-#pragma unroll
-        for (uint32_t u = 0; u < kPairLoadAhead; ++u) {
-            const uint64_t k = kb + (uint64_t)u * blockDim.x;
-            const bool ok = k < k1;
-            wi[u] = ok ? comp_win[k] : 0u;
-            lo[u] = ok ? comp_los[k] : 0u;
-            lv[u] = ok ? pair_lv[k] : 0u;
-            wq[u] = ok ? comp_wq[k] : 0;
-        }
-        uint32_t wb[kPairLoadAhead], lb[kPairLoadAhead], wl[kPairLoadAhead], ll[kPairLoadAhead];
-#pragma unroll
-        for (uint32_t u = 0; u < kPairLoadAhead; ++u) {
-            wb[u] = col[wi[u]];
-            lb[u] = col[lo[u]];
-            wl[u] = lv[u] & 0x7FFFu;
-            ll[u] = (lv[u] >> 16) & 0x7FFFu;
-        }
-#pragma unroll
-        for (uint32_t u = 0; u < kPairLoadAhead; ++u) {
-            if (kb + (uint64_t)u * blockDim.x >= k1 || wi[u] == lo[u]) continue;
-            const unsigned long long neg = (unsigned long long)(-wq[u]);
-            const bool wg = wb[u] > lb[u];
-            const size_t run = ((size_t)(wg ? ll[u] : wl[u]) * P + (wg ? wl[u] : ll[u])) * 2 * B;
-            atomicAdd(acc + run + (wg ? lb[u] : wb[u]), neg);
-            atomicAdd(acc + run + B + (wg ? wb[u] : lb[u]), neg);
+// PairLogit derivatives, one thread per row (pairlogit_group_der,
+// crates/cb-compute/src/ranking_der.rs:408-445).  The reference walks a query group's rows
+// ascending, each winner's pairs in order: a loser's derivatives are decremented as its
+// winners are visited, and a winner adds its own sums after its pair loop.  Row i receives
+// exactly those operations in that order: its decrements as a loser from the winners before
+// it (its pairs as a loser, los_idx, ascend in competitor order, i.e. by winner), then its own
+// pair loop (a pair with itself as loser decremented inside it, as there), then its sums, then
+// the decrements from the winners after it -- the same sequential f64 values, with no atomics.
+static __global__ __launch_bounds__(256) void pairlogit_row_ders_kernel(
+    uint64_t n, const uint32_t* __restrict__ comp_off, const uint32_t* __restrict__ comp_win,
+    const uint32_t* __restrict__ comp_los, const double* __restrict__ comp_w, const uint32_t* __restrict__ los_off,
+    const uint32_t* __restrict__ los_idx, const double* __restrict__ approx, double* __restrict__ der1,
+    double* __restrict__ der2) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const double ai = approx[i];
+    const uint32_t own0 = comp_off[i], own1 = comp_off[i + 1];
+    const uint32_t l0 = los_off[i], l1 = los_off[i + 1];
+    double d1 = 0.0, d2 = 0.0;
+    uint32_t q = l0;
+    for (; q < l1 && los_idx[q] < own0; ++q) {   // winners before row i
+        const uint32_t k = los_idx[q];
+        const double p = pairlogit_p(approx[comp_win[k]], ai), w = comp_w[k];
+        d1 -= w * p;
+        d2 += w * p * (p - 1.0);
+    }
+    double wd = 0.0, wd2 = 0.0;
+    for (uint32_t k = own0; k < own1; ++k) {   // row i's own pairs
+        const uint32_t l = comp_los[k];
+        const double p = pairlogit_p(ai, approx[l]), w = comp_w[k];
+        wd += w * p;
+        wd2 += w * p * (p - 1.0);
+        if (l == i) {
+            d1 -= w * p;
+            d2 += w * p * (p - 1.0);
         }
     }
-    __syncthreads();
-    for (size_t i = threadIdx.x; i < cells; i += blockDim.x) {   // st index i = (pair, bucket, c)
-        const size_t pr = i / (2 * B), rem = i % (2 * B);
-        const long long v = sh_st[(pr * 2 + (rem & 1)) * B + (rem >> 1)];
-        if (v != 0) atomicAdd(out + i, (unsigned long long)v);
+    d1 += wd;
+    d2 += wd2;
+    for (; q < l1; ++q) {   // winners after row i (its own pairs with itself were taken above)
+        const uint32_t k = los_idx[q];
+        if (k < own1) continue;
+        const double p = pairlogit_p(approx[comp_win[k]], ai), w = comp_w[k];
+        d1 -= w * p;
+        d2 += w * p * (p - 1.0);
     }
+    der1[i] = d1;
+    der2[i] = d2;
 }
 
-// ---- statistics with many parents (P >= 8): pairs grouped by their unordered leaf pair
-// {a, b}; one workgroup per (feature, leaf pair) owns the cells [a][b][*][*] and [b][a][*][*]
-// of that feature, accumulates them in LDS, takes the prefix over buckets and writes the
-// cumulative values (no zeroing, no global atomics, no separate scan).
+// ---- pairs grouped by their unordered leaf pair {a <= b} (levels of 2 leaves and more)
 
 __device__ __forceinline__ uint32_t pair_key(uint32_t wl, uint32_t ll, uint32_t P) {
     return wl < ll ? wl * P + ll : ll * P + wl;
@@ -178,34 +117,6 @@ static __global__ __launch_bounds__(256) void pair_key_count_kernel(
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < P * P; i += blockDim.x)
         if (c[i]) atomicAdd(cnt + i, c[i]);
-}
-
-// Exclusive scan of the P*P key counts (one workgroup of 1024 threads, each over a run of
-// ceil(nk / 1024) consecutive keys): key_off[P*P + 1], cursor = key_off[0 .. P*P).
-static __global__ __launch_bounds__(1024) void pair_key_scan_kernel(const uint32_t* __restrict__ cnt, uint32_t nk,
-                                                                    uint32_t* __restrict__ key_off,
-                                                                    uint32_t* __restrict__ cursor) {
-    __shared__ uint32_t sh[1024];
-    const uint32_t t = threadIdx.x;
-    const uint32_t per = (nk + 1023) / 1024;
-    const uint32_t k0 = min(t * per, nk), k1 = min(k0 + per, nk);
-    uint32_t v = 0;
-    for (uint32_t k = k0; k < k1; ++k) v += cnt[k];
-    sh[t] = v;
-    __syncthreads();
-    for (uint32_t o = 1; o < 1024; o <<= 1) {
-        const uint32_t a = t >= o ? sh[t - o] : 0u;
-        __syncthreads();
-        sh[t] += a;
-        __syncthreads();
-    }
-    uint32_t run = sh[t] - v;
-    for (uint32_t k = k0; k < k1; ++k) {
-        key_off[k] = run;
-        cursor[k] = run;
-        run += cnt[k];
-    }
-    if (t == 1023) key_off[nk] = sh[t];
 }
 
 // Scatter the pairs by key as compact records (order inside a key is free: the sums are
@@ -249,138 +160,104 @@ static __global__ __launch_bounds__(256) void pair_key_scatter_kernel(
     }
 }
 
-// Feature tiles of the keyed statistics: tf features (a multiple of 4, whole row words) whose
-// cells [tf][2][B][2] fit the LDS budget.
-inline uint32_t pair_tile_features(uint32_t F, uint32_t B, size_t budget) {
-    const size_t per_f = (size_t)2 * B * 2 * sizeof(long long);
-    uint32_t tf = (uint32_t)(budget / per_f) & ~3u;
-    if (tf < 4) tf = 4;
-    return std::min<uint32_t>(tf, (F + 3) / 4 * 4);
-}
+// ---- statistics with feature lanes: one workgroup per (leaf-pair key, chunk of its pairs,
+// tile of 16 features).  16 lanes take the 16 features of one pair, so the two atomics of a
+// (pair, feature) land in LDS cells laid out [bucket][channel][block][16 features]: the 16 lanes
+// of a pair always hit 16 distinct bank pairs (the block and feature give the bank; the bucket
+// only the row).  A key whose pairs fit one chunk writes its cumulative runs straight into the
+// statistics; the chunks of a larger key add their cells into a zeroed region that
+// pair_multi_scan_kernel then turns into prefix form.
 
-// Inclusive prefix, in place, of nseq contiguous runs of B values in LDS (run q starts at
-// base + q B): a workgroup-wide two-level scan, tps threads per run.
-__device__ inline void lds_runs_prefix(unsigned long long* base, uint32_t nseq, uint32_t B,
-                                       unsigned long long* part /* [blockDim.x] */) {
-    uint32_t tps = 1;
-    while (tps * 2 * nseq <= blockDim.x && tps * 2 <= 64) tps *= 2;
-    const uint32_t t = threadIdx.x, q = t / tps, j = t % tps;
-    const uint32_t chunk = (B + tps - 1) / tps;
-    const uint32_t b0 = min(j * chunk, B), b1 = min(b0 + chunk, B);
-    unsigned long long* p = q < nseq ? base + (size_t)q * B : nullptr;
-    unsigned long long run = 0;
-    if (p)
-        for (uint32_t bb = b0; bb < b1; ++bb) {
-            run += p[bb];
-            p[bb] = run;
-        }
-    part[t] = run;
-    __syncthreads();
-    if (p && j > 0) {
-        unsigned long long off = 0;
-        for (uint32_t i = 0; i < j; ++i) off += part[q * tps + i];
-        for (uint32_t bb = b0; bb < b1; ++bb) p[bb] += off;
-    }
-    __syncthreads();
-}
+constexpr uint32_t kStatTileF = 16;       // features per tile (lanes of one pair)
+constexpr uint32_t kStatThreads = 1024;   // 64 pairs per pass of a workgroup
+constexpr uint32_t kStatChunkMin = 4096;  // pairs per chunk: at least, the session picks per level
 
-// One workgroup per (leaf pair {a <= b}, feature tile).  Each pair reads the row words of its
-// winner and loser once for the whole tile.  Writes the cumulative statistics of the cells [a][b] and
-// [b][a] of the tile's features, whole bucket runs (every cell of st is written once per
-// level: no zeroing, no global atomics, no separate scan).
-static __global__ __launch_bounds__(256) void pair_stats_key_kernel(
-    const uint32_t* __restrict__ rows, uint32_t W, const uint2* __restrict__ rec,
-    const long long* __restrict__ rec_wq, const uint32_t* __restrict__ key_off, uint32_t F,
-    uint32_t P, uint32_t B, uint32_t tf, uint32_t n_tiles, long long* __restrict__ st) {
-    extern __shared__ unsigned long long cell_k[];   // [tf][blk][c][bucket]
-    // block ids go round-robin over the 8 XCDs: the tiles of one leaf pair run on one XCD,
-    // consecutively, so the rows its pairs gather come from that XCD's L2 after the first tile
-    const uint32_t bid = blockIdx.x;
-    const uint32_t xcd = bid & 7u, q = bid >> 3;
-    const uint32_t tile = q % n_tiles;
-    const uint32_t idx = (q / n_tiles) * 8u + xcd;   // leaf pair {a <= b}: idx = b (b + 1) / 2 + a
-    if (idx >= P * (P + 1) / 2) return;
-    uint32_t b = (uint32_t)((sqrtf(8.0f * (float)idx + 1.0f) - 1.0f) * 0.5f);
-    while (b * (b + 1) / 2 > idx) --b;
-    while ((b + 1) * (b + 2) / 2 <= idx) ++b;
-    const uint32_t a = idx - b * (b + 1) / 2;
-    const uint32_t key = a * P + b;
-    const uint32_t f0 = tile * tf;
-    const uint32_t nf = min(tf, F - f0);
-    const uint32_t w0 = f0 / 4, nw = (nf + 3) / 4;
-    const size_t per_f = (size_t)2 * B * 2;
-    for (size_t i = threadIdx.x; i < (size_t)nf * per_f; i += blockDim.x) cell_k[i] = 0;
-    __syncthreads();
-    const uint32_t j0 = key_off[key], j1 = key_off[key + 1];
-    for (uint32_t jb = j0 + threadIdx.x; jb < j1; jb += blockDim.x * kKeyLoadAhead) {
-        // kKeyLoadAhead pairs per thread at a time: records first, then kKeyWords row words
-        // of each winner and loser, all in flight together
-        uint2 r[kKeyLoadAhead];
-        long long wq[kKeyLoadAhead];
-#pragma unroll
-        for (uint32_t u = 0; u < kKeyLoadAhead; ++u) {
-            const uint32_t j = jb + u * blockDim.x;
-            const bool ok = j < j1;
-            r[u] = ok ? rec[j] : make_uint2(0u, 0u);
-            wq[u] = ok ? rec_wq[j] : 0;
-        }
-        for (uint32_t wc = 0; wc < nw; wc += kKeyWords) {
-            uint32_t ww[kKeyLoadAhead][kKeyWords], wlw[kKeyLoadAhead][kKeyWords];
-#pragma unroll
-            for (uint32_t u = 0; u < kKeyLoadAhead; ++u)
-#pragma unroll
-                for (uint32_t w = 0; w < kKeyWords; ++w) {
-                    const uint32_t wa = wc + w < nw ? w0 + wc + w : w0;   // in-row, in-bounds
-                    ww[u][w] = rows[(size_t)r[u].x * W + wa];
-                    wlw[u][w] = rows[(size_t)(r[u].y & 0x7FFFFFFFu) * W + wa];
-                }
-#pragma unroll
-            for (uint32_t u = 0; u < kKeyLoadAhead; ++u) {
-                if (jb + u * blockDim.x >= j1) continue;
-                const bool win_in_a = (r[u].y >> 31) != 0;
-                const unsigned long long neg = (unsigned long long)(-wq[u]);
-#pragma unroll
-                for (uint32_t w = 0; w < kKeyWords; ++w) {
-                    if (wc + w >= nw) break;
-                    for (uint32_t k = 0; k < 4; ++k) {
-                        const uint32_t f = 4 * (wc + w) + k;
-                        if (f >= nf) break;
-                        const uint32_t wb = (ww[u][w] >> (8 * k)) & 0xFFu, lb = (wlw[u][w] >> (8 * k)) & 0xFFu;
-                        // first index x = loser leaf when wb > lb, else winner leaf; block 0 = [a][b]
-                        const uint32_t blk = a == b ? 0u : ((wb > lb) == win_in_a ? 1u : 0u);
-                        const uint32_t bs = wb > lb ? lb : wb, bg = wb > lb ? wb : lb;
-                        unsigned long long* c = cell_k + (size_t)f * per_f + (size_t)blk * B * 2;
-                        atomicAdd(c + bs, neg);
-                        atomicAdd(c + B + bg, neg);
-                    }
-                }
-            }
-        }
+// Chunk plan of one level (one workgroup of 1024 threads, each over a run of consecutive keys):
+// key_off / cursor = exclusive scan of the pair counts of the P*P keys (pair_key_scatter), and
+// per key {a <= b}: max(1, ceil(count / chunk)) chunk descriptors {key, first pair, pairs,
+// multi}; keys of several chunks are also listed in mk.  direct: one key (a single leaf) over
+// the m pairs in input order.
+static __global__ __launch_bounds__(1024) void pair_plan_kernel(
+    const uint32_t* __restrict__ cnt, uint32_t P, int direct, uint32_t m, uint32_t chunk, uint32_t* __restrict__ key_off,
+    uint32_t* __restrict__ cursor, uint4* __restrict__ desc, uint32_t* __restrict__ n_desc,
+    uint32_t* __restrict__ mk, uint32_t* __restrict__ n_multi) {
+    __shared__ uint32_t sc[1024], sn[1024], sm[1024];
+    const uint32_t t = threadIdx.x;
+    const uint32_t nk = direct ? 1u : P * P;
+    const uint32_t per = (nk + 1023) / 1024;
+    const uint32_t k0 = min(t * per, nk), k1 = min(k0 + per, nk);
+    auto count_of = [&](uint32_t k) -> uint32_t { return direct ? m : cnt[k]; };
+    auto chunks_of = [&](uint32_t k, uint32_t c) -> uint32_t {
+        if (!direct && k / P > k % P) return 0u;   // keys are {min, max}
+        return c == 0 ? 1u : (c + chunk - 1) / chunk;
+    };
+    uint32_t vc = 0, vn = 0, vm = 0;
+    for (uint32_t k = k0; k < k1; ++k) {
+        const uint32_t c = count_of(k), nc = chunks_of(k, c);
+        vc += c;
+        vn += nc;
+        vm += nc > 1 ? 1u : 0u;
     }
+    sc[t] = vc;
+    sn[t] = vn;
+    sm[t] = vm;
     __syncthreads();
-    // prefix over buckets of every (f, blk, c) run
-    __shared__ unsigned long long part[256];
-    lds_runs_prefix(cell_k, nf * 4, B, part);
-    const uint32_t nblk = a == b ? 1u : 2u;
-    for (uint32_t fb = 0; fb < nf * nblk; ++fb) {   // whole contiguous runs of 2B values
-        const uint32_t f = fb / nblk, blk = fb % nblk;
-        const uint32_t x = blk == 0 ? a : b, y = blk == 0 ? b : a;
-        const unsigned long long* src = cell_k + (size_t)f * per_f + (size_t)blk * B * 2;
-        long long* dst = st + (((size_t)(f0 + f) * P + x) * P + y) * B * 2;
-        for (uint32_t i = threadIdx.x; i < 2 * B; i += blockDim.x) dst[i] = (long long)src[(i & 1u) * B + (i >> 1)];
+    for (uint32_t o = 1; o < 1024; o <<= 1) {
+        const uint32_t ac = t >= o ? sc[t - o] : 0u, an = t >= o ? sn[t - o] : 0u, am = t >= o ? sm[t - o] : 0u;
+        __syncthreads();
+        sc[t] += ac;
+        sn[t] += an;
+        sm[t] += am;
+        __syncthreads();
+    }
+    uint32_t oc = sc[t] - vc, on = sn[t] - vn, om = sm[t] - vm;
+    for (uint32_t k = k0; k < k1; ++k) {
+        const uint32_t c = count_of(k), nc = chunks_of(k, c);
+        if (!direct) {
+            key_off[k] = oc;
+            cursor[k] = oc;
+        }
+        for (uint32_t j = 0; j < nc; ++j)
+            desc[on + j] = make_uint4(k, oc + j * chunk, min(chunk, c - j * chunk), nc > 1 ? 1u : 0u);
+        if (nc > 1) mk[om++] = k;
+        oc += c;
+        on += nc;
+    }
+    if (t == 1023) {
+        if (!direct) key_off[nk] = sc[t];
+        *n_desc = sn[t];
+        *n_multi = sm[t];
     }
 }
 
-// Inclusive prefix over the bucket axis, in place: one wavefront per (f, x, y, c) run of B
-// values at stride 2; lane l takes buckets [l k, l k + k), k = ceil(B / 64), and the lane
-// totals are scanned across the wave.
-static __global__ __launch_bounds__(256) void pair_scan_kernel(long long* __restrict__ st, uint32_t n_runs,
-                                                               uint32_t B) {
-    const uint32_t run = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (run >= n_runs) return;
-    long long* p = st + (size_t)(run >> 1) * B * 2 + (run & 1u);
-    const uint32_t k = (B + 63) / 64;
-    const uint32_t b0 = min(lane * k, B), b1 = min(b0 + k, B);
+// Zero the statistics runs of the keys of several chunks (grid: (max multi keys, F)).
+static __global__ __launch_bounds__(256) void pair_multi_zero_kernel(const uint32_t* __restrict__ mk,
+                                                                     const uint32_t* __restrict__ n_multi, uint32_t P,
+                                                                     uint32_t B, long long* __restrict__ st) {
+    if (blockIdx.x >= *n_multi) return;
+    const uint32_t k = mk[blockIdx.x], a = k / P, b = k % P, f = blockIdx.y;
+    long long* r0 = st + (((size_t)f * P + a) * P + b) * B * 2;
+    long long* r1 = st + (((size_t)f * P + b) * P + a) * B * 2;
+    for (uint32_t i = threadIdx.x; i < 2 * B; i += blockDim.x) {
+        r0[i] = 0;
+        r1[i] = 0;
+    }
+}
+
+// Inclusive prefix over buckets of the runs of the keys of several chunks: one wavefront per
+// (block, channel) run of a (key, feature); lane l takes buckets [l k, l k + k), k = ceil(B / 64).
+static __global__ __launch_bounds__(256) void pair_multi_scan_kernel(const uint32_t* __restrict__ mk,
+                                                                     const uint32_t* __restrict__ n_multi, uint32_t P,
+                                                                     uint32_t B, long long* __restrict__ st) {
+    if (blockIdx.x >= *n_multi) return;
+    const uint32_t k = mk[blockIdx.x], a = k / P, b = k % P, f = blockIdx.y;
+    const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63;   // w = block * 2 + channel
+    const uint32_t blk = w >> 1, c = w & 1u;
+    if (blk == 1 && a == b) return;
+    const uint32_t x = blk == 0 ? a : b, y = blk == 0 ? b : a;
+    long long* p = st + (((size_t)f * P + x) * P + y) * B * 2 + c;
+    const uint32_t kk = (B + 63) / 64;
+    const uint32_t b0 = min(lane * kk, B), b1 = min(b0 + kk, B);
     long long v[4];   // B <= 256
     long long tot = 0;
 #pragma unroll
@@ -392,13 +269,162 @@ static __global__ __launch_bounds__(256) void pair_scan_kernel(long long* __rest
     long long incl = tot;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const long long t = __shfl_up(incl, o, 64);
-        if ((int)lane >= o) incl += t;
+        const long long tt = __shfl_up(incl, o, 64);
+        if ((int)lane >= o) incl += tt;
     }
     const long long off = incl - tot;
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i)
         if (b0 + i < b1) p[(size_t)(b0 + i) * 2] = v[i] + off;
+}
+
+// Accumulate one chunk of one key's pairs for one tile of 16 features (grid: (max descriptors,
+// feature tiles)).  Records come grouped by key (rec: winner, loser | winner-in-leaf-a << 31),
+// or, at a level of one leaf, straight from the pair arrays (direct).  For a pair with winner
+// bucket > loser bucket the cells [loserLeaf][winnerLeaf] receive -w at (loser bucket, smaller)
+// and (winner bucket, greater), otherwise [winnerLeaf][loserLeaf] at (winner bucket, smaller)
+// and (loser bucket, greater) (compute_pair_weight_statistics, pairwise_scoring.rs:163-196);
+// block 0 of a key {a <= b} is [a][b], block 1 is [b][a].
+template <bool kBuf>   // row words by 32-bit buffer offsets (the row buffer is under 4 GiB)
+static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel(
+    const uint32_t* __restrict__ rows, uint32_t Ws, const uint4* __restrict__ desc, const uint32_t* __restrict__ n_desc,
+    const uint2* __restrict__ rec, const long long* __restrict__ rec_wq, const uint32_t* __restrict__ comp_win,
+    const uint32_t* __restrict__ comp_los, const long long* __restrict__ comp_wq, int direct, uint32_t F, uint32_t P,
+    uint32_t B, long long* __restrict__ st) {
+    extern __shared__ unsigned long long cells[];   // [B][channel][block][16]
+    if (blockIdx.x >= *n_desc) return;
+    const uint4 ds = desc[blockIdx.x];
+    const uint32_t key = ds.x, a = key / P, b = key % P;
+    const uint32_t t = threadIdx.x, fl = t & 15, slot = t >> 4;
+    const uint32_t f = blockIdx.y * kStatTileF + fl;
+    const bool fok = f < F;
+    const uint32_t word = (fok ? f : F - 1) >> 2, sh = (f & 3u) * 8u;
+    for (uint32_t i = t; i < B * 64; i += kStatThreads) cells[i] = 0;
+    __syncthreads();
+    // each 16-lane row takes 16 consecutive pairs per pass: lane fl loads the record of pair
+    // fl (one coalesced load for the row, the next pass's prefetched), the records reach the
+    // row's lanes by row_newbcast, and the 32 row words of the 16 pairs are loaded together
+    const uint32_t first = ds.y, cnt = ds.z;
+    constexpr uint32_t kRows = kStatThreads / 16, kPass = kRows * 16;
+    auto load_rec = [&](uint32_t j, uint32_t& wi, uint32_t& lo, uint32_t& wa, long long& wq) {
+        const bool ok = j < cnt;
+        const size_t k = (size_t)first + (ok ? j : 0u);
+        if (direct) {
+            wi = ok ? comp_win[k] : 0u;
+            lo = ok ? comp_los[k] : 0u;
+            wa = 0;
+            wq = ok ? comp_wq[k] : 0;
+        } else {
+            const uint2 r = ok ? rec[k] : make_uint2(0u, 0u);
+            wi = r.x;
+            lo = r.y & 0x7FFFFFFFu;
+            wa = r.y >> 31;
+            wq = ok ? rec_wq[k] : 0;
+        }
+    };
+    const uint32_t row = t >> 4;
+    uint32_t n_wi, n_lo, n_wa;
+    long long n_wq;
+    load_rec(row * 16 + fl, n_wi, n_lo, n_wa, n_wq);
+    for (uint32_t base = row * 16; base < cnt; base += kPass) {
+        const uint32_t c_wi = n_wi, c_lo = n_lo, c_wa = n_wa;
+        const long long c_wq = n_wq;
+        load_rec(base + kPass + fl, n_wi, n_lo, n_wa, n_wq);   // the next pass's records
+        uint32_t wi[16], lo[16], ww[16], lw[16];
+        wi[0] = row_bcast<0>(c_wi); lo[0] = row_bcast<0>(c_lo);
+        wi[1] = row_bcast<1>(c_wi); lo[1] = row_bcast<1>(c_lo);
+        wi[2] = row_bcast<2>(c_wi); lo[2] = row_bcast<2>(c_lo);
+        wi[3] = row_bcast<3>(c_wi); lo[3] = row_bcast<3>(c_lo);
+        wi[4] = row_bcast<4>(c_wi); lo[4] = row_bcast<4>(c_lo);
+        wi[5] = row_bcast<5>(c_wi); lo[5] = row_bcast<5>(c_lo);
+        wi[6] = row_bcast<6>(c_wi); lo[6] = row_bcast<6>(c_lo);
+        wi[7] = row_bcast<7>(c_wi); lo[7] = row_bcast<7>(c_lo);
+        wi[8] = row_bcast<8>(c_wi); lo[8] = row_bcast<8>(c_lo);
+        wi[9] = row_bcast<9>(c_wi); lo[9] = row_bcast<9>(c_lo);
+        wi[10] = row_bcast<10>(c_wi); lo[10] = row_bcast<10>(c_lo);
+        wi[11] = row_bcast<11>(c_wi); lo[11] = row_bcast<11>(c_lo);
+        wi[12] = row_bcast<12>(c_wi); lo[12] = row_bcast<12>(c_lo);
+        wi[13] = row_bcast<13>(c_wi); lo[13] = row_bcast<13>(c_lo);
+        wi[14] = row_bcast<14>(c_wi); lo[14] = row_bcast<14>(c_lo);
+        wi[15] = row_bcast<15>(c_wi); lo[15] = row_bcast<15>(c_lo);
+        if constexpr (kBuf) {
+            const __amdgpu_buffer_rsrc_t rr = make_rsrc(rows, 0xFFFFFFFFull);
+#pragma unroll
+            for (uint32_t u = 0; u < 16; ++u) {
+                ww[u] = ldw(rr, (wi[u] * Ws + word) * 4u);
+                lw[u] = ldw(rr, (lo[u] * Ws + word) * 4u);
+            }
+        } else {
+#pragma unroll
+            for (uint32_t u = 0; u < 16; ++u) {
+                ww[u] = rows[(size_t)wi[u] * Ws + word];
+                lw[u] = rows[(size_t)lo[u] * Ws + word];
+            }
+        }
+        // pairs of this pass that add nothing: past the chunk, or winner == loser
+        uint32_t skip = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < 16; ++u) skip |= (base + u >= cnt || wi[u] == lo[u] ? 1u : 0u) << u;
+        if (!fok) skip = 0xFFFFu;
+        // (the broadcasts run in every lane: a lane switched off by the branch would read as 0)
+#define CBH_STAT_PAIR(U)                                                                                     \
+    {                                                                                                         \
+    const uint32_t wau = row_bcast<U>(c_wa);                                                                  \
+    const unsigned long long neg = (unsigned long long)(-(long long)row_bcast64<U>((unsigned long long)c_wq));   \
+    if (!((skip >> U) & 1u)) {                                                                                \
+        const uint32_t wb = (ww[U] >> sh) & 0xFFu, lb = (lw[U] >> sh) & 0xFFu;                                \
+        const uint32_t blk = a == b ? 0u : ((wb > lb) == (wau != 0) ? 1u : 0u);                               \
+        const uint32_t bs = wb > lb ? lb : wb, bg = wb > lb ? wb : lb;                                        \
+        atomicAdd(cells + ((size_t)(bs * 2 + 0) * 2 + blk) * 16 + fl, neg);                                   \
+        atomicAdd(cells + ((size_t)(bg * 2 + 1) * 2 + blk) * 16 + fl, neg);                                   \
+    }                                                                                                         \
+    }
+        CBH_STAT_PAIR(0) CBH_STAT_PAIR(1) CBH_STAT_PAIR(2) CBH_STAT_PAIR(3)
+        CBH_STAT_PAIR(4) CBH_STAT_PAIR(5) CBH_STAT_PAIR(6) CBH_STAT_PAIR(7)
+        CBH_STAT_PAIR(8) CBH_STAT_PAIR(9) CBH_STAT_PAIR(10) CBH_STAT_PAIR(11)
+        CBH_STAT_PAIR(12) CBH_STAT_PAIR(13) CBH_STAT_PAIR(14) CBH_STAT_PAIR(15)
+#undef CBH_STAT_PAIR
+    }
+    __syncthreads();
+    if (ds.w == 0) {
+        // the key's only chunk: its cumulative runs go straight into the statistics.  Thread t
+        // takes run t & 63 (= channel, block, feature: consecutive lanes read consecutive cells)
+        // and the 16 buckets of segment t >> 6; the segment totals give each segment its offset.
+        __shared__ unsigned long long seg_tot[16][64];
+        const uint32_t run = t & 63u, seg = t >> 6, c = run >> 5, blk = (run >> 4) & 1u, rf = blockIdx.y * kStatTileF + (run & 15u);
+        unsigned long long v[16];
+        unsigned long long acc = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+            const uint32_t bk = seg * 16 + i;
+            acc += bk < B ? cells[(size_t)bk * 64 + run] : 0ull;
+            v[i] = acc;
+        }
+        seg_tot[seg][run] = acc;
+        __syncthreads();
+        unsigned long long off = 0;
+        for (uint32_t g = 0; g < seg; ++g) off += seg_tot[g][run];
+        if (rf < F && (blk == 0 || a != b)) {
+            const uint32_t x = blk == 0 ? a : b, y = blk == 0 ? b : a;
+            long long* dst = st + (((size_t)rf * P + x) * P + y) * B * 2 + c;
+#pragma unroll
+            for (uint32_t i = 0; i < 16; ++i) {
+                const uint32_t bk = seg * 16 + i;
+                if (bk < B) dst[(size_t)bk * 2] = (long long)(v[i] + off);
+            }
+        }
+    } else {
+        // one chunk of several: add the raw cells (the region was zeroed; pair_multi_scan_kernel
+        // takes the prefix)
+        for (uint32_t i = t; i < B * 64; i += kStatThreads) {
+            const long long v = (long long)cells[i];
+            const uint32_t l = i & 63u, c = l >> 5, blk = (l >> 4) & 1u, ff = blockIdx.y * kStatTileF + (l & 15u);
+            if (v == 0 || ff >= F || (blk == 1 && a == b)) continue;
+            const uint32_t x = blk == 0 ? a : b, y = blk == 0 ? b : a;
+            atomicAdd((unsigned long long*)(st + ((((size_t)ff * P + x) * P + y) * B + (i >> 6)) * 2 + c),
+                      (unsigned long long)v);
+        }
+    }
 }
 
 // MakeZeroAverage (pairwise_scoring.rs:255-265), sequential sum as the reference; every
@@ -416,8 +442,9 @@ __device__ inline void zero_average_block(double* r, int n) {
     __syncthreads();
 }
 
-// In-place Cholesky of the m x m packed system M (right-looking, the reference's row order)
-// and the forward / back substitutions of y, by every thread of the workgroup (rows strided
+// In-place Cholesky of the m x m packed system M (right-looking: every element receives its
+// pivot subtractions in ascending order, as the reference's left-looking loop applies them)
+// and the forward / back substitutions of y, by the threads of the workgroup (rows strided
 // over the threads); M may be in LDS or global memory.  The forward pass writes its result
 // to fwd (y[p] is read by every thread of step p while other rows of y change), the back
 // pass to res[0..m); res[m] = 0.  A non-positive pivot gives the zero solution
@@ -466,7 +493,12 @@ __device__ inline void pairwise_factor_solve_block(double* __restrict__ M, int m
             for (int i = p + 1 + t; i < m; i += nt) y[i] -= M[tri(i, p)] * yp;
             __syncthreads();
         }
-        for (int p = m - 1; p >= 0; --p) {   // back: L^T x = y
+        // back, right-looking: x[p] = y[p] / L[p][p], then y[i] -= L[p][i] x[p] for i < p.  Row i
+        // receives its subtractions p descending where the reference's left-looking loop sums
+        // them p ascending (leaf.rs:409-415): the last bits of x may differ, as they do anyway
+        // from the fixed-point der sums; the chain of the reference's order would serialize
+        // m^2 / 2 steps
+        for (int p = m - 1; p >= 0; --p) {
             const double xp = fwd[p] / M[tri(p, p)];
             if (t == 0) res[p] = xp;
             for (int i = t; i < p; i += nt) fwd[i] -= M[tri(p, i)] * xp;
@@ -585,6 +617,186 @@ __device__ inline double readlane_f64(double v, int l) {
     const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)bits, l);
     const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(bits >> 32), l);
     return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// The weight-matrix entries between the rows of two different leaves lo < hi at one border,
+// from the cumulative statistics at that border (R, cell stride rs) and at the last border
+// (T, stride ts): one load of the four cells PairRow::wp reads.
+struct PairCells {
+    long long w00, w01, w10, w11, total;
+};
+__device__ __forceinline__ PairCells pair_cells(const long long* R, uint32_t rs, const long long* T, uint32_t ts,
+                                                uint32_t P, uint32_t lo, uint32_t hi) {
+    const long long xs = R[(size_t)(hi * P + lo) * rs], xg = R[(size_t)(hi * P + lo) * rs + 1];
+    const long long ys = R[(size_t)(lo * P + hi) * rs], yg = R[(size_t)(lo * P + hi) * rs + 1];
+    const long long total = T[(size_t)(hi * P + lo) * ts] + T[(size_t)(lo * P + hi) * ts];
+    return {xg + yg, xs - xg, ys - yg, -(xs + ys), total};
+}
+// Row (a, u) of the system at the columns (2b, 2b + 1) of another leaf b, and that block's part
+// of the row's diagonal entry (PairRow::wp with a > b given as a_gt_b).
+__device__ __forceinline__ void pair_row_entries(const PairCells& c, bool a_gt_b, uint32_t u, long long& e0,
+                                                 long long& e1, long long& dpart) {
+    if (u == 0) {
+        e0 = c.w00;
+        e1 = a_gt_b ? c.w01 : c.w10;
+        dpart = a_gt_b ? (c.w00 + c.w01) : (c.w00 + c.w10);
+    } else {
+        e0 = a_gt_b ? c.w10 : c.w01;
+        e1 = c.w11 + c.total;
+        dpart = (a_gt_b ? (c.w10 + c.w11) : (c.w01 + c.w11)) + c.total;
+    }
+}
+
+// Levels of up to 8 leaves (2P <= 16 unknowns): one border per lane, 64 consecutive borders of
+// one feature per wavefront, the whole system in the lane's registers (calculate_pairwise_score,
+// pairwise_scoring.rs:471-581).  Every IEEE operation is the reference's, in its order:
+// the matrix M = W + prior terms, the Cholesky factorization (leaf.rs:363-389, here
+// right-looking: every element receives its pivot subtractions in ascending order), the
+// forward and back substitutions with their sums taken p ascending (:390-423), a non-positive
+// pivot giving zeros, MakeZeroAverage, and the score with sequential inner and outer sums
+// (calculate_score :352-375).  A lane's statistics of one cell are 16 bytes at stride 16 bytes
+// from its neighbour's: every load is one contiguous 1 KB run per wavefront.
+template <uint32_t P_>
+static __global__ __launch_bounds__(64) void pairwise_candidate_lane_kernel(
+    const long long* __restrict__ st, const long long* __restrict__ hist, uint32_t C, uint32_t F,
+    const uint32_t* __restrict__ n_cand, uint32_t B, const Scales* __restrict__ sc, double pair_inv,
+    double l2, double prior, double* __restrict__ scores /* [F][B] */) {
+    constexpr uint32_t P = P_;
+    constexpr int n = 2 * (int)P, m = n - 1;
+    constexpr int nL = m * (m + 1) / 2;
+    static_assert(P >= 1 && P <= 8, "register-resident systems up to 15 unknowns");
+    const uint32_t f = blockIdx.y;
+    const uint32_t s = blockIdx.x * 64 + threadIdx.x;
+    if (s >= B - 1) return;
+    if (s >= n_cand[f]) {
+        scores[(size_t)f * B + s] = -INFINITY;
+        return;
+    }
+    const long long* base = st + (size_t)f * P * P * B * 2;
+    const long long* R = base + (size_t)s * 2;
+    const long long* T = base + (size_t)(B - 1) * 2;
+    const uint32_t rs = 2 * B;
+    const double inv_d = sc->inv[kScoreDer];
+    double der[n];
+#pragma unroll
+    for (uint32_t yl = 0; yl < P; ++yl) {   // der channel of the level histogram, prefix over bins
+        const long long* h = hist + ((size_t)yl * C * F + f) * B;
+        const long long dp = h[s], dt = h[B - 1];
+        der[2 * yl] = (double)dp * inv_d;
+        der[2 * yl + 1] = (double)(dt - dp) * inv_d;
+    }
+    const double cell_prior = 1.0 / (double)n;
+    const double non_diag = -prior * cell_prior;
+    const double diag = prior * (1.0 - cell_prior) + l2;
+    // ---- M (packed lower triangle, rows < m) and the diagonal entries of W (every row) ----
+    double L[nL];
+    long long dg[n], da[P];
+#pragma unroll
+    for (uint32_t a = 0; a < P; ++a) {
+        da[a] = R[(size_t)(a * P + a) * rs] - R[(size_t)(a * P + a) * rs + 1];
+        dg[2 * a] = -da[a];
+        dg[2 * a + 1] = -da[a];
+    }
+#pragma unroll
+    for (uint32_t hi = 1; hi < P; ++hi)
+#pragma unroll
+        for (uint32_t lo = 0; lo < hi; ++lo) {
+            const PairCells c = pair_cells(R, rs, T, rs, P, lo, hi);
+#pragma unroll
+            for (uint32_t u = 0; u < 2; ++u) {
+                long long e0, e1, dp;
+                pair_row_entries(c, true, u, e0, e1, dp);   // row of leaf hi, columns of lo (below the diagonal)
+                dg[2 * hi + u] -= dp;
+                const int r = 2 * (int)hi + (int)u;
+                if (r < m) {
+                    L[tri(r, 2 * lo)] = (double)e0 * pair_inv + non_diag;
+                    L[tri(r, 2 * lo + 1)] = (double)e1 * pair_inv + non_diag;
+                }
+                pair_row_entries(c, false, u, e0, e1, dp);  // row of leaf lo: above the diagonal
+                dg[2 * lo + u] -= dp;
+            }
+        }
+#pragma unroll
+    for (int r = 0; r < m; ++r) {
+        L[tri(r, r)] = (double)dg[r] * pair_inv + diag;
+        if (r & 1) L[tri(r, r - 1)] = (double)da[r >> 1] * pair_inv + non_diag;
+    }
+    // ---- solve ----
+    double x[n];
+    x[m] = 0.0;
+    if constexpr (m == 1) {   // one leaf: the 1 x 1 system (the reference's n == 2 case)
+        const double den = L[0];
+        x[0] = den != 0.0 ? der[0] / den : 0.0;
+    } else {
+        bool good = true;
+#pragma unroll
+        for (int j = 0; j < m; ++j) {
+            const double d = L[tri(j, j)];
+            if (d <= 0.0) good = false;   // the reference returns None; the rest is discarded
+            const double ljj = sqrt(d);
+#pragma unroll
+            for (int i = j + 1; i < m; ++i) L[tri(i, j)] = L[tri(i, j)] / ljj;
+            L[tri(j, j)] = ljj;
+#pragma unroll
+            for (int i = j + 1; i < m; ++i)
+#pragma unroll
+                for (int k = j + 1; k <= i; ++k) L[tri(i, k)] = L[tri(i, k)] - L[tri(i, j)] * L[tri(k, j)];
+        }
+        double y[m];
+#pragma unroll
+        for (int i = 0; i < m; ++i) {   // forward: L y = der
+            double sum = der[i];
+#pragma unroll
+            for (int p = 0; p < i; ++p) sum -= L[tri(i, p)] * y[p];
+            y[i] = sum / L[tri(i, i)];
+        }
+#pragma unroll
+        for (int i = m - 1; i >= 0; --i) {   // back: L^T x = y
+            double sum = y[i];
+#pragma unroll
+            for (int p = i + 1; p < m; ++p) sum -= L[tri(p, i)] * x[p];
+            x[i] = sum / L[tri(i, i)];
+        }
+        if (!good)
+#pragma unroll
+            for (int i = 0; i < m; ++i) x[i] = 0.0;
+    }
+    {   // MakeZeroAverage (pairwise_scoring.rs:255-265)
+        double avg = 0.0;
+#pragma unroll
+        for (int i = 0; i < n; ++i) avg += x[i];
+        avg = avg / (double)n;
+#pragma unroll
+        for (int i = 0; i < n; ++i) x[i] -= avg;
+    }
+    // ---- score: rows of W in column order (b ascending), inner sums per row ----
+    double inner[n];
+#pragma unroll
+    for (int i = 0; i < n; ++i) inner[i] = 0.0;
+#pragma unroll
+    for (uint32_t b = 0; b < P; ++b)
+#pragma unroll
+        for (uint32_t a = 0; a < P; ++a) {
+#pragma unroll
+            for (uint32_t u = 0; u < 2; ++u) {
+                const int r = 2 * (int)a + (int)u;
+                long long e0, e1;
+                if (a == b) {
+                    e0 = u == 0 ? dg[r] : da[a];
+                    e1 = u == 0 ? da[a] : dg[r];
+                } else {
+                    const PairCells c = pair_cells(R, rs, T, rs, P, a < b ? a : b, a < b ? b : a);
+                    long long dp;
+                    pair_row_entries(c, a > b, u, e0, e1, dp);
+                }
+                inner[r] += x[2 * b] * ((double)e0 * pair_inv);
+                inner[r] += x[2 * b + 1] * ((double)e1 * pair_inv);
+            }
+        }
+    double outer = 0.0;
+#pragma unroll
+    for (int i = 0; i < n; ++i) outer += x[i] * (der[i] - 0.5 * inner[i]);
+    scores[(size_t)f * B + s] = outer;
 }
 
 // One wavefront per (border s, feature f) at a level of P_ leaves: the weight matrix of border

@@ -155,6 +155,8 @@ struct cbh_session {
     uint64_t n_pairs = 0;
     double pair_inv = 1.0;
     uint32_t* group_off = nullptr;   // [n_groups + 1]
+    uint32_t* los_off = nullptr;     // [n + 1] pairs of each row as a loser: los_idx[los_off[i] ..]
+    uint32_t* los_idx = nullptr;     // [m] their indices in competitor order, ascending
     uint32_t* comp_off = nullptr;    // [n + 1]
     uint32_t* comp_win = nullptr;    // [m]
     uint32_t* comp_los = nullptr;    // [m]
@@ -169,9 +171,11 @@ struct cbh_session {
     uint32_t* key_off = nullptr;     // [Pmax^2 + 1]
     uint32_t* key_cur = nullptr;     // [Pmax^2]
     uint2* key_rec = nullptr;        // [m] pair records grouped by leaf pair
-    uint32_t* pair_lv = nullptr;     // [m] leaves of winner and loser of every pair, this level
     long long* key_wq = nullptr;     // [m]
-    uint32_t pair_tf = 4, pair_tiles = 1;
+    uint4* pair_desc = nullptr;      // chunk descriptors of a level's statistics (pair_plan_kernel)
+    uint32_t pair_cus = 256;         // CUs of the device: a level's chunks are sized to fill them once
+    uint32_t* pair_mk = nullptr;     // keys of several chunks
+    uint32_t* pair_nd = nullptr;     // [2] descriptors, keys of several chunks
     double* pair_ws = nullptr;       // global workspace of the 256-leaf solves (depth 8)
     uint32_t pair_cand_wgs = 0;      // workgroups of the 128-leaf-level candidate solves (global workspace)
     size_t pair_leaf_lds = 0;        // LDS of the leaf solve (0: global workspace)
@@ -260,10 +264,11 @@ struct cbh_session {
         dfree(out_dev);
         plans = nullptr; splits = nullptr; bounds = nullptr; leaf_raw = nullptr;
         dfree(partials);
-        dfree(group_off); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
+        dfree(group_off); dfree(los_off); dfree(los_idx); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st);
         dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows);
-        dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_lv); dfree(pair_ws);
+        dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_ws);
+        dfree(pair_desc); dfree(pair_mk); dfree(pair_nd);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
         dfree(phantom_cnt); dfree(fweight); dfree(ctr_pow); dfree(ctr_group_dev); dfree(ctr_used_dev);
         dfree(phantom_off_lv);
@@ -416,15 +421,15 @@ int session_alloc(cbh_session* s) {
         CHECK(dalloc(&s->key_cnt, pmax * pmax));
         CHECK(dalloc(&s->key_off, pmax * pmax + 1));
         CHECK(dalloc(&s->key_cur, pmax * pmax));
-        s->pair_tf = pair_tile_features(s->F, s->B, 64 * 1024);
-        s->pair_tiles = (s->F + s->pair_tf - 1) / s->pair_tf;
-        HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_key_kernel,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)((size_t)s->pair_tf * 2 * s->B * 2 * sizeof(long long))));
+        CHECK(dalloc(&s->pair_nd, 2));
+        int cus = 0;
+        HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
+        s->pair_cus = (uint32_t)std::max(cus, 1);
         // every LDS size a level can ask for is set here, before any tree is recorded as a graph
-        const size_t p4 = std::min<size_t>(pmax, 4);
-        HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)((size_t)s->B * p4 * p4 * 2 * sizeof(long long))));
+        HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_feature_kernel<true>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)s->B * 64 * sizeof(long long))));
+        HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_feature_kernel<false>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)s->B * 64 * sizeof(long long))));
         HIP_TRY(hipFuncSetAttribute((const void*)pair_key_count_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)(pmax * pmax * sizeof(uint32_t))));
         HIP_TRY(hipFuncSetAttribute((const void*)pair_key_scatter_kernel,
@@ -1094,23 +1099,35 @@ int upload_pairs(cbh_session* s, const cbh_family* fam) {
     const int shift = std::min(60 - e, 100);
     std::vector<long long> wq(m);
     for (uint64_t j = 0; j < m; ++j) wq[j] = std::llrint(std::ldexp(w[j], shift));
+    // the pairs of each row as a loser, ascending in competitor order (a stable counting sort)
+    std::vector<uint32_t> loff(n + 1, 0), lidx(m);
+    for (uint64_t j = 0; j < m; ++j) loff[los[j] + 1]++;
+    for (uint64_t i = 0; i < n; ++i) loff[i + 1] += loff[i];
+    {
+        std::vector<uint32_t> lpos(loff.begin(), loff.end() - 1);
+        for (uint64_t j = 0; j < m; ++j) lidx[lpos[los[j]]++] = (uint32_t)j;
+    }
     // a recorded tree holds the pair count, the group count, the weight scale and the pair
     // buffers: a change of any of them records it again
     if (m != s->n_pairs || G != s->n_groups || std::ldexp(1.0, -shift) != s->pair_inv) drop_tree_graphs(s);
     s->pair_inv = std::ldexp(1.0, -shift);
     if (m != s->n_pairs || !s->comp_win) {
-        dfree(s->comp_win); dfree(s->comp_los); dfree(s->comp_w); dfree(s->comp_wq);
-        dfree(s->key_rec); dfree(s->key_wq); dfree(s->pair_lv);
+        dfree(s->comp_win); dfree(s->comp_los); dfree(s->comp_w); dfree(s->comp_wq); dfree(s->los_idx);
+        dfree(s->key_rec); dfree(s->key_wq); dfree(s->pair_desc); dfree(s->pair_mk);
         CHECK(dalloc(&s->comp_win, m));
         CHECK(dalloc(&s->comp_los, m));
         CHECK(dalloc(&s->comp_w, m));
         CHECK(dalloc(&s->comp_wq, m));
-        if (s->pairwise) {
+        CHECK(dalloc(&s->los_idx, m));
+        if (s->pairwise) {   // keyed records, and the chunk plans of the deepest level
+            const uint64_t pmax = 1ull << (s->depth - 1), n_tri = pmax * (pmax + 1) / 2;
             CHECK(dalloc(&s->key_rec, m));
             CHECK(dalloc(&s->key_wq, m));
-            CHECK(dalloc(&s->pair_lv, m));
+            CHECK(dalloc(&s->pair_desc, n_tri + (m + kStatChunkMin - 1) / kStatChunkMin));
+            CHECK(dalloc(&s->pair_mk, n_tri));
         }
     }
+    if (!s->los_off) CHECK(dalloc(&s->los_off, n + 1));
     if (G != s->n_groups || !s->group_off) {
         dfree(s->group_off);
         CHECK(dalloc(&s->group_off, (size_t)G + 1));
@@ -1123,8 +1140,10 @@ int upload_pairs(cbh_session* s, const cbh_family* fam) {
         HIP_TRY(hipMemcpyAsync(s->comp_los, los.data(), sizeof(uint32_t) * m, hipMemcpyHostToDevice, st));
         HIP_TRY(hipMemcpyAsync(s->comp_w, w.data(), sizeof(double) * m, hipMemcpyHostToDevice, st));
         HIP_TRY(hipMemcpyAsync(s->comp_wq, wq.data(), sizeof(long long) * m, hipMemcpyHostToDevice, st));
+        HIP_TRY(hipMemcpyAsync(s->los_idx, lidx.data(), sizeof(uint32_t) * m, hipMemcpyHostToDevice, st));
     }
     HIP_TRY(hipMemcpyAsync(s->comp_off, off.data(), sizeof(uint32_t) * (n + 1), hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(s->los_off, loff.data(), sizeof(uint32_t) * (n + 1), hipMemcpyHostToDevice, st));
     HIP_TRY(hipMemcpyAsync(s->group_off, go, sizeof(uint32_t) * ((size_t)G + 1), hipMemcpyHostToDevice, st));
     HIP_TRY(hipMemcpyAsync(s->score_w, pw.data(), sizeof(double) * n, hipMemcpyHostToDevice, st));
     HIP_TRY(hipStreamSynchronize(st));
@@ -1137,24 +1156,19 @@ int upload_pairs(cbh_session* s, const cbh_family* fam) {
 int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     hipStream_t st = s->stream;
     const uint32_t P = 1u << level, B = s->B, F = s->F;
-    const size_t cells = (size_t)F * B * P * P * 2;
-    if (P <= 4) {   // few cells per feature: LDS-privatized chunks, global flush, bucket scan
-        CHECK(launch_zero(s->pair_st, cells, st));
-        if (s->n_pairs) {
-            pair_leaves_kernel<<<grid_for(s->n_pairs, 256, 2048), 256, 0, st>>>(s->comp_win, s->comp_los,
-                                                                               s->n_pairs, s->leaf, s->pair_lv);
-            HIP_TRY(hipGetLastError());
-            const uint32_t n_chunks = (uint32_t)((s->n_pairs + kPairChunk - 1) / kPairChunk);
-            const uint32_t grid = 8u * n_chunks * ((F + 7) / 8);
-            const size_t lds = (size_t)B * P * P * 2 * sizeof(long long);   // attribute set at open
-            pair_stats_kernel<<<grid, 256, lds, st>>>(s->cols, s->n, s->pair_lv, s->comp_win, s->comp_los,
-                                                     s->comp_wq, s->n_pairs, n_chunks, F, P, B, s->pair_st);
-            HIP_TRY(hipGetLastError());
-        }
-        const uint32_t runs = F * P * P * 2;
-        pair_scan_kernel<<<(runs + 3) / 4, 256, 0, st>>>(s->pair_st, runs, B);
-        HIP_TRY(hipGetLastError());
-    } else {        // pairs grouped by leaf pair; one workgroup per (feature, leaf pair)
+    // statistics: pairs grouped by leaf-pair key (a level of one leaf reads them in input
+    // order), one workgroup per (key, chunk, 16-feature tile); keys of one chunk write their
+    // cumulative runs, the chunks of larger keys add into zeroed runs that are scanned after
+    const bool direct = P == 1;
+    const uint32_t n_tri = P * (P + 1) / 2;
+    const uint32_t tiles = (F + kStatTileF - 1) / kStatTileF;
+    // chunk: the pairs times the tiles spread once over the CUs (one workgroup each: its cells
+    // take most of the LDS), in whole 1024-pair passes
+    const uint64_t spread = (s->n_pairs * tiles + s->pair_cus - 1) / s->pair_cus;
+    const uint32_t chunk = (uint32_t)std::max<uint64_t>(kStatChunkMin, (spread + 1023) / 1024 * 1024);
+    const uint32_t nchunk = (uint32_t)((s->n_pairs + chunk - 1) / chunk);
+    const uint32_t max_desc = n_tri + nchunk, max_multi = std::min(n_tri, nchunk);
+    if (!direct) {
         const uint32_t nk = P * P;
         zero_u32_kernel<<<grid_for(nk, 256), 256, 0, st>>>(s->key_cnt, nk);
         HIP_TRY(hipGetLastError());
@@ -1163,20 +1177,28 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
                 s->comp_win, s->comp_los, s->n_pairs, s->leaf, P, s->key_cnt);
             HIP_TRY(hipGetLastError());
         }
-        pair_key_scan_kernel<<<1, 1024, 0, st>>>(s->key_cnt, nk, s->key_off, s->key_cur);
+    }
+    pair_plan_kernel<<<1, 1024, 0, st>>>(s->key_cnt, P, direct ? 1 : 0, (uint32_t)s->n_pairs, chunk, s->key_off, s->key_cur,
+                                         s->pair_desc, s->pair_nd, s->pair_mk, s->pair_nd + 1);
+    HIP_TRY(hipGetLastError());
+    if (!direct && s->n_pairs) {
+        pair_key_scatter_kernel<<<(unsigned)((s->n_pairs + 256 * kScatterItems - 1) / (256 * kScatterItems)), 256,
+                                  P * P * sizeof(uint32_t), st>>>(s->comp_win, s->comp_los, s->comp_wq, s->n_pairs,
+                                                                  s->leaf, P, s->key_cur, s->key_rec, s->key_wq);
         HIP_TRY(hipGetLastError());
-        if (s->n_pairs) {
-            pair_key_scatter_kernel<<<(unsigned)((s->n_pairs + 256 * kScatterItems - 1) / (256 * kScatterItems)),
-                                      256, nk * sizeof(uint32_t), st>>>(
-                s->comp_win, s->comp_los, s->comp_wq, s->n_pairs, s->leaf, P, s->key_cur, s->key_rec,
-                s->key_wq);
-            HIP_TRY(hipGetLastError());
-        }
-        const uint32_t n_tri = P * (P + 1) / 2;   // leaf pairs {a <= b}
-        const uint32_t grid = 8u * s->pair_tiles * ((n_tri + 7) / 8);
-        const size_t lds = (size_t)s->pair_tf * 2 * B * 2 * sizeof(long long);
-        pair_stats_key_kernel<<<grid, 256, lds, st>>>(s->rows, s->Ws, s->key_rec, s->key_wq, s->key_off, F,
-                                                          P, B, s->pair_tf, s->pair_tiles, s->pair_st);
+    }
+    if (max_multi) {
+        pair_multi_zero_kernel<<<dim3(max_multi, F), 256, 0, st>>>(s->pair_mk, s->pair_nd + 1, P, B, s->pair_st);
+        HIP_TRY(hipGetLastError());
+    }
+    const bool buf = (uint64_t)s->n * s->Ws * 4 < (1ull << 32);
+    (buf ? pair_stats_feature_kernel<true> : pair_stats_feature_kernel<false>)
+        <<<dim3(max_desc, tiles), kStatThreads, (size_t)B * 64 * sizeof(long long), st>>>(
+            s->rows, s->Ws, s->pair_desc, s->pair_nd, s->key_rec, s->key_wq, s->comp_win, s->comp_los, s->comp_wq,
+            direct ? 1 : 0, F, P, B, s->pair_st);
+    HIP_TRY(hipGetLastError());
+    if (max_multi) {
+        pair_multi_scan_kernel<<<dim3(max_multi, F), 256, 0, st>>>(s->pair_mk, s->pair_nd + 1, P, B, s->pair_st);
         HIP_TRY(hipGetLastError());
     }
     {
@@ -1184,11 +1206,16 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
 #define CBH_PAIR_CAND(PV)                                                                                \
     pairwise_candidate_kernel<PV><<<grid, 64, kPairCandLds, st>>>(s->pair_st, cur, s->C, F, s->n_cand, B, s->scales, \
                                                                   s->pair_inv, s->l2, s->prior, s->cand_scores)
+        // up to 8 leaves: one border per lane, the system in the lane's registers
+        const dim3 lgrid((B - 1 + 63) / 64, F);
+#define CBH_PAIR_LANE(PV)                                                                             \
+    pairwise_candidate_lane_kernel<PV><<<lgrid, 64, 0, st>>>(s->pair_st, cur, s->C, F, s->n_cand, B, s->scales, \
+                                                             s->pair_inv, s->l2, s->prior, s->cand_scores)
         switch (P) {
-            case 1: CBH_PAIR_CAND(1); break;
-            case 2: CBH_PAIR_CAND(2); break;
-            case 4: CBH_PAIR_CAND(4); break;
-            case 8: CBH_PAIR_CAND(8); break;
+            case 1: CBH_PAIR_LANE(1); break;
+            case 2: CBH_PAIR_LANE(2); break;
+            case 4: CBH_PAIR_LANE(4); break;
+            case 8: CBH_PAIR_LANE(8); break;
             case 16: CBH_PAIR_CAND(16); break;
             case 32: CBH_PAIR_CAND(32); break;
             case 64:   // one workgroup per candidate, its system in LDS
@@ -1204,6 +1231,7 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
             default: return fail(CBH_ERR_UNSUPPORTED, "pairwise scoring: level of " + std::to_string(P) + " leaves");
         }
 #undef CBH_PAIR_CAND
+#undef CBH_PAIR_LANE
         HIP_TRY(hipGetLastError());
     }
     pairwise_best_kernel<<<F, 256, 0, st>>>(s->cand_scores, s->n_cand, B, s->best_score, s->best_bin);
@@ -1326,9 +1354,13 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
     // ---- prepare: apply previous tree, ders, sample, score channels, bounds ----
     CHECK(s->stage_begin(kStPrepare));
     if (s->ranking) {   // pair ders need every row's updated approximant: apply, then ders
-        pairlogit_ders_kernel<<<grid_for(s->n_groups, 256), 256, 0, st>>>(
-            s->group_off, s->n_groups, s->comp_off, s->comp_los, s->comp_w, s->approx, s->leaf,
-            apply_prev ? s->leaf_scaled : nullptr, s->ext_der, s->ext_der + n);
+        if (apply_prev) {
+            apply_leaves_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->approx, s->leaf, s->leaf_scaled, n);
+            HIP_TRY(hipGetLastError());
+        }
+        pairlogit_row_ders_kernel<<<grid_for(n, 256), 256, 0, st>>>(n, s->comp_off, s->comp_win, s->comp_los,
+                                                                  s->comp_w, s->los_off, s->los_idx, s->approx,
+                                                                  s->ext_der, s->ext_der + n);
         HIP_TRY(hipGetLastError());
     }
     const unsigned pgrid = grid_for(n, 256, kPrepBlocks);
