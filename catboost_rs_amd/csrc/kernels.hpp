@@ -649,16 +649,17 @@ __device__ __forceinline__ void packed_flush_channel(unsigned long long* __restr
     }
 }
 
-// The four byte visits of one row's word: rotated once so step k reads byte k, cell column
-// byte k of offs (the rotation spreads the lanes of an instruction over distinct bank pairs).
-__device__ __forceinline__ void packed_row_atomics(unsigned long long* __restrict__ pk, uint32_t word, uint32_t rot,
+// The four byte visits of one row's word.  Step k reads the byte at bit sk[k] of the word
+// (v_bfe with a per-lane shift) and adds to the cell column at byte offset off8[k]; the lane's
+// visit order (rotated by lane) spreads the lanes of an instruction over distinct bank pairs.
+__device__ __forceinline__ void packed_row_atomics(unsigned long long* __restrict__ pk, uint32_t word,
+                                                   const uint32_t* sk /* bit shifts of the 4 steps */,
                                                    const uint32_t* off8 /* byte offsets of the 4 columns */,
                                                    unsigned long long st) {
-    const uint32_t wr = __builtin_amdgcn_alignbyte(word, word, rot);
     char* base = (char*)pk;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t bin = __builtin_amdgcn_ubfe(wr, 8 * k, 8);
+        const uint32_t bin = __builtin_amdgcn_ubfe(word, sk[k], 8);
         atomicAdd((unsigned long long*)(base + ((bin << 9) + off8[k])), st);   // [bin][64] x 8 bytes
     }
 }
@@ -675,6 +676,12 @@ __device__ __forceinline__ uint32_t ldw(__amdgpu_buffer_rsrc_t r, uint32_t off) 
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
 constexpr uint32_t kPastEnd = 0xFFFFFFF0u;   // a byte offset past every packed-fill buffer
+
+// A buffer load at a per-lane offset plus a workgroup-uniform one (soffset); callers keep the
+// sum inside the resource.
+__device__ __forceinline__ uint32_t ldw_s(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, (int)soff, 0);
+}
 
 __device__ __forceinline__ unsigned long long ldq(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
@@ -706,82 +713,105 @@ __device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + U, 0xF, 0xF, true);
 }
 template <int U>
-__device__ __forceinline__ unsigned long long row_bcast64(unsigned long long v) {
-    return (unsigned long long)row_bcast<U>((uint32_t)v) | ((unsigned long long)row_bcast<U>((uint32_t)(v >> 32)) << 32);
+__device__ __forceinline__ unsigned long long row_bcast64(unsigned long long v) {   // one v_mov_b64_dpp
+    return __builtin_amdgcn_update_dpp(0ull, v, 0x150 + U, 0xF, 0xF, true);
 }
 
 // The rows [pos, end) of a tile (up to 16 words: the 16 lanes of a row are one 16-lane DPP row
-// of the wave, 4 rows per wave, passes of 64 rows), in blocks of kPackIterRows = 16 passes, each
-// block in two halves of 8 passes.  Lane w of a DPP row loads the packed statistic (and,
-// gathered, the row index) of that row's pass w; pass u broadcasts lane u to the row's 16 lanes
-// (row_newbcast), so statistics and indices cost one load per row and no LDS round trip -- the
-// atomics of consecutive rows issue back to back.  Software pipeline: block j+1's statistics and
-// indices are loaded when block j starts, and the words of a half of block j+1 right after that
-// half of block j is consumed, so they are in flight across the other half, the barrier and the
-// swap.  Rows past the range carry a zero statistic (their atomics add nothing).
+// of the wave), in blocks of kPackIterRows rows: DPP row r of the workgroup takes the 16
+// consecutive positions q = base + 16 r .. q + 15 of a block, in two halves of 8.  Lane w of a
+// DPP row loads the packed statistic (and, gathered, the row index) of position q + w; row u of
+// the half broadcasts lane u to the DPP row's 16 lanes (row_newbcast), so statistics and indices
+// cost one load per row and no LDS round trip -- the atomics of consecutive rows issue back to
+// back.  At the dense level the 16 rows of a DPP row are consecutive in memory, so their word
+// loads share one per-lane offset and differ by a uniform one: no per-row address arithmetic.
+// Software pipeline: block j+1's statistics and indices are loaded when block j starts (indices
+// two blocks ahead), and the words of a half of block j+1 right after that half of block j is
+// consumed, so they are in flight across the other half, the barrier and the swap.  Positions
+// past the range carry a zero statistic (their atomics add nothing).
 template <bool kGather>
 __device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk,
                                              __amdgpu_buffer_rsrc_t rbase, uint32_t sh, uint32_t wl4,
-                                                  uint32_t wl, __amdgpu_buffer_rsrc_t idx,
-                                                  __amdgpu_buffer_rsrc_t sbase, uint32_t pos,
-                                                  uint32_t end, uint32_t r0, uint32_t rot, const uint32_t* off8,
-                                                  uint32_t swap_every,
-                                                  long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
-    constexpr uint32_t rpp = kPackThreads / kPackTileWords;   // 64 rows per pass
-    static_assert(2 * kPackHalf * rpp == kPackIterRows && kPackHalf == 8, "block layout");
-    uint32_t six, six_n = 0, six_nn = 0;
+                                             uint32_t wl, __amdgpu_buffer_rsrc_t idx,
+                                             __amdgpu_buffer_rsrc_t sbase, uint32_t pos, uint32_t end,
+                                             uint32_t n, uint32_t r0, const uint32_t* sk, const uint32_t* off8,
+                                             uint32_t swap_every,
+                                             long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
+    static_assert(2 * kPackHalf * 64 == kPackIterRows && kPackHalf == 8, "block layout");
+    uint32_t six = 0, six_n = 0, six_nn = 0;
     unsigned long long ssv, ssv_n = 0;
-    // this lane: pass wl of block bb.  The row index (a load when gathered) is staged two blocks
+    // the first position of this DPP row's 16 in the block at bb; at the dense level the rows
+    // read are clamped to [0, n) as a group (q - qc positions before q are re-read with a zero
+    // statistic), so every word load stays inside the tile's rows
+    auto dense_q = [&](uint32_t bb) -> uint32_t {
+        const uint32_t q = bb + 16u * r0;
+        return q + 16u <= n ? q : n - 16u;
+    };
+    // this lane's position in the block at bb: gathered, its row index is staged two blocks
     // ahead, so the word loads that depend on it never wait for it; the statistic (stored in
-    // position order) one block ahead.  A row past the range reads its statistic from past the
-    // end of the buffer, which returns 0 (buffer range checking), so no select waits on the load
+    // position order) one block ahead.  A position outside the range reads its statistic from
+    // past the end of the buffer, which returns 0 (buffer range checking), so no select waits on
+    // the load
     auto stage_ix = [&](uint32_t bb) -> uint32_t {
-        const uint32_t p = bb + r0 + wl * rpp;
-        const uint32_t pc = p < end ? p : bb;
-        return kGather ? ldw(idx, 4u * pc) : pc;
+        const uint32_t p = bb + 16u * r0 + wl;
+        return ldw(idx, 4u * (p < end ? p : bb));
     };
     auto stage_sv = [&](uint32_t bb) -> unsigned long long {
-        const uint32_t p = bb + r0 + wl * rpp;
-        return ldq(sbase, p < end ? 8u * p : kPastEnd);
+        if (kGather) {
+            const uint32_t p = bb + 16u * r0 + wl;
+            return ldq(sbase, p < end ? 8u * p : kPastEnd);
+        }
+        const uint32_t q = bb + 16u * r0, p = dense_q(bb) + wl;
+        return ldq(sbase, (p >= q && p < end) ? 8u * p : kPastEnd);
     };
-    // row index of pass U (this lane's DPP row) from the staged indices of a block
-#define CBH_DOC(U, SIX) (kGather ? row_bcast<U>(SIX) : row_bcast<U>(SIX))
     uint32_t wA[kPackHalf], wB[kPackHalf];
     uint32_t base = pos;
-    six = stage_ix(base);
+    if (kGather) {
+        six = stage_ix(base);
+        if (base + kPackIterRows < end) six_n = stage_ix(base + kPackIterRows);
+    }
     ssv = stage_sv(base);
-    if (base + kPackIterRows < end) six_n = stage_ix(base + kPackIterRows);
-#define CBH_LOADA(SIX)                                                                       \
-    wA[0] = ldw(rbase, (CBH_DOC(0, SIX) << sh) + wl4); wA[1] = ldw(rbase, (CBH_DOC(1, SIX) << sh) + wl4); \
-    wA[2] = ldw(rbase, (CBH_DOC(2, SIX) << sh) + wl4); wA[3] = ldw(rbase, (CBH_DOC(3, SIX) << sh) + wl4); \
-    wA[4] = ldw(rbase, (CBH_DOC(4, SIX) << sh) + wl4); wA[5] = ldw(rbase, (CBH_DOC(5, SIX) << sh) + wl4); \
-    wA[6] = ldw(rbase, (CBH_DOC(6, SIX) << sh) + wl4); wA[7] = ldw(rbase, (CBH_DOC(7, SIX) << sh) + wl4);
-#define CBH_LOADB(SIX)                                                                       \
-    wB[0] = ldw(rbase, (CBH_DOC(8, SIX) << sh) + wl4); wB[1] = ldw(rbase, (CBH_DOC(9, SIX) << sh) + wl4); \
-    wB[2] = ldw(rbase, (CBH_DOC(10, SIX) << sh) + wl4); wB[3] = ldw(rbase, (CBH_DOC(11, SIX) << sh) + wl4); \
-    wB[4] = ldw(rbase, (CBH_DOC(12, SIX) << sh) + wl4); wB[5] = ldw(rbase, (CBH_DOC(13, SIX) << sh) + wl4); \
-    wB[6] = ldw(rbase, (CBH_DOC(14, SIX) << sh) + wl4); wB[7] = ldw(rbase, (CBH_DOC(15, SIX) << sh) + wl4);
+#define CBH_GLOAD(W, I, U, SIX) W[I] = ldw(rbase, (row_bcast<U>(SIX) << sh) + wl4);
+#define CBH_DLOAD(W, I, U, OFF) W[I] = ldw_s(rbase, OFF, (uint32_t)(U) << sh);
+#define CBH_LOADA(SIX, BB)                                                                    \
+    if (kGather) {                                                                            \
+        CBH_GLOAD(wA, 0, 0, SIX) CBH_GLOAD(wA, 1, 1, SIX) CBH_GLOAD(wA, 2, 2, SIX) CBH_GLOAD(wA, 3, 3, SIX) \
+        CBH_GLOAD(wA, 4, 4, SIX) CBH_GLOAD(wA, 5, 5, SIX) CBH_GLOAD(wA, 6, 6, SIX) CBH_GLOAD(wA, 7, 7, SIX) \
+    } else {                                                                                  \
+        const uint32_t o = (dense_q(BB) << sh) + wl4;                                         \
+        CBH_DLOAD(wA, 0, 0, o) CBH_DLOAD(wA, 1, 1, o) CBH_DLOAD(wA, 2, 2, o) CBH_DLOAD(wA, 3, 3, o) \
+        CBH_DLOAD(wA, 4, 4, o) CBH_DLOAD(wA, 5, 5, o) CBH_DLOAD(wA, 6, 6, o) CBH_DLOAD(wA, 7, 7, o) \
+    }
+#define CBH_LOADB(SIX, BB)                                                                    \
+    if (kGather) {                                                                            \
+        CBH_GLOAD(wB, 0, 8, SIX) CBH_GLOAD(wB, 1, 9, SIX) CBH_GLOAD(wB, 2, 10, SIX) CBH_GLOAD(wB, 3, 11, SIX) \
+        CBH_GLOAD(wB, 4, 12, SIX) CBH_GLOAD(wB, 5, 13, SIX) CBH_GLOAD(wB, 6, 14, SIX) CBH_GLOAD(wB, 7, 15, SIX) \
+    } else {                                                                                  \
+        const uint32_t o = (dense_q(BB) << sh) + wl4;                                         \
+        CBH_DLOAD(wB, 0, 8, o) CBH_DLOAD(wB, 1, 9, o) CBH_DLOAD(wB, 2, 10, o) CBH_DLOAD(wB, 3, 11, o) \
+        CBH_DLOAD(wB, 4, 12, o) CBH_DLOAD(wB, 5, 13, o) CBH_DLOAD(wB, 6, 14, o) CBH_DLOAD(wB, 7, 15, o) \
+    }
 #define CBH_ATOMS(W, U0, SSV)                                                                \
-    packed_row_atomics(pk, W[0], rot, off8, row_bcast64<U0 + 0>(SSV));                       \
-    packed_row_atomics(pk, W[1], rot, off8, row_bcast64<U0 + 1>(SSV));                       \
-    packed_row_atomics(pk, W[2], rot, off8, row_bcast64<U0 + 2>(SSV));                       \
-    packed_row_atomics(pk, W[3], rot, off8, row_bcast64<U0 + 3>(SSV));                       \
-    packed_row_atomics(pk, W[4], rot, off8, row_bcast64<U0 + 4>(SSV));                       \
-    packed_row_atomics(pk, W[5], rot, off8, row_bcast64<U0 + 5>(SSV));                       \
-    packed_row_atomics(pk, W[6], rot, off8, row_bcast64<U0 + 6>(SSV));                       \
-    packed_row_atomics(pk, W[7], rot, off8, row_bcast64<U0 + 7>(SSV));
-    CBH_LOADA(six)
-    CBH_LOADB(six)
+    packed_row_atomics(pk, W[0], sk, off8, row_bcast64<U0 + 0>(SSV));                         \
+    packed_row_atomics(pk, W[1], sk, off8, row_bcast64<U0 + 1>(SSV));                         \
+    packed_row_atomics(pk, W[2], sk, off8, row_bcast64<U0 + 2>(SSV));                         \
+    packed_row_atomics(pk, W[3], sk, off8, row_bcast64<U0 + 3>(SSV));                         \
+    packed_row_atomics(pk, W[4], sk, off8, row_bcast64<U0 + 4>(SSV));                         \
+    packed_row_atomics(pk, W[5], sk, off8, row_bcast64<U0 + 5>(SSV));                         \
+    packed_row_atomics(pk, W[6], sk, off8, row_bcast64<U0 + 6>(SSV));                         \
+    packed_row_atomics(pk, W[7], sk, off8, row_bcast64<U0 + 7>(SSV));
+    CBH_LOADA(six, base)
+    CBH_LOADB(six, base)
     uint32_t blk = 0;
     for (;;) {   // workgroup-uniform
         const uint32_t nb = base + kPackIterRows;
         const bool more = nb < end;
-        if (nb + kPackIterRows < end) six_nn = stage_ix(nb + kPackIterRows);
+        if (kGather && nb + kPackIterRows < end) six_nn = stage_ix(nb + kPackIterRows);
         if (more) ssv_n = stage_sv(nb);
         CBH_ATOMS(wA, 0, ssv)
-        if (more) { CBH_LOADA(six_n) }
+        if (more) { CBH_LOADA(six_n, nb) }
         CBH_ATOMS(wB, 8, ssv)
-        if (more) { CBH_LOADB(six_n) }
+        if (more) { CBH_LOADB(six_n, nb) }
         six_n = six_nn;
         ssv = ssv_n;
         if (++blk >= swap_every || !more) {
@@ -795,7 +825,8 @@ __device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk
 #undef CBH_ATOMS
 #undef CBH_LOADB
 #undef CBH_LOADA
-#undef CBH_DOC
+#undef CBH_DLOAD
+#undef CBH_GLOAD
 }
 
 template <bool kGather>
@@ -804,52 +835,51 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     uint64_t n, const uint32_t* __restrict__ idx /* kGather: rows listed by the partition */,
     const LevelPlan* __restrict__ plan, const unsigned long long* __restrict__ spack /* [n] */,
     const unsigned long long* __restrict__ sseq /* nullable [V]: packed stats in idx order */,
-    uint32_t n_full, uint32_t F, uint32_t B, uint32_t G, uint32_t Gn, long long* __restrict__ hist,
-    uint32_t swap_every /* blocks of rows between two swaps: 2 * swap_every * kPackIterRows * 2^pack_bits <= 2^30 */) {
+    uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
+    uint32_t swap_every /* blocks of rows between two swaps: 2 * swap_every * kPackIterRows * 2^pack_bits <= 2^30 */,
+    const uint32_t* __restrict__ rows_rm /* nullable, kGather: row-major words, 2^rm_sh bytes per row */,
+    uint32_t rm_sh) {
     constexpr uint32_t C = 2;
     extern __shared__ unsigned long long pk[];   // [B][64] packed cells
-    // blocks: the n_full full 64-feature tiles first, G row ranges each.  Workgroups go to the
-    // 8 XCDs round robin (block b to XCD b % 8), so the (range, tile) pairs are numbered
-    // range-major and XCD x takes the x-th run of per = ceil(n_full G / 8) of them: the tiles
-    // of one range sit on one XCD and share its rows' lines in that L2, and no XCD holds more
-    // pairs than its CUs when n_full G fits the resident slots (pairs past the last exit).
-    // Then, when Gn > 0, the narrow last tile (tile n_full, W not a multiple of 16 words) in
-    // Gn ranges, sized by the host from the relative cost of its rows.
-    const uint32_t pairs = n_full * G;
+    // blocks: n_tiles 64-feature tiles (the last one narrower when W is not a multiple of 16
+    // words; its row costs about as much as a full one's), G row ranges each.  Workgroups go to
+    // the 8 XCDs round robin (block b to XCD b % 8), so the (range, tile) pairs are numbered
+    // range-major and XCD x takes the x-th run of per = ceil(n_tiles G / 8) of them: every tile
+    // of one range sits on one XCD, so at the gathered levels the row-major lines of a listed
+    // row come from HBM once and from that L2 for the other tiles, and no XCD holds more pairs
+    // than its CUs when n_tiles G fits the resident slots (pairs past the last exit).
+    const uint32_t pairs = n_tiles * G;
     const uint32_t per = (pairs + 7u) / 8u;
-    const uint32_t full_blocks = 8u * per;
     const uint32_t b = blockIdx.x;
-    uint32_t t, g, GR;
-    if (b < full_blocks) {
-        const uint32_t i = (b & 7u) * per + (b >> 3);
-        if (i >= pairs) return;   // workgroup-uniform, before any barrier
-        t = i % n_full;
-        g = i / n_full;
-        GR = G;
-    } else {
-        t = n_full;
-        g = b - full_blocks;
-        GR = Gn;
-    }
+    const uint32_t i = (b & 7u) * per + (b >> 3);
+    if (i >= pairs) return;   // workgroup-uniform, before any barrier
+    const uint32_t t = i % n_tiles;
+    const uint32_t g = i / n_tiles;
+    const uint32_t GR = G;
     const uint32_t w0 = t * kPackTileWords;
     const uint32_t TW = min(kPackTileWords, W - w0);
     const uint32_t f0 = 4u * w0;
     const uint32_t TF = min(4u * TW, F - f0);
-    const uint32_t sh = packed_slice_shift(TW);   // a row of this tile's slice: 2^sh bytes
+    // a row of this tile's tile-major slice: 2^sh bytes; gathered from row-major words: 2^rm_sh
+    const bool rm = kGather && rows_rm != nullptr;
+    const uint32_t sh = rm ? rm_sh : packed_slice_shift(TW);
     for (uint32_t i = threadIdx.x; i < kPackCells; i += kPackThreads) pk[i] = 0ull;
     // lanes: a 16-lane DPP row per row; a narrow tile's lanes past its words read the zero
     // padding of the slice (or the next row's words) and add to LDS columns >= TF, never read
     constexpr uint32_t rpp = kPackThreads / kPackTileWords;
     const uint32_t r0 = threadIdx.x / kPackTileWords;
     const uint32_t wl = threadIdx.x % kPackTileWords;
-    // the word is rotated right by rot bytes once per row, so step k reads byte k of the rotated
-    // word: feature 4 * wl + ((k + rot) & 3).  rot = (wl / 4 + r) mod 4 makes the 16 lanes of a
-    // row hit 16 distinct features mod 16 and any two rows 32 distinct features mod 32, i.e.
-    // distinct bank pairs of the [bin][64] cells whatever the bins.
+    // step k of a row visits byte (k + rot) & 3 of the lane's word: feature 4 * wl + ((k + rot) & 3).
+    // rot = (wl / 4 + r) mod 4 makes the 16 lanes of a DPP row hit 16 distinct features mod 16
+    // and any two DPP rows 32 distinct features mod 32, i.e. distinct bank pairs of the
+    // [bin][64] cells whatever the bins.
     const uint32_t rot = ((wl >> 2) + (r0 & 1u)) & 3u;
-    uint32_t off8[4];   // byte offset of the column of step k
+    uint32_t sk[4], off8[4];   // bit shift in the word and byte offset of the column of step k
 #pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) off8[k] = 8u * (4u * wl + ((k + rot) & 3u));
+    for (uint32_t k = 0; k < 4; ++k) {
+        sk[k] = 8u * ((k + rot) & 3u);
+        off8[k] = 8u * (4u * wl + ((k + rot) & 3u));
+    }
     long long acc_d[kPackOwn], acc_w[kPackOwn];
 #pragma unroll
     for (int k = 0; k < kPackOwn; ++k) acc_d[k] = acc_w[k] = 0;
@@ -861,8 +891,11 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     uint32_t seg = 0;
     if (kGather)
         while (seg + 1 < n_seg && plan->seg_begin[seg + 1] <= rb) ++seg;
-    // tile-major rows: this tile's slice starts at word n * w0, 2^sh bytes per row
-    const __amdgpu_buffer_rsrc_t rbase = make_rsrc(rows + n * w0, (uint64_t)n << sh);
+    // tile-major rows: this tile's slice starts at word n * w0, 2^sh bytes per row; row-major:
+    // word w0 of row 0, rows 2^sh bytes apart (a narrow tile's lanes past W read the row's zero
+    // padding: rows are padded to whole 16-word multiples)
+    const __amdgpu_buffer_rsrc_t rbase =
+        rm ? make_rsrc(rows_rm + w0, ((uint64_t)n << sh) - 4ull * w0) : make_rsrc(rows + n * w0, (uint64_t)n << sh);
     const uint32_t wl4 = 4u * wl;
     const __amdgpu_buffer_rsrc_t sbase = make_rsrc(kGather ? sseq : spack, n * 8u);
     const __amdgpu_buffer_rsrc_t ibase = make_rsrc(kGather ? (const void*)idx : (const void*)spack, kGather ? n * 4u : 0u);
@@ -872,8 +905,8 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = kGather ? plan->built[seg] : 0u;
         if (end > pos) {
-            packed_range<kGather>(pk, rbase, sh, wl4, wl, ibase, sbase, pos, end, r0, rot, off8, swap_every,
-                                  acc_d, acc_w);
+            packed_range<kGather>(pk, rbase, sh, wl4, wl, ibase, sbase, pos, end, (uint32_t)n, r0, sk, off8,
+                                  swap_every, acc_d, acc_w);
             // every contribution of the segment is in the registers now (the last swap follows
             // the last barrier); flush both channels, then clear the cells and registers
             long long* hd = hist + (size_t)slot * C * F * B;

@@ -295,7 +295,7 @@ static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel
     if (blockIdx.x >= *n_desc) return;
     const uint4 ds = desc[blockIdx.x];
     const uint32_t key = ds.x, a = key / P, b = key % P;
-    const uint32_t t = threadIdx.x, fl = t & 15, slot = t >> 4;
+    const uint32_t t = threadIdx.x, fl = t & 15;
     const uint32_t f = blockIdx.y * kStatTileF + fl;
     const bool fok = f < F;
     const uint32_t word = (fok ? f : F - 1) >> 2, sh = (f & 3u) * 8u;

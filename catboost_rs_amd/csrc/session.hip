@@ -195,8 +195,8 @@ struct cbh_session {
     unsigned long long* sseq = nullptr;    // the same for the idx rows, in idx order
     uint32_t* trows = nullptr;             // packed fill: tile-major row words (pack_tiles_kernel)
     uint32_t pk_tiles = 0, pk_ranges = 8, pk_swap = 1;
-    uint32_t pk_ranges_n = 0, pk_blocks = 0;   // packed fill: ranges of a narrow last tile, blocks
-    uint32_t pk_full = 0;                      // full 64-feature tiles
+    uint32_t pk_blocks = 0;                    // packed fill: workgroups per launch
+    uint32_t pk_rm_sh = 0;                     // packed fill: log2 bytes of a row-major row (0: tile-major gathers)
     bool pk_signed_w = false;              // some object or pair weight is negative
     size_t pk_lds = 0;
     JumpTabs jt() const {
@@ -498,42 +498,30 @@ uint32_t pick_ranges(uint32_t cus, uint32_t per_cu, uint32_t nt, uint64_t n) {
     return G;
 }
 
-// Row ranges of the packed fill: G per full 64-feature tile and Gn for a narrow last tile
-// (TW < 16 words), in the ratio of their cost per row, so one round of workgroups fills the
-// resident slots with about equal work each.  A narrow tile runs the full tiles' loop (its
-// lanes past TW add to columns that are never read), so a row costs as much as a full one:
-// Gn = G.  (Measured alternatives, config 2's 2-word last tile: 0.4 x as many ranges, 2.1x
-// slower fill; a launch of its own with 8 rows per DPP row and per-copy LDS columns, 5%
-// slower -- its loop stays latency-bound.)  CBH_PACK_NARROW_COST sets the ratio (a
-// measurement knob).
+// Row ranges of the packed fill: G per 64-feature tile, the narrow last tile (TW < 16 words)
+// included, so one round of workgroups fills the resident slots.  A narrow tile runs the full
+// tiles' loop (its lanes past TW add to columns that are never read), so its row costs about
+// as much as a full one's and equal ranges balance the work.  (Measured alternatives, config
+// 2's 2-word last tile: 0.4 x as many ranges, 2.1x slower fill; a launch of its own with 8
+// rows per DPP row and per-copy LDS columns, 5% slower -- its loop stays latency-bound.)
+// The gathered levels read row-major words (2^rm_sh bytes per row) when the padded row is a
+// power of two under 4 GiB in all: the tiles of a range run on one XCD, so a listed row's
+// lines come from HBM once for all its tiles.  CBH_PACK_GATHER=tiles keeps the tile-major
+// slices there (a measurement knob).
 void pick_packed_ranges(cbh_session* s, uint32_t cus, uint32_t per_cu) {
     const uint32_t cap = cus * std::max<uint32_t>(per_cu, 1);
-    const uint32_t tw_last = s->W % kPackTileWords;
-    const uint32_t n_full = s->W / kPackTileWords;
-    double r = tw_last ? 1.0 : 0.0;
-    if (const char* e = std::getenv("CBH_PACK_NARROW_COST")) {
-        const double v = std::strtod(e, nullptr);
-        if (v > 0.0 && v <= 1.0 && tw_last) r = v;
-    }
-    uint32_t G = 0, Gn = 0;
-    if (n_full == 0) {   // one narrow tile: every slot
-        Gn = cap;
-    } else {
-        G = std::max<uint32_t>(1, (uint32_t)std::floor((double)cap / ((double)n_full + r)));
-        Gn = tw_last ? std::max<uint32_t>(1, (uint32_t)std::lround(G * r)) : 0;
-        while (G > 1 && n_full * G + Gn > cap) {
-            --G;
-            Gn = tw_last ? std::max<uint32_t>(1, (uint32_t)std::lround(G * r)) : 0;
-        }
-    }
+    const uint32_t nt = s->pk_tiles;
+    uint32_t G = std::max<uint32_t>(1, cap / nt);
     // short inputs: at least 4096 rows per range, so the per-workgroup flush stays small
     const uint64_t min_rows = 4096;
     while (G > 1 && s->n / G < min_rows) G = G / 2;
-    while (Gn > 1 && s->n / Gn < min_rows) Gn = Gn / 2;
-    s->pk_full = n_full;
     s->pk_ranges = G;
-    s->pk_ranges_n = Gn;
-    s->pk_blocks = 8 * ((n_full * G + 7) / 8) + Gn;
+    s->pk_blocks = 8 * ((nt * G + 7) / 8);
+    const uint64_t rb = 4ull * s->Ws;
+    s->pk_rm_sh = 0;
+    const char* e = std::getenv("CBH_PACK_GATHER");
+    if ((rb & (rb - 1)) == 0 && s->n * rb < (1ull << 32) && !(e && std::string(e) == "tiles"))
+        while ((1ull << s->pk_rm_sh) < rb) ++s->pk_rm_sh;
 }
 
 // Feature tiles of the fill: the widest LDS slot stride whose histogram fits the budget.
@@ -583,7 +571,8 @@ int plan_fill_mode(cbh_session* s) {
     const bool want_split = v == "split";
     if (!want_packed && !want_split) return CBH_OK;
     // the packed fill addresses its buffers (a tile's row words, statistics) by 32-bit byte offsets
-    if (want_packed && (uint64_t)s->n * kPackTileWords * 4u >= (1ull << 32)) return CBH_OK;
+    // and reads the dense level's rows in groups of 16 clamped to [0, n)
+    if (want_packed && ((uint64_t)s->n * kPackTileWords * 4u >= (1ull << 32) || s->n < 1024)) return CBH_OK;
     int lds_max = 0, cus = 0, per_cu = 0;
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device));
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
@@ -1411,12 +1400,12 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         CHECK(s->stage_begin(kStFill));   // the fill kernel alone
         if (s->packed && level == 0)
             fill_packed_kernel<false><<<s->pk_blocks, kPackThreads, s->pk_lds, st>>>(
-                s->trows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_full, s->F, s->B,
-                s->pk_ranges, s->pk_ranges_n, cur, s->pk_swap);
+                s->trows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_tiles, s->F, s->B,
+                s->pk_ranges, cur, s->pk_swap, nullptr, 0u);
         else if (s->packed)
             fill_packed_kernel<true><<<s->pk_blocks, kPackThreads, s->pk_lds, st>>>(
-                s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_full, s->F, s->B,
-                s->pk_ranges, s->pk_ranges_n, cur, s->pk_swap);
+                s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_tiles, s->F, s->B,
+                s->pk_ranges, cur, s->pk_swap, s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh);
         else if (s->split && level == 0)
             fill_split_kernel<false><<<s->pk_ranges * s->pk_tiles * C, 1024, s->pk_lds, st>>>(
                 s->rows, s->Ws, s->W, n, nullptr, nullptr, (const long long*)s->spack, nullptr, C, s->pk_tiles,
