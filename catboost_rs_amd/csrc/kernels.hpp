@@ -591,17 +591,19 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
 
 // ---------------------------------------------------------------------------------
 // Packed fill (two score channels, K == 1).  A row's two fixed-point channels travel in one
-// 64-bit word, p = q_der * 2^32 + q_w (mod 2^64) with |q| <= 2^pack_bits, so ONE 64-bit LDS
-// atomic per (row, feature) adds both channels.  The 32-bit fields of an LDS cell stay
-// exactly decodable while the contributions that landed since the cell was last emptied sum
-// to less than 2^31 in magnitude.  Every thread owns kPackOwn cells of the tile and swaps
-// them with zero (ds_wrxchg) after the barrier that ends every block of at most
-// kPackIterRows rows; atomics of threads already in the next block may land before the swap,
-// so at most 2 * kPackIterRows rows fall between two swaps of a cell, and pack_bits =
-// 30 - log2(2 * kPackIterRows) keeps every field below 2^30.  The swapped words are decoded
-// into int64 registers, which flush to the level histogram at segment ends.  Every sum stays
-// an exact integer (order-free, reproducible); only the per-row quantization step is coarser
-// than the two-atomic fill's (2^-pack_bits of the largest row instead of 2^-61 of the sum).
+// 64-bit word, p = q_der * 2^32 + q_w (mod 2^64) with |q| <= 2^pack_bits - 1 (rounded on a scale
+// set by the largest row, then clamped), so ONE 64-bit LDS atomic per (row, feature) adds both
+// channels.  The 32-bit fields of an LDS cell stay exactly decodable while the contributions
+// that landed since the cell was last emptied sum to less than 2^31 in magnitude (q_w >= 0, so
+// the weight field never borrows).  Every thread owns kPackOwn cells of the tile and swaps them
+// with zero (ds_wrxchg) after the barrier that ends every swap period of swap_every blocks of
+// kPackIterRows rows; atomics of threads already in the next period may land before the swap,
+// so at most R = 2 * swap_every * kPackIterRows rows fall between two swaps of a cell, and
+// pack_bits = 31 - log2(R) keeps every field sum within R * (2^pack_bits - 1) < 2^31.  The
+// swapped words are decoded into int64 registers, which flush to the level histogram at
+// segment ends.  Every sum stays an exact integer (order-free, reproducible); only the per-row
+// quantization step is coarser than the two-atomic fill's (2^-pack_bits of the largest row
+// instead of 2^-61 of the sum).
 //
 // Tiles are 64 features (16 words): a workgroup reads one aligned 64-byte sector of every
 // 256-byte padded row it visits, so no two tiles share a sector and the gathers of the deeper
@@ -618,7 +620,9 @@ constexpr uint32_t kPackIterRows = 1024;    // rows of the workgroup per block (
 constexpr int kPackOwn = 16;                // cells per thread: 64 x 256 / 1024
 constexpr uint32_t kPackCells = kPackStride * 256;   // LDS cells of a packed tile (any B <= 256)
 static_assert(kPackOwn * kPackThreads == kPackCells, "every thread owns kPackOwn cells");
-constexpr int kPackBitsDefault = 19;        // 2 * 1024 * 2^19 = 2^30 < 2^31
+// pack_bits for swap_every = 1 (2 * 1024 rows between swaps): 2^11 * (2^20 - 1) < 2^31; each
+// doubling of swap_every takes one bit
+constexpr int kPackBitsSwap1 = 20;
 constexpr int kPackHalf = 8;                // passes per half block of a full tile (64 rows each)
 
 // Decode a swapped cell: no weight is negative (the session checks), so the weight field is a
@@ -633,7 +637,8 @@ __device__ __forceinline__ void unpack_add_nonneg(unsigned long long v, long lon
 // the global histogram) with integer global atomics.
 __device__ __forceinline__ void packed_flush_channel(unsigned long long* __restrict__ pk, const long long* acc,
                                                     uint32_t TF, uint32_t B, uint32_t F, uint32_t f0,
-                                                    long long* __restrict__ dst_plane /* hist + ((slot*C+ch)*F)*B */) {
+                                                    long long* __restrict__ dst_plane /* hist + ((slot*C+ch)*F)*B */,
+                                                    uint32_t copies = 1, uint32_t cstride = 0 /* narrow tile */) {
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kPackOwn; ++k) pk[threadIdx.x + (uint32_t)k * kPackThreads] = (unsigned long long)acc[k];
@@ -644,22 +649,23 @@ __device__ __forceinline__ void packed_flush_channel(unsigned long long* __restr
         const uint32_t l = i & 63u, j = i >> 6;
         const uint32_t f = (j / nbb) * 8 + (l >> 3), bin = (j % nbb) * 8 + (l & 7u);
         if (f >= TF || bin >= B) continue;
-        const unsigned long long v = pk[bin * kPackStride + f];
+        unsigned long long v = 0;
+        for (uint32_t c = 0; c < copies; ++c) v += pk[bin * kPackStride + c * cstride + f];
         if (v != 0) atomicAdd((unsigned long long*)dst_plane + ((size_t)(f0 + f) * B + bin), v);
     }
 }
 
-// The four byte visits of one row's word.  Step k reads the byte at bit sk[k] of the word
-// (v_bfe with a per-lane shift) and adds to the cell column at byte offset off8[k]; the lane's
-// visit order (rotated by lane) spreads the lanes of an instruction over distinct bank pairs.
+// The four byte visits of one row's word.  Step k adds to the cell column at byte offset
+// off8[k] = 8 (4 wl + b) the byte b of the word, b = (k + rot) & 3: v_bfe reads the low 5 bits
+// of its offset operand, which are 8 b, so off8 doubles as the bit shift.  The lane's visit
+// order (rotated by lane) spreads the lanes of an instruction over distinct bank pairs.
 __device__ __forceinline__ void packed_row_atomics(unsigned long long* __restrict__ pk, uint32_t word,
-                                                   const uint32_t* sk /* bit shifts of the 4 steps */,
                                                    const uint32_t* off8 /* byte offsets of the 4 columns */,
                                                    unsigned long long st) {
     char* base = (char*)pk;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t bin = __builtin_amdgcn_ubfe(word, sk[k], 8);
+        const uint32_t bin = __builtin_amdgcn_ubfe(word, off8[k], 8);   // bits [off8 & 31, +8)
         atomicAdd((unsigned long long*)(base + ((bin << 9) + off8[k])), st);   // [bin][64] x 8 bytes
     }
 }
@@ -734,7 +740,7 @@ __device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk
                                              __amdgpu_buffer_rsrc_t rbase, uint32_t sh, uint32_t wl4,
                                              uint32_t wl, __amdgpu_buffer_rsrc_t idx,
                                              __amdgpu_buffer_rsrc_t sbase, uint32_t pos, uint32_t end,
-                                             uint32_t n, uint32_t r0, const uint32_t* sk, const uint32_t* off8,
+                                             uint32_t n, uint32_t r0, const uint32_t* off8,
                                              uint32_t swap_every,
                                              long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
     static_assert(2 * kPackHalf * 64 == kPackIterRows && kPackHalf == 8, "block layout");
@@ -792,14 +798,14 @@ __device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk
         CBH_DLOAD(wB, 4, 12, o) CBH_DLOAD(wB, 5, 13, o) CBH_DLOAD(wB, 6, 14, o) CBH_DLOAD(wB, 7, 15, o) \
     }
 #define CBH_ATOMS(W, U0, SSV)                                                                \
-    packed_row_atomics(pk, W[0], sk, off8, row_bcast64<U0 + 0>(SSV));                         \
-    packed_row_atomics(pk, W[1], sk, off8, row_bcast64<U0 + 1>(SSV));                         \
-    packed_row_atomics(pk, W[2], sk, off8, row_bcast64<U0 + 2>(SSV));                         \
-    packed_row_atomics(pk, W[3], sk, off8, row_bcast64<U0 + 3>(SSV));                         \
-    packed_row_atomics(pk, W[4], sk, off8, row_bcast64<U0 + 4>(SSV));                         \
-    packed_row_atomics(pk, W[5], sk, off8, row_bcast64<U0 + 5>(SSV));                         \
-    packed_row_atomics(pk, W[6], sk, off8, row_bcast64<U0 + 6>(SSV));                         \
-    packed_row_atomics(pk, W[7], sk, off8, row_bcast64<U0 + 7>(SSV));
+    packed_row_atomics(pk, W[0], off8, row_bcast64<U0 + 0>(SSV));                         \
+    packed_row_atomics(pk, W[1], off8, row_bcast64<U0 + 1>(SSV));                         \
+    packed_row_atomics(pk, W[2], off8, row_bcast64<U0 + 2>(SSV));                         \
+    packed_row_atomics(pk, W[3], off8, row_bcast64<U0 + 3>(SSV));                         \
+    packed_row_atomics(pk, W[4], off8, row_bcast64<U0 + 4>(SSV));                         \
+    packed_row_atomics(pk, W[5], off8, row_bcast64<U0 + 5>(SSV));                         \
+    packed_row_atomics(pk, W[6], off8, row_bcast64<U0 + 6>(SSV));                         \
+    packed_row_atomics(pk, W[7], off8, row_bcast64<U0 + 7>(SSV));
     CBH_LOADA(six, base)
     CBH_LOADB(six, base)
     uint32_t blk = 0;
@@ -829,33 +835,140 @@ __device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk
 #undef CBH_GLOAD
 }
 
+// Broadcast lane 2 (i / 2) + U of each group of four lanes to lane i (DPP quad_perm
+// [U, U, 2 + U, 2 + U]).
+template <int U>
+__device__ __forceinline__ uint32_t quad_pair_bcast(uint32_t v) {
+    constexpr int ctrl = U | (U << 2) | ((2 + U) << 4) | ((2 + U) << 6);
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, ctrl, 0xF, 0xF, true);
+}
+template <int U>
+__device__ __forceinline__ unsigned long long quad_pair_bcast64(unsigned long long v) {
+    return (unsigned long long)quad_pair_bcast<U>((uint32_t)v) |
+           ((unsigned long long)quad_pair_bcast<U>((uint32_t)(v >> 32)) << 32);
+}
+
+// The rows [pos, end) of a narrow last tile of 2 words at the dense level (a tile-major slice of
+// 2 words per row): a 16-lane DPP row takes 8 rows per pass, lane wl = 2 j + w word w of row
+// j, so every atomic instruction carries 64 useful lanes (the full tiles' loop would leave 14 of
+// every 16 lanes on padding).  The LDS columns are the full tiles' (lane wl, step k: column
+// 4 wl + ((k + rot) & 3)), i.e. 8 copies of the tile's 8 feature columns, one per row of a pass
+// -- the same conflict-free bank pairs; the flush sums the copies.  The positions a DPP row
+// covers in a block are the full tiles' (q .. q + 15, clamped into [0, n)), in 2 passes of 8:
+// lane 2 j + w stages the statistic of position q + 8 w + j, and pass u broadcasts lane
+// 2 j + u to lanes 2 j, 2 j + 1 (DPP quad_perm).  A block holds only 8 atomics per lane, so
+// four blocks are in flight: four fixed register sets (words and statistic of a block), each
+// reloaded right after its block is consumed.  Positions past the range read a zero statistic,
+// so the loads of blocks past the end need no guard.  (At the gathered levels every listed row
+// costs its own random line whatever the tile's width, so the narrow tile keeps the 16-lane
+// loop there, in as many ranges as a full tile.)
+struct NarrowSet {
+    uint32_t w[2];                 // words of the set's block (passes 0, 1)
+    unsigned long long sv;         // statistic of the staged position of the set's block
+};
+
+__device__ __forceinline__ void packed_range_narrow(unsigned long long* __restrict__ pk,
+                                                    __amdgpu_buffer_rsrc_t rbase, uint32_t sh,
+                                                    __amdgpu_buffer_rsrc_t sbase, uint32_t pos, uint32_t end,
+                                                    uint32_t n, uint32_t r0, uint32_t wl, const uint32_t* off8,
+                                                    uint32_t swap_every,
+                                                    long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
+    constexpr uint32_t D = 4 * kPackIterRows;   // rows of four blocks
+    const uint32_t j = wl >> 1, w = wl & 1u, w4 = 4u * w;
+    auto qbase = [&](uint32_t bb) -> uint32_t {   // first row of this DPP row's 16, clamped into [0, n)
+        const uint32_t q = bb + 16u * r0;
+        return q + 16u <= n ? q : n - 16u;
+    };
+    auto stage_sv = [&](uint32_t bb) -> unsigned long long {   // this lane's staged position
+        const uint32_t p = qbase(bb) + 8u * w + j;
+        return ldq(sbase, (p < end && p >= bb + 16u * r0) ? 8u * p : kPastEnd);
+    };
+    auto load = [&](NarrowSet& S, uint32_t bb) {
+        S.sv = stage_sv(bb);
+        const uint32_t o = ((qbase(bb) + j) << sh) + w4;
+        S.w[0] = ldw(rbase, o);
+        S.w[1] = ldw(rbase, o + (8u << sh));
+    };
+    NarrowSet S0, S1, S2, S3;
+    // the sets load in the loop's order (compiler memory barriers between them): the loop's first
+    // use, set 0, then waits for set 0's loads only, on entry as on every later round
+    load(S0, pos);
+    asm volatile("" ::: "memory");
+    load(S1, pos + kPackIterRows);
+    asm volatile("" ::: "memory");
+    load(S2, pos + 2 * kPackIterRows);
+    asm volatile("" ::: "memory");
+    load(S3, pos + 3 * kPackIterRows);
+    asm volatile("" ::: "memory");
+    // one block of a set: its atomics, then the set reloaded for the block four later.  The loop
+    // runs whole rounds of four blocks (blocks past the range add zero statistics), so its body
+    // has no exit between blocks and the loads of every set stay in flight across the round;
+    // swaps come every swap_every blocks (a multiple of 4) and once after the last round.
+    auto step = [&](NarrowSet& S, uint32_t bb) {
+        packed_row_atomics(pk, S.w[0], off8, quad_pair_bcast64<0>(S.sv));
+        packed_row_atomics(pk, S.w[1], off8, quad_pair_bcast64<1>(S.sv));
+        load(S, bb + D);
+    };
+    const uint32_t rounds = (end - pos + D - 1) / D;
+    const uint32_t swap_rounds = swap_every / 4;
+    uint32_t base = pos;
+    for (uint32_t rd = 0, since = 0; rd < rounds; ++rd, base += D) {
+        step(S0, base);
+        __builtin_amdgcn_sched_barrier(0);   // keep every set's reload in its own step
+        step(S1, base + kPackIterRows);
+        __builtin_amdgcn_sched_barrier(0);
+        step(S2, base + 2 * kPackIterRows);
+        __builtin_amdgcn_sched_barrier(0);
+        step(S3, base + 3 * kPackIterRows);
+        __builtin_amdgcn_sched_barrier(0);
+        if (++since >= swap_rounds && rd + 1 < rounds) {
+            since = 0;
+            __syncthreads();
+            packed_swap(pk, acc_d, acc_w);
+        }
+    }
+    __syncthreads();
+    packed_swap(pk, acc_d, acc_w);
+}
+
 template <bool kGather>
 static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     const uint32_t* __restrict__ rows /* tile-major (pack_tiles_kernel) */, uint32_t W,
     uint64_t n, const uint32_t* __restrict__ idx /* kGather: rows listed by the partition */,
     const LevelPlan* __restrict__ plan, const unsigned long long* __restrict__ spack /* [n] */,
     const unsigned long long* __restrict__ sseq /* nullable [V]: packed stats in idx order */,
-    uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
+    uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, uint32_t Gn, long long* __restrict__ hist,
     uint32_t swap_every /* blocks of rows between two swaps: 2 * swap_every * kPackIterRows * 2^pack_bits <= 2^30 */,
     const uint32_t* __restrict__ rows_rm /* nullable, kGather: row-major words, 2^rm_sh bytes per row */,
     uint32_t rm_sh) {
     constexpr uint32_t C = 2;
     extern __shared__ unsigned long long pk[];   // [B][64] packed cells
-    // blocks: n_tiles 64-feature tiles (the last one narrower when W is not a multiple of 16
-    // words; its row costs about as much as a full one's), G row ranges each.  Workgroups go to
-    // the 8 XCDs round robin (block b to XCD b % 8), so the (range, tile) pairs are numbered
-    // range-major and XCD x takes the x-th run of per = ceil(n_tiles G / 8) of them: every tile
-    // of one range sits on one XCD, so at the gathered levels the row-major lines of a listed
-    // row come from HBM once and from that L2 for the other tiles, and no XCD holds more pairs
-    // than its CUs when n_tiles G fits the resident slots (pairs past the last exit).
+    // blocks: n_tiles tiles of the 16-lane row loop (64 features; the last one narrower when W
+    // is not a multiple of 16 words and its slice is wider than 2 words: its row costs about as
+    // much as a full one's), G row ranges each.  Workgroups go to the 8 XCDs round robin (block
+    // b to XCD b % 8), so the (range, tile) pairs are numbered range-major and XCD x takes the
+    // x-th run of per = ceil(n_tiles G / 8) of them: every tile of one range sits on one XCD, so
+    // at the gathered levels the row-major lines of a listed row come from HBM once and from that
+    // L2 for the other tiles, and no XCD holds more pairs than its CUs when n_tiles G fits the
+    // resident slots (pairs past the last exit).  Then, when Gn > 0 (the dense level only), the
+    // narrow last tile (tile n_tiles, 2 words) in Gn ranges of the narrow loop.
     const uint32_t pairs = n_tiles * G;
     const uint32_t per = (pairs + 7u) / 8u;
     const uint32_t b = blockIdx.x;
-    const uint32_t i = (b & 7u) * per + (b >> 3);
-    if (i >= pairs) return;   // workgroup-uniform, before any barrier
-    const uint32_t t = i % n_tiles;
-    const uint32_t g = i / n_tiles;
-    const uint32_t GR = G;
+    const bool narrow = b >= 8u * per;
+    uint32_t t, g, GR;
+    if (!narrow) {
+        const uint32_t i = (b & 7u) * per + (b >> 3);
+        if (i >= pairs) return;   // workgroup-uniform, before any barrier
+        t = i % n_tiles;
+        g = i / n_tiles;
+        GR = G;
+    } else {
+        t = n_tiles;
+        g = b - 8u * per;
+        GR = Gn;
+        if (g >= Gn) return;
+    }
     const uint32_t w0 = t * kPackTileWords;
     const uint32_t TW = min(kPackTileWords, W - w0);
     const uint32_t f0 = 4u * w0;
@@ -864,9 +977,9 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     const bool rm = kGather && rows_rm != nullptr;
     const uint32_t sh = rm ? rm_sh : packed_slice_shift(TW);
     for (uint32_t i = threadIdx.x; i < kPackCells; i += kPackThreads) pk[i] = 0ull;
-    // lanes: a 16-lane DPP row per row; a narrow tile's lanes past its words read the zero
-    // padding of the slice (or the next row's words) and add to LDS columns >= TF, never read
-    constexpr uint32_t rpp = kPackThreads / kPackTileWords;
+    // lanes: a 16-lane DPP row per row (the narrow loop: 16 / TW rows); in the 16-lane loop, a
+    // tile narrower than 16 words has lanes past its words read the zero padding of the slice
+    // (or the next row's words) and add to LDS columns >= TF, never read
     const uint32_t r0 = threadIdx.x / kPackTileWords;
     const uint32_t wl = threadIdx.x % kPackTileWords;
     // step k of a row visits byte (k + rot) & 3 of the lane's word: feature 4 * wl + ((k + rot) & 3).
@@ -874,12 +987,9 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     // and any two DPP rows 32 distinct features mod 32, i.e. distinct bank pairs of the
     // [bin][64] cells whatever the bins.
     const uint32_t rot = ((wl >> 2) + (r0 & 1u)) & 3u;
-    uint32_t sk[4], off8[4];   // bit shift in the word and byte offset of the column of step k
+    uint32_t off8[4];   // byte offset of the column of step k (its low 5 bits: the byte's bit shift)
 #pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) {
-        sk[k] = 8u * ((k + rot) & 3u);
-        off8[k] = 8u * (4u * wl + ((k + rot) & 3u));
-    }
+    for (uint32_t k = 0; k < 4; ++k) off8[k] = 8u * (4u * wl + ((k + rot) & 3u));
     long long acc_d[kPackOwn], acc_w[kPackOwn];
 #pragma unroll
     for (int k = 0; k < kPackOwn; ++k) acc_d[k] = acc_w[k] = 0;
@@ -905,13 +1015,19 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = kGather ? plan->built[seg] : 0u;
         if (end > pos) {
-            packed_range<kGather>(pk, rbase, sh, wl4, wl, ibase, sbase, pos, end, (uint32_t)n, r0, sk, off8,
-                                  swap_every, acc_d, acc_w);
+            if (kGather || !narrow)
+                packed_range<kGather>(pk, rbase, sh, wl4, wl, ibase, sbase, pos, end, (uint32_t)n, r0, off8,
+                                      swap_every, acc_d, acc_w);
+            else   // a cell takes 1/8 of the rows a full tile's does: swaps 8x rarer
+                packed_range_narrow(pk, rbase, sh, sbase, pos, end, (uint32_t)n, r0, wl, off8, 8u * swap_every,
+                                    acc_d, acc_w);
             // every contribution of the segment is in the registers now (the last swap follows
-            // the last barrier); flush both channels, then clear the cells and registers
+            // the last barrier); flush both channels (a narrow tile's 16 / TW copies summed), then
+            // clear the cells and registers
             long long* hd = hist + (size_t)slot * C * F * B;
-            packed_flush_channel(pk, acc_d, TF, B, F, f0, hd);
-            packed_flush_channel(pk, acc_w, TF, B, F, f0, hd + (size_t)F * B);
+            const uint32_t copies = narrow ? 16u / TW : 1u, cstride = 4u * TW;
+            packed_flush_channel(pk, acc_d, TF, B, F, f0, hd, copies, cstride);
+            packed_flush_channel(pk, acc_w, TF, B, F, f0, hd + (size_t)F * B, copies, cstride);
             __syncthreads();
 #pragma unroll
             for (int k = 0; k < kPackOwn; ++k) {
@@ -923,7 +1039,6 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
         pos = end;
         ++seg;
     }
-    (void)rpp;
 }
 
 // ---------------------------------------------------------------------------------
@@ -1052,12 +1167,14 @@ static __global__ void planar_stats_fixed_kernel(const double* __restrict__ ssta
 // low field), each channel rounded with its own scale.
 static __global__ void pack_stats_fixed_kernel(const double* __restrict__ sstat, uint64_t n,
                                                const Scales* __restrict__ sc,
-                                               unsigned long long* __restrict__ spack) {
+                                               unsigned long long* __restrict__ spack,
+                                               long long qmax /* 2^pack_bits - 1 */) {
     const double md = sc->mul[kScoreDer], mw = sc->mul[kScoreW];
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (uint64_t)gridDim.x * blockDim.x) {
-        const long long qd = to_fixed(sstat[2 * i], md);
-        const long long qw = to_fixed(sstat[2 * i + 1], mw);
+        // |v * 2^S| < 2^pack_bits, so rounding reaches 2^pack_bits at most: clamped one unit down
+        const long long qd = max(-qmax, min(qmax, to_fixed(sstat[2 * i], md)));
+        const long long qw = max(-qmax, min(qmax, to_fixed(sstat[2 * i + 1], mw)));
         spack[i] = ((unsigned long long)qd << 32) + (unsigned long long)qw;
     }
 }

@@ -195,7 +195,9 @@ struct cbh_session {
     unsigned long long* sseq = nullptr;    // the same for the idx rows, in idx order
     uint32_t* trows = nullptr;             // packed fill: tile-major row words (pack_tiles_kernel)
     uint32_t pk_tiles = 0, pk_ranges = 8, pk_swap = 1;
-    uint32_t pk_blocks = 0;                    // packed fill: workgroups per launch
+    struct PackPlan {                          // packed fill launch: tiles of the 16-lane loop, ranges
+        uint32_t tiles16 = 0, ranges = 0, ranges_n = 0, blocks = 0;   // of each, narrow-tile ranges, workgroups
+    } pk_dense, pk_gath;                       // the dense level; the gathered levels
     uint32_t pk_rm_sh = 0;                     // packed fill: log2 bytes of a row-major row (0: tile-major gathers)
     bool pk_signed_w = false;              // some object or pair weight is negative
     size_t pk_lds = 0;
@@ -498,25 +500,65 @@ uint32_t pick_ranges(uint32_t cus, uint32_t per_cu, uint32_t nt, uint64_t n) {
     return G;
 }
 
-// Row ranges of the packed fill: G per 64-feature tile, the narrow last tile (TW < 16 words)
-// included, so one round of workgroups fills the resident slots.  A narrow tile runs the full
-// tiles' loop (its lanes past TW add to columns that are never read), so its row costs about
-// as much as a full one's and equal ranges balance the work.  (Measured alternatives, config
-// 2's 2-word last tile: 0.4 x as many ranges, 2.1x slower fill; a launch of its own with 8
-// rows per DPP row and per-copy LDS columns, 5% slower -- its loop stays latency-bound.)
-// The gathered levels read row-major words (2^rm_sh bytes per row) when the padded row is a
-// power of two under 4 GiB in all: the tiles of a range run on one XCD, so a listed row's
-// lines come from HBM once for all its tiles.  CBH_PACK_GATHER=tiles keeps the tile-major
-// slices there (a measurement knob).
+// Row ranges of the packed fill.  Tiles of the 16-lane row loop (64 features; a last tile of
+// 3..15 words runs the same loop, its lanes past TW adding to columns that are never read, so its
+// row costs about as much as a full one's) get G ranges each.  At the dense level a last tile of
+// 2 words runs the narrow loop (8 rows per DPP row) in Gn = G * r ranges, r its cost per row
+// relative to a full tile's (CBH_PACK_NARROW_COST, a measurement knob; CBH_PACK_NARROW=off keeps
+// the 16-lane loop); at the gathered levels every listed row costs its tile a random line, so
+// the narrow tile keeps the 16-lane loop there.  One round of workgroups fills the resident
+// slots.  The gathered levels read row-major words (2^rm_sh bytes per row) when the padded row
+// is a power of two under 4 GiB in all: the tiles of a range run on one XCD, so a listed row's
+// lines come from HBM once for all its tiles (CBH_PACK_GATHER=tiles keeps the tile-major slices
+// there, a measurement knob).
 void pick_packed_ranges(cbh_session* s, uint32_t cus, uint32_t per_cu) {
     const uint32_t cap = cus * std::max<uint32_t>(per_cu, 1);
-    const uint32_t nt = s->pk_tiles;
-    uint32_t G = std::max<uint32_t>(1, cap / nt);
-    // short inputs: at least 4096 rows per range, so the per-workgroup flush stays small
-    const uint64_t min_rows = 4096;
-    while (G > 1 && s->n / G < min_rows) G = G / 2;
-    s->pk_ranges = G;
-    s->pk_blocks = 8 * ((nt * G + 7) / 8);
+    double r = 0.2;
+    if (const char* e = std::getenv("CBH_PACK_NARROW_COST")) {
+        const double v = std::strtod(e, nullptr);
+        if (v > 0.0 && v <= 1.0) r = v;
+    }
+    auto plan = [&](bool narrow) {
+        cbh_session::PackPlan pl;
+        const uint32_t nt = narrow ? s->W / kPackTileWords : s->pk_tiles;
+        auto gn_of = [&](uint32_t g) { return narrow ? std::max<uint32_t>(1, (uint32_t)std::ceil(g * r)) : 0u; };
+        uint32_t G = 0, Gn = 0;
+        if (nt == 0) {   // one narrow tile: every slot
+            Gn = cap;
+        } else {
+            G = std::max<uint32_t>(1, cap / nt);
+            while (G > 1 && nt * G + gn_of(G) > cap) --G;
+            Gn = gn_of(G);
+            // blocks go to the 8 XCDs round robin: the full tiles' pairs fill per = nt G / 8 slots
+            // of each XCD (G a multiple of 8), the narrow ranges the rest, so no XCD holds more
+            // workgroups than its resident slots (one more would wait for a second round)
+            const uint32_t per_xcd = cap / 8;
+            if (narrow && cap % 8 == 0) {
+                for (uint32_t g8 = (cap / nt) / 8 * 8; g8 >= 8; g8 -= 8) {
+                    const uint32_t per = nt * g8 / 8;
+                    if (per < per_xcd && 8 * (per_xcd - per) >= gn_of(g8)) {
+                        G = g8;
+                        Gn = 8 * (per_xcd - per);
+                        break;
+                    }
+                }
+            }
+        }
+        // short inputs: at least 4096 rows per range, so the per-workgroup flush stays small
+        const uint64_t min_rows = 4096;
+        while (G > 1 && s->n / G < min_rows) G = G / 2;
+        while (Gn > 1 && s->n / Gn < min_rows) Gn = Gn / 2;
+        pl.tiles16 = nt;
+        pl.ranges = G;
+        pl.ranges_n = Gn;
+        pl.blocks = 8 * ((nt * G + 7) / 8) + Gn;
+        return pl;
+    };
+    const char* ne = std::getenv("CBH_PACK_NARROW");
+    const bool narrow = s->W % kPackTileWords == 2 && !(ne && std::string(ne) == "off");
+    s->pk_dense = plan(narrow);
+    s->pk_gath = plan(false);
+    s->pk_ranges = s->pk_gath.ranges;
     const uint64_t rb = 4ull * s->Ws;
     s->pk_rm_sh = 0;
     const char* e = std::getenv("CBH_PACK_GATHER");
@@ -593,14 +635,14 @@ int plan_fill_mode(cbh_session* s) {
     if (want_packed) pick_packed_ranges(s, (uint32_t)cus, (uint32_t)per_cu);
     if (want_packed) {
         // CBH_PACK_SWAP (1, 2, 4, 8): blocks of rows between two swaps; each doubling costs
-        // one bit of a row's rounded value (a measurement knob).  Default 2: 18-bit rows, and
-        // half the swap work of 1 (config 2: fill 3.59 -> 3.40 ms per tree)
-        s->pk_swap = 2;
+        // one bit of a row's rounded value (a measurement knob).  Default 4: 18-bit rows (rows
+        // clamped to 2^18 - 1, so 8192 of them stay below 2^31), a quarter of the swap work of 1
+        s->pk_swap = 4;
         if (const char* sw = std::getenv("CBH_PACK_SWAP")) {
             const long v2 = std::strtol(sw, nullptr, 10);
             if (v2 == 1 || v2 == 2 || v2 == 4 || v2 == 8) s->pk_swap = (uint32_t)v2;
         }
-        s->pack_bits = kPackBitsDefault - (s->pk_swap >= 2) - (s->pk_swap >= 4) - (s->pk_swap >= 8);
+        s->pack_bits = kPackBitsSwap1 - (s->pk_swap >= 2) - (s->pk_swap >= 4) - (s->pk_swap >= 8);
     }
     CHECK(dalloc(&s->spack, (size_t)s->n * planes));
     CHECK(dalloc(&s->sseq, (size_t)s->n * planes));
@@ -1362,7 +1404,8 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
     scales_kernel<<<1, 256, 0, st>>>(s->partials, pgrid, s->bounds, s->scales, s->packed ? s->pack_bits : 0);
     HIP_TRY(hipGetLastError());
     if (s->packed)
-        pack_stats_fixed_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack);
+        pack_stats_fixed_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack,
+                                                                         (1ll << s->pack_bits) - 1);
     else if (s->split)
         planar_stats_fixed_kernel<C><<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales,
                                                                            (long long*)s->spack);
@@ -1399,13 +1442,13 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         }
         CHECK(s->stage_begin(kStFill));   // the fill kernel alone
         if (s->packed && level == 0)
-            fill_packed_kernel<false><<<s->pk_blocks, kPackThreads, s->pk_lds, st>>>(
-                s->trows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_tiles, s->F, s->B,
-                s->pk_ranges, cur, s->pk_swap, nullptr, 0u);
+            fill_packed_kernel<false><<<s->pk_dense.blocks, kPackThreads, s->pk_lds, st>>>(
+                s->trows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_dense.tiles16, s->F, s->B,
+                s->pk_dense.ranges, s->pk_dense.ranges_n, cur, s->pk_swap, nullptr, 0u);
         else if (s->packed)
-            fill_packed_kernel<true><<<s->pk_blocks, kPackThreads, s->pk_lds, st>>>(
-                s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_tiles, s->F, s->B,
-                s->pk_ranges, cur, s->pk_swap, s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh);
+            fill_packed_kernel<true><<<s->pk_gath.blocks, kPackThreads, s->pk_lds, st>>>(
+                s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_gath.tiles16, s->F, s->B,
+                s->pk_gath.ranges, 0u, cur, s->pk_swap, s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh);
         else if (s->split && level == 0)
             fill_split_kernel<false><<<s->pk_ranges * s->pk_tiles * C, 1024, s->pk_lds, st>>>(
                 s->rows, s->Ws, s->W, n, nullptr, nullptr, (const long long*)s->spack, nullptr, C, s->pk_tiles,
