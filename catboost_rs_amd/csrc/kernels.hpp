@@ -1340,6 +1340,67 @@ static __global__ __launch_bounds__(256) void seg_totals_kernel(const uint32_t* 
 // TRUE children 0..P-1; Cosine = num / sqrt(1e-100 + sum avg^2 w).  The block argmax keeps
 // the highest score, ties to the lowest border (strict first-wins, tree.rs:355-366).
 // ---------------------------------------------------------------------------------
+// The score terms of candidate border b of feature f over all parents, folded into num and
+// den in the reference order (d, side, p): score.rs:192-265.  The cells of kPre parents are
+// loaded ahead of their terms, from clamped (always valid) addresses with the values of parents
+// past P (and, for one-hot, bin -1) replaced by zero, so the loads need no branches; zero cells
+// give s = w = 0, avg = 0 and terms of exactly 0 (num and den only hold non-negative sums).  The
+// quotient is computed for every term and kept only where w > 0 (branch-free).  Lanes past the
+// bins read bin B-1 (their score is discarded).
+template <int K, bool kOneHot>
+__device__ __forceinline__ void score_fold(const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
+                                           uint32_t f, uint32_t b, double inv_d, double inv_w, double l2,
+                                           double& num, double& den) {
+    constexpr int C = K + 1;
+    constexpr uint32_t kPre = 8;   // parents whose cells are loaded ahead of their terms
+    const uint32_t bc = min(b, B - 1);
+    const uint32_t bq = bc > 0 ? bc - 1 : 0;
+    for (int d = 0; d < K; ++d) {
+        for (int side = 0; side < 2; ++side) {
+            for (uint32_t p0 = 0; p0 < P; p0 += kPre) {
+                long long pdv[kPre], pwv[kPre], tdv[kPre], twv[kPre], qdv[kPre], qwv[kPre];
+#pragma unroll
+                for (uint32_t u = 0; u < kPre; ++u) {
+                    const uint32_t p = p0 + u;
+                    const bool ok = p < P;
+                    const uint32_t pc = ok ? p : P - 1;
+                    const long long* hd = hist + (((size_t)pc * C + d) * F + f) * B;
+                    const long long* hw = hist + (((size_t)pc * C + K) * F + f) * B;
+                    const long long a = hd[bc], c = hw[bc], e = hd[B - 1], g = hw[B - 1];
+                    pdv[u] = ok ? a : 0;
+                    pwv[u] = ok ? c : 0;
+                    tdv[u] = ok ? e : 0;
+                    twv[u] = ok ? g : 0;
+                    if (kOneHot) {
+                        const long long qa = hd[bq], qc = hw[bq];
+                        qdv[u] = (ok && b > 0) ? qa : 0;
+                        qwv[u] = (ok && b > 0) ? qc : 0;
+                    }
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < kPre; ++u) {
+                    const long long pd = pdv[u], pw = pwv[u], td = tdv[u], tw = twv[u];
+                    long long xd, xw;
+                    if (!kOneHot) {
+                        xd = side == 0 ? pd : td - pd;
+                        xw = side == 0 ? pw : tw - pw;
+                    } else {
+                        const long long vd = pd - qdv[u], vw = pw - qwv[u];
+                        xd = side == 0 ? td - vd : vd;
+                        xw = side == 0 ? tw - vw : vw;
+                    }
+                    const double s = (double)xd * inv_d;
+                    const double w = (double)xw * inv_w;
+                    const double q = s / (w + l2);
+                    const double avg = w > 0.0 ? q : 0.0;
+                    num += avg * s;
+                    den += avg * avg * w;
+                }
+            }
+        }
+    }
+}
+
 template <int K, int NW>
 __global__ __launch_bounds__(64 * NW) void score_kernel(
     long long* __restrict__ zero_buf, uint32_t zero_leaves, uint32_t HC,   // next level's histogram
@@ -1347,8 +1408,6 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     const uint32_t* __restrict__ n_cand, const uint8_t* __restrict__ one_hot,
     const Scales* __restrict__ sc, double l2, int cosine, double* __restrict__ best_score,
     uint32_t* __restrict__ best_bin, const double* __restrict__ fweight /* nullable [F] */) {
-    constexpr int C = K + 1;
-    constexpr uint32_t kPre = 8;   // parents whose cells are loaded ahead of their terms
     __shared__ double red_s[NW];
     __shared__ uint32_t red_b[NW];
     const uint32_t f = blockIdx.x;
@@ -1372,48 +1431,11 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     double den = 0.0;
     den += 1e-100;
     // the histograms are in prefix form over bins: prefix = cell b, total = cell B-1, the
-    // bin itself (one-hot) = cell b - cell b-1.  The cells of kPre parents are loaded ahead
-    // of their terms; the fold order over (d, side, p) is the reference's
-    const bool in = b < B;
-    for (int d = 0; d < K; ++d) {
-        for (int side = 0; side < 2; ++side) {
-            for (uint32_t p0 = 0; p0 < P; p0 += kPre) {
-                long long pdv[kPre], pwv[kPre], tdv[kPre], twv[kPre], qdv[kPre], qwv[kPre];
-#pragma unroll
-                for (uint32_t u = 0; u < kPre; ++u) {
-                    const uint32_t p = p0 + u;
-                    const bool ok = in && p < P;
-                    const long long* hd = hist + (((size_t)p * C + d) * F + f) * B;
-                    const long long* hw = hist + (((size_t)p * C + K) * F + f) * B;
-                    pdv[u] = ok ? hd[b] : 0;
-                    pwv[u] = ok ? hw[b] : 0;
-                    tdv[u] = ok ? hd[B - 1] : 0;
-                    twv[u] = ok ? hw[B - 1] : 0;
-                    qdv[u] = (ok && oh && b > 0) ? hd[b - 1] : 0;
-                    qwv[u] = (ok && oh && b > 0) ? hw[b - 1] : 0;
-                }
-#pragma unroll
-                for (uint32_t u = 0; u < kPre; ++u) {
-                    if (p0 + u >= P) break;
-                    const long long pd = pdv[u], pw = pwv[u], td = tdv[u], tw = twv[u];
-                    const long long vd = pd - qdv[u], vw = pw - qwv[u];
-                    long long xd, xw;
-                    if (!oh) {
-                        xd = side == 0 ? pd : td - pd;
-                        xw = side == 0 ? pw : tw - pw;
-                    } else {
-                        xd = side == 0 ? td - vd : vd;
-                        xw = side == 0 ? tw - vw : vw;
-                    }
-                    const double s = (double)xd * inv_d;
-                    const double w = (double)xw * inv_w;
-                    const double avg = w > 0.0 ? s / (w + l2) : 0.0;
-                    num += avg * s;
-                    den += avg * avg * w;
-                }
-            }
-        }
-    }
+    // bin itself (one-hot) = cell b - cell b-1; the fold order over (d, side, p) is the reference's
+    if (oh)
+        score_fold<K, true>(hist, P, F, B, f, b, inv_d, inv_w, l2, num, den);
+    else
+        score_fold<K, false>(hist, P, F, B, f, b, inv_d, inv_w, l2, num, den);
     double score = cosine ? num / sqrt(den) : num;
     // the model_size_reg weight of a CTR column multiplies every candidate's score
     // (weight * score, tree.rs:3340-3346)
