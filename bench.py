@@ -322,11 +322,12 @@ def main():
         f"{achieved:.1f} GB/s algorithmic")
 
     # LDS-atomic roofline of the fill: every visited (row, feature) adds one 64-bit LDS atomic
-    # (packed fill: both channels in one word) or K+1 (two-channel / channel-split fills); the
+    # (packed fill: both channels in one word), ceil((K+1)/2) (packed multi-channel fill: two
+    # channels per word) or K+1 (two-channel / channel-split fills); the
     # cap is the contiguous (conflict-free) 64-bit LDS atomic rate measured on this GPU, the
     # pattern the fills' rotated lane layouts reach
     K = kw["approx_dim"] if P["loss"] == "MultiClass" else 1
-    per_pair = 1 if st["fill_mode"] == 1 else K + 1
+    per_pair = {1: 1, 3: (K + 2) // 2}.get(st["fill_mode"], K + 1)
     lds = None
     rates = _lds_rates()
     if "contiguous_u64" in rates and fill_s > 0:
@@ -365,7 +366,8 @@ def main():
         tr2.close()
         cpu["splits_match_gpu"] = bool(np.array_equal(first, exp["splits"]))
 
-    fill_kernel = {0: "fill_kernel", 1: "fill_packed_kernel", 2: "fill_split_kernel"}[st["fill_mode"]]
+    fill_kernel = {0: "fill_kernel", 1: "fill_packed_kernel", 2: "fill_split_kernel",
+                   3: "fill_pkk_kernel"}[st["fill_mode"]]
     names = {1: "config1: RMSE, no bootstrap, depth 6, 128 borders",
              2: ("config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 GreedyLogSum borders selected on the "
                  "device from the raw f32 columns, quantized on the device" if raw else
@@ -387,7 +389,9 @@ def main():
         "vs_baseline": None,
         "dtype": "u8 bins, int64 fixed-point sums, f64 scores",
         "fill": {0: "two-channel 32-feature tiles", 1: f"packed 64-feature tiles ({st['fill_pack_bits']}-bit rows)",
-                 2: "channel-split 64-feature tiles"}[st["fill_mode"]],
+                 2: "channel-split 64-feature tiles",
+                 3: f"packed multi-channel 32-feature tiles (two channels per word, {st['fill_pack_bits']}-bit rows)"
+                 }[st["fill_mode"]],
         "data": f"synthetic (seeded; datagen.config{args.config}{'_raw' if raw else ''})",
         "config": {"workload": names[args.config], "rows": n, "features": F, "depth": P["depth"],
                    "parallelism": "single GPU"},

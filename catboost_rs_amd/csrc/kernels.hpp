@@ -36,6 +36,19 @@ struct LevelPlan {            // written by plan_finalize, read by fill/derive/c
     uint32_t seg_begin[kMaxLeaves / 2];
 };
 
+// The segment of the idx list that position rb falls in: the last s with seg_begin[s] <= rb
+// (seg_begin is non-decreasing, seg_begin[0] = 0), by binary search -- a few dependent loads of
+// the plan instead of one per segment before rb.
+__device__ __forceinline__ uint32_t first_segment(const LevelPlan* __restrict__ plan, uint32_t n_seg, uint32_t rb) {
+    uint32_t lo = 0, hi = n_seg;   // answer in [lo, hi)
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (plan->seg_begin[mid] <= rb) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
 struct SampleParams {
     int32_t kind;             // 0 none, 1 Bayesian, 2 Bernoulli
     float temperature;
@@ -541,7 +554,7 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t n_seg = idx ? plan->n_parent : 1u;
     uint32_t seg = 0;
     if (idx)
-        while (seg + 1 < n_seg && plan->seg_begin[seg + 1] <= rb) ++seg;
+        seg = first_segment(plan, n_seg, rb);
     uint32_t pos = rb;
     while (pos < re) {
         const uint32_t seg_end = (idx && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
@@ -1000,7 +1013,7 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     const uint32_t n_seg = kGather ? plan->n_parent : 1u;
     uint32_t seg = 0;
     if (kGather)
-        while (seg + 1 < n_seg && plan->seg_begin[seg + 1] <= rb) ++seg;
+        seg = first_segment(plan, n_seg, rb);
     // tile-major rows: this tile's slice starts at word n * w0, 2^sh bytes per row; row-major:
     // word w0 of row 0, rows 2^sh bytes apart (a narrow tile's lanes past W read the row's zero
     // padding: rows are padded to whole 16-word multiples)
@@ -1033,6 +1046,221 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
             for (int k = 0; k < kPackOwn; ++k) {
                 pk[threadIdx.x + (uint32_t)k * kPackThreads] = 0ull;
                 acc_d[k] = acc_w[k] = 0;
+            }
+            __syncthreads();
+        }
+        pos = end;
+        ++seg;
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Packed multi-channel fill (K > 1, NP * B <= 512 with NP = ceil(C / 2) planes).  The score
+// channels 2j and 2j + 1 of a row travel in one 64-bit word, p_j = q_{2j+1} * 2^32 + q_{2j}
+// (mod 2^64), each |q| <= 2^kPkkBits - 1 (rounded on the scale of the largest row, clamped), so
+// a (row, feature) costs NP = 6 LDS atomics at C = 11 instead of 11 -- the fill of a many-class
+// session is bound by the LDS atomic instruction rate, whatever share of lanes the dominant-bin
+// skip leaves active.  Both fields are signed: a cell decodes as lo = sext(low 32 bits),
+// hi = (cell - lo) / 2^32, exact while each field's sum stays below 2^31 in magnitude.  Every
+// thread owns kPkkOwn cells and swaps them with zero after the barrier that ends every
+// kPkkSwapBlocks blocks of kPkkBlockRows rows; atomics of threads already in the next period
+// may land before the swap, so at most R = 2 * kPkkSwapBlocks * kPkkBlockRows rows fall between
+// two swaps of a cell and R * (2^kPkkBits - 1) < 2^31.  The swapped fields are added to int64
+// registers, flushed to the level histogram at segment ends: every sum is an exact integer of
+// the rounded rows (order-free, reproducible).  Tiles of 32 features (8 words), LDS
+// [plane][bin][32] with the two-channel bin-major fill's rotated visits (any 16 consecutive
+// lanes hit 16 distinct features mod 16: distinct bank pairs whatever the bins), 8 lanes per
+// row.  A lane past the tile's words reads the row's zero
+// padding and adds to columns >= TF, which are never flushed.
+// ---------------------------------------------------------------------------------
+constexpr uint32_t kPkkThreads = 1024;
+constexpr int kPkkOwn = 16;                                            // cells per thread
+constexpr uint32_t kPkkCells = (uint32_t)kPkkOwn * kPkkThreads;        // NP * B * 32 <= 16384
+constexpr uint32_t kPkkBlockRows = kPkkThreads / 8;                   // 128 rows per block
+constexpr uint32_t kPkkSwapBlocks = 8;                                 // 1024 rows per swap period
+constexpr int kPkkBits = 20;                                           // 2048 * (2^20 - 1) < 2^31
+static_assert(2ull * kPkkSwapBlocks * kPkkBlockRows * ((1ull << kPkkBits) - 1) < (1ull << 31),
+              "packed multi-channel fields stay below 2^31");
+
+__device__ __forceinline__ void unpack_add_signed(unsigned long long v, long long& lo_acc, long long& hi_acc) {
+    const int32_t lo = (int32_t)(uint32_t)v;
+    lo_acc += lo;
+    hi_acc += (long long)(int32_t)(uint32_t)((v - (unsigned long long)(long long)lo) >> 32);
+}
+
+// Score channels f64 -> clamped fixed point in place ([n][C] doubles become int64, which the
+// dominant-bin segment totals read) and the NP packed words of every row [n][NP] the fill reads.
+template <int C>
+static __global__ void quantize_pack_kernel(double* __restrict__ sstat, uint64_t n, const Scales* __restrict__ sc,
+                                            unsigned long long* __restrict__ spk, long long qmax) {
+    constexpr int NP = (C + 1) / 2;
+    const double md = sc->mul[kScoreDer], mw = sc->mul[kScoreW];
+    long long* out = (long long*)sstat;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        long long q[2 * NP];
+#pragma unroll
+        for (int ch = 0; ch < C; ++ch) {
+            q[ch] = max(-qmax, min(qmax, to_fixed(sstat[i * C + ch], ch == C - 1 ? mw : md)));
+            out[i * C + ch] = q[ch];
+        }
+        if (C & 1) q[C] = 0;
+#pragma unroll
+        for (int j = 0; j < NP; ++j)
+            spk[i * NP + j] = ((unsigned long long)(uint32_t)q[2 * j + 1] << 32) + (unsigned long long)q[2 * j];
+    }
+}
+
+template <int C, bool kSkip, bool kGather>
+static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
+    const uint32_t* __restrict__ rows, uint32_t W, uint32_t stride /* words per row in memory */, uint64_t n,
+    const uint32_t* __restrict__ idx, const LevelPlan* __restrict__ plan,
+    const unsigned long long* __restrict__ spk /* [n][NP] */, uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
+    const uint32_t* __restrict__ skip_bin /* kSkip: [F] */) {
+    constexpr int NP = (C + 1) / 2;
+    extern __shared__ unsigned long long pk[];   // [NP][B][32], kPkkCells cells
+    const uint32_t b = blockIdx.x;
+    const uint32_t xcd = b & 7u, q = b >> 3;
+    const uint32_t t = q % n_tiles;
+    const uint32_t g = (q / n_tiles) * 8u + xcd;   // row range (ranges of a tile spread over the XCDs)
+    const uint32_t w0 = t * 8u;
+    const uint32_t TW = min(8u, W - w0);
+    const uint32_t f0 = 4u * w0;
+    const uint32_t TF = min(4u * TW, F - f0);
+    const uint32_t plane = B * 32u;
+    for (uint32_t i = threadIdx.x; i < kPkkCells; i += kPkkThreads) pk[i] = 0ull;
+    const uint32_t r0 = threadIdx.x >> 3, wl = threadIdx.x & 7u;   // 128 rows per pass
+    const uint32_t rot = (2u * (r0 & 1u) + ((wl >> 2) ^ ((r0 >> 1) & 1u))) & 3u;
+    uint32_t off8[4], skp[4];   // byte offset of the step's column (low 5 bits: the byte's bit shift)
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t kb = (k + rot) & 3u;
+        const uint32_t f = 4u * wl + kb;
+        off8[k] = 8u * f;
+        skp[k] = (kSkip && f < TF) ? skip_bin[f0 + f] : 256u;
+    }
+    long long acc_lo[kPkkOwn], acc_hi[kPkkOwn];
+#pragma unroll
+    for (int k = 0; k < kPkkOwn; ++k) acc_lo[k] = acc_hi[k] = 0;
+    __syncthreads();
+    const uint32_t V = kGather ? plan->rows : (uint32_t)n;
+    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
+    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
+    const uint32_t n_seg = kGather ? plan->n_parent : 1u;
+    uint32_t seg = 0;
+    if (kGather)
+        seg = first_segment(plan, n_seg, rb);
+    auto swap_cells = [&]() {
+#pragma unroll
+        for (int k = 0; k < kPkkOwn; ++k) {
+            const unsigned long long v = atomicExch(pk + threadIdx.x + (uint32_t)k * kPkkThreads, 0ull);
+            unpack_add_signed(v, acc_lo[k], acc_hi[k]);
+        }
+    };
+    uint32_t pos = rb;
+    while (pos < re) {
+        const uint32_t seg_lo = kGather ? plan->seg_begin[seg] : 0u;
+        const uint32_t seg_end = (kGather && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
+        const uint32_t end = min(re, seg_end);
+        const uint32_t slot = kGather ? plan->built[seg] : 0u;
+        if (end > pos) {
+            // blocks of 128 rows (one per row slot), two register sets SA and SB in flight: the
+            // words and statistics of a block are loaded two blocks ahead, gathered row indices
+            // four, so a block's atomics never wait for its loads (fixed set roles: no register
+            // moves that would wait on loads in flight)
+            struct Set {
+                uint32_t word;
+                unsigned long long st[NP];
+            } SA, SB;
+            auto ldix = [&](uint32_t bb) -> uint32_t {
+                const uint32_t p = bb + r0;
+                return kGather ? idx[p < end ? p : pos] : (p < end ? p : pos);
+            };
+            auto load_set = [&](Set& S, uint32_t bb, uint32_t doc) {
+                const uint32_t p = bb + r0;
+                const bool ok = p < end;
+                S.word = rows[(size_t)doc * stride + w0 + wl];
+#pragma unroll
+                for (int j = 0; j < NP; ++j) {
+                    const unsigned long long v = spk[(size_t)doc * NP + j];
+                    S.st[j] = ok ? v : 0ull;
+                }
+            };
+            auto atoms = [&](const Set& S) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t bin = __builtin_amdgcn_ubfe(S.word, off8[k], 8);
+                    if (kSkip && bin == skp[k]) continue;   // dominant bin: rebuilt from the totals
+                    unsigned long long* cell = (unsigned long long*)((char*)pk + ((bin << 8) + off8[k]));
+#pragma unroll
+                    for (int j = 0; j < NP; ++j) atomicAdd(cell + (size_t)j * plane, S.st[j]);
+                }
+            };
+            uint32_t blk = 0;
+            auto after_block = [&](uint32_t bb) {   // swap at the end of a period and of the segment
+                if (++blk >= kPkkSwapBlocks || bb + kPkkBlockRows >= end) {
+                    blk = 0;
+                    __syncthreads();
+                    swap_cells();
+                }
+            };
+            uint32_t ixA = ldix(pos), ixB = ldix(pos + kPkkBlockRows);
+            load_set(SA, pos, ixA);
+            asm volatile("" ::: "memory");
+            load_set(SB, pos + kPkkBlockRows, ixB);
+            asm volatile("" ::: "memory");
+            if (kGather) {
+                ixA = ldix(pos + 2 * kPkkBlockRows);
+                ixB = ldix(pos + 3 * kPkkBlockRows);
+            }
+            asm volatile("" ::: "memory");
+            for (uint32_t bb = pos;; bb += 2 * kPkkBlockRows) {   // workgroup-uniform
+                atoms(SA);
+                load_set(SA, bb + 2 * kPkkBlockRows, kGather ? ixA : ldix(bb + 2 * kPkkBlockRows));
+                if (kGather) ixA = ldix(bb + 4 * kPkkBlockRows);
+                after_block(bb);
+                if (bb + kPkkBlockRows >= end) break;
+                atoms(SB);
+                load_set(SB, bb + 3 * kPkkBlockRows, kGather ? ixB : ldix(bb + 3 * kPkkBlockRows));
+                if (kGather) ixB = ldix(bb + 5 * kPkkBlockRows);
+                after_block(bb + kPkkBlockRows);
+                if (bb + 2 * kPkkBlockRows >= end) break;
+            }
+            // every contribution of the segment is in the registers now: flush each plane's two
+            // channels (stage the registers in the cells, then write the non-zero cells).  A segment
+            // that lies wholly in this workgroup's range is this tile's only writer of its rows: its
+            // cells are stored (the level histogram starts zeroed); a segment shared with the
+            // neighbouring range is added with global atomics
+            const bool owned = pos == seg_lo && end == seg_end;
+            long long* hd = hist + (size_t)slot * C * F * B;
+            for (int half = 0; half < 2; ++half) {
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < kPkkOwn; ++k)
+                    pk[threadIdx.x + (uint32_t)k * kPkkThreads] = (unsigned long long)(half ? acc_hi[k] : acc_lo[k]);
+                __syncthreads();
+                // a wave takes 8 features x 8 bins of one plane (64-byte runs of bins in the histogram)
+                const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
+                const uint32_t vcells = (uint32_t)NP * nfb * nbb * 64;
+                for (uint32_t i = threadIdx.x; i < vcells; i += kPkkThreads) {
+                    const uint32_t l = i & 63u, jj = i >> 6;
+                    const uint32_t j = jj / (nfb * nbb), jb = jj - j * (nfb * nbb);
+                    const uint32_t f = (jb / nbb) * 8 + (l >> 3), bin = (jb % nbb) * 8 + (l & 7u);
+                    const uint32_t ch = 2u * j + (uint32_t)half;
+                    if (f >= TF || bin >= B || ch >= (uint32_t)C) continue;
+                    const unsigned long long v = pk[j * plane + bin * 32u + f];
+                    unsigned long long* d = (unsigned long long*)hd + (((size_t)ch * F + f0 + f) * B + bin);
+                    if (v != 0) {
+                        if (owned) *d = v;
+                        else atomicAdd(d, v);
+                    }
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kPkkOwn; ++k) {
+                pk[threadIdx.x + (uint32_t)k * kPkkThreads] = 0ull;
+                acc_lo[k] = acc_hi[k] = 0;
             }
             __syncthreads();
         }
@@ -1087,7 +1315,7 @@ static __global__ __launch_bounds__(1024) void fill_split_kernel(
     const uint32_t n_seg = kGather ? plan->n_parent : 1u;
     uint32_t seg = 0;
     if (kGather)
-        while (seg + 1 < n_seg && plan->seg_begin[seg + 1] <= rb) ++seg;
+        seg = first_segment(plan, n_seg, rb);
     const uint32_t* rsrc = rows + w0 + wl;
     const bool seq = kGather && sseqp != nullptr;
     const long long* sbase = (seq ? sseqp : splanar) + (size_t)c * n;
@@ -1682,24 +1910,39 @@ static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __r
         const uint64_t i = beg + (uint64_t)u * 64 + lane;
         lfs[u] = i < end ? leaf[i] : 0x8000u;
     }
+    // listed rows: key = parent, valid = the row lies in its parent's directly built child
+    uint32_t vmask = 0;   // validity bit per u
+    uint32_t key_of[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t lf = lfs[u];
+        const uint32_t p = lf & (n_parent - 1u);
+        const bool valid = !(lf & 0x8000u) && built[p] == lf;
+        key_of[u] = valid ? p : 0u;
+        vmask |= (valid ? 1u : 0u) << u;
+    }
+    // one plane of statistics (the packed fill's): every listed row's word is loaded before
+    // the first store, so the wave waits for memory once, not once per 64 rows
+    unsigned long long spv[U];
+    const bool one_plane = sp_out && sp_ch == 1;
+    if (one_plane) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t i = beg + (uint64_t)u * 64 + lane;
+            spv[u] = ((vmask >> u) & 1u) ? sp_in[i] : 0ull;
+        }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint64_t i = beg + (uint64_t)u * 64 + lane;
-        uint32_t key = 0;
-        bool valid = false;
-        const uint32_t lf = lfs[u];
-        if (!(lf & 0x8000u)) {
-            const uint32_t p = lf & (n_parent - 1u);
-            if (built[p] == lf) {
-                key = p;
-                valid = true;
-            }
-        }
+        const bool valid = (vmask >> u) & 1u;
+        const uint32_t key = key_of[u];
         const uint64_t mask = wave_peers(key, valid, level);
         const uint32_t rank = mbcnt64(mask);
         const uint32_t base = valid ? run[wave][key] : 0u;
         if (valid) idx[base + rank] = (uint32_t)i;
-        if (valid && sp_out)
+        if (valid && one_plane) sp_out[base + rank] = spv[u];
+        else if (valid && sp_out)
             for (uint32_t c = 0; c < sp_ch; ++c) sp_out[(size_t)c * n + base + rank] = sp_in[(size_t)c * n + i];
         if (valid && rank == 0) run[wave][key] = base + (uint32_t)__popcll(mask);
     }

@@ -191,6 +191,9 @@ struct cbh_session {
     // one LDS atomic per (row, feature)) or channel-split (exact int64, one workgroup per
     // channel of a tile)
     bool packed = false, split = false;
+    // packed multi-channel fill (K > 1: two score channels per 64-bit word, NP = ceil(C/2) planes)
+    bool pkk = false;
+    uint32_t pkk_tiles = 0, pkk_ranges = 8;
     int pack_bits = 0;
     unsigned long long* spack = nullptr;   // packed: [n] words; split: [C][n] fixed-point planes
     unsigned long long* sseq = nullptr;    // the same for the idx rows, in idx order
@@ -604,10 +607,44 @@ int plan_tiles(cbh_session* s) {
 // 64-feature fill (K == 1), =split the channel-split 64-feature fill; the default picks the
 // channel-split fill from 2^20 rows on (where the fill's memory traffic dominates the tree).
 // None of the 64-feature fills handles the dominant-bin skip.
+template <int C>
+int set_pkk_attr(size_t lds) {
+    for (const void* k : {(const void*)fill_pkk_kernel<C, false, false>, (const void*)fill_pkk_kernel<C, false, true>,
+                          (const void*)fill_pkk_kernel<C, true, false>, (const void*)fill_pkk_kernel<C, true, true>})
+        HIP_TRY(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    return CBH_OK;
+}
+
+// Packed multi-channel fill plan (K > 1): from 500000 rows (CBH_FILL=packed at any size,
+// CBH_FILL=exact keeps the two-channel fill) when the NP planes of a 32-feature tile fit the
+// per-thread cells (NP * B * 32 <= kPkkCells).
+int plan_pkk(cbh_session* s, const std::string& v) {
+    const uint32_t NP = (s->C + 1) / 2;
+    const bool want = v == "packed" || (v.empty() && s->n >= 500000);
+    if (!want || (uint64_t)NP * s->B * 32u > kPkkCells) return CBH_OK;
+    int lds_max = 0, cus = 0;
+    HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device));
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
+    const size_t lds = (size_t)kPkkCells * sizeof(unsigned long long);
+    if (lds > (size_t)lds_max) return CBH_OK;
+    CHECK(with_k((int)s->K, [&](auto kc) { return set_pkk_attr<decltype(kc)::value + 1>(lds); }));
+    s->pkk_tiles = (s->W + 7) / 8;
+    s->pkk_ranges = pick_ranges((uint32_t)cus, 1u, s->pkk_tiles, s->n);
+    if (const char* e = std::getenv("CBH_PKK_RANGES")) {   // ranges per tile (a measurement knob)
+        const long r = std::strtol(e, nullptr, 10);
+        if (r >= 8 && r <= 256 && r % 8 == 0) s->pkk_ranges = (uint32_t)r;
+    }
+    CHECK(dalloc(&s->spack, (size_t)s->n * NP));
+    s->pack_bits = kPkkBits;
+    s->pkk = true;
+    return CBH_OK;
+}
+
 int plan_fill_mode(cbh_session* s) {
-    s->packed = s->split = false;
+    s->packed = s->split = s->pkk = false;
     const char* e = std::getenv("CBH_FILL");
     const std::string v = e ? e : "";
+    if (s->K > 1 && v != "exact" && v != "split") return plan_pkk(s, v);
     if (v == "exact" || s->use_skip) return CBH_OK;
     // (the packed decode takes non-negative weights: a negative object weight keeps the other fills)
     const bool want_packed = (v == "packed" || (v.empty() && s->n >= (1ull << 20))) && s->K == 1 && !s->pk_signed_w;
@@ -1407,9 +1444,13 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         s->smp_dev, s->jt(), use_host_sample ? s->host_sample : nullptr, s->sstat, newton, s->partials,
         s->ranking ? s->ext_der : nullptr, s->ranking ? s->score_w : nullptr);
     HIP_TRY(hipGetLastError());
-    scales_kernel<<<1, 256, 0, st>>>(s->partials, pgrid, s->bounds, s->scales, s->packed ? s->pack_bits : 0);
+    scales_kernel<<<1, 256, 0, st>>>(s->partials, pgrid, s->bounds, s->scales,
+                                     (s->packed || s->pkk) ? s->pack_bits : 0);
     HIP_TRY(hipGetLastError());
-    if (s->packed)
+    if (s->pkk)
+        quantize_pack_kernel<C><<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack,
+                                                                        (1ll << s->pack_bits) - 1);
+    else if (s->packed)
         pack_stats_fixed_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack,
                                                                          (1ll << s->pack_bits) - 1);
     else if (s->split)
@@ -1463,7 +1504,26 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             fill_split_kernel<true><<<s->pk_ranges * s->pk_tiles * C, 1024, s->pk_lds, st>>>(
                 s->rows, s->Ws, s->W, n, lidx, lplan, (const long long*)s->spack, (const long long*)s->sseq, C,
                 s->pk_tiles, s->F, s->B, s->pk_ranges, cur);
-        else if (s->use_skip)
+        else if (s->pkk) {
+            const size_t lds = (size_t)kPkkCells * sizeof(unsigned long long);
+            const unsigned grid = s->pkk_ranges * s->pkk_tiles;
+            if (s->use_skip && level == 0)
+                fill_pkk_kernel<C, true, false><<<grid, kPkkThreads, lds, st>>>(
+                    s->rows, s->W, s->Ws, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur,
+                    s->skip_bin);
+            else if (s->use_skip)
+                fill_pkk_kernel<C, true, true><<<grid, kPkkThreads, lds, st>>>(
+                    s->rows, s->W, s->Ws, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur,
+                    s->skip_bin);
+            else if (level == 0)
+                fill_pkk_kernel<C, false, false><<<grid, kPkkThreads, lds, st>>>(
+                    s->rows, s->W, s->Ws, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur,
+                    nullptr);
+            else
+                fill_pkk_kernel<C, false, true><<<grid, kPkkThreads, lds, st>>>(
+                    s->rows, s->W, s->Ws, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur,
+                    nullptr);
+        } else if (s->use_skip)
             fill_kernel<C, true><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
                 s->rows, s->W, s->Ws, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
                 s->skip_bin, (int)s->tiles.bin_major);
@@ -1835,7 +1895,8 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
         for (uint64_t i = 0; i < n; ++i) out->leaf_of[i] = lf[i] & 0x7FFFu;
     }
     // traffic accounting of the fill launches (algorithmic bytes per launch)
-    const double wbytes = 4.0 * s->W, sbytes = s->packed ? 8.0 : 8.0 * s->C;   // split: 8 per channel
+    const double wbytes = 4.0 * s->W,
+                 sbytes = s->packed ? 8.0 : s->pkk ? 8.0 * ((s->C + 1) / 2) : 8.0 * s->C;   // split: 8 per channel
     const double per_leaf_bytes = (double)s->F * s->B * s->C * 8.0;
     for (uint32_t l = 0; l < s->depth; ++l) {
         const uint64_t V = l == 0 ? bounds.sampled_rows : plans[l - 1].rows;
@@ -1876,8 +1937,8 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
     if (!s || !out) return fail(CBH_ERR_INVALID_ARG, "null argument");
     *out = s->stats;
     out->skip_features = s->n_skip;
-    out->fill_mode = s->packed ? 1u : s->split ? 2u : 0u;
-    out->fill_pack_bits = s->packed ? s->pack_bits : 0;
+    out->fill_mode = s->packed ? 1u : s->split ? 2u : s->pkk ? 3u : 0u;
+    out->fill_pack_bits = (s->packed || s->pkk) ? s->pack_bits : 0;
     return CBH_OK;
 }
 

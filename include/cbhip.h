@@ -207,8 +207,9 @@ typedef struct {
     double quantize_bytes;        /* algorithmic bytes: 4 read + 1 written per value + borders */
     uint32_t fill_mode;           /* 0: 32-feature tiles, both channels per workgroup; 1: packed 64-feature
                                      tiles (one 64-bit atomic carries both channels); 2: channel-split
-                                     64-feature tiles (one workgroup per channel) */
-    int32_t fill_pack_bits;       /* packed fill: bits of a row's rounded channel value (|q| <= 2^bits) */
+                                     64-feature tiles (one workgroup per channel); 3: packed multi-channel
+                                     32-feature tiles (K > 1: two channels per 64-bit atomic) */
+    int32_t fill_pack_bits;       /* packed fills: bits of a row's rounded channel value (|q| < 2^bits) */
 } cbh_stats;
 
 int cbh_session_stats(const cbh_session* s, cbh_stats* out);
