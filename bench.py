@@ -406,8 +406,9 @@ def main():
                      "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE (copy-calibrated) of the last 120 fill "
                                        "dispatches of this command, profiles/fill_kernel_config2.md"
                                        if _profiled_traffic(args.config, n, F, fill_kernel) else None,
-                     "limiter": "issue of dependent VALU-address / LDS-atomic pairs (LDS pipe and VALU each "
-                                "busy <= 50% of CU cycles, HBM 56% of peak; counters in profiles/)"
+                     "limiter": "LDS atomic instruction rate: one 64-bit ds_add per (row, feature), the LDS pipe "
+                                "issuing 85% (dense level) and 78% (gathered levels) of the conflict-free rate; HBM "
+                                "4.1 / 3.7 TB/s (counters in profiles/fill_kernel_config2.md)"
                                 if fill_kernel == "fill_packed_kernel" else None,
                      "launches": st["fill_launches"],
                      "avg_launch_ms": round(st["fill_ms"] / max(1, st["fill_launches"]), 5),

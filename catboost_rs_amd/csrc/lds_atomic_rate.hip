@@ -1,9 +1,12 @@
 // Measures the LDS atomic-add rate of the GPU for the address patterns that bound the
 // histogram fill: scattered cells (the fill's pattern: every lane a random bin) and
 // contiguous cells (64 lanes on 64 neighbouring cells, the best case), for 64-bit cells
-// (the fill's) and 32-bit cells with and without a returned value.  Two 1024-thread
-// workgroups per CU, 128 KB of LDS each, every address reduced into the array.
-// Prints one line per pattern: "<pattern> <lane-atomics per second>".
+// (the fill's) and 32-bit cells with and without a returned value, and contiguous 64-bit
+// atomics with 16 of every 64 lanes active (an instruction's cost does not shrink with its
+// active lanes: the fills are bound by the wave-level atomic instruction rate).  1024-thread
+// workgroups, 128 KB of LDS each, every address reduced into the array.
+// Prints one line per pattern: "<pattern> <lane-atomics per second>" (the 16-of-64 pattern:
+// instructions per second x 64).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -30,8 +33,9 @@ __device__ __forceinline__ uint32_t mix32(uint32_t x) {
     return x;
 }
 
-// T: cell type (u64 or u32); kRtn: use the returned old value (an atomic with return).
-template <int kScattered, typename T, int kRtn>
+// T: cell type (u64 or u32); kRtn: use the returned old value (an atomic with return);
+// kQuarter: only lanes 0-15 of every wave issue (an instruction with 16 of 64 lanes active).
+template <int kScattered, typename T, int kRtn, int kQuarter = 0>
 __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uint32_t seed) {
     extern __shared__ unsigned long long cells_raw[];
     T* cells = (T*)cells_raw;
@@ -41,7 +45,8 @@ __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uin
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t h = mix32(threadIdx.x * 7919u + blockIdx.x * 104729u + seed);
     T carry = 0;
-    for (int it = 0; it < kIters; ++it) {
+    const bool issue = !(kQuarter && lane >= 16);
+    for (int it = 0; issue && it < kIters; ++it) {
         uint32_t idx;
         if (kScattered) {
             h = mix32(h + (uint32_t)it);
@@ -56,22 +61,24 @@ __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uin
     if (threadIdx.x == 0) out[blockIdx.x] = (unsigned long long)cells[0] + (unsigned long long)carry;
 }
 
-template <int kScattered, typename T, int kRtn>
+template <int kScattered, typename T, int kRtn, int kQuarter = 0>
 int measure(const char* name, int blocks, unsigned long long* d) {
-    CK(hipFuncSetAttribute((const void*)rate_kernel<kScattered, T, kRtn>,
+    CK(hipFuncSetAttribute((const void*)rate_kernel<kScattered, T, kRtn, kQuarter>,
                            hipFuncAttributeMaxDynamicSharedMemorySize, kCells * 8));
-    rate_kernel<kScattered, T, kRtn><<<blocks, 1024, kCells * 8>>>(d, 1u);
+    rate_kernel<kScattered, T, kRtn, kQuarter><<<blocks, 1024, kCells * 8>>>(d, 1u);
     CK(hipGetLastError());
     CK(hipDeviceSynchronize());
     hipEvent_t a, b;
     CK(hipEventCreate(&a));
     CK(hipEventCreate(&b));
     CK(hipEventRecord(a));
-    rate_kernel<kScattered, T, kRtn><<<blocks, 1024, kCells * 8>>>(d, 2u);
+    rate_kernel<kScattered, T, kRtn, kQuarter><<<blocks, 1024, kCells * 8>>>(d, 2u);
     CK(hipEventRecord(b));
     CK(hipEventSynchronize(b));
     float ms = 0.f;
     CK(hipEventElapsedTime(&ms, a, b));
+    // lane-atomics per second; with kQuarter the wave-level instruction rate x 64 (each
+    // instruction counted as if all 64 lanes were active), comparable with the full-lane line
     const double lanes = (double)blocks * 1024.0 * kIters;
     std::printf("%s %.6e\n", name, lanes / (ms * 1e-3));
     return 0;
@@ -89,6 +96,7 @@ int main() {
     if (measure<1, unsigned int, 0>("scattered_u32", blocks, d)) return 1;
     if (measure<1, unsigned int, 1>("scattered_u32_rtn", blocks, d)) return 1;
     if (measure<0, unsigned int, 0>("contiguous_u32", blocks, d)) return 1;
+    if (measure<0, unsigned long long, 0, 1>("contiguous_u64_16of64_lanes", blocks, d)) return 1;
     CK(hipFree(d));
     return 0;
 }

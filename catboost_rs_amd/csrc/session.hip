@@ -135,7 +135,6 @@ struct cbh_session {
     uint32_t* best_bin = nullptr;
     uint32_t* n_cand = nullptr;
     uint32_t max_cand = 0;           // most candidates of any feature (threads of the scorer)
-    uint32_t score_lds = 0;          // dynamic LDS requested by the scorer (caps its workgroups per CU)
     uint8_t* one_hot = nullptr;
     Scales* scales = nullptr;
     Bounds* bounds = nullptr;
@@ -630,10 +629,6 @@ int plan_pkk(cbh_session* s, const std::string& v) {
     CHECK(with_k((int)s->K, [&](auto kc) { return set_pkk_attr<decltype(kc)::value + 1>(lds); }));
     s->pkk_tiles = (s->W + 7) / 8;
     s->pkk_ranges = pick_ranges((uint32_t)cus, 1u, s->pkk_tiles, s->n);
-    if (const char* e = std::getenv("CBH_PKK_RANGES")) {   // ranges per tile (a measurement knob)
-        const long r = std::strtol(e, nullptr, 10);
-        if (r >= 8 && r <= 256 && r % 8 == 0) s->pkk_ranges = (uint32_t)r;
-    }
     CHECK(dalloc(&s->spack, (size_t)s->n * NP));
     s->pack_bits = kPkkBits;
     s->pkk = true;
@@ -1069,11 +1064,6 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
         const bool oh = !s->one_hot_host.empty() && s->one_hot_host[f];
         nc[f] = oh ? folds : (folds > 0 ? folds - 1 : 0);
         s->max_cand = std::max(s->max_cand, nc[f]);
-    }
-    if (const char* e = std::getenv("CBH_SCORE_WG_PER_CU")) {
-        const long v = std::strtol(e, nullptr, 10);
-        if (v >= 1 && v <= 64) s->score_lds = (uint32_t)(160 * 1024 / v) & ~255u;
-        if (s->score_lds > 64 * 1024) s->score_lds = 64 * 1024;
     }
     HIP_TRY(hipMemcpy(s->n_cand, nc.data(), sizeof(uint32_t) * F, hipMemcpyHostToDevice));
     bool any_oh = false;
@@ -1555,7 +1545,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         if (s->pairwise) {
             CHECK(pairwise_level(s, cur, level));
         } else if (s->max_cand <= 64)
-            score_kernel<K, 1><<<s->F, 64, s->score_lds, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
+            score_kernel<K, 1><<<s->F, 64, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin,
                                                    s->ctr_n ? s->fweight : nullptr);
         else if (s->max_cand <= 128)
