@@ -36,6 +36,31 @@ struct LevelPlan {            // written by plan_finalize, read by fill/derive/c
     uint32_t seg_begin[kMaxLeaves / 2];
 };
 
+// Row range g of G over the idx list of a gathered level, balanced by cost rather than rows:
+// position x costs C(x) = x + lambda * s(x), s(x) the segment holding x, so a range pays lambda
+// rows' worth for every segment boundary it crosses (each costs a flush of its LDS tile), and
+// ranges over many small segments get fewer rows.  Range g is [C^-1(g T / G), C^-1((g+1) T / G))
+// with T = V + lambda (n_seg - 1); C^-1 by binary search over the segments.
+__device__ __forceinline__ uint32_t cost_inverse(const LevelPlan* __restrict__ plan, uint32_t n_seg, uint32_t V,
+                                                 uint64_t lambda, uint64_t target) {
+    uint32_t lo = 0, hi = n_seg;   // last s with seg_begin[s] + lambda * s <= target
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) / 2;
+        if ((uint64_t)plan->seg_begin[mid] + lambda * mid <= target) lo = mid;
+        else hi = mid;
+    }
+    const uint64_t seg_end = lo + 1 < n_seg ? plan->seg_begin[lo + 1] : V;
+    const uint64_t x = target - lambda * lo;
+    return (uint32_t)(x < seg_end ? x : seg_end);
+}
+
+__device__ __forceinline__ void balanced_range(const LevelPlan* __restrict__ plan, uint32_t n_seg, uint32_t V,
+                                               uint32_t g, uint32_t G, uint32_t lambda, uint32_t& rb, uint32_t& re) {
+    const uint64_t T = (uint64_t)V + (uint64_t)lambda * (n_seg - 1);
+    rb = g == 0 ? 0u : cost_inverse(plan, n_seg, V, lambda, T * g / G);
+    re = g + 1 == G ? V : cost_inverse(plan, n_seg, V, lambda, T * (g + 1) / G);
+}
+
 // The segment of the idx list that position rb falls in: the last s with seg_begin[s] <= rb
 // (seg_begin is non-decreasing, seg_begin[0] = 0), by binary search -- a few dependent loads of
 // the plan instead of one per segment before rb.
@@ -637,6 +662,7 @@ static_assert(kPackOwn * kPackThreads == kPackCells, "every thread owns kPackOwn
 // doubling of swap_every takes one bit
 constexpr int kPackBitsSwap1 = 20;
 constexpr int kPackHalf = 8;                // passes per half block of a full tile (64 rows each)
+constexpr uint32_t kPackSegmentCost = 2048;  // rows' worth of time a segment's flush costs (ranges)
 
 // Decode a swapped cell: no weight is negative (the session checks), so the weight field is a
 // sum of non-negative values below 2^31 that never borrows from the der field.
@@ -1008,9 +1034,9 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     for (int k = 0; k < kPackOwn; ++k) acc_d[k] = acc_w[k] = 0;
     __syncthreads();
     const uint32_t V = kGather ? plan->rows : (uint32_t)n;
-    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / GR);
-    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / GR);
     const uint32_t n_seg = kGather ? plan->n_parent : 1u;
+    uint32_t rb = (uint32_t)(((uint64_t)V * g) / GR), re = (uint32_t)(((uint64_t)V * (g + 1)) / GR);
+    if (kGather) balanced_range(plan, n_seg, V, g, GR, kPackSegmentCost, rb, re);
     uint32_t seg = 0;
     if (kGather)
         seg = first_segment(plan, n_seg, rb);
@@ -1079,6 +1105,7 @@ constexpr uint32_t kPkkCells = (uint32_t)kPkkOwn * kPkkThreads;        // NP * B
 constexpr uint32_t kPkkBlockRows = kPkkThreads / 8;                   // 128 rows per block
 constexpr uint32_t kPkkSwapBlocks = 8;                                 // 1024 rows per swap period
 constexpr int kPkkBits = 20;                                           // 2048 * (2^20 - 1) < 2^31
+constexpr uint32_t kPkkSegmentCost = 512;   // rows' worth of time a segment's flush costs (ranges)
 static_assert(2ull * kPkkSwapBlocks * kPkkBlockRows * ((1ull << kPkkBits) - 1) < (1ull << 31),
               "packed multi-channel fields stay below 2^31");
 
@@ -1144,9 +1171,9 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
     for (int k = 0; k < kPkkOwn; ++k) acc_lo[k] = acc_hi[k] = 0;
     __syncthreads();
     const uint32_t V = kGather ? plan->rows : (uint32_t)n;
-    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
-    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
     const uint32_t n_seg = kGather ? plan->n_parent : 1u;
+    uint32_t rb = (uint32_t)(((uint64_t)V * g) / G), re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
+    if (kGather) balanced_range(plan, n_seg, V, g, G, kPkkSegmentCost, rb, re);
     uint32_t seg = 0;
     if (kGather)
         seg = first_segment(plan, n_seg, rb);
