@@ -1155,6 +1155,9 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
     const uint32_t f0 = 4u * w0;
     const uint32_t TF = min(4u * TW, F - f0);
     const uint32_t plane = B * 32u;
+    // cells in use: NP planes of B bins x 32 features; a thread's cells past them stay zero, so
+    // the swaps, staging and clears skip them (kc of its kPkkOwn slots)
+    const uint32_t kc = ((uint32_t)NP * plane + kPkkThreads - 1) / kPkkThreads;
     for (uint32_t i = threadIdx.x; i < kPkkCells; i += kPkkThreads) pk[i] = 0ull;
     const uint32_t r0 = threadIdx.x >> 3, wl = threadIdx.x & 7u;   // 128 rows per pass
     const uint32_t rot = (2u * (r0 & 1u) + ((wl >> 2) ^ ((r0 >> 1) & 1u))) & 3u;
@@ -1180,8 +1183,10 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
     auto swap_cells = [&]() {
 #pragma unroll
         for (int k = 0; k < kPkkOwn; ++k) {
-            const unsigned long long v = atomicExch(pk + threadIdx.x + (uint32_t)k * kPkkThreads, 0ull);
-            unpack_add_signed(v, acc_lo[k], acc_hi[k]);
+            if ((uint32_t)k < kc) {
+                const unsigned long long v = atomicExch(pk + threadIdx.x + (uint32_t)k * kPkkThreads, 0ull);
+                unpack_add_signed(v, acc_lo[k], acc_hi[k]);
+            }
         }
     };
     uint32_t pos = rb;
@@ -1264,7 +1269,8 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
                 __syncthreads();
 #pragma unroll
                 for (int k = 0; k < kPkkOwn; ++k)
-                    pk[threadIdx.x + (uint32_t)k * kPkkThreads] = (unsigned long long)(half ? acc_hi[k] : acc_lo[k]);
+                    if ((uint32_t)k < kc)
+                        pk[threadIdx.x + (uint32_t)k * kPkkThreads] = (unsigned long long)(half ? acc_hi[k] : acc_lo[k]);
                 __syncthreads();
                 // a wave takes 8 features x 8 bins of one plane (64-byte runs of bins in the histogram)
                 const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
@@ -1286,7 +1292,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
             __syncthreads();
 #pragma unroll
             for (int k = 0; k < kPkkOwn; ++k) {
-                pk[threadIdx.x + (uint32_t)k * kPkkThreads] = 0ull;
+                if ((uint32_t)k < kc) pk[threadIdx.x + (uint32_t)k * kPkkThreads] = 0ull;
                 acc_lo[k] = acc_hi[k] = 0;
             }
             __syncthreads();
