@@ -425,6 +425,7 @@ static __global__ void quantize_stats_kernel(double* __restrict__ sstat, uint64_
 // Every lane keeps kFillRows rows in flight.
 // ---------------------------------------------------------------------------------
 constexpr int kFillRows = 4;
+constexpr uint32_t kFillSegmentCost = 1024;   // rows' worth of time a segment's flush costs (ranges)
 
 struct FillTiles {       // host-side plan of the feature tiles
     uint32_t n_tiles;
@@ -574,9 +575,9 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
         fl.skip[k] = (kSkip && kb < nf) ? skip_bin[f0 + f] : 256u;
     }
     const uint32_t V = idx ? plan->rows : (uint32_t)n;
-    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
-    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
     const uint32_t n_seg = idx ? plan->n_parent : 1u;
+    uint32_t rb = (uint32_t)(((uint64_t)V * g) / G), re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
+    if (idx) balanced_range(plan, n_seg, V, g, G, kFillSegmentCost, rb, re);
     uint32_t seg = 0;
     if (idx)
         seg = first_segment(plan, n_seg, rb);
