@@ -1732,6 +1732,247 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------------
+// Split scoring with the parents split over waves (many parents, K > 1, <= 64 candidates).
+// The fold of score_fold is, per border, one chain of additions in the order (d, side, p).
+// Here wave j of the workgroup owns parents [j*PW, j*PW + PW) and the chain passes from wave to
+// wave: wave j adds its parents' terms of slab (d, side) to the running (num, den) it takes from
+// LDS and hands them on; wave 0 takes slab (d, side) + 1 from the last wave.  Each wave keeps its
+// parents' weight terms of both sides in registers for every dimension and loads each of its
+// der cells once (the next dimension's while the chain is elsewhere), and computes a slab's
+// terms before its turn comes, so the serial part is only the additions, in exactly the order
+// of score_fold.
+// Hand-off: every wave has an outbox of (num, den) per lane in LDS, read by the next wave
+// (wave 0 reads the last wave's); an empty entry holds an all-ones NaN pattern, which num >= 0
+// and den > 0 never take.  A hop polls its lanes' den in the previous wave's outbox until all are
+// set, reads num (written before den), marks both empty again and writes its own outbox, num
+// first.  An outbox holds one hop at a time: its reader is the only wave that clears it, and its
+// writer's next hop comes after the reader's hop that cleared it (a wave's LDS operations
+// complete in order).
+// ---------------------------------------------------------------------------------
+constexpr uint32_t kChainSpinLimit = 1u << 22;   // bound on a wave's wait for its turn
+
+// A wave-uniform row pointer kept in SGPRs (loads then take a per-lane 32-bit offset), and a
+// wave-uniform cell read through the scalar cache (constant address space): the level's
+// histogram is read-only in the scorer.
+using GlobalI64 = const long long __attribute__((address_space(1)))*;
+using GlobalU8 = const char __attribute__((address_space(1)))*;
+using ConstI64 = const long long __attribute__((address_space(4)))*;
+__device__ __forceinline__ GlobalI64 uniform_ptr(const long long* p) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return (GlobalI64)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ long long uniform_cell(GlobalI64 p) { return *(ConstI64)(uintptr_t)p; }
+__device__ __forceinline__ long long readlane64(long long v, int lane) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)(unsigned long long)v, lane);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((unsigned long long)v >> 32), lane);
+    return (long long)(((unsigned long long)hi << 32) | lo);
+}
+
+constexpr unsigned long long kChainEmpty = ~0ull;
+
+__device__ __forceinline__ void chain_take(unsigned long long* slot, uint32_t lane, double& num, double& den) {
+    // the hop before runs in another wave of this workgroup (or this one), each of which
+    // reaches every hop it owns; the bound only keeps a broken schedule from hanging the GPU.
+    // The poll reads den alone and sleeps between reads (a polling wave would otherwise take
+    // VALU issue from the waves computing terms); num, written before den, is then set too.
+    unsigned long long b = kChainEmpty;
+    for (uint32_t k = 0; k < kChainSpinLimit; ++k) {
+        b = __hip_atomic_load(slot + 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (__all(b != kChainEmpty)) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    const unsigned long long a = __hip_atomic_load(slot + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    num = __longlong_as_double((long long)a);
+    den = __longlong_as_double((long long)b);
+    __hip_atomic_store(slot + lane, kChainEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_store(slot + 64 + lane, kChainEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");   // the clearing is issued before this wave's next slot write
+}
+
+__device__ __forceinline__ void chain_give(unsigned long long* slot, uint32_t lane, double num, double den) {
+    __hip_atomic_store(slot + lane, (unsigned long long)__double_as_longlong(num), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_WORKGROUP);
+    asm volatile("" ::: "memory");   // num is issued before den (the reader polls den)
+    __hip_atomic_store(slot + 64 + lane, (unsigned long long)__double_as_longlong(den), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// One term of the fold (score_fold): s = der sum, w = weight sum of one child.
+__device__ __forceinline__ void score_term(double s, double w, double l2, double& x, double& y) {
+    const double q = s / (w + l2);
+    const double avg = w > 0.0 ? q : 0.0;
+    x = avg * s;
+    y = avg * avg * w;
+}
+
+template <int K, int PW, bool kOneHot>
+__device__ __forceinline__ void score_chain(const long long* __restrict__ hist, uint32_t P, uint32_t F,
+                                            uint32_t B, uint32_t f, double inv_d, double inv_w, double l2,
+                                            unsigned long long* ring /* [waves][2][64] */, double& num,
+                                            double& den) {
+    constexpr int C = K + 1;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const uint32_t bc = min(lane, B - 1);
+    const uint32_t p0 = wv * PW;
+    const uint32_t np = min((uint32_t)PW, P - p0);   // >= 1: nw = ceil(P / PW)
+    // weight sums of both children of every parent of this wave (FALSE side 0, TRUE side 1)
+    double w0[PW], w1[PW];
+#pragma unroll
+    for (int u = 0; u < PW; ++u) {
+        const uint32_t p = p0 + min((uint32_t)u, np - 1);
+        const GlobalI64 hw = uniform_ptr(hist + (((size_t)p * C + K) * F + f) * B);
+        const long long pw = hw[bc], tw = uniform_cell(hw + (B - 1));
+        long long x0, x1;
+        if (kOneHot) {   // the bin itself = prefix[b] - prefix[b-1]; TRUE = the bin
+            long long qw = __shfl_up(pw, 1, 64);
+            if (lane == 0) qw = 0;
+            x1 = pw - qw;
+            x0 = tw - x1;
+        } else {
+            x0 = pw;
+            x1 = tw - pw;
+        }
+        w0[u] = (double)x0 * inv_w;
+        w1[u] = (double)x1 * inv_w;
+    }
+    // a dimension's cells: the prefixes of every parent (one vector load each), and the
+    // totals of all PW parents in one vector load (lane u holds parent u's), read out per
+    // parent with readlane (wave-uniform values)
+    long long pd[PW], tdv;
+    // byte offsets from the row of (parent p0, dimension d): parent p0 + u is u * C * F * B
+    // cells further (the launcher keeps PW of those strides below 2^31 bytes)
+    const uint32_t pstride = (uint32_t)C * F * B * 8u;
+    const uint32_t off_d = bc * 8u;
+    const uint32_t off_t = min(min(lane, (uint32_t)PW - 1), np - 1) * pstride + (B - 1) * 8u;
+    auto load_der = [&](int d) {
+        if (PW <= 8) {   // uniform row bases from one base and the parent stride
+            const GlobalU8 base = (GlobalU8)uniform_ptr(hist + (((size_t)p0 * C + d) * F + f) * B);
+#pragma unroll
+            for (int u = 0; u < PW; ++u) {
+                const GlobalU8 bu =
+                    (GlobalU8)uniform_ptr((const long long*)(base + min((uint32_t)u, np - 1) * pstride));
+                pd[u] = *(GlobalI64)(bu + off_d);
+            }
+            tdv = *(GlobalI64)(base + off_t);
+        } else {         // 16 parents: full row addresses (fewer registers live across the loop)
+#pragma unroll
+            for (int u = 0; u < PW; ++u)
+                pd[u] = uniform_ptr(hist + (((size_t)(p0 + min((uint32_t)u, np - 1)) * C + d) * F + f) * B)[bc];
+            const uint32_t pt = p0 + min(min(lane, (uint32_t)PW - 1), np - 1);
+            tdv = hist[(((size_t)pt * C + d) * F + f) * B + (B - 1)];
+        }
+    };
+    load_der(0);
+    uint32_t hop = wv;   // this wave's hop of slab t is t * nw + wv
+    double x[PW], y[PW];
+    for (int d = 0; d < K; ++d) {
+#pragma unroll
+        for (int side = 0; side < 2; ++side) {
+#pragma unroll
+            for (int u = 0; u < PW; ++u) {
+                long long xd;
+                const long long td = readlane64(tdv, u);
+                if (kOneHot) {
+                    long long qd = __shfl_up(pd[u], 1, 64);
+                    if (lane == 0) qd = 0;
+                    xd = side == 0 ? td - (pd[u] - qd) : pd[u] - qd;
+                } else {
+                    xd = side == 0 ? pd[u] : td - pd[u];
+                }
+                score_term((double)xd * inv_d, side == 0 ? w0[u] : w1[u], l2, x[u], y[u]);
+                // parents past P add exact zeros (num >= +0, den > 0 are unchanged by them):
+                // 16-parent waves select per term (a branch around the selects costs them
+                // registers), 8-parent waves branch, only a last wave with a partial block
+                // having any
+                if (PW > 8 && (uint32_t)u >= np) x[u] = y[u] = 0.0;
+            }
+            if (PW <= 8 && np < (uint32_t)PW) {
+#pragma unroll
+                for (int u = 0; u < PW; ++u)
+                    if ((uint32_t)u >= np) x[u] = y[u] = 0.0;
+            }
+            // the terms are computed here, before the wait for this wave's turn (the compiler
+            // would otherwise sink them past it, into the serial part)
+#pragma unroll
+            for (int u = 0; u < PW; ++u) asm volatile("" ::"v"(x[u]), "v"(y[u]) : "memory");
+            // the next dimension's cells load while the chain is in other waves
+            if (side == 1 && d + 1 < K) load_der(d + 1);
+            // the serial part runs at raised wave priority: its dependent additions would
+            // otherwise share the SIMD's issue with the co-resident wave's term computation
+            __builtin_amdgcn_s_setprio(3);
+            if (hop > 0) chain_take(ring + 128 * (wv == 0 ? nw - 1 : wv - 1), lane, num, den);
+#pragma unroll
+            for (int u = 0; u < PW; ++u) {
+                num += x[u];
+                den += y[u];
+            }
+            chain_give(ring + 128 * wv, lane, num, den);
+            __builtin_amdgcn_s_setprio(0);
+            // nothing of the next slab (whose first use of the prefetched cells waits for
+            // them) is scheduled before the hand-off
+            __builtin_amdgcn_sched_barrier(0);
+            hop += nw;
+        }
+    }
+}
+
+template <int K, int PW>
+__global__ __launch_bounds__(512) void score_chain_kernel(
+    long long* __restrict__ zero_buf, uint32_t zero_leaves, uint32_t HC,   // next level's histogram
+    const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
+    const uint32_t* __restrict__ n_cand, const uint8_t* __restrict__ one_hot,
+    const Scales* __restrict__ sc, double l2, int cosine, double* __restrict__ best_score,
+    uint32_t* __restrict__ best_bin, const double* __restrict__ fweight /* nullable [F] */) {
+    __shared__ unsigned long long ring[8 * 2 * 64];   // outboxes [wave][num, den][lane]
+    const uint32_t f = blockIdx.x;
+    // clear feature f's cells of the next level's histogram [leaf][HC][F][B] (its fill adds)
+    for (uint32_t i = threadIdx.x; i < zero_leaves * HC * B; i += blockDim.x) {
+        const uint32_t lc = i / B, bb = i - lc * B;
+        zero_buf[((size_t)lc * F + f) * B + bb] = 0;
+    }
+    const uint32_t nc = n_cand[f];
+    if (nc == 0) {   // workgroup-uniform: no wave enters the chain
+        if (threadIdx.x == 0) {
+            best_score[f] = -INFINITY;
+            best_bin[f] = 0;
+        }
+        return;
+    }
+    for (uint32_t i = threadIdx.x; i < 8 * 2 * 64; i += blockDim.x) ring[i] = kChainEmpty;
+    __syncthreads();
+    const double inv_d = sc->inv[kScoreDer], inv_w = sc->inv[kScoreW];
+    double num = 0.0;
+    double den = 0.0;
+    den += 1e-100;
+    if (one_hot != nullptr && one_hot[f] != 0)
+        score_chain<K, PW, true>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den);
+    else
+        score_chain<K, PW, false>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den);
+    // the last wave made the last hop: its (num, den) are the full fold
+    if ((threadIdx.x >> 6) != (blockDim.x >> 6) - 1) return;
+    const uint32_t b = threadIdx.x & 63u;
+    double score = cosine ? num / sqrt(den) : num;
+    if (fweight) score = fweight[f] * score;
+    if (b >= nc || score != score) score = -INFINITY;
+    uint32_t bb = b;
+    for (int o = 32; o > 0; o >>= 1) {
+        double os = __shfl_xor(score, o, 64);
+        uint32_t ob = __shfl_xor(bb, o, 64);
+        if (os > score || (os == score && ob < bb)) {
+            score = os;
+            bb = ob;
+        }
+    }
+    if (b == 0) {
+        best_score[f] = score;
+        best_bin[f] = bb;
+    }
+}
+
 // Level argmax over features in enumeration order (floats ascending, then one-hot
 // columns ascending); strict first-wins.  One workgroup of 1024 threads.
 static __global__ __launch_bounds__(1024) void argmax_kernel(const double* __restrict__ best_score,

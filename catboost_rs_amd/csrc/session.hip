@@ -135,6 +135,7 @@ struct cbh_session {
     uint32_t* best_bin = nullptr;
     uint32_t* n_cand = nullptr;
     uint32_t max_cand = 0;           // most candidates of any feature (threads of the scorer)
+    bool score_chain = true;         // parents split over waves for K > 1 (CBH_SCORE_CHAIN=off: one wave)
     uint8_t* one_hot = nullptr;
     Scales* scales = nullptr;
     Bounds* bounds = nullptr;
@@ -1066,6 +1067,7 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
         s->max_cand = std::max(s->max_cand, nc[f]);
     }
     HIP_TRY(hipMemcpy(s->n_cand, nc.data(), sizeof(uint32_t) * F, hipMemcpyHostToDevice));
+    if (const char* e = std::getenv("CBH_SCORE_CHAIN")) s->score_chain = std::string(e) != "off";
     bool any_oh = false;
     for (uint8_t v : s->one_hot_host) any_oh |= v != 0;
     if (any_oh) {
@@ -1542,8 +1544,28 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         // derive above has run)
         long long* zbuf = level + 1 < s->depth ? par : nullptr;
         const uint32_t zleaves = level + 1 < s->depth ? 2u * n_leaves : 0u;
+        // K > 1 with many parents: the parents are split over the (at most 8) waves of a
+        // feature's workgroup, 16 per wave from 64 parents at K >= 3 (registers), else 8; the
+        // fold passes from wave to wave
+        const uint32_t chain_pw = n_leaves >= 64 && K >= 3 ? 16u : 8u;
+        const bool chain = K > 1 && s->score_chain && s->max_cand <= 64 && n_leaves >= 16 &&
+                           n_leaves <= 8 * chain_pw &&
+                           (uint64_t)chain_pw * s->C * s->F * s->B * 8u < (1ull << 31);
         if (s->pairwise) {
             CHECK(pairwise_level(s, cur, level));
+        } else if (chain) {
+            if constexpr (K >= 3) {
+                if (chain_pw == 16)
+                    score_chain_kernel<K, 16><<<s->F, 64 * ((n_leaves + 15) / 16), 0, st>>>(
+                        zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
+                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr);
+            }
+            if constexpr (K > 1) {
+                if (chain_pw == 8)
+                    score_chain_kernel<K, 8><<<s->F, 64 * ((n_leaves + 7) / 8), 0, st>>>(
+                        zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
+                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr);
+            }
         } else if (s->max_cand <= 64)
             score_kernel<K, 1><<<s->F, 64, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin,

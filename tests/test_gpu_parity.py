@@ -394,6 +394,34 @@ def test_one_hot_boosting_matches_oracle(loss, score):
     _close(approx, exp["approx"])
 
 
+def test_one_hot_multiclass_matches_oracle():
+    """MultiClass (K = 3) over float and one-hot columns at depth 6: levels of 16 and 32 leaves
+    are scored with the parents split over waves, for equality and border candidates alike."""
+    bins, one_hot, nb, rf, g = _mixed_case(11, 20_000, 9, [2, 3, 5, 9, 16])
+    z = g.normal(size=bins.shape[1]) + 0.8 * (bins[11] == 2) - 0.6 * (bins[13] == 7) + 0.3 * bins[0] / 40
+    y = np.digitize(z, [-0.3, 0.5]).astype(np.float64)
+    depth, iters, K = 6, 6, 3
+    exp = O.train(bins, nb, y, loss="MultiClass", depth=depth, iterations=iters, learning_rate=0.3,
+                  l2_leaf_reg=2.0, score="Cosine", leaf_method="Newton", bootstrap_type="No",
+                  one_hot=one_hot, approx_dim=K)
+    tr = cb.Trainer(bins, int(rf.max()), y, loss="MultiClass", depth=depth, learning_rate=0.3,
+                    l2_leaf_reg=2.0, score="Cosine", leaf_method="Newton", bootstrap_type="No",
+                    real_folds=rf, one_hot_flags=one_hot, approx_dim=K)
+    try:
+        splits, leaves, kinds = tr.fit(iters, with_one_hot=True)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    assert exp["one_hot"].any() and kinds.any()
+    for t in range(iters):
+        ok, flip = same_partition(bins, splits[t], kinds[t], exp["splits"][t], exp["one_hot"][t])
+        assert ok, f"tree {t}: {splits[t].tolist()} {kinds[t].tolist()} vs " \
+                   f"{exp['splits'][t].tolist()} {exp['one_hot'][t].tolist()}"
+        perm = np.arange(leaves.shape[2]) ^ flip
+        _close(leaves[t][:, perm], exp["leaf_values"][t])
+    _close(approx, exp["approx"])
+
+
 # ----------------------------------------------------------------------------- pair losses
 RANKING = {"PairLogit": (3.0, "Newton"), "PairLogitPairwise": (5.0, "Gradient")}
 
