@@ -1808,9 +1808,10 @@ __device__ __forceinline__ void score_term(double s, double w, double l2, double
     y = avg * avg * w;
 }
 
+// The launcher passes P = PW * (waves of the workgroup): every wave owns a full block.
 template <int K, int PW, bool kOneHot>
-__device__ __forceinline__ void score_chain(const long long* __restrict__ hist, uint32_t P, uint32_t F,
-                                            uint32_t B, uint32_t f, double inv_d, double inv_w, double l2,
+__device__ __forceinline__ void score_chain(const long long* __restrict__ hist, uint32_t F, uint32_t B,
+                                            uint32_t f, double inv_d, double inv_w, double l2,
                                             unsigned long long* ring /* [waves][2][64] */, double& num,
                                             double& den) {
     constexpr int C = K + 1;
@@ -1818,13 +1819,11 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
     const uint32_t bc = min(lane, B - 1);
     const uint32_t p0 = wv * PW;
-    const uint32_t np = min((uint32_t)PW, P - p0);   // >= 1: nw = ceil(P / PW)
     // weight sums of both children of every parent of this wave (FALSE side 0, TRUE side 1)
     double w0[PW], w1[PW];
 #pragma unroll
     for (int u = 0; u < PW; ++u) {
-        const uint32_t p = p0 + min((uint32_t)u, np - 1);
-        const GlobalI64 hw = uniform_ptr(hist + (((size_t)p * C + K) * F + f) * B);
+        const GlobalI64 hw = uniform_ptr(hist + (((size_t)(p0 + u) * C + K) * F + f) * B);
         const long long pw = hw[bc], tw = uniform_cell(hw + (B - 1));
         long long x0, x1;
         if (kOneHot) {   // the bin itself = prefix[b] - prefix[b-1]; TRUE = the bin
@@ -1847,24 +1846,19 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
     // cells further (the launcher keeps PW of those strides below 2^31 bytes)
     const uint32_t pstride = (uint32_t)C * F * B * 8u;
     const uint32_t off_d = bc * 8u;
-    const uint32_t off_t = min(min(lane, (uint32_t)PW - 1), np - 1) * pstride + (B - 1) * 8u;
+    const uint32_t off_t = min(lane, (uint32_t)PW - 1) * pstride + (B - 1) * 8u;
     auto load_der = [&](int d) {
-        if (PW <= 8) {   // uniform row bases from one base and the parent stride
-            const GlobalU8 base = (GlobalU8)uniform_ptr(hist + (((size_t)p0 * C + d) * F + f) * B);
+        const GlobalU8 base = (GlobalU8)uniform_ptr(hist + (((size_t)p0 * C + d) * F + f) * B);
+        if (PW <= 8) {   // uniform row bases from the base and the parent stride
 #pragma unroll
-            for (int u = 0; u < PW; ++u) {
-                const GlobalU8 bu =
-                    (GlobalU8)uniform_ptr((const long long*)(base + min((uint32_t)u, np - 1) * pstride));
-                pd[u] = *(GlobalI64)(bu + off_d);
-            }
-            tdv = *(GlobalI64)(base + off_t);
+            for (int u = 0; u < PW; ++u)
+                pd[u] = *(GlobalI64)((GlobalU8)uniform_ptr((const long long*)(base + u * pstride)) + off_d);
         } else {         // 16 parents: full row addresses (fewer registers live across the loop)
 #pragma unroll
             for (int u = 0; u < PW; ++u)
-                pd[u] = uniform_ptr(hist + (((size_t)(p0 + min((uint32_t)u, np - 1)) * C + d) * F + f) * B)[bc];
-            const uint32_t pt = p0 + min(min(lane, (uint32_t)PW - 1), np - 1);
-            tdv = hist[(((size_t)pt * C + d) * F + f) * B + (B - 1)];
+                pd[u] = uniform_ptr(hist + (((size_t)(p0 + u) * C + d) * F + f) * B)[bc];
         }
+        tdv = *(GlobalI64)(base + off_t);
     };
     load_der(0);
     uint32_t hop = wv;   // this wave's hop of slab t is t * nw + wv
@@ -1884,16 +1878,6 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
                     xd = side == 0 ? pd[u] : td - pd[u];
                 }
                 score_term((double)xd * inv_d, side == 0 ? w0[u] : w1[u], l2, x[u], y[u]);
-                // parents past P add exact zeros (num >= +0, den > 0 are unchanged by them):
-                // 16-parent waves select per term (a branch around the selects costs them
-                // registers), 8-parent waves branch, only a last wave with a partial block
-                // having any
-                if (PW > 8 && (uint32_t)u >= np) x[u] = y[u] = 0.0;
-            }
-            if (PW <= 8 && np < (uint32_t)PW) {
-#pragma unroll
-                for (int u = 0; u < PW; ++u)
-                    if ((uint32_t)u >= np) x[u] = y[u] = 0.0;
             }
             // the terms are computed here, before the wait for this wave's turn (the compiler
             // would otherwise sink them past it, into the serial part)
@@ -1901,9 +1885,6 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
             for (int u = 0; u < PW; ++u) asm volatile("" ::"v"(x[u]), "v"(y[u]) : "memory");
             // the next dimension's cells load while the chain is in other waves
             if (side == 1 && d + 1 < K) load_der(d + 1);
-            // the serial part runs at raised wave priority: its dependent additions would
-            // otherwise share the SIMD's issue with the co-resident wave's term computation
-            __builtin_amdgcn_s_setprio(3);
             if (hop > 0) chain_take(ring + 128 * (wv == 0 ? nw - 1 : wv - 1), lane, num, den);
 #pragma unroll
             for (int u = 0; u < PW; ++u) {
@@ -1911,7 +1892,6 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
                 den += y[u];
             }
             chain_give(ring + 128 * wv, lane, num, den);
-            __builtin_amdgcn_s_setprio(0);
             // nothing of the next slab (whose first use of the prefetched cells waits for
             // them) is scheduled before the hand-off
             __builtin_amdgcn_sched_barrier(0);
@@ -1949,9 +1929,9 @@ __global__ __launch_bounds__(512) void score_chain_kernel(
     double den = 0.0;
     den += 1e-100;
     if (one_hot != nullptr && one_hot[f] != 0)
-        score_chain<K, PW, true>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den);
+        score_chain<K, PW, true>(hist, F, B, f, inv_d, inv_w, l2, ring, num, den);
     else
-        score_chain<K, PW, false>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den);
+        score_chain<K, PW, false>(hist, F, B, f, inv_d, inv_w, l2, ring, num, den);
     // the last wave made the last hop: its (num, den) are the full fold
     if ((threadIdx.x >> 6) != (blockDim.x >> 6) - 1) return;
     const uint32_t b = threadIdx.x & 63u;
