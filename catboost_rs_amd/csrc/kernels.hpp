@@ -1808,10 +1808,12 @@ __device__ __forceinline__ void score_term(double s, double w, double l2, double
     y = avg * avg * w;
 }
 
-// The launcher passes P = PW * (waves of the workgroup): every wave owns a full block.
-template <int K, int PW, bool kOneHot>
-__device__ __forceinline__ void score_chain(const long long* __restrict__ hist, uint32_t F, uint32_t B,
-                                            uint32_t f, double inv_d, double inv_w, double l2,
+// The launcher passes P = PW * (waves of the workgroup), every wave owning a full block, or
+// (kPartial) one wave with P < PW parents: its blocks' parents past P read parent P-1's cells
+// and add exact zeros (num >= +0 and den > 0 are unchanged by them).
+template <int K, int PW, bool kPartial, bool kOneHot>
+__device__ __forceinline__ void score_chain(const long long* __restrict__ hist, uint32_t P, uint32_t F,
+                                            uint32_t B, uint32_t f, double inv_d, double inv_w, double l2,
                                             unsigned long long* ring /* [waves][2][64] */, double& num,
                                             double& den) {
     constexpr int C = K + 1;
@@ -1819,11 +1821,12 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
     const uint32_t bc = min(lane, B - 1);
     const uint32_t p0 = wv * PW;
+    auto pu = [&](uint32_t u) { return kPartial ? min(u, P - 1) : u; };   // block slot -> parent offset
     // weight sums of both children of every parent of this wave (FALSE side 0, TRUE side 1)
     double w0[PW], w1[PW];
 #pragma unroll
     for (int u = 0; u < PW; ++u) {
-        const GlobalI64 hw = uniform_ptr(hist + (((size_t)(p0 + u) * C + K) * F + f) * B);
+        const GlobalI64 hw = uniform_ptr(hist + (((size_t)(p0 + pu(u)) * C + K) * F + f) * B);
         const long long pw = hw[bc], tw = uniform_cell(hw + (B - 1));
         long long x0, x1;
         if (kOneHot) {   // the bin itself = prefix[b] - prefix[b-1]; TRUE = the bin
@@ -1846,17 +1849,17 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
     // cells further (the launcher keeps PW of those strides below 2^31 bytes)
     const uint32_t pstride = (uint32_t)C * F * B * 8u;
     const uint32_t off_d = bc * 8u;
-    const uint32_t off_t = min(lane, (uint32_t)PW - 1) * pstride + (B - 1) * 8u;
+    const uint32_t off_t = pu(min(lane, (uint32_t)PW - 1)) * pstride + (B - 1) * 8u;
     auto load_der = [&](int d) {
         const GlobalU8 base = (GlobalU8)uniform_ptr(hist + (((size_t)p0 * C + d) * F + f) * B);
         if (PW <= 8) {   // uniform row bases from the base and the parent stride
 #pragma unroll
             for (int u = 0; u < PW; ++u)
-                pd[u] = *(GlobalI64)((GlobalU8)uniform_ptr((const long long*)(base + u * pstride)) + off_d);
+                pd[u] = *(GlobalI64)((GlobalU8)uniform_ptr((const long long*)(base + pu(u) * pstride)) + off_d);
         } else {         // 16 parents: full row addresses (fewer registers live across the loop)
 #pragma unroll
             for (int u = 0; u < PW; ++u)
-                pd[u] = uniform_ptr(hist + (((size_t)(p0 + u) * C + d) * F + f) * B)[bc];
+                pd[u] = uniform_ptr(hist + (((size_t)(p0 + pu(u)) * C + d) * F + f) * B)[bc];
         }
         tdv = *(GlobalI64)(base + off_t);
     };
@@ -1879,6 +1882,11 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
                 }
                 score_term((double)xd * inv_d, side == 0 ? w0[u] : w1[u], l2, x[u], y[u]);
             }
+            if (kPartial) {
+#pragma unroll
+                for (int u = 0; u < PW; ++u)
+                    if ((uint32_t)u >= P) x[u] = y[u] = 0.0;
+            }
             // the terms are computed here, before the wait for this wave's turn (the compiler
             // would otherwise sink them past it, into the serial part)
 #pragma unroll
@@ -1900,7 +1908,7 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
     }
 }
 
-template <int K, int PW>
+template <int K, int PW, bool kPartial>
 __global__ __launch_bounds__(512) void score_chain_kernel(
     long long* __restrict__ zero_buf, uint32_t zero_leaves, uint32_t HC,   // next level's histogram
     const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
@@ -1929,9 +1937,9 @@ __global__ __launch_bounds__(512) void score_chain_kernel(
     double den = 0.0;
     den += 1e-100;
     if (one_hot != nullptr && one_hot[f] != 0)
-        score_chain<K, PW, true>(hist, F, B, f, inv_d, inv_w, l2, ring, num, den);
+        score_chain<K, PW, kPartial, true>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den);
     else
-        score_chain<K, PW, false>(hist, F, B, f, inv_d, inv_w, l2, ring, num, den);
+        score_chain<K, PW, kPartial, false>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den);
     // the last wave made the last hop: its (num, den) are the full fold
     if ((threadIdx.x >> 6) != (blockDim.x >> 6) - 1) return;
     const uint32_t b = threadIdx.x & 63u;

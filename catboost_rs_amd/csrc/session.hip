@@ -1544,25 +1544,28 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         // derive above has run)
         long long* zbuf = level + 1 < s->depth ? par : nullptr;
         const uint32_t zleaves = level + 1 < s->depth ? 2u * n_leaves : 0u;
-        // K > 1 with many parents: the parents are split over the (at most 8) waves of a
-        // feature's workgroup, 16 per wave from 64 parents at K >= 3 (registers), else 8; the
-        // fold passes from wave to wave
+        // K > 1: the parents are split over the (at most 8) waves of a feature's workgroup, 16
+        // per wave from 64 parents at K >= 3 (registers), else 8 (fewer than 8: one wave)
         const uint32_t chain_pw = n_leaves >= 64 && K >= 3 ? 16u : 8u;
-        const bool chain = K > 1 && s->score_chain && s->max_cand <= 64 && n_leaves >= 16 &&
-                           n_leaves <= 8 * chain_pw && n_leaves % chain_pw == 0 &&
+        const bool chain = K > 1 && s->score_chain && s->max_cand <= 64 && n_leaves <= 8 * chain_pw &&
+                           (n_leaves < 8 || n_leaves % chain_pw == 0) &&
                            (uint64_t)chain_pw * s->C * s->F * s->B * 8u < (1ull << 31);
         if (s->pairwise) {
             CHECK(pairwise_level(s, cur, level));
         } else if (chain) {
             if constexpr (K >= 3) {
                 if (chain_pw == 16)
-                    score_chain_kernel<K, 16><<<s->F, 64 * (n_leaves / 16), 0, st>>>(
+                    score_chain_kernel<K, 16, false><<<s->F, 64 * (n_leaves / 16), 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
                         cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr);
             }
             if constexpr (K > 1) {
-                if (chain_pw == 8)
-                    score_chain_kernel<K, 8><<<s->F, 64 * (n_leaves / 8), 0, st>>>(
+                if (chain_pw == 8 && n_leaves >= 8)
+                    score_chain_kernel<K, 8, false><<<s->F, 64 * (n_leaves / 8), 0, st>>>(
+                        zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
+                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr);
+                else if (chain_pw == 8)
+                    score_chain_kernel<K, 8, true><<<s->F, 64, 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
                         cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr);
             }
