@@ -202,6 +202,28 @@ def test_boosting_matches_oracle(case):
     _close(approx, exp["approx"])
 
 
+@pytest.mark.parametrize("K", [2, 4])
+def test_multiclass_depth7_matches_oracle(K):
+    """MultiClass at depth 7 (levels of 1 to 64 parents): the level scorer's one-wave variant
+    below 8 parents, 8 parents per wave, and (K >= 3, 64 parents) 16 per wave."""
+    bins, nb, y, w = datagen.random_case(300 + K, 20_000, 23, max_borders=50, K=K)
+    p = dict(loss="MultiClass", score="Cosine", leaf_method="Newton", bootstrap_type="No", approx_dim=K)
+    depth, iters = 7, 4
+    exp = O.train(bins, nb, y, depth=depth, iterations=iters, learning_rate=0.3, l2_leaf_reg=2.0,
+                  weight=w, random_seed=7, **p)
+    tr = cb.Trainer(bins, int(nb.max()) + 1, y, depth=depth, learning_rate=0.3, l2_leaf_reg=2.0, weight=w,
+                    random_seed=7, real_folds=nb + 1, **p)
+    try:
+        splits, leaves = tr.fit(iters)
+        approx = tr.approx()
+    finally:
+        tr.close()
+    for it in range(iters):
+        assert np.array_equal(splits[it], exp["splits"][it]), f"tree {it} splits differ"
+        _close(leaves[it], exp["leaf_values"][it])
+    _close(approx, exp["approx"])
+
+
 @pytest.mark.parametrize("n", [1, 2, 5, 63, 65, 257])
 @pytest.mark.parametrize("F", [1, 3])
 @pytest.mark.parametrize("case", [0, 1, 2, 4])
