@@ -27,7 +27,7 @@ struct SplitRec {
     double score;
 };
 
-struct LevelPlan {            // written by plan_finalize, read by fill/derive/compact
+struct LevelPlan {            // written by compact (block 0), read by fill/derive
     uint32_t pad0;
     uint32_t n_parent;
     uint32_t rows;            // rows visited by the next fill (sum of built segments)
@@ -2015,9 +2015,9 @@ static __global__ __launch_bounds__(1024) void argmax_kernel(const double* __res
 //   split_count: leaf |= pass << level for every row; per-block counts of sampled rows
 //                per new leaf -> cnt[leaf][block]
 //   plan_scan:   per leaf, exclusive scan over blocks (in place) + total
-//   plan_finalize: smaller child per parent (ties -> the TRUE child, tree.rs:1109) and the
-//                segment offsets of the next fill
-//   compact:     rows of the built children written in ascending row order per segment;
+//   compact:     the plan (smaller child per parent, ties -> the TRUE child, tree.rs:1109,
+//                and the segment offsets of the next fill) from the totals, then the rows
+//                of the built children written in ascending row order per segment;
 //                inside a block, ranks come from wave ballots (match on the key bits) and
 //                mbcnt, across waves from per-wave counts in LDS.
 // ---------------------------------------------------------------------------------
@@ -2125,22 +2125,6 @@ static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __rest
     if (threadIdx.x == blockDim.x - 1) totals[blockIdx.x] = sh[threadIdx.x];
 }
 
-static __global__ void plan_finalize_kernel(const uint32_t* __restrict__ totals, uint32_t level,
-                                            LevelPlan* __restrict__ plan) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    const uint32_t n_parent = 1u << level;  // parents of the next level = current leaves
-    uint32_t off = 0;
-    for (uint32_t p = 0; p < n_parent; ++p) {
-        const uint32_t nf = totals[p], nt = totals[p + n_parent];
-        const bool true_smaller = nt <= nf;
-        plan->built[p] = true_smaller ? p + n_parent : p;
-        plan->seg_begin[p] = off;
-        off += true_smaller ? nt : nf;
-    }
-    plan->n_parent = n_parent;
-    plan->rows = off;
-}
-
 // Stable compaction of the rows of every directly built child into idx (grouped by parent in
 // plan order, object order inside each group).  Each wave walks its own rows with per-leaf
 // running offsets in its LDS slice (seeded from the scanned per-wave counts), so the loop
@@ -2149,20 +2133,64 @@ static __global__ void plan_finalize_kernel(const uint32_t* __restrict__ totals,
 // With sp_out given, the score words of every listed row are written beside its index
 // (sp_out[c][k] = sp_in[c][idx[k]] for the sp_ch planes of n words), so the next fill reads the
 // statistics of its rows in order instead of gathering them.
+// The level's plan (the smaller child of every parent, ties to the TRUE child, tree.rs:1109, and
+// the segment offsets of the next fill) comes from the children's totals: every block derives it
+// (at most 128 parents, one wave) and block 0 stores it for the kernels after.
 static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __restrict__ leaf, uint64_t n,
                                                       uint32_t level, const uint32_t* __restrict__ cnt,
-                                                      uint32_t n_waves, const LevelPlan* __restrict__ plan,
+                                                      uint32_t n_waves, const uint32_t* __restrict__ totals,
+                                                      LevelPlan* __restrict__ plan,
                                                       uint32_t* __restrict__ idx,
                                                       const unsigned long long* __restrict__ sp_in,
                                                       unsigned long long* __restrict__ sp_out, uint32_t sp_ch) {
     __shared__ uint32_t run[4][kMaxLeaves / 2];
     __shared__ uint32_t built[kMaxLeaves / 2];
+    __shared__ uint32_t segb[kMaxLeaves / 2];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t n_parent = 1u << level;
     const uint64_t wid = (uint64_t)blockIdx.x * 4 + wave;
-    for (uint32_t p = threadIdx.x; p < n_parent; p += blockDim.x) built[p] = plan->built[p];
+    static_assert(kMaxLeaves / 2 <= 128, "two parents per lane of one wave");
+    if (wave == 0) {
+        uint32_t sz[2], inc[2];
+#pragma unroll
+        for (uint32_t q = 0; q < 2; ++q) {
+            const uint32_t p = lane + 64u * q;
+            sz[q] = 0;
+            if (p < n_parent) {
+                const uint32_t nf = totals[p], nt = totals[p + n_parent];
+                const bool true_smaller = nt <= nf;
+                built[p] = true_smaller ? p + n_parent : p;
+                sz[q] = true_smaller ? nt : nf;
+            }
+            inc[q] = sz[q];
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t u = __shfl_up(inc[q], o, 64);
+                if (lane >= (uint32_t)o) inc[q] += u;
+            }
+        }
+        const uint32_t tot0 = __shfl(inc[0], 63, 64), tot1 = __shfl(inc[1], 63, 64);
+        const uint32_t b0 = inc[0] - sz[0], b1 = tot0 + inc[1] - sz[1];
+        if (lane < n_parent) segb[lane] = b0;
+        if (lane + 64u < n_parent) segb[lane + 64u] = b1;
+        if (blockIdx.x == 0) {
+            if (lane < n_parent) {
+                plan->built[lane] = built[lane];
+                plan->seg_begin[lane] = b0;
+            }
+            if (lane + 64u < n_parent) {
+                plan->built[lane + 64u] = built[lane + 64u];
+                plan->seg_begin[lane + 64u] = b1;
+            }
+            if (lane == 0) {
+                plan->n_parent = n_parent;
+                plan->rows = tot0 + tot1;
+            }
+        }
+    }
+    __syncthreads();
     for (uint32_t p = lane; p < n_parent; p += 64)
-        run[wave][p] = plan->seg_begin[p] + cnt[(size_t)plan->built[p] * n_waves + wid];
+        run[wave][p] = segb[p] + cnt[(size_t)built[p] * n_waves + wid];
     __syncthreads();
     const uint64_t beg = wid * kPartWaveRows;
     const uint64_t end = min(beg + kPartWaveRows, n);

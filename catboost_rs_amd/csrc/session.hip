@@ -1596,9 +1596,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         if (!last) {
             plan_scan_kernel<<<2u << level, 1024, 0, st>>>(s->cnt, 4 * NB, s->totals);
             HIP_TRY(hipGetLastError());
-            plan_finalize_kernel<<<1, 64, 0, st>>>(s->totals, level, s->plans + level);
-            HIP_TRY(hipGetLastError());
-            compact_kernel<<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->plans + level, s->idx,
+            compact_kernel<<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->totals, s->plans + level, s->idx,
                                                (s->packed || s->split) ? s->spack : nullptr,
                                                (s->packed || s->split) ? s->sseq : nullptr, s->split ? C : 1u);
             HIP_TRY(hipGetLastError());
