@@ -35,6 +35,9 @@ __device__ __forceinline__ uint32_t mix32(uint32_t x) {
 
 // T: cell type (u64 or u32); kRtn: use the returned old value (an atomic with return);
 // kQuarter: only lanes 0-15 of every wave issue (an instruction with 16 of 64 lanes active).
+// kScattered 2 (u64): the 16 lanes of each DPP row hit 16 distinct bank pairs, and the four DPP
+// rows the same 16 pairs at other addresses (cells (l & 15) + 32 (l >> 4) + 128 it), which
+// shows whether an instruction's conflicts count within 16 or within 32 lanes.
 template <int kScattered, typename T, int kRtn, int kQuarter = 0>
 __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uint32_t seed) {
     extern __shared__ unsigned long long cells_raw[];
@@ -48,7 +51,9 @@ __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uin
     const bool issue = !(kQuarter && lane >= 16);
     for (int it = 0; issue && it < kIters; ++it) {
         uint32_t idx;
-        if (kScattered) {
+        if (kScattered == 2) {
+            idx = ((lane & 15u) + 32u * (lane >> 4) + 128u * (uint32_t)it) % n_cells;
+        } else if (kScattered) {
             h = mix32(h + (uint32_t)it);
             idx = h % n_cells;
         } else {
@@ -97,6 +102,7 @@ int main() {
     if (measure<1, unsigned int, 1>("scattered_u32_rtn", blocks, d)) return 1;
     if (measure<0, unsigned int, 0>("contiguous_u32", blocks, d)) return 1;
     if (measure<0, unsigned long long, 0, 1>("contiguous_u64_16of64_lanes", blocks, d)) return 1;
+    if (measure<2, unsigned long long, 0>("dpp_rows_same_pairs_u64", blocks, d)) return 1;
     CK(hipFree(d));
     return 0;
 }
