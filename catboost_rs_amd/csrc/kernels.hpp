@@ -1304,6 +1304,222 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
 }
 
 // ---------------------------------------------------------------------------------
+// Packed multi-channel fill over sparse entries (sessions whose features mostly sit in their
+// dominant bin).  An instruction of 64-bit LDS atomics costs the same whatever lanes are active,
+// and its bank conflicts count within each 16-lane DPP row only (a DPP row whose lanes hit
+// distinct bank pairs runs at the full rate whatever the other rows hit).  So a DPP row takes
+// one row of a 32-feature tile and lane e its e-th non-dominant (feature, bin) entry, in feature
+// order: distinct features, i.e. distinct bank pairs of the [plane][bin][32] cells, and about
+// twice the active lanes of the dense fill's 8-lanes-per-row visit when 30% of the entries are
+// non-dominant.  The entries are built once per session (pack_sparse_kernel): per (tile, row)
+// 16 codes in slots A and the rest (a row with more than 16 entries in a tile) in slots B, a
+// code being the entry's byte offset in a plane, bin * 256 + 8 * feature, bit 0 of A's last
+// code flagging the overflow, 0xFFFF an empty lane.  Statistics, swaps, flushes and the cells'
+// bound are the packed multi-channel fill's (64 rows per block, swaps every 16 blocks: at most
+// 2048 rows between two swaps of a cell).
+// ---------------------------------------------------------------------------------
+// sv[j] = lane j's v in every lane of its DPP row (row_newbcast), j < NP
+template <int NP, int J = 0>
+__device__ __forceinline__ void bcast_planes(unsigned long long v, unsigned long long* sv) {
+    if constexpr (J < NP) {
+        sv[J] = row_bcast64<J>(v);
+        bcast_planes<NP, J + 1>(v, sv);
+    }
+}
+
+constexpr uint32_t kPksBlockRows = kPkkThreads / 16;   // 64 rows per block
+constexpr uint32_t kPksSwapBlocks = 16;                // 1024 rows per swap period
+constexpr uint16_t kPksEmpty = 0xFFFFu;
+static_assert(2ull * kPksSwapBlocks * kPksBlockRows * ((1ull << kPkkBits) - 1) < (1ull << 31),
+              "packed multi-channel fields stay below 2^31");
+
+// Entries of every (tile, row): thread per (tile, row), rows consecutive (coalesced column reads).
+static __global__ __launch_bounds__(256) void pack_sparse_kernel(const uint8_t* __restrict__ cols /* [F][n] */,
+                                                                 uint64_t n, uint32_t F, uint32_t n_tiles,
+                                                                 const uint32_t* __restrict__ skip_bin,
+                                                                 uint16_t* __restrict__ A, uint16_t* __restrict__ Bo) {
+    for (uint64_t q = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; q < (uint64_t)n_tiles * n;
+         q += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t t = (uint32_t)(q / n);
+        const uint64_t i = q - (uint64_t)t * n;
+        uint16_t* a = A + q * 16;
+        uint16_t* bo = Bo + q * 16;
+        for (uint32_t k = 0; k < 16; ++k) {
+            a[k] = kPksEmpty;
+            bo[k] = kPksEmpty;
+        }
+        uint32_t cnt = 0;
+        uint16_t last_a = kPksEmpty;
+        for (uint32_t fl = 0; fl < 32; ++fl) {
+            const uint32_t f = 32u * t + fl;
+            if (f >= F) break;
+            const uint32_t bin = cols[(size_t)f * n + i];
+            if (bin == skip_bin[f]) continue;
+            const uint16_t code = (uint16_t)((bin << 8) | (fl << 3));
+            if (cnt < 16) a[cnt] = code;
+            else bo[cnt - 16] = code;
+            if (cnt == 15) last_a = code;
+            ++cnt;
+        }
+        if (cnt > 16) a[15] = (uint16_t)(last_a | 1u);
+    }
+}
+
+template <int C, bool kGather>
+static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bo /* [n_tiles][n][16] each */, uint64_t n,
+    const uint32_t* __restrict__ idx, const LevelPlan* __restrict__ plan,
+    const unsigned long long* __restrict__ spk /* [n][NP] */, uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G,
+    long long* __restrict__ hist) {
+    constexpr int NP = (C + 1) / 2;
+    extern __shared__ unsigned long long pk[];   // [NP][B][32], kPkkCells cells
+    const uint32_t b = blockIdx.x;
+    const uint32_t xcd = b & 7u, q = b >> 3;
+    const uint32_t t = q % n_tiles;
+    const uint32_t g = (q / n_tiles) * 8u + xcd;   // row range (ranges of a tile spread over the XCDs)
+    const uint32_t f0 = 32u * t;
+    const uint32_t TF = min(32u, F - f0);
+    const uint32_t plane = B * 32u;
+    const uint32_t kc = ((uint32_t)NP * plane + kPkkThreads - 1) / kPkkThreads;
+    for (uint32_t i = threadIdx.x; i < kPkkCells; i += kPkkThreads) pk[i] = 0ull;
+    const uint32_t r0 = threadIdx.x >> 4, e = threadIdx.x & 15u;   // 64 rows per pass, lane e: entry e
+    const uint16_t* At = A + (size_t)t * n * 16 + e;
+    const uint16_t* Bt = Bo + (size_t)t * n * 16 + e;
+    long long acc_lo[kPkkOwn], acc_hi[kPkkOwn];
+#pragma unroll
+    for (int k = 0; k < kPkkOwn; ++k) acc_lo[k] = acc_hi[k] = 0;
+    __syncthreads();
+    const uint32_t V = kGather ? plan->rows : (uint32_t)n;
+    const uint32_t n_seg = kGather ? plan->n_parent : 1u;
+    uint32_t rb = (uint32_t)(((uint64_t)V * g) / G), re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
+    if (kGather) balanced_range(plan, n_seg, V, g, G, kPkkSegmentCost, rb, re);
+    uint32_t seg = 0;
+    if (kGather)
+        seg = first_segment(plan, n_seg, rb);
+    auto swap_cells = [&]() {
+#pragma unroll
+        for (int k = 0; k < kPkkOwn; ++k) {
+            if ((uint32_t)k < kc) {
+                const unsigned long long v = atomicExch(pk + threadIdx.x + (uint32_t)k * kPkkThreads, 0ull);
+                unpack_add_signed(v, acc_lo[k], acc_hi[k]);
+            }
+        }
+    };
+    uint32_t pos = rb;
+    while (pos < re) {
+        const uint32_t seg_lo = kGather ? plan->seg_begin[seg] : 0u;
+        const uint32_t seg_end = (kGather && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
+        const uint32_t end = min(re, seg_end);
+        const uint32_t slot = kGather ? plan->built[seg] : 0u;
+        if (end > pos) {
+            // blocks of 64 rows (one per DPP row), two register sets in flight as in the dense
+            // multi-channel fill; lane j < NP of a DPP row loads plane j of the row's statistics
+            // (one load instruction for all planes; lane j broadcasts plane j at use)
+            struct Set {
+                uint32_t code, doc;
+                unsigned long long st;
+            } SA, SB;
+            auto ldix = [&](uint32_t bb) -> uint32_t {
+                const uint32_t p = bb + r0;
+                return kGather ? idx[p < end ? p : pos] : (p < end ? p : pos);
+            };
+            auto load_set = [&](Set& S, uint32_t bb, uint32_t doc) {
+                const bool ok = bb + r0 < end;
+                S.doc = doc;
+                const uint32_t c = At[(size_t)doc * 16];
+                S.code = ok ? c : (uint32_t)kPksEmpty;
+                const unsigned long long v = spk[(size_t)doc * NP + (e < (uint32_t)NP ? e : 0u)];
+                S.st = ok ? v : 0ull;
+            };
+            auto atoms = [&](const Set& S) {
+                unsigned long long sv[NP];
+                bcast_planes<NP>(S.st, sv);
+                // a row with more than 16 entries flags A's last code: its DPP row reads B too
+                const uint32_t over = row_bcast<15>(S.code != kPksEmpty ? (S.code & 1u) : 0u);
+                if (S.code != kPksEmpty) {
+                    unsigned long long* cell = (unsigned long long*)((char*)pk + (S.code & ~7u));
+#pragma unroll
+                    for (int j = 0; j < NP; ++j) atomicAdd(cell + (size_t)j * plane, sv[j]);
+                }
+                if (__any(over != 0u)) {   // rare: wave-uniform branch
+                    const uint32_t c2 = over ? (uint32_t)Bt[(size_t)S.doc * 16] : (uint32_t)kPksEmpty;
+                    if (c2 != kPksEmpty) {
+                        unsigned long long* cell = (unsigned long long*)((char*)pk + (c2 & ~7u));
+#pragma unroll
+                        for (int j = 0; j < NP; ++j) atomicAdd(cell + (size_t)j * plane, sv[j]);
+                    }
+                }
+            };
+            uint32_t blk = 0;
+            auto after_block = [&](uint32_t bb) {   // swap at the end of a period and of the segment
+                if (++blk >= kPksSwapBlocks || bb + kPksBlockRows >= end) {
+                    blk = 0;
+                    __syncthreads();
+                    swap_cells();
+                }
+            };
+            uint32_t ixA = ldix(pos), ixB = ldix(pos + kPksBlockRows);
+            load_set(SA, pos, ixA);
+            asm volatile("" ::: "memory");
+            load_set(SB, pos + kPksBlockRows, ixB);
+            asm volatile("" ::: "memory");
+            if (kGather) {
+                ixA = ldix(pos + 2 * kPksBlockRows);
+                ixB = ldix(pos + 3 * kPksBlockRows);
+            }
+            asm volatile("" ::: "memory");
+            for (uint32_t bb = pos;; bb += 2 * kPksBlockRows) {   // workgroup-uniform
+                atoms(SA);
+                load_set(SA, bb + 2 * kPksBlockRows, kGather ? ixA : ldix(bb + 2 * kPksBlockRows));
+                if (kGather) ixA = ldix(bb + 4 * kPksBlockRows);
+                after_block(bb);
+                if (bb + kPksBlockRows >= end) break;
+                atoms(SB);
+                load_set(SB, bb + 3 * kPksBlockRows, kGather ? ixB : ldix(bb + 3 * kPksBlockRows));
+                if (kGather) ixB = ldix(bb + 5 * kPksBlockRows);
+                after_block(bb + kPksBlockRows);
+                if (bb + 2 * kPksBlockRows >= end) break;
+            }
+            // flush: as the dense multi-channel fill's (same cells, same ownership rule)
+            const bool owned = pos == seg_lo && end == seg_end;
+            long long* hd = hist + (size_t)slot * C * F * B;
+            for (int half = 0; half < 2; ++half) {
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < kPkkOwn; ++k)
+                    if ((uint32_t)k < kc)
+                        pk[threadIdx.x + (uint32_t)k * kPkkThreads] = (unsigned long long)(half ? acc_hi[k] : acc_lo[k]);
+                __syncthreads();
+                const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
+                const uint32_t vcells = (uint32_t)NP * nfb * nbb * 64;
+                for (uint32_t i = threadIdx.x; i < vcells; i += kPkkThreads) {
+                    const uint32_t l = i & 63u, jj = i >> 6;
+                    const uint32_t j = jj / (nfb * nbb), jb = jj - j * (nfb * nbb);
+                    const uint32_t f = (jb / nbb) * 8 + (l >> 3), bin = (jb % nbb) * 8 + (l & 7u);
+                    const uint32_t ch = 2u * j + (uint32_t)half;
+                    if (f >= TF || bin >= B || ch >= (uint32_t)C) continue;
+                    const unsigned long long v = pk[j * plane + bin * 32u + f];
+                    unsigned long long* d = (unsigned long long*)hd + (((size_t)ch * F + f0 + f) * B + bin);
+                    if (v != 0) {
+                        if (owned) *d = v;
+                        else atomicAdd(d, v);
+                    }
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kPkkOwn; ++k) {
+                if ((uint32_t)k < kc) pk[threadIdx.x + (uint32_t)k * kPkkThreads] = 0ull;
+                acc_lo[k] = acc_hi[k] = 0;
+            }
+            __syncthreads();
+        }
+        pos = end;
+        ++seg;
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // Channel-split fill (exact int64, any K).  One workgroup = (64-feature tile, channel, row
 // range): its LDS holds one channel of the tile, [bin][64] int64 (130 KB at 255 bins), and it
 // adds one 64-bit atomic per (row, feature) -- no packing, no periodic drains, no barrier

@@ -186,6 +186,10 @@ struct cbh_session {
     long long* seg_tot = nullptr;    // [kMaxLeaves / 2][C] channel totals per built segment
     bool use_skip = false;
     uint64_t n_skip = 0;
+    double nd_per_tile = 32.0;       // mean non-dominant (feature, bin) entries of a row per 32-feature tile
+    bool pks = false;                // packed multi-channel fill over sparse entries
+    uint16_t* pks_a = nullptr;       // [pkk_tiles][n][16] entry codes 0..15 of every (tile, row)
+    uint16_t* pks_b = nullptr;       // [pkk_tiles][n][16] entry codes 16..31
 
     // 64-feature-tile fills: packed (K == 1: both score channels in one 64-bit word per row,
     // one LDS atomic per (row, feature)) or channel-split (exact int64, one workgroup per
@@ -272,7 +276,7 @@ struct cbh_session {
         dfree(partials);
         dfree(group_off); dfree(los_off); dfree(los_idx); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st);
-        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows);
+        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows); dfree(pks_a); dfree(pks_b);
         dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_ws);
         dfree(pair_desc); dfree(pair_mk); dfree(pair_nd);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
@@ -610,7 +614,8 @@ int plan_tiles(cbh_session* s) {
 template <int C>
 int set_pkk_attr(size_t lds) {
     for (const void* k : {(const void*)fill_pkk_kernel<C, false, false>, (const void*)fill_pkk_kernel<C, false, true>,
-                          (const void*)fill_pkk_kernel<C, true, false>, (const void*)fill_pkk_kernel<C, true, true>})
+                          (const void*)fill_pkk_kernel<C, true, false>, (const void*)fill_pkk_kernel<C, true, true>,
+                          (const void*)fill_pks_kernel<C, false>, (const void*)fill_pks_kernel<C, true>})
         HIP_TRY(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     return CBH_OK;
 }
@@ -633,6 +638,22 @@ int plan_pkk(cbh_session* s, const std::string& v) {
     CHECK(dalloc(&s->spack, (size_t)s->n * NP));
     s->pack_bits = kPkkBits;
     s->pkk = true;
+    // sparse entries when the dominant-bin skip leaves at most 12 of a tile's 32 entries per row
+    // on average (a DPP row of 16 lanes per row then carries about twice the active lanes of the
+    // dense visit); CBH_PKK_SPARSE=off keeps the dense visit, =on takes the entries whatever
+    // their count (measurement and test knobs)
+    const char* se = std::getenv("CBH_PKK_SPARSE");
+    const std::string sv = se ? se : "";
+    if (s->use_skip && sv != "off" && (sv == "on" || s->nd_per_tile <= 12.0)) {
+        const size_t slots = (size_t)s->pkk_tiles * s->n * 16;
+        CHECK(dalloc(&s->pks_a, slots));
+        CHECK(dalloc(&s->pks_b, slots));
+        pack_sparse_kernel<<<grid_for((uint64_t)s->pkk_tiles * s->n, 256), 256, 0, s->stream>>>(
+            s->cols, s->n, s->F, s->pkk_tiles, s->skip_bin, s->pks_a, s->pks_b);
+        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess)
+            return fail(CBH_ERR_DEVICE, "sparse entry packing failed");
+        s->pks = true;
+    }
     return CBH_OK;
 }
 
@@ -744,6 +765,12 @@ int plan_skip_bins(cbh_session* s) {
     s->use_skip = any;
     s->n_skip = 0;
     for (uint32_t v : skip) s->n_skip += v < 256u;
+    {   // mean entries a row keeps per 32-feature tile once dominant bins are left out
+        double kept = 0.0;
+        for (uint32_t f = 0; f < s->F; ++f)
+            kept += skip[f] < 256u ? 1.0 - (double)h[(size_t)f * 256 + skip[f]] / (double)s->n : 1.0;
+        s->nd_per_tile = kept / (double)((s->F + 31) / 32);
+    }
     if (!any) return CBH_OK;
     CHECK(dalloc(&s->skip_bin, s->F));
     CHECK(dalloc(&s->seg_tot, (size_t)(kMaxLeaves / 2) * s->C));
@@ -1499,7 +1526,13 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         else if (s->pkk) {
             const size_t lds = (size_t)kPkkCells * sizeof(unsigned long long);
             const unsigned grid = s->pkk_ranges * s->pkk_tiles;
-            if (s->use_skip && level == 0)
+            if (s->pks && level == 0)
+                fill_pks_kernel<C, false><<<grid, kPkkThreads, lds, st>>>(
+                    s->pks_a, s->pks_b, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur);
+            else if (s->pks)
+                fill_pks_kernel<C, true><<<grid, kPkkThreads, lds, st>>>(
+                    s->pks_a, s->pks_b, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur);
+            else if (s->use_skip && level == 0)
                 fill_pkk_kernel<C, true, false><<<grid, kPkkThreads, lds, st>>>(
                     s->rows, s->W, s->Ws, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur,
                     s->skip_bin);

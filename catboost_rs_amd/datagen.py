@@ -238,17 +238,17 @@ def config4(n_rows=2_000_000, n_float=30, n_cat=20, seed=4):
                             ctr=("Borders", 0.5), ctr_border_count=15))
 
 
-def config5(scale=1.0, seed=5, n_rows=None, n_features=4096, n_classes=10):
+def config5(scale=1.0, seed=5, n_rows=None, n_features=4096, n_classes=10, zero_frac=0.7):
     """MultiClass K=10: n x 4096 sparse-ish (70% exact zeros, else N(0,1)); 64 borders;
     depth 8, 50 iterations, Newton leaves, no bootstrap.  Labels: argmax of 10 noisy
-    linear scores of the first 32 features."""
+    linear scores of the first 32 features.  (zero_frac: the share of exact zeros, for tests.)"""
     n = int(n_rows if n_rows is not None else 1_000_000 * scale)
     F = n_features
 
     def make_col(f):
         g = np.random.default_rng([seed, f])
         c = g.standard_normal(n, dtype=np.float32)
-        c[g.random(n) < 0.7] = 0.0
+        c[g.random(n) < zero_frac] = 0.0
         return c
 
     bins, nb, cols = _columns(n, F, make_col, 64, seed, keep_cols=range(32))

@@ -681,6 +681,17 @@ def test_config3_reduced_matches_oracle(loss, fill, monkeypatch):
     _assert_same_fit(*_fit_both(d, 5))
 
 
+@pytest.mark.parametrize("zeros,sparse", [(0.7, "auto"), (0.7, "off"), (0.45, "on")])
+def test_multiclass_packed_fill_entries_match_oracle(zeros, sparse, monkeypatch):
+    """The packed multi-channel fill forced on config 5's shape at 20k x 256: over sparse
+    entries (a row per 16-lane DPP row; at 45% zeros a row holds about 18 of a tile's 32 entries,
+    so most rows also read their second slots) and over the dense visit."""
+    monkeypatch.setenv("CBH_FILL", "packed")
+    monkeypatch.setenv("CBH_PKK_SPARSE", sparse)
+    d = datagen.config5(n_rows=20_000, n_features=256, zero_frac=zeros)
+    _assert_same_fit(*_fit_both(d, 3))
+
+
 def test_config5_shape_matches_oracle():
     """Config 5 shape (MultiClass K=10, depth 8, 70%-zero columns, 64 borders) at 20k x 256."""
     d = datagen.config5(n_rows=20_000, n_features=256)
