@@ -1412,13 +1412,13 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = kGather ? plan->built[seg] : 0u;
         if (end > pos) {
-            // blocks of 64 rows (one per DPP row), two register sets in flight as in the dense
-            // multi-channel fill; lane j < NP of a DPP row loads plane j of the row's statistics
+            // blocks of 64 rows (one per DPP row); lane j < NP of a DPP row loads plane j of the
+            // row's statistics
             // (one load instruction for all planes; lane j broadcasts plane j at use)
             struct Set {
                 uint32_t code, doc;
                 unsigned long long st;
-            } SA, SB;
+            };
             auto ldix = [&](uint32_t bb) -> uint32_t {
                 const uint32_t p = bb + r0;
                 return kGather ? idx[p < end ? p : pos] : (p < end ? p : pos);
@@ -1458,27 +1458,41 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
                     swap_cells();
                 }
             };
-            uint32_t ixA = ldix(pos), ixB = ldix(pos + kPksBlockRows);
-            load_set(SA, pos, ixA);
+            // four sets in flight (a block's atomics are few: the loads need four blocks' time),
+            // gathered row indices four blocks ahead of their set's loads
+            constexpr uint32_t R = kPksBlockRows;
+            Set S0, S1, S2, S3;
+            uint32_t ix0 = ldix(pos), ix1 = ldix(pos + R), ix2 = ldix(pos + 2 * R), ix3 = ldix(pos + 3 * R);
+            load_set(S0, pos, ix0);
             asm volatile("" ::: "memory");
-            load_set(SB, pos + kPksBlockRows, ixB);
+            load_set(S1, pos + R, ix1);
+            asm volatile("" ::: "memory");
+            load_set(S2, pos + 2 * R, ix2);
+            asm volatile("" ::: "memory");
+            load_set(S3, pos + 3 * R, ix3);
             asm volatile("" ::: "memory");
             if (kGather) {
-                ixA = ldix(pos + 2 * kPksBlockRows);
-                ixB = ldix(pos + 3 * kPksBlockRows);
+                ix0 = ldix(pos + 4 * R);
+                ix1 = ldix(pos + 5 * R);
+                ix2 = ldix(pos + 6 * R);
+                ix3 = ldix(pos + 7 * R);
             }
             asm volatile("" ::: "memory");
-            for (uint32_t bb = pos;; bb += 2 * kPksBlockRows) {   // workgroup-uniform
-                atoms(SA);
-                load_set(SA, bb + 2 * kPksBlockRows, kGather ? ixA : ldix(bb + 2 * kPksBlockRows));
-                if (kGather) ixA = ldix(bb + 4 * kPksBlockRows);
+            auto step = [&](Set& S, uint32_t& ix, uint32_t bb) {   // block bb: atomics, reload for bb + 4R
+                atoms(S);
+                load_set(S, bb + 4 * R, kGather ? ix : ldix(bb + 4 * R));
+                if (kGather) ix = ldix(bb + 8 * R);
                 after_block(bb);
-                if (bb + kPksBlockRows >= end) break;
-                atoms(SB);
-                load_set(SB, bb + 3 * kPksBlockRows, kGather ? ixB : ldix(bb + 3 * kPksBlockRows));
-                if (kGather) ixB = ldix(bb + 5 * kPksBlockRows);
-                after_block(bb + kPksBlockRows);
-                if (bb + 2 * kPksBlockRows >= end) break;
+            };
+            for (uint32_t bb = pos;; bb += 4 * R) {   // workgroup-uniform
+                step(S0, ix0, bb);
+                if (bb + R >= end) break;
+                step(S1, ix1, bb + R);
+                if (bb + 2 * R >= end) break;
+                step(S2, ix2, bb + 2 * R);
+                if (bb + 3 * R >= end) break;
+                step(S3, ix3, bb + 3 * R);
+                if (bb + 4 * R >= end) break;
             }
             // flush: as the dense multi-channel fill's (same cells, same ownership rule)
             const bool owned = pos == seg_lo && end == seg_end;
