@@ -327,7 +327,7 @@ def main():
     # cap is the contiguous (conflict-free) 64-bit LDS atomic rate measured on this GPU, the
     # pattern the fills' rotated lane layouts reach
     K = kw["approx_dim"] if P["loss"] == "MultiClass" else 1
-    per_pair = {1: 1, 3: (K + 2) // 2}.get(st["fill_mode"], K + 1)
+    per_pair = {1: 1, 3: (K + 2) // 2, 4: (K + 2) // 2}.get(st["fill_mode"], K + 1)
     lds = None
     rates = _lds_rates()
     if "contiguous_u64" in rates and fill_s > 0:
@@ -367,7 +367,7 @@ def main():
         cpu["splits_match_gpu"] = bool(np.array_equal(first, exp["splits"]))
 
     fill_kernel = {0: "fill_kernel", 1: "fill_packed_kernel", 2: "fill_split_kernel",
-                   3: "fill_pkk_kernel"}[st["fill_mode"]]
+                   3: "fill_pkk_kernel", 4: "fill_pks_kernel"}[st["fill_mode"]]
     names = {1: "config1: RMSE, no bootstrap, depth 6, 128 borders",
              2: ("config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 GreedyLogSum borders selected on the "
                  "device from the raw f32 columns, quantized on the device" if raw else
@@ -390,7 +390,9 @@ def main():
         "dtype": "u8 bins, int64 fixed-point sums, f64 scores",
         "fill": {0: "two-channel 32-feature tiles", 1: f"packed 64-feature tiles ({st['fill_pack_bits']}-bit rows)",
                  2: "channel-split 64-feature tiles",
-                 3: f"packed multi-channel 32-feature tiles (two channels per word, {st['fill_pack_bits']}-bit rows)"
+                 3: f"packed multi-channel 32-feature tiles (two channels per word, {st['fill_pack_bits']}-bit rows)",
+                 4: f"packed multi-channel 32-feature tiles over sparse entries (a row per 16-lane DPP row, "
+                    f"two channels per word, {st['fill_pack_bits']}-bit rows)"
                  }[st["fill_mode"]],
         "data": f"synthetic (seeded; datagen.config{args.config}{'_raw' if raw else ''})",
         "config": {"workload": names[args.config], "rows": n, "features": F, "depth": P["depth"],

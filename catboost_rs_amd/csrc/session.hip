@@ -1941,7 +1941,8 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
         for (uint64_t i = 0; i < n; ++i) out->leaf_of[i] = lf[i] & 0x7FFFu;
     }
     // traffic accounting of the fill launches (algorithmic bytes per launch)
-    const double wbytes = 4.0 * s->W,
+    // (sparse entries: the first 16 codes of every tile, 32 bytes; second slots not counted)
+    const double wbytes = s->pks ? 32.0 * s->pkk_tiles : 4.0 * s->W,
                  sbytes = s->packed ? 8.0 : s->pkk ? 8.0 * ((s->C + 1) / 2) : 8.0 * s->C;   // split: 8 per channel
     const double per_leaf_bytes = (double)s->F * s->B * s->C * 8.0;
     for (uint32_t l = 0; l < s->depth; ++l) {
@@ -1983,7 +1984,7 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
     if (!s || !out) return fail(CBH_ERR_INVALID_ARG, "null argument");
     *out = s->stats;
     out->skip_features = s->n_skip;
-    out->fill_mode = s->packed ? 1u : s->split ? 2u : s->pkk ? 3u : 0u;
+    out->fill_mode = s->packed ? 1u : s->split ? 2u : s->pks ? 4u : s->pkk ? 3u : 0u;
     out->fill_pack_bits = (s->packed || s->pkk) ? s->pack_bits : 0;
     return CBH_OK;
 }

@@ -208,7 +208,9 @@ typedef struct {
     uint32_t fill_mode;           /* 0: 32-feature tiles, both channels per workgroup; 1: packed 64-feature
                                      tiles (one 64-bit atomic carries both channels); 2: channel-split
                                      64-feature tiles (one workgroup per channel); 3: packed multi-channel
-                                     32-feature tiles (K > 1: two channels per 64-bit atomic) */
+                                     32-feature tiles (K > 1: two channels per 64-bit atomic); 4: the same
+                                     cells over sparse entries (a row per 16-lane DPP row, one lane per
+                                     non-dominant (feature, bin)) */
     int32_t fill_pack_bits;       /* packed fills: bits of a row's rounded channel value (|q| < 2^bits) */
 } cbh_stats;
 
