@@ -2080,18 +2080,18 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
     const uint32_t pstride = (uint32_t)C * F * B * 8u;
     const uint32_t off_d = bc * 8u;
     const uint32_t off_t = pu(min(lane, (uint32_t)PW - 1)) * pstride + (B - 1) * 8u;
+    // wave-uniform byte addresses (kept in SGPRs, 64-bit scalar adds): the row of (parent p0,
+    // dimension d) is row0 + d * dstride; parent p0 + u is u parent strides further
+    const uint64_t pstride64 = (uint64_t)C * F * B * 8u, dstride64 = (uint64_t)F * B * 8u;
+    const uint64_t row0 = (uint64_t)(uintptr_t)uniform_ptr(hist + ((size_t)p0 * C * F + f) * B);
     auto load_der = [&](int d) {
-        const GlobalU8 base = (GlobalU8)uniform_ptr(hist + (((size_t)p0 * C + d) * F + f) * B);
-        if (PW <= 8) {   // uniform row bases from the base and the parent stride
+        uint64_t a = row0 + (uint64_t)d * dstride64;
+        tdv = *(GlobalI64)((GlobalU8)(uintptr_t)a + off_t);
 #pragma unroll
-            for (int u = 0; u < PW; ++u)
-                pd[u] = *(GlobalI64)((GlobalU8)uniform_ptr((const long long*)(base + pu(u) * pstride)) + off_d);
-        } else {         // 16 parents: full row addresses (fewer registers live across the loop)
-#pragma unroll
-            for (int u = 0; u < PW; ++u)
-                pd[u] = uniform_ptr(hist + (((size_t)(p0 + pu(u)) * C + d) * F + f) * B)[bc];
+        for (int u = 0; u < PW; ++u) {
+            if (u > 0 && (!kPartial || (uint32_t)u < P)) a += pstride64;   // parent p0 + pu(u)
+            pd[u] = *(GlobalI64)((GlobalU8)(uintptr_t)a + off_d);
         }
-        tdv = *(GlobalI64)(base + off_t);
     };
     load_der(0);
     uint32_t hop = wv;   // this wave's hop of slab t is t * nw + wv
