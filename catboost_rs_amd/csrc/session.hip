@@ -1564,9 +1564,14 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             // their dominant bins rebuilt from the segment totals, and their siblings = parent -
             // built (levels >= 1)
             const uint64_t rows = (uint64_t)n_seg * C * s->F;
-            hist_prefix_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(
-                cur, lplan, n_seg, C, s->F, s->B, level > 0 ? par : nullptr, s->use_skip ? s->skip_bin : nullptr,
-                s->seg_tot);
+            if (s->B <= 96)   // a half-wave per row
+                hist_prefix_half_kernel<<<(unsigned)((rows + 7) / 8), 256, 0, st>>>(
+                    cur, lplan, n_seg, C, s->F, s->B, level > 0 ? par : nullptr,
+                    s->use_skip ? s->skip_bin : nullptr, s->seg_tot);
+            else
+                hist_prefix_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(
+                    cur, lplan, n_seg, C, s->F, s->B, level > 0 ? par : nullptr,
+                    s->use_skip ? s->skip_bin : nullptr, s->seg_tot);
             HIP_TRY(hipGetLastError());
         }
         CHECK(s->stage_end());
