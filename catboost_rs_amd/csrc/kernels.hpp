@@ -1738,17 +1738,18 @@ static __global__ __launch_bounds__(256) void hist_prefix_kernel(long long* __re
     }
 }
 
-// The same pass for B <= 96 bins: a half-wave (32 lanes, up to 3 bins each) per row, two rows
-// per wave (half the waves of the 64-lane form, whose lanes past 33 idle at 65 bins).
-static __global__ __launch_bounds__(256) void hist_prefix_half_kernel(long long* __restrict__ hist,
-                                                                      const LevelPlan* __restrict__ plan,
-                                                                      uint32_t n_built, uint32_t C, uint32_t F,
-                                                                      uint32_t B,
-                                                                      const long long* __restrict__ parent,
-                                                                      const uint32_t* __restrict__ skip_bin,
-                                                                      const long long* __restrict__ seg_tot) {
-    const uint32_t hl = threadIdx.x & 31u;
-    const uint64_t row = (uint64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+// The same pass for few bins: a group of GL lanes (32 or 16, up to EM bins each) per row, 64 / GL
+// rows per wave (fewer waves than the 64-lane form, whose lanes past 33 idle at 65 bins).
+template <uint32_t GL, uint32_t EM>
+static __global__ __launch_bounds__(256) void hist_prefix_group_kernel(long long* __restrict__ hist,
+                                                                       const LevelPlan* __restrict__ plan,
+                                                                       uint32_t n_built, uint32_t C, uint32_t F,
+                                                                       uint32_t B,
+                                                                       const long long* __restrict__ parent,
+                                                                       const uint32_t* __restrict__ skip_bin,
+                                                                       const long long* __restrict__ seg_tot) {
+    const uint32_t hl = threadIdx.x & (GL - 1u);
+    const uint64_t row = (uint64_t)blockIdx.x * (256 / GL) + (threadIdx.x / GL);
     const uint64_t rows = (uint64_t)n_built * C * F;
     const bool valid = row < rows;   // the shuffles below run in every lane of the wave
     const uint64_t rc = valid ? row : rows - 1;
@@ -1756,12 +1757,12 @@ static __global__ __launch_bounds__(256) void hist_prefix_half_kernel(long long*
     const uint32_t rem = (uint32_t)(rc - (uint64_t)seg * C * F);
     const uint32_t slot = plan ? plan->built[seg] : 0u;
     long long* h = hist + ((size_t)slot * C * F + rem) * B;
-    const uint32_t E = (B + 31) / 32;   // bins per lane, <= 3
+    const uint32_t E = (B + GL - 1) / GL;   // bins per lane, <= EM
     const uint32_t b0 = hl * E;
-    long long v[3];
+    long long v[EM];
     long long run = 0;
 #pragma unroll
-    for (uint32_t e = 0; e < 3; ++e) {
+    for (uint32_t e = 0; e < EM; ++e) {
         const uint32_t b = b0 + e;
         v[e] = (e < E && b < B) ? h[b] : 0;
         run += v[e];
@@ -1769,14 +1770,14 @@ static __global__ __launch_bounds__(256) void hist_prefix_half_kernel(long long*
     }
     long long incl = run;
 #pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-        const long long u = __shfl_up(incl, o, 32);
+    for (int o = 1; o < (int)GL; o <<= 1) {
+        const long long u = __shfl_up(incl, o, GL);
         if (hl >= (uint32_t)o) incl += u;
     }
     const long long off = incl - run;
     long long dv = 0;
     uint32_t d = B;
-    const long long tot = __shfl(incl, 31, 32);
+    const long long tot = __shfl(incl, GL - 1, GL);
     if (skip_bin) {
         const uint32_t ch = rem / F, f = rem - ch * F;
         d = skip_bin[f];
@@ -1784,7 +1785,7 @@ static __global__ __launch_bounds__(256) void hist_prefix_half_kernel(long long*
     }
     if (!valid) return;
 #pragma unroll
-    for (uint32_t e = 0; e < 3; ++e) {
+    for (uint32_t e = 0; e < EM; ++e) {
         const uint32_t b = b0 + e;
         v[e] += off + (b >= d ? dv : 0);
         if (e < E && b < B) h[b] = v[e];
@@ -1794,7 +1795,7 @@ static __global__ __launch_bounds__(256) void hist_prefix_half_kernel(long long*
     const long long* pr = parent + ((size_t)seg * C * F + rem) * B;
     long long* sib = hist + ((size_t)other * C * F + rem) * B;
 #pragma unroll
-    for (uint32_t e = 0; e < 3; ++e) {
+    for (uint32_t e = 0; e < EM; ++e) {
         const uint32_t b = b0 + e;
         if (e < E && b < B) sib[b] = pr[b] - v[e];
     }

@@ -1564,8 +1564,12 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             // their dominant bins rebuilt from the segment totals, and their siblings = parent -
             // built (levels >= 1)
             const uint64_t rows = (uint64_t)n_seg * C * s->F;
-            if (s->B <= 96)   // a half-wave per row
-                hist_prefix_half_kernel<<<(unsigned)((rows + 7) / 8), 256, 0, st>>>(
+            if (s->B <= 80)   // 16 lanes per row
+                hist_prefix_group_kernel<16, 5><<<(unsigned)((rows + 15) / 16), 256, 0, st>>>(
+                    cur, lplan, n_seg, C, s->F, s->B, level > 0 ? par : nullptr,
+                    s->use_skip ? s->skip_bin : nullptr, s->seg_tot);
+            else if (s->B <= 96)   // a half-wave per row
+                hist_prefix_group_kernel<32, 3><<<(unsigned)((rows + 7) / 8), 256, 0, st>>>(
                     cur, lplan, n_seg, C, s->F, s->B, level > 0 ? par : nullptr,
                     s->use_skip ? s->skip_bin : nullptr, s->seg_tot);
             else
