@@ -1564,7 +1564,11 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             // their dominant bins rebuilt from the segment totals, and their siblings = parent -
             // built (levels >= 1)
             const uint64_t rows = (uint64_t)n_seg * C * s->F;
-            if (s->B <= 80)   // 16 lanes per row
+            if (s->B <= 72)   // 8 lanes per row
+                hist_prefix_group_kernel<8, 9><<<(unsigned)((rows + 31) / 32), 256, 0, st>>>(
+                    cur, lplan, n_seg, C, s->F, s->B, level > 0 ? par : nullptr,
+                    s->use_skip ? s->skip_bin : nullptr, s->seg_tot);
+            else if (s->B <= 80)   // 16 lanes per row
                 hist_prefix_group_kernel<16, 5><<<(unsigned)((rows + 15) / 16), 256, 0, st>>>(
                     cur, lplan, n_seg, C, s->F, s->B, level > 0 ? par : nullptr,
                     s->use_skip ? s->skip_bin : nullptr, s->seg_tot);
