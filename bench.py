@@ -366,7 +366,7 @@ def main():
         tr2.close()
         cpu["splits_match_gpu"] = bool(np.array_equal(first, exp["splits"]))
 
-    fill_kernel = {0: "fill_kernel", 1: "fill_packed_kernel", 2: "fill_split_kernel",
+    fill_kernel = {0: "fill_kernel", 1: "fill_packed_kernel", 2: "fill_exact_kernel",
                    3: "fill_pkk_kernel", 4: "fill_pks_kernel"}[st["fill_mode"]]
     names = {1: "config1: RMSE, no bootstrap, depth 6, 128 borders",
              2: ("config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 GreedyLogSum borders selected on the "
@@ -388,8 +388,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u8 bins, int64 fixed-point sums, f64 scores",
-        "fill": {0: "two-channel 32-feature tiles", 1: f"packed 64-feature tiles ({st['fill_pack_bits']}-bit rows)",
-                 2: "channel-split 64-feature tiles",
+        "fill": {0: "generic 32-feature tiles (one 64-bit atomic per channel, full fixed-point scale)", 1: f"packed 64-feature tiles ({st['fill_pack_bits']}-bit rows)",
+                 2: "tiled exact 32-feature tiles (one 64-bit atomic per channel, full fixed-point scale)",
                  3: f"packed multi-channel 32-feature tiles (two channels per word, {st['fill_pack_bits']}-bit rows)",
                  4: f"packed multi-channel 32-feature tiles over sparse entries (a row per 16-lane DPP row, "
                     f"two channels per word, {st['fill_pack_bits']}-bit rows)"

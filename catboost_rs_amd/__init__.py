@@ -125,7 +125,7 @@ EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_version", "cbh_last_error", "cbt_open", "cbt_open_raw", "cbt_set_pairs", "cbt_step",
            "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close", "cbh_session_set_profile",
            "cbt_set_profile", "cbh_session_set_ctr", "cbt_set_ctr", "cbh_session_read_ctr_bins",
-           "cbt_open_ctr", "cbh_hist_build_noalloc"]
+           "cbt_open_ctr", "cbh_hist_build_noalloc", "cbh_session_capture_hists", "cbh_session_level_hist"]
 
 _lib = None
 
@@ -177,6 +177,8 @@ def load(path: str = LIB_PATH):
     L.cbt_bias.argtypes = [P]
     L.cbt_bias.restype = C.c_double
     L.cbh_session_set_profile.argtypes = [P, C.c_int32]
+    L.cbh_session_capture_hists.argtypes = [P, C.c_int32]
+    L.cbh_session_level_hist.argtypes = [P, C.c_uint32, P, C.c_uint64]
     L.cbh_session_set_ctr.argtypes = [P, C.POINTER(CtrInfo)]
     L.cbt_set_ctr.argtypes = [P, C.POINTER(CtrInfo)]
     L.cbt_set_profile.argtypes = [P, C.c_int32]
@@ -561,6 +563,17 @@ class HipBackend:
         a = np.zeros(self.n * self.K)
         _check(load().cbh_session_read_approx(self._s, _ptr(a), a.shape[0]))
         return a.reshape(self.K, self.n)
+
+    def capture_hists(self, on=True):
+        """Keep every later tree's level histograms (cbh_session_capture_hists)."""
+        _check(load().cbh_session_capture_hists(self._s, int(bool(on))))
+
+    def level_hist(self, level, n_features, n_bins):
+        """Level ``level`` of the last tree: bin sums [2^level][F][n_bins][K+1] (channel K the
+        weight), the reference's layout."""
+        out = np.zeros(((1 << level), n_features, n_bins, self.K + 1), np.float64)
+        _check(load().cbh_session_level_hist(self._s, level, _ptr(out), out.size))
+        return out
 
     def stats(self):
         st = Stats()

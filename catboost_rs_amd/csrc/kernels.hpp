@@ -130,11 +130,11 @@ static __global__ void pack_rows_kernel(const uint8_t* __restrict__ cols, uint64
     }
 }
 
-// Tile-major packing for the packed fill: tile t (words [16t, 16t + TW_t), TW_t = min(16,
-// W - 16t)) of row r at trows[n * 16t + r * TS_t + w], so a workgroup of a tile streams its rows
-// contiguously.  TS_t = 2^(shift - 2) words: 16 (64 bytes) for a full tile, the next power of
-// two of TW for a narrow last tile (its padding words are zero), so a row's offset is one
-// shift whatever the tile.
+// Tile-major packing for the tiled fills: tile t (words [M t, M t + TW_t), TW_t = min(M,
+// W - M t), M the words of a full tile) of row r at trows[n * M t + r * TS_t + w], so a
+// workgroup of a tile streams its rows contiguously.  TS_t = 2^(shift - 2) words: M for a full
+// tile, the next power of two of TW for a narrow last tile (its padding words are zero), so a
+// row's offset is one shift whatever the tile.
 __host__ __device__ inline uint32_t packed_slice_shift(uint32_t TW) {
     uint32_t sh = 2;
     while ((1u << sh) < 4u * TW) ++sh;
@@ -142,13 +142,16 @@ __host__ __device__ inline uint32_t packed_slice_shift(uint32_t TW) {
 }
 __host__ __device__ inline uint32_t packed_slice_words(uint32_t TW) { return 1u << (packed_slice_shift(TW) - 2); }
 
+// TWM: words of a full tile (16 for the packed fill's 64-feature tiles, 8 for the exact fill's
+// 32-feature tiles).
 static __global__ void pack_tiles_kernel(const uint8_t* __restrict__ cols, uint64_t n, uint32_t F, uint32_t W,
-                                         uint32_t* __restrict__ trows, uint64_t total /* words of trows */) {
+                                         uint32_t* __restrict__ trows, uint64_t total /* words of trows */,
+                                         uint32_t TWM) {
     for (uint64_t o = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
          o += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t t = (uint32_t)(o / (n * 16u));
-        const uint32_t w0 = 16u * t;
-        const uint32_t TS = packed_slice_words(min(16u, W - w0));   // words per row in the slice
+        const uint32_t t = (uint32_t)(o / (n * TWM));
+        const uint32_t w0 = TWM * t;
+        const uint32_t TS = packed_slice_words(min(TWM, W - w0));   // words per row in the slice
         const uint64_t rem = o - (uint64_t)n * w0;
         const uint64_t r = rem / TS;
         const uint32_t w = (uint32_t)(rem - r * TS) + w0;
@@ -1082,6 +1085,387 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
 }
 
 // ---------------------------------------------------------------------------------
+// Tiled exact fill (K == 1).  Both score channels keep the tree's full fixed-point scale
+// (round(v * 2^S), S = 61 - ceil(log2 sum|v|) per channel, 2^-37 at config 2), one 64-bit LDS
+// atomic per (row, feature, channel).  The LDS cells are exact int64 sums: nothing is rounded
+// beyond the per-row quantization, no cell is swapped, and the tile flushes straight from LDS to
+// the level histogram at segment ends.
+//
+// Tiles of 32 features (8 words); LDS [bin][ch][32] of u64, 512 bytes per bin, the weight cell
+// of a column 256 bytes past its der cell (one immediate offset apart).  A 16-lane DPP row
+// takes two rows per pass, lane 8 j + w word w of row j.  The 16 positions a DPP row covers in
+// a block of 1024 are staged one per lane (16 bytes of statistics; gathered, the row index), and
+// pass u broadcasts lane u to lanes 0-7 and lane 8 + u to lanes 8-15 (row_newbcast, the second
+// under a bank mask), so a row's statistics cost one load and no LDS round trip.  Step k of a
+// lane visits byte (k + rot) & 3 of its word, rot = (2 j + w / 4) mod 4: the 16 lanes of every
+// atomic hit 16 distinct columns mod 16, i.e. distinct bank pairs whatever the bins.
+//
+// A last tile of at most 2 words runs the narrow loop: 8 rows per DPP row (lane 2 j + w word w
+// of row j), four LDS copies of its 8 feature columns (copy j mod 4, summed at the flush), the
+// statistics of a pass broadcast within lane quads (quad_perm), so its atomics carry 64 useful
+// lanes instead of 16.
+//
+// Rows: the dense level streams each tile's tile-major slice, the gathered levels read the
+// row-major words through the partition's index list (all tiles of a range on one XCD: a listed
+// row's lines come from HBM once); statistics in position order ([n][2], or the listed rows'
+// copy in idx order written by the compaction).
+// ---------------------------------------------------------------------------------
+constexpr uint32_t kExThreads = 1024;           // 16 waves, one workgroup per CU
+constexpr uint32_t kExTileWords = 8;
+constexpr uint32_t kExCells = 256u * 2u * 32u;   // [bin][ch][32] u64: 128 KiB
+constexpr uint32_t kExBlockRows = 1024;         // positions of a block: 16 per DPP row
+constexpr uint32_t kExSegmentCost = 1024;       // rows' worth of time a segment's flush costs (ranges)
+
+// Lanes 0-7 of every DPP row take lane U of the row, lanes 8-15 lane 8 + U.
+template <int U>
+__device__ __forceinline__ unsigned long long half_bcast64(unsigned long long v) {
+    const unsigned long long a = __builtin_amdgcn_update_dpp(0ull, v, 0x150 + U, 0xF, 0xF, true);
+    return __builtin_amdgcn_update_dpp(a, v, 0x150 + 8 + U, 0xF, 0xC, false);
+}
+template <int U>
+__device__ __forceinline__ uint32_t half_bcast32(uint32_t v) {
+    const int a = __builtin_amdgcn_update_dpp(0, (int)v, 0x150 + U, 0xF, 0xF, true);
+    return (uint32_t)__builtin_amdgcn_update_dpp(a, (int)v, 0x150 + 8 + U, 0xF, 0xC, false);
+}
+
+// The four byte visits of one row's word, both channels: off8[k] = 8 * column (its low 5 bits
+// are the byte's bit shift, the v_bfe offset); der cell at bin * 512 + off8, weight cell 256
+// bytes further.
+__device__ __forceinline__ void exact_row_atomics(unsigned long long* __restrict__ ex, uint32_t word,
+                                                  const uint32_t* off8, unsigned long long sd,
+                                                  unsigned long long sw) {
+    char* base = (char*)ex;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t bin = __builtin_amdgcn_ubfe(word, off8[k], 8);
+        unsigned long long* c = (unsigned long long*)(base + ((bin << 9) + off8[k]));
+        atomicAdd(c, sd);
+        atomicAdd(c + 32, sw);
+    }
+}
+
+// A 16-byte load at kPastEnd16 lies wholly past every buffer of the tiled exact fill (whose
+// sizes the session keeps below 2^31 bytes) without wrapping the 32-bit offset: it returns 0.
+constexpr uint32_t kPastEnd16 = 0xFFFFFFE0u;
+__device__ __forceinline__ void ldq2(__amdgpu_buffer_rsrc_t r, uint32_t off, unsigned long long& a,
+                                     unsigned long long& b) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+    a = (unsigned long long)v[0] | ((unsigned long long)v[1] << 32);
+    b = (unsigned long long)v[2] | ((unsigned long long)v[3] << 32);
+}
+
+// One block's worth of a DPP row in flight: the words of its 8 passes, the staged statistics and,
+// gathered, the staged row index of the set's next block.
+struct ExSet {
+    uint32_t w[8];
+    unsigned long long sd, sw;
+    uint32_t ix;
+};
+
+template <int U>
+__device__ __forceinline__ void exact_pass(unsigned long long* __restrict__ ex, const ExSet& S, const uint32_t* off8) {
+    exact_row_atomics(ex, S.w[U], off8, half_bcast64<U>(S.sd), half_bcast64<U>(S.sw));
+}
+
+// Positions [pos, end) of a full tile.  Two sets alternate: while one block's atomics issue, the
+// next block's words and statistics are in flight; gathered, a set's row indices are staged a
+// round (two blocks) before its words need them.  Blocks past the range read zero statistics
+// (a buffer load past the resource returns 0) and, at the dense level, rows clamped into
+// [0, n) in groups of 16; gathered, the indices of positions past the range repeat idx[pos].
+template <bool kGather, int NS>
+__device__ __forceinline__ void exact_range(unsigned long long* __restrict__ ex, __amdgpu_buffer_rsrc_t rbase,
+                                            uint32_t sh, uint32_t wl4, uint32_t j8, uint32_t l,
+                                            __amdgpu_buffer_rsrc_t ibase, __amdgpu_buffer_rsrc_t sbase,
+                                            bool seq, uint32_t pos, uint32_t end, uint32_t n, uint32_t r0,
+                                            const uint32_t* off8) {
+    auto q_of = [&](uint32_t bb) -> uint32_t { return bb + 16u * r0; };
+    auto dense_q = [&](uint32_t bb) -> uint32_t {
+        const uint32_t q = q_of(bb);
+        return q + 16u <= n ? q : n - 16u;
+    };
+    auto stage_ix = [&](uint32_t bb) -> uint32_t {
+        const uint32_t p = q_of(bb) + l;
+        return ldw(ibase, 4u * (p < end ? p : pos));
+    };
+    auto load = [&](ExSet& S, uint32_t bb) {
+        uint32_t p;
+        bool ok;
+        if (kGather) {
+            p = q_of(bb) + l;
+            ok = p < end;
+        } else {
+            p = dense_q(bb) + l;
+            ok = p >= q_of(bb) && p < end;
+        }
+        // gathered: the statistics of the staged position, in idx order (seq) or through its row
+        // index
+        const uint32_t sp = (kGather && !seq) ? S.ix : p;
+        ldq2(sbase, ok ? 16u * sp : kPastEnd16, S.sd, S.sw);
+        if (kGather) {
+            const uint32_t ix = S.ix;
+            S.w[0] = ldw(rbase, (half_bcast32<0>(ix) << sh) + wl4);
+            S.w[1] = ldw(rbase, (half_bcast32<1>(ix) << sh) + wl4);
+            S.w[2] = ldw(rbase, (half_bcast32<2>(ix) << sh) + wl4);
+            S.w[3] = ldw(rbase, (half_bcast32<3>(ix) << sh) + wl4);
+            S.w[4] = ldw(rbase, (half_bcast32<4>(ix) << sh) + wl4);
+            S.w[5] = ldw(rbase, (half_bcast32<5>(ix) << sh) + wl4);
+            S.w[6] = ldw(rbase, (half_bcast32<6>(ix) << sh) + wl4);
+            S.w[7] = ldw(rbase, (half_bcast32<7>(ix) << sh) + wl4);
+            S.ix = stage_ix(bb + NS * kExBlockRows);
+        } else {
+            const uint32_t o = ((dense_q(bb) + j8) << sh) + wl4;
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u) S.w[u] = ldw_s(rbase, o, u << sh);
+        }
+    };
+    auto consume = [&](const ExSet& S) {
+        exact_pass<0>(ex, S, off8);
+        exact_pass<1>(ex, S, off8);
+        exact_pass<2>(ex, S, off8);
+        exact_pass<3>(ex, S, off8);
+        exact_pass<4>(ex, S, off8);
+        exact_pass<5>(ex, S, off8);
+        exact_pass<6>(ex, S, off8);
+        exact_pass<7>(ex, S, off8);
+    };
+    static_assert(NS == 2 || NS == 3, "two or three sets");
+    ExSet S0, S1, S2;
+    if (kGather) {
+        S0.ix = stage_ix(pos);
+        S1.ix = stage_ix(pos + kExBlockRows);
+        if (NS == 3) S2.ix = stage_ix(pos + 2u * kExBlockRows);
+    }
+    load(S0, pos);
+    load(S1, pos + kExBlockRows);
+    if (NS == 3) load(S2, pos + 2u * kExBlockRows);
+    for (uint32_t bb = pos;; bb += NS * kExBlockRows) {   // workgroup-uniform
+        consume(S0);
+        if (bb + kExBlockRows >= end) break;
+        load(S0, bb + NS * kExBlockRows);
+        consume(S1);
+        if (bb + 2u * kExBlockRows >= end) break;
+        load(S1, bb + (NS + 1) * kExBlockRows);
+        if (NS == 3) {
+            consume(S2);
+            if (bb + 3u * kExBlockRows >= end) break;
+            load(S2, bb + (NS + 2) * kExBlockRows);
+        }
+    }
+}
+
+// The narrow loop's set: the words of its 2 passes, staged statistics and row index.
+struct ExNarrowSet {
+    uint32_t w[2];
+    unsigned long long sd, sw;
+    uint32_t ix;
+};
+
+template <int U>
+__device__ __forceinline__ void exact_narrow_pass(unsigned long long* __restrict__ ex, const ExNarrowSet& S,
+                                                  const uint32_t* off8) {
+    exact_row_atomics(ex, S.w[U], off8, quad_pair_bcast64<U>(S.sd), quad_pair_bcast64<U>(S.sw));
+}
+
+// Positions [pos, end) of a narrow last tile (at most 2 words).  A DPP row covers the same 16
+// positions q .. q + 15 per block as in the full loop, in 2 passes of 8 rows: lane 2 j + w stages
+// position q + 8 w + j, so pass u broadcasts lane 2 j + u to lanes 2 j, 2 j + 1 (quad_perm).  A
+// block holds 16 atomics per lane, so four sets are in flight, each reloaded right after its
+// block is consumed; gathered, a set's indices are staged a round (four blocks) ahead.
+template <bool kGather>
+__device__ __forceinline__ void exact_range_narrow(unsigned long long* __restrict__ ex, __amdgpu_buffer_rsrc_t rbase,
+                                                   uint32_t sh, uint32_t wl4, uint32_t l,
+                                                   __amdgpu_buffer_rsrc_t ibase, __amdgpu_buffer_rsrc_t sbase,
+                                                   bool seq, uint32_t pos, uint32_t end, uint32_t n, uint32_t r0,
+                                                   const uint32_t* off8) {
+    constexpr uint32_t NS = 4;
+    const uint32_t j = l >> 1, stg = 8u * (l & 1u) + j;   // this lane's staged position in a block
+    auto q_of = [&](uint32_t bb) -> uint32_t { return bb + 16u * r0; };
+    auto dense_q = [&](uint32_t bb) -> uint32_t {
+        const uint32_t q = q_of(bb);
+        return q + 16u <= n ? q : n - 16u;
+    };
+    auto stage_ix = [&](uint32_t bb) -> uint32_t {
+        const uint32_t p = q_of(bb) + stg;
+        return ldw(ibase, 4u * (p < end ? p : pos));
+    };
+    auto load = [&](ExNarrowSet& S, uint32_t bb) {
+        uint32_t p;
+        bool ok;
+        if (kGather) {
+            p = q_of(bb) + stg;
+            ok = p < end;
+        } else {
+            p = dense_q(bb) + stg;
+            ok = p >= q_of(bb) && p < end;
+        }
+        const uint32_t sp = (kGather && !seq) ? S.ix : p;
+        ldq2(sbase, ok ? 16u * sp : kPastEnd16, S.sd, S.sw);
+        if (kGather) {
+            const uint32_t ix = S.ix;
+            S.w[0] = ldw(rbase, (quad_pair_bcast<0>(ix) << sh) + wl4);
+            S.w[1] = ldw(rbase, (quad_pair_bcast<1>(ix) << sh) + wl4);
+            S.ix = stage_ix(bb + NS * kExBlockRows);
+        } else {
+            const uint32_t o = ((dense_q(bb) + j) << sh) + wl4;
+            S.w[0] = ldw(rbase, o);
+            S.w[1] = ldw_s(rbase, o, 8u << sh);
+        }
+    };
+    ExNarrowSet S0, S1, S2, S3;
+    static_assert(NS == 4, "four sets");
+    if (kGather) {
+        S0.ix = stage_ix(pos);
+        S1.ix = stage_ix(pos + kExBlockRows);
+        S2.ix = stage_ix(pos + 2u * kExBlockRows);
+        S3.ix = stage_ix(pos + 3u * kExBlockRows);
+    }
+    // the sets load in the loop's order (compiler memory barriers between them), so the loop's
+    // first use waits for that set's loads only
+    load(S0, pos);
+    asm volatile("" ::: "memory");
+    load(S1, pos + kExBlockRows);
+    asm volatile("" ::: "memory");
+    load(S2, pos + 2u * kExBlockRows);
+    asm volatile("" ::: "memory");
+    load(S3, pos + 3u * kExBlockRows);
+    asm volatile("" ::: "memory");
+    // one block of a set: its atomics, then (unless the range ends) the set reloaded for the block
+    // four later
+    auto step = [&](ExNarrowSet& S, uint32_t bb) -> bool {
+        exact_narrow_pass<0>(ex, S, off8);
+        exact_narrow_pass<1>(ex, S, off8);
+        if (bb + kExBlockRows >= end) return true;
+        load(S, bb + NS * kExBlockRows);
+        return false;
+    };
+    for (uint32_t bb = pos;; bb += NS * kExBlockRows) {   // workgroup-uniform
+        if (step(S0, bb)) break;
+        if (step(S1, bb + kExBlockRows)) break;
+        if (step(S2, bb + 2u * kExBlockRows)) break;
+        if (step(S3, bb + 3u * kExBlockRows)) break;
+    }
+}
+
+// Level histogram flush of the tile: a wave takes 8 features x 8 bins of one channel (64-byte
+// runs of bins in the histogram); every cell is read and cleared by one thread (a narrow tile's
+// copies summed).  Columns >= TF (lanes past a short tile's words) are never read.
+__device__ __forceinline__ void exact_flush(unsigned long long* __restrict__ ex, uint32_t TF, uint32_t B,
+                                            uint32_t F, uint32_t f0, long long* __restrict__ hd /* hist + slot*2*F*B */,
+                                            uint32_t copies) {
+    const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
+    const uint32_t per_ch = nfb * nbb;
+    for (uint32_t i = threadIdx.x; i < 2u * per_ch * 64u; i += kExThreads) {
+        const uint32_t lane = i & 63u, jj = i >> 6;
+        const uint32_t ch = jj >= per_ch ? 1u : 0u, jb = jj - ch * per_ch;
+        const uint32_t f = (jb / nbb) * 8 + (lane >> 3), bin = (jb % nbb) * 8 + (lane & 7u);
+        if (f >= TF || bin >= B) continue;
+        unsigned long long v = 0;
+        for (uint32_t c = 0; c < copies; ++c) {
+            unsigned long long* cell = ex + bin * 64u + ch * 32u + c * 8u + f;
+            v += *cell;
+            *cell = 0ull;
+        }
+        if (v != 0) atomicAdd((unsigned long long*)hd + ((size_t)(ch * F + f0 + f) * B + bin), v);
+    }
+}
+
+template <bool kGather>
+static __global__ __launch_bounds__(kExThreads) void fill_exact_kernel(
+    const uint32_t* __restrict__ trows /* tile-major 8-word slices (pack_tiles_kernel) */, uint32_t W,
+    uint64_t n, const uint32_t* __restrict__ idx /* kGather: rows listed by the partition */,
+    const LevelPlan* __restrict__ plan, const long long* __restrict__ sfix /* [n][2] */,
+    const long long* __restrict__ sseq /* kGather, nullable: [V][2], the listed rows' statistics in idx order */,
+    uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, uint32_t Gn, long long* __restrict__ hist,
+    const uint32_t* __restrict__ rows_rm /* nullable, kGather: row-major words, 2^rm_sh bytes per row */,
+    uint32_t rm_sh, uint32_t sets /* blocks in flight of the full loop: 2 or 3 */) {
+    extern __shared__ unsigned long long ex[];
+    // blocks: n_tiles tiles of the 8-lane loop in G row ranges each, numbered range-major and
+    // dealt to the 8 XCDs in runs (block b to XCD b % 8: XCD x takes pairs [x per, (x + 1) per)),
+    // so all tiles of a range share one L2; then, when Gn > 0, the narrow last tile (tile
+    // n_tiles) in Gn ranges of the narrow loop
+    const uint32_t pairs = n_tiles * G;
+    const uint32_t per = (pairs + 7u) / 8u;
+    const uint32_t b = blockIdx.x;
+    const bool narrow = b >= 8u * per;
+    uint32_t t, g, GR;
+    if (!narrow) {
+        const uint32_t i = (b & 7u) * per + (b >> 3);
+        if (i >= pairs) return;   // workgroup-uniform, before any barrier
+        t = i % n_tiles;
+        g = i / n_tiles;
+        GR = G;
+    } else {
+        t = n_tiles;
+        g = b - 8u * per;
+        GR = Gn;
+        if (g >= Gn) return;
+    }
+    const uint32_t w0 = t * kExTileWords;
+    const uint32_t TW = min(kExTileWords, W - w0);
+    const uint32_t f0 = 4u * w0;
+    const uint32_t TF = min(4u * TW, F - f0);
+    const bool rm = kGather && rows_rm != nullptr;
+    const uint32_t sh = rm ? rm_sh : packed_slice_shift(TW);
+    for (uint32_t i = threadIdx.x; i < kExCells; i += kExThreads) ex[i] = 0ull;
+    const uint32_t r0 = threadIdx.x >> 4;   // DPP row of the workgroup
+    const uint32_t l = threadIdx.x & 15u;   // lane in the DPP row
+    uint32_t off8[4], wl4;
+    if (!narrow) {
+        const uint32_t j = l >> 3, w = l & 7u;
+        const uint32_t rot = (2u * j + (w >> 2)) & 3u;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) off8[k] = 8u * (4u * w + ((k + rot) & 3u));
+        wl4 = 4u * w;
+    } else {
+        // lane 2 j + w: copy j mod 4 of the 8 columns, rot = j / 2, so the 16 lanes of an
+        // atomic still hit 16 distinct columns mod 16
+        const uint32_t j = l >> 1, w = l & 1u;
+        const uint32_t rot = j >> 1;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) off8[k] = 8u * (8u * (j & 3u) + 4u * w + ((k + rot) & 3u));
+        wl4 = 4u * w;
+    }
+    __syncthreads();
+    const uint32_t V = kGather ? plan->rows : (uint32_t)n;
+    const uint32_t n_seg = kGather ? plan->n_parent : 1u;
+    uint32_t rb = (uint32_t)(((uint64_t)V * g) / GR), re = (uint32_t)(((uint64_t)V * (g + 1)) / GR);
+    if (kGather) balanced_range(plan, n_seg, V, g, GR, kExSegmentCost, rb, re);
+    uint32_t seg = 0;
+    if (kGather)
+        seg = first_segment(plan, n_seg, rb);
+    const __amdgpu_buffer_rsrc_t rbase = rm ? make_rsrc(rows_rm + w0, ((uint64_t)n << sh) - 4ull * w0)
+                                            : make_rsrc(trows + n * w0, (uint64_t)n << sh);
+    // gathered: statistics in idx order when the compaction wrote them (sseq), else through the
+    // listed rows' indices
+    const bool seq = kGather && sseq != nullptr;
+    const __amdgpu_buffer_rsrc_t sbase = make_rsrc(seq ? (const void*)sseq : (const void*)sfix, n * 16u);
+    const __amdgpu_buffer_rsrc_t ibase =
+        make_rsrc(kGather ? (const void*)idx : (const void*)sfix, kGather ? n * 4u : 0u);
+    uint32_t pos = rb;
+    while (pos < re) {
+        const uint32_t seg_end = (kGather && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
+        const uint32_t end = min(re, seg_end);
+        const uint32_t slot = kGather ? plan->built[seg] : 0u;
+        if (end > pos) {
+            if (!narrow && sets == 3)
+                exact_range<kGather, 3>(ex, rbase, sh, wl4, 8u * (l >> 3), l, ibase, sbase, seq, pos, end,
+                                        (uint32_t)n, r0, off8);
+            else if (!narrow)
+                exact_range<kGather, 2>(ex, rbase, sh, wl4, 8u * (l >> 3), l, ibase, sbase, seq, pos, end,
+                                        (uint32_t)n, r0, off8);
+            else
+                exact_range_narrow<kGather>(ex, rbase, sh, wl4, l, ibase, sbase, seq, pos, end, (uint32_t)n, r0,
+                                            off8);
+            __syncthreads();
+            exact_flush(ex, TF, B, F, f0, hist + (size_t)slot * 2u * F * B, narrow ? 4u : 1u);
+            __syncthreads();
+        }
+        pos = end;
+        ++seg;
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // Packed multi-channel fill (K > 1, NP * B <= 512 with NP = ceil(C / 2) planes).  The score
 // channels 2j and 2j + 1 of a row travel in one 64-bit word, p_j = q_{2j+1} * 2^32 + q_{2j}
 // (mod 2^64), each |q| <= 2^kPkkBits - 1 (rounded on the scale of the largest row, clamped), so
@@ -1530,128 +1914,6 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
         }
         pos = end;
         ++seg;
-    }
-}
-
-// ---------------------------------------------------------------------------------
-// Channel-split fill (exact int64, any K).  One workgroup = (64-feature tile, channel, row
-// range): its LDS holds one channel of the tile, [bin][64] int64 (130 KB at 255 bins), and it
-// adds one 64-bit atomic per (row, feature) -- no packing, no periodic drains, no barrier
-// inside the row loop, so every lane keeps kSplitRows rows in flight.  The C channel
-// workgroups of a (tile, range) are adjacent blocks on one XCD and walk the same rows in the
-// same order at the same speed, so a row's 64-byte sector comes from HBM once and from L2 for
-// the other channels.  Statistics are channel-planar int64 ([C][n], and [C][V] in idx order
-// for the gathered levels): every workgroup reads 8 contiguous bytes per row.  Lane layout and
-// visit rotation as in the packed fill (conflict-free bank pairs).
-// ---------------------------------------------------------------------------------
-constexpr int kSplitRows = 16;
-
-template <bool kGather>
-static __global__ __launch_bounds__(1024) void fill_split_kernel(
-    const uint32_t* __restrict__ rows, uint32_t stride, uint32_t W, uint64_t n,
-    const uint32_t* __restrict__ idx, const LevelPlan* __restrict__ plan,
-    const long long* __restrict__ splanar /* [C][n] fixed point */,
-    const long long* __restrict__ sseqp /* nullable [C][n]: the idx rows' values in idx order */,
-    uint32_t C, uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist) {
-    extern __shared__ unsigned long long pk[];
-    const uint32_t b = blockIdx.x;
-    const uint32_t xcd = b & 7u, q = b >> 3;
-    const uint32_t c = q % C;
-    const uint32_t t = (q / C) % n_tiles;
-    const uint32_t g = (q / (C * n_tiles)) * 8u + xcd;
-    const uint32_t w0 = t * kPackTileWords;
-    const uint32_t TW = min(kPackTileWords, W - w0);
-    const uint32_t f0 = 4u * w0;
-    const uint32_t TF = min(4u * TW, F - f0);
-    for (uint32_t i = threadIdx.x; i < kPackStride * B; i += blockDim.x) pk[i] = 0ull;
-    __syncthreads();
-    const uint32_t rpp = blockDim.x / TW;
-    const uint32_t r0 = threadIdx.x / TW;
-    const uint32_t wl = threadIdx.x - r0 * TW;
-    const bool lane_on = r0 < rpp;
-    const uint32_t rot = ((wl >> 2) + (r0 & 1u)) & 3u;
-    uint32_t off[4];
-#pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) off[k] = 4u * wl + ((k + rot) & 3u);
-    const uint32_t V = kGather ? plan->rows : (uint32_t)n;
-    const uint32_t rb = (uint32_t)(((uint64_t)V * g) / G);
-    const uint32_t re = (uint32_t)(((uint64_t)V * (g + 1)) / G);
-    const uint32_t n_seg = kGather ? plan->n_parent : 1u;
-    uint32_t seg = 0;
-    if (kGather)
-        seg = first_segment(plan, n_seg, rb);
-    const uint32_t* rsrc = rows + w0 + wl;
-    const bool seq = kGather && sseqp != nullptr;
-    const long long* sbase = (seq ? sseqp : splanar) + (size_t)c * n;
-    uint32_t pos = rb;
-    while (pos < re) {
-        const uint32_t seg_end = (kGather && seg + 1 < n_seg) ? plan->seg_begin[seg + 1] : V;
-        const uint32_t end = min(re, seg_end);
-        const uint32_t slot = kGather ? plan->built[seg] : 0u;
-        if (end > pos) {
-            if (lane_on) {
-                for (uint32_t p0 = pos + r0; p0 < end; p0 += kSplitRows * rpp) {
-                    uint32_t pu[kSplitRows], vmask = 0;
-#pragma unroll
-                    for (int u = 0; u < kSplitRows; ++u) {
-                        const uint32_t p = p0 + (uint32_t)u * rpp;
-                        const bool v = p < end;
-                        vmask |= (v ? 1u : 0u) << u;
-                        pu[u] = v ? p : p0;
-                    }
-                    uint32_t doc[kSplitRows];
-#pragma unroll
-                    for (int u = 0; u < kSplitRows; ++u) doc[u] = kGather ? idx[pu[u]] : pu[u];
-                    long long st[kSplitRows];
-                    uint32_t word[kSplitRows];
-#pragma unroll
-                    for (int u = 0; u < kSplitRows; ++u) {
-                        st[u] = sbase[seq ? pu[u] : doc[u]];
-                        word[u] = rsrc[(size_t)doc[u] * stride];
-                    }
-#pragma unroll
-                    for (int u = 0; u < kSplitRows; ++u) {
-                        if (!((vmask >> u) & 1u) || st[u] == 0) continue;
-                        const uint32_t wr = __builtin_amdgcn_alignbyte(word[u], word[u], rot);
-#pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            atomicAdd(pk + ((wr >> (8 * k)) & 0xFFu) * kPackStride + off[k],
-                                      (unsigned long long)st[u]);
-                    }
-                }
-            }
-            __syncthreads();
-            // flush: a wave takes 8 features x 8 bins (64-byte runs of bins in the histogram);
-            // each cell is read and cleared by one thread
-            long long* dst = hist + ((size_t)slot * C + c) * F * B;
-            const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
-            for (uint32_t i = threadIdx.x; i < nfb * nbb * 64; i += blockDim.x) {
-                const uint32_t l = i & 63u, j = i >> 6;
-                const uint32_t f = (j / nbb) * 8 + (l >> 3), bin = (j % nbb) * 8 + (l & 7u);
-                if (f >= TF || bin >= B) continue;
-                const uint32_t li = bin * kPackStride + f;
-                const unsigned long long v = pk[li];
-                if (v != 0) {
-                    atomicAdd((unsigned long long*)dst + ((size_t)(f0 + f) * B + bin), v);
-                    pk[li] = 0ull;
-                }
-            }
-            __syncthreads();
-        }
-        pos = end;
-        ++seg;
-    }
-}
-
-// Fixed-point score channels, channel-planar: sstat f64 [n][C] -> out int64 [C][n].
-template <int C>
-static __global__ void planar_stats_fixed_kernel(const double* __restrict__ sstat, uint64_t n,
-                                                 const Scales* __restrict__ sc, long long* __restrict__ out) {
-    const double md = sc->mul[kScoreDer], mw = sc->mul[kScoreW];
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (uint64_t)gridDim.x * blockDim.x) {
-#pragma unroll
-        for (int ch = 0; ch < C; ++ch) out[(size_t)ch * n + i] = to_fixed(sstat[i * C + ch], ch == C - 1 ? mw : md);
     }
 }
 
@@ -2423,19 +2685,20 @@ static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __rest
 // running offsets in its LDS slice (seeded from the scanned per-wave counts), so the loop
 // needs no block barrier: lanes read their group's offset, then one leader per group
 // advances it.
-// With sp_out given, the score words of every listed row are written beside its index
-// (sp_out[c][k] = sp_in[c][idx[k]] for the sp_ch planes of n words), so the next fill reads the
-// statistics of its rows in order instead of gathering them.
+// With SPW > 0, the SPW score words of every listed row ([n][SPW] in row order) are written
+// beside its index (sp_out[k] = sp_in[idx[k]], [V][SPW]), so the next fill reads the statistics
+// of its rows in order instead of gathering them.
 // The level's plan (the smaller child of every parent, ties to the TRUE child, tree.rs:1109, and
 // the segment offsets of the next fill) comes from the children's totals: every block derives it
 // (at most 128 parents, one wave) and block 0 stores it for the kernels after.
+template <int SPW>
 static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __restrict__ leaf, uint64_t n,
                                                       uint32_t level, const uint32_t* __restrict__ cnt,
                                                       uint32_t n_waves, const uint32_t* __restrict__ totals,
                                                       LevelPlan* __restrict__ plan,
                                                       uint32_t* __restrict__ idx,
                                                       const unsigned long long* __restrict__ sp_in,
-                                                      unsigned long long* __restrict__ sp_out, uint32_t sp_ch) {
+                                                      unsigned long long* __restrict__ sp_out) {
     __shared__ uint32_t run[4][kMaxLeaves / 2];
     __shared__ uint32_t built[kMaxLeaves / 2];
     __shared__ uint32_t segb[kMaxLeaves / 2];
@@ -2505,15 +2768,17 @@ static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __r
         key_of[u] = valid ? p : 0u;
         vmask |= (valid ? 1u : 0u) << u;
     }
-    // one plane of statistics (the packed fill's): every listed row's word is loaded before
-    // the first store, so the wave waits for memory once, not once per 64 rows
-    unsigned long long spv[U];
-    const bool one_plane = sp_out && sp_ch == 1;
-    if (one_plane) {
+    // the statistics: every listed row's words are loaded before the first store, so the wave
+    // waits for memory once, not once per 64 rows
+    constexpr int SW = SPW > 0 ? SPW : 1;
+    unsigned long long spv[U][SW];
+    if (SPW > 0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint64_t i = beg + (uint64_t)u * 64 + lane;
-            spv[u] = ((vmask >> u) & 1u) ? sp_in[i] : 0ull;
+            const bool valid = (vmask >> u) & 1u;
+#pragma unroll
+            for (int c = 0; c < SW; ++c) spv[u][c] = valid ? sp_in[i * SW + c] : 0ull;
         }
     }
 #pragma unroll
@@ -2525,9 +2790,10 @@ static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __r
         const uint32_t rank = mbcnt64(mask);
         const uint32_t base = valid ? run[wave][key] : 0u;
         if (valid) idx[base + rank] = (uint32_t)i;
-        if (valid && one_plane) sp_out[base + rank] = spv[u];
-        else if (valid && sp_out)
-            for (uint32_t c = 0; c < sp_ch; ++c) sp_out[(size_t)c * n + base + rank] = sp_in[(size_t)c * n + i];
+        if (SPW > 0 && valid) {
+#pragma unroll
+            for (int c = 0; c < SW; ++c) sp_out[(size_t)(base + rank) * SW + c] = spv[u][c];
+        }
         if (valid && rank == 0) run[wave][key] = base + (uint32_t)__popcll(mask);
     }
 }

@@ -191,23 +191,29 @@ struct cbh_session {
     uint16_t* pks_a = nullptr;       // [pkk_tiles][n][16] entry codes 0..15 of every (tile, row)
     uint16_t* pks_b = nullptr;       // [pkk_tiles][n][16] entry codes 16..31
 
-    // 64-feature-tile fills: packed (K == 1: both score channels in one 64-bit word per row,
-    // one LDS atomic per (row, feature)) or channel-split (exact int64, one workgroup per
-    // channel of a tile)
-    bool packed = false, split = false;
+    // K == 1 tiled fills: the tiled exact fill (32-feature tiles, both channels at the tree's
+    // full fixed-point scale, one 64-bit LDS atomic per (row, feature, channel)) or the rounded
+    // packed fill (64-feature tiles, both channels rounded to 18-bit rows in one 64-bit word,
+    // one LDS atomic per (row, feature); a measurement knob)
+    bool packed = false, tiled = false;
+    uint32_t ex_sets = 3;                      // tiled: blocks in flight of the full loop
     // packed multi-channel fill (K > 1: two score channels per 64-bit word, NP = ceil(C/2) planes)
     bool pkk = false;
     uint32_t pkk_tiles = 0, pkk_ranges = 8;
     int pack_bits = 0;
-    unsigned long long* spack = nullptr;   // packed: [n] words; split: [C][n] fixed-point planes
-    unsigned long long* sseq = nullptr;    // the same for the idx rows, in idx order
-    uint32_t* trows = nullptr;             // packed fill: tile-major row words (pack_tiles_kernel)
+    unsigned long long* spack = nullptr;   // packed: [n] words
+    unsigned long long* sseq = nullptr;    // the listed rows' statistics in idx order (packed: [V]; tiled: [V][2])
+    uint32_t* trows = nullptr;             // tiled fills: tile-major row words (pack_tiles_kernel)
     uint32_t pk_tiles = 0, pk_ranges = 8, pk_swap = 1;
-    struct PackPlan {                          // packed fill launch: tiles of the 16-lane loop, ranges
+    struct PackPlan {                          // tiled fill launch: tiles of the full loop, ranges
         uint32_t tiles16 = 0, ranges = 0, ranges_n = 0, blocks = 0;   // of each, narrow-tile ranges, workgroups
     } pk_dense, pk_gath;                       // the dense level; the gathered levels
-    uint32_t pk_rm_sh = 0;                     // packed fill: log2 bytes of a row-major row (0: tile-major gathers)
+    uint32_t pk_rm_sh = 0;                     // tiled fills: log2 bytes of a row-major row (0: tile-major gathers)
     bool pk_signed_w = false;              // some object or pair weight is negative
+    // level histograms of the last tree kept for inspection (cbh_session_capture_hists): level l
+    // at hist_cap + hist_cap_off[l], the level's 2^l leaves in prefix form, as the scorer read them
+    long long* hist_cap = nullptr;
+    size_t hist_cap_off[kMaxDepth + 1] = {};
     size_t pk_lds = 0;
     JumpTabs jt() const {
         return JumpTabs{jump, jump + 1024, jump + 2048, jump + 2048 + n_coarse};
@@ -281,7 +287,7 @@ struct cbh_session {
         dfree(pair_desc); dfree(pair_mk); dfree(pair_nd);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
         dfree(phantom_cnt); dfree(fweight); dfree(ctr_pow); dfree(ctr_group_dev); dfree(ctr_used_dev);
-        dfree(phantom_off_lv);
+        dfree(phantom_off_lv); dfree(hist_cap);
         if (pin_ctr_used) (void)hipHostFree(pin_ctr_used);
         pin_ctr_used = nullptr;
         for (auto& g : tree_graph)
@@ -508,27 +514,29 @@ uint32_t pick_ranges(uint32_t cus, uint32_t per_cu, uint32_t nt, uint64_t n) {
     return G;
 }
 
-// Row ranges of the packed fill.  Tiles of the 16-lane row loop (64 features; a last tile of
-// 3..15 words runs the same loop, its lanes past TW adding to columns that are never read, so its
-// row costs about as much as a full one's) get G ranges each.  At the dense level a last tile of
-// 2 words runs the narrow loop (8 rows per DPP row) in Gn = G * r ranges, r its cost per row
-// relative to a full tile's (CBH_PACK_NARROW_COST, a measurement knob; CBH_PACK_NARROW=off keeps
-// the 16-lane loop); at the gathered levels every listed row costs its tile a random line, so
-// the narrow tile keeps the 16-lane loop there.  One round of workgroups fills the resident
-// slots.  The gathered levels read row-major words (2^rm_sh bytes per row) when the padded row
-// is a power of two under 4 GiB in all: the tiles of a range run on one XCD, so a listed row's
-// lines come from HBM once for all its tiles (CBH_PACK_GATHER=tiles keeps the tile-major slices
-// there, a measurement knob).
-void pick_packed_ranges(cbh_session* s, uint32_t cus, uint32_t per_cu) {
+// Row ranges of the tiled fills.  Tiles of the full loop (TWM words: 16 for the packed fill, 8
+// for the tiled exact fill; a shorter last tile runs the same loop, its lanes past TW adding to
+// columns that are never read, so its row costs about as much as a full one's) get G ranges
+// each.  A narrow last tile (the packed fill: exactly 2 words, at the dense level only; the
+// exact fill: at most 2 words, at every level) runs the narrow loop (8 rows per DPP row) in
+// Gn = G * r ranges, r its cost per row relative to a full tile's (CBH_PACK_NARROW_COST, a
+// measurement knob; CBH_PACK_NARROW=off keeps the full loop).  One round of workgroups fills
+// the resident slots.  The gathered levels read row-major words (2^rm_sh bytes per row) when
+// the padded row is a power of two under 4 GiB in all: the tiles of a range run on one XCD, so
+// a listed row's lines come from HBM once for all its tiles (CBH_PACK_GATHER=tiles keeps the
+// tile-major slices there, a measurement knob).
+void pick_tile_ranges(cbh_session* s, uint32_t cus, uint32_t per_cu, uint32_t TWM) {
     const uint32_t cap = cus * std::max<uint32_t>(per_cu, 1);
-    double r = 0.2;
+    const bool exact = TWM == kExTileWords;
+    double r = exact ? 0.3 : 0.2;
     if (const char* e = std::getenv("CBH_PACK_NARROW_COST")) {
         const double v = std::strtod(e, nullptr);
         if (v > 0.0 && v <= 1.0) r = v;
     }
+    const uint32_t n_tiles = (s->W + TWM - 1) / TWM;
     auto plan = [&](bool narrow) {
         cbh_session::PackPlan pl;
-        const uint32_t nt = narrow ? s->W / kPackTileWords : s->pk_tiles;
+        const uint32_t nt = narrow ? s->W / TWM : n_tiles;
         auto gn_of = [&](uint32_t g) { return narrow ? std::max<uint32_t>(1, (uint32_t)std::ceil(g * r)) : 0u; };
         uint32_t G = 0, Gn = 0;
         if (nt == 0) {   // one narrow tile: every slot
@@ -563,9 +571,15 @@ void pick_packed_ranges(cbh_session* s, uint32_t cus, uint32_t per_cu) {
         return pl;
     };
     const char* ne = std::getenv("CBH_PACK_NARROW");
-    const bool narrow = s->W % kPackTileWords == 2 && !(ne && std::string(ne) == "off");
+    const bool off = ne && std::string(ne) == "off";
+    const uint32_t last = s->W % TWM;
+    const bool narrow = !off && (exact ? (last == 1 || last == 2) : last == 2);
     s->pk_dense = plan(narrow);
-    s->pk_gath = plan(false);
+    // (the exact fill's narrow loop at the gathered levels measured 2x slower there: 760 against
+    // 360 us per level at config 2, each of its workgroups' few 8-byte gathers waiting on random
+    // lines; CBH_PACK_NARROW_GATHER=on takes it, a measurement knob)
+    const char* ng = std::getenv("CBH_PACK_NARROW_GATHER");
+    s->pk_gath = plan(exact && narrow && ng && std::string(ng) == "on");
     s->pk_ranges = s->pk_gath.ranges;
     const uint64_t rb = 4ull * s->Ws;
     s->pk_rm_sh = 0;
@@ -607,10 +621,6 @@ int plan_tiles(cbh_session* s) {
     return CBH_OK;
 }
 
-// Fill plan.  CBH_FILL=exact keeps the 32-feature two-channel fill, =packed the packed
-// 64-feature fill (K == 1), =split the channel-split 64-feature fill; the default picks the
-// channel-split fill from 2^20 rows on (where the fill's memory traffic dominates the tree).
-// None of the 64-feature fills handles the dominant-bin skip.
 template <int C>
 int set_pkk_attr(size_t lds) {
     for (const void* k : {(const void*)fill_pkk_kernel<C, false, false>, (const void*)fill_pkk_kernel<C, false, true>,
@@ -657,37 +667,40 @@ int plan_pkk(cbh_session* s, const std::string& v) {
     return CBH_OK;
 }
 
+// Fill plan.  The default: K == 1 from 2^20 rows the tiled exact fill, K > 1 from 500000 rows
+// the packed multi-channel fill, otherwise (and with the dominant-bin skip at K == 1) the generic
+// fill.  CBH_FILL (a measurement and test knob) forces one: =generic the generic fill (any K),
+// =tiled the tiled exact fill (K == 1), =packed the rounded packed fill (K == 1: 18-bit rows) or
+// the packed multi-channel fill (K > 1).
 int plan_fill_mode(cbh_session* s) {
-    s->packed = s->split = s->pkk = false;
+    s->packed = s->tiled = s->pkk = false;
     const char* e = std::getenv("CBH_FILL");
     const std::string v = e ? e : "";
-    if (s->K > 1 && v != "exact" && v != "split") return plan_pkk(s, v);
-    if (v == "exact" || s->use_skip) return CBH_OK;
+    if (s->K > 1) return (v.empty() || v == "packed") ? plan_pkk(s, v) : CBH_OK;
+    if (v == "generic" || s->use_skip) return CBH_OK;
     // (the packed decode takes non-negative weights: a negative object weight keeps the other fills)
-    const bool want_packed = (v == "packed" || (v.empty() && s->n >= (1ull << 20))) && s->K == 1 && !s->pk_signed_w;
-    const bool want_split = v == "split";
-    if (!want_packed && !want_split) return CBH_OK;
-    // the packed fill addresses its buffers (a tile's row words, statistics) by 32-bit byte offsets
-    // and reads the dense level's rows in groups of 16 clamped to [0, n)
-    if (want_packed && ((uint64_t)s->n * kPackTileWords * 4u >= (1ull << 32) || s->n < 1024)) return CBH_OK;
+    const bool want_packed = v == "packed" && !s->pk_signed_w;
+    const bool want_tiled = !want_packed && (v == "tiled" || (v.empty() && s->n >= (1ull << 20)));
+    if (!want_packed && !want_tiled) return CBH_OK;
+    // the tiled fills address their buffers (a tile's row words, statistics) by 32-bit byte
+    // offsets and read the dense level's rows in groups of 16 clamped to [0, n)
+    const uint32_t TWM = want_packed ? kPackTileWords : kExTileWords;
+    if ((uint64_t)s->n * TWM * 4u >= (1ull << 31) || s->n < 1024) return CBH_OK;
     int lds_max = 0, cus = 0, per_cu = 0;
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device));
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
-    // packed: every thread owns kPackOwn cells of a 256-bin tile whatever B (branch-free swaps)
-    const size_t lds = (want_packed ? (size_t)kPackCells : (size_t)kPackStride * s->B) * sizeof(unsigned long long);
+    // every thread owns the same cells of a 256-bin tile whatever B
+    const size_t lds = (size_t)(want_packed ? kPackCells : kExCells) * sizeof(unsigned long long);
     if (lds > (size_t)lds_max) return CBH_OK;
-    const void* kg = want_packed ? (const void*)fill_packed_kernel<true> : (const void*)fill_split_kernel<true>;
-    const void* kd = want_packed ? (const void*)fill_packed_kernel<false> : (const void*)fill_split_kernel<false>;
+    const void* kg = want_packed ? (const void*)fill_packed_kernel<true> : (const void*)fill_exact_kernel<true>;
+    const void* kd = want_packed ? (const void*)fill_packed_kernel<false> : (const void*)fill_exact_kernel<false>;
     for (const void* k : {kg, kd})
         HIP_TRY(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    const int threads = want_packed ? (int)kPackThreads : 1024;
-    HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kg, threads, lds));
+    HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kg, (int)kPackThreads, lds));
     if (per_cu < 1) return CBH_OK;
     s->pk_lds = lds;
-    s->pk_tiles = (s->W + kPackTileWords - 1) / kPackTileWords;
-    const uint32_t planes = want_packed ? 1u : s->C;
-    s->pk_ranges = pick_ranges((uint32_t)cus, (uint32_t)per_cu, s->pk_tiles * planes, s->n);
-    if (want_packed) pick_packed_ranges(s, (uint32_t)cus, (uint32_t)per_cu);
+    s->pk_tiles = (s->W + TWM - 1) / TWM;
+    pick_tile_ranges(s, (uint32_t)cus, (uint32_t)per_cu, TWM);
     if (want_packed) {
         // CBH_PACK_SWAP (1, 2, 4, 8): blocks of rows between two swaps; each doubling costs
         // one bit of a row's rounded value (a measurement knob).  Default 4: 18-bit rows (rows
@@ -698,19 +711,27 @@ int plan_fill_mode(cbh_session* s) {
             if (v2 == 1 || v2 == 2 || v2 == 4 || v2 == 8) s->pk_swap = (uint32_t)v2;
         }
         s->pack_bits = kPackBitsSwap1 - (s->pk_swap >= 2) - (s->pk_swap >= 4) - (s->pk_swap >= 8);
+        CHECK(dalloc(&s->spack, (size_t)s->n));
     }
-    CHECK(dalloc(&s->spack, (size_t)s->n * planes));
-    CHECK(dalloc(&s->sseq, (size_t)s->n * planes));
-    if (want_packed) {   // the packed fill reads tile-major rows (the row-major words stay for a fallback)
-        const uint32_t tw_last = s->W - kPackTileWords * (s->pk_tiles - 1);
-        const uint64_t words = (uint64_t)s->n * (kPackTileWords * (s->pk_tiles - 1) + packed_slice_words(tw_last));
-        CHECK(dalloc(&s->trows, words));
-        pack_tiles_kernel<<<grid_for(words, 256), 256, 0, s->stream>>>(s->cols, s->n, s->F, s->W, s->trows, words);
-        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess)
-            return fail(CBH_ERR_DEVICE, "tile-major packing failed");
-    }
+    // the listed rows' statistics in idx order (packed: one word per row; tiled: both channels;
+    // CBH_EX_STATS=idx, a measurement knob, has the tiled fill read them through the listed rows'
+    // indices instead: gathered levels 360 -> 400-650 us at config 2).  CBH_EX_SETS=2: two
+    // blocks in flight in the tiled fill's full loop instead of three (a measurement knob; three
+    // took config 2's fill from 443 to 436 us per launch)
+    const char* es = std::getenv("CBH_EX_STATS");
+    if (want_packed || !(es && std::string(es) == "idx"))
+        CHECK(dalloc(&s->sseq, (size_t)s->n * (want_packed ? 1u : 2u)));
+    if (const char* ns = std::getenv("CBH_EX_SETS")) s->ex_sets = std::string(ns) == "2" ? 2u : 3u;
+    // tile-major row words: each tile's rows contiguous (the row-major words stay for the
+    // gathered levels and the other fills)
+    const uint32_t tw_last = s->W - TWM * (s->pk_tiles - 1);
+    const uint64_t words = (uint64_t)s->n * (TWM * (s->pk_tiles - 1) + packed_slice_words(tw_last));
+    CHECK(dalloc(&s->trows, words));
+    pack_tiles_kernel<<<grid_for(words, 256), 256, 0, s->stream>>>(s->cols, s->n, s->F, s->W, s->trows, words, TWM);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess)
+        return fail(CBH_ERR_DEVICE, "tile-major packing failed");
     s->packed = want_packed;
-    s->split = !want_packed;
+    s->tiled = want_tiled;
     return CBH_OK;
 }
 
@@ -1472,9 +1493,6 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
     else if (s->packed)
         pack_stats_fixed_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack,
                                                                          (1ll << s->pack_bits) - 1);
-    else if (s->split)
-        planar_stats_fixed_kernel<C><<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales,
-                                                                           (long long*)s->spack);
     else
         quantize_stats_kernel<C><<<grid_for(n * C, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales);
     HIP_TRY(hipGetLastError());
@@ -1515,14 +1533,15 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             fill_packed_kernel<true><<<s->pk_gath.blocks, kPackThreads, s->pk_lds, st>>>(
                 s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_gath.tiles16, s->F, s->B,
                 s->pk_gath.ranges, 0u, cur, s->pk_swap, s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh);
-        else if (s->split && level == 0)
-            fill_split_kernel<false><<<s->pk_ranges * s->pk_tiles * C, 1024, s->pk_lds, st>>>(
-                s->rows, s->Ws, s->W, n, nullptr, nullptr, (const long long*)s->spack, nullptr, C, s->pk_tiles,
-                s->F, s->B, s->pk_ranges, cur);
-        else if (s->split)
-            fill_split_kernel<true><<<s->pk_ranges * s->pk_tiles * C, 1024, s->pk_lds, st>>>(
-                s->rows, s->Ws, s->W, n, lidx, lplan, (const long long*)s->spack, (const long long*)s->sseq, C,
-                s->pk_tiles, s->F, s->B, s->pk_ranges, cur);
+        else if (s->tiled && level == 0)
+            fill_exact_kernel<false><<<s->pk_dense.blocks, kExThreads, s->pk_lds, st>>>(
+                s->trows, s->W, n, nullptr, nullptr, (const long long*)s->sstat, nullptr, s->pk_dense.tiles16, s->F,
+                s->B, s->pk_dense.ranges, s->pk_dense.ranges_n, cur, nullptr, 0u, s->ex_sets);
+        else if (s->tiled)
+            fill_exact_kernel<true><<<s->pk_gath.blocks, kExThreads, s->pk_lds, st>>>(
+                s->trows, s->W, n, lidx, lplan, (const long long*)s->sstat, (const long long*)s->sseq,
+                s->pk_gath.tiles16, s->F, s->B, s->pk_gath.ranges, s->pk_gath.ranges_n, cur,
+                s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh, s->ex_sets);
         else if (s->pkk) {
             const size_t lds = (size_t)kPkkCells * sizeof(unsigned long long);
             const unsigned grid = s->pkk_ranges * s->pkk_tiles;
@@ -1583,6 +1602,9 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             HIP_TRY(hipGetLastError());
         }
         CHECK(s->stage_end());
+        if (s->hist_cap)   // the level's histograms as the scorer reads them (inspection only)
+            HIP_TRY(hipMemcpyAsync(s->hist_cap + s->hist_cap_off[level], cur, sizeof(long long) * per_leaf * n_leaves,
+                                   hipMemcpyDeviceToDevice, st));
         // ---- score + argmax ----
         if (s->ctr_n) CHECK(s->ctr_dev ? ctr_level_weights_dev(s, level) : ctr_level_weights(s, level));
         CHECK(s->stage_begin(kStScore));
@@ -1642,9 +1664,15 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         if (!last) {
             plan_scan_kernel<<<2u << level, 1024, 0, st>>>(s->cnt, 4 * NB, s->totals);
             HIP_TRY(hipGetLastError());
-            compact_kernel<<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->totals, s->plans + level, s->idx,
-                                               (s->packed || s->split) ? s->spack : nullptr,
-                                               (s->packed || s->split) ? s->sseq : nullptr, s->split ? C : 1u);
+            if (s->packed)   // the listed rows' packed statistic
+                compact_kernel<1><<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->totals, s->plans + level,
+                                                      s->idx, s->spack, s->sseq);
+            else if (s->tiled && s->sseq)   // both fixed-point channels of the listed rows
+                compact_kernel<2><<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->totals, s->plans + level,
+                                                      s->idx, (const unsigned long long*)s->sstat, s->sseq);
+            else
+                compact_kernel<0><<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->totals, s->plans + level,
+                                                      s->idx, nullptr, nullptr);
             HIP_TRY(hipGetLastError());
         }
         CHECK(s->stage_end());
@@ -1732,7 +1760,7 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         s->pin_ctr_used[s->ctr_n] = ctr_all_used(s) ? 1 : 0;   // then no phantom count is needed
         HIP_TRY(hipMemcpyAsync(s->ctr_used_dev, s->pin_ctr_used, s->ctr_n + 1, hipMemcpyHostToDevice, st));
     }
-    const bool replay = s->pending && !s->cfg.profile && !s->graph_off && ctr_static;
+    const bool replay = s->pending && !s->cfg.profile && !s->graph_off && ctr_static && !s->hist_cap;
     hipGraphExec_t& ge = s->tree_graph[use_host_sample ? 1 : 0];
     if (replay && !ge) record_tree<K>(s, use_host_sample);
     if (replay && ge) {
@@ -1956,7 +1984,7 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
     // traffic accounting of the fill launches (algorithmic bytes per launch)
     // (sparse entries: the first 16 codes of every tile, 32 bytes; second slots not counted)
     const double wbytes = s->pks ? 32.0 * s->pkk_tiles : 4.0 * s->W,
-                 sbytes = s->packed ? 8.0 : s->pkk ? 8.0 * ((s->C + 1) / 2) : 8.0 * s->C;   // split: 8 per channel
+                 sbytes = s->packed ? 8.0 : s->pkk ? 8.0 * ((s->C + 1) / 2) : 8.0 * s->C;
     const double per_leaf_bytes = (double)s->F * s->B * s->C * 8.0;
     for (uint32_t l = 0; l < s->depth; ++l) {
         const uint64_t V = l == 0 ? bounds.sampled_rows : plans[l - 1].rows;
@@ -1997,7 +2025,7 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
     if (!s || !out) return fail(CBH_ERR_INVALID_ARG, "null argument");
     *out = s->stats;
     out->skip_features = s->n_skip;
-    out->fill_mode = s->packed ? 1u : s->split ? 2u : s->pks ? 4u : s->pkk ? 3u : 0u;
+    out->fill_mode = s->packed ? 1u : s->tiled ? 2u : s->pks ? 4u : s->pkk ? 3u : 0u;
     out->fill_pack_bits = (s->packed || s->pkk) ? s->pack_bits : 0;
     return CBH_OK;
 }
@@ -2046,6 +2074,52 @@ int cbh_session_read_ctr_bins(const cbh_session* s, int32_t averaging, uint8_t* 
 int cbh_session_set_profile(cbh_session* s, int32_t on) {
     if (!s) return fail(CBH_ERR_INVALID_ARG, "session is null");
     s->cfg.profile = on ? 1 : 0;
+    return CBH_OK;
+}
+
+int cbh_session_capture_hists(cbh_session* s, int32_t on) {
+    if (!s) return fail(CBH_ERR_INVALID_ARG, "session is null");
+    if (s->pairwise) return fail(CBH_ERR_UNSUPPORTED, "pairwise sessions score pair statistics");
+    if (!on) {
+        dfree(s->hist_cap);
+        return CBH_OK;
+    }
+    if (s->hist_cap) return CBH_OK;
+    const size_t per_leaf = (size_t)s->F * s->B * s->C;
+    size_t off = 0;
+    for (uint32_t l = 0; l < s->depth; ++l) {
+        s->hist_cap_off[l] = off;
+        off += per_leaf << l;
+    }
+    s->hist_cap_off[s->depth] = off;
+    return dalloc(&s->hist_cap, off);
+}
+
+int cbh_session_level_hist(const cbh_session* s, uint32_t level, double* out, uint64_t n_cells) {
+    if (!s || !out) return fail(CBH_ERR_INVALID_ARG, "null argument");
+    if (!s->hist_cap) return fail(CBH_ERR_INVALID_ARG, "histogram capture is off");
+    if (level >= s->depth) return fail(CBH_ERR_OUT_OF_RANGE, "level >= depth");
+    const uint32_t F = s->F, B = s->B, C = s->C;
+    const size_t cells = ((size_t)F * B * C) << level;
+    if (n_cells != cells) return fail(CBH_ERR_LENGTH_MISMATCH, "n_cells != 2^level * F * n_bins * C");
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    std::vector<long long> h(cells);
+    HIP_TRY(hipMemcpy(h.data(), s->hist_cap + s->hist_cap_off[level], sizeof(long long) * cells, hipMemcpyDeviceToHost));
+    Scales sc{};
+    HIP_TRY(hipMemcpy(&sc, s->scales, sizeof(Scales), hipMemcpyDeviceToHost));
+    // [leaf][ch][f][bin] prefix sums -> [leaf][f][bin][ch] bin sums (the reference's layout,
+    // histogram.rs:176-177), channel K the weight
+    for (size_t leaf = 0; leaf < ((size_t)1 << level); ++leaf)
+        for (uint32_t ch = 0; ch < C; ++ch) {
+            const double inv = ch == C - 1 ? sc.inv[kScoreW] : sc.inv[kScoreDer];
+            for (uint32_t f = 0; f < F; ++f) {
+                const long long* row = h.data() + ((leaf * C + ch) * F + f) * B;
+                for (uint32_t b = 0; b < B; ++b) {
+                    const long long v = row[b] - (b ? row[b - 1] : 0);
+                    out[((leaf * F + f) * B + b) * C + ch] = (double)v * inv;
+                }
+            }
+        }
     return CBH_OK;
 }
 

@@ -199,17 +199,23 @@ typedef struct {
     uint64_t fill_launches;
     uint64_t fill_rows;           /* rows visited by fill launches (sum of V) */
     uint64_t fill_row_features;   /* sum of V * n_features */
-    double fill_bytes;            /* algorithmic bytes V*(W*4 + 8*(K+1) + 4) + H */
+    double fill_bytes;            /* algorithmic bytes V*(W*4 + S + 4) + H: S bytes of statistics per row,
+                                     8*(K+1) for the exact fills, 8 for the rounded packed fill, 8*ceil((K+1)/2)
+                                     for the packed multi-channel fills; the 4 bytes of a row index at the
+                                     levels that gather rows through the partition's index list; H the
+                                     histogram cells built x 8 */
     uint64_t trees;
     uint64_t skip_features;       /* features whose dominant bin the fill leaves out */
     double quantize_ms;           /* raw float channel: device quantize launches at open */
     uint64_t quantize_launches;
     double quantize_bytes;        /* algorithmic bytes: 4 read + 1 written per value + borders */
-    uint32_t fill_mode;           /* 0: 32-feature tiles, both channels per workgroup; 1: packed 64-feature
-                                     tiles (one 64-bit atomic carries both channels); 2: channel-split
-                                     64-feature tiles (one workgroup per channel); 3: packed multi-channel
-                                     32-feature tiles (K > 1: two channels per 64-bit atomic); 4: the same
-                                     cells over sparse entries (a row per 16-lane DPP row, one lane per
+    uint32_t fill_mode;           /* 0: generic fill (32-feature tiles, one exact 64-bit atomic per channel,
+                                     any K); 1: rounded packed fill (K = 1, 64-feature tiles, both channels
+                                     rounded to 18-bit rows in one 64-bit atomic); 2: tiled exact fill (K = 1,
+                                     32-feature tiles, one exact 64-bit atomic per channel, DPP-broadcast
+                                     statistics); 3: packed multi-channel fill (K > 1, 32-feature tiles, two
+                                     channels rounded to 20-bit rows per 64-bit atomic); 4: the same cells
+                                     over sparse entries (a row per 16-lane DPP row, one lane per
                                      non-dominant (feature, bin)) */
     int32_t fill_pack_bits;       /* packed fills: bits of a row's rounded channel value (|q| < 2^bits) */
 } cbh_stats;
@@ -302,6 +308,15 @@ int cbh_session_read_ctr_bins(const cbh_session* s, int32_t averaging, uint8_t* 
  * per-kernel timing is a build-time diagnostic). */
 int cbh_session_set_profile(cbh_session* s, int32_t on);
 void cbh_session_reset_stats(cbh_session* s);
+
+/* Inspection entries (no counterpart in the reference): with capture on, every later tree
+ * keeps its level histograms as the split scorer read them (trees then run eagerly, not as a
+ * recorded graph; pairwise sessions decline).  cbh_session_level_hist returns level `level` of
+ * the last tree as f64 bin sums in the reference's layout [2^level leaves][F][n_bins][K+1]
+ * (histogram.rs:176-177; channel K the weight), each exact integer sum times 2^-S of its
+ * channel; n_cells must be 2^level * F * n_bins * (K+1). */
+int cbh_session_capture_hists(cbh_session* s, int32_t on);
+int cbh_session_level_hist(const cbh_session* s, uint32_t level, double* out, uint64_t n_cells);
 
 /* Release the session.  Mirrors end_device_training (runtime.rs:1648). */
 int cbh_session_end(cbh_session* s);

@@ -96,6 +96,69 @@ def test_histogram_fill_matches_bruteforce(K):
         np.testing.assert_allclose(got, exp, rtol=1e-9, atol=1e-9)
 
 
+FILL_MODE = {"generic": 0, "packed": 1, "tiled": 2, "pkk": 3, "pks": 4}
+
+
+@pytest.mark.parametrize("fill,rel", [("generic", 1e-9), ("tiled", 1e-9), ("packed", REL)])
+def test_level_histograms_match_oracle_config2_shape(fill, rel, monkeypatch):
+    """Every level histogram of one config-2-shaped tree (Logloss, 200 features, 254 borders,
+    Bayesian-like sample weights, depth 6) under each K = 1 fill, cell by cell against the CPU
+    restatement's level histograms (histogram.rs:643-698): within 1e-9 of the level's largest
+    cell for the exact fills (integer sums of rows rounded at 2^-37), 1e-5 for the rounded packed
+    fill.  The tree's splits equal the oracle's, so every level compares the same leaves."""
+    monkeypatch.setenv("CBH_FILL", fill)
+    d = datagen.config2(n_rows=200_000)
+    bins, nb, y = d["bins"], d["n_borders"], d["target"]
+    F, n = bins.shape
+    B = int(nb.max()) + 1
+    s = -np.log1p(-np.random.default_rng(3).random(n))   # Bayesian (T = 1) sample weights
+    o = O.grow_tree(bins, nb, (y - 0.5) * s, s, 6, "Cosine", 3.0, want_hists=True)
+    be = cb.HipBackend()
+    assert be.begin_device_training("Logloss", 6, True, 1, "Cosine", bins, None, n, F, B, 0.1, 3.0,
+                                    sample_from_host=True, real_folds=nb + 1)
+    try:
+        assert be.stats()["fill_mode"] == FILL_MODE[fill]
+        be.capture_hists()
+        t = be.grow_tree_on_device(target=y, sample=s)
+        assert [(f, b) for f, b, _ in t["splits"]] == [tuple(x) for x in o["splits"].tolist()]
+        for level in range(6):
+            _close(be.level_hist(level, F, B), o["hists"][level], rel=rel)
+    finally:
+        be.end_device_training()
+
+
+@pytest.mark.parametrize("fill,rel", [("generic", 1e-9), ("pkk", REL), ("pks", REL)])
+def test_level_histograms_match_oracle_config5_shape(fill, rel, monkeypatch):
+    """Every level histogram of one config-5-shaped tree (MultiClass K = 10, 256 features with
+    70% zeros, 64 borders, depth 8) under each K > 1 fill, cell by cell against the CPU
+    restatement (11 channels: the ten softmax ders at approx 0, then the weight)."""
+    if fill == "generic":
+        monkeypatch.setenv("CBH_FILL", "generic")
+    else:
+        monkeypatch.setenv("CBH_FILL", "packed")
+        monkeypatch.setenv("CBH_PKK_SPARSE", "on" if fill == "pks" else "off")
+    K, depth = 10, 8
+    d = datagen.config5(n_rows=20_000, n_features=256)
+    bins, nb, y = d["bins"], d["n_borders"], d["target"]
+    F, n = bins.shape
+    B = int(nb.max()) + 1
+    der = -np.full((K, n), 1.0 / K)
+    der[y.astype(np.int64), np.arange(n)] += 1.0
+    o = O.grow_tree(bins, nb, der, np.ones(n), depth, "Cosine", 3.0, want_hists=True)
+    be = cb.HipBackend()
+    assert be.begin_device_training("MultiClass", depth, True, 1, "Cosine", bins, None, n, F, B, 0.1, 3.0,
+                                    approx_dim=K, leaf_method="Newton", real_folds=nb + 1)
+    try:
+        assert be.stats()["fill_mode"] == FILL_MODE[fill]
+        be.capture_hists()
+        t = be.grow_tree_on_device(target=y)
+        assert [(f, b) for f, b, _ in t["splits"]] == [tuple(x) for x in o["splits"].tolist()]
+        for level in range(depth):
+            _close(be.level_hist(level, F, B), o["hists"][level], rel=rel)
+    finally:
+        be.end_device_training()
+
+
 # -------------------------------------------------------------------------- one tree
 @pytest.mark.parametrize("loss", ["rmse", "logloss"])
 def test_depth6_golden_tree_on_gpu(loss):
@@ -579,24 +642,24 @@ def _assert_same_fit(exp, splits, leaves, approx):
     _close(approx, exp["approx"])
 
 
-@pytest.mark.parametrize("fill", ["auto", "packed"])
+@pytest.mark.parametrize("fill", ["auto", "tiled", "packed"])
 def test_config1_full_size_matches_oracle(fill, monkeypatch):
     """Config 1 at its full size: RMSE, 100k x 50, 128 borders, depth 6, 100 trees (the
-    default two-channel fill below 2^20 rows, and the packed fill forced)."""
+    default generic fill below 2^20 rows, and the tiled exact and rounded packed fills forced)."""
     if fill != "auto":
         monkeypatch.setenv("CBH_FILL", fill)
     d = datagen.config1()
     _assert_same_fit(*_fit_both(d, d["params"]["iterations"]))
 
 
-@pytest.mark.parametrize("layout", ["auto", "bin", "feature", "packed", "split"])
+@pytest.mark.parametrize("layout", ["auto", "bin", "feature", "packed", "tiled"])
 def test_config2_reduced_matches_oracle(layout, monkeypatch):
     """Config 2 shape (Logloss, 200 features, 254 borders, depth 6, Bayesian T=1) at 200k rows,
-    with each fill: the 32-feature two-channel fill in both LDS layouts (bin-major is what it
-    uses at 10M rows), the packed 64-feature fill (the default from 2^20 rows: one 64-bit atomic
-    carries both channels, 18-bit rounded rows) and the channel-split 64-feature fill."""
+    with each fill: the generic fill in both LDS layouts, the tiled exact fill (the default from
+    2^20 rows) and the rounded packed fill (one 64-bit atomic carries both channels, 18-bit
+    rounded rows)."""
     if layout in ("bin", "feature"):
-        monkeypatch.setenv("CBH_FILL", "exact")
+        monkeypatch.setenv("CBH_FILL", "generic")
         monkeypatch.setenv("CBH_FILL_LAYOUT", layout)
     elif layout != "auto":
         monkeypatch.setenv("CBH_FILL", layout)
@@ -605,17 +668,18 @@ def test_config2_reduced_matches_oracle(layout, monkeypatch):
 
 
 def test_config2_full_size_first_trees_match_oracle():
-    """Config 2 at its full 10M x 200 size (the packed fill): the first ten trees (splits, leaf
-    values, approximant) against the oracle on 16 host threads; about a minute, most of it data
-    generation and the oracle."""
+    """Config 2 at its full 10M x 200 size (the tiled exact fill): the first ten trees (splits,
+    leaf values, approximant) against the oracle on 16 host threads; about a minute, most of it
+    data generation and the oracle."""
     d = datagen.config2()
     _assert_same_fit(*_fit_both(d, 10, n_threads=16))
 
 
-def test_config2_full_size_packed_equals_two_channel_fill(monkeypatch):
-    """Config 2 at 10M x 200 over 40 trees: the packed fill (18-bit rounded rows in 32-bit
-    fields) chooses the same split at every level as the two-channel fill (61-bit exact sums),
-    so the trees, leaves and approximant are identical."""
+def test_config2_full_size_all_trees_tiled_equals_generic_fill(monkeypatch):
+    """Config 2 at 10M x 200 over all 200 trees: the tiled exact fill and the generic fill sum
+    the same rows at the same fixed-point scale, so every histogram cell, split, leaf and the
+    approximant are bit-identical (a mistake in the tiled fill's lanes, copies or ranges that
+    dropped or doubled a row would change a sum)."""
     d = datagen.config2()
     P = dict(d["params"])
     nb = d["n_borders"]
@@ -623,32 +687,34 @@ def test_config2_full_size_packed_equals_two_channel_fill(monkeypatch):
               l2_leaf_reg=P["l2_leaf_reg"], score=P["score"], leaf_method=P["leaf_method"],
               bootstrap_type=P["bootstrap_type"], boost_from_average=P["boost_from_average"],
               bagging_temperature=P.get("bagging_temperature", 1.0), random_seed=P.get("random_seed", 0))
+    iters = P["iterations"]
     out = {}
-    for mode in ("exact", "packed"):
+    for mode in ("generic", "tiled"):
         monkeypatch.setenv("CBH_FILL", mode)
         tr = cb.Trainer(d["bins"], int(nb.max()) + 1, d["target"], real_folds=nb + 1, **kw)
         try:
-            assert tr.stats()["fill_mode"] == (0 if mode == "exact" else 1)
-            sp, lv = tr.fit(40)
+            assert tr.stats()["fill_mode"] == FILL_MODE[mode]
+            sp, lv = tr.fit(iters)
             out[mode] = (sp, lv, tr.approx())
         finally:
             tr.close()
-    (s0, l0, a0), (s1, l1, a1) = out["exact"], out["packed"]
-    for it in range(40):
+    (s0, l0, a0), (s1, l1, a1) = out["generic"], out["tiled"]
+    for it in range(iters):
         assert np.array_equal(s0[it], s1[it]), f"tree {it} splits differ"
     assert np.array_equal(l0, l1)
     assert np.array_equal(a0, a1)
 
 
-@pytest.mark.parametrize("layout", ["bin", "feature", "packed", "split"])
+@pytest.mark.parametrize("layout", ["bin", "feature", "packed", "tiled"])
 @pytest.mark.parametrize("F,B,K", [(37, 17, 1), (5, 256, 1), (65, 33, 3), (33, 2, 1), (100, 255, 1),
-                                   (129, 256, 1), (64, 255, 1)])
+                                   (129, 256, 1), (64, 255, 1), (36, 40, 1), (44, 129, 1)])
 def test_fill_layouts_ragged_shapes_match_oracle(layout, F, B, K, monkeypatch):
-    """Every fill on ragged tiles: feature counts that leave a short last tile or a partial
-    word, 2 to 256 bins, K = 1 and a 3-class MultiClass (4 channels; the packed fill is K = 1
-    only, so that case runs the two-channel fill)."""
+    """Every fill on ragged tiles: feature counts that leave a short last tile (1 to 7 words of
+    the tiled fill's 8: a narrow 1- or 2-word tile runs its own loop) or a partial word, 2 to 256
+    bins, K = 1 and a 3-class MultiClass (4 channels; "packed" then means the packed
+    multi-channel fill, "tiled" the generic fill)."""
     if layout in ("bin", "feature"):
-        monkeypatch.setenv("CBH_FILL", "exact")
+        monkeypatch.setenv("CBH_FILL", "generic")
         monkeypatch.setenv("CBH_FILL_LAYOUT", layout)
     else:
         monkeypatch.setenv("CBH_FILL", layout)
@@ -670,7 +736,7 @@ def test_fill_layouts_ragged_shapes_match_oracle(layout, F, B, K, monkeypatch):
     _assert_same_fit(*_fit_both(d, 3))
 
 
-@pytest.mark.parametrize("loss,fill", [("PairLogit", "auto"), ("PairLogit", "packed"),
+@pytest.mark.parametrize("loss,fill", [("PairLogit", "auto"), ("PairLogit", "tiled"), ("PairLogit", "packed"),
                                        ("PairLogitPairwise", "auto")])
 def test_config3_reduced_matches_oracle(loss, fill, monkeypatch):
     """Config 3 shape (groups of 20, ~10 pairs per group, 100 features, 254 borders, depth 6);
