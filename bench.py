@@ -234,6 +234,8 @@ def main():
     ap.add_argument("--cpu-trees", type=int, default=-1)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--bootstrap", default="",
+                    help="override the config's bootstrap type (a measurement option; the line then names it)")
     ap.add_argument("--prep", action="store_true",
                     help="measure float-feature preparation (borders, quantize) instead of boosting")
     ap.add_argument("--copy-calib", type=int, default=0,
@@ -270,6 +272,8 @@ def main():
     raw = "floats" in data
     bins, nb, y = data.get("bins"), data["n_borders"], data["target"]
     P = data["params"]
+    if args.bootstrap:
+        P = dict(P, bootstrap_type=args.bootstrap)
     F, n = (data["floats"] if raw else bins).shape
     n_bins = int(nb.max()) + 1
     kw = _train_kwargs(P)
@@ -327,7 +331,7 @@ def main():
     # cap is the contiguous (conflict-free) 64-bit LDS atomic rate measured on this GPU, the
     # pattern the fills' rotated lane layouts reach
     K = kw["approx_dim"] if P["loss"] == "MultiClass" else 1
-    per_pair = {1: 1, 3: (K + 2) // 2, 4: (K + 2) // 2}.get(st["fill_mode"], K + 1)
+    per_pair = {1: 1, 3: (K + 2) // 2, 4: (K + 2) // 2, 5: 1}.get(st["fill_mode"], K + 1)
     lds = None
     rates = _lds_rates()
     if "contiguous_u64" in rates and fill_s > 0:
@@ -367,7 +371,7 @@ def main():
         cpu["splits_match_gpu"] = bool(np.array_equal(first, exp["splits"]))
 
     fill_kernel = {0: "fill_kernel", 1: "fill_packed_kernel", 2: "fill_exact_kernel",
-                   3: "fill_pkk_kernel", 4: "fill_pks_kernel"}[st["fill_mode"]]
+                   3: "fill_pkk_kernel", 4: "fill_pks_kernel", 5: "fill_packed_kernel"}[st["fill_mode"]]
     names = {1: "config1: RMSE, no bootstrap, depth 6, 128 borders",
              2: ("config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 GreedyLogSum borders selected on the "
                  "device from the raw f32 columns, quantized on the device" if raw else
@@ -392,10 +396,13 @@ def main():
                  2: "tiled exact 32-feature tiles (one 64-bit atomic per channel, full fixed-point scale)",
                  3: f"packed multi-channel 32-feature tiles (two channels per word, {st['fill_pack_bits']}-bit rows)",
                  4: f"packed multi-channel 32-feature tiles over sparse entries (a row per 16-lane DPP row, "
-                    f"two channels per word, {st['fill_pack_bits']}-bit rows)"
+                    f"two channels per word, {st['fill_pack_bits']}-bit rows)",
+                 5: "count-packed 64-feature tiles (der at >= 2^-30 and the integer weight in one 64-bit atomic)",
                  }[st["fill_mode"]],
         "data": f"synthetic (seeded; datagen.config{args.config}{'_raw' if raw else ''})",
-        "config": {"workload": names[args.config], "rows": n, "features": F, "depth": P["depth"],
+        "config": {"workload": names[args.config] + (f" (bootstrap overridden: {args.bootstrap})"
+                                                     if args.bootstrap else ""),
+                   "rows": n, "features": F, "depth": P["depth"],
                    "parallelism": "single GPU"},
         "hist_rows_features_per_s": round(st["fill_row_features"] / fill_s, 1) if fill_s else None,
         "hist_rows_features_per_s_logical": round(n * F * P["depth"] * prof_steps / fill_s, 1) if fill_s else None,

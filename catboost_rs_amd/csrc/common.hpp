@@ -143,7 +143,8 @@ struct Scales {
     double mul[kNumScales];   // 2^S
     double inv[kNumScales];   // 2^-S
     int32_t shift[kNumScales];
-    int32_t pad;
+    int32_t pk_k;             // count-packed fill: bits of the weight field of a packed cell
+    int32_t pk_swap;          // count-packed fill: blocks of rows between two swaps
 };
 
 // Per-tree bound accumulators: sum of ceil(|v| * 2^kBoundShift) per slot (integers, so

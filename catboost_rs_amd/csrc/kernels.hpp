@@ -353,14 +353,42 @@ static __global__ __launch_bounds__(256) void prepare_kernel(
     }
 }
 
+// Count-packed fill (K == 1, integer score weights).  A row's two score channels travel in
+// one 64-bit word p = q_der * 2^k + q_w (mod 2^64): q_w the row's integer score weight (0 or 1
+// without object weights) in the low k bits, q_der = round(der * w * s * 2^S) in the high
+// 64 - k bits.  A cell decodes as lo = p mod 2^k (a sum of non-negative weights: it never
+// borrows from the der field) and der = (p - lo) / 2^k, exactly, while at most D rows have
+// landed since the cell was emptied: D * wmax < 2^k and D * max|q_der| < 2^(63 - k).  With
+// swaps every `swap` blocks of 1024 rows, D = 2 * 1024 * swap (atomics of the next period may
+// land before a swap).  The plan takes the longest swap period of 4, 2, 1 blocks whose der
+// scale S = 62 - k - log2 D - e is at least 30 -- the reference's per-row resolution 2^-30
+// (kernels.rs:4145-4150) -- for the largest row |der * w * s| < 2^e; failing that, one block
+// and its S (every sum stays exact; only the per-row step is coarser).
+struct CountPack {
+    int k, swap, shift;
+};
+__host__ __device__ inline CountPack count_pack_plan(int e, unsigned long long wmax) {
+    CountPack cp{1, 1, 0};
+    for (int sw = 4; sw >= 1; sw >>= 1) {
+        const int lg = sw == 4 ? 13 : sw == 2 ? 12 : 11;   // log2 D
+        int k = 1;
+        while (k < 40 && (1ull << k) <= (wmax << lg)) ++k;   // D * wmax < 2^k
+        cp = CountPack{k, sw, 62 - k - lg - e};
+        if (cp.shift >= 30) break;
+    }
+    return cp;
+}
+
 // Sum the per-block partials (integers: exact in any order) and pick S per slot so that
 // 2^S * sum|v| <= 2^61: no partial sum of rounded values can overflow int64.  With
 // pack_bits > 0 the two score slots instead take S = pack_bits - e for the largest row
 // bound M < 2^e, so every rounded row value fits pack_bits bits (|q| <= 2^pack_bits): the
-// packed fill's 32-bit fields.
+// rounded packed fill's 32-bit fields.  With count set (the count-packed fill: integer score
+// weights) the weight slot takes S = 0 (the weights themselves) and the der slot the finest
+// scale whose packed cells stay decodable (count_pack_plan).
 static __global__ __launch_bounds__(256) void scales_kernel(const unsigned long long* __restrict__ partials,
                                                            uint32_t n_blocks, Bounds* __restrict__ b,
-                                                           Scales* __restrict__ sc, int pack_bits) {
+                                                           Scales* __restrict__ sc, int pack_bits, int count) {
     __shared__ unsigned long long red[256][7];
     unsigned long long acc[7] = {0, 0, 0, 0, 0, 0, 0};
     for (uint32_t i = threadIdx.x; i < n_blocks; i += blockDim.x) {
@@ -390,6 +418,16 @@ static __global__ __launch_bounds__(256) void scales_kernel(const unsigned long 
         if (bound > 0.0) frexp(bound, &e);   // bound < 2^e
         int s = (packed ? pack_bits : 61) - e;
         if (s > 100) s = 100;
+        if (count && k == kScoreW) s = 0;
+        if (count && k == kScoreDer) {
+            int mx = -20;   // largest row |der * w * s| < 2^mx
+            const double mb = (double)acc[5] / (double)(1 << kBoundShift);
+            if (mb > 0.0) frexp(mb, &mx);
+            const CountPack cp = count_pack_plan(mx, acc[6] >> kBoundShift);
+            s = min(s, cp.shift);
+            sc->pk_k = cp.k;
+            sc->pk_swap = cp.swap;
+        }
         sc->shift[k] = s;
         sc->mul[k] = ldexp(1.0, s);
         sc->inv[k] = ldexp(1.0, -s);
@@ -737,12 +775,23 @@ __device__ __forceinline__ unsigned long long ldq(__amdgpu_buffer_rsrc_t r, uint
     return (unsigned long long)v[0] | ((unsigned long long)v[1] << 32);
 }
 
+// Decode a swapped cell of the count-packed fill: the weight field's low kb bits, the der
+// field the rest (an arithmetic shift of the signed difference).
+__device__ __forceinline__ void unpack_add_count(unsigned long long v, uint32_t kb, long long& acc_d,
+                                                 long long& acc_w) {
+    const unsigned long long lo = v & ((1ull << kb) - 1ull);
+    acc_w += (long long)lo;
+    acc_d += (long long)(v - lo) >> kb;
+}
+
 // Swap the cells a thread owns with zero and add their decoded fields to its registers.
 // The cells of thread t are t + k * kPackThreads, k < kPackOwn: the LDS always holds 256 bin
 // rows, so every thread owns kPackOwn cells and the swaps carry no per-cell branch (the LDS
 // exchanges issue back to back and return together).  Cells of bins >= B, or of columns
 // >= TF (the zero padding of a partial last word), are swapped too and never flushed.
-__device__ __forceinline__ void packed_swap(unsigned long long* __restrict__ pk,
+// kCount: the count-packed encoding (weight field of kb bits), else the rounded one.
+template <bool kCount>
+__device__ __forceinline__ void packed_swap(unsigned long long* __restrict__ pk, uint32_t kb,
                                             long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
     unsigned long long* c = pk + threadIdx.x;
     constexpr int kBatch = 4;   // exchanges in flight: few registers beyond the accumulators
@@ -752,7 +801,10 @@ __device__ __forceinline__ void packed_swap(unsigned long long* __restrict__ pk,
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) v[j] = atomicExch(c + (uint32_t)(k0 + j) * kPackThreads, 0ull);
 #pragma unroll
-        for (int j = 0; j < kBatch; ++j) unpack_add_nonneg(v[j], acc_d[k0 + j], acc_w[k0 + j]);
+        for (int j = 0; j < kBatch; ++j) {
+            if (kCount) unpack_add_count(v[j], kb, acc_d[k0 + j], acc_w[k0 + j]);
+            else unpack_add_nonneg(v[j], acc_d[k0 + j], acc_w[k0 + j]);
+        }
     }
 }
 
@@ -778,13 +830,13 @@ __device__ __forceinline__ unsigned long long row_bcast64(unsigned long long v) 
 // two blocks ahead), and the words of a half of block j+1 right after that half of block j is
 // consumed, so they are in flight across the other half, the barrier and the swap.  Positions
 // past the range carry a zero statistic (their atomics add nothing).
-template <bool kGather>
+template <bool kGather, bool kCount>
 __device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk,
                                              __amdgpu_buffer_rsrc_t rbase, uint32_t sh, uint32_t wl4,
                                              uint32_t wl, __amdgpu_buffer_rsrc_t idx,
                                              __amdgpu_buffer_rsrc_t sbase, uint32_t pos, uint32_t end,
                                              uint32_t n, uint32_t r0, const uint32_t* off8,
-                                             uint32_t swap_every,
+                                             uint32_t swap_every, uint32_t kb,
                                              long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
     static_assert(2 * kPackHalf * 64 == kPackIterRows && kPackHalf == 8, "block layout");
     uint32_t six = 0, six_n = 0, six_nn = 0;
@@ -866,7 +918,7 @@ __device__ __forceinline__ void packed_range(unsigned long long* __restrict__ pk
         if (++blk >= swap_every || !more) {
             blk = 0;
             __syncthreads();
-            packed_swap(pk, acc_d, acc_w);
+            packed_swap<kCount>(pk, kb, acc_d, acc_w);
         }
         if (!more) break;
         base = nb;
@@ -910,11 +962,12 @@ struct NarrowSet {
     unsigned long long sv;         // statistic of the staged position of the set's block
 };
 
+template <bool kCount>
 __device__ __forceinline__ void packed_range_narrow(unsigned long long* __restrict__ pk,
                                                     __amdgpu_buffer_rsrc_t rbase, uint32_t sh,
                                                     __amdgpu_buffer_rsrc_t sbase, uint32_t pos, uint32_t end,
                                                     uint32_t n, uint32_t r0, uint32_t wl, const uint32_t* off8,
-                                                    uint32_t swap_every,
+                                                    uint32_t swap_every, uint32_t kb,
                                                     long long (&acc_d)[kPackOwn], long long (&acc_w)[kPackOwn]) {
     constexpr uint32_t D = 4 * kPackIterRows;   // rows of four blocks
     const uint32_t j = wl >> 1, w = wl & 1u, w4 = 4u * w;
@@ -967,23 +1020,23 @@ __device__ __forceinline__ void packed_range_narrow(unsigned long long* __restri
         if (++since >= swap_rounds && rd + 1 < rounds) {
             since = 0;
             __syncthreads();
-            packed_swap(pk, acc_d, acc_w);
+            packed_swap<kCount>(pk, kb, acc_d, acc_w);
         }
     }
     __syncthreads();
-    packed_swap(pk, acc_d, acc_w);
+    packed_swap<kCount>(pk, kb, acc_d, acc_w);
 }
 
-template <bool kGather>
+template <bool kGather, bool kCount>
 static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     const uint32_t* __restrict__ rows /* tile-major (pack_tiles_kernel) */, uint32_t W,
     uint64_t n, const uint32_t* __restrict__ idx /* kGather: rows listed by the partition */,
     const LevelPlan* __restrict__ plan, const unsigned long long* __restrict__ spack /* [n] */,
     const unsigned long long* __restrict__ sseq /* nullable [V]: packed stats in idx order */,
     uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, uint32_t Gn, long long* __restrict__ hist,
-    uint32_t swap_every /* blocks of rows between two swaps: 2 * swap_every * kPackIterRows * 2^pack_bits <= 2^30 */,
+    uint32_t swap_every /* rounded: blocks of rows between two swaps: 2 * swap_every * kPackIterRows * 2^pack_bits <= 2^30 */,
     const uint32_t* __restrict__ rows_rm /* nullable, kGather: row-major words, 2^rm_sh bytes per row */,
-    uint32_t rm_sh) {
+    uint32_t rm_sh, const Scales* __restrict__ sc /* kCount: the tree's swap period and weight-field bits */) {
     constexpr uint32_t C = 2;
     extern __shared__ unsigned long long pk[];   // [B][64] packed cells
     // blocks: n_tiles tiles of the 16-lane row loop (64 features; the last one narrower when W
@@ -1036,6 +1089,10 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
     long long acc_d[kPackOwn], acc_w[kPackOwn];
 #pragma unroll
     for (int k = 0; k < kPackOwn; ++k) acc_d[k] = acc_w[k] = 0;
+    // the swap period and the weight field's bits: the count-packed fill takes the tree's (set on
+    // the device by scales_kernel, so a replayed tree follows its own data)
+    const uint32_t swap = kCount ? (uint32_t)sc->pk_swap : swap_every;
+    const uint32_t kb = kCount ? (uint32_t)sc->pk_k : 0u;
     __syncthreads();
     const uint32_t V = kGather ? plan->rows : (uint32_t)n;
     const uint32_t n_seg = kGather ? plan->n_parent : 1u;
@@ -1059,11 +1116,11 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
         const uint32_t slot = kGather ? plan->built[seg] : 0u;
         if (end > pos) {
             if (kGather || !narrow)
-                packed_range<kGather>(pk, rbase, sh, wl4, wl, ibase, sbase, pos, end, (uint32_t)n, r0, off8,
-                                      swap_every, acc_d, acc_w);
+                packed_range<kGather, kCount>(pk, rbase, sh, wl4, wl, ibase, sbase, pos, end, (uint32_t)n, r0, off8,
+                                              swap, kb, acc_d, acc_w);
             else   // a cell takes 1/8 of the rows a full tile's does: swaps 8x rarer
-                packed_range_narrow(pk, rbase, sh, sbase, pos, end, (uint32_t)n, r0, wl, off8, 8u * swap_every,
-                                    acc_d, acc_w);
+                packed_range_narrow<kCount>(pk, rbase, sh, sbase, pos, end, (uint32_t)n, r0, wl, off8, 8u * swap,
+                                            kb, acc_d, acc_w);
             // every contribution of the segment is in the registers now (the last swap follows
             // the last barrier); flush both channels (a narrow tile's 16 / TW copies summed), then
             // clear the cells and registers
@@ -1930,6 +1987,22 @@ static __global__ void pack_stats_fixed_kernel(const double* __restrict__ sstat,
         const long long qd = max(-qmax, min(qmax, to_fixed(sstat[2 * i], md)));
         const long long qw = max(-qmax, min(qmax, to_fixed(sstat[2 * i + 1], mw)));
         spack[i] = ((unsigned long long)qd << 32) + (unsigned long long)qw;
+    }
+}
+
+// Score channels f64 [n][2] -> one count-packed word per row: the der channel rounded at the
+// tree's scale in the high field, the integer score weight (w * s, an integer in a session that
+// takes this fill) in the low pk_k bits.
+static __global__ void pack_stats_count_kernel(const double* __restrict__ sstat, uint64_t n,
+                                               const Scales* __restrict__ sc,
+                                               unsigned long long* __restrict__ spack) {
+    const double md = sc->mul[kScoreDer];
+    const uint32_t kb = (uint32_t)sc->pk_k;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const long long qd = to_fixed(sstat[2 * i], md);
+        const unsigned long long qw = (unsigned long long)sstat[2 * i + 1];
+        spack[i] = ((unsigned long long)qd << kb) + qw;
     }
 }
 

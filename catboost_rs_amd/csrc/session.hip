@@ -196,6 +196,11 @@ struct cbh_session {
     // packed fill (64-feature tiles, both channels rounded to 18-bit rows in one 64-bit word,
     // one LDS atomic per (row, feature); a measurement knob)
     bool packed = false, tiled = false;
+    // count-packed fill (K == 1, integer score weights: bootstrap No or Bernoulli over integer
+    // object weights): the der channel at >= 2^-30 and the integer weight in one 64-bit word per
+    // row, one LDS atomic per (row, feature), 64-feature tiles (the rounded packed fill's loops)
+    bool count = false;
+    bool int_w = true;                         // every object weight is an integer in [0, 2^20]
     uint32_t ex_sets = 3;                      // tiled: blocks in flight of the full loop
     // packed multi-channel fill (K > 1: two score channels per 64-bit word, NP = ceil(C/2) planes)
     bool pkk = false;
@@ -560,8 +565,10 @@ void pick_tile_ranges(cbh_session* s, uint32_t cus, uint32_t per_cu, uint32_t TW
                 }
             }
         }
-        // short inputs: at least 4096 rows per range, so the per-workgroup flush stays small
-        const uint64_t min_rows = 4096;
+        // short inputs: at least min_rows rows per range, so the per-workgroup flush stays small
+        // (CBH_FILL_MIN_ROWS, a measurement knob)
+        uint64_t min_rows = 2048;
+        if (const char* mr = std::getenv("CBH_FILL_MIN_ROWS")) min_rows = std::max<uint64_t>(256, std::strtoull(mr, nullptr, 10));
         while (G > 1 && s->n / G < min_rows) G = G / 2;
         while (Gn > 1 && s->n / Gn < min_rows) Gn = Gn / 2;
         pl.tiles16 = nt;
@@ -673,27 +680,45 @@ int plan_pkk(cbh_session* s, const std::string& v) {
 // =tiled the tiled exact fill (K == 1), =packed the rounded packed fill (K == 1: 18-bit rows) or
 // the packed multi-channel fill (K > 1).
 int plan_fill_mode(cbh_session* s) {
-    s->packed = s->tiled = s->pkk = false;
+    s->packed = s->tiled = s->pkk = s->count = false;
     const char* e = std::getenv("CBH_FILL");
     const std::string v = e ? e : "";
     if (s->K > 1) return (v.empty() || v == "packed") ? plan_pkk(s, v) : CBH_OK;
-    if (v == "generic" || s->use_skip) return CBH_OK;
-    // (the packed decode takes non-negative weights: a negative object weight keeps the other fills)
+    if (v == "generic") return CBH_OK;
+    // integer score weights: no per-row sample beyond Bernoulli's keep mask, integer object
+    // weights, no pair weights (they arrive after the plan)
+    const bool count_ok = !s->ranking && !s->cfg.sample_from_host && s->int_w &&
+                          (s->cfg.bootstrap_type == CBH_BOOT_NO || s->cfg.bootstrap_type == CBH_BOOT_BERNOULLI);
+    // (the packed decodes take non-negative weights: a negative object weight keeps the other fills)
     const bool want_packed = v == "packed" && !s->pk_signed_w;
-    const bool want_tiled = !want_packed && (v == "tiled" || (v.empty() && s->n >= (1ull << 20)));
-    if (!want_packed && !want_tiled) return CBH_OK;
+    // defaults by measurement: the count-packed fill from 4M rows (config 2's data under Bernoulli:
+    // 380 against 324 iters/s for the tiled exact fill); below, its per-workgroup swaps and
+    // register flush outweigh the halved atomics (config 4 at 2M rows: 861 against 953 iters/s,
+    // config 1: 2578 against 2616), so the tiled exact fill takes over from 64k rows (config 1:
+    // 2616 against 2234 iters/s for the generic fill) -- from 2^20 rows with pair weights, whose
+    // sessions below that ran faster on the generic fill (config 3 at 1M rows: 1419 against 1311)
+    const bool want_count = !want_packed && count_ok && (v == "count" || (v.empty() && s->n >= (1ull << 22)));
+    const bool want_tiled = !want_packed && !want_count &&
+                            (v == "tiled" || v == "count" ||
+                             (v.empty() && s->n >= (s->ranking ? (1ull << 20) : (1ull << 16))));
+    if (!want_packed && !want_count && !want_tiled) return CBH_OK;
     // the tiled fills address their buffers (a tile's row words, statistics) by 32-bit byte
     // offsets and read the dense level's rows in groups of 16 clamped to [0, n)
-    const uint32_t TWM = want_packed ? kPackTileWords : kExTileWords;
+    const bool pk64 = want_packed || want_count;   // the 64-feature loops
+    const uint32_t TWM = pk64 ? kPackTileWords : kExTileWords;
     if ((uint64_t)s->n * TWM * 4u >= (1ull << 31) || s->n < 1024) return CBH_OK;
     int lds_max = 0, cus = 0, per_cu = 0;
     HIP_TRY(hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, s->device));
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
     // every thread owns the same cells of a 256-bin tile whatever B
-    const size_t lds = (size_t)(want_packed ? kPackCells : kExCells) * sizeof(unsigned long long);
+    const size_t lds = (size_t)(pk64 ? kPackCells : kExCells) * sizeof(unsigned long long);
     if (lds > (size_t)lds_max) return CBH_OK;
-    const void* kg = want_packed ? (const void*)fill_packed_kernel<true> : (const void*)fill_exact_kernel<true>;
-    const void* kd = want_packed ? (const void*)fill_packed_kernel<false> : (const void*)fill_exact_kernel<false>;
+    const void* kg = want_packed  ? (const void*)fill_packed_kernel<true, false>
+                     : want_count ? (const void*)fill_packed_kernel<true, true>
+                                  : (const void*)fill_exact_kernel<true>;
+    const void* kd = want_packed  ? (const void*)fill_packed_kernel<false, false>
+                     : want_count ? (const void*)fill_packed_kernel<false, true>
+                                  : (const void*)fill_exact_kernel<false>;
     for (const void* k : {kg, kd})
         HIP_TRY(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kg, (int)kPackThreads, lds));
@@ -711,16 +736,15 @@ int plan_fill_mode(cbh_session* s) {
             if (v2 == 1 || v2 == 2 || v2 == 4 || v2 == 8) s->pk_swap = (uint32_t)v2;
         }
         s->pack_bits = kPackBitsSwap1 - (s->pk_swap >= 2) - (s->pk_swap >= 4) - (s->pk_swap >= 8);
-        CHECK(dalloc(&s->spack, (size_t)s->n));
     }
+    if (pk64) CHECK(dalloc(&s->spack, (size_t)s->n));
     // the listed rows' statistics in idx order (packed: one word per row; tiled: both channels;
     // CBH_EX_STATS=idx, a measurement knob, has the tiled fill read them through the listed rows'
     // indices instead: gathered levels 360 -> 400-650 us at config 2).  CBH_EX_SETS=2: two
     // blocks in flight in the tiled fill's full loop instead of three (a measurement knob; three
     // took config 2's fill from 443 to 436 us per launch)
     const char* es = std::getenv("CBH_EX_STATS");
-    if (want_packed || !(es && std::string(es) == "idx"))
-        CHECK(dalloc(&s->sseq, (size_t)s->n * (want_packed ? 1u : 2u)));
+    if (pk64 || !(es && std::string(es) == "idx")) CHECK(dalloc(&s->sseq, (size_t)s->n * (pk64 ? 1u : 2u)));
     if (const char* ns = std::getenv("CBH_EX_SETS")) s->ex_sets = std::string(ns) == "2" ? 2u : 3u;
     // tile-major row words: each tile's rows contiguous (the row-major words stay for the
     // gathered levels and the other fills)
@@ -731,7 +755,13 @@ int plan_fill_mode(cbh_session* s) {
     if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess)
         return fail(CBH_ERR_DEVICE, "tile-major packing failed");
     s->packed = want_packed;
+    s->count = want_count;
     s->tiled = want_tiled;
+    // the tiled fills visit every bin: the 16 lanes of a DPP row add to 16 distinct features, so
+    // rows crowding one bin never meet on one cell within the lanes an atomic's conflicts count
+    // over (the generic fill leaves such bins out instead, rebuilding them from the totals)
+    s->use_skip = false;
+    s->n_skip = 0;
     return CBH_OK;
 }
 
@@ -1130,6 +1160,8 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     if (weight) {
         HIP_TRY(hipMemcpy(s->weight, weight, sizeof(double) * n, hipMemcpyHostToDevice));
         for (uint64_t i = 0; i < n && !s->pk_signed_w; ++i) s->pk_signed_w = weight[i] < 0.0;
+        for (uint64_t i = 0; i < n && s->int_w; ++i)
+            s->int_w = weight[i] >= 0.0 && weight[i] <= 1048576.0 && weight[i] == std::floor(weight[i]);
     }
     CHECK(plan_fill_mode(s.get()));
     // resident approximant seeded with the bias (DeviceTrainConfig::bias, runtime.rs:1276)
@@ -1485,7 +1517,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         s->ranking ? s->ext_der : nullptr, s->ranking ? s->score_w : nullptr);
     HIP_TRY(hipGetLastError());
     scales_kernel<<<1, 256, 0, st>>>(s->partials, pgrid, s->bounds, s->scales,
-                                     (s->packed || s->pkk) ? s->pack_bits : 0);
+                                     (s->packed || s->pkk) ? s->pack_bits : 0, s->count ? 1 : 0);
     HIP_TRY(hipGetLastError());
     if (s->pkk)
         quantize_pack_kernel<C><<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack,
@@ -1493,6 +1525,8 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
     else if (s->packed)
         pack_stats_fixed_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack,
                                                                          (1ll << s->pack_bits) - 1);
+    else if (s->count)
+        pack_stats_count_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack);
     else
         quantize_stats_kernel<C><<<grid_for(n * C, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales);
     HIP_TRY(hipGetLastError());
@@ -1526,13 +1560,21 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         }
         CHECK(s->stage_begin(kStFill));   // the fill kernel alone
         if (s->packed && level == 0)
-            fill_packed_kernel<false><<<s->pk_dense.blocks, kPackThreads, s->pk_lds, st>>>(
+            fill_packed_kernel<false, false><<<s->pk_dense.blocks, kPackThreads, s->pk_lds, st>>>(
                 s->trows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_dense.tiles16, s->F, s->B,
-                s->pk_dense.ranges, s->pk_dense.ranges_n, cur, s->pk_swap, nullptr, 0u);
+                s->pk_dense.ranges, s->pk_dense.ranges_n, cur, s->pk_swap, nullptr, 0u, s->scales);
         else if (s->packed)
-            fill_packed_kernel<true><<<s->pk_gath.blocks, kPackThreads, s->pk_lds, st>>>(
+            fill_packed_kernel<true, false><<<s->pk_gath.blocks, kPackThreads, s->pk_lds, st>>>(
                 s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_gath.tiles16, s->F, s->B,
-                s->pk_gath.ranges, 0u, cur, s->pk_swap, s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh);
+                s->pk_gath.ranges, 0u, cur, s->pk_swap, s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh, s->scales);
+        else if (s->count && level == 0)
+            fill_packed_kernel<false, true><<<s->pk_dense.blocks, kPackThreads, s->pk_lds, st>>>(
+                s->trows, s->W, n, nullptr, nullptr, s->spack, nullptr, s->pk_dense.tiles16, s->F, s->B,
+                s->pk_dense.ranges, s->pk_dense.ranges_n, cur, 0u, nullptr, 0u, s->scales);
+        else if (s->count)
+            fill_packed_kernel<true, true><<<s->pk_gath.blocks, kPackThreads, s->pk_lds, st>>>(
+                s->trows, s->W, n, lidx, lplan, s->spack, s->sseq, s->pk_gath.tiles16, s->F, s->B,
+                s->pk_gath.ranges, 0u, cur, 0u, s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh, s->scales);
         else if (s->tiled && level == 0)
             fill_exact_kernel<false><<<s->pk_dense.blocks, kExThreads, s->pk_lds, st>>>(
                 s->trows, s->W, n, nullptr, nullptr, (const long long*)s->sstat, nullptr, s->pk_dense.tiles16, s->F,
@@ -1664,7 +1706,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         if (!last) {
             plan_scan_kernel<<<2u << level, 1024, 0, st>>>(s->cnt, 4 * NB, s->totals);
             HIP_TRY(hipGetLastError());
-            if (s->packed)   // the listed rows' packed statistic
+            if (s->packed || s->count)   // the listed rows' packed statistic
                 compact_kernel<1><<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->totals, s->plans + level,
                                                       s->idx, s->spack, s->sseq);
             else if (s->tiled && s->sseq)   // both fixed-point channels of the listed rows
@@ -1931,6 +1973,8 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
     if (n_sample != 0 && !sample) return fail(CBH_ERR_INVALID_ARG, "sample is null");
     if (n_sample != 0 && !s->cfg.sample_from_host)
         return fail(CBH_ERR_INVALID_ARG, "host sample given to a session without sample_from_host");
+    if (s->count && sampling && sampling->kind == CBH_BOOT_BAYESIAN)
+        return fail(CBH_ERR_INVALID_ARG, "a session configured without Bayesian bootstrap got a Bayesian sample");
     if (n_sample != 0 && sampling && sampling->kind != CBH_BOOT_NO)
         return fail(CBH_ERR_INVALID_ARG, "host sample and device sampling are mutually exclusive");
     hipStream_t st = s->stream;
@@ -1984,7 +2028,7 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
     // traffic accounting of the fill launches (algorithmic bytes per launch)
     // (sparse entries: the first 16 codes of every tile, 32 bytes; second slots not counted)
     const double wbytes = s->pks ? 32.0 * s->pkk_tiles : 4.0 * s->W,
-                 sbytes = s->packed ? 8.0 : s->pkk ? 8.0 * ((s->C + 1) / 2) : 8.0 * s->C;
+                 sbytes = (s->packed || s->count) ? 8.0 : s->pkk ? 8.0 * ((s->C + 1) / 2) : 8.0 * s->C;
     const double per_leaf_bytes = (double)s->F * s->B * s->C * 8.0;
     for (uint32_t l = 0; l < s->depth; ++l) {
         const uint64_t V = l == 0 ? bounds.sampled_rows : plans[l - 1].rows;
@@ -2025,7 +2069,7 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
     if (!s || !out) return fail(CBH_ERR_INVALID_ARG, "null argument");
     *out = s->stats;
     out->skip_features = s->n_skip;
-    out->fill_mode = s->packed ? 1u : s->tiled ? 2u : s->pks ? 4u : s->pkk ? 3u : 0u;
+    out->fill_mode = s->packed ? 1u : s->tiled ? 2u : s->pks ? 4u : s->pkk ? 3u : s->count ? 5u : 0u;
     out->fill_pack_bits = (s->packed || s->pkk) ? s->pack_bits : 0;
     return CBH_OK;
 }

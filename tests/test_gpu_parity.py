@@ -96,7 +96,14 @@ def test_histogram_fill_matches_bruteforce(K):
         np.testing.assert_allclose(got, exp, rtol=1e-9, atol=1e-9)
 
 
-FILL_MODE = {"generic": 0, "packed": 1, "tiled": 2, "pkk": 3, "pks": 4}
+FILL_MODE = {"generic": 0, "packed": 1, "tiled": 2, "pkk": 3, "pks": 4, "count": 5}
+
+
+def _close_level_hist(got, exp, nb, rel):
+    """A level's histograms [leaves][F][bins][C] against the oracle's, over the features that have
+    a candidate (the reference builds no histogram for a border-less feature, WR-04)."""
+    keep = np.asarray(nb) > 0
+    _close(got[:, keep], exp[:, keep], rel=rel)
 
 
 @pytest.mark.parametrize("fill,rel", [("generic", 1e-9), ("tiled", 1e-9), ("packed", REL)])
@@ -122,7 +129,36 @@ def test_level_histograms_match_oracle_config2_shape(fill, rel, monkeypatch):
         t = be.grow_tree_on_device(target=y, sample=s)
         assert [(f, b) for f, b, _ in t["splits"]] == [tuple(x) for x in o["splits"].tolist()]
         for level in range(6):
-            _close(be.level_hist(level, F, B), o["hists"][level], rel=rel)
+            _close_level_hist(be.level_hist(level, F, B), o["hists"][level], nb, rel)
+    finally:
+        be.end_device_training()
+
+
+@pytest.mark.parametrize("fill", ["generic", "tiled", "count"])
+def test_level_histograms_match_oracle_integer_weights(fill, monkeypatch):
+    """Every level histogram of one RMSE tree over integer object weights (1 to 3, no bootstrap:
+    integer score weights, the count-packed fill's case) at config 4's row count scale, cell by
+    cell against the CPU restatement within 1e-9 of the level's largest cell: the count-packed
+    fill rounds a row's der at 2^-30 or finer and carries the weight exactly."""
+    monkeypatch.setenv("CBH_FILL", fill)
+    g = np.random.default_rng(41)
+    n, F = 300_000, 77
+    nb = g.integers(16, 255, F).astype(np.uint32)   # no dominant bin: every fill takes the session
+    nb[0] = 254
+    bins = np.minimum((g.random((F, n)) * (nb[:, None] + 1)).astype(np.int64), nb[:, None]).astype(np.uint8)
+    B = int(nb.max()) + 1
+    y = g.standard_normal(n) + bins[:8].astype(np.float64).sum(0) / 256.0   # a signal over the first features
+    w = g.integers(1, 4, n).astype(np.float64)
+    o = O.grow_tree(bins, nb, y * w, w, 6, "Cosine", 3.0, want_hists=True)
+    be = cb.HipBackend()
+    assert be.begin_device_training("RMSE", 6, True, 1, "Cosine", bins, w, n, F, B, 0.1, 3.0, real_folds=nb + 1)
+    try:
+        assert be.stats()["fill_mode"] == FILL_MODE[fill]
+        be.capture_hists()
+        t = be.grow_tree_on_device(target=y)
+        assert [(f, b) for f, b, _ in t["splits"]] == [tuple(x) for x in o["splits"].tolist()]
+        for level in range(6):
+            _close_level_hist(be.level_hist(level, F, B), o["hists"][level], nb, 1e-9)
     finally:
         be.end_device_training()
 
@@ -154,7 +190,7 @@ def test_level_histograms_match_oracle_config5_shape(fill, rel, monkeypatch):
         t = be.grow_tree_on_device(target=y)
         assert [(f, b) for f, b, _ in t["splits"]] == [tuple(x) for x in o["splits"].tolist()]
         for level in range(depth):
-            _close(be.level_hist(level, F, B), o["hists"][level], rel=rel)
+            _close_level_hist(be.level_hist(level, F, B), o["hists"][level], nb, rel)
     finally:
         be.end_device_training()
 
@@ -642,10 +678,10 @@ def _assert_same_fit(exp, splits, leaves, approx):
     _close(approx, exp["approx"])
 
 
-@pytest.mark.parametrize("fill", ["auto", "tiled", "packed"])
+@pytest.mark.parametrize("fill", ["auto", "tiled", "count", "packed"])
 def test_config1_full_size_matches_oracle(fill, monkeypatch):
     """Config 1 at its full size: RMSE, 100k x 50, 128 borders, depth 6, 100 trees (the
-    default generic fill below 2^20 rows, and the tiled exact and rounded packed fills forced)."""
+    default fill, and the tiled exact, count-packed and rounded packed fills forced)."""
     if fill != "auto":
         monkeypatch.setenv("CBH_FILL", fill)
     d = datagen.config1()
@@ -705,7 +741,7 @@ def test_config2_full_size_all_trees_tiled_equals_generic_fill(monkeypatch):
     assert np.array_equal(a0, a1)
 
 
-@pytest.mark.parametrize("layout", ["bin", "feature", "packed", "tiled"])
+@pytest.mark.parametrize("layout", ["bin", "feature", "packed", "tiled", "count"])
 @pytest.mark.parametrize("F,B,K", [(37, 17, 1), (5, 256, 1), (65, 33, 3), (33, 2, 1), (100, 255, 1),
                                    (129, 256, 1), (64, 255, 1), (36, 40, 1), (44, 129, 1)])
 def test_fill_layouts_ragged_shapes_match_oracle(layout, F, B, K, monkeypatch):
