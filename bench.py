@@ -45,27 +45,29 @@ sys.path.insert(0, ROOT)
 METRIC = "histogram rows·features/s + HBM GB/s; boosting iters/s at 10M×200, depth 6"
 HBM_PEAK_GBS = 8000.0
 DEFAULT_STEPS = {1: 100, 2: 200, 3: 100, 4: 200, 5: 20}
-DEFAULT_CPU_TREES = {1: 5, 2: 2, 3: 3, 4: 3, 5: 1}
+DEFAULT_CPU_TREES = {1: 5, 2: 5, 3: 3, 4: 3, 5: 1}
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def _profiled_traffic(config, n, F, kernel):
-    """HBM bytes per fill launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, copy-calibrated)
-    for the default workload shape, read from the committed profile summary of the same fill
-    kernel on the same bench command (its last 120 fill dispatches are the 20 profiled trees this
-    line's avg_launch_ms and algorithmic bytes come from); None if absent or of another kernel."""
+def _profile_facts(config, n, F, kernel):
+    """(traffic, limiter) of the fill kernel from the committed profile summary of the same
+    kernel on the same bench command: HBM bytes per launch measured by rocprofv3 (FETCH_SIZE +
+    WRITE_SIZE, copy-calibrated; its last 120 fill dispatches are the 20 profiled trees this
+    line's avg_launch_ms and algorithmic bytes come from) and the bound its SQ counters show;
+    (None, None) if absent or of another kernel or shape."""
     path = os.path.join(ROOT, "profiles", "fill_kernel_config2.md")
     if config != 2 or n != 10_000_000 or F != 200 or not os.path.exists(path):
-        return None
+        return None, None
     text = open(path).read()
     k = re.search(r"^kernel: (\S+)", text, re.M)
     m = re.search(r"mean per dispatch: fetch ([0-9.]+) GB write ([0-9.]+) GB", text)
+    lim = re.search(r"^limiter: (.+)$", text, re.M)
     if not k or k.group(1) != kernel or not m:
-        return None
-    return round((float(m.group(1)) + float(m.group(2))) * 1e9)
+        return None, None
+    return round((float(m.group(1)) + float(m.group(2))) * 1e9), (lim.group(1).strip() if lim else None)
 
 
 def _lds_rates():
@@ -351,7 +353,10 @@ def main():
     if not args.no_cpu and cpu_trees > 0:
         from oracle import oracle as O
 
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        # the host threads this process may use (nproc), capped by the box's CPU share when the
+        # environment states one (OMP_NUM_THREADS: 16 per GPU on the GPU boxes)
+        nproc = len(os.sched_getaffinity(0))
+        threads = args.cpu_threads or min(nproc, int(os.environ.get("OMP_NUM_THREADS") or nproc))
         if raw:   # the oracle's bins: the same borders, quantized on the host (bin_of)
             from catboost_rs_amd import datagen
 
@@ -359,7 +364,7 @@ def main():
         t0 = time.perf_counter()
         exp = O.train(bins, nb, y, iterations=cpu_trees, n_threads=threads, pairs=pairs, ctr=ctr, **kw)
         cpu_wall = time.perf_counter() - t0
-        cpu = {"value": round(cpu_trees / cpu_wall, 6), "unit": "iters/s", "cores": threads,
+        cpu = {"value": round(cpu_trees / cpu_wall, 6), "unit": "iters/s", "cores": threads, "nproc": nproc,
                "kind": "port",
                "sample": f"first {cpu_trees} trees of the same {n}x{F} workload "
                          f"(CPU restatement of the reference algorithm, OpenMP over features)"}
@@ -369,9 +374,18 @@ def main():
         first, _ = tr2.fit(cpu_trees)
         tr2.close()
         cpu["splits_match_gpu"] = bool(np.array_equal(first, exp["splits"]))
+        if args.config == 1:   # the single-core leg of the CPU baseline (the whole fit)
+            t0 = time.perf_counter()
+            O.train(bins, nb, y, iterations=P["iterations"], n_threads=1, pairs=pairs, ctr=ctr, **kw)
+            one = time.perf_counter() - t0
+            cpu["single_core"] = {"value": round(P["iterations"] / one, 4), "unit": "iters/s", "cores": 1,
+                                  "sample": f"all {P['iterations']} trees of the same workload"}
+            log(f"cpu: {P['iterations']} trees in {one:.1f}s on 1 thread")
 
+    traffic, limiter = None, None   # (set below from the committed profile)
     fill_kernel = {0: "fill_kernel", 1: "fill_packed_kernel", 2: "fill_exact_kernel",
                    3: "fill_pkk_kernel", 4: "fill_pks_kernel", 5: "fill_packed_kernel"}[st["fill_mode"]]
+    traffic, limiter = _profile_facts(args.config, n, F, fill_kernel)
     names = {1: "config1: RMSE, no bootstrap, depth 6, 128 borders",
              2: ("config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 GreedyLogSum borders selected on the "
                  "device from the raw f32 columns, quantized on the device" if raw else
@@ -391,7 +405,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8 bins, int64 fixed-point sums, f64 scores",
+        "dtype": (f"u8 bins; int64 fixed-point histogram sums, a row's value v entering as round(v * 2^S): "
+                  f"S = {st['score_shift_der']} (der), {st['score_shift_w']} (weight) in the last tree "
+                  f"(the reference: 2^30); f64 scores"
+                  if st["fill_mode"] in (0, 2) else
+                  f"u8 bins; int64 fixed-point histogram sums: der rows as round(v * 2^{st['score_shift_der']}) "
+                  f"(the reference: 2^30), integer weights exact; f64 scores"
+                  if st["fill_mode"] == 5 else
+                  f"u8 bins; int64 sums of rows rounded to {st['fill_pack_bits']}-bit fields of the tree's "
+                  f"largest row (coarser than the reference's 2^-30); f64 scores"),
         "fill": {0: "generic 32-feature tiles (one 64-bit atomic per channel, full fixed-point scale)", 1: f"packed 64-feature tiles ({st['fill_pack_bits']}-bit rows)",
                  2: "tiled exact 32-feature tiles (one 64-bit atomic per channel, full fixed-point scale)",
                  3: f"packed multi-channel 32-feature tiles (two channels per word, {st['fill_pack_bits']}-bit rows)",
@@ -411,14 +433,11 @@ def main():
         "ms_per_step_profiled_eager": round(1000.0 * prof_wall / prof_steps, 4),
         "roofline": {"bound": "hbm", "kernel": fill_kernel, "achieved": round(achieved, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": _profiled_traffic(args.config, n, F, fill_kernel),
+                     "traffic": traffic,
                      "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE (copy-calibrated) of the last 120 fill "
                                        "dispatches of this command, profiles/fill_kernel_config2.md"
-                                       if _profiled_traffic(args.config, n, F, fill_kernel) else None,
-                     "limiter": "LDS atomic instruction rate: one 64-bit ds_add per (row, feature), the LDS pipe "
-                                "issuing 85% (dense level) and 78% (gathered levels) of the conflict-free rate; HBM "
-                                "4.1 / 3.7 TB/s (counters in profiles/fill_kernel_config2.md)"
-                                if fill_kernel == "fill_packed_kernel" else None,
+                                       if traffic else None,
+                     "limiter": limiter,
                      "launches": st["fill_launches"],
                      "avg_launch_ms": round(st["fill_ms"] / max(1, st["fill_launches"]), 5),
                      "algorithmic_bytes_per_launch": round(st["fill_bytes"] / max(1, st["fill_launches"]))},

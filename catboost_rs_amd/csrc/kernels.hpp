@@ -1285,16 +1285,18 @@ __device__ __forceinline__ void exact_range(unsigned long long* __restrict__ ex,
         exact_pass<6>(ex, S, off8);
         exact_pass<7>(ex, S, off8);
     };
-    static_assert(NS == 2 || NS == 3, "two or three sets");
-    ExSet S0, S1, S2;
+    static_assert(NS >= 2 && NS <= 4, "two to four sets");
+    ExSet S0, S1, S2, S3;
     if (kGather) {
         S0.ix = stage_ix(pos);
         S1.ix = stage_ix(pos + kExBlockRows);
-        if (NS == 3) S2.ix = stage_ix(pos + 2u * kExBlockRows);
+        if (NS >= 3) S2.ix = stage_ix(pos + 2u * kExBlockRows);
+        if (NS >= 4) S3.ix = stage_ix(pos + 3u * kExBlockRows);
     }
     load(S0, pos);
     load(S1, pos + kExBlockRows);
-    if (NS == 3) load(S2, pos + 2u * kExBlockRows);
+    if (NS >= 3) load(S2, pos + 2u * kExBlockRows);
+    if (NS >= 4) load(S3, pos + 3u * kExBlockRows);
     for (uint32_t bb = pos;; bb += NS * kExBlockRows) {   // workgroup-uniform
         consume(S0);
         if (bb + kExBlockRows >= end) break;
@@ -1302,10 +1304,15 @@ __device__ __forceinline__ void exact_range(unsigned long long* __restrict__ ex,
         consume(S1);
         if (bb + 2u * kExBlockRows >= end) break;
         load(S1, bb + (NS + 1) * kExBlockRows);
-        if (NS == 3) {
+        if (NS >= 3) {
             consume(S2);
             if (bb + 3u * kExBlockRows >= end) break;
             load(S2, bb + (NS + 2) * kExBlockRows);
+        }
+        if (NS >= 4) {
+            consume(S3);
+            if (bb + 4u * kExBlockRows >= end) break;
+            load(S3, bb + (NS + 3) * kExBlockRows);
         }
     }
 }
@@ -1434,7 +1441,7 @@ static __global__ __launch_bounds__(kExThreads) void fill_exact_kernel(
     const long long* __restrict__ sseq /* kGather, nullable: [V][2], the listed rows' statistics in idx order */,
     uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, uint32_t Gn, long long* __restrict__ hist,
     const uint32_t* __restrict__ rows_rm /* nullable, kGather: row-major words, 2^rm_sh bytes per row */,
-    uint32_t rm_sh, uint32_t sets /* blocks in flight of the full loop: 2 or 3 */) {
+    uint32_t rm_sh, uint32_t sets /* blocks in flight of the full loop: 2 to 4 */) {
     extern __shared__ unsigned long long ex[];
     // blocks: n_tiles tiles of the 8-lane loop in G row ranges each, numbered range-major and
     // dealt to the 8 XCDs in runs (block b to XCD b % 8: XCD x takes pairs [x per, (x + 1) per)),
@@ -1504,7 +1511,10 @@ static __global__ __launch_bounds__(kExThreads) void fill_exact_kernel(
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = kGather ? plan->built[seg] : 0u;
         if (end > pos) {
-            if (!narrow && sets == 3)
+            if (!narrow && sets == 4)
+                exact_range<kGather, 4>(ex, rbase, sh, wl4, 8u * (l >> 3), l, ibase, sbase, seq, pos, end,
+                                        (uint32_t)n, r0, off8);
+            else if (!narrow && sets == 3)
                 exact_range<kGather, 3>(ex, rbase, sh, wl4, 8u * (l >> 3), l, ibase, sbase, seq, pos, end,
                                         (uint32_t)n, r0, off8);
             else if (!narrow)

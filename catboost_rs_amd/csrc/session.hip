@@ -740,12 +740,15 @@ int plan_fill_mode(cbh_session* s) {
     if (pk64) CHECK(dalloc(&s->spack, (size_t)s->n));
     // the listed rows' statistics in idx order (packed: one word per row; tiled: both channels;
     // CBH_EX_STATS=idx, a measurement knob, has the tiled fill read them through the listed rows'
-    // indices instead: gathered levels 360 -> 400-650 us at config 2).  CBH_EX_SETS=2: two
-    // blocks in flight in the tiled fill's full loop instead of three (a measurement knob; three
-    // took config 2's fill from 443 to 436 us per launch)
+    // indices instead: gathered levels 360 -> 400-650 us at config 2).  CBH_EX_SETS=2..4: blocks
+    // in flight in the tiled fill's full loop (a measurement knob; three instead of two took
+    // config 2's fill from 443 to 436 us per launch)
     const char* es = std::getenv("CBH_EX_STATS");
     if (pk64 || !(es && std::string(es) == "idx")) CHECK(dalloc(&s->sseq, (size_t)s->n * (pk64 ? 1u : 2u)));
-    if (const char* ns = std::getenv("CBH_EX_SETS")) s->ex_sets = std::string(ns) == "2" ? 2u : 3u;
+    if (const char* ns = std::getenv("CBH_EX_SETS")) {
+        const long v2 = std::strtol(ns, nullptr, 10);
+        if (v2 >= 2 && v2 <= 4) s->ex_sets = (uint32_t)v2;
+    }
     // tile-major row words: each tile's rows contiguous (the row-major words stay for the
     // gathered levels and the other fills)
     const uint32_t tw_last = s->W - TWM * (s->pk_tiles - 1);
@@ -2071,6 +2074,13 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
     out->skip_features = s->n_skip;
     out->fill_mode = s->packed ? 1u : s->tiled ? 2u : s->pks ? 4u : s->pkk ? 3u : s->count ? 5u : 0u;
     out->fill_pack_bits = (s->packed || s->pkk) ? s->pack_bits : 0;
+    Scales sc{};
+    if (s->scales && s->stats.trees) {
+        HIP_TRY(hipStreamSynchronize(s->stream));
+        HIP_TRY(hipMemcpy(&sc, s->scales, sizeof(Scales), hipMemcpyDeviceToHost));
+    }
+    out->score_shift_der = sc.shift[kScoreDer];
+    out->score_shift_w = sc.shift[kScoreW];
     return CBH_OK;
 }
 

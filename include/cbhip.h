@@ -218,6 +218,8 @@ typedef struct {
                                      over sparse entries (a row per 16-lane DPP row, one lane per
                                      non-dominant (feature, bin)) */
     int32_t fill_pack_bits;       /* packed fills: bits of a row's rounded channel value (|q| < 2^bits) */
+    int32_t score_shift_der;      /* the last tree's fixed-point scales S of the score channels: a row's */
+    int32_t score_shift_w;        /* value v enters the histogram as round(v * 2^S) (der; weight) */
 } cbh_stats;
 
 int cbh_session_stats(const cbh_session* s, cbh_stats* out);
