@@ -153,7 +153,8 @@ constexpr int kBoundShift = 10;
 struct Bounds {
     unsigned long long sum_abs[kNumScales];
     unsigned long long sampled_rows;
-    unsigned long long pad[3];
+    unsigned long long device_err;   // nonzero: a kernel of the tree gave up a bounded wait (cleared per tree)
+    unsigned long long pad[2];
 };
 
 __device__ __forceinline__ long long to_fixed(double v, double mul) {

@@ -411,6 +411,7 @@ static __global__ __launch_bounds__(256) void scales_kernel(const unsigned long 
     }
     for (int k = 0; k < kNumScales; ++k) b->sum_abs[k] = acc[k];
     b->sampled_rows = acc[4];
+    b->device_err = 0;   // the tree's kernels after this one report a failed bounded wait here
     for (int k = 0; k < kNumScales; ++k) {
         const bool packed = pack_bits > 0 && (k == kScoreDer || k == kScoreW);
         const double bound = (double)acc[packed ? 5 + k : k] / (double)(1 << kBoundShift);
@@ -2388,7 +2389,7 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
 // writer's next hop comes after the reader's hop that cleared it (a wave's LDS operations
 // complete in order).
 // ---------------------------------------------------------------------------------
-constexpr uint32_t kChainSpinLimit = 1u << 22;   // bound on a wave's wait for its turn
+constexpr uint32_t kChainSpinLimit = 1u << 22;   // default bound on a wave's wait for its turn
 
 // A wave-uniform row pointer kept in SGPRs (loads then take a per-lane 32-bit offset), and a
 // wave-uniform cell read through the scalar cache (constant address space): the level's
@@ -2411,30 +2412,36 @@ __device__ __forceinline__ long long readlane64(long long v, int lane) {
 
 constexpr unsigned long long kChainEmpty = ~0ull;
 
-__device__ __forceinline__ void chain_take(unsigned long long* slot, uint32_t lane, double& num, double& den) {
-    // the hop before runs in another wave of this workgroup (or this one), each of which
-    // reaches every hop it owns; the bound only keeps a broken schedule from hanging the GPU.
-    // The poll reads den alone and sleeps between reads (a polling wave would otherwise take
-    // VALU issue from the waves computing terms); num, written before den, is then set too.
+// Take the previous hop's (num, den).  The hop before runs in another wave of this workgroup
+// (or this one), each of which reaches every hop it owns; the bound (spin polls) only keeps a
+// broken schedule from hanging the GPU.  The poll reads den alone with acquire ordering at
+// workgroup scope, paired with the writer's release store of den, so num (stored before den)
+// is visible once den is; it sleeps between reads (a polling wave would otherwise take VALU
+// issue from the waves computing terms).  A wait that runs out leaves den NaN and sets the
+// tree's device error word, which the host turns into an error for the tree.
+__device__ __forceinline__ void chain_take(unsigned long long* slot, uint32_t lane, double& num, double& den,
+                                           uint32_t spin, unsigned long long* err) {
     unsigned long long b = kChainEmpty;
-    for (uint32_t k = 0; k < kChainSpinLimit; ++k) {
-        b = __hip_atomic_load(slot + 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (uint32_t k = 0; k < spin; ++k) {
+        b = __hip_atomic_load(slot + 64 + lane, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (__all(b != kChainEmpty)) break;
         __builtin_amdgcn_s_sleep(1);
     }
+    if (!__all(b != kChainEmpty) && lane == 0) atomicOr(err, 1ull);
     const unsigned long long a = __hip_atomic_load(slot + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     num = __longlong_as_double((long long)a);
     den = __longlong_as_double((long long)b);
+    // the clearing precedes this wave's release of its own outbox (chain_give), so the wave
+    // that writes this outbox next -- after the chain has passed through this wave -- sees it
     __hip_atomic_store(slot + lane, kChainEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     __hip_atomic_store(slot + 64 + lane, kChainEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    asm volatile("" ::: "memory");   // the clearing is issued before this wave's next slot write
 }
 
 __device__ __forceinline__ void chain_give(unsigned long long* slot, uint32_t lane, double num, double den) {
     __hip_atomic_store(slot + lane, (unsigned long long)__double_as_longlong(num), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_WORKGROUP);
-    asm volatile("" ::: "memory");   // num is issued before den (the reader polls den)
-    __hip_atomic_store(slot + 64 + lane, (unsigned long long)__double_as_longlong(den), __ATOMIC_RELAXED,
+    // release: num and every earlier LDS write of this wave are visible before den
+    __hip_atomic_store(slot + 64 + lane, (unsigned long long)__double_as_longlong(den), __ATOMIC_RELEASE,
                        __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
@@ -2453,7 +2460,7 @@ template <int K, int PW, bool kPartial, bool kOneHot>
 __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, uint32_t P, uint32_t F,
                                             uint32_t B, uint32_t f, double inv_d, double inv_w, double l2,
                                             unsigned long long* ring /* [waves][2][64] */, double& num,
-                                            double& den) {
+                                            double& den, uint32_t spin, unsigned long long* err) {
     constexpr int C = K + 1;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
@@ -2531,7 +2538,7 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
             for (int u = 0; u < PW; ++u) asm volatile("" ::"v"(x[u]), "v"(y[u]) : "memory");
             // the next dimension's cells load while the chain is in other waves
             if (side == 1 && d + 1 < K) load_der(d + 1);
-            if (hop > 0) chain_take(ring + 128 * (wv == 0 ? nw - 1 : wv - 1), lane, num, den);
+            if (hop > 0) chain_take(ring + 128 * (wv == 0 ? nw - 1 : wv - 1), lane, num, den, spin, err);
 #pragma unroll
             for (int u = 0; u < PW; ++u) {
                 num += x[u];
@@ -2552,7 +2559,9 @@ __global__ __launch_bounds__(512) void score_chain_kernel(
     const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
     const uint32_t* __restrict__ n_cand, const uint8_t* __restrict__ one_hot,
     const Scales* __restrict__ sc, double l2, int cosine, double* __restrict__ best_score,
-    uint32_t* __restrict__ best_bin, const double* __restrict__ fweight /* nullable [F] */) {
+    uint32_t* __restrict__ best_bin, const double* __restrict__ fweight /* nullable [F] */,
+    uint32_t spin /* polls a wave's wait for its turn may take */,
+    unsigned long long* __restrict__ err /* the tree's device error word */) {
     __shared__ unsigned long long ring[8 * 2 * 64];   // outboxes [wave][num, den][lane]
     const uint32_t f = blockIdx.x;
     // clear feature f's cells of the next level's histogram [leaf][HC][F][B] (its fill adds)
@@ -2575,9 +2584,9 @@ __global__ __launch_bounds__(512) void score_chain_kernel(
     double den = 0.0;
     den += 1e-100;
     if (one_hot != nullptr && one_hot[f] != 0)
-        score_chain<K, PW, kPartial, true>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den);
+        score_chain<K, PW, kPartial, true>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den, spin, err);
     else
-        score_chain<K, PW, kPartial, false>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den);
+        score_chain<K, PW, kPartial, false>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den, spin, err);
     // the last wave made the last hop: its (num, den) are the full fold
     if ((threadIdx.x >> 6) != (blockDim.x >> 6) - 1) return;
     const uint32_t b = threadIdx.x & 63u;

@@ -136,6 +136,7 @@ struct cbh_session {
     uint32_t* n_cand = nullptr;
     uint32_t max_cand = 0;           // most candidates of any feature (threads of the scorer)
     bool score_chain = true;         // parents split over waves for K > 1 (CBH_SCORE_CHAIN=off: one wave)
+    uint32_t chain_spin = kChainSpinLimit;   // polls of a chained scorer wave's wait (CBH_CHAIN_SPIN: a test knob)
     uint8_t* one_hot = nullptr;
     Scales* scales = nullptr;
     Bounds* bounds = nullptr;
@@ -1149,6 +1150,9 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     }
     HIP_TRY(hipMemcpy(s->n_cand, nc.data(), sizeof(uint32_t) * F, hipMemcpyHostToDevice));
     if (const char* e = std::getenv("CBH_SCORE_CHAIN")) s->score_chain = std::string(e) != "off";
+    // CBH_CHAIN_SPIN (a test knob): the polls a chained scorer wave takes before it gives up its
+    // wait for its turn (0: without polling), so the error path runs with every kernel exiting
+    if (const char* e = std::getenv("CBH_CHAIN_SPIN")) s->chain_spin = (uint32_t)std::strtoul(e, nullptr, 10);
     bool any_oh = false;
     for (uint8_t v : s->one_hot_host) any_oh |= v != 0;
     if (any_oh) {
@@ -1670,17 +1674,20 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
                 if (chain_pw == 16)
                     score_chain_kernel<K, 16, false><<<s->F, 64 * (n_leaves / 16), 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
-                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr);
+                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
+                        &s->bounds->device_err);
             }
             if constexpr (K > 1) {
                 if (chain_pw == 8 && n_leaves >= 8)
                     score_chain_kernel<K, 8, false><<<s->F, 64 * (n_leaves / 8), 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
-                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr);
+                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
+                        &s->bounds->device_err);
                 else if (chain_pw == 8)
                     score_chain_kernel<K, 8, true><<<s->F, 64, 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
-                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr);
+                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
+                        &s->bounds->device_err);
             }
         } else if (s->max_cand <= 64)
             score_kernel<K, 1><<<s->F, 64, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
@@ -1820,6 +1827,10 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
     plans_out.assign(s->pin_plans, s->pin_plans + s->depth);
     bounds_out = *s->pin_bounds;
     leaf_out.assign(s->pin_leaves, s->pin_leaves + n_leaves * K);
+    if (bounds_out.device_err) {   // a bounded wait of the tree gave up: its splits are not valid
+        s->pending = false;
+        return fail(CBH_ERR_DEVICE, "the chained split scorer's wait for its turn ran out");
+    }
     // a level without a candidate split: the tree is not part of the model (CbError::Degenerate
     // leaves it untouched), so its leaves are never applied and its CTR groups stay unused
     for (uint32_t l = 0; l < s->depth; ++l)

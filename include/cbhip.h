@@ -31,7 +31,7 @@ extern "C" {
 #define CBH_ERR_DEGENERATE (-3)      /* CbError::Degenerate (e.g. no candidate split) */
 #define CBH_ERR_UNSUPPORTED (-4)     /* CbError::Unsupported */
 #define CBH_ERR_INVALID_ARG (-5)     /* CbError::InvalidArgument-style caller bug */
-#define CBH_ERR_DEVICE (-6)          /* HIP runtime / allocation failure */
+#define CBH_ERR_DEVICE (-6)          /* HIP runtime / allocation failure, or a kernel's bounded wait gave up */
 
 /* ---- enums (cb-compute Loss / EScoreFunction / ELeavesEstimation / bootstrap) ---- */
 enum {

@@ -195,6 +195,48 @@ def test_level_histograms_match_oracle_config5_shape(fill, rel, monkeypatch):
         be.end_device_training()
 
 
+@pytest.mark.parametrize("depth", [2, 5])
+def test_chained_scorer_wait_expiry_fails_the_tree(depth, monkeypatch):
+    """The chained MultiClass scorer hands each border's running (num, den) from wave to wave
+    through LDS; a wave's wait for its turn is bounded.  With the bound set to 0 polls from the
+    host (CBH_CHAIN_SPIN, read at open) every wait gives up at once -- all kernels still exit
+    normally -- and the tree fails with CBH_ERR_DEVICE instead of dropping candidates silently
+    (one wave per feature at depth 2, several waves at depth 5).  A session opened without the
+    knob then grows the same tree as the oracle."""
+    g = np.random.default_rng(9)
+    n, F, K = 20_000, 12, 3
+    bins = g.integers(0, 40, (F, n)).astype(np.uint8)
+    y = g.integers(0, K, n).astype(np.float64)
+    nb = np.full(F, 39, np.uint32)
+
+    def open_(spin):
+        if spin is None:
+            monkeypatch.delenv("CBH_CHAIN_SPIN", raising=False)
+        else:
+            monkeypatch.setenv("CBH_CHAIN_SPIN", str(spin))
+        be = cb.HipBackend()
+        assert be.begin_device_training("MultiClass", depth, True, 1, "Cosine", bins, None, n, F, 40, 0.1, 3.0,
+                                        approx_dim=K, leaf_method="Newton", real_folds=nb + 1)
+        return be
+
+    be = open_(0)
+    try:
+        with pytest.raises(cb.CbhError) as ei:
+            be.grow_tree_on_device(target=y)
+        assert ei.value.code == -6, str(ei.value)
+    finally:
+        be.end_device_training()
+    der = -np.full((K, n), 1.0 / K)
+    der[y.astype(np.int64), np.arange(n)] += 1.0
+    o = O.grow_tree(bins, nb, der, np.ones(n), depth, "Cosine", 3.0)
+    be = open_(None)
+    try:
+        t = be.grow_tree_on_device(target=y)
+    finally:
+        be.end_device_training()
+    assert [(f, b) for f, b, _ in t["splits"]] == [tuple(x) for x in o["splits"].tolist()]
+
+
 # -------------------------------------------------------------------------- one tree
 @pytest.mark.parametrize("loss", ["rmse", "logloss"])
 def test_depth6_golden_tree_on_gpu(loss):
