@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(HERE, "libcbhip.so")
 
 LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2, "CrossEntropy": 3, "PairLogit": 4,
         "PairLogitPairwise": 5}
-SCORE = {"Cosine": 0, "L2": 1}
+SCORE = {"Cosine": 0, "L2": 1, "SolarL2": 2, "LOOL2": 3, "SatL2": 4}
 LEAF = {"Gradient": 0, "Newton": 1, "Simple": 2}
 BOOT = {"No": 0, "Bayesian": 1, "Bernoulli": 2}
 

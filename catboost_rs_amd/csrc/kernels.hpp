@@ -2248,9 +2248,24 @@ static __global__ __launch_bounds__(256) void seg_totals_kernel(const uint32_t* 
 // give s = w = 0, avg = 0 and terms of exactly 0 (num and den only hold non-negative sums).  The
 // quotient is computed for every term and kept only where w > 0 (branch-free).  Lanes past the
 // bins read bin B-1 (their score is discarded).
+// One leaf's additive term of the SolarL2 / LOOL2 / SatL2 calcers (score.rs:283-350,
+// kernels.rs:3338-3390): der sum s, weight sum w, no L2 regularizer.
+__device__ __forceinline__ double leaf_score_term(int sf, double s, double w) {
+    if (sf == 2) return w > 1e-20 ? (-s * s) * (1.0 + 2.0 * log(w + 1.0)) / w : 0.0;
+    if (sf == 3) {
+        double adjust = w > 1.0 ? w / (w - 1.0) : 0.0;
+        adjust *= adjust;
+        return w > 0.0 ? adjust * (-s * s) / w : 0.0;
+    }
+    const double adjust = w > 2.0 ? w * (w - 2.0) / (w * w - 3.0 * w + 1.0) : 0.0;
+    return w > 0.0 ? adjust * (-s * s) / w : 0.0;
+}
+
+// sf (CBH_SCORE_*): Cosine and L2 fold avg * s into num and avg^2 * w into den; SolarL2, LOOL2 and
+// SatL2 fold their per-leaf terms into num, in the same (d, side, p) order.
 template <int K, bool kOneHot>
 __device__ __forceinline__ void score_fold(const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
-                                           uint32_t f, uint32_t b, double inv_d, double inv_w, double l2,
+                                           uint32_t f, uint32_t b, double inv_d, double inv_w, double l2, int sf,
                                            double& num, double& den) {
     constexpr int C = K + 1;
     constexpr uint32_t kPre = 8;   // parents whose cells are loaded ahead of their terms
@@ -2292,6 +2307,10 @@ __device__ __forceinline__ void score_fold(const long long* __restrict__ hist, u
                     }
                     const double s = (double)xd * inv_d;
                     const double w = (double)xw * inv_w;
+                    if (sf > 1) {   // workgroup-uniform
+                        num += leaf_score_term(sf, s, w);
+                        continue;
+                    }
                     const double q = s / (w + l2);
                     const double avg = w > 0.0 ? q : 0.0;
                     num += avg * s;
@@ -2307,7 +2326,7 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     long long* __restrict__ zero_buf, uint32_t zero_leaves, uint32_t HC,   // next level's histogram
     const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
     const uint32_t* __restrict__ n_cand, const uint8_t* __restrict__ one_hot,
-    const Scales* __restrict__ sc, double l2, int cosine, double* __restrict__ best_score,
+    const Scales* __restrict__ sc, double l2, int sf /* CBH_SCORE_* */, double* __restrict__ best_score,
     uint32_t* __restrict__ best_bin, const double* __restrict__ fweight /* nullable [F] */) {
     __shared__ double red_s[NW];
     __shared__ uint32_t red_b[NW];
@@ -2334,10 +2353,10 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     // the histograms are in prefix form over bins: prefix = cell b, total = cell B-1, the
     // bin itself (one-hot) = cell b - cell b-1; the fold order over (d, side, p) is the reference's
     if (oh)
-        score_fold<K, true>(hist, P, F, B, f, b, inv_d, inv_w, l2, num, den);
+        score_fold<K, true>(hist, P, F, B, f, b, inv_d, inv_w, l2, sf, num, den);
     else
-        score_fold<K, false>(hist, P, F, B, f, b, inv_d, inv_w, l2, num, den);
-    double score = cosine ? num / sqrt(den) : num;
+        score_fold<K, false>(hist, P, F, B, f, b, inv_d, inv_w, l2, sf, num, den);
+    double score = sf == 0 ? num / sqrt(den) : num;
     // the model_size_reg weight of a CTR column multiplies every candidate's score
     // (weight * score, tree.rs:3340-3346)
     if (fweight) score = fweight[f] * score;
@@ -2558,7 +2577,7 @@ __global__ __launch_bounds__(512) void score_chain_kernel(
     long long* __restrict__ zero_buf, uint32_t zero_leaves, uint32_t HC,   // next level's histogram
     const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
     const uint32_t* __restrict__ n_cand, const uint8_t* __restrict__ one_hot,
-    const Scales* __restrict__ sc, double l2, int cosine, double* __restrict__ best_score,
+    const Scales* __restrict__ sc, double l2, int sf /* CBH_SCORE_COSINE or _L2 */, double* __restrict__ best_score,
     uint32_t* __restrict__ best_bin, const double* __restrict__ fweight /* nullable [F] */,
     uint32_t spin /* polls a wave's wait for its turn may take */,
     unsigned long long* __restrict__ err /* the tree's device error word */) {
@@ -2590,7 +2609,7 @@ __global__ __launch_bounds__(512) void score_chain_kernel(
     // the last wave made the last hop: its (num, den) are the full fold
     if ((threadIdx.x >> 6) != (blockDim.x >> 6) - 1) return;
     const uint32_t b = threadIdx.x & 63u;
-    double score = cosine ? num / sqrt(den) : num;
+    double score = sf == 0 ? num / sqrt(den) : num;
     if (fweight) score = fweight[f] * score;
     if (b >= nc || score != score) score = -INFINITY;
     uint32_t bb = b;

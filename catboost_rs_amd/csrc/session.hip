@@ -381,8 +381,12 @@ int validate_config(const cbh_config* cfg, uint32_t n_bins, uint64_t n, uint32_t
     } else if (cfg->approx_dim != 1) {
         return fail(CBH_ERR_INVALID_ARG, "approx_dim must be 1 for scalar losses");
     }
-    if (cfg->score_function != CBH_SCORE_COSINE && cfg->score_function != CBH_SCORE_L2)
+    // Cosine, L2, SolarL2, LOOL2, SatL2 (map_score_fn, session.rs:1118-1128); the pairwise
+    // scorer of PairLogitPairwise has its own score
+    if (cfg->score_function < CBH_SCORE_COSINE || cfg->score_function > CBH_SCORE_SAT_L2)
         return fail(CBH_DECLINED, "score function not covered on device");
+    if (cfg->score_function > CBH_SCORE_L2 && cfg->loss == CBH_LOSS_PAIRLOGIT_PAIRWISE)
+        return fail(CBH_DECLINED, "SolarL2 / LOOL2 / SatL2 are pointwise score calcers");
     if (n_bins < 2 || n_bins > 256)
         return fail(CBH_DECLINED, "n_bins must be in 2..256 (u8 bins)");
     if (n == 0 || F == 0) return fail(CBH_ERR_DEGENERATE, "empty dataset");
@@ -1501,7 +1505,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
     const uint64_t n = s->n;
     hipStream_t st = s->stream;
     const int newton = s->cfg.leaf_method == CBH_LEAF_NEWTON ? 1 : 0;
-    const int cosine = s->cfg.score_function == CBH_SCORE_COSINE ? 1 : 0;
+    const int sfn = s->cfg.score_function;   // CBH_SCORE_*
     const int loss = s->cfg.loss == CBH_LOSS_RMSE ? 0 : 1;
 
     // ---- prepare: apply previous tree, ders, sample, score channels, bounds ----
@@ -1664,7 +1668,8 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         // K > 1: the parents are split over the (at most 8) waves of a feature's workgroup, 16
         // per wave from 64 parents at K >= 3 (registers), else 8 (fewer than 8: one wave)
         const uint32_t chain_pw = n_leaves >= 64 && K >= 3 ? 16u : 8u;
-        const bool chain = K > 1 && s->score_chain && s->max_cand <= 64 && n_leaves <= 8 * chain_pw &&
+        const bool chain = K > 1 && s->score_chain && sfn <= CBH_SCORE_L2 && s->max_cand <= 64 &&
+                           n_leaves <= 8 * chain_pw &&
                            (n_leaves < 8 || n_leaves % chain_pw == 0) &&
                            (uint64_t)chain_pw * s->C * s->F * s->B * 8u < (1ull << 31);
         if (s->pairwise) {
@@ -1674,32 +1679,32 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
                 if (chain_pw == 16)
                     score_chain_kernel<K, 16, false><<<s->F, 64 * (n_leaves / 16), 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
-                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
+                        sfn, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
                         &s->bounds->device_err);
             }
             if constexpr (K > 1) {
                 if (chain_pw == 8 && n_leaves >= 8)
                     score_chain_kernel<K, 8, false><<<s->F, 64 * (n_leaves / 8), 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
-                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
+                        sfn, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
                         &s->bounds->device_err);
                 else if (chain_pw == 8)
                     score_chain_kernel<K, 8, true><<<s->F, 64, 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
-                        cosine, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
+                        sfn, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
                         &s->bounds->device_err);
             }
         } else if (s->max_cand <= 64)
             score_kernel<K, 1><<<s->F, 64, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
-                                                   s->scales, s->l2, cosine, s->best_score, s->best_bin,
+                                                   s->scales, s->l2, sfn, s->best_score, s->best_bin,
                                                    s->ctr_n ? s->fweight : nullptr);
         else if (s->max_cand <= 128)
             score_kernel<K, 2><<<s->F, 128, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
-                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin,
+                                                    s->scales, s->l2, sfn, s->best_score, s->best_bin,
                                                    s->ctr_n ? s->fweight : nullptr);
         else
             score_kernel<K, 4><<<s->F, 256, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
-                                                    s->scales, s->l2, cosine, s->best_score, s->best_bin,
+                                                    s->scales, s->l2, sfn, s->best_score, s->best_bin,
                                                    s->ctr_n ? s->fweight : nullptr);
         HIP_TRY(hipGetLastError());
         if (!s->pairwise) {

@@ -42,7 +42,13 @@ enum {
     CBH_LOSS_PAIRLOGIT = 4,          /* pointwise scoring over pairwise weights */
     CBH_LOSS_PAIRLOGIT_PAIRWISE = 5  /* pairwise split scoring + Cholesky leaves */
 };
-enum { CBH_SCORE_COSINE = 0, CBH_SCORE_L2 = 1 };
+enum {   /* EScoreFunction (runtime.rs:834-870) arms of the device session (session.rs:1118-1128) */
+    CBH_SCORE_COSINE = 0,
+    CBH_SCORE_L2 = 1,
+    CBH_SCORE_SOLAR_L2 = 2,   /* per leaf: w > 1e-20 ? -s^2 (1 + 2 ln(w + 1)) / w : 0 (no L2 regularizer) */
+    CBH_SCORE_LOO_L2 = 3,     /* (w > 1 ? w / (w - 1) : 0)^2 * -s^2 / w, w > 0 */
+    CBH_SCORE_SAT_L2 = 4      /* (w > 2 ? w (w - 2) / (w^2 - 3w + 1) : 0) * -s^2 / w, w > 0 */
+};
 enum { CBH_LEAF_GRADIENT = 0, CBH_LEAF_NEWTON = 1, CBH_LEAF_SIMPLE = 2 };
 enum { CBH_BOOT_NO = 0, CBH_BOOT_BAYESIAN = 1, CBH_BOOT_BERNOULLI = 2 };
 /* float-feature preparation (crates/cb-data/src/borders.rs, nan_mode.rs) */

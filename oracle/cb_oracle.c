@@ -388,10 +388,34 @@ static void parent_totals(const double* h, uint32_t n_parent, uint32_t n_bins, i
     }
 }
 
+/* Per-leaf terms of the SolarL2 / LOOL2 / SatL2 calcers, without the L2 regularizer:
+ * solar_l2_terms (score.rs:283-299), loo_l2_terms (:304-325), sat_l2_terms (:330-350). */
+double orc_leaf_score_term(int32_t score_fn, double s, double w) {
+    if (score_fn == ORC_SCORE_SOLAR_L2) return w > 1e-20 ? (-s * s) * (1.0 + 2.0 * log(w + 1.0)) / w : 0.0;
+    if (score_fn == ORC_SCORE_LOO_L2) {
+        double adjust = w > 1.0 ? w / (w - 1.0) : 0.0;
+        adjust *= adjust;
+        return w > 0.0 ? adjust * (-s * s) / w : 0.0;
+    }
+    if (score_fn == ORC_SCORE_SAT_L2) {
+        const double adjust = w > 2.0 ? w * (w - 2.0) / (w * w - 3.0 * w + 1.0) : 0.0;
+        return w > 0.0 ? adjust * (-s * s) / w : 0.0;
+    }
+    return 0.0;
+}
+
 /* multi_dim_split_score_into (score.rs:192-265): fold in dimension-then-leaf order over the
- * 2P children (leaves 0..P-1 FALSE, P..2P-1 TRUE); sd is [K][2P], sw is [2P]. */
+ * 2P children (leaves 0..P-1 FALSE, P..2P-1 TRUE); sd is [K][2P], sw is [2P].  SolarL2, LOOL2
+ * and SatL2 (:236-265) sum their per-leaf terms in the same order. */
 static double fold_score(const double* sd, const double* sw, uint32_t n_parent, int K,
                          int score_fn, double l2) {
+    if (score_fn >= ORC_SCORE_SOLAR_L2) {
+        double acc = 0.0;
+        for (int d = 0; d < K; ++d)
+            for (uint32_t l = 0; l < 2 * n_parent; ++l)
+                acc += orc_leaf_score_term(score_fn, sd[(size_t)d * 2 * n_parent + l], sw[l]);
+        return acc;
+    }
     double num = 0.0;
     for (int d = 0; d < K; ++d)
         for (uint32_t l = 0; l < 2 * n_parent; ++l) {

@@ -39,7 +39,11 @@ typedef struct {
 
 enum { ORC_LOSS_RMSE = 0, ORC_LOSS_LOGLOSS = 1, ORC_LOSS_MULTICLASS = 2, ORC_LOSS_PAIRLOGIT = 3,
        ORC_LOSS_PAIRLOGIT_PAIRWISE = 4 };
-enum { ORC_SCORE_COSINE = 0, ORC_SCORE_L2 = 1 };
+enum { ORC_SCORE_COSINE = 0, ORC_SCORE_L2 = 1, ORC_SCORE_SOLAR_L2 = 2, ORC_SCORE_LOO_L2 = 3, ORC_SCORE_SAT_L2 = 4 };
+
+/* One leaf's additive score term of the SolarL2 / LOOL2 / SatL2 calcers (score.rs:236-330):
+ * der sum s and weight sum w of the leaf; no L2 regularizer. */
+double orc_leaf_score_term(int32_t score_fn, double s, double w);
 enum { ORC_BOOT_NO = 0, ORC_BOOT_BAYESIAN = 1, ORC_BOOT_BERNOULLI = 2 };
 enum { ORC_LEAF_GRADIENT = 0, ORC_LEAF_NEWTON = 1 };
 

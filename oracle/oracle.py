@@ -17,7 +17,7 @@ _LIB_PATH = os.path.join(_HERE, "libcb_oracle.so")
 _lib = None
 
 LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2, "PairLogit": 3, "PairLogitPairwise": 4}
-SCORE = {"Cosine": 0, "L2": 1}
+SCORE = {"Cosine": 0, "L2": 1, "SolarL2": 2, "LOOL2": 3, "SatL2": 4}
 BOOT = {"No": 0, "Bayesian": 1, "Bernoulli": 2}
 LEAF = {"Gradient": 0, "Newton": 1}
 
@@ -71,6 +71,8 @@ def lib():
         L.orc_rng_uniform.argtypes = [C.POINTER(Rng), C.c_uint64]
         L.orc_rng_uniform.restype = C.c_uint64
         L.orc_std_normal.argtypes = [C.POINTER(Rng)]
+        L.orc_leaf_score_term.argtypes = [C.c_int32, C.c_double, C.c_double]
+        L.orc_leaf_score_term.restype = C.c_double
         L.orc_std_normal.restype = C.c_double
         L.orc_fast_logf.argtypes = [C.c_float]
         L.orc_fast_logf.restype = C.c_float
@@ -162,6 +164,11 @@ def _split_flags(splits):
     splits = splits.copy()
     splits[..., 0] &= ~ONE_HOT_SPLIT
     return splits, one_hot
+
+
+def leaf_score_term(score, s, w):
+    """One leaf's additive term of the SolarL2 / LOOL2 / SatL2 calcers (der sum s, weight w)."""
+    return lib().orc_leaf_score_term(SCORE[score], float(s), float(w))
 
 
 def grow_tree(bins_fm, n_borders, score_der, score_w, depth, score="Cosine", scaled_l2=3.0,

@@ -195,6 +195,29 @@ def test_level_histograms_match_oracle_config5_shape(fill, rel, monkeypatch):
         be.end_device_training()
 
 
+@pytest.mark.parametrize("score", ["SolarL2", "LOOL2", "SatL2"])
+@pytest.mark.parametrize("loss,boot,K", [("RMSE", "Bernoulli", 1), ("Logloss", "Bayesian", 1),
+                                         ("MultiClass", "No", 3)])
+def test_solar_loo_sat_calcers_match_oracle(score, loss, boot, K):
+    """The device's SolarL2 / LOOL2 / SatL2 split scores (admitted as the reference's device
+    session does, session.rs:1118-1128) grow the oracle's trees: splits bit-exact, leaf values
+    and approximant within 1e-5, over 6 trees at depth 6 (K = 3 through the per-feature scorer)."""
+    g = np.random.default_rng(3)
+    n, F = 30_000, 24
+    bins, nb, y, _ = datagen.random_case(21, n, F, max_borders=60)
+    if loss == "Logloss":
+        y = (y + bins[0] / 30.0 > 0.5).astype(np.float64)
+    elif loss == "MultiClass":
+        y = np.clip((y + bins[1] / 20.0 + 1.5).astype(np.int64), 0, K - 1).astype(np.float64)
+    else:
+        y = y + bins[2] / 10.0
+    d = dict(bins=bins, n_borders=nb, target=y,
+             params=dict(loss=loss, depth=6, learning_rate=0.2, l2_leaf_reg=3.0, score=score,
+                         leaf_method="Newton" if K > 1 else "Gradient", bootstrap_type=boot,
+                         subsample=0.7, boost_from_average=False, approx_dim=K))
+    _assert_same_fit(*_fit_both(d, 6))
+
+
 @pytest.mark.parametrize("depth", [2, 5])
 def test_chained_scorer_wait_expiry_fails_the_tree(depth, monkeypatch):
     """The chained MultiClass scorer hands each border's running (num, den) from wave to wave

@@ -196,6 +196,80 @@ def test_tree_matches_bruteforce_partition_scoring(seed):
     assert np.array_equal(out["leaf_of"], leaf_of)
 
 
+# SolarL2 / LOOL2 / SatL2 per-leaf terms (score.rs:283-350; GPU-only upstream, so no fixture
+# holds them): values worked out by hand from the published formulas, edges included.
+CALCER_TERMS = [
+    ("SolarL2", 2.0, 3.0, -(4.0 / 3.0) * (1.0 + 2.0 * 1.3862943611198906)),   # -s^2 (1 + 2 ln 4) / 3
+    ("SolarL2", -1.0, 1.0, -(1.0 + 2.0 * 0.6931471805599453)),              # ln 2
+    ("SolarL2", 5.0, 1e-21, 0.0),                                            # w <= 1e-20
+    ("LOOL2", 2.0, 3.0, -3.0),         # (3/2)^2 * -4 / 3
+    ("LOOL2", 2.0, 1.0, 0.0),          # w <= 1: adjust 0
+    ("LOOL2", 3.0, 0.5, 0.0),
+    ("LOOL2", -4.0, 5.0, -(25.0 / 16.0) * 16.0 / 5.0),   # (5/4)^2 * -16 / 5 = -5
+    ("SatL2", 2.0, 3.0, -4.0),         # 3 (3-2) / (9-9+1) = 3;  3 * -4 / 3
+    ("SatL2", 1.0, 4.0, -0.4),         # 4 * 2 / (16-12+1) = 8/5;  1.6 * -1 / 4
+    ("SatL2", 2.0, 2.0, 0.0),          # w <= 2: adjust 0
+    ("SatL2", 2.0, 0.0, 0.0),
+]
+
+
+@pytest.mark.parametrize("score,s,w,exp", CALCER_TERMS)
+def test_leaf_score_terms_hand_computed(score, s, w, exp):
+    got = O.leaf_score_term(score, s, w)
+    assert abs(got - exp) <= 1e-15 * max(1.0, abs(exp)), (got, exp)
+
+
+def _hand_term(score, s, w):
+    """The per-leaf terms as worked out above, vectorized over leaves (test-side restatement
+    for the partition brute force; the constants above pin the formula itself)."""
+    s = np.asarray(s, np.float64)
+    w = np.asarray(w, np.float64)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        if score == "SolarL2":
+            t = (-s * s) * (1.0 + 2.0 * np.log(w + 1.0)) / w
+            return np.where(w > 1e-20, t, 0.0)
+        if score == "LOOL2":
+            adj = np.where(w > 1.0, w / (w - 1.0), 0.0) ** 2
+        else:
+            adj = np.where(w > 2.0, w * (w - 2.0) / (w * w - 3.0 * w + 1.0), 0.0)
+        return np.where(w > 0.0, adj * (-s * s) / w, 0.0)
+
+
+@pytest.mark.parametrize("score", ["SolarL2", "LOOL2", "SatL2"])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_calcer_tree_matches_bruteforce_partition_scoring(score, seed):
+    """The oracle's tree under each calcer: every level's split scores highest among the sums of
+    per-leaf terms over the 2P children, from per-leaf partition sums, and no candidate before it
+    in (feature, border) order scores higher (beyond f64 rounding of the fold: partitions that
+    coincide tie exactly).  Few rows, integer weights: leaves cross the w = 1 and w = 2 edges."""
+    rng = np.random.default_rng(10 + seed)
+    n, F, depth = 60, 5, 4
+    nb = rng.integers(1, 9, size=F).astype(np.uint32)
+    bins = np.stack([rng.integers(0, nb[f] + 1, size=n) for f in range(F)]).astype(np.uint8)
+    der = rng.normal(size=n) + 0.3 * bins[0]
+    w = rng.integers(0, 3, size=n).astype(np.float64)   # integer weights: leaves cross w = 1, 2
+    der[w == 0] = 0.0
+    out = O.grow_tree(bins, nb, der * w, w, depth, score, 1.5)
+    leaf_of = np.zeros(n, np.int64)
+    for level in range(depth):
+        P = 1 << level
+        sc = {}
+        for f in range(F):
+            for b in range(int(nb[f])):
+                nl = leaf_of + (bins[f] > b) * P
+                ss = np.bincount(nl, weights=der * w, minlength=2 * P)
+                ww = np.bincount(nl, weights=w, minlength=2 * P)
+                sc[(f, b)] = float(np.sum(_hand_term(score, ss, ww)))
+        best = max(sc.values())
+        tol = 1e-12 * max(1.0, abs(best))
+        f, b = out["splits"][level]
+        chosen = sc[(int(f), int(b))]
+        assert chosen >= best - tol
+        assert all(v <= chosen + tol for k, v in sc.items() if k < (int(f), int(b)))
+        leaf_of = leaf_of + (bins[f] > b) * P
+    assert np.array_equal(out["leaf_of"], leaf_of)
+
+
 # ------------------------------------------------------------------------------ one-hot
 def _upstream_one_hot_fit(name):
     u = G.upstream_one_hot(name)
