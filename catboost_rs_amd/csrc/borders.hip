@@ -11,7 +11,6 @@
 // column -- runs on the host, one worker per column.  Device atomics on one address cost
 // about a microsecond each in series here, so no step counts through a shared counter.
 #include <hip/hip_runtime.h>
-#include <hipcub/hipcub.hpp>
 
 #include <algorithm>
 #include <cmath>
@@ -24,6 +23,7 @@
 
 #include "../../include/cbhip.h"
 #include "common.hpp"
+#include "prim.hpp"
 
 int cbh_internal_fail(int code, const std::string& msg);  // session.hip
 
@@ -278,11 +278,11 @@ int cbh_select_borders(const float* const* columns, uint64_t n, uint32_t n_featu
     BRD_TRY(hipMemcpy(dbeg.p, beg.data(), sizeof(int) * F, hipMemcpyHostToDevice));
     BRD_TRY(hipMemcpy(dend.p, end.data(), sizeof(int) * F, hipMemcpyHostToDevice));
     size_t tmp_bytes = 0;
-    BRD_TRY(hipcub::DeviceSegmentedRadixSort::SortKeys(nullptr, tmp_bytes, dv.p, ds.p, (int)vals.size(), (int)F,
+    BRD_TRY(cbh::prim::segmented_sort_keys(nullptr, tmp_bytes, dv.p, ds.p, (int)vals.size(), (int)F,
                                                        dbeg.p, dend.p, 0, 32));
     Buf<uint8_t> tmp;
     BRD_TRY(tmp.alloc(tmp_bytes));
-    BRD_TRY(hipcub::DeviceSegmentedRadixSort::SortKeys(tmp.p, tmp_bytes, dv.p, ds.p, (int)vals.size(), (int)F,
+    BRD_TRY(cbh::prim::segmented_sort_keys(tmp.p, tmp_bytes, dv.p, ds.p, (int)vals.size(), (int)F,
                                                        dbeg.p, dend.p, 0, 32));
     BRD_TRY(hipMemcpy(vals.data(), ds.p, sizeof(float) * vals.size(), hipMemcpyDeviceToHost));
     std::vector<uint64_t> cnt(F);

@@ -14,7 +14,6 @@
 // address: device atomics on one address serialize at about a microsecond each on this GPU,
 // and category frequencies are heavily skewed.
 #include <hip/hip_runtime.h>
-#include <hipcub/hipcub.hpp>
 
 #include <algorithm>
 #include <cmath>
@@ -23,6 +22,7 @@
 
 #include "../../include/cbhip.h"
 #include "common.hpp"
+#include "prim.hpp"
 
 int cbh_internal_fail(int code, const std::string& msg);  // session.hip
 
@@ -272,10 +272,10 @@ int cbh_internal_ctr_bins(const cbh_device_ctr_column* cols, uint32_t m, const u
         const uint64_t nb = n_buckets[c0];
         const int kbits = (int)bits_for(nb ? nb - 1 : 0);
         size_t t1 = 0, t2 = 0, t3 = 0, t4 = 0;
-        CAT_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, t1, key.p, skey.p, pos.p, spos.p, N, 0, kbits, st));
-        CAT_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, t2, c.p, excl.p, N, st));
-        CAT_TRY(hipcub::DeviceScan::InclusiveScan(nullptr, t3, head.p, start.p, hipcub::Max(), N, st));
-        CAT_TRY(hipcub::DeviceReduce::Max(nullptr, t4, bsize.p, maxsz.p, (int)nb, st));
+        CAT_TRY(cbh::prim::sort_pairs(nullptr, t1, key.p, skey.p, pos.p, spos.p, N, 0, kbits, st));
+        CAT_TRY(cbh::prim::exclusive_sum(nullptr, t2, c.p, excl.p, N, st));
+        CAT_TRY(cbh::prim::inclusive_max(nullptr, t3, head.p, start.p, N, st));
+        CAT_TRY(cbh::prim::reduce_max(nullptr, t4, bsize.p, maxsz.p, (int)nb, st));
         const size_t need = std::max(std::max(t1, t2), std::max(t3, t4));
         if (need > tb) {
             CAT_TRY(hipStreamSynchronize(st));
@@ -288,18 +288,18 @@ int cbh_internal_ctr_bins(const cbh_device_ctr_column* cols, uint32_t m, const u
         gather_keys_kernel<<<grid_for(n), 256, 0, st>>>(db.p, dperm.p, n, key.p, pos.p);
         CAT_TRY(hipGetLastError());
         size_t tbx = tb;
-        CAT_TRY(hipcub::DeviceRadixSort::SortPairs(tmp.p, tbx, key.p, skey.p, pos.p, spos.p, N, 0, kbits, st));
+        CAT_TRY(cbh::prim::sort_pairs(tmp.p, tbx, key.p, skey.p, pos.p, spos.p, N, 0, kbits, st));
         segment_prep_kernel<<<grid_for(n), 256, 0, st>>>(skey.p, spos.p, dperm.p, dcls.p, n, c.p, head.p);
         CAT_TRY(hipGetLastError());
         tbx = tb;
-        CAT_TRY(hipcub::DeviceScan::ExclusiveSum(tmp.p, tbx, c.p, excl.p, N, st));
+        CAT_TRY(cbh::prim::exclusive_sum(tmp.p, tbx, c.p, excl.p, N, st));
         tbx = tb;
-        CAT_TRY(hipcub::DeviceScan::InclusiveScan(tmp.p, tbx, head.p, start.p, hipcub::Max(), N, st));
+        CAT_TRY(cbh::prim::inclusive_max(tmp.p, tbx, head.p, start.p, N, st));
         CAT_TRY(hipMemsetAsync(bsize.p, 0, sizeof(uint32_t) * nb, st));
         segment_size_kernel<<<grid_for(n), 256, 0, st>>>(skey.p, start.p, n, bsize.p);
         CAT_TRY(hipGetLastError());
         tbx = tb;
-        CAT_TRY(hipcub::DeviceReduce::Max(tmp.p, tbx, bsize.p, maxsz.p, (int)nb, st));
+        CAT_TRY(cbh::prim::reduce_max(tmp.p, tbx, bsize.p, maxsz.p, (int)nb, st));
         for (uint32_t k = c0; k < m; ++k) {
             if (done[k] || cols[k].member_bins[0] != member) continue;
             done[k] = true;
@@ -349,24 +349,24 @@ int cbh_perfect_hash(const uint32_t* keys, uint64_t n, uint32_t* bins_out, uint3
     CAT_TRY(hipMemcpy(k.p, keys, sizeof(uint32_t) * n, hipMemcpyHostToDevice));
     const int N = (int)n;
     size_t t1 = 0, t2 = 0, t3 = 0;
-    CAT_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, t1, k.p, ks.p, idx.p, sidx.p, N, 0, 32));
-    CAT_TRY(hipcub::DeviceScan::InclusiveSum(nullptr, t2, flag.p, segid1.p, N));
-    CAT_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, t3, first.p, sfirst.p, seg.p, sseg.p, N, 0,
+    CAT_TRY(cbh::prim::sort_pairs(nullptr, t1, k.p, ks.p, idx.p, sidx.p, N, 0, 32));
+    CAT_TRY(cbh::prim::inclusive_sum(nullptr, t2, flag.p, segid1.p, N));
+    CAT_TRY(cbh::prim::sort_pairs(nullptr, t3, first.p, sfirst.p, seg.p, sseg.p, N, 0,
                                                (int)bits_for(n)));
     Buf<uint8_t> tmp;
     size_t tb = std::max(t1, std::max(t2, t3));
     CAT_TRY(tmp.alloc(tb));
     iota_kernel<<<grid_for(n), 256>>>(idx.p, n);
     CAT_TRY(hipGetLastError());
-    CAT_TRY(hipcub::DeviceRadixSort::SortPairs(tmp.p, tb, k.p, ks.p, idx.p, sidx.p, N, 0, 32));
+    CAT_TRY(cbh::prim::sort_pairs(tmp.p, tb, k.p, ks.p, idx.p, sidx.p, N, 0, 32));
     head_flag_kernel<<<grid_for(n), 256>>>(ks.p, n, flag.p);
     CAT_TRY(hipGetLastError());
-    CAT_TRY(hipcub::DeviceScan::InclusiveSum(tmp.p, tb, flag.p, segid1.p, N));
+    CAT_TRY(cbh::prim::inclusive_sum(tmp.p, tb, flag.p, segid1.p, N));
     uint32_t d = 0;
     CAT_TRY(hipMemcpy(&d, segid1.p + (n - 1), sizeof(uint32_t), hipMemcpyDeviceToHost));
     segment_first_kernel<<<grid_for(n), 256>>>(ks.p, sidx.p, segid1.p, n, first.p, seg.p);
     CAT_TRY(hipGetLastError());
-    CAT_TRY(hipcub::DeviceRadixSort::SortPairs(tmp.p, tb, first.p, sfirst.p, seg.p, sseg.p, (int)d, 0,
+    CAT_TRY(cbh::prim::sort_pairs(tmp.p, tb, first.p, sfirst.p, seg.p, sseg.p, (int)d, 0,
                                                (int)bits_for(n)));
     rank_kernel<<<grid_for(d), 256>>>(sseg.p, d, rank.p);
     CAT_TRY(hipGetLastError());
@@ -433,29 +433,29 @@ int cbh_ctr_columns(const uint32_t* buckets, uint32_t n_buckets, uint64_t n, con
     const int N = (int)n;
     const int kbits = (int)bits_for(n_buckets ? n_buckets - 1 : 0);
     size_t t1 = 0, t2 = 0, t3 = 0, t4 = 0;
-    CAT_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, t1, key.p, skey.p, pos.p, spos.p, N, 0, kbits));
-    CAT_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, t2, c.p, excl.p, N));
-    CAT_TRY(hipcub::DeviceScan::InclusiveScan(nullptr, t3, head.p, start.p, hipcub::Max(), N));
-    CAT_TRY(hipcub::DeviceReduce::Max(nullptr, t4, bsize.p, maxsz.p, (int)n_buckets));
+    CAT_TRY(cbh::prim::sort_pairs(nullptr, t1, key.p, skey.p, pos.p, spos.p, N, 0, kbits));
+    CAT_TRY(cbh::prim::exclusive_sum(nullptr, t2, c.p, excl.p, N));
+    CAT_TRY(cbh::prim::inclusive_max(nullptr, t3, head.p, start.p, N));
+    CAT_TRY(cbh::prim::reduce_max(nullptr, t4, bsize.p, maxsz.p, (int)n_buckets));
     Buf<uint8_t> tmp;
     const size_t tb = std::max(std::max(t1, t2), std::max(t3, t4));
     CAT_TRY(tmp.alloc(tb));
     gather_keys_kernel<<<grid_for(n), 256>>>(db.p, dperm.p, n, key.p, pos.p);
     CAT_TRY(hipGetLastError());
     size_t tbx = tb;
-    CAT_TRY(hipcub::DeviceRadixSort::SortPairs(tmp.p, tbx, key.p, skey.p, pos.p, spos.p, N, 0, kbits));
+    CAT_TRY(cbh::prim::sort_pairs(tmp.p, tbx, key.p, skey.p, pos.p, spos.p, N, 0, kbits));
     segment_prep_kernel<<<grid_for(n), 256>>>(skey.p, spos.p, dperm.p, dcls.p, n, c.p, head.p);
     CAT_TRY(hipGetLastError());
     tbx = tb;
-    CAT_TRY(hipcub::DeviceScan::ExclusiveSum(tmp.p, tbx, c.p, excl.p, N));
+    CAT_TRY(cbh::prim::exclusive_sum(tmp.p, tbx, c.p, excl.p, N));
     tbx = tb;
-    CAT_TRY(hipcub::DeviceScan::InclusiveScan(tmp.p, tbx, head.p, start.p, hipcub::Max(), N));
+    CAT_TRY(cbh::prim::inclusive_max(tmp.p, tbx, head.p, start.p, N));
     // bucket sizes: zero-filled (empty buckets stay 0), the last slot of each segment writes
     CAT_TRY(hipMemset(bsize.p, 0, sizeof(uint32_t) * n_buckets));
     segment_size_kernel<<<grid_for(n), 256>>>(skey.p, start.p, n, bsize.p);
     CAT_TRY(hipGetLastError());
     tbx = tb;
-    CAT_TRY(hipcub::DeviceReduce::Max(tmp.p, tbx, bsize.p, maxsz.p, (int)n_buckets));
+    CAT_TRY(cbh::prim::reduce_max(tmp.p, tbx, bsize.p, maxsz.p, (int)n_buckets));
     ctr_finalize_kernel<<<grid_for(n), 256>>>(skey.p, spos.p, dperm.p, excl.p, start.p, bsize.p, maxsz.p, n, sp,
                                               n_specs, border_count, dbins.p, values_out ? dvals.p : nullptr,
                                               class_counts_out ? counts.p : nullptr);

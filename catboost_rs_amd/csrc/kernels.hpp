@@ -2263,7 +2263,7 @@ __device__ __forceinline__ double leaf_score_term(int sf, double s, double w) {
 
 // sf (CBH_SCORE_*): Cosine and L2 fold avg * s into num and avg^2 * w into den; SolarL2, LOOL2 and
 // SatL2 fold their per-leaf terms into num, in the same (d, side, p) order.
-template <int K, bool kOneHot>
+template <int K, bool kOneHot, bool kTerms /* SolarL2 / LOOL2 / SatL2 (sf) */>
 __device__ __forceinline__ void score_fold(const long long* __restrict__ hist, uint32_t P, uint32_t F, uint32_t B,
                                            uint32_t f, uint32_t b, double inv_d, double inv_w, double l2, int sf,
                                            double& num, double& den) {
@@ -2307,7 +2307,7 @@ __device__ __forceinline__ void score_fold(const long long* __restrict__ hist, u
                     }
                     const double s = (double)xd * inv_d;
                     const double w = (double)xw * inv_w;
-                    if (sf > 1) {   // workgroup-uniform
+                    if (kTerms) {
                         num += leaf_score_term(sf, s, w);
                         continue;
                     }
@@ -2352,10 +2352,14 @@ __global__ __launch_bounds__(64 * NW) void score_kernel(
     den += 1e-100;
     // the histograms are in prefix form over bins: prefix = cell b, total = cell B-1, the
     // bin itself (one-hot) = cell b - cell b-1; the fold order over (d, side, p) is the reference's
-    if (oh)
-        score_fold<K, true>(hist, P, F, B, f, b, inv_d, inv_w, l2, sf, num, den);
+    if (sf > 1 && oh)
+        score_fold<K, true, true>(hist, P, F, B, f, b, inv_d, inv_w, l2, sf, num, den);
+    else if (sf > 1)
+        score_fold<K, false, true>(hist, P, F, B, f, b, inv_d, inv_w, l2, sf, num, den);
+    else if (oh)
+        score_fold<K, true, false>(hist, P, F, B, f, b, inv_d, inv_w, l2, sf, num, den);
     else
-        score_fold<K, false>(hist, P, F, B, f, b, inv_d, inv_w, l2, sf, num, den);
+        score_fold<K, false, false>(hist, P, F, B, f, b, inv_d, inv_w, l2, sf, num, den);
     double score = sf == 0 ? num / sqrt(den) : num;
     // the model_size_reg weight of a CTR column multiplies every candidate's score
     // (weight * score, tree.rs:3340-3346)
