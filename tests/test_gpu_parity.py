@@ -873,6 +873,37 @@ def test_config3_full_size_first_trees_match_oracle(loss):
     _assert_same_fit(*_fit_both(d, 20, n_threads=16))
 
 
+def test_config5_full_size_all_trees_packed_equals_exact_fill(monkeypatch):
+    """Config 5 at its full size (1M x 4096, 70% zeros, MultiClass K=10, depth 8) over all 50
+    trees: the packed multi-channel fill (its default: two channels rounded to 20-bit fields per
+    64-bit atomic, over sparse entries) and the generic fill (exact 61-bit sums) choose the same
+    split at every level, so trees, leaves and approximant are identical."""
+    d = datagen.config5()
+    P = dict(d["params"])
+    nb = d["n_borders"]
+    K = P.get("approx_dim", 10)
+    kw = dict(loss=P["loss"], depth=P["depth"], learning_rate=P["learning_rate"],
+              l2_leaf_reg=P["l2_leaf_reg"], score=P["score"], leaf_method=P["leaf_method"],
+              bootstrap_type=P["bootstrap_type"], boost_from_average=P["boost_from_average"],
+              random_seed=P.get("random_seed", 0), approx_dim=K)
+    iters = P["iterations"]
+    out = {}
+    for mode in ("generic", "packed"):
+        monkeypatch.setenv("CBH_FILL", mode)
+        tr = cb.Trainer(d["bins"], int(nb.max()) + 1, d["target"], real_folds=nb + 1, **kw)
+        try:
+            assert tr.stats()["fill_mode"] in ((0,) if mode == "generic" else (3, 4))
+            sp, lv = tr.fit(iters)
+            out[mode] = (sp, lv, tr.approx())
+        finally:
+            tr.close()
+    (s0, l0, a0), (s1, l1, a1) = out["generic"], out["packed"]
+    for it in range(iters):
+        assert np.array_equal(s0[it], s1[it]), f"tree {it} splits differ"
+    assert np.array_equal(l0, l1)
+    assert np.array_equal(a0, a1)
+
+
 def test_config5_full_size_first_trees_match_oracle():
     """Config 5 at its full size (1M x 4096, 70% zeros, MultiClass K=10, depth 8): the first
     three trees against the oracle on 16 host threads."""
