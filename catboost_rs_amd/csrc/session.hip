@@ -668,8 +668,13 @@ int plan_pkk(cbh_session* s, const std::string& v) {
     const std::string sv = se ? se : "";
     if (s->use_skip && sv != "off" && (sv == "on" || s->nd_per_tile <= 12.0)) {
         const size_t slots = (size_t)s->pkk_tiles * s->n * 16;
-        CHECK(dalloc(&s->pks_a, slots));
-        CHECK(dalloc(&s->pks_b, slots));
+        if (dalloc(&s->pks_a, slots) != CBH_OK || dalloc(&s->pks_b, slots) != CBH_OK) {
+            // no room for the entries (64 bytes per row and tile): the dense visit needs none
+            dfree(s->pks_a);
+            dfree(s->pks_b);
+            (void)hipGetLastError();
+            return CBH_OK;
+        }
         pack_sparse_kernel<<<grid_for((uint64_t)s->pkk_tiles * s->n, 256), 256, 0, s->stream>>>(
             s->cols, s->n, s->F, s->pkk_tiles, s->skip_bin, s->pks_a, s->pks_b);
         if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess)
@@ -1109,11 +1114,12 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     // of a row never straddles a 64-byte sector and a row spans whole 128-byte lines, which
     // the fill's gathers through the partitioned index list fetch (config 2: fill 0.559 ->
     // 0.531 ms per launch; configs 1, 3, 4 unchanged).  CBH_ROW_ALIGN_WORDS sets another
-    // multiple (1: unpadded), a measurement knob
+    // multiple, rounded up to 8 words (a measurement knob): the multi-channel fills read a
+    // row's words in whole 8-word tiles, which must stay inside the row
     uint32_t align = 16;
     if (const char* e = std::getenv("CBH_ROW_ALIGN_WORDS")) {
         const long a = std::strtol(e, nullptr, 10);
-        if (a >= 1 && a <= 64) align = (uint32_t)a;
+        if (a >= 1 && a <= 64) align = (uint32_t)((a + 7) / 8 * 8);
     }
     s->Ws = (s->W + align - 1) / align * align;
     s->K = (uint32_t)cfg->approx_dim;

@@ -354,7 +354,9 @@ int cbh_hist_build(const uint8_t* bins_fm, uint64_t n, uint32_t n_features, uint
  * (K + 1) bytes plus 5 KiB must fit, else CBH_ERR_OUT_OF_RANGE.  Every call on one GPU
  * shares that array: calls that overlap on one GPU (other streams, other host threads)
  * race.  The result equals cbh_hist_build's with slot_of_row NULL (the same scale rule
- * from the sums of max_d |der| and |w|, summed on the device). */
+ * from the sums of max_d |der| and |w|, summed on the device).  Precondition: every bin is
+ * below n_bins (cbh_hist_build checks this on the host; here the bins are never read by the
+ * host, and a larger bin adds to another feature's cells: the result is then undefined). */
 int cbh_hist_build_noalloc(const uint8_t* bins_fm, uint64_t n, uint32_t n_features, uint32_t n_bins,
                            const double* der, const double* w, uint32_t K, double* hist_out, void* stream);
 

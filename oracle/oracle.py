@@ -16,7 +16,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libcb_oracle.so")
 _lib = None
 
-LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2, "PairLogit": 3, "PairLogitPairwise": 4}
+# CrossEntropy (soft targets in [0, 1]) runs the Logloss arm: its ders are the Logloss ders by
+# definition (cross_entropy_der1/2, loss.rs:80-97)
+LOSS = {"RMSE": 0, "Logloss": 1, "MultiClass": 2, "PairLogit": 3, "PairLogitPairwise": 4, "CrossEntropy": 1}
 SCORE = {"Cosine": 0, "L2": 1, "SolarL2": 2, "LOOL2": 3, "SatL2": 4}
 BOOT = {"No": 0, "Bayesian": 1, "Bernoulli": 2}
 LEAF = {"Gradient": 0, "Newton": 1}

@@ -218,6 +218,26 @@ def test_solar_loo_sat_calcers_match_oracle(score, loss, boot, K):
     _assert_same_fit(*_fit_both(d, 6))
 
 
+@pytest.mark.parametrize("boot", ["No", "Bayesian"])
+def test_crossentropy_soft_targets_match_oracle(boot):
+    """CrossEntropy, which the device session admits (runtime.rs loss arms; ders identical to
+    Logloss's, loss.rs:80-97), over soft targets in [0, 1]: gradients, and a 6-tree depth-6 fit
+    against the oracle (splits bit-exact, leaves and approximant within 1e-5)."""
+    g = np.random.default_rng(8)
+    n, F = 40_000, 20
+    bins, nb, _, _ = datagen.random_case(33, n, F, max_borders=50)
+    t = 1.0 / (1.0 + np.exp(-(bins[:4].astype(np.float64).sum(0) / 40.0 - 1.0 + 0.5 * g.standard_normal(n))))
+    a = g.normal(size=n)
+    d1, d2 = cb.compute_gradients("CrossEntropy", a, t)
+    e1, e2 = O.ders("CrossEntropy", a, t)
+    np.testing.assert_allclose(d1, e1, rtol=1e-14, atol=1e-15)
+    np.testing.assert_allclose(d2, e2, rtol=1e-14, atol=1e-15)
+    d = dict(bins=bins, n_borders=nb, target=t,
+             params=dict(loss="CrossEntropy", depth=6, learning_rate=0.3, l2_leaf_reg=3.0, score="Cosine",
+                         leaf_method="Gradient", bootstrap_type=boot, boost_from_average=False))
+    _assert_same_fit(*_fit_both(d, 6))
+
+
 @pytest.mark.parametrize("depth", [2, 5])
 def test_chained_scorer_wait_expiry_fails_the_tree(depth, monkeypatch):
     """The chained MultiClass scorer hands each border's running (num, den) from wave to wave
@@ -808,12 +828,14 @@ def test_config2_full_size_all_trees_tiled_equals_generic_fill(monkeypatch):
 
 @pytest.mark.parametrize("layout", ["bin", "feature", "packed", "tiled", "count"])
 @pytest.mark.parametrize("F,B,K", [(37, 17, 1), (5, 256, 1), (65, 33, 3), (33, 2, 1), (100, 255, 1),
-                                   (129, 256, 1), (64, 255, 1), (36, 40, 1), (44, 129, 1)])
+                                   (129, 256, 1), (64, 255, 1), (36, 40, 1), (44, 129, 1), (40, 76, 3),
+                                   (40, 90, 3), (50, 76, 1), (50, 90, 1)])
 def test_fill_layouts_ragged_shapes_match_oracle(layout, F, B, K, monkeypatch):
     """Every fill on ragged tiles: feature counts that leave a short last tile (1 to 7 words of
     the tiled fill's 8: a narrow 1- or 2-word tile runs its own loop) or a partial word, 2 to 256
-    bins, K = 1 and a 3-class MultiClass (4 channels; "packed" then means the packed
-    multi-channel fill, "tiled" the generic fill)."""
+    bins (76 and 90 bins take the 16- and 32-lane prefix passes), K = 1 and a 3-class
+    MultiClass (4 channels; "packed" then means the packed multi-channel fill, "tiled" the
+    generic fill)."""
     if layout in ("bin", "feature"):
         monkeypatch.setenv("CBH_FILL", "generic")
         monkeypatch.setenv("CBH_FILL_LAYOUT", layout)

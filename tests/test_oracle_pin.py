@@ -196,6 +196,21 @@ def test_tree_matches_bruteforce_partition_scoring(seed):
     assert np.array_equal(out["leaf_of"], leaf_of)
 
 
+def test_crossentropy_ders_are_the_logloss_ders():
+    """cross_entropy_der1/2 (loss.rs:80-97) are defined as the Logloss ders over the same
+    (soft) targets; the oracle's CrossEntropy arm equals its Logloss arm, and the Logloss ders
+    hold their closed form at sampled points (der1 = t - p, der2 = -p (1 - p))."""
+    g = np.random.default_rng(2)
+    a = g.normal(size=1000) * 4
+    t = g.random(1000)
+    c1, c2 = O.ders("CrossEntropy", a, t)
+    l1, l2 = O.ders("Logloss", a, t)
+    assert np.array_equal(c1, l1) and np.array_equal(c2, l2)
+    p = 1.0 / (1.0 + np.exp(-a))
+    np.testing.assert_allclose(l1, t - p, rtol=1e-12, atol=1e-15)
+    np.testing.assert_allclose(l2, -p * (1.0 - p), rtol=1e-12, atol=1e-15)
+
+
 # SolarL2 / LOOL2 / SatL2 per-leaf terms (score.rs:283-350; GPU-only upstream, so no fixture
 # holds them): values worked out by hand from the published formulas, edges included.
 CALCER_TERMS = [
