@@ -327,25 +327,30 @@ def main():
     log(f"fill: {st['fill_launches']} launches, avg {st['fill_ms'] / max(1, st['fill_launches']):.4f} ms, "
         f"{achieved:.1f} GB/s algorithmic")
 
-    # LDS-atomic roofline of the fill: every visited (row, feature) adds one 64-bit LDS atomic
-    # (packed fill: both channels in one word), ceil((K+1)/2) (packed multi-channel fill: two
-    # channels per word) or K+1 (two-channel / channel-split fills); the
-    # cap is the contiguous (conflict-free) 64-bit LDS atomic rate measured on this GPU, the
-    # pattern the fills' rotated lane layouts reach
+    # LDS-atomic roofline of the fill: every (row, feature) entry the fill adds costs one 64-bit
+    # LDS atomic (packed and count-packed fills: both channels in one word), ceil((K+1)/2)
+    # (packed multi-channel fills: two channels per word) or K+1 (two-channel / channel-split
+    # fills); with the dominant-bin skip the entries are the issued ones (bins other than the
+    # feature's dominant bin), counted by the library over the profiled trees.  The cap is the
+    # contiguous (conflict-free) 64-bit LDS atomic rate measured on this GPU, the pattern the
+    # fills' rotated lane layouts reach
     K = kw["approx_dim"] if P["loss"] == "MultiClass" else 1
     per_pair = {1: 1, 3: (K + 2) // 2, 4: (K + 2) // 2, 5: 1}.get(st["fill_mode"], K + 1)
     lds = None
     rates = _lds_rates()
     if "contiguous_u64" in rates and fill_s > 0:
-        ach = st["fill_row_features"] * per_pair / fill_s
-        # with a dominant-bin skip (sparse columns) fewer atomics are issued than counted
+        entries = st["fill_entries"] if st["skip_features"] else st["fill_row_features"]
+        ach = entries * per_pair / fill_s
         lds = {"achieved_lane_atomics_per_s": round(ach, 1),
-               "atomics_per_row_feature": per_pair,
+               "atomics_per_entry": per_pair,
+               "entries": entries,
                "counted_as": "all (row, feature) pairs" if not st["skip_features"] else
-               f"all (row, feature) pairs; {st['skip_features']} of {F} features skip their dominant bin",
+               f"issued: the {entries} (row, feature) entries whose bin is not the feature's dominant bin, "
+               f"of {st['fill_row_features']} visited pairs ({st['skip_features']} of {F} features skip "
+               f"their dominant bin)",
                "cap_contiguous_u64_per_s": rates["contiguous_u64"],
                "frac_of_contiguous_cap": round(ach / rates["contiguous_u64"], 4)}
-        log(f"fill LDS atomics: {ach:.3e}/s ({per_pair} per row-feature) = "
+        log(f"fill LDS atomics: {ach:.3e}/s ({per_pair} per entry, {entries} entries) = "
             f"{100 * ach / rates['contiguous_u64']:.1f}% of the measured conflict-free 64-bit cap "
             f"{rates['contiguous_u64']:.3e}/s")
 

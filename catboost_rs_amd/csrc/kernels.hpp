@@ -2190,6 +2190,33 @@ static __global__ __launch_bounds__(256) void bin_census_kernel(const uint8_t* _
         atomicAdd(counts + (size_t)blockIdx.y * 256 + threadIdx.x, (unsigned long long)c[threadIdx.x]);
 }
 
+// Entries a row adds to the level histograms when the fill leaves out the dominant bins: the
+// features with no dominant bin plus those whose bin is not it ([n], counted once).
+static __global__ __launch_bounds__(256) void row_entries_kernel(const uint8_t* __restrict__ cols /* [F][n] */,
+                                                                 uint64_t n, uint32_t F,
+                                                                 const uint32_t* __restrict__ skip_bin,
+                                                                 uint16_t* __restrict__ out) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+        uint32_t c = 0;
+        for (uint32_t f = 0; f < F; ++f) c += cols[(size_t)f * n + i] != skip_bin[f];
+        out[i] = (uint16_t)c;
+    }
+}
+
+// The entries one fill launch adds (profiling only): the sum of the visited rows' entry counts
+// (idx: the partition's listed rows, plan->rows of them; else rows [0, n)).
+static __global__ __launch_bounds__(256) void fill_entries_kernel(const uint32_t* __restrict__ idx,
+                                                                  const LevelPlan* __restrict__ plan, uint64_t n,
+                                                                  const uint16_t* __restrict__ ent,
+                                                                  unsigned long long* __restrict__ total) {
+    const uint32_t V = idx ? plan->rows : (uint32_t)n;
+    unsigned long long c = 0;
+    for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < V; p += gridDim.x * blockDim.x)
+        c += ent[idx ? idx[p] : p];
+    c = wave_sum_u64(c);
+    if (lane_id() == 0 && c != 0) atomicAdd(total, c);
+}
+
 // Channel totals of the rows of every directly built segment: tot [segment][C].
 static __global__ __launch_bounds__(256) void seg_totals_kernel(const uint32_t* __restrict__ idx,
                                                                 const LevelPlan* __restrict__ plan, uint64_t n,
@@ -2479,15 +2506,23 @@ __device__ __forceinline__ void score_term(double s, double w, double l2, double
 // The launcher passes P = PW * (waves of the workgroup), every wave owning a full block, or
 // (kPartial) one wave with P < PW parents: its blocks' parents past P read parent P-1's cells
 // and add exact zeros (num >= +0 and den > 0 are unchanged by them).
+// A workgroup scores nf features f, f + 1, ... (nf * B <= 64; nf > 1 only without one-hot
+// features): lane gi * B + b is border b of feature f + gi, lanes past the groups (or past F) read
+// border B-1 of feature f and their scores are discarded.
 template <int K, int PW, bool kPartial, bool kOneHot>
 __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, uint32_t P, uint32_t F,
-                                            uint32_t B, uint32_t f, double inv_d, double inv_w, double l2,
-                                            unsigned long long* ring /* [waves][2][64] */, double& num,
+                                            uint32_t B, uint32_t f, uint32_t nf, double inv_d, double inv_w,
+                                            double l2, unsigned long long* ring /* [waves][2][64] */, double& num,
                                             double& den, uint32_t spin, unsigned long long* err) {
     constexpr int C = K + 1;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
-    const uint32_t bc = min(lane, B - 1);
+    const uint32_t gr = lane / B;
+    const bool lane_on = gr < nf && f + gr < F;
+    const uint32_t gi = lane_on ? gr : 0u;                 // feature f + gi
+    const uint32_t bc = lane_on ? lane - gr * B : B - 1;   // border
+    const uint32_t off_c = gi * B + bc;                    // cells from feature f's row
+    const uint32_t off_tot = gi * B + (B - 1);             // feature f + gi's total
     const uint32_t p0 = wv * PW;
     auto pu = [&](uint32_t u) { return kPartial ? min(u, P - 1) : u; };   // block slot -> parent offset
     // weight sums of both children of every parent of this wave (FALSE side 0, TRUE side 1)
@@ -2495,7 +2530,7 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
 #pragma unroll
     for (int u = 0; u < PW; ++u) {
         const GlobalI64 hw = uniform_ptr(hist + (((size_t)(p0 + pu(u)) * C + K) * F + f) * B);
-        const long long pw = hw[bc], tw = uniform_cell(hw + (B - 1));
+        const long long pw = hw[off_c], tw = nf == 1 ? uniform_cell(hw + (B - 1)) : hw[off_tot];
         long long x0, x1;
         if (kOneHot) {   // the bin itself = prefix[b] - prefix[b-1]; TRUE = the bin
             long long qw = __shfl_up(pw, 1, 64);
@@ -2510,14 +2545,17 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
         w1[u] = (double)x1 * inv_w;
     }
     // a dimension's cells: the prefixes of every parent (one vector load each), and the
-    // totals of all PW parents in one vector load (lane u holds parent u's), read out per
-    // parent with readlane (wave-uniform values)
+    // totals of all PW parents of all nf features in one vector load (lane g * PW + u holds
+    // feature f + g's total of parent u), read out per parent with readlane (nf == 1: wave-uniform
+    // values) or a lane shuffle
     long long pd[PW], tdv;
     // byte offsets from the row of (parent p0, dimension d): parent p0 + u is u * C * F * B
     // cells further (the launcher keeps PW of those strides below 2^31 bytes)
     const uint32_t pstride = (uint32_t)C * F * B * 8u;
-    const uint32_t off_d = bc * 8u;
-    const uint32_t off_t = pu(min(lane, (uint32_t)PW - 1)) * pstride + (B - 1) * 8u;
+    const uint32_t off_d = off_c * 8u;
+    const uint32_t nfe = min(nf, F - f);   // features of this workgroup (the last may hold fewer)
+    const uint32_t tg = min(lane / (uint32_t)PW, nfe - 1), tu = nf == 1 ? min(lane, (uint32_t)PW - 1) : lane % PW;
+    const uint32_t off_t = pu(tu) * pstride + (tg * B + (B - 1)) * 8u;
     // wave-uniform byte addresses (kept in SGPRs, 64-bit scalar adds): the row of (parent p0,
     // dimension d) is row0 + d * dstride; parent p0 + u is u parent strides further
     const uint64_t pstride64 = (uint64_t)C * F * B * 8u, dstride64 = (uint64_t)F * B * 8u;
@@ -2540,7 +2578,7 @@ __device__ __forceinline__ void score_chain(const long long* __restrict__ hist, 
 #pragma unroll
             for (int u = 0; u < PW; ++u) {
                 long long xd;
-                const long long td = readlane64(tdv, u);
+                const long long td = nf == 1 ? readlane64(tdv, u) : __shfl(tdv, (int)(gi * PW + u), 64);
                 if (kOneHot) {
                     long long qd = __shfl_up(pd[u], 1, 64);
                     if (lane == 0) qd = 0;
@@ -2584,19 +2622,23 @@ __global__ __launch_bounds__(512) void score_chain_kernel(
     const Scales* __restrict__ sc, double l2, int sf /* CBH_SCORE_COSINE or _L2 */, double* __restrict__ best_score,
     uint32_t* __restrict__ best_bin, const double* __restrict__ fweight /* nullable [F] */,
     uint32_t spin /* polls a wave's wait for its turn may take */,
-    unsigned long long* __restrict__ err /* the tree's device error word */) {
+    unsigned long long* __restrict__ err /* the tree's device error word */, uint32_t nf /* features per workgroup */) {
     __shared__ unsigned long long ring[8 * 2 * 64];   // outboxes [wave][num, den][lane]
-    const uint32_t f = blockIdx.x;
-    // clear feature f's cells of the next level's histogram [leaf][HC][F][B] (its fill adds)
-    for (uint32_t i = threadIdx.x; i < zero_leaves * HC * B; i += blockDim.x) {
-        const uint32_t lc = i / B, bb = i - lc * B;
-        zero_buf[((size_t)lc * F + f) * B + bb] = 0;
+    __shared__ double red[64];
+    // features f .. f + nf - 1 (nf > 1: B <= 64 / nf and no one-hot features)
+    const uint32_t f = blockIdx.x * nf;
+    const uint32_t nfe = min(nf, F - f);
+    // clear the features' cells of the next level's histogram [leaf][HC][F][B] (its fill adds)
+    for (uint32_t i = threadIdx.x; i < zero_leaves * HC * nfe * B; i += blockDim.x) {
+        const uint32_t lc = i / (nfe * B), fb = i - lc * (nfe * B);
+        zero_buf[((size_t)lc * F + f) * B + fb] = 0;
     }
-    const uint32_t nc = n_cand[f];
-    if (nc == 0) {   // workgroup-uniform: no wave enters the chain
-        if (threadIdx.x == 0) {
-            best_score[f] = -INFINITY;
-            best_bin[f] = 0;
+    uint32_t any_cand = 0;
+    for (uint32_t g = 0; g < nfe; ++g) any_cand |= n_cand[f + g];
+    if (any_cand == 0) {   // workgroup-uniform: no wave enters the chain
+        if (threadIdx.x < nfe) {
+            best_score[f + threadIdx.x] = -INFINITY;
+            best_bin[f + threadIdx.x] = 0;
         }
         return;
     }
@@ -2607,27 +2649,50 @@ __global__ __launch_bounds__(512) void score_chain_kernel(
     double den = 0.0;
     den += 1e-100;
     if (one_hot != nullptr && one_hot[f] != 0)
-        score_chain<K, PW, kPartial, true>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den, spin, err);
+        score_chain<K, PW, kPartial, true>(hist, P, F, B, f, 1u, inv_d, inv_w, l2, ring, num, den, spin, err);
     else
-        score_chain<K, PW, kPartial, false>(hist, P, F, B, f, inv_d, inv_w, l2, ring, num, den, spin, err);
+        score_chain<K, PW, kPartial, false>(hist, P, F, B, f, nf, inv_d, inv_w, l2, ring, num, den, spin, err);
     // the last wave made the last hop: its (num, den) are the full fold
     if ((threadIdx.x >> 6) != (blockDim.x >> 6) - 1) return;
-    const uint32_t b = threadIdx.x & 63u;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t gr = lane / B, b = lane - gr * B;
+    const bool on = gr < nfe;
     double score = sf == 0 ? num / sqrt(den) : num;
-    if (fweight) score = fweight[f] * score;
-    if (b >= nc || score != score) score = -INFINITY;
-    uint32_t bb = b;
-    for (int o = 32; o > 0; o >>= 1) {
-        double os = __shfl_xor(score, o, 64);
-        uint32_t ob = __shfl_xor(bb, o, 64);
-        if (os > score || (os == score && ob < bb)) {
-            score = os;
-            bb = ob;
+    if (on && fweight) score = fweight[f + gr] * score;
+    if (!on || b >= n_cand[f + gr] || score != score) score = -INFINITY;
+    if (nf == 1) {
+        uint32_t bb = lane;
+        for (int o = 32; o > 0; o >>= 1) {
+            double os = __shfl_xor(score, o, 64);
+            uint32_t ob = __shfl_xor(bb, o, 64);
+            if (os > score || (os == score && ob < bb)) {
+                score = os;
+                bb = ob;
+            }
         }
+        if (lane == 0) {
+            best_score[f] = score;
+            best_bin[f] = bb;
+        }
+        return;
     }
-    if (b == 0) {
-        best_score[f] = score;
-        best_bin[f] = bb;
+    // nf > 1: lane g scans feature f + g's B borders in order (strict first-wins)
+    red[lane] = score;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < nfe) {
+        double best = -INFINITY;
+        uint32_t bb = 0;
+        for (uint32_t k = 0; k < B; ++k) {
+            const double v = red[lane * B + k];
+            if (v > best) {
+                best = v;
+                bb = k;
+            }
+        }
+        best_score[f + lane] = best;
+        best_bin[f + lane] = bb;
     }
 }
 

@@ -137,6 +137,7 @@ struct cbh_session {
     uint32_t max_cand = 0;           // most candidates of any feature (threads of the scorer)
     bool score_chain = true;         // parents split over waves for K > 1 (CBH_SCORE_CHAIN=off: one wave)
     uint32_t chain_spin = kChainSpinLimit;   // polls of a chained scorer wave's wait (CBH_CHAIN_SPIN: a test knob)
+    uint32_t chain_nf = 0;   // features per chained-scorer workgroup at most (CBH_CHAIN_FEATURES; 0: no cap)
     uint8_t* one_hot = nullptr;
     Scales* scales = nullptr;
     Bounds* bounds = nullptr;
@@ -188,6 +189,8 @@ struct cbh_session {
     bool use_skip = false;
     uint64_t n_skip = 0;
     double nd_per_tile = 32.0;       // mean non-dominant (feature, bin) entries of a row per 32-feature tile
+    uint16_t* row_ent = nullptr;     // profiling with the dominant-bin skip: entries per row
+    unsigned long long* fill_ent = nullptr;   // profiling: entries the fill launches added (device)
     bool pks = false;                // packed multi-channel fill over sparse entries
     uint16_t* pks_a = nullptr;       // [pkk_tiles][n][16] entry codes 0..15 of every (tile, row)
     uint16_t* pks_b = nullptr;       // [pkk_tiles][n][16] entry codes 16..31
@@ -288,7 +291,7 @@ struct cbh_session {
         dfree(partials);
         dfree(group_off); dfree(los_off); dfree(los_idx); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st);
-        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows); dfree(pks_a); dfree(pks_b);
+        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows); dfree(pks_a); dfree(pks_b); dfree(row_ent); dfree(fill_ent);
         dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_ws);
         dfree(pair_desc); dfree(pair_mk); dfree(pair_nd);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
@@ -1163,6 +1166,8 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     // CBH_CHAIN_SPIN (a test knob): the polls a chained scorer wave takes before it gives up its
     // wait for its turn (0: without polling), so the error path runs with every kernel exiting
     if (const char* e = std::getenv("CBH_CHAIN_SPIN")) s->chain_spin = (uint32_t)std::strtoul(e, nullptr, 10);
+    // CBH_CHAIN_FEATURES (a measurement and test knob): cap on the features per chained-scorer workgroup
+    if (const char* e = std::getenv("CBH_CHAIN_FEATURES")) s->chain_nf = (uint32_t)std::strtoul(e, nullptr, 10);
     bool any_oh = false;
     for (uint8_t v : s->one_hot_host) any_oh |= v != 0;
     if (any_oh) {
@@ -1636,6 +1641,19 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
                 nullptr, (int)s->tiles.bin_major);
         HIP_TRY(hipGetLastError());
         CHECK(s->stage_end());
+        if (s->cfg.profile && s->use_skip) {   // the entries this launch added (untimed)
+            if (!s->row_ent) {
+                CHECK(dalloc(&s->row_ent, n));
+                row_entries_kernel<<<grid_for(n, 256), 256, 0, st>>>(s->cols, n, s->F, s->skip_bin, s->row_ent);
+                HIP_TRY(hipGetLastError());
+            }
+            if (!s->fill_ent) {
+                CHECK(dalloc(&s->fill_ent, 1));
+                HIP_TRY(hipMemsetAsync(s->fill_ent, 0, sizeof(unsigned long long), st));
+            }
+            fill_entries_kernel<<<grid_for(n, 256, 1024), 256, 0, st>>>(lidx, lplan, n, s->row_ent, s->fill_ent);
+            HIP_TRY(hipGetLastError());
+        }
         // ---- histogram finishing: dominant bins, prefix form, siblings ----
         CHECK(s->stage_begin(kStDerive));
         {   // built children to prefix form over bins (the level's histograms stay in it), with
@@ -1681,24 +1699,30 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         if (s->pairwise) {
             CHECK(pairwise_level(s, cur, level));
         } else if (chain) {
+            // several features per workgroup when B lanes per feature leave most of a wave idle
+            // (config 5's 20 bins: 3 features in 60 lanes) and no feature is one-hot; at most 64 /
+            // chain_pw (the lane-per-(feature, parent) totals load)
+            uint32_t nf = s->one_hot ? 1u : std::max<uint32_t>(1u, std::min<uint32_t>(64u / s->B, 64u / chain_pw));
+            if (s->chain_nf) nf = std::min<uint32_t>(nf, s->chain_nf);
+            const uint32_t groups = (s->F + nf - 1) / nf;
             if constexpr (K >= 3) {
                 if (chain_pw == 16)
-                    score_chain_kernel<K, 16, false><<<s->F, 64 * (n_leaves / 16), 0, st>>>(
+                    score_chain_kernel<K, 16, false><<<groups, 64 * (n_leaves / 16), 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
                         sfn, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
-                        &s->bounds->device_err);
+                        &s->bounds->device_err, nf);
             }
             if constexpr (K > 1) {
                 if (chain_pw == 8 && n_leaves >= 8)
-                    score_chain_kernel<K, 8, false><<<s->F, 64 * (n_leaves / 8), 0, st>>>(
+                    score_chain_kernel<K, 8, false><<<groups, 64 * (n_leaves / 8), 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
                         sfn, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
-                        &s->bounds->device_err);
+                        &s->bounds->device_err, nf);
                 else if (chain_pw == 8)
-                    score_chain_kernel<K, 8, true><<<s->F, 64, 0, st>>>(
+                    score_chain_kernel<K, 8, true><<<groups, 64, 0, st>>>(
                         zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot, s->scales, s->l2,
                         sfn, s->best_score, s->best_bin, s->ctr_n ? s->fweight : nullptr, s->chain_spin,
-                        &s->bounds->device_err);
+                        &s->bounds->device_err, nf);
             }
         } else if (s->max_cand <= 64)
             score_kernel<K, 1><<<s->F, 64, 0, st>>>(zbuf, zleaves, s->C, cur, n_leaves, s->F, s->B, s->n_cand, s->one_hot,
@@ -2103,11 +2127,22 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
     }
     out->score_shift_der = sc.shift[kScoreDer];
     out->score_shift_w = sc.shift[kScoreW];
+    out->fill_entries = out->fill_row_features;
+    if (s->use_skip) {   // counted in profiled trees only (0 without them)
+        unsigned long long e = 0;
+        if (s->fill_ent) {
+            HIP_TRY(hipStreamSynchronize(s->stream));
+            HIP_TRY(hipMemcpy(&e, s->fill_ent, sizeof(e), hipMemcpyDeviceToHost));
+        }
+        out->fill_entries = e;
+    }
     return CBH_OK;
 }
 
 void cbh_session_reset_stats(cbh_session* s) {
-    if (s) s->stats = cbh_stats{};
+    if (!s) return;
+    s->stats = cbh_stats{};
+    if (s->fill_ent) (void)hipMemsetAsync(s->fill_ent, 0, sizeof(unsigned long long), s->stream);
 }
 
 int cbh_session_set_ctr(cbh_session* s, const cbh_ctr_info* info) {

@@ -222,10 +222,15 @@ typedef struct {
                                      statistics); 3: packed multi-channel fill (K > 1, 32-feature tiles, two
                                      channels rounded to 20-bit rows per 64-bit atomic); 4: the same cells
                                      over sparse entries (a row per 16-lane DPP row, one lane per
-                                     non-dominant (feature, bin)) */
+                                     non-dominant (feature, bin)); 5: count-packed fill (K = 1, integer
+                                     score weights, 64-feature tiles, a row's der rounded at 2^-30 or
+                                     finer and its weight exact in one 64-bit atomic) */
     int32_t fill_pack_bits;       /* packed fills: bits of a row's rounded channel value (|q| < 2^bits) */
     int32_t score_shift_der;      /* the last tree's fixed-point scales S of the score channels: a row's */
     int32_t score_shift_w;        /* value v enters the histogram as round(v * 2^S) (der; weight) */
+    uint64_t fill_entries;        /* (row, feature) entries the fill launches added: fill_row_features, or
+                                     with the dominant-bin skip those whose bin is not the dominant one,
+                                     counted over the trees grown with profiling on */
 } cbh_stats;
 
 int cbh_session_stats(const cbh_session* s, cbh_stats* out);

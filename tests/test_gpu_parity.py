@@ -887,6 +887,69 @@ def test_config5_shape_matches_oracle():
     _assert_same_fit(*_fit_both(d, 4))
 
 
+def test_fill_entries_count_the_non_dominant_entries():
+    """With the dominant-bin skip, the entries the fill adds (cbh_stats.fill_entries, counted in
+    profiled trees) are the visited rows' features whose bin is not the feature's dominant bin
+    (the most frequent bin, lowest on ties, when it holds at least n/8 rows): level 0 visits every
+    row, level 1 the rows of the smaller child (ties: the TRUE child, bin > split bin)."""
+    d = datagen.config5(n_rows=20_000, n_features=96)
+    bins, nb, y = d["bins"], d["n_borders"], d["target"]
+    F, n = bins.shape
+    B = int(nb.max()) + 1
+    kw = dict(loss="MultiClass", depth=2, learning_rate=0.1, l2_leaf_reg=3.0, score="Cosine",
+              leaf_method="Newton", bootstrap_type="No", boost_from_average=False, approx_dim=10)
+    tr = cb.Trainer(bins, B, y, real_folds=nb + 1, **kw)
+    try:
+        assert tr.stats()["skip_features"] > 0
+        tr.set_profile(True)
+        tr.reset_stats()
+        sp, _ = tr.fit(1)
+        st = tr.stats()
+    finally:
+        tr.close()
+    ent = np.zeros(n, np.int64)
+    for f in range(F):
+        c = np.bincount(bins[f], minlength=256)
+        dom = int(np.argmax(c))
+        ent += (bins[f] != dom) if c[dom] * 8 >= n else 1
+    f0, b0 = sp[0][0]
+    true = bins[f0] > b0
+    built = true if true.sum() <= n - true.sum() else ~true
+    assert st["fill_row_features"] == F * (n + int(built.sum()))
+    assert st["fill_entries"] == int(ent.sum()) + int(ent[built].sum())
+
+
+@pytest.mark.parametrize("F,B", [(257, 20), (31, 3), (50, 30)])
+def test_chained_scorer_feature_groups_equal_one_feature_per_workgroup(F, B, monkeypatch):
+    """The chained MultiClass scorer puts floor(64 / B) features in a workgroup (B lanes each;
+    257 features at 20 bins: 3 per workgroup, the last holding 2; 3 bins: 8; 30 bins: 2) and
+    gives every lane the fold of one border in the (d, side, p) order, as with one feature per
+    workgroup: splits, leaves and approximant of 4 depth-8 trees are bit-identical."""
+    g = np.random.default_rng(F * 100 + B)
+    n, K = 40_000, 4
+    nb = g.integers(1, B, F).astype(np.uint32)
+    nb[0] = B - 1
+    bins = np.minimum((g.random((F, n)) * (nb[:, None] + 1)).astype(np.int64), nb[:, None]).astype(np.uint8)
+    score = bins[:6].astype(np.float64).sum(0) / (6.0 * B) + 0.3 * g.standard_normal(n)
+    y = np.digitize(score, np.quantile(score, [0.25, 0.5, 0.75])).astype(np.float64)
+    kw = dict(loss="MultiClass", depth=8, learning_rate=0.1, l2_leaf_reg=3.0, score="Cosine",
+              leaf_method="Newton", bootstrap_type="No", boost_from_average=False, approx_dim=K)
+    out = {}
+    for cap in ("1", ""):
+        monkeypatch.setenv("CBH_CHAIN_FEATURES", cap)
+        tr = cb.Trainer(bins, B, y, real_folds=nb + 1, **kw)
+        try:
+            sp, lv = tr.fit(4)
+            out[cap] = (sp, lv, tr.approx())
+        finally:
+            tr.close()
+    (s0, l0, a0), (s1, l1, a1) = out["1"], out[""]
+    for it in range(4):
+        assert np.array_equal(s0[it], s1[it]), f"tree {it} splits differ"
+    assert np.array_equal(l0, l1)
+    assert np.array_equal(a0, a1)
+
+
 @pytest.mark.parametrize("loss", ["PairLogit", "PairLogitPairwise"])
 def test_config3_full_size_first_trees_match_oracle(loss):
     """Config 3 at its full size (1M docs in 50k groups, ~500k pairs, 100 features): the
