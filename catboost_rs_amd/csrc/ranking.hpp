@@ -557,10 +557,16 @@ __device__ inline void pairwise_solve_block(const double* __restrict__ W, const 
 // each.  In LDS up to 128 leaves (136 KB), else in a global workspace.
 __host__ __device__ constexpr size_t pair_leaf_solve_doubles(uint32_t L) { return (size_t)L * L + 5 * (size_t)L; }
 
-// LDS of the candidate solve (8-byte words): L (packed lower triangle, up to 63 rows; the
-// border's statistics once the solve is done) | der, res, part, dgs 64 each.  ~18 KB, so eight
-// waves share a CU.
-constexpr size_t kPairCandLds = (2080 + 4 * 64) * sizeof(double);
+// LDS of the candidate solve at P leaves (8-byte words): L (packed lower triangle of the 2P-1
+// rows; the border's 2 P^2 statistics once the solve is done) | der, res, part, dgs 64 each.
+// 18 KB at 32 leaves (eight waves a CU, as its 243 VGPRs allow), 6 KB at 16 (its 115 VGPRs:
+// four waves a SIMD).
+__host__ __device__ constexpr uint32_t pair_cand_l_words(uint32_t P) {
+    return (2 * P - 1) * 2 * P / 2 > 2 * P * P ? (2 * P - 1) * 2 * P / 2 : 2 * P * P;
+}
+__host__ __device__ constexpr size_t pair_cand_lds(uint32_t P) {
+    return ((size_t)pair_cand_l_words(P) + 4 * 64) * sizeof(double);
+}
 // Leaf pairs whose statistics one lane loads before using any of them.
 constexpr uint32_t kPairBatch = 8;
 
@@ -827,7 +833,7 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
         return;
     }
     double* M = sh_pw;   // L for the back substitution, then the staged statistics
-    double* der = M + 2080;
+    double* der = M + pair_cand_l_words(P);
     double* res = der + 64;
     double* part = res + 64;
     long long* dgs = (long long*)(part + 64);   // W[r][r] per row, kept for the score

@@ -1372,7 +1372,7 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     {
         const dim3 grid((B - 1 + 7) / 8 * 8, F);
 #define CBH_PAIR_CAND(PV)                                                                                \
-    pairwise_candidate_kernel<PV><<<grid, 64, kPairCandLds, st>>>(s->pair_st, cur, s->C, F, s->n_cand, B, s->scales, \
+    pairwise_candidate_kernel<PV><<<grid, 64, pair_cand_lds(PV), st>>>(s->pair_st, cur, s->C, F, s->n_cand, B, s->scales, \
                                                                   s->pair_inv, s->l2, s->prior, s->cand_scores)
         // up to 8 leaves: one border per lane, the system in the lane's registers
         const dim3 lgrid((B - 1 + 63) / 64, F);
