@@ -397,7 +397,9 @@ def main():
                  "config2: Logloss, Bayesian bootstrap T=1, depth 6, 254 quantile borders (host bins)"),
              3: f"config3: {P['loss']}, groups of 20, ~10 pairs per group, depth 6, 254 borders",
              4: "config4: RMSE, Bernoulli 0.66, depth 6, 30 float (254 borders) + 20 categorical as "
-                "Borders CTR columns (prior 0.5, 16 bins; model_size_reg 0.5, averaging-permutation leaves)",
+                "Borders CTR columns (prior 0.5, 16 bins; model_size_reg 0.5, averaging-permutation leaves), "
+                "max_ctr_complexity=1 (single-feature CTR projections; the reference's default 4 also scores "
+                "feature combinations)",
              5: "config5: MultiClass K=10, depth 8, 64 borders, 70% zeros"}
     out = {
         "metric": METRIC,

@@ -1817,7 +1817,9 @@ static __global__ __launch_bounds__(256) void pack_sparse_kernel(const uint8_t* 
     }
 }
 
-template <int C, bool kGather>
+// kOwn: cells per thread (NP * B * 32 <= kOwn * 1024; the registers holding their int64 partial
+// sums are sized by it); kSets: blocks in flight per wave.
+template <int C, bool kGather, int kOwn = kPkkOwn, int kSets = 4>
 static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bo /* [n_tiles][n][16] each */, uint64_t n,
     const uint32_t* __restrict__ idx, const LevelPlan* __restrict__ plan,
@@ -1833,13 +1835,14 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
     const uint32_t TF = min(32u, F - f0);
     const uint32_t plane = B * 32u;
     const uint32_t kc = ((uint32_t)NP * plane + kPkkThreads - 1) / kPkkThreads;
-    for (uint32_t i = threadIdx.x; i < kPkkCells; i += kPkkThreads) pk[i] = 0ull;
+    for (uint32_t i = threadIdx.x; i < (uint32_t)kOwn * kPkkThreads; i += kPkkThreads) pk[i] = 0ull;
     const uint32_t r0 = threadIdx.x >> 4, e = threadIdx.x & 15u;   // 64 rows per pass, lane e: entry e
     const uint16_t* At = A + (size_t)t * n * 16 + e;
     const uint16_t* Bt = Bo + (size_t)t * n * 16 + e;
-    long long acc_lo[kPkkOwn], acc_hi[kPkkOwn];
+    static_assert(kOwn >= 1 && kOwn <= kPkkOwn, "owned cells");
+    long long acc_lo[kOwn], acc_hi[kOwn];
 #pragma unroll
-    for (int k = 0; k < kPkkOwn; ++k) acc_lo[k] = acc_hi[k] = 0;
+    for (int k = 0; k < kOwn; ++k) acc_lo[k] = acc_hi[k] = 0;
     __syncthreads();
     const uint32_t V = kGather ? plan->rows : (uint32_t)n;
     const uint32_t n_seg = kGather ? plan->n_parent : 1u;
@@ -1850,7 +1853,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
         seg = first_segment(plan, n_seg, rb);
     auto swap_cells = [&]() {
 #pragma unroll
-        for (int k = 0; k < kPkkOwn; ++k) {
+        for (int k = 0; k < kOwn; ++k) {
             if ((uint32_t)k < kc) {
                 const unsigned long long v = atomicExch(pk + threadIdx.x + (uint32_t)k * kPkkThreads, 0ull);
                 unpack_add_signed(v, acc_lo[k], acc_hi[k]);
@@ -1910,41 +1913,58 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
                     swap_cells();
                 }
             };
-            // four sets in flight (a block's atomics are few: the loads need four blocks' time),
-            // gathered row indices four blocks ahead of their set's loads
+            // kSets sets in flight (a block's atomics are few: the loads need several blocks'
+            // time), gathered row indices kSets blocks ahead of their set's loads; named sets
+            // (an array of them indexed in the loop went to scratch)
+            static_assert(kSets == 4 || kSets == 8, "four or eight sets");
             constexpr uint32_t R = kPksBlockRows;
-            Set S0, S1, S2, S3;
-            uint32_t ix0 = ldix(pos), ix1 = ldix(pos + R), ix2 = ldix(pos + 2 * R), ix3 = ldix(pos + 3 * R);
-            load_set(S0, pos, ix0);
-            asm volatile("" ::: "memory");
-            load_set(S1, pos + R, ix1);
-            asm volatile("" ::: "memory");
-            load_set(S2, pos + 2 * R, ix2);
-            asm volatile("" ::: "memory");
-            load_set(S3, pos + 3 * R, ix3);
-            asm volatile("" ::: "memory");
+            Set S0, S1, S2, S3, S4, S5, S6, S7;
+            uint32_t ix0 = 0, ix1 = 0, ix2 = 0, ix3 = 0, ix4 = 0, ix5 = 0, ix6 = 0, ix7 = 0;
+#define CBH_PKS_SET(Q, X)                                                                   \
+    if constexpr (kSets > Q) X
+            CBH_PKS_SET(0, ix0 = ldix(pos);)
+            CBH_PKS_SET(1, ix1 = ldix(pos + R);)
+            CBH_PKS_SET(2, ix2 = ldix(pos + 2 * R);)
+            CBH_PKS_SET(3, ix3 = ldix(pos + 3 * R);)
+            CBH_PKS_SET(4, ix4 = ldix(pos + 4 * R);)
+            CBH_PKS_SET(5, ix5 = ldix(pos + 5 * R);)
+            CBH_PKS_SET(6, ix6 = ldix(pos + 6 * R);)
+            CBH_PKS_SET(7, ix7 = ldix(pos + 7 * R);)
+#define CBH_PKS_LOAD(Q)                                                                     \
+    if constexpr (kSets > Q) {                                                              \
+        load_set(S##Q, pos + Q * R, ix##Q);                                                 \
+        asm volatile("" ::: "memory");                                                      \
+    }
+            CBH_PKS_LOAD(0) CBH_PKS_LOAD(1) CBH_PKS_LOAD(2) CBH_PKS_LOAD(3)
+            CBH_PKS_LOAD(4) CBH_PKS_LOAD(5) CBH_PKS_LOAD(6) CBH_PKS_LOAD(7)
+#undef CBH_PKS_LOAD
             if (kGather) {
-                ix0 = ldix(pos + 4 * R);
-                ix1 = ldix(pos + 5 * R);
-                ix2 = ldix(pos + 6 * R);
-                ix3 = ldix(pos + 7 * R);
+                CBH_PKS_SET(0, ix0 = ldix(pos + kSets * R);)
+                CBH_PKS_SET(1, ix1 = ldix(pos + (kSets + 1) * R);)
+                CBH_PKS_SET(2, ix2 = ldix(pos + (kSets + 2) * R);)
+                CBH_PKS_SET(3, ix3 = ldix(pos + (kSets + 3) * R);)
+                CBH_PKS_SET(4, ix4 = ldix(pos + (kSets + 4) * R);)
+                CBH_PKS_SET(5, ix5 = ldix(pos + (kSets + 5) * R);)
+                CBH_PKS_SET(6, ix6 = ldix(pos + (kSets + 6) * R);)
+                CBH_PKS_SET(7, ix7 = ldix(pos + (kSets + 7) * R);)
             }
+#undef CBH_PKS_SET
             asm volatile("" ::: "memory");
-            auto step = [&](Set& S, uint32_t& ix, uint32_t bb) {   // block bb: atomics, reload for bb + 4R
-                atoms(S);
-                load_set(S, bb + 4 * R, kGather ? ix : ldix(bb + 4 * R));
-                if (kGather) ix = ldix(bb + 8 * R);
+            auto step = [&](Set& Sq, uint32_t& ixq, uint32_t bb) {   // block bb: atomics, reload for bb + kSets R
+                atoms(Sq);
+                load_set(Sq, bb + kSets * R, kGather ? ixq : ldix(bb + kSets * R));
+                if (kGather) ixq = ldix(bb + 2u * kSets * R);
                 after_block(bb);
             };
-            for (uint32_t bb = pos;; bb += 4 * R) {   // workgroup-uniform
-                step(S0, ix0, bb);
-                if (bb + R >= end) break;
-                step(S1, ix1, bb + R);
-                if (bb + 2 * R >= end) break;
-                step(S2, ix2, bb + 2 * R);
-                if (bb + 3 * R >= end) break;
-                step(S3, ix3, bb + 3 * R);
-                if (bb + 4 * R >= end) break;
+            for (uint32_t bb = pos;; bb += kSets * R) {   // workgroup-uniform
+#define CBH_PKS_STEP(Q)                                                                     \
+    if constexpr (kSets > Q) {                                                              \
+        step(S##Q, ix##Q, bb + Q * R);                                                      \
+        if (bb + (Q + 1) * R >= end) break;                                                 \
+    }
+                CBH_PKS_STEP(0) CBH_PKS_STEP(1) CBH_PKS_STEP(2) CBH_PKS_STEP(3)
+                CBH_PKS_STEP(4) CBH_PKS_STEP(5) CBH_PKS_STEP(6) CBH_PKS_STEP(7)
+#undef CBH_PKS_STEP
             }
             // flush: as the dense multi-channel fill's (same cells, same ownership rule)
             const bool owned = pos == seg_lo && end == seg_end;
@@ -1952,7 +1972,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
             for (int half = 0; half < 2; ++half) {
                 __syncthreads();
 #pragma unroll
-                for (int k = 0; k < kPkkOwn; ++k)
+                for (int k = 0; k < kOwn; ++k)
                     if ((uint32_t)k < kc)
                         pk[threadIdx.x + (uint32_t)k * kPkkThreads] = (unsigned long long)(half ? acc_hi[k] : acc_lo[k]);
                 __syncthreads();
@@ -1974,7 +1994,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
             }
             __syncthreads();
 #pragma unroll
-            for (int k = 0; k < kPkkOwn; ++k) {
+            for (int k = 0; k < kOwn; ++k) {
                 if ((uint32_t)k < kc) pk[threadIdx.x + (uint32_t)k * kPkkThreads] = 0ull;
                 acc_lo[k] = acc_hi[k] = 0;
             }

@@ -209,6 +209,7 @@ struct cbh_session {
     // packed multi-channel fill (K > 1: two score channels per 64-bit word, NP = ceil(C/2) planes)
     bool pkk = false;
     uint32_t pkk_tiles = 0, pkk_ranges = 8;
+    bool pks_small = false;          // sparse entries, NP * B * 32 <= 4096: 4 cells per thread
     int pack_bits = 0;
     unsigned long long* spack = nullptr;   // packed: [n] words
     unsigned long long* sseq = nullptr;    // the listed rows' statistics in idx order (packed: [V]; tiled: [V][2])
@@ -640,7 +641,8 @@ template <int C>
 int set_pkk_attr(size_t lds) {
     for (const void* k : {(const void*)fill_pkk_kernel<C, false, false>, (const void*)fill_pkk_kernel<C, false, true>,
                           (const void*)fill_pkk_kernel<C, true, false>, (const void*)fill_pkk_kernel<C, true, true>,
-                          (const void*)fill_pks_kernel<C, false>, (const void*)fill_pks_kernel<C, true>})
+                          (const void*)fill_pks_kernel<C, false>, (const void*)fill_pks_kernel<C, true>,
+                          (const void*)fill_pks_kernel<C, false, 4, 8>, (const void*)fill_pks_kernel<C, true, 4, 8>})
         HIP_TRY(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     return CBH_OK;
 }
@@ -683,6 +685,10 @@ int plan_pkk(cbh_session* s, const std::string& v) {
         if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s->stream) != hipSuccess)
             return fail(CBH_ERR_DEVICE, "sparse entry packing failed");
         s->pks = true;
+        // tiles of at most 4096 cells (NP * B * 32: config 5's 6 planes of 20 bins) take the
+        // 4-cells-per-thread variant (CBH_PKS_SMALL=off, a measurement knob, keeps the general one)
+        const char* sm = std::getenv("CBH_PKS_SMALL");
+        s->pks_small = (uint64_t)NP * s->B * 32u <= 4u * kPkkThreads && !(sm && std::string(sm) == "off");
     }
     return CBH_OK;
 }
@@ -1609,7 +1615,15 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         else if (s->pkk) {
             const size_t lds = (size_t)kPkkCells * sizeof(unsigned long long);
             const unsigned grid = s->pkk_ranges * s->pkk_tiles;
-            if (s->pks && level == 0)
+            // (small tiles: 4 cells per thread, their registers leaving room for 8 blocks in flight)
+            const size_t lds4 = (size_t)4 * kPkkThreads * sizeof(unsigned long long);
+            if (s->pks && s->pks_small && level == 0)
+                fill_pks_kernel<C, false, 4, 8><<<grid, kPkkThreads, lds4, st>>>(
+                    s->pks_a, s->pks_b, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur);
+            else if (s->pks && s->pks_small)
+                fill_pks_kernel<C, true, 4, 8><<<grid, kPkkThreads, lds4, st>>>(
+                    s->pks_a, s->pks_b, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur);
+            else if (s->pks && level == 0)
                 fill_pks_kernel<C, false><<<grid, kPkkThreads, lds, st>>>(
                     s->pks_a, s->pks_b, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur);
             else if (s->pks)

@@ -214,7 +214,10 @@ def config4(n_rows=2_000_000, n_float=30, n_cat=20, seed=4):
     Bernoulli 0.66.  Returns the float bins, every categorical column as first-seen keys
     (category codes; the caller turns them into bins on the device), the CTR target class
     (y > 0.5, the reference's binclf binarization) and the parameters.  The CTR columns
-    themselves depend on the learn permutation and are built by the caller."""
+    themselves depend on the learn permutation and are built by the caller.  CTR candidates
+    are single-feature projections only, i.e. max_ctr_complexity=1: the reference's default
+    of 4 (crates/cb-train/src/boosting.rs:1010-1017) also scores feature-combination CTRs,
+    which this build does not construct."""
     n = int(n_rows)
     g = np.random.default_rng(seed)
     X = g.standard_normal((n, n_float)).astype(np.float32)
