@@ -1,12 +1,20 @@
 // Measures the LDS atomic-add rate of the GPU for the address patterns that bound the
-// histogram fill: scattered cells (the fill's pattern: every lane a random bin) and
-// contiguous cells (64 lanes on 64 neighbouring cells, the best case), for 64-bit cells
-// (the fill's) and 32-bit cells with and without a returned value, and contiguous 64-bit
-// atomics with 16 of every 64 lanes active (an instruction's cost does not shrink with its
-// active lanes: the fills are bound by the wave-level atomic instruction rate).  1024-thread
-// workgroups, 128 KB of LDS each, every address reduced into the array.
-// Prints one line per pattern: "<pattern> <lane-atomics per second>" (the 16-of-64 pattern:
-// instructions per second x 64).
+// histogram fills.  Every thread computes its addresses before the timed loop (8 per thread,
+// reused every iteration), so the loop issues back-to-back LDS atomics and nothing else: the
+// rate is the LDS pipe's, not the address arithmetic's.  1024-thread workgroups, 128 KB of LDS
+// each (16384 64-bit cells), two workgroups per CU in the grid.
+// Patterns (a DPP row is a group of 16 consecutive lanes):
+//   contiguous_u64 / _u32        64 lanes on 64 neighbouring cells (the best case)
+//   scattered_u64 / _u32 / _rtn  every lane a random cell (with return: the old value used)
+//   contiguous_u64_16of64_lanes  contiguous, only lanes 0-15 of a wave active (printed as
+//                                instructions per second x 64: an instruction's cost does not
+//                                shrink with its active lanes)
+//   dpp_rows_same_pairs_u64      the four DPP rows on the same 16 bank pairs at other addresses
+//   dpp_row_pairs_random_rows_u64 the fills' pattern: lane l of a DPP row at column l of a
+//                                random 256-byte bin row (16 distinct bank pairs, random rows)
+//   dpp_row_mod16_pairs_u64      columns (r + 2 l) mod 32 of random bin rows: 8 pairs of lanes
+//                                of a DPP row on the same bank pair (column mod 16)
+// Prints one line per pattern: "<pattern> <lane-atomics per second>".
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -21,8 +29,9 @@
         }                                                                       \
     } while (0)
 
-constexpr int kIters = 4096;
-constexpr int kCells = 16384;  // 128 KB of u64 cells
+constexpr int kIters = 2048;
+constexpr int kAddr = 8;        // addresses per thread
+constexpr int kCells = 16384;   // 128 KB of u64 cells
 
 __device__ __forceinline__ uint32_t mix32(uint32_t x) {
     x ^= x >> 16;
@@ -33,59 +42,72 @@ __device__ __forceinline__ uint32_t mix32(uint32_t x) {
     return x;
 }
 
+enum Pattern : int {
+    kContiguous = 0,
+    kScattered = 1,
+    kDppSamePairs = 2,
+    kDppPairsRandomRows = 3,
+    kDppMod16Pairs = 4,
+};
+
 // T: cell type (u64 or u32); kRtn: use the returned old value (an atomic with return);
-// kQuarter: only lanes 0-15 of every wave issue (an instruction with 16 of 64 lanes active).
-// kScattered 2 (u64): the 16 lanes of each DPP row hit 16 distinct bank pairs, and the four DPP
-// rows the same 16 pairs at other addresses (cells (l & 15) + 32 (l >> 4) + 128 it), which
-// shows whether an instruction's conflicts count within 16 or within 32 lanes.
-template <int kScattered, typename T, int kRtn, int kQuarter = 0>
+// kQuarter: only lanes 0-15 of every wave issue.
+template <int kPattern, typename T, int kRtn, int kQuarter = 0>
 __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uint32_t seed) {
     extern __shared__ unsigned long long cells_raw[];
     T* cells = (T*)cells_raw;
     constexpr uint32_t n_cells = kCells * 8 / sizeof(T);
     for (uint32_t i = threadIdx.x; i < n_cells; i += blockDim.x) cells[i] = 0;
     __syncthreads();
-    const uint32_t lane = threadIdx.x & 63u;
-    uint32_t h = mix32(threadIdx.x * 7919u + blockIdx.x * 104729u + seed);
+    const uint32_t lane = threadIdx.x & 63u, l = threadIdx.x & 15u, row = threadIdx.x >> 4;
+    uint32_t idx[kAddr];
+#pragma unroll
+    for (int q = 0; q < kAddr; ++q) {
+        const uint32_t h = mix32(threadIdx.x * 7919u + blockIdx.x * 104729u + seed * 31u + (uint32_t)q * 1000003u);
+        const uint32_t hr = mix32(row * 7919u + blockIdx.x * 104729u + seed * 31u + (uint32_t)q * 1000003u);
+        uint32_t c;
+        if (kPattern == kContiguous) c = (uint32_t)q * 64u + lane + 512u * (threadIdx.x >> 6);
+        else if (kPattern == kScattered) c = h;
+        else if (kPattern == kDppSamePairs) c = l + 32u * ((threadIdx.x >> 4) & 3u) + 128u * (uint32_t)q;
+        else if (kPattern == kDppPairsRandomRows) c = (h & 255u) * 32u + l;
+        else c = (h & 255u) * 32u + (((hr & 31u) + 2u * l) & 31u);
+        idx[q] = c % n_cells;
+    }
     T carry = 0;
     const bool issue = !(kQuarter && lane >= 16);
     for (int it = 0; issue && it < kIters; ++it) {
-        uint32_t idx;
-        if (kScattered == 2) {
-            idx = ((lane & 15u) + 32u * (lane >> 4) + 128u * (uint32_t)it) % n_cells;
-        } else if (kScattered) {
-            h = mix32(h + (uint32_t)it);
-            idx = h % n_cells;
-        } else {
-            idx = ((uint32_t)it * 64u + lane) % n_cells;
+#pragma unroll
+        for (int q = 0; q < kAddr; ++q) {
+            if (kRtn) carry += atomicAdd(&cells[idx[q]], (T)1) >> 31;
+            else atomicAdd(&cells[idx[q]], (T)1);
         }
-        if (kRtn) carry += atomicAdd(&cells[idx], (T)1) >> 31;
-        else atomicAdd(&cells[idx], (T)1);
     }
     __syncthreads();
     if (threadIdx.x == 0) out[blockIdx.x] = (unsigned long long)cells[0] + (unsigned long long)carry;
 }
 
-template <int kScattered, typename T, int kRtn, int kQuarter = 0>
+template <int kPattern, typename T, int kRtn, int kQuarter = 0>
 int measure(const char* name, int blocks, unsigned long long* d) {
-    CK(hipFuncSetAttribute((const void*)rate_kernel<kScattered, T, kRtn, kQuarter>,
+    CK(hipFuncSetAttribute((const void*)rate_kernel<kPattern, T, kRtn, kQuarter>,
                            hipFuncAttributeMaxDynamicSharedMemorySize, kCells * 8));
-    rate_kernel<kScattered, T, kRtn, kQuarter><<<blocks, 1024, kCells * 8>>>(d, 1u);
+    rate_kernel<kPattern, T, kRtn, kQuarter><<<blocks, 1024, kCells * 8>>>(d, 1u);
     CK(hipGetLastError());
     CK(hipDeviceSynchronize());
     hipEvent_t a, b;
     CK(hipEventCreate(&a));
     CK(hipEventCreate(&b));
     CK(hipEventRecord(a));
-    rate_kernel<kScattered, T, kRtn, kQuarter><<<blocks, 1024, kCells * 8>>>(d, 2u);
+    rate_kernel<kPattern, T, kRtn, kQuarter><<<blocks, 1024, kCells * 8>>>(d, 2u);
     CK(hipEventRecord(b));
     CK(hipEventSynchronize(b));
     float ms = 0.f;
     CK(hipEventElapsedTime(&ms, a, b));
     // lane-atomics per second; with kQuarter the wave-level instruction rate x 64 (each
     // instruction counted as if all 64 lanes were active), comparable with the full-lane line
-    const double lanes = (double)blocks * 1024.0 * kIters;
+    const double lanes = (double)blocks * 1024.0 * kIters * kAddr;
     std::printf("%s %.6e\n", name, lanes / (ms * 1e-3));
+    CK(hipEventDestroy(a));
+    CK(hipEventDestroy(b));
     return 0;
 }
 
@@ -96,13 +118,16 @@ int main() {
     unsigned long long* d = nullptr;
     const int blocks = 2 * cus;
     CK(hipMalloc(&d, sizeof(unsigned long long) * blocks));
-    if (measure<1, unsigned long long, 0>("scattered_u64", blocks, d)) return 1;
-    if (measure<0, unsigned long long, 0>("contiguous_u64", blocks, d)) return 1;
-    if (measure<1, unsigned int, 0>("scattered_u32", blocks, d)) return 1;
-    if (measure<1, unsigned int, 1>("scattered_u32_rtn", blocks, d)) return 1;
-    if (measure<0, unsigned int, 0>("contiguous_u32", blocks, d)) return 1;
-    if (measure<0, unsigned long long, 0, 1>("contiguous_u64_16of64_lanes", blocks, d)) return 1;
-    if (measure<2, unsigned long long, 0>("dpp_rows_same_pairs_u64", blocks, d)) return 1;
+    using u64 = unsigned long long;
+    if (measure<kScattered, u64, 0>("scattered_u64", blocks, d)) return 1;
+    if (measure<kContiguous, u64, 0>("contiguous_u64", blocks, d)) return 1;
+    if (measure<kScattered, unsigned int, 0>("scattered_u32", blocks, d)) return 1;
+    if (measure<kScattered, unsigned int, 1>("scattered_u32_rtn", blocks, d)) return 1;
+    if (measure<kContiguous, unsigned int, 0>("contiguous_u32", blocks, d)) return 1;
+    if (measure<kContiguous, u64, 0, 1>("contiguous_u64_16of64_lanes", blocks, d)) return 1;
+    if (measure<kDppSamePairs, u64, 0>("dpp_rows_same_pairs_u64", blocks, d)) return 1;
+    if (measure<kDppPairsRandomRows, u64, 0>("dpp_row_pairs_random_rows_u64", blocks, d)) return 1;
+    if (measure<kDppMod16Pairs, u64, 0>("dpp_row_mod16_pairs_u64", blocks, d)) return 1;
     CK(hipFree(d));
     return 0;
 }
