@@ -693,11 +693,13 @@ int plan_pkk(cbh_session* s, const std::string& v) {
     return CBH_OK;
 }
 
-// Fill plan.  The default: K == 1 from 2^20 rows the tiled exact fill, K > 1 from 500000 rows
-// the packed multi-channel fill, otherwise (and with the dominant-bin skip at K == 1) the generic
-// fill.  CBH_FILL (a measurement and test knob) forces one: =generic the generic fill (any K),
-// =tiled the tiled exact fill (K == 1), =packed the rounded packed fill (K == 1: 18-bit rows) or
-// the packed multi-channel fill (K > 1).
+// Fill plan.  The default: K == 1 with integer score weights from 2^22 rows the count-packed
+// fill, else from 2^16 rows (2^20 with pairs) the tiled exact fill (which visits every bin: its
+// lanes add to distinct features, so a dominant bin does not serialize them); K > 1 from 500000
+// rows the packed multi-channel fill; otherwise the generic fill.  CBH_FILL (a measurement and
+// test knob) forces one: =generic the generic fill (any K), =tiled the tiled exact fill (K == 1),
+// =count the count-packed fill (K == 1, integer score weights), =packed the rounded packed fill
+// (K == 1: 18-bit rows) or the packed multi-channel fill (K > 1).
 int plan_fill_mode(cbh_session* s) {
     s->packed = s->tiled = s->pkk = s->count = false;
     const char* e = std::getenv("CBH_FILL");

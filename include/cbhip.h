@@ -206,10 +206,11 @@ typedef struct {
     uint64_t fill_rows;           /* rows visited by fill launches (sum of V) */
     uint64_t fill_row_features;   /* sum of V * n_features */
     double fill_bytes;            /* algorithmic bytes V*(W*4 + S + 4) + H: S bytes of statistics per row,
-                                     8*(K+1) for the exact fills, 8 for the rounded packed fill, 8*ceil((K+1)/2)
-                                     for the packed multi-channel fills; the 4 bytes of a row index at the
-                                     levels that gather rows through the partition's index list; H the
-                                     histogram cells built x 8 */
+                                     8*(K+1) for the generic and tiled exact fills, 8 for the rounded packed
+                                     and count-packed fills, 8*ceil((K+1)/2) for the packed multi-channel
+                                     fills (over sparse entries: 32 bytes of entry codes per 32-feature tile
+                                     instead of W*4); the 4 bytes of a row index at the levels that gather
+                                     rows through the partition's index list; H the histogram cells built x 8 */
     uint64_t trees;
     uint64_t skip_features;       /* features whose dominant bin the fill leaves out */
     double quantize_ms;           /* raw float channel: device quantize launches at open */
