@@ -1596,7 +1596,8 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
     const uint32_t* __restrict__ rows, uint32_t W, uint32_t stride /* words per row in memory */, uint64_t n,
     const uint32_t* __restrict__ idx, const LevelPlan* __restrict__ plan,
     const unsigned long long* __restrict__ spk /* [n][NP] */, uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, long long* __restrict__ hist,
-    const uint32_t* __restrict__ skip_bin /* kSkip: [F] */) {
+    const uint32_t* __restrict__ skip_bin /* kSkip: [F] */,
+    uint32_t np_fill /* planes filled: NP, or NP - 1 when the last (the weight alone) comes from elsewhere */) {
     constexpr int NP = (C + 1) / 2;
     extern __shared__ unsigned long long pk[];   // [NP][B][32], kPkkCells cells
     const uint32_t b = blockIdx.x;
@@ -1678,7 +1679,8 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
                     if (kSkip && bin == skp[k]) continue;   // dominant bin: rebuilt from the totals
                     unsigned long long* cell = (unsigned long long*)((char*)pk + ((bin << 8) + off8[k]));
 #pragma unroll
-                    for (int j = 0; j < NP; ++j) atomicAdd(cell + (size_t)j * plane, S.st[j]);
+                    for (int j = 0; j < NP; ++j)
+                        if ((uint32_t)j < np_fill) atomicAdd(cell + (size_t)j * plane, S.st[j]);
                 }
             };
             uint32_t blk = 0;
@@ -1733,7 +1735,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
                     const uint32_t j = jj / (nfb * nbb), jb = jj - j * (nfb * nbb);
                     const uint32_t f = (jb / nbb) * 8 + (l >> 3), bin = (jb % nbb) * 8 + (l & 7u);
                     const uint32_t ch = 2u * j + (uint32_t)half;
-                    if (f >= TF || bin >= B || ch >= (uint32_t)C) continue;
+                    if (f >= TF || bin >= B || ch >= (uint32_t)C || j >= np_fill) continue;
                     const unsigned long long v = pk[j * plane + bin * 32u + f];
                     unsigned long long* d = (unsigned long long*)hd + (((size_t)ch * F + f0 + f) * B + bin);
                     if (v != 0) {
@@ -1824,9 +1826,10 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bo /* [n_tiles][n][16] each */, uint64_t n,
     const uint32_t* __restrict__ idx, const LevelPlan* __restrict__ plan,
     const unsigned long long* __restrict__ spk /* [n][NP] */, uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G,
-    long long* __restrict__ hist) {
+    long long* __restrict__ hist,
+    uint32_t np_fill /* planes filled: NP, or NP - 1 when the last (the weight alone) comes from elsewhere */) {
     constexpr int NP = (C + 1) / 2;
-    extern __shared__ unsigned long long pk[];   // [NP][B][32], kPkkCells cells
+    extern __shared__ unsigned long long pk[];   // [NP][B][32], kOwn * 1024 cells
     const uint32_t b = blockIdx.x;
     const uint32_t xcd = b & 7u, q = b >> 3;
     const uint32_t t = q % n_tiles;
@@ -1894,14 +1897,16 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
                 if (S.code != kPksEmpty) {
                     unsigned long long* cell = (unsigned long long*)((char*)pk + (S.code & ~7u));
 #pragma unroll
-                    for (int j = 0; j < NP; ++j) atomicAdd(cell + (size_t)j * plane, sv[j]);
+                    for (int j = 0; j < NP; ++j)
+                        if ((uint32_t)j < np_fill) atomicAdd(cell + (size_t)j * plane, sv[j]);
                 }
                 if (__any(over != 0u)) {   // rare: wave-uniform branch
                     const uint32_t c2 = over ? (uint32_t)Bt[(size_t)S.doc * 16] : (uint32_t)kPksEmpty;
                     if (c2 != kPksEmpty) {
                         unsigned long long* cell = (unsigned long long*)((char*)pk + (c2 & ~7u));
 #pragma unroll
-                        for (int j = 0; j < NP; ++j) atomicAdd(cell + (size_t)j * plane, sv[j]);
+                        for (int j = 0; j < NP; ++j)
+                            if ((uint32_t)j < np_fill) atomicAdd(cell + (size_t)j * plane, sv[j]);
                     }
                 }
             };
@@ -1983,7 +1988,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
                     const uint32_t j = jj / (nfb * nbb), jb = jj - j * (nfb * nbb);
                     const uint32_t f = (jb / nbb) * 8 + (l >> 3), bin = (jb % nbb) * 8 + (l & 7u);
                     const uint32_t ch = 2u * j + (uint32_t)half;
-                    if (f >= TF || bin >= B || ch >= (uint32_t)C) continue;
+                    if (f >= TF || bin >= B || ch >= (uint32_t)C || j >= np_fill) continue;
                     const unsigned long long v = pk[j * plane + bin * 32u + f];
                     unsigned long long* d = (unsigned long long*)hd + (((size_t)ch * F + f0 + f) * B + bin);
                     if (v != 0) {

@@ -210,6 +210,9 @@ struct cbh_session {
     bool pkk = false;
     uint32_t pkk_tiles = 0, pkk_ranges = 8;
     bool pks_small = false;          // sparse entries, NP * B * 32 <= 4096: 4 cells per thread
+    bool w_static = false;           // packed multi-channel fill, the weight alone in the last plane and
+    bool w0_ready = false;           // the same every tree: its level-0 cells cached after the first tree
+    long long* w0_cache = nullptr;   // [F][B] (the fill's cells, before the dominant-bin rebuild)
     int pack_bits = 0;
     unsigned long long* spack = nullptr;   // packed: [n] words
     unsigned long long* sseq = nullptr;    // the listed rows' statistics in idx order (packed: [V]; tiled: [V][2])
@@ -292,7 +295,7 @@ struct cbh_session {
         dfree(partials);
         dfree(group_off); dfree(los_off); dfree(los_idx); dfree(comp_off); dfree(comp_win); dfree(comp_los); dfree(comp_w);
         dfree(comp_wq); dfree(ext_der); dfree(score_w); dfree(pair_st);
-        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows); dfree(pks_a); dfree(pks_b); dfree(row_ent); dfree(fill_ent);
+        dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows); dfree(pks_a); dfree(pks_b); dfree(row_ent); dfree(fill_ent); dfree(w0_cache);
         dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_ws);
         dfree(pair_desc); dfree(pair_mk); dfree(pair_nd);
         dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
@@ -665,6 +668,13 @@ int plan_pkk(cbh_session* s, const std::string& v) {
     CHECK(dalloc(&s->spack, (size_t)s->n * NP));
     s->pack_bits = kPkkBits;
     s->pkk = true;
+    // the score weight alone in the last plane (C odd) and the same every tree (no bootstrap, no
+    // per-tree sample from the host): level 0 fills it once (CBH_PKK_W0=off, a measurement knob,
+    // fills it every tree)
+    const char* w0e = std::getenv("CBH_PKK_W0");
+    s->w_static = (s->C & 1u) && s->cfg.bootstrap_type == CBH_BOOT_NO && !s->cfg.sample_from_host &&
+                  !(w0e && std::string(w0e) == "off");
+    if (s->w_static) CHECK(dalloc(&s->w0_cache, (size_t)s->F * s->B));
     // sparse entries when the dominant-bin skip leaves at most 12 of a tile's 32 entries per row
     // on average (a DPP row of 16 lanes per row then carries about twice the active lanes of the
     // dense visit); CBH_PKK_SPARSE=off keeps the dense visit, =on takes the entries whatever
@@ -1617,36 +1627,46 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         else if (s->pkk) {
             const size_t lds = (size_t)kPkkCells * sizeof(unsigned long long);
             const unsigned grid = s->pkk_ranges * s->pkk_tiles;
+            // level 0 of a session whose weight channel is the same every tree (alone in the last
+            // plane, no per-tree sample): after the first tree the plane's cells come from the
+            // cache of its level-0 histogram, copied in before the fill, and the fill adds the
+            // other planes only
+            const uint32_t NPl = (C + 1) / 2;
+            const bool w0_use = level == 0 && s->w_static && s->w0_ready;
+            const uint32_t npf = w0_use ? NPl - 1 : NPl;
+            if (w0_use)
+                HIP_TRY(hipMemcpyAsync(cur + (size_t)(C - 1) * s->F * s->B, s->w0_cache,
+                                       sizeof(long long) * s->F * s->B, hipMemcpyDeviceToDevice, st));
             // (small tiles: 4 cells per thread, their registers leaving room for 8 blocks in flight)
             const size_t lds4 = (size_t)4 * kPkkThreads * sizeof(unsigned long long);
             if (s->pks && s->pks_small && level == 0)
                 fill_pks_kernel<C, false, 4, 8><<<grid, kPkkThreads, lds4, st>>>(
-                    s->pks_a, s->pks_b, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur);
+                    s->pks_a, s->pks_b, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur, npf);
             else if (s->pks && s->pks_small)
                 fill_pks_kernel<C, true, 4, 8><<<grid, kPkkThreads, lds4, st>>>(
-                    s->pks_a, s->pks_b, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur);
+                    s->pks_a, s->pks_b, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur, npf);
             else if (s->pks && level == 0)
                 fill_pks_kernel<C, false><<<grid, kPkkThreads, lds, st>>>(
-                    s->pks_a, s->pks_b, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur);
+                    s->pks_a, s->pks_b, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur, npf);
             else if (s->pks)
                 fill_pks_kernel<C, true><<<grid, kPkkThreads, lds, st>>>(
-                    s->pks_a, s->pks_b, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur);
+                    s->pks_a, s->pks_b, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur, npf);
             else if (s->use_skip && level == 0)
                 fill_pkk_kernel<C, true, false><<<grid, kPkkThreads, lds, st>>>(
                     s->rows, s->W, s->Ws, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur,
-                    s->skip_bin);
+                    s->skip_bin, npf);
             else if (s->use_skip)
                 fill_pkk_kernel<C, true, true><<<grid, kPkkThreads, lds, st>>>(
                     s->rows, s->W, s->Ws, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur,
-                    s->skip_bin);
+                    s->skip_bin, npf);
             else if (level == 0)
                 fill_pkk_kernel<C, false, false><<<grid, kPkkThreads, lds, st>>>(
                     s->rows, s->W, s->Ws, n, nullptr, nullptr, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur,
-                    nullptr);
+                    nullptr, npf);
             else
                 fill_pkk_kernel<C, false, true><<<grid, kPkkThreads, lds, st>>>(
                     s->rows, s->W, s->Ws, n, lidx, lplan, s->spack, s->pkk_tiles, s->F, s->B, s->pkk_ranges, cur,
-                    nullptr);
+                    nullptr, npf);
         } else if (s->use_skip)
             fill_kernel<C, true><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
                 s->rows, s->W, s->Ws, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
@@ -1657,6 +1677,11 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
                 nullptr, (int)s->tiles.bin_major);
         HIP_TRY(hipGetLastError());
         CHECK(s->stage_end());
+        if (s->pkk && level == 0 && s->w_static && !s->w0_ready) {   // the weight channel's cache
+            HIP_TRY(hipMemcpyAsync(s->w0_cache, cur + (size_t)(C - 1) * s->F * s->B, sizeof(long long) * s->F * s->B,
+                                   hipMemcpyDeviceToDevice, st));
+            s->w0_ready = true;
+        }
         if (s->cfg.profile && s->use_skip) {   // the entries this launch added (untimed)
             if (!s->row_ent) {
                 CHECK(dalloc(&s->row_ent, n));
@@ -2042,6 +2067,18 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
         return fail(CBH_ERR_INVALID_ARG, "a session configured without Bayesian bootstrap got a Bayesian sample");
     if (n_sample != 0 && sampling && sampling->kind != CBH_BOOT_NO)
         return fail(CBH_ERR_INVALID_ARG, "host sample and device sampling are mutually exclusive");
+    if (s->w_static && sampling &&
+        ((sampling->kind == CBH_BOOT_BAYESIAN && sampling->bagging_temperature != 0.0f) ||
+         (sampling->kind == CBH_BOOT_BERNOULLI && sampling->subsample < 1.0))) {
+        // a per-tree sample in a session opened without bootstrap: the weight channel changes from
+        // tree to tree, so its level-0 cache and the trees recorded with it are dropped
+        s->w_static = s->w0_ready = false;
+        for (hipGraphExec_t& g : s->tree_graph)
+            if (g) {
+                (void)hipGraphExecDestroy(g);
+                g = nullptr;
+            }
+    }
     hipStream_t st = s->stream;
     if (target) {
         HIP_TRY(hipMemcpyAsync(s->target, target, sizeof(double) * n, hipMemcpyHostToDevice, st));

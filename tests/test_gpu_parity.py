@@ -881,6 +881,36 @@ def test_multiclass_packed_fill_entries_match_oracle(zeros, sparse, monkeypatch)
     _assert_same_fit(*_fit_both(d, 3))
 
 
+@pytest.mark.parametrize("sparse", ["on", "off"])
+def test_multiclass_static_weight_plane_equals_filling_it(sparse, monkeypatch):
+    """MultiClass K = 10 without bootstrap: the score weight is alone in the packed fill's last
+    plane and the same every tree, so level 0 fills it in the first tree only and copies it from
+    that tree's histogram afterwards; trees, leaves and approximant over 6 trees are bit-identical
+    to filling it every tree (CBH_PKK_W0=off), over sparse entries and the dense visit."""
+    d = datagen.config5(n_rows=30_000, n_features=128)
+    nb = d["n_borders"]
+    P = dict(d["params"])
+    kw = dict(loss=P["loss"], depth=6, learning_rate=P["learning_rate"], l2_leaf_reg=P["l2_leaf_reg"],
+              score=P["score"], leaf_method=P["leaf_method"], bootstrap_type="No",
+              boost_from_average=P["boost_from_average"], approx_dim=P["approx_dim"])
+    monkeypatch.setenv("CBH_FILL", "packed")
+    monkeypatch.setenv("CBH_PKK_SPARSE", sparse)
+    out = {}
+    for w0 in ("off", ""):
+        monkeypatch.setenv("CBH_PKK_W0", w0)
+        tr = cb.Trainer(d["bins"], int(nb.max()) + 1, d["target"], real_folds=nb + 1, **kw)
+        try:
+            assert tr.stats()["fill_mode"] == (4 if sparse == "on" else 3)
+            sp, lv = tr.fit(6)
+            out[w0] = (sp, lv, tr.approx())
+        finally:
+            tr.close()
+    (s0, l0, a0), (s1, l1, a1) = out["off"], out[""]
+    assert np.array_equal(s0, s1)
+    assert np.array_equal(l0, l1)
+    assert np.array_equal(a0, a1)
+
+
 def test_config5_shape_matches_oracle():
     """Config 5 shape (MultiClass K=10, depth 8, 70%-zero columns, 64 borders) at 20k x 256."""
     d = datagen.config5(n_rows=20_000, n_features=256)
