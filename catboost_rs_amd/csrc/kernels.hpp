@@ -1680,7 +1680,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pkk_kernel(
                     unsigned long long* cell = (unsigned long long*)((char*)pk + ((bin << 8) + off8[k]));
 #pragma unroll
                     for (int j = 0; j < NP; ++j)
-                        if ((uint32_t)j < np_fill) atomicAdd(cell + (size_t)j * plane, S.st[j]);
+                        if (j + 1 < NP || np_fill == (uint32_t)NP) atomicAdd(cell + (size_t)j * plane, S.st[j]);
                 }
             };
             uint32_t blk = 0;
@@ -1829,6 +1829,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
     long long* __restrict__ hist,
     uint32_t np_fill /* planes filled: NP, or NP - 1 when the last (the weight alone) comes from elsewhere */) {
     constexpr int NP = (C + 1) / 2;
+    const bool fill_last = np_fill == (uint32_t)NP;   // workgroup-uniform
     extern __shared__ unsigned long long pk[];   // [NP][B][32], kOwn * 1024 cells
     const uint32_t b = blockIdx.x;
     const uint32_t xcd = b & 7u, q = b >> 3;
@@ -1898,7 +1899,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
                     unsigned long long* cell = (unsigned long long*)((char*)pk + (S.code & ~7u));
 #pragma unroll
                     for (int j = 0; j < NP; ++j)
-                        if ((uint32_t)j < np_fill) atomicAdd(cell + (size_t)j * plane, sv[j]);
+                        if (j + 1 < NP || fill_last) atomicAdd(cell + (size_t)j * plane, sv[j]);
                 }
                 if (__any(over != 0u)) {   // rare: wave-uniform branch
                     const uint32_t c2 = over ? (uint32_t)Bt[(size_t)S.doc * 16] : (uint32_t)kPksEmpty;
@@ -1906,7 +1907,7 @@ static __global__ __launch_bounds__(kPkkThreads) void fill_pks_kernel(
                         unsigned long long* cell = (unsigned long long*)((char*)pk + (c2 & ~7u));
 #pragma unroll
                         for (int j = 0; j < NP; ++j)
-                            if ((uint32_t)j < np_fill) atomicAdd(cell + (size_t)j * plane, sv[j]);
+                            if (j + 1 < NP || fill_last) atomicAdd(cell + (size_t)j * plane, sv[j]);
                     }
                 }
             };
