@@ -329,20 +329,22 @@ def main():
 
     # LDS-atomic roofline of the fill: every (row, feature) entry the fill adds costs one 64-bit
     # LDS atomic (packed and count-packed fills: both channels in one word), ceil((K+1)/2)
-    # (packed multi-channel fills: two channels per word) or K+1 (two-channel / channel-split
-    # fills); with the dominant-bin skip the entries are the issued ones (bins other than the
-    # feature's dominant bin), counted by the library over the profiled trees.  The cap is the
-    # contiguous (conflict-free) 64-bit LDS atomic rate measured on this GPU, the pattern the
-    # fills' rotated lane layouts reach
-    K = kw["approx_dim"] if P["loss"] == "MultiClass" else 1
-    per_pair = {1: 1, 3: (K + 2) // 2, 4: (K + 2) // 2, 5: 1}.get(st["fill_mode"], K + 1)
+    # (packed multi-channel fills: two channels per word, one fewer at level 0 when the weight's
+    # plane comes from its cache) or K+1 (two-channel / channel-split fills); the library counts
+    # the lane atomics issued (cbh_stats.fill_lane_atomics) over the profiled trees, with the
+    # dominant-bin skip over the issued entries only (bins other than the feature's dominant
+    # bin).  The cap is the contiguous (conflict-free) 64-bit LDS atomic rate measured on this
+    # GPU, the pattern the fills' rotated lane layouts reach
     lds = None
     rates = _lds_rates()
     if "contiguous_u64" in rates and fill_s > 0:
         entries = st["fill_entries"] if st["skip_features"] else st["fill_row_features"]
-        ach = entries * per_pair / fill_s
+        issued = st["fill_lane_atomics"]
+        per_pair = round(issued / entries, 4) if entries else 0.0
+        ach = issued / fill_s
         lds = {"achieved_lane_atomics_per_s": round(ach, 1),
                "atomics_per_entry": per_pair,
+               "lane_atomics": issued,
                "entries": entries,
                "counted_as": "all (row, feature) pairs" if not st["skip_features"] else
                f"issued: the {entries} (row, feature) entries whose bin is not the feature's dominant bin, "

@@ -76,7 +76,8 @@ class Stats(C.Structure):
                 ("skip_features", C.c_uint64), ("quantize_ms", C.c_double),
                 ("quantize_launches", C.c_uint64), ("quantize_bytes", C.c_double),
                 ("fill_mode", C.c_uint32), ("fill_pack_bits", C.c_int32), ("score_shift_der", C.c_int32),
-                ("score_shift_w", C.c_int32), ("fill_entries", C.c_uint64)]
+                ("score_shift_w", C.c_int32), ("fill_entries", C.c_uint64),
+                ("fill_lane_atomics", C.c_uint64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}

@@ -2234,13 +2234,17 @@ static __global__ __launch_bounds__(256) void row_entries_kernel(const uint8_t* 
 static __global__ __launch_bounds__(256) void fill_entries_kernel(const uint32_t* __restrict__ idx,
                                                                   const LevelPlan* __restrict__ plan, uint64_t n,
                                                                   const uint16_t* __restrict__ ent,
-                                                                  unsigned long long* __restrict__ total) {
+                                                                  unsigned long long* __restrict__ total /* [2] */,
+                                                                  uint32_t atomics_per_entry) {
     const uint32_t V = idx ? plan->rows : (uint32_t)n;
     unsigned long long c = 0;
     for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < V; p += gridDim.x * blockDim.x)
         c += ent[idx ? idx[p] : p];
     c = wave_sum_u64(c);
-    if (lane_id() == 0 && c != 0) atomicAdd(total, c);
+    if (lane_id() == 0 && c != 0) {
+        atomicAdd(total, c);
+        atomicAdd(total + 1, c * atomics_per_entry);
+    }
 }
 
 // Channel totals of the rows of every directly built segment: tot [segment][C].

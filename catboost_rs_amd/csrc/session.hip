@@ -213,6 +213,8 @@ struct cbh_session {
     bool w_static = false;           // packed multi-channel fill, the weight alone in the last plane and
     bool w0_ready = false;           // the same every tree: its level-0 cells cached after the first tree
     long long* w0_cache = nullptr;   // [F][B] (the fill's cells, before the dominant-bin rebuild)
+    bool l0_cached = false;          // the last recorded or enqueued tree took the weight's level-0 cells
+                                     // from the cache (its level-0 fill one plane short)
     int pack_bits = 0;
     unsigned long long* spack = nullptr;   // packed: [n] words
     unsigned long long* sseq = nullptr;    // the listed rows' statistics in idx order (packed: [V]; tiled: [V][2])
@@ -1527,6 +1529,15 @@ int ctr_level_weights_dev(cbh_session* s, uint32_t level) {
 // into pinned staging.  No host decision happens between launches (the split, partition
 // plan and leaf values stay on the device), so the sequence can be recorded once as a graph
 // and replayed for every later tree.
+// 64-bit LDS atomics a (row, feature) entry of the level's fill issues: one per channel (generic
+// and tiled exact fills), one (rounded packed and count-packed fills), one per plane of two
+// channels (packed multi-channel fills; the weight's plane left out at level 0 once it is cached).
+uint32_t fill_atomics_per_entry(const cbh_session* s, uint32_t level) {
+    if (s->packed || s->count) return 1u;
+    if (s->pkk) return (s->C + 1) / 2 - ((level == 0 && s->l0_cached) ? 1u : 0u);
+    return s->C;
+}
+
 template <int K>
 int enqueue_tree(cbh_session* s, bool use_host_sample) {
     constexpr int C = K + 1;
@@ -1634,6 +1645,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             const uint32_t NPl = (C + 1) / 2;
             const bool w0_use = level == 0 && s->w_static && s->w0_ready;
             const uint32_t npf = w0_use ? NPl - 1 : NPl;
+            if (level == 0) s->l0_cached = w0_use;
             if (w0_use)
                 HIP_TRY(hipMemcpyAsync(cur + (size_t)(C - 1) * s->F * s->B, s->w0_cache,
                                        sizeof(long long) * s->F * s->B, hipMemcpyDeviceToDevice, st));
@@ -1689,10 +1701,11 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
                 HIP_TRY(hipGetLastError());
             }
             if (!s->fill_ent) {
-                CHECK(dalloc(&s->fill_ent, 1));
-                HIP_TRY(hipMemsetAsync(s->fill_ent, 0, sizeof(unsigned long long), st));
+                CHECK(dalloc(&s->fill_ent, 2));
+                HIP_TRY(hipMemsetAsync(s->fill_ent, 0, 2 * sizeof(unsigned long long), st));
             }
-            fill_entries_kernel<<<grid_for(n, 256, 1024), 256, 0, st>>>(lidx, lplan, n, s->row_ent, s->fill_ent);
+            fill_entries_kernel<<<grid_for(n, 256, 1024), 256, 0, st>>>(lidx, lplan, n, s->row_ent, s->fill_ent,
+                                                                       fill_atomics_per_entry(s, level));
             HIP_TRY(hipGetLastError());
         }
         // ---- histogram finishing: dominant bins, prefix form, siblings ----
@@ -2138,6 +2151,7 @@ int cbh_session_grow(cbh_session* s, const double* approx, const double* target,
         s->stats.fill_launches += 1;
         s->stats.fill_rows += V;
         s->stats.fill_row_features += V * s->F;
+        if (!s->use_skip) s->stats.fill_lane_atomics += V * s->F * fill_atomics_per_entry(s, l);
         s->stats.fill_bytes += (double)V * (wbytes + sbytes + (l == 0 ? 0.0 : 4.0)) + built * per_leaf_bytes;
     }
     s->stats.trees += 1;
@@ -2182,12 +2196,13 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
     out->score_shift_w = sc.shift[kScoreW];
     out->fill_entries = out->fill_row_features;
     if (s->use_skip) {   // counted in profiled trees only (0 without them)
-        unsigned long long e = 0;
+        unsigned long long e[2] = {0, 0};
         if (s->fill_ent) {
             HIP_TRY(hipStreamSynchronize(s->stream));
-            HIP_TRY(hipMemcpy(&e, s->fill_ent, sizeof(e), hipMemcpyDeviceToHost));
+            HIP_TRY(hipMemcpy(e, s->fill_ent, sizeof(e), hipMemcpyDeviceToHost));
         }
-        out->fill_entries = e;
+        out->fill_entries = e[0];
+        out->fill_lane_atomics = e[1];
     }
     return CBH_OK;
 }
@@ -2195,7 +2210,7 @@ int cbh_session_stats(const cbh_session* s, cbh_stats* out) {
 void cbh_session_reset_stats(cbh_session* s) {
     if (!s) return;
     s->stats = cbh_stats{};
-    if (s->fill_ent) (void)hipMemsetAsync(s->fill_ent, 0, sizeof(unsigned long long), s->stream);
+    if (s->fill_ent) (void)hipMemsetAsync(s->fill_ent, 0, 2 * sizeof(unsigned long long), s->stream);
 }
 
 int cbh_session_set_ctr(cbh_session* s, const cbh_ctr_info* info) {

@@ -232,6 +232,9 @@ typedef struct {
     uint64_t fill_entries;        /* (row, feature) entries the fill launches added: fill_row_features, or
                                      with the dominant-bin skip those whose bin is not the dominant one,
                                      counted over the trees grown with profiling on */
+    uint64_t fill_lane_atomics;   /* 64-bit LDS atomics (lanes) the fill launches issued for those entries:
+                                     entries x atomics per entry (one per channel, one, or one per plane of
+                                     two channels, by fill) */
 } cbh_stats;
 
 int cbh_session_stats(const cbh_session* s, cbh_stats* out);

@@ -159,6 +159,9 @@ def test_level_histograms_match_oracle_integer_weights(fill, monkeypatch):
         assert [(f, b) for f, b, _ in t["splits"]] == [tuple(x) for x in o["splits"].tolist()]
         for level in range(6):
             _close_level_hist(be.level_hist(level, F, B), o["hists"][level], nb, 1e-9)
+        # 64-bit LDS atomics issued: one per channel (der, weight) per entry, one when packed
+        st = be.stats()
+        assert st["fill_lane_atomics"] == st["fill_row_features"] * (1 if fill == "count" else 2)
     finally:
         be.end_device_training()
 
@@ -917,11 +920,16 @@ def test_config5_shape_matches_oracle():
     _assert_same_fit(*_fit_both(d, 4))
 
 
-def test_fill_entries_count_the_non_dominant_entries():
+@pytest.mark.parametrize("fill", ["generic", "packed"])
+def test_fill_entries_count_the_non_dominant_entries(fill, monkeypatch):
     """With the dominant-bin skip, the entries the fill adds (cbh_stats.fill_entries, counted in
     profiled trees) are the visited rows' features whose bin is not the feature's dominant bin
     (the most frequent bin, lowest on ties, when it holds at least n/8 rows): level 0 visits every
-    row, level 1 the rows of the smaller child (ties: the TRUE child, bin > split bin)."""
+    row, level 1 the rows of the smaller child (ties: the TRUE child, bin > split bin).  The lane
+    atomics issued (cbh_stats.fill_lane_atomics) are 11 per entry under the generic fill (one per
+    channel); under the packed multi-channel fill 6 (two channels per plane), 5 at the second
+    tree's level 0, whose weight plane comes from the first tree's."""
+    monkeypatch.setenv("CBH_FILL", fill)
     d = datagen.config5(n_rows=20_000, n_features=96)
     bins, nb, y = d["bins"], d["n_borders"], d["target"]
     F, n = bins.shape
@@ -931,10 +939,14 @@ def test_fill_entries_count_the_non_dominant_entries():
     tr = cb.Trainer(bins, B, y, real_folds=nb + 1, **kw)
     try:
         assert tr.stats()["skip_features"] > 0
+        assert tr.stats()["fill_mode"] in ((0,) if fill == "generic" else (3, 4))
         tr.set_profile(True)
-        tr.reset_stats()
-        sp, _ = tr.fit(1)
-        st = tr.stats()
+        sts, sps = [], []
+        for _ in range(2):
+            tr.reset_stats()
+            sp, _ = tr.fit(1)
+            sps.append(sp[0])
+            sts.append(tr.stats())
     finally:
         tr.close()
     ent = np.zeros(n, np.int64)
@@ -942,11 +954,14 @@ def test_fill_entries_count_the_non_dominant_entries():
         c = np.bincount(bins[f], minlength=256)
         dom = int(np.argmax(c))
         ent += (bins[f] != dom) if c[dom] * 8 >= n else 1
-    f0, b0 = sp[0][0]
-    true = bins[f0] > b0
-    built = true if true.sum() <= n - true.sum() else ~true
-    assert st["fill_row_features"] == F * (n + int(built.sum()))
-    assert st["fill_entries"] == int(ent.sum()) + int(ent[built].sum())
+    for t, (sp, st) in enumerate(zip(sps, sts)):
+        f0, b0 = sp[0]
+        true = bins[f0] > b0
+        built = true if true.sum() <= n - true.sum() else ~true
+        assert st["fill_row_features"] == F * (n + int(built.sum()))
+        assert st["fill_entries"] == int(ent.sum()) + int(ent[built].sum())
+        l0, l1 = (11, 11) if fill == "generic" else (6 if t == 0 else 5, 6)
+        assert st["fill_lane_atomics"] == l0 * int(ent.sum()) + l1 * int(ent[built].sum())
 
 
 @pytest.mark.parametrize("F,B", [(257, 20), (31, 3), (50, 30)])
