@@ -14,6 +14,10 @@
 //                                random 256-byte bin row (16 distinct bank pairs, random rows)
 //   dpp_row_mod16_pairs_u64      columns (r + 2 l) mod 32 of random bin rows: 8 pairs of lanes
 //                                of a DPP row on the same bank pair (column mod 16)
+//   *_160k_lo / *_160k_hi        160 KiB workgroups (the whole LDS), addresses in the low 128 KiB
+//                                or in the top 32 KiB: contiguous, and the folded narrow words'
+//                                pattern (lane l: cell bin * 16 + 8 (l >> 3) + ... 16 distinct
+//                                bank pairs of random bin rows of 16 cells)
 // Prints one line per pattern: "<pattern> <lane-atomics per second>".
 #include <hip/hip_runtime.h>
 
@@ -32,6 +36,7 @@
 constexpr int kIters = 2048;
 constexpr int kAddr = 8;        // addresses per thread
 constexpr int kCells = 16384;   // 128 KB of u64 cells
+constexpr int kBigCells = 20480;   // 160 KB
 
 __device__ __forceinline__ uint32_t mix32(uint32_t x) {
     x ^= x >> 16;
@@ -48,16 +53,19 @@ enum Pattern : int {
     kDppSamePairs = 2,
     kDppPairsRandomRows = 3,
     kDppMod16Pairs = 4,
+    kFoldRows = 5,
 };
 
 // T: cell type (u64 or u32); kRtn: use the returned old value (an atomic with return);
 // kQuarter: only lanes 0-15 of every wave issue.
-template <int kPattern, typename T, int kRtn, int kQuarter = 0>
+// kBig: a 160 KiB workgroup; kBase: the first cell the addresses use (16384 = the top 32 KiB)
+template <int kPattern, typename T, int kRtn, int kQuarter = 0, int kBig = 0, uint32_t kBase = 0>
 __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uint32_t seed) {
     extern __shared__ unsigned long long cells_raw[];
-    T* cells = (T*)cells_raw;
-    constexpr uint32_t n_cells = kCells * 8 / sizeof(T);
-    for (uint32_t i = threadIdx.x; i < n_cells; i += blockDim.x) cells[i] = 0;
+    T* cells = (T*)(cells_raw + kBase);
+    constexpr uint32_t all_cells = (kBig ? kBigCells : kCells) * 8 / sizeof(T);
+    constexpr uint32_t n_cells = (kBase ? 4096u : kCells) * 8 / sizeof(T);   // the cells the addresses span
+    for (uint32_t i = threadIdx.x; i < all_cells; i += blockDim.x) ((T*)cells_raw)[i] = 0;
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, l = threadIdx.x & 15u, row = threadIdx.x >> 4;
     uint32_t idx[kAddr];
@@ -70,7 +78,8 @@ __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uin
         else if (kPattern == kScattered) c = h;
         else if (kPattern == kDppSamePairs) c = l + 32u * ((threadIdx.x >> 4) & 3u) + 128u * (uint32_t)q;
         else if (kPattern == kDppPairsRandomRows) c = (h & 255u) * 32u + l;
-        else c = (h & 255u) * 32u + (((hr & 31u) + 2u * l) & 31u);
+        else if (kPattern == kDppMod16Pairs) c = (h & 255u) * 32u + (((hr & 31u) + 2u * l) & 31u);
+        else c = (h & 255u) * 16u + 8u * (l >> 3) + (((uint32_t)q + (l & 7u)) & 3u) + 4u * ((l >> 2) & 1u);
         idx[q] = c % n_cells;
     }
     T carry = 0;
@@ -86,18 +95,19 @@ __global__ __launch_bounds__(1024) void rate_kernel(unsigned long long* out, uin
     if (threadIdx.x == 0) out[blockIdx.x] = (unsigned long long)cells[0] + (unsigned long long)carry;
 }
 
-template <int kPattern, typename T, int kRtn, int kQuarter = 0>
+template <int kPattern, typename T, int kRtn, int kQuarter = 0, int kBig = 0, uint32_t kBase = 0>
 int measure(const char* name, int blocks, unsigned long long* d) {
-    CK(hipFuncSetAttribute((const void*)rate_kernel<kPattern, T, kRtn, kQuarter>,
-                           hipFuncAttributeMaxDynamicSharedMemorySize, kCells * 8));
-    rate_kernel<kPattern, T, kRtn, kQuarter><<<blocks, 1024, kCells * 8>>>(d, 1u);
+    constexpr int bytes = (kBig ? kBigCells : kCells) * 8;
+    CK(hipFuncSetAttribute((const void*)rate_kernel<kPattern, T, kRtn, kQuarter, kBig, kBase>,
+                           hipFuncAttributeMaxDynamicSharedMemorySize, bytes));
+    rate_kernel<kPattern, T, kRtn, kQuarter, kBig, kBase><<<blocks, 1024, bytes>>>(d, 1u);
     CK(hipGetLastError());
     CK(hipDeviceSynchronize());
     hipEvent_t a, b;
     CK(hipEventCreate(&a));
     CK(hipEventCreate(&b));
     CK(hipEventRecord(a));
-    rate_kernel<kPattern, T, kRtn, kQuarter><<<blocks, 1024, kCells * 8>>>(d, 2u);
+    rate_kernel<kPattern, T, kRtn, kQuarter, kBig, kBase><<<blocks, 1024, bytes>>>(d, 2u);
     CK(hipEventRecord(b));
     CK(hipEventSynchronize(b));
     float ms = 0.f;
@@ -128,6 +138,11 @@ int main() {
     if (measure<kDppSamePairs, u64, 0>("dpp_rows_same_pairs_u64", blocks, d)) return 1;
     if (measure<kDppPairsRandomRows, u64, 0>("dpp_row_pairs_random_rows_u64", blocks, d)) return 1;
     if (measure<kDppMod16Pairs, u64, 0>("dpp_row_mod16_pairs_u64", blocks, d)) return 1;
+    if (measure<kContiguous, u64, 0, 0, 1>("contiguous_u64_160k_lo", blocks, d)) return 1;
+    if (measure<kContiguous, u64, 0, 0, 1, 16384>("contiguous_u64_160k_hi", blocks, d)) return 1;
+    if (measure<kFoldRows, u64, 0, 0, 1>("fold_rows_u64_160k_lo", blocks, d)) return 1;
+    if (measure<kFoldRows, u64, 0, 0, 1, 16384>("fold_rows_u64_160k_hi", blocks, d)) return 1;
+    if (measure<kDppPairsRandomRows, u64, 0, 0, 1>("dpp_row_pairs_random_rows_u64_160k_lo", blocks, d)) return 1;
     CK(hipFree(d));
     return 0;
 }
