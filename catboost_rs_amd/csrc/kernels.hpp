@@ -389,7 +389,7 @@ __host__ __device__ inline CountPack count_pack_plan(int e, unsigned long long w
 static __global__ __launch_bounds__(256) void scales_kernel(const unsigned long long* __restrict__ partials,
                                                            uint32_t n_blocks, Bounds* __restrict__ b,
                                                            Scales* __restrict__ sc, int pack_bits, int count) {
-    __shared__ unsigned long long red[256][7];
+    __shared__ unsigned long long red[4][7];   // per wave (256 threads)
     unsigned long long acc[7] = {0, 0, 0, 0, 0, 0, 0};
     for (uint32_t i = threadIdx.x; i < n_blocks; i += blockDim.x) {
         for (int k = 0; k < 5; ++k) acc[k] += partials[(size_t)i * kPartials + k];
@@ -398,13 +398,27 @@ static __global__ __launch_bounds__(256) void scales_kernel(const unsigned long 
             acc[k] = u > acc[k] ? u : acc[k];
         }
     }
-    for (int k = 0; k < 7; ++k) red[threadIdx.x][k] = acc[k];
+    // integer sums and maxima: any order gives the same values
+    const uint32_t wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+        unsigned long long v = acc[k];
+        if (k < 5) {
+            v = wave_sum_u64(v);
+        } else {
+            for (int o = 32; o > 0; o >>= 1) {
+                const unsigned long long u = __shfl_xor(v, o, 64);
+                v = u > v ? u : v;
+            }
+        }
+        if (lane_id() == 0) red[wave][k] = v;
+    }
     __syncthreads();
     if (threadIdx.x != 0) return;
     for (int k = 0; k < 7; ++k) {
         unsigned long long v = 0;
-        for (uint32_t tI = 0; tI < blockDim.x; ++tI) {
-            const unsigned long long u = red[tI][k];
+        for (uint32_t w = 0; w < blockDim.x / 64; ++w) {
+            const unsigned long long u = red[w][k];
             v = k < 5 ? v + u : (u > v ? u : v);
         }
         acc[k] = v;
@@ -2846,7 +2860,7 @@ static __global__ __launch_bounds__(256) void split_count_kernel(
 static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __restrict__ cnt,
                                                          uint32_t n_blocks,
                                                          uint32_t* __restrict__ totals) {
-    __shared__ uint32_t sh[1024];
+    __shared__ uint32_t sh[128];   // [0, 16): wave totals, [64, 80): their exclusive prefix
     uint32_t* row = cnt + (size_t)blockIdx.x * n_blocks;
     const uint32_t per = (n_blocks + blockDim.x - 1) / blockDim.x;
     const uint32_t b0 = threadIdx.x * per;
@@ -2862,15 +2876,29 @@ static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __rest
 #pragma unroll
         for (uint32_t q = 0; q < kBatch; ++q) local += v[q];
     }
-    sh[threadIdx.x] = local;
-    __syncthreads();
-    for (uint32_t o = 1; o < blockDim.x; o <<= 1) {
-        uint32_t v = threadIdx.x >= o ? sh[threadIdx.x - o] : 0;
-        __syncthreads();
-        sh[threadIdx.x] += v;
-        __syncthreads();
+    // inclusive scan of the threads' sums: within each wave by shuffles, then over the wave
+    // totals by wave 0 (two barriers)
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, n_waves = blockDim.x >> 6;
+    uint32_t inc = local;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = __shfl_up(inc, o, 64);
+        if (lane >= (uint32_t)o) inc += u;
     }
-    uint32_t run = sh[threadIdx.x] - local;  // exclusive prefix of this thread's range
+    if (lane == 63) sh[wave] = inc;
+    __syncthreads();
+    if (wave == 0) {
+        const uint32_t t = lane < n_waves ? sh[lane] : 0u;
+        uint32_t wi = t;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t u = __shfl_up(wi, o, 64);
+            if (lane >= (uint32_t)o) wi += u;
+        }
+        if (lane < n_waves) sh[64 + lane] = wi - t;   // exclusive prefix of the wave totals
+    }
+    __syncthreads();
+    uint32_t run = sh[64 + wave] + inc - local;  // exclusive prefix of this thread's range
     for (uint32_t k0 = 0; k0 < per; k0 += kBatch) {
         uint32_t v[kBatch];
 #pragma unroll
@@ -2887,7 +2915,7 @@ static __global__ __launch_bounds__(1024) void plan_scan_kernel(uint32_t* __rest
             }
         }
     }
-    if (threadIdx.x == blockDim.x - 1) totals[blockIdx.x] = sh[threadIdx.x];
+    if (threadIdx.x == blockDim.x - 1) totals[blockIdx.x] = sh[64 + wave] + inc;
 }
 
 // Stable compaction of the rows of every directly built child into idx (grouped by parent in
