@@ -1235,8 +1235,16 @@ struct ExSet {
 };
 
 template <int U>
-__device__ __forceinline__ void exact_pass(unsigned long long* __restrict__ ex, const ExSet& S, const uint32_t* off8) {
-    exact_row_atomics(ex, S.w[U], off8, half_bcast64<U>(S.sd), half_bcast64<U>(S.sw));
+__device__ __forceinline__ void exact_pass(unsigned long long* __restrict__ ex, const ExSet& S, const uint32_t* off8,
+                                           unsigned long long qd, unsigned long long qw) {
+    exact_row_atomics(ex, S.w[U], off8, half_bcast64<U>(qd), half_bcast64<U>(qw));
+}
+
+// A staged row's score channels: the f64 values (their bits as loaded) on the tree's fixed-point
+// scales, round(v * 2^S) as the score channels are everywhere (to_fixed); a position past the
+// range loaded 0 and stays 0.
+__device__ __forceinline__ unsigned long long stat_fixed(unsigned long long bits, double mul) {
+    return (unsigned long long)to_fixed(__longlong_as_double((long long)bits), mul);
 }
 
 // Positions [pos, end) of a full tile.  Two sets alternate: while one block's atomics issue, the
@@ -1249,7 +1257,7 @@ __device__ __forceinline__ void exact_range(unsigned long long* __restrict__ ex,
                                             uint32_t sh, uint32_t wl4, uint32_t j8, uint32_t l,
                                             __amdgpu_buffer_rsrc_t ibase, __amdgpu_buffer_rsrc_t sbase,
                                             bool seq, uint32_t pos, uint32_t end, uint32_t n, uint32_t r0,
-                                            const uint32_t* off8) {
+                                            const uint32_t* off8, double md, double mw) {
     auto q_of = [&](uint32_t bb) -> uint32_t { return bb + 16u * r0; };
     auto dense_q = [&](uint32_t bb) -> uint32_t {
         const uint32_t q = q_of(bb);
@@ -1291,14 +1299,15 @@ __device__ __forceinline__ void exact_range(unsigned long long* __restrict__ ex,
         }
     };
     auto consume = [&](const ExSet& S) {
-        exact_pass<0>(ex, S, off8);
-        exact_pass<1>(ex, S, off8);
-        exact_pass<2>(ex, S, off8);
-        exact_pass<3>(ex, S, off8);
-        exact_pass<4>(ex, S, off8);
-        exact_pass<5>(ex, S, off8);
-        exact_pass<6>(ex, S, off8);
-        exact_pass<7>(ex, S, off8);
+        const unsigned long long qd = stat_fixed(S.sd, md), qw = stat_fixed(S.sw, mw);
+        exact_pass<0>(ex, S, off8, qd, qw);
+        exact_pass<1>(ex, S, off8, qd, qw);
+        exact_pass<2>(ex, S, off8, qd, qw);
+        exact_pass<3>(ex, S, off8, qd, qw);
+        exact_pass<4>(ex, S, off8, qd, qw);
+        exact_pass<5>(ex, S, off8, qd, qw);
+        exact_pass<6>(ex, S, off8, qd, qw);
+        exact_pass<7>(ex, S, off8, qd, qw);
     };
     static_assert(NS >= 2 && NS <= 4, "two to four sets");
     ExSet S0, S1, S2, S3;
@@ -1341,8 +1350,8 @@ struct ExNarrowSet {
 
 template <int U>
 __device__ __forceinline__ void exact_narrow_pass(unsigned long long* __restrict__ ex, const ExNarrowSet& S,
-                                                  const uint32_t* off8) {
-    exact_row_atomics(ex, S.w[U], off8, quad_pair_bcast64<U>(S.sd), quad_pair_bcast64<U>(S.sw));
+                                                  const uint32_t* off8, unsigned long long qd, unsigned long long qw) {
+    exact_row_atomics(ex, S.w[U], off8, quad_pair_bcast64<U>(qd), quad_pair_bcast64<U>(qw));
 }
 
 // Positions [pos, end) of a narrow last tile (at most 2 words).  A DPP row covers the same 16
@@ -1355,7 +1364,7 @@ __device__ __forceinline__ void exact_range_narrow(unsigned long long* __restric
                                                    uint32_t sh, uint32_t wl4, uint32_t l,
                                                    __amdgpu_buffer_rsrc_t ibase, __amdgpu_buffer_rsrc_t sbase,
                                                    bool seq, uint32_t pos, uint32_t end, uint32_t n, uint32_t r0,
-                                                   const uint32_t* off8) {
+                                                   const uint32_t* off8, double md, double mw) {
     constexpr uint32_t NS = 4;
     const uint32_t j = l >> 1, stg = 8u * (l & 1u) + j;   // this lane's staged position in a block
     auto q_of = [&](uint32_t bb) -> uint32_t { return bb + 16u * r0; };
@@ -1411,8 +1420,9 @@ __device__ __forceinline__ void exact_range_narrow(unsigned long long* __restric
     // one block of a set: its atomics, then (unless the range ends) the set reloaded for the block
     // four later
     auto step = [&](ExNarrowSet& S, uint32_t bb) -> bool {
-        exact_narrow_pass<0>(ex, S, off8);
-        exact_narrow_pass<1>(ex, S, off8);
+        const unsigned long long qd = stat_fixed(S.sd, md), qw = stat_fixed(S.sw, mw);
+        exact_narrow_pass<0>(ex, S, off8, qd, qw);
+        exact_narrow_pass<1>(ex, S, off8, qd, qw);
         if (bb + kExBlockRows >= end) return true;
         load(S, bb + NS * kExBlockRows);
         return false;
@@ -1452,12 +1462,14 @@ template <bool kGather>
 static __global__ __launch_bounds__(kExThreads) void fill_exact_kernel(
     const uint32_t* __restrict__ trows /* tile-major 8-word slices (pack_tiles_kernel) */, uint32_t W,
     uint64_t n, const uint32_t* __restrict__ idx /* kGather: rows listed by the partition */,
-    const LevelPlan* __restrict__ plan, const long long* __restrict__ sfix /* [n][2] */,
-    const long long* __restrict__ sseq /* kGather, nullable: [V][2], the listed rows' statistics in idx order */,
+    const LevelPlan* __restrict__ plan, const long long* __restrict__ sfix /* [n][2] f64 score channels */,
+    const long long* __restrict__ sseq /* kGather, nullable: [V][2], the listed rows' channels in idx order */,
     uint32_t n_tiles, uint32_t F, uint32_t B, uint32_t G, uint32_t Gn, long long* __restrict__ hist,
     const uint32_t* __restrict__ rows_rm /* nullable, kGather: row-major words, 2^rm_sh bytes per row */,
-    uint32_t rm_sh, uint32_t sets /* blocks in flight of the full loop: 2 to 4 */) {
+    uint32_t rm_sh, uint32_t sets /* blocks in flight of the full loop: 2 to 4 */,
+    const Scales* __restrict__ sc /* the score channels' scales: sfix and sseq hold f64 values */) {
     extern __shared__ unsigned long long ex[];
+    const double md = sc->mul[kScoreDer], mw = sc->mul[kScoreW];
     // blocks: n_tiles tiles of the 8-lane loop in G row ranges each, numbered range-major and
     // dealt to the 8 XCDs in runs (block b to XCD b % 8: XCD x takes pairs [x per, (x + 1) per)),
     // so all tiles of a range share one L2; then, when Gn > 0, the narrow last tile (tile
@@ -1528,16 +1540,16 @@ static __global__ __launch_bounds__(kExThreads) void fill_exact_kernel(
         if (end > pos) {
             if (!narrow && sets == 4)
                 exact_range<kGather, 4>(ex, rbase, sh, wl4, 8u * (l >> 3), l, ibase, sbase, seq, pos, end,
-                                        (uint32_t)n, r0, off8);
+                                        (uint32_t)n, r0, off8, md, mw);
             else if (!narrow && sets == 3)
                 exact_range<kGather, 3>(ex, rbase, sh, wl4, 8u * (l >> 3), l, ibase, sbase, seq, pos, end,
-                                        (uint32_t)n, r0, off8);
+                                        (uint32_t)n, r0, off8, md, mw);
             else if (!narrow)
                 exact_range<kGather, 2>(ex, rbase, sh, wl4, 8u * (l >> 3), l, ibase, sbase, seq, pos, end,
-                                        (uint32_t)n, r0, off8);
+                                        (uint32_t)n, r0, off8, md, mw);
             else
                 exact_range_narrow<kGather>(ex, rbase, sh, wl4, l, ibase, sbase, seq, pos, end, (uint32_t)n, r0,
-                                            off8);
+                                            off8, md, mw);
             __syncthreads();
             exact_flush(ex, TF, B, F, f0, hist + (size_t)slot * 2u * F * B, narrow ? 4u : 1u);
             __syncthreads();

@@ -1578,7 +1578,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
                                                                          (1ll << s->pack_bits) - 1);
     else if (s->count)
         pack_stats_count_kernel<<<grid_for(n, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales, s->spack);
-    else
+    else if (!s->tiled)   // (the tiled exact fill rounds the f64 channels as it stages them)
         quantize_stats_kernel<C><<<grid_for(n * C, 256, 8192), 256, 0, st>>>(s->sstat, n, s->scales);
     HIP_TRY(hipGetLastError());
     CHECK(s->stage_end());
@@ -1629,12 +1629,12 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         else if (s->tiled && level == 0)
             fill_exact_kernel<false><<<s->pk_dense.blocks, kExThreads, s->pk_lds, st>>>(
                 s->trows, s->W, n, nullptr, nullptr, (const long long*)s->sstat, nullptr, s->pk_dense.tiles16, s->F,
-                s->B, s->pk_dense.ranges, s->pk_dense.ranges_n, cur, nullptr, 0u, s->ex_sets);
+                s->B, s->pk_dense.ranges, s->pk_dense.ranges_n, cur, nullptr, 0u, s->ex_sets, s->scales);
         else if (s->tiled)
             fill_exact_kernel<true><<<s->pk_gath.blocks, kExThreads, s->pk_lds, st>>>(
                 s->trows, s->W, n, lidx, lplan, (const long long*)s->sstat, (const long long*)s->sseq,
                 s->pk_gath.tiles16, s->F, s->B, s->pk_gath.ranges, s->pk_gath.ranges_n, cur,
-                s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh, s->ex_sets);
+                s->pk_rm_sh ? s->rows : nullptr, s->pk_rm_sh, s->ex_sets, s->scales);
         else if (s->pkk) {
             const size_t lds = (size_t)kPkkCells * sizeof(unsigned long long);
             const unsigned grid = s->pkk_ranges * s->pkk_tiles;
@@ -1808,7 +1808,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             if (s->packed || s->count)   // the listed rows' packed statistic
                 compact_kernel<1><<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->totals, s->plans + level,
                                                       s->idx, s->spack, s->sseq);
-            else if (s->tiled && s->sseq)   // both fixed-point channels of the listed rows
+            else if (s->tiled && s->sseq)   // both f64 score channels of the listed rows
                 compact_kernel<2><<<NB, 256, 0, st>>>(s->leaf, n, level, s->cnt, 4 * NB, s->totals, s->plans + level,
                                                       s->idx, (const unsigned long long*)s->sstat, s->sseq);
             else
