@@ -1,5 +1,6 @@
 // Host mirror of cb-train's device branch (crates/cb-train/src/boosting.rs:6532-7300),
-// driving the session through the public C-ABI only.  It owns the persistent training RNG: the
+// driving the session through the public C-ABI (plus one internal hook, which runs the per-tree
+// draw replay while the device grows the tree).  It owns the persistent training RNG: the
 // device never draws on the main stream, it receives the per-tree sampling phase
 // (Bayesian seed / Bernoulli raw state) and the host advances its stream exactly as the
 // CPU branch would, including the per-level draws of the perturbed level search that the
@@ -16,6 +17,7 @@
 #include "common.hpp"
 
 int cbh_internal_fail(int code, const std::string& msg);  // session.hip: sets cbh_last_error()
+extern "C" void cbh_internal_set_overlap(cbh_session* s, void (*fn)(void*), void* arg);  // session.hip
 
 namespace {
 
@@ -41,6 +43,7 @@ struct cbt_trainer {
     uint32_t F = 0, K = 1;
     cbh::Rng rng{};
     bool draws_active = false;
+    bool draws_done = false;   // this step's draw replay ran (during the device grow)
     bool first = true;
     std::vector<double> target;
     double bias = 0.0;
@@ -189,6 +192,19 @@ int cbt_set_ctr(cbt_trainer* t, const cbh_ctr_info* info) {
     return rc;
 }
 
+// Step 3 of a tree: the per-level draws of the CPU grower's perturbed level search (none with
+// CTR columns), then the post-tree draws (device_draw_replay.rs).
+static void replay_draws(void* arg) {
+    cbt_trainer* t = (cbt_trainer*)arg;
+    for (int level = 0; level < t->p.depth && !t->ctr; ++level) {
+        for (uint32_t f = 0; f < t->F; ++f) (void)cbh::rng_real1(t->rng);
+        (void)cbh::rng_gen(t->rng);
+        for (uint32_t f = 0; f < t->F; ++f) (void)std_normal(t->rng);
+    }
+    for (int k = 0; k < kPostTreeExtraDraws; ++k) (void)cbh::rng_gen(t->rng);
+    t->draws_done = true;
+}
+
 int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8_t* split_one_hot,
              double* leaf_values) {
     if (!t) return CBH_ERR_INVALID_ARG;
@@ -230,20 +246,22 @@ int cbt_step(cbt_trainer* t, uint32_t* split_feature, uint32_t* split_bin, uint8
         fam.pair_weight = t->pair_w.empty() ? nullptr : t->pair_w.data();
         fam.n_pairs = t->pair_win.size();
     }
+    // 3. the CPU grower's per-level draws, then the post-tree draws: they depend on nothing the
+    // tree computes, so they run while the device grows it (kept only if the tree is taken)
+    const cbh::Rng rng_before = t->rng;
+    if (t->draws_active) cbh_internal_set_overlap(t->s, &replay_draws, t);
     int rc = cbh_session_grow(t->s, nullptr, t->first ? t->target.data() : nullptr, t->n, nullptr, 0,
                               &smp, t->pairs_pending ? &fam : nullptr, &out);
-    if (rc != CBH_OK) return rc;
+    cbh_internal_set_overlap(t->s, nullptr, nullptr);
+    if (rc != CBH_OK) {
+        t->rng = rng_before;
+        t->draws_done = false;
+        return rc;
+    }
+    if (t->draws_active && !t->draws_done) replay_draws(t);   // (a grow that never launched)
+    t->draws_done = false;
     t->first = false;
     t->pairs_pending = false;
-    // 3. replay the CPU grower's per-level draws, then the post-tree draws
-    if (t->draws_active) {
-        for (int level = 0; level < p.depth && !t->ctr; ++level) {
-            for (uint32_t f = 0; f < t->F; ++f) (void)cbh::rng_real1(t->rng);
-            (void)cbh::rng_gen(t->rng);
-            for (uint32_t f = 0; f < t->F; ++f) (void)std_normal(t->rng);
-        }
-        for (int k = 0; k < kPostTreeExtraDraws; ++k) (void)cbh::rng_gen(t->rng);
-    }
     if (split_feature) std::memcpy(split_feature, t->sf.data(), sizeof(uint32_t) * p.depth);
     if (split_bin) std::memcpy(split_bin, t->sb.data(), sizeof(uint32_t) * p.depth);
     if (split_one_hot) std::memcpy(split_one_hot, t->so.data(), p.depth);

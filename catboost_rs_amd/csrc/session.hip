@@ -111,6 +111,10 @@ struct cbh_session {
     uint32_t F = 0, B = 0, W = 0, Ws = 0, K = 1, C = 2, depth = 0;   // Ws: words per packed row in memory
     double lr = 0.0, l2 = 0.0;
     bool has_weight = false, target_set = false, pending = false;
+    // host work that the caller runs while the device grows the tree (between the launch and the
+    // wait of cbh_session_grow; cbh_internal_set_overlap)
+    void (*overlap_fn)(void*) = nullptr;
+    void* overlap_arg = nullptr;
     hipStream_t stream = nullptr;
     int device = 0;
 
@@ -1910,6 +1914,7 @@ int grow_impl(cbh_session* s, const SampleParams& smp, bool use_host_sample,
         CHECK(enqueue_tree<K>(s, use_host_sample));
     }
     s->pending = true;
+    if (s->overlap_fn) s->overlap_fn(s->overlap_arg);   // host work while the tree grows
     HIP_TRY(hipStreamSynchronize(st));
     const size_t n_leaves = (size_t)1 << s->depth;
     splits_out.assign(s->pin_splits, s->pin_splits + s->depth);
@@ -2248,6 +2253,14 @@ int cbh_session_read_ctr_bins(const cbh_session* s, int32_t averaging, uint8_t* 
     HIP_TRY(hipStreamSynchronize(s->stream));
     HIP_TRY(hipMemcpy(out, src, total, hipMemcpyDeviceToHost));
     return CBH_OK;
+}
+
+// The driver's host work for the next cbh_session_grow calls, run once the tree is launched and
+// before the wait for it (null: none).
+void cbh_internal_set_overlap(cbh_session* s, void (*fn)(void*), void* arg) {
+    if (!s) return;
+    s->overlap_fn = fn;
+    s->overlap_arg = arg;
 }
 
 int cbh_session_set_profile(cbh_session* s, int32_t on) {
