@@ -18,14 +18,18 @@ for the stage breakdown and the fill roofline.
 
 Reported next to the GPU figure:
   * roofline of the dominant kernel (histogram fill): algorithmic bytes per launch
-    (V rows x (W*4 + S + 4) + histogram bytes, S = 8 bytes of packed statistics per row for the
-    packed fill, 8*(K+1) otherwise) / average launch time from HIP events
+    (V rows x (W*4 + S + 4) + histogram bytes, S = bytes of a row's statistics: 8 for the
+    packed and count-packed fills, 8*ceil((K+1)/2) for the packed multi-channel fills,
+    8*(K+1) otherwise) / average launch time from HIP events
     recorded on the session stream, against MI355X's 8 TB/s; HBM traffic per launch from
     the copy-calibrated rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/;
   * the fill's LDS-atomic rate against the measured conflict-free 64-bit LDS atomic cap;
   * cpu_baseline: the CPU restatement of the reference algorithm (oracle/) timed on the
     host cores for the first trees of the same data, with a check that its splits equal
-    the GPU's.
+    the GPU's;
+  * reference_published_cells (config 2): the reference's own published speed cells (a
+    whole fit of 30 trees from a row-major f32 matrix, then a 1024-row prediction) timed on
+    this GPU, next to the seconds the reference publishes for them on a Tesla P100.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--rows N]
 """
@@ -236,6 +240,8 @@ def main():
     ap.add_argument("--cpu-trees", type=int, default=-1)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-published", action="store_true",
+                    help="config 2: leave out the reference's published speed cells")
     ap.add_argument("--bootstrap", default="",
                     help="override the config's bootstrap type (a measurement option; the line then names it)")
     ap.add_argument("--prep", action="store_true",
@@ -457,7 +463,79 @@ def main():
         out["ctr_columns_s"] = round(data["ctr_s"], 4)
     if raw:
         out["select_borders_s"] = round(data["borders_s"], 4)
+    if args.config == 2 and not args.no_published:
+        try:
+            out["reference_published_cells"] = _reference_cells()
+        except Exception as e:   # an informational block: it never voids the measurement
+            out["reference_published_cells"] = {"error": repr(e)}
     print(json.dumps(out), flush=True)
+
+
+# The reference's published GPU fit wall-clock (seconds per fit, median of 3, Tesla P100;
+# bench/full_param_gpu_speed/kaggle-output-260808-r6/report.md:13,17,29,33): catboost_rs and
+# official CatBoost 1.2.10 with task_type GPU, for the SymmetricTree cells without weights or CTRs.
+REFERENCE_CELLS = (("RMSE", 300_000, 0.435, 1.223), ("Logloss", 300_000, 0.460, 1.434),
+                   ("RMSE", 1_000_000, 0.992, 1.661), ("Logloss", 1_000_000, 0.987, 1.838))
+
+
+def _reference_cells():
+    """The reference's published speed cells on this GPU, timed as its grid times them
+    (bench/full_param_gpu_speed/bench.py:51-62,545-572): fit(X, y) from a row-major f32 X in
+    host memory -- the columns of X, 32 GreedyLogSum borders per feature, the session open
+    (upload, device quantization), 30 depth-6 trees (L2 score, Gradient leaves, no bootstrap,
+    no boost from average, learning rate 0.1, L2 3.0) -- plus a prediction of the first 1024
+    rows; one untimed warm fit (whose predictions are checked against the training
+    approximant), then the median of 3.  Other hardware than the reference's numbers (a
+    Tesla P100), the same recipe."""
+    import numpy as np
+
+    import catboost_rs_amd as cb
+    from catboost_rs_amd import datagen
+
+    cells = []
+    for loss, n, ref_s, off_s in REFERENCE_CELLS:
+        X, y = datagen.reference_speed_cell(n, 50, classification=loss == "Logloss")
+
+        def fit_once(check=False):
+            t = [time.perf_counter()]
+            cols = cb.columns_from_rows(X)
+            t.append(time.perf_counter())
+            borders = cb.select_borders(cols, 32, "Min", "GreedyLogSum")
+            t.append(time.perf_counter())
+            tr = cb.Trainer.from_floats(cols, borders, y, loss=loss, depth=6, learning_rate=0.1,
+                                        l2_leaf_reg=3.0, score="L2", leaf_method="Gradient",
+                                        bootstrap_type="No", boost_from_average=False)
+            t.append(time.perf_counter())
+            try:
+                splits, leaves = tr.fit(30)
+                approx = tr.approx()[0, :1024] if check else None
+            finally:
+                tr.close()
+            t.append(time.perf_counter())
+            sf = np.concatenate([sp[:, 0] for sp in splits]).astype(np.uint32)
+            sb = np.array([borders[f][b] for sp in splits for f, b in sp], np.float64)
+            so = np.arange(0, 6 * len(splits) + 1, 6, dtype=np.uint32)
+            lv = np.concatenate([lvs[0] for lvs in leaves]).astype(np.float64)
+            lo = np.arange(0, 64 * len(splits) + 1, 64, dtype=np.uint32)
+            pred = cb.apply_oblivious(cols[:, :1024], sf, sb, so, lv, lo)
+            t.append(time.perf_counter())
+            if check and not np.allclose(pred[0], approx, rtol=1e-12, atol=1e-12):
+                raise RuntimeError(f"{loss} {n}: predictions differ from the training approximant")
+            return t[-1] - t[0], [t[i + 1] - t[i] for i in range(5)]
+
+        fit_once(check=True)
+        runs = [fit_once() for _ in range(3)]
+        order = sorted(range(3), key=lambda i: runs[i][0])
+        med = runs[order[1]]
+        cells.append({"cell": f"SymmetricTree|{loss}|unw|noctr|{n // 1000}k", "rows": n, "features": 50,
+                      "fit_s": round(med[0], 4), "fit_s_all": [round(r[0], 4) for r in runs],
+                      "stages_s": dict(zip(("columns", "borders", "open", "trees", "predict"),
+                                           (round(v, 4) for v in med[1]))),
+                      "reference_catboost_rs_p100_s": ref_s, "official_catboost_gpu_p100_s": off_s,
+                      "speedup_vs_reference_p100": round(ref_s / med[0], 2)})
+        log(f"published cell {cells[-1]['cell']}: {med[0]:.3f} s per fit "
+            f"(reference on a P100: {ref_s} s; stages {cells[-1]['stages_s']})")
+    return cells
 
 
 if __name__ == "__main__":

@@ -127,7 +127,8 @@ EXPORTS = ["cbh_session_begin", "cbh_session_begin_u8", "cbh_session_grow",
            "cbh_version", "cbh_last_error", "cbt_open", "cbt_open_raw", "cbt_set_pairs", "cbt_step",
            "cbt_read_approx", "cbt_stats", "cbt_reset_stats", "cbt_bias", "cbt_close", "cbh_session_set_profile",
            "cbt_set_profile", "cbh_session_set_ctr", "cbt_set_ctr", "cbh_session_read_ctr_bins",
-           "cbt_open_ctr", "cbh_hist_build_noalloc", "cbh_session_capture_hists", "cbh_session_level_hist"]
+           "cbt_open_ctr", "cbh_hist_build_noalloc", "cbh_session_capture_hists", "cbh_session_level_hist",
+           "cbh_columns_from_rows"]
 
 _lib = None
 
@@ -165,6 +166,7 @@ def load(path: str = LIB_PATH):
     L.cbh_session_begin_raw.argtypes = [C.POINTER(Config), P, P, P, P, C.c_uint64, C.c_uint32, C.c_uint32,
                                         C.c_double, C.c_double, C.POINTER(P)]
     L.cbh_select_borders.argtypes = [P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_int32, C.c_int32, P, P]
+    L.cbh_columns_from_rows.argtypes = [P, C.c_uint64, C.c_uint32, P]
     L.cbh_quantize.argtypes = [P, C.c_uint64, P, C.c_uint32, P]
     L.cbh_perfect_hash.argtypes = [P, C.c_uint64, P, P]
     L.cbh_shuffled_indices.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32, P]
@@ -287,6 +289,18 @@ def _border_ptrs(borders):
         ptrs[f] = b.ctypes.data if b.size else None
     nb = np.array([b.size for b in bs], np.uint32)
     return bs, ptrs, nb
+
+
+def columns_from_rows(rows):
+    """Per-feature f32 columns [F][n] of a row-major (n, F) matrix (``cbh_columns_from_rows``,
+    a threaded host copy)."""
+    x = np.ascontiguousarray(rows, np.float32)
+    if x.ndim != 2:
+        raise ValueError("rows must be an (n_rows, n_features) matrix")
+    n, F = x.shape
+    out = np.empty((F, n), np.float32)
+    _check(load().cbh_columns_from_rows(_ptr(x), n, F, _ptr(out)))
+    return out
 
 
 def select_borders(columns, border_count=254, nan_mode="Min", border_type="GreedyLogSum"):

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <queue>
@@ -171,6 +172,17 @@ int cbh_internal_quantize(const float* d_col, uint64_t n, const double* d_border
     return CBH_OK;
 }
 
+// Host worker threads: the hardware's, at most 16 (the CPU share a GPU of a shared host gets)
+// and at most OMP_NUM_THREADS when the environment sets it.
+static unsigned host_threads() {
+    unsigned t = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    if (const char* e = std::getenv("OMP_NUM_THREADS")) {
+        const long v = std::strtol(e, nullptr, 10);
+        if (v >= 1 && (unsigned long)v < t) t = (unsigned)v;
+    }
+    return t;
+}
+
 extern "C" {
 
 int cbh_quantize(const float* column, uint64_t n, const double* borders, uint32_t n_borders, uint8_t* bins_out) {
@@ -220,8 +232,12 @@ int cbh_select_borders(const float* const* columns, uint64_t n, uint32_t n_featu
             const uint64_t off = cbh::rng_uniform(r, n - i);
             std::swap(idx[i], idx[i + off]);
         }
-        sample.assign(idx.begin(), idx.begin() + kMaxSubsetForBorders);
-        std::sort(sample.begin(), sample.end());
+        // the subset in ascending order: a bitmap of the drawn rows, read back in order
+        std::vector<uint64_t> bits((n + 63) / 64, 0);
+        for (uint64_t i = 0; i < kMaxSubsetForBorders; ++i) bits[idx[i] >> 6] |= 1ull << (idx[i] & 63);
+        sample.reserve(kMaxSubsetForBorders);
+        for (uint64_t w = 0; w < bits.size(); ++w)
+            for (uint64_t b = bits[w]; b; b &= b - 1) sample.push_back((uint32_t)(w * 64 + __builtin_ctzll(b)));
     }
     const uint64_t S = sampled ? kMaxSubsetForBorders : n;
     if (S == 0 || (uint64_t)F * S >= (1ull << 31)) {
@@ -232,7 +248,7 @@ int cbh_select_borders(const float* const* columns, uint64_t n, uint32_t n_featu
         return cbh_internal_fail(CBH_ERR_UNSUPPORTED, "n_features x sample rows exceeds 2^31 values");
     }
     // gather the subset and find the NaN-bearing columns (over every row), a worker per column
-    const unsigned nt = std::max(1u, std::min<unsigned>(std::thread::hardware_concurrency(), F));
+    const unsigned nt = std::max(1u, std::min<unsigned>(host_threads(), F));
     std::vector<float> vals((size_t)F * S);
     std::vector<uint8_t> has_nan(F, 0);
     {

@@ -7,9 +7,11 @@
 // device path does not run (crates/cb-train/src/device_draw_replay.rs).
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/cbhip.h"
@@ -300,3 +302,35 @@ double cbt_bias(const cbt_trainer* t) { return t ? t->bias : 0.0; }
 void cbt_close(cbt_trainer* t) { delete t; }
 
 }  // extern "C"
+
+// Row-major f32 matrix -> per-feature columns (ingest_py.rs:157-203): threads over disjoint
+// runs of rows; a block of 64 rows (64 * n_features floats, read once) is scattered to each
+// column as one run of 64 consecutive floats.
+int cbh_columns_from_rows(const float* rows, uint64_t n, uint32_t n_features, float* columns) {
+    if (!rows || !columns) return cbh_internal_fail(CBH_ERR_INVALID_ARG, "rows and columns are required");
+    if (n == 0 || n_features == 0) return CBH_OK;
+    uint32_t hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    if (const char* e = std::getenv("OMP_NUM_THREADS")) {   // the host's CPU share, when set
+        const long v = std::strtol(e, nullptr, 10);
+        if (v >= 1 && (unsigned long)v < hw) hw = (uint32_t)v;
+    }
+    const uint64_t T = std::min<uint64_t>(hw, (n + 65535) / 65536);
+    auto run = [&](uint64_t r0, uint64_t r1) {
+        constexpr uint64_t kBlock = 64;
+        for (uint64_t b = r0; b < r1; b += kBlock) {
+            const uint64_t e = std::min(r1, b + kBlock);
+            for (uint32_t f = 0; f < n_features; ++f) {
+                float* dst = columns + (size_t)f * n;
+                for (uint64_t r = b; r < e; ++r) dst[r] = rows[r * n_features + f];
+            }
+        }
+    };
+    if (T <= 1) {
+        run(0, n);
+        return CBH_OK;
+    }
+    std::vector<std::thread> pool;
+    for (uint64_t t = 0; t < T; ++t) pool.emplace_back(run, n * t / T, n * (t + 1) / T);
+    for (std::thread& th : pool) th.join();
+    return CBH_OK;
+}

@@ -283,3 +283,22 @@ def random_case(seed, n, F, max_borders=16, K=1, zero_weight_frac=0.0):
     if zero_weight_frac:
         w[g.random(n) < zero_weight_frac] = 0.0
     return bins, nb, y, w
+
+
+def reference_speed_cell(n_rows, n_features=50, classification=False, seed=42):
+    """A cell of the reference's published GPU speed grid (bench/full_param_gpu_speed/
+    bench.py:51-62,460-470 over bench/generator.py:106-138): row-major f32 X (n_rows,
+    n_features) of standard normals, the regression target X @ w + 0.1 N(0, 1), or for
+    classification {0, 1} drawn through a logistic link of X @ w' (w, w' standard normal).
+    The recipe is the reference's; the values come from numpy's seeded Generator, not its
+    RandomState stream (a speed workload, not a fixture)."""
+    g = np.random.default_rng(seed)
+    X = g.standard_normal((n_rows, n_features), dtype=np.float32)
+    if classification:
+        w = g.standard_normal(n_features)
+        p = 1.0 / (1.0 + np.exp(-(X.astype(np.float64) @ w)))
+        y = (g.random(n_rows) < p).astype(np.float64)
+    else:
+        w = g.standard_normal(n_features).astype(np.float32)
+        y = (X @ w + 0.1 * g.standard_normal(n_rows, dtype=np.float32)).astype(np.float64)
+    return X, y

@@ -393,6 +393,14 @@ int cbh_apply_oblivious(const float* features_fm, uint64_t n_objects, uint32_t n
                         const uint32_t* tree_leaf_offsets, uint32_t n_trees, uint32_t approx_dim,
                         const double* bias, const uint8_t* nan_as_true, double* out);
 
+/* The float columns of a C-contiguous row-major matrix, as the reference's ingest of an
+ * (n_rows, n_features) f32 array builds them (crates/catboost-rs-py/src/ingest_py.rs:157-203):
+ *   rows     [n][n_features] f32, row-major
+ *   columns  [n_features][n] f32 out, feature f's column at columns + f * n
+ * A host copy in blocks of rows, over the host's threads (at most 16; the same values in
+ * the same order whatever the split).  CBH_ERR_INVALID_ARG on a null pointer. */
+int cbh_columns_from_rows(const float* rows, uint64_t n, uint32_t n_features, float* columns);
+
 /* Greedy border selection of float columns; mirrors Pool::quantize's border step
  * (crates/cb-data/src/quantize.rs:74-110) over select_borders_greedy_logsum_f32 and its
  * GreedyMinEntropy twin (crates/cb-data/src/borders.rs:298-420):

@@ -137,6 +137,18 @@ def test_float_preparation_argument_checks(lib):
     assert e.value.code == -2  # n_borders + 1 > n_bins
 
 
+@pytest.mark.parametrize("n,F", [(1, 1), (63, 3), (1000, 50), (131_073, 17), (300_001, 50)])
+def test_columns_from_rows_is_the_transpose(lib, n, F):
+    """The row-major ingest (host code, no device) gives every column of the matrix, bit for
+    bit: single- and multi-threaded splits, runs of rows not a multiple of the 64-row block."""
+    import numpy as np
+    x = np.random.default_rng(n + F).standard_normal((n, F)).astype(np.float32)
+    x[::7, F // 2] = np.nan
+    got = cb.columns_from_rows(x)
+    assert got.shape == (F, n)
+    assert np.array_equal(got.view(np.uint32), np.ascontiguousarray(x.T).view(np.uint32))
+
+
 def test_categorical_argument_checks(lib):
     """CTR columns validate the permutation, bucket range and classes before any device call."""
     import numpy as np
