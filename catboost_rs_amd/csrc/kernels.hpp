@@ -1179,8 +1179,9 @@ static __global__ __launch_bounds__(kPackThreads) void fill_packed_kernel(
 //
 // Rows: the dense level streams each tile's tile-major slice, the gathered levels read the
 // row-major words through the partition's index list (all tiles of a range on one XCD: a listed
-// row's lines come from HBM once); statistics in position order ([n][2], or the listed rows'
-// copy in idx order written by the compaction).
+// row's lines come from HBM once); statistics in position order ([n][2] f64, or the listed
+// rows' copy in idx order written by the compaction), rounded onto the tree's fixed-point
+// scales as a block's set is consumed (to_fixed, the score channels' rounding everywhere).
 // ---------------------------------------------------------------------------------
 constexpr uint32_t kExThreads = 1024;           // 16 waves, one workgroup per CU
 constexpr uint32_t kExTileWords = 8;

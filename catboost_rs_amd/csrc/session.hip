@@ -124,7 +124,7 @@ struct cbh_session {
     double* weight = nullptr;
     double* target = nullptr;
     double* approx = nullptr;
-    double* sstat = nullptr;
+    double* sstat = nullptr;         // [n][C] score channels (f64; int64 in place for the generic fill)
     double* host_sample = nullptr;
     uint16_t* leaf = nullptr;
     uint32_t* idx = nullptr;
@@ -221,7 +221,7 @@ struct cbh_session {
                                      // from the cache (its level-0 fill one plane short)
     int pack_bits = 0;
     unsigned long long* spack = nullptr;   // packed: [n] words
-    unsigned long long* sseq = nullptr;    // the listed rows' statistics in idx order (packed: [V]; tiled: [V][2])
+    unsigned long long* sseq = nullptr;    // the listed rows' statistics in idx order (packed: [V]; tiled: [V][2] f64)
     uint32_t* trows = nullptr;             // tiled fills: tile-major row words (pack_tiles_kernel)
     uint32_t pk_tiles = 0, pk_ranges = 8, pk_swap = 1;
     struct PackPlan {                          // tiled fill launch: tiles of the full loop, ranges
