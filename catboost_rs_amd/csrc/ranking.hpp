@@ -278,9 +278,12 @@ static __global__ __launch_bounds__(256) void pair_multi_scan_kernel(const uint3
         if (b0 + i < b1) p[(size_t)(b0 + i) * 2] = v[i] + off;
 }
 
-// Accumulate one chunk of one key's pairs for one tile of 16 features (grid: (max descriptors,
-// feature tiles)).  Records come grouped by key (rec: winner, loser | winner-in-leaf-a << 31),
-// or, at a level of one leaf, straight from the pair arrays (direct).  For a pair with winner
+// Accumulate one chunk of one key's pairs for one tile of 16 features.  Grid: 8 * tiles *
+// ceil(max descriptors / 8) workgroups; workgroup g runs descriptor 8 (q / tiles) + g mod 8 and
+// tile q mod tiles (q = g / 8), so the tiles of a descriptor share an XCD (workgroups go to the 8
+// XCDs round-robin) and start together: the pairs' rows they all gather come from HBM into that
+// XCD's L2 once rather than once per tile.  Records come grouped by key (rec: winner, loser |
+// winner-in-leaf-a << 31), or, at a level of one leaf, straight from the pair arrays (direct).  For a pair with winner
 // bucket > loser bucket the cells [loserLeaf][winnerLeaf] receive -w at (loser bucket, smaller)
 // and (winner bucket, greater), otherwise [winnerLeaf][loserLeaf] at (winner bucket, smaller)
 // and (loser bucket, greater) (compute_pair_weight_statistics, pairwise_scoring.rs:163-196);
@@ -290,13 +293,14 @@ static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel
     const uint32_t* __restrict__ rows, uint32_t Ws, const uint4* __restrict__ desc, const uint32_t* __restrict__ n_desc,
     const uint2* __restrict__ rec, const long long* __restrict__ rec_wq, const uint32_t* __restrict__ comp_win,
     const uint32_t* __restrict__ comp_los, const long long* __restrict__ comp_wq, int direct, uint32_t F, uint32_t P,
-    uint32_t B, long long* __restrict__ st) {
+    uint32_t B, long long* __restrict__ st, uint32_t tiles) {
     extern __shared__ unsigned long long cells[];   // [B][channel][block][16]
-    if (blockIdx.x >= *n_desc) return;
-    const uint4 ds = desc[blockIdx.x];
+    const uint32_t qg = blockIdx.x >> 3, tile = qg % tiles, di = (qg / tiles) * 8u + (blockIdx.x & 7u);
+    if (di >= *n_desc) return;   // workgroup-uniform, before any barrier
+    const uint4 ds = desc[di];
     const uint32_t key = ds.x, a = key / P, b = key % P;
     const uint32_t t = threadIdx.x, fl = t & 15;
-    const uint32_t f = blockIdx.y * kStatTileF + fl;
+    const uint32_t f = tile * kStatTileF + fl;
     const bool fok = f < F;
     const uint32_t word = (fok ? f : F - 1) >> 2, sh = (f & 3u) * 8u;
     for (uint32_t i = t; i < B * 64; i += kStatThreads) cells[i] = 0;
@@ -391,7 +395,7 @@ static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel
         // takes run t & 63 (= channel, block, feature: consecutive lanes read consecutive cells)
         // and the 16 buckets of segment t >> 6; the segment totals give each segment its offset.
         __shared__ unsigned long long seg_tot[16][64];
-        const uint32_t run = t & 63u, seg = t >> 6, c = run >> 5, blk = (run >> 4) & 1u, rf = blockIdx.y * kStatTileF + (run & 15u);
+        const uint32_t run = t & 63u, seg = t >> 6, c = run >> 5, blk = (run >> 4) & 1u, rf = tile * kStatTileF + (run & 15u);
         unsigned long long v[16];
         unsigned long long acc = 0;
 #pragma unroll
@@ -418,7 +422,7 @@ static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel
         // takes the prefix)
         for (uint32_t i = t; i < B * 64; i += kStatThreads) {
             const long long v = (long long)cells[i];
-            const uint32_t l = i & 63u, c = l >> 5, blk = (l >> 4) & 1u, ff = blockIdx.y * kStatTileF + (l & 15u);
+            const uint32_t l = i & 63u, c = l >> 5, blk = (l >> 4) & 1u, ff = tile * kStatTileF + (l & 15u);
             if (v == 0 || ff >= F || (blk == 1 && a == b)) continue;
             const uint32_t x = blk == 0 ? a : b, y = blk == 0 ? b : a;
             atomicAdd((unsigned long long*)(st + ((((size_t)ff * P + x) * P + y) * B + (i >> 6)) * 2 + c),

@@ -1385,9 +1385,9 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     }
     const bool buf = (uint64_t)s->n * s->Ws * 4 < (1ull << 32);
     (buf ? pair_stats_feature_kernel<true> : pair_stats_feature_kernel<false>)
-        <<<dim3(max_desc, tiles), kStatThreads, (size_t)B * 64 * sizeof(long long), st>>>(
+        <<<8u * tiles * ((max_desc + 7) / 8), kStatThreads, (size_t)B * 64 * sizeof(long long), st>>>(
             s->rows, s->Ws, s->pair_desc, s->pair_nd, s->key_rec, s->key_wq, s->comp_win, s->comp_los, s->comp_wq,
-            direct ? 1 : 0, F, P, B, s->pair_st);
+            direct ? 1 : 0, F, P, B, s->pair_st, tiles);
     HIP_TRY(hipGetLastError());
     if (max_multi) {
         pair_multi_scan_kernel<<<dim3(max_multi, F), 256, 0, st>>>(s->pair_mk, s->pair_nd + 1, P, B, s->pair_st);
