@@ -288,7 +288,7 @@ static __global__ __launch_bounds__(256) void pair_multi_scan_kernel(const uint3
 // and (winner bucket, greater), otherwise [winnerLeaf][loserLeaf] at (winner bucket, smaller)
 // and (loser bucket, greater) (compute_pair_weight_statistics, pairwise_scoring.rs:163-196);
 // block 0 of a key {a <= b} is [a][b], block 1 is [b][a].
-template <bool kBuf>   // row words by 32-bit buffer offsets (the row buffer is under 4 GiB)
+template <bool kBuf>   // row words by 32-bit buffer offsets (row buffer under 4 GiB, rows < 2^24)
 static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel(
     const uint32_t* __restrict__ rows, uint32_t Ws, const uint4* __restrict__ desc, const uint32_t* __restrict__ n_desc,
     const uint2* __restrict__ rec, const long long* __restrict__ rec_wq, const uint32_t* __restrict__ comp_win,
@@ -302,7 +302,9 @@ static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel
     const uint32_t t = threadIdx.x, fl = t & 15;
     const uint32_t f = tile * kStatTileF + fl;
     const bool fok = f < F;
-    const uint32_t word = (fok ? f : F - 1) >> 2, sh = (f & 3u) * 8u;
+    // a lane past the last feature reads feature F - 1's bins (< B) into its own cells, which
+    // are never flushed
+    const uint32_t word = (fok ? f : F - 1) >> 2, sh = ((fok ? f : F - 1) & 3u) * 8u;
     for (uint32_t i = t; i < B * 64; i += kStatThreads) cells[i] = 0;
     __syncthreads();
     // each 16-lane row takes 16 consecutive pairs per pass: lane fl loads the record of pair
@@ -310,23 +312,31 @@ static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel
     // row's lanes by row_newbcast, and the 32 row words of the 16 pairs are loaded together
     const uint32_t first = ds.y, cnt = ds.z;
     constexpr uint32_t kRows = kStatThreads / 16, kPass = kRows * 16;
+    // A pair past the chunk or with winner == loser adds nothing: its weight is zeroed here and
+    // its two atomics add 0 (no per-pair branch).  The weight is kept negated.
     auto load_rec = [&](uint32_t j, uint32_t& wi, uint32_t& lo, uint32_t& wa, long long& wq) {
         const bool ok = j < cnt;
         const size_t k = (size_t)first + (ok ? j : 0u);
+        long long q;
         if (direct) {
-            wi = ok ? comp_win[k] : 0u;
-            lo = ok ? comp_los[k] : 0u;
+            wi = comp_win[k];
+            lo = comp_los[k];
             wa = 0;
-            wq = ok ? comp_wq[k] : 0;
+            q = comp_wq[k];
         } else {
-            const uint2 r = ok ? rec[k] : make_uint2(0u, 0u);
+            const uint2 r = rec[k];
             wi = r.x;
             lo = r.y & 0x7FFFFFFFu;
             wa = r.y >> 31;
-            wq = ok ? rec_wq[k] : 0;
+            q = rec_wq[k];
         }
+        wq = ok && wi != lo ? -q : 0;
     };
     const uint32_t row = t >> 4;
+    // cell (bucket, channel, block, lane) at byte 512 bucket + 256 channel + 128 block + 8 lane
+    char* const cl0 = (char*)cells + fl * 8u;                    // block 0 of lane fl
+    char* const cl1 = cl0 + (a == b ? 0u : 128u);               // block 1 (a == b: block 0)
+    const uint32_t Ws4 = Ws * 4u, word4 = word * 4u;
     uint32_t n_wi, n_lo, n_wa;
     long long n_wq;
     load_rec(row * 16 + fl, n_wi, n_lo, n_wa, n_wq);
@@ -334,54 +344,34 @@ static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel
         const uint32_t c_wi = n_wi, c_lo = n_lo, c_wa = n_wa;
         const long long c_wq = n_wq;
         load_rec(base + kPass + fl, n_wi, n_lo, n_wa, n_wq);   // the next pass's records
-        uint32_t wi[16], lo[16], ww[16], lw[16];
-        wi[0] = row_bcast<0>(c_wi); lo[0] = row_bcast<0>(c_lo);
-        wi[1] = row_bcast<1>(c_wi); lo[1] = row_bcast<1>(c_lo);
-        wi[2] = row_bcast<2>(c_wi); lo[2] = row_bcast<2>(c_lo);
-        wi[3] = row_bcast<3>(c_wi); lo[3] = row_bcast<3>(c_lo);
-        wi[4] = row_bcast<4>(c_wi); lo[4] = row_bcast<4>(c_lo);
-        wi[5] = row_bcast<5>(c_wi); lo[5] = row_bcast<5>(c_lo);
-        wi[6] = row_bcast<6>(c_wi); lo[6] = row_bcast<6>(c_lo);
-        wi[7] = row_bcast<7>(c_wi); lo[7] = row_bcast<7>(c_lo);
-        wi[8] = row_bcast<8>(c_wi); lo[8] = row_bcast<8>(c_lo);
-        wi[9] = row_bcast<9>(c_wi); lo[9] = row_bcast<9>(c_lo);
-        wi[10] = row_bcast<10>(c_wi); lo[10] = row_bcast<10>(c_lo);
-        wi[11] = row_bcast<11>(c_wi); lo[11] = row_bcast<11>(c_lo);
-        wi[12] = row_bcast<12>(c_wi); lo[12] = row_bcast<12>(c_lo);
-        wi[13] = row_bcast<13>(c_wi); lo[13] = row_bcast<13>(c_lo);
-        wi[14] = row_bcast<14>(c_wi); lo[14] = row_bcast<14>(c_lo);
-        wi[15] = row_bcast<15>(c_wi); lo[15] = row_bcast<15>(c_lo);
-        if constexpr (kBuf) {
-            const __amdgpu_buffer_rsrc_t rr = make_rsrc(rows, 0xFFFFFFFFull);
-#pragma unroll
-            for (uint32_t u = 0; u < 16; ++u) {
-                ww[u] = ldw(rr, (wi[u] * Ws + word) * 4u);
-                lw[u] = ldw(rr, (lo[u] * Ws + word) * 4u);
-            }
-        } else {
-#pragma unroll
-            for (uint32_t u = 0; u < 16; ++u) {
-                ww[u] = rows[(size_t)wi[u] * Ws + word];
-                lw[u] = rows[(size_t)lo[u] * Ws + word];
-            }
-        }
-        // pairs of this pass that add nothing: past the chunk, or winner == loser
-        uint32_t skip = 0;
-#pragma unroll
-        for (uint32_t u = 0; u < 16; ++u) skip |= (base + u >= cnt || wi[u] == lo[u] ? 1u : 0u) << u;
-        if (!fok) skip = 0xFFFFu;
-        // (the broadcasts run in every lane: a lane switched off by the branch would read as 0)
+        uint32_t ww[16], lw[16];
+#define CBH_STAT_GATHER(U)                                                                                   \
+    {                                                                                                         \
+        const uint32_t wiu = row_bcast<U>(c_wi), lou = row_bcast<U>(c_lo);                                   \
+        if constexpr (kBuf) {   /* rows < 2^24 and 4 Ws < 2^24: one 24-bit multiply-add per offset */        \
+            const __amdgpu_buffer_rsrc_t rr = make_rsrc(rows, 0xFFFFFFFFull);                                 \
+            ww[U] = ldw(rr, __umul24(wiu, Ws4) + word4);                                                      \
+            lw[U] = ldw(rr, __umul24(lou, Ws4) + word4);                                                      \
+        } else {                                                                                              \
+            ww[U] = rows[(size_t)wiu * Ws + word];                                                            \
+            lw[U] = rows[(size_t)lou * Ws + word];                                                            \
+        }                                                                                                     \
+    }
+        CBH_STAT_GATHER(0) CBH_STAT_GATHER(1) CBH_STAT_GATHER(2) CBH_STAT_GATHER(3)
+        CBH_STAT_GATHER(4) CBH_STAT_GATHER(5) CBH_STAT_GATHER(6) CBH_STAT_GATHER(7)
+        CBH_STAT_GATHER(8) CBH_STAT_GATHER(9) CBH_STAT_GATHER(10) CBH_STAT_GATHER(11)
+        CBH_STAT_GATHER(12) CBH_STAT_GATHER(13) CBH_STAT_GATHER(14) CBH_STAT_GATHER(15)
+#undef CBH_STAT_GATHER
+        // block 1 when (winner bucket > loser bucket) == winner-in-leaf-a, block 0 when a == b
 #define CBH_STAT_PAIR(U)                                                                                     \
     {                                                                                                         \
-    const uint32_t wau = row_bcast<U>(c_wa);                                                                  \
-    const unsigned long long neg = (unsigned long long)(-(long long)row_bcast64<U>((unsigned long long)c_wq));   \
-    if (!((skip >> U) & 1u)) {                                                                                \
+        const uint32_t wau = row_bcast<U>(c_wa);                                                              \
+        const unsigned long long neg = row_bcast64<U>((unsigned long long)c_wq);                              \
         const uint32_t wb = (ww[U] >> sh) & 0xFFu, lb = (lw[U] >> sh) & 0xFFu;                                \
-        const uint32_t blk = a == b ? 0u : ((wb > lb) == (wau != 0) ? 1u : 0u);                               \
+        char* const cl = (wb > lb) == (wau != 0) ? cl1 : cl0;                                                 \
         const uint32_t bs = wb > lb ? lb : wb, bg = wb > lb ? wb : lb;                                        \
-        atomicAdd(cells + ((size_t)(bs * 2 + 0) * 2 + blk) * 16 + fl, neg);                                   \
-        atomicAdd(cells + ((size_t)(bg * 2 + 1) * 2 + blk) * 16 + fl, neg);                                   \
-    }                                                                                                         \
+        atomicAdd((unsigned long long*)(cl + (bs << 9)), neg);                                                \
+        atomicAdd((unsigned long long*)(cl + (bg << 9) + 256u), neg);                                         \
     }
         CBH_STAT_PAIR(0) CBH_STAT_PAIR(1) CBH_STAT_PAIR(2) CBH_STAT_PAIR(3)
         CBH_STAT_PAIR(4) CBH_STAT_PAIR(5) CBH_STAT_PAIR(6) CBH_STAT_PAIR(7)
@@ -809,6 +799,51 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_lane_kernel(
     scores[(size_t)f * B + s] = outer;
 }
 
+// The m x m SPD system of one wavefront, row r in lane r's registers (entries above the
+// diagonal are don't-care) and the right-hand side y in lane r: right-looking Cholesky (the
+// pivot and the pivot column come from the owning lanes by readlane; every element receives
+// its pivot subtractions in ascending order with the reference's roundings, as
+// pairwise_factor_solve_block), the forward substitution p ascending, then the back
+// substitution reading L^T from Lbuf (m (m + 1) / 2 doubles of LDS).  Returns the lane's
+// component of the solution: 0 past m, and 0 everywhere when a pivot is not positive.
+template <int m>
+__device__ __forceinline__ double pairwise_rows_solve(double (&row)[m], double y, double* __restrict__ Lbuf,
+                                                      int lane) {
+    bool good = true;
+#pragma unroll
+    for (int j = 0; j < m; ++j) {
+        const double d = readlane_f64(row[j], j);
+        if (d <= 0.0) {
+            good = false;
+            break;
+        }
+        const double ljj = sqrt(d);
+        row[j] = lane == j ? ljj : row[j] / ljj;
+#pragma unroll
+        for (int k = j + 1; k < m; ++k) row[k] = row[k] - row[j] * readlane_f64(row[j], k);
+    }
+    if (good) {
+#pragma unroll
+        for (int p = 0; p < m; ++p) {   // forward: y[i] -= L[i][p] y[p], p ascending
+            const double yp = readlane_f64(y, p) / readlane_f64(row[p], p);
+            y = lane == p ? yp : (lane > p ? y - row[p] * yp : y);
+        }
+        if (lane < m) {
+#pragma unroll
+            for (int c = 0; c < m; ++c)
+                if (c <= lane) Lbuf[tri(lane, c)] = row[c];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = m - 1; p >= 0; --p) {   // back: L^T x = y
+            const double xp = readlane_f64(y, p) / readlane_f64(row[p], p);
+            const double lpi = lane < p ? Lbuf[tri(p, lane)] : 0.0;
+            y = lane == p ? xp : (lane < p ? y - lpi * xp : y);
+        }
+    }
+    return good && lane < m ? y : 0.0;
+}
+
 // One wavefront per (border s, feature f) at a level of P_ leaves: the weight matrix of border
 // s from the cumulative pair statistics (calculate_pairwise_score's leaf system,
 // pairwise_scoring.rs:471-581), the prior terms, the 2P-1 Cholesky solve, MakeZeroAverage and
@@ -890,40 +925,7 @@ static __global__ __launch_bounds__(64) void pairwise_candidate_kernel(
         const double den = readlane_f64(row[0], 0);
         x = lane == 0 && den != 0.0 ? der[0] / den : 0.0;
     } else {
-        bool good = true;
-#pragma unroll
-        for (int j = 0; j < m; ++j) {
-            const double d = readlane_f64(row[j], j);
-            if (d <= 0.0) {
-                good = false;
-                break;
-            }
-            const double ljj = sqrt(d);
-            row[j] = lane == j ? ljj : row[j] / ljj;
-#pragma unroll
-            for (int k = j + 1; k < m; ++k) row[k] = row[k] - row[j] * readlane_f64(row[j], k);
-        }
-        double y = lane < m ? der[lane] : 0.0;
-        if (good) {
-#pragma unroll
-            for (int p = 0; p < m; ++p) {   // forward: y[i] -= L[i][p] y[p], p ascending
-                const double yp = readlane_f64(y, p) / readlane_f64(row[p], p);
-                y = lane == p ? yp : (lane > p ? y - row[p] * yp : y);
-            }
-            if (lane < m) {
-#pragma unroll
-                for (int c = 0; c < m; ++c)
-                    if (c <= lane) M[tri(lane, c)] = row[c];
-            }
-            __syncthreads();
-#pragma unroll
-            for (int p = m - 1; p >= 0; --p) {   // back: L^T x = y
-                const double xp = readlane_f64(y, p) / readlane_f64(row[p], p);
-                const double lpi = lane < p ? M[tri(p, lane)] : 0.0;
-                y = lane == p ? xp : (lane < p ? y - lpi * xp : y);
-            }
-        }
-        x = good && lane < m ? y : 0.0;
+        x = pairwise_rows_solve<m>(row, lane < m ? der[lane] : 0.0, M, lane);
     }
     if (lane < n) res[lane] = x;
     __syncthreads();
@@ -1088,6 +1090,48 @@ static __global__ __launch_bounds__(256) void pairwise_leaf_kernel(
     for (uint32_t l = threadIdx.x; l < L; l += blockDim.x) raw[l] = res[l];
     __syncthreads();
     if (threadIdx.x == 0) pairwise_center_lane0(raw, sums, CL, L, lr, scaled);
+}
+
+// PairLogitPairwise leaves of 3 to 64 leaves in one wavefront (the arithmetic of
+// pairwise_leaf_kernel, whose steps here need no barrier): lane r < L - 1 holds row r of
+// M = W + prior terms in registers, lanes L - 1 .. 62 rows of the identity, so that the
+// 63 x 63 system factors as blockdiag(M, I) with M's elements getting exactly their own
+// operations (the identity rows contribute 0 * x terms and unit pivots).  LDS: the L^T buffer
+// (2016 doubles) and the L doubles of the solution.
+constexpr uint32_t kPairLeafWaveDoubles = 63 * 64 / 2 + 64;
+static __global__ __launch_bounds__(64) void pairwise_leaf_wave_kernel(
+    const long long* __restrict__ lw, uint32_t L, const long long* __restrict__ sums, uint32_t CL,
+    const Scales* __restrict__ sc, double pair_inv, double l2, double prior, double lr,
+    double* __restrict__ raw, double* __restrict__ scaled) {
+    constexpr int m = 63;
+    __shared__ double Lbuf[kPairLeafWaveDoubles];
+    double* res = Lbuf + 63 * 64 / 2;
+    const int lane = threadIdx.x, mm = (int)L - 1;
+    const double cell_prior = 1.0 / (double)L;
+    const double non_diag = -prior * cell_prior;
+    const double diag = prior * (1.0 - cell_prior) + l2;
+    const double inv_d = sc->inv[kLeafDer];
+    double row[m];
+#pragma unroll
+    for (int c = 0; c < m; ++c) {
+        double v;
+        if (lane < mm) {
+            const double wrc = c <= lane ? (double)lw[(size_t)lane * L + c] * pair_inv : 0.0;
+            v = c < lane ? wrc + non_diag : (c == lane ? wrc + diag : 0.0);
+        } else {
+            v = c == lane ? 1.0 : 0.0;
+        }
+        row[c] = v;
+    }
+    const double y = lane < mm ? (double)sums[(size_t)lane * CL] * inv_d : 0.0;
+    const double x = pairwise_rows_solve<m>(row, y, Lbuf, lane);
+    __syncthreads();
+    if (lane < (int)L) res[lane] = lane < mm ? x : 0.0;
+    __syncthreads();
+    zero_average_block(res, (int)L);
+    if (lane < (int)L) raw[lane] = res[lane];
+    __syncthreads();
+    if (lane == 0) pairwise_center_lane0(raw, sums, CL, L, lr, scaled);
 }
 
 // Doubles of one candidate solve of the workgroup kernel at a level of P leaves (n = 2P

@@ -1383,7 +1383,8 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
         pair_multi_zero_kernel<<<dim3(max_multi, F), 256, 0, st>>>(s->pair_mk, s->pair_nd + 1, P, B, s->pair_st);
         HIP_TRY(hipGetLastError());
     }
-    const bool buf = (uint64_t)s->n * s->Ws * 4 < (1ull << 32);
+    // 32-bit buffer offsets formed by one 24-bit multiply-add (row < 2^24, 4 Ws < 2^24)
+    const bool buf = (uint64_t)s->n * s->Ws * 4 < (1ull << 32) && s->n < (1u << 24) && s->Ws < (1u << 22);
     (buf ? pair_stats_feature_kernel<true> : pair_stats_feature_kernel<false>)
         <<<8u * tiles * ((max_desc + 7) / 8), kStatThreads, (size_t)B * 64 * sizeof(long long), st>>>(
             s->rows, s->Ws, s->pair_desc, s->pair_nd, s->key_rec, s->key_wq, s->comp_win, s->comp_los, s->comp_wq,
@@ -1847,10 +1848,15 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
                 s->comp_win, s->comp_los, s->comp_wq, s->n_pairs, s->leaf, n_leaves, s->leaf_w, lw_lds ? 1 : 0);
             HIP_TRY(hipGetLastError());
         }
-        // one wavefront up to 64 leaves (the solve is a chain of short steps), else 256 threads
-        pairwise_leaf_kernel<<<1, n_leaves <= 64 ? 64 : 256, s->pair_leaf_lds, st>>>(
-            s->leaf_w, n_leaves, s->leaf_sums, CL, s->scales, s->pair_inv, s->l2, s->prior, s->lr, s->leaf_raw,
-            s->leaf_scaled, s->pair_leaf_lds ? nullptr : s->pair_ws);
+        // 4 to 64 leaves: the system in one wavefront's registers; else the workgroup solve over
+        // LDS or the workspace (the solve is a chain of short steps)
+        if (n_leaves >= 4 && n_leaves <= 64)
+            pairwise_leaf_wave_kernel<<<1, 64, 0, st>>>(s->leaf_w, n_leaves, s->leaf_sums, CL, s->scales, s->pair_inv,
+                                                        s->l2, s->prior, s->lr, s->leaf_raw, s->leaf_scaled);
+        else
+            pairwise_leaf_kernel<<<1, n_leaves <= 64 ? 64 : 256, s->pair_leaf_lds, st>>>(
+                s->leaf_w, n_leaves, s->leaf_sums, CL, s->scales, s->pair_inv, s->l2, s->prior, s->lr, s->leaf_raw,
+                s->leaf_scaled, s->pair_leaf_lds ? nullptr : s->pair_ws);
         HIP_TRY(hipGetLastError());
     } else {
         leaf_values_kernel<K><<<(n_leaves + 63) / 64, 64, 0, st>>>(s->leaf_sums, s->scales, n_leaves, newton,
