@@ -278,6 +278,14 @@ static __global__ __launch_bounds__(256) void pair_multi_scan_kernel(const uint3
         if (b0 + i < b1) p[(size_t)(b0 + i) * 2] = v[i] + off;
 }
 
+// Words of one (block, feature) row of the pair statistics' flush in LDS: 2B (bucket, channel)
+// padded to 2 mod 32, so that the 64 runs' writes of one bucket spread over the banks.
+__host__ __device__ constexpr uint32_t pair_stat_row_words(uint32_t B) { return 2 * B + (34u - (2 * B) % 32u) % 32u; }
+// LDS of pair_stats_feature_kernel: the cells [B][channel][block][16], then the flush rows.
+__host__ __device__ constexpr size_t pair_stat_lds(uint32_t B) {
+    return (B * 64 > 32 * pair_stat_row_words(B) ? B * 64 : 32 * pair_stat_row_words(B)) * sizeof(unsigned long long);
+}
+
 // Accumulate one chunk of one key's pairs for one tile of 16 features.  Grid: 8 * tiles *
 // ceil(max descriptors / 8) workgroups; workgroup g runs descriptor 8 (q / tiles) + g mod 8 and
 // tile q mod tiles (q = g / 8), so the tiles of a descriptor share an XCD (workgroups go to the 8
@@ -380,43 +388,56 @@ static __global__ __launch_bounds__(kStatThreads) void pair_stats_feature_kernel
 #undef CBH_STAT_PAIR
     }
     __syncthreads();
-    if (ds.w == 0) {
-        // the key's only chunk: its cumulative runs go straight into the statistics.  Thread t
-        // takes run t & 63 (= channel, block, feature: consecutive lanes read consecutive cells)
-        // and the 16 buckets of segment t >> 6; the segment totals give each segment its offset.
-        __shared__ unsigned long long seg_tot[16][64];
-        const uint32_t run = t & 63u, seg = t >> 6, c = run >> 5, blk = (run >> 4) & 1u, rf = tile * kStatTileF + (run & 15u);
+    // Flush.  The key's only chunk writes its cumulative runs straight into the statistics; one
+    // chunk of several adds its raw cells into the zeroed runs (pair_multi_scan_kernel takes the
+    // prefix).  Thread t takes run t & 63 (= channel, block, feature: consecutive lanes read
+    // consecutive cells) and the 16 buckets of segment t >> 6, the segment totals giving each
+    // segment its offset; the values go back to LDS as one row per (block, feature) of 2B
+    // words (bucket, channel), which each wavefront then copies out 1 KB at a time.
+    const bool single = ds.w == 0;
+    __shared__ unsigned long long seg_tot[16][64];
+    {
+        const uint32_t run = t & 63u, seg = t >> 6, c = run >> 5;
         unsigned long long v[16];
-        unsigned long long acc = 0;
 #pragma unroll
         for (uint32_t i = 0; i < 16; ++i) {
             const uint32_t bk = seg * 16 + i;
-            acc += bk < B ? cells[(size_t)bk * 64 + run] : 0ull;
-            v[i] = acc;
+            v[i] = bk < B ? cells[(size_t)bk * 64 + run] : 0ull;
         }
-        seg_tot[seg][run] = acc;
-        __syncthreads();
-        unsigned long long off = 0;
-        for (uint32_t g = 0; g < seg; ++g) off += seg_tot[g][run];
-        if (rf < F && (blk == 0 || a != b)) {
-            const uint32_t x = blk == 0 ? a : b, y = blk == 0 ? b : a;
-            long long* dst = st + (((size_t)rf * P + x) * P + y) * B * 2 + c;
+        if (single) {
 #pragma unroll
-            for (uint32_t i = 0; i < 16; ++i) {
-                const uint32_t bk = seg * 16 + i;
-                if (bk < B) dst[(size_t)bk * 2] = (long long)(v[i] + off);
-            }
+            for (uint32_t i = 1; i < 16; ++i) v[i] += v[i - 1];
+            seg_tot[seg][run] = v[15];
         }
-    } else {
-        // one chunk of several: add the raw cells (the region was zeroed; pair_multi_scan_kernel
-        // takes the prefix)
-        for (uint32_t i = t; i < B * 64; i += kStatThreads) {
-            const long long v = (long long)cells[i];
-            const uint32_t l = i & 63u, c = l >> 5, blk = (l >> 4) & 1u, ff = tile * kStatTileF + (l & 15u);
-            if (v == 0 || ff >= F || (blk == 1 && a == b)) continue;
+        __syncthreads();   // every cell read before the rows overwrite them
+        unsigned long long off = 0;
+        if (single)
+            for (uint32_t g = 0; g < seg; ++g) off += seg_tot[g][run];
+        unsigned long long* trow = cells + (size_t)(run & 31u) * pair_stat_row_words(B);
+#pragma unroll
+        for (uint32_t i = 0; i < 16; ++i) {
+            const uint32_t bk = seg * 16 + i;
+            if (bk < B) trow[bk * 2 + c] = v[i] + off;
+        }
+    }
+    __syncthreads();
+    {
+        const uint32_t w = t >> 6, lane = t & 63u;
+        for (uint32_t q = w; q < 32; q += kStatThreads / 64) {   // row q: block q >> 4, feature q & 15
+            const uint32_t blk = q >> 4, ff = tile * kStatTileF + (q & 15u);
+            if (ff >= F || (blk == 1 && a == b)) continue;   // uniform over the wavefront
             const uint32_t x = blk == 0 ? a : b, y = blk == 0 ? b : a;
-            atomicAdd((unsigned long long*)(st + ((((size_t)ff * P + x) * P + y) * B + (i >> 6)) * 2 + c),
-                      (unsigned long long)v);
+            long long* dst = st + (((size_t)ff * P + x) * P + y) * B * 2;
+            const unsigned long long* src = cells + (size_t)q * pair_stat_row_words(B);
+            for (uint32_t e = lane * 2; e < 2 * B; e += 128) {
+                const ulonglong2 v2 = *reinterpret_cast<const ulonglong2*>(src + e);
+                if (single) {
+                    *reinterpret_cast<longlong2*>(dst + e) = make_longlong2((long long)v2.x, (long long)v2.y);
+                } else {
+                    if (v2.x) atomicAdd((unsigned long long*)(dst + e), v2.x);
+                    if (v2.y) atomicAdd((unsigned long long*)(dst + e + 1), v2.y);
+                }
+            }
         }
     }
 }

@@ -466,9 +466,9 @@ int session_alloc(cbh_session* s) {
         s->pair_cus = (uint32_t)std::max(cus, 1);
         // every LDS size a level can ask for is set here, before any tree is recorded as a graph
         HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_feature_kernel<true>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)s->B * 64 * sizeof(long long))));
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)pair_stat_lds(s->B)));
         HIP_TRY(hipFuncSetAttribute((const void*)pair_stats_feature_kernel<false>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)s->B * 64 * sizeof(long long))));
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)pair_stat_lds(s->B)));
         HIP_TRY(hipFuncSetAttribute((const void*)pair_key_count_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)(pmax * pmax * sizeof(uint32_t))));
         HIP_TRY(hipFuncSetAttribute((const void*)pair_key_scatter_kernel,
@@ -1386,7 +1386,7 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     // 32-bit buffer offsets formed by one 24-bit multiply-add (row < 2^24, 4 Ws < 2^24)
     const bool buf = (uint64_t)s->n * s->Ws * 4 < (1ull << 32) && s->n < (1u << 24) && s->Ws < (1u << 22);
     (buf ? pair_stats_feature_kernel<true> : pair_stats_feature_kernel<false>)
-        <<<8u * tiles * ((max_desc + 7) / 8), kStatThreads, (size_t)B * 64 * sizeof(long long), st>>>(
+        <<<8u * tiles * ((max_desc + 7) / 8), kStatThreads, pair_stat_lds(B), st>>>(
             s->rows, s->Ws, s->pair_desc, s->pair_nd, s->key_rec, s->key_wq, s->comp_win, s->comp_los, s->comp_wq,
             direct ? 1 : 0, F, P, B, s->pair_st, tiles);
     HIP_TRY(hipGetLastError());
