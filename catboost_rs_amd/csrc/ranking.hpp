@@ -101,19 +101,33 @@ __device__ __forceinline__ uint32_t pair_key(uint32_t wl, uint32_t ll, uint32_t 
     return wl < ll ? wl * P + ll : ll * P + wl;
 }
 
-// Count the pairs of every key (P*P keys, those with a > b stay 0).
+// Count the pairs of every key (P*P keys, those with a > b stay 0).  Each thread takes
+// kCountItems pairs (their loads and leaf lookups all in flight at once) and each workgroup
+// adds its nonzero counts once: few workgroups, so few global atomics per key.
+constexpr uint32_t kCountItems = 16;
 static __global__ __launch_bounds__(256) void pair_key_count_kernel(
     const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los, uint64_t m,
     const uint16_t* __restrict__ leaf, uint32_t P, uint32_t* __restrict__ cnt) {
     extern __shared__ uint32_t c[];   // [P * P]
     for (uint32_t i = threadIdx.x; i < P * P; i += blockDim.x) c[i] = 0;
     __syncthreads();
-    for (uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; k < m;
-         k += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t wi = comp_win[k], lo = comp_los[k];
-        if (wi == lo) continue;
-        atomicAdd(&c[pair_key(leaf[wi] & 0x7FFFu, leaf[lo] & 0x7FFFu, P)], 1u);
+    const uint64_t base = (uint64_t)blockIdx.x * blockDim.x * kCountItems + threadIdx.x;
+    uint32_t wi[kCountItems], lo[kCountItems];
+#pragma unroll
+    for (uint32_t r = 0; r < kCountItems; ++r) {
+        const uint64_t k = base + (uint64_t)r * blockDim.x;
+        wi[r] = k < m ? comp_win[k] : 0u;
+        lo[r] = k < m ? comp_los[k] : 0u;   // k past m: winner == loser, not counted
     }
+    uint32_t wl[kCountItems], ll[kCountItems];
+#pragma unroll
+    for (uint32_t r = 0; r < kCountItems; ++r) {
+        wl[r] = leaf[wi[r]] & 0x7FFFu;
+        ll[r] = leaf[lo[r]] & 0x7FFFu;
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < kCountItems; ++r)
+        if (wi[r] != lo[r]) atomicAdd(&c[pair_key(wl[r], ll[r], P)], 1u);
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < P * P; i += blockDim.x)
         if (c[i]) atomicAdd(cnt + i, c[i]);
@@ -132,30 +146,34 @@ static __global__ __launch_bounds__(256) void pair_key_scatter_kernel(
     const uint32_t nk = P * P;
     for (uint32_t i = threadIdx.x; i < nk; i += blockDim.x) lcnt[i] = 0;
     __syncthreads();
-    const uint64_t base = (uint64_t)blockIdx.x * blockDim.x * kScatterItems;
-    uint32_t key[kScatterItems], slot[kScatterItems];
+    const uint64_t base = (uint64_t)blockIdx.x * blockDim.x * kScatterItems + threadIdx.x;
+    // every item's loads and leaf lookups in flight at once; the records are kept for the write
+    uint32_t wi[kScatterItems], lo[kScatterItems], key[kScatterItems], slot[kScatterItems];
+#pragma unroll
     for (uint32_t r = 0; r < kScatterItems; ++r) {
-        const uint64_t k = base + (uint64_t)r * blockDim.x + threadIdx.x;
-        key[r] = 0xFFFFFFFFu;
-        if (k < m) {
-            const uint32_t wi = comp_win[k], lo = comp_los[k];
-            if (wi != lo) {
-                key[r] = pair_key(leaf[wi] & 0x7FFFu, leaf[lo] & 0x7FFFu, P);
-                slot[r] = atomicAdd(&lcnt[key[r]], 1u);
-            }
-        }
+        const uint64_t k = base + (uint64_t)r * blockDim.x;
+        wi[r] = k < m ? comp_win[k] : 0u;
+        lo[r] = k < m ? comp_los[k] : 0u;   // k past m: winner == loser, skipped
     }
+#pragma unroll
+    for (uint32_t r = 0; r < kScatterItems; ++r) {
+        const uint32_t wl = leaf[wi[r]] & 0x7FFFu, ll = leaf[lo[r]] & 0x7FFFu;
+        key[r] = wi[r] != lo[r] ? pair_key(wl, ll, P) : 0xFFFFFFFFu;
+        lo[r] |= (wl <= ll ? 1u : 0u) << 31;
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < kScatterItems; ++r)
+        if (key[r] != 0xFFFFFFFFu) slot[r] = atomicAdd(&lcnt[key[r]], 1u);
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < nk; i += blockDim.x)
         if (lcnt[i]) lcnt[i] = atomicAdd(cursor + i, lcnt[i]);   // count -> reserved base
     __syncthreads();
+#pragma unroll
     for (uint32_t r = 0; r < kScatterItems; ++r) {
         if (key[r] == 0xFFFFFFFFu) continue;
-        const uint64_t k = base + (uint64_t)r * blockDim.x + threadIdx.x;
-        const uint32_t wi = comp_win[k], lo = comp_los[k];
+        const uint64_t k = base + (uint64_t)r * blockDim.x;
         const uint32_t pos = lcnt[key[r]] + slot[r];
-        const uint32_t wl = leaf[wi] & 0x7FFFu, ll = leaf[lo] & 0x7FFFu;
-        rec[pos] = make_uint2(wi, lo | ((wl <= ll ? 1u : 0u) << 31));
+        rec[pos] = make_uint2(wi[r], lo[r]);
         rec_wq[pos] = comp_wq[k];
     }
 }
@@ -176,11 +194,12 @@ constexpr uint32_t kStatChunkMin = 4096;  // pairs per chunk: at least, the sess
 // key_off / cursor = exclusive scan of the pair counts of the P*P keys (pair_key_scatter), and
 // per key {a <= b}: max(1, ceil(count / chunk)) chunk descriptors {key, first pair, pairs,
 // multi}; keys of several chunks are also listed in mk.  direct: one key (a single leaf) over
-// the m pairs in input order.
+// the m pairs in input order.  Once read, the counts [0, n_zero) are cleared for the next
+// level's pair_key_count_kernel (cnt_next: the same buffer).
 static __global__ __launch_bounds__(1024) void pair_plan_kernel(
-    const uint32_t* __restrict__ cnt, uint32_t P, int direct, uint32_t m, uint32_t chunk, uint32_t* __restrict__ key_off,
+    const uint32_t* cnt, uint32_t P, int direct, uint32_t m, uint32_t chunk, uint32_t* __restrict__ key_off,
     uint32_t* __restrict__ cursor, uint4* __restrict__ desc, uint32_t* __restrict__ n_desc,
-    uint32_t* __restrict__ mk, uint32_t* __restrict__ n_multi) {
+    uint32_t* __restrict__ mk, uint32_t* __restrict__ n_multi, uint32_t* cnt_next, uint32_t n_zero) {
     __shared__ uint32_t sc[1024], sn[1024], sm[1024];
     const uint32_t t = threadIdx.x;
     const uint32_t nk = direct ? 1u : P * P;
@@ -228,6 +247,8 @@ static __global__ __launch_bounds__(1024) void pair_plan_kernel(
         *n_desc = sn[t];
         *n_multi = sm[t];
     }
+    __syncthreads();   // every count read
+    for (uint32_t i = t; i < n_zero; i += 1024) cnt_next[i] = 0;
 }
 
 // Zero the statistics runs of the keys of several chunks (grid: (max multi keys, F)).

@@ -1361,17 +1361,18 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
     const uint32_t nchunk = (uint32_t)((s->n_pairs + chunk - 1) / chunk);
     const uint32_t max_desc = n_tri + nchunk, max_multi = std::min(n_tri, nchunk);
     if (!direct) {
-        const uint32_t nk = P * P;
-        zero_u32_kernel<<<grid_for(nk, 256), 256, 0, st>>>(s->key_cnt, nk);
-        HIP_TRY(hipGetLastError());
+        const uint32_t nk = P * P;   // (the previous level's plan cleared the counts)
         if (s->n_pairs) {
-            pair_key_count_kernel<<<grid_for(s->n_pairs, 256, 1024), 256, nk * sizeof(uint32_t), st>>>(
+            pair_key_count_kernel<<<(unsigned)((s->n_pairs + 256 * kCountItems - 1) / (256 * kCountItems)), 256,
+                                    nk * sizeof(uint32_t), st>>>(
                 s->comp_win, s->comp_los, s->n_pairs, s->leaf, P, s->key_cnt);
             HIP_TRY(hipGetLastError());
         }
     }
+    const uint32_t pmax = 1u << (s->depth - 1), next = std::min(4 * P * P, pmax * pmax);
     pair_plan_kernel<<<1, 1024, 0, st>>>(s->key_cnt, P, direct ? 1 : 0, (uint32_t)s->n_pairs, chunk, s->key_off, s->key_cur,
-                                         s->pair_desc, s->pair_nd, s->pair_mk, s->pair_nd + 1);
+                                         s->pair_desc, s->pair_nd, s->pair_mk, s->pair_nd + 1, s->key_cnt,
+                                         level + 1 < s->depth ? next : 0u);
     HIP_TRY(hipGetLastError());
     if (!direct && s->n_pairs) {
         pair_key_scatter_kernel<<<(unsigned)((s->n_pairs + 256 * kScatterItems - 1) / (256 * kScatterItems)), 256,
