@@ -138,10 +138,31 @@ static __global__ __launch_bounds__(256) void pair_key_count_kernel(
 // Each workgroup takes kScatterItems pairs per thread, ranks them per key in LDS, reserves one
 // range per key with a single global atomic, then writes.
 constexpr uint32_t kScatterItems = 8;
+// Zero the statistics runs of multi-chunk key mk[i] of feature f (pair_multi_zero_kernel's work).
+__device__ __forceinline__ void pair_multi_zero_runs(const uint32_t* __restrict__ mk, uint32_t i, uint32_t f,
+                                                     uint32_t P, uint32_t B, long long* __restrict__ st) {
+    const uint32_t k = mk[i], a = k / P, b = k % P;
+    long long* r0 = st + (((size_t)f * P + a) * P + b) * B * 2;
+    long long* r1 = st + (((size_t)f * P + b) * P + a) * B * 2;
+    for (uint32_t j = threadIdx.x; j < 2 * B; j += blockDim.x) {
+        r0[j] = 0;
+        r1[j] = 0;
+    }
+}
+
+// Workgroups past n_sc zero the runs of the multi-chunk keys (one per (key, feature), F per
+// key): the zeroing rides in the scatter's launch.
 static __global__ __launch_bounds__(256) void pair_key_scatter_kernel(
     const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los,
     const long long* __restrict__ comp_wq, uint64_t m, const uint16_t* __restrict__ leaf, uint32_t P,
-    uint32_t* __restrict__ cursor, uint2* __restrict__ rec, long long* __restrict__ rec_wq) {
+    uint32_t* __restrict__ cursor, uint2* __restrict__ rec, long long* __restrict__ rec_wq, uint32_t n_sc,
+    const uint32_t* __restrict__ mk, const uint32_t* __restrict__ n_multi, uint32_t F, uint32_t B,
+    long long* __restrict__ st) {
+    if (blockIdx.x >= n_sc) {   // uniform over the workgroup, before any barrier
+        const uint32_t z = blockIdx.x - n_sc, i = z / F;
+        if (i < *n_multi) pair_multi_zero_runs(mk, i, z % F, P, B, st);
+        return;
+    }
     extern __shared__ uint32_t lcnt[];   // [P * P]
     const uint32_t nk = P * P;
     for (uint32_t i = threadIdx.x; i < nk; i += blockDim.x) lcnt[i] = 0;
@@ -256,13 +277,7 @@ static __global__ __launch_bounds__(256) void pair_multi_zero_kernel(const uint3
                                                                      const uint32_t* __restrict__ n_multi, uint32_t P,
                                                                      uint32_t B, long long* __restrict__ st) {
     if (blockIdx.x >= *n_multi) return;
-    const uint32_t k = mk[blockIdx.x], a = k / P, b = k % P, f = blockIdx.y;
-    long long* r0 = st + (((size_t)f * P + a) * P + b) * B * 2;
-    long long* r1 = st + (((size_t)f * P + b) * P + a) * B * 2;
-    for (uint32_t i = threadIdx.x; i < 2 * B; i += blockDim.x) {
-        r0[i] = 0;
-        r1[i] = 0;
-    }
+    pair_multi_zero_runs(mk, blockIdx.x, blockIdx.y, P, B, st);
 }
 
 // Inclusive prefix over buckets of the runs of the keys of several chunks: one wavefront per

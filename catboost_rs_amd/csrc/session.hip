@@ -1374,13 +1374,13 @@ int pairwise_level(cbh_session* s, const long long* cur, uint32_t level) {
                                          s->pair_desc, s->pair_nd, s->pair_mk, s->pair_nd + 1, s->key_cnt,
                                          level + 1 < s->depth ? next : 0u);
     HIP_TRY(hipGetLastError());
-    if (!direct && s->n_pairs) {
-        pair_key_scatter_kernel<<<(unsigned)((s->n_pairs + 256 * kScatterItems - 1) / (256 * kScatterItems)), 256,
-                                  P * P * sizeof(uint32_t), st>>>(s->comp_win, s->comp_los, s->comp_wq, s->n_pairs,
-                                                                  s->leaf, P, s->key_cur, s->key_rec, s->key_wq);
+    if (!direct && s->n_pairs) {   // the scatter, and in the same launch the multi-chunk runs' zeroing
+        const unsigned n_sc = (unsigned)((s->n_pairs + 256 * kScatterItems - 1) / (256 * kScatterItems));
+        pair_key_scatter_kernel<<<n_sc + max_multi * F, 256, P * P * sizeof(uint32_t), st>>>(
+            s->comp_win, s->comp_los, s->comp_wq, s->n_pairs, s->leaf, P, s->key_cur, s->key_rec, s->key_wq, n_sc,
+            s->pair_mk, s->pair_nd + 1, F, B, s->pair_st);
         HIP_TRY(hipGetLastError());
-    }
-    if (max_multi) {
+    } else if (max_multi) {
         pair_multi_zero_kernel<<<dim3(max_multi, F), 256, 0, st>>>(s->pair_mk, s->pair_nd + 1, P, B, s->pair_st);
         HIP_TRY(hipGetLastError());
     }
