@@ -221,7 +221,7 @@ static __global__ __launch_bounds__(1024) void pair_plan_kernel(
     const uint32_t* cnt, uint32_t P, int direct, uint32_t m, uint32_t chunk, uint32_t* __restrict__ key_off,
     uint32_t* __restrict__ cursor, uint4* __restrict__ desc, uint32_t* __restrict__ n_desc,
     uint32_t* __restrict__ mk, uint32_t* __restrict__ n_multi, uint32_t* cnt_next, uint32_t n_zero) {
-    __shared__ uint32_t sc[1024], sn[1024], sm[1024];
+    __shared__ uint32_t sc[32], sn[32], sm[32];   // wave totals [0, 16), then their exclusive prefixes
     const uint32_t t = threadIdx.x;
     const uint32_t nk = direct ? 1u : P * P;
     const uint32_t per = (nk + 1023) / 1024;
@@ -238,19 +238,50 @@ static __global__ __launch_bounds__(1024) void pair_plan_kernel(
         vn += nc;
         vm += nc > 1 ? 1u : 0u;
     }
-    sc[t] = vc;
-    sn[t] = vn;
-    sm[t] = vm;
-    __syncthreads();
-    for (uint32_t o = 1; o < 1024; o <<= 1) {
-        const uint32_t ac = t >= o ? sc[t - o] : 0u, an = t >= o ? sn[t - o] : 0u, am = t >= o ? sm[t - o] : 0u;
-        __syncthreads();
-        sc[t] += ac;
-        sn[t] += an;
-        sm[t] += am;
-        __syncthreads();
+    // exclusive prefixes of the three sums over the threads: within each wave by shuffles, then
+    // over the 16 wave totals by wave 0 (two barriers)
+    const uint32_t lane = t & 63u, wave = t >> 6;
+    uint32_t ic = vc, in_ = vn, im = vm;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t uc = __shfl_up(ic, o, 64), un = __shfl_up(in_, o, 64), um = __shfl_up(im, o, 64);
+        if (lane >= (uint32_t)o) {
+            ic += uc;
+            in_ += un;
+            im += um;
+        }
     }
-    uint32_t oc = sc[t] - vc, on = sn[t] - vn, om = sm[t] - vm;
+    if (lane == 63) {
+        sc[wave] = ic;
+        sn[wave] = in_;
+        sm[wave] = im;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const uint32_t tc = lane < 16 ? sc[lane] : 0u, tn = lane < 16 ? sn[lane] : 0u, tm = lane < 16 ? sm[lane] : 0u;
+        uint32_t wc = tc, wn = tn, wm = tm;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            const uint32_t uc = __shfl_up(wc, o, 64), un = __shfl_up(wn, o, 64), um = __shfl_up(wm, o, 64);
+            if (lane >= (uint32_t)o) {
+                wc += uc;
+                wn += un;
+                wm += um;
+            }
+        }
+        if (lane < 16) {
+            sc[16 + lane] = wc - tc;
+            sn[16 + lane] = wn - tn;
+            sm[16 + lane] = wm - tm;
+        }
+        if (lane == 15) {   // the grand totals
+            if (!direct) key_off[nk] = wc;
+            *n_desc = wn;
+            *n_multi = wm;
+        }
+    }
+    __syncthreads();
+    uint32_t oc = sc[16 + wave] + ic - vc, on = sn[16 + wave] + in_ - vn, om = sm[16 + wave] + im - vm;
     for (uint32_t k = k0; k < k1; ++k) {
         const uint32_t c = count_of(k), nc = chunks_of(k, c);
         if (!direct) {
@@ -262,11 +293,6 @@ static __global__ __launch_bounds__(1024) void pair_plan_kernel(
         if (nc > 1) mk[om++] = k;
         oc += c;
         on += nc;
-    }
-    if (t == 1023) {
-        if (!direct) key_off[nk] = sc[t];
-        *n_desc = sn[t];
-        *n_multi = sm[t];
     }
     __syncthreads();   // every count read
     for (uint32_t i = t; i < n_zero; i += 1024) cnt_next[i] = 0;
