@@ -535,7 +535,8 @@ struct FillLane {
     uint32_t bin_stride;
 };
 
-template <int C, bool kSkip>
+// CU: the channels filled, 0 .. CU-1 of the C a row holds (the others stay as they are)
+template <int C, bool kSkip, int CU = C>
 __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, uint32_t W,
                                            const uint32_t* __restrict__ idx,
                                            const long long* __restrict__ sfix, uint32_t beg,
@@ -555,18 +556,18 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
             const uint32_t p = p0 + (uint32_t)u * rows_per_pass;
             doc[u] = p < end ? (idx ? idx[p] : p) : 0xFFFFFFFFu;
         }
-        long long st[U][C];
+        long long st[U][CU];
         uint32_t word[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (doc[u] != 0xFFFFFFFFu) {
                 const long long* sp_ = sfix + (size_t)doc[u] * C;
 #pragma unroll
-                for (int ch = 0; ch < C; ++ch) st[u][ch] = sp_[ch];
+                for (int ch = 0; ch < CU; ++ch) st[u][ch] = sp_[ch];
                 word[u] = rows[(size_t)doc[u] * W + w0 + wl];
             } else {
 #pragma unroll
-                for (int ch = 0; ch < C; ++ch) st[u][ch] = 0;
+                for (int ch = 0; ch < CU; ++ch) st[u][ch] = 0;
                 word[u] = 0;
             }
         }
@@ -574,7 +575,7 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
         for (int u = 0; u < U; ++u) {
             bool zero = true;  // a row of zeros (outside the sample, padding) adds nothing
 #pragma unroll
-            for (int ch = 0; ch < C; ++ch) zero &= st[u][ch] == 0;
+            for (int ch = 0; ch < CU; ++ch) zero &= st[u][ch] == 0;
             if (zero) continue;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -583,7 +584,7 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
                     if (kSkip && bin == fl.skip[k]) continue;   // dominant bin: rebuilt from the totals
                     unsigned long long* cell = lds64 + bin * fl.bin_stride + fl.off[k];
 #pragma unroll
-                    for (int ch = 0; ch < C; ++ch)
+                    for (int ch = 0; ch < CU; ++ch)
                         atomicAdd(cell + (size_t)ch * plane, (unsigned long long)st[u][ch]);
                 }
             }
@@ -591,7 +592,7 @@ __device__ __forceinline__ void fill_range(const uint32_t* __restrict__ rows, ui
     }
 }
 
-template <int C, bool kSkip>
+template <int C, bool kSkip, int CU = C>   // CU: channels filled (hist keeps C per leaf)
 static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t* __restrict__ rows, uint32_t W, uint32_t stride /* words per row in memory, >= W */,
     uint64_t n,
@@ -610,7 +611,7 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
     const uint32_t f0 = 4u * w0;
     const uint32_t TF = min(4u * TW, F - f0);
     const uint32_t plane = TF * B;                      // cells of one channel plane
-    const uint32_t cells = plane * C;
+    const uint32_t cells = plane * CU;
     for (uint32_t i = threadIdx.x; i < cells; i += blockDim.x) lds[i] = 0;
     __syncthreads();
     const uint32_t r0 = threadIdx.x / TW;
@@ -643,7 +644,7 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
         const uint32_t end = min(re, seg_end);
         const uint32_t slot = idx ? plan->built[seg] : 0u;
         if (end > pos) {
-            fill_range<C, kSkip>(rows, stride, idx, sfix, pos, end, w0, TW, plane, (unsigned long long*)lds, fl);
+            fill_range<C, kSkip, CU>(rows, stride, idx, sfix, pos, end, w0, TW, plane, (unsigned long long*)lds, fl);
             __syncthreads();
             // flush LDS -> hist[leaf][ch][f0 + f][bin]
             if (!bin_major) {   // [ch][f][bin]: i is the global order (coalesced atomics)
@@ -661,7 +662,7 @@ static __global__ __launch_bounds__(1024) void fill_kernel(
             } else {   // [ch][bin][f]: a wave takes 8 features x 8 bins (8-way LDS conflicts,
                        // 64-byte runs of bins in the global histogram)
                 const uint32_t nfb = (TF + 7) / 8, nbb = (B + 7) / 8;
-                const uint32_t vcells = C * nfb * nbb * 64;
+                const uint32_t vcells = CU * nfb * nbb * 64;
                 for (uint32_t i = threadIdx.x; i < vcells; i += blockDim.x) {
                     const uint32_t l = i & 63u, j = i >> 6;
                     const uint32_t ch = j / (nfb * nbb), jb = j - ch * (nfb * nbb);

@@ -811,6 +811,9 @@ int set_fill_attr(size_t lds) {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     HIP_TRY(hipFuncSetAttribute((const void*)fill_kernel<C, true>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    if constexpr (C == 2)   // the der-only fill of PairLogitPairwise sessions
+        HIP_TRY(hipFuncSetAttribute((const void*)fill_kernel<2, false, 1>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     return CBH_OK;
 }
 
@@ -1689,6 +1692,13 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
             fill_kernel<C, true><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
                 s->rows, s->W, s->Ws, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
                 s->skip_bin, (int)s->tiles.bin_major);
+        else if (C == 2 && s->pairwise)
+            // PairLogitPairwise scores from the der channel and the pair statistics alone: the
+            // weight channel is left out of the fill (its cells stay zero; such sessions refuse
+            // histogram capture)
+            fill_kernel<2, false, 1><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
+                s->rows, s->W, s->Ws, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
+                nullptr, (int)s->tiles.bin_major);
         else
             fill_kernel<C, false><<<G * nt, 1024, s->tiles.lds_bytes, st>>>(
                 s->rows, s->W, s->Ws, n, lidx, lplan, (const long long*)s->sstat, nt, s->tiles.tw, s->F, s->B, G, cur,
