@@ -3061,6 +3061,7 @@ static __global__ __launch_bounds__(256) void compact_kernel(const uint16_t* __r
 // ---------------------------------------------------------------------------------
 constexpr uint32_t kPhantomLdsWords = 16384;   // 64 KiB of bitmap per block
 constexpr uint32_t kPhantomBlocks = 32;        // row chunks per column
+constexpr uint32_t kPhantomThreads = 1024;     // a block's rows in flight: its loop is latency-bound
 
 // Block g of column c sets its rows' (bucket, float leaf) bits in an LDS bitmap and stores
 // it whole into its own slice of part (no global atomics: a hot category would otherwise
@@ -3075,14 +3076,18 @@ __device__ __forceinline__ uint32_t float_split_mask(const SplitRec* __restrict_
 }
 
 // float_mask < 0: taken from the device splits (float_split_mask); a level with no float split
-// yet sets nothing (its phantom count is not used).
-static __global__ __launch_bounds__(256) void phantom_bits_kernel(
+// yet sets nothing (its phantom count is not used).  Buckets are 16-bit (every column under
+// 65536 buckets) or 32-bit (TB).  Block (0, c) first clears cnt[c], which phantom_count_kernel's
+// blocks then add into.
+template <typename TB>
+static __global__ __launch_bounds__(kPhantomThreads) void phantom_bits_kernel(
     const uint16_t* __restrict__ leaf, uint64_t n, int64_t float_mask_arg, uint32_t L,
-    const uint32_t* __restrict__ cat_bk, const uint32_t* __restrict__ cat_nb,
+    const TB* __restrict__ cat_bk, const uint32_t* __restrict__ cat_nb,
     const uint64_t* __restrict__ word_off, uint32_t* __restrict__ part, const SplitRec* __restrict__ splits,
     uint32_t level, uint32_t fc0, const uint8_t* __restrict__ skip /* nullable: set = no count needed */,
-    uint64_t m_lo) {
+    uint64_t m_lo, unsigned long long* __restrict__ cnt) {
     extern __shared__ uint32_t lbits[];
+    if (blockIdx.x == 0 && threadIdx.x == 0) cnt[blockIdx.y] = 0;
     if (skip && *skip) return;
     const uint32_t float_mask =
         float_mask_arg >= 0 ? (uint32_t)float_mask_arg : float_split_mask(splits, level, fc0);
@@ -3096,7 +3101,7 @@ static __global__ __launch_bounds__(256) void phantom_bits_kernel(
     uint32_t* bits = lds ? lbits : slice;   // a block owns its slice: it clears it itself
     for (uint64_t w = threadIdx.x; w < words; w += blockDim.x) bits[w] = 0;
     __syncthreads();
-    const uint32_t* bk = cat_bk + (size_t)c * n;
+    const TB* bk = cat_bk + (size_t)c * n;
     const uint64_t per = (n + gridDim.x - 1) / gridDim.x;
     const uint64_t beg = (uint64_t)g * per;
     const uint64_t end = min(beg + per, n);
@@ -3110,7 +3115,7 @@ static __global__ __launch_bounds__(256) void phantom_bits_kernel(
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const uint64_t i = i0 + (uint64_t)u * blockDim.x;
-            b[u] = i < end ? bk[i] : 0xFFFFFFFFu;
+            b[u] = i < end ? (uint32_t)bk[i] : 0xFFFFFFFFu;
             lf[u] = i < end ? (uint32_t)leaf[i] : 0u;
         }
 #pragma unroll
@@ -3127,8 +3132,10 @@ static __global__ __launch_bounds__(256) void phantom_bits_kernel(
     for (uint32_t w = threadIdx.x; w < words; w += blockDim.x) slice[w] = lbits[w];
 }
 
-// distinct pairs of every column: OR of its kPhantomBlocks slices, popcounted (one block per
-// column)
+// distinct pairs of every column: OR of its kPhantomBlocks slices, popcounted; grid (column,
+// kPhantomCountSplit word ranges), each block adding its popcount to cnt[c] (cleared by
+// phantom_bits_kernel)
+constexpr uint32_t kPhantomCountSplit = 16;
 static __global__ __launch_bounds__(256) void phantom_count_kernel(const uint32_t* __restrict__ part,
                                                                    const uint64_t* __restrict__ word_off,
                                                                    const uint32_t* __restrict__ cat_nb, uint32_t L,
@@ -3137,28 +3144,31 @@ static __global__ __launch_bounds__(256) void phantom_count_kernel(const uint32_
                                                                    uint32_t level, uint32_t fc0,
                                                                    const uint8_t* __restrict__ skip,
                                                                    int64_t float_mask_arg, uint64_t m_lo) {
-    __shared__ unsigned long long red[256];
+    __shared__ unsigned long long red[4];
     const uint32_t c = blockIdx.x;
     const uint32_t fm = float_mask_arg >= 0 ? (uint32_t)float_mask_arg : float_split_mask(splits, level, fc0);
-    if ((skip && *skip) || fm == 0 || ((uint64_t)cat_nb[c] << __popc(fm)) <= m_lo) {   // no count
-        if (threadIdx.x == 0) cnt[c] = 0;
-        return;
-    }
+    if ((skip && *skip) || fm == 0 || ((uint64_t)cat_nb[c] << __popc(fm)) <= m_lo) return;   // no count
     const uint64_t words = ((uint64_t)cat_nb[c] * L + 31) / 32;
+    const uint64_t per = (words + gridDim.y - 1) / gridDim.y;
+    const uint64_t w0 = (uint64_t)blockIdx.y * per, w1 = min(w0 + per, words);
     const uint32_t* base = part + word_off[c];
     unsigned long long acc = 0;
-    for (uint64_t w = threadIdx.x; w < words; w += blockDim.x) {
-        uint32_t v = 0;
-        for (uint32_t g = 0; g < kPhantomBlocks; ++g) v |= base[(uint64_t)g * words + w];
-        acc += (unsigned long long)__popc(v);
+    for (uint64_t w = w0 + threadIdx.x; w < w1; w += blockDim.x) {
+        uint32_t v[kPhantomBlocks];
+#pragma unroll
+        for (uint32_t g = 0; g < kPhantomBlocks; ++g) v[g] = base[(uint64_t)g * words + w];
+        uint32_t o = 0;
+#pragma unroll
+        for (uint32_t g = 0; g < kPhantomBlocks; ++g) o |= v[g];
+        acc += (unsigned long long)__popc(o);
     }
-    red[threadIdx.x] = acc;
+    for (int d = 32; d > 0; d >>= 1) acc += __shfl_xor(acc, d, 64);
+    if (lane_id() == 0) red[threadIdx.x >> 6] = acc;
     __syncthreads();
-    for (uint32_t o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned long long t = red[0] + red[1] + red[2] + red[3];
+        if (t) atomicAdd(cnt + c, t);
     }
-    if (threadIdx.x == 0) cnt[c] = red[0];
 }
 
 // model_size_reg weights of the CTR columns for one level, on the device: a column whose

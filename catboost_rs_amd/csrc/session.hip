@@ -246,7 +246,8 @@ struct cbh_session {
     std::vector<uint8_t> ctr_used;              // [ctr_n] groups chosen by an earlier tree
     uint64_t ctr_eligible_max = 1;
     uint32_t cat_n = 0;
-    uint32_t* cat_bk = nullptr;                 // [cat_n][n] first-seen buckets
+    uint32_t* cat_bk = nullptr;                 // [cat_n][n] first-seen buckets (32-bit) ...
+    uint16_t* cat_bk16 = nullptr;               // ... or 16-bit, when every column has < 65536
     uint32_t* cat_nb_dev = nullptr;             // [cat_n]
     std::vector<uint32_t> cat_nb;
     uint64_t* phantom_off = nullptr;            // [cat_n] word offsets of the bitmaps
@@ -304,7 +305,7 @@ struct cbh_session {
         dfree(cand_scores); dfree(leaf_w); dfree(skip_bin); dfree(seg_tot); dfree(spack); dfree(sseq); dfree(trows); dfree(pks_a); dfree(pks_b); dfree(row_ent); dfree(fill_ent); dfree(w0_cache);
         dfree(key_cnt); dfree(key_off); dfree(key_cur); dfree(key_rec); dfree(key_wq); dfree(pair_ws);
         dfree(pair_desc); dfree(pair_mk); dfree(pair_nd);
-        dfree(ctr_avg); dfree(cat_bk); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
+        dfree(ctr_avg); dfree(cat_bk); dfree(cat_bk16); dfree(cat_nb_dev); dfree(phantom_off); dfree(phantom_bits);
         dfree(phantom_cnt); dfree(fweight); dfree(ctr_pow); dfree(ctr_group_dev); dfree(ctr_used_dev);
         dfree(phantom_off_lv); dfree(hist_cap);
         if (pin_ctr_used) (void)hipHostFree(pin_ctr_used);
@@ -1482,11 +1483,18 @@ int ctr_level_weights(cbh_session* s, uint32_t level) {
         }
         HIP_TRY(hipMemcpyAsync(s->phantom_off, off.data(), sizeof(uint64_t) * s->cat_n, hipMemcpyHostToDevice, st));
         (void)words;
-        phantom_bits_kernel<<<dim3(kPhantomBlocks, s->cat_n), 256, kPhantomLdsWords * sizeof(uint32_t), st>>>(
-            s->leaf, s->n, (int64_t)float_mask, L, s->cat_bk, s->cat_nb_dev, s->phantom_off, s->phantom_bits,
-            nullptr, 0u, 0u, nullptr, s->ctr_eligible_max);
+        const dim3 bg(kPhantomBlocks, s->cat_n);
+        const size_t bl = kPhantomLdsWords * sizeof(uint32_t);
+        if (s->cat_bk16)
+            phantom_bits_kernel<uint16_t><<<bg, kPhantomThreads, bl, st>>>(s->leaf, s->n, (int64_t)float_mask, L, s->cat_bk16,
+                                                               s->cat_nb_dev, s->phantom_off, s->phantom_bits, nullptr,
+                                                               0u, 0u, nullptr, s->ctr_eligible_max, s->phantom_cnt);
+        else
+            phantom_bits_kernel<uint32_t><<<bg, kPhantomThreads, bl, st>>>(s->leaf, s->n, (int64_t)float_mask, L, s->cat_bk,
+                                                               s->cat_nb_dev, s->phantom_off, s->phantom_bits, nullptr,
+                                                               0u, 0u, nullptr, s->ctr_eligible_max, s->phantom_cnt);
         HIP_TRY(hipGetLastError());
-        phantom_count_kernel<<<s->cat_n, 256, 0, st>>>(s->phantom_bits, s->phantom_off, s->cat_nb_dev, L,
+        phantom_count_kernel<<<dim3(s->cat_n, kPhantomCountSplit), 256, 0, st>>>(s->phantom_bits, s->phantom_off, s->cat_nb_dev, L,
                                                        s->phantom_cnt, nullptr, 0u, 0u, nullptr, (int64_t)float_mask,
                                                        s->ctr_eligible_max);
         HIP_TRY(hipGetLastError());
@@ -1518,11 +1526,18 @@ int ctr_level_weights_dev(cbh_session* s, uint32_t level) {
     if (level >= 1 && s->cat_n) {
         const uint32_t L = 1u << level;
         const uint64_t* off = s->phantom_off_lv + (size_t)level * s->cat_n;
-        phantom_bits_kernel<<<dim3(kPhantomBlocks, s->cat_n), 256, kPhantomLdsWords * sizeof(uint32_t), st>>>(
-            s->leaf, s->n, -1, L, s->cat_bk, s->cat_nb_dev, off, s->phantom_bits, s->splits, level, fc0,
-            s->ctr_used_dev + s->ctr_n, s->ctr_m_lo);
+        const dim3 bg(kPhantomBlocks, s->cat_n);
+        const size_t bl = kPhantomLdsWords * sizeof(uint32_t);
+        if (s->cat_bk16)
+            phantom_bits_kernel<uint16_t><<<bg, kPhantomThreads, bl, st>>>(s->leaf, s->n, -1, L, s->cat_bk16, s->cat_nb_dev, off,
+                                                               s->phantom_bits, s->splits, level, fc0,
+                                                               s->ctr_used_dev + s->ctr_n, s->ctr_m_lo, s->phantom_cnt);
+        else
+            phantom_bits_kernel<uint32_t><<<bg, kPhantomThreads, bl, st>>>(s->leaf, s->n, -1, L, s->cat_bk, s->cat_nb_dev, off,
+                                                               s->phantom_bits, s->splits, level, fc0,
+                                                               s->ctr_used_dev + s->ctr_n, s->ctr_m_lo, s->phantom_cnt);
         HIP_TRY(hipGetLastError());
-        phantom_count_kernel<<<s->cat_n, 256, 0, st>>>(s->phantom_bits, off, s->cat_nb_dev, L, s->phantom_cnt,
+        phantom_count_kernel<<<dim3(s->cat_n, kPhantomCountSplit), 256, 0, st>>>(s->phantom_bits, off, s->cat_nb_dev, L, s->phantom_cnt,
                                                        s->splits, level, fc0, s->ctr_used_dev + s->ctr_n, -1,
                                                        s->ctr_m_lo);
         HIP_TRY(hipGetLastError());
@@ -1973,9 +1988,22 @@ int install_ctr(cbh_session* s, uint32_t m, const uint32_t* bucket_count, const 
     s->fweight_host.assign(s->F, 1.0);
     HIP_TRY(hipMemcpy(s->fweight, s->fweight_host.data(), sizeof(double) * s->F, hipMemcpyHostToDevice));
     if (n_cat) {
-        CHECK(dalloc(&s->cat_bk, (size_t)n_cat * n));
-        for (uint32_t c = 0; c < n_cat; ++c)
-            HIP_TRY(hipMemcpy(s->cat_bk + (size_t)c * n, cat_cols[c], sizeof(uint32_t) * n, hipMemcpyHostToDevice));
+        // the phantom bitmaps read every bucket of every column once a level: 16-bit buckets
+        // when every column has fewer than 65536
+        bool narrow = true;
+        for (uint32_t c = 0; c < n_cat; ++c) narrow = narrow && cat_bucket_count[c] <= 65536u;
+        if (narrow) {
+            CHECK(dalloc(&s->cat_bk16, (size_t)n_cat * n));
+            std::vector<uint16_t> col(n);
+            for (uint32_t c = 0; c < n_cat; ++c) {
+                for (uint64_t i = 0; i < n; ++i) col[i] = (uint16_t)cat_cols[c][i];
+                HIP_TRY(hipMemcpy(s->cat_bk16 + (size_t)c * n, col.data(), sizeof(uint16_t) * n, hipMemcpyHostToDevice));
+            }
+        } else {
+            CHECK(dalloc(&s->cat_bk, (size_t)n_cat * n));
+            for (uint32_t c = 0; c < n_cat; ++c)
+                HIP_TRY(hipMemcpy(s->cat_bk + (size_t)c * n, cat_cols[c], sizeof(uint32_t) * n, hipMemcpyHostToDevice));
+        }
         CHECK(dalloc(&s->cat_nb_dev, n_cat));
         HIP_TRY(hipMemcpy(s->cat_nb_dev, cat_bucket_count, sizeof(uint32_t) * n_cat, hipMemcpyHostToDevice));
         CHECK(dalloc(&s->phantom_off, n_cat));
@@ -1987,7 +2015,9 @@ int install_ctr(cbh_session* s, uint32_t m, const uint32_t* bucket_count, const 
     s->ctr_used.assign(m, 0);
     s->ctr_eligible_max = 1;
     for (uint32_t v : s->ctr_bc) s->ctr_eligible_max = std::max<uint64_t>(s->ctr_eligible_max, v);
-    HIP_TRY(hipFuncSetAttribute((const void*)phantom_bits_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+    HIP_TRY(hipFuncSetAttribute((const void*)phantom_bits_kernel<uint16_t>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(kPhantomLdsWords * sizeof(uint32_t))));
+    HIP_TRY(hipFuncSetAttribute((const void*)phantom_bits_kernel<uint32_t>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)(kPhantomLdsWords * sizeof(uint32_t))));
     s->cat_n = n_cat;
     s->cat_nb.assign(cat_bucket_count, cat_bucket_count + n_cat);
