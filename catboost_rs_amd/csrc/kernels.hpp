@@ -2828,8 +2828,10 @@ __device__ __forceinline__ uint64_t wave_peers(uint32_t key, bool valid, uint32_
 }
 
 // Leaf update of one level and the per-wave row counts of every new leaf.  Each wave owns
-// kPartWaveRows consecutive rows; its counts go to cnt[leaf][wave] (one leader per distinct
-// leaf adds the popcount of its peers, so no LDS cell takes more than one add per 64 rows).
+// kPartWaveRows consecutive rows; its counts go to cnt[leaf][wave].  Up to 4 new leaves a
+// leader per distinct leaf adds the popcount of its peers (one ballot per key bit, so no LDS
+// cell takes more than one add per 64 rows); with more leaves every row adds 1 to its leaf's
+// LDS counter (few lanes share a counter, and the ballots would grow with the level).
 static __global__ __launch_bounds__(256) void split_count_kernel(
     const uint8_t* __restrict__ cols, uint64_t n, const SplitRec* __restrict__ split,
     uint32_t level, uint16_t* __restrict__ leaf, uint32_t* __restrict__ cnt, uint32_t n_waves,
@@ -2863,8 +2865,12 @@ static __global__ __launch_bounds__(256) void split_count_kernel(
         if (in) leaf[i] = (uint16_t)lf[u];
         if (write_counts) {
             const bool valid = in && !(lf[u] & 0x8000u);
-            const uint64_t mask = wave_peers(lf[u], valid, level + 1);
-            if (valid && mbcnt64(mask) == 0) c[wave][lf[u]] += (uint32_t)__popcll(mask);
+            if (level >= 2) {   // uniform
+                if (valid) atomicAdd(&c[wave][lf[u]], 1u);
+            } else {
+                const uint64_t mask = wave_peers(lf[u], valid, level + 1);
+                if (valid && mbcnt64(mask) == 0) c[wave][lf[u]] += (uint32_t)__popcll(mask);
+            }
         }
     }
     if (!write_counts) return;
