@@ -83,19 +83,23 @@ def _config4_columns(d, perm):
     return dev
 
 
-@pytest.mark.parametrize("weights,n_rows,iters", [("device", 200_000, 6), ("host", 200_000, 6),
-                                                  ("device", 2_000_000, 10)])
-def test_config4_all_ctr_matches_oracle(weights, n_rows, iters, monkeypatch):
+@pytest.mark.parametrize("weights,n_rows,iters,wide", [("device", 200_000, 6, False), ("host", 200_000, 6, False),
+                                                       ("device", 200_000, 6, True), ("device", 2_000_000, 10, False)])
+def test_config4_all_ctr_matches_oracle(weights, n_rows, iters, wide, monkeypatch):
     """Config 4's reference-legal all-CTR variant (RMSE, Bernoulli 0.66, depth 6) with the
     reference's CTR training semantics (model_size_reg weights with the phantom count, leaves
     over the averaging-permutation columns): device CTR columns equal the oracle's, then the
     trees equal the oracle's -- at 200k rows with the weights picked on the device from the
-    tabulated pow values and with the per-level host step, and at the full 2M rows."""
+    tabulated pow values and with the per-level host step, and at the full 2M rows.  wide: the
+    first categorical column takes uniform keys over 100000 values (more than 65536 buckets:
+    32-bit buckets and a phantom bitmap too large for LDS)."""
     if weights == "host":
         monkeypatch.setenv("CBH_CTR_WEIGHTS", "host")
     from catboost_rs_amd import datagen
     from tests.test_gpu_parity import _close
     d = datagen.config4(n_rows=n_rows)
+    if wide:
+        d["cat_keys"][0] = np.random.default_rng(7).integers(0, 100_000, d["target"].size).astype(np.uint32)
     P = d["params"]
     n = d["target"].size
     two = cb.shuffled_indices(n, P["random_seed"], count=2)
@@ -105,6 +109,7 @@ def test_config4_all_ctr_matches_oracle(weights, n_rows, iters, monkeypatch):
     avg = _config4_columns(d, avg_perm)
     buckets = np.stack([O.perfect_hash(k)[0] for k in d["cat_keys"]])
     counts = np.array([int(b.max()) + 1 for b in buckets], np.uint32)
+    assert not wide or counts[0] > 65536
     info = dict(avg_bins=avg, bucket_count=counts, group=np.arange(len(counts), dtype=np.uint32),
                 cat_buckets=buckets, cat_bucket_count=counts, model_size_reg=0.5)
     bins = np.concatenate([d["bins"], ctr], 0)
