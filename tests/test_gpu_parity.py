@@ -863,10 +863,12 @@ def test_fill_layouts_ragged_shapes_match_oracle(layout, F, B, K, monkeypatch):
 
 
 @pytest.mark.parametrize("loss,fill", [("PairLogit", "auto"), ("PairLogit", "tiled"), ("PairLogit", "packed"),
-                                       ("PairLogitPairwise", "auto")])
+                                       ("PairLogitPairwise", "auto"), ("PairLogitPairwise", "tiled")])
 def test_config3_reduced_matches_oracle(loss, fill, monkeypatch):
     """Config 3 shape (groups of 20, ~10 pairs per group, 100 features, 254 borders, depth 6);
-    PairLogit also through the packed fill (its weight channel holds the pairwise weights)."""
+    PairLogit also through the packed fill (its weight channel holds the pairwise weights);
+    PairLogitPairwise through the generic fill of its der channel alone (auto, below 2^20 rows)
+    and through the tiled exact fill (both channels, its default from 2^20 rows)."""
     if fill != "auto":
         monkeypatch.setenv("CBH_FILL", fill)
     d = datagen.config3(n_rows=20_000 if loss == "PairLogit" else 4_000, loss=loss)
