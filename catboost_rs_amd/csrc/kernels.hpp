@@ -3228,8 +3228,9 @@ static __global__ __launch_bounds__(256) void averaging_leaf_kernel(uint16_t* __
 template <int K>
 constexpr int leaf_cells() { return K == 1 ? 3 : K + K * (K + 1) / 2; }
 
+constexpr uint32_t kLeafThreads = 1024;
 template <int K>
-static __global__ __launch_bounds__(256) void leaf_reduce_kernel(
+static __global__ __launch_bounds__(kLeafThreads) void leaf_reduce_kernel(
     uint64_t n, int loss, int newton, const double* __restrict__ approx,
     const double* __restrict__ target, const double* __restrict__ weight,
     const uint16_t* __restrict__ leaf, const Scales* __restrict__ sc, uint32_t n_leaves,

@@ -181,6 +181,7 @@ struct cbh_session {
     long long* key_wq = nullptr;     // [m]
     uint4* pair_desc = nullptr;      // chunk descriptors of a level's statistics (pair_plan_kernel)
     uint32_t pair_cus = 256;         // CUs of the device: a level's chunks are sized to fill them once
+    uint32_t cus = 256;              // CUs of the device (the leaf reduction's grid)
     uint32_t* pair_mk = nullptr;     // keys of several chunks
     uint32_t* pair_nd = nullptr;     // [2] descriptors, keys of several chunks
     double* pair_ws = nullptr;       // global workspace of the 256-leaf solves (depth 8)
@@ -1172,6 +1173,11 @@ int session_open(const cbh_config* cfg, const double* weight, uint64_t n, uint32
     HIP_TRY(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
     CHECK(session_alloc(s.get()));
     CHECK(plan_tiles(s.get()));
+    {
+        int cus = 0;
+        HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device));
+        s->cus = (uint32_t)std::max(cus, 1);
+    }
     CHECK(with_k((int)s->K, [&](auto kc) {
         constexpr int K = decltype(kc)::value;
         CHECK(set_fill_attr<K + 1>(s->tiles.lds_bytes));
@@ -1861,7 +1867,9 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
     const uint32_t CL = (uint32_t)leaf_cells<K>();
     CHECK(launch_zero(s->leaf_sums, (size_t)n_leaves * CL, st));
     const size_t lds = (size_t)n_leaves * CL * sizeof(long long);   // attribute set at open
-    leaf_reduce_kernel<K><<<grid_for(n, 256, 1024), 256, lds, st>>>(
+    // one workgroup of 1024 threads a CU: each flushes its LDS sums once (n_leaves * CL global
+    // atomics a workgroup: 16.6k at K = 10 and 256 leaves, so few workgroups)
+    leaf_reduce_kernel<K><<<grid_for(n, kLeafThreads, s->cus), kLeafThreads, lds, st>>>(
         n, loss, newton, s->approx, s->target, s->weight, s->leaf, s->scales, n_leaves, s->leaf_sums,
         s->ranking ? s->ext_der : nullptr, s->ranking ? s->score_w : nullptr);
     HIP_TRY(hipGetLastError());
