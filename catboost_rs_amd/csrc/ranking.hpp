@@ -1097,8 +1097,9 @@ static __global__ __launch_bounds__(256) void pairwise_best_kernel(const double*
 
 // Pairwise weight sums of the final leaves (compute_pairwise_weight_sums,
 // pairwise_leaves.rs:47-88): out [L][L] int64, same-leaf pairs skipped.  The L x L sums are
-// privatized in LDS up to 128 leaves (in_lds), else added to out directly.
-static __global__ __launch_bounds__(256) void pair_leaf_weights_kernel(
+// privatized in LDS up to 128 leaves (in_lds), else added to out directly.  Launched as one
+// 1024-thread workgroup a CU, so that few LDS images are flushed.
+static __global__ __launch_bounds__(1024) void pair_leaf_weights_kernel(
     const uint32_t* __restrict__ comp_win, const uint32_t* __restrict__ comp_los,
     const long long* __restrict__ comp_wq, uint64_t m, const uint16_t* __restrict__ leaf, uint32_t L,
     long long* __restrict__ out, int in_lds) {

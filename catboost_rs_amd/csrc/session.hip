@@ -1878,7 +1878,7 @@ int enqueue_tree(cbh_session* s, bool use_host_sample) {
         if (s->n_pairs) {
             const size_t lw_bytes = (size_t)n_leaves * n_leaves * sizeof(long long);
             const bool lw_lds = lw_bytes <= kPairLdsMax;
-            pair_leaf_weights_kernel<<<grid_for(s->n_pairs, 256, 1024), 256, lw_lds ? lw_bytes : 0, st>>>(
+            pair_leaf_weights_kernel<<<grid_for(s->n_pairs, 1024, s->cus), 1024, lw_lds ? lw_bytes : 0, st>>>(
                 s->comp_win, s->comp_los, s->comp_wq, s->n_pairs, s->leaf, n_leaves, s->leaf_w, lw_lds ? 1 : 0);
             HIP_TRY(hipGetLastError());
         }
